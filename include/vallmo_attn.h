@@ -1,0 +1,221 @@
+/*
+ * vallmo_attn.h — C ABI of libvallmo_attn.so, the MI355X (gfx950) gated
+ * full-attention path of Vallmo.jl: per-head QK-RMSNorm, partial RoPE, GQA
+ * causal attention for prefill and KV-cache decode, and the sigmoid output gate.
+ *
+ * Conventions (every entry point):
+ *   - Returns int status: 0 = ok, > 0 = a passed-through hipError_t,
+ *     < 0 = an argument/shape error (VM_E_*). vm_last_error() returns the
+ *     message of the last failure on the calling thread.
+ *   - Every data pointer is a DEVICE pointer. bf16 tensors are passed as
+ *     vm_bf16* (the raw 16-bit pattern). Lengths/positions are device int32.
+ *   - Strides are in ELEMENTS; the innermost (head_dim) stride is always 1.
+ *   - Tensor layouts are named in the reference's column-major order, e.g.
+ *     K_cache (D, Ctx, Hk, B), which is row-major [B][Hk][Ctx][D] here.
+ *   - Compute entry points are asynchronous on `stream` (NULL = default
+ *     stream), allocate nothing, never synchronise, and are legal under
+ *     hipStreamBeginCapture (hipGraph replay), as the reference requires of
+ *     its decode step (src/llm/generate.jl:17-27).
+ *   - Compiled for head_dim D = 256 and HALF_ROT = 32 (rotary dim 64), the
+ *     Qwen3.5 attention facts (src/llm/qwen35.jl:15-23). Other D/HALF_ROT are
+ *     rejected with VM_E_UNSUPPORTED. GQA group H/Hk <= 16 for decode.
+ */
+#ifndef VALLMO_ATTN_H
+#define VALLMO_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t vm_bf16;   /* bfloat16 bit pattern                         */
+typedef void*    vm_stream; /* hipStream_t; NULL selects the default stream */
+
+enum {
+  VM_OK             = 0,
+  VM_E_ARG          = -1, /* null pointer / negative size / bad stride      */
+  VM_E_DIM          = -2, /* shape mismatch (the reference's DimensionMismatch) */
+  VM_E_UNSUPPORTED  = -3, /* shape outside what the kernels are built for   */
+  VM_E_SCRATCH      = -4  /* scratch buffer too small                       */
+};
+
+/* ---- errors / version ------------------------------------------------- */
+const char* vm_last_error(void);
+int vm_abi_version(void);
+
+/* ---- kernel timing (benchmarks; not a reference op) ----------------------
+ * While enabled on the calling thread, every kernel a compute entry point
+ * launches outside graph capture is bracketed by hipEvents on its stream.
+ * vm_profile_enable(1) also clears earlier records. vm_profile_read waits for
+ * the recorded events and returns the launch count and summed duration of one
+ * kernel class.                                                              */
+enum {
+  VM_K_ROWS = 0,          /* norm+RoPE / append row kernels                  */
+  VM_K_DECODE_SPLIT = 1,  /* split-KV decode attention                       */
+  VM_K_DECODE_COMBINE = 2,/* LSE merge (+ gate)                              */
+  VM_K_PREFILL = 3,       /* flash attention (prefill)                       */
+  VM_K_ADVANCE = 4,       /* device clock                                    */
+  VM_K_COUNT = 5
+};
+int vm_profile_enable(int on);
+int vm_profile_read(int kernel, int* count, double* total_ms);
+
+/* ---- runtime (thin HIP wrappers so FFI hosts need no HIP headers) ------ */
+int vm_malloc(void** ptr, size_t bytes);
+int vm_free(void* ptr);
+int vm_memcpy_h2d(void* dst, const void* src, size_t bytes, vm_stream stream);
+int vm_memcpy_d2h(void* dst, const void* src, size_t bytes, vm_stream stream);
+int vm_memcpy_d2d(void* dst, const void* src, size_t bytes, vm_stream stream);
+int vm_memset(void* dst, int value, size_t bytes, vm_stream stream);
+int vm_stream_create(vm_stream* stream);
+int vm_stream_destroy(vm_stream stream);
+int vm_stream_sync(vm_stream stream);
+int vm_device_sync(void);
+int vm_event_create(void** event);
+int vm_event_destroy(void* event);
+int vm_event_record(void* event, vm_stream stream);
+int vm_event_elapsed_ms(float* ms, void* start, void* stop);
+/* Graph capture of everything launched on `stream` between begin and end
+ * (src/llm/generate.jl:185-191: capture → instantiate → launch). */
+int vm_graph_begin_capture(vm_stream stream);
+int vm_graph_end_capture(vm_stream stream, void** graph_exec);
+int vm_graph_launch(void* graph_exec, vm_stream stream);
+int vm_graph_destroy(void* graph_exec);
+
+/* ---- a1: RoPE tables (src/llm/qwen35.jl:115-119) -----------------------
+ * cos/sin :: (HALF_ROT, Ctx) fp32 = row-major [Ctx][half_rot].
+ * inv_freq_i = f32(theta^(-i/half_rot)) (power in f64); angle = inv_freq_i *
+ * f32(t) in f32; table = f32 of the f64 cos/sin of that f32 angle. */
+int vm_rope_tables(float* cos_tab, float* sin_tab, int half_rot, int64_t ctx,
+                   double theta, vm_stream stream);
+
+/* ---- a3: qnorm_rope! (src/kernels/qknorm_rope_append.jl:100-117) -------
+ * In place on Q :: (D, Hq, B) bf16 with head stride q_sh, batch stride q_sb.
+ * q = q / sqrt(mean(q^2) + eps) * (qw + w_offset), then rotate-half RoPE on
+ * dims [0, 2*half_rot) at 0-based position positions[b]-1.                  */
+int vm_qnorm_rope(vm_bf16* q, int64_t q_sh, int64_t q_sb,
+                  const vm_bf16* qw, const float* cos_tab, const float* sin_tab,
+                  int64_t ctx, const int32_t* positions,
+                  int B, int Hq, int D, int half_rot, float eps, float w_offset,
+                  vm_stream stream);
+
+/* ---- a4: knorm_rope_append! (src/kernels/qknorm_rope_append.jl:119-141)
+ * K_cache/V_cache :: (D, Ctx, Hk, B) with strides (c_st, c_sh, c_sb);
+ * K_raw/V_raw :: (D, Hk, B) with strides (r_sh, r_sb) (one set for both).
+ * Writes norm+RoPE(k) and v into cache column positions[b] (1-based).      */
+int vm_knorm_rope_append(vm_bf16* k_cache, vm_bf16* v_cache,
+                         int64_t c_st, int64_t c_sh, int64_t c_sb, int64_t ctx,
+                         const vm_bf16* k_raw, const vm_bf16* v_raw,
+                         int64_t r_sh, int64_t r_sb,
+                         const vm_bf16* kw, const float* cos_tab, const float* sin_tab,
+                         const int32_t* positions,
+                         int B, int Hk, int D, int half_rot, float eps, float w_offset,
+                         vm_stream stream);
+
+/* ---- a5: decode_attention! (src/kernels/attention_decode.jl:268-315) ----
+ * Split-KV flash-decoding: Q :: (D, H, B) (normalised + rotated), caches as
+ * above, lengths[b] = attended keys (cache columns 1..len). O :: (D, H, B).
+ * n_splits = 0 chooses the split count from (B, Hk, ctx) to fill 256 CUs;
+ * otherwise the reference's split_size = cld(cld(ctx, n_splits), tile)*tile.
+ * scratch holds the fp32 split partials; size it with vm_decode_scratch_bytes
+ * using the same (B, H, Hk, D, ctx, n_splits).                              */
+size_t vm_decode_scratch_bytes(int B, int H, int Hk, int D, int64_t ctx, int n_splits);
+int vm_decode_attention(vm_bf16* o, int64_t o_sh, int64_t o_sb,
+                        const vm_bf16* q, int64_t q_sh, int64_t q_sb,
+                        const vm_bf16* k_cache, const vm_bf16* v_cache,
+                        int64_t c_st, int64_t c_sh, int64_t c_sb, int64_t ctx,
+                        const int32_t* lengths, int B, int H, int Hk, int D,
+                        int n_splits, void* scratch, size_t scratch_bytes,
+                        vm_stream stream);
+
+/* ---- a6: decode gate O .*= sigmoid.(q_gate) (src/llm/qwen35.jl:205) ---- */
+int vm_sigmoid_gate(vm_bf16* o, int64_t o_sh, int64_t o_sb,
+                    const vm_bf16* g, int64_t g_sh, int64_t g_sb,
+                    int B, int H, int D, vm_stream stream);
+
+/* ---- a7: decode!(h, ::AttnLayer, …) attention part (src/llm/qwen35.jl:187-208)
+ * qkv :: packed projection (D, 2Hq+2Hk, B), slots [q1 g1 … qHq gHq | k1…kHk |
+ * v1…vHk], batch stride qkv_sb. Runs a3 (fused into the split kernel), a4,
+ * a5 and a6 (fused into the merge) and writes out :: (D, Hq, B) = the Wo
+ * input, batch stride out_sb. positions[b] = 1-based column of the new token
+ * = attended length. If advance != 0, positions[b] += 1 on the device after
+ * the step (src/llm/generate.jl:82-88), so a captured graph self-advances.  */
+int vm_gated_attn_decode(vm_bf16* out, int64_t out_sb,
+                         const vm_bf16* qkv, int64_t qkv_sb,
+                         vm_bf16* k_cache, vm_bf16* v_cache,
+                         int64_t c_st, int64_t c_sh, int64_t c_sb, int64_t ctx,
+                         const vm_bf16* qw, const vm_bf16* kw,
+                         const float* cos_tab, const float* sin_tab,
+                         int32_t* positions, int advance,
+                         int B, int Hq, int Hk, int D, int half_rot,
+                         float eps, float w_offset, int n_splits,
+                         void* scratch, size_t scratch_bytes, vm_stream stream);
+
+/* ---- a12: advance! (src/llm/generate.jl:82-88): positions[b] += 1 ------ */
+int vm_advance_positions(int32_t* positions, int B, vm_stream stream);
+
+/* ---- a8: attention! (src/kernels/attention.jl:93-129) ------------------
+ * Flash attention. Q :: (D, L, H, B) strides (q_st, q_sh, q_sb); K, V ::
+ * (D, Lk, Hk, B) strides (kv_st, kv_sh, kv_sb) (typically a cache prefix);
+ * O :: (D, L, H, B). k_lengths/q_lengths (device, nullable) give ragged
+ * lengths; queries are the suffix of keys, causal offset = k_len - q_len.
+ * Rows t >= q_len[b] are not written.                                      */
+int vm_attention_fwd(vm_bf16* o, int64_t o_st, int64_t o_sh, int64_t o_sb,
+                     const vm_bf16* q, int64_t q_st, int64_t q_sh, int64_t q_sb,
+                     const vm_bf16* k, const vm_bf16* v,
+                     int64_t kv_st, int64_t kv_sh, int64_t kv_sb,
+                     const int32_t* k_lengths, const int32_t* q_lengths,
+                     int B, int H, int Hk, int D, int L, int Lk, int causal,
+                     vm_stream stream);
+
+/* ---- a9: prefill prologue (src/llm/qwen35.jl:293-307) ------------------
+ * From the packed projection qkv :: (D, 2Hq+2Hk, T, B) (token stride qkv_st,
+ * batch stride qkv_sb): norm+RoPE(k) and v of chunk token t (0-based
+ * position prior[b]+t) into cache column prior[b]+t+1. prior (device,
+ * nullable = all 0) is the prefix already in the cache; q_lengths (device,
+ * nullable = all T) the ragged chunk lengths.                                */
+int vm_prefill_kv_append(vm_bf16* k_cache, vm_bf16* v_cache,
+                         int64_t c_st, int64_t c_sh, int64_t c_sb, int64_t ctx,
+                         const vm_bf16* qkv, int64_t qkv_st, int64_t qkv_sb,
+                         const vm_bf16* kw, const float* cos_tab, const float* sin_tab,
+                         const int32_t* prior, const int32_t* q_lengths,
+                         int B, int T, int Hq, int Hk, int D, int half_rot,
+                         float eps, float w_offset, vm_stream stream);
+/* norm+RoPE(q) of the packed projection into Q :: (D, T, Hq, B) bf16 with
+ * strides (q_st, q_sh, q_sb) — the unfused prologue, for attention!.         */
+int vm_prefill_q_norm_rope(vm_bf16* q_out, int64_t q_st, int64_t q_sh, int64_t q_sb,
+                           const vm_bf16* qkv, int64_t qkv_st, int64_t qkv_sb,
+                           const vm_bf16* qw, const float* cos_tab, const float* sin_tab,
+                           const int32_t* prior, const int32_t* q_lengths,
+                           int B, int T, int Hq, int Hk, int D, int half_rot,
+                           float eps, float w_offset, vm_stream stream);
+
+/* ---- a11: forward(::AttnLayer, …; offset) attention part
+ * (src/llm/qwen35.jl:292-318): a9 (K/V into the cache), then one flash-
+ * attention kernel whose prologue norms+rotates q from qkv and whose
+ * epilogue applies the sigmoid gate (a10) and writes out :: (D*Hq, T, B) —
+ * the Wo input layout, token stride out_st, batch stride out_sb.
+ * Attends cache columns 1..prior[b]+q_len[b] of each sequence.             */
+int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb,
+                          const vm_bf16* qkv, int64_t qkv_st, int64_t qkv_sb,
+                          vm_bf16* k_cache, vm_bf16* v_cache,
+                          int64_t c_st, int64_t c_sh, int64_t c_sb, int64_t ctx,
+                          const vm_bf16* qw, const vm_bf16* kw,
+                          const float* cos_tab, const float* sin_tab,
+                          const int32_t* prior, const int32_t* q_lengths,
+                          int B, int T, int Hq, int Hk, int D, int half_rot,
+                          float eps, float w_offset, vm_stream stream);
+
+/* ---- synthetic inputs for tests and benchmarks (not a reference op) ----
+ * Fills n bf16 values with the seeded N(0,1) stream used by the CPU oracle
+ * (SplitMix64 -> Box-Muller in f64 -> f32 -> bf16 RNE), element i of stream
+ * `seed` scaled by `scale` and shifted by `shift` before rounding.           */
+int vm_fill_normal_bf16(vm_bf16* dst, int64_t n, uint64_t seed,
+                        float scale, float shift, vm_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VALLMO_ATTN_H */

@@ -1,0 +1,159 @@
+"""CPU fp32 oracle for the gated full-attention path — TEST INFRASTRUCTURE.
+
+Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
+may import this package, and only as the checker (never as the measured or
+shipped path). ``liboracle.so`` is built from ``oracle.c`` by ``oracle/Makefile``.
+
+Parity pinning (the reference ships no golden vectors or known-answer tests for
+this path; its tests cover checkpoint loaders only, test/runtests.jl:48-207):
+every function here is checked in tests/test_oracle.py against an independent
+library or closed form — torch.nn.functional.rms_norm, complex-number rotation,
+torch scaled_dot_product_attention (fp32, CPU), the relative-position and
+scale invariances, and brute-force special cases — see that file's docstrings.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+from .rng import normal_bf16, bf16_to_f32, f32_to_bf16  # noqa: F401
+
+_HERE = Path(__file__).resolve().parent
+_LIB = None
+
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+
+
+def build() -> Path:
+    """Compile liboracle.so with the committed Makefile (gcc, OpenMP)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
+    return _HERE / "liboracle.so"
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = _HERE / "liboracle.so"
+        if not path.exists():
+            build()
+        L = ctypes.CDLL(str(path))
+        i64, i32, f32, f64 = ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_double
+        L.orc_rope_tables.argtypes = [_f32p, _f32p, i32, i64, f64]
+        L.orc_rope_tables.restype = None
+        L.orc_head_norm_rope.argtypes = [_f32p, _f32p, f32, f32, _f32p, _f32p, i64, i32, i32, _f32p]
+        L.orc_head_norm_rope.restype = None
+        L.orc_attention.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_void_p, ctypes.c_void_p,
+                                    i32, i32, i32, i32, i32, i32, i32, i32, i32]
+        L.orc_attention.restype = None
+        L.orc_gated_decode.argtypes = [_u16p, _u16p, _u16p, i64, _i32p, _u16p, _u16p, _f32p, _f32p,
+                                       i32, i32, i32, i32, i32, f32, f32, _f32p, _f32p, _f32p, i32]
+        L.orc_gated_decode.restype = None
+        L.orc_gated_prefill.argtypes = [_u16p, _u16p, _u16p, i64, _i32p, _i32p, _u16p, _u16p,
+                                        _f32p, _f32p, i32, i32, i32, i32, i32, i32, f32, f32,
+                                        _f32p, _f32p, _f32p, i32, i32]
+        L.orc_gated_prefill.restype = None
+        L.orc_max_threads.restype = i32
+        _LIB = L
+    return _LIB
+
+
+def max_threads() -> int:
+    return int(lib().orc_max_threads())
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def rope_tables(half: int, ctx: int, theta: float):
+    """(cos, sin) as [ctx][half] fp32 — src/llm/qwen35.jl:115-119."""
+    c = np.empty((ctx, half), np.float32)
+    s = np.empty((ctx, half), np.float32)
+    lib().orc_rope_tables(c, s, half, ctx, float(theta))
+    return c, s
+
+
+def head_norm_rope(x, w, eps, w_offset, cos_tab, sin_tab, pos):
+    """rope(rmsnorm(x) * (w + w_offset), pos) for one head vector (fp32)."""
+    x = _c(x, np.float32)
+    y = np.empty_like(x)
+    half = cos_tab.shape[1]
+    lib().orc_head_norm_rope(x, _c(w, np.float32), eps, w_offset, _c(cos_tab, np.float32),
+                             _c(sin_tab, np.float32), int(pos), x.shape[0], half, y)
+    return y
+
+
+def attention(q, k, v, *, causal, k_lengths=None, q_lengths=None, row_step=1, nthreads=0):
+    """o = softmax(q k^T / sqrt(D)) v per (b, h); q [B][H][L][D], k/v [B][Hk][Lk][D] fp32.
+
+    src/kernels/attention.jl:12-91: GQA head h uses kv head h // (H/Hk); causal
+    offset k_len - q_len; o = 0 for rows with no key. Rows t >= q_len (and rows
+    skipped by row_step) are returned as NaN.
+    """
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    B, H, L, D = q.shape
+    Hk, Lk = k.shape[1], k.shape[2]
+    o = np.full_like(q, np.nan)
+    kl = _c(k_lengths, np.int32) if k_lengths is not None else None
+    ql = _c(q_lengths, np.int32) if q_lengths is not None else None
+    lib().orc_attention(q, k, v, o,
+                        kl.ctypes.data if kl is not None else None,
+                        ql.ctypes.data if ql is not None else None,
+                        B, H, Hk, L, Lk, D, int(bool(causal)), int(row_step), int(nthreads))
+    return o
+
+
+def gated_decode(qkv, kc, vc, positions, qw, kw, cos_tab, sin_tab, *, Hq, Hk, eps, w_offset,
+                 nthreads=0):
+    """One decode step of the attention layer (src/llm/qwen35.jl:187-208).
+
+    qkv [B][2Hq+2Hk][D] bf16 bits, kc/vc [B][Hk][ctx][D] bf16 bits, positions
+    [B] (1-based column of the new token). Returns (out [B][Hq][D],
+    k_new [B][Hk][D], v_new [B][Hk][D]) in fp32.
+    """
+    qkv, kc, vc = _c(qkv, np.uint16), _c(kc, np.uint16), _c(vc, np.uint16)
+    B, S, D = qkv.shape
+    assert S == 2 * Hq + 2 * Hk
+    ctx = kc.shape[2]
+    out = np.empty((B, Hq, D), np.float32)
+    kn = np.empty((B, Hk, D), np.float32)
+    vn = np.empty((B, Hk, D), np.float32)
+    lib().orc_gated_decode(qkv, kc, vc, ctx, _c(positions, np.int32), _c(qw, np.uint16),
+                           _c(kw, np.uint16), _c(cos_tab, np.float32), _c(sin_tab, np.float32),
+                           B, Hq, Hk, D, cos_tab.shape[1], eps, w_offset, out, kn, vn,
+                           int(nthreads))
+    return out, kn, vn
+
+
+def gated_prefill(qkv, kc, vc, prior, q_len, qw, kw, cos_tab, sin_tab, *, Hq, Hk, eps, w_offset,
+                  row_step=1, nthreads=0):
+    """Chunked prefill of the attention layer (src/llm/qwen35.jl:292-318), ragged.
+
+    qkv [B][T][2Hq+2Hk][D] bf16 bits; kc/vc [B][Hk][ctx][D] bf16 bits holding
+    prior[b] cached tokens; q_len[b] chunk lengths. Returns (out [B][T][Hq][D],
+    k_new [B][Hk][T][D], v_new [B][Hk][T][D]) in fp32; unevaluated rows are NaN.
+    """
+    qkv, kc, vc = _c(qkv, np.uint16), _c(kc, np.uint16), _c(vc, np.uint16)
+    B, T, S, D = qkv.shape
+    assert S == 2 * Hq + 2 * Hk
+    ctx = kc.shape[2]
+    out = np.full((B, T, Hq, D), np.nan, np.float32)
+    kn = np.full((B, Hk, T, D), np.nan, np.float32)
+    vn = np.full((B, Hk, T, D), np.nan, np.float32)
+    lib().orc_gated_prefill(qkv, kc, vc, ctx, _c(prior, np.int32), _c(q_len, np.int32),
+                            _c(qw, np.uint16), _c(kw, np.uint16), _c(cos_tab, np.float32),
+                            _c(sin_tab, np.float32), B, T, Hq, Hk, D, cos_tab.shape[1], eps,
+                            w_offset, out, kn, vn, int(row_step), int(nthreads))
+    return out, kn, vn
+
+
+def threads_env() -> int:
+    """OpenMP threads the oracle will use (OMP_NUM_THREADS or all cores)."""
+    n = os.environ.get("OMP_NUM_THREADS")
+    return int(n) if n else max_threads()

@@ -1,0 +1,332 @@
+/*
+ * oracle.c — CPU fp32 restatement of the reference's gated full-attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the parity checker: only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and
+ * never as the thing measured or shipped. The product path (libvallmo_attn.so)
+ * does not link or call it.
+ *
+ * Every quantity is evaluated in fp32 from the bf16 inputs (taken as their
+ * exact fp32 values); nothing is rounded back to bf16, so it is the "plain
+ * fp32 evaluation of the same math" the parity tolerances are stated against.
+ * Layouts are row-major with the reference's column-major dims reversed,
+ * e.g. K_cache (D, Ctx, Hk, B) is [B][Hk][Ctx][D] here.
+ *
+ * Reference lines followed (relative to the reference checkout):
+ *   rope tables ............ src/llm/qwen35.jl:115-119
+ *   per-head RMSNorm ........ src/llm/qwen35.jl:276-278, src/kernels/qknorm_rope_append.jl:41,80
+ *   partial rotate-half RoPE  src/llm/qwen35.jl:280-287, qknorm_rope_append.jl:49-54,87-92
+ *   cache append ............ qknorm_rope_append.jl:82-95, src/llm/qwen35.jl:306-307
+ *   attention (mask, GQA,
+ *     suffix offset, l==0) .. src/kernels/attention.jl:28-88
+ *   decode attention ........ src/kernels/attention_decode.jl:148-266 (unsplit here)
+ *   sigmoid gate ............ src/kernels/kernels.jl:34, src/llm/qwen35.jl:205,315
+ *   decode! / forward ....... src/llm/qwen35.jl:187-208, 292-318
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static inline float bf(uint16_t h) {
+  union { uint32_t u; float f; } c;
+  c.u = (uint32_t)h << 16;
+  return c.f;
+}
+
+/* f32 -> bf16 round-to-nearest-even (finite inputs). */
+uint16_t orc_f2bf(float f) {
+  union { uint32_t u; float f; } c;
+  c.f = f;
+  uint32_t u = c.u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+/* rope_tables (qwen35.jl:115-119): inv_freq = Float32(theta^-(i/half)) with the
+ * power in Float64; angle = inv_freq * Float32(t) in Float32; cos/sin of the
+ * Float32 angle (evaluated in f64 and rounded once). Tables are [ctx][half]. */
+void orc_rope_tables(float* cos_tab, float* sin_tab, int half, int64_t ctx, double theta) {
+  for (int64_t t = 0; t < ctx; ++t)
+    for (int i = 0; i < half; ++i) {
+      float inv = (float)pow(theta, -((double)i / (double)half));
+      float ang = inv * (float)t;
+      cos_tab[t * half + i] = (float)cos((double)ang);
+      sin_tab[t * half + i] = (float)sin((double)ang);
+    }
+}
+
+/* y = rope(x / sqrt(mean(x^2) + eps) * (w + w_off), pos); rotate-half on the
+ * first 2*half dims (qwen35.jl:276-287). x, y may not alias. */
+void orc_head_norm_rope(const float* x, const float* w, float eps, float w_off,
+                        const float* cos_tab, const float* sin_tab, int64_t pos, int D,
+                        int half, float* y) {
+  float ss = 0.f;
+  for (int d = 0; d < D; ++d) ss += x[d] * x[d];
+  const float r = 1.0f / sqrtf(ss / (float)D + eps);
+  for (int d = 0; d < D; ++d) y[d] = x[d] * r * (w[d] + w_off);
+  const float* c = cos_tab + pos * half;
+  const float* s = sin_tab + pos * half;
+  for (int i = 0; i < half; ++i) {
+    const float x1 = y[i], x2 = y[i + half];
+    y[i] = x1 * c[i] - x2 * s[i];
+    y[i + half] = x2 * c[i] + x1 * s[i];
+  }
+}
+
+static inline float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* One query row against keys [0, nk): o = softmax(scale * q.k) v, o = 0 if nk == 0
+ * (attention.jl:86). k_rows/v_rows are arrays of row pointers (so the oracle can
+ * mix cache rows and freshly computed rows without copying). */
+static void attend_row(const float* q, const float* const* k_rows, const float* const* v_rows,
+                       int64_t nk, int D, float scale, float* s_buf, float* o) {
+  for (int d = 0; d < D; ++d) o[d] = 0.f;
+  if (nk <= 0) return;
+  float m = -INFINITY;
+  for (int64_t u = 0; u < nk; ++u) {
+    const float* k = k_rows[u];
+    float acc = 0.f;
+#pragma omp simd reduction(+ : acc)
+    for (int d = 0; d < D; ++d) acc += q[d] * k[d];
+    s_buf[u] = acc * scale;
+    if (s_buf[u] > m) m = s_buf[u];
+  }
+  float l = 0.f;
+  for (int64_t u = 0; u < nk; ++u) {
+    const float p = expf(s_buf[u] - m);
+    l += p;
+    const float* v = v_rows[u];
+#pragma omp simd
+    for (int d = 0; d < D; ++d) o[d] += p * v[d];
+  }
+  const float inv = 1.0f / l;
+  for (int d = 0; d < D; ++d) o[d] *= inv;
+}
+
+static void set_threads(int nthreads) {
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+  (void)nthreads;
+#endif
+}
+
+/* attention! core (attention.jl:12-91): q [B][H][L][D], k/v [B][Hk][Lk][D] (fp32),
+ * o [B][H][L][D]. k_len = k_lengths ? k_lengths[b] : Lk, q_len likewise; the
+ * causal offset is k_len - q_len (queries are the suffix of keys). Rows
+ * t >= q_len are left untouched. row_step > 1 evaluates every row_step-th row
+ * only (the others are left untouched) to bound the cost of large checks. */
+void orc_attention(const float* q, const float* k, const float* v, float* o,
+                   const int32_t* k_lengths, const int32_t* q_lengths, int B, int H, int Hk,
+                   int L, int Lk, int D, int causal, int row_step, int nthreads) {
+  set_threads(nthreads);
+  const int G = H / Hk;
+  const float scale = 1.0f / sqrtf((float)D);
+  if (row_step < 1) row_step = 1;
+#pragma omp parallel
+  {
+    float* s_buf = (float*)malloc(sizeof(float) * (size_t)(Lk > 0 ? Lk : 1));
+    const float** kr = (const float**)malloc(sizeof(float*) * (size_t)(Lk > 0 ? Lk : 1));
+    const float** vr = (const float**)malloc(sizeof(float*) * (size_t)(Lk > 0 ? Lk : 1));
+#pragma omp for collapse(3) schedule(dynamic, 1)
+    for (int b = 0; b < B; ++b)
+      for (int h = 0; h < H; ++h)
+        for (int t = 0; t < L; t += row_step) {
+          const int k_len = k_lengths ? k_lengths[b] : Lk;
+          const int q_len = q_lengths ? q_lengths[b] : L;
+          if (t >= q_len) continue;
+          const int off = k_len - q_len;
+          const int hk = h / G;
+          int64_t nk = causal ? (int64_t)t + off + 1 : k_len;
+          if (nk > k_len) nk = k_len;
+          if (nk < 0) nk = 0;
+          const float* kb = k + ((size_t)b * Hk + hk) * (size_t)Lk * D;
+          const float* vb = v + ((size_t)b * Hk + hk) * (size_t)Lk * D;
+          for (int64_t u = 0; u < nk; ++u) {
+            kr[u] = kb + u * D;
+            vr[u] = vb + u * D;
+          }
+          attend_row(q + (((size_t)b * H + h) * L + t) * D, kr, vr, nk, D, scale, s_buf,
+                     o + (((size_t)b * H + h) * L + t) * D);
+        }
+    free(s_buf);
+    free(kr);
+    free(vr);
+  }
+}
+
+/* decode!(h, ::AttnLayer, ...) attention part (qwen35.jl:187-208) for one step.
+ * qkv  [B][2Hq+2Hk][D] bf16 packed [q1 g1 .. qHq gHq | k1..kHk | v1..vHk]
+ * kc/vc [B][Hk][ctx][D] bf16 prior cache; columns 0..pos-2 are attended from it
+ * positions[b] = 1-based column of the new token = attended length
+ * out  [B][Hq][D] fp32 = (attention over the cache + new row) * sigmoid(gate)
+ * knew/vnew [B][Hk][D] fp32 = the rows the step appends at column positions[b]. */
+void orc_gated_decode(const uint16_t* qkv, const uint16_t* kc, const uint16_t* vc, int64_t ctx,
+                      const int32_t* positions, const uint16_t* qw, const uint16_t* kw,
+                      const float* cos_tab, const float* sin_tab, int B, int Hq, int Hk, int D,
+                      int half, float eps, float w_off, float* out, float* knew, float* vnew,
+                      int nthreads) {
+  set_threads(nthreads);
+  const int S = 2 * Hq + 2 * Hk, G = Hq / Hk;
+  const float scale = 1.0f / sqrtf((float)D);
+  float* qwf = (float*)malloc(sizeof(float) * D);
+  float* kwf = (float*)malloc(sizeof(float) * D);
+  for (int d = 0; d < D; ++d) {
+    qwf[d] = bf(qw[d]);
+    kwf[d] = bf(kw[d]);
+  }
+  /* new K/V rows first (knorm_rope_append!) */
+  for (int b = 0; b < B; ++b) {
+    const int64_t pos = positions[b] - 1;
+    for (int j = 0; j < Hk; ++j) {
+      float x[1024];
+      const uint16_t* kr = qkv + ((size_t)b * S + 2 * Hq + j) * D;
+      const uint16_t* vr = qkv + ((size_t)b * S + 2 * Hq + Hk + j) * D;
+      for (int d = 0; d < D; ++d) x[d] = bf(kr[d]);
+      orc_head_norm_rope(x, kwf, eps, w_off, cos_tab, sin_tab, pos, D, half,
+                         knew + ((size_t)b * Hk + j) * D);
+      for (int d = 0; d < D; ++d) vnew[((size_t)b * Hk + j) * D + d] = bf(vr[d]);
+    }
+  }
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < Hq; ++h) {
+      const int64_t len = positions[b];
+      const int hk = h / G;
+      float x[1024], qn[1024], o[1024];
+      const uint16_t* qr = qkv + ((size_t)b * S + 2 * h) * D;
+      const uint16_t* gr = qkv + ((size_t)b * S + 2 * h + 1) * D;
+      for (int d = 0; d < D; ++d) x[d] = bf(qr[d]);
+      orc_head_norm_rope(x, qwf, eps, w_off, cos_tab, sin_tab, len - 1, D, half, qn);
+      float* s_buf = (float*)malloc(sizeof(float) * (size_t)len);
+      float* krow = (float*)malloc(sizeof(float) * (size_t)len * D);
+      float* vrow = (float*)malloc(sizeof(float) * (size_t)len * D);
+      const float** kp = (const float**)malloc(sizeof(float*) * (size_t)len);
+      const float** vp = (const float**)malloc(sizeof(float*) * (size_t)len);
+      const uint16_t* kb = kc + ((size_t)b * Hk + hk) * (size_t)ctx * D;
+      const uint16_t* vb = vc + ((size_t)b * Hk + hk) * (size_t)ctx * D;
+      for (int64_t u = 0; u + 1 < len; ++u) {
+        for (int d = 0; d < D; ++d) {
+          krow[u * D + d] = bf(kb[u * D + d]);
+          vrow[u * D + d] = bf(vb[u * D + d]);
+        }
+        kp[u] = krow + u * D;
+        vp[u] = vrow + u * D;
+      }
+      kp[len - 1] = knew + ((size_t)b * Hk + hk) * D;
+      vp[len - 1] = vnew + ((size_t)b * Hk + hk) * D;
+      attend_row(qn, kp, vp, len, D, scale, s_buf, o);
+      for (int d = 0; d < D; ++d) out[((size_t)b * Hq + h) * D + d] = o[d] * sigmoid_f(bf(gr[d]));
+      free(s_buf);
+      free(krow);
+      free(vrow);
+      free(kp);
+      free(vp);
+    }
+  free(qwf);
+  free(kwf);
+}
+
+/* forward(::AttnLayer, ...; offset) attention part (qwen35.jl:292-318), ragged.
+ * qkv  [B][T][2Hq+2Hk][D] bf16; kc/vc [B][Hk][ctx][D] bf16 prior cache
+ * prior[b] = tokens already cached (the chunk starts at 0-based position prior[b]);
+ * q_len[b] <= T chunk length. Chunk token t attends cache columns
+ * 0..prior[b]+t (causal, queries are the suffix of keys).
+ * out [B][T][Hq][D] fp32 (rows t >= q_len untouched; with row_step > 1 only rows
+ * t % row_step == 0 are evaluated); kout/vout [B][Hk][T][D] fp32 = appended rows. */
+void orc_gated_prefill(const uint16_t* qkv, const uint16_t* kc, const uint16_t* vc, int64_t ctx,
+                       const int32_t* prior, const int32_t* q_len, const uint16_t* qw,
+                       const uint16_t* kw, const float* cos_tab, const float* sin_tab, int B,
+                       int T, int Hq, int Hk, int D, int half, float eps, float w_off,
+                       float* out, float* kout, float* vout, int row_step, int nthreads) {
+  set_threads(nthreads);
+  const int S = 2 * Hq + 2 * Hk, G = Hq / Hk;
+  const float scale = 1.0f / sqrtf((float)D);
+  if (row_step < 1) row_step = 1;
+  float* qwf = (float*)malloc(sizeof(float) * D);
+  float* kwf = (float*)malloc(sizeof(float) * D);
+  for (int d = 0; d < D; ++d) {
+    qwf[d] = bf(qw[d]);
+    kwf[d] = bf(kw[d]);
+  }
+  /* appended rows (the prologue): norm+rope(k), v */
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int b = 0; b < B; ++b)
+    for (int t = 0; t < T; ++t) {
+      if (t >= q_len[b]) continue;
+      for (int j = 0; j < Hk; ++j) {
+        float x[1024];
+        const uint16_t* kr = qkv + (((size_t)b * T + t) * S + 2 * Hq + j) * D;
+        const uint16_t* vr = qkv + (((size_t)b * T + t) * S + 2 * Hq + Hk + j) * D;
+        for (int d = 0; d < D; ++d) x[d] = bf(kr[d]);
+        orc_head_norm_rope(x, kwf, eps, w_off, cos_tab, sin_tab, (int64_t)prior[b] + t, D, half,
+                           kout + (((size_t)b * Hk + j) * T + t) * D);
+        for (int d = 0; d < D; ++d) vout[(((size_t)b * Hk + j) * T + t) * D + d] = bf(vr[d]);
+      }
+    }
+  /* prior cache rows as fp32 */
+  int64_t maxp = 0;
+  for (int b = 0; b < B; ++b)
+    if (prior[b] > maxp) maxp = prior[b];
+  float* kpf = (float*)malloc(sizeof(float) * (size_t)B * Hk * (size_t)(maxp > 0 ? maxp : 1) * D);
+  float* vpf = (float*)malloc(sizeof(float) * (size_t)B * Hk * (size_t)(maxp > 0 ? maxp : 1) * D);
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int b = 0; b < B; ++b)
+    for (int j = 0; j < Hk; ++j)
+      for (int64_t u = 0; u < prior[b]; ++u)
+        for (int d = 0; d < D; ++d) {
+          kpf[(((size_t)b * Hk + j) * maxp + u) * D + d] = bf(kc[(((size_t)b * Hk + j) * ctx + u) * D + d]);
+          vpf[(((size_t)b * Hk + j) * maxp + u) * D + d] = bf(vc[(((size_t)b * Hk + j) * ctx + u) * D + d]);
+        }
+#pragma omp parallel
+  {
+    const int64_t maxk = maxp + T;
+    float* s_buf = (float*)malloc(sizeof(float) * (size_t)maxk);
+    const float** kp = (const float**)malloc(sizeof(float*) * (size_t)maxk);
+    const float** vp = (const float**)malloc(sizeof(float*) * (size_t)maxk);
+#pragma omp for collapse(3) schedule(dynamic, 1)
+    for (int b = 0; b < B; ++b)
+      for (int h = 0; h < Hq; ++h)
+        for (int t = 0; t < T; t += row_step) {
+          if (t >= q_len[b]) continue;
+          const int hk = h / G;
+          const int64_t P = prior[b];
+          float x[1024], qn[1024], o[1024];
+          const uint16_t* qr = qkv + (((size_t)b * T + t) * S + 2 * h) * D;
+          const uint16_t* gr = qkv + (((size_t)b * T + t) * S + 2 * h + 1) * D;
+          for (int d = 0; d < D; ++d) x[d] = bf(qr[d]);
+          orc_head_norm_rope(x, qwf, eps, w_off, cos_tab, sin_tab, P + t, D, half, qn);
+          const int64_t nk = P + t + 1;
+          for (int64_t u = 0; u < P; ++u) {
+            kp[u] = kpf + (((size_t)b * Hk + hk) * maxp + u) * D;
+            vp[u] = vpf + (((size_t)b * Hk + hk) * maxp + u) * D;
+          }
+          for (int64_t u = 0; u <= t; ++u) {
+            kp[P + u] = kout + (((size_t)b * Hk + hk) * T + u) * D;
+            vp[P + u] = vout + (((size_t)b * Hk + hk) * T + u) * D;
+          }
+          attend_row(qn, kp, vp, nk, D, scale, s_buf, o);
+          float* orow = out + (((size_t)b * T + t) * Hq + h) * D;
+          for (int d = 0; d < D; ++d) orow[d] = o[d] * sigmoid_f(bf(gr[d]));
+        }
+    free(s_buf);
+    free(kp);
+    free(vp);
+  }
+  free(kpf);
+  free(vpf);
+  free(qwf);
+  free(kwf);
+}
+
+int orc_max_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}

@@ -1,0 +1,169 @@
+"""Prefill path on the GPU vs the oracle: attention! (a8) alone, the fused
+forward(::AttnLayer) (a9 prologue + a8 + a10 gate epilogue, a11) including
+ragged chunked prefill, BASELINE configs 2 and 5 at full size (sampled query
+rows against the oracle, every appended cache row checked), and the
+cross-kernel identities: decode == last prefill row, chunked == full prefill."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import (D, EPS, HALF, HK, HQ, S, THETA, TOL_MAX, TOL_MEAN, banner, dev_f32,
+                      from_dev, i32, maxmean, to_dev)
+from oracle.rng import bf16_to_f32, normal_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("H,Hk,L,Lk", [(16, 4, 200, 300), (8, 8, 130, 130), (16, 2, 1, 77),
+                                       (4, 1, 257, 1000)])
+def test_attention_operator(vm, orc, causal, H, Hk, L, Lk):
+    banner(f"attention_ causal={causal} H={H} Hk={Hk} L={L} Lk={Lk}")
+    B = 2
+    q = normal_bf16((B, H, L, D), 11)
+    k = normal_bf16((B, Hk, Lk, D), 12)
+    v = normal_bf16((B, Hk, Lk, D), 13)
+    o = vm.attention(to_dev(q), to_dev(k), to_dev(v), causal=causal)["O"]
+    torch.cuda.synchronize()
+    ref = orc.attention(bf16_to_f32(q).reshape(q.shape), bf16_to_f32(k).reshape(k.shape),
+                        bf16_to_f32(v).reshape(v.shape), causal=causal)
+    mx, mn = maxmean(dev_f32(o), ref)
+    assert mx <= TOL_MAX and mn <= TOL_MEAN
+
+
+def test_attention_ragged_rows_untouched(vm, orc):
+    banner("attention_ ragged k/q lengths")
+    B, H, Hk, L, Lk = 3, 16, 4, 300, 700
+    q = normal_bf16((B, H, L, D), 21)
+    k = normal_bf16((B, Hk, Lk, D), 22)
+    v = normal_bf16((B, Hk, Lk, D), 23)
+    kl = np.array([700, 300, 129], np.int32)
+    ql = np.array([300, 1, 129], np.int32)
+    O = torch.full((B, H, L, D), 7.0, dtype=torch.bfloat16, device="cuda")
+    vm.attention_({"O": O}, to_dev(q), to_dev(k), to_dev(v), causal=True, k_lengths=i32(kl),
+                  q_lengths=i32(ql))
+    torch.cuda.synchronize()
+    ref = orc.attention(bf16_to_f32(q).reshape(q.shape), bf16_to_f32(k).reshape(k.shape),
+                        bf16_to_f32(v).reshape(v.shape), causal=True, k_lengths=kl, q_lengths=ql)
+    got = dev_f32(O)
+    fin = ~np.isnan(ref)
+    mx, mn = maxmean(got[fin], ref[fin])
+    assert mx <= TOL_MAX and mn <= TOL_MEAN
+    assert np.all(got[~fin] == 7.0)
+
+
+def _fused(vm, orc, B, T, ctx, prior, qlen, seed, row_step=1, fill_gpu=False):
+    cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
+    qw = normal_bf16((D,), seed + 1, scale=0.05)
+    kw = normal_bf16((D,), seed + 2, scale=0.05)
+    if fill_gpu:
+        K = torch.empty((B, HK, ctx, D), dtype=torch.bfloat16, device="cuda")
+        V = torch.empty_like(K)
+        vm.fill_normal_(K, seed + 3)
+        vm.fill_normal_(V, seed + 4)
+    else:
+        K = to_dev(normal_bf16((B, HK, ctx, D), seed + 3))
+        V = to_dev(normal_bf16((B, HK, ctx, D), seed + 4))
+    kc, vc = from_dev(K), from_dev(V)
+    qkv = normal_bf16((B, T, S, D), seed + 5)
+    m = vm.AttnModel(cfg)
+    layer = vm.AttnLayer(qw=to_dev(qw), kw=to_dev(kw), K_cache=K, V_cache=V)
+    out = vm.forward(layer, m, to_dev(qkv), T, B, prior=i32(prior), q_lengths=i32(qlen))
+    torch.cuda.synchronize()
+    got = dev_f32(out).reshape(B, T, HQ, D)
+    c, s = orc.rope_tables(HALF, ctx, THETA)
+    ref, kn, vn = orc.gated_prefill(qkv, kc, vc, prior, qlen, qw, kw, c, s, Hq=HQ, Hk=HK, eps=EPS,
+                                    w_offset=1.0, row_step=row_step)
+    fin = ~np.isnan(ref)
+    mx, mn = maxmean(got[fin], ref[fin])
+    kg, vg = from_dev(layer.K_cache), from_dev(layer.V_cache)
+    kerr = []
+    vex = True
+    for b in range(B):
+        P, C = int(prior[b]), int(qlen[b])
+        kerr.append(np.abs(bf16_to_f32(kg[b, :, P:P + C]).reshape(HK, C, D) - kn[b, :, :C]))
+        vex &= np.array_equal(bf16_to_f32(vg[b, :, P:P + C]).reshape(HK, C, D), vn[b, :, :C])
+        # columns outside [P, P+C) untouched
+        keep = np.ones(ctx, bool)
+        keep[P:P + C] = False
+        vex &= np.array_equal(kg[b][:, keep], kc[b][:, keep])
+    kerr = np.concatenate([e.ravel() for e in kerr])
+    return (mx, mn), (float(kerr.max()), float(kerr.mean())), vex, out
+
+
+def test_fused_prefill_small_ragged(vm, orc):
+    banner("fused prefill B=3 ragged")
+    (mx, mn), (kmx, kmn), ok, _ = _fused(vm, orc, 3, 300, 1024, np.array([0, 129, 700], np.int32),
+                                         np.array([300, 31, 257], np.int32), 50)
+    assert mx <= TOL_MAX and mn <= TOL_MEAN and kmx <= TOL_MAX and kmn <= TOL_MEAN and ok
+
+
+def test_config2_prefill_full_size(vm, orc):
+    """causal prefill, B=1, T=4096, offset 0; every 8th query
+    row re-evaluated by the oracle, every appended K/V row checked."""
+    banner("config2 prefill T=4096")
+    (mx, mn), (kmx, kmn), ok, _ = _fused(vm, orc, 1, 4096, 4096, np.array([0], np.int32),
+                                         np.array([4096], np.int32), 60, row_step=8)
+    print(f"config2: out max {mx:.3e} mean {mn:.3e}; K max {kmx:.3e} mean {kmn:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN and kmx <= TOL_MAX and kmn <= TOL_MEAN and ok
+
+
+def test_config5_chunked_prefill_full_size(vm, orc):
+    """B=4 ragged chunks (a seeded permutation of
+    {512, 1024, 2048, 2048}) after prior caches ~U{8192..32768}; every 64th row
+    re-evaluated by the oracle."""
+    rng = np.random.default_rng(5)
+    qlen = rng.permutation(np.array([512, 1024, 2048, 2048], np.int32)).astype(np.int32)
+    prior = rng.integers(8192, 32769, size=4).astype(np.int32)
+    ctx = int((prior + qlen).max())
+    banner(f"config5 chunked prefill prior={prior.tolist()} chunks={qlen.tolist()} ctx={ctx}")
+    (mx, mn), (kmx, kmn), ok, _ = _fused(vm, orc, 4, 2048, ctx, prior, qlen, 70, row_step=64,
+                                         fill_gpu=True)
+    print(f"config5: out max {mx:.3e} mean {mn:.3e}; K max {kmx:.3e} mean {kmn:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN and kmx <= TOL_MAX and kmn <= TOL_MEAN and ok
+
+
+def test_decode_equals_last_prefill_row(vm):
+    """A decode step at position p equals the last row of a causal prefill over
+    p tokens (both on the GPU; same cache contents)."""
+    banner("decode == last prefill row")
+    B, T, ctx = 2, 333, 512
+    cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
+    qw, kw = to_dev(normal_bf16((D,), 81, scale=0.05)), to_dev(normal_bf16((D,), 82, scale=0.05))
+    qkv = to_dev(normal_bf16((B, T, S, D), 83))
+    m = vm.AttnModel(cfg)
+    la = vm.attn_layer(cfg, qw, kw)
+    full = vm.forward(la, m, qkv, T, B)
+    lb = vm.attn_layer(cfg, qw, kw)
+    vm.forward(lb, m, qkv[:, :T - 1].contiguous(), T - 1, B)
+    gen = vm.Generation(B)
+    gen.positions.fill_(T)
+    O = torch.empty((B, HQ, D), dtype=torch.bfloat16, device="cuda")
+    vm.decode_(O, lb, m, gen, qkv[:, T - 1].contiguous())
+    torch.cuda.synchronize()
+    a = full.reshape(B, T, HQ, D)[:, T - 1].float().cpu().numpy()
+    b = O.float().cpu().numpy()
+    mx, mn = maxmean(a, b)
+    assert mx <= TOL_MAX and mn <= TOL_MEAN
+    assert torch.equal(la.K_cache, lb.K_cache) and torch.equal(la.V_cache, lb.V_cache)
+
+
+def test_chunked_equals_full_prefill(vm):
+    """attention.jl:3-7 — chunk after P cached tokens == rows P.. of the full prefill."""
+    banner("chunked == full prefill")
+    B, T, P, ctx = 1, 700, 300, 1024
+    cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
+    qw, kw = to_dev(normal_bf16((D,), 91, scale=0.05)), to_dev(normal_bf16((D,), 92, scale=0.05))
+    qkv = to_dev(normal_bf16((B, T, S, D), 93))
+    m = vm.AttnModel(cfg)
+    la = vm.attn_layer(cfg, qw, kw)
+    full = vm.forward(la, m, qkv, T, B)
+    lb = vm.attn_layer(cfg, qw, kw)
+    vm.forward(lb, m, qkv[:, :P].contiguous(), P, B)
+    part = vm.forward(lb, m, qkv[:, P:].contiguous(), T - P, B, offset=P)
+    torch.cuda.synchronize()
+    mx, mn = maxmean(full[:, P:].float().cpu().numpy(), part.float().cpu().numpy())
+    assert mx <= 1e-2 and mn <= 1e-3
+    assert torch.equal(la.K_cache, lb.K_cache)

@@ -1,0 +1,21 @@
+"""vallmo.jl_amd — the gated full-attention path of Vallmo.jl on MI355X (gfx950).
+
+Hand-written CDNA4 HIP kernels in ``csrc/`` built into ``libvallmo_attn.so``
+(C ABI: include/vallmo_attn.h); this package is the host-side mirror of the
+reference's operator and layer call surface (src/kernels/*.jl,
+src/llm/qwen35.jl, src/llm/generate.jl) over that ABI.
+
+The directory name is not a Python identifier; load it with
+``__graft_entry__.load_package()`` (registered as module ``vallmo_amd``).
+"""
+from ._lib import (ArgumentError, DimensionMismatch, HIPError, UnsupportedShape,  # noqa: F401
+                   LIB_PATH, EXPORTED)
+from .sizes import sizes  # noqa: F401
+from .ops import (attention, attention_, decode_attention, decode_attention_,  # noqa: F401
+                  decode_scratch_bytes, fill_normal_, knorm_rope_append_, qnorm_rope_,
+                  rope_tables, sigmoid, sigmoid_gate_)
+from .layer import (AttnConfig, AttnLayer, AttnModel, CaptureSession, Generation,  # noqa: F401
+                    attn_layer, decode_, forward)
+from . import _lib  # noqa: F401
+
+__version__ = "0.1.0"

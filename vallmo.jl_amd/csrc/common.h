@@ -1,0 +1,88 @@
+// common.h — device-side building blocks shared by the gated-attention kernels
+// (gfx950 / CDNA4 only: wave64, bf16 MFMA 16x16x32 and 32x32x16, LDS transpose
+// reads). Host-side argument checking lives in vallmo_attn.cpp.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s16x4 __attribute__((__vector_size__(4 * sizeof(short))));
+
+// Compile-time facts of the Qwen3.5 attention block (src/llm/qwen35.jl:15-23).
+constexpr int HEAD_DIM = 256;
+constexpr int HALF_ROT = 32;       // rotary dim 64, rotate-half pairs (i, i+32)
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float QK_SCALE = 0.0625f;  // 1/sqrt(256), a power of two: folding it
+                                     // into bf16 q is exact
+
+__device__ __forceinline__ float bf2f(uint16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+// f32 -> bf16 round-to-nearest-even (finite inputs), the rounding the oracle uses.
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// 8 bf16 held as 4 dwords; converts to the MFMA operand type by bit cast.
+struct alignas(16) U4 { uint32_t x, y, z, w; };
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) {
+  return __builtin_bit_cast(bf16x8, v);
+}
+__device__ __forceinline__ uint4 load16(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
+  f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xffff0000u);
+  f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xffff0000u);
+  f[4] = __uint_as_float(v.z << 16); f[5] = __uint_as_float(v.z & 0xffff0000u);
+  f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xffff0000u);
+}
+__device__ __forceinline__ uint4 pack8(const float* f) {
+  uint4 v;
+  v.x = pack2(f[0], f[1]); v.y = pack2(f[2], f[3]);
+  v.z = pack2(f[4], f[5]); v.w = pack2(f[6], f[7]);
+  return v;
+}
+
+// D = A*B + C. 16x16x32: A lane l holds A[l%16][8*(l/16)+j], B lane l holds
+// B[8*(l/16)+j][l%16], D lane l holds D[4*(l/16)+j][l%16].
+__device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+// 32x32x16: A lane l holds A[l%32][8*(l/32)+j], B lane l holds B[8*(l/32)+j][l%32],
+// D lane l holds D[8*(j/4)+4*(l/32)+j%4][l%32].
+__device__ __forceinline__ f32x16 mfma32(const uint4& a, const uint4& b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, output lane i slot r is
+// component i%4 of the 4 halves read by source lane 4r + i/4.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* lds_ptr) {
+  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(lds_ptr));
+  return __builtin_bit_cast(uint2, r);
+}
+
+__device__ __forceinline__ float wave_max_xor(float v, int mask) {
+  return fmaxf(v, __shfl_xor(v, mask, 64));
+}
+__device__ __forceinline__ float wave_sum_all(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+}  // namespace vm

@@ -1,0 +1,96 @@
+// kernels.h — argument blocks and launchers shared between the kernel sources
+// and the C-ABI layer (vallmo_attn.cpp). Strides are in elements.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vm {
+
+constexpr int HEAD_DIM_ABI = 256;     // compiled head_dim
+constexpr int HALF_ROT_ABI = 32;      // compiled rotary half-width
+constexpr int PREFILL_ROWS_ABI = 128; // query rows per prefill workgroup
+
+struct RowArgs {
+  const uint16_t* in;   // first tensor: normed + rotated
+  const uint16_t* in2;  // optional second tensor (V): copied verbatim
+  int64_t in_st, in_sh, in_sb;
+  uint16_t* out;
+  uint16_t* out2;
+  int64_t out_st, out_sh, out_sb;
+  const uint16_t* w;    // per-head norm weight (D,), applied as (w + w_offset)
+  const float* cos_tab;
+  const float* sin_tab;
+  int64_t ctx;          // columns of the tables (and of the cache when appending)
+  const int32_t* positions;  // decode: 1-based column per sequence (T must be 1)
+  const int32_t* prior;      // prefill: tokens already in the cache (nullable)
+  const int32_t* q_lengths;  // prefill: ragged chunk lengths (nullable)
+  int B, H, T;
+  int out_at_pos;       // 1: token index of the output row = position
+  float eps, w_offset;
+};
+
+struct DecodeArgs {
+  const uint16_t* q;    // raw q (fused) or normalised q
+  int64_t q_sh, q_sb;
+  const uint16_t* qw;   // fused prologue only
+  const float* cos_tab;
+  const float* sin_tab;
+  float eps, w_offset;
+  const uint16_t* kc;
+  const uint16_t* vc;
+  int64_t c_st, c_sh, c_sb, ctx;
+  const int32_t* lengths;
+  float* part_o;        // [B][Hk][NS][G][256]
+  float* part_ml;       // [B][Hk][NS][G][2]
+  int B, Hk, G, NS, split;
+};
+
+struct CombineArgs {
+  const float* part_o;
+  const float* part_ml;
+  const int32_t* lengths;
+  uint16_t* out;
+  int64_t o_sh, o_sb;
+  const uint16_t* gate;  // nullable: sigmoid gate logits
+  int64_t g_sh, g_sb;
+  int B, Hk, G, NS, split;
+};
+
+struct PrefillArgs {
+  // q: normalised (QRAW = false) or the raw packed projection (QRAW = true)
+  const uint16_t* q;
+  int64_t q_st, q_sh, q_sb;
+  const uint16_t* qw;
+  const float* cos_tab;
+  const float* sin_tab;
+  float eps, w_offset;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t kv_st, kv_sh, kv_sb;
+  uint16_t* o;
+  int64_t o_st, o_sh, o_sb;
+  const uint16_t* gate;   // GATE only
+  int64_t g_st, g_sh, g_sb;
+  const int32_t* k_lengths;  // nullable -> Lk
+  const int32_t* q_lengths;  // nullable -> L
+  const int32_t* prior;      // fused path: k_len = prior + q_len (nullable -> 0)
+  int B, H, Hk, L, Lk, n_qt, causal;
+};
+
+hipError_t launch_rope_tables(float* c, float* s, int half, int64_t ctx, double theta,
+                              hipStream_t st);
+hipError_t launch_norm_rope_rows(const RowArgs& a, hipStream_t st);
+hipError_t launch_sigmoid_gate(uint16_t* o, int64_t o_sh, int64_t o_sb, const uint16_t* g,
+                               int64_t g_sh, int64_t g_sb, int B, int H, hipStream_t st);
+hipError_t launch_advance(int32_t* positions, int B, hipStream_t st);
+hipError_t launch_fill_normal(uint16_t* dst, int64_t n, uint64_t seed, float scale, float shift,
+                              hipStream_t st);
+hipError_t launch_decode(const DecodeArgs& a, bool fused_q, hipStream_t st);
+hipError_t launch_combine(const CombineArgs& a, hipStream_t st);
+hipError_t launch_prefill(const PrefillArgs& a, bool qraw, bool gate, hipStream_t st);
+
+// Decode split policy shared by the scratch-size query and the launcher.
+constexpr int DECODE_WG_TOKENS = 128;  // 4 waves x 32-token steps
+int decode_split_tokens(int B, int Hk, int64_t ctx, int n_splits);
+
+}  // namespace vm

@@ -1,0 +1,514 @@
+// vallmo_attn.cpp — the C ABI of libvallmo_attn.so (declared in
+// include/vallmo_attn.h). Host code only: argument and shape validation with
+// the reference's error semantics, then kernel launches on the caller's stream.
+//
+// Error convention: < 0 = argument/shape error (message in vm_last_error()),
+// > 0 = hipError_t passed through. Shape errors mirror @sizes
+// (src/sizes.jl:3-22) and the H % Hk check (src/kernels/attention.jl:110-111).
+#include <hip/hip_runtime.h>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+#include "../../include/vallmo_attn.h"
+#include "kernels.h"
+
+namespace {
+
+// ---- optional per-kernel timing (vm_profile_*): hipEvents around each launch
+struct ProfRec {
+  int id;
+  hipEvent_t a, b;
+};
+struct Prof {
+  bool on = false;
+  std::vector<ProfRec> recs;
+  std::vector<hipEvent_t> pool;
+};
+thread_local Prof g_prof;
+
+hipEvent_t prof_event() {
+  if (!g_prof.pool.empty()) {
+    hipEvent_t e = g_prof.pool.back();
+    g_prof.pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Launch through `f`, bracketed by events on `st` when profiling is on and the
+// stream is not being captured into a graph.
+template <class F>
+hipError_t timed(int id, hipStream_t st, F&& f) {
+  if (!g_prof.on) return f();
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return f();
+  hipEvent_t a = prof_event(), b = prof_event();
+  if (!a || !b) return f();
+  (void)hipEventRecord(a, st);
+  hipError_t e = f();
+  (void)hipEventRecord(b, st);
+  g_prof.recs.push_back({id, a, b});
+  return e;
+}
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+int hip_status(hipError_t e, const char* where) {
+  if (e == hipSuccess) return VM_OK;
+  snprintf(g_err, sizeof g_err, "%s: %s", where, hipGetErrorString(e));
+  return (int)e;
+}
+inline hipStream_t S(vm_stream s) { return reinterpret_cast<hipStream_t>(s); }
+
+#define REQUIRE(cond, code, ...) \
+  do {                           \
+    if (!(cond)) return fail(code, __VA_ARGS__); \
+  } while (0)
+
+int check_head(int D, int half_rot) {
+  REQUIRE(D == vm::HEAD_DIM_ABI, VM_E_UNSUPPORTED,
+          "head_dim D = %d is not supported (this build is compiled for D = 256)", D);
+  REQUIRE(half_rot == vm::HALF_ROT_ABI, VM_E_UNSUPPORTED,
+          "HALF_ROT = %d is not supported (this build is compiled for HALF_ROT = 32)", half_rot);
+  return VM_OK;
+}
+int check_gqa(int H, int Hk) {
+  REQUIRE(H > 0 && Hk > 0, VM_E_ARG, "head counts must be positive (H = %d, Hk = %d)", H, Hk);
+  REQUIRE(H % Hk == 0, VM_E_DIM,
+          "Attention heads (%d) is not a multiple of key-value heads (%d)", H, Hk);
+  return VM_OK;
+}
+int check_aligned(const void* p, const char* name) {
+  REQUIRE(p != nullptr, VM_E_ARG, "%s is NULL", name);
+  REQUIRE((reinterpret_cast<uintptr_t>(p) & 15u) == 0, VM_E_ARG,
+          "%s must be 16-byte aligned", name);
+  return VM_OK;
+}
+int check_stride(int64_t s, const char* name) {
+  REQUIRE(s >= 0 && (s % 8) == 0, VM_E_ARG,
+          "stride %s = %lld must be a non-negative multiple of 8 elements", name, (long long)s);
+  return VM_OK;
+}
+#define TRY(x)                 \
+  do {                         \
+    int _rc = (x);             \
+    if (_rc != VM_OK) return _rc; \
+  } while (0)
+
+size_t decode_part_o_bytes(int B, int Hk, int NS, int G) {
+  return (size_t)B * Hk * NS * G * vm::HEAD_DIM_ABI * sizeof(float);
+}
+size_t decode_part_ml_bytes(int B, int Hk, int NS, int G) {
+  return (size_t)B * Hk * NS * G * 2 * sizeof(float);
+}
+int decode_ns(int64_t ctx, int split) { return (int)((ctx + split - 1) / split); }
+
+}  // namespace
+
+extern "C" {
+
+const char* vm_last_error(void) { return g_err; }
+int vm_abi_version(void) { return 1; }
+
+// ---- kernel timing ----------------------------------------------------------
+int vm_profile_enable(int on) {
+  for (auto& r : g_prof.recs) {
+    g_prof.pool.push_back(r.a);
+    g_prof.pool.push_back(r.b);
+  }
+  g_prof.recs.clear();
+  g_prof.on = on != 0;
+  return VM_OK;
+}
+int vm_profile_read(int kernel, int* count, double* total_ms) {
+  REQUIRE(count && total_ms, VM_E_ARG, "vm_profile_read: NULL output");
+  REQUIRE(kernel >= 0 && kernel < VM_K_COUNT, VM_E_ARG, "vm_profile_read: kernel id %d", kernel);
+  int n = 0;
+  double t = 0.0;
+  for (auto& r : g_prof.recs) {
+    if (r.id != kernel) continue;
+    int rc = hip_status(hipEventSynchronize(r.b), "hipEventSynchronize");
+    if (rc) return rc;
+    float ms = 0.f;
+    rc = hip_status(hipEventElapsedTime(&ms, r.a, r.b), "hipEventElapsedTime");
+    if (rc) return rc;
+    ++n;
+    t += ms;
+  }
+  *count = n;
+  *total_ms = t;
+  return VM_OK;
+}
+
+// ---- runtime --------------------------------------------------------------
+int vm_malloc(void** ptr, size_t bytes) {
+  REQUIRE(ptr, VM_E_ARG, "vm_malloc: ptr is NULL");
+  return hip_status(hipMalloc(ptr, bytes), "hipMalloc");
+}
+int vm_free(void* ptr) { return hip_status(hipFree(ptr), "hipFree"); }
+int vm_memcpy_h2d(void* dst, const void* src, size_t n, vm_stream s) {
+  return hip_status(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, S(s)), "hipMemcpyAsync");
+}
+int vm_memcpy_d2h(void* dst, const void* src, size_t n, vm_stream s) {
+  return hip_status(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, S(s)), "hipMemcpyAsync");
+}
+int vm_memcpy_d2d(void* dst, const void* src, size_t n, vm_stream s) {
+  return hip_status(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, S(s)), "hipMemcpyAsync");
+}
+int vm_memset(void* dst, int v, size_t n, vm_stream s) {
+  return hip_status(hipMemsetAsync(dst, v, n, S(s)), "hipMemsetAsync");
+}
+int vm_stream_create(vm_stream* s) {
+  REQUIRE(s, VM_E_ARG, "vm_stream_create: out pointer is NULL");
+  hipStream_t st;
+  int rc = hip_status(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreate");
+  *s = rc == VM_OK ? (vm_stream)st : nullptr;
+  return rc;
+}
+int vm_stream_destroy(vm_stream s) { return hip_status(hipStreamDestroy(S(s)), "hipStreamDestroy"); }
+int vm_stream_sync(vm_stream s) { return hip_status(hipStreamSynchronize(S(s)), "hipStreamSynchronize"); }
+int vm_device_sync(void) { return hip_status(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
+int vm_event_create(void** e) {
+  REQUIRE(e, VM_E_ARG, "vm_event_create: out pointer is NULL");
+  hipEvent_t ev;
+  int rc = hip_status(hipEventCreate(&ev), "hipEventCreate");
+  *e = rc == VM_OK ? (void*)ev : nullptr;
+  return rc;
+}
+int vm_event_destroy(void* e) { return hip_status(hipEventDestroy((hipEvent_t)e), "hipEventDestroy"); }
+int vm_event_record(void* e, vm_stream s) {
+  return hip_status(hipEventRecord((hipEvent_t)e, S(s)), "hipEventRecord");
+}
+int vm_event_elapsed_ms(float* ms, void* a, void* b) {
+  REQUIRE(ms, VM_E_ARG, "vm_event_elapsed_ms: out pointer is NULL");
+  return hip_status(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b), "hipEventElapsedTime");
+}
+int vm_graph_begin_capture(vm_stream s) {
+  REQUIRE(s, VM_E_ARG, "graph capture needs a non-default stream");
+  return hip_status(hipStreamBeginCapture(S(s), hipStreamCaptureModeThreadLocal),
+                    "hipStreamBeginCapture");
+}
+int vm_graph_end_capture(vm_stream s, void** exec) {
+  REQUIRE(exec, VM_E_ARG, "vm_graph_end_capture: out pointer is NULL");
+  hipGraph_t g = nullptr;
+  int rc = hip_status(hipStreamEndCapture(S(s), &g), "hipStreamEndCapture");
+  if (rc != VM_OK) return rc;
+  hipGraphExec_t ge = nullptr;
+  rc = hip_status(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+  (void)hipGraphDestroy(g);
+  *exec = rc == VM_OK ? (void*)ge : nullptr;
+  return rc;
+}
+int vm_graph_launch(void* exec, vm_stream s) {
+  REQUIRE(exec, VM_E_ARG, "vm_graph_launch: graph is NULL");
+  return hip_status(hipGraphLaunch((hipGraphExec_t)exec, S(s)), "hipGraphLaunch");
+}
+int vm_graph_destroy(void* exec) {
+  return hip_status(hipGraphExecDestroy((hipGraphExec_t)exec), "hipGraphExecDestroy");
+}
+
+// ---- a1 -------------------------------------------------------------------
+int vm_rope_tables(float* c, float* s, int half_rot, int64_t ctx, double theta, vm_stream st) {
+  REQUIRE(c && s, VM_E_ARG, "rope_tables: NULL table pointer");
+  REQUIRE(half_rot > 0 && ctx >= 0, VM_E_ARG, "rope_tables: half_rot = %d, Ctx = %lld", half_rot,
+          (long long)ctx);
+  REQUIRE(theta > 0, VM_E_ARG, "rope_tables: theta must be positive");
+  return hip_status(vm::launch_rope_tables(c, s, half_rot, ctx, theta, S(st)), "rope_tables");
+}
+
+// ---- a3 -------------------------------------------------------------------
+int vm_qnorm_rope(vm_bf16* q, int64_t q_sh, int64_t q_sb, const vm_bf16* qw, const float* cs,
+                  const float* sn, int64_t ctx, const int32_t* positions, int B, int Hq, int D,
+                  int half_rot, float eps, float w_offset, vm_stream st) {
+  TRY(check_head(D, half_rot));
+  REQUIRE(B >= 0 && Hq > 0 && ctx > 0, VM_E_ARG, "qnorm_rope: B = %d, Hq = %d, Ctx = %lld", B, Hq,
+          (long long)ctx);
+  REQUIRE(q && qw && cs && sn && positions, VM_E_ARG, "qnorm_rope: NULL pointer argument");
+  TRY(check_stride(q_sh, "q_sh"));
+  TRY(check_stride(q_sb, "q_sb"));
+  vm::RowArgs a{};
+  a.in = q; a.out = q; a.in_sh = a.out_sh = q_sh; a.in_sb = a.out_sb = q_sb;
+  a.w = qw; a.cos_tab = cs; a.sin_tab = sn; a.ctx = ctx; a.positions = positions;
+  a.B = B; a.H = Hq; a.T = 1; a.out_at_pos = 0; a.eps = eps; a.w_offset = w_offset;
+  return hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_norm_rope_rows(a, S(st)); }), "qnorm_rope");
+}
+
+// ---- a4 -------------------------------------------------------------------
+int vm_knorm_rope_append(vm_bf16* kc, vm_bf16* vc, int64_t c_st, int64_t c_sh, int64_t c_sb,
+                         int64_t ctx, const vm_bf16* k_raw, const vm_bf16* v_raw, int64_t r_sh,
+                         int64_t r_sb, const vm_bf16* kw, const float* cs, const float* sn,
+                         const int32_t* positions, int B, int Hk, int D, int half_rot, float eps,
+                         float w_offset, vm_stream st) {
+  TRY(check_head(D, half_rot));
+  REQUIRE(B >= 0 && Hk > 0 && ctx > 0, VM_E_ARG, "knorm_rope_append: B = %d, Hk = %d, Ctx = %lld",
+          B, Hk, (long long)ctx);
+  REQUIRE(kc && vc && k_raw && v_raw && kw && cs && sn && positions, VM_E_ARG,
+          "knorm_rope_append: NULL pointer argument");
+  TRY(check_stride(c_st, "c_st"));
+  TRY(check_stride(c_sh, "c_sh"));
+  TRY(check_stride(c_sb, "c_sb"));
+  TRY(check_stride(r_sh, "r_sh"));
+  TRY(check_stride(r_sb, "r_sb"));
+  vm::RowArgs a{};
+  a.in = k_raw; a.in2 = v_raw; a.in_sh = r_sh; a.in_sb = r_sb;
+  a.out = kc; a.out2 = vc; a.out_st = c_st; a.out_sh = c_sh; a.out_sb = c_sb;
+  a.w = kw; a.cos_tab = cs; a.sin_tab = sn; a.ctx = ctx; a.positions = positions;
+  a.B = B; a.H = Hk; a.T = 1; a.out_at_pos = 1; a.eps = eps; a.w_offset = w_offset;
+  return hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_norm_rope_rows(a, S(st)); }), "knorm_rope_append");
+}
+
+// ---- a5 -------------------------------------------------------------------
+size_t vm_decode_scratch_bytes(int B, int H, int Hk, int D, int64_t ctx, int n_splits) {
+  if (B <= 0 || H <= 0 || Hk <= 0 || H % Hk || D != vm::HEAD_DIM_ABI || ctx <= 0) return 0;
+  const int split = vm::decode_split_tokens(B, Hk, ctx, n_splits);
+  const int NS = decode_ns(ctx, split);
+  const int G = H / Hk;
+  return decode_part_o_bytes(B, Hk, NS, G) + decode_part_ml_bytes(B, Hk, NS, G);
+}
+
+static int decode_common(vm::DecodeArgs& a, vm::CombineArgs& c, void* scratch, size_t scratch_bytes,
+                         int B, int H, int Hk, int64_t ctx, int n_splits) {
+  TRY(check_gqa(H, Hk));
+  const int G = H / Hk;
+  REQUIRE(G <= 8, VM_E_UNSUPPORTED, "decode: GQA group %d > 8 is not supported", G);
+  REQUIRE(n_splits >= 0, VM_E_ARG, "decode: n_splits = %d", n_splits);
+  REQUIRE(ctx > 0 && ctx < (int64_t)1 << 31, VM_E_ARG, "decode: Ctx = %lld", (long long)ctx);
+  const int split = vm::decode_split_tokens(B, Hk, ctx, n_splits);
+  const int NS = decode_ns(ctx, split);
+  const size_t need = decode_part_o_bytes(B, Hk, NS, G) + decode_part_ml_bytes(B, Hk, NS, G);
+  REQUIRE(scratch != nullptr && scratch_bytes >= need, VM_E_SCRATCH,
+          "decode: scratch of %zu bytes < %zu required (vm_decode_scratch_bytes)", scratch_bytes,
+          need);
+  TRY(check_aligned(scratch, "scratch"));
+  a.part_o = reinterpret_cast<float*>(scratch);
+  a.part_ml = reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) +
+                                       decode_part_o_bytes(B, Hk, NS, G));
+  a.B = B; a.Hk = Hk; a.G = G; a.NS = NS; a.split = split; a.ctx = ctx;
+  c.part_o = a.part_o; c.part_ml = a.part_ml;
+  c.B = B; c.Hk = Hk; c.G = G; c.NS = NS; c.split = split;
+  return VM_OK;
+}
+
+int vm_decode_attention(vm_bf16* o, int64_t o_sh, int64_t o_sb, const vm_bf16* q, int64_t q_sh,
+                        int64_t q_sb, const vm_bf16* kc, const vm_bf16* vc, int64_t c_st,
+                        int64_t c_sh, int64_t c_sb, int64_t ctx, const int32_t* lengths, int B,
+                        int H, int Hk, int D, int n_splits, void* scratch, size_t scratch_bytes,
+                        vm_stream st) {
+  REQUIRE(D == vm::HEAD_DIM_ABI, VM_E_UNSUPPORTED,
+          "head_dim D = %d is not supported (this build is compiled for D = 256)", D);
+  REQUIRE(B >= 0, VM_E_ARG, "decode_attention: B = %d", B);
+  REQUIRE(o && lengths, VM_E_ARG, "decode_attention: NULL pointer argument");
+  TRY(check_aligned(q, "Q"));
+  TRY(check_aligned(kc, "K"));
+  TRY(check_aligned(vc, "V"));
+  for (int64_t s : {o_sh, o_sb, q_sh, q_sb, c_st, c_sh, c_sb}) TRY(check_stride(s, "decode"));
+  vm::DecodeArgs a{};
+  vm::CombineArgs c{};
+  TRY(decode_common(a, c, scratch, scratch_bytes, B, H, Hk, ctx, n_splits));
+  if (B == 0) return VM_OK;
+  a.q = q; a.q_sh = q_sh; a.q_sb = q_sb;
+  a.kc = kc; a.vc = vc; a.c_st = c_st; a.c_sh = c_sh; a.c_sb = c_sb;
+  a.lengths = lengths;
+  int rc = hip_status(timed(VM_K_DECODE_SPLIT, S(st), [&] { return vm::launch_decode(a, false, S(st)); }), "decode_attention split");
+  if (rc) return rc;
+  c.lengths = lengths; c.out = o; c.o_sh = o_sh; c.o_sb = o_sb; c.gate = nullptr;
+  return hip_status(timed(VM_K_DECODE_COMBINE, S(st), [&] { return vm::launch_combine(c, S(st)); }), "decode_attention combine");
+}
+
+// ---- a6 -------------------------------------------------------------------
+int vm_sigmoid_gate(vm_bf16* o, int64_t o_sh, int64_t o_sb, const vm_bf16* g, int64_t g_sh,
+                    int64_t g_sb, int B, int H, int D, vm_stream st) {
+  REQUIRE(D == vm::HEAD_DIM_ABI, VM_E_UNSUPPORTED, "sigmoid_gate: D = %d (need 256)", D);
+  REQUIRE(B >= 0 && H >= 0, VM_E_ARG, "sigmoid_gate: B = %d, H = %d", B, H);
+  TRY(check_aligned(o, "O"));
+  TRY(check_aligned(g, "gate"));
+  for (int64_t s : {o_sh, o_sb, g_sh, g_sb}) TRY(check_stride(s, "gate"));
+  return hip_status(vm::launch_sigmoid_gate(o, o_sh, o_sb, g, g_sh, g_sb, B, H, S(st)),
+                    "sigmoid_gate");
+}
+
+// ---- a7 -------------------------------------------------------------------
+int vm_gated_attn_decode(vm_bf16* out, int64_t out_sb, const vm_bf16* qkv, int64_t qkv_sb,
+                         vm_bf16* kc, vm_bf16* vc, int64_t c_st, int64_t c_sh, int64_t c_sb,
+                         int64_t ctx, const vm_bf16* qw, const vm_bf16* kw, const float* cs,
+                         const float* sn, int32_t* positions, int advance, int B, int Hq, int Hk,
+                         int D, int half_rot, float eps, float w_offset, int n_splits,
+                         void* scratch, size_t scratch_bytes, vm_stream st) {
+  TRY(check_head(D, half_rot));
+  REQUIRE(B >= 0, VM_E_ARG, "gated_attn_decode: B = %d", B);
+  REQUIRE(out && qw && kw && cs && sn && positions, VM_E_ARG,
+          "gated_attn_decode: NULL pointer argument");
+  TRY(check_aligned(qkv, "qkv"));
+  TRY(check_aligned(kc, "K_cache"));
+  TRY(check_aligned(vc, "V_cache"));
+  TRY(check_aligned(qw, "qw"));
+  for (int64_t s : {out_sb, qkv_sb, c_st, c_sh, c_sb}) TRY(check_stride(s, "gated_attn_decode"));
+  REQUIRE(qkv_sb >= (int64_t)(2 * Hq + 2 * Hk) * D || B <= 1, VM_E_DIM,
+          "gated_attn_decode: qkv batch stride %lld < (2Hq+2Hk)*D = %lld", (long long)qkv_sb,
+          (long long)(2 * Hq + 2 * Hk) * D);
+  vm::DecodeArgs a{};
+  vm::CombineArgs c{};
+  TRY(decode_common(a, c, scratch, scratch_bytes, B, Hq, Hk, ctx, n_splits));
+  if (B == 0) return VM_OK;
+  const int64_t Dl = D;
+  // a4: K/V of the new token into the cache (the split kernel then reads it)
+  vm::RowArgs r{};
+  r.in = qkv + 2 * Hq * Dl; r.in2 = qkv + (2 * Hq + Hk) * Dl; r.in_sh = Dl; r.in_sb = qkv_sb;
+  r.out = kc; r.out2 = vc; r.out_st = c_st; r.out_sh = c_sh; r.out_sb = c_sb;
+  r.w = kw; r.cos_tab = cs; r.sin_tab = sn; r.ctx = ctx; r.positions = positions;
+  r.B = B; r.H = Hk; r.T = 1; r.out_at_pos = 1; r.eps = eps; r.w_offset = w_offset;
+  int rc = hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_norm_rope_rows(r, S(st)); }), "gated_attn_decode append");
+  if (rc) return rc;
+  // a3 + a5: split-KV attention with the q norm+RoPE prologue fused
+  a.q = qkv; a.q_sh = 2 * Dl; a.q_sb = qkv_sb;
+  a.qw = qw; a.cos_tab = cs; a.sin_tab = sn; a.eps = eps; a.w_offset = w_offset;
+  a.kc = kc; a.vc = vc; a.c_st = c_st; a.c_sh = c_sh; a.c_sb = c_sb;
+  a.lengths = positions;
+  rc = hip_status(timed(VM_K_DECODE_SPLIT, S(st), [&] { return vm::launch_decode(a, true, S(st)); }), "gated_attn_decode split");
+  if (rc) return rc;
+  // a5 merge + a6 gate, written as the Wo input (D, Hq, B)
+  c.lengths = positions; c.out = out; c.o_sh = Dl; c.o_sb = out_sb;
+  c.gate = qkv + Dl; c.g_sh = 2 * Dl; c.g_sb = qkv_sb;
+  rc = hip_status(timed(VM_K_DECODE_COMBINE, S(st), [&] { return vm::launch_combine(c, S(st)); }), "gated_attn_decode combine");
+  if (rc || !advance) return rc;
+  return hip_status(timed(VM_K_ADVANCE, S(st), [&] { return vm::launch_advance(positions, B, S(st)); }), "advance");
+}
+
+int vm_advance_positions(int32_t* positions, int B, vm_stream st) {
+  REQUIRE(positions || B == 0, VM_E_ARG, "advance_positions: NULL positions");
+  REQUIRE(B >= 0, VM_E_ARG, "advance_positions: B = %d", B);
+  return hip_status(vm::launch_advance(positions, B, S(st)), "advance");
+}
+
+// ---- a8 -------------------------------------------------------------------
+int vm_attention_fwd(vm_bf16* o, int64_t o_st, int64_t o_sh, int64_t o_sb, const vm_bf16* q,
+                     int64_t q_st, int64_t q_sh, int64_t q_sb, const vm_bf16* k, const vm_bf16* v,
+                     int64_t kv_st, int64_t kv_sh, int64_t kv_sb, const int32_t* k_lengths,
+                     const int32_t* q_lengths, int B, int H, int Hk, int D, int L, int Lk,
+                     int causal, vm_stream st) {
+  REQUIRE(D == vm::HEAD_DIM_ABI, VM_E_UNSUPPORTED,
+          "head_dim D = %d is not supported (this build is compiled for D = 256)", D);
+  TRY(check_gqa(H, Hk));
+  REQUIRE(B >= 0 && L >= 0 && Lk >= 0, VM_E_ARG, "attention: B = %d, L = %d, Lk = %d", B, L, Lk);
+  TRY(check_aligned(o, "O"));
+  TRY(check_aligned(q, "Q"));
+  TRY(check_aligned(k, "K"));
+  TRY(check_aligned(v, "V"));
+  for (int64_t s : {o_st, o_sh, o_sb, q_st, q_sh, q_sb, kv_st, kv_sh, kv_sb})
+    TRY(check_stride(s, "attention"));
+  if (B == 0 || L == 0) return VM_OK;
+  REQUIRE(Lk > 0, VM_E_ARG, "attention: k_len must be >= 1 (Lk = 0)");
+  vm::PrefillArgs a{};
+  a.q = q; a.q_st = q_st; a.q_sh = q_sh; a.q_sb = q_sb;
+  a.k = k; a.v = v; a.kv_st = kv_st; a.kv_sh = kv_sh; a.kv_sb = kv_sb;
+  a.o = o; a.o_st = o_st; a.o_sh = o_sh; a.o_sb = o_sb;
+  a.k_lengths = k_lengths; a.q_lengths = q_lengths; a.prior = nullptr;
+  a.B = B; a.H = H; a.Hk = Hk; a.L = L; a.Lk = Lk; a.causal = causal ? 1 : 0;
+  a.n_qt = (L + vm::PREFILL_ROWS_ABI - 1) / vm::PREFILL_ROWS_ABI;
+  return hip_status(timed(VM_K_PREFILL, S(st), [&] { return vm::launch_prefill(a, false, false, S(st)); }), "attention");
+}
+
+// ---- a9 -------------------------------------------------------------------
+static int prefill_row_common(int B, int T, int Hq, int Hk, int D, int half_rot, int64_t ctx,
+                              const void* qkv, int64_t qkv_st, int64_t qkv_sb) {
+  TRY(check_head(D, half_rot));
+  TRY(check_gqa(Hq, Hk));
+  REQUIRE(B >= 0 && T >= 0 && ctx > 0, VM_E_ARG, "prefill: B = %d, T = %d, Ctx = %lld", B, T,
+          (long long)ctx);
+  TRY(check_aligned(qkv, "qkv"));
+  TRY(check_stride(qkv_st, "qkv_st"));
+  TRY(check_stride(qkv_sb, "qkv_sb"));
+  REQUIRE(qkv_st >= (int64_t)(2 * Hq + 2 * Hk) * D || T <= 1, VM_E_DIM,
+          "prefill: qkv token stride %lld < (2Hq+2Hk)*D = %lld", (long long)qkv_st,
+          (long long)(2 * Hq + 2 * Hk) * D);
+  return VM_OK;
+}
+
+int vm_prefill_kv_append(vm_bf16* kc, vm_bf16* vc, int64_t c_st, int64_t c_sh, int64_t c_sb,
+                         int64_t ctx, const vm_bf16* qkv, int64_t qkv_st, int64_t qkv_sb,
+                         const vm_bf16* kw, const float* cs, const float* sn, const int32_t* prior,
+                         const int32_t* q_lengths, int B, int T, int Hq, int Hk, int D,
+                         int half_rot, float eps, float w_offset, vm_stream st) {
+  TRY(prefill_row_common(B, T, Hq, Hk, D, half_rot, ctx, qkv, qkv_st, qkv_sb));
+  REQUIRE(kc && vc && kw && cs && sn, VM_E_ARG, "prefill_kv_append: NULL pointer argument");
+  for (int64_t s : {c_st, c_sh, c_sb}) TRY(check_stride(s, "cache"));
+  const int64_t Dl = D;
+  vm::RowArgs r{};
+  r.in = qkv + 2 * Hq * Dl; r.in2 = qkv + (2 * Hq + Hk) * Dl;
+  r.in_st = qkv_st; r.in_sh = Dl; r.in_sb = qkv_sb;
+  r.out = kc; r.out2 = vc; r.out_st = c_st; r.out_sh = c_sh; r.out_sb = c_sb;
+  r.w = kw; r.cos_tab = cs; r.sin_tab = sn; r.ctx = ctx; r.positions = nullptr;
+  r.prior = prior; r.q_lengths = q_lengths;
+  r.B = B; r.H = Hk; r.T = T; r.out_at_pos = 1; r.eps = eps; r.w_offset = w_offset;
+  return hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_norm_rope_rows(r, S(st)); }), "prefill_kv_append");
+}
+
+int vm_prefill_q_norm_rope(vm_bf16* q_out, int64_t q_st, int64_t q_sh, int64_t q_sb,
+                           const vm_bf16* qkv, int64_t qkv_st, int64_t qkv_sb, const vm_bf16* qw,
+                           const float* cs, const float* sn, const int32_t* prior,
+                           const int32_t* q_lengths, int B, int T, int Hq, int Hk, int D,
+                           int half_rot, float eps, float w_offset, vm_stream st) {
+  // ctx is not known here: positions prior[b]+t must lie inside the tables (caller's contract)
+  TRY(prefill_row_common(B, T, Hq, Hk, D, half_rot, INT64_MAX, qkv, qkv_st, qkv_sb));
+  REQUIRE(q_out && qw && cs && sn, VM_E_ARG, "prefill_q_norm_rope: NULL pointer argument");
+  for (int64_t s : {q_st, q_sh, q_sb}) TRY(check_stride(s, "q_out"));
+  const int64_t Dl = D;
+  vm::RowArgs r{};
+  r.in = qkv; r.in2 = nullptr; r.in_st = qkv_st; r.in_sh = 2 * Dl; r.in_sb = qkv_sb;
+  r.out = q_out; r.out_st = q_st; r.out_sh = q_sh; r.out_sb = q_sb;
+  r.w = qw; r.cos_tab = cs; r.sin_tab = sn; r.ctx = INT64_MAX; r.positions = nullptr;
+  r.prior = prior; r.q_lengths = q_lengths;
+  r.B = B; r.H = Hq; r.T = T; r.out_at_pos = 0; r.eps = eps; r.w_offset = w_offset;
+  return hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_norm_rope_rows(r, S(st)); }), "prefill_q_norm_rope");
+}
+
+// ---- a11 ------------------------------------------------------------------
+int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm_bf16* qkv,
+                          int64_t qkv_st, int64_t qkv_sb, vm_bf16* kc, vm_bf16* vc, int64_t c_st,
+                          int64_t c_sh, int64_t c_sb, int64_t ctx, const vm_bf16* qw,
+                          const vm_bf16* kw, const float* cs, const float* sn,
+                          const int32_t* prior, const int32_t* q_lengths, int B, int T, int Hq,
+                          int Hk, int D, int half_rot, float eps, float w_offset, vm_stream st) {
+  TRY(vm_prefill_kv_append(kc, vc, c_st, c_sh, c_sb, ctx, qkv, qkv_st, qkv_sb, kw, cs, sn, prior,
+                           q_lengths, B, T, Hq, Hk, D, half_rot, eps, w_offset, st));
+  REQUIRE(out && qw, VM_E_ARG, "gated_attn_prefill: NULL pointer argument");
+  TRY(check_aligned(out, "out"));
+  TRY(check_aligned(qw, "qw"));
+  TRY(check_aligned(kc, "K_cache"));
+  TRY(check_aligned(vc, "V_cache"));
+  TRY(check_stride(out_st, "out_st"));
+  TRY(check_stride(out_sb, "out_sb"));
+  if (B == 0 || T == 0) return VM_OK;
+  REQUIRE(ctx < (int64_t)1 << 31, VM_E_ARG, "gated_attn_prefill: Ctx too large");
+  const int64_t Dl = D;
+  vm::PrefillArgs a{};
+  a.q = qkv; a.q_st = qkv_st; a.q_sh = 2 * Dl; a.q_sb = qkv_sb;
+  a.qw = qw; a.cos_tab = cs; a.sin_tab = sn; a.eps = eps; a.w_offset = w_offset;
+  a.k = kc; a.v = vc; a.kv_st = c_st; a.kv_sh = c_sh; a.kv_sb = c_sb;
+  a.o = out; a.o_st = out_st; a.o_sh = Dl; a.o_sb = out_sb;
+  a.gate = qkv + Dl; a.g_st = qkv_st; a.g_sh = 2 * Dl; a.g_sb = qkv_sb;
+  a.k_lengths = nullptr; a.q_lengths = q_lengths; a.prior = prior;
+  a.B = B; a.H = Hq; a.Hk = Hk; a.L = T; a.Lk = (int)ctx; a.causal = 1;
+  a.n_qt = (T + vm::PREFILL_ROWS_ABI - 1) / vm::PREFILL_ROWS_ABI;
+  return hip_status(timed(VM_K_PREFILL, S(st), [&] { return vm::launch_prefill(a, true, true, S(st)); }), "gated_attn_prefill");
+}
+
+// ---- synthetic inputs ------------------------------------------------------
+int vm_fill_normal_bf16(vm_bf16* dst, int64_t n, uint64_t seed, float scale, float shift,
+                        vm_stream st) {
+  REQUIRE(dst || n == 0, VM_E_ARG, "fill_normal: NULL destination");
+  REQUIRE(n >= 0, VM_E_ARG, "fill_normal: n = %lld", (long long)n);
+  return hip_status(vm::launch_fill_normal(dst, n, seed, scale, shift, S(st)), "fill_normal");
+}
+
+}  // extern "C"

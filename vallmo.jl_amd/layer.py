@@ -1,0 +1,199 @@
+"""Attention-layer verbs and the decode clock — src/llm/qwen35.jl and generate.jl.
+
+The reference's ``decode!(h, l::AttnLayer, m, gen, xn)`` and
+``forward(l::AttnLayer, m, xn, T, B; offset)`` bracket the attention block
+between the qkv projection and the Wo projection (cuBLASLt GEMMs, outside this
+path). Here the verbs start from the packed projection ``qkv`` and end at the
+Wo input, which is exactly the part that runs on the gated-attention kernels:
+
+    decode_(O, l, m, gen, qkv)           qwen35.jl:195-205 (after the qkv GEMV,
+                                         before the Wo GEMV)
+    forward(l, m, qkv, T, B; offset)     qwen35.jl:293-317 (after the qkv GEMM,
+                                         returns the (Dh*Hq, T*B) Wo input)
+
+Packed projection slots per token (qwen35.jl:189-192): [q1 g1 q2 g2 .. qHq gHq |
+k1..kHkv | v1..vHkv], each Dh wide. The KV cache layout (Dh, Ctx, Hkv, B) of
+qwen35.jl:138-139 is kept: it is the on-device format shared by prefill and decode.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+from ._lib import ArgumentError, call
+from .sizes import sizes
+
+
+@dataclass(frozen=True)
+class AttnConfig:
+    """The attention facts of a Qwen3.5 text config (qwen35.jl:82-96)."""
+    Hq: int = 16
+    Hkv: int = 4
+    Dh: int = 256
+    rot_half: int = 32          # head_dim * partial_rotary_factor / 2
+    theta: float = 1.0e7
+    eps: float = 1.0e-6
+    Ctx: int = 4096
+    B: int = 1
+
+
+@dataclass
+class AttnLayer:
+    """qwen35.jl:129-142: norm weights and the layer's own KV cache."""
+    qw: torch.Tensor            # (Dh,) bf16, applied as (w + 1)
+    kw: torch.Tensor            # (Dh,) bf16
+    K_cache: torch.Tensor       # (Dh, Ctx, Hkv, B) -> torch (B, Hkv, Ctx, Dh) bf16
+    V_cache: torch.Tensor
+
+
+def attn_layer(cfg: AttnConfig, qw: torch.Tensor, kw: torch.Tensor) -> AttnLayer:
+    """Allocate a layer with zeroed caches (qwen35.jl:138-139)."""
+    shape = (cfg.B, cfg.Hkv, cfg.Ctx, cfg.Dh)
+    return AttnLayer(qw=qw, kw=kw,
+                     K_cache=torch.zeros(shape, dtype=torch.bfloat16, device="cuda"),
+                     V_cache=torch.zeros(shape, dtype=torch.bfloat16, device="cuda"))
+
+
+class AttnModel:
+    """The model-level state the attention verbs read: cfg, RoPE tables and the
+    decode scratch space (the reference's Arena, qwen35.jl:110) sized once so a
+    captured step replays the same addresses."""
+
+    def __init__(self, cfg: AttnConfig, *, n_splits: int = 0):
+        self.cfg = cfg
+        self.rope = ops.rope_tables(cfg)
+        self.n_splits = int(n_splits)
+        nbytes = int(ops._lib.load().vm_decode_scratch_bytes(
+            cfg.B, cfg.Hq, cfg.Hkv, cfg.Dh, cfg.Ctx, self.n_splits))
+        self.space = torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda")
+
+
+class Generation:
+    """The device clock (generate.jl:54-72): positions[b] is the 1-based column
+    of the current token = rope column = cache column = attended length."""
+
+    def __init__(self, B: int):
+        self.positions = torch.zeros((B,), dtype=torch.int32, device="cuda")
+
+    def advance_(self):
+        """positions .+= 1 on the device (generate.jl:82-88)."""
+        call("vm_advance_positions", ops._p(self.positions), self.positions.numel(),
+             ops._stream())
+        return self
+
+
+def _qkv_views(qkv, cfg):
+    """q, gate, k, v views of a packed (B, 2Hq+2Hkv, Dh) projection (qwen35.jl:195-198)."""
+    q = qkv[:, 0:2 * cfg.Hq:2, :]
+    g = qkv[:, 1:2 * cfg.Hq:2, :]
+    k = qkv[:, 2 * cfg.Hq:2 * cfg.Hq + cfg.Hkv, :]
+    v = qkv[:, 2 * cfg.Hq + cfg.Hkv:, :]
+    return q, g, k, v
+
+
+def decode_(O, l: AttnLayer, m: AttnModel, gen: Generation, qkv, *, advance: bool = False):
+    """One decode step of the attention block (qwen35.jl:195-205), fused:
+    qnorm_rope! + knorm_rope_append! + decode_attention + ``O .*= sigmoid.(q_gate)``.
+
+    qkv :: (Dh, 2Hq+2Hkv, B) packed projection; O :: (Dh, Hq, B) = the Wo input.
+    Reads gen.positions; with ``advance`` also bumps it on the device (so one
+    call is a capturable (step!; advance!)). Allocates nothing.
+    """
+    cfg = m.cfg
+    d = sizes(qkv=(qkv, f"Dh {2 * cfg.Hq + 2 * cfg.Hkv} B"), O=(O, f"Dh {cfg.Hq} B"),
+              K_cache=(l.K_cache, "Dh Ctx Hkv B"), V_cache=(l.V_cache, "Dh Ctx Hkv B"),
+              positions=(gen.positions, "B"))
+    if qkv.stride(1) != d["Dh"] or O.stride(1) != d["Dh"]:
+        raise ArgumentError("qkv and O must be packed along the head axis")
+    if l.K_cache.stride() != l.V_cache.stride():
+        raise ArgumentError("K_cache and V_cache must share strides")
+    c = l.K_cache
+    call("vm_gated_attn_decode", ops._p(O), O.stride(0), ops._p(qkv), qkv.stride(0),
+         ops._p(l.K_cache), ops._p(l.V_cache), c.stride(2), c.stride(1), c.stride(0), d["Ctx"],
+         ops._p(l.qw), ops._p(l.kw), ops._p(m.rope["cos"]), ops._p(m.rope["sin"]),
+         ops._p(gen.positions), int(bool(advance)), d["B"], cfg.Hq, cfg.Hkv, d["Dh"],
+         cfg.rot_half, float(cfg.eps), 1.0, m.n_splits, ops._p(m.space), m.space.numel(),
+         ops._stream())
+    return O
+
+
+def forward(l: AttnLayer, m: AttnModel, qkv, T: int, B: int, *, offset: int = 0,
+            prior=None, q_lengths=None, out=None):
+    """Prefill / chunked prefill of the attention block (qwen35.jl:293-317), fused:
+    head_rmsnorm + apply_rope of q and k, the K/V cache write at columns
+    offset+1..offset+T, causal attention over columns 1..offset+T, and the
+    sigmoid gate, written directly in the Wo input layout (Dh*Hq, T*B).
+
+    qkv :: (Dh*(2Hq+2Hkv), T*B) (any view reshapeable to torch (B, T, 2Hq+2Hkv, Dh)).
+    ``offset`` is the uniform prior cache length (the reference's keyword);
+    ``prior``/``q_lengths`` (B,) int32 device tensors make the batch ragged
+    (each sequence b appends q_lengths[b] <= T tokens after prior[b]).
+    Returns out :: torch (B, T, Hq*Dh).
+    """
+    cfg = m.cfg
+    S = 2 * cfg.Hq + 2 * cfg.Hkv
+    qkv4 = qkv.reshape(B, T, S, cfg.Dh)
+    if qkv4.stride(3) != 1 or qkv4.stride(2) != cfg.Dh:
+        raise ArgumentError("qkv must be packed along the slot axis")
+    if prior is None:
+        prior = torch.full((B,), int(offset), dtype=torch.int32, device="cuda")
+    d = sizes(K_cache=(l.K_cache, "Dh Ctx Hkv B"), prior=(prior, "B"),
+              q_lengths=(q_lengths, "B"))
+    if d["B"] != B:
+        raise ArgumentError(f"cache batch {d['B']} != B = {B}")
+    if out is None:
+        out = torch.empty((B, T, cfg.Hq * cfg.Dh), dtype=torch.bfloat16, device="cuda")
+    c = l.K_cache
+    call("vm_gated_attn_prefill", ops._p(out), out.stride(1), out.stride(0), ops._p(qkv4),
+         qkv4.stride(1), qkv4.stride(0), ops._p(l.K_cache), ops._p(l.V_cache), c.stride(2),
+         c.stride(1), c.stride(0), d["Ctx"], ops._p(l.qw), ops._p(l.kw), ops._p(m.rope["cos"]),
+         ops._p(m.rope["sin"]), ops._p(prior), ops._p(q_lengths), B, T, cfg.Hq, cfg.Hkv, cfg.Dh,
+         cfg.rot_half, float(cfg.eps), 1.0, ops._stream())
+    return out
+
+
+class CaptureSession:
+    """A captured decode step (generate.jl:158-196): capture once, replay many.
+
+    ``capture(fn)`` records everything ``fn`` launches on a private stream into
+    a hipGraph; ``launch()`` replays it on torch's current stream. The step must
+    be device-driven (positions read and advanced on the device), which decode_
+    with ``advance=True`` is.
+    """
+
+    def __init__(self):
+        self.exec = None
+        self.stream = None
+
+    def capture(self, fn):
+        if self.exec is not None:
+            raise ArgumentError("session already holds a graph")
+        self.stream = torch.cuda.Stream()
+        self.stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(self.stream):
+            s = ctypes.c_void_p(self.stream.cuda_stream)
+            call("vm_graph_begin_capture", s)
+            try:
+                fn()
+            finally:
+                ge = ctypes.c_void_p()
+                call("vm_graph_end_capture", s, ctypes.byref(ge))
+        self.exec = ge
+        return self
+
+    def launch(self):
+        call("vm_graph_launch", self.exec, ops._stream())
+
+    def close(self):
+        if self.exec is not None:
+            call("vm_graph_destroy", self.exec)
+            self.exec = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,215 @@
+"""Operators of the gated-attention path — the call surface of src/kernels/*.jl.
+
+Each function keeps the reference's name (Julia's mutating ``op!`` is ``op_``
+here), argument order, keyword arguments and error behaviour, and forwards to
+the C ABI of libvallmo_attn.so. Tensors are torch tensors on the GPU (torch is
+only the device-memory and stream plumbing); their shapes are the reference's
+column-major dims reversed (Julia ``Q :: (D, Hq, B)`` is torch ``(B, Hq, D)``),
+so strides map one to one. Launches go on torch's current stream, allocate
+nothing (the allocating variants allocate outputs only) and never synchronise.
+
+bf16 tensors are torch.bfloat16; lengths/positions torch.int32; tables float32.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import ArgumentError, DimensionMismatch, call
+from .sizes import sizes
+
+__all__ = [
+    "rope_tables", "qnorm_rope_", "knorm_rope_append_", "attention_", "attention",
+    "decode_attention_", "decode_attention", "decode_scratch_bytes", "sigmoid_gate_",
+    "sigmoid", "fill_normal_",
+]
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need(t, dtype, name):
+    if t is None:
+        return
+    if not t.is_cuda:
+        raise ArgumentError(f"{name} must be a GPU tensor")
+    if t.dtype != dtype:
+        raise ArgumentError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.dim() > 0 and t.stride(-1) != 1:
+        raise ArgumentError(f"{name}: innermost dimension must be contiguous")
+
+
+def _need_contig(t, name):
+    if t is not None and not t.is_contiguous():
+        raise ArgumentError(f"{name} must be contiguous")
+
+
+def sigmoid(x):
+    """1 / (1 + exp(-x)) — src/kernels/kernels.jl:34 (host-side scalar helper)."""
+    import math
+    return 1.0 / (1.0 + math.exp(-x))
+
+
+def rope_tables(cfg) -> dict:
+    """(cos, sin) :: (HALF_ROT, Ctx) fp32 — src/llm/qwen35.jl:115-119.
+
+    ``cfg`` needs ``rot_half``, ``theta`` and ``Ctx``. Built on the device by
+    vm_rope_tables; torch shape (Ctx, HALF_ROT).
+    """
+    half, ctx, theta = int(cfg.rot_half), int(cfg.Ctx), float(cfg.theta)
+    cos = torch.empty((ctx, half), dtype=torch.float32, device="cuda")
+    sin = torch.empty((ctx, half), dtype=torch.float32, device="cuda")
+    call("vm_rope_tables", _p(cos), _p(sin), half, ctx, theta, _stream())
+    return {"cos": cos, "sin": sin}
+
+
+def qnorm_rope_(Q, QW, Cos, Sin, *, positions, eps, offset):
+    """In-place per-head RMSNorm ``(w + offset)`` then partial RoPE on Q.
+
+    src/kernels/qknorm_rope_append.jl:100-117. Q :: (D, Hq, B) (may be a strided
+    view of the packed projection), QW :: (D,), Cos/Sin :: (HALF_ROT, Ctx),
+    positions :: (B,) int32, 1-based column = rope column.
+    """
+    d = sizes(Q=(Q, "D Hq B"), QW=(QW, "D"), Cos=(Cos, "HALF_ROT Ctx"),
+              Sin=(Sin, "HALF_ROT Ctx"), positions=(positions, "B"))
+    if d["D"] & (d["D"] - 1):
+        raise ArgumentError(f"D = {d['D']} must be a power of two")
+    _need(Q, torch.bfloat16, "Q"); _need(QW, torch.bfloat16, "QW")
+    _need(Cos, torch.float32, "Cos"); _need(Sin, torch.float32, "Sin")
+    _need(positions, torch.int32, "positions")
+    _need_contig(Cos, "Cos"); _need_contig(Sin, "Sin")
+    call("vm_qnorm_rope", _p(Q), Q.stride(1), Q.stride(0), _p(QW), _p(Cos), _p(Sin), d["Ctx"],
+         _p(positions), d["B"], d["Hq"], d["D"], d["HALF_ROT"], float(eps), float(offset),
+         _stream())
+    return Q
+
+
+def knorm_rope_append_(K_cache, V_cache, K_raw, V_raw, KW, Cos, Sin, *, positions, eps, offset):
+    """K norm + RoPE written into K_cache at column positions[b]; V copied alongside.
+
+    src/kernels/qknorm_rope_append.jl:119-141. K_cache/V_cache :: (D, Ctx, Hk, B),
+    K_raw/V_raw :: (D, Hk, B) (views of the packed projection), KW :: (D,).
+    """
+    d = sizes(K_cache=(K_cache, "Dk Ctx Hk B"), V_cache=(V_cache, "Dv Ctx Hk B"),
+              K_raw=(K_raw, "Dk Hk B"), V_raw=(V_raw, "Dv Hk B"), KW=(KW, "Dk"),
+              Cos=(Cos, "HALF_ROT Ctx"), Sin=(Sin, "HALF_ROT Ctx"), positions=(positions, "B"))
+    for t, n in ((K_cache, "K_cache"), (V_cache, "V_cache"), (K_raw, "K_raw"), (V_raw, "V_raw"),
+                 (KW, "KW")):
+        _need(t, torch.bfloat16, n)
+    _need(positions, torch.int32, "positions")
+    _need_contig(Cos, "Cos"); _need_contig(Sin, "Sin")
+    if K_cache.stride() != V_cache.stride() or K_raw.stride() != V_raw.stride():
+        raise ArgumentError("K and V operands must share strides")
+    if d["Dk"] != d["Dv"]:
+        raise ArgumentError("Dk != Dv is not supported")
+    call("vm_knorm_rope_append", _p(K_cache), _p(V_cache), K_cache.stride(2), K_cache.stride(1),
+         K_cache.stride(0), d["Ctx"], _p(K_raw), _p(V_raw), K_raw.stride(1), K_raw.stride(0),
+         _p(KW), _p(Cos), _p(Sin), _p(positions), d["B"], d["Hk"], d["Dk"], d["HALF_ROT"],
+         float(eps), float(offset), _stream())
+
+
+def _out(outs, key="O"):
+    return outs[key] if isinstance(outs, dict) else getattr(outs, key)
+
+
+def attention_(outs, Q, K, V, *, causal=False, k_lengths=None, q_lengths=None):
+    """Flash attention forward (prefill) — src/kernels/attention.jl:93-129.
+
+    Q :: (Dk, L, H, B), K :: (Dk, Lk, Hk, B), V :: (Dv, Lk, Hk, B) (typically
+    cache prefixes), O :: (Dv, L, H, B). Queries are the suffix of keys: the
+    causal offset is k_len - q_len per sequence. Optional k_lengths/q_lengths ::
+    (B,) int32 make the batch ragged; rows past q_len are not written.
+    """
+    O = _out(outs)
+    d = sizes(Q=(Q, "Dk L H B"), K=(K, "Dk Lk Hk B"), V=(V, "Dv Lk Hk B"), O=(O, "Dv L H B"),
+              k_lengths=(k_lengths, "B"), q_lengths=(q_lengths, "B"))
+    if d["H"] % d["Hk"]:
+        raise DimensionMismatch(
+            f"Attention heads ({d['H']}) is not a multiple of key-value heads ({d['Hk']})")
+    for t, n in ((Q, "Q"), (K, "K"), (V, "V"), (O, "O")):
+        _need(t, torch.bfloat16, n)
+    _need(k_lengths, torch.int32, "k_lengths"); _need(q_lengths, torch.int32, "q_lengths")
+    if K.stride() != V.stride():
+        raise ArgumentError("K and V must share strides")
+    call("vm_attention_fwd", _p(O), O.stride(2), O.stride(1), O.stride(0), _p(Q), Q.stride(2),
+         Q.stride(1), Q.stride(0), _p(K), _p(V), K.stride(2), K.stride(1), K.stride(0),
+         _p(k_lengths), _p(q_lengths), d["B"], d["H"], d["Hk"], d["Dk"], d["L"], d["Lk"],
+         int(bool(causal)), _stream())
+    return outs
+
+
+def attention(Q, K, V, **kw) -> dict:
+    """Allocating attention (src/kernels/attention.jl:131-134): returns {"O": O}."""
+    B, H, L, _ = Q.shape
+    O = torch.empty((B, H, L, V.shape[-1]), dtype=Q.dtype, device=Q.device)
+    return attention_({"O": O}, Q, K, V, **kw)
+
+
+def decode_scratch_bytes(Q, K, *, n_splits=0) -> int:
+    """Scratch the split-KV decode needs (Pol.scratch, attention_decode.jl:320-331)."""
+    B, H, D = Q.shape
+    Hk, L = K.shape[1], K.shape[2]
+    return int(_lib.load().vm_decode_scratch_bytes(B, H, Hk, D, L, int(n_splits)))
+
+
+def decode_attention_(outs, Q, K, V, *, lengths, n_splits=0, scratch=None):
+    """Split-KV flash-decoding — src/kernels/attention_decode.jl:268-315.
+
+    Q :: (Dk, H, Batch) normalised+rotated, K/V :: (Dk, L, Hk, Batch) caches,
+    lengths :: (Batch,) int32 attended keys, O :: (Dv, H, Batch). n_splits = 0
+    sizes the split grid for the 256 CUs (the reference's default is 8 splits);
+    ``scratch`` is a uint8 GPU tensor of >= decode_scratch_bytes (allocated if None).
+    """
+    O = _out(outs)
+    d = sizes(Q=(Q, "Dk H Batch"), K=(K, "Dk L Hk Batch"), V=(V, "Dv L Hk Batch"),
+              O=(O, "Dv H Batch"), lengths=(lengths, "Batch"))
+    if d["H"] % d["Hk"]:
+        raise DimensionMismatch(
+            f"Attention heads ({d['H']}) is not a multiple of key-value heads ({d['Hk']})")
+    for t, n in ((Q, "Q"), (K, "K"), (V, "V"), (O, "O")):
+        _need(t, torch.bfloat16, n)
+    _need(lengths, torch.int32, "lengths")
+    if K.stride() != V.stride():
+        raise ArgumentError("K and V must share strides")
+    need = decode_scratch_bytes(Q, K, n_splits=n_splits)
+    if scratch is None:
+        scratch = torch.empty(max(need, 16), dtype=torch.uint8, device=Q.device)
+    call("vm_decode_attention", _p(O), O.stride(1), O.stride(0), _p(Q), Q.stride(1), Q.stride(0),
+         _p(K), _p(V), K.stride(2), K.stride(1), K.stride(0), d["L"], _p(lengths), d["Batch"],
+         d["H"], d["Hk"], d["Dk"], int(n_splits), _p(scratch), scratch.numel(), _stream())
+    return outs
+
+
+def decode_attention(Q, K, V, *, lengths, **kw) -> dict:
+    """Allocating decode attention (attention_decode.jl:317-334): returns {"O": O}."""
+    O = torch.empty((Q.shape[0], Q.shape[1], V.shape[-1]), dtype=Q.dtype, device=Q.device)
+    return decode_attention_({"O": O}, Q, K, V, lengths=lengths, **kw)
+
+
+def sigmoid_gate_(O, G):
+    """O .*= sigmoid.(G) in place — the decode gate of src/llm/qwen35.jl:205.
+
+    O, G :: (D, H, B) bf16 (G typically the stride-2 gate view of the projection).
+    """
+    d = sizes(O=(O, "D H B"), G=(G, "D H B"))
+    _need(O, torch.bfloat16, "O"); _need(G, torch.bfloat16, "G")
+    call("vm_sigmoid_gate", _p(O), O.stride(1), O.stride(0), _p(G), G.stride(1), G.stride(0),
+         d["B"], d["H"], d["D"], _stream())
+    return O
+
+
+def fill_normal_(X, seed: int, *, scale: float = 1.0, shift: float = 0.0):
+    """Fill a contiguous bf16 GPU tensor with the seeded N(0,1) synthetic stream
+    (SplitMix64 + Box-Muller, the generator the CPU tests use)."""
+    _need(X, torch.bfloat16, "X")
+    _need_contig(X, "X")
+    call("vm_fill_normal_bf16", _p(X), X.numel(), int(seed) & (2 ** 64 - 1), float(scale),
+         float(shift), _stream())
+    return X
