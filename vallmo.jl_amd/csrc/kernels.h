@@ -61,6 +61,7 @@ struct PrefillArgs {
   const uint16_t* q;
   int64_t q_st, q_sh, q_sb;
   const uint16_t* qw;
+  const uint16_t* kw;   // QRAW: bounds |k| for the static softmax max
   const float* cos_tab;
   const float* sin_tab;
   float eps, w_offset;

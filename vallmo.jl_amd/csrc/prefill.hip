@@ -4,33 +4,199 @@
 // of forward(::AttnLayer) (src/llm/qwen35.jl:292-318).
 //
 // Workgroup = 4 waves = 128 query rows of one (head, sequence); wave w owns 32
-// rows. Per 32-key step, all on 32x32x16 bf16 MFMA with fp32 accumulate:
-//   S^T[key][row] = K[key][:] . Q[row][:]     A = K (LDS, ds_read_b128),
-//                                             B = Q (registers, loaded once)
+// rows. Per 32-key tile, all on 32x32x16 bf16 MFMA with fp32 accumulate:
+//   S^T[key][row] = K[key][:] . Q[row][:]         A = K (LDS, ds_read_b128),
+//                                                 B = Q (registers, loaded once)
 //   O^T[d][row]  += V^T[d][key] . P^T[key][row]   A = V^T (LDS, ds_read_b64_tr_b16),
-//                                             B = P^T (the S^T accumulator, in place)
+//                                                 B = P^T (the S^T accumulator, in place)
 // The S^T accumulator layout (lane l: row l%32, keys 8(j/4)+4(l/32)+j%4) is the
-// P^T operand layout up to a key permutation, which the V^T transpose reads
-// reproduce, so P never leaves registers. K/V tiles are double-buffered in LDS
-// with a 544-byte row pitch (bank-conflict-free for both read patterns).
-// Softmax is exp2-based with the running max rescaled lazily (only when it
-// grows by > 8, keeping p <= 256), and the fully-masked-row guard of the
-// reference (o = 0 when l = 0).
+// P^T operand layout up to a key permutation that the V^T transpose reads
+// reproduce, so P never leaves registers.
+//
+// K/V tiles stream through a 3-stage LDS ring filled by direct global->LDS
+// loads (global_load_lds_dwordx4: no VGPR staging), issued two tiles ahead.
+// Rows are 512 B with the 16-byte chunks XOR-swizzled by row (swz below) so that
+// both read patterns hit distinct banks.
+//
+// Softmax is exp2-based. With QK-norm the logits are bounded: |s| <= |q~| *
+// max|k~| and |k~| <= sqrt(D) * max|kw + w_offset| (RoPE preserves norms), so
+// the fused path uses that per-row bound as a fixed softmax shift (no running
+// max, no accumulator rescale) whenever it is <= 64 in log2 units, which keeps
+// every exp2 in [2^-128, ~1]. Rows with a larger bound, and the unfused
+// attention! operator, use the online running max (rescaled lazily, only when
+// it grows by > 8). Rows with no valid key produce 0 (attention.jl:86).
 #include "common.h"
 #include "kernels.h"
 
 namespace vm {
 
-constexpr int PF_BM = 128;     // query rows per workgroup
-constexpr int PF_BN = 32;      // keys per step
-constexpr int LDS_ROW = 272;   // bf16 per LDS row: 256 + 16 pad (544 B)
+constexpr int PF_BM = 128;                   // query rows per workgroup
+constexpr int PF_BN = 32;                    // keys per tile
+constexpr int TILE = PF_BN * HEAD_DIM;       // bf16 per K (or V) tile: 16 KB
 constexpr float RESCALE_SLACK = 8.0f;
+constexpr float STATIC_MAX_LIMIT = 64.0f;
+
+// chunk swizzle: 16-byte chunk c of tile row r lives at chunk c ^ swz(r)
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Workgroup barrier without the release/acquire fences of __syncthreads(): those
+// would wait for every outstanding load (vmcnt(0)), including the tiles still in
+// flight. LDS visibility is established by each wave's explicit vmcnt wait on its
+// own DMA before the barrier; the asm memory clobbers keep the compiler from
+// moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+struct PrefillCtx {
+  const uint16_t* kbase;   // K rows of (b, hk)
+  const uint16_t* vbase;
+  int64_t kv_st;
+  int k_len, off, row, wrow0, wrow1, q_len, lane, wave;
+  int krow_max;            // last row that may be read (finite data)
+};
+
+// Issue this wave's share (4 K + 4 V instructions of 1 KB) of tile `jt`: the
+// 16-KB tile is 16 one-KB slots of two 512-byte rows each, 4 slots per wave.
+constexpr int LOADS_PER_TILE = 8;  // vmem instructions per wave per tile
+__device__ __forceinline__ void issue_tile(const PrefillCtx& c, int jt, uint16_t* kd,
+                                           uint16_t* vd) {
+  const int l = c.lane;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int g = 4 * c.wave + i;              // 1-KB slot of the tile: rows 2g, 2g+1
+    const int r = 2 * g + (l >> 5);
+    const int chunk = (l & 31) ^ swz(r);
+    const int64_t key = min(jt * PF_BN + r, c.krow_max);
+    const int64_t go = key * c.kv_st + chunk * 8;
+    __builtin_amdgcn_global_load_lds((const void*)(c.kbase + go),
+                                     (__attribute__((address_space(3))) void*)(kd + g * 512), 16,
+                                     0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(c.vbase + go),
+                                     (__attribute__((address_space(3))) void*)(vd + g * 512), 16,
+                                     0, 0);
+  }
+}
+
+template <bool STATIC, bool CAUSAL>
+__device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_tiles,
+                                          const uint16_t* kb, const uint16_t* vb, uint16_t* kn,
+                                          uint16_t* vn, const uint4 (&qop)[16], f32x16 (&acc)[8],
+                                          float& m_run, float& l_part, const int (&koff)[4],
+                                          const int (&voff)[2]) {
+  // tile jt resident for every wave: this wave's loads of jt done, then barrier
+  if (jt + 1 < n_tiles)
+    wait_vmcnt<LOADS_PER_TILE>();
+  else
+    wait_vmcnt<0>();
+  lds_barrier();
+  if (jt + 2 < n_tiles) issue_tile(c, jt + 2, kn, vn);
+
+  const bool skip = c.wrow0 >= c.q_len || (CAUSAL && jt * PF_BN > c.off + c.wrow1);
+  if (skip) return;
+
+  // S^T = K Q^T: chunk 2kk+h2 of row l%32 sits at ((2kk+h2) ^ swz) -> koff[kk&3] + 128*(kk>>2)
+  const char* kl = reinterpret_cast<const char*>(kb);
+  uint4 kf[16];
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk)
+    kf[kk] = *reinterpret_cast<const uint4*>(kl + koff[kk & 3] + 128 * (kk >> 2));
+  f32x16 sacc;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) sacc[j] = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) sacc = mfma32(kf[kk], qop[kk], sacc);
+
+  const int h2 = c.lane >> 5;
+  const bool need_mask = (jt * PF_BN + PF_BN > c.k_len) ||
+                         (CAUSAL && jt * PF_BN + PF_BN - 1 > c.off + c.wrow0);
+  if (need_mask) {
+    const int lim = CAUSAL ? min(c.k_len - 1, c.row + c.off) : c.k_len - 1;
+    const int key0 = jt * PF_BN + 4 * h2;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int key = key0 + 8 * (j >> 2) + (j & 3);
+      sacc[j] = key <= lim ? sacc[j] : -INFINITY;
+    }
+  }
+  float m_eff;
+  if (STATIC) {
+    m_eff = m_run;
+  } else {
+    float mx = sacc[0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sacc[j]);
+    mx = wave_max_xor(mx, 32) * LOG2E;
+    const float m_new = fmaxf(m_run, mx);
+    const bool need = m_new > m_run + RESCALE_SLACK;
+    if (__ballot(need) != 0ull) {
+      const float m_use = need ? m_new : m_run;
+      const float alpha = (m_use == m_run) ? 1.0f : fast_exp2(m_run - m_use);
+      l_part *= alpha;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+      m_run = m_use;
+    }
+    m_eff = m_run == -INFINITY ? 0.f : m_run;
+  }
+  float p[16], psum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    p[j] = fast_exp2(__builtin_fmaf(sacc[j], LOG2E, -m_eff));
+    psum += p[j];
+  }
+  l_part += psum;
+  uint4 pop[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    pop[ks].x = pack2(p[8 * ks + 0], p[8 * ks + 1]);
+    pop[ks].y = pack2(p[8 * ks + 2], p[8 * ks + 3]);
+    pop[ks].z = pack2(p[8 * ks + 4], p[8 * ks + 5]);
+    pop[ks].w = pack2(p[8 * ks + 6], p[8 * ks + 7]);
+  }
+  // O^T += V^T P^T; voff[dt&1] + 128*(dt>>1) addresses d-block dt of the key rows
+  const char* vl = reinterpret_cast<const char*>(vb);
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const uint16_t* p0 =
+          reinterpret_cast<const uint16_t*>(vl + voff[dt & 1] + 128 * (dt >> 1) + ks * 16 * 512);
+      const uint2 lo = lds_read_tr16(p0);
+      const uint2 hi = lds_read_tr16(p0 + 8 * HEAD_DIM);
+      acc[dt] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), pop[ks], acc[dt]);
+    }
+  }
+}
+
+template <bool STATIC, bool CAUSAL>
+__device__ __forceinline__ void tile_loop(const PrefillCtx& c, int n_tiles, uint16_t* K0,
+                                          uint16_t* K1, uint16_t* K2, uint16_t* V0, uint16_t* V1,
+                                          uint16_t* V2, const uint4 (&qop)[16], f32x16 (&acc)[8],
+                                          float& m_run, float& l_part, const int (&koff)[4],
+                                          const int (&voff)[2]) {
+  for (int jt = 0; jt < n_tiles; jt += 3) {
+    tile_step<STATIC, CAUSAL>(c, jt, n_tiles, K0, V0, K2, V2, qop, acc, m_run, l_part, koff, voff);
+    if (jt + 1 < n_tiles)
+      tile_step<STATIC, CAUSAL>(c, jt + 1, n_tiles, K1, V1, K0, V0, qop, acc, m_run, l_part, koff,
+                                voff);
+    if (jt + 2 < n_tiles)
+      tile_step<STATIC, CAUSAL>(c, jt + 2, n_tiles, K2, V2, K1, V1, qop, acc, m_run, l_part, koff,
+                                voff);
+  }
+}
 
 template <bool QRAW, bool GATE, bool CAUSAL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][PF_BN * LDS_ROW];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][PF_BN * LDS_ROW];
+  __shared__ __attribute__((aligned(1024))) uint16_t K0[TILE], K1[TILE], K2[TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t V0[TILE], V1[TILE], V2[TILE];
 
   // ---- work item: heaviest query tiles first; the query heads of one
   // kv head land on the same XCD (workgroup id mod 8) when H*B % 8 == 0.
@@ -55,11 +221,24 @@ void prefill_kernel(PrefillArgs a) {
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, h2 = lane >> 5;
-  const int row = r0 + 32 * wave + l32;                 // query row in the chunk
-  const int wrow0 = r0 + 32 * wave, wrow1 = wrow0 + 31;  // this wave's rows
+  const int row = r0 + 32 * wave + l32;  // query row in the chunk
+
+  PrefillCtx c;
+  c.kbase = a.k + (int64_t)b * a.kv_sb + (int64_t)hk * a.kv_sh;
+  c.vbase = a.v + (int64_t)b * a.kv_sb + (int64_t)hk * a.kv_sh;
+  c.kv_st = a.kv_st;
+  c.k_len = k_len; c.off = off; c.row = row; c.q_len = q_len;
+  c.wrow0 = r0 + 32 * wave; c.wrow1 = c.wrow0 + 31;
+  c.lane = lane; c.wave = wave;
+  c.krow_max = max(0, min(k_len, a.Lk) - 1);  // rows past k_len are masked; read finite data
+
+  // the first two tiles go out before the q prologue so their latency overlaps it
+  if (n_tiles > 0) issue_tile(c, 0, K0, V0);
+  if (n_tiles > 1) issue_tile(c, 1, K1, V1);
 
   // ---- Q operand: lane holds q[row][16kk + 8*h2 + j], pre-scaled by 1/16.
   uint4 qop[16];
+  float qn2 = 0.f;  // |q operand|^2 (fp32, before rounding)
   {
     const int qrow = min(row, a.L - 1);
     const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
@@ -89,15 +268,18 @@ void prefill_kernel(PrefillArgs a) {
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float c = cs[16 * kk + j], si = sn[16 * kk + j];
+          const float cc = cs[16 * kk + j], si = sn[16 * kk + j];
           const float x1 = x[kk][j], x2 = x[kk + 2][j];
-          x[kk][j] = x1 * c - x2 * si;
-          x[kk + 2][j] = x2 * c + x1 * si;
+          x[kk][j] = x1 * cc - x2 * si;
+          x[kk + 2][j] = x2 * cc + x1 * si;
         }
 #pragma unroll
       for (int kk = 0; kk < 16; ++kk) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[kk][j] *= QK_SCALE;
+        for (int j = 0; j < 8; ++j) {
+          x[kk][j] *= QK_SCALE;
+          qn2 += x[kk][j] * x[kk][j];
+        }
         qop[kk] = pack8(x[kk]);
       }
     } else {
@@ -112,127 +294,57 @@ void prefill_kernel(PrefillArgs a) {
     }
   }
 
+  // static softmax shift (fused path): bound on s * log2(e) for this row
+  bool use_static = false;
+  float m_run = -INFINITY;
+  if (QRAW) {
+    qn2 += __shfl_xor(qn2, 32, 64);
+    uint2 wv = *reinterpret_cast<const uint2*>(a.kw + 4 * lane);
+    float wmax = fmaxf(fmaxf(fabsf(__uint_as_float(wv.x << 16) + a.w_offset),
+                             fabsf(__uint_as_float(wv.x & 0xffff0000u) + a.w_offset)),
+                       fmaxf(fabsf(__uint_as_float(wv.y << 16) + a.w_offset),
+                             fabsf(__uint_as_float(wv.y & 0xffff0000u) + a.w_offset)));
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) wmax = fmaxf(wmax, __shfl_xor(wmax, m, 64));
+    const float kbound = 16.0f * wmax * 1.01f;                // sqrt(D) * max|kw+off|, + rounding
+    const float bound = sqrtf(qn2) * 1.01f * kbound * LOG2E;  // |q op| also rounded to bf16
+    use_static = __ballot(!(bound <= STATIC_MAX_LIMIT)) == 0ull;
+    if (use_static) m_run = bound;
+  }
+
+  // swizzled LDS read offsets (bytes): K chunk 2kk+h2 of row l32; V for the
+  // transpose reads (rows 4*(grp>>1) + (i16>>2) [+8], column chunk 2*(grp&1) + ((i16&3)>>1))
+  int koff[4], voff[2];
+  {
+    const int sk = swz(l32);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) koff[q] = l32 * 512 + (((2 * q + h2) ^ sk) * 16);
+    const int i16 = lane & 15, grp = lane >> 4;
+    const int vr = 4 * (grp >> 1) + (i16 >> 2);
+    const int sv = swz(vr);
+    const int cc = 2 * (grp & 1) + ((i16 & 3) >> 1);
+#pragma unroll
+    for (int par = 0; par < 2; ++par)
+      voff[par] = vr * 512 + (((4 * par + cc) ^ sv) * 16) + (i16 & 1) * 8;
+  }
+
   f32x16 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[i][j] = 0.f;
-  float m_run = -INFINITY, l_part = 0.f;
+  float l_part = 0.f;
 
-  const uint16_t* kbase = a.k + (int64_t)b * a.kv_sb + (int64_t)hk * a.kv_sh;
-  const uint16_t* vbase = a.v + (int64_t)b * a.kv_sb + (int64_t)hk * a.kv_sh;
-
-  // global -> registers: thread owns 16-byte chunks c = tid + 256*i of the tile
-  uint4 kreg[4], vreg[4];
-  auto load_tile = [&](int jt) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i;
-      const int key = jt * PF_BN + (c >> 5);
-      const int64_t krow = min(key, a.Lk - 1);
-      const int col = (c & 31) * 8;
-      kreg[i] = load16(kbase + krow * a.kv_st + col);
-      vreg[i] = load16(vbase + krow * a.kv_st + col);
-      if (key >= k_len) vreg[i] = make_uint4(0, 0, 0, 0);  // p = 0 must meet finite v
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i;
-      const int off_l = (c >> 5) * LDS_ROW + (c & 31) * 8;
-      *reinterpret_cast<uint4*>(&Ks[buf][off_l]) = kreg[i];
-      *reinterpret_cast<uint4*>(&Vs[buf][off_l]) = vreg[i];
-    }
-  };
-
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  const bool wave_live = wrow0 < q_len;
-  // V^T read addressing (see ds_read_b64_tr_b16 in common.h)
-  const int i16 = lane & 15, grp = lane >> 4;
-  const int tr_key = 4 * (grp >> 1) + (i16 >> 2);
-  const int tr_col = 16 * (grp & 1) + 4 * (i16 & 3);
-
-  for (int jt = 0; jt < n_tiles; ++jt) {
-    const int buf = jt & 1;
-    const bool more = jt + 1 < n_tiles;
-    if (more) load_tile(jt + 1);
-
-    const bool skip = !wave_live || (CAUSAL && jt * PF_BN > off + wrow1);
-    if (!skip) {
-      const uint16_t* kl = &Ks[buf][l32 * LDS_ROW + 8 * h2];
-      f32x16 sacc;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) sacc[j] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) sacc = mfma32(load16(kl + 16 * kk), qop[kk], sacc);
-
-      float sv[16];
-      float mx = -INFINITY;
-      const int key0 = jt * PF_BN + 4 * h2;
-      const bool need_mask = (jt * PF_BN + PF_BN > k_len) ||
-                             (CAUSAL && jt * PF_BN + PF_BN - 1 > off + wrow0);
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int key = key0 + 8 * (j >> 2) + (j & 3);
-        bool valid = true;
-        if (need_mask) valid = key < k_len && (!CAUSAL || key <= row + off);
-        sv[j] = valid ? sacc[j] * LOG2E : -INFINITY;
-        mx = fmaxf(mx, sv[j]);
-      }
-      mx = wave_max_xor(mx, 32);
-      const float m_new = fmaxf(m_run, mx);
-      const bool need = m_new > m_run + RESCALE_SLACK;
-      if (__ballot(need) != 0ull) {
-        const float m_use = need ? m_new : m_run;
-        const float alpha = (m_use == m_run) ? 1.0f : fast_exp2(m_run - m_use);
-        l_part *= alpha;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-        m_run = m_use;
-      }
-      const float m_eff = m_run == -INFINITY ? 0.f : m_run;
-      float psum = 0.f;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        sv[j] = fast_exp2(sv[j] - m_eff);
-        psum += sv[j];
-      }
-      l_part += psum;
-      uint4 pop[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        pop[ks].x = pack2(sv[8 * ks + 0], sv[8 * ks + 1]);
-        pop[ks].y = pack2(sv[8 * ks + 2], sv[8 * ks + 3]);
-        pop[ks].z = pack2(sv[8 * ks + 4], sv[8 * ks + 5]);
-        pop[ks].w = pack2(sv[8 * ks + 6], sv[8 * ks + 7]);
-      }
-      const uint16_t* vl = &Vs[buf][0];
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const uint16_t* p0 = vl + (16 * ks + tr_key) * LDS_ROW + 32 * dt + tr_col;
-          const uint2 lo = lds_read_tr16(p0);
-          const uint2 hi = lds_read_tr16(p0 + 8 * LDS_ROW);
-          const uint4 vt = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          acc[dt] = mfma32(vt, pop[ks], acc[dt]);
-        }
-      }
-    }
-    if (more) store_tile(buf ^ 1);
-    __syncthreads();
-  }
+  if (QRAW && use_static)
+    tile_loop<true, CAUSAL>(c, n_tiles, K0, K1, K2, V0, V1, V2, qop, acc, m_run, l_part, koff, voff);
+  else
+    tile_loop<false, CAUSAL>(c, n_tiles, K0, K1, K2, V0, V1, V2, qop, acc, m_run, l_part, koff,
+                             voff);
 
   // ---- epilogue: normalise, gate, store (row-major d within each row)
   if (row >= q_len) return;
   float l_tot = l_part + __shfl_xor(l_part, 32, 64);
-  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;  // fully-masked row -> 0
+  const float inv = l_tot > 0.f ? fast_rcp(l_tot) : 0.f;  // fully-masked row -> 0
   uint16_t* op = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)row * a.o_st;
   const uint16_t* gp = nullptr;
   if (GATE) gp = a.gate + (int64_t)b * a.g_sb + (int64_t)h * a.g_sh + (int64_t)row * a.g_st;
@@ -243,7 +355,7 @@ void prefill_kernel(PrefillArgs a) {
       const int d0 = 32 * dt + 8 * jb + 4 * h2;
       float o4[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) o4[c] = acc[dt][4 * jb + c] * inv;
+      for (int q = 0; q < 4; ++q) o4[q] = acc[dt][4 * jb + q] * inv;
       if (GATE) {
         const uint2 gv = *reinterpret_cast<const uint2*>(gp + d0);
         o4[0] *= sigmoidf(__uint_as_float(gv.x << 16));
@@ -275,7 +387,5 @@ hipError_t launch_prefill(const PrefillArgs& a, bool qraw, bool gate, hipStream_
     return hipErrorInvalidValue;
   return hipGetLastError();
 }
-
-constexpr int prefill_rows_per_wg() { return PF_BM; }
 
 }  // namespace vm

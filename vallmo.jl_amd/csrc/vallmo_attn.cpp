@@ -493,7 +493,7 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm
   const int64_t Dl = D;
   vm::PrefillArgs a{};
   a.q = qkv; a.q_st = qkv_st; a.q_sh = 2 * Dl; a.q_sb = qkv_sb;
-  a.qw = qw; a.cos_tab = cs; a.sin_tab = sn; a.eps = eps; a.w_offset = w_offset;
+  a.qw = qw; a.kw = kw; a.cos_tab = cs; a.sin_tab = sn; a.eps = eps; a.w_offset = w_offset;
   a.k = kc; a.v = vc; a.kv_st = c_st; a.kv_sh = c_sh; a.kv_sb = c_sb;
   a.o = out; a.o_st = out_st; a.o_sh = Dl; a.o_sb = out_sb;
   a.gate = qkv + Dl; a.g_st = qkv_st; a.g_sh = 2 * Dl; a.g_sb = qkv_sb;
