@@ -13,8 +13,10 @@
 // P^T operand layout up to a key permutation that the V^T transpose reads
 // reproduce, so P never leaves registers.
 //
-// K/V tiles stream through a 3-stage LDS ring filled by direct global->LDS
-// loads (global_load_lds_dwordx4: no VGPR staging), issued two tiles ahead.
+// K/V tiles stream through a 4-slot LDS ring filled by direct global->LDS
+// loads (global_load_lds_dwordx4: no VGPR staging), issued two tiles ahead of
+// use; each iteration issues QK of the next tile on the matrix cores before the
+// softmax of the current one, so the VALU work runs under the MFMAs.
 // Rows are 512 B with the 16-byte chunks XOR-swizzled by row (swz below) so that
 // both read patterns hit distinct banks.
 //
@@ -60,6 +62,7 @@ struct PrefillCtx {
   int64_t kv_st;
   int k_len, off, row, wrow0, wrow1, q_len, lane, wave;
   int krow_max;            // last row that may be read (finite data)
+  int dma_off[4];          // per-lane element offsets of this wave's 4 DMA slots
 };
 
 // Issue this wave's share (4 K + 4 V instructions of 1 KB) of tile `jt`: the
@@ -67,71 +70,103 @@ struct PrefillCtx {
 constexpr int LOADS_PER_TILE = 8;  // vmem instructions per wave per tile
 __device__ __forceinline__ void issue_tile(const PrefillCtx& c, int jt, uint16_t* kd,
                                            uint16_t* vd) {
-  const int l = c.lane;
+  const int row0 = jt * PF_BN;
+  if (row0 + PF_BN - 1 <= c.krow_max) {
+    // whole tile in range: uniform tile base + precomputed per-lane offsets
+    const uint16_t* kt = c.kbase + (int64_t)row0 * c.kv_st;
+    const uint16_t* vt = c.vbase + (int64_t)row0 * c.kv_st;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int g = 4 * c.wave + i;              // 1-KB slot of the tile: rows 2g, 2g+1
-    const int r = 2 * g + (l >> 5);
-    const int chunk = (l & 31) ^ swz(r);
-    const int64_t key = min(jt * PF_BN + r, c.krow_max);
-    const int64_t go = key * c.kv_st + chunk * 8;
-    __builtin_amdgcn_global_load_lds((const void*)(c.kbase + go),
-                                     (__attribute__((address_space(3))) void*)(kd + g * 512), 16,
-                                     0, 0);
-    __builtin_amdgcn_global_load_lds((const void*)(c.vbase + go),
-                                     (__attribute__((address_space(3))) void*)(vd + g * 512), 16,
-                                     0, 0);
+    for (int i = 0; i < 4; ++i) {
+      const int g = 4 * c.wave + i;  // 1-KB slot of the tile: rows 2g, 2g+1
+      __builtin_amdgcn_global_load_lds((const void*)(kt + c.dma_off[i]),
+                                       (__attribute__((address_space(3))) void*)(kd + g * 512),
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vt + c.dma_off[i]),
+                                       (__attribute__((address_space(3))) void*)(vd + g * 512),
+                                       16, 0, 0);
+    }
+  } else {
+    // last tile: rows past the last readable row re-read it (their keys are masked)
+    const int l = c.lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int g = 4 * c.wave + i;
+      const int r = 2 * g + (l >> 5);
+      const int chunk = (l & 31) ^ swz(r);
+      const int64_t key = min(row0 + r, c.krow_max);
+      const int64_t go = key * c.kv_st + chunk * 8;
+      __builtin_amdgcn_global_load_lds((const void*)(c.kbase + go),
+                                       (__attribute__((address_space(3))) void*)(kd + g * 512),
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(c.vbase + go),
+                                       (__attribute__((address_space(3))) void*)(vd + g * 512),
+                                       16, 0, 0);
+    }
   }
 }
 
-template <bool STATIC, bool CAUSAL>
-__device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_tiles,
-                                          const uint16_t* kb, const uint16_t* vb, uint16_t* kn,
-                                          uint16_t* vn, const uint4 (&qop)[16], f32x16 (&acc)[8],
-                                          float& m_run, float& l_part, const int (&koff)[4],
-                                          const int (&voff)[2]) {
-  // tile jt resident for every wave: this wave's loads of jt done, then barrier
-  if (jt + 1 < n_tiles)
-    wait_vmcnt<LOADS_PER_TILE>();
-  else
-    wait_vmcnt<0>();
-  lds_barrier();
-  if (jt + 2 < n_tiles) issue_tile(c, jt + 2, kn, vn);
-
-  const bool skip = c.wrow0 >= c.q_len || (CAUSAL && jt * PF_BN > c.off + c.wrow1);
-  if (skip) return;
-
-  // S^T = K Q^T: chunk 2kk+h2 of row l%32 sits at ((2kk+h2) ^ swz) -> koff[kk&3] + 128*(kk>>2)
+// S^T = K Q^T for one tile: chunk 2kk+h2 of row l%32 sits at
+// ((2kk+h2) ^ swz) -> koff[kk&3] + 128*(kk>>2) bytes.
+__device__ __forceinline__ f32x16 qk_tile(const uint16_t* kb, const uint4 (&qop)[16],
+                                          const int (&koff)[4]) {
   const char* kl = reinterpret_cast<const char*>(kb);
   uint4 kf[16];
 #pragma unroll
   for (int kk = 0; kk < 16; ++kk)
     kf[kk] = *reinterpret_cast<const uint4*>(kl + koff[kk & 3] + 128 * (kk >> 2));
-  f32x16 sacc;
+  f32x16 s;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) sacc[j] = 0.f;
+  for (int j = 0; j < 16; ++j) s[j] = 0.f;
 #pragma unroll
-  for (int kk = 0; kk < 16; ++kk) sacc = mfma32(kf[kk], qop[kk], sacc);
+  for (int kk = 0; kk < 16; ++kk) s = mfma32(kf[kk], qop[kk], s);
+  return s;
+}
 
-  const int h2 = c.lane >> 5;
+// Mask keys past k_len and (causal) past row + off with -inf.
+template <bool CAUSAL>
+__device__ __forceinline__ void mask_tile(const PrefillCtx& c, int jt, f32x16& s) {
+  const int lim = CAUSAL ? min(c.k_len - 1, c.row + c.off) : c.k_len - 1;
+  const int key0 = jt * PF_BN + 4 * (c.lane >> 5);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int key = key0 + 8 * (j >> 2) + (j & 3);
+    s[j] = key <= lim ? s[j] : -INFINITY;
+  }
+}
+
+// One pipelined iteration on ring slot SLOT = jt % 4: wait for tile jt+1, issue
+// tile jt+3, then QK(jt+1) on the matrix cores while the VALU runs softmax(jt),
+// then PV(jt). `sc` holds S^T of tile jt on entry and of tile jt+1 on exit.
+template <bool STATIC, bool CAUSAL, int SLOT>
+__device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_tiles, int my_tiles,
+                                          uint16_t* const (&K)[4], uint16_t* const (&V)[4],
+                                          const uint4 (&qop)[16], f32x16 (&acc)[8], f32x16& sc,
+                                          float& m_run, float& l_part, const int (&koff)[4],
+                                          const int (&voff)[2]) {
+  // tiles jt+1 and jt+2 may be in flight; tile jt+1 must be resident for all waves
+  if (jt + 2 < n_tiles)
+    wait_vmcnt<LOADS_PER_TILE>();
+  else
+    wait_vmcnt<0>();
+  lds_barrier();
+  if (jt + 3 < n_tiles) issue_tile(c, jt + 3, K[(SLOT + 3) & 3], V[(SLOT + 3) & 3]);
+  if (jt >= my_tiles) return;
+
   const bool need_mask = (jt * PF_BN + PF_BN > c.k_len) ||
                          (CAUSAL && jt * PF_BN + PF_BN - 1 > c.off + c.wrow0);
-  if (need_mask) {
-    const int lim = CAUSAL ? min(c.k_len - 1, c.row + c.off) : c.k_len - 1;
-    const int key0 = jt * PF_BN + 4 * h2;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int key = key0 + 8 * (j >> 2) + (j & 3);
-      sacc[j] = key <= lim ? sacc[j] : -INFINITY;
-    }
-  }
+  if (need_mask) mask_tile<CAUSAL>(c, jt, sc);
+
+  // S^T of the next tile (its slot is resident; past this wave's last tile the
+  // result is simply unused)
+  const f32x16 sn = qk_tile(K[(SLOT + 1) & 3], qop, koff);
+
   float m_eff;
   if (STATIC) {
     m_eff = m_run;
   } else {
-    float mx = sacc[0];
+    float mx = sc[0];
 #pragma unroll
-    for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sacc[j]);
+    for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sc[j]);
     mx = wave_max_xor(mx, 32) * LOG2E;
     const float m_new = fmaxf(m_run, mx);
     const bool need = m_new > m_run + RESCALE_SLACK;
@@ -148,7 +183,7 @@ __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_til
   float p[16], psum = 0.f;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    p[j] = fast_exp2(__builtin_fmaf(sacc[j], LOG2E, -m_eff));
+    p[j] = fast_exp2(__builtin_fmaf(sc[j], LOG2E, -m_eff));
     psum += p[j];
   }
   l_part += psum;
@@ -161,7 +196,7 @@ __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_til
     pop[ks].w = pack2(p[8 * ks + 6], p[8 * ks + 7]);
   }
   // O^T += V^T P^T; voff[dt&1] + 128*(dt>>1) addresses d-block dt of the key rows
-  const char* vl = reinterpret_cast<const char*>(vb);
+  const char* vl = reinterpret_cast<const char*>(V[SLOT]);
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
@@ -173,30 +208,48 @@ __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_til
       acc[dt] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), pop[ks], acc[dt]);
     }
   }
+  sc = sn;
 }
 
+// Ring of 4 tile slots; tiles 0..2 are issued by the caller.
 template <bool STATIC, bool CAUSAL>
-__device__ __forceinline__ void tile_loop(const PrefillCtx& c, int n_tiles, uint16_t* K0,
-                                          uint16_t* K1, uint16_t* K2, uint16_t* V0, uint16_t* V1,
-                                          uint16_t* V2, const uint4 (&qop)[16], f32x16 (&acc)[8],
+__device__ __forceinline__ void tile_loop(const PrefillCtx& c, int n_tiles, int my_tiles,
+                                          uint16_t* const (&K)[4], uint16_t* const (&V)[4],
+                                          const uint4 (&qop)[16], f32x16 (&acc)[8],
                                           float& m_run, float& l_part, const int (&koff)[4],
                                           const int (&voff)[2]) {
-  for (int jt = 0; jt < n_tiles; jt += 3) {
-    tile_step<STATIC, CAUSAL>(c, jt, n_tiles, K0, V0, K2, V2, qop, acc, m_run, l_part, koff, voff);
+  // tile 0 resident (tiles 1 and 2 may still be in flight), then S^T of tile 0
+  if (n_tiles > 2)
+    wait_vmcnt<2 * LOADS_PER_TILE>();
+  else if (n_tiles > 1)
+    wait_vmcnt<LOADS_PER_TILE>();
+  else
+    wait_vmcnt<0>();
+  lds_barrier();
+  f32x16 sc;
+  if (my_tiles > 0) sc = qk_tile(K[0], qop, koff);
+  for (int jt = 0; jt < n_tiles; jt += 4) {
+    tile_step<STATIC, CAUSAL, 0>(c, jt, n_tiles, my_tiles, K, V, qop, acc, sc, m_run, l_part,
+                                 koff, voff);
     if (jt + 1 < n_tiles)
-      tile_step<STATIC, CAUSAL>(c, jt + 1, n_tiles, K1, V1, K0, V0, qop, acc, m_run, l_part, koff,
-                                voff);
+      tile_step<STATIC, CAUSAL, 1>(c, jt + 1, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
+                                   l_part, koff, voff);
     if (jt + 2 < n_tiles)
-      tile_step<STATIC, CAUSAL>(c, jt + 2, n_tiles, K2, V2, K1, V1, qop, acc, m_run, l_part, koff,
-                                voff);
+      tile_step<STATIC, CAUSAL, 2>(c, jt + 2, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
+                                   l_part, koff, voff);
+    if (jt + 3 < n_tiles)
+      tile_step<STATIC, CAUSAL, 3>(c, jt + 3, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
+                                   l_part, koff, voff);
   }
 }
 
 template <bool QRAW, bool GATE, bool CAUSAL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint16_t K0[TILE], K1[TILE], K2[TILE];
-  __shared__ __attribute__((aligned(1024))) uint16_t V0[TILE], V1[TILE], V2[TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t K0[TILE], K1[TILE], K2[TILE], K3[TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t V0[TILE], V1[TILE], V2[TILE], V3[TILE];
+  uint16_t* const K[4] = {K0, K1, K2, K3};
+  uint16_t* const V[4] = {V0, V1, V2, V3};
 
   // ---- work item: heaviest query tiles first; the query heads of one
   // kv head land on the same XCD (workgroup id mod 8) when H*B % 8 == 0.
@@ -231,10 +284,19 @@ void prefill_kernel(PrefillArgs a) {
   c.wrow0 = r0 + 32 * wave; c.wrow1 = c.wrow0 + 31;
   c.lane = lane; c.wave = wave;
   c.krow_max = max(0, min(k_len, a.Lk) - 1);  // rows past k_len are masked; read finite data
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 2 * (4 * wave + i) + (lane >> 5);
+    c.dma_off[i] = r * (int)a.kv_st + (((lane & 31) ^ swz(r)) * 8);
+  }
 
-  // the first two tiles go out before the q prologue so their latency overlaps it
+  // the first three tiles go out before the q prologue so their latency overlaps it
   if (n_tiles > 0) issue_tile(c, 0, K0, V0);
   if (n_tiles > 1) issue_tile(c, 1, K1, V1);
+  if (n_tiles > 2) issue_tile(c, 2, K2, V2);
+  // tiles this wave computes (causal: keys <= off + its last row)
+  int my_tiles = c.wrow0 < q_len ? n_tiles : 0;
+  if (CAUSAL && my_tiles > 0) my_tiles = min(n_tiles, (off + c.wrow1) / PF_BN + 1);
 
   // ---- Q operand: lane holds q[row][16kk + 8*h2 + j], pre-scaled by 1/16.
   uint4 qop[16];
@@ -336,10 +398,9 @@ void prefill_kernel(PrefillArgs a) {
   float l_part = 0.f;
 
   if (QRAW && use_static)
-    tile_loop<true, CAUSAL>(c, n_tiles, K0, K1, K2, V0, V1, V2, qop, acc, m_run, l_part, koff, voff);
+    tile_loop<true, CAUSAL>(c, n_tiles, my_tiles, K, V, qop, acc, m_run, l_part, koff, voff);
   else
-    tile_loop<false, CAUSAL>(c, n_tiles, K0, K1, K2, V0, V1, V2, qop, acc, m_run, l_part, koff,
-                             voff);
+    tile_loop<false, CAUSAL>(c, n_tiles, my_tiles, K, V, qop, acc, m_run, l_part, koff, voff);
 
   // ---- epilogue: normalise, gate, store (row-major d within each row)
   if (row >= q_len) return;

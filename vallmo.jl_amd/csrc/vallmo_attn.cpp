@@ -408,6 +408,7 @@ int vm_attention_fwd(vm_bf16* o, int64_t o_st, int64_t o_sh, int64_t o_sb, const
     TRY(check_stride(s, "attention"));
   if (B == 0 || L == 0) return VM_OK;
   REQUIRE(Lk > 0, VM_E_ARG, "attention: k_len must be >= 1 (Lk = 0)");
+  REQUIRE(kv_st < ((int64_t)1 << 25), VM_E_ARG, "attention: K/V token stride too large");
   vm::PrefillArgs a{};
   a.q = q; a.q_st = q_st; a.q_sh = q_sh; a.q_sb = q_sb;
   a.k = k; a.v = v; a.kv_st = kv_st; a.kv_sh = kv_sh; a.kv_sb = kv_sb;
@@ -490,6 +491,7 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm
   TRY(check_stride(out_sb, "out_sb"));
   if (B == 0 || T == 0) return VM_OK;
   REQUIRE(ctx < (int64_t)1 << 31, VM_E_ARG, "gated_attn_prefill: Ctx too large");
+  REQUIRE(c_st < ((int64_t)1 << 25), VM_E_ARG, "gated_attn_prefill: cache token stride too large");
   const int64_t Dl = D;
   vm::PrefillArgs a{};
   a.q = qkv; a.q_st = qkv_st; a.q_sh = 2 * Dl; a.q_sb = qkv_sb;
