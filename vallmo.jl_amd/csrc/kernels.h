@@ -33,6 +33,7 @@ struct DecodeArgs {
   const uint16_t* q;    // raw q (fused) or normalised q
   int64_t q_sh, q_sb;
   const uint16_t* qw;   // fused prologue only
+  const uint16_t* kw;   // fused: bounds |k| for the static softmax shift
   const float* cos_tab;
   const float* sin_tab;
   float eps, w_offset;
@@ -40,9 +41,12 @@ struct DecodeArgs {
   const uint16_t* vc;
   int64_t c_st, c_sh, c_sb, ctx;
   const int32_t* lengths;
-  float* part_o;        // [B][Hk][NS][G][256]
-  float* part_ml;       // [B][Hk][NS][G][2]
-  int B, Hk, G, NS, split;
+  float* part_o;        // [slots][G][256], slots = NW + B*Hk
+  float* part_ml;       // [slots][G][2]  (shift m in log2 units, sum l)
+  int B, Hk, G;
+  int NW;               // waves of the stream partition (multiple of 4)
+  int min_chunk;        // smallest per-wave chunk (token-heads, multiple of 16)
+  int32_t* counter;     // nullable: merge completion counter, zeroed here
 };
 
 struct CombineArgs {
@@ -53,7 +57,10 @@ struct CombineArgs {
   int64_t o_sh, o_sb;
   const uint16_t* gate;  // nullable: sigmoid gate logits
   int64_t g_sh, g_sb;
-  int B, Hk, G, NS, split;
+  int B, Hk, G, NW, min_chunk;
+  int64_t ctx;
+  int32_t* advance;      // nullable: positions to bump once every workgroup has read them
+  int32_t* counter;      // with advance: completion counter (zeroed by the stream kernel)
 };
 
 struct PrefillArgs {
@@ -90,8 +97,9 @@ hipError_t launch_decode(const DecodeArgs& a, bool fused_q, hipStream_t st);
 hipError_t launch_combine(const CombineArgs& a, hipStream_t st);
 hipError_t launch_prefill(const PrefillArgs& a, bool qraw, bool gate, hipStream_t st);
 
-// Decode split policy shared by the scratch-size query and the launcher.
-constexpr int DECODE_WG_TOKENS = 128;  // 4 waves x 32-token steps
-int decode_split_tokens(int B, int Hk, int64_t ctx, int n_splits);
+// Decode stream partition shared by the scratch-size query and the launchers:
+// NW waves cover the token-heads sum_b len_b * Hk in equal contiguous chunks.
+constexpr int DECODE_MIN_CHUNK = 64;
+int decode_stream_waves(int B, int Hk, int n_splits);
 
 }  // namespace vm

@@ -105,13 +105,14 @@ int check_stride(int64_t s, const char* name) {
     if (_rc != VM_OK) return _rc; \
   } while (0)
 
-size_t decode_part_o_bytes(int B, int Hk, int NS, int G) {
-  return (size_t)B * Hk * NS * G * vm::HEAD_DIM_ABI * sizeof(float);
+size_t decode_slots(int B, int Hk, int NW) { return (size_t)NW + (size_t)B * Hk; }
+size_t decode_part_o_bytes(int B, int Hk, int NW, int G) {
+  return decode_slots(B, Hk, NW) * G * vm::HEAD_DIM_ABI * sizeof(float);
 }
-size_t decode_part_ml_bytes(int B, int Hk, int NS, int G) {
-  return (size_t)B * Hk * NS * G * 2 * sizeof(float);
+size_t decode_part_ml_bytes(int B, int Hk, int NW, int G) {
+  return decode_slots(B, Hk, NW) * G * 2 * sizeof(float);
 }
-int decode_ns(int64_t ctx, int split) { return (int)((ctx + split - 1) / split); }
+constexpr size_t DECODE_COUNTER_BYTES = 256;  // completion counter, own 256-byte block
 
 }  // namespace
 
@@ -270,10 +271,10 @@ int vm_knorm_rope_append(vm_bf16* kc, vm_bf16* vc, int64_t c_st, int64_t c_sh, i
 // ---- a5 -------------------------------------------------------------------
 size_t vm_decode_scratch_bytes(int B, int H, int Hk, int D, int64_t ctx, int n_splits) {
   if (B <= 0 || H <= 0 || Hk <= 0 || H % Hk || D != vm::HEAD_DIM_ABI || ctx <= 0) return 0;
-  const int split = vm::decode_split_tokens(B, Hk, ctx, n_splits);
-  const int NS = decode_ns(ctx, split);
+  const int NW = vm::decode_stream_waves(B, Hk, n_splits);
   const int G = H / Hk;
-  return decode_part_o_bytes(B, Hk, NS, G) + decode_part_ml_bytes(B, Hk, NS, G);
+  const size_t pm_end = decode_part_o_bytes(B, Hk, NW, G) + decode_part_ml_bytes(B, Hk, NW, G);
+  return (pm_end + 255) / 256 * 256 + DECODE_COUNTER_BYTES;
 }
 
 static int decode_common(vm::DecodeArgs& a, vm::CombineArgs& c, void* scratch, size_t scratch_bytes,
@@ -282,20 +283,25 @@ static int decode_common(vm::DecodeArgs& a, vm::CombineArgs& c, void* scratch, s
   const int G = H / Hk;
   REQUIRE(G <= 8, VM_E_UNSUPPORTED, "decode: GQA group %d > 8 is not supported", G);
   REQUIRE(n_splits >= 0, VM_E_ARG, "decode: n_splits = %d", n_splits);
-  REQUIRE(ctx > 0 && ctx < (int64_t)1 << 31, VM_E_ARG, "decode: Ctx = %lld", (long long)ctx);
-  const int split = vm::decode_split_tokens(B, Hk, ctx, n_splits);
-  const int NS = decode_ns(ctx, split);
-  const size_t need = decode_part_o_bytes(B, Hk, NS, G) + decode_part_ml_bytes(B, Hk, NS, G);
+  REQUIRE(ctx > 0, VM_E_ARG, "decode: Ctx = %lld", (long long)ctx);
+  REQUIRE((int64_t)B * ctx * Hk < ((int64_t)1 << 31), VM_E_UNSUPPORTED,
+          "decode: B*Ctx*Hk = %lld token-heads exceeds 2^31", (long long)B * ctx * Hk);
+  const int NW = vm::decode_stream_waves(B, Hk, n_splits);
+  const size_t po = decode_part_o_bytes(B, Hk, NW, G), pm = decode_part_ml_bytes(B, Hk, NW, G);
+  const size_t ctr = (po + pm + 255) / 256 * 256;  // completion counter offset
+  const size_t need = ctr + DECODE_COUNTER_BYTES;
   REQUIRE(scratch != nullptr && scratch_bytes >= need, VM_E_SCRATCH,
           "decode: scratch of %zu bytes < %zu required (vm_decode_scratch_bytes)", scratch_bytes,
           need);
   TRY(check_aligned(scratch, "scratch"));
-  a.part_o = reinterpret_cast<float*>(scratch);
-  a.part_ml = reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) +
-                                       decode_part_o_bytes(B, Hk, NS, G));
-  a.B = B; a.Hk = Hk; a.G = G; a.NS = NS; a.split = split; a.ctx = ctx;
+  char* sp = reinterpret_cast<char*>(scratch);
+  a.part_o = reinterpret_cast<float*>(sp);
+  a.part_ml = reinterpret_cast<float*>(sp + po);
+  a.counter = reinterpret_cast<int32_t*>(sp + ctr);
+  a.B = B; a.Hk = Hk; a.G = G; a.NW = NW; a.min_chunk = vm::DECODE_MIN_CHUNK; a.ctx = ctx;
   c.part_o = a.part_o; c.part_ml = a.part_ml;
-  c.B = B; c.Hk = Hk; c.G = G; c.NS = NS; c.split = split;
+  c.B = B; c.Hk = Hk; c.G = G; c.NW = NW; c.min_chunk = vm::DECODE_MIN_CHUNK; c.ctx = ctx;
+  c.advance = nullptr; c.counter = a.counter;
   return VM_OK;
 }
 
@@ -371,17 +377,16 @@ int vm_gated_attn_decode(vm_bf16* out, int64_t out_sb, const vm_bf16* qkv, int64
   if (rc) return rc;
   // a3 + a5: split-KV attention with the q norm+RoPE prologue fused
   a.q = qkv; a.q_sh = 2 * Dl; a.q_sb = qkv_sb;
-  a.qw = qw; a.cos_tab = cs; a.sin_tab = sn; a.eps = eps; a.w_offset = w_offset;
+  a.qw = qw; a.kw = kw; a.cos_tab = cs; a.sin_tab = sn; a.eps = eps; a.w_offset = w_offset;
   a.kc = kc; a.vc = vc; a.c_st = c_st; a.c_sh = c_sh; a.c_sb = c_sb;
   a.lengths = positions;
   rc = hip_status(timed(VM_K_DECODE_SPLIT, S(st), [&] { return vm::launch_decode(a, true, S(st)); }), "gated_attn_decode split");
   if (rc) return rc;
-  // a5 merge + a6 gate, written as the Wo input (D, Hq, B)
+  // a5 merge + a6 gate, written as the Wo input (D, Hq, B); a12 advance fused
   c.lengths = positions; c.out = out; c.o_sh = Dl; c.o_sb = out_sb;
   c.gate = qkv + Dl; c.g_sh = 2 * Dl; c.g_sb = qkv_sb;
-  rc = hip_status(timed(VM_K_DECODE_COMBINE, S(st), [&] { return vm::launch_combine(c, S(st)); }), "gated_attn_decode combine");
-  if (rc || !advance) return rc;
-  return hip_status(timed(VM_K_ADVANCE, S(st), [&] { return vm::launch_advance(positions, B, S(st)); }), "advance");
+  c.advance = advance ? positions : nullptr;
+  return hip_status(timed(VM_K_DECODE_COMBINE, S(st), [&] { return vm::launch_combine(c, S(st)); }), "gated_attn_decode combine");
 }
 
 int vm_advance_positions(int32_t* positions, int B, vm_stream st) {
