@@ -89,11 +89,13 @@ def test_bad_stride_rejected(vm):
 
 def test_decode_scratch_size_and_shortfall(vm):
     lib = vm._lib.load()
-    # B=32, H=16, Hk=4, ctx=32768: the size is partials (G*256 + 2G floats) per split
+    # B=32, H=16, Hk=4: n_splits=8 gives a stream partition of 8*B*Hk waves; one
+    # partial slot (G*256 + 2G floats) per wave plus one per (b, hk) segment, then
+    # a 256-byte completion counter
     n = lib.vm_decode_scratch_bytes(32, 16, 4, 256, 32768, 8)
-    split = -(-(-(-32768 // 8)) // 128) * 128
-    ns = -(-32768 // split)
-    assert n == 32 * 4 * ns * 4 * (256 + 2) * 4
+    slots = 8 * 32 * 4 + 32 * 4
+    body = slots * 4 * (256 + 2) * 4
+    assert n == -(-body // 256) * 256 + 256
     assert lib.vm_decode_scratch_bytes(1, 16, 3, 256, 512, 0) == 0  # invalid GQA -> 0
     rc = lib.vm_decode_attention(_p(FAKE), 256, 4096, _p(FAKE), 256, 4096, _p(FAKE), _p(FAKE),
                                  256, 256 * 512, 256 * 512 * 4, 512, _p(FAKE), 1, 16, 4, 256, 0,
