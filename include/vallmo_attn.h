@@ -18,7 +18,7 @@
  *     its decode step (src/llm/generate.jl:17-27).
  *   - Compiled for head_dim D = 256 and HALF_ROT = 32 (rotary dim 64), the
  *     Qwen3.5 attention facts (src/llm/qwen35.jl:15-23). Other D/HALF_ROT are
- *     rejected with VM_E_UNSUPPORTED. GQA group H/Hk <= 16 for decode.
+ *     rejected with VM_E_UNSUPPORTED. GQA group H/Hk <= 8 for decode.
  */
 #ifndef VALLMO_ATTN_H
 #define VALLMO_ATTN_H
@@ -114,13 +114,19 @@ int vm_knorm_rope_append(vm_bf16* k_cache, vm_bf16* v_cache,
                          int B, int Hk, int D, int half_rot, float eps, float w_offset,
                          vm_stream stream);
 
-/* ---- a5: decode_attention! (src/kernels/attention_decode.jl:268-315) ----
+/* ---- a5: decode_attention! (src/kernels/attention_decode.jl:134-200) ----
  * Split-KV flash-decoding: Q :: (D, H, B) (normalised + rotated), caches as
  * above, lengths[b] = attended keys (cache columns 1..len). O :: (D, H, B).
- * n_splits = 0 chooses the split count from (B, Hk, ctx) to fill 256 CUs;
- * otherwise the reference's split_size = cld(cld(ctx, n_splits), tile)*tile.
- * scratch holds the fp32 split partials; size it with vm_decode_scratch_bytes
- * using the same (B, H, Hk, D, ctx, n_splits).                              */
+ * Work is split as a stream over all token-heads sum_b lengths[b] * Hk: NW
+ * waves each take one contiguous equal chunk (>= 64 keys, a multiple of 16),
+ * so every CU streams the same bytes whatever the length mix. n_splits > 0
+ * gives NW = n_splits * B * Hk (the reference's n_splits per (b, hk) on
+ * average); n_splits = 0 gives NW = 4 waves per CU of the device. The result
+ * does not depend on NW beyond fp32 rounding of the merge.
+ * scratch holds one fp32 partial (G*D values + G (max, sum) pairs) per wave
+ * and per (b, hk) segment, then a 256-byte completion counter; size it with
+ * vm_decode_scratch_bytes using the same (B, H, Hk, D, ctx, n_splits).
+ * H / Hk <= 8.                                                              */
 size_t vm_decode_scratch_bytes(int B, int H, int Hk, int D, int64_t ctx, int n_splits);
 int vm_decode_attention(vm_bf16* o, int64_t o_sh, int64_t o_sb,
                         const vm_bf16* q, int64_t q_sh, int64_t q_sb,

@@ -19,7 +19,7 @@
  *   cache append ............ qknorm_rope_append.jl:82-95, src/llm/qwen35.jl:306-307
  *   attention (mask, GQA,
  *     suffix offset, l==0) .. src/kernels/attention.jl:28-88
- *   decode attention ........ src/kernels/attention_decode.jl:148-266 (unsplit here)
+ *   decode attention ........ src/kernels/attention_decode.jl:14-181 (unsplit here)
  *   sigmoid gate ............ src/kernels/kernels.jl:34, src/llm/qwen35.jl:205,315
  *   decode! / forward ....... src/llm/qwen35.jl:187-208, 292-318
  */

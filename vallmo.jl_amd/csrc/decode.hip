@@ -1,5 +1,5 @@
 // decode.hip — split-KV flash-decoding for one new token per sequence
-// (the work of src/kernels/attention_decode.jl:148-266, re-designed for CDNA4).
+// (the work of src/kernels/attention_decode.jl:14-181, re-designed for CDNA4).
 //
 // Work partition ("stream-K"): the token-heads of the batch, sum_b len_b * Hk,
 // are cut into NW equal contiguous chunks, one per wave, so every wave streams
@@ -313,7 +313,7 @@ void decode_stream_kernel(DecodeArgs a) {
   }
 }
 
-// Log-sum-exp merge of a segment's partials (src/kernels/attention_decode.jl:225-266)
+// Log-sum-exp merge of a segment's partials (src/kernels/attention_decode.jl:91-132)
 // and the sigmoid gate (src/llm/qwen35.jl:205). One workgroup per (16-wide d
 // chunk, head of the group, hk, b); thread (sg, dd) merges slots w_first+sg,
 // +16, ..., then an LDS merge over the 16 groups. With `advance`, the last
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
         Of += sO[i][dd] * c;
       }
     }
-    float out = Lf > 0.f ? Of / Lf : 0.f;  // no valid key: o = 0 (attention_decode.jl:261)
+    float out = Lf > 0.f ? Of / Lf : 0.f;  // no valid key: o = 0 (attention_decode.jl:126-128)
     const int h = hk * a.G + n;
     if (a.gate) out *= sigmoidf(bf2f(a.gate[(int64_t)b * a.g_sb + (int64_t)h * a.g_sh + d]));
     a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = f2bf(out);

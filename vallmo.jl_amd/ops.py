@@ -153,18 +153,20 @@ def attention(Q, K, V, **kw) -> dict:
 
 
 def decode_scratch_bytes(Q, K, *, n_splits=0) -> int:
-    """Scratch the split-KV decode needs (Pol.scratch, attention_decode.jl:320-331)."""
+    """Scratch the split-KV decode needs (Pol.scratch, attention_decode.jl:186-197)."""
     B, H, D = Q.shape
     Hk, L = K.shape[1], K.shape[2]
     return int(_lib.load().vm_decode_scratch_bytes(B, H, Hk, D, L, int(n_splits)))
 
 
 def decode_attention_(outs, Q, K, V, *, lengths, n_splits=0, scratch=None):
-    """Split-KV flash-decoding — src/kernels/attention_decode.jl:268-315.
+    """Split-KV flash-decoding — src/kernels/attention_decode.jl:134-181.
 
     Q :: (Dk, H, Batch) normalised+rotated, K/V :: (Dk, L, Hk, Batch) caches,
-    lengths :: (Batch,) int32 attended keys, O :: (Dv, H, Batch). n_splits = 0
-    sizes the split grid for the 256 CUs (the reference's default is 8 splits);
+    lengths :: (Batch,) int32 attended keys, O :: (Dv, H, Batch). The keys of
+    all (sequence, kv-head) pairs form one stream cut into equal chunks, one per
+    wave: n_splits = 0 uses 4 waves per CU, n_splits > 0 uses n_splits waves per
+    (sequence, kv-head) on average (the reference's default is 8 fixed splits);
     ``scratch`` is a uint8 GPU tensor of >= decode_scratch_bytes (allocated if None).
     """
     O = _out(outs)
@@ -188,7 +190,7 @@ def decode_attention_(outs, Q, K, V, *, lengths, n_splits=0, scratch=None):
 
 
 def decode_attention(Q, K, V, *, lengths, **kw) -> dict:
-    """Allocating decode attention (attention_decode.jl:317-334): returns {"O": O}."""
+    """Allocating decode attention (attention_decode.jl:183-184, 200): returns {"O": O}."""
     O = torch.empty((Q.shape[0], Q.shape[1], V.shape[-1]), dtype=Q.dtype, device=Q.device)
     return decode_attention_({"O": O}, Q, K, V, lengths=lengths, **kw)
 
