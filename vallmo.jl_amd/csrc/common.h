@@ -45,6 +45,13 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) {
 __device__ __forceinline__ uint4 load16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
+// Streaming 16-byte load with the non-temporal hint: data read exactly once
+// (decode K/V) should not displace reused lines in L2 / MALL.
+__device__ __forceinline__ uint4 load16_nt(const void* p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
 __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
   f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xffff0000u);
   f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xffff0000u);
@@ -75,6 +82,18 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* lds_ptr) {
   s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) s16x4*)(lds_ptr));
   return __builtin_bit_cast(uint2, r);
+}
+
+// LDS tiles of 512-byte rows (one D = 256 bf16 row each) keep 16-byte chunk c of
+// row r at chunk c ^ swz(r): the 8 rows that one b128 read cycle touches then
+// fall on distinct banks for the MFMA operand reads.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (they complete in issue order); used to consume direct global->LDS loads.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 __device__ __forceinline__ float wave_max_xor(float v, int mask) {

@@ -53,6 +53,17 @@ __device__ __forceinline__ int clamp_len(const int32_t* lengths, int b, int64_t 
   return (int)l;
 }
 
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// lengths[b] for a wave-uniform b through a scalar load: unlike a vector load it
+// is not counted by vmcnt, so reading it does not drain the K/V loads in flight.
+// (lengths is only read by this kernel.)
+__device__ __forceinline__ int sload_len(const int32_t* lengths, int b) {
+  const int32_t* p = lengths + uniform(b);
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return v;
+}
+
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -66,12 +77,40 @@ struct StepBuf {
   uint4 k[8], v[8];
 };
 
-__device__ __forceinline__ void load_step(StepBuf& s, const uint16_t* kb, const uint16_t* vb,
-                                          int64_t row, int64_t c_st) {
+// Per-wave LDS ring: DSLOTS slots of one 16-token step, K then V, each 16 rows of
+// 512 B with chunk c of row r at c ^ swz(r).
+constexpr int DSLOTS = 2;
+constexpr int STEP_ELEMS = DSTEP * HEAD_DIM;  // bf16 per K (or V) step: 8 KB
+
+// Issue the direct global->LDS loads of tokens [t, t + 16) of one (b, hk):
+// instruction u moves rows t+2u and t+2u+1 (1 KB contiguous per instruction,
+// non-temporal), 8 for K and 8 for V. Rows past `last` re-read row `last`.
+__device__ __forceinline__ void issue_step(uint16_t* lk, uint16_t* lv, const uint16_t* kb,
+                                           const uint16_t* vb, int t, int64_t last,
+                                           int64_t c_st, int lane) {
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) s.k[kk] = load16(kb + row * c_st + 32 * kk);
+  for (int u = 0; u < 8; ++u) {
+    const int r = 2 * u + (lane >> 5);
+    const int64_t row = min((int64_t)(t + r), last);
+    const int64_t off = row * c_st + 8 * ((lane & 31) ^ swz(r));
+    __builtin_amdgcn_global_load_lds(kb + off, (__attribute__((address_space(3))) void*)(lk + 512 * u),
+                                     16, 0, 2);
+    __builtin_amdgcn_global_load_lds(vb + off, (__attribute__((address_space(3))) void*)(lv + 512 * u),
+                                     16, 0, 2);
+  }
+}
+
+// MFMA operand layout from a landed slot: lane (n, g) chunk kk = row n, dims
+// 32kk + 8g .. +7.
+__device__ __forceinline__ void read_step(StepBuf& s, const uint16_t* lk, const uint16_t* lv,
+                                          int n, int g) {
+  const int sw = swz(n);
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) s.v[kk] = load16(vb + row * c_st + 32 * kk);
+  for (int kk = 0; kk < 8; ++kk) {
+    const int off = n * HEAD_DIM + 8 * ((4 * kk + g) ^ sw);
+    s.k[kk] = *reinterpret_cast<const uint4*>(lk + off);
+    s.v[kk] = *reinterpret_cast<const uint4*>(lv + off);
+  }
 }
 
 __device__ __forceinline__ void compute_step(StepBuf& s, int t, int hi, int n, int g,
@@ -124,6 +163,123 @@ __device__ __forceinline__ void compute_step(StepBuf& s, int t, int hi, int n, i
   }
 }
 
+// The new token's cache row (knorm_rope_append_fwd, src/kernels/qknorm_rope_append.jl:59-98),
+// built in the StepBuf layout of one 16-token step (every lane n holds the same
+// row: lane (n, g) chunk kk = dims 32kk + 8g .. +7) and written to cache row
+// `row` of (b, hk) by the lanes n == 0.
+__device__ __forceinline__ void append_row(StepBuf& s, const DecodeArgs& a, int b, int hk,
+                                           int row, int n, int g) {
+  const uint16_t* kr = a.k_new + (int64_t)b * a.new_sb + (int64_t)hk * a.new_sh + 8 * g;
+  const uint16_t* vr = a.v_new + (int64_t)b * a.new_sb + (int64_t)hk * a.new_sh + 8 * g;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    s.k[kk] = load16(kr + 32 * kk);
+    s.v[kk] = load16(vr + 32 * kk);
+  }
+  // transformed in place, a chunk at a time (few live floats)
+  float ss = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    float x[8];
+    unpack8(s.k[kk], x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+  }
+  ss += __shfl_xor(ss, 16, 64);
+  ss += __shfl_xor(ss, 32, 64);
+  const float r = 1.0f / sqrtf(ss * (1.0f / HEAD_DIM) + a.eps);
+  {
+    // chunks 0 and 1 hold the rotate-half pairs (d, d + 32), d = 8g + j
+    float x1[8], x2[8], w1[8], w2[8];
+    unpack8(s.k[0], x1);
+    unpack8(s.k[1], x2);
+    unpack8(load16(a.kw + 8 * g), w1);
+    unpack8(load16(a.kw + 32 + 8 * g), w2);
+    const float* cs = a.cos_tab + (int64_t)row * HALF_ROT + 8 * g;
+    const float* sn = a.sin_tab + (int64_t)row * HALF_ROT + 8 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float c = cs[j], si = sn[j];
+      const float u1 = x1[j] * r * (w1[j] + a.w_offset), u2 = x2[j] * r * (w2[j] + a.w_offset);
+      x1[j] = u1 * c - u2 * si;
+      x2[j] = u2 * c + u1 * si;
+    }
+    s.k[0] = pack8(x1);
+    s.k[1] = pack8(x2);
+  }
+#pragma unroll
+  for (int kk = 2; kk < 8; ++kk) {
+    float x[8], wf[8];
+    unpack8(s.k[kk], x);
+    unpack8(load16(a.kw + 32 * kk + 8 * g), wf);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = x[j] * r * (wf[j] + a.w_offset);
+    s.k[kk] = pack8(x);
+  }
+  if (n == 0) {
+    const int64_t off = (int64_t)b * a.c_sb + (int64_t)hk * a.c_sh + (int64_t)row * a.c_st + 8 * g;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      *reinterpret_cast<uint4*>(a.kc + off + 32 * kk) = s.k[kk];
+      *reinterpret_cast<uint4*>(a.vc + off + 32 * kk) = s.v[kk];
+    }
+  }
+}
+
+// One (b, hk) segment of a wave's chunk: its tokens [lo, hi) (a suffix of the
+// previous segment's end); hm = hi - 1 when the wave appends the new token.
+struct Seg {
+  int b, hk, len, seg_b_start;
+  int raw;  // lengths[b] as passed (may exceed ctx)
+  int lo, hi, hm;
+  bool append;
+};
+
+__device__ __forceinline__ void seg_bounds(Seg& s, int pos, int gw1, const DecodeArgs& a,
+                                           bool fused) {
+  const int seg_start = s.seg_b_start + s.hk * s.len;
+  s.lo = pos - seg_start;
+  s.hi = min(gw1 - seg_start, s.len);
+  // fused append: the one wave whose range ends the segment makes row len-1
+  // from the raw projection (in contract only: lengths[b] <= ctx)
+  s.append = fused && a.k_new != nullptr && s.hi == s.len && s.raw <= a.ctx;
+  s.hm = s.append ? s.hi - 1 : s.hi;
+}
+
+// Move to the next non-empty segment of the chunk; false when the chunk ends.
+__device__ __forceinline__ bool seg_next(Seg& s, int gw1, const DecodeArgs& a, bool fused) {
+  const int pos = s.seg_b_start + s.hk * s.len + s.hi;
+  if (pos >= gw1) return false;
+  if (++s.hk == a.Hk) {
+    s.hk = 0;
+    s.seg_b_start += a.Hk * s.len;
+    do {
+      ++s.b;
+      s.raw = sload_len(a.lengths, s.b);
+      s.len = s.raw < 0 ? 0 : (s.raw > a.ctx ? (int)a.ctx : s.raw);
+    } while (s.len == 0 && s.b + 1 < a.B);
+  }
+  seg_bounds(s, pos, gw1, a, fused);
+  return true;
+}
+
+// Issue side of the step pipeline: the next 16-token step of the chunk.
+struct Issuer {
+  Seg s;
+  int t;
+  __device__ __forceinline__ bool next(uint16_t* slot, const DecodeArgs& a, int gw1, int64_t last,
+                                       int lane, bool fused) {
+    while (t >= s.hm) {
+      if (!seg_next(s, gw1, a, fused)) return false;
+      t = s.lo;
+    }
+    const int64_t base = (int64_t)s.b * a.c_sb + (int64_t)s.hk * a.c_sh;
+    issue_step(slot, slot + STEP_ELEMS, a.kc + base, a.vc + base, t, last, a.c_st, lane);
+    t += DSTEP;
+    return true;
+  }
+};
+
 template <bool FUSED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void decode_stream_kernel(DecodeArgs a) {
@@ -141,7 +297,7 @@ void decode_stream_kernel(DecodeArgs a) {
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
     W += v;
   }
-  W *= Hk;
+  W = uniform(W * Hk);
   const int chunk = stream_chunk(W, a.NW, a.min_chunk);
   const int gw0 = w * chunk;
   if (gw0 >= W) return;
@@ -164,8 +320,11 @@ void decode_stream_kernel(DecodeArgs a) {
       pre = __shfl(incl, 63, 64);
     }
   }
-  int len = clamp_len(a.lengths, b, a.ctx);
-  int hk = (gw0 - seg_b_start) / len;
+  b = uniform(b);
+  seg_b_start = uniform(seg_b_start);
+  const int raw = a.lengths[b];
+  const int len = raw < 0 ? 0 : (raw > a.ctx ? (int)a.ctx : raw);
+  const int hk = (gw0 - seg_b_start) / len;
 
   // 0/1 selection operands for the V transpose: Sel_h[8g+j][n] = (8g+j == n+16h)
   uint4 sel[2];
@@ -193,19 +352,36 @@ void decode_stream_kernel(DecodeArgs a) {
     kbound = 16.0f * wm * 1.01f;
   }
 
-  int pos = gw0;
-  while (true) {
-    const int seg_start = seg_b_start + hk * len;
-    const int lo = pos - seg_start;
-    const int hi = min(gw1 - seg_start, len);
+  // ---- one continuous 16-token step pipeline over the segments of the chunk:
+  // the issue side runs DSLOTS steps ahead of the compute side and crosses
+  // segment boundaries on its own, so a new segment starts with its first
+  // steps already in flight
+  // one __shared__ object per ring slot: the compiler then sees that reads of one
+  // slot do not alias the loads still landing in the other
+  __shared__ __attribute__((aligned(16))) uint16_t ring0[4][2 * STEP_ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t ring1[4][2 * STEP_ELEMS];
+  uint16_t* const r0 = ring0[threadIdx.x >> 6];
+  uint16_t* const r1 = ring1[threadIdx.x >> 6];
+  const int64_t last = a.ctx - 1;
 
+  Seg cs;  // compute side
+  cs.b = b; cs.hk = hk; cs.len = len; cs.seg_b_start = seg_b_start; cs.raw = raw;
+  seg_bounds(cs, gw0, gw1, a, FUSED);
+  Issuer is;  // issue side, DSLOTS steps ahead
+  is.s = cs;
+  is.t = cs.lo;
+  int ct = cs.lo, inflight = 0, cslot = 0;
+  if (is.next(r0, a, gw1, last, lane, FUSED)) ++inflight;
+  if (is.next(r1, a, gw1, last, lane, FUSED)) ++inflight;
+
+  while (true) {
     // ---- Q operand for (b, hk): lane (n, g) holds q[head n][32kk + 8g + j] / 16
     uint4 qop[8];
     float qn2 = 0.f;
     {
       const int nn = n < G ? n : 0;
       const uint16_t* qp =
-          a.q + (int64_t)b * a.q_sb + (int64_t)(hk * G + nn) * a.q_sh + 8 * g;
+          a.q + (int64_t)cs.b * a.q_sb + (int64_t)(cs.hk * G + nn) * a.q_sh + 8 * g;
       float x[8][8];
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) unpack8(load16(qp + 32 * kk), x[kk]);
@@ -226,12 +402,12 @@ void decode_stream_kernel(DecodeArgs a) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) x[kk][j] = x[kk][j] * r * (wf[j] + a.w_offset);
         }
-        const int p = len - 1;  // fused decode: lengths are the positions
-        const float* cs = a.cos_tab + (int64_t)p * HALF_ROT + 8 * g;
-        const float* sn = a.sin_tab + (int64_t)p * HALF_ROT + 8 * g;
+        const int p = cs.len - 1;  // fused decode: lengths are the positions
+        const float* cp = a.cos_tab + (int64_t)p * HALF_ROT + 8 * g;
+        const float* sp = a.sin_tab + (int64_t)p * HALF_ROT + 8 * g;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float c = cs[j], si = sn[j];
+          const float c = cp[j], si = sp[j];
           const float x1 = x[0][j], x2 = x[1][j];
           x[0][j] = x1 * c - x2 * si;
           x[1][j] = x2 * c + x1 * si;
@@ -251,43 +427,52 @@ void decode_stream_kernel(DecodeArgs a) {
       qn2 += __shfl_xor(qn2, 32, 64);
     }
     float m_run = -INFINITY;
-    bool use_static = false;
     if (FUSED) {
       const float bound = sqrtf(qn2) * 1.01f * kbound * LOG2E;
-      use_static = __ballot(n < G && !(bound <= D_STATIC_LIMIT)) == 0ull;
-      if (use_static) m_run = bound;
+      if (__ballot(n < G && !(bound <= D_STATIC_LIMIT)) == 0ull) m_run = bound;
     }
 
-    // ---- stream tokens [lo, hi) of (b, hk), double-buffered 16-token steps
+    // ---- stream tokens [lo, hm) of (b, hk)
     f32x4 acc[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     float l_part = 0.f;
-    const uint16_t* kb = a.kc + (int64_t)b * a.c_sb + (int64_t)hk * a.c_sh + 8 * g;
-    const uint16_t* vb = a.vc + (int64_t)b * a.c_sb + (int64_t)hk * a.c_sh + 8 * g;
-    const int64_t last = a.ctx - 1;
-    // three register stages: two 16-token steps in flight while one computes;
-    // one loop for both shifts (with the static bound m_run never moves)
-    StepBuf s0, s1, s2;
-    load_step(s0, kb, vb, min((int64_t)(lo + n), last), a.c_st);
-    if (lo + DSTEP < hi) load_step(s1, kb, vb, min((int64_t)(lo + DSTEP + n), last), a.c_st);
-    for (int t = lo; t < hi; t += 3 * DSTEP) {
-      if (t + 2 * DSTEP < hi)
-        load_step(s2, kb, vb, min((int64_t)(t + 2 * DSTEP + n), last), a.c_st);
-      compute_step(s0, t, hi, n, g, qop, sel, acc, m_run, l_part);
-      if (t + 3 * DSTEP < hi)
-        load_step(s0, kb, vb, min((int64_t)(t + 3 * DSTEP + n), last), a.c_st);
-      if (t + DSTEP < hi) compute_step(s1, t + DSTEP, hi, n, g, qop, sel, acc, m_run, l_part);
-      if (t + 4 * DSTEP < hi)
-        load_step(s1, kb, vb, min((int64_t)(t + 4 * DSTEP + n), last), a.c_st);
-      if (t + 2 * DSTEP < hi)
-        compute_step(s2, t + 2 * DSTEP, hi, n, g, qop, sel, acc, m_run, l_part);
+    // one 16-token step from ring slot `slot` (inlined per slot: the two slots are
+    // distinct LDS objects in the generated code)
+    auto step = [&](uint16_t* slot) __attribute__((always_inline)) {
+      // the oldest step in flight is this one; the 16 loads of a later step may stay out
+      if (inflight >= 2) wait_vmcnt<16>(); else wait_vmcnt<0>();
+      StepBuf sb;
+      read_step(sb, slot, slot + STEP_ELEMS, n, g);
+      --inflight;
+      // the slot is free once its reads have returned; refill it
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (is.next(slot, a, gw1, last, lane, FUSED)) ++inflight;
+      compute_step(sb, ct, cs.hm, n, g, qop, sel, acc, m_run, l_part);
+      ct += DSTEP;
+    };
+    if (cslot == 1 && ct < cs.hm) {
+      step(r1);
+      cslot = 0;
+    }
+    while (ct < cs.hm) {
+      step(r0);
+      cslot = 1;
+      if (ct >= cs.hm) break;
+      step(r1);
+      cslot = 0;
+    }
+    if (cs.append) {
+      // the new token as a one-row step (rows n >= 1 are masked)
+      StepBuf sb;
+      append_row(sb, a, cs.b, cs.hk, cs.hi - 1, n, g);
+      compute_step(sb, cs.hi - 1, cs.hi, n, g, qop, sel, acc, m_run, l_part);
     }
 
     // ---- partial for (w, segment): slot w + b*Hk + hk
     float l_tot = l_part + __shfl_xor(l_part, 16, 64);
     l_tot += __shfl_xor(l_tot, 32, 64);
-    const int64_t slot = (int64_t)w + (int64_t)b * Hk + hk;
+    const int64_t slot = (int64_t)w + (int64_t)cs.b * Hk + cs.hk;
     if (n < G) {
       float* dst = a.part_o + (slot * G + n) * HEAD_DIM + 4 * g;
 #pragma unroll
@@ -299,82 +484,112 @@ void decode_stream_kernel(DecodeArgs a) {
         a.part_ml[2 * (slot * G + n) + 1] = l_tot;
       }
     }
-
-    pos = seg_start + hi;
-    if (pos >= gw1) break;
-    if (++hk == Hk) {  // next sequence with a non-empty cache
-      hk = 0;
-      seg_b_start += Hk * len;
-      do {
-        ++b;
-        len = clamp_len(a.lengths, b, a.ctx);
-      } while (len == 0 && b + 1 < a.B);
-    }
+    if (!seg_next(cs, gw1, a, FUSED)) break;
+    ct = cs.lo;
   }
+  wait_vmcnt<0>();  // no LDS load may land after the wave is gone
 }
 
 // Log-sum-exp merge of a segment's partials (src/kernels/attention_decode.jl:91-132)
-// and the sigmoid gate (src/llm/qwen35.jl:205). One workgroup per (16-wide d
-// chunk, head of the group, hk, b); thread (sg, dd) merges slots w_first+sg,
-// +16, ..., then an LDS merge over the 16 groups. With `advance`, the last
-// workgroup to finish bumps positions[b] (src/llm/generate.jl:82-88).
+// and the sigmoid gate (src/llm/qwen35.jl:205). One workgroup per (64-wide d
+// range, head n of the group, hk, b). Thread (sg, dq) merges slots w_first+sg,
+// +16, ... of its float4 column, CM slots per batch with every load issued
+// before the merge arithmetic; the 16 slot groups then merge through LDS.
+// With `advance`, the last workgroup to finish bumps positions[b]
+// (src/llm/generate.jl:82-88).
+constexpr int CM = 8;
+
 __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
-  const int chunk16 = blockIdx.x & 15, n = blockIdx.x >> 4, hk = blockIdx.y, b = blockIdx.z;
-  const int sg = threadIdx.x >> 4, dd = threadIdx.x & 15;
-  const int d = chunk16 * 16 + dd;
+  const int dr = blockIdx.x & 3, n = blockIdx.x >> 2, hk = blockIdx.y, b = blockIdx.z;
+  const int t = threadIdx.x, lane = t & 63;
+  const int sg = t >> 4, dq = t & 15;
+  const int d = dr * 64 + 4 * dq;
+  // stream geometry (as in decode_stream_kernel): total token-heads and b's prefix
   int W = 0, pre_b = 0;
-  for (int i = 0; i < a.B; ++i) {
-    const int l = clamp_len(a.lengths, i, a.ctx);
-    W += l;
-    if (i < b) pre_b += l;
+  for (int b0 = 0; b0 < a.B; b0 += 64) {
+    const int i = b0 + lane;
+    const int l = i < a.B ? clamp_len(a.lengths, i, a.ctx) : 0;
+    int v = l, u = i < b ? l : 0;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      v += __shfl_xor(v, o, 64);
+      u += __shfl_xor(u, o, 64);
+    }
+    W += v;
+    pre_b += u;
   }
   W *= a.Hk;
   const int len = clamp_len(a.lengths, b, a.ctx);
   const int seg_start = pre_b * a.Hk + hk * len;
   const int chunk = stream_chunk(W, a.NW, a.min_chunk);
-  float M = -INFINITY, L = 0.f, O = 0.f;
+  float M = -INFINITY, L = 0.f;
+  float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
   if (len > 0) {
     const int w_first = seg_start / chunk, w_last = (seg_start + len - 1) / chunk;
     const int64_t base = (int64_t)b * a.Hk + hk;
-    for (int w = w_first + sg; w <= w_last; w += 16) {
-      const int64_t r = (w + base) * a.G + n;
-      const float m = a.part_ml[2 * r], l = a.part_ml[2 * r + 1];
-      const float o = a.part_o[r * HEAD_DIM + d];
-      const float mn = fmaxf(M, m);
-      const float c1 = fast_exp2(M - mn), c2 = fast_exp2(m - mn);
-      L = L * c1 + l * c2;
-      O = O * c1 + o * c2;
-      M = mn;
+    for (int w0 = w_first + sg; w0 <= w_last; w0 += 16 * CM) {
+      float2 ml[CM];
+      float4 o[CM];
+#pragma unroll
+      for (int u = 0; u < CM; ++u) {
+        const int w = w0 + 16 * u;
+        if (w <= w_last) {
+          const int64_t r = (w + base) * a.G + n;
+          ml[u] = *reinterpret_cast<const float2*>(a.part_ml + 2 * r);
+          o[u] = *reinterpret_cast<const float4*>(a.part_o + r * HEAD_DIM + d);
+        } else {
+          ml[u] = make_float2(-INFINITY, 0.f);
+          o[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < CM; ++u) {
+        const float mn = fmaxf(M, ml[u].x);
+        const float c1 = M == mn ? 1.0f : fast_exp2(M - mn);
+        const float c2 = ml[u].x == mn ? 1.0f : fast_exp2(ml[u].x - mn);
+        L = L * c1 + ml[u].y * c2;
+        O.x = O.x * c1 + o[u].x * c2;
+        O.y = O.y * c1 + o[u].y * c2;
+        O.z = O.z * c1 + o[u].z * c2;
+        O.w = O.w * c1 + o[u].w * c2;
+        M = mn;
+      }
     }
   }
-  __shared__ float sM[16][16], sL[16][16], sO[16][16];
-  sM[sg][dd] = M;
-  sL[sg][dd] = L;
-  sO[sg][dd] = O;
+  __shared__ float sM[16], sL[16];
+  __shared__ float4 sO[16][16];
+  if (dq == 0) {
+    sM[sg] = M;
+    sL[sg] = L;
+  }
+  sO[sg][dq] = O;
   __syncthreads();
-  if (sg == 0) {
+  if (t < 64) {
+    // thread t finishes d = dr*64 + t
     float Mf = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) Mf = fmaxf(Mf, sM[i][dd]);
+    for (int i = 0; i < 16; ++i) Mf = fmaxf(Mf, sM[i]);
     float Lf = 0.f, Of = 0.f;
     if (Mf > -INFINITY) {
+      const float* so = reinterpret_cast<const float*>(&sO[0][0]);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float c = fast_exp2(sM[i][dd] - Mf);
-        Lf += sL[i][dd] * c;
-        Of += sO[i][dd] * c;
+        const float c = fast_exp2(sM[i] - Mf);
+        Lf += sL[i] * c;
+        Of += so[i * 64 + t] * c;
       }
     }
     float out = Lf > 0.f ? Of / Lf : 0.f;  // no valid key: o = 0 (attention_decode.jl:126-128)
     const int h = hk * a.G + n;
-    if (a.gate) out *= sigmoidf(bf2f(a.gate[(int64_t)b * a.g_sb + (int64_t)h * a.g_sh + d]));
-    a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = f2bf(out);
+    const int dd = dr * 64 + t;
+    if (a.gate) out *= sigmoidf(bf2f(a.gate[(int64_t)b * a.g_sb + (int64_t)h * a.g_sh + dd]));
+    a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + dd] = f2bf(out);
   }
   if (a.advance) {
     // every workgroup has read lengths (== positions) above; the last one to
     // arrive advances the clock
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (t == 0) {
       __threadfence();
       const int total = (int)(gridDim.x * gridDim.y * gridDim.z);
       const int prev = atomicAdd(a.counter, 1);
@@ -413,7 +628,7 @@ hipError_t launch_decode(const DecodeArgs& a, bool fused_q, hipStream_t st) {
 
 hipError_t launch_combine(const CombineArgs& a, hipStream_t st) {
   if (a.B == 0 || a.Hk == 0) return hipSuccess;
-  dim3 grid(16 * a.G, a.Hk, a.B);
+  dim3 grid(4 * a.G, a.Hk, a.B);
   hipLaunchKernelGGL(decode_combine_kernel, grid, dim3(256), 0, st, a);
   return hipGetLastError();
 }

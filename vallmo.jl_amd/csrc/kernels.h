@@ -37,10 +37,15 @@ struct DecodeArgs {
   const float* cos_tab;
   const float* sin_tab;
   float eps, w_offset;
-  const uint16_t* kc;
-  const uint16_t* vc;
+  uint16_t* kc;          // written only at the appended row (fused, k_new set)
+  uint16_t* vc;
   int64_t c_st, c_sh, c_sb, ctx;
   const int32_t* lengths;
+  // fused only (nullable): raw k / v of the new token, (D, Hk, B) with strides
+  // (new_sh, new_sb); normed + rotated k and v go to cache row lengths[b]-1
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  int64_t new_sh, new_sb;
   float* part_o;        // [slots][G][256], slots = NW + B*Hk
   float* part_ml;       // [slots][G][2]  (shift m in log2 units, sum l)
   int B, Hk, G;

@@ -38,13 +38,6 @@ constexpr int TILE = PF_BN * HEAD_DIM;       // bf16 per K (or V) tile: 16 KB
 constexpr float RESCALE_SLACK = 8.0f;
 constexpr float STATIC_MAX_LIMIT = 64.0f;
 
-// chunk swizzle: 16-byte chunk c of tile row r lives at chunk c ^ swz(r)
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 // Workgroup barrier without the release/acquire fences of __syncthreads(): those
 // would wait for every outstanding load (vmcnt(0)), including the tiles still in
 // flight. LDS visibility is established by each wave's explicit vmcnt wait on its

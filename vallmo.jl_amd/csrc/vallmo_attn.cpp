@@ -323,7 +323,9 @@ int vm_decode_attention(vm_bf16* o, int64_t o_sh, int64_t o_sb, const vm_bf16* q
   TRY(decode_common(a, c, scratch, scratch_bytes, B, H, Hk, ctx, n_splits));
   if (B == 0) return VM_OK;
   a.q = q; a.q_sh = q_sh; a.q_sb = q_sb;
-  a.kc = kc; a.vc = vc; a.c_st = c_st; a.c_sh = c_sh; a.c_sb = c_sb;
+  // read-only here: the unfused operator appends nothing (k_new stays NULL)
+  a.kc = const_cast<uint16_t*>(kc); a.vc = const_cast<uint16_t*>(vc);
+  a.c_st = c_st; a.c_sh = c_sh; a.c_sb = c_sb;
   a.lengths = lengths;
   int rc = hip_status(timed(VM_K_DECODE_SPLIT, S(st), [&] { return vm::launch_decode(a, false, S(st)); }), "decode_attention split");
   if (rc) return rc;
@@ -358,6 +360,7 @@ int vm_gated_attn_decode(vm_bf16* out, int64_t out_sb, const vm_bf16* qkv, int64
   TRY(check_aligned(kc, "K_cache"));
   TRY(check_aligned(vc, "V_cache"));
   TRY(check_aligned(qw, "qw"));
+  TRY(check_aligned(kw, "kw"));
   for (int64_t s : {out_sb, qkv_sb, c_st, c_sh, c_sb}) TRY(check_stride(s, "gated_attn_decode"));
   REQUIRE(qkv_sb >= (int64_t)(2 * Hq + 2 * Hk) * D || B <= 1, VM_E_DIM,
           "gated_attn_decode: qkv batch stride %lld < (2Hq+2Hk)*D = %lld", (long long)qkv_sb,
@@ -367,20 +370,16 @@ int vm_gated_attn_decode(vm_bf16* out, int64_t out_sb, const vm_bf16* qkv, int64
   TRY(decode_common(a, c, scratch, scratch_bytes, B, Hq, Hk, ctx, n_splits));
   if (B == 0) return VM_OK;
   const int64_t Dl = D;
-  // a4: K/V of the new token into the cache (the split kernel then reads it)
-  vm::RowArgs r{};
-  r.in = qkv + 2 * Hq * Dl; r.in2 = qkv + (2 * Hq + Hk) * Dl; r.in_sh = Dl; r.in_sb = qkv_sb;
-  r.out = kc; r.out2 = vc; r.out_st = c_st; r.out_sh = c_sh; r.out_sb = c_sb;
-  r.w = kw; r.cos_tab = cs; r.sin_tab = sn; r.ctx = ctx; r.positions = positions;
-  r.B = B; r.H = Hk; r.T = 1; r.out_at_pos = 1; r.eps = eps; r.w_offset = w_offset;
-  int rc = hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_norm_rope_rows(r, S(st)); }), "gated_attn_decode append");
-  if (rc) return rc;
-  // a3 + a5: split-KV attention with the q norm+RoPE prologue fused
+  // a3 + a4 + a5: split-KV attention with the q norm+RoPE prologue fused; the
+  // wave that covers each (b, hk)'s last token builds the new K/V row from the
+  // raw projection, attends it and writes it to cache column positions[b]
   a.q = qkv; a.q_sh = 2 * Dl; a.q_sb = qkv_sb;
   a.qw = qw; a.kw = kw; a.cos_tab = cs; a.sin_tab = sn; a.eps = eps; a.w_offset = w_offset;
   a.kc = kc; a.vc = vc; a.c_st = c_st; a.c_sh = c_sh; a.c_sb = c_sb;
   a.lengths = positions;
-  rc = hip_status(timed(VM_K_DECODE_SPLIT, S(st), [&] { return vm::launch_decode(a, true, S(st)); }), "gated_attn_decode split");
+  a.k_new = qkv + 2 * Hq * Dl; a.v_new = qkv + (2 * Hq + Hk) * Dl;
+  a.new_sh = Dl; a.new_sb = qkv_sb;
+  int rc = hip_status(timed(VM_K_DECODE_SPLIT, S(st), [&] { return vm::launch_decode(a, true, S(st)); }), "gated_attn_decode split");
   if (rc) return rc;
   // a5 merge + a6 gate, written as the Wo input (D, Hq, B); a12 advance fused
   c.lengths = positions; c.out = out; c.o_sh = Dl; c.o_sb = out_sb;
