@@ -124,7 +124,8 @@ int vm_knorm_rope_append(vm_bf16* k_cache, vm_bf16* v_cache,
  * average); n_splits = 0 gives NW = 4 waves per CU of the device. The result
  * does not depend on NW beyond fp32 rounding of the merge.
  * scratch holds one fp32 partial (G*D values + G (max, sum) pairs) per wave
- * and per (b, hk) segment, then a 256-byte completion counter; size it with
+ * and per (b, hk) segment, then a snapshot of the partition (1 + 2B int32
+ * in whole 256-byte blocks) that the merge reads instead of lengths; size it with
  * vm_decode_scratch_bytes using the same (B, H, Hk, D, ctx, n_splits).
  * H / Hk <= 8.                                                              */
 size_t vm_decode_scratch_bytes(int B, int H, int Hk, int D, int64_t ctx, int n_splits);

@@ -91,11 +91,11 @@ def test_decode_scratch_size_and_shortfall(vm):
     lib = vm._lib.load()
     # B=32, H=16, Hk=4: n_splits=8 gives a stream partition of 8*B*Hk waves; one
     # partial slot (G*256 + 2G floats) per wave plus one per (b, hk) segment, then
-    # a 256-byte completion counter
+    # the partition snapshot (1 + 2B int32) in its own 256-byte blocks
     n = lib.vm_decode_scratch_bytes(32, 16, 4, 256, 32768, 8)
     slots = 8 * 32 * 4 + 32 * 4
     body = slots * 4 * (256 + 2) * 4
-    assert n == -(-body // 256) * 256 + 256
+    assert n == -(-body // 256) * 256 + -(-(1 + 2 * 32) * 4 // 256) * 256
     assert lib.vm_decode_scratch_bytes(1, 16, 3, 256, 512, 0) == 0  # invalid GQA -> 0
     rc = lib.vm_decode_attention(_p(FAKE), 256, 4096, _p(FAKE), 256, 4096, _p(FAKE), _p(FAKE),
                                  256, 256 * 512, 256 * 512 * 4, 512, _p(FAKE), 1, 16, 4, 256, 0,

@@ -287,8 +287,6 @@ void decode_stream_kernel(DecodeArgs a) {
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int G = a.G, Hk = a.Hk;
-  if (a.counter && blockIdx.x == 0 && threadIdx.x == 0) a.counter[0] = 0;  // for the merge
-
   // ---- stream partition: total work and this wave's chunk [gw0, gw1)
   int W = 0;
   for (int b0 = 0; b0 < a.B; b0 += 64) {
@@ -299,6 +297,22 @@ void decode_stream_kernel(DecodeArgs a) {
   }
   W = uniform(W * Hk);
   const int chunk = stream_chunk(W, a.NW, a.min_chunk);
+  if (w == 0) {
+    // snapshot of the partition for the merge, which then never reads lengths
+    // (so it may advance them): chunk, then per sequence its clamped length and
+    // first token-head
+    int pre = 0;
+    for (int b0 = 0; b0 < a.B; b0 += 64) {
+      const int l = (b0 + lane < a.B) ? clamp_len(a.lengths, b0 + lane, a.ctx) : 0;
+      const int incl = wave_incl_scan(l * Hk, lane) + pre;
+      if (b0 + lane < a.B) {
+        a.geom[1 + b0 + lane] = l;
+        a.geom[1 + a.B + b0 + lane] = incl - l * Hk;
+      }
+      pre = __shfl(incl, 63, 64);
+    }
+    if (lane == 0) a.geom[0] = chunk;
+  }
   const int gw0 = w * chunk;
   if (gw0 >= W) return;
   const int gw1 = min(gw0 + chunk, W);
@@ -371,8 +385,7 @@ void decode_stream_kernel(DecodeArgs a) {
   is.s = cs;
   is.t = cs.lo;
   int ct = cs.lo, inflight = 0, cslot = 0;
-  if (is.next(r0, a, gw1, last, lane, FUSED)) ++inflight;
-  if (is.next(r1, a, gw1, last, lane, FUSED)) ++inflight;
+  bool primed = false;
 
   while (true) {
     // ---- Q operand for (b, hk): lane (n, g) holds q[head n][32kk + 8g + j] / 16
@@ -382,9 +395,29 @@ void decode_stream_kernel(DecodeArgs a) {
       const int nn = n < G ? n : 0;
       const uint16_t* qp =
           a.q + (int64_t)cs.b * a.q_sb + (int64_t)(cs.hk * G + nn) * a.q_sh + 8 * g;
+      // every prologue load first; the first K/V steps go out right behind them
+      // (loads return in order: the prologue math then runs under the K/V steps)
+      uint4 qraw[8], qwv[8];
+      float4 cv[2], sv[2];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) qraw[kk] = load16(qp + 32 * kk);
+      if (FUSED) {
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) qwv[kk] = load16(a.qw + 32 * kk + 8 * g);
+        const int64_t p = cs.len - 1;  // fused decode: lengths are the positions
+        const float4* cp = reinterpret_cast<const float4*>(a.cos_tab + p * HALF_ROT + 8 * g);
+        const float4* sp = reinterpret_cast<const float4*>(a.sin_tab + p * HALF_ROT + 8 * g);
+        cv[0] = cp[0]; cv[1] = cp[1];
+        sv[0] = sp[0]; sv[1] = sp[1];
+      }
+      if (!primed) {
+        if (is.next(r0, a, gw1, last, lane, FUSED)) ++inflight;
+        if (is.next(r1, a, gw1, last, lane, FUSED)) ++inflight;
+        primed = true;
+      }
       float x[8][8];
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) unpack8(load16(qp + 32 * kk), x[kk]);
+      for (int kk = 0; kk < 8; ++kk) unpack8(qraw[kk], x[kk]);
       if (FUSED) {
         // qnorm_rope_fwd (src/kernels/qknorm_rope_append.jl:25-57) on the fly
         float ss = 0.f;
@@ -398,19 +431,17 @@ void decode_stream_kernel(DecodeArgs a) {
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
           float wf[8];
-          unpack8(load16(a.qw + 32 * kk + 8 * g), wf);
+          unpack8(qwv[kk], wf);
 #pragma unroll
           for (int j = 0; j < 8; ++j) x[kk][j] = x[kk][j] * r * (wf[j] + a.w_offset);
         }
-        const int p = cs.len - 1;  // fused decode: lengths are the positions
-        const float* cp = a.cos_tab + (int64_t)p * HALF_ROT + 8 * g;
-        const float* sp = a.sin_tab + (int64_t)p * HALF_ROT + 8 * g;
+        const float cf[8] = {cv[0].x, cv[0].y, cv[0].z, cv[0].w, cv[1].x, cv[1].y, cv[1].z, cv[1].w};
+        const float sf[8] = {sv[0].x, sv[0].y, sv[0].z, sv[0].w, sv[1].x, sv[1].y, sv[1].z, sv[1].w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float c = cp[j], si = sp[j];
           const float x1 = x[0][j], x2 = x[1][j];
-          x[0][j] = x1 * c - x2 * si;
-          x[1][j] = x2 * c + x1 * si;
+          x[0][j] = x1 * cf[j] - x2 * sf[j];
+          x[1][j] = x2 * cf[j] + x1 * sf[j];
         }
       }
 #pragma unroll
@@ -437,6 +468,13 @@ void decode_stream_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     float l_part = 0.f;
+    if (cs.append) {
+      // the new token as a one-row step (rows n >= 1 are masked), taken first so
+      // that its loads overlap the K/V steps already in flight
+      StepBuf sb;
+      append_row(sb, a, cs.b, cs.hk, cs.hi - 1, n, g);
+      compute_step(sb, cs.hi - 1, cs.hi, n, g, qop, sel, acc, m_run, l_part);
+    }
     // one 16-token step from ring slot `slot` (inlined per slot: the two slots are
     // distinct LDS objects in the generated code)
     auto step = [&](uint16_t* slot) __attribute__((always_inline)) {
@@ -462,12 +500,6 @@ void decode_stream_kernel(DecodeArgs a) {
       step(r1);
       cslot = 0;
     }
-    if (cs.append) {
-      // the new token as a one-row step (rows n >= 1 are masked)
-      StepBuf sb;
-      append_row(sb, a, cs.b, cs.hk, cs.hi - 1, n, g);
-      compute_step(sb, cs.hi - 1, cs.hi, n, g, qop, sel, acc, m_run, l_part);
-    }
 
     // ---- partial for (w, segment): slot w + b*Hk + hk
     float l_tot = l_part + __shfl_xor(l_part, 16, 64);
@@ -491,48 +523,47 @@ void decode_stream_kernel(DecodeArgs a) {
 }
 
 // Log-sum-exp merge of a segment's partials (src/kernels/attention_decode.jl:91-132)
-// and the sigmoid gate (src/llm/qwen35.jl:205). One workgroup per (64-wide d
-// range, head n of the group, hk, b). Thread (sg, dq) merges slots w_first+sg,
-// +16, ... of its float4 column, CM slots per batch with every load issued
-// before the merge arithmetic; the 16 slot groups then merge through LDS.
-// With `advance`, the last workgroup to finish bumps positions[b]
+// and the sigmoid gate (src/llm/qwen35.jl:205). One workgroup per (DW-wide d
+// range, head n of the group, hk, b); thread (sg, dq) merges slots w_first+sg,
+// +NSG, ... of its float4 column, CM slots per batch with every load issued
+// before the merge arithmetic; the NSG slot groups then merge through LDS.
+// DW = 64 suits many short segments, DW = 16 a few long ones (more workgroups,
+// more slot groups). With `advance`, workgroup 0 bumps positions[b]
 // (src/llm/generate.jl:82-88).
 constexpr int CM = 8;
 
+template <int DW>
 __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
-  const int dr = blockIdx.x & 3, n = blockIdx.x >> 2, hk = blockIdx.y, b = blockIdx.z;
-  const int t = threadIdx.x, lane = t & 63;
-  const int sg = t >> 4, dq = t & 15;
-  const int d = dr * 64 + 4 * dq;
-  // stream geometry (as in decode_stream_kernel): total token-heads and b's prefix
-  int W = 0, pre_b = 0;
-  for (int b0 = 0; b0 < a.B; b0 += 64) {
-    const int i = b0 + lane;
-    const int l = i < a.B ? clamp_len(a.lengths, i, a.ctx) : 0;
-    int v = l, u = i < b ? l : 0;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      v += __shfl_xor(v, o, 64);
-      u += __shfl_xor(u, o, 64);
-    }
-    W += v;
-    pre_b += u;
+  constexpr int NDR = HEAD_DIM / DW;  // d ranges
+  constexpr int NDQ = DW / 4;         // float4 columns per range
+  constexpr int NSG = 256 / NDQ;      // slot groups
+  const int dr = blockIdx.x % NDR, n = blockIdx.x / NDR, hk = blockIdx.y, b = blockIdx.z;
+  const int t = threadIdx.x;
+  const int sg = t / NDQ, dq = t % NDQ;
+  const int d = dr * DW + 4 * dq;
+  if (a.advance && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {
+    // the stream kernel has read every position and this kernel reads none
+    // (it works from the partition snapshot): the clock can move right away
+    for (int i = t; i < a.B; i += 256) a.advance[i] += 1;
   }
-  W *= a.Hk;
-  const int len = clamp_len(a.lengths, b, a.ctx);
-  const int seg_start = pre_b * a.Hk + hk * len;
-  const int chunk = stream_chunk(W, a.NW, a.min_chunk);
+  // partition snapshot written by decode_stream_kernel
+  const int chunk = a.geom[0];
+  const int len = a.geom[1 + b];
+  const int seg_start = a.geom[1 + a.B + b] + hk * len;
+  const int h = hk * a.G + n;
+  float gate = 0.f;  // fetched early: it does not depend on the partials
+  if (a.gate && t < DW) gate = bf2f(a.gate[(int64_t)b * a.g_sb + (int64_t)h * a.g_sh + dr * DW + t]);
   float M = -INFINITY, L = 0.f;
   float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
   if (len > 0) {
     const int w_first = seg_start / chunk, w_last = (seg_start + len - 1) / chunk;
     const int64_t base = (int64_t)b * a.Hk + hk;
-    for (int w0 = w_first + sg; w0 <= w_last; w0 += 16 * CM) {
+    for (int w0 = w_first + sg; w0 <= w_last; w0 += NSG * CM) {
       float2 ml[CM];
       float4 o[CM];
 #pragma unroll
       for (int u = 0; u < CM; ++u) {
-        const int w = w0 + 16 * u;
+        const int w = w0 + NSG * u;
         if (w <= w_last) {
           const int64_t r = (w + base) * a.G + n;
           ml[u] = *reinterpret_cast<const float2*>(a.part_ml + 2 * r);
@@ -556,49 +587,33 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
       }
     }
   }
-  __shared__ float sM[16], sL[16];
-  __shared__ float4 sO[16][16];
+  __shared__ float sM[NSG], sL[NSG];
+  __shared__ float4 sO[NSG][NDQ];
   if (dq == 0) {
     sM[sg] = M;
     sL[sg] = L;
   }
   sO[sg][dq] = O;
   __syncthreads();
-  if (t < 64) {
-    // thread t finishes d = dr*64 + t
+  if (t < DW) {
+    // thread t finishes d = dr*DW + t
     float Mf = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) Mf = fmaxf(Mf, sM[i]);
+#pragma unroll 8
+    for (int i = 0; i < NSG; ++i) Mf = fmaxf(Mf, sM[i]);
     float Lf = 0.f, Of = 0.f;
     if (Mf > -INFINITY) {
       const float* so = reinterpret_cast<const float*>(&sO[0][0]);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
+#pragma unroll 8
+      for (int i = 0; i < NSG; ++i) {
         const float c = fast_exp2(sM[i] - Mf);
         Lf += sL[i] * c;
-        Of += so[i * 64 + t] * c;
+        Of += so[i * DW + t] * c;
       }
     }
     float out = Lf > 0.f ? Of / Lf : 0.f;  // no valid key: o = 0 (attention_decode.jl:126-128)
-    const int h = hk * a.G + n;
-    const int dd = dr * 64 + t;
-    if (a.gate) out *= sigmoidf(bf2f(a.gate[(int64_t)b * a.g_sb + (int64_t)h * a.g_sh + dd]));
+    const int dd = dr * DW + t;
+    if (a.gate) out *= sigmoidf(gate);
     a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + dd] = f2bf(out);
-  }
-  if (a.advance) {
-    // every workgroup has read lengths (== positions) above; the last one to
-    // arrive advances the clock
-    __syncthreads();
-    if (t == 0) {
-      __threadfence();
-      const int total = (int)(gridDim.x * gridDim.y * gridDim.z);
-      const int prev = atomicAdd(a.counter, 1);
-      if (prev == total - 1) {
-        __threadfence();
-        for (int i = 0; i < a.B; ++i) a.advance[i] += 1;
-        a.counter[0] = 0;
-      }
-    }
   }
 }
 
@@ -628,8 +643,13 @@ hipError_t launch_decode(const DecodeArgs& a, bool fused_q, hipStream_t st) {
 
 hipError_t launch_combine(const CombineArgs& a, hipStream_t st) {
   if (a.B == 0 || a.Hk == 0) return hipSuccess;
-  dim3 grid(4 * a.G, a.Hk, a.B);
-  hipLaunchKernelGGL(decode_combine_kernel, grid, dim3(256), 0, st, a);
+  // partials per segment on average: many -> narrow d ranges, more slot groups
+  const bool wide = a.NW >= 32 * a.B * a.Hk;
+  if (wide) {
+    hipLaunchKernelGGL(decode_combine_kernel<16>, dim3(16 * a.G, a.Hk, a.B), dim3(256), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(decode_combine_kernel<64>, dim3(4 * a.G, a.Hk, a.B), dim3(256), 0, st, a);
+  }
   return hipGetLastError();
 }
 

@@ -51,21 +51,20 @@ struct DecodeArgs {
   int B, Hk, G;
   int NW;               // waves of the stream partition (multiple of 4)
   int min_chunk;        // smallest per-wave chunk (token-heads, multiple of 16)
-  int32_t* counter;     // nullable: merge completion counter, zeroed here
+  int32_t* geom;        // partition snapshot for the merge: [chunk | len_b (B) | start_b (B)]
 };
 
 struct CombineArgs {
   const float* part_o;
   const float* part_ml;
-  const int32_t* lengths;
+  const int32_t* geom;   // written by the stream kernel (the merge never reads lengths)
   uint16_t* out;
   int64_t o_sh, o_sb;
   const uint16_t* gate;  // nullable: sigmoid gate logits
   int64_t g_sh, g_sb;
-  int B, Hk, G, NW, min_chunk;
-  int64_t ctx;
-  int32_t* advance;      // nullable: positions to bump once every workgroup has read them
-  int32_t* counter;      // with advance: completion counter (zeroed by the stream kernel)
+  int B, Hk, G;
+  int NW;                // waves of the stream partition (chooses the merge shape)
+  int32_t* advance;      // nullable: positions[b] += 1 (no other merge thread reads them)
 };
 
 struct PrefillArgs {

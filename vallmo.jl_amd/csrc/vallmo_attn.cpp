@@ -112,7 +112,8 @@ size_t decode_part_o_bytes(int B, int Hk, int NW, int G) {
 size_t decode_part_ml_bytes(int B, int Hk, int NW, int G) {
   return decode_slots(B, Hk, NW) * G * 2 * sizeof(float);
 }
-constexpr size_t DECODE_COUNTER_BYTES = 256;  // completion counter, own 256-byte block
+// partition snapshot for the merge: chunk, then len_b and start_b per sequence
+size_t decode_geom_bytes(int B) { return ((size_t)(1 + 2 * B) * sizeof(int32_t) + 255) / 256 * 256; }
 
 }  // namespace
 
@@ -274,7 +275,7 @@ size_t vm_decode_scratch_bytes(int B, int H, int Hk, int D, int64_t ctx, int n_s
   const int NW = vm::decode_stream_waves(B, Hk, n_splits);
   const int G = H / Hk;
   const size_t pm_end = decode_part_o_bytes(B, Hk, NW, G) + decode_part_ml_bytes(B, Hk, NW, G);
-  return (pm_end + 255) / 256 * 256 + DECODE_COUNTER_BYTES;
+  return (pm_end + 255) / 256 * 256 + decode_geom_bytes(B);
 }
 
 static int decode_common(vm::DecodeArgs& a, vm::CombineArgs& c, void* scratch, size_t scratch_bytes,
@@ -288,8 +289,8 @@ static int decode_common(vm::DecodeArgs& a, vm::CombineArgs& c, void* scratch, s
           "decode: B*Ctx*Hk = %lld token-heads exceeds 2^31", (long long)B * ctx * Hk);
   const int NW = vm::decode_stream_waves(B, Hk, n_splits);
   const size_t po = decode_part_o_bytes(B, Hk, NW, G), pm = decode_part_ml_bytes(B, Hk, NW, G);
-  const size_t ctr = (po + pm + 255) / 256 * 256;  // completion counter offset
-  const size_t need = ctr + DECODE_COUNTER_BYTES;
+  const size_t geo = (po + pm + 255) / 256 * 256;  // partition snapshot offset
+  const size_t need = geo + decode_geom_bytes(B);
   REQUIRE(scratch != nullptr && scratch_bytes >= need, VM_E_SCRATCH,
           "decode: scratch of %zu bytes < %zu required (vm_decode_scratch_bytes)", scratch_bytes,
           need);
@@ -297,11 +298,12 @@ static int decode_common(vm::DecodeArgs& a, vm::CombineArgs& c, void* scratch, s
   char* sp = reinterpret_cast<char*>(scratch);
   a.part_o = reinterpret_cast<float*>(sp);
   a.part_ml = reinterpret_cast<float*>(sp + po);
-  a.counter = reinterpret_cast<int32_t*>(sp + ctr);
+  a.geom = reinterpret_cast<int32_t*>(sp + geo);
   a.B = B; a.Hk = Hk; a.G = G; a.NW = NW; a.min_chunk = vm::DECODE_MIN_CHUNK; a.ctx = ctx;
   c.part_o = a.part_o; c.part_ml = a.part_ml;
-  c.B = B; c.Hk = Hk; c.G = G; c.NW = NW; c.min_chunk = vm::DECODE_MIN_CHUNK; c.ctx = ctx;
-  c.advance = nullptr; c.counter = a.counter;
+  c.geom = a.geom;
+  c.B = B; c.Hk = Hk; c.G = G; c.NW = NW;
+  c.advance = nullptr;
   return VM_OK;
 }
 
@@ -329,7 +331,7 @@ int vm_decode_attention(vm_bf16* o, int64_t o_sh, int64_t o_sb, const vm_bf16* q
   a.lengths = lengths;
   int rc = hip_status(timed(VM_K_DECODE_SPLIT, S(st), [&] { return vm::launch_decode(a, false, S(st)); }), "decode_attention split");
   if (rc) return rc;
-  c.lengths = lengths; c.out = o; c.o_sh = o_sh; c.o_sb = o_sb; c.gate = nullptr;
+  c.out = o; c.o_sh = o_sh; c.o_sb = o_sb; c.gate = nullptr;
   return hip_status(timed(VM_K_DECODE_COMBINE, S(st), [&] { return vm::launch_combine(c, S(st)); }), "decode_attention combine");
 }
 
@@ -382,7 +384,7 @@ int vm_gated_attn_decode(vm_bf16* out, int64_t out_sb, const vm_bf16* qkv, int64
   int rc = hip_status(timed(VM_K_DECODE_SPLIT, S(st), [&] { return vm::launch_decode(a, true, S(st)); }), "gated_attn_decode split");
   if (rc) return rc;
   // a5 merge + a6 gate, written as the Wo input (D, Hq, B); a12 advance fused
-  c.lengths = positions; c.out = out; c.o_sh = Dl; c.o_sb = out_sb;
+  c.out = out; c.o_sh = Dl; c.o_sb = out_sb;
   c.gate = qkv + Dl; c.g_sh = 2 * Dl; c.g_sb = qkv_sb;
   c.advance = advance ? positions : nullptr;
   return hip_status(timed(VM_K_DECODE_COMBINE, S(st), [&] { return vm::launch_combine(c, S(st)); }), "gated_attn_decode combine");
