@@ -77,9 +77,8 @@ struct StepBuf {
   uint4 k[8], v[8];
 };
 
-// Per-wave LDS ring: DSLOTS slots of one 16-token step, K then V, each 16 rows of
+// Per-wave LDS ring: two slots of one 16-token step, K then V, each 16 rows of
 // 512 B with chunk c of row r at c ^ swz(r).
-constexpr int DSLOTS = 2;
 constexpr int STEP_ELEMS = DSTEP * HEAD_DIM;  // bf16 per K (or V) step: 8 KB
 
 // Issue the direct global->LDS loads of tokens [t, t + 16) of one (b, hk):
@@ -367,7 +366,7 @@ void decode_stream_kernel(DecodeArgs a) {
   }
 
   // ---- one continuous 16-token step pipeline over the segments of the chunk:
-  // the issue side runs DSLOTS steps ahead of the compute side and crosses
+  // the issue side runs two steps ahead of the compute side and crosses
   // segment boundaries on its own, so a new segment starts with its first
   // steps already in flight
   // one __shared__ object per ring slot: the compiler then sees that reads of one
@@ -381,7 +380,7 @@ void decode_stream_kernel(DecodeArgs a) {
   Seg cs;  // compute side
   cs.b = b; cs.hk = hk; cs.len = len; cs.seg_b_start = seg_b_start; cs.raw = raw;
   seg_bounds(cs, gw0, gw1, a, FUSED);
-  Issuer is;  // issue side, DSLOTS steps ahead
+  Issuer is;  // issue side, two steps ahead
   is.s = cs;
   is.t = cs.lo;
   int ct = cs.lo, inflight = 0, cslot = 0;

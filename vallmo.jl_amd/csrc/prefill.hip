@@ -17,7 +17,7 @@
 // loads (global_load_lds_dwordx4: no VGPR staging), issued two tiles ahead of
 // use; each iteration issues QK of the next tile on the matrix cores before the
 // softmax of the current one, so the VALU work runs under the MFMAs.
-// Rows are 512 B with the 16-byte chunks XOR-swizzled by row (swz below) so that
+// Rows are 512 B with the 16-byte chunks XOR-swizzled by row (swz_pf below) so that
 // both read patterns hit distinct banks.
 //
 // Softmax is exp2-based. With QK-norm the logits are bounded: |s| <= |q~| *
@@ -48,6 +48,12 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
+
+// chunk c of tile row r lives at chunk c ^ swz_pf(r), swz_pf(r) = 4(r & 3) + ((r >> 2) & 3):
+// the 16 rows of each 16-lane group of a b128 K read, and the 4 rows x 64 B of
+// each 32-lane half of a transposing V read, fall on distinct banks (gfx950 LDS:
+// 64 banks of 4 bytes).
+__device__ __forceinline__ int swz_pf(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 struct PrefillCtx {
   const uint16_t* kbase;   // K rows of (b, hk)
@@ -85,7 +91,7 @@ __device__ __forceinline__ void issue_tile(const PrefillCtx& c, int jt, uint16_t
     for (int i = 0; i < 4; ++i) {
       const int g = 4 * c.wave + i;
       const int r = 2 * g + (l >> 5);
-      const int chunk = (l & 31) ^ swz(r);
+      const int chunk = (l & 31) ^ swz_pf(r);
       const int64_t key = min(row0 + r, c.krow_max);
       const int64_t go = key * c.kv_st + chunk * 8;
       __builtin_amdgcn_global_load_lds((const void*)(c.kbase + go),
@@ -99,14 +105,14 @@ __device__ __forceinline__ void issue_tile(const PrefillCtx& c, int jt, uint16_t
 }
 
 // S^T = K Q^T for one tile: chunk 2kk+h2 of row l%32 sits at
-// ((2kk+h2) ^ swz) -> koff[kk&3] + 128*(kk>>2) bytes.
+// ((2kk+h2) ^ swz_pf) -> koff[kk&7] + 256*(kk>>3) bytes.
 __device__ __forceinline__ f32x16 qk_tile(const uint16_t* kb, const uint4 (&qop)[16],
-                                          const int (&koff)[4]) {
+                                          const int (&koff)[8]) {
   const char* kl = reinterpret_cast<const char*>(kb);
   uint4 kf[16];
 #pragma unroll
   for (int kk = 0; kk < 16; ++kk)
-    kf[kk] = *reinterpret_cast<const uint4*>(kl + koff[kk & 3] + 128 * (kk >> 2));
+    kf[kk] = *reinterpret_cast<const uint4*>(kl + koff[kk & 7] + 256 * (kk >> 3));
   f32x16 s;
 #pragma unroll
   for (int j = 0; j < 16; ++j) s[j] = 0.f;
@@ -134,8 +140,8 @@ template <bool STATIC, bool CAUSAL, int SLOT>
 __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_tiles, int my_tiles,
                                           uint16_t* const (&K)[4], uint16_t* const (&V)[4],
                                           const uint4 (&qop)[16], f32x16 (&acc)[8], f32x16& sc,
-                                          float& m_run, float& l_part, const int (&koff)[4],
-                                          const int (&voff)[2]) {
+                                          float& m_run, float& l_part, const int (&koff)[8],
+                                          const int (&voff)[4][2]) {
   // tiles jt+1 and jt+2 may be in flight; tile jt+1 must be resident for all waves
   if (jt + 2 < n_tiles)
     wait_vmcnt<LOADS_PER_TILE>();
@@ -188,16 +194,16 @@ __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_til
     pop[ks].z = pack2(p[8 * ks + 4], p[8 * ks + 5]);
     pop[ks].w = pack2(p[8 * ks + 6], p[8 * ks + 7]);
   }
-  // O^T += V^T P^T; voff[dt&1] + 128*(dt>>1) addresses d-block dt of the key rows
+  // O^T += V^T P^T; d-block dt, key half ks, row half hi at
+  // voff[dt&3][hi] + 256*(dt>>2) + 8192*ks bytes
   const char* vl = reinterpret_cast<const char*>(V[SLOT]);
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const uint16_t* p0 =
-          reinterpret_cast<const uint16_t*>(vl + voff[dt & 1] + 128 * (dt >> 1) + ks * 16 * 512);
-      const uint2 lo = lds_read_tr16(p0);
-      const uint2 hi = lds_read_tr16(p0 + 8 * HEAD_DIM);
+      const char* p0 = vl + 256 * (dt >> 2) + 8192 * ks;
+      const uint2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(p0 + voff[dt & 3][0]));
+      const uint2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(p0 + voff[dt & 3][1]));
       acc[dt] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), pop[ks], acc[dt]);
     }
   }
@@ -209,8 +215,8 @@ template <bool STATIC, bool CAUSAL>
 __device__ __forceinline__ void tile_loop(const PrefillCtx& c, int n_tiles, int my_tiles,
                                           uint16_t* const (&K)[4], uint16_t* const (&V)[4],
                                           const uint4 (&qop)[16], f32x16 (&acc)[8],
-                                          float& m_run, float& l_part, const int (&koff)[4],
-                                          const int (&voff)[2]) {
+                                          float& m_run, float& l_part, const int (&koff)[8],
+                                          const int (&voff)[4][2]) {
   // tile 0 resident (tiles 1 and 2 may still be in flight), then S^T of tile 0
   if (n_tiles > 2)
     wait_vmcnt<2 * LOADS_PER_TILE>();
@@ -280,7 +286,7 @@ void prefill_kernel(PrefillArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 2 * (4 * wave + i) + (lane >> 5);
-    c.dma_off[i] = r * (int)a.kv_st + (((lane & 31) ^ swz(r)) * 8);
+    c.dma_off[i] = r * (int)a.kv_st + (((lane & 31) ^ swz_pf(r)) * 8);
   }
 
   // the first three tiles go out before the q prologue so their latency overlaps it
@@ -367,20 +373,26 @@ void prefill_kernel(PrefillArgs a) {
     if (use_static) m_run = bound;
   }
 
-  // swizzled LDS read offsets (bytes): K chunk 2kk+h2 of row l32; V for the
-  // transpose reads (rows 4*(grp>>1) + (i16>>2) [+8], column chunk 2*(grp&1) + ((i16&3)>>1))
-  int koff[4], voff[2];
+  // swizzled LDS read offsets (bytes). K: chunk c = 2kk + h2 of row l32 sits at
+  // chunk c ^ S, S = swz_pf(l32) < 16, i.e. 16((2(kk&7) + h2) ^ S) + 256(kk>>3).
+  // V^T: a transposing read by source lane i of 16-lane group m reads key row
+  // rr = 8hi + 4(m>>1) + (i>>2) (+16 ks), d-chunk 4dt + u, u = 2(m&1) + ((i&3)>>1),
+  // 8-byte half i&1; with S(rr) = 4(i>>2) + 2hi + (m>>1) the chunk lands at
+  // 4((dt&3) ^ (i>>2)) + 16(dt>>2) + (u ^ (2hi + (m>>1))).
+  int koff[8], voff[4][2];
   {
-    const int sk = swz(l32);
+    const int sk = swz_pf(l32);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) koff[q] = l32 * 512 + (((2 * q + h2) ^ sk) * 16);
-    const int i16 = lane & 15, grp = lane >> 4;
-    const int vr = 4 * (grp >> 1) + (i16 >> 2);
-    const int sv = swz(vr);
-    const int cc = 2 * (grp & 1) + ((i16 & 3) >> 1);
+    for (int q = 0; q < 8; ++q) koff[q] = l32 * 512 + 16 * ((2 * q + h2) ^ sk);
+    const int m = lane >> 4, i = lane & 15;
+    const int u = 2 * (m & 1) + ((i & 3) >> 1);
 #pragma unroll
-    for (int par = 0; par < 2; ++par)
-      voff[par] = vr * 512 + (((4 * par + cc) ^ sv) * 16) + (i16 & 1) * 8;
+    for (int d3 = 0; d3 < 4; ++d3)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi) {
+        const int rr = 8 * hi + 4 * (m >> 1) + (i >> 2);
+        voff[d3][hi] = rr * 512 + 16 * ((4 * d3 + u) ^ swz_pf(rr)) + 8 * (i & 1);
+      }
   }
 
   f32x16 acc[8];
