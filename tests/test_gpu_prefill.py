@@ -167,3 +167,62 @@ def test_chunked_equals_full_prefill(vm):
     mx, mn = maxmean(full[:, P:].float().cpu().numpy(), part.float().cpu().numpy())
     assert mx <= 1e-2 and mn <= 1e-3
     assert torch.equal(la.K_cache, lb.K_cache)
+
+
+def test_fused_prefill_prior_null_attends_chunk_only(vm, orc):
+    """prior == NULL means no prior tokens (vallmo_attn.h): the fused prefill must
+    attend cache columns 1..q_len only, never the rest of a larger cache (filled
+    here with keys that would dominate every softmax if they were attended)."""
+    banner("fused prefill prior=NULL ctx > T")
+    B, T, ctx = 2, 200, 512
+    qw = normal_bf16((D,), 101, scale=0.05)
+    kw = normal_bf16((D,), 102, scale=0.05)
+    qkv = normal_bf16((B, T, S, D), 103)
+    stale = np.full((B, HK, ctx, D), 0x4200, np.uint16)  # bf16 32.0
+    K, V = to_dev(stale), to_dev(stale)
+    cos = torch.empty((ctx, HALF), dtype=torch.float32, device="cuda")
+    sin = torch.empty_like(cos)
+    vm._lib.call("vm_rope_tables", cos.data_ptr(), sin.data_ptr(), HALF, ctx, THETA, None)
+    out = torch.empty((B, T, HQ * D), dtype=torch.bfloat16, device="cuda")
+    dq, dqw, dkw = to_dev(qkv), to_dev(qw), to_dev(kw)  # held: the call takes raw pointers
+    vm._lib.call("vm_gated_attn_prefill", out.data_ptr(), out.stride(1), out.stride(0),
+                 dq.data_ptr(), S * D, T * S * D, K.data_ptr(), V.data_ptr(), D, ctx * D,
+                 HK * ctx * D, ctx, dqw.data_ptr(), dkw.data_ptr(), cos.data_ptr(),
+                 sin.data_ptr(), None, None, B, T, HQ, HK, D, HALF, EPS, 1.0, None)
+    torch.cuda.synchronize()
+    c, s = orc.rope_tables(HALF, ctx, THETA)
+    ref, _, _ = orc.gated_prefill(qkv, stale, stale, np.zeros(B, np.int32),
+                                  np.full(B, T, np.int32), qw, kw, c, s, Hq=HQ, Hk=HK, eps=EPS,
+                                  w_offset=1.0)
+    mx, mn = maxmean(dev_f32(out).reshape(B, T, HQ, D), ref)
+    assert mx <= TOL_MAX and mn <= TOL_MEAN
+
+
+def test_fused_prefill_online_max_path(vm, orc):
+    """One large K-norm weight (kw[0] = 4, so max|kw + 1| = 5) lifts the QK-norm
+    logit bound to ~118 log2 units, past the static-shift limit of 64, while the
+    actual logits stay moderate: the fused kernel then runs its online running max
+    with lazy rescaling, and must still match the oracle."""
+    banner("fused prefill online-max path (one large k-norm weight)")
+    B, T, ctx = 2, 384, 640
+    cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
+    qw = normal_bf16((D,), 111, scale=0.05)
+    kw = normal_bf16((D,), 112, scale=0.05)
+    kw[0] = 0x4080  # bf16 4.0
+    kc = normal_bf16((B, HK, ctx, D), 113)
+    vc = normal_bf16((B, HK, ctx, D), 114)
+    qkv = normal_bf16((B, T, S, D), 115)
+    prior = np.array([0, 256], np.int32)
+    qlen = np.array([384, 300], np.int32)
+    m = vm.AttnModel(cfg)
+    layer = vm.AttnLayer(qw=to_dev(qw), kw=to_dev(kw), K_cache=to_dev(kc), V_cache=to_dev(vc))
+    out = vm.forward(layer, m, to_dev(qkv), T, B, prior=i32(prior), q_lengths=i32(qlen))
+    torch.cuda.synchronize()
+    c, s = orc.rope_tables(HALF, ctx, THETA)
+    ref, _, _ = orc.gated_prefill(qkv, kc, vc, prior, qlen, qw, kw, c, s, Hq=HQ, Hk=HK, eps=EPS,
+                                  w_offset=1.0)
+    got = dev_f32(out).reshape(B, T, HQ, D)
+    fin = ~np.isnan(ref)
+    mx, mn = maxmean(got[fin], ref[fin])
+    print(f"online-max path: out max {mx:.3e} mean {mn:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN

@@ -100,6 +100,8 @@ hipError_t launch_fill_normal(uint16_t* dst, int64_t n, uint64_t seed, float sca
 hipError_t launch_decode(const DecodeArgs& a, bool fused_q, hipStream_t st);
 hipError_t launch_combine(const CombineArgs& a, hipStream_t st);
 hipError_t launch_prefill(const PrefillArgs& a, bool qraw, bool gate, hipStream_t st);
+// fused gated prefill (q norm+RoPE prologue, sigmoid-gate epilogue), persistent
+hipError_t launch_prefill_fused(const PrefillArgs& a, hipStream_t st);
 
 // Decode stream partition shared by the scratch-size query and the launchers:
 // NW waves cover the token-heads sum_b len_b * Hk in equal contiguous chunks.

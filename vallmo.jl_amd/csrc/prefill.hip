@@ -260,9 +260,23 @@ void prefill_kernel(PrefillArgs a) {
   const int b = hb / a.H, h = hb % a.H;
   const int hk = h / (a.H / a.Hk);
 
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, h2 = lane >> 5;
+  const int r0 = qt * PF_BM;
+  const int row = r0 + 32 * wave + l32;  // query row in the chunk
+
+  // Raw q rows first: they depend on nothing the length lookups below return,
+  // so their HBM latency overlaps those lookups (rows past q_len are clamped
+  // in-bounds and never used).
+  const int qrow = min(row, a.L - 1);
+  const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
+                       (int64_t)qrow * a.q_st + 8 * h2;
+  uint4 qraw[16];
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) qraw[kk] = load16(qp + 16 * kk);
+
   // q_len > L is out of contract; clamp so rows past the tensor are never written
   const int q_len = a.q_lengths ? min(a.q_lengths[b], a.L) : a.L;
-  const int r0 = qt * PF_BM;
   if (r0 >= q_len) return;
   int k_len;
   if (a.prior) k_len = a.prior[b] + q_len;
@@ -270,10 +284,6 @@ void prefill_kernel(PrefillArgs a) {
   const int off = k_len - q_len;  // queries are the suffix of keys
   const int kend = CAUSAL ? min(k_len, off + r0 + PF_BM) : k_len;
   const int n_tiles = kend > 0 ? (kend + PF_BN - 1) / PF_BN : 0;
-
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int l32 = lane & 31, h2 = lane >> 5;
-  const int row = r0 + 32 * wave + l32;  // query row in the chunk
 
   PrefillCtx c;
   c.kbase = a.k + (int64_t)b * a.kv_sb + (int64_t)hk * a.kv_sh;
@@ -301,13 +311,10 @@ void prefill_kernel(PrefillArgs a) {
   uint4 qop[16];
   float qn2 = 0.f;  // |q operand|^2 (fp32, before rounding)
   {
-    const int qrow = min(row, a.L - 1);
-    const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
-                         (int64_t)qrow * a.q_st + 8 * h2;
     if (QRAW) {
       float x[16][8];
 #pragma unroll
-      for (int kk = 0; kk < 16; ++kk) unpack8(load16(qp + 16 * kk), x[kk]);
+      for (int kk = 0; kk < 16; ++kk) unpack8(qraw[kk], x[kk]);
       float ss = 0.f;
 #pragma unroll
       for (int kk = 0; kk < 16; ++kk)
@@ -347,7 +354,7 @@ void prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int kk = 0; kk < 16; ++kk) {
         float x[8];
-        unpack8(load16(qp + 16 * kk), x);
+        unpack8(qraw[kk], x);
 #pragma unroll
         for (int j = 0; j < 8; ++j) x[j] *= QK_SCALE;
         qop[kk] = pack8(x);
@@ -412,8 +419,17 @@ void prefill_kernel(PrefillArgs a) {
   float l_tot = l_part + __shfl_xor(l_part, 32, 64);
   const float inv = l_tot > 0.f ? fast_rcp(l_tot) : 0.f;  // fully-masked row -> 0
   uint16_t* op = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)row * a.o_st;
-  const uint16_t* gp = nullptr;
-  if (GATE) gp = a.gate + (int64_t)b * a.g_sb + (int64_t)h * a.g_sh + (int64_t)row * a.g_st;
+  // every gate load goes out before the first store (o and gate may alias as far
+  // as the compiler knows, so it would otherwise serialise load -> store pairs)
+  uint2 gv[8][4];
+  if (GATE) {
+    const uint16_t* gp = a.gate + (int64_t)b * a.g_sb + (int64_t)h * a.g_sh + (int64_t)row * a.g_st;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+        gv[dt][jb] = *reinterpret_cast<const uint2*>(gp + 32 * dt + 8 * jb + 4 * h2);
+  }
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
@@ -423,11 +439,11 @@ void prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) o4[q] = acc[dt][4 * jb + q] * inv;
       if (GATE) {
-        const uint2 gv = *reinterpret_cast<const uint2*>(gp + d0);
-        o4[0] *= sigmoidf(__uint_as_float(gv.x << 16));
-        o4[1] *= sigmoidf(__uint_as_float(gv.x & 0xffff0000u));
-        o4[2] *= sigmoidf(__uint_as_float(gv.y << 16));
-        o4[3] *= sigmoidf(__uint_as_float(gv.y & 0xffff0000u));
+        const uint2 g2 = gv[dt][jb];
+        o4[0] *= sigmoidf(__uint_as_float(g2.x << 16));
+        o4[1] *= sigmoidf(__uint_as_float(g2.x & 0xffff0000u));
+        o4[2] *= sigmoidf(__uint_as_float(g2.y << 16));
+        o4[3] *= sigmoidf(__uint_as_float(g2.y & 0xffff0000u));
       }
       uint2 ov;
       ov.x = pack2(o4[0], o4[1]);

@@ -508,7 +508,7 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm
   a.k_lengths = nullptr; a.q_lengths = q_lengths; a.prior = prior;
   a.B = B; a.H = Hq; a.Hk = Hk; a.L = T; a.Lk = (int)ctx; a.causal = 1;
   a.n_qt = (T + vm::PREFILL_ROWS_ABI - 1) / vm::PREFILL_ROWS_ABI;
-  return hip_status(timed(VM_K_PREFILL, S(st), [&] { return vm::launch_prefill(a, true, true, S(st)); }), "gated_attn_prefill");
+  return hip_status(timed(VM_K_PREFILL, S(st), [&] { return vm::launch_prefill_fused(a, S(st)); }), "gated_attn_prefill");
 }
 
 // ---- synthetic inputs ------------------------------------------------------
