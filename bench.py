@@ -3,8 +3,8 @@
 Headline (BASELINE.json ``metric``, configs[1]): causal gated-attention prefill,
 B=1, T=4096, 16 q / 4 kv heads, head_dim 256, 64-dim partial RoPE (theta 1e7).
 One step = vm_gated_attn_prefill over one synthetic packed projection: the K/V
-norm+RoPE cache append, then the flash-attention kernel with the q norm+RoPE
-prologue and sigmoid-gate epilogue. ``value`` = algorithmic TFLOP/s =
+norm+RoPE cache append, the V -> V^T workspace staging, then the flash-attention
+kernel with the q norm+RoPE prologue and sigmoid-gate epilogue. ``value`` = algorithmic TFLOP/s =
 4*D*Hq*sum_{i=1..T} i / step time (QK^T + PV over unmasked pairs only).
 
 Also reported (same JSON line, key "decode"): BASELINE configs 3 (B=32 batched
@@ -92,14 +92,16 @@ def bench_prefill(vm, torch, steps, warmup, T=4096, seed=2):
     wall = time.perf_counter() - t0
     n_attn, ms_attn = lib.profile_read(lib.VM_K_PREFILL)
     n_rows, ms_rows = lib.profile_read(lib.VM_K_ROWS)
+    n_tr, ms_tr = lib.profile_read(lib.VM_K_TRANSPOSE)
     lib.profile_enable(False)
-    assert n_attn == steps and n_rows == steps
+    assert n_attn == steps and n_rows == steps and n_tr == steps
     flops = prefill_flops(T)
     return {
         "ms_per_step": 1e3 * wall / steps,
         "tflops": flops / (wall / steps) / 1e12,
         "attn_kernel_ms": ms_attn / n_attn,
         "append_kernel_ms": ms_rows / n_rows,
+        "transpose_kernel_ms": ms_tr / n_tr,
         "flops": flops,
     }
 
@@ -282,7 +284,8 @@ def main():
         log("[bench] prefill config2 T=4096")
         pf = bench_prefill(vm, torch, args.steps, args.warmup)
         log(f"[bench] prefill: {pf['ms_per_step']:.3f} ms/step, {pf['tflops']:.1f} TFLOP/s, "
-            f"attn kernel {pf['attn_kernel_ms']:.3f} ms, append {pf['append_kernel_ms']:.4f} ms")
+            f"attn kernel {pf['attn_kernel_ms']:.3f} ms, append {pf['append_kernel_ms']:.4f} ms, "
+            f"V transpose {pf['transpose_kernel_ms']:.4f} ms")
     decode = None
     if not args.no_decode:
         log("[bench] decode config3 B=32")

@@ -57,7 +57,8 @@ enum {
   VM_K_DECODE_COMBINE = 2,/* LSE merge (+ gate)                              */
   VM_K_PREFILL = 3,       /* flash attention (prefill)                       */
   VM_K_ADVANCE = 4,       /* device clock                                    */
-  VM_K_COUNT = 5
+  VM_K_TRANSPOSE = 5,     /* prefill: cached V -> V^T workspace tiles        */
+  VM_K_COUNT = 6
 };
 int vm_profile_enable(int on);
 int vm_profile_read(int kernel, int* count, double* total_ms);
@@ -204,7 +205,12 @@ int vm_prefill_q_norm_rope(vm_bf16* q_out, int64_t q_st, int64_t q_sh, int64_t q
  * attention kernel whose prologue norms+rotates q from qkv and whose
  * epilogue applies the sigmoid gate (a10) and writes out :: (D*Hq, T, B) —
  * the Wo input layout, token stride out_st, batch stride out_sb.
- * Attends cache columns 1..prior[b]+q_len[b] of each sequence.             */
+ * Attends cache columns 1..prior[b]+q_len[b] of each sequence (prior NULL:
+ * no prior tokens). scratch (device, 256-byte aligned) is a workspace of at
+ * least vm_prefill_scratch_bytes(B, Hk, D, ctx) bytes: the attended V is staged
+ * there transposed for the attention kernel. Its contents are not preserved
+ * (the role of the reference's arena scratch, attention_decode.jl:183-200).  */
+size_t vm_prefill_scratch_bytes(int B, int Hk, int D, int64_t ctx);
 int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb,
                           const vm_bf16* qkv, int64_t qkv_st, int64_t qkv_sb,
                           vm_bf16* k_cache, vm_bf16* v_cache,
@@ -213,7 +219,8 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb,
                           const float* cos_tab, const float* sin_tab,
                           const int32_t* prior, const int32_t* q_lengths,
                           int B, int T, int Hq, int Hk, int D, int half_rot,
-                          float eps, float w_offset, vm_stream stream);
+                          float eps, float w_offset, void* scratch, size_t scratch_bytes,
+                          vm_stream stream);
 
 /* ---- synthetic inputs for tests and benchmarks (not a reference op) ----
  * Fills n bf16 values with the seeded N(0,1) stream used by the CPU oracle

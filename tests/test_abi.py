@@ -118,8 +118,21 @@ def test_fused_prefill_checks_qkv_stride(vm):
     rc = lib.vm_gated_attn_prefill(_p(FAKE), 4096, 4096 * 8, _p(FAKE), 256 * 39, 256 * 39 * 8,
                                    _p(FAKE), _p(FAKE), 256, 256 * 64, 256 * 64 * 4, 64,
                                    _p(FAKE), _p(FAKE), _p(FAKE), _p(FAKE), None, None, 1, 8,
-                                   16, 4, 256, 32, 1e-6, 1.0, None)
+                                   16, 4, 256, 32, 1e-6, 1.0, _p(FAKE), 1 << 30, None)
     assert rc == vm._lib.VM_E_DIM
+
+
+def test_fused_prefill_checks_scratch(vm):
+    lib = vm._lib.load()
+    need = lib.vm_prefill_scratch_bytes(1, 4, 256, 64)
+    assert need == 1 * 4 * 2 * 32 * 256 * 2  # one 16-KB V^T tile per 32 keys per (b, hk)
+    assert lib.vm_prefill_scratch_bytes(1, 4, 128, 64) == 0  # unsupported head_dim
+    rc = lib.vm_gated_attn_prefill(_p(FAKE), 4096, 4096 * 8, _p(FAKE), 256 * 40, 256 * 40 * 8,
+                                   _p(FAKE), _p(FAKE), 256, 256 * 64, 256 * 64 * 4, 64,
+                                   _p(FAKE), _p(FAKE), _p(FAKE), _p(FAKE), None, None, 1, 8,
+                                   16, 4, 256, 32, 1e-6, 1.0, _p(FAKE), need - 1, None)
+    assert rc == vm._lib.VM_E_SCRATCH
+    assert "vm_prefill_scratch_bytes" in lib.vm_last_error().decode()
 
 
 def test_sizes_contract_messages(vm):

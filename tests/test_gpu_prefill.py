@@ -185,10 +185,13 @@ def test_fused_prefill_prior_null_attends_chunk_only(vm, orc):
     vm._lib.call("vm_rope_tables", cos.data_ptr(), sin.data_ptr(), HALF, ctx, THETA, None)
     out = torch.empty((B, T, HQ * D), dtype=torch.bfloat16, device="cuda")
     dq, dqw, dkw = to_dev(qkv), to_dev(qw), to_dev(kw)  # held: the call takes raw pointers
+    nws = vm._lib.load().vm_prefill_scratch_bytes(B, HK, D, ctx)
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
     vm._lib.call("vm_gated_attn_prefill", out.data_ptr(), out.stride(1), out.stride(0),
                  dq.data_ptr(), S * D, T * S * D, K.data_ptr(), V.data_ptr(), D, ctx * D,
                  HK * ctx * D, ctx, dqw.data_ptr(), dkw.data_ptr(), cos.data_ptr(),
-                 sin.data_ptr(), None, None, B, T, HQ, HK, D, HALF, EPS, 1.0, None)
+                 sin.data_ptr(), None, None, B, T, HQ, HK, D, HALF, EPS, 1.0, ws.data_ptr(),
+                 nws, None)
     torch.cuda.synchronize()
     c, s = orc.rope_tables(HALF, ctx, THETA)
     ref, _, _ = orc.gated_prefill(qkv, stale, stale, np.zeros(B, np.int32),

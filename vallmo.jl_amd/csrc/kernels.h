@@ -87,7 +87,23 @@ struct PrefillArgs {
   const int32_t* q_lengths;  // nullable -> L
   const int32_t* prior;      // fused path: k_len = prior + q_len (nullable -> 0)
   int B, H, Hk, L, Lk, n_qt, causal;
+  const uint16_t* vt;        // fused path: V^T tiles of the attended keys (workspace)
+  int vt_tiles;              // tiles per (b, hk) in the workspace: ceil(Lk / 32)
 };
+
+// V cache -> V^T tiles for the fused prefill (one 16-KB tile per 32 keys)
+struct VtArgs {
+  const uint16_t* v;
+  int64_t v_st, v_sh, v_sb;
+  uint16_t* vt;
+  int vt_tiles;
+  const int32_t* prior;      // nullable -> 0
+  const int32_t* q_lengths;  // nullable -> L
+  int B, Hk, L;
+  int64_t ctx;
+};
+constexpr int PREFILL_VT_TILE_KEYS = 32;
+constexpr int64_t PREFILL_VT_TILE_BYTES = 32 * 256 * 2;
 
 hipError_t launch_rope_tables(float* c, float* s, int half, int64_t ctx, double theta,
                               hipStream_t st);
@@ -102,6 +118,7 @@ hipError_t launch_combine(const CombineArgs& a, hipStream_t st);
 hipError_t launch_prefill(const PrefillArgs& a, bool qraw, bool gate, hipStream_t st);
 // fused gated prefill (q norm+RoPE prologue, sigmoid-gate epilogue), persistent
 hipError_t launch_prefill_fused(const PrefillArgs& a, hipStream_t st);
+hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st);
 
 // Decode stream partition shared by the scratch-size query and the launchers:
 // NW waves cover the token-heads sum_b len_b * Hk in equal contiguous chunks.

@@ -12,8 +12,12 @@
 // * Workgroup = 4 waves x 32 query rows, 32-key tiles, all on 32x32x16 bf16 MFMA
 //   with fp32 accumulation:
 //     S^T[key][row] = K[key][:] . Q[row][:]       A = K (LDS, ds_read_b128), B = Q (VGPRs)
-//     O^T[d][row]  += V^T[d][key] . P^T[key][row] A = V^T (LDS, ds_read_b64_tr_b16),
+//     O^T[d][row]  += V^T[d][key] . P^T[key][row] A = V^T (LDS, ds_read_b128),
 //                                                 B = P^T (the S^T accumulator, packed)
+//   V^T comes ready-made: vt_transpose_kernel (below) writes each 32-key tile of
+//   the cached V as V^T in exactly the byte layout the MFMA reads from LDS, into a
+//   caller-provided workspace, so the tiles are plain 16-KB copies and every V
+//   operand is one b128 read (transposing LDS reads cost about 1.6x the time).
 // * Three-stage software pipeline per iteration j: QK(j+1) on the matrix cores,
 //   softmax(j) on the VALU and PV(j-1) on the matrix cores, in one straight-line
 //   block whose instruction groups are pinned so the LDS reads run ahead of the
@@ -82,9 +86,55 @@ __device__ __forceinline__ int item_index(int p, int w, int P, int HB) {
   return p * P + (P - 1 - w);
 }
 
+// ---- V^T tiles. Tile t of (b, hk) holds keys 32t .. 32t+31 as 256 d-rows of 64
+// bytes. Row d holds four 16-byte chunks; logical chunk c = 2ks + h carries the 8
+// keys 16ks + {4h..4h+3, 8+4h..8+4h+3} -- the key order of the P^T operand that
+// lane half h holds for key half ks -- and is stored at chunk c ^ ((d >> 2) & 3),
+// so the 16 rows of a b128 read group fall on distinct banks. Byte offset of
+// logical chunk c of row m of a 32-row d-block:
+__device__ __forceinline__ int vt_chunk_offset(int m, int c) {
+  return 64 * m + 16 * (c ^ ((m >> 2) & 3));
+}
+
+// One workgroup per (32-key tile, kv head, sequence): 16 KB of the cached V in
+// (coalesced 16-byte rows), through LDS, out as one V^T tile (coalesced). Keys
+// past the attended length repeat the last one (they are masked; V stays finite).
+__global__ __launch_bounds__(256) void vt_transpose_kernel(VtArgs a) {
+  const int t = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int q_len = a.q_lengths ? min(a.q_lengths[b], a.L) : a.L;
+  const int64_t k_len = min((int64_t)(a.prior ? a.prior[b] : 0) + q_len, a.ctx);
+  if ((int64_t)t * FN >= k_len) return;
+  __shared__ __attribute__((aligned(16))) uint16_t tile[FN][HEAD_DIM + 8];  // 16-B row pad
+  const int tid = threadIdx.x;
+  const uint16_t* src = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+#pragma unroll
+  for (int q = tid; q < FN * 32; q += 256) {
+    const int row = q >> 5, c16 = q & 31;
+    const int64_t key = min((int64_t)t * FN + row, k_len - 1);
+    *reinterpret_cast<uint4*>(&tile[row][c16 * 8]) = load16(src + key * a.v_st + c16 * 8);
+  }
+  __syncthreads();
+  uint16_t* dst = a.vt + ((int64_t)b * a.Hk + hk) * a.vt_tiles * FT + (int64_t)t * FT;
+#pragma unroll
+  for (int o = tid; o < HEAD_DIM * 4; o += 256) {
+    const int d = o >> 2;
+    const int c = (o & 3) ^ ((d >> 2) & 3);
+    const int ks = c >> 1, h = c & 1;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int b0 = 2 * e, b1 = 2 * e + 1;
+      const uint32_t lo = tile[16 * ks + 8 * (b0 >> 2) + 4 * h + (b0 & 3)][d];
+      const uint32_t hi = tile[16 * ks + 8 * (b1 >> 2) + 4 * h + (b1 & 3)][d];
+      w[e] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4*>(dst + o * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 struct FCtx {
   const uint16_t* kbase;
-  const uint16_t* vbase;
+  const uint16_t* vtbase;  // V^T tiles of (b, hk): 16 KB each
   int64_t kv_st;
   int krow_max;   // last cache row that may be read
   int n_tiles;
@@ -122,6 +172,20 @@ __device__ __forceinline__ void issue_quarter(const FCtx& c, const uint16_t* bas
                                        (__attribute__((address_space(3))) void*)(dst + g * 512),
                                        16, 0, 0);
     }
+  }
+}
+
+// This wave's quarter of V^T tile t (clamped to the last tile): 4 one-KB pieces,
+// a plain copy (the transpose kernel wrote the LDS byte layout).
+__device__ __forceinline__ void issue_quarter_vt(const FCtx& c, int t, uint16_t* dst) {
+  t = min(t, c.n_tiles - 1);
+  const char* src = reinterpret_cast<const char*>(c.vtbase + (int64_t)t * FT) + 16 * c.lane;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int g = 4 * c.wave + i;
+    __builtin_amdgcn_global_load_lds((const void*)(src + 1024 * g),
+                                     (__attribute__((address_space(3))) void*)(dst + g * 512),
+                                     16, 0, 0);
   }
 }
 
@@ -247,13 +311,6 @@ __device__ __forceinline__ u32x4 ds_b128(uint32_t addr) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
   return r;
 }
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-template <int OFF>
-__device__ __forceinline__ u32x2 ds_tr_b64(uint32_t addr) {
-  u32x2 r;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
-  return r;
-}
 // wait until at most N LDS reads are outstanding; the two fragments a step
 // consumes are threaded through it so their MFMAs cannot be scheduled ahead of
 // the wait (and no copy of them can be made before it)
@@ -264,38 +321,30 @@ __device__ __forceinline__ void lds_wait(u32x4& x, u32x4& y) {
 
 // The steady-state iteration (softmax(j), QK(j+1), PV(j-1)) as 16 fixed steps.
 // Step k issues QK MFMA k (chain on S(j+1)) and PV MFMA k (chain pairs on the
-// accumulator), the LDS reads of step k + AHEAD (K fragment k+AHEAD: one b128;
-// V fragment k+AHEAD: two transposing b64), and a few VALU ops of softmax(j):
+// accumulator), the two b128 LDS reads of step k + AHEAD (K fragment and V^T
+// fragment k+AHEAD), and a few VALU ops of softmax(j):
 //   steps 0-1 row max, 2 cross-half max, 3 shift update, 4-11 two exps each,
 //   12-14 bf16 packing and the row sum.
 // QK and PV MFMAs alternate, so a dependent MFMA always has an independent one
-// between it and its producer. Reads complete in issue order (3 per step), so
-// the operands of step k are in once at most 3*AHEAD - 3 reads are outstanding.
+// between it and its producer. Reads complete in issue order (2 per step), so
+// the operands of step k are in once at most 2*AHEAD - 2 reads are outstanding.
 constexpr int AHEAD = 3;
 template <int J4>
 __device__ __forceinline__ void steady_block(WaveState& st, const LdsRing& ring,
-                                             const int (&koff)[8], const int (&voff)[4][2],
+                                             const int (&koff)[8], const int (&vof)[2],
                                              float& alpha) {
   // K slot j+1 and V slot j-1 share one LDS object (see the ring layout)
   const uint32_t kb = lds_addr(ring.K[(J4 + 1) % NS]);
   const uint32_t vb = lds_addr(ring.V[(J4 + 3) % NS]);
-  uint32_t ka[8], va[8];
+  uint32_t ka[8], va[2];
 #pragma unroll
   for (int q = 0; q < 8; ++q) ka[q] = kb + koff[q];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    va[2 * q] = vb + voff[q][0];
-    va[2 * q + 1] = vb + voff[q][1];
-  }
+  va[0] = vb + vof[0];
+  va[1] = vb + vof[1];
   // K fragment k: chunk 2k+h2 of row l%32 at koff[k&7] + 256*(k>>3)
-  // V fragment v = 2dt+ks: halves at voff[dt&3][0/1] + 256*(dt>>2) + 8192*ks
+  // V^T fragment v = 2dt+ks: d-row 32dt + l%32 at vof[ks] + 2048*dt
 #define RK(k) (kf[k] = ds_b128<256 * ((k) >> 3)>(ka[(k) & 7]))
-#define RV(v)                                                                          \
-  do {                                                                                 \
-    const u32x2 lo = ds_tr_b64<256 * (((v) >> 1) >> 2) + 8192 * ((v) & 1)>(va[2 * (((v) >> 1) & 3)]);     \
-    const u32x2 hi = ds_tr_b64<256 * (((v) >> 1) >> 2) + 8192 * ((v) & 1)>(va[2 * (((v) >> 1) & 3) + 1]); \
-    vf[v] = u32x4{lo.x, lo.y, hi.x, hi.y};                                             \
-  } while (0)
+#define RV(v) (vf[v] = ds_b128<2048 * ((v) >> 1)>(va[(v) & 1]))
 
   f32x16 s = st.sc;
   pin(s);  // the softmax starts inside this block
@@ -310,9 +359,9 @@ __device__ __forceinline__ void steady_block(WaveState& st, const LdsRing& ring,
     // operands of step k: issued 3 per step, AHEAD steps back; the reads of
     // the AHEAD-1 later steps (3 each) may still be outstanding
     if (k <= 16 - AHEAD) {
-      lds_wait<3 * (AHEAD - 1)>(kf[k], vf[k]);
+      lds_wait<2 * (AHEAD - 1)>(kf[k], vf[k]);
     } else if (k == 14) {
-      lds_wait<3>(kf[k], vf[k]);
+      lds_wait<2>(kf[k], vf[k]);
     } else {
       lds_wait<0>(kf[k], vf[k]);
     }
@@ -402,19 +451,19 @@ __device__ __forceinline__ void steady_block(WaveState& st, const LdsRing& ring,
 template <bool CAUSAL, int J4, bool PV, bool SM, bool QK>
 __device__ __forceinline__ void iter(WaveState& st, const FCtx& c, const LdsRing& ring,
                                      const WaveGeo& g, int j, const int (&koff)[8],
-                                     const int (&voff)[4][2]) {
+                                     const int (&vof)[2]) {
   // K(j+1) and V(j-1) landed for every wave (loads of iterations j-2, j-1 may
   // still be in flight), and every wave is past iteration j-1
   fwait_vmcnt<2 * DMA_PER_ITER>();
   fbarrier();
   issue_quarter(c, c.kbase, j + NS, ring.K[J4 % NS]);
-  issue_quarter(c, c.vbase, j + NS - 2, ring.V[(J4 + 2) % NS]);
+  issue_quarter_vt(c, j + NS - 2, ring.V[(J4 + 2) % NS]);
 
   if (SM && tile_needs_mask<CAUSAL>(g, j)) mask_s<CAUSAL>(g, j, c.lane, st.sc);
   float alpha = 1.0f;
 
   if (QK && PV && SM) {
-    steady_block<J4>(st, ring, koff, voff, alpha);
+    steady_block<J4>(st, ring, koff, vof, alpha);
   } else {
     __builtin_amdgcn_sched_barrier(0);
     uint4 kf[16];
@@ -434,11 +483,9 @@ __device__ __forceinline__ void iter(WaveState& st, const FCtx& c, const LdsRing
       for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          // V^T fragment: d-block dt, key half ks (two transposing reads)
-          const char* p0 = vl + 256 * (dt >> 2) + 8192 * ks;
-          const uint2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(p0 + voff[dt & 3][0]));
-          const uint2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(p0 + voff[dt & 3][1]));
-          st.acc[dt] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), st.pprev[ks], st.acc[dt]);
+          // V^T fragment: d-rows 32dt.., key half ks
+          const uint4 vfrag = *reinterpret_cast<const uint4*>(vl + vof[ks] + 2048 * dt);
+          st.acc[dt] = mfma32(vfrag, st.pprev[ks], st.acc[dt]);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -459,28 +506,28 @@ __device__ __forceinline__ void iter(WaveState& st, const FCtx& c, const LdsRing
 template <bool CAUSAL>
 __device__ __forceinline__ void run_tiles(WaveState& st, const FCtx& c, const LdsRing& ring,
                                           const WaveGeo& g, const int (&koff)[8],
-                                          const int (&voff)[4][2]) {
+                                          const int (&vof)[2]) {
   const int n = c.n_tiles;
   // iteration 0: softmax(0), QK(1); no PV yet
-  iter<CAUSAL, 0, false, true, true>(st, c, ring, g, 0, koff, voff);
+  iter<CAUSAL, 0, false, true, true>(st, c, ring, g, 0, koff, vof);
   // steady iterations 1 .. n-1 (QK(n) at j = n-1 reads a repeated tile; unused)
   int j = 1;
   for (; j + 3 < n; j += 4) {
-    iter<CAUSAL, 1, true, true, true>(st, c, ring, g, j, koff, voff);
-    iter<CAUSAL, 2, true, true, true>(st, c, ring, g, j + 1, koff, voff);
-    iter<CAUSAL, 3, true, true, true>(st, c, ring, g, j + 2, koff, voff);
-    iter<CAUSAL, 0, true, true, true>(st, c, ring, g, j + 3, koff, voff);
+    iter<CAUSAL, 1, true, true, true>(st, c, ring, g, j, koff, vof);
+    iter<CAUSAL, 2, true, true, true>(st, c, ring, g, j + 1, koff, vof);
+    iter<CAUSAL, 3, true, true, true>(st, c, ring, g, j + 2, koff, vof);
+    iter<CAUSAL, 0, true, true, true>(st, c, ring, g, j + 3, koff, vof);
   }
   // remaining steady iterations, then the PV(n-1)-only iteration j = n
   const int rem = n - j;  // 0..3 steady iterations left
-  if (rem >= 1) iter<CAUSAL, 1, true, true, true>(st, c, ring, g, j, koff, voff);
-  if (rem >= 2) iter<CAUSAL, 2, true, true, true>(st, c, ring, g, j + 1, koff, voff);
-  if (rem >= 3) iter<CAUSAL, 3, true, true, true>(st, c, ring, g, j + 2, koff, voff);
+  if (rem >= 1) iter<CAUSAL, 1, true, true, true>(st, c, ring, g, j, koff, vof);
+  if (rem >= 2) iter<CAUSAL, 2, true, true, true>(st, c, ring, g, j + 1, koff, vof);
+  if (rem >= 3) iter<CAUSAL, 3, true, true, true>(st, c, ring, g, j + 2, koff, vof);
   switch (n & 3) {  // the last iteration is j = n, slot n % 4
-    case 0: iter<CAUSAL, 0, true, false, false>(st, c, ring, g, n, koff, voff); break;
-    case 1: iter<CAUSAL, 1, true, false, false>(st, c, ring, g, n, koff, voff); break;
-    case 2: iter<CAUSAL, 2, true, false, false>(st, c, ring, g, n, koff, voff); break;
-    default: iter<CAUSAL, 3, true, false, false>(st, c, ring, g, n, koff, voff); break;
+    case 0: iter<CAUSAL, 0, true, false, false>(st, c, ring, g, n, koff, vof); break;
+    case 1: iter<CAUSAL, 1, true, false, false>(st, c, ring, g, n, koff, vof); break;
+    case 2: iter<CAUSAL, 2, true, false, false>(st, c, ring, g, n, koff, vof); break;
+    default: iter<CAUSAL, 3, true, false, false>(st, c, ring, g, n, koff, vof); break;
   }
 }
 
@@ -509,20 +556,13 @@ void prefill_fused_kernel(PrefillArgs a, int n_items, int P) {
   // chunk c ^ fswz(l32). V^T: a transposing read by lane i of 16-lane group m
   // reads key row rr = 8hi + 4(m>>1) + (i>>2) (+16 ks), d-chunk 4dt + u with
   // u = 2(m&1) + ((i&3)>>1), 8-byte half i&1.
-  int koff[8], voff[4][2];
+  int koff[8], vof[2];
   {
     const int sk = fswz(l32);
 #pragma unroll
     for (int q = 0; q < 8; ++q) koff[q] = l32 * 512 + 16 * ((2 * q + h2) ^ sk);
-    const int m = lane >> 4, i = lane & 15;
-    const int u = 2 * (m & 1) + ((i & 3) >> 1);
 #pragma unroll
-    for (int d3 = 0; d3 < 4; ++d3)
-#pragma unroll
-      for (int hi = 0; hi < 2; ++hi) {
-        const int rr = 8 * hi + 4 * (m >> 1) + (i >> 2);
-        voff[d3][hi] = rr * 512 + 16 * ((4 * d3 + u) ^ fswz(rr)) + 8 * (i & 1);
-      }
+    for (int ks = 0; ks < 2; ++ks) vof[ks] = vt_chunk_offset(l32, 2 * ks + h2);
   }
   // static bound on |k~| (rows of any kv head): sqrt(D) * max|kw + w_offset|
   float kbound;
@@ -568,7 +608,7 @@ void prefill_fused_kernel(PrefillArgs a, int n_items, int P) {
 
     FCtx c;
     c.kbase = a.k + (int64_t)b * a.kv_sb + (int64_t)it.hk * a.kv_sh;
-    c.vbase = a.v + (int64_t)b * a.kv_sb + (int64_t)it.hk * a.kv_sh;
+    c.vtbase = a.vt + ((int64_t)b * a.Hk + it.hk) * a.vt_tiles * FT;
     c.kv_st = a.kv_st;
     c.krow_max = max(0, min(k_len, a.Lk) - 1);
     c.n_tiles = max(1, (kend + FN - 1) / FN);
@@ -603,9 +643,9 @@ void prefill_fused_kernel(PrefillArgs a, int n_items, int P) {
     issue_quarter(c, c.kbase, 0, ring.K[0]);
     issue_quarter(c, c.kbase, 1, ring.K[1]);
     issue_quarter(c, c.kbase, 2, ring.K[2]);
-    issue_quarter(c, c.vbase, 0, ring.V[0]);
+    issue_quarter_vt(c, 0, ring.V[0]);
     issue_quarter(c, c.kbase, 3, ring.K[3]);
-    issue_quarter(c, c.vbase, 1, ring.V[1]);
+    issue_quarter_vt(c, 1, ring.V[1]);
 
     // ---- q prologue: qnorm_rope (src/kernels/qknorm_rope_append.jl:25-57) and
     // the 1/16 scale (exact in bf16); lane holds q[row][16kk + 8h2 + j]
@@ -670,7 +710,7 @@ void prefill_fused_kernel(PrefillArgs a, int n_items, int P) {
 #pragma unroll
       for (int kk = 0; kk < 16; ++kk) st.sc = mfma32(kf[kk], st.qop[kk], st.sc);
     }
-    run_tiles<CAUSAL>(st, c, ring, g, koff, voff);
+    run_tiles<CAUSAL>(st, c, ring, g, koff, vof);
 
     // ---- epilogue: normalise, gate (sigmoid, src/kernels/kernels.jl:34), store
     // in the Wo input layout. Every gate load goes out before the first store.
@@ -706,6 +746,12 @@ void prefill_fused_kernel(PrefillArgs a, int n_items, int P) {
     fbarrier();
   }
   fwait_vmcnt<0>();  // no LDS load may land after the workgroup is gone
+}
+
+hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st) {
+  if (a.B == 0 || a.Hk == 0 || a.vt_tiles == 0) return hipSuccess;
+  hipLaunchKernelGGL(vt_transpose_kernel, dim3(a.vt_tiles, a.Hk, a.B), dim3(256), 0, st, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_prefill_fused(const PrefillArgs& a, hipStream_t st) {

@@ -480,14 +480,23 @@ int vm_prefill_q_norm_rope(vm_bf16* q_out, int64_t q_st, int64_t q_sh, int64_t q
 }
 
 // ---- a11 ------------------------------------------------------------------
+static int64_t prefill_vt_tiles(int64_t ctx) {
+  return (ctx + vm::PREFILL_VT_TILE_KEYS - 1) / vm::PREFILL_VT_TILE_KEYS;
+}
+
+size_t vm_prefill_scratch_bytes(int B, int Hk, int D, int64_t ctx) {
+  if (B <= 0 || Hk <= 0 || D != vm::HEAD_DIM_ABI || ctx <= 0) return 0;
+  return (size_t)B * Hk * prefill_vt_tiles(ctx) * vm::PREFILL_VT_TILE_BYTES;
+}
+
 int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm_bf16* qkv,
                           int64_t qkv_st, int64_t qkv_sb, vm_bf16* kc, vm_bf16* vc, int64_t c_st,
                           int64_t c_sh, int64_t c_sb, int64_t ctx, const vm_bf16* qw,
                           const vm_bf16* kw, const float* cs, const float* sn,
                           const int32_t* prior, const int32_t* q_lengths, int B, int T, int Hq,
-                          int Hk, int D, int half_rot, float eps, float w_offset, vm_stream st) {
-  TRY(vm_prefill_kv_append(kc, vc, c_st, c_sh, c_sb, ctx, qkv, qkv_st, qkv_sb, kw, cs, sn, prior,
-                           q_lengths, B, T, Hq, Hk, D, half_rot, eps, w_offset, st));
+                          int Hk, int D, int half_rot, float eps, float w_offset, void* scratch,
+                          size_t scratch_bytes, vm_stream st) {
+  // every argument is checked before anything is launched
   REQUIRE(out && qw, VM_E_ARG, "gated_attn_prefill: NULL pointer argument");
   TRY(check_aligned(out, "out"));
   TRY(check_aligned(qw, "qw"));
@@ -495,9 +504,22 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm
   TRY(check_aligned(vc, "V_cache"));
   TRY(check_stride(out_st, "out_st"));
   TRY(check_stride(out_sb, "out_sb"));
-  if (B == 0 || T == 0) return VM_OK;
-  REQUIRE(ctx < (int64_t)1 << 31, VM_E_ARG, "gated_attn_prefill: Ctx too large");
-  REQUIRE(c_st < ((int64_t)1 << 25), VM_E_ARG, "gated_attn_prefill: cache token stride too large");
+  const bool work = B > 0 && T > 0;
+  if (work) {
+    REQUIRE(ctx < (int64_t)1 << 31, VM_E_ARG, "gated_attn_prefill: Ctx too large");
+    REQUIRE(c_st < ((int64_t)1 << 25), VM_E_ARG,
+            "gated_attn_prefill: cache token stride too large");
+    const size_t need = vm_prefill_scratch_bytes(B, Hk, D, ctx);
+    REQUIRE(scratch != nullptr && scratch_bytes >= need, VM_E_SCRATCH,
+            "gated_attn_prefill: scratch of %zu bytes < %zu required (vm_prefill_scratch_bytes)",
+            scratch_bytes, need);
+    REQUIRE(((uintptr_t)scratch & 255) == 0, VM_E_ARG,
+            "gated_attn_prefill: scratch must be 256-byte aligned");
+  }
+  // a9: checks its own arguments, then appends K/V to the cache
+  TRY(vm_prefill_kv_append(kc, vc, c_st, c_sh, c_sb, ctx, qkv, qkv_st, qkv_sb, kw, cs, sn, prior,
+                           q_lengths, B, T, Hq, Hk, D, half_rot, eps, w_offset, st));
+  if (!work) return VM_OK;
   const int64_t Dl = D;
   vm::PrefillArgs a{};
   a.q = qkv; a.q_st = qkv_st; a.q_sh = 2 * Dl; a.q_sb = qkv_sb;
@@ -508,6 +530,13 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm
   a.k_lengths = nullptr; a.q_lengths = q_lengths; a.prior = prior;
   a.B = B; a.H = Hq; a.Hk = Hk; a.L = T; a.Lk = (int)ctx; a.causal = 1;
   a.n_qt = (T + vm::PREFILL_ROWS_ABI - 1) / vm::PREFILL_ROWS_ABI;
+  // the attended V (prior + chunk) as V^T tiles in the workspace
+  vm::VtArgs t{};
+  t.v = vc; t.v_st = c_st; t.v_sh = c_sh; t.v_sb = c_sb;
+  t.vt = reinterpret_cast<uint16_t*>(scratch); t.vt_tiles = (int)prefill_vt_tiles(ctx);
+  t.prior = prior; t.q_lengths = q_lengths; t.B = B; t.Hk = Hk; t.L = T; t.ctx = ctx;
+  TRY(hip_status(timed(VM_K_TRANSPOSE, S(st), [&] { return vm::launch_vt_transpose(t, S(st)); }), "gated_attn_prefill transpose"));
+  a.vt = t.vt; a.vt_tiles = t.vt_tiles;
   return hip_status(timed(VM_K_PREFILL, S(st), [&] { return vm::launch_prefill_fused(a, S(st)); }), "gated_attn_prefill");
 }
 

@@ -69,6 +69,15 @@ class AttnModel:
         nbytes = int(ops._lib.load().vm_decode_scratch_bytes(
             cfg.B, cfg.Hq, cfg.Hkv, cfg.Dh, cfg.Ctx, self.n_splits))
         self.space = torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda")
+        self.prefill_space = None
+
+    def prefill_workspace(self, B: int, ctx: int) -> torch.Tensor:
+        """The prefill workspace (V staged transposed), grown on demand and kept,
+        so repeated prefills reuse one buffer."""
+        need = int(ops._lib.load().vm_prefill_scratch_bytes(B, self.cfg.Hkv, self.cfg.Dh, ctx))
+        if self.prefill_space is None or self.prefill_space.numel() < need:
+            self.prefill_space = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
+        return self.prefill_space
 
 
 class Generation:
@@ -147,11 +156,12 @@ def forward(l: AttnLayer, m: AttnModel, qkv, T: int, B: int, *, offset: int = 0,
     if out is None:
         out = torch.empty((B, T, cfg.Hq * cfg.Dh), dtype=torch.bfloat16, device="cuda")
     c = l.K_cache
+    ws = m.prefill_workspace(B, d["Ctx"])
     call("vm_gated_attn_prefill", ops._p(out), out.stride(1), out.stride(0), ops._p(qkv4),
          qkv4.stride(1), qkv4.stride(0), ops._p(l.K_cache), ops._p(l.V_cache), c.stride(2),
          c.stride(1), c.stride(0), d["Ctx"], ops._p(l.qw), ops._p(l.kw), ops._p(m.rope["cos"]),
          ops._p(m.rope["sin"]), ops._p(prior), ops._p(q_lengths), B, T, cfg.Hq, cfg.Hkv, cfg.Dh,
-         cfg.rot_half, float(cfg.eps), 1.0, ops._stream())
+         cfg.rot_half, float(cfg.eps), 1.0, ops._p(ws), ws.numel(), ops._stream())
     return out
 
 
