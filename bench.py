@@ -327,7 +327,7 @@ def main():
                    "global_batch": 1, "seq_len": 4096, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": profiled_traffic(), "kernel": "prefill_kernel<QRAW,GATE,CAUSAL>",
+                     "traffic": profiled_traffic(), "kernel": "prefill_fused_kernel<CAUSAL>",
                      "kernel_ms": round(pf["attn_kernel_ms"], 5),
                      "flop_per_launch": pf["flops"]},
         "cpu_baseline": cpu,

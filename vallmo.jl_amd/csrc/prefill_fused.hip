@@ -1,35 +1,43 @@
 // prefill_fused.hip — the fused gated-attention prefill of forward(::AttnLayer)
 // (src/llm/qwen35.jl:292-318): q norm + RoPE prologue, causal GQA flash attention
 // over the cache (src/kernels/attention.jl:12-91), sigmoid-gate epilogue written in
-// the Wo input layout. Re-designed for CDNA4:
+// the Wo input layout. Re-designed for CDNA4.
 //
-// * Persistent workgroups. One workgroup per CU walks a static list of work
-//   items (b, h, 128-row q-block), heaviest causal q-blocks first, in a
-//   serpentine order (pass 0 forward, pass 1 backward, ...), so every CU gets
-//   about the same number of key tiles and no second dispatch round exists.
-//   Items of one pass that share a workgroup slot keep the same (b, h), so the
-//   four query heads of a kv head stay on one XCD and share its L2.
-// * Workgroup = 4 waves x 32 query rows, 32-key tiles, all on 32x32x16 bf16 MFMA
-//   with fp32 accumulation:
-//     S^T[key][row] = K[key][:] . Q[row][:]       A = K (LDS, ds_read_b128), B = Q (VGPRs)
-//     O^T[d][row]  += V^T[d][key] . P^T[key][row] A = V^T (LDS, ds_read_b128),
-//                                                 B = P^T (the S^T accumulator, packed)
-//   V^T comes ready-made: vt_transpose_kernel (below) writes each 32-key tile of
-//   the cached V as V^T in exactly the byte layout the MFMA reads from LDS, into a
-//   caller-provided workspace, so the tiles are plain 16-KB copies and every V
-//   operand is one b128 read (transposing LDS reads cost about 1.6x the time).
-// * Three-stage software pipeline per iteration j: QK(j+1) on the matrix cores,
-//   softmax(j) on the VALU and PV(j-1) on the matrix cores, in one straight-line
-//   block whose instruction groups are pinned so the LDS reads run ahead of the
-//   MFMAs that consume them and the softmax spreads over all 32 MFMAs.
-// * K and V tiles stream through separate 4-slot LDS rings filled by direct
-//   global->LDS loads; K(t) is issued three iterations before QK(t), V(t) three
-//   before PV(t). Every iteration issues the same 8 loads per wave (past the
-//   last tile, the last tile again), so the wait before each barrier is the
-//   constant vmcnt(16).
-// * Softmax: exp2 with the QK-norm bound as a static shift when it is <= 64 in
-//   log2 units (no running max, no accumulator rescale), else an online max
-//   rescaled lazily (only when it grows by > 8).
+// One workgroup (4 waves, one per SIMD, the whole 160-KB LDS) per work item
+// (b, h, 128-row q-block), heaviest causal q-blocks first (the hardware hands the
+// next item to the first CU that frees up). All products are 32x32x16 bf16 MFMAs
+// with fp32 accumulation, over 32-key tiles:
+//     S^T[key][row] = K[key][:] . Q[row][:]       A = K fragment, B = Q^T fragment
+//     O^T[d][row]  += V^T[d][key] . P^T[key][row] A = V^T fragment, B = P^T fragment
+//
+// Wave pairs: the two waves of a pair share 64 query rows. Wave e of the pair
+// takes every other key tile (tiles t = e mod 2): QK of its tile for all 64 rows
+// (each K fragment read from LDS feeds two MFMAs), the softmax of that tile, and
+// PV of d-half e (d in 128e .. 128e+127) for all 64 rows over both tiles of the
+// pair step (each V fragment feeds two MFMAs), its own tile's P^T first (read
+// back before the barrier), the partner's through LDS. This halves the LDS
+// operand traffic of one-wave-per-32-rows tiling (one b128 read per MFMA). K
+// tiles stream through an 8-slot LDS ring by direct global->LDS loads (issued
+// two pair steps ahead); V^T fragments come straight from the workspace into
+// registers one pair step ahead (the V^T transpose kernel writes each 32-key tile
+// fragment-major, so every fragment is one coalesced 1-KB load). Per pair step
+// and wave: 64 MFMAs, 16 K reads, 8 P reads, 4 P writes, 16 V loads, 8 tile
+// loads, 32 exponentials; a three-stage software pipeline (QK of the next tile,
+// softmax of the current one, PV of the previous pair) with one barrier.
+//
+// Loads whose results feed MFMAs directly (V^T, K and P^T fragments) are issued
+// from inline asm with counted waits (the compiler would drain every load in
+// flight, including the tile loads two steps ahead, before each use). Each of
+// these registers is loaded and consumed inside one straight-line pair step: V^T
+// at the start of the step for that step's PV (the QK phase hides the latency),
+// K four fragments ahead within the QK phase, P^T just before the PV; the
+// consumer reads the value through the wait statement, so no copy of it can be
+// placed before its data has landed.
+//
+// Softmax: a static shift. The QK-norm weights bound every logit (|q op| <=
+// max|qw + w_offset|, |k~| <= 16 max|kw + w_offset|); when that bound is at most
+// 64 in log2 units it is the shift for every row. Otherwise an exact row max is
+// taken first by a QK-only pass over the same tiles and used as each row's shift.
 #include "common.h"
 #include "kernels.h"
 
@@ -40,13 +48,7 @@ namespace {
 constexpr int FM = 128;                    // query rows per item
 constexpr int FN = 32;                     // keys per tile
 constexpr int FT = FN * HEAD_DIM;          // bf16 per K (or V) tile: 16 KB
-constexpr int NS = 4;                      // ring slots (K and V each)
-constexpr int DMA_PER_ITER = 8;            // load instructions per wave per iteration
 constexpr float FSTATIC_LIMIT = 64.0f;
-constexpr float FRESCALE_SLACK = 8.0f;
-constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_DSR = 0x100;
-
-#define FSGB(mask, n) __builtin_amdgcn_sched_group_barrier((mask), (n), 0)
 
 __device__ __forceinline__ void fbarrier() {
   asm volatile("" ::: "memory");
@@ -54,9 +56,8 @@ __device__ __forceinline__ void fbarrier() {
   asm volatile("" ::: "memory");
 }
 
-// chunk c of tile row r lives at chunk c ^ fswz(r): the 16 rows of each 16-lane
-// group of a b128 K read and the 4 rows x 64 B of each 32-lane half of a
-// transposing V read fall on distinct banks (64 banks of 4 bytes).
+// chunk c of K tile row r lives at chunk c ^ fswz(r): the 16 rows of each 16-lane
+// group of a b128 read fall on distinct banks (64 banks of 4 bytes).
 __device__ __forceinline__ int fswz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 struct FItem {
@@ -78,24 +79,13 @@ __device__ __forceinline__ FItem item_at(const PrefillArgs& a, int i) {
   return it;
 }
 
-// item of pass p for workgroup w of P: even passes forward, odd passes backward
-// over the q-block ranks (keeping the workgroup's (b, h) slot when P % HB == 0)
-__device__ __forceinline__ int item_index(int p, int w, int P, int HB) {
-  if ((p & 1) == 0) return p * P + w;
-  if (P % HB == 0) return p * P + (P / HB - 1 - w / HB) * HB + w % HB;
-  return p * P + (P - 1 - w);
-}
-
-// ---- V^T tiles. Tile t of (b, hk) holds keys 32t .. 32t+31 as 256 d-rows of 64
-// bytes. Row d holds four 16-byte chunks; logical chunk c = 2ks + h carries the 8
-// keys 16ks + {4h..4h+3, 8+4h..8+4h+3} -- the key order of the P^T operand that
-// lane half h holds for key half ks -- and is stored at chunk c ^ ((d >> 2) & 3),
-// so the 16 rows of a b128 read group fall on distinct banks. Byte offset of
-// logical chunk c of row m of a 32-row d-block:
-__device__ __forceinline__ int vt_chunk_offset(int m, int c) {
-  return 64 * m + 16 * (c ^ ((m >> 2) & 3));
-}
-
+// ---- V^T tiles. Tile t of (b, hk) holds keys 32t .. 32t+31 as 16 MFMA
+// A-operand fragments of 1 KB, fragment f = 2 * dblk + ks (d-block dblk of 32
+// d-rows, key half ks): lane l's 16 bytes (at 1024 f + 16 l) are the 8 keys
+// 16 ks + {4h .. 4h+3, 8+4h .. 8+4h+3} (h = l / 32) of d-row 32 dblk + l % 32 --
+// the key order of the P^T operand that lane half h holds for key half ks (the
+// S^T accumulator layout).
+//
 // One workgroup per (32-key tile, kv head, sequence): 16 KB of the cached V in
 // (coalesced 16-byte rows), through LDS, out as one V^T tile (coalesced). Keys
 // past the attended length repeat the last one (they are masked; V stays finite).
@@ -117,15 +107,15 @@ __global__ __launch_bounds__(256) void vt_transpose_kernel(VtArgs a) {
   uint16_t* dst = a.vt + ((int64_t)b * a.Hk + hk) * a.vt_tiles * FT + (int64_t)t * FT;
 #pragma unroll
   for (int o = tid; o < HEAD_DIM * 4; o += 256) {
-    const int d = o >> 2;
-    const int c = (o & 3) ^ ((d >> 2) & 3);
-    const int ks = c >> 1, h = c & 1;
+    const int f = o >> 6, l = o & 63;
+    const int d = 32 * (f >> 1) + (l & 31);
+    const int k0 = 16 * (f & 1) + 4 * (l >> 5);
     uint32_t w[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int b0 = 2 * e, b1 = 2 * e + 1;
-      const uint32_t lo = tile[16 * ks + 8 * (b0 >> 2) + 4 * h + (b0 & 3)][d];
-      const uint32_t hi = tile[16 * ks + 8 * (b1 >> 2) + 4 * h + (b1 & 3)][d];
+      const int u0 = 2 * e, u1 = 2 * e + 1;  // element u: key k0 + (u & 3) + 8 (u >> 2)
+      const uint32_t lo = tile[k0 + (u0 & 3) + 8 * (u0 >> 2)][d];
+      const uint32_t hi = tile[k0 + (u1 & 3) + 8 * (u1 >> 2)][d];
       w[e] = lo | (hi << 16);
     }
     *reinterpret_cast<uint4*>(dst + o * 8) = make_uint4(w[0], w[1], w[2], w[3]);
@@ -143,16 +133,15 @@ struct FCtx {
   int wave, lane;
 };
 
-// This wave's quarter of tile t (clamped to the last tile) of K or V into `dst`:
-// piece i = rows 2g, 2g+1 (g = 4 wave + i) as 64 lanes x 16 B. A whole tile is a
+// This wave's quarter of K tile t (clamped to the last tile) into `dst`: piece
+// i = rows 2g, 2g+1 (g = 4 wave + i) as 64 lanes x 16 B. A whole tile is a
 // scalar base plus per-lane unsigned byte offsets (the scalar-base addressing
 // form); the last tile re-reads the last readable row past it (its keys are
-// masked, and V must stay finite).
-__device__ __forceinline__ void issue_quarter(const FCtx& c, const uint16_t* base, int t,
-                                              uint16_t* dst) {
+// masked).
+__device__ __forceinline__ void issue_quarter(const FCtx& c, int t, uint16_t* dst) {
   t = min(t, c.n_tiles - 1);
   const int row0 = t * FN;
-  const char* src = reinterpret_cast<const char*>(base + (int64_t)row0 * c.kv_st);
+  const char* src = reinterpret_cast<const char*>(c.kbase + (int64_t)row0 * c.kv_st);
   if (row0 + FN - 1 <= c.krow_max) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -175,576 +164,771 @@ __device__ __forceinline__ void issue_quarter(const FCtx& c, const uint16_t* bas
   }
 }
 
-// This wave's quarter of V^T tile t (clamped to the last tile): 4 one-KB pieces,
-// a plain copy (the transpose kernel wrote the LDS byte layout).
-__device__ __forceinline__ void issue_quarter_vt(const FCtx& c, int t, uint16_t* dst) {
-  t = min(t, c.n_tiles - 1);
-  const char* src = reinterpret_cast<const char*>(c.vtbase + (int64_t)t * FT) + 16 * c.lane;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int g = 4 * c.wave + i;
-    __builtin_amdgcn_global_load_lds((const void*)(src + 1024 * g),
-                                     (__attribute__((address_space(3))) void*)(dst + g * 512),
-                                     16, 0, 0);
-  }
-}
-
 template <int N>
 __device__ __forceinline__ void fwait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
+// waits for the inline-asm loads: they order against the asm that consumes
+// their registers by program order alone
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
+}
 
-// ---- explicit ordering. Empty volatile asm statements keep their source order;
-// passing a value through one pins the instruction that produced it before that
-// point (and its consumers after), and a memory clobber pins LDS reads and tile
-// loads. The steady-state iteration below is written as a fixed sequence of
-// steps this way; the MFMAs themselves stay builtins, so the compiler still
-// inserts the LDS waits and hazard NOPs they need.
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void mem_fence_order() { asm volatile("" ::: "memory"); }
-__device__ __forceinline__ void pin(f32x16& x) { asm volatile("" : "+v"(x)); }
-__device__ __forceinline__ void pin_acc(f32x16& x) { asm volatile("" : "+a"(x)); }
+__device__ __forceinline__ void pin(uint32_t& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
-__device__ __forceinline__ void pin(uint4& x) {
+__device__ __forceinline__ void pin(f32x16& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin_acc(uint4& x) {
   u32x4 t = __builtin_bit_cast(u32x4, x);
-  asm volatile("" : "+v"(t));
+  asm volatile("" : "+a"(t));
   x = __builtin_bit_cast(uint4, t);
 }
-// max / sum with the lane 32 apart (wave64), on the VALU (no LDS instruction)
 __device__ __forceinline__ float xor32_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-__device__ __forceinline__ float xor32_sum(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+// acc + (the two bf16 of w summed), the row sum of a packed P^T pair
+__device__ __forceinline__ float dot2_ones(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w),
+                                         __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
 }
-
-struct LdsRing {
-  uint16_t* K[NS];
-  uint16_t* V[NS];
-};
-
-// softmax of one S^T tile (this lane: row l%32, 16 keys) -> packed P^T operands
-// Softmax of one S^T tile (this lane: row l%32, 16 keys), branch-free: the running
-// shift m_run (log2 units) moves to the tile's row max only when that exceeds it
-// by > FRESCALE_SLACK (lazy rescale); alpha = 2^(old - new) (1 when it stays) is
-// applied to l_part here and to the accumulator by the caller. With m_run
-// starting at the QK-norm bound the shift never moves (the bound dominates every
-// logit), which is the static-shift case at the price of a row max per tile.
-// Outputs the packed P^T operands.
-__device__ __forceinline__ void softmax_tile(const f32x16& s, float& m_run, float& l_part,
-                                             uint4 (&pop)[2], float& alpha) {
-  float mx = fmaxf(s[0], s[1]);
-#pragma unroll
-  for (int j = 2; j < 16; j += 2) mx = fmaxf(mx, fmaxf(s[j], s[j + 1]));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * LOG2E;
-  const float m_new = fmaxf(m_run, mx);
-  const float m_use = m_new > m_run + FRESCALE_SLACK ? m_new : m_run;
-  alpha = m_use == m_run ? 1.0f : fast_exp2(m_run - m_use);
-  m_run = m_use;
-  const float m_eff = m_use == -INFINITY ? 0.f : m_use;
-  float p[16], psum = 0.f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    p[j] = fast_exp2(__builtin_fmaf(s[j], LOG2E, -m_eff));
-    psum += p[j];
-  }
-  l_part = l_part * alpha + psum;
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    pop[ks].x = pack2(p[8 * ks + 0], p[8 * ks + 1]);
-    pop[ks].y = pack2(p[8 * ks + 2], p[8 * ks + 3]);
-    pop[ks].z = pack2(p[8 * ks + 4], p[8 * ks + 5]);
-    pop[ks].w = pack2(p[8 * ks + 6], p[8 * ks + 7]);
-  }
-}
-
-struct WaveGeo {
-  int row, wrow0, wrow1, off, k_len;
-};
-
-template <bool CAUSAL>
-__device__ __forceinline__ bool tile_needs_mask(const WaveGeo& g, int j) {
-  return (j * FN + FN > g.k_len) || (CAUSAL && j * FN + FN - 1 > g.off + g.wrow0);
-}
-template <bool CAUSAL>
-__device__ __forceinline__ void mask_s(const WaveGeo& g, int j, int lane, f32x16& s) {
-  const int lim = CAUSAL ? min(g.k_len - 1, g.row + g.off) : g.k_len - 1;
-  const int key0 = j * FN + 4 * (lane >> 5);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int key = key0 + 8 * (i >> 2) + (i & 3);
-    s[i] = key <= lim ? s[i] : -INFINITY;
-  }
-}
-
-// K fragments of one ring slot: chunk 2kk+h2 of row l%32 at koff[kk&7] + 256*(kk>>3)
-__device__ __forceinline__ void read_kf(const uint16_t* kb, const int (&koff)[8], uint4 (&kf)[16]) {
-  const char* kl = reinterpret_cast<const char*>(kb);
-#pragma unroll
-  for (int kk = 0; kk < 16; ++kk)
-    kf[kk] = *reinterpret_cast<const uint4*>(kl + koff[kk & 7] + 256 * (kk >> 3));
-}
-
-struct WaveState {
-  uint4 qop[16];
-  f32x16 acc[8];
-  f32x16 sc;       // S^T of the tile whose softmax runs next
-  uint4 pprev[2];  // P^T of the tile whose PV runs next
-  float m_run, l_part;
-};
-
-// LDS reads issued from inline asm, with explicit waits. While a direct
-// global->LDS load is in flight the compiler's wait pass can only wait for all
-// LDS reads (lgkmcnt(0)) before using any of them, which would serialise every
-// MFMA behind the latest read; here the reads of the steady block are counted
-// by hand instead (no other LDS or scalar-memory instruction runs in that block,
-// and waits the compiler places elsewhere can only wait for more, never less).
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
+template <int OFF>
+__device__ __forceinline__ void ds_w128(uint32_t addr, const uint4& v) {
+  asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(addr), "v"(__builtin_bit_cast(u32x4, v)),
+               "i"(OFF));
+}
+
+// ---- asm loads into compiler registers and the waits that release them. A load
+// defines its value; the wait takes it (tied) so every reader is placed after the
+// wait; the waits count in issue order (loads of one kind complete in order).
 template <int OFF>
 __device__ __forceinline__ u32x4 ds_b128(uint32_t addr) {
   u32x4 r;
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
   return r;
 }
-// wait until at most N LDS reads are outstanding; the two fragments a step
-// consumes are threaded through it so their MFMAs cannot be scheduled ahead of
-// the wait (and no copy of them can be made before it)
+template <int IMM>
+__device__ __forceinline__ u32x4 g_b128(const char* base, uint32_t off) {
+  static_assert(IMM >= 0 && IMM < 4096, "global offset is 13-bit signed");
+  u32x4 r;
+  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(r) : "v"(off), "s"(base), "i"(IMM));
+  return r;
+}
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+template <int IMM>
+__device__ __forceinline__ u32x2 g_b64(const void* p) {
+  u32x2 r;
+  asm volatile("global_load_dwordx2 %0, %1, off offset:%2" : "=v"(r) : "v"(p), "i"(IMM));
+  return r;
+}
 template <int N>
-__device__ __forceinline__ void lds_wait(u32x4& x, u32x4& y) {
+__device__ __forceinline__ void vm_take8(u32x2 (&g)[4][4], int dq0) {
+  asm volatile("s_waitcnt vmcnt(%8)"
+               : "+v"(g[dq0][0]), "+v"(g[dq0][1]), "+v"(g[dq0][2]), "+v"(g[dq0][3]),
+                 "+v"(g[dq0 + 1][0]), "+v"(g[dq0 + 1][1]), "+v"(g[dq0 + 1][2]), "+v"(g[dq0 + 1][3])
+               : "n"(N));
+}
+template <int N>
+__device__ __forceinline__ void lgkm_take(u32x4& x, u32x4& y) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N));
 }
-
-// The steady-state iteration (softmax(j), QK(j+1), PV(j-1)) as 16 fixed steps.
-// Step k issues QK MFMA k (chain on S(j+1)) and PV MFMA k (chain pairs on the
-// accumulator), the two b128 LDS reads of step k + AHEAD (K fragment and V^T
-// fragment k+AHEAD), and a few VALU ops of softmax(j):
-//   steps 0-1 row max, 2 cross-half max, 3 shift update, 4-11 two exps each,
-//   12-14 bf16 packing and the row sum.
-// QK and PV MFMAs alternate, so a dependent MFMA always has an independent one
-// between it and its producer. Reads complete in issue order (2 per step), so
-// the operands of step k are in once at most 2*AHEAD - 2 reads are outstanding.
-constexpr int AHEAD = 3;
-template <int J4>
-__device__ __forceinline__ void steady_block(WaveState& st, const LdsRing& ring,
-                                             const int (&koff)[8], const int (&vof)[2],
-                                             float& alpha) {
-  // K slot j+1 and V slot j-1 share one LDS object (see the ring layout)
-  const uint32_t kb = lds_addr(ring.K[(J4 + 1) % NS]);
-  const uint32_t vb = lds_addr(ring.V[(J4 + 3) % NS]);
-  uint32_t ka[8], va[2];
-#pragma unroll
-  for (int q = 0; q < 8; ++q) ka[q] = kb + koff[q];
-  va[0] = vb + vof[0];
-  va[1] = vb + vof[1];
-  // K fragment k: chunk 2k+h2 of row l%32 at koff[k&7] + 256*(k>>3)
-  // V^T fragment v = 2dt+ks: d-row 32dt + l%32 at vof[ks] + 2048*dt
-#define RK(k) (kf[k] = ds_b128<256 * ((k) >> 3)>(ka[(k) & 7]))
-#define RV(v) (vf[v] = ds_b128<2048 * ((v) >> 1)>(va[(v) & 1]))
-
-  f32x16 s = st.sc;
-  pin(s);  // the softmax starts inside this block
-  u32x4 kf[16], vf[16];
-  RK(0); RV(0); RK(1); RV(1); RK(2); RV(2);
-
-  f32x16 sn;
-  float mx[8], m_eff = 0.f, psum = 0.f, p[16];
-  uint4 pcur[2];
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    // operands of step k: issued 3 per step, AHEAD steps back; the reads of
-    // the AHEAD-1 later steps (3 each) may still be outstanding
-    if (k <= 16 - AHEAD) {
-      lds_wait<2 * (AHEAD - 1)>(kf[k], vf[k]);
-    } else if (k == 14) {
-      lds_wait<2>(kf[k], vf[k]);
-    } else {
-      lds_wait<0>(kf[k], vf[k]);
-    }
-    if (k == 0) {
-      f32x16 z;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) z[i] = 0.f;
-      sn = mfma32(__builtin_bit_cast(uint4, kf[0]), st.qop[0], z);
-    } else {
-      sn = mfma32(__builtin_bit_cast(uint4, kf[k]), st.qop[k], sn);
-    }
-    pin_acc(sn);
-    st.acc[k >> 1] = mfma32(__builtin_bit_cast(uint4, vf[k]), st.pprev[k & 1], st.acc[k >> 1]);
-    pin_acc(st.acc[k >> 1]);
-    switch (k + AHEAD) {
-      case 3: RK(3); RV(3); break;
-      case 4: RK(4); RV(4); break;
-      case 5: RK(5); RV(5); break;
-      case 6: RK(6); RV(6); break;
-      case 7: RK(7); RV(7); break;
-      case 8: RK(8); RV(8); break;
-      case 9: RK(9); RV(9); break;
-      case 10: RK(10); RV(10); break;
-      case 11: RK(11); RV(11); break;
-      case 12: RK(12); RV(12); break;
-      case 13: RK(13); RV(13); break;
-      case 14: RK(14); RV(14); break;
-      case 15: RK(15); RV(15); break;
-      default: break;
-    }
-    // softmax(j), a few VALU ops per step
-    if (k == 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) { mx[i] = fmaxf(s[2 * i], s[2 * i + 1]); pin(mx[i]); }
-    } else if (k == 1) {
-#pragma unroll
-      for (int i = 4; i < 8; ++i) { mx[i] = fmaxf(s[2 * i], s[2 * i + 1]); pin(mx[i]); }
-    } else if (k == 2) {
-      mx[0] = fmaxf(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])),
-                    fmaxf(fmaxf(mx[4], mx[5]), fmaxf(mx[6], mx[7])));
-      mx[0] = xor32_max(mx[0]) * LOG2E;
-      pin(mx[0]);
-    } else if (k == 3) {
-      // lazy shift update (never moves when m_run starts at the QK-norm bound)
-      const float m_run = st.m_run;
-      const float m_new = fmaxf(m_run, mx[0]);
-      const float m_use = m_new > m_run + FRESCALE_SLACK ? m_new : m_run;
-      alpha = m_use == m_run ? 1.0f : fast_exp2(m_run - m_use);
-      st.m_run = m_use;
-      m_eff = m_use == -INFINITY ? 0.f : m_use;
-      pin(m_eff);
-      pin(alpha);
-    } else if (k < 12) {
-      const int e = 2 * (k - 4);
-      p[e] = fast_exp2(__builtin_fmaf(s[e], LOG2E, -m_eff));
-      p[e + 1] = fast_exp2(__builtin_fmaf(s[e + 1], LOG2E, -m_eff));
-      psum += p[e] + p[e + 1];
-      pin(p[e]);
-      pin(p[e + 1]);
-      pin(psum);
-    } else if (k == 12) {
-      pcur[0].x = pack2(p[0], p[1]);
-      pcur[0].y = pack2(p[2], p[3]);
-      pcur[0].z = pack2(p[4], p[5]);
-      pcur[0].w = pack2(p[6], p[7]);
-      pin(pcur[0]);
-    } else if (k == 13) {
-      pcur[1].x = pack2(p[8], p[9]);
-      pcur[1].y = pack2(p[10], p[11]);
-      pcur[1].z = pack2(p[12], p[13]);
-      pcur[1].w = pack2(p[14], p[15]);
-      pin(pcur[1]);
-    } else if (k == 14) {
-      st.l_part = st.l_part * alpha + psum;
-      pin(st.l_part);
-    }
-  }
-#undef RK
-#undef RV
-  st.sc = sn;
-  st.pprev[0] = pcur[0];
-  st.pprev[1] = pcur[1];
+template <int N>
+__device__ __forceinline__ void lgkm_take(u32x4& x, u32x4& y, u32x4& z, u32x4& w) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(x), "+v"(y), "+v"(z), "+v"(w) : "n"(N));
+}
+template <int N>
+__device__ __forceinline__ void vm_take(u32x4& x, u32x4& y, u32x4& z, u32x4& w) {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(x), "+v"(y), "+v"(z), "+v"(w) : "n"(N));
+}
+// S^T[key][row] (+)= K fragment . Q^T (S in VGPRs, Q in AGPRs); the builtin would
+// accumulate in AGPRs. A dependent product always has another MFMA between it and
+// its producer (the two row blocks alternate), which needs no wait states.
+__device__ __forceinline__ void mfma_qk0(f32x16& s, const u32x4& k, const uint4& q) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0"
+               : "=&v"(s) : "v"(k), "a"(__builtin_bit_cast(u32x4, q)));
+}
+__device__ __forceinline__ void mfma_qk(f32x16& s, const u32x4& k, const uint4& q) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+               : "+v"(s) : "v"(k), "a"(__builtin_bit_cast(u32x4, q)));
 }
 
-// Iteration j of the pipeline on compile-time ring slots (slot = tile % NS).
-// PV: PV(j-1) runs; SM: softmax(j) runs; QK: QK(j+1) runs.
-template <bool CAUSAL, int J4, bool PV, bool SM, bool QK>
-__device__ __forceinline__ void iter(WaveState& st, const FCtx& c, const LdsRing& ring,
-                                     const WaveGeo& g, int j, const int (&koff)[8],
-                                     const int (&vof)[2]) {
-  // K(j+1) and V(j-1) landed for every wave (loads of iterations j-2, j-1 may
-  // still be in flight), and every wave is past iteration j-1
-  fwait_vmcnt<2 * DMA_PER_ITER>();
-  fbarrier();
-  issue_quarter(c, c.kbase, j + NS, ring.K[J4 % NS]);
-  issue_quarter_vt(c, j + NS - 2, ring.V[(J4 + 2) % NS]);
+// 11+ wait states before a VALU reads what an 8-pass MFMA wrote (threaded
+// through the results so no reader moves above the padding)
+__device__ __forceinline__ void mfma_drain(f32x16& s0, f32x16& s1) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(s0), "+v"(s1));
+}
 
-  if (SM && tile_needs_mask<CAUSAL>(g, j)) mask_s<CAUSAL>(g, j, c.lane, st.sc);
-  float alpha = 1.0f;
+// Item geometry.
+struct ItemGeo {
+  int b, h, hk, r0, q_len, prior, k_len, off, kend;
+};
 
-  if (QK && PV && SM) {
-    steady_block<J4>(st, ring, koff, vof, alpha);
+__device__ __forceinline__ ItemGeo item_geo(const PrefillArgs& a, const FItem& it, bool causal) {
+  ItemGeo ig;
+  ig.b = it.b; ig.h = it.h; ig.hk = it.hk;
+  ig.r0 = it.qt * FM;
+  ig.q_len = a.q_lengths ? min(a.q_lengths[it.b], a.L) : a.L;
+  ig.prior = a.prior ? a.prior[it.b] : 0;
+  ig.k_len = ig.prior + ig.q_len;  // queries are the suffix of the attended keys
+  ig.off = ig.k_len - ig.q_len;
+  ig.kend = causal ? min(ig.k_len, ig.off + ig.r0 + FM) : ig.k_len;
+  return ig;
+}
+
+__device__ __forceinline__ void init_fctx(FCtx& c, const PrefillArgs& a, const ItemGeo& ig,
+                                          int wave, int lane) {
+  c.kbase = a.k + (int64_t)ig.b * a.kv_sb + (int64_t)ig.hk * a.kv_sh;
+  c.vtbase = a.vt + ((int64_t)ig.b * a.Hk + ig.hk) * a.vt_tiles * FT;
+  c.kv_st = a.kv_st;
+  c.krow_max = max(0, min(ig.k_len, a.Lk) - 1);
+  // tiles never reach past the cache (prior + q_len > Lk is a caller error: the
+  // keys past Lk were never appended), so neither do the V^T workspace reads
+  c.n_tiles = max(1, (min(ig.kend, a.Lk) + FN - 1) / FN);
+  c.wave = wave;
+  c.lane = lane;
+  c.row_bytes = (uint32_t)(2 * a.kv_st);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 2 * (4 * wave + i) + (lane >> 5);
+    c.dma_boff[i] = (uint32_t)r * c.row_bytes + (uint32_t)(((lane & 31) ^ fswz(r)) * 16);
+  }
+}
+
+// raw q row, norm weight, and RoPE table operands of this lane (row `row` of head h)
+struct QLoads {
+  uint4 qraw[16], qwv[16];
+  float4 cv[4], sv[4];
+};
+
+__device__ __forceinline__ void q_load_raw(const PrefillArgs& a, int b, int h, int row, int h2,
+                                           QLoads& ql) {
+  const int qrow = min(row, a.L - 1);
+  const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qrow * a.q_st + 8 * h2;
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) ql.qraw[kk] = load16(qp + 16 * kk);
+}
+__device__ __forceinline__ void q_load_rest(const PrefillArgs& a, int row, int prior, int h2,
+                                            QLoads& ql) {
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) ql.qwv[kk] = load16(a.qw + 16 * kk + 8 * h2);
+  const int64_t pos = min((int64_t)prior + min(row, a.L - 1), (int64_t)a.Lk - 1);
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      ql.cv[2 * kk + u] = *reinterpret_cast<const float4*>(a.cos_tab + pos * HALF_ROT + 8 * h2 + 16 * kk + 4 * u);
+      ql.sv[2 * kk + u] = *reinterpret_cast<const float4*>(a.sin_tab + pos * HALF_ROT + 8 * h2 + 16 * kk + 4 * u);
+    }
+}
+
+// q rows of one 32-row block: qnorm_rope (src/kernels/qknorm_rope_append.jl:25-57)
+// and the 1/16 scale, with the per-row 1/rms folded into that final scale (RoPE
+// is linear); lane holds q[row][16kk + 8h2 + j]
+__device__ __forceinline__ void q_prologue(const PrefillArgs& a, const QLoads& ql, uint4 (&qop)[16]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) {
+    float x[8];
+    unpack8(ql.qraw[kk], x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+  }
+  ss += __shfl_xor(ss, 32, 64);
+  const float scale = QK_SCALE / sqrtf(ss * (1.0f / HEAD_DIM) + a.eps);
+  const float* cs = reinterpret_cast<const float*>(ql.cv);
+  const float* sn = reinterpret_cast<const float*>(ql.sv);
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) {
+    if (kk == 2 || kk == 3) continue;  // rotated with d-steps 0, 1
+    float x1[8], wf[8];
+    unpack8(ql.qraw[kk], x1);
+    unpack8(ql.qwv[kk], wf);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x1[j] *= wf[j] + a.w_offset;
+    if (kk < 2) {
+      // d-steps 0..3 carry the rotary dims: pairs (d, d + 32) = d-steps (kk, kk + 2)
+      float x2[8];
+      unpack8(ql.qraw[kk + 2], x2);
+      unpack8(ql.qwv[kk + 2], wf);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        x2[j] *= wf[j] + a.w_offset;
+        const float cc = cs[8 * kk + j], si = sn[8 * kk + j];
+        const float r1 = x1[j] * cc - x2[j] * si;
+        const float r2 = x2[j] * cc + x1[j] * si;
+        x1[j] = r1;
+        x2[j] = r2;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x2[j] *= scale;
+      qop[kk + 2] = pack8(x2);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x1[j] *= scale;
+    qop[kk] = pack8(x1);
+  }
+}
+
+// ============================ pair path ============================
+
+struct PairState {
+  uint4 qop[2][16];     // Q^T operands of the pair's two 32-row blocks (held in AGPRs)
+  f32x16 o[4][2];       // O^T of d-blocks 4e .. 4e+3 x the two row blocks (AGPRs)
+  f32x16 s[2];          // S^T of this wave's current tile, per row block
+  uint32_t pprev[2][8]; // packed P^T of this wave's tile of the previous step
+  float lsum[2];        // row sums over this wave's tiles (this lane's keys)
+};
+
+struct PairCtx {
+  FCtx c;             // K tile loads
+  const char* vt;     // V^T tiles of (b, hk)
+  uint32_t voff;      // e * 8 KB + 16 lane: this lane's bytes of the wave's d-half
+  int koffe[8];       // K fragment byte offsets in a ring object (this wave's half)
+  uint32_t pxr;       // P exchange: this pair's region (tile-0 wave; tile-1 wave +4 KB)
+  uint32_t pxw;       // P exchange: this wave's region
+  float negm[2];      // minus the softmax shift of this lane's row in each row block
+  const uint16_t* gate_row[2];  // gate logits of this lane's row in each row block
+};
+
+struct PairGeo {
+  int prow0;   // first row of the pair
+  int row[2];  // this lane's row in each row block
+  int off, k_len;
+};
+
+// LDS objects: K ring slots 2s, 2s+1 in object s (halves), and the P exchange
+// area (two buffers x four waves x 4 KB)
+struct PairLds {
+  uint16_t* L[4];
+  uint16_t* PX;
+};
+
+template <bool CAUSAL>
+__device__ __forceinline__ bool pair_needs_mask(const PairGeo& g, int t) {
+  return (t * FN + FN > g.k_len) || (CAUSAL && t * FN + FN - 1 > g.off + g.prow0);
+}
+template <bool CAUSAL>
+__device__ __forceinline__ void pair_mask(const PairGeo& g, int t, int lane, f32x16 (&s)[2]) {
+  const int key0 = t * FN + 4 * (lane >> 5);
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int lim = CAUSAL ? min(g.k_len - 1, g.row[rb] + g.off) : g.k_len - 1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = key0 + 8 * (i >> 2) + (i & 3);
+      s[rb][i] = key <= lim ? s[rb][i] : -INFINITY;
+    }
+  }
+}
+
+// softmax of elements j0, j0+1 of one row block with the shift: packed P^T word
+// (bf16 pair) and the row sum of what was packed
+__device__ __forceinline__ uint32_t pair_p2(const f32x16& s, int j0, float negm, float& lsum) {
+  const float p0 = fast_exp2(__builtin_fmaf(s[j0], LOG2E, negm));
+  const float p1 = fast_exp2(__builtin_fmaf(s[j0 + 1], LOG2E, negm));
+  uint32_t w = pack2(p0, p1);
+  pin(w);
+  lsum = dot2_ones(w, lsum);
+  pin(lsum);  // summed here, not deferred (which would keep every word live)
+  return w;
+}
+
+__device__ __forceinline__ void k_addrs(const PairCtx& pc, const uint16_t* obj, uint32_t (&ka)[8]) {
+  const uint32_t kb = lds_addr(obj);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) ka[q] = kb + pc.koffe[q];
+}
+
+// QK of this wave's tile for both row blocks, as 8 pairs of K fragments (fragment
+// kk: chunk 2kk + h2 of row l%32, at ka[kk & 7] + 256 (kk >> 3)), read 4 ahead.
+// The caller issued reads 0..3 (nothing LDS older is outstanding). PV: the
+// partner's 4 P^T fragments are read after fragment 15. SM: softmax slice p
+// (words 2p, 2p+1 of row block p >> 2) rides along pair p.
+#define PRK(kk) (kf[kk] = ds_b128<256 * ((kk) >> 3)>(ka[(kk) & 7]))
+template <int P, bool PV, bool SM>
+__device__ __forceinline__ void qk_pair(PairState& st, const PairCtx& pc, const uint32_t (&ka)[8],
+                                        u32x4 (&kf)[16], u32x4 (&pf)[4], uint32_t prd,
+                                        const f32x16& s0, const f32x16& s1, uint32_t (&pw)[2][8]) {
+  // LDS ops issued after read 2P+1 at this point: reads 2P+2, 2P+3, plus (PV)
+  // the 4 P reads once issued (after read 15)
+  constexpr int W = P < 6 ? 2 : P == 6 ? (PV ? 6 : 2) : (PV ? 4 : 0);
+  lgkm_take<W>(kf[2 * P], kf[2 * P + 1]);
+  if constexpr (P == 0) {
+    mfma_qk0(st.s[0], kf[0], st.qop[0][0]);
+    mfma_qk0(st.s[1], kf[0], st.qop[1][0]);
   } else {
-    __builtin_amdgcn_sched_barrier(0);
-    uint4 kf[16];
-    if (QK) read_kf(ring.K[(J4 + 1) % NS], koff, kf);
-    uint4 pcur[2];
-    if (SM) softmax_tile(st.sc, st.m_run, st.l_part, pcur, alpha);
-    f32x16 sn;
-    if (QK) {
+    mfma_qk(st.s[0], kf[2 * P], st.qop[0][2 * P]);
+    mfma_qk(st.s[1], kf[2 * P], st.qop[1][2 * P]);
+  }
+  mfma_qk(st.s[0], kf[2 * P + 1], st.qop[0][2 * P + 1]);
+  mfma_qk(st.s[1], kf[2 * P + 1], st.qop[1][2 * P + 1]);
+  if constexpr (P < 6) {
+    PRK(2 * P + 4);
+    PRK(2 * P + 5);
+  }
+  if constexpr (PV && P == 5) {
+    pf[0] = ds_b128<0>(prd);
+    pf[1] = ds_b128<1024>(prd);
+    pf[2] = ds_b128<2048>(prd);
+    pf[3] = ds_b128<3072>(prd);
+  }
+  if constexpr (SM) {
+    constexpr int RB = P >> 2, W0 = (2 * P) & 7;
+    pw[RB][W0] = pair_p2(RB == 0 ? s0 : s1, 2 * W0, pc.negm[RB], st.lsum[RB]);
+    pw[RB][W0 + 1] = pair_p2(RB == 0 ? s0 : s1, 2 * W0 + 2, pc.negm[RB], st.lsum[RB]);
+  }
+}
+template <bool PV, bool SM>
+__device__ __forceinline__ void qk_phase(PairState& st, const PairCtx& pc, const uint32_t (&ka)[8],
+                                         u32x4 (&kf)[16], u32x4 (&pf)[4], uint32_t prd,
+                                         const f32x16& s0, const f32x16& s1, uint32_t (&pw)[2][8]) {
+#define QP(p) qk_pair<p, PV, SM>(st, pc, ka, kf, pf, prd, s0, s1, pw)
+  QP(0); QP(1); QP(2); QP(3); QP(4); QP(5); QP(6); QP(7);
+#undef QP
+  mfma_drain(st.s[0], st.s[1]);
+}
+
+// this wave's P^T words of its tile to the exchange
+__device__ __forceinline__ void p_publish(const PairCtx& pc, uint32_t pbuf, const uint32_t (&pw)[2][8]) {
+  const uint32_t wa = pc.pxw + pbuf;
+  ds_w128<0>(wa, make_uint4(pw[0][0], pw[0][1], pw[0][2], pw[0][3]));
+  ds_w128<1024>(wa, make_uint4(pw[0][4], pw[0][5], pw[0][6], pw[0][7]));
+  ds_w128<2048>(wa, make_uint4(pw[1][0], pw[1][1], pw[1][2], pw[1][3]));
+  ds_w128<3072>(wa, make_uint4(pw[1][4], pw[1][5], pw[1][6], pw[1][7]));
+}
+
+// Kinds of pair step: FIRST (i = 0: softmax, QK, no PV), STEADY, NOQK (the last
+// full step i = n_it - 1: its QK would only serve tiles past the end), LAST
+// (i = n_it: PV only).
+enum { PS_FIRST = 0, PS_STEADY = 1, PS_NOQK = 2, PS_LAST = 3 };
+
+// Pair step i (J4 = i % 4), in this order: the V^T of this step's PV (tiles
+// 2i-2+e, then 2i-1-e) and the K loads of tiles 2i+6, 2i+7 (ring object
+// (J4+3) % 4) go out; QK of this wave's tile 2i+2+e (object (J4+1) % 4) with the
+// softmax of its tile 2i+e riding along; the P^T of that tile to the exchange;
+// PV of tiles 2i-2, 2i-1: own tile with the P^T kept from the last step, the
+// partner's from the exchange. GV: the gate loads of the epilogue go out with
+// the V^T (PV-only step).
+template <bool CAUSAL, int J4, int KIND>
+__device__ __forceinline__ void pair_step(PairState& st, const PairCtx& pc, const PairLds& L,
+                                          const PairGeo& g, int i, int e, int lane,
+                                          u32x2 (&gv)[2][4][4]) {
+  constexpr bool QK = KIND == PS_FIRST || KIND == PS_STEADY;  // QK of tile 2i+2+e
+  constexpr bool SM = KIND != PS_LAST;                       // softmax of tile 2i+e
+  constexpr bool PV = KIND != PS_FIRST;                      // PV of tiles 2i-2, 2i-1
+  constexpr bool DMA = QK;                                   // K loads of tiles 2i+6, 2i+7
+  constexpr bool GV = KIND == PS_LAST;
+  // the K tiles read here landed (they went out at step i-2 or before; only the
+  // last step's 8 tile loads may still be in flight) and every wave is past
+  // step i-1 (its P writes landed)
+  fwait_vmcnt<8>();
+  fbarrier();
+  const int n = pc.c.n_tiles;
+  if (SM && pair_needs_mask<CAUSAL>(g, 2 * i + e)) pair_mask<CAUSAL>(g, 2 * i + e, lane, st.s);
+  // P exchange buffers: 16 KB each (four waves x 4 KB); step i writes buffer i & 1
+  // and reads buffer (i-1) & 1
+  constexpr uint32_t pbuf_r = ((J4 + 1) & 1) * 16384u;
+  constexpr uint32_t pbuf_w = (J4 & 1) * 16384u;
+  const uint32_t prd = pc.pxr + pbuf_r + (1 - e) * 4096;
+  uint32_t ka[8];
+  u32x4 kf[16], pf[4], vf[16];
+  if constexpr (QK) {
+    k_addrs(pc, L.L[(J4 + 1) % 4], ka);
+    PRK(0); PRK(1); PRK(2); PRK(3);
+  }
+  if constexpr (PV) {
+    const char* vbo = pc.vt + (int64_t)min(2 * i - 2 + e, n - 1) * (2 * FT);
+    const char* vbp = pc.vt + (int64_t)min(2 * i - 1 - e, n - 1) * (2 * FT);
+    const uint32_t vo0 = pc.voff, vo1 = pc.voff + 4096;
+    vf[0] = g_b128<0>(vbo, vo0);     vf[1] = g_b128<1024>(vbo, vo0);
+    vf[2] = g_b128<2048>(vbo, vo0);  vf[3] = g_b128<3072>(vbo, vo0);
+    vf[4] = g_b128<0>(vbo, vo1);     vf[5] = g_b128<1024>(vbo, vo1);
+    vf[6] = g_b128<2048>(vbo, vo1);  vf[7] = g_b128<3072>(vbo, vo1);
+    vf[8] = g_b128<0>(vbp, vo0);     vf[9] = g_b128<1024>(vbp, vo0);
+    vf[10] = g_b128<2048>(vbp, vo0); vf[11] = g_b128<3072>(vbp, vo0);
+    vf[12] = g_b128<0>(vbp, vo1);    vf[13] = g_b128<1024>(vbp, vo1);
+    vf[14] = g_b128<2048>(vbp, vo1); vf[15] = g_b128<3072>(vbp, vo1);
+  }
+  if constexpr (GV) {
+    // the epilogue's gate logits: 4 bf16 at d = 32 (4e + dq) + 8 jb + 4 h2 of this
+    // lane's row in each row block (32 loads)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sn[i] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) sn = mfma32(kf[kk], st.qop[kk], sn);
-    }
-    if (PV) {
-      const char* vl = reinterpret_cast<const char*>(ring.V[(J4 + 3) % NS]);
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          // V^T fragment: d-rows 32dt.., key half ks
-          const uint4 vfrag = *reinterpret_cast<const uint4*>(vl + vof[ks] + 2048 * dt);
-          st.acc[dt] = mfma32(vfrag, st.pprev[ks], st.acc[dt]);
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (QK) st.sc = sn;
-    if (SM) {
-      st.pprev[0] = pcur[0];
-      st.pprev[1] = pcur[1];
+    for (int rb = 0; rb < 2; ++rb) {
+      const uint16_t* gp = pc.gate_row[rb] + 32 * (4 * e) + 4 * (lane >> 5);
+      gv[rb][0][0] = g_b64<0>(gp);    gv[rb][0][1] = g_b64<16>(gp);
+      gv[rb][0][2] = g_b64<32>(gp);   gv[rb][0][3] = g_b64<48>(gp);
+      gv[rb][1][0] = g_b64<64>(gp);   gv[rb][1][1] = g_b64<80>(gp);
+      gv[rb][1][2] = g_b64<96>(gp);   gv[rb][1][3] = g_b64<112>(gp);
+      gv[rb][2][0] = g_b64<128>(gp);  gv[rb][2][1] = g_b64<144>(gp);
+      gv[rb][2][2] = g_b64<160>(gp);  gv[rb][2][3] = g_b64<176>(gp);
+      gv[rb][3][0] = g_b64<192>(gp);  gv[rb][3][1] = g_b64<208>(gp);
+      gv[rb][3][2] = g_b64<224>(gp);  gv[rb][3][3] = g_b64<240>(gp);
     }
   }
-  if (SM && __ballot(alpha != 1.0f) != 0ull) {
-    // the shift grew: what the accumulator holds (through PV(j-1), at the old
-    // shift) moves to the new one (rare)
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) st.acc[dt] *= alpha;
+  if constexpr (DMA) {
+    issue_quarter(pc.c, 2 * i + 6, L.L[(J4 + 3) % 4]);
+    issue_quarter(pc.c, 2 * i + 7, L.L[(J4 + 3) % 4] + FT);
   }
+  uint32_t pw[2][8];
+  f32x16 s0, s1;
+  if constexpr (SM) {
+    s0 = st.s[0];
+    s1 = st.s[1];
+    pin(s0);
+    pin(s1);
+  }
+  if constexpr (QK) {
+    qk_phase<PV, SM>(st, pc, ka, kf, pf, prd, s0, s1, pw);
+  } else {
+    if constexpr (PV) {
+      pf[0] = ds_b128<0>(prd);
+      pf[1] = ds_b128<1024>(prd);
+      pf[2] = ds_b128<2048>(prd);
+      pf[3] = ds_b128<3072>(prd);
+    }
+    if constexpr (SM) {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) pw[rb][q] = pair_p2(rb == 0 ? s0 : s1, 2 * q, pc.negm[rb], st.lsum[rb]);
+    }
+  }
+  if constexpr (SM) p_publish(pc, pbuf_w, pw);
+  if constexpr (PV) {
+    // V^T slots 4g .. 4g+3 landed: loads issued after slot 4g+3 are the later V
+    // loads (12 - 4g) and this step's tile loads (8) or gate loads (32)
+    constexpr int VX = DMA ? 8 : (GV ? 32 : 0);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int dq = (k & 7) >> 1, ks = k & 1;
+      if (k == 0) vm_take<12 + VX>(vf[0], vf[1], vf[2], vf[3]);
+      if (k == 4) vm_take<8 + VX>(vf[4], vf[5], vf[6], vf[7]);
+      if (k == 8) {
+        vm_take<4 + VX>(vf[8], vf[9], vf[10], vf[11]);
+        // the partner's P^T: only this step's P writes (if any) are younger
+        if constexpr (SM) lgkm_take<4>(pf[0], pf[1], pf[2], pf[3]);
+        else lgkm_take<0>(pf[0], pf[1], pf[2], pf[3]);
+      }
+      if (k == 12) vm_take<VX>(vf[12], vf[13], vf[14], vf[15]);
+      uint4 p0, p1;
+      if (k < 8) {
+        p0 = make_uint4(st.pprev[0][4 * ks], st.pprev[0][4 * ks + 1], st.pprev[0][4 * ks + 2], st.pprev[0][4 * ks + 3]);
+        p1 = make_uint4(st.pprev[1][4 * ks], st.pprev[1][4 * ks + 1], st.pprev[1][4 * ks + 2], st.pprev[1][4 * ks + 3]);
+      } else {
+        p0 = __builtin_bit_cast(uint4, pf[ks]);
+        p1 = __builtin_bit_cast(uint4, pf[2 + ks]);
+      }
+      st.o[dq][0] = mfma32(__builtin_bit_cast(uint4, vf[k]), p0, st.o[dq][0]);
+      st.o[dq][1] = mfma32(__builtin_bit_cast(uint4, vf[k]), p1, st.o[dq][1]);
+    }
+  }
+  if constexpr (SM) {
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) st.pprev[rb][q] = pw[rb][q];
+  }
+  lgkm_wait<0>();  // this step's LDS writes land before the next barrier
+}
+
+// Exact row max of S over the item's keys for this pair's rows (the QK-only pass
+// for weights whose bound is too loose for a static shift). Step i reads K(2i),
+// K(2i+1) from ring object i % 4 and loads K(2i+6), K(2i+7) into object (i+3) % 4.
+template <bool CAUSAL, int J4>
+__device__ __forceinline__ void max_step(PairState& st, const PairCtx& pc, const PairLds& L,
+                                         const PairGeo& g, int i, int e, int lane, float (&m)[2]) {
+  // K(2i), K(2i+1) landed: the loads after them are two steps' tile loads
+  fwait_vmcnt<16>();
+  fbarrier();
+  uint32_t ka[8];
+  u32x4 kf[16], pf[4];
+  uint32_t pw[2][8];
+  k_addrs(pc, L.L[J4], ka);
+  PRK(0); PRK(1); PRK(2); PRK(3);
+  issue_quarter(pc.c, 2 * i + 6, L.L[(J4 + 3) % 4]);
+  issue_quarter(pc.c, 2 * i + 7, L.L[(J4 + 3) % 4] + FT);
+  qk_phase<false, false>(st, pc, ka, kf, pf, 0u, st.s[0], st.s[1], pw);
+  if (pair_needs_mask<CAUSAL>(g, 2 * i + e)) pair_mask<CAUSAL>(g, 2 * i + e, lane, st.s);
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) m[rb] = fmaxf(m[rb], st.s[rb][j]);
 }
 
 template <bool CAUSAL>
-__device__ __forceinline__ void run_tiles(WaveState& st, const FCtx& c, const LdsRing& ring,
-                                          const WaveGeo& g, const int (&koff)[8],
-                                          const int (&vof)[2]) {
-  const int n = c.n_tiles;
-  // iteration 0: softmax(0), QK(1); no PV yet
-  iter<CAUSAL, 0, false, true, true>(st, c, ring, g, 0, koff, vof);
-  // steady iterations 1 .. n-1 (QK(n) at j = n-1 reads a repeated tile; unused)
-  int j = 1;
-  for (; j + 3 < n; j += 4) {
-    iter<CAUSAL, 1, true, true, true>(st, c, ring, g, j, koff, vof);
-    iter<CAUSAL, 2, true, true, true>(st, c, ring, g, j + 1, koff, vof);
-    iter<CAUSAL, 3, true, true, true>(st, c, ring, g, j + 2, koff, vof);
-    iter<CAUSAL, 0, true, true, true>(st, c, ring, g, j + 3, koff, vof);
-  }
-  // remaining steady iterations, then the PV(n-1)-only iteration j = n
-  const int rem = n - j;  // 0..3 steady iterations left
-  if (rem >= 1) iter<CAUSAL, 1, true, true, true>(st, c, ring, g, j, koff, vof);
-  if (rem >= 2) iter<CAUSAL, 2, true, true, true>(st, c, ring, g, j + 1, koff, vof);
-  if (rem >= 3) iter<CAUSAL, 3, true, true, true>(st, c, ring, g, j + 2, koff, vof);
-  switch (n & 3) {  // the last iteration is j = n, slot n % 4
-    case 0: iter<CAUSAL, 0, true, false, false>(st, c, ring, g, n, koff, vof); break;
-    case 1: iter<CAUSAL, 1, true, false, false>(st, c, ring, g, n, koff, vof); break;
-    case 2: iter<CAUSAL, 2, true, false, false>(st, c, ring, g, n, koff, vof); break;
-    default: iter<CAUSAL, 3, true, false, false>(st, c, ring, g, n, koff, vof); break;
-  }
+__device__ __forceinline__ void prime_ring(const PairCtx& pc, const PairLds& L) {
+  // K(0) .. K(5) into objects 0..2 (object 3 and the exchange area are free)
+  issue_quarter(pc.c, 0, L.L[0]);
+  issue_quarter(pc.c, 1, L.L[0] + FT);
+  issue_quarter(pc.c, 2, L.L[1]);
+  issue_quarter(pc.c, 3, L.L[1] + FT);
+  issue_quarter(pc.c, 4, L.L[2]);
+  issue_quarter(pc.c, 5, L.L[2] + FT);
 }
 
-}  // namespace
-
-template <bool CAUSAL, bool PERSIST>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void prefill_fused_kernel(PrefillArgs a, int n_items, int P) {
-  // four __shared__ objects A_s, each holding K slot s and V slot (s+2)%4: the two
-  // loads issued in iteration j both go to A_{j%4}, its reads (K slot j+1, V slot
-  // j-1) come from A_{(j+1)%4}, whose last loads finished three iterations back,
-  // so the compiler can see that no read aliases a load in flight (one object for
-  // the whole ring would make it drain every load before each read)
-  __shared__ __attribute__((aligned(1024))) uint16_t A0[2 * FT], A1[2 * FT], A2[2 * FT], A3[2 * FT];
-  LdsRing ring;
-  ring.K[0] = A0; ring.K[1] = A1; ring.K[2] = A2; ring.K[3] = A3;
-  ring.V[0] = A2 + FT; ring.V[1] = A3 + FT; ring.V[2] = A0 + FT; ring.V[3] = A1 + FT;
-
-  // the wave index through readfirstlane: a scalar, so tile-load LDS addresses
-  // (M0) are scalar arithmetic rather than hoisted vector registers
+// One item (shift: the static softmax shift in log2 units, or < 0 for the
+// exact-max pass).
+template <bool CAUSAL>
+__device__ __forceinline__ void pair_item(const PrefillArgs& a, const FItem& it, const PairLds& L,
+                                          float shift) {
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int l32 = lane & 31, h2 = lane >> 5;
-  const int HB = a.H * a.B;
-
-  // swizzled LDS read offsets (bytes). K: chunk c = 2kk + h2 of row l32 sits at
-  // chunk c ^ fswz(l32). V^T: a transposing read by lane i of 16-lane group m
-  // reads key row rr = 8hi + 4(m>>1) + (i>>2) (+16 ks), d-chunk 4dt + u with
-  // u = 2(m&1) + ((i&3)>>1), 8-byte half i&1.
-  int koff[8], vof[2];
+  const int pr = wave >> 1, e = wave & 1;
+  const ItemGeo ig = item_geo(a, it, CAUSAL);
+  const int prow0 = ig.r0 + 64 * pr;
+  const int row_own = prow0 + 32 * e + l32;  // this wave computes row block e's q
+  QLoads ql;
+  q_load_raw(a, ig.b, ig.h, row_own, h2, ql);
+  if (ig.r0 >= ig.q_len) return;  // uniform over the workgroup
+  PairGeo g;
+  g.prow0 = prow0;
+  g.row[0] = prow0 + l32;
+  g.row[1] = prow0 + 32 + l32;
+  g.off = ig.off;
+  g.k_len = ig.k_len;
+  PairCtx pc;
+  init_fctx(pc.c, a, ig, wave, lane);
+  pc.vt = reinterpret_cast<const char*>(pc.c.vtbase);
+  pc.voff = (uint32_t)(e * 8192 + 16 * lane);
   {
     const int sk = fswz(l32);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) koff[q] = l32 * 512 + 16 * ((2 * q + h2) ^ sk);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) vof[ks] = vt_chunk_offset(l32, 2 * ks + h2);
+    for (int q = 0; q < 8; ++q) pc.koffe[q] = e * (2 * FT) + l32 * 512 + 16 * ((2 * q + h2) ^ sk);
   }
-  // static bound on |k~| (rows of any kv head): sqrt(D) * max|kw + w_offset|
-  float kbound;
+  pc.pxr = lds_addr(L.PX) + (2 * pr) * 4096 + 16 * lane;
+  pc.pxw = lds_addr(L.PX) + wave * 4096 + 16 * lane;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+    pc.gate_row[rb] = a.gate + (int64_t)ig.b * a.g_sb + (int64_t)ig.h * a.g_sh +
+                      (int64_t)min(g.row[rb], a.L - 1) * a.g_st;
+  q_load_rest(a, row_own, ig.prior, h2, ql);
+  prime_ring<CAUSAL>(pc, L);
+
+  PairState st;
   {
-    const uint2 wv = *reinterpret_cast<const uint2*>(a.kw + 4 * lane);
-    float wmax = fmaxf(fmaxf(fabsf(__uint_as_float(wv.x << 16) + a.w_offset),
-                             fabsf(__uint_as_float(wv.x & 0xffff0000u) + a.w_offset)),
-                       fmaxf(fabsf(__uint_as_float(wv.y << 16) + a.w_offset),
-                             fabsf(__uint_as_float(wv.y & 0xffff0000u) + a.w_offset)));
+    uint4 qown[16];
+    q_prologue(a, ql, qown);
+    // exchange: wave w's 16 fragments (16 KB) in object 3 (waves 0, 1) or PX (2, 3)
+    const uint32_t xbase = wave < 2 ? lds_addr(L.L[3]) : lds_addr(L.PX);
+    const uint32_t xw = xbase + e * (2 * FT) + 16 * lane;
+    const uint32_t xr = xbase + (1 - e) * (2 * FT) + 16 * lane;
+    ds_w128<0>(xw, qown[0]);         ds_w128<1024>(xw, qown[1]);
+    ds_w128<2048>(xw, qown[2]);      ds_w128<3072>(xw, qown[3]);
+    ds_w128<4096>(xw, qown[4]);      ds_w128<5120>(xw, qown[5]);
+    ds_w128<6144>(xw, qown[6]);      ds_w128<7168>(xw, qown[7]);
+    ds_w128<8192>(xw, qown[8]);      ds_w128<9216>(xw, qown[9]);
+    ds_w128<10240>(xw, qown[10]);    ds_w128<11264>(xw, qown[11]);
+    ds_w128<12288>(xw, qown[12]);    ds_w128<13312>(xw, qown[13]);
+    ds_w128<14336>(xw, qown[14]);    ds_w128<15360>(xw, qown[15]);
+    // K(0), K(1) landed (K(2) .. K(5) may be in flight); the exchange written
+    fwait_vmcnt<16>();
+    lgkm_wait<0>();
+    fbarrier();
+    // the partner's fragments: reads and their wait in one statement (the
+    // outputs exist only once the data is in)
+    u32x4 qx[16];
+    asm volatile(
+        "ds_read_b128 %0, %16 offset:0\n\tds_read_b128 %1, %16 offset:1024\n\t"
+        "ds_read_b128 %2, %16 offset:2048\n\tds_read_b128 %3, %16 offset:3072\n\t"
+        "ds_read_b128 %4, %16 offset:4096\n\tds_read_b128 %5, %16 offset:5120\n\t"
+        "ds_read_b128 %6, %16 offset:6144\n\tds_read_b128 %7, %16 offset:7168\n\t"
+        "ds_read_b128 %8, %16 offset:8192\n\tds_read_b128 %9, %16 offset:9216\n\t"
+        "ds_read_b128 %10, %16 offset:10240\n\tds_read_b128 %11, %16 offset:11264\n\t"
+        "ds_read_b128 %12, %16 offset:12288\n\tds_read_b128 %13, %16 offset:13312\n\t"
+        "ds_read_b128 %14, %16 offset:14336\n\tds_read_b128 %15, %16 offset:15360\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(qx[0]), "=&v"(qx[1]), "=&v"(qx[2]), "=&v"(qx[3]), "=&v"(qx[4]), "=&v"(qx[5]),
+          "=&v"(qx[6]), "=&v"(qx[7]), "=&v"(qx[8]), "=&v"(qx[9]), "=&v"(qx[10]), "=&v"(qx[11]),
+          "=&v"(qx[12]), "=&v"(qx[13]), "=&v"(qx[14]), "=&v"(qx[15])
+        : "v"(xr));
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) wmax = fmaxf(wmax, __shfl_xor(wmax, m, 64));
-    kbound = 16.0f * wmax * 1.01f;  // + bf16 rounding of the cached rows
+    for (int kk = 0; kk < 16; ++kk) {
+      const uint4 other = __builtin_bit_cast(uint4, qx[kk]);
+      st.qop[0][kk] = e == 0 ? qown[kk] : other;
+      st.qop[1][kk] = e == 0 ? other : qown[kk];
+    }
+  }
+  // rows past the chunk hold finite junk q; their outputs are never stored
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) pin_acc(st.qop[rb][kk]);
+
+  const int n_it = (pc.c.n_tiles + 1) >> 1;
+  if (shift >= 0.f) {
+    pc.negm[0] = -shift;
+    pc.negm[1] = -shift;
+  } else {
+    // exact row max (QK only), combined over the pair through the exchange area
+    float m[2] = {-INFINITY, -INFINITY};
+    int i = 0;
+    for (; i + 3 < n_it; i += 4) {
+      max_step<CAUSAL, 0>(st, pc, L, g, i, e, lane, m);
+      max_step<CAUSAL, 1>(st, pc, L, g, i + 1, e, lane, m);
+      max_step<CAUSAL, 2>(st, pc, L, g, i + 2, e, lane, m);
+      max_step<CAUSAL, 3>(st, pc, L, g, i + 3, e, lane, m);
+    }
+    if (i < n_it) max_step<CAUSAL, 0>(st, pc, L, g, i, e, lane, m);
+    if (i + 1 < n_it) max_step<CAUSAL, 1>(st, pc, L, g, i + 1, e, lane, m);
+    if (i + 2 < n_it) max_step<CAUSAL, 2>(st, pc, L, g, i + 2, e, lane, m);
+    fwait_vmcnt<0>();
+    fbarrier();  // ring and exchange area free again
+    float* lx = reinterpret_cast<float*>(L.PX);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      m[rb] = xor32_max(m[rb]);
+      if (h2 == 0) lx[wave * 64 + rb * 32 + l32] = m[rb];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const float mr = fmaxf(m[rb], lx[(wave ^ 1) * 64 + rb * 32 + l32]) * LOG2E;
+      pc.negm[rb] = mr == -INFINITY ? 0.f : -mr;  // fully-masked row: P = 0
+    }
+    __syncthreads();
+    prime_ring<CAUSAL>(pc, L);
+    fwait_vmcnt<16>();  // K(0), K(1)
+    fbarrier();
+  }
+#pragma unroll
+  for (int dq = 0; dq < 4; ++dq)
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) st.o[dq][rb][j] = 0.f;
+  st.lsum[0] = 0.f;
+  st.lsum[1] = 0.f;
+
+  // S^T of tile e (object 0, half e)
+  {
+    uint32_t ka[8];
+    u32x4 kf[16], pf[4];
+    uint32_t pw[2][8];
+    k_addrs(pc, L.L[0], ka);
+    PRK(0); PRK(1); PRK(2); PRK(3);
+    qk_phase<false, false>(st, pc, ka, kf, pf, 0u, st.s[0], st.s[1], pw);
   }
 
-  WaveState st;
-  for (int p = 0; PERSIST || p < 1; ++p) {
-    const int idx = PERSIST ? item_index(p, blockIdx.x, P, HB) : (int)blockIdx.x;
-    if (idx >= n_items) break;
-    const FItem it = item_at(a, idx);
-    const int b = it.b, h = it.h;
-    const int r0 = it.qt * FM;
-    const int row = r0 + 32 * wave + l32;
-
-    // raw q rows first: they depend on nothing the length lookups return
-    const int qrow = min(row, a.L - 1);
-    const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
-                         (int64_t)qrow * a.q_st + 8 * h2;
-    uint4 qraw[16];
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) qraw[kk] = load16(qp + 16 * kk);
-
-    const int q_len = a.q_lengths ? min(a.q_lengths[b], a.L) : a.L;
-    if (r0 >= q_len) continue;  // uniform over the workgroup
-    const int prior = a.prior ? a.prior[b] : 0;
-    const int k_len = prior + q_len;  // queries are the suffix of the attended keys
-    WaveGeo g;
-    g.row = row;
-    g.wrow0 = r0 + 32 * wave;
-    g.wrow1 = g.wrow0 + 31;
-    g.off = k_len - q_len;
-    g.k_len = k_len;
-    const int kend = CAUSAL ? min(k_len, g.off + r0 + FM) : k_len;
-
-    FCtx c;
-    c.kbase = a.k + (int64_t)b * a.kv_sb + (int64_t)it.hk * a.kv_sh;
-    c.vtbase = a.vt + ((int64_t)b * a.Hk + it.hk) * a.vt_tiles * FT;
-    c.kv_st = a.kv_st;
-    c.krow_max = max(0, min(k_len, a.Lk) - 1);
-    c.n_tiles = max(1, (kend + FN - 1) / FN);
-    c.wave = wave;
-    c.lane = lane;
-    c.row_bytes = (uint32_t)(2 * a.kv_st);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 2 * (4 * wave + i) + (lane >> 5);
-      c.dma_boff[i] = (uint32_t)r * c.row_bytes + (uint32_t)(((lane & 31) ^ fswz(r)) * 16);
+  u32x2 gv[2][4][4];
+  pair_step<CAUSAL, 0, PS_FIRST>(st, pc, L, g, 0, e, lane, gv);
+  // steps 1 .. n_it-2 steady, n_it-1 without QK, n_it PV only
+  int i = 1;
+  for (; i + 3 < n_it - 1; i += 4) {
+    pair_step<CAUSAL, 1, PS_STEADY>(st, pc, L, g, i, e, lane, gv);
+    pair_step<CAUSAL, 2, PS_STEADY>(st, pc, L, g, i + 1, e, lane, gv);
+    pair_step<CAUSAL, 3, PS_STEADY>(st, pc, L, g, i + 2, e, lane, gv);
+    pair_step<CAUSAL, 0, PS_STEADY>(st, pc, L, g, i + 3, e, lane, gv);
+  }
+  const int rem = n_it - 1 - i;  // steady steps left: -1 .. 3 (-1: n_it = 1)
+  if (rem >= 1) pair_step<CAUSAL, 1, PS_STEADY>(st, pc, L, g, i, e, lane, gv);
+  if (rem >= 2) pair_step<CAUSAL, 2, PS_STEADY>(st, pc, L, g, i + 1, e, lane, gv);
+  if (rem >= 3) pair_step<CAUSAL, 3, PS_STEADY>(st, pc, L, g, i + 2, e, lane, gv);
+  if (n_it >= 2) {
+    switch ((n_it - 1) & 3) {
+      case 0: pair_step<CAUSAL, 0, PS_NOQK>(st, pc, L, g, n_it - 1, e, lane, gv); break;
+      case 1: pair_step<CAUSAL, 1, PS_NOQK>(st, pc, L, g, n_it - 1, e, lane, gv); break;
+      case 2: pair_step<CAUSAL, 2, PS_NOQK>(st, pc, L, g, n_it - 1, e, lane, gv); break;
+      default: pair_step<CAUSAL, 3, PS_NOQK>(st, pc, L, g, n_it - 1, e, lane, gv); break;
     }
-    // the other prologue operands, also ahead of the tile loads (loads complete
-    // in order: the prologue math must not wait behind six tiles)
-    // (qw is the same for every item: an opaque zero keeps the compiler from
-    // hoisting these 64 registers out of the item loop and through the main loop)
-    int opaque0 = 0;
-    asm volatile("" : "+v"(opaque0));
-    uint4 qwv[16];
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) qwv[kk] = load16(a.qw + opaque0 + 16 * kk + 8 * h2);
-    const int64_t pos = min((int64_t)prior + qrow, (int64_t)a.Lk - 1);
-    float4 cv[4], sv[4];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        cv[2 * kk + u] = *reinterpret_cast<const float4*>(a.cos_tab + pos * HALF_ROT + 8 * h2 + 16 * kk + 4 * u);
-        sv[2 * kk + u] = *reinterpret_cast<const float4*>(a.sin_tab + pos * HALF_ROT + 8 * h2 + 16 * kk + 4 * u);
-      }
-    // pre-loop loads, in the order of the virtual iterations -4 .. -1 of the
-    // pipeline: K(0), K(1), K(2)+V(0), K(3)+V(1)
-    issue_quarter(c, c.kbase, 0, ring.K[0]);
-    issue_quarter(c, c.kbase, 1, ring.K[1]);
-    issue_quarter(c, c.kbase, 2, ring.K[2]);
-    issue_quarter_vt(c, 0, ring.V[0]);
-    issue_quarter(c, c.kbase, 3, ring.K[3]);
-    issue_quarter_vt(c, 1, ring.V[1]);
+  }
+  switch (n_it & 3) {  // the PV-only step n_it
+    case 0: pair_step<CAUSAL, 0, PS_LAST>(st, pc, L, g, n_it, e, lane, gv); break;
+    case 1: pair_step<CAUSAL, 1, PS_LAST>(st, pc, L, g, n_it, e, lane, gv); break;
+    case 2: pair_step<CAUSAL, 2, PS_LAST>(st, pc, L, g, n_it, e, lane, gv); break;
+    default: pair_step<CAUSAL, 3, PS_LAST>(st, pc, L, g, n_it, e, lane, gv); break;
+  }
 
-    // ---- q prologue: qnorm_rope (src/kernels/qknorm_rope_append.jl:25-57) and
-    // the 1/16 scale (exact in bf16); lane holds q[row][16kk + 8h2 + j]
-    float qn2 = 0.f;
-    {
-      float x[16][8];
+  // ---- epilogue: row sums of both waves of the pair through LDS, normalise,
+  // gate (sigmoid, src/kernels/kernels.jl:34), store this wave's d-half in the Wo
+  // input layout
+  fbarrier();  // every wave is done with the P exchange area
+  float* lx = reinterpret_cast<float*>(L.PX);
+  float lrow[2];
 #pragma unroll
-      for (int kk = 0; kk < 16; ++kk) unpack8(qraw[kk], x[kk]);
-      float ss = 0.f;
+  for (int rb = 0; rb < 2; ++rb) {
+    lrow[rb] = st.lsum[rb] + __shfl_xor(st.lsum[rb], 32, 64);
+    if (h2 == 0) lx[wave * 64 + rb * 32 + l32] = lrow[rb];
+  }
+  __syncthreads();
+  vm_take8<0>(gv[0], 0);
+  vm_take8<0>(gv[0], 2);
+  vm_take8<0>(gv[1], 0);
+  vm_take8<0>(gv[1], 2);
 #pragma unroll
-      for (int kk = 0; kk < 16; ++kk)
+  for (int rb = 0; rb < 2; ++rb) {
+    const float l_tot = lrow[rb] + lx[(wave ^ 1) * 64 + rb * 32 + l32];
+    const float inv = l_tot > 0.f ? fast_rcp(l_tot) : 0.f;  // fully-masked row -> 0
+    const int row = g.row[rb];
+    if (row < ig.q_len) {
+      uint16_t* op = a.o + (int64_t)ig.b * a.o_sb + (int64_t)ig.h * a.o_sh + (int64_t)row * a.o_st;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ss += x[kk][j] * x[kk][j];
-      ss += __shfl_xor(ss, 32, 64);
-      const float rn = 1.0f / sqrtf(ss * (1.0f / HEAD_DIM) + a.eps);
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) {
-        float wf[8];
-        unpack8(qwv[kk], wf);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[kk][j] = x[kk][j] * rn * (wf[j] + a.w_offset);
-      }
-      const float* cs = reinterpret_cast<const float*>(cv);
-      const float* sn = reinterpret_cast<const float*>(sv);
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float cc = cs[8 * kk + j], si = sn[8 * kk + j];
-          const float x1 = x[kk][j], x2 = x[kk + 2][j];
-          x[kk][j] = x1 * cc - x2 * si;
-          x[kk + 2][j] = x2 * cc + x1 * si;
-        }
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          x[kk][j] *= QK_SCALE;
-          qn2 += x[kk][j] * x[kk][j];
-        }
-        st.qop[kk] = pack8(x[kk]);
-      }
-    }
-    qn2 += __shfl_xor(qn2, 32, 64);
-    const float bound = sqrtf(qn2) * 1.01f * kbound * LOG2E;  // |q op| rounded to bf16
-    const bool use_static = __ballot(!(bound <= FSTATIC_LIMIT)) == 0ull;
-    st.m_run = use_static ? bound : -INFINITY;
-    st.l_part = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) st.acc[i][j] = 0.f;
-
-    // S^T(0): K(0) landed (K(1), K(2)+V(0), K(3)+V(1) may be in flight)
-    fwait_vmcnt<20>();
-    fbarrier();
-    {
-      uint4 kf[16];
-      read_kf(ring.K[0], koff, kf);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) st.sc[i] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) st.sc = mfma32(kf[kk], st.qop[kk], st.sc);
-    }
-    run_tiles<CAUSAL>(st, c, ring, g, koff, vof);
-
-    // ---- epilogue: normalise, gate (sigmoid, src/kernels/kernels.jl:34), store
-    // in the Wo input layout. Every gate load goes out before the first store.
-    if (row < q_len) {
-      const float l_tot = st.l_part + __shfl_xor(st.l_part, 32, 64);
-      const float inv = l_tot > 0.f ? fast_rcp(l_tot) : 0.f;  // fully-masked row -> 0
-      const uint16_t* gp = a.gate + (int64_t)b * a.g_sb + (int64_t)h * a.g_sh + (int64_t)row * a.g_st;
-      uint2 gv[8][4];
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb)
-          gv[dt][jb] = *reinterpret_cast<const uint2*>(gp + 32 * dt + 8 * jb + 4 * h2);
-      uint16_t* op = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)row * a.o_st;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
+      for (int dq = 0; dq < 4; ++dq) {
+        const f32x16& acc = st.o[dq][rb];
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
-          const int d0 = 32 * dt + 8 * jb + 4 * h2;
-          const uint2 g2 = gv[dt][jb];
-          const float o0 = st.acc[dt][4 * jb + 0] * inv * sigmoidf(__uint_as_float(g2.x << 16));
-          const float o1 = st.acc[dt][4 * jb + 1] * inv * sigmoidf(__uint_as_float(g2.x & 0xffff0000u));
-          const float o2 = st.acc[dt][4 * jb + 2] * inv * sigmoidf(__uint_as_float(g2.y << 16));
-          const float o3 = st.acc[dt][4 * jb + 3] * inv * sigmoidf(__uint_as_float(g2.y & 0xffff0000u));
+          const int d0 = 32 * (4 * e + dq) + 8 * jb + 4 * h2;
+          const uint2 g2 = make_uint2(gv[rb][dq][jb].x, gv[rb][dq][jb].y);
+          const float o0 = acc[4 * jb + 0] * inv * sigmoidf(__uint_as_float(g2.x << 16));
+          const float o1 = acc[4 * jb + 1] * inv * sigmoidf(__uint_as_float(g2.x & 0xffff0000u));
+          const float o2 = acc[4 * jb + 2] * inv * sigmoidf(__uint_as_float(g2.y << 16));
+          const float o3 = acc[4 * jb + 3] * inv * sigmoidf(__uint_as_float(g2.y & 0xffff0000u));
           uint2 ov;
           ov.x = pack2(o0, o1);
           ov.y = pack2(o2, o3);
           *reinterpret_cast<uint2*>(op + d0) = ov;
         }
+      }
     }
-    // the ring is reused by the next item: every load landed, every wave done
-    fwait_vmcnt<0>();
-    fbarrier();
   }
+}
+#undef PRK
+
+}  // namespace
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void prefill_fused_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint16_t A0[2 * FT], A1[2 * FT], A2[2 * FT], A3[2 * FT],
+      PX[2 * FT];
+  const int lane = threadIdx.x & 63;
+  // static bounds from the norm weights: |k~| <= sqrt(D) * max|kw + w_offset| for
+  // every cached row, |q op| <= max|qw + w_offset| for every scaled query row
+  // (RMS-normalised rows have norm <= sqrt(D)); 1% covers the bf16 roundings
+  float kmax, qmax;
+  {
+    const uint2 kv = *reinterpret_cast<const uint2*>(a.kw + 4 * lane);
+    const uint2 qv = *reinterpret_cast<const uint2*>(a.qw + 4 * lane);
+    kmax = fmaxf(fmaxf(fabsf(__uint_as_float(kv.x << 16) + a.w_offset),
+                       fabsf(__uint_as_float(kv.x & 0xffff0000u) + a.w_offset)),
+                 fmaxf(fabsf(__uint_as_float(kv.y << 16) + a.w_offset),
+                       fabsf(__uint_as_float(kv.y & 0xffff0000u) + a.w_offset)));
+    qmax = fmaxf(fmaxf(fabsf(__uint_as_float(qv.x << 16) + a.w_offset),
+                       fabsf(__uint_as_float(qv.x & 0xffff0000u) + a.w_offset)),
+                 fmaxf(fabsf(__uint_as_float(qv.y << 16) + a.w_offset),
+                       fabsf(__uint_as_float(qv.y & 0xffff0000u) + a.w_offset)));
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      kmax = fmaxf(kmax, __shfl_xor(kmax, m, 64));
+      qmax = fmaxf(qmax, __shfl_xor(qmax, m, 64));
+    }
+  }
+  const float bound = qmax * 1.01f * 16.0f * kmax * 1.01f * LOG2E;  // >= every |logit|, log2 units
+  PairLds L;
+  L.L[0] = A0; L.L[1] = A1; L.L[2] = A2; L.L[3] = A3;
+  L.PX = PX;
+  pair_item<CAUSAL>(a, item_at(a, blockIdx.x), L, bound <= FSTATIC_LIMIT ? bound : -1.0f);
   fwait_vmcnt<0>();  // no LDS load may land after the workgroup is gone
 }
 
@@ -757,22 +941,12 @@ hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st) {
 hipError_t launch_prefill_fused(const PrefillArgs& a, hipStream_t st) {
   const int64_t n_items = (int64_t)a.n_qt * a.H * a.B;
   if (n_items == 0) return hipSuccess;
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 256;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-      n = 256;
-    cus = n;
-  }
   // one item per workgroup, heaviest first (the hardware hands the next item to
   // the first CU that frees up)
-  const int P = (int)n_items;
-  (void)cus;
   if (a.causal)
-    hipLaunchKernelGGL((prefill_fused_kernel<true, false>), dim3(P), dim3(256), 0, st, a, (int)n_items, P);
+    hipLaunchKernelGGL((prefill_fused_kernel<true>), dim3((unsigned)n_items), dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((prefill_fused_kernel<false, false>), dim3(P), dim3(256), 0, st, a, (int)n_items, P);
+    hipLaunchKernelGGL((prefill_fused_kernel<false>), dim3((unsigned)n_items), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
