@@ -142,25 +142,17 @@ __device__ __forceinline__ void issue_quarter(const FCtx& c, int t, uint16_t* ds
   t = min(t, c.n_tiles - 1);
   const int row0 = t * FN;
   const char* src = reinterpret_cast<const char*>(c.kbase + (int64_t)row0 * c.kv_st);
-  if (row0 + FN - 1 <= c.krow_max) {
+  // rows past the last readable one re-read it (they are masked); one code path,
+  // so every step issues the same count of loads
+  const int last = c.krow_max - row0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int g = 4 * c.wave + i;
-      __builtin_amdgcn_global_load_lds((const void*)(src + c.dma_boff[i]),
-                                       (__attribute__((address_space(3))) void*)(dst + g * 512),
-                                       16, 0, 0);
-    }
-  } else {
-    const int last = c.krow_max - row0;  // last readable row of the tile
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int g = 4 * c.wave + i;
-      const int r = 2 * g + (c.lane >> 5);
-      const uint32_t over = (uint32_t)max(0, r - last);
-      __builtin_amdgcn_global_load_lds((const void*)(src + (c.dma_boff[i] - over * c.row_bytes)),
-                                       (__attribute__((address_space(3))) void*)(dst + g * 512),
-                                       16, 0, 0);
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int g = 4 * c.wave + i;
+    const int r = 2 * g + (c.lane >> 5);
+    const uint32_t over = (uint32_t)max(0, r - last);
+    __builtin_amdgcn_global_load_lds((const void*)(src + (c.dma_boff[i] - over * c.row_bytes)),
+                                     (__attribute__((address_space(3))) void*)(dst + g * 512),
+                                     16, 0, 0);
   }
 }
 
@@ -238,6 +230,13 @@ __device__ __forceinline__ void vm_take8(u32x2 (&g)[4][4], int dq0) {
                : "+v"(g[dq0][0]), "+v"(g[dq0][1]), "+v"(g[dq0][2]), "+v"(g[dq0][3]),
                  "+v"(g[dq0 + 1][0]), "+v"(g[dq0 + 1][1]), "+v"(g[dq0 + 1][2]), "+v"(g[dq0 + 1][3])
                : "n"(N));
+}
+// a 16-byte workspace load into v in place (tied: whatever read the old contents
+// of v is placed before it, and nothing can read the new contents before vm_take)
+template <int IMM>
+__device__ __forceinline__ void g_b128_into(u32x4& v, const char* base, uint32_t off) {
+  static_assert(IMM >= 0 && IMM < 4096, "global offset is 13-bit signed");
+  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "+v"(v) : "v"(off), "s"(base), "i"(IMM));
 }
 template <int N>
 __device__ __forceinline__ void lgkm_take(u32x4& x, u32x4& y) {
@@ -388,6 +387,8 @@ struct PairState {
   f32x16 o[4][2];       // O^T of d-blocks 4e .. 4e+3 x the two row blocks (AGPRs)
   f32x16 s[2];          // S^T of this wave's current tile, per row block
   uint32_t pprev[2][8]; // packed P^T of this wave's tile of the previous step
+  u32x4 v[16];          // V^T of the next PV: own tile (0..7) then the partner's,
+                        // d-block 4e + ((k & 7) >> 1), key half k & 1
   float lsum[2];        // row sums over this wave's tiles (this lane's keys)
 };
 
@@ -411,8 +412,9 @@ struct PairGeo {
 // LDS objects: K ring slots 2s, 2s+1 in object s (halves), and the P exchange
 // area (two buffers x four waves x 4 KB)
 struct PairLds {
-  uint16_t* L[4];
+  uint16_t* ring;  // the four objects, 2 FT elements each
   uint16_t* PX;
+  __device__ __forceinline__ uint16_t* obj(int j) const { return ring + j * (2 * FT); }
 };
 
 template <bool CAUSAL>
@@ -453,17 +455,16 @@ __device__ __forceinline__ void k_addrs(const PairCtx& pc, const uint16_t* obj, 
 
 // QK of this wave's tile for both row blocks, as 8 pairs of K fragments (fragment
 // kk: chunk 2kk + h2 of row l%32, at ka[kk & 7] + 256 (kk >> 3)), read 4 ahead.
-// The caller issued reads 0..3 (nothing LDS older is outstanding). PV: the
-// partner's 4 P^T fragments are read after fragment 15. SM: softmax slice p
-// (words 2p, 2p+1 of row block p >> 2) rides along pair p.
+// The caller issued reads 0..3 last (anything LDS older may be outstanding: the
+// waits only need those to be done too). SM: softmax slice p (words 2p, 2p+1 of
+// row block p >> 2) rides along pair p.
 #define PRK(kk) (kf[kk] = ds_b128<256 * ((kk) >> 3)>(ka[(kk) & 7]))
-template <int P, bool PV, bool SM>
+template <int P, bool SM>
 __device__ __forceinline__ void qk_pair(PairState& st, const PairCtx& pc, const uint32_t (&ka)[8],
-                                        u32x4 (&kf)[16], u32x4 (&pf)[4], uint32_t prd,
-                                        const f32x16& s0, const f32x16& s1, uint32_t (&pw)[2][8]) {
-  // LDS ops issued after read 2P+1 at this point: reads 2P+2, 2P+3, plus (PV)
-  // the 4 P reads once issued (after read 15)
-  constexpr int W = P < 6 ? 2 : P == 6 ? (PV ? 6 : 2) : (PV ? 4 : 0);
+                                        u32x4 (&kf)[16], const f32x16& s0, const f32x16& s1,
+                                        uint32_t (&pw)[2][8]) {
+  // LDS ops issued after read 2P+1 at this point: reads 2P+2, 2P+3
+  constexpr int W = P < 7 ? 2 : 0;
   lgkm_take<W>(kf[2 * P], kf[2 * P + 1]);
   if constexpr (P == 0) {
     mfma_qk0(st.s[0], kf[0], st.qop[0][0]);
@@ -478,23 +479,17 @@ __device__ __forceinline__ void qk_pair(PairState& st, const PairCtx& pc, const 
     PRK(2 * P + 4);
     PRK(2 * P + 5);
   }
-  if constexpr (PV && P == 5) {
-    pf[0] = ds_b128<0>(prd);
-    pf[1] = ds_b128<1024>(prd);
-    pf[2] = ds_b128<2048>(prd);
-    pf[3] = ds_b128<3072>(prd);
-  }
   if constexpr (SM) {
     constexpr int RB = P >> 2, W0 = (2 * P) & 7;
     pw[RB][W0] = pair_p2(RB == 0 ? s0 : s1, 2 * W0, pc.negm[RB], st.lsum[RB]);
     pw[RB][W0 + 1] = pair_p2(RB == 0 ? s0 : s1, 2 * W0 + 2, pc.negm[RB], st.lsum[RB]);
   }
 }
-template <bool PV, bool SM>
+template <bool SM>
 __device__ __forceinline__ void qk_phase(PairState& st, const PairCtx& pc, const uint32_t (&ka)[8],
-                                         u32x4 (&kf)[16], u32x4 (&pf)[4], uint32_t prd,
-                                         const f32x16& s0, const f32x16& s1, uint32_t (&pw)[2][8]) {
-#define QP(p) qk_pair<p, PV, SM>(st, pc, ka, kf, pf, prd, s0, s1, pw)
+                                         u32x4 (&kf)[16], const f32x16& s0, const f32x16& s1,
+                                         uint32_t (&pw)[2][8]) {
+#define QP(p) qk_pair<p, SM>(st, pc, ka, kf, s0, s1, pw)
   QP(0); QP(1); QP(2); QP(3); QP(4); QP(5); QP(6); QP(7);
 #undef QP
   mfma_drain(st.s[0], st.s[1]);
@@ -509,138 +504,183 @@ __device__ __forceinline__ void p_publish(const PairCtx& pc, uint32_t pbuf, cons
   ds_w128<3072>(wa, make_uint4(pw[1][4], pw[1][5], pw[1][6], pw[1][7]));
 }
 
-// Kinds of pair step: FIRST (i = 0: softmax, QK, no PV), STEADY, NOQK (the last
-// full step i = n_it - 1: its QK would only serve tiles past the end), LAST
-// (i = n_it: PV only).
-enum { PS_FIRST = 0, PS_STEADY = 1, PS_NOQK = 2, PS_LAST = 3 };
-
-// Pair step i (J4 = i % 4), in this order: the V^T of this step's PV (tiles
-// 2i-2+e, then 2i-1-e) and the K loads of tiles 2i+6, 2i+7 (ring object
-// (J4+3) % 4) go out; QK of this wave's tile 2i+2+e (object (J4+1) % 4) with the
-// softmax of its tile 2i+e riding along; the P^T of that tile to the exchange;
-// PV of tiles 2i-2, 2i-1: own tile with the P^T kept from the last step, the
-// partner's from the exchange. GV: the gate loads of the epilogue go out with
-// the V^T (PV-only step).
-template <bool CAUSAL, int J4, int KIND>
-__device__ __forceinline__ void pair_step(PairState& st, const PairCtx& pc, const PairLds& L,
-                                          const PairGeo& g, int i, int e, int lane,
-                                          u32x2 (&gv)[2][4][4]) {
-  constexpr bool QK = KIND == PS_FIRST || KIND == PS_STEADY;  // QK of tile 2i+2+e
-  constexpr bool SM = KIND != PS_LAST;                       // softmax of tile 2i+e
-  constexpr bool PV = KIND != PS_FIRST;                      // PV of tiles 2i-2, 2i-1
-  constexpr bool DMA = QK;                                   // K loads of tiles 2i+6, 2i+7
-  constexpr bool GV = KIND == PS_LAST;
-  // the K tiles read here landed (they went out at step i-2 or before; only the
-  // last step's 8 tile loads may still be in flight) and every wave is past
-  // step i-1 (its P writes landed)
-  fwait_vmcnt<8>();
-  fbarrier();
+// V^T of one PV position k (own tile for k < 8, the partner's after) into slot k
+template <int K>
+__device__ __forceinline__ void v_load(PairState& st, const char* vbo, const char* vbp, uint32_t vo0,
+                                       uint32_t vo1) {
+  g_b128_into<(K & 3) * 1024>(st.v[K], K < 8 ? vbo : vbp, (K & 4) ? vo1 : vo0);
+}
+__device__ __forceinline__ void v_tiles(const PairCtx& pc, int t_own, int t_part, const char*& vbo,
+                                        const char*& vbp) {
   const int n = pc.c.n_tiles;
-  if (SM && pair_needs_mask<CAUSAL>(g, 2 * i + e)) pair_mask<CAUSAL>(g, 2 * i + e, lane, st.s);
-  // P exchange buffers: 16 KB each (four waves x 4 KB); step i writes buffer i & 1
-  // and reads buffer (i-1) & 1
-  constexpr uint32_t pbuf_r = ((J4 + 1) & 1) * 16384u;
-  constexpr uint32_t pbuf_w = (J4 & 1) * 16384u;
-  const uint32_t prd = pc.pxr + pbuf_r + (1 - e) * 4096;
+  vbo = pc.vt + (int64_t)min(t_own, n - 1) * (2 * FT);
+  vbp = pc.vt + (int64_t)min(t_part, n - 1) * (2 * FT);
+}
+
+// Step 0: softmax of this wave's tile e, the V^T of step 1 (tiles e, 1-e; order:
+// 4 V, the K loads of tiles 6, 7 into object 3, 12 V), QK of its tile 2+e (object
+// 1), the P^T of tile e to the exchange (buffer 0).
+template <bool CAUSAL>
+__device__ __forceinline__ void pair_first(PairState& st, const PairCtx& pc, const PairLds& L,
+                                           const PairGeo& g, int e, int lane) {
+  fwait_vmcnt<8>();  // K(2), K(3) (K(4), K(5) may be in flight)
+  fbarrier();
+  if (pair_needs_mask<CAUSAL>(g, e)) pair_mask<CAUSAL>(g, e, lane, st.s);
   uint32_t ka[8];
-  u32x4 kf[16], pf[4], vf[16];
-  if constexpr (QK) {
-    k_addrs(pc, L.L[(J4 + 1) % 4], ka);
-    PRK(0); PRK(1); PRK(2); PRK(3);
-  }
-  if constexpr (PV) {
-    const char* vbo = pc.vt + (int64_t)min(2 * i - 2 + e, n - 1) * (2 * FT);
-    const char* vbp = pc.vt + (int64_t)min(2 * i - 1 - e, n - 1) * (2 * FT);
-    const uint32_t vo0 = pc.voff, vo1 = pc.voff + 4096;
-    vf[0] = g_b128<0>(vbo, vo0);     vf[1] = g_b128<1024>(vbo, vo0);
-    vf[2] = g_b128<2048>(vbo, vo0);  vf[3] = g_b128<3072>(vbo, vo0);
-    vf[4] = g_b128<0>(vbo, vo1);     vf[5] = g_b128<1024>(vbo, vo1);
-    vf[6] = g_b128<2048>(vbo, vo1);  vf[7] = g_b128<3072>(vbo, vo1);
-    vf[8] = g_b128<0>(vbp, vo0);     vf[9] = g_b128<1024>(vbp, vo0);
-    vf[10] = g_b128<2048>(vbp, vo0); vf[11] = g_b128<3072>(vbp, vo0);
-    vf[12] = g_b128<0>(vbp, vo1);    vf[13] = g_b128<1024>(vbp, vo1);
-    vf[14] = g_b128<2048>(vbp, vo1); vf[15] = g_b128<3072>(vbp, vo1);
-  }
-  if constexpr (GV) {
-    // the epilogue's gate logits: 4 bf16 at d = 32 (4e + dq) + 8 jb + 4 h2 of this
-    // lane's row in each row block (32 loads)
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const uint16_t* gp = pc.gate_row[rb] + 32 * (4 * e) + 4 * (lane >> 5);
-      gv[rb][0][0] = g_b64<0>(gp);    gv[rb][0][1] = g_b64<16>(gp);
-      gv[rb][0][2] = g_b64<32>(gp);   gv[rb][0][3] = g_b64<48>(gp);
-      gv[rb][1][0] = g_b64<64>(gp);   gv[rb][1][1] = g_b64<80>(gp);
-      gv[rb][1][2] = g_b64<96>(gp);   gv[rb][1][3] = g_b64<112>(gp);
-      gv[rb][2][0] = g_b64<128>(gp);  gv[rb][2][1] = g_b64<144>(gp);
-      gv[rb][2][2] = g_b64<160>(gp);  gv[rb][2][3] = g_b64<176>(gp);
-      gv[rb][3][0] = g_b64<192>(gp);  gv[rb][3][1] = g_b64<208>(gp);
-      gv[rb][3][2] = g_b64<224>(gp);  gv[rb][3][3] = g_b64<240>(gp);
-    }
-  }
-  if constexpr (DMA) {
-    issue_quarter(pc.c, 2 * i + 6, L.L[(J4 + 3) % 4]);
-    issue_quarter(pc.c, 2 * i + 7, L.L[(J4 + 3) % 4] + FT);
-  }
+  u32x4 kf[16];
+  k_addrs(pc, L.obj(1), ka);
+  PRK(0); PRK(1); PRK(2); PRK(3);
+  const char *vbo, *vbp;
+  v_tiles(pc, e, 1 - e, vbo, vbp);
+  const uint32_t vo0 = pc.voff, vo1 = pc.voff + 4096;
+  v_load<0>(st, vbo, vbp, vo0, vo1); v_load<1>(st, vbo, vbp, vo0, vo1);
+  v_load<2>(st, vbo, vbp, vo0, vo1); v_load<3>(st, vbo, vbp, vo0, vo1);
+  issue_quarter(pc.c, 6, L.obj(3));
+  issue_quarter(pc.c, 7, L.obj(3) + FT);
+  v_load<4>(st, vbo, vbp, vo0, vo1);   v_load<5>(st, vbo, vbp, vo0, vo1);
+  v_load<6>(st, vbo, vbp, vo0, vo1);   v_load<7>(st, vbo, vbp, vo0, vo1);
+  v_load<8>(st, vbo, vbp, vo0, vo1);   v_load<9>(st, vbo, vbp, vo0, vo1);
+  v_load<10>(st, vbo, vbp, vo0, vo1);  v_load<11>(st, vbo, vbp, vo0, vo1);
+  v_load<12>(st, vbo, vbp, vo0, vo1);  v_load<13>(st, vbo, vbp, vo0, vo1);
+  v_load<14>(st, vbo, vbp, vo0, vo1);  v_load<15>(st, vbo, vbp, vo0, vo1);
+  f32x16 s0 = st.s[0], s1 = st.s[1];
+  pin(s0);
+  pin(s1);
   uint32_t pw[2][8];
-  f32x16 s0, s1;
-  if constexpr (SM) {
-    s0 = st.s[0];
-    s1 = st.s[1];
-    pin(s0);
-    pin(s1);
-  }
-  if constexpr (QK) {
-    qk_phase<PV, SM>(st, pc, ka, kf, pf, prd, s0, s1, pw);
+  qk_phase<true>(st, pc, ka, kf, s0, s1, pw);
+  p_publish(pc, 0u, pw);
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int q = 0; q < 8; ++q) st.pprev[rb][q] = pw[rb][q];
+  lgkm_wait<0>();  // the P writes land before the next barrier
+}
+
+// One PV position k of a step: slot k on both row blocks (own tile with the P^T
+// kept from the last step, the partner's with pf), then (LOAD) slot k's
+// successor for the next step, the K loads after slot 3.
+template <int K, bool LOAD>
+__device__ __forceinline__ void pv_pos(PairState& st, const PairCtx& pc, const u32x4 (&pf)[4],
+                                       const char* vbo, const char* vbp, uint32_t vo0, uint32_t vo1,
+                                       int i, uint16_t* dma_dst) {
+  constexpr int DQ = (K & 7) >> 1, KS = K & 1;
+  uint4 p0, p1;
+  if constexpr (K < 8) {
+    p0 = make_uint4(st.pprev[0][4 * KS], st.pprev[0][4 * KS + 1], st.pprev[0][4 * KS + 2], st.pprev[0][4 * KS + 3]);
+    p1 = make_uint4(st.pprev[1][4 * KS], st.pprev[1][4 * KS + 1], st.pprev[1][4 * KS + 2], st.pprev[1][4 * KS + 3]);
   } else {
-    if constexpr (PV) {
-      pf[0] = ds_b128<0>(prd);
-      pf[1] = ds_b128<1024>(prd);
-      pf[2] = ds_b128<2048>(prd);
-      pf[3] = ds_b128<3072>(prd);
-    }
-    if constexpr (SM) {
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int q = 0; q < 8; ++q) pw[rb][q] = pair_p2(rb == 0 ? s0 : s1, 2 * q, pc.negm[rb], st.lsum[rb]);
-    }
+    p0 = __builtin_bit_cast(uint4, pf[KS]);
+    p1 = __builtin_bit_cast(uint4, pf[2 + KS]);
   }
-  if constexpr (SM) p_publish(pc, pbuf_w, pw);
-  if constexpr (PV) {
-    // V^T slots 4g .. 4g+3 landed: loads issued after slot 4g+3 are the later V
-    // loads (12 - 4g) and this step's tile loads (8) or gate loads (32)
-    constexpr int VX = DMA ? 8 : (GV ? 32 : 0);
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int dq = (k & 7) >> 1, ks = k & 1;
-      if (k == 0) vm_take<12 + VX>(vf[0], vf[1], vf[2], vf[3]);
-      if (k == 4) vm_take<8 + VX>(vf[4], vf[5], vf[6], vf[7]);
-      if (k == 8) {
-        vm_take<4 + VX>(vf[8], vf[9], vf[10], vf[11]);
-        // the partner's P^T: only this step's P writes (if any) are younger
-        if constexpr (SM) lgkm_take<4>(pf[0], pf[1], pf[2], pf[3]);
-        else lgkm_take<0>(pf[0], pf[1], pf[2], pf[3]);
-      }
-      if (k == 12) vm_take<VX>(vf[12], vf[13], vf[14], vf[15]);
-      uint4 p0, p1;
-      if (k < 8) {
-        p0 = make_uint4(st.pprev[0][4 * ks], st.pprev[0][4 * ks + 1], st.pprev[0][4 * ks + 2], st.pprev[0][4 * ks + 3]);
-        p1 = make_uint4(st.pprev[1][4 * ks], st.pprev[1][4 * ks + 1], st.pprev[1][4 * ks + 2], st.pprev[1][4 * ks + 3]);
-      } else {
-        p0 = __builtin_bit_cast(uint4, pf[ks]);
-        p1 = __builtin_bit_cast(uint4, pf[2 + ks]);
-      }
-      st.o[dq][0] = mfma32(__builtin_bit_cast(uint4, vf[k]), p0, st.o[dq][0]);
-      st.o[dq][1] = mfma32(__builtin_bit_cast(uint4, vf[k]), p1, st.o[dq][1]);
+  st.o[DQ][0] = mfma32(__builtin_bit_cast(uint4, st.v[K]), p0, st.o[DQ][0]);
+  st.o[DQ][1] = mfma32(__builtin_bit_cast(uint4, st.v[K]), p1, st.o[DQ][1]);
+  if constexpr (LOAD) {
+    v_load<K>(st, vbo, vbp, vo0, vo1);
+    if constexpr (K == 3) {
+      issue_quarter(pc.c, 2 * i + 6, dma_dst);
+      issue_quarter(pc.c, 2 * i + 7, dma_dst + FT);
     }
   }
-  if constexpr (SM) {
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int q = 0; q < 8; ++q) st.pprev[rb][q] = pw[rb][q];
+}
+
+// Steps 1 .. n_it-1 (ring slots from i at run time): PV of tiles 2i-2, 2i-1 from
+// the V^T loaded last step (own tile first: its P^T is in registers; the
+// partner's P^T was read at the start), each slot reloaded for step i+1 (tiles
+// 2i, 2i+1; the K loads of tiles 2i+6, 2i+7 into object (i+3) % 4 after slot 3);
+// then QK of this wave's tile 2i+2+e (object (i+1) % 4) with the softmax of its
+// tile 2i+e riding along; its P^T to exchange buffer i & 1. (The last of these
+// steps computes a QK nobody reads.)
+template <bool CAUSAL>
+__device__ __forceinline__ void pair_steady(PairState& st, const PairCtx& pc, const PairLds& L,
+                                            const PairGeo& g, int i, int e, int lane) {
+  // K(2i+2), K(2i+3) (loaded at step i-2) landed: only step i-1's 8 tile + 16 V
+  // loads may still be in flight; every wave is past step i-1
+  fwait_vmcnt<24>();
+  fbarrier();
+  if (pair_needs_mask<CAUSAL>(g, 2 * i + e)) pair_mask<CAUSAL>(g, 2 * i + e, lane, st.s);
+  const uint32_t pbuf_r = ((i - 1) & 1) * 16384u, pbuf_w = (i & 1) * 16384u;
+  u32x4 pf[4], kf[16];
+  {
+    const uint32_t prd = pc.pxr + pbuf_r + (1 - e) * 4096;
+    pf[0] = ds_b128<0>(prd);
+    pf[1] = ds_b128<1024>(prd);
+    pf[2] = ds_b128<2048>(prd);
+    pf[3] = ds_b128<3072>(prd);
   }
-  lgkm_wait<0>();  // this step's LDS writes land before the next barrier
+  uint32_t ka[8];
+  k_addrs(pc, L.obj((i + 1) & 3), ka);
+  PRK(0); PRK(1); PRK(2); PRK(3);
+  const char *vbo, *vbp;
+  v_tiles(pc, 2 * i + e, 2 * i + 1 - e, vbo, vbp);
+  const uint32_t vo0 = pc.voff, vo1 = pc.voff + 4096;
+  uint16_t* dma_dst = L.obj((i + 3) & 3);
+  // slots 4g .. 4g+3 of step i-1 landed: loads issued after slot 4g+3 are its
+  // 12 - 4g later V loads and its 8 tile loads (after slot 3), plus this step's
+  // 4g V loads and (g > 0) 8 tile loads: 20 in every case
+#define PVP(k) pv_pos<k, true>(st, pc, pf, vbo, vbp, vo0, vo1, i, dma_dst)
+  vm_take<20>(st.v[0], st.v[1], st.v[2], st.v[3]);
+  PVP(0); PVP(1); PVP(2); PVP(3);
+  vm_take<20>(st.v[4], st.v[5], st.v[6], st.v[7]);
+  PVP(4); PVP(5); PVP(6); PVP(7);
+  vm_take<20>(st.v[8], st.v[9], st.v[10], st.v[11]);
+  lgkm_take<4>(pf[0], pf[1], pf[2], pf[3]);  // only K reads 0..3 are younger
+  PVP(8); PVP(9); PVP(10); PVP(11);
+  vm_take<20>(st.v[12], st.v[13], st.v[14], st.v[15]);
+  PVP(12); PVP(13); PVP(14); PVP(15);
+#undef PVP
+  f32x16 s0 = st.s[0], s1 = st.s[1];
+  pin(s0);
+  pin(s1);
+  uint32_t pw[2][8];
+  qk_phase<true>(st, pc, ka, kf, s0, s1, pw);
+  p_publish(pc, pbuf_w, pw);
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int q = 0; q < 8; ++q) st.pprev[rb][q] = pw[rb][q];
+  lgkm_wait<0>();  // the P writes land before the next barrier
+}
+
+// Step n_it: PV of the last two tiles only; the epilogue's gate logits go out
+// first (4 bf16 at d = 32 (4e + dq) + 8 jb + 4 h2 of this lane's row in each row
+// block: 32 loads).
+__device__ __forceinline__ void pair_last(PairState& st, const PairCtx& pc, int i, int e, int lane,
+                                          u32x2 (&gv)[2][4][4]) {
+  fbarrier();  // the partner's P^T of step i-1 is in
+  const uint32_t pbuf_r = ((i - 1) & 1) * 16384u;
+  u32x4 pf[4];
+  {
+    const uint32_t prd = pc.pxr + pbuf_r + (1 - e) * 4096;
+    pf[0] = ds_b128<0>(prd);
+    pf[1] = ds_b128<1024>(prd);
+    pf[2] = ds_b128<2048>(prd);
+    pf[3] = ds_b128<3072>(prd);
+  }
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const uint16_t* gp = pc.gate_row[rb] + 32 * (4 * e) + 4 * (lane >> 5);
+    gv[rb][0][0] = g_b64<0>(gp);    gv[rb][0][1] = g_b64<16>(gp);
+    gv[rb][0][2] = g_b64<32>(gp);   gv[rb][0][3] = g_b64<48>(gp);
+    gv[rb][1][0] = g_b64<64>(gp);   gv[rb][1][1] = g_b64<80>(gp);
+    gv[rb][1][2] = g_b64<96>(gp);   gv[rb][1][3] = g_b64<112>(gp);
+    gv[rb][2][0] = g_b64<128>(gp);  gv[rb][2][1] = g_b64<144>(gp);
+    gv[rb][2][2] = g_b64<160>(gp);  gv[rb][2][3] = g_b64<176>(gp);
+    gv[rb][3][0] = g_b64<192>(gp);  gv[rb][3][1] = g_b64<208>(gp);
+    gv[rb][3][2] = g_b64<224>(gp);  gv[rb][3][3] = g_b64<240>(gp);
+  }
+  // slots 4g .. 4g+3 of step i-1 landed: after slot 4g+3 came its 12 - 4g later
+  // V loads, (g = 0) its 8 tile loads, and the 32 gate loads
+#define PVP(k) pv_pos<k, false>(st, pc, pf, nullptr, nullptr, 0u, 0u, i, nullptr)
+  vm_take<52>(st.v[0], st.v[1], st.v[2], st.v[3]);
+  PVP(0); PVP(1); PVP(2); PVP(3);
+  vm_take<40>(st.v[4], st.v[5], st.v[6], st.v[7]);
+  PVP(4); PVP(5); PVP(6); PVP(7);
+  vm_take<36>(st.v[8], st.v[9], st.v[10], st.v[11]);
+  lgkm_take<0>(pf[0], pf[1], pf[2], pf[3]);
+  PVP(8); PVP(9); PVP(10); PVP(11);
+  vm_take<32>(st.v[12], st.v[13], st.v[14], st.v[15]);
+  PVP(12); PVP(13); PVP(14); PVP(15);
+#undef PVP
 }
 
 // Exact row max of S over the item's keys for this pair's rows (the QK-only pass
@@ -653,13 +693,13 @@ __device__ __forceinline__ void max_step(PairState& st, const PairCtx& pc, const
   fwait_vmcnt<16>();
   fbarrier();
   uint32_t ka[8];
-  u32x4 kf[16], pf[4];
+  u32x4 kf[16];
   uint32_t pw[2][8];
-  k_addrs(pc, L.L[J4], ka);
+  k_addrs(pc, L.obj(J4), ka);
   PRK(0); PRK(1); PRK(2); PRK(3);
-  issue_quarter(pc.c, 2 * i + 6, L.L[(J4 + 3) % 4]);
-  issue_quarter(pc.c, 2 * i + 7, L.L[(J4 + 3) % 4] + FT);
-  qk_phase<false, false>(st, pc, ka, kf, pf, 0u, st.s[0], st.s[1], pw);
+  issue_quarter(pc.c, 2 * i + 6, L.obj((J4 + 3) % 4));
+  issue_quarter(pc.c, 2 * i + 7, L.obj((J4 + 3) % 4) + FT);
+  qk_phase<false>(st, pc, ka, kf, st.s[0], st.s[1], pw);
   if (pair_needs_mask<CAUSAL>(g, 2 * i + e)) pair_mask<CAUSAL>(g, 2 * i + e, lane, st.s);
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
@@ -670,12 +710,12 @@ __device__ __forceinline__ void max_step(PairState& st, const PairCtx& pc, const
 template <bool CAUSAL>
 __device__ __forceinline__ void prime_ring(const PairCtx& pc, const PairLds& L) {
   // K(0) .. K(5) into objects 0..2 (object 3 and the exchange area are free)
-  issue_quarter(pc.c, 0, L.L[0]);
-  issue_quarter(pc.c, 1, L.L[0] + FT);
-  issue_quarter(pc.c, 2, L.L[1]);
-  issue_quarter(pc.c, 3, L.L[1] + FT);
-  issue_quarter(pc.c, 4, L.L[2]);
-  issue_quarter(pc.c, 5, L.L[2] + FT);
+  issue_quarter(pc.c, 0, L.obj(0));
+  issue_quarter(pc.c, 1, L.obj(0) + FT);
+  issue_quarter(pc.c, 2, L.obj(1));
+  issue_quarter(pc.c, 3, L.obj(1) + FT);
+  issue_quarter(pc.c, 4, L.obj(2));
+  issue_quarter(pc.c, 5, L.obj(2) + FT);
 }
 
 // One item (shift: the static softmax shift in log2 units, or < 0 for the
@@ -721,7 +761,7 @@ __device__ __forceinline__ void pair_item(const PrefillArgs& a, const FItem& it,
     uint4 qown[16];
     q_prologue(a, ql, qown);
     // exchange: wave w's 16 fragments (16 KB) in object 3 (waves 0, 1) or PX (2, 3)
-    const uint32_t xbase = wave < 2 ? lds_addr(L.L[3]) : lds_addr(L.PX);
+    const uint32_t xbase = wave < 2 ? lds_addr(L.obj(3)) : lds_addr(L.PX);
     const uint32_t xw = xbase + e * (2 * FT) + 16 * lane;
     const uint32_t xr = xbase + (1 - e) * (2 * FT) + 16 * lane;
     ds_w128<0>(xw, qown[0]);         ds_w128<1024>(xw, qown[1]);
@@ -814,41 +854,17 @@ __device__ __forceinline__ void pair_item(const PrefillArgs& a, const FItem& it,
   // S^T of tile e (object 0, half e)
   {
     uint32_t ka[8];
-    u32x4 kf[16], pf[4];
+    u32x4 kf[16];
     uint32_t pw[2][8];
-    k_addrs(pc, L.L[0], ka);
+    k_addrs(pc, L.obj(0), ka);
     PRK(0); PRK(1); PRK(2); PRK(3);
-    qk_phase<false, false>(st, pc, ka, kf, pf, 0u, st.s[0], st.s[1], pw);
+    qk_phase<false>(st, pc, ka, kf, st.s[0], st.s[1], pw);
   }
 
   u32x2 gv[2][4][4];
-  pair_step<CAUSAL, 0, PS_FIRST>(st, pc, L, g, 0, e, lane, gv);
-  // steps 1 .. n_it-2 steady, n_it-1 without QK, n_it PV only
-  int i = 1;
-  for (; i + 3 < n_it - 1; i += 4) {
-    pair_step<CAUSAL, 1, PS_STEADY>(st, pc, L, g, i, e, lane, gv);
-    pair_step<CAUSAL, 2, PS_STEADY>(st, pc, L, g, i + 1, e, lane, gv);
-    pair_step<CAUSAL, 3, PS_STEADY>(st, pc, L, g, i + 2, e, lane, gv);
-    pair_step<CAUSAL, 0, PS_STEADY>(st, pc, L, g, i + 3, e, lane, gv);
-  }
-  const int rem = n_it - 1 - i;  // steady steps left: -1 .. 3 (-1: n_it = 1)
-  if (rem >= 1) pair_step<CAUSAL, 1, PS_STEADY>(st, pc, L, g, i, e, lane, gv);
-  if (rem >= 2) pair_step<CAUSAL, 2, PS_STEADY>(st, pc, L, g, i + 1, e, lane, gv);
-  if (rem >= 3) pair_step<CAUSAL, 3, PS_STEADY>(st, pc, L, g, i + 2, e, lane, gv);
-  if (n_it >= 2) {
-    switch ((n_it - 1) & 3) {
-      case 0: pair_step<CAUSAL, 0, PS_NOQK>(st, pc, L, g, n_it - 1, e, lane, gv); break;
-      case 1: pair_step<CAUSAL, 1, PS_NOQK>(st, pc, L, g, n_it - 1, e, lane, gv); break;
-      case 2: pair_step<CAUSAL, 2, PS_NOQK>(st, pc, L, g, n_it - 1, e, lane, gv); break;
-      default: pair_step<CAUSAL, 3, PS_NOQK>(st, pc, L, g, n_it - 1, e, lane, gv); break;
-    }
-  }
-  switch (n_it & 3) {  // the PV-only step n_it
-    case 0: pair_step<CAUSAL, 0, PS_LAST>(st, pc, L, g, n_it, e, lane, gv); break;
-    case 1: pair_step<CAUSAL, 1, PS_LAST>(st, pc, L, g, n_it, e, lane, gv); break;
-    case 2: pair_step<CAUSAL, 2, PS_LAST>(st, pc, L, g, n_it, e, lane, gv); break;
-    default: pair_step<CAUSAL, 3, PS_LAST>(st, pc, L, g, n_it, e, lane, gv); break;
-  }
+  pair_first<CAUSAL>(st, pc, L, g, e, lane);
+  for (int i = 1; i < n_it; ++i) pair_steady<CAUSAL>(st, pc, L, g, i, e, lane);
+  pair_last(st, pc, n_it, e, lane, gv);
 
   // ---- epilogue: row sums of both waves of the pair through LDS, normalise,
   // gate (sigmoid, src/kernels/kernels.jl:34), store this wave's d-half in the Wo
@@ -900,8 +916,7 @@ __device__ __forceinline__ void pair_item(const PrefillArgs& a, const FItem& it,
 template <bool CAUSAL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_fused_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint16_t A0[2 * FT], A1[2 * FT], A2[2 * FT], A3[2 * FT],
-      PX[2 * FT];
+  __shared__ __attribute__((aligned(1024))) uint16_t RING[4 * 2 * FT], PX[2 * FT];
   const int lane = threadIdx.x & 63;
   // static bounds from the norm weights: |k~| <= sqrt(D) * max|kw + w_offset| for
   // every cached row, |q op| <= max|qw + w_offset| for every scaled query row
@@ -926,7 +941,7 @@ void prefill_fused_kernel(PrefillArgs a) {
   }
   const float bound = qmax * 1.01f * 16.0f * kmax * 1.01f * LOG2E;  // >= every |logit|, log2 units
   PairLds L;
-  L.L[0] = A0; L.L[1] = A1; L.L[2] = A2; L.L[3] = A3;
+  L.ring = RING;
   L.PX = PX;
   pair_item<CAUSAL>(a, item_at(a, blockIdx.x), L, bound <= FSTATIC_LIMIT ? bound : -1.0f);
   fwait_vmcnt<0>();  // no LDS load may land after the workgroup is gone
