@@ -291,7 +291,7 @@ __device__ __forceinline__ void init_fctx(FCtx& c, const PrefillArgs& a, const I
   c.kbase = a.k + (int64_t)ig.b * a.kv_sb + (int64_t)ig.hk * a.kv_sh;
   c.vtbase = a.vt + ((int64_t)ig.b * a.Hk + ig.hk) * a.vt_tiles * FT;
   c.kv_st = a.kv_st;
-  c.krow_max = max(0, min(ig.k_len, a.Lk) - 1);
+  c.krow_max = a.Lk - 1;  // rows up to here are readable (past k_len: masked)
   // tiles never reach past the cache (prior + q_len > Lk is a caller error: the
   // keys past Lk were never appended), so neither do the V^T workspace reads
   c.n_tiles = max(1, (min(ig.kend, a.Lk) + FN - 1) / FN);
@@ -345,7 +345,7 @@ __device__ __forceinline__ void q_prologue(const PrefillArgs& a, const QLoads& q
     for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
   }
   ss += __shfl_xor(ss, 32, 64);
-  const float scale = QK_SCALE / sqrtf(ss * (1.0f / HEAD_DIM) + a.eps);
+  const float scale = QK_SCALE * LOG2E / sqrtf(ss * (1.0f / HEAD_DIM) + a.eps);
   const float* cs = reinterpret_cast<const float*>(ql.cv);
   const float* sn = reinterpret_cast<const float*>(ql.sv);
 #pragma unroll
@@ -380,543 +380,386 @@ __device__ __forceinline__ void q_prologue(const PrefillArgs& a, const QLoads& q
   }
 }
 
-// ============================ pair path ============================
+// ============================ one wave per 32 rows ============================
 
-struct PairState {
-  uint4 qop[2][16];     // Q^T operands of the pair's two 32-row blocks (held in AGPRs)
-  f32x16 o[4][2];       // O^T of d-blocks 4e .. 4e+3 x the two row blocks (AGPRs)
-  f32x16 s[2];          // S^T of this wave's current tile, per row block
-  uint32_t pprev[2][8]; // packed P^T of this wave's tile of the previous step
-  u32x4 v[16];          // V^T of the next PV: own tile (0..7) then the partner's,
-                        // d-block 4e + ((k & 7) >> 1), key half k & 1
-  float lsum[2];        // row sums over this wave's tiles (this lane's keys)
+constexpr int NSLOT = 16;  // slots per step: 4 MFMAs, 4 LDS reads, 1 softmax word each
+
+// nothing is scheduled across this point (pins the VALU work between the MFMAs)
+__device__ __forceinline__ void sfence() { __builtin_amdgcn_sched_barrier(0); }
+
+struct SoloState {
+  uint4 qop[16];     // Q^T operands of this wave's 32 rows (AGPRs)
+  f32x16 o[8];       // O^T, d-blocks 0..7 (AGPRs)
+  f32x16 s[2][2];    // shifted S^T in log2 units, by step parity and tile
+  u32x4 p[2][4];     // packed P^T, by step parity and key step
+  f32x16 c0;         // minus this lane's row shift in every element (first QK accumulator)
+  float lsum;        // row sum of this lane's packed P^T
 };
 
-struct PairCtx {
+struct SoloCtx {
   FCtx c;             // K tile loads
   const char* vt;     // V^T tiles of (b, hk)
-  uint32_t voff;      // e * 8 KB + 16 lane: this lane's bytes of the wave's d-half
-  int koffe[8];       // K fragment byte offsets in a ring object (this wave's half)
-  uint32_t pxr;       // P exchange: this pair's region (tile-0 wave; tile-1 wave +4 KB)
-  uint32_t pxw;       // P exchange: this wave's region
-  float negm[2];      // minus the softmax shift of this lane's row in each row block
-  const uint16_t* gate_row[2];  // gate logits of this lane's row in each row block
+  uint32_t vsrc;      // this wave's first V^T piece of a tile, this lane's bytes: 4 KB wave + 16 lane
+  uint32_t kaddr[8];  // LDS address of K fragment q (and q + 8 at +256) in tile 0 of K object 0
+  uint32_t vaddr;     // LDS address of this lane's V^T bytes in tile 0 of V object 0
 };
 
-struct PairGeo {
-  int prow0;   // first row of the pair
-  int row[2];  // this lane's row in each row block
+struct SoloGeo {
+  int wrow0;  // first row of this wave
+  int row;    // this lane's row
   int off, k_len;
 };
 
-// LDS objects: K ring slots 2s, 2s+1 in object s (halves), and the P exchange
-// area (two buffers x four waves x 4 KB)
-struct PairLds {
-  uint16_t* ring;  // the four objects, 2 FT elements each
-  uint16_t* PX;
-  __device__ __forceinline__ uint16_t* obj(int j) const { return ring + j * (2 * FT); }
+// K objects (two tiles each, swizzled rows) and V^T objects (two tiles each,
+// fragment-major); object j holds step block j's tiles
+struct SoloLds {
+  uint16_t* k;
+  uint16_t* v;
 };
 
 template <bool CAUSAL>
-__device__ __forceinline__ bool pair_needs_mask(const PairGeo& g, int t) {
-  return (t * FN + FN > g.k_len) || (CAUSAL && t * FN + FN - 1 > g.off + g.prow0);
+__device__ __forceinline__ bool solo_needs_mask(const SoloGeo& g, int blk) {
+  const int last = blk * (2 * FN) + 2 * FN - 1;
+  return (last >= g.k_len) || (CAUSAL && last > g.off + g.wrow0);
 }
 template <bool CAUSAL>
-__device__ __forceinline__ void pair_mask(const PairGeo& g, int t, int lane, f32x16 (&s)[2]) {
-  const int key0 = t * FN + 4 * (lane >> 5);
+__device__ __forceinline__ void solo_mask(const SoloGeo& g, int blk, int lane, f32x16 (&s)[2]) {
+  const int lim = CAUSAL ? min(g.k_len - 1, g.row + g.off) : g.k_len - 1;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int lim = CAUSAL ? min(g.k_len - 1, g.row[rb] + g.off) : g.k_len - 1;
+  for (int t = 0; t < 2; ++t) {
+    const int key0 = blk * (2 * FN) + t * FN + 4 * (lane >> 5);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int key = key0 + 8 * (i >> 2) + (i & 3);
-      s[rb][i] = key <= lim ? s[rb][i] : -INFINITY;
+    for (int j = 0; j < 16; ++j) {
+      const int key = key0 + 8 * (j >> 2) + (j & 3);
+      s[t][j] = key <= lim ? s[t][j] : -INFINITY;
     }
   }
 }
 
-// softmax of elements j0, j0+1 of one row block with the shift: packed P^T word
-// (bf16 pair) and the row sum of what was packed
-__device__ __forceinline__ uint32_t pair_p2(const f32x16& s, int j0, float negm, float& lsum) {
-  const float p0 = fast_exp2(__builtin_fmaf(s[j0], LOG2E, negm));
-  const float p1 = fast_exp2(__builtin_fmaf(s[j0 + 1], LOG2E, negm));
-  uint32_t w = pack2(p0, p1);
-  pin(w);
-  lsum = dot2_ones(w, lsum);
-  pin(lsum);  // summed here, not deferred (which would keep every word live)
-  return w;
+// S^T = K fragment . Q^T + c: the first d-step, the accumulator starts at the shift
+__device__ __forceinline__ void mfma_qkc(f32x16& s, const u32x4& k, const uint4& q, const f32x16& c) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3"
+               : "=&v"(s) : "v"(k), "a"(__builtin_bit_cast(u32x4, q)), "v"(c));
+}
+// O^T += V^T fragment . P^T, O in AGPRs
+__device__ __forceinline__ void mfma_pv(f32x16& o, const u32x4& v, const u32x4& p) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(o) : "v"(v), "v"(p));
 }
 
-__device__ __forceinline__ void k_addrs(const PairCtx& pc, const uint16_t* obj, uint32_t (&ka)[8]) {
-  const uint32_t kb = lds_addr(obj);
-#pragma unroll
-  for (int q = 0; q < 8; ++q) ka[q] = kb + pc.koffe[q];
+// K tile t (clamped to the last tile) piece p of this wave (rows 2g, 2g+1 with
+// g = 4 wave + p) into the tile at dst; a tile reaching past the cache re-reads
+// its last row (those keys are masked)
+__device__ __forceinline__ void k_dma(const FCtx& c, int t, uint16_t* dst, int p) {
+  t = min(t, c.n_tiles - 1);
+  const int row0 = t * FN;
+  const char* src = reinterpret_cast<const char*>(c.kbase + (int64_t)row0 * c.kv_st);
+  const int g = 4 * c.wave + p;
+  uint32_t off = c.dma_boff[p];
+  if (row0 + FN - 1 > c.krow_max) {
+    const int r = 2 * g + (c.lane >> 5);
+    off -= (uint32_t)max(0, r - (c.krow_max - row0)) * c.row_bytes;
+  }
+  __builtin_amdgcn_global_load_lds((const void*)(src + off),
+                                   (__attribute__((address_space(3))) void*)(dst + g * 512), 16, 0, 0);
+}
+// V^T tile t (clamped) piece 4 wave + p (1 KB) into the tile at dst
+__device__ __forceinline__ void v_dma(const SoloCtx& sc, int t, uint16_t* dst, int p) {
+  t = min(t, sc.c.n_tiles - 1);
+  const char* src = sc.vt + (int64_t)t * (2 * FT) + sc.vsrc + p * 1024;
+  __builtin_amdgcn_global_load_lds((const void*)src,
+                                   (__attribute__((address_space(3))) void*)(dst + (4 * sc.c.wave + p) * 512),
+                                   16, 0, 0);
 }
 
-// QK of this wave's tile for both row blocks, as 8 pairs of K fragments (fragment
-// kk: chunk 2kk + h2 of row l%32, at ka[kk & 7] + 256 (kk >> 3)), read 4 ahead.
-// The caller issued reads 0..3 last (anything LDS older may be outstanding: the
-// waits only need those to be done too). SM: softmax slice p (words 2p, 2p+1 of
-// row block p >> 2) rides along pair p.
-#define PRK(kk) (kf[kk] = ds_b128<256 * ((kk) >> 3)>(ka[(kk) & 7]))
-template <int P, bool SM>
-__device__ __forceinline__ void qk_pair(PairState& st, const PairCtx& pc, const uint32_t (&ka)[8],
-                                        u32x4 (&kf)[16], const f32x16& s0, const f32x16& s1,
-                                        uint32_t (&pw)[2][8]) {
-  // LDS ops issued after read 2P+1 at this point: reads 2P+2, 2P+3
-  constexpr int W = P < 7 ? 2 : 0;
-  lgkm_take<W>(kf[2 * P], kf[2 * P + 1]);
-  if constexpr (P == 0) {
-    mfma_qk0(st.s[0], kf[0], st.qop[0][0]);
-    mfma_qk0(st.s[1], kf[0], st.qop[1][0]);
-  } else {
-    mfma_qk(st.s[0], kf[2 * P], st.qop[0][2 * P]);
-    mfma_qk(st.s[1], kf[2 * P], st.qop[1][2 * P]);
+// LDS reads of slot m: K fragments d-step m of both tiles (QK), V^T fragments
+// d-blocks 2(m & 3), 2(m & 3) + 1 of key step m >> 2 (PV)
+template <bool QK, bool PV, int J, int MM>
+__device__ __forceinline__ void slot_reads(const SoloCtx& sc, u32x4 (&kf)[3][2], u32x4 (&vf)[3][2]) {
+  constexpr int B = MM % 3;
+  if constexpr (QK) {
+    kf[B][0] = ds_b128<J * 32768 + 256 * (MM >> 3)>(sc.kaddr[MM & 7]);
+    kf[B][1] = ds_b128<J * 32768 + 16384 + 256 * (MM >> 3)>(sc.kaddr[MM & 7]);
   }
-  mfma_qk(st.s[0], kf[2 * P + 1], st.qop[0][2 * P + 1]);
-  mfma_qk(st.s[1], kf[2 * P + 1], st.qop[1][2 * P + 1]);
-  if constexpr (P < 6) {
-    PRK(2 * P + 4);
-    PRK(2 * P + 5);
+  if constexpr (PV) {
+    constexpr int KS = MM >> 2, D0 = 2 * (MM & 3);
+    constexpr int base = J * 32768 + (KS >> 1) * 16384 + (KS & 1) * 1024;
+    vf[B][0] = ds_b128<base + 2048 * D0>(sc.vaddr);
+    vf[B][1] = ds_b128<base + 2048 * (D0 + 1)>(sc.vaddr);
   }
+}
+
+// Slot m of step i: QK d-step m of both tiles of block i + 2 (MFMAs 1, 3),
+// PV d-blocks 2(m & 3), 2(m & 3) + 1 of key step m >> 2 of block i (MFMAs 2, 4),
+// softmax word m of block i + 1 (its two exponentials and the pack between the
+// MFMAs), the reads of slot m + 2, and (m < 8) two of this wave's 16 tile loads
+// of the step: K of block i + 3 (m < 4), V^T of block i + 1.
+template <bool QK, bool SM, bool PV, bool DV, int J, int M>
+__device__ __forceinline__ void solo_slot(SoloState& st, const SoloCtx& sc, const SoloLds& L, int i,
+                                          u32x4 (&kf)[3][2], u32x4 (&vf)[3][2]) {
+  constexpr int B = M % 3, KS = M >> 2, D0 = 2 * (M & 3);
+  constexpr int NR = (QK ? 2 : 0) + (PV ? 2 : 0);
+  constexpr int W = M < NSLOT - 1 ? NR : 0;  // after slot m's reads: slot m + 1's
+  if constexpr (QK && PV) lgkm_take<W>(kf[B][0], kf[B][1], vf[B][0], vf[B][1]);
+  else if constexpr (QK) lgkm_take<W>(kf[B][0], kf[B][1]);
+  else if constexpr (PV) lgkm_take<W>(vf[B][0], vf[B][1]);
+  sfence();
+  if constexpr (QK) {
+    if constexpr (M == 0) mfma_qkc(st.s[J][0], kf[B][0], st.qop[0], st.c0);
+    else mfma_qk(st.s[J][0], kf[B][0], st.qop[M]);
+  }
+  sfence();
+  float e0 = 0.f, e1 = 0.f;
   if constexpr (SM) {
-    constexpr int RB = P >> 2, W0 = (2 * P) & 7;
-    pw[RB][W0] = pair_p2(RB == 0 ? s0 : s1, 2 * W0, pc.negm[RB], st.lsum[RB]);
-    pw[RB][W0 + 1] = pair_p2(RB == 0 ? s0 : s1, 2 * W0 + 2, pc.negm[RB], st.lsum[RB]);
+    e0 = fast_exp2(st.s[1 - J][M >> 3][2 * (M & 7)]);
+    pin(e0);  // computed here (a pure value would otherwise sink to its use)
   }
-}
-template <bool SM>
-__device__ __forceinline__ void qk_phase(PairState& st, const PairCtx& pc, const uint32_t (&ka)[8],
-                                         u32x4 (&kf)[16], const f32x16& s0, const f32x16& s1,
-                                         uint32_t (&pw)[2][8]) {
-#define QP(p) qk_pair<p, SM>(st, pc, ka, kf, s0, s1, pw)
-  QP(0); QP(1); QP(2); QP(3); QP(4); QP(5); QP(6); QP(7);
-#undef QP
-  mfma_drain(st.s[0], st.s[1]);
+  sfence();
+  if constexpr (PV) mfma_pv(st.o[D0], vf[B][0], st.p[J][KS]);
+  sfence();
+  if constexpr (SM) {
+    e1 = fast_exp2(st.s[1 - J][M >> 3][2 * (M & 7) + 1]);
+    pin(e1);
+  }
+  sfence();
+  if constexpr (QK) {
+    if constexpr (M == 0) mfma_qkc(st.s[J][1], kf[B][1], st.qop[0], st.c0);
+    else mfma_qk(st.s[J][1], kf[B][1], st.qop[M]);
+  }
+  sfence();
+  if constexpr (SM) {
+    uint32_t w = pack2(e0, e1);
+    pin(w);
+    st.p[1 - J][M >> 2][M & 3] = w;
+    st.lsum = dot2_ones(w, st.lsum);
+    pin(st.lsum);
+  }
+  sfence();
+  if constexpr (PV) mfma_pv(st.o[D0 + 1], vf[B][1], st.p[J][KS]);
+  sfence();
+  if constexpr (M + 2 < NSLOT) slot_reads<QK, PV, J, M + 2>(sc, kf, vf);
+  if constexpr (M < 4) {
+    uint16_t* dst = L.k + (1 - J) * (2 * FT) + (M >> 1) * FT;
+    const int t = 2 * (i + 3) + (M >> 1);
+    k_dma(sc.c, t, dst, 2 * (M & 1));
+    k_dma(sc.c, t, dst, 2 * (M & 1) + 1);
+  } else if constexpr (M < 8 && DV) {
+    uint16_t* dst = L.v + (1 - J) * (2 * FT) + ((M - 4) >> 1) * FT;
+    const int t = 2 * (i + 1) + ((M - 4) >> 1);
+    v_dma(sc, t, dst, 2 * (M & 1));
+    v_dma(sc, t, dst, 2 * (M & 1) + 1);
+  }
+  sfence();
 }
 
-// this wave's P^T words of its tile to the exchange
-__device__ __forceinline__ void p_publish(const PairCtx& pc, uint32_t pbuf, const uint32_t (&pw)[2][8]) {
-  const uint32_t wa = pc.pxw + pbuf;
-  ds_w128<0>(wa, make_uint4(pw[0][0], pw[0][1], pw[0][2], pw[0][3]));
-  ds_w128<1024>(wa, make_uint4(pw[0][4], pw[0][5], pw[0][6], pw[0][7]));
-  ds_w128<2048>(wa, make_uint4(pw[1][0], pw[1][1], pw[1][2], pw[1][3]));
-  ds_w128<3072>(wa, make_uint4(pw[1][4], pw[1][5], pw[1][6], pw[1][7]));
-}
-
-// V^T of one PV position k (own tile for k < 8, the partner's after) into slot k
-template <int K>
-__device__ __forceinline__ void v_load(PairState& st, const char* vbo, const char* vbp, uint32_t vo0,
-                                       uint32_t vo1) {
-  g_b128_into<(K & 3) * 1024>(st.v[K], K < 8 ? vbo : vbp, (K & 4) ? vo1 : vo0);
-}
-__device__ __forceinline__ void v_tiles(const PairCtx& pc, int t_own, int t_part, const char*& vbo,
-                                        const char*& vbp) {
-  const int n = pc.c.n_tiles;
-  vbo = pc.vt + (int64_t)min(t_own, n - 1) * (2 * FT);
-  vbp = pc.vt + (int64_t)min(t_part, n - 1) * (2 * FT);
-}
-
-// Step 0: softmax of this wave's tile e, the V^T of step 1 (tiles e, 1-e; order:
-// 4 V, the K loads of tiles 6, 7 into object 3, 12 V), QK of its tile 2+e (object
-// 1), the P^T of tile e to the exchange (buffer 0).
-template <bool CAUSAL>
-__device__ __forceinline__ void pair_first(PairState& st, const PairCtx& pc, const PairLds& L,
-                                           const PairGeo& g, int e, int lane) {
-  fwait_vmcnt<8>();  // K(2), K(3) (K(4), K(5) may be in flight)
+// Step i (parity J = i & 1): QK of block i + 2 (K object J) into s[J], the softmax
+// of block i + 1 from s[1 - J] into p[1 - J], PV of block i from p[J] (V object J);
+// this wave's loads of K block i + 3 and V^T block i + 1 into the objects of
+// parity 1 - J (their last readers were in step i - 1). One barrier: every wave's
+// loads of step i - 1 are in, and every wave is done with step i - 1's reads.
+template <bool CAUSAL, int J, bool QK, bool SM, bool PV, bool DV>
+__device__ __forceinline__ void solo_step(SoloState& st, const SoloCtx& sc, const SoloLds& L,
+                                          const SoloGeo& g, int i, int lane) {
+  fwait_vmcnt<0>();
   fbarrier();
-  if (pair_needs_mask<CAUSAL>(g, e)) pair_mask<CAUSAL>(g, e, lane, st.s);
-  uint32_t ka[8];
-  u32x4 kf[16];
-  k_addrs(pc, L.obj(1), ka);
-  PRK(0); PRK(1); PRK(2); PRK(3);
-  const char *vbo, *vbp;
-  v_tiles(pc, e, 1 - e, vbo, vbp);
-  const uint32_t vo0 = pc.voff, vo1 = pc.voff + 4096;
-  v_load<0>(st, vbo, vbp, vo0, vo1); v_load<1>(st, vbo, vbp, vo0, vo1);
-  v_load<2>(st, vbo, vbp, vo0, vo1); v_load<3>(st, vbo, vbp, vo0, vo1);
-  issue_quarter(pc.c, 6, L.obj(3));
-  issue_quarter(pc.c, 7, L.obj(3) + FT);
-  v_load<4>(st, vbo, vbp, vo0, vo1);   v_load<5>(st, vbo, vbp, vo0, vo1);
-  v_load<6>(st, vbo, vbp, vo0, vo1);   v_load<7>(st, vbo, vbp, vo0, vo1);
-  v_load<8>(st, vbo, vbp, vo0, vo1);   v_load<9>(st, vbo, vbp, vo0, vo1);
-  v_load<10>(st, vbo, vbp, vo0, vo1);  v_load<11>(st, vbo, vbp, vo0, vo1);
-  v_load<12>(st, vbo, vbp, vo0, vo1);  v_load<13>(st, vbo, vbp, vo0, vo1);
-  v_load<14>(st, vbo, vbp, vo0, vo1);  v_load<15>(st, vbo, vbp, vo0, vo1);
-  f32x16 s0 = st.s[0], s1 = st.s[1];
-  pin(s0);
-  pin(s1);
-  uint32_t pw[2][8];
-  qk_phase<true>(st, pc, ka, kf, s0, s1, pw);
-  p_publish(pc, 0u, pw);
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int q = 0; q < 8; ++q) st.pprev[rb][q] = pw[rb][q];
-  lgkm_wait<0>();  // the P writes land before the next barrier
+  u32x4 kf[3][2], vf[3][2];
+  slot_reads<QK, PV, J, 0>(sc, kf, vf);
+  slot_reads<QK, PV, J, 1>(sc, kf, vf);
+  if constexpr (SM) {
+    if (solo_needs_mask<CAUSAL>(g, i + 1)) solo_mask<CAUSAL>(g, i + 1, lane, st.s[1 - J]);
+  }
+  sfence();
+#define SS(m) solo_slot<QK, SM, PV, DV, J, m>(st, sc, L, i, kf, vf)
+  SS(0); SS(1); SS(2); SS(3); SS(4); SS(5); SS(6); SS(7);
+  SS(8); SS(9); SS(10); SS(11); SS(12); SS(13); SS(14); SS(15);
+#undef SS
+  if constexpr (QK) mfma_drain(st.s[J][0], st.s[J][1]);
 }
 
-// One PV position k of a step: slot k on both row blocks (own tile with the P^T
-// kept from the last step, the partner's with pf), then (LOAD) slot k's
-// successor for the next step, the K loads after slot 3.
-template <int K, bool LOAD>
-__device__ __forceinline__ void pv_pos(PairState& st, const PairCtx& pc, const u32x4 (&pf)[4],
-                                       const char* vbo, const char* vbp, uint32_t vo0, uint32_t vo1,
-                                       int i, uint16_t* dma_dst) {
-  constexpr int DQ = (K & 7) >> 1, KS = K & 1;
-  uint4 p0, p1;
-  if constexpr (K < 8) {
-    p0 = make_uint4(st.pprev[0][4 * KS], st.pprev[0][4 * KS + 1], st.pprev[0][4 * KS + 2], st.pprev[0][4 * KS + 3]);
-    p1 = make_uint4(st.pprev[1][4 * KS], st.pprev[1][4 * KS + 1], st.pprev[1][4 * KS + 2], st.pprev[1][4 * KS + 3]);
-  } else {
-    p0 = __builtin_bit_cast(uint4, pf[KS]);
-    p1 = __builtin_bit_cast(uint4, pf[2 + KS]);
-  }
-  st.o[DQ][0] = mfma32(__builtin_bit_cast(uint4, st.v[K]), p0, st.o[DQ][0]);
-  st.o[DQ][1] = mfma32(__builtin_bit_cast(uint4, st.v[K]), p1, st.o[DQ][1]);
-  if constexpr (LOAD) {
-    v_load<K>(st, vbo, vbp, vo0, vo1);
-    if constexpr (K == 3) {
-      issue_quarter(pc.c, 2 * i + 6, dma_dst);
-      issue_quarter(pc.c, 2 * i + 7, dma_dst + FT);
+// Exact row max of the shifted-free S over the item's keys (QK only, K object
+// b & 1 for block b; block 0 primed by the caller). Returns the row max (log2
+// units) of this lane's row.
+template <bool CAUSAL>
+__device__ __forceinline__ float solo_max(const SoloState& st, const SoloCtx& sc, const SoloLds& L,
+                                       const SoloGeo& g, int nb, int lane) {
+  float m = -INFINITY;
+  for (int b = 0; b < nb; ++b) {
+    fwait_vmcnt<0>();
+    fbarrier();
+    uint16_t* nxt = L.k + ((b + 1) & 1) * (2 * FT);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      k_dma(sc.c, 2 * (b + 1), nxt, p);
+      k_dma(sc.c, 2 * (b + 1) + 1, nxt + FT, p);
     }
+    const uint32_t ob = (b & 1) * 32768;
+    f32x16 s[2];
+    u32x4 kf[3][2];
+    kf[0][0] = ds_b128<0>(sc.kaddr[0] + ob);
+    kf[0][1] = ds_b128<16384>(sc.kaddr[0] + ob);
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      if (kk < 15) {
+        kf[(kk + 1) % 3][0] = ds_b128<0>(sc.kaddr[(kk + 1) & 7] + ob + 256 * ((kk + 1) >> 3));
+        kf[(kk + 1) % 3][1] = ds_b128<16384>(sc.kaddr[(kk + 1) & 7] + ob + 256 * ((kk + 1) >> 3));
+        lgkm_take<2>(kf[kk % 3][0], kf[kk % 3][1]);
+      } else {
+        lgkm_take<0>(kf[kk % 3][0], kf[kk % 3][1]);
+      }
+      if (kk == 0) {
+        mfma_qk0(s[0], kf[0][0], st.qop[0]);
+        mfma_qk0(s[1], kf[0][1], st.qop[0]);
+      } else {
+        mfma_qk(s[0], kf[kk % 3][0], st.qop[kk]);
+        mfma_qk(s[1], kf[kk % 3][1], st.qop[kk]);
+      }
+    }
+    mfma_drain(s[0], s[1]);
+    if (solo_needs_mask<CAUSAL>(g, b)) solo_mask<CAUSAL>(g, b, lane, s);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) m = fmaxf(m, s[t][j]);
   }
+  return xor32_max(m);
 }
 
-// Steps 1 .. n_it-1 (ring slots from i at run time): PV of tiles 2i-2, 2i-1 from
-// the V^T loaded last step (own tile first: its P^T is in registers; the
-// partner's P^T was read at the start), each slot reloaded for step i+1 (tiles
-// 2i, 2i+1; the K loads of tiles 2i+6, 2i+7 into object (i+3) % 4 after slot 3);
-// then QK of this wave's tile 2i+2+e (object (i+1) % 4) with the softmax of its
-// tile 2i+e riding along; its P^T to exchange buffer i & 1. (The last of these
-// steps computes a QK nobody reads.)
-template <bool CAUSAL>
-__device__ __forceinline__ void pair_steady(PairState& st, const PairCtx& pc, const PairLds& L,
-                                            const PairGeo& g, int i, int e, int lane) {
-  // K(2i+2), K(2i+3) (loaded at step i-2) landed: only step i-1's 8 tile + 16 V
-  // loads may still be in flight; every wave is past step i-1
-  fwait_vmcnt<24>();
-  fbarrier();
-  if (pair_needs_mask<CAUSAL>(g, 2 * i + e)) pair_mask<CAUSAL>(g, 2 * i + e, lane, st.s);
-  const uint32_t pbuf_r = ((i - 1) & 1) * 16384u, pbuf_w = (i & 1) * 16384u;
-  u32x4 pf[4], kf[16];
-  {
-    const uint32_t prd = pc.pxr + pbuf_r + (1 - e) * 4096;
-    pf[0] = ds_b128<0>(prd);
-    pf[1] = ds_b128<1024>(prd);
-    pf[2] = ds_b128<2048>(prd);
-    pf[3] = ds_b128<3072>(prd);
-  }
-  uint32_t ka[8];
-  k_addrs(pc, L.obj((i + 1) & 3), ka);
-  PRK(0); PRK(1); PRK(2); PRK(3);
-  const char *vbo, *vbp;
-  v_tiles(pc, 2 * i + e, 2 * i + 1 - e, vbo, vbp);
-  const uint32_t vo0 = pc.voff, vo1 = pc.voff + 4096;
-  uint16_t* dma_dst = L.obj((i + 3) & 3);
-  // slots 4g .. 4g+3 of step i-1 landed: loads issued after slot 4g+3 are its
-  // 12 - 4g later V loads and its 8 tile loads (after slot 3), plus this step's
-  // 4g V loads and (g > 0) 8 tile loads: 20 in every case
-#define PVP(k) pv_pos<k, true>(st, pc, pf, vbo, vbp, vo0, vo1, i, dma_dst)
-  vm_take<20>(st.v[0], st.v[1], st.v[2], st.v[3]);
-  PVP(0); PVP(1); PVP(2); PVP(3);
-  vm_take<20>(st.v[4], st.v[5], st.v[6], st.v[7]);
-  PVP(4); PVP(5); PVP(6); PVP(7);
-  vm_take<20>(st.v[8], st.v[9], st.v[10], st.v[11]);
-  lgkm_take<4>(pf[0], pf[1], pf[2], pf[3]);  // only K reads 0..3 are younger
-  PVP(8); PVP(9); PVP(10); PVP(11);
-  vm_take<20>(st.v[12], st.v[13], st.v[14], st.v[15]);
-  PVP(12); PVP(13); PVP(14); PVP(15);
-#undef PVP
-  f32x16 s0 = st.s[0], s1 = st.s[1];
-  pin(s0);
-  pin(s1);
-  uint32_t pw[2][8];
-  qk_phase<true>(st, pc, ka, kf, s0, s1, pw);
-  p_publish(pc, pbuf_w, pw);
+// 8-byte loads into AGPRs (held across the item) and the wait that releases them
+template <int IMM>
+__device__ __forceinline__ void g_b64a(u32x2& r, const void* p) {
+  asm volatile("global_load_dwordx2 %0, %1, off offset:%2" : "=a"(r) : "v"(p), "i"(IMM));
+}
+__device__ __forceinline__ void gate_loads(const uint16_t* gp, u32x2 (&g)[8][4]) {
+#define GL(db, jb) g_b64a<64 * (db) + 16 * (jb)>(g[db][jb], gp)
+  GL(0, 0); GL(0, 1); GL(0, 2); GL(0, 3); GL(1, 0); GL(1, 1); GL(1, 2); GL(1, 3);
+  GL(2, 0); GL(2, 1); GL(2, 2); GL(2, 3); GL(3, 0); GL(3, 1); GL(3, 2); GL(3, 3);
+  GL(4, 0); GL(4, 1); GL(4, 2); GL(4, 3); GL(5, 0); GL(5, 1); GL(5, 2); GL(5, 3);
+  GL(6, 0); GL(6, 1); GL(6, 2); GL(6, 3); GL(7, 0); GL(7, 1); GL(7, 2); GL(7, 3);
+#undef GL
+}
+__device__ __forceinline__ void gate_take(u32x2 (&g)[8][4]) {
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int q = 0; q < 8; ++q) st.pprev[rb][q] = pw[rb][q];
-  lgkm_wait<0>();  // the P writes land before the next barrier
+  for (int db = 0; db < 8; db += 2)
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+a"(g[db][0]), "+a"(g[db][1]), "+a"(g[db][2]), "+a"(g[db][3]),
+                   "+a"(g[db + 1][0]), "+a"(g[db + 1][1]), "+a"(g[db + 1][2]), "+a"(g[db + 1][3]));
 }
 
-// Step n_it: PV of the last two tiles only; the epilogue's gate logits go out
-// first (4 bf16 at d = 32 (4e + dq) + 8 jb + 4 h2 of this lane's row in each row
-// block: 32 loads).
-__device__ __forceinline__ void pair_last(PairState& st, const PairCtx& pc, int i, int e, int lane,
-                                          u32x2 (&gv)[2][4][4]) {
-  fbarrier();  // the partner's P^T of step i-1 is in
-  const uint32_t pbuf_r = ((i - 1) & 1) * 16384u;
-  u32x4 pf[4];
-  {
-    const uint32_t prd = pc.pxr + pbuf_r + (1 - e) * 4096;
-    pf[0] = ds_b128<0>(prd);
-    pf[1] = ds_b128<1024>(prd);
-    pf[2] = ds_b128<2048>(prd);
-    pf[3] = ds_b128<3072>(prd);
+// K block 0 (tiles 0, 1) into K object 0
+__device__ __forceinline__ void solo_prime(const SoloCtx& sc, const SoloLds& L) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    k_dma(sc.c, 0, L.k, p);
+    k_dma(sc.c, 1, L.k + FT, p);
   }
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const uint16_t* gp = pc.gate_row[rb] + 32 * (4 * e) + 4 * (lane >> 5);
-    gv[rb][0][0] = g_b64<0>(gp);    gv[rb][0][1] = g_b64<16>(gp);
-    gv[rb][0][2] = g_b64<32>(gp);   gv[rb][0][3] = g_b64<48>(gp);
-    gv[rb][1][0] = g_b64<64>(gp);   gv[rb][1][1] = g_b64<80>(gp);
-    gv[rb][1][2] = g_b64<96>(gp);   gv[rb][1][3] = g_b64<112>(gp);
-    gv[rb][2][0] = g_b64<128>(gp);  gv[rb][2][1] = g_b64<144>(gp);
-    gv[rb][2][2] = g_b64<160>(gp);  gv[rb][2][3] = g_b64<176>(gp);
-    gv[rb][3][0] = g_b64<192>(gp);  gv[rb][3][1] = g_b64<208>(gp);
-    gv[rb][3][2] = g_b64<224>(gp);  gv[rb][3][3] = g_b64<240>(gp);
-  }
-  // slots 4g .. 4g+3 of step i-1 landed: after slot 4g+3 came its 12 - 4g later
-  // V loads, (g = 0) its 8 tile loads, and the 32 gate loads
-#define PVP(k) pv_pos<k, false>(st, pc, pf, nullptr, nullptr, 0u, 0u, i, nullptr)
-  vm_take<52>(st.v[0], st.v[1], st.v[2], st.v[3]);
-  PVP(0); PVP(1); PVP(2); PVP(3);
-  vm_take<40>(st.v[4], st.v[5], st.v[6], st.v[7]);
-  PVP(4); PVP(5); PVP(6); PVP(7);
-  vm_take<36>(st.v[8], st.v[9], st.v[10], st.v[11]);
-  lgkm_take<0>(pf[0], pf[1], pf[2], pf[3]);
-  PVP(8); PVP(9); PVP(10); PVP(11);
-  vm_take<32>(st.v[12], st.v[13], st.v[14], st.v[15]);
-  PVP(12); PVP(13); PVP(14); PVP(15);
-#undef PVP
-}
-
-// Exact row max of S over the item's keys for this pair's rows (the QK-only pass
-// for weights whose bound is too loose for a static shift). Step i reads K(2i),
-// K(2i+1) from ring object i % 4 and loads K(2i+6), K(2i+7) into object (i+3) % 4.
-template <bool CAUSAL, int J4>
-__device__ __forceinline__ void max_step(PairState& st, const PairCtx& pc, const PairLds& L,
-                                         const PairGeo& g, int i, int e, int lane, float (&m)[2]) {
-  // K(2i), K(2i+1) landed: the loads after them are two steps' tile loads
-  fwait_vmcnt<16>();
-  fbarrier();
-  uint32_t ka[8];
-  u32x4 kf[16];
-  uint32_t pw[2][8];
-  k_addrs(pc, L.obj(J4), ka);
-  PRK(0); PRK(1); PRK(2); PRK(3);
-  issue_quarter(pc.c, 2 * i + 6, L.obj((J4 + 3) % 4));
-  issue_quarter(pc.c, 2 * i + 7, L.obj((J4 + 3) % 4) + FT);
-  qk_phase<false>(st, pc, ka, kf, st.s[0], st.s[1], pw);
-  if (pair_needs_mask<CAUSAL>(g, 2 * i + e)) pair_mask<CAUSAL>(g, 2 * i + e, lane, st.s);
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) m[rb] = fmaxf(m[rb], st.s[rb][j]);
-}
-
-template <bool CAUSAL>
-__device__ __forceinline__ void prime_ring(const PairCtx& pc, const PairLds& L) {
-  // K(0) .. K(5) into objects 0..2 (object 3 and the exchange area are free)
-  issue_quarter(pc.c, 0, L.obj(0));
-  issue_quarter(pc.c, 1, L.obj(0) + FT);
-  issue_quarter(pc.c, 2, L.obj(1));
-  issue_quarter(pc.c, 3, L.obj(1) + FT);
-  issue_quarter(pc.c, 4, L.obj(2));
-  issue_quarter(pc.c, 5, L.obj(2) + FT);
 }
 
 // One item (shift: the static softmax shift in log2 units, or < 0 for the
 // exact-max pass).
 template <bool CAUSAL>
-__device__ __forceinline__ void pair_item(const PrefillArgs& a, const FItem& it, const PairLds& L,
+__device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it, const SoloLds& L,
                                           float shift) {
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int l32 = lane & 31, h2 = lane >> 5;
-  const int pr = wave >> 1, e = wave & 1;
   const ItemGeo ig = item_geo(a, it, CAUSAL);
-  const int prow0 = ig.r0 + 64 * pr;
-  const int row_own = prow0 + 32 * e + l32;  // this wave computes row block e's q
-  QLoads ql;
-  q_load_raw(a, ig.b, ig.h, row_own, h2, ql);
-  if (ig.r0 >= ig.q_len) return;  // uniform over the workgroup
-  PairGeo g;
-  g.prow0 = prow0;
-  g.row[0] = prow0 + l32;
-  g.row[1] = prow0 + 32 + l32;
+  SoloGeo g;
+  g.wrow0 = ig.r0 + 32 * wave;
+  g.row = g.wrow0 + l32;
   g.off = ig.off;
   g.k_len = ig.k_len;
-  PairCtx pc;
-  init_fctx(pc.c, a, ig, wave, lane);
-  pc.vt = reinterpret_cast<const char*>(pc.c.vtbase);
-  pc.voff = (uint32_t)(e * 8192 + 16 * lane);
+  QLoads ql;
+  q_load_raw(a, ig.b, ig.h, g.row, h2, ql);
+  if (ig.r0 >= ig.q_len) return;  // uniform over the workgroup
+  SoloCtx sc;
+  init_fctx(sc.c, a, ig, wave, lane);
+  sc.vt = reinterpret_cast<const char*>(sc.c.vtbase);
+  sc.vsrc = (uint32_t)(wave * 4096 + 16 * lane);
   {
     const int sk = fswz(l32);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) pc.koffe[q] = e * (2 * FT) + l32 * 512 + 16 * ((2 * q + h2) ^ sk);
+    for (int q = 0; q < 8; ++q) sc.kaddr[q] = lds_addr(L.k) + l32 * 512 + 16 * ((2 * q + h2) ^ sk);
   }
-  pc.pxr = lds_addr(L.PX) + (2 * pr) * 4096 + 16 * lane;
-  pc.pxw = lds_addr(L.PX) + wave * 4096 + 16 * lane;
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-    pc.gate_row[rb] = a.gate + (int64_t)ig.b * a.g_sb + (int64_t)ig.h * a.g_sh +
-                      (int64_t)min(g.row[rb], a.L - 1) * a.g_st;
-  q_load_rest(a, row_own, ig.prior, h2, ql);
-  prime_ring<CAUSAL>(pc, L);
-
-  PairState st;
+  sc.vaddr = lds_addr(L.v) + 16 * lane;
+  // gate logits of this lane's row: 4 at d = 32 dblk + 8 jb + 4 h2, loaded into
+  // AGPRs now (the first step's wait covers them), read in the epilogue
+  u32x2 gv[8][4];
   {
-    uint4 qown[16];
-    q_prologue(a, ql, qown);
-    // exchange: wave w's 16 fragments (16 KB) in object 3 (waves 0, 1) or PX (2, 3)
-    const uint32_t xbase = wave < 2 ? lds_addr(L.obj(3)) : lds_addr(L.PX);
-    const uint32_t xw = xbase + e * (2 * FT) + 16 * lane;
-    const uint32_t xr = xbase + (1 - e) * (2 * FT) + 16 * lane;
-    ds_w128<0>(xw, qown[0]);         ds_w128<1024>(xw, qown[1]);
-    ds_w128<2048>(xw, qown[2]);      ds_w128<3072>(xw, qown[3]);
-    ds_w128<4096>(xw, qown[4]);      ds_w128<5120>(xw, qown[5]);
-    ds_w128<6144>(xw, qown[6]);      ds_w128<7168>(xw, qown[7]);
-    ds_w128<8192>(xw, qown[8]);      ds_w128<9216>(xw, qown[9]);
-    ds_w128<10240>(xw, qown[10]);    ds_w128<11264>(xw, qown[11]);
-    ds_w128<12288>(xw, qown[12]);    ds_w128<13312>(xw, qown[13]);
-    ds_w128<14336>(xw, qown[14]);    ds_w128<15360>(xw, qown[15]);
-    // K(0), K(1) landed (K(2) .. K(5) may be in flight); the exchange written
-    fwait_vmcnt<16>();
-    lgkm_wait<0>();
-    fbarrier();
-    // the partner's fragments: reads and their wait in one statement (the
-    // outputs exist only once the data is in)
-    u32x4 qx[16];
-    asm volatile(
-        "ds_read_b128 %0, %16 offset:0\n\tds_read_b128 %1, %16 offset:1024\n\t"
-        "ds_read_b128 %2, %16 offset:2048\n\tds_read_b128 %3, %16 offset:3072\n\t"
-        "ds_read_b128 %4, %16 offset:4096\n\tds_read_b128 %5, %16 offset:5120\n\t"
-        "ds_read_b128 %6, %16 offset:6144\n\tds_read_b128 %7, %16 offset:7168\n\t"
-        "ds_read_b128 %8, %16 offset:8192\n\tds_read_b128 %9, %16 offset:9216\n\t"
-        "ds_read_b128 %10, %16 offset:10240\n\tds_read_b128 %11, %16 offset:11264\n\t"
-        "ds_read_b128 %12, %16 offset:12288\n\tds_read_b128 %13, %16 offset:13312\n\t"
-        "ds_read_b128 %14, %16 offset:14336\n\tds_read_b128 %15, %16 offset:15360\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(qx[0]), "=&v"(qx[1]), "=&v"(qx[2]), "=&v"(qx[3]), "=&v"(qx[4]), "=&v"(qx[5]),
-          "=&v"(qx[6]), "=&v"(qx[7]), "=&v"(qx[8]), "=&v"(qx[9]), "=&v"(qx[10]), "=&v"(qx[11]),
-          "=&v"(qx[12]), "=&v"(qx[13]), "=&v"(qx[14]), "=&v"(qx[15])
-        : "v"(xr));
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      const uint4 other = __builtin_bit_cast(uint4, qx[kk]);
-      st.qop[0][kk] = e == 0 ? qown[kk] : other;
-      st.qop[1][kk] = e == 0 ? other : qown[kk];
-    }
+    const uint16_t* gp = a.gate + (int64_t)ig.b * a.g_sb + (int64_t)ig.h * a.g_sh +
+                         (int64_t)min(g.row, a.L - 1) * a.g_st + 4 * h2;
+    gate_loads(gp, gv);
   }
+  q_load_rest(a, g.row, ig.prior, h2, ql);
+  solo_prime(sc, L);
+
+  SoloState st;
+  q_prologue(a, ql, st.qop);
   // rows past the chunk hold finite junk q; their outputs are never stored
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int kk = 0; kk < 16; ++kk) pin_acc(st.qop[kk]);
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) pin_acc(st.qop[rb][kk]);
+  for (int db = 0; db < 8; ++db)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) st.o[db][j] = 0.f;
+  st.lsum = 0.f;
 
-  const int n_it = (pc.c.n_tiles + 1) >> 1;
+  const int nb = (sc.c.n_tiles + 1) >> 1;  // step blocks of two tiles
+  float negm;
   if (shift >= 0.f) {
-    pc.negm[0] = -shift;
-    pc.negm[1] = -shift;
+    negm = -shift;
   } else {
-    // exact row max (QK only), combined over the pair through the exchange area
-    float m[2] = {-INFINITY, -INFINITY};
-    int i = 0;
-    for (; i + 3 < n_it; i += 4) {
-      max_step<CAUSAL, 0>(st, pc, L, g, i, e, lane, m);
-      max_step<CAUSAL, 1>(st, pc, L, g, i + 1, e, lane, m);
-      max_step<CAUSAL, 2>(st, pc, L, g, i + 2, e, lane, m);
-      max_step<CAUSAL, 3>(st, pc, L, g, i + 3, e, lane, m);
-    }
-    if (i < n_it) max_step<CAUSAL, 0>(st, pc, L, g, i, e, lane, m);
-    if (i + 1 < n_it) max_step<CAUSAL, 1>(st, pc, L, g, i + 1, e, lane, m);
-    if (i + 2 < n_it) max_step<CAUSAL, 2>(st, pc, L, g, i + 2, e, lane, m);
+    const float mr = solo_max<CAUSAL>(st, sc, L, g, nb, lane);
+    negm = mr == -INFINITY ? 0.f : -mr;  // fully-masked row: P = 0
     fwait_vmcnt<0>();
-    fbarrier();  // ring and exchange area free again
-    float* lx = reinterpret_cast<float*>(L.PX);
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      m[rb] = xor32_max(m[rb]);
-      if (h2 == 0) lx[wave * 64 + rb * 32 + l32] = m[rb];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const float mr = fmaxf(m[rb], lx[(wave ^ 1) * 64 + rb * 32 + l32]) * LOG2E;
-      pc.negm[rb] = mr == -INFINITY ? 0.f : -mr;  // fully-masked row: P = 0
-    }
-    __syncthreads();
-    prime_ring<CAUSAL>(pc, L);
-    fwait_vmcnt<16>();  // K(0), K(1)
-    fbarrier();
+    fbarrier();  // every wave is done with the K objects
+    solo_prime(sc, L);
   }
 #pragma unroll
-  for (int dq = 0; dq < 4; ++dq)
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) st.o[dq][rb][j] = 0.f;
-  st.lsum[0] = 0.f;
-  st.lsum[1] = 0.f;
+  for (int j = 0; j < 16; ++j) st.c0[j] = negm;
 
-  // S^T of tile e (object 0, half e)
-  {
-    uint32_t ka[8];
-    u32x4 kf[16];
-    uint32_t pw[2][8];
-    k_addrs(pc, L.obj(0), ka);
-    PRK(0); PRK(1); PRK(2); PRK(3);
-    qk_phase<false>(st, pc, ka, kf, st.s[0], st.s[1], pw);
+  solo_step<CAUSAL, 0, true, false, false, false>(st, sc, L, g, -2, lane);
+  solo_step<CAUSAL, 1, true, true, false, true>(st, sc, L, g, -1, lane);
+  int i = 0;
+  for (; i + 1 < nb; i += 2) {
+    solo_step<CAUSAL, 0, true, true, true, true>(st, sc, L, g, i, lane);
+    solo_step<CAUSAL, 1, true, true, true, true>(st, sc, L, g, i + 1, lane);
   }
+  if (i < nb) solo_step<CAUSAL, 0, true, true, true, true>(st, sc, L, g, i, lane);
 
-  u32x2 gv[2][4][4];
-  pair_first<CAUSAL>(st, pc, L, g, e, lane);
-  for (int i = 1; i < n_it; ++i) pair_steady<CAUSAL>(st, pc, L, g, i, e, lane);
-  pair_last(st, pc, n_it, e, lane, gv);
-
-  // ---- epilogue: row sums of both waves of the pair through LDS, normalise,
-  // gate (sigmoid, src/kernels/kernels.jl:34), store this wave's d-half in the Wo
-  // input layout
-  fbarrier();  // every wave is done with the P exchange area
-  float* lx = reinterpret_cast<float*>(L.PX);
-  float lrow[2];
+  // ---- epilogue: normalise, gate (sigmoid, src/kernels/kernels.jl:34), store in
+  // the Wo input layout
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
+               : "+a"(st.o[0]), "+a"(st.o[1]), "+a"(st.o[2]), "+a"(st.o[3]),
+                 "+a"(st.o[4]), "+a"(st.o[5]), "+a"(st.o[6]), "+a"(st.o[7]));
+  gate_take(gv);
+  const float l_tot = st.lsum + __shfl_xor(st.lsum, 32, 64);
+  const float inv = l_tot > 0.f ? fast_rcp(l_tot) : 0.f;  // fully-masked row -> 0
+  if (g.row < ig.q_len) {
+    uint16_t* op = a.o + (int64_t)ig.b * a.o_sb + (int64_t)ig.h * a.o_sh + (int64_t)g.row * a.o_st;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    lrow[rb] = st.lsum[rb] + __shfl_xor(st.lsum[rb], 32, 64);
-    if (h2 == 0) lx[wave * 64 + rb * 32 + l32] = lrow[rb];
-  }
-  __syncthreads();
-  vm_take8<0>(gv[0], 0);
-  vm_take8<0>(gv[0], 2);
-  vm_take8<0>(gv[1], 0);
-  vm_take8<0>(gv[1], 2);
+    for (int db = 0; db < 8; ++db) {
+      const f32x16& acc = st.o[db];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const float l_tot = lrow[rb] + lx[(wave ^ 1) * 64 + rb * 32 + l32];
-    const float inv = l_tot > 0.f ? fast_rcp(l_tot) : 0.f;  // fully-masked row -> 0
-    const int row = g.row[rb];
-    if (row < ig.q_len) {
-      uint16_t* op = a.o + (int64_t)ig.b * a.o_sb + (int64_t)ig.h * a.o_sh + (int64_t)row * a.o_st;
-#pragma unroll
-      for (int dq = 0; dq < 4; ++dq) {
-        const f32x16& acc = st.o[dq][rb];
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-          const int d0 = 32 * (4 * e + dq) + 8 * jb + 4 * h2;
-          const uint2 g2 = make_uint2(gv[rb][dq][jb].x, gv[rb][dq][jb].y);
-          const float o0 = acc[4 * jb + 0] * inv * sigmoidf(__uint_as_float(g2.x << 16));
-          const float o1 = acc[4 * jb + 1] * inv * sigmoidf(__uint_as_float(g2.x & 0xffff0000u));
-          const float o2 = acc[4 * jb + 2] * inv * sigmoidf(__uint_as_float(g2.y << 16));
-          const float o3 = acc[4 * jb + 3] * inv * sigmoidf(__uint_as_float(g2.y & 0xffff0000u));
-          uint2 ov;
-          ov.x = pack2(o0, o1);
-          ov.y = pack2(o2, o3);
-          *reinterpret_cast<uint2*>(op + d0) = ov;
-        }
+      for (int jb = 0; jb < 4; ++jb) {
+        const int d0 = 32 * db + 8 * jb + 4 * h2;
+        const u32x2 g2 = gv[db][jb];
+        const float o0 = acc[4 * jb + 0] * inv * sigmoidf(__uint_as_float(g2.x << 16));
+        const float o1 = acc[4 * jb + 1] * inv * sigmoidf(__uint_as_float(g2.x & 0xffff0000u));
+        const float o2 = acc[4 * jb + 2] * inv * sigmoidf(__uint_as_float(g2.y << 16));
+        const float o3 = acc[4 * jb + 3] * inv * sigmoidf(__uint_as_float(g2.y & 0xffff0000u));
+        uint2 ov;
+        ov.x = pack2(o0, o1);
+        ov.y = pack2(o2, o3);
+        *reinterpret_cast<uint2*>(op + d0) = ov;
       }
     }
   }
 }
-#undef PRK
 
 }  // namespace
 
 template <bool CAUSAL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_fused_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint16_t RING[4 * 2 * FT], PX[2 * FT];
+  __shared__ __attribute__((aligned(1024))) uint16_t KO[2 * 2 * FT], VO[2 * 2 * FT];
   const int lane = threadIdx.x & 63;
   // static bounds from the norm weights: |k~| <= sqrt(D) * max|kw + w_offset| for
   // every cached row, |q op| <= max|qw + w_offset| for every scaled query row
@@ -940,10 +783,10 @@ void prefill_fused_kernel(PrefillArgs a) {
     }
   }
   const float bound = qmax * 1.01f * 16.0f * kmax * 1.01f * LOG2E;  // >= every |logit|, log2 units
-  PairLds L;
-  L.ring = RING;
-  L.PX = PX;
-  pair_item<CAUSAL>(a, item_at(a, blockIdx.x), L, bound <= FSTATIC_LIMIT ? bound : -1.0f);
+  SoloLds L;
+  L.k = KO;
+  L.v = VO;
+  solo_item<CAUSAL>(a, item_at(a, blockIdx.x), L, bound <= FSTATIC_LIMIT ? bound : -1.0f);
   fwait_vmcnt<0>();  // no LDS load may land after the workgroup is gone
 }
 
