@@ -129,32 +129,13 @@ struct FCtx {
   int krow_max;   // last cache row that may be read
   int n_tiles;
   uint32_t row_bytes;   // cache row stride in bytes
-  uint32_t dma_boff[4]; // per-lane byte offsets of this wave's 4 one-KB pieces of a tile
+  // per-lane byte offsets of this wave's 4 one-KB pieces of a tile, less 1 KB per
+  // piece (the load's immediate offset adds it back, and moves the LDS side too)
+  uint32_t dma_boff[4];
+  uint32_t dma_clamp[4];  // the same for the tile that reaches past the cache
+  int t_part;             // that tile, or -1
   int wave, lane;
 };
-
-// This wave's quarter of K tile t (clamped to the last tile) into `dst`: piece
-// i = rows 2g, 2g+1 (g = 4 wave + i) as 64 lanes x 16 B. A whole tile is a
-// scalar base plus per-lane unsigned byte offsets (the scalar-base addressing
-// form); the last tile re-reads the last readable row past it (its keys are
-// masked).
-__device__ __forceinline__ void issue_quarter(const FCtx& c, int t, uint16_t* dst) {
-  t = min(t, c.n_tiles - 1);
-  const int row0 = t * FN;
-  const char* src = reinterpret_cast<const char*>(c.kbase + (int64_t)row0 * c.kv_st);
-  // rows past the last readable one re-read it (they are masked); one code path,
-  // so every step issues the same count of loads
-  const int last = c.krow_max - row0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int g = 4 * c.wave + i;
-    const int r = 2 * g + (c.lane >> 5);
-    const uint32_t over = (uint32_t)max(0, r - last);
-    __builtin_amdgcn_global_load_lds((const void*)(src + (c.dma_boff[i] - over * c.row_bytes)),
-                                     (__attribute__((address_space(3))) void*)(dst + g * 512),
-                                     16, 0, 0);
-  }
-}
 
 template <int N>
 __device__ __forceinline__ void fwait_vmcnt() {
@@ -298,10 +279,15 @@ __device__ __forceinline__ void init_fctx(FCtx& c, const PrefillArgs& a, const I
   c.wave = wave;
   c.lane = lane;
   c.row_bytes = (uint32_t)(2 * a.kv_st);
+  const int tl = c.n_tiles - 1;
+  c.t_part = tl * FN + FN - 1 > c.krow_max ? tl : -1;
+  const int last = c.krow_max - tl * FN;  // last readable row of that tile
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 2 * (4 * wave + i) + (lane >> 5);
-    c.dma_boff[i] = (uint32_t)r * c.row_bytes + (uint32_t)(((lane & 31) ^ fswz(r)) * 16);
+    const uint32_t chunk = (uint32_t)(((lane & 31) ^ fswz(r)) * 16);
+    c.dma_boff[i] = (uint32_t)r * c.row_bytes + chunk - 1024u * i;
+    c.dma_clamp[i] = (uint32_t)min(r, max(last, 0)) * c.row_bytes + chunk - 1024u * i;
   }
 }
 
@@ -390,9 +376,9 @@ __device__ __forceinline__ void sfence() { __builtin_amdgcn_sched_barrier(0); }
 struct SoloState {
   uint4 qop[16];     // Q^T operands of this wave's 32 rows (AGPRs)
   f32x16 o[8];       // O^T, d-blocks 0..7 (AGPRs)
-  f32x16 s[2][2];    // shifted S^T in log2 units, by step parity and tile
+  f32x16 s[2][2];    // S^T in log2 units, by step parity and tile
   u32x4 p[2][4];     // packed P^T, by step parity and key step
-  f32x16 c0;         // minus this lane's row shift in every element (first QK accumulator)
+  float negm;        // minus this lane's row shift (log2 units)
   float lsum;        // row sum of this lane's packed P^T
 };
 
@@ -410,8 +396,8 @@ struct SoloGeo {
   int off, k_len;
 };
 
-// K objects (two tiles each, swizzled rows) and V^T objects (two tiles each,
-// fragment-major); object j holds step block j's tiles
+// K objects (three, two tiles each, swizzled rows; block j in object j % 3) and
+// V^T objects (two, two tiles each, fragment-major; block j in object j % 2)
 struct SoloLds {
   uint16_t* k;
   uint16_t* v;
@@ -436,139 +422,258 @@ __device__ __forceinline__ void solo_mask(const SoloGeo& g, int blk, int lane, f
   }
 }
 
-// S^T = K fragment . Q^T + c: the first d-step, the accumulator starts at the shift
-__device__ __forceinline__ void mfma_qkc(f32x16& s, const u32x4& k, const uint4& q, const f32x16& c) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3"
-               : "=&v"(s) : "v"(k), "a"(__builtin_bit_cast(u32x4, q)), "v"(c));
-}
 // O^T += V^T fragment . P^T, O in AGPRs
 __device__ __forceinline__ void mfma_pv(f32x16& o, const u32x4& v, const u32x4& p) {
   asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(o) : "v"(v), "v"(p));
 }
 
-// K tile t (clamped to the last tile) piece p of this wave (rows 2g, 2g+1 with
-// g = 4 wave + p) into the tile at dst; a tile reaching past the cache re-reads
-// its last row (those keys are masked)
-__device__ __forceinline__ void k_dma(const FCtx& c, int t, uint16_t* dst, int p) {
+// Global->LDS tile loads. A tile is 16 one-KB pieces; wave w loads pieces 4w ..
+// 4w+3 (K: rows 2g, 2g+1 of piece g, re-laid to the swizzled LDS rows through
+// the per-lane source offsets; V^T: fragments g). Tile indices are clamped to the
+// last tile of the item; a K tile reaching past the cache re-reads its last row
+// there (those keys are masked).
+struct TileSrc {
+  const char* p;  // the tile's first byte
+  bool part;      // K: the tile reaching past the cache
+};
+__device__ __forceinline__ TileSrc k_tile(const FCtx& c, int t) {
   t = min(t, c.n_tiles - 1);
-  const int row0 = t * FN;
-  const char* src = reinterpret_cast<const char*>(c.kbase + (int64_t)row0 * c.kv_st);
-  const int g = 4 * c.wave + p;
-  uint32_t off = c.dma_boff[p];
-  if (row0 + FN - 1 > c.krow_max) {
-    const int r = 2 * g + (c.lane >> 5);
-    off -= (uint32_t)max(0, r - (c.krow_max - row0)) * c.row_bytes;
-  }
-  __builtin_amdgcn_global_load_lds((const void*)(src + off),
-                                   (__attribute__((address_space(3))) void*)(dst + g * 512), 16, 0, 0);
+  TileSrc r;
+  r.p = reinterpret_cast<const char*>(c.kbase + (int64_t)(t * FN) * c.kv_st);
+  r.part = t == c.t_part;
+  return r;
 }
-// V^T tile t (clamped) piece 4 wave + p (1 KB) into the tile at dst
-__device__ __forceinline__ void v_dma(const SoloCtx& sc, int t, uint16_t* dst, int p) {
-  t = min(t, sc.c.n_tiles - 1);
-  const char* src = sc.vt + (int64_t)t * (2 * FT) + sc.vsrc + p * 1024;
-  __builtin_amdgcn_global_load_lds((const void*)src,
-                                   (__attribute__((address_space(3))) void*)(dst + (4 * sc.c.wave + p) * 512),
-                                   16, 0, 0);
+// Tile sources of a stream advanced two tiles per step: tiles t, t + 1 clamped to
+// the item's last tile (and, for K, the partial-tile flag)
+struct TileStream {
+  const char* p;     // tile t (unclamped)
+  const char* last;  // the last tile
+  int64_t stride;    // bytes per tile
+  int t, tl, tpart;
+  __device__ __forceinline__ TileSrc at(int k) const {
+    TileSrc r;
+    r.p = t + k <= tl ? p + k * stride : last;
+    r.part = min(t + k, tl) == tpart;
+    return r;
+  }
+  __device__ __forceinline__ void advance() {
+    p += 2 * stride;
+    t += 2;
+  }
+};
+__device__ __forceinline__ TileStream k_stream(const FCtx& c, int t0) {
+  TileStream s;
+  s.stride = (int64_t)FN * c.kv_st * 2;
+  s.tl = c.n_tiles - 1;
+  s.t = t0;
+  s.tpart = c.t_part;
+  s.p = reinterpret_cast<const char*>(c.kbase) + t0 * s.stride;
+  s.last = reinterpret_cast<const char*>(c.kbase) + s.tl * s.stride;
+  return s;
+}
+template <int P>
+__device__ __forceinline__ void k_piece(const FCtx& c, const TileSrc& src, uint16_t* dst) {
+  const uint32_t off = src.part ? c.dma_clamp[P] : c.dma_boff[P];
+  __builtin_amdgcn_global_load_lds((const void*)(src.p + off),
+                                   (__attribute__((address_space(3))) void*)(dst + 4 * c.wave * 512),
+                                   16, 1024 * P, 0);
+}
+template <int P>
+__device__ __forceinline__ void v_piece(const SoloCtx& sc, const char* src, uint16_t* dst) {
+  __builtin_amdgcn_global_load_lds((const void*)(src + sc.vsrc),
+                                   (__attribute__((address_space(3))) void*)(dst + 4 * sc.c.wave * 512),
+                                   16, 1024 * P, 0);
+}
+__device__ __forceinline__ void k_tile_load(const FCtx& c, int t, uint16_t* dst) {
+  const TileSrc src = k_tile(c, t);
+  k_piece<0>(c, src, dst);
+  k_piece<1>(c, src, dst);
+  k_piece<2>(c, src, dst);
+  k_piece<3>(c, src, dst);
 }
 
-// LDS reads of slot m: K fragments d-step m of both tiles (QK), V^T fragments
-// d-blocks 2(m & 3), 2(m & 3) + 1 of key step m >> 2 (PV)
-template <bool QK, bool PV, int J, int MM>
-__device__ __forceinline__ void slot_reads(const SoloCtx& sc, u32x4 (&kf)[3][2], u32x4 (&vf)[3][2]) {
+__device__ __forceinline__ TileStream v_stream(const SoloCtx& sc, int t0) {
+  TileStream s;
+  s.stride = 2 * FT;
+  s.tl = sc.c.n_tiles - 1;
+  s.t = t0;
+  s.tpart = -1;
+  s.p = sc.vt + t0 * s.stride;
+  s.last = sc.vt + s.tl * s.stride;
+  return s;
+}
+
+// Slot operands: QK reads K fragments d-step m of tiles 0, 1 (kb: the step's K
+// object); PV reads V^T fragments d-blocks 2(m & 3), 2(m & 3) + 1 of key step
+// m >> 2. Operand r of slot m lives in ops[m % 3][r] (QK's first).
+template <bool QK, bool PV>
+constexpr int slot_nops() { return (QK ? 2 : 0) + (PV ? 2 : 0); }
+template <bool QK, bool PV, int J, int MM, int R>
+__device__ __forceinline__ void slot_read(const SoloCtx& sc, const uint32_t (&kb)[8], u32x4 (&ops)[3][4]) {
   constexpr int B = MM % 3;
+  if constexpr (QK && R < 2) {
+    ops[B][R] = ds_b128<16384 * R + 256 * (MM >> 3)>(kb[MM & 7]);
+  } else {
+    constexpr int U = QK ? R - 2 : R;
+    constexpr int KS = MM >> 2, DB = 2 * (MM & 3) + U;
+    ops[B][R] = ds_b128<J * 32768 + (KS >> 1) * 16384 + (KS & 1) * 1024 + 2048 * DB>(sc.vaddr);
+  }
+}
+// LDS ops issued after operand r of slot m when the slot's r-th MFMA issues: the
+// rest of slot m's reads, slot m + 1's, and the r reads of slot m + 2 issued so far
+template <int N, int M, int R>
+constexpr int slot_wait() {
+  return (N - 1 - R) + (M + 1 < NSLOT ? N : 0) + (M + 2 < NSLOT ? R : 0);
+}
+
+// the products with the wait for their LDS operand in front (one statement: no
+// reader of the operand can be placed between the two)
+template <int W>
+__device__ __forceinline__ void qk_w0(f32x16& s, const u32x4& k, const uint4& q) {
+  asm volatile("s_waitcnt lgkmcnt(%3)\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0"
+               : "=&v"(s) : "v"(k), "a"(__builtin_bit_cast(u32x4, q)), "n"(W));
+}
+template <int W>
+__device__ __forceinline__ void qk_w(f32x16& s, const u32x4& k, const uint4& q) {
+  asm volatile("s_waitcnt lgkmcnt(%3)\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+               : "+v"(s) : "v"(k), "a"(__builtin_bit_cast(u32x4, q)), "n"(W));
+}
+template <int W>
+__device__ __forceinline__ void pv_w0(f32x16& o, const u32x4& v, const u32x4& p) {
+  asm volatile("s_waitcnt lgkmcnt(%3)\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0"
+               : "=&a"(o) : "v"(v), "v"(p), "n"(W));
+}
+template <int W>
+__device__ __forceinline__ void pv_w(f32x16& o, const u32x4& v, const u32x4& p) {
+  asm volatile("s_waitcnt lgkmcnt(%3)\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+               : "+a"(o) : "v"(v), "v"(p), "n"(W));
+}
+
+// Slot m of step i: QK d-step m of both tiles of block i + 2, PV d-blocks
+// 2(m & 3), 2(m & 3) + 1 of key step m >> 2 of block i, softmax word m of block
+// i + 1, one LDS read of slot m + 2 after each product, and one of this wave's 16
+// tile loads of the step: V^T of block i + 1 (m < 8, needed next step), K of
+// block i + 4 (needed two steps on; kd: its object; ks, vs: the tiles' sources).
+// The VALU work sits between the products (fences keep it there).
+template <bool SHIFT, bool QK, bool SM, bool PV, bool DV, bool FIRST, int J, int M>
+__device__ __forceinline__ void solo_slot(SoloState& st, const SoloCtx& sc, const SoloLds& L,
+                                          const uint32_t (&kb)[8], uint16_t* kd, const TileSrc (&ks)[2],
+                                          const TileSrc (&vs)[2], u32x4 (&ops)[3][4]) {
+  constexpr int B = M % 3, KS = M >> 2, D0 = 2 * (M & 3);
+  constexpr int N = slot_nops<QK, PV>();
+  constexpr bool RD = M + 2 < NSLOT;
+  float e0 = 0.f, e1 = 0.f;
+  uint32_t w = 0;
+  // product r, then read r of slot m + 2, then the VALU piece placed after it
+#define SLOT_READ(r) \
+  if constexpr (RD) slot_read<QK, PV, J, M + 2, r>(sc, kb, ops)
   if constexpr (QK) {
-    kf[B][0] = ds_b128<J * 32768 + 256 * (MM >> 3)>(sc.kaddr[MM & 7]);
-    kf[B][1] = ds_b128<J * 32768 + 16384 + 256 * (MM >> 3)>(sc.kaddr[MM & 7]);
+    if constexpr (M == 0) qk_w0<slot_wait<N, M, 0>()>(st.s[J][0], ops[B][0], st.qop[0]);
+    else qk_w<slot_wait<N, M, 0>()>(st.s[J][0], ops[B][0], st.qop[M]);
+    SLOT_READ(0);
+    sfence();
+    if constexpr (SM) {
+      e0 = fast_exp2(SHIFT ? st.s[1 - J][M >> 3][2 * (M & 7)] + st.negm : st.s[1 - J][M >> 3][2 * (M & 7)]);
+      pin(e0);  // computed here (a pure value would otherwise sink to its use)
+    }
+    sfence();
+    if constexpr (M == 0) qk_w0<slot_wait<N, M, 1>()>(st.s[J][1], ops[B][1], st.qop[0]);
+    else qk_w<slot_wait<N, M, 1>()>(st.s[J][1], ops[B][1], st.qop[M]);
+    SLOT_READ(1);
+    sfence();
+    if constexpr (SM) {
+      e1 = fast_exp2(SHIFT ? st.s[1 - J][M >> 3][2 * (M & 7) + 1] + st.negm
+                           : st.s[1 - J][M >> 3][2 * (M & 7) + 1]);
+      pin(e1);
+      if constexpr (!PV) {
+        w = pack2(e0, e1);
+        pin(w);
+        st.p[1 - J][M >> 2][M & 3] = w;
+        st.lsum = dot2_ones(w, st.lsum);
+        pin(st.lsum);
+      }
+    }
+    sfence();
   }
   if constexpr (PV) {
-    constexpr int KS = MM >> 2, D0 = 2 * (MM & 3);
-    constexpr int base = J * 32768 + (KS >> 1) * 16384 + (KS & 1) * 1024;
-    vf[B][0] = ds_b128<base + 2048 * D0>(sc.vaddr);
-    vf[B][1] = ds_b128<base + 2048 * (D0 + 1)>(sc.vaddr);
+    constexpr int R0 = QK ? 2 : 0;
+    if constexpr (FIRST && KS == 0) pv_w0<slot_wait<N, M, R0>()>(st.o[D0], ops[B][R0], st.p[J][KS]);
+    else pv_w<slot_wait<N, M, R0>()>(st.o[D0], ops[B][R0], st.p[J][KS]);
+    SLOT_READ(R0);
+    sfence();
+    if constexpr (SM) {
+      w = pack2(e0, e1);
+      pin(w);
+      st.p[1 - J][M >> 2][M & 3] = w;
+    }
+    sfence();
+    if constexpr (FIRST && KS == 0) pv_w0<slot_wait<N, M, R0 + 1>()>(st.o[D0 + 1], ops[B][R0 + 1], st.p[J][KS]);
+    else pv_w<slot_wait<N, M, R0 + 1>()>(st.o[D0 + 1], ops[B][R0 + 1], st.p[J][KS]);
+    SLOT_READ(R0 + 1);
+    sfence();
+    if constexpr (SM) {
+      st.lsum = dot2_ones(w, st.lsum);
+      pin(st.lsum);
+    }
   }
-}
-
-// Slot m of step i: QK d-step m of both tiles of block i + 2 (MFMAs 1, 3),
-// PV d-blocks 2(m & 3), 2(m & 3) + 1 of key step m >> 2 of block i (MFMAs 2, 4),
-// softmax word m of block i + 1 (its two exponentials and the pack between the
-// MFMAs), the reads of slot m + 2, and (m < 8) two of this wave's 16 tile loads
-// of the step: K of block i + 3 (m < 4), V^T of block i + 1.
-template <bool QK, bool SM, bool PV, bool DV, int J, int M>
-__device__ __forceinline__ void solo_slot(SoloState& st, const SoloCtx& sc, const SoloLds& L, int i,
-                                          u32x4 (&kf)[3][2], u32x4 (&vf)[3][2]) {
-  constexpr int B = M % 3, KS = M >> 2, D0 = 2 * (M & 3);
-  constexpr int NR = (QK ? 2 : 0) + (PV ? 2 : 0);
-  constexpr int W = M < NSLOT - 1 ? NR : 0;  // after slot m's reads: slot m + 1's
-  if constexpr (QK && PV) lgkm_take<W>(kf[B][0], kf[B][1], vf[B][0], vf[B][1]);
-  else if constexpr (QK) lgkm_take<W>(kf[B][0], kf[B][1]);
-  else if constexpr (PV) lgkm_take<W>(vf[B][0], vf[B][1]);
-  sfence();
-  if constexpr (QK) {
-    if constexpr (M == 0) mfma_qkc(st.s[J][0], kf[B][0], st.qop[0], st.c0);
-    else mfma_qk(st.s[J][0], kf[B][0], st.qop[M]);
-  }
-  sfence();
-  float e0 = 0.f, e1 = 0.f;
-  if constexpr (SM) {
-    e0 = fast_exp2(st.s[1 - J][M >> 3][2 * (M & 7)]);
-    pin(e0);  // computed here (a pure value would otherwise sink to its use)
-  }
-  sfence();
-  if constexpr (PV) mfma_pv(st.o[D0], vf[B][0], st.p[J][KS]);
-  sfence();
-  if constexpr (SM) {
-    e1 = fast_exp2(st.s[1 - J][M >> 3][2 * (M & 7) + 1]);
-    pin(e1);
-  }
-  sfence();
-  if constexpr (QK) {
-    if constexpr (M == 0) mfma_qkc(st.s[J][1], kf[B][1], st.qop[0], st.c0);
-    else mfma_qk(st.s[J][1], kf[B][1], st.qop[M]);
-  }
-  sfence();
-  if constexpr (SM) {
-    uint32_t w = pack2(e0, e1);
-    pin(w);
-    st.p[1 - J][M >> 2][M & 3] = w;
-    st.lsum = dot2_ones(w, st.lsum);
-    pin(st.lsum);
-  }
-  sfence();
-  if constexpr (PV) mfma_pv(st.o[D0 + 1], vf[B][1], st.p[J][KS]);
-  sfence();
-  if constexpr (M + 2 < NSLOT) slot_reads<QK, PV, J, M + 2>(sc, kf, vf);
-  if constexpr (M < 4) {
-    uint16_t* dst = L.k + (1 - J) * (2 * FT) + (M >> 1) * FT;
-    const int t = 2 * (i + 3) + (M >> 1);
-    k_dma(sc.c, t, dst, 2 * (M & 1));
-    k_dma(sc.c, t, dst, 2 * (M & 1) + 1);
-  } else if constexpr (M < 8 && DV) {
-    uint16_t* dst = L.v + (1 - J) * (2 * FT) + ((M - 4) >> 1) * FT;
-    const int t = 2 * (i + 1) + ((M - 4) >> 1);
-    v_dma(sc, t, dst, 2 * (M & 1));
-    v_dma(sc, t, dst, 2 * (M & 1) + 1);
+#undef SLOT_READ
+  if constexpr (M < 8) {
+    if constexpr (DV) v_piece<M & 3>(sc, vs[M >> 2].p, L.v + (1 - J) * (2 * FT) + (M >> 2) * FT);
+  } else {
+    k_piece<M & 3>(sc.c, ks[(M - 8) >> 2], kd + ((M - 8) >> 2) * FT);
   }
   sfence();
 }
 
-// Step i (parity J = i & 1): QK of block i + 2 (K object J) into s[J], the softmax
-// of block i + 1 from s[1 - J] into p[1 - J], PV of block i from p[J] (V object J);
-// this wave's loads of K block i + 3 and V^T block i + 1 into the objects of
-// parity 1 - J (their last readers were in step i - 1). One barrier: every wave's
-// loads of step i - 1 are in, and every wave is done with step i - 1's reads.
-template <bool CAUSAL, int J, bool QK, bool SM, bool PV, bool DV>
+// Step i (parity J = i & 1): QK of block i + 2 (K object (i + 2) % 3) into s[J],
+// the softmax of block i + 1 from s[1 - J] into p[1 - J], PV of block i from p[J]
+// (V object J); this wave's loads of V^T block i + 1 (V object 1 - J) and then K
+// block i + 4 (K object (i + 1) % 3), whose last readers were in step i - 1. One
+// barrier: every wave's loads of V^T block i and K block i + 2 (issued one and two
+// steps back; only the last step's K loads may still be in flight) are in, and
+// every wave is done with step i - 1's reads.
+template <bool CAUSAL, bool SHIFT, int J, bool QK, bool SM, bool PV, bool DV, bool FIRST = false>
 __device__ __forceinline__ void solo_step(SoloState& st, const SoloCtx& sc, const SoloLds& L,
-                                          const SoloGeo& g, int i, int lane) {
-  fwait_vmcnt<0>();
+                                          const SoloGeo& g, int i, int lane, TileStream& kst,
+                                          TileStream& vst) {
+  fwait_vmcnt<8>();
   fbarrier();
-  u32x4 kf[3][2], vf[3][2];
-  slot_reads<QK, PV, J, 0>(sc, kf, vf);
-  slot_reads<QK, PV, J, 1>(sc, kf, vf);
+  uint32_t kb[8];
+  {
+    const uint32_t ko = (uint32_t)((i + 2) % 3) * 32768u;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) kb[q] = sc.kaddr[q] + ko;
+  }
+  uint16_t* kd = L.k + ((i + 4) % 3) * (2 * FT);
+  // kst: tiles 2(i + 4), 2(i + 4) + 1; vst: 2(i + 1), 2(i + 1) + 1
+  const TileSrc ks[2] = {kst.at(0), kst.at(1)};
+  const TileSrc vs[2] = {vst.at(0), vst.at(1)};
+  kst.advance();
+  if constexpr (DV) vst.advance();
+  u32x4 ops[3][4];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    if (m == 0) {
+      slot_read<QK, PV, J, 0, 0>(sc, kb, ops);
+      slot_read<QK, PV, J, 0, 1>(sc, kb, ops);
+      if constexpr (QK && PV) {
+        slot_read<QK, PV, J, 0, 2>(sc, kb, ops);
+        slot_read<QK, PV, J, 0, 3>(sc, kb, ops);
+      }
+    } else {
+      slot_read<QK, PV, J, 1, 0>(sc, kb, ops);
+      slot_read<QK, PV, J, 1, 1>(sc, kb, ops);
+      if constexpr (QK && PV) {
+        slot_read<QK, PV, J, 1, 2>(sc, kb, ops);
+        slot_read<QK, PV, J, 1, 3>(sc, kb, ops);
+      }
+    }
+  }
   if constexpr (SM) {
     if (solo_needs_mask<CAUSAL>(g, i + 1)) solo_mask<CAUSAL>(g, i + 1, lane, st.s[1 - J]);
   }
   sfence();
-#define SS(m) solo_slot<QK, SM, PV, DV, J, m>(st, sc, L, i, kf, vf)
+#define SS(m) solo_slot<SHIFT, QK, SM, PV, DV, FIRST, J, m>(st, sc, L, kb, kd, ks, vs, ops)
   SS(0); SS(1); SS(2); SS(3); SS(4); SS(5); SS(6); SS(7);
   SS(8); SS(9); SS(10); SS(11); SS(12); SS(13); SS(14); SS(15);
 #undef SS
@@ -586,11 +691,8 @@ __device__ __forceinline__ float solo_max(const SoloState& st, const SoloCtx& sc
     fwait_vmcnt<0>();
     fbarrier();
     uint16_t* nxt = L.k + ((b + 1) & 1) * (2 * FT);
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      k_dma(sc.c, 2 * (b + 1), nxt, p);
-      k_dma(sc.c, 2 * (b + 1) + 1, nxt + FT, p);
-    }
+    k_tile_load(sc.c, 2 * (b + 1), nxt);
+    k_tile_load(sc.c, 2 * (b + 1) + 1, nxt + FT);
     const uint32_t ob = (b & 1) * 32768;
     f32x16 s[2];
     u32x4 kf[3][2];
@@ -623,41 +725,17 @@ __device__ __forceinline__ float solo_max(const SoloState& st, const SoloCtx& sc
   return xor32_max(m);
 }
 
-// 8-byte loads into AGPRs (held across the item) and the wait that releases them
-template <int IMM>
-__device__ __forceinline__ void g_b64a(u32x2& r, const void* p) {
-  asm volatile("global_load_dwordx2 %0, %1, off offset:%2" : "=a"(r) : "v"(p), "i"(IMM));
-}
-__device__ __forceinline__ void gate_loads(const uint16_t* gp, u32x2 (&g)[8][4]) {
-#define GL(db, jb) g_b64a<64 * (db) + 16 * (jb)>(g[db][jb], gp)
-  GL(0, 0); GL(0, 1); GL(0, 2); GL(0, 3); GL(1, 0); GL(1, 1); GL(1, 2); GL(1, 3);
-  GL(2, 0); GL(2, 1); GL(2, 2); GL(2, 3); GL(3, 0); GL(3, 1); GL(3, 2); GL(3, 3);
-  GL(4, 0); GL(4, 1); GL(4, 2); GL(4, 3); GL(5, 0); GL(5, 1); GL(5, 2); GL(5, 3);
-  GL(6, 0); GL(6, 1); GL(6, 2); GL(6, 3); GL(7, 0); GL(7, 1); GL(7, 2); GL(7, 3);
-#undef GL
-}
-__device__ __forceinline__ void gate_take(u32x2 (&g)[8][4]) {
-#pragma unroll
-  for (int db = 0; db < 8; db += 2)
-    asm volatile("s_waitcnt vmcnt(0)"
-                 : "+a"(g[db][0]), "+a"(g[db][1]), "+a"(g[db][2]), "+a"(g[db][3]),
-                   "+a"(g[db + 1][0]), "+a"(g[db + 1][1]), "+a"(g[db + 1][2]), "+a"(g[db + 1][3]));
-}
-
-// K block 0 (tiles 0, 1) into K object 0
+// K blocks 0 and 1 (tiles 0 .. 3) into K objects 0 and 1
 __device__ __forceinline__ void solo_prime(const SoloCtx& sc, const SoloLds& L) {
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    k_dma(sc.c, 0, L.k, p);
-    k_dma(sc.c, 1, L.k + FT, p);
-  }
+  for (int t = 0; t < 4; ++t) k_tile_load(sc.c, t, L.k + t * FT);
 }
 
-// One item (shift: the static softmax shift in log2 units, or < 0 for the
-// exact-max pass).
-template <bool CAUSAL>
-__device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it, const SoloLds& L,
-                                          float shift) {
+// One item. SHIFT = false: every logit is within +-64 (log2 units), so
+// P = exp2(S) needs no shift (the normalisation cancels any common scale);
+// SHIFT = true: an exact row-max pass first, P = exp2(S - row max).
+template <bool CAUSAL, bool SHIFT>
+__device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it, const SoloLds& L) {
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int l32 = lane & 31, h2 = lane >> 5;
   const ItemGeo ig = item_geo(a, it, CAUSAL);
@@ -679,14 +757,6 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
     for (int q = 0; q < 8; ++q) sc.kaddr[q] = lds_addr(L.k) + l32 * 512 + 16 * ((2 * q + h2) ^ sk);
   }
   sc.vaddr = lds_addr(L.v) + 16 * lane;
-  // gate logits of this lane's row: 4 at d = 32 dblk + 8 jb + 4 h2, loaded into
-  // AGPRs now (the first step's wait covers them), read in the epilogue
-  u32x2 gv[8][4];
-  {
-    const uint16_t* gp = a.gate + (int64_t)ig.b * a.g_sb + (int64_t)ig.h * a.g_sh +
-                         (int64_t)min(g.row, a.L - 1) * a.g_st + 4 * h2;
-    gate_loads(gp, gv);
-  }
   q_load_rest(a, g.row, ig.prior, h2, ql);
   solo_prime(sc, L);
 
@@ -695,41 +765,46 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
   // rows past the chunk hold finite junk q; their outputs are never stored
 #pragma unroll
   for (int kk = 0; kk < 16; ++kk) pin_acc(st.qop[kk]);
-#pragma unroll
-  for (int db = 0; db < 8; ++db)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) st.o[db][j] = 0.f;
   st.lsum = 0.f;
 
   const int nb = (sc.c.n_tiles + 1) >> 1;  // step blocks of two tiles
-  float negm;
-  if (shift >= 0.f) {
-    negm = -shift;
-  } else {
+  float negm = 0.f;
+  if constexpr (SHIFT) {
     const float mr = solo_max<CAUSAL>(st, sc, L, g, nb, lane);
     negm = mr == -INFINITY ? 0.f : -mr;  // fully-masked row: P = 0
     fwait_vmcnt<0>();
     fbarrier();  // every wave is done with the K objects
     solo_prime(sc, L);
   }
-#pragma unroll
-  for (int j = 0; j < 16; ++j) st.c0[j] = negm;
+  st.negm = negm;
 
-  solo_step<CAUSAL, 0, true, false, false, false>(st, sc, L, g, -2, lane);
-  solo_step<CAUSAL, 1, true, true, false, true>(st, sc, L, g, -1, lane);
-  int i = 0;
+  TileStream kst = k_stream(sc.c, 4), vst = v_stream(sc, 0);
+  solo_step<CAUSAL, SHIFT, 0, true, false, false, false>(st, sc, L, g, -2, lane, kst, vst);
+  solo_step<CAUSAL, SHIFT, 1, true, true, false, true>(st, sc, L, g, -1, lane, kst, vst);
+  // step 0 starts O (its first products take a zero accumulator)
+  solo_step<CAUSAL, SHIFT, 0, true, true, true, true, true>(st, sc, L, g, 0, lane, kst, vst);
+  int i = 1;
   for (; i + 1 < nb; i += 2) {
-    solo_step<CAUSAL, 0, true, true, true, true>(st, sc, L, g, i, lane);
-    solo_step<CAUSAL, 1, true, true, true, true>(st, sc, L, g, i + 1, lane);
+    solo_step<CAUSAL, SHIFT, 1, true, true, true, true>(st, sc, L, g, i, lane, kst, vst);
+    solo_step<CAUSAL, SHIFT, 0, true, true, true, true>(st, sc, L, g, i + 1, lane, kst, vst);
   }
-  if (i < nb) solo_step<CAUSAL, 0, true, true, true, true>(st, sc, L, g, i, lane);
+  if (i < nb) solo_step<CAUSAL, SHIFT, 1, true, true, true, true>(st, sc, L, g, i, lane, kst, vst);
 
   // ---- epilogue: normalise, gate (sigmoid, src/kernels/kernels.jl:34), store in
   // the Wo input layout
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
                : "+a"(st.o[0]), "+a"(st.o[1]), "+a"(st.o[2]), "+a"(st.o[3]),
                  "+a"(st.o[4]), "+a"(st.o[5]), "+a"(st.o[6]), "+a"(st.o[7]));
-  gate_take(gv);
+  // gate logits of this lane's row: 4 at d = 32 dblk + 8 jb + 4 h2
+  uint2 gv[8][4];
+  {
+    const uint16_t* gp = a.gate + (int64_t)ig.b * a.g_sb + (int64_t)ig.h * a.g_sh +
+                         (int64_t)min(g.row, a.L - 1) * a.g_st + 4 * h2;
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) gv[db][jb] = *reinterpret_cast<const uint2*>(gp + 32 * db + 8 * jb);
+  }
   const float l_tot = st.lsum + __shfl_xor(st.lsum, 32, 64);
   const float inv = l_tot > 0.f ? fast_rcp(l_tot) : 0.f;  // fully-masked row -> 0
   if (g.row < ig.q_len) {
@@ -740,7 +815,7 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
         const int d0 = 32 * db + 8 * jb + 4 * h2;
-        const u32x2 g2 = gv[db][jb];
+        const uint2 g2 = gv[db][jb];
         const float o0 = acc[4 * jb + 0] * inv * sigmoidf(__uint_as_float(g2.x << 16));
         const float o1 = acc[4 * jb + 1] * inv * sigmoidf(__uint_as_float(g2.x & 0xffff0000u));
         const float o2 = acc[4 * jb + 2] * inv * sigmoidf(__uint_as_float(g2.y << 16));
@@ -759,7 +834,7 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
 template <bool CAUSAL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_fused_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint16_t KO[2 * 2 * FT], VO[2 * 2 * FT];
+  __shared__ __attribute__((aligned(1024))) uint16_t KO[3 * 2 * FT], VO[2 * 2 * FT];
   const int lane = threadIdx.x & 63;
   // static bounds from the norm weights: |k~| <= sqrt(D) * max|kw + w_offset| for
   // every cached row, |q op| <= max|qw + w_offset| for every scaled query row
@@ -786,7 +861,10 @@ void prefill_fused_kernel(PrefillArgs a) {
   SoloLds L;
   L.k = KO;
   L.v = VO;
-  solo_item<CAUSAL>(a, item_at(a, blockIdx.x), L, bound <= FSTATIC_LIMIT ? bound : -1.0f);
+  if (bound <= FSTATIC_LIMIT)
+    solo_item<CAUSAL, false>(a, item_at(a, blockIdx.x), L);
+  else
+    solo_item<CAUSAL, true>(a, item_at(a, blockIdx.x), L);
   fwait_vmcnt<0>();  // no LDS load may land after the workgroup is gone
 }
 
