@@ -44,7 +44,7 @@ def prefill_flops(T: int, prior: int = 0) -> float:
     return 4.0 * D * HQ * (T * prior + T * (T + 1) / 2)
 
 
-def profiled_traffic(name="prefill_kernel_config2.md"):
+def profiled_traffic(name="prefill_fused_kernel_config2.md"):
     """HBM bytes per launch of the prefill kernel from the committed rocprofv3
     FETCH_SIZE/WRITE_SIZE summary (counters cannot be read from inside this
     process); None when the summary is absent."""

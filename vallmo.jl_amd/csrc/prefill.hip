@@ -457,16 +457,13 @@ hipError_t launch_prefill(const PrefillArgs& a, bool qraw, bool gate, hipStream_
   const int64_t nwg = (int64_t)a.n_qt * a.H * a.B;
   if (nwg == 0) return hipSuccess;
   dim3 grid((unsigned)nwg), block(256);
-  if (qraw && gate && a.causal)
-    hipLaunchKernelGGL((prefill_kernel<true, true, true>), grid, block, 0, st, a);
-  else if (!qraw && !gate && a.causal)
+  // the fused gated path is prefill_fused_kernel; this one serves the attention!
+  // operator (normalised q, no gate)
+  if (qraw || gate) return hipErrorInvalidValue;
+  if (a.causal)
     hipLaunchKernelGGL((prefill_kernel<false, false, true>), grid, block, 0, st, a);
-  else if (!qraw && !gate && !a.causal)
-    hipLaunchKernelGGL((prefill_kernel<false, false, false>), grid, block, 0, st, a);
-  else if (qraw && gate && !a.causal)
-    hipLaunchKernelGGL((prefill_kernel<true, true, false>), grid, block, 0, st, a);
   else
-    return hipErrorInvalidValue;
+    hipLaunchKernelGGL((prefill_kernel<false, false, false>), grid, block, 0, st, a);
   return hipGetLastError();
 }
 

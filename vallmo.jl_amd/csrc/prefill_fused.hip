@@ -5,39 +5,31 @@
 //
 // One workgroup (4 waves, one per SIMD, the whole 160-KB LDS) per work item
 // (b, h, 128-row q-block), heaviest causal q-blocks first (the hardware hands the
-// next item to the first CU that frees up). All products are 32x32x16 bf16 MFMAs
-// with fp32 accumulation, over 32-key tiles:
-//     S^T[key][row] = K[key][:] . Q[row][:]       A = K fragment, B = Q^T fragment
-//     O^T[d][row]  += V^T[d][key] . P^T[key][row] A = V^T fragment, B = P^T fragment
+// next item to the first CU that frees up). Each wave owns 32 query rows. All
+// products are 32x32x16 bf16 MFMAs with fp32 accumulation:
+//     S^T[key][row] = K[key][:] . Q[row][:]       A = K fragment, B = Q^T (AGPRs)
+//     O^T[d][row]  += V^T[d][key] . P^T[key][row] A = V^T fragment, B = P^T
+// P^T is packed from the wave's own S^T accumulator, so P never leaves the wave.
 //
-// Wave pairs: the two waves of a pair share 64 query rows. Wave e of the pair
-// takes every other key tile (tiles t = e mod 2): QK of its tile for all 64 rows
-// (each K fragment read from LDS feeds two MFMAs), the softmax of that tile, and
-// PV of d-half e (d in 128e .. 128e+127) for all 64 rows over both tiles of the
-// pair step (each V fragment feeds two MFMAs), its own tile's P^T first (read
-// back before the barrier), the partner's through LDS. This halves the LDS
-// operand traffic of one-wave-per-32-rows tiling (one b128 read per MFMA). K
-// tiles stream through an 8-slot LDS ring by direct global->LDS loads (issued
-// two pair steps ahead); V^T fragments come straight from the workspace into
-// registers one pair step ahead (the V^T transpose kernel writes each 32-key tile
-// fragment-major, so every fragment is one coalesced 1-KB load). Per pair step
-// and wave: 64 MFMAs, 16 K reads, 8 P reads, 4 P writes, 16 V loads, 8 tile
-// loads, 32 exponentials; a three-stage software pipeline (QK of the next tile,
-// softmax of the current one, PV of the previous pair) with one barrier.
+// Steps of 64 keys (two 32-key tiles). K tiles and V^T tiles (fragment-major,
+// written by the V^T transpose kernel) stream into LDS by direct global->LDS
+// loads shared by the four waves: V^T one step ahead into two objects, K two
+// steps ahead into three (160 KB). Step i is a three-stage software pipeline --
+// QK of block i+2, the softmax of block i+1, PV of block i -- cut into 16 slots
+// of four products; after each product the wave issues one LDS read for the slot
+// two ahead and one piece of the softmax, and each slot issues one tile load.
+// Scheduling fences keep the VALU work between the products. One barrier per step.
 //
-// Loads whose results feed MFMAs directly (V^T, K and P^T fragments) are issued
-// from inline asm with counted waits (the compiler would drain every load in
-// flight, including the tile loads two steps ahead, before each use). Each of
-// these registers is loaded and consumed inside one straight-line pair step: V^T
-// at the start of the step for that step's PV (the QK phase hides the latency),
-// K four fragments ahead within the QK phase, P^T just before the PV; the
-// consumer reads the value through the wait statement, so no copy of it can be
-// placed before its data has landed.
+// LDS reads feeding the products are issued from inline asm and waited for by a
+// counted s_waitcnt inside the product's own asm statement (the compiler would
+// drain every load in flight, including the tile loads two steps ahead, before
+// each use). Every read's register is consumed within its step.
 //
-// Softmax: a static shift. The QK-norm weights bound every logit (|q op| <=
-// max|qw + w_offset|, |k~| <= 16 max|kw + w_offset|); when that bound is at most
-// 64 in log2 units it is the shift for every row. Otherwise an exact row max is
-// taken first by a QK-only pass over the same tiles and used as each row's shift.
+// Softmax: the QK-norm weights bound every logit (|q op| <= max|qw + w_offset|,
+// |k~| <= 16 max|kw + w_offset|). When the bound is at most 64 in log2 units,
+// P = exp2(S) needs no shift (P stays within 2^+-64 and the final 1/l cancels any
+// common scale). Otherwise an exact row max is taken first by a QK-only pass over
+// the same tiles and P = exp2(S - max).
 #include "common.h"
 #include "kernels.h"
 
@@ -142,23 +134,9 @@ __device__ __forceinline__ void fwait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
-// waits for the inline-asm loads: they order against the asm that consumes
-// their registers by program order alone
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
-}
-template <int N>
-__device__ __forceinline__ void lgkm_wait() {
-  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
-  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
-}
-
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void pin(uint32_t& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
-__device__ __forceinline__ void pin(f32x16& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin_acc(uint4& x) {
   u32x4 t = __builtin_bit_cast(u32x4, x);
   asm volatile("" : "+a"(t));
@@ -176,61 +154,18 @@ __device__ __forceinline__ float dot2_ones(uint32_t w, float acc) {
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
-template <int OFF>
-__device__ __forceinline__ void ds_w128(uint32_t addr, const uint4& v) {
-  asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(addr), "v"(__builtin_bit_cast(u32x4, v)),
-               "i"(OFF));
-}
-
-// ---- asm loads into compiler registers and the waits that release them. A load
-// defines its value; the wait takes it (tied) so every reader is placed after the
-// wait; the waits count in issue order (loads of one kind complete in order).
+// ---- LDS reads into compiler registers and the waits that release them. A read
+// defines its value; the wait takes it (tied, or inside the consuming asm) so
+// every reader is placed after the wait; LDS reads complete in issue order.
 template <int OFF>
 __device__ __forceinline__ u32x4 ds_b128(uint32_t addr) {
   u32x4 r;
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
   return r;
 }
-template <int IMM>
-__device__ __forceinline__ u32x4 g_b128(const char* base, uint32_t off) {
-  static_assert(IMM >= 0 && IMM < 4096, "global offset is 13-bit signed");
-  u32x4 r;
-  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(r) : "v"(off), "s"(base), "i"(IMM));
-  return r;
-}
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-template <int IMM>
-__device__ __forceinline__ u32x2 g_b64(const void* p) {
-  u32x2 r;
-  asm volatile("global_load_dwordx2 %0, %1, off offset:%2" : "=v"(r) : "v"(p), "i"(IMM));
-  return r;
-}
-template <int N>
-__device__ __forceinline__ void vm_take8(u32x2 (&g)[4][4], int dq0) {
-  asm volatile("s_waitcnt vmcnt(%8)"
-               : "+v"(g[dq0][0]), "+v"(g[dq0][1]), "+v"(g[dq0][2]), "+v"(g[dq0][3]),
-                 "+v"(g[dq0 + 1][0]), "+v"(g[dq0 + 1][1]), "+v"(g[dq0 + 1][2]), "+v"(g[dq0 + 1][3])
-               : "n"(N));
-}
-// a 16-byte workspace load into v in place (tied: whatever read the old contents
-// of v is placed before it, and nothing can read the new contents before vm_take)
-template <int IMM>
-__device__ __forceinline__ void g_b128_into(u32x4& v, const char* base, uint32_t off) {
-  static_assert(IMM >= 0 && IMM < 4096, "global offset is 13-bit signed");
-  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "+v"(v) : "v"(off), "s"(base), "i"(IMM));
-}
 template <int N>
 __device__ __forceinline__ void lgkm_take(u32x4& x, u32x4& y) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N));
-}
-template <int N>
-__device__ __forceinline__ void lgkm_take(u32x4& x, u32x4& y, u32x4& z, u32x4& w) {
-  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(x), "+v"(y), "+v"(z), "+v"(w) : "n"(N));
-}
-template <int N>
-__device__ __forceinline__ void vm_take(u32x4& x, u32x4& y, u32x4& z, u32x4& w) {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(x), "+v"(y), "+v"(z), "+v"(w) : "n"(N));
 }
 // S^T[key][row] (+)= K fragment . Q^T (S in VGPRs, Q in AGPRs); the builtin would
 // accumulate in AGPRs. A dependent product always has another MFMA between it and
@@ -420,11 +355,6 @@ __device__ __forceinline__ void solo_mask(const SoloGeo& g, int blk, int lane, f
       s[t][j] = key <= lim ? s[t][j] : -INFINITY;
     }
   }
-}
-
-// O^T += V^T fragment . P^T, O in AGPRs
-__device__ __forceinline__ void mfma_pv(f32x16& o, const u32x4& v, const u32x4& p) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(o) : "v"(v), "v"(p));
 }
 
 // Global->LDS tile loads. A tile is 16 one-KB pieces; wave w loads pieces 4w ..
