@@ -135,6 +135,7 @@ __device__ __forceinline__ void fwait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void pin(uint32_t& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin_acc(uint4& x) {
@@ -314,6 +315,8 @@ struct SoloState {
   f32x16 s[2][2];    // S^T in log2 units, by step parity and tile
   u32x4 p[2][4];     // packed P^T, by step parity and key step
   float negm;        // minus this lane's row shift (log2 units)
+  uint32_t kb[8];    // LDS address of K fragment q (q + 8 at +256) in this step's K object
+  u32x4 gv[16];      // gate logits of this wave's rows, coalesced (see gate_loads; AGPRs)
   float lsum;        // row sum of this lane's packed P^T
 };
 
@@ -562,18 +565,14 @@ __device__ __forceinline__ void solo_slot(SoloState& st, const SoloCtx& sc, cons
 // barrier: every wave's loads of V^T block i and K block i + 2 (issued one and two
 // steps back; only the last step's K loads may still be in flight) are in, and
 // every wave is done with step i - 1's reads.
-template <bool CAUSAL, bool SHIFT, int J, bool QK, bool SM, bool PV, bool DV, bool FIRST = false>
+template <bool CAUSAL, bool SHIFT, int J, bool QK, bool SM, bool PV, bool DV, bool FIRST = false,
+          int WAITV = 8>
 __device__ __forceinline__ void solo_step(SoloState& st, const SoloCtx& sc, const SoloLds& L,
                                           const SoloGeo& g, int i, int lane, TileStream& kst,
                                           TileStream& vst) {
-  fwait_vmcnt<8>();
+  fwait_vmcnt<WAITV>();
   fbarrier();
-  uint32_t kb[8];
-  {
-    const uint32_t ko = (uint32_t)((i + 2) % 3) * 32768u;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) kb[q] = sc.kaddr[q] + ko;
-  }
+  const uint32_t (&kb)[8] = st.kb;
   uint16_t* kd = L.k + ((i + 4) % 3) * (2 * FT);
   // kst: tiles 2(i + 4), 2(i + 4) + 1; vst: 2(i + 1), 2(i + 1) + 1
   const TileSrc ks[2] = {kst.at(0), kst.at(1)};
@@ -608,6 +607,12 @@ __device__ __forceinline__ void solo_step(SoloState& st, const SoloCtx& sc, cons
   SS(8); SS(9); SS(10); SS(11); SS(12); SS(13); SS(14); SS(15);
 #undef SS
   if constexpr (QK) mfma_drain(st.s[J][0], st.s[J][1]);
+  {
+    // next step's K object: (i + 3) % 3
+    const int dk = (i + 2) % 3 == 2 ? -65536 : 32768;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) st.kb[q] += dk;
+  }
 }
 
 // Exact row max of the shifted-free S over the item's keys (QK only, K object
@@ -655,6 +660,31 @@ __device__ __forceinline__ float solo_max(const SoloState& st, const SoloCtx& sc
   return xor32_max(m);
 }
 
+// Gate logits of the wave's 32 rows, loaded once into AGPRs after the prologue
+// and held to the epilogue: load i holds row 2i + h of the wave (h = lane / 32),
+// bf16 8 (lane % 32) .. +7 -- one 1-KB coalesced access per load. The epilogue
+// regroups them (and the output) through LDS.
+__device__ __forceinline__ void gate_loads(const uint16_t* base, int64_t row_st, int row0, int last_row,
+                                           u32x4 (&g)[16]) {
+  // one pointer steps through the rows; it stops at the last valid row (the
+  // epilogue stores no row past it, so any in-bounds gate serves there)
+  const uint16_t* p = base + (int64_t)min(row0, last_row) * row_st;
+  const int64_t step = 2 * row_st;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=a"(g[i]) : "v"(p));
+    if (i < 15) {
+      p += row0 + 2 * i + 2 <= last_row ? step : 0;
+      asm volatile("" : "+v"(p));
+    }
+  }
+}
+__device__ __forceinline__ void gate_take(u32x4 (&g)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; i += 4)
+    asm volatile("s_waitcnt vmcnt(0)" : "+a"(g[i]), "+a"(g[i + 1]), "+a"(g[i + 2]), "+a"(g[i + 3]));
+}
+
 // K blocks 0 and 1 (tiles 0 .. 3) into K objects 0 and 1
 __device__ __forceinline__ void solo_prime(const SoloCtx& sc, const SoloLds& L) {
 #pragma unroll
@@ -674,9 +704,8 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
   g.row = g.wrow0 + l32;
   g.off = ig.off;
   g.k_len = ig.k_len;
-  QLoads ql;
-  q_load_raw(a, ig.b, ig.h, g.row, h2, ql);
   if (ig.r0 >= ig.q_len) return;  // uniform over the workgroup
+  SoloState st;
   SoloCtx sc;
   init_fctx(sc.c, a, ig, wave, lane);
   sc.vt = reinterpret_cast<const char*>(sc.c.vtbase);
@@ -687,14 +716,19 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
     for (int q = 0; q < 8; ++q) sc.kaddr[q] = lds_addr(L.k) + l32 * 512 + 16 * ((2 * q + h2) ^ sk);
   }
   sc.vaddr = lds_addr(L.v) + 16 * lane;
+  solo_prime(sc, L);  // K blocks 0, 1 land while q is loaded and rotated
+  QLoads ql;
+  q_load_raw(a, ig.b, ig.h, g.row, h2, ql);
   q_load_rest(a, g.row, ig.prior, h2, ql);
-  solo_prime(sc, L);
 
-  SoloState st;
   q_prologue(a, ql, st.qop);
   // rows past the chunk hold finite junk q; their outputs are never stored
 #pragma unroll
   for (int kk = 0; kk < 16; ++kk) pin_acc(st.qop[kk]);
+  // gate logits now (after q is in: the compiler's waits for q know nothing of
+  // these); the two pipeline-filling steps leave them in flight
+  gate_loads(a.gate + (int64_t)ig.b * a.g_sb + (int64_t)ig.h * a.g_sh + 8 * l32, a.g_st, g.wrow0 + h2,
+             a.L - 1, st.gv);
   st.lsum = 0.f;
 
   const int nb = (sc.c.n_tiles + 1) >> 1;  // step blocks of two tiles
@@ -709,8 +743,13 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
   st.negm = negm;
 
   TileStream kst = k_stream(sc.c, 4), vst = v_stream(sc, 0);
-  solo_step<CAUSAL, SHIFT, 0, true, false, false, false>(st, sc, L, g, -2, lane, kst, vst);
-  solo_step<CAUSAL, SHIFT, 1, true, true, false, true>(st, sc, L, g, -1, lane, kst, vst);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) st.kb[q] = sc.kaddr[q];  // step -2 reads K object 0
+  // younger than K block 0 (-2) / 1 (-1): 8 tile loads, and the 16 gate loads
+  // unless the row-max pass has already waited for them
+  constexpr int WG = SHIFT ? 8 : 24;
+  solo_step<CAUSAL, SHIFT, 0, true, false, false, false, false, WG>(st, sc, L, g, -2, lane, kst, vst);
+  solo_step<CAUSAL, SHIFT, 1, true, true, false, true, false, WG>(st, sc, L, g, -1, lane, kst, vst);
   // step 0 starts O (its first products take a zero accumulator)
   solo_step<CAUSAL, SHIFT, 0, true, true, true, true, true>(st, sc, L, g, 0, lane, kst, vst);
   int i = 1;
@@ -721,41 +760,57 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
   if (i < nb) solo_step<CAUSAL, SHIFT, 1, true, true, true, true>(st, sc, L, g, i, lane, kst, vst);
 
   // ---- epilogue: normalise, gate (sigmoid, src/kernels/kernels.jl:34), store in
-  // the Wo input layout
+  // the Wo input layout. The gates (coalesced) and the result (this lane's row)
+  // change layout through a padded 32-row region of LDS per wave.
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
                : "+a"(st.o[0]), "+a"(st.o[1]), "+a"(st.o[2]), "+a"(st.o[3]),
                  "+a"(st.o[4]), "+a"(st.o[5]), "+a"(st.o[6]), "+a"(st.o[7]));
-  // gate logits of this lane's row: 4 at d = 32 dblk + 8 jb + 4 h2
-  uint2 gv[8][4];
-  {
-    const uint16_t* gp = a.gate + (int64_t)ig.b * a.g_sb + (int64_t)ig.h * a.g_sh +
-                         (int64_t)min(g.row, a.L - 1) * a.g_st + 4 * h2;
+  fbarrier();  // every wave is done with the tile objects
+  gate_take(st.gv);
+  // lane index recomputed here so no prologue value has to live this long
+  int elane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(elane));
+  const int el = elane & 31, eh = elane >> 5;
+  constexpr int XROW = HEAD_DIM + 8;  // elements per row of the region (16-B pad)
+  uint16_t* xr = L.k + wave * (32 * XROW);
 #pragma unroll
-    for (int db = 0; db < 8; ++db)
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb) gv[db][jb] = *reinterpret_cast<const uint2*>(gp + 32 * db + 8 * jb);
-  }
+  for (int i = 0; i < 16; ++i)
+    *reinterpret_cast<u32x4*>(xr + (2 * i + eh) * XROW + 8 * el) = st.gv[i];
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's own writes are in
+  asm volatile("" ::: "memory");
   const float l_tot = st.lsum + __shfl_xor(st.lsum, 32, 64);
   const float inv = l_tot > 0.f ? fast_rcp(l_tot) : 0.f;  // fully-masked row -> 0
-  if (g.row < ig.q_len) {
-    uint16_t* op = a.o + (int64_t)ig.b * a.o_sb + (int64_t)ig.h * a.o_sh + (int64_t)g.row * a.o_st;
+  uint2 ov[8][4];
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      const f32x16& acc = st.o[db];
+  for (int db = 0; db < 8; ++db) {
+    const f32x16& acc = st.o[db];
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb) {
-        const int d0 = 32 * db + 8 * jb + 4 * h2;
-        const uint2 g2 = gv[db][jb];
-        const float o0 = acc[4 * jb + 0] * inv * sigmoidf(__uint_as_float(g2.x << 16));
-        const float o1 = acc[4 * jb + 1] * inv * sigmoidf(__uint_as_float(g2.x & 0xffff0000u));
-        const float o2 = acc[4 * jb + 2] * inv * sigmoidf(__uint_as_float(g2.y << 16));
-        const float o3 = acc[4 * jb + 3] * inv * sigmoidf(__uint_as_float(g2.y & 0xffff0000u));
-        uint2 ov;
-        ov.x = pack2(o0, o1);
-        ov.y = pack2(o2, o3);
-        *reinterpret_cast<uint2*>(op + d0) = ov;
-      }
+    for (int jb = 0; jb < 4; ++jb) {
+      const int d0 = 32 * db + 8 * jb + 4 * eh;
+      const uint2 g2 = *reinterpret_cast<const uint2*>(xr + el * XROW + d0);
+      const float o0 = acc[4 * jb + 0] * inv * sigmoidf(__uint_as_float(g2.x << 16));
+      const float o1 = acc[4 * jb + 1] * inv * sigmoidf(__uint_as_float(g2.x & 0xffff0000u));
+      const float o2 = acc[4 * jb + 2] * inv * sigmoidf(__uint_as_float(g2.y << 16));
+      const float o3 = acc[4 * jb + 3] * inv * sigmoidf(__uint_as_float(g2.y & 0xffff0000u));
+      ov[db][jb].x = pack2(o0, o1);
+      ov[db][jb].y = pack2(o2, o3);
     }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // every gate read is done before the region is rewritten
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int db = 0; db < 8; ++db)
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+      *reinterpret_cast<uint2*>(xr + el * XROW + 32 * db + 8 * jb + 4 * eh) = ov[db][jb];
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  asm volatile("" ::: "memory");
+  uint16_t* ob = a.o + (int64_t)ig.b * a.o_sb + (int64_t)ig.h * a.o_sh + 8 * el;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = g.wrow0 + 2 * i + eh;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + (2 * i + eh) * XROW + 8 * el);
+    if (row < ig.q_len) *reinterpret_cast<u32x4*>(ob + (int64_t)row * a.o_st) = v;
   }
 }
 
