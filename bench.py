@@ -2,9 +2,10 @@
 
 Headline (BASELINE.json ``metric``, configs[1]): causal gated-attention prefill,
 B=1, T=4096, 16 q / 4 kv heads, head_dim 256, 64-dim partial RoPE (theta 1e7).
-One step = vm_gated_attn_prefill over one synthetic packed projection: the K/V
-norm+RoPE cache append, the V -> V^T workspace staging, then the flash-attention
-kernel with the q norm+RoPE prologue and sigmoid-gate epilogue. ``value`` = algorithmic TFLOP/s =
+One step = vm_gated_attn_prefill over one synthetic packed projection: one
+kernel for the K/V norm+RoPE cache append and the V -> V^T workspace staging,
+then the flash-attention kernel with the q norm+RoPE prologue and sigmoid-gate
+epilogue. ``value`` = algorithmic TFLOP/s =
 4*D*Hq*sum_{i=1..T} i / step time (QK^T + PV over unmasked pairs only).
 
 Also reported (same JSON line, key "decode"): BASELINE configs 3 (B=32 batched
@@ -13,8 +14,9 @@ in a hipGraph and replayed 256 times with the position advancing on the device)
 in HBM GB/s of K/V actually attended (4096 B per token) + 32 KiB per sequence.
 
 ``roofline`` is for the dominant kernel (the prefill attention kernel): its
-launches are bracketed by hipEvents on the launch stream inside the timed
-region (libvallmo_attn's vm_profile_*). ``cpu_baseline`` times the C fp32
+launches, and only its, are bracketed by hipEvents on the launch stream inside
+the timed region (libvallmo_attn's vm_profile_*); the other kernels are timed
+in separate untimed passes. ``cpu_baseline`` times the C fp32
 oracle (oracle/, test infrastructure) on a bounded row sample of the same
 workload on this host's cores.
 
@@ -84,6 +86,9 @@ def bench_prefill(vm, torch, steps, warmup, T=4096, seed=2):
         step()
     torch.cuda.synchronize()
     lib = vm._lib
+    # timed region: hipEvents bracket only the dominant kernel (each pair of
+    # events costs the step a few microseconds)
+    lib.profile_select(lib.VM_K_PREFILL)
     lib.profile_enable(True)
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -91,17 +96,25 @@ def bench_prefill(vm, torch, steps, warmup, T=4096, seed=2):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     n_attn, ms_attn = lib.profile_read(lib.VM_K_PREFILL)
-    n_rows, ms_rows = lib.profile_read(lib.VM_K_ROWS)
-    n_tr, ms_tr = lib.profile_read(lib.VM_K_TRANSPOSE)
     lib.profile_enable(False)
-    assert n_attn == steps and n_rows == steps and n_tr == steps
+    assert n_attn == steps
+    # untimed: the append + V^T staging kernel on its own events
+    lib.profile_select(lib.VM_K_ROWS)
+    lib.profile_enable(True)
+    n_side = min(steps, 20)
+    for _ in range(n_side):
+        step()
+    torch.cuda.synchronize()
+    n_rows, ms_rows = lib.profile_read(lib.VM_K_ROWS)
+    lib.profile_enable(False)
+    lib.profile_select()
+    assert n_rows == n_side
     flops = prefill_flops(T)
     return {
         "ms_per_step": 1e3 * wall / steps,
         "tflops": flops / (wall / steps) / 1e12,
         "attn_kernel_ms": ms_attn / n_attn,
-        "append_kernel_ms": ms_rows / n_rows,
-        "transpose_kernel_ms": ms_tr / n_tr,
+        "append_vt_kernel_ms": ms_rows / n_rows,
         "flops": flops,
     }
 
@@ -133,13 +146,18 @@ def bench_decode3(vm, torch, steps, warmup, seed=3):
         vm.decode_(O, layer, m, gen, qkv)
     torch.cuda.synchronize()
     gen.positions.copy_(pos)
-    lib = vm._lib
-    lib.profile_enable(True)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         vm.decode_(O, layer, m, gen, qkv)   # same position each step: same bytes
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # untimed: both kernels on their own hipEvents
+    lib = vm._lib
+    lib.profile_enable(True)
+    for _ in range(min(steps, 20)):
+        vm.decode_(O, layer, m, gen, qkv)
+    torch.cuda.synchronize()
     n_s, ms_s = lib.profile_read(lib.VM_K_DECODE_SPLIT)
     n_c, ms_c = lib.profile_read(lib.VM_K_DECODE_COMBINE)
     lib.profile_enable(False)
@@ -252,8 +270,10 @@ def cpu_baseline(T=4096, target_s=12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    # defaults: ~50 ms of untimed prefill steps first, so the timed ones run at
+    # the GPU's settled clocks (a cold start runs the first tens of ms slower)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
@@ -284,8 +304,8 @@ def main():
         log("[bench] prefill config2 T=4096")
         pf = bench_prefill(vm, torch, args.steps, args.warmup)
         log(f"[bench] prefill: {pf['ms_per_step']:.3f} ms/step, {pf['tflops']:.1f} TFLOP/s, "
-            f"attn kernel {pf['attn_kernel_ms']:.3f} ms, append {pf['append_kernel_ms']:.4f} ms, "
-            f"V transpose {pf['transpose_kernel_ms']:.4f} ms")
+            f"attn kernel {pf['attn_kernel_ms']:.3f} ms, "
+            f"K/V append + V^T staging {pf['append_vt_kernel_ms']:.4f} ms")
     decode = None
     if not args.no_decode:
         log("[bench] decode config3 B=32")

@@ -52,16 +52,21 @@ int vm_abi_version(void);
  * the recorded events and returns the launch count and summed duration of one
  * kernel class.                                                              */
 enum {
-  VM_K_ROWS = 0,          /* norm+RoPE / append row kernels                  */
+  VM_K_ROWS = 0,          /* norm+RoPE / append row kernels (the gated
+                             prefill's append + V^T staging kernel too)      */
   VM_K_DECODE_SPLIT = 1,  /* split-KV decode attention                       */
   VM_K_DECODE_COMBINE = 2,/* LSE merge (+ gate)                              */
   VM_K_PREFILL = 3,       /* flash attention (prefill)                       */
   VM_K_ADVANCE = 4,       /* device clock                                    */
-  VM_K_TRANSPOSE = 5,     /* prefill: cached V -> V^T workspace tiles        */
+  VM_K_TRANSPOSE = 5,     /* reserved (V^T staging is counted as VM_K_ROWS)  */
   VM_K_COUNT = 6
 };
 int vm_profile_enable(int on);
 int vm_profile_read(int kernel, int* count, double* total_ms);
+/* Restricts the bracketing to the kernel classes whose bit (1 << VM_K_*) is
+ * set in kernel_mask (default: all), so a benchmark can time one kernel
+ * without events around the others.                                          */
+int vm_profile_select(unsigned kernel_mask);
 
 /* ---- runtime (thin HIP wrappers so FFI hosts need no HIP headers) ------ */
 int vm_malloc(void** ptr, size_t bytes);
@@ -201,7 +206,8 @@ int vm_prefill_q_norm_rope(vm_bf16* q_out, int64_t q_st, int64_t q_sh, int64_t q
                            float eps, float w_offset, vm_stream stream);
 
 /* ---- a11: forward(::AttnLayer, …; offset) attention part
- * (src/llm/qwen35.jl:292-318): a9 (K/V into the cache), then one flash-
+ * (src/llm/qwen35.jl:292-318): one kernel appends the chunk's K/V to the
+ * cache (a9) and stages the attended V transposed in scratch, then one flash-
  * attention kernel whose prologue norms+rotates q from qkv and whose
  * epilogue applies the sigmoid gate (a10) and writes out :: (D*Hq, T, B) —
  * the Wo input layout, token stride out_st, batch stride out_sb.

@@ -89,6 +89,7 @@ def _fused(vm, orc, B, T, ctx, prior, qlen, seed, row_step=1, fill_gpu=False):
         keep = np.ones(ctx, bool)
         keep[P:P + C] = False
         vex &= np.array_equal(kg[b][:, keep], kc[b][:, keep])
+        vex &= np.array_equal(vg[b][:, keep], vc[b][:, keep])
     kerr = np.concatenate([e.ravel() for e in kerr])
     return (mx, mn), (float(kerr.max()), float(kerr.mean())), vex, out
 
@@ -123,6 +124,35 @@ def test_config5_chunked_prefill_full_size(vm, orc):
                                          fill_gpu=True)
     print(f"config5: out max {mx:.3e} mean {mn:.3e}; K max {kmx:.3e} mean {kmn:.3e}")
     assert mx <= TOL_MAX and mn <= TOL_MEAN and kmx <= TOL_MAX and kmn <= TOL_MEAN and ok
+
+
+def test_fused_append_equals_standalone_append(vm):
+    """The gated prefill appends K/V inside its V^T staging kernel; the cache it
+    leaves is bit-identical to vm_prefill_kv_append's (a9, qwen35.jl:306-307),
+    ragged, with a prior prefix and a chunk that stops short of the cache end."""
+    banner("fused append == vm_prefill_kv_append")
+    ops, call = vm.ops, vm._lib.call
+    B, T, ctx = 3, 300, 1024
+    prior = np.array([0, 129, 700], np.int32)
+    qlen = np.array([300, 31, 257], np.int32)
+    cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
+    m = vm.AttnModel(cfg)
+    qw = to_dev(normal_bf16((D,), 71, scale=0.05))
+    kw = to_dev(normal_bf16((D,), 72, scale=0.05))
+    kc0 = to_dev(normal_bf16((B, HK, ctx, D), 73))
+    vc0 = to_dev(normal_bf16((B, HK, ctx, D), 74))
+    qkv = to_dev(normal_bf16((B, T, S, D), 75))
+    la = vm.AttnLayer(qw=qw, kw=kw, K_cache=kc0.clone(), V_cache=vc0.clone())
+    vm.forward(la, m, qkv, T, B, prior=i32(prior), q_lengths=i32(qlen))
+    K, V = kc0.clone(), vc0.clone()
+    pr, ql = i32(prior), i32(qlen)  # held: the C ABI takes bare device pointers
+    call("vm_prefill_kv_append", ops._p(K), ops._p(V), K.stride(2), K.stride(1), K.stride(0), ctx,
+         ops._p(qkv), qkv.stride(1), qkv.stride(0), ops._p(kw), ops._p(m.rope["cos"]),
+         ops._p(m.rope["sin"]), ops._p(pr), ops._p(ql), B, T, HQ, HK, D, HALF, float(EPS), 1.0,
+         ops._stream())
+    torch.cuda.synchronize()
+    assert torch.equal(la.K_cache, K) and torch.equal(la.V_cache, V)
+    assert not torch.equal(K, kc0)  # the append did write
 
 
 def test_decode_equals_last_prefill_row(vm):

@@ -109,4 +109,66 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 __device__ __forceinline__ float sigmoidf(float x) { return fast_rcp(1.0f + __expf(-x)); }
 
+// ---------------------------------------------------------------------------
+// One (head, token) row of D = 256 per wave64: lane l holds d = 4l .. 4l+3 (one
+// 8-byte load). The rotate-half partner of d < 32 is d + 32, i.e. lane l ^ 8.
+// Norm + RoPE of one row held as 4 floats per lane (d = 4*lane + c):
+// qknorm_rope_append.jl:41-54 / :80-92.
+__device__ __forceinline__ void norm_rope_row_cs(float x[4], const uint16_t* __restrict__ w,
+                                                 float4 cv, float4 sv, float eps, float w_offset,
+                                                 int lane) {
+  // Every rounding step is spelled out (fmaf / __fmul_rn / __fadd_rn): left to
+  // contraction, the compiler would fuse differently in each kernel that
+  // inlines this, and the cache rows that decode and prefill append must be
+  // bit-identical.
+  float ss = __fmul_rn(x[0], x[0]);
+  ss = fmaf(x[1], x[1], ss);
+  ss = fmaf(x[2], x[2], ss);
+  ss = fmaf(x[3], x[3], ss);
+  ss = wave_sum_all(ss);
+  const float r = 1.0f / sqrtf(fmaf(ss, 1.0f / HEAD_DIM, eps));
+  uint2 wv = *reinterpret_cast<const uint2*>(w + 4 * lane);
+  float wf[4] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xffff0000u),
+                 __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xffff0000u)};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) x[c] = __fmul_rn(__fmul_rn(x[c], r), __fadd_rn(wf[c], w_offset));
+  // rotate-half on d < 64: lanes 0..7 hold x1 (d < 32), lanes 8..15 hold x2.
+  float other[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) other[c] = __shfl_xor(x[c], 8, 64);
+  if (lane < 16) {
+    const float cc[4] = {cv.x, cv.y, cv.z, cv.w}, ssn[4] = {sv.x, sv.y, sv.z, sv.w};
+    if (lane < 8) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) x[c] = fmaf(x[c], cc[c], -__fmul_rn(other[c], ssn[c]));
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) x[c] = fmaf(x[c], cc[c], __fmul_rn(other[c], ssn[c]));
+    }
+  }
+}
+// cs, sn: the position's cos / sin table rows (lanes 0..15 read 4 each)
+__device__ __forceinline__ void norm_rope_row(float x[4], const uint16_t* __restrict__ w,
+                                              const float* __restrict__ cs,
+                                              const float* __restrict__ sn, float eps,
+                                              float w_offset, int lane) {
+  float4 cv = make_float4(0.f, 0.f, 0.f, 0.f), sv = cv;
+  if (lane < 16) {
+    const int i0 = 4 * (lane & 7);
+    cv = *reinterpret_cast<const float4*>(cs + i0);
+    sv = *reinterpret_cast<const float4*>(sn + i0);
+  }
+  norm_rope_row_cs(x, w, cv, sv, eps, w_offset, lane);
+}
+
+__device__ __forceinline__ void load_row4(const uint16_t* p, int lane, float x[4]) {
+  uint2 v = *reinterpret_cast<const uint2*>(p + 4 * lane);
+  x[0] = __uint_as_float(v.x << 16); x[1] = __uint_as_float(v.x & 0xffff0000u);
+  x[2] = __uint_as_float(v.y << 16); x[3] = __uint_as_float(v.y & 0xffff0000u);
+}
+__device__ __forceinline__ void store_row4(uint16_t* p, int lane, const float x[4]) {
+  uint2 v; v.x = pack2(x[0], x[1]); v.y = pack2(x[2], x[3]);
+  *reinterpret_cast<uint2*>(p + 4 * lane) = v;
+}
+
 }  // namespace vm

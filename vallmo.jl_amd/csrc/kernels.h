@@ -93,14 +93,25 @@ struct PrefillArgs {
 
 // V cache -> V^T tiles for the fused prefill (one 16-KB tile per 32 keys)
 struct VtArgs {
-  const uint16_t* v;
-  int64_t v_st, v_sh, v_sb;
+  uint16_t* v;               // V cache (read; written for the chunk's keys when fused)
+  int64_t v_st, v_sh, v_sb;  // cache strides (the K cache shares them)
   uint16_t* vt;
   int vt_tiles;
   const int32_t* prior;      // nullable -> 0
   const int32_t* q_lengths;  // nullable -> L
   int B, Hk, L;
   int64_t ctx;
+  // fused cache append (k_raw != nullptr): the chunk's K rows are normed,
+  // rotated and written to kc, its V rows copied to the V cache, and the V^T
+  // tiles of the chunk's keys are built from those same rows
+  uint16_t* kc;
+  const uint16_t* k_raw;
+  const uint16_t* v_raw;
+  int64_t raw_st, raw_sh, raw_sb;
+  const uint16_t* kw;
+  const float* cos_tab;
+  const float* sin_tab;
+  float eps, w_offset;
 };
 constexpr int PREFILL_VT_TILE_KEYS = 32;
 constexpr int64_t PREFILL_VT_TILE_BYTES = 32 * 256 * 2;

@@ -78,22 +78,59 @@ __device__ __forceinline__ FItem item_at(const PrefillArgs& a, int i) {
 // the key order of the P^T operand that lane half h holds for key half ks (the
 // S^T accumulator layout).
 //
-// One workgroup per (32-key tile, kv head, sequence): 16 KB of the cached V in
-// (coalesced 16-byte rows), through LDS, out as one V^T tile (coalesced). Keys
+// One workgroup per (32-key tile, kv head, sequence): the tile's 32 V rows into
+// LDS (one 512-byte row per wave load), out as one V^T tile (coalesced). Keys
 // past the attended length repeat the last one (they are masked; V stays finite).
+// With the fused append (k_raw set), the chunk's keys prior .. k_len-1 come from
+// the packed projection instead of the cache: their K rows are normed and
+// rotated into the K cache and their V rows copied into the V cache, as
+// knorm_rope_append does (src/kernels/qknorm_rope_append.jl:59-98; prefill
+// src/llm/qwen35.jl:306-307), and the V^T tile is built from the same rows.
 __global__ __launch_bounds__(256) void vt_transpose_kernel(VtArgs a) {
   const int t = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int q_len = a.q_lengths ? min(a.q_lengths[b], a.L) : a.L;
-  const int64_t k_len = min((int64_t)(a.prior ? a.prior[b] : 0) + q_len, a.ctx);
+  const int64_t prior = a.prior ? a.prior[b] : 0;
+  const int64_t k_len = min(prior + q_len, a.ctx);
   if ((int64_t)t * FN >= k_len) return;
   __shared__ __attribute__((aligned(16))) uint16_t tile[FN][HEAD_DIM + 8];  // 16-B row pad
-  const int tid = threadIdx.x;
-  const uint16_t* src = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t cache_off = (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+  const bool fused = a.k_raw != nullptr;
+  constexpr int RW = FN / 4;  // rows per wave: r = wave + 4 j
+  // every load of the wave's rows first (one memory latency, not RW of them)
+  uint2 vv[RW], kv[RW];
+  float4 cv[RW], sv[RW];
+  bool app[RW];
+  int64_t key_of[RW];
 #pragma unroll
-  for (int q = tid; q < FN * 32; q += 256) {
-    const int row = q >> 5, c16 = q & 31;
-    const int64_t key = min((int64_t)t * FN + row, k_len - 1);
-    *reinterpret_cast<uint4*>(&tile[row][c16 * 8]) = load16(src + key * a.v_st + c16 * 8);
+  for (int j = 0; j < RW; ++j) {
+    const int64_t key = (int64_t)t * FN + wave + 4 * j;
+    const int64_t src = min(key, k_len - 1);
+    const bool chunk = fused && src >= prior;  // a key of this chunk: not in the cache yet
+    const int64_t raw_off = (int64_t)b * a.raw_sb + (int64_t)hk * a.raw_sh + (src - prior) * a.raw_st;
+    const uint16_t* vp = chunk ? a.v_raw + raw_off : a.v + cache_off + src * a.v_st;
+    vv[j] = *reinterpret_cast<const uint2*>(vp + 4 * lane);
+    app[j] = chunk && key == src;  // append column `key` (position key, 0-based)
+    key_of[j] = key;
+    if (app[j]) {
+      kv[j] = *reinterpret_cast<const uint2*>(a.k_raw + raw_off + 4 * lane);
+      const int i0 = 4 * (lane & 7);
+      cv[j] = *reinterpret_cast<const float4*>(a.cos_tab + key * HALF_ROT + i0);
+      sv[j] = *reinterpret_cast<const float4*>(a.sin_tab + key * HALF_ROT + i0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < RW; ++j) {
+    const int r = wave + 4 * j;
+    *reinterpret_cast<uint2*>(&tile[r][4 * lane]) = vv[j];
+    if (app[j]) {
+      const int64_t key = key_of[j];
+      *reinterpret_cast<uint2*>(a.v + cache_off + key * a.v_st + 4 * lane) = vv[j];
+      float x[4] = {__uint_as_float(kv[j].x << 16), __uint_as_float(kv[j].x & 0xffff0000u),
+                    __uint_as_float(kv[j].y << 16), __uint_as_float(kv[j].y & 0xffff0000u)};
+      norm_rope_row_cs(x, a.kw, cv[j], sv[j], a.eps, a.w_offset, lane);
+      store_row4(a.kc + cache_off + key * a.v_st, lane, x);
+    }
   }
   __syncthreads();
   uint16_t* dst = a.vt + ((int64_t)b * a.Hk + hk) * a.vt_tiles * FT + (int64_t)t * FT;

@@ -26,49 +26,6 @@ __global__ void rope_tables_kernel(float* __restrict__ cos_tab, float* __restric
   sin_tab[idx] = (float)sin((double)ang);
 }
 
-// ---------------------------------------------------------------------------
-// Norm + RoPE of one row held as 4 floats per lane (d = 4*lane + c).
-__device__ __forceinline__ void norm_rope_row(float x[4], const uint16_t* __restrict__ w,
-                                              const float* __restrict__ cs,
-                                              const float* __restrict__ sn, float eps,
-                                              float w_offset, int lane) {
-  float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
-  ss = wave_sum_all(ss);
-  float r = 1.0f / sqrtf(ss * (1.0f / HEAD_DIM) + eps);
-  uint2 wv = *reinterpret_cast<const uint2*>(w + 4 * lane);
-  float wf[4] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xffff0000u),
-                 __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xffff0000u)};
-#pragma unroll
-  for (int c = 0; c < 4; ++c) x[c] = x[c] * r * (wf[c] + w_offset);
-  // rotate-half on d < 64: lanes 0..7 hold x1 (d < 32), lanes 8..15 hold x2.
-  float other[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) other[c] = __shfl_xor(x[c], 8, 64);
-  if (lane < 16) {
-    const int i0 = 4 * (lane & 7);
-    float4 cv = *reinterpret_cast<const float4*>(cs + i0);
-    float4 sv = *reinterpret_cast<const float4*>(sn + i0);
-    float cc[4] = {cv.x, cv.y, cv.z, cv.w}, ssn[4] = {sv.x, sv.y, sv.z, sv.w};
-    if (lane < 8) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) x[c] = x[c] * cc[c] - other[c] * ssn[c];
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) x[c] = x[c] * cc[c] + other[c] * ssn[c];
-    }
-  }
-}
-
-__device__ __forceinline__ void load_row4(const uint16_t* p, int lane, float x[4]) {
-  uint2 v = *reinterpret_cast<const uint2*>(p + 4 * lane);
-  x[0] = __uint_as_float(v.x << 16); x[1] = __uint_as_float(v.x & 0xffff0000u);
-  x[2] = __uint_as_float(v.y << 16); x[3] = __uint_as_float(v.y & 0xffff0000u);
-}
-__device__ __forceinline__ void store_row4(uint16_t* p, int lane, const float x[4]) {
-  uint2 v; v.x = pack2(x[0], x[1]); v.y = pack2(x[2], x[3]);
-  *reinterpret_cast<uint2*>(p + 4 * lane) = v;
-}
-
 // Generic row kernel. Row r -> (b, h, t) with t fastest. Position (0-based)
 // of the row: decode = positions[b]-1 (T = 1), prefill = prior[b] + t.
 // The output row index along the token axis is the position when

@@ -22,6 +22,7 @@ struct ProfRec {
 };
 struct Prof {
   bool on = false;
+  unsigned mask = ~0u;  // kernel classes bracketed while on
   std::vector<ProfRec> recs;
   std::vector<hipEvent_t> pool;
 };
@@ -42,7 +43,7 @@ hipEvent_t prof_event() {
 // stream is not being captured into a graph.
 template <class F>
 hipError_t timed(int id, hipStream_t st, F&& f) {
-  if (!g_prof.on) return f();
+  if (!g_prof.on || !((g_prof.mask >> id) & 1u)) return f();
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return f();
   hipEvent_t a = prof_event(), b = prof_event();
@@ -130,6 +131,10 @@ int vm_profile_enable(int on) {
   }
   g_prof.recs.clear();
   g_prof.on = on != 0;
+  return VM_OK;
+}
+int vm_profile_select(unsigned kernel_mask) {
+  g_prof.mask = kernel_mask;
   return VM_OK;
 }
 int vm_profile_read(int kernel, int* count, double* total_ms) {
@@ -441,14 +446,26 @@ static int prefill_row_common(int B, int T, int Hq, int Hk, int D, int half_rot,
   return VM_OK;
 }
 
+// Argument checks of the prefill K/V append (shared by vm_prefill_kv_append and
+// vm_gated_attn_prefill, which fuses the append into its V^T kernel).
+static int prefill_kv_append_check(vm_bf16* kc, vm_bf16* vc, int64_t c_st, int64_t c_sh,
+                                   int64_t c_sb, int64_t ctx, const vm_bf16* qkv, int64_t qkv_st,
+                                   int64_t qkv_sb, const vm_bf16* kw, const float* cs,
+                                   const float* sn, int B, int T, int Hq, int Hk, int D,
+                                   int half_rot) {
+  TRY(prefill_row_common(B, T, Hq, Hk, D, half_rot, ctx, qkv, qkv_st, qkv_sb));
+  REQUIRE(kc && vc && kw && cs && sn, VM_E_ARG, "prefill_kv_append: NULL pointer argument");
+  for (int64_t s : {c_st, c_sh, c_sb}) TRY(check_stride(s, "cache"));
+  return VM_OK;
+}
+
 int vm_prefill_kv_append(vm_bf16* kc, vm_bf16* vc, int64_t c_st, int64_t c_sh, int64_t c_sb,
                          int64_t ctx, const vm_bf16* qkv, int64_t qkv_st, int64_t qkv_sb,
                          const vm_bf16* kw, const float* cs, const float* sn, const int32_t* prior,
                          const int32_t* q_lengths, int B, int T, int Hq, int Hk, int D,
                          int half_rot, float eps, float w_offset, vm_stream st) {
-  TRY(prefill_row_common(B, T, Hq, Hk, D, half_rot, ctx, qkv, qkv_st, qkv_sb));
-  REQUIRE(kc && vc && kw && cs && sn, VM_E_ARG, "prefill_kv_append: NULL pointer argument");
-  for (int64_t s : {c_st, c_sh, c_sb}) TRY(check_stride(s, "cache"));
+  TRY(prefill_kv_append_check(kc, vc, c_st, c_sh, c_sb, ctx, qkv, qkv_st, qkv_sb, kw, cs, sn, B, T,
+                              Hq, Hk, D, half_rot));
   const int64_t Dl = D;
   vm::RowArgs r{};
   r.in = qkv + 2 * Hq * Dl; r.in2 = qkv + (2 * Hq + Hk) * Dl;
@@ -516,9 +533,9 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm
     REQUIRE(((uintptr_t)scratch & 255) == 0, VM_E_ARG,
             "gated_attn_prefill: scratch must be 256-byte aligned");
   }
-  // a9: checks its own arguments, then appends K/V to the cache
-  TRY(vm_prefill_kv_append(kc, vc, c_st, c_sh, c_sb, ctx, qkv, qkv_st, qkv_sb, kw, cs, sn, prior,
-                           q_lengths, B, T, Hq, Hk, D, half_rot, eps, w_offset, st));
+  // a9's checks; its append runs inside the V^T kernel below
+  TRY(prefill_kv_append_check(kc, vc, c_st, c_sh, c_sb, ctx, qkv, qkv_st, qkv_sb, kw, cs, sn, B, T,
+                              Hq, Hk, D, half_rot));
   if (!work) return VM_OK;
   const int64_t Dl = D;
   vm::PrefillArgs a{};
@@ -530,12 +547,16 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm
   a.k_lengths = nullptr; a.q_lengths = q_lengths; a.prior = prior;
   a.B = B; a.H = Hq; a.Hk = Hk; a.L = T; a.Lk = (int)ctx; a.causal = 1;
   a.n_qt = (T + vm::PREFILL_ROWS_ABI - 1) / vm::PREFILL_ROWS_ABI;
-  // the attended V (prior + chunk) as V^T tiles in the workspace
+  // one kernel: the chunk's K/V appended to the cache (a9) and the attended V
+  // (prior + chunk) as V^T tiles in the workspace
   vm::VtArgs t{};
   t.v = vc; t.v_st = c_st; t.v_sh = c_sh; t.v_sb = c_sb;
   t.vt = reinterpret_cast<uint16_t*>(scratch); t.vt_tiles = (int)prefill_vt_tiles(ctx);
   t.prior = prior; t.q_lengths = q_lengths; t.B = B; t.Hk = Hk; t.L = T; t.ctx = ctx;
-  TRY(hip_status(timed(VM_K_TRANSPOSE, S(st), [&] { return vm::launch_vt_transpose(t, S(st)); }), "gated_attn_prefill transpose"));
+  t.kc = kc; t.k_raw = qkv + 2 * Hq * Dl; t.v_raw = qkv + (2 * Hq + Hk) * Dl;
+  t.raw_st = qkv_st; t.raw_sh = Dl; t.raw_sb = qkv_sb;
+  t.kw = kw; t.cos_tab = cs; t.sin_tab = sn; t.eps = eps; t.w_offset = w_offset;
+  TRY(hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_vt_transpose(t, S(st)); }), "gated_attn_prefill append"));
   a.vt = t.vt; a.vt_tiles = t.vt_tiles;
   return hip_status(timed(VM_K_PREFILL, S(st), [&] { return vm::launch_prefill_fused(a, S(st)); }), "gated_attn_prefill");
 }
