@@ -295,13 +295,15 @@ __device__ __forceinline__ void q_load_rest(const PrefillArgs& a, int row, int p
 // and the 1/16 scale, with the per-row 1/rms folded into that final scale (RoPE
 // is linear); lane holds q[row][16kk + 8h2 + j]
 __device__ __forceinline__ void q_prologue(const PrefillArgs& a, const QLoads& ql, uint4 (&qop)[16]) {
+  // sum of squares straight from the packed pairs (bf16 products are exact in f32)
   float ss = 0.f;
 #pragma unroll
   for (int kk = 0; kk < 16; ++kk) {
-    float x[8];
-    unpack8(ql.qraw[kk], x);
+    const uint32_t w4[4] = {ql.qraw[kk].x, ql.qraw[kk].y, ql.qraw[kk].z, ql.qraw[kk].w};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+    for (int j = 0; j < 4; ++j)
+      ss = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w4[j]), __builtin_bit_cast(bf16x2, w4[j]),
+                                           ss, false);
   }
   ss += __shfl_xor(ss, 32, 64);
   const float scale = QK_SCALE * LOG2E / sqrtf(ss * (1.0f / HEAD_DIM) + a.eps);
