@@ -804,8 +804,11 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
                : "+a"(st.o[0]), "+a"(st.o[1]), "+a"(st.o[2]), "+a"(st.o[3]),
                  "+a"(st.o[4]), "+a"(st.o[5]), "+a"(st.o[6]), "+a"(st.o[7]));
-  fbarrier();  // every wave is done with the tile objects
+  // vmcnt(0) before the barrier: this wave's gate loads and its last tile loads
+  // (which target the K objects the region below reuses) have landed, so after
+  // the barrier no tile load of any wave is still writing LDS
   gate_take(st.gv);
+  fbarrier();  // every wave is done with the tile objects
   // lane index recomputed here so no prologue value has to live this long
   int elane;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(elane));
