@@ -12,7 +12,9 @@ kernel by a data-flow pass over its basic blocks:
      (global_load_dword*, ds_read*) before an s_waitcnt that covers it, counting
      every vector-memory / LDS operation in issue order;
   2. no instruction other than a dependent MFMA touches an MFMA's destination
-     within 11 wait states of its issue (8-pass XDL write -> VALU read).
+     within 11 wait states of its issue (8-pass XDL write -> VALU read);
+  3. the fused prefill's epilogue drains its tile loads before the barrier after
+     which it reuses their LDS.
 The checks were validated against deliberately weakened builds (a vmcnt raised
 by 8, a spill of a pending AGPR load) that they flag.
 """
@@ -176,6 +178,23 @@ def test_fused_prefill_no_async_or_mfma_hazard(fused_asm, causal):
     name = next(k for k in ks if "prefill_fused_kernel" in k and ("ILb1" in k) == causal)
     bad = check(ks[name])
     assert not bad, "\n".join(f"{kind}: '{line}' touches {what}" for kind, line, what in bad[:20])
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_fused_prefill_epilogue_waits_for_tile_loads_before_its_barrier(fused_asm, causal):
+    """The epilogue reuses K-object LDS for the gate/output regrouping, and the last
+    steps' tile loads (global_load_lds) write those objects. Each wave must drain
+    its own loads (vmcnt(0)) before the barrier that opens the epilogue, so no
+    wave's late tile load lands after another wave has started writing there."""
+    ks = kernels(fused_asm)
+    body = ks[next(k for k in ks if "prefill_fused_kernel" in k and ("ILb1" in k) == causal)]
+    writes = [i for i, l in enumerate(body) if re.match(r"ds_write_b128 v\d+, a\[", l)]
+    assert writes, "epilogue gate writes (ds_write_b128 from AGPRs) not found"
+    first = writes[0]
+    bar = max(i for i in range(first) if body[i].startswith("s_barrier"))
+    last_dma = max((i for i in range(bar) if body[i].startswith("global_load_lds")), default=-1)
+    drains = [i for i in range(last_dma + 1, bar) if re.match(r"s_waitcnt vmcnt\(0\)", body[i])]
+    assert drains, "no vmcnt(0) between the last tile load and the epilogue's barrier"
 
 
 def test_checker_flags_a_read_before_its_wait():
