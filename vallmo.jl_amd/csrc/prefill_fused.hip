@@ -86,7 +86,8 @@ __device__ __forceinline__ FItem item_at(const PrefillArgs& a, int i) {
 // rotated into the K cache and their V rows copied into the V cache, as
 // knorm_rope_append does (src/kernels/qknorm_rope_append.jl:59-98; prefill
 // src/llm/qwen35.jl:306-307), and the V^T tile is built from the same rows.
-__global__ __launch_bounds__(256) void vt_transpose_kernel(VtArgs a) {
+constexpr int VT_WAVES = 16;  // waves per V^T staging workgroup
+__global__ __launch_bounds__(64 * VT_WAVES) void vt_transpose_kernel(VtArgs a) {
   const int t = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int q_len = a.q_lengths ? min(a.q_lengths[b], a.L) : a.L;
   const int64_t prior = a.prior ? a.prior[b] : 0;
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(256) void vt_transpose_kernel(VtArgs a) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t cache_off = (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
   const bool fused = a.k_raw != nullptr;
-  constexpr int RW = FN / 4;  // rows per wave: r = wave + 4 j
+  constexpr int RW = FN / VT_WAVES;  // rows per wave: r = wave + VT_WAVES j
   // every load of the wave's rows first (one memory latency, not RW of them)
   uint2 vv[RW], kv[RW];
   float4 cv[RW], sv[RW];
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(256) void vt_transpose_kernel(VtArgs a) {
   int64_t key_of[RW];
 #pragma unroll
   for (int j = 0; j < RW; ++j) {
-    const int64_t key = (int64_t)t * FN + wave + 4 * j;
+    const int64_t key = (int64_t)t * FN + wave + VT_WAVES * j;
     const int64_t src = min(key, k_len - 1);
     const bool chunk = fused && src >= prior;  // a key of this chunk: not in the cache yet
     const int64_t raw_off = (int64_t)b * a.raw_sb + (int64_t)hk * a.raw_sh + (src - prior) * a.raw_st;
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(256) void vt_transpose_kernel(VtArgs a) {
   }
 #pragma unroll
   for (int j = 0; j < RW; ++j) {
-    const int r = wave + 4 * j;
+    const int r = wave + VT_WAVES * j;
     *reinterpret_cast<uint2*>(&tile[r][4 * lane]) = vv[j];
     if (app[j]) {
       const int64_t key = key_of[j];
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(256) void vt_transpose_kernel(VtArgs a) {
   __syncthreads();
   uint16_t* dst = a.vt + ((int64_t)b * a.Hk + hk) * a.vt_tiles * FT + (int64_t)t * FT;
 #pragma unroll
-  for (int o = tid; o < HEAD_DIM * 4; o += 256) {
+  for (int o = tid; o < HEAD_DIM * 4; o += 64 * VT_WAVES) {
     const int f = o >> 6, l = o & 63;
     const int d = 32 * (f >> 1) + (l & 31);
     const int k0 = 16 * (f & 1) + 4 * (l >> 5);
@@ -897,7 +898,7 @@ void prefill_fused_kernel(PrefillArgs a) {
 
 hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st) {
   if (a.B == 0 || a.Hk == 0 || a.vt_tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL(vt_transpose_kernel, dim3(a.vt_tiles, a.Hk, a.B), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(vt_transpose_kernel, dim3(a.vt_tiles, a.Hk, a.B), dim3(64 * VT_WAVES), 0, st, a);
   return hipGetLastError();
 }
 
