@@ -128,7 +128,10 @@ hipError_t launch_decode(const DecodeArgs& a, bool fused_q, hipStream_t st);
 hipError_t launch_combine(const CombineArgs& a, hipStream_t st);
 hipError_t launch_prefill(const PrefillArgs& a, bool qraw, bool gate, hipStream_t st);
 // fused gated prefill (q norm+RoPE prologue, sigmoid-gate epilogue), persistent
-hipError_t launch_prefill_fused(const PrefillArgs& a, hipStream_t st);
+// t0 / t1 (nullable): events stamped by the dispatch itself at the kernel's
+// start and end (hipExtLaunchKernelGGL), for timing without extra packets
+hipError_t launch_prefill_fused(const PrefillArgs& a, hipStream_t st, hipEvent_t t0 = nullptr,
+                                hipEvent_t t1 = nullptr);
 hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st);
 
 // Decode stream partition shared by the scratch-size query and the launchers:

@@ -30,6 +30,8 @@
 // P = exp2(S) needs no shift (P stays within 2^+-64 and the final 1/l cancels any
 // common scale). Otherwise an exact row max is taken first by a QK-only pass over
 // the same tiles and P = exp2(S - max).
+#include <hip/hip_ext.h>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -902,15 +904,22 @@ hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_prefill_fused(const PrefillArgs& a, hipStream_t st) {
+hipError_t launch_prefill_fused(const PrefillArgs& a, hipStream_t st, hipEvent_t t0, hipEvent_t t1) {
   const int64_t n_items = (int64_t)a.n_qt * a.H * a.B;
   if (n_items == 0) return hipSuccess;
   // one item per workgroup, heaviest first (the hardware hands the next item to
   // the first CU that frees up)
-  if (a.causal)
-    hipLaunchKernelGGL((prefill_fused_kernel<true>), dim3((unsigned)n_items), dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((prefill_fused_kernel<false>), dim3((unsigned)n_items), dim3(256), 0, st, a);
+  const dim3 grid((unsigned)n_items), block(256);
+  if (t0 && t1) {
+    if (a.causal)
+      hipExtLaunchKernelGGL((prefill_fused_kernel<true>), grid, block, 0, st, t0, t1, 0, a);
+    else
+      hipExtLaunchKernelGGL((prefill_fused_kernel<false>), grid, block, 0, st, t0, t1, 0, a);
+  } else if (a.causal) {
+    hipLaunchKernelGGL((prefill_fused_kernel<true>), grid, block, 0, st, a);
+  } else {
+    hipLaunchKernelGGL((prefill_fused_kernel<false>), grid, block, 0, st, a);
+  }
   return hipGetLastError();
 }
 

@@ -55,6 +55,22 @@ hipError_t timed(int id, hipStream_t st, F&& f) {
   return e;
 }
 
+// As timed(), for a launcher that takes (start, stop) events and has the
+// dispatch stamp them (hipExtLaunchKernelGGL): the kernel's own span, with no
+// event packets between launches.
+template <class F>
+hipError_t timed_ext(int id, hipStream_t st, F&& f) {
+  if (!g_prof.on || !((g_prof.mask >> id) & 1u)) return f(nullptr, nullptr);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+    return f(nullptr, nullptr);
+  hipEvent_t a = prof_event(), b = prof_event();
+  if (!a || !b) return f(nullptr, nullptr);
+  hipError_t e = f(a, b);
+  g_prof.recs.push_back({id, a, b});
+  return e;
+}
+
 thread_local char g_err[512] = "";
 
 int fail(int code, const char* fmt, ...) {
@@ -558,7 +574,9 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm
   t.kw = kw; t.cos_tab = cs; t.sin_tab = sn; t.eps = eps; t.w_offset = w_offset;
   TRY(hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_vt_transpose(t, S(st)); }), "gated_attn_prefill append"));
   a.vt = t.vt; a.vt_tiles = t.vt_tiles;
-  return hip_status(timed(VM_K_PREFILL, S(st), [&] { return vm::launch_prefill_fused(a, S(st)); }), "gated_attn_prefill");
+  return hip_status(timed_ext(VM_K_PREFILL, S(st),
+                              [&](hipEvent_t t0, hipEvent_t t1) { return vm::launch_prefill_fused(a, S(st), t0, t1); }),
+                    "gated_attn_prefill");
 }
 
 // ---- synthetic inputs ------------------------------------------------------
