@@ -11,7 +11,10 @@ epilogue. ``value`` = algorithmic TFLOP/s =
 Also reported (same JSON line, key "decode"): BASELINE configs 3 (B=32 batched
 decode, lengths ~U{1024..32768}) and 4 (B=1 at 131072 tokens, one step captured
 in a hipGraph and replayed 256 times with the position advancing on the device)
-in HBM GB/s of K/V actually attended (4096 B per token) + 32 KiB per sequence.
+in HBM GB/s of K/V actually attended (4096 B per token) + 32 KiB per sequence,
+and config 1 (B=1 at 512 tokens, launch-latency-bound) as time per step.
+Key "prefill_config5": BASELINE config 5 (B=4 ragged chunks after 8-32 K
+priors) in algorithmic TFLOP/s, step and attention kernel.
 
 ``roofline`` is for the dominant kernel (the prefill attention kernel): its
 launches, and only its, are bracketed by hipEvents on the launch stream inside
@@ -116,6 +119,96 @@ def bench_prefill(vm, torch, steps, warmup, T=4096, seed=2):
         "attn_kernel_ms": ms_attn / n_attn,
         "append_vt_kernel_ms": ms_rows / n_rows,
         "flops": flops,
+    }
+
+
+def bench_prefill5(vm, torch, steps, warmup, seed=5):
+    """Config 5: B=4 ragged chunks (a seeded permutation of {512, 1024, 2048, 2048})
+    after prior caches ~U{8192..32768} (the same draws as the config-5 GPU test)."""
+    rng = np.random.default_rng(seed)
+    qlen = rng.permutation(np.array([512, 1024, 2048, 2048], np.int32)).astype(np.int32)
+    prior = rng.integers(8192, 32769, size=4).astype(np.int32)
+    B, T = 4, int(qlen.max())
+    ctx = int((prior + qlen).max())
+    cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
+    qw = torch.empty(D, dtype=torch.bfloat16, device="cuda")
+    kw = torch.empty_like(qw)
+    vm.fill_normal_(qw, seed * 100 + 1, scale=0.05)
+    vm.fill_normal_(kw, seed * 100 + 2, scale=0.05)
+    layer = vm.attn_layer(cfg, qw, kw)
+    vm.fill_normal_(layer.K_cache, seed * 100 + 3)
+    vm.fill_normal_(layer.V_cache, seed * 100 + 4)
+    qkv = torch.empty((B, T, S, D), dtype=torch.bfloat16, device="cuda")
+    vm.fill_normal_(qkv, seed * 100 + 5)
+    m = vm.AttnModel(cfg)
+    out = torch.empty((B, T, HQ * D), dtype=torch.bfloat16, device="cuda")
+    pr = torch.from_numpy(prior).cuda()
+    ql = torch.from_numpy(qlen).cuda()
+
+    def step():   # appends the same chunk columns each time: same work per step
+        vm.forward(layer, m, qkv, T, B, prior=pr, q_lengths=ql, out=out)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    lib = vm._lib
+    lib.profile_select(lib.VM_K_PREFILL)
+    lib.profile_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    n_attn, ms_attn = lib.profile_read(lib.VM_K_PREFILL)
+    lib.profile_enable(False)
+    lib.profile_select()
+    assert n_attn == steps
+    c, p = qlen.astype(np.float64), prior.astype(np.float64)
+    flops = float(4 * D * HQ * np.sum(c * p + c * (c + 1) / 2))
+    kms = ms_attn / n_attn
+    return {
+        "config": f"config5: ragged chunked prefill B=4 chunks={qlen.tolist()} "
+                  f"priors={prior.tolist()} (seed {seed})",
+        "flop_per_step": flops,
+        "ms_per_step": 1e3 * wall / steps,
+        "tflops": flops / (wall / steps) / 1e12,
+        "attn_kernel_ms": kms,
+        "attn_kernel_tflops": flops / (kms * 1e-3) / 1e12,
+        "frac_of_bf16_peak": flops / (kms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+    }
+
+
+def bench_decode1(vm, torch, steps, warmup, seed=1):
+    """Config 1: B=1, attended length 512 (prior 511 tokens + the new one)."""
+    B, ctx, L = 1, 512, 512
+    cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
+    qw = torch.empty(D, dtype=torch.bfloat16, device="cuda")
+    kw = torch.empty_like(qw)
+    vm.fill_normal_(qw, seed * 100 + 1, scale=0.05)
+    vm.fill_normal_(kw, seed * 100 + 2, scale=0.05)
+    layer = vm.attn_layer(cfg, qw, kw)
+    vm.fill_normal_(layer.K_cache, seed * 100 + 3)
+    vm.fill_normal_(layer.V_cache, seed * 100 + 4)
+    qkv = torch.empty((B, S, D), dtype=torch.bfloat16, device="cuda")
+    vm.fill_normal_(qkv, seed * 100 + 5)
+    m = vm.AttnModel(cfg)
+    gen = vm.Generation(B)
+    gen.positions.fill_(L)
+    O = torch.empty((B, HQ, D), dtype=torch.bfloat16, device="cuda")
+    for _ in range(warmup):
+        vm.decode_(O, layer, m, gen, qkv)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        vm.decode_(O, layer, m, gen, qkv)   # same position each step: same bytes
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    nbytes = decode_bytes([L])
+    return {
+        "config": "config1: decode B=1 at attended length 512 (launch-latency-bound parity config)",
+        "bytes_per_step": nbytes,
+        "us_per_step": 1e6 * wall / steps,
+        "gbs": nbytes / (wall / steps) / 1e9,
     }
 
 
@@ -306,6 +399,12 @@ def main():
         log(f"[bench] prefill: {pf['ms_per_step']:.3f} ms/step, {pf['tflops']:.1f} TFLOP/s, "
             f"attn kernel {pf['attn_kernel_ms']:.3f} ms, "
             f"K/V append + V^T staging {pf['append_vt_kernel_ms']:.4f} ms")
+    pf5 = None
+    if not args.no_prefill:
+        log("[bench] prefill config5 (ragged chunked, B=4)")
+        pf5 = bench_prefill5(vm, torch, max(10, args.steps // 15), max(3, args.warmup // 30))
+        log(f"[bench] prefill5: {pf5['ms_per_step']:.3f} ms/step, {pf5['tflops']:.1f} TFLOP/s, "
+            f"attn kernel {pf5['attn_kernel_ms']:.3f} ms = {pf5['attn_kernel_tflops']:.1f} TFLOP/s")
     decode = None
     if not args.no_decode:
         log("[bench] decode config3 B=32")
@@ -316,9 +415,12 @@ def main():
         d4 = bench_decode4(vm, torch)
         log(f"[bench] decode4: {d4['ms_per_replay'] * 1e3:.1f} us/replay {d4['gbs']:.0f} GB/s "
             f"(split kernel {d4['split_kernel_gbs']:.0f} GB/s)")
-        for d in (d3, d4):
+        log("[bench] decode config1 B=1 at 512")
+        d1 = bench_decode1(vm, torch, max(20, args.steps // 3), 10)
+        log(f"[bench] decode1: {d1['us_per_step']:.1f} us/step")
+        for d in (d3, d4, d1):
             d["frac_of_hbm_peak"] = d["gbs"] / PEAK_HBM_GBS
-        decode = {"config3": d3, "config4": d4, "peak_GBs": PEAK_HBM_GBS}
+        decode = {"config3": d3, "config4": d4, "config1": d1, "peak_GBs": PEAK_HBM_GBS}
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle)")
@@ -351,6 +453,7 @@ def main():
                      "kernel_ms": round(pf["attn_kernel_ms"], 5),
                      "flop_per_launch": pf["flops"]},
         "cpu_baseline": cpu,
+        "prefill_config5": pf5,
         "decode": decode,
     }
     print(json.dumps(line), flush=True)

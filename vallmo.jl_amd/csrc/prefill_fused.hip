@@ -73,6 +73,45 @@ __device__ __forceinline__ FItem item_at(const PrefillArgs& a, int i) {
   return it;
 }
 
+// Batches (B > 1, at most 256 (sequence, q-block) pairs): the pairs are ranked
+// by the keys their last row attends (prior + chunk rows, from the device-side
+// lengths), heaviest first, ties by index, and rank r takes the H items
+// r H .. r H + H - 1 (heads grouped per XCD as above). With ragged priors the
+// q-block index alone says little about an item's work. All threads of the
+// workgroup take part; `scratch` is 257 ints of LDS.
+__device__ __forceinline__ FItem item_ranked(const PrefillArgs& a, int i, bool causal, int* scratch) {
+  const int NB = a.B * a.n_qt;
+  if (a.B == 1 || NB > 256) return item_at(a, i);
+  const int r = i / a.H, rem = i % a.H;
+  const int t = threadIdx.x;
+  if (t < NB) {
+    const int b = t / a.n_qt, qt = t % a.n_qt;
+    const int q_len = a.q_lengths ? min(a.q_lengths[b], a.L) : a.L;
+    const int prior = a.prior ? a.prior[b] : 0;
+    const int r0 = qt * FM;
+    scratch[t] = r0 >= q_len ? 0 : (causal ? prior + min(q_len, r0 + FM) : prior + q_len);
+  }
+  __syncthreads();
+  if (t < NB) {
+    const int w = scratch[t];
+    int rank = 0;
+    for (int u = 0; u < NB; ++u) {
+      const int wu = scratch[u];
+      rank += (wu > w) || (wu == w && u < t);
+    }
+    if (rank == r) scratch[256] = t;
+  }
+  __syncthreads();
+  const int blk = scratch[256];
+  __syncthreads();  // every thread has read it before the LDS is reused
+  FItem it;
+  it.b = blk / a.n_qt;
+  it.qt = blk % a.n_qt;
+  it.h = (a.H & 7) == 0 ? (rem & 7) * (a.H >> 3) + (rem >> 3) : rem;
+  it.hk = it.h / (a.H / a.Hk);
+  return it;
+}
+
 // ---- V^T tiles. Tile t of (b, hk) holds keys 32t .. 32t+31 as 16 MFMA
 // A-operand fragments of 1 KB, fragment f = 2 * dblk + ks (d-block dblk of 32
 // d-rows, key half ks): lane l's 16 bytes (at 1024 f + 16 l) are the 8 keys
@@ -891,10 +930,11 @@ void prefill_fused_kernel(PrefillArgs a) {
   SoloLds L;
   L.k = KO;
   L.v = VO;
+  const FItem it = item_ranked(a, blockIdx.x, CAUSAL, reinterpret_cast<int*>(KO));
   if (bound <= FSTATIC_LIMIT)
-    solo_item<CAUSAL, false>(a, item_at(a, blockIdx.x), L);
+    solo_item<CAUSAL, false>(a, it, L);
   else
-    solo_item<CAUSAL, true>(a, item_at(a, blockIdx.x), L);
+    solo_item<CAUSAL, true>(a, it, L);
   fwait_vmcnt<0>();  // no LDS load may land after the workgroup is gone
 }
 
