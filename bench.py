@@ -19,9 +19,11 @@ priors) in algorithmic TFLOP/s, step and attention kernel.
 ``roofline`` is for the dominant kernel (the prefill attention kernel): its
 launches, and only its, are bracketed by hipEvents on the launch stream inside
 the timed region (libvallmo_attn's vm_profile_*); the other kernels are timed
-in separate untimed passes. ``cpu_baseline`` times the C fp32
-oracle (oracle/, test infrastructure) on a bounded row sample of the same
-workload on this host's cores.
+in separate untimed passes. Before the timed steps, after --warmup steps, a
+clock-settle phase runs untimed steps until successive block means of the
+attention kernel agree within 1% (``settle_ms`` in the JSON line).
+``cpu_baseline`` times the C fp32 oracle (oracle/, test infrastructure) on this
+host's cores for every config (key "configs"), with the CPU model and core count.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
 """
@@ -68,7 +70,42 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def bench_prefill(vm, torch, steps, warmup, T=4096, seed=2):
+def settle_clocks(vm, torch, step, block=20, tol=0.01, min_s=0.25, max_s=5.0):
+    """Untimed steps until the GPU clocks have settled: blocks of `block` steps
+    are run with the attention kernel on its own events, until the last three
+    block means agree within `tol` (after at least min_s, at most max_s). A cold
+    GPU runs its first tens of milliseconds at lower clocks (the first 20 prefill
+    launches average ~169 us against ~140 us settled); --warmup alone counts
+    steps, not time, so this phase keeps the timed steps off that ramp."""
+    lib = vm._lib
+    means = []
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        lib.profile_select(lib.VM_K_PREFILL)
+        lib.profile_enable(True)
+        for _ in range(block):
+            step()
+        torch.cuda.synchronize()
+        k, ms = lib.profile_read(lib.VM_K_PREFILL)
+        lib.profile_enable(False)
+        lib.profile_select()
+        n += block
+        means.append(ms / max(k, 1))
+        el = time.perf_counter() - t0
+        if el >= max_s:
+            break
+        if el >= min_s and len(means) >= 3:
+            last = means[-3:]
+            if max(last) / min(last) - 1.0 < tol:
+                break
+    return {"settle_ms": round(1e3 * (time.perf_counter() - t0), 1), "settle_steps": n,
+            "block_means_us": [round(1e3 * m, 2) for m in means[:3]] + ["..."] +
+                              [round(1e3 * m, 2) for m in means[-3:]]
+            if len(means) > 6 else [round(1e3 * m, 2) for m in means]}
+
+
+def bench_prefill(vm, torch, steps, warmup, T=4096, seed=2, settle=True):
     B, ctx = 1, T
     cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
     qw = torch.empty(D, dtype=torch.bfloat16, device="cuda")
@@ -89,6 +126,7 @@ def bench_prefill(vm, torch, steps, warmup, T=4096, seed=2):
         step()
     torch.cuda.synchronize()
     lib = vm._lib
+    settle = settle_clocks(vm, torch, step) if settle else {"settle_ms": 0.0, "settle_steps": 0}
     # timed region: hipEvents bracket only the dominant kernel (each pair of
     # events costs the step a few microseconds)
     lib.profile_select(lib.VM_K_PREFILL)
@@ -114,6 +152,7 @@ def bench_prefill(vm, torch, steps, warmup, T=4096, seed=2):
     assert n_rows == n_side
     flops = prefill_flops(T)
     return {
+        "settle": settle,
         "ms_per_step": 1e3 * wall / steps,
         "tflops": flops / (wall / steps) / 1e12,
         "attn_kernel_ms": ms_attn / n_attn,
@@ -320,54 +359,168 @@ def bench_decode4(vm, torch, replays=256, seed=4):
     }
 
 
-def cpu_baseline(T=4096, target_s=12.0):
-    """Time the fp32 C oracle on a row sample of the config-2 prefill."""
-    import oracle
-    from oracle.rng import normal_bf16
-    B, ctx = 1, T
-    qkv = normal_bf16((B, T, S, D), 203)
-    qw = normal_bf16((D,), 201, scale=0.05)
-    kw = normal_bf16((D,), 202, scale=0.05)
-    zero = np.zeros((B, HK, ctx, D), np.uint16)
-    c, s = oracle.rope_tables(HALF, ctx, THETA)
-    threads = oracle.threads_env()
-    prior, qlen = np.zeros(B, np.int32), np.full(B, T, np.int32)
-    # calibrate on a sparse sample, then size the timed sample to ~target_s;
-    # when the whole problem takes less, time it several times (median)
-    step = 256
-    t0 = time.perf_counter()
-    oracle.gated_prefill(qkv, zero, zero, prior, qlen, qw, kw, c, s, Hq=HQ, Hk=HK, eps=EPS,
-                         w_offset=1.0, row_step=step, nthreads=threads)
-    t_cal = time.perf_counter() - t0
-    step = int(max(1, min(256, step * t_cal / target_s)))
+def cpu_info():
+    """CPU model, sockets x physical cores per socket, and logical CPUs of this host."""
+    import subprocess
+    info = {"cpu_model": None, "physical_cores": None, "logical_cpus": os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = {}
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                kv[k.strip()] = v.strip()
+        info["cpu_model"] = kv.get("Model name")
+        cps, sock = kv.get("Core(s) per socket"), kv.get("Socket(s)")
+        if cps and sock and cps.isdigit() and sock.isdigit():
+            info["physical_cores"] = int(cps) * int(sock)
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return info
+
+
+def _median_time(fn, min_runs, max_runs, budget_s):
+    """Median wall time of fn() over at least min_runs runs (at most max_runs, or
+    fewer once budget_s is spent after min_runs)."""
     times = []
     while True:
         t0 = time.perf_counter()
-        oracle.gated_prefill(qkv, zero, zero, prior, qlen, qw, kw, c, s, Hq=HQ, Hk=HK, eps=EPS,
-                             w_offset=1.0, row_step=step, nthreads=threads)
+        fn()
         times.append(time.perf_counter() - t0)
-        if len(times) >= 7 or (len(times) >= 3 and sum(times) > target_s / 2) \
-                or sum(times) > target_s:
+        if len(times) >= max_runs or (len(times) >= min_runs and sum(times) > budget_s):
             break
-    reps = len(times)
+    return float(np.median(times)), len(times)
+
+
+def _dev_normal(vm, torch, shape, seed, scale=1.0):
+    t = torch.empty(shape, dtype=torch.bfloat16, device="cuda")
+    vm.fill_normal_(t, seed, scale=scale)
+    return t
+
+
+def cpu_baseline(vm, torch):
+    """The fp32 C oracle (oracle/, test infrastructure) timed on this host's cores
+    for every BASELINE config, on the same seeded inputs as the GPU legs (generated
+    on the device by the same generator and copied to host memory):
+      config 1, 3: one decode step (median of repeated steps);
+      config 4: 8 consecutive decode steps at 131072.. (per-step median);
+      config 2, 5: the whole prefill problem, median of 3 runs (7 for config 2).
+    Decode figures are GB/s of the same algorithmic bytes as the GPU legs, prefill
+    figures TFLOP/s of the same algorithmic FLOP."""
+    import oracle
+    threads = oracle.threads_env()
+    res = {}
+
+    def hb(t):
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+    # ---- config 2: the headline (whole problem)
+    T = 4096
+    qkv = hb(_dev_normal(vm, torch, (1, T, S, D), 203))
+    qw, kw = hb(_dev_normal(vm, torch, (D,), 201, 0.05)), hb(_dev_normal(vm, torch, (D,), 202, 0.05))
+    zero = np.zeros((1, HK, T, D), np.uint16)
+    c, s = oracle.rope_tables(HALF, T, THETA)
+    one = np.zeros(1, np.int32)
+    dt, n = _median_time(lambda: oracle.gated_prefill(
+        qkv, zero, zero, one, np.full(1, T, np.int32), qw, kw, c, s, Hq=HQ, Hk=HK, eps=EPS,
+        w_offset=1.0, nthreads=threads), 3, 7, 12.0)
+    fl = prefill_flops(T)
+    res["config2"] = {"tflops": fl / dt / 1e12, "s_per_step": dt, "runs": n,
+                      "sample": f"the whole config2 problem ({fl / 1e9:.1f} GFLOP)"}
+    del qkv, zero
+
+    # ---- config 1: B=1 at 512 (bench_decode1's draws)
+    ctx, L = 512, 512
+    qw1, kw1 = hb(_dev_normal(vm, torch, (D,), 101, 0.05)), hb(_dev_normal(vm, torch, (D,), 102, 0.05))
+    kc, vc = hb(_dev_normal(vm, torch, (1, HK, ctx, D), 103)), hb(_dev_normal(vm, torch, (1, HK, ctx, D), 104))
+    q1 = hb(_dev_normal(vm, torch, (1, S, D), 105))
+    c, s = oracle.rope_tables(HALF, ctx, THETA)
+    dt, n = _median_time(lambda: oracle.gated_decode(
+        q1, kc, vc, np.array([L], np.int32), qw1, kw1, c, s, Hq=HQ, Hk=HK, eps=EPS, w_offset=1.0,
+        nthreads=threads), 20, 2000, 1.0)
+    nb = decode_bytes([L])
+    res["config1"] = {"gbs": nb / dt / 1e9, "us_per_step": 1e6 * dt, "runs": n,
+                      "sample": "one decode step, B=1 at attended length 512"}
+
+    # ---- config 3: B=32 ragged (bench_decode3's draws), one whole step
+    B, ctx = 32, 32768
+    lengths = np.random.default_rng(3).integers(1024, 32769, size=B).astype(np.int32)
+    qw3, kw3 = hb(_dev_normal(vm, torch, (D,), 301, 0.05)), hb(_dev_normal(vm, torch, (D,), 302, 0.05))
+    kc = hb(_dev_normal(vm, torch, (B, HK, ctx, D), 303))
+    vc = hb(_dev_normal(vm, torch, (B, HK, ctx, D), 304))
+    q3 = hb(_dev_normal(vm, torch, (B, S, D), 305))
+    torch.cuda.empty_cache()
+    c, s = oracle.rope_tables(HALF, ctx, THETA)
+    dt, n = _median_time(lambda: oracle.gated_decode(
+        q3, kc, vc, lengths, qw3, kw3, c, s, Hq=HQ, Hk=HK, eps=EPS, w_offset=1.0,
+        nthreads=threads), 3, 5, 8.0)
+    nb = decode_bytes(lengths)
+    res["config3"] = {"gbs": nb / dt / 1e9, "ms_per_step": 1e3 * dt, "runs": n,
+                      "sample": f"one whole decode step, B=32, sum of lengths {int(lengths.sum())}"}
+    del kc, vc
+
+    # ---- config 4: B=1 at 131072.. (bench_decode4's draws), 8 consecutive steps
+    p0, ctx = 131072, 131072 + 256
+    qw4, kw4 = hb(_dev_normal(vm, torch, (D,), 401, 0.05)), hb(_dev_normal(vm, torch, (D,), 402, 0.05))
+    kc = hb(_dev_normal(vm, torch, (1, HK, ctx, D), 403))
+    vc = hb(_dev_normal(vm, torch, (1, HK, ctx, D), 404))
+    q4 = hb(_dev_normal(vm, torch, (1, S, D), 405))
+    torch.cuda.empty_cache()
+    c, s = oracle.rope_tables(HALF, ctx, THETA)
+    times = []
+    for i in range(8):
+        t0 = time.perf_counter()
+        oracle.gated_decode(q4, kc, vc, np.array([p0 + i], np.int32), qw4, kw4, c, s, Hq=HQ,
+                            Hk=HK, eps=EPS, w_offset=1.0, nthreads=threads)
+        times.append(time.perf_counter() - t0)
     dt = float(np.median(times))
-    rows = np.arange(0, T, step)
-    flops = 4.0 * D * HQ * float(np.sum(rows + 1))
-    what = (f"the whole config2 problem (all {T} rows, 16 heads" if step == 1 else
-            f"config2 query rows t = 0, {step}, 2*{step}, ... (all 16 heads; {len(rows)} of {T} rows")
-    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{what}, {flops / 1e9:.1f} GFLOP): median of {reps} runs = {dt:.3f} s "
-                      f"with {threads} OpenMP threads of the fp32 C oracle"}
+    nb = decode_bytes([p0 + 4])
+    res["config4"] = {"gbs": nb / dt / 1e9, "ms_per_step": 1e3 * dt, "runs": 8,
+                      "sample": "8 consecutive decode steps at attended lengths 131072..131079 "
+                                "(median per step)"}
+    del kc, vc
+
+    # ---- config 5: ragged chunked prefill (bench_prefill5's draws), whole problem
+    seed = 5
+    rng = np.random.default_rng(seed)
+    qlen = rng.permutation(np.array([512, 1024, 2048, 2048], np.int32)).astype(np.int32)
+    prior = rng.integers(8192, 32769, size=4).astype(np.int32)
+    B, T = 4, int(qlen.max())
+    ctx = int((prior + qlen).max())
+    qw5, kw5 = hb(_dev_normal(vm, torch, (D,), seed * 100 + 1, 0.05)), hb(_dev_normal(vm, torch, (D,), seed * 100 + 2, 0.05))
+    kc = hb(_dev_normal(vm, torch, (B, HK, ctx, D), seed * 100 + 3))
+    vc = hb(_dev_normal(vm, torch, (B, HK, ctx, D), seed * 100 + 4))
+    q5 = hb(_dev_normal(vm, torch, (B, T, S, D), seed * 100 + 5))
+    torch.cuda.empty_cache()
+    c, s = oracle.rope_tables(HALF, ctx, THETA)
+    dt, n = _median_time(lambda: oracle.gated_prefill(
+        q5, kc, vc, prior, qlen, qw5, kw5, c, s, Hq=HQ, Hk=HK, eps=EPS, w_offset=1.0,
+        nthreads=threads), 3, 3, 30.0)
+    cc, pp = qlen.astype(np.float64), prior.astype(np.float64)
+    fl = float(4 * D * HQ * np.sum(cc * pp + cc * (cc + 1) / 2))
+    res["config5"] = {"tflops": fl / dt / 1e12, "s_per_step": dt, "runs": n,
+                      "sample": f"the whole config5 problem ({fl / 1e12:.2f} TFLOP)"}
+    del kc, vc
+
+    info = cpu_info()
+    c2 = res["config2"]
+    return {"value": c2["tflops"], "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{c2['sample']}: median of {c2['runs']} runs = {c2['s_per_step']:.3f} s with "
+                      f"{threads} OpenMP threads of the fp32 C oracle; every config in 'configs'",
+            "cpu_model": info["cpu_model"], "physical_cores": info["physical_cores"],
+            "logical_cpus": info["logical_cpus"], "threads": threads, "configs": res}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # defaults: ~50 ms of untimed prefill steps first, so the timed ones run at
-    # the GPU's settled clocks (a cold start runs the first tens of ms slower)
-    ap.add_argument("--steps", type=int, default=300)
-    ap.add_argument("--warmup", type=int, default=300)
+    # untimed steps before the timed ones: --warmup steps, then a time-sized
+    # clock-settle phase (settle_clocks) whose length the JSON line reports
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-settle", action="store_true",
+                    help="skip the clock-settle phase (counter-collection runs)")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--calib-copy", action="store_true",
@@ -395,7 +548,8 @@ def main():
     pf = None
     if not args.no_prefill:
         log("[bench] prefill config2 T=4096")
-        pf = bench_prefill(vm, torch, args.steps, args.warmup)
+        pf = bench_prefill(vm, torch, args.steps, args.warmup, settle=not args.no_settle)
+        log(f"[bench] settle: {pf['settle']}")
         log(f"[bench] prefill: {pf['ms_per_step']:.3f} ms/step, {pf['tflops']:.1f} TFLOP/s, "
             f"attn kernel {pf['attn_kernel_ms']:.3f} ms, "
             f"K/V append + V^T staging {pf['append_vt_kernel_ms']:.4f} ms")
@@ -423,9 +577,11 @@ def main():
         decode = {"config3": d3, "config4": d4, "config1": d1, "peak_GBs": PEAK_HBM_GBS}
     cpu = None
     if not args.no_cpu:
-        log("[bench] cpu baseline (oracle)")
-        cpu = cpu_baseline()
-        log(f"[bench] cpu: {cpu['value']:.4f} TFLOP/s ({cpu['sample']})")
+        log("[bench] cpu baseline (oracle), configs 1-5")
+        cpu = cpu_baseline(vm, torch)
+        for k, v in sorted(cpu["configs"].items()):
+            fig = f"{v['tflops']:.4f} TFLOP/s" if "tflops" in v else f"{v['gbs']:.1f} GB/s"
+            log(f"[bench] cpu {k}: {fig} ({v['sample']}, {v['runs']} runs)")
 
     if pf is None:
         print(json.dumps({"decode": decode, "cpu_baseline": cpu}), flush=True)
@@ -439,6 +595,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(pf["ms_per_step"], 4),
+        "settle_ms": pf["settle"]["settle_ms"],
+        "settle_steps": pf["settle"]["settle_steps"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

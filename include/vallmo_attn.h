@@ -58,8 +58,7 @@ enum {
   VM_K_DECODE_COMBINE = 2,/* LSE merge (+ gate)                              */
   VM_K_PREFILL = 3,       /* flash attention (prefill)                       */
   VM_K_ADVANCE = 4,       /* device clock                                    */
-  VM_K_TRANSPOSE = 5,     /* reserved (V^T staging is counted as VM_K_ROWS)  */
-  VM_K_COUNT = 6
+  VM_K_COUNT = 5
 };
 int vm_profile_enable(int on);
 int vm_profile_read(int kernel, int* count, double* total_ms);
@@ -212,7 +211,9 @@ int vm_prefill_q_norm_rope(vm_bf16* q_out, int64_t q_st, int64_t q_sh, int64_t q
  * epilogue applies the sigmoid gate (a10) and writes out :: (D*Hq, T, B) —
  * the Wo input layout, token stride out_st, batch stride out_sb.
  * Attends cache columns 1..prior[b]+q_len[b] of each sequence (prior NULL:
- * no prior tokens). scratch (device, 256-byte aligned) is a workspace of at
+ * no prior tokens). Contract: prior[b] + q_len[b] <= ctx (the reference's
+ * cache view throws a BoundsError past it, src/llm/qwen35.jl:306); device-side
+ * values are not read on the host, so keys past ctx are masked instead. scratch (device, 256-byte aligned) is a workspace of at
  * least vm_prefill_scratch_bytes(B, Hk, D, ctx) bytes: the attended V is staged
  * there transposed for the attention kernel. Its contents are not preserved
  * (the role of the reference's arena scratch, attention_decode.jl:183-200).  */

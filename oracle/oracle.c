@@ -182,6 +182,11 @@ void orc_gated_decode(const uint16_t* qkv, const uint16_t* kc, const uint16_t* v
   /* new K/V rows first (knorm_rope_append!) */
   for (int b = 0; b < B; ++b) {
     const int64_t pos = positions[b] - 1;
+    if (pos < 0) { /* no new token: nothing is appended (rows returned as NaN) */
+      for (size_t i = (size_t)b * Hk * D; i < (size_t)(b + 1) * Hk * D; ++i)
+        knew[i] = vnew[i] = NAN;
+      continue;
+    }
     for (int j = 0; j < Hk; ++j) {
       float x[1024];
       const uint16_t* kr = qkv + ((size_t)b * S + 2 * Hq + j) * D;
@@ -192,41 +197,79 @@ void orc_gated_decode(const uint16_t* qkv, const uint16_t* kc, const uint16_t* v
       for (int d = 0; d < D; ++d) vnew[((size_t)b * Hk + j) * D + d] = bf(vr[d]);
     }
   }
-#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+  /* attention per (b, kv head): the group's G query heads share the fp32 copy
+   * of the attended rows; the token loops run in parallel (one sequence may
+   * hold all the work) */
+  float* qn = (float*)malloc(sizeof(float) * (size_t)G * D);
+  float* o = (float*)malloc(sizeof(float) * (size_t)G * D);
   for (int b = 0; b < B; ++b)
-    for (int h = 0; h < Hq; ++h) {
+    for (int hk = 0; hk < Hk; ++hk) {
       const int64_t len = positions[b];
-      const int hk = h / G;
-      float x[1024], qn[1024], o[1024];
-      const uint16_t* qr = qkv + ((size_t)b * S + 2 * h) * D;
-      const uint16_t* gr = qkv + ((size_t)b * S + 2 * h + 1) * D;
-      for (int d = 0; d < D; ++d) x[d] = bf(qr[d]);
-      orc_head_norm_rope(x, qwf, eps, w_off, cos_tab, sin_tab, len - 1, D, half, qn);
-      float* s_buf = (float*)malloc(sizeof(float) * (size_t)len);
+      if (len <= 0) { /* no key: o = 0 (attention_decode.jl:126-128) */
+        for (int g = 0; g < G; ++g)
+          for (int d = 0; d < D; ++d) out[((size_t)b * Hq + hk * G + g) * D + d] = 0.f;
+        continue;
+      }
       float* krow = (float*)malloc(sizeof(float) * (size_t)len * D);
       float* vrow = (float*)malloc(sizeof(float) * (size_t)len * D);
-      const float** kp = (const float**)malloc(sizeof(float*) * (size_t)len);
-      const float** vp = (const float**)malloc(sizeof(float*) * (size_t)len);
+      float* s_buf = (float*)malloc(sizeof(float) * (size_t)len * G);
       const uint16_t* kb = kc + ((size_t)b * Hk + hk) * (size_t)ctx * D;
       const uint16_t* vb = vc + ((size_t)b * Hk + hk) * (size_t)ctx * D;
-      for (int64_t u = 0; u + 1 < len; ++u) {
+#pragma omp parallel for schedule(static)
+      for (int64_t u = 0; u < len; ++u) {
+        const float* kn = knew + ((size_t)b * Hk + hk) * D;
+        const float* vn = vnew + ((size_t)b * Hk + hk) * D;
         for (int d = 0; d < D; ++d) {
-          krow[u * D + d] = bf(kb[u * D + d]);
-          vrow[u * D + d] = bf(vb[u * D + d]);
+          krow[u * D + d] = u + 1 < len ? bf(kb[u * D + d]) : kn[d];
+          vrow[u * D + d] = u + 1 < len ? bf(vb[u * D + d]) : vn[d];
         }
-        kp[u] = krow + u * D;
-        vp[u] = vrow + u * D;
       }
-      kp[len - 1] = knew + ((size_t)b * Hk + hk) * D;
-      vp[len - 1] = vnew + ((size_t)b * Hk + hk) * D;
-      attend_row(qn, kp, vp, len, D, scale, s_buf, o);
-      for (int d = 0; d < D; ++d) out[((size_t)b * Hq + h) * D + d] = o[d] * sigmoid_f(bf(gr[d]));
-      free(s_buf);
+      for (int g = 0; g < G; ++g) {
+        float x[1024];
+        const uint16_t* qr = qkv + ((size_t)b * S + 2 * (hk * G + g)) * D;
+        for (int d = 0; d < D; ++d) x[d] = bf(qr[d]);
+        orc_head_norm_rope(x, qwf, eps, w_off, cos_tab, sin_tab, len - 1, D, half, qn + g * D);
+      }
+      /* scores, then the softmax max, then p and o = sum_u p_u v_u / l */
+#pragma omp parallel for schedule(static)
+      for (int64_t u = 0; u < len; ++u)
+        for (int g = 0; g < G; ++g) {
+          float acc = 0.f;
+          for (int d = 0; d < D; ++d) acc += qn[g * D + d] * krow[u * D + d];
+          s_buf[u * G + g] = acc * scale;
+        }
+      for (int g = 0; g < G; ++g) {
+        float m = -INFINITY, l = 0.f;
+        for (int64_t u = 0; u < len; ++u) m = s_buf[u * G + g] > m ? s_buf[u * G + g] : m;
+        for (int d = 0; d < D; ++d) o[g * D + d] = 0.f;
+#pragma omp parallel
+        {
+          float* op = (float*)calloc((size_t)D, sizeof(float));
+          float lp = 0.f;
+#pragma omp for schedule(static)
+          for (int64_t u = 0; u < len; ++u) {
+            const float p = expf(s_buf[u * G + g] - m);
+            lp += p;
+            for (int d = 0; d < D; ++d) op[d] += p * vrow[u * D + d];
+          }
+#pragma omp critical
+          {
+            l += lp;
+            for (int d = 0; d < D; ++d) o[g * D + d] += op[d];
+          }
+          free(op);
+        }
+        const float inv = 1.0f / l;
+        const uint16_t* gr = qkv + ((size_t)b * S + 2 * (hk * G + g) + 1) * D;
+        for (int d = 0; d < D; ++d)
+          out[((size_t)b * Hq + hk * G + g) * D + d] = o[g * D + d] * inv * sigmoid_f(bf(gr[d]));
+      }
       free(krow);
       free(vrow);
-      free(kp);
-      free(vp);
+      free(s_buf);
     }
+  free(qn);
+  free(o);
   free(qwf);
   free(kwf);
 }

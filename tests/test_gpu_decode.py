@@ -11,15 +11,17 @@ import torch
 
 from conftest import (D, EPS, HALF, HK, HQ, S, THETA, TOL_MAX, TOL_MEAN, banner, dev_f32,
                       from_dev, i32, maxmean, to_dev)
-from oracle.rng import bf16_to_f32, normal_bf16
+from oracle.rng import bf16_to_f32, f32_to_bf16, normal_bf16
 
 pytestmark = pytest.mark.gpu
 
 
-def make_layer(vm, B, ctx, Hq=HQ, Hk=HK, seed=0, n_splits=0, caches=None):
+def make_layer(vm, B, ctx, Hq=HQ, Hk=HK, seed=0, n_splits=0, caches=None, kw_big=None):
     cfg = vm.AttnConfig(Hq=Hq, Hkv=Hk, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
     qw = normal_bf16((D,), seed + 1, scale=0.05)
     kw = normal_bf16((D,), seed + 2, scale=0.05)
+    if kw_big is not None:
+        kw[0] = f32_to_bf16(np.array([kw_big], np.float32))[0]
     if caches is None:
         kc = normal_bf16((B, Hk, ctx, D), seed + 3)
         vc = normal_bf16((B, Hk, ctx, D), seed + 4)
@@ -31,9 +33,9 @@ def make_layer(vm, B, ctx, Hq=HQ, Hk=HK, seed=0, n_splits=0, caches=None):
     return cfg, m, layer, qw, kw
 
 
-def run_decode_vs_oracle(vm, orc, B, ctx, pos, Hq=HQ, Hk=HK, seed=0, n_splits=0):
+def run_decode_vs_oracle(vm, orc, B, ctx, pos, Hq=HQ, Hk=HK, seed=0, n_splits=0, kw_big=None):
     S_ = 2 * Hq + 2 * Hk
-    cfg, m, layer, qw, kw = make_layer(vm, B, ctx, Hq, Hk, seed, n_splits)
+    cfg, m, layer, qw, kw = make_layer(vm, B, ctx, Hq, Hk, seed, n_splits, kw_big=kw_big)
     kc, vc = from_dev(layer.K_cache), from_dev(layer.V_cache)
     qkv = normal_bf16((B, S_, D), seed + 5)
     gen = vm.Generation(B)
@@ -48,8 +50,12 @@ def run_decode_vs_oracle(vm, orc, B, ctx, pos, Hq=HQ, Hk=HK, seed=0, n_splits=0)
     mx, mn = maxmean(got, ref)
     kg, vg = from_dev(layer.K_cache), from_dev(layer.V_cache)
     cols = np.asarray(pos) - 1
-    kmx, kmn = maxmean(np.stack([bf16_to_f32(kg[b, :, cols[b]]) for b in range(B)]), kn)
-    vexact = all(np.array_equal(bf16_to_f32(vg[b, :, cols[b]]), vn[b]) for b in range(B))
+    live = [b for b in range(B) if cols[b] >= 0]   # position 0: no token appended
+    kmx, kmn = (maxmean(np.stack([bf16_to_f32(kg[b, :, cols[b]]) for b in live]), kn[live])
+                if live else (0.0, 0.0))
+    vexact = all(np.array_equal(bf16_to_f32(vg[b, :, cols[b]]), vn[b]) for b in live)
+    vexact &= all(np.array_equal(kg[b], kc[b]) and np.array_equal(vg[b], vc[b])
+                  for b in range(B) if cols[b] < 0)
     return (mx, mn), (kmx, kmn), vexact, got, ref
 
 
@@ -76,6 +82,49 @@ def test_gqa_groups(vm, orc, Hq, Hk):
     (mx, mn), _, vexact, _, _ = run_decode_vs_oracle(vm, orc, 2, 640, [640, 77], Hq=Hq, Hk=Hk,
                                                      seed=300)
     assert mx <= TOL_MAX and mn <= TOL_MEAN and vexact
+
+
+def test_fused_decode_running_max_path(vm, orc):
+    """A norm weight of 4 (|kw + 1| = 5) lifts the QK-norm logit bound past the
+    static limit of 64 (log2 units), so the fused decode takes its running-max
+    path (appended row first, from m = -inf); checked against the oracle."""
+    banner("fused decode running-max path (kw[0] = 4)")
+    (mx, mn), (kmx, kmn), vexact, _, _ = run_decode_vs_oracle(
+        vm, orc, 4, 2048, [2048, 1, 700, 1500], seed=250, kw_big=4.0)
+    print(f"running-max decode: out max {mx:.3e} mean {mn:.3e}; K max {kmx:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN and kmx <= TOL_MAX and kmn <= TOL_MEAN and vexact
+
+
+def test_fused_decode_zero_position(vm, orc):
+    """positions[b] = 0 in a batch: that sequence attends no key, so its output is
+    0 (attention_decode.jl:114-128) and its cache is not written; the others are
+    unaffected. A whole batch at 0 gives all zeros."""
+    banner("fused decode with zero positions")
+    (mx, mn), (kmx, _), ok, got, _ = run_decode_vs_oracle(vm, orc, 4, 1024, [0, 513, 0, 1024],
+                                                          seed=260)
+    assert np.all(got[0] == 0.0) and np.all(got[2] == 0.0)
+    assert mx <= TOL_MAX and mn <= TOL_MEAN and kmx <= TOL_MAX and ok
+    _, _, ok, got, _ = run_decode_vs_oracle(vm, orc, 2, 256, [0, 0], seed=270)
+    assert np.all(got == 0.0) and ok
+
+
+def test_decode_attention_zero_length(vm, orc):
+    """decode_attention! with lengths[b] = 0: o = 0 for that sequence (the empty-split
+    guards, attention_decode.jl:80-82, 114-128); the rest match the oracle."""
+    banner("decode_attention_ zero lengths")
+    B, H, Hk, ctx = 4, 16, 4, 1024
+    q_bits = normal_bf16((B, H, D), 511)
+    kc, vc = normal_bf16((B, Hk, ctx, D), 512), normal_bf16((B, Hk, ctx, D), 513)
+    lengths = np.array([0, 700, 0, 1], np.int32)
+    out = vm.decode_attention(to_dev(q_bits), to_dev(kc), to_dev(vc), lengths=i32(lengths))["O"]
+    torch.cuda.synchronize()
+    got = dev_f32(out)
+    ref = orc.attention(bf16_to_f32(q_bits).reshape(B, H, 1, D), bf16_to_f32(kc).reshape(kc.shape),
+                        bf16_to_f32(vc).reshape(vc.shape), causal=False, k_lengths=lengths)[:, :, 0]
+    assert np.all(ref[[0, 2]] == 0.0)
+    assert np.all(got[0] == 0.0) and np.all(got[2] == 0.0)
+    mx, mn = maxmean(got, ref)
+    assert mx <= TOL_MAX and mn <= TOL_MEAN
 
 
 def test_split_count_invariance(vm, orc):
@@ -145,10 +194,11 @@ def test_config3_batched_decode_full_size(vm, orc):
 
 def test_config4_graph_replay_matches_eager(vm, orc):
     """one decode step (append, split-K, merge, gate, advance)
-    captured once in a hipGraph; replays advance the device clock. 8 replays
-    equal 8 eager steps bit for bit, and the last step matches the oracle."""
-    banner("config4 graph replay B=1 ctx=131328")
-    B, ctx, p0, n = 1, 131328, 131072, 8
+    captured once in a hipGraph; replays advance the device clock. 256 replays
+    (positions 131072..131327) equal 256 eager steps bit for bit (outputs and the
+    256 appended cache rows), and the last step matches the oracle."""
+    banner("config4 graph replay B=1 ctx=131328, 256 replays")
+    B, ctx, p0, n = 1, 131328, 131072, 256
     K = torch.empty((B, HK, ctx, D), dtype=torch.bfloat16, device="cuda")
     V = torch.empty_like(K)
     vm.fill_normal_(K, 4001)
@@ -167,7 +217,7 @@ def test_config4_graph_replay_matches_eager(vm, orc):
         eager.append(O.clone())
     torch.cuda.synchronize()
     assert gen.positions.item() == p0 + n
-    K_eager = K.clone()
+    K_eager, V_eager = K.clone(), V.clone()
 
     K.copy_(K0)
     V.copy_(V0)
@@ -184,8 +234,8 @@ def test_config4_graph_replay_matches_eager(vm, orc):
     assert gen.positions.item() == p0 + n
     for a, b in zip(eager, replay):
         assert torch.equal(a, b)
-    assert torch.equal(K_eager, K)
-    # oracle on the last step (its cache holds the 7 rows appended before it)
+    assert torch.equal(K_eager, K) and torch.equal(V_eager, V)
+    # oracle on the last step (its cache holds the 255 rows appended before it)
     c, s = orc.rope_tables(HALF, ctx, THETA)
     kc, vc = from_dev(K), from_dev(V)
     ref, _, _ = orc.gated_decode(qkv_bits, kc, vc, np.array([p0 + n - 1], np.int32), qw, kw, c, s,

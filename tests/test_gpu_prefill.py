@@ -259,3 +259,66 @@ def test_fused_prefill_online_max_path(vm, orc):
     mx, mn = maxmean(got[fin], ref[fin])
     print(f"online-max path: out max {mx:.3e} mean {mn:.3e}")
     assert mx <= TOL_MAX and mn <= TOL_MEAN
+
+
+def test_attention_zero_k_length(vm, orc):
+    """attention! with k_lengths[b] = 0: no key is valid, so every row of that
+    sequence is 0 (the l == 0 guard, attention.jl:86), causal or not; a sequence
+    with q_lengths[b] = 0 is not written at all; the rest match the oracle."""
+    B, H, Hk, L, Lk = 3, 16, 4, 96, 256
+    q = normal_bf16((B, H, L, D), 31)
+    k = normal_bf16((B, Hk, Lk, D), 32)
+    v = normal_bf16((B, Hk, Lk, D), 33)
+    kl = np.array([0, 200, 0], np.int32)
+    ql = np.array([96, 96, 0], np.int32)
+    for causal in (False, True):
+        banner(f"attention_ zero k_length causal={causal}")
+        O = torch.full((B, H, L, D), 7.0, dtype=torch.bfloat16, device="cuda")
+        vm.attention_({"O": O}, to_dev(q), to_dev(k), to_dev(v), causal=causal,
+                      k_lengths=i32(kl), q_lengths=i32(ql))
+        torch.cuda.synchronize()
+        got = dev_f32(O)
+        assert np.all(got[0] == 0.0)
+        assert np.all(got[2] == 7.0)
+        ref = orc.attention(bf16_to_f32(q).reshape(q.shape), bf16_to_f32(k).reshape(k.shape),
+                            bf16_to_f32(v).reshape(v.shape), causal=causal, k_lengths=kl,
+                            q_lengths=ql)
+        assert np.all(ref[0] == 0.0)
+        mx, mn = maxmean(got[1], ref[1])
+        assert mx <= TOL_MAX and mn <= TOL_MEAN
+
+
+def test_prefill_q_norm_rope_operator(vm, orc):
+    """vm_prefill_q_norm_rope (the unfused prefill prologue for attention!,
+    qwen35.jl:297-304): per-head RMSNorm (w + 1) and partial RoPE of q read from
+    the packed projection, at position prior[b] + t, into Q :: (D, T, Hq, B);
+    rows t >= q_lengths[b] are not written."""
+    banner("vm_prefill_q_norm_rope ragged")
+    B, T, ctx = 2, 150, 1024
+    prior = np.array([0, 700], np.int32)
+    qlen = np.array([150, 61], np.int32)
+    qw = normal_bf16((D,), 121, scale=0.05)
+    qkv = normal_bf16((B, T, S, D), 122)
+    cos = torch.empty((ctx, HALF), dtype=torch.float32, device="cuda")
+    sin = torch.empty_like(cos)
+    vm._lib.call("vm_rope_tables", cos.data_ptr(), sin.data_ptr(), HALF, ctx, THETA, None)
+    Q = torch.full((B, HQ, T, D), 7.0, dtype=torch.bfloat16, device="cuda")
+    dq, dqw, pr, ql = to_dev(qkv), to_dev(qw), i32(prior), i32(qlen)
+    vm._lib.call("vm_prefill_q_norm_rope", Q.data_ptr(), Q.stride(2), Q.stride(1), Q.stride(0),
+                 dq.data_ptr(), S * D, T * S * D, dqw.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                 pr.data_ptr(), ql.data_ptr(), B, T, HQ, HK, D, HALF, EPS, 1.0, None)
+    torch.cuda.synchronize()
+    got = dev_f32(Q)
+    c, s = orc.rope_tables(HALF, ctx, THETA)
+    wf = bf16_to_f32(qw)
+    ref = np.full((B, HQ, T, D), np.nan, np.float32)
+    for b in range(B):
+        for t in range(int(qlen[b])):
+            for h in range(HQ):
+                x = bf16_to_f32(qkv[b, t, 2 * h])
+                ref[b, h, t] = orc.head_norm_rope(x, wf, EPS, 1.0, c, s, int(prior[b]) + t)
+    fin = ~np.isnan(ref)
+    mx, mn = maxmean(got[fin], ref[fin])
+    print(f"prefill q norm+rope: max {mx:.3e} mean {mn:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN
+    assert np.all(got[~fin] == 7.0)

@@ -8,7 +8,8 @@ src/llm/qwen35.jl, src/llm/generate.jl) over that ABI.
 The directory name is not a Python identifier; load it with
 ``__graft_entry__.load_package()`` (registered as module ``vallmo_amd``).
 """
-from ._lib import (ArgumentError, DimensionMismatch, HIPError, UnsupportedShape,  # noqa: F401
+from ._lib import (ArgumentError, BoundsError, DimensionMismatch, HIPError,  # noqa: F401
+                   UnsupportedShape,
                    LIB_PATH, EXPORTED)
 from .sizes import sizes  # noqa: F401
 from .ops import (attention, attention_, decode_attention, decode_attention_,  # noqa: F401

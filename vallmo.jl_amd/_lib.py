@@ -18,7 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent / "csrc" / "libvallmo_attn.so"
 
 VM_E_ARG, VM_E_DIM, VM_E_UNSUPPORTED, VM_E_SCRATCH = -1, -2, -3, -4
 # kernel classes of vm_profile_read
-VM_K_ROWS, VM_K_DECODE_SPLIT, VM_K_DECODE_COMBINE, VM_K_PREFILL, VM_K_ADVANCE, VM_K_TRANSPOSE = range(6)
+VM_K_ROWS, VM_K_DECODE_SPLIT, VM_K_DECODE_COMBINE, VM_K_PREFILL, VM_K_ADVANCE = range(5)
 
 
 class DimensionMismatch(ValueError):
@@ -27,6 +27,10 @@ class DimensionMismatch(ValueError):
 
 class ArgumentError(ValueError):
     """Invalid argument (Julia's Base.ArgumentError)."""
+
+
+class BoundsError(IndexError):
+    """Out-of-range index (Julia's Base.BoundsError)."""
 
 
 class UnsupportedShape(ArgumentError):

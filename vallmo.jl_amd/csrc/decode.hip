@@ -12,19 +12,24 @@
 //
 // Per wave, 16-token steps on bf16 MFMA with the GQA group (G <= 8 query heads
 // sharing hk) on the N = 16 side, so each K/V byte is read from HBM once:
-//   S^T[tok][head] = K[tok][:] . Q[head][:]    16x16x32; A = K straight from HBM
-//                                                (16 B per lane), B = Q in registers
+//   S^T[tok][head] = K[tok][:] . Q[head][:]    16x16x32; A = K fragment, B = Q
+//                                                in registers
 //   O^T[d][head]  += V^T[d][tok] . P^T[tok][head]   16x16x16
 // S^T already sits in the lanes/slots of the P^T operand. V^T comes from the
 // natural-layout V fragments through a 16x16x32 MFMA against a 0/1 selection
-// matrix (bf16 * 1.0 plus exact zeros is exact in fp32), so no LDS is used.
-// K/V fragments are triple-buffered in registers (one wave per SIMD): steps
-// i+1 and i+2 are in flight while step i computes.
+// matrix (bf16 * 1.0 plus exact zeros is exact in fp32).
+// K/V rows stream through a per-wave LDS ring of two 16-token slots, filled by
+// direct global->LDS loads (non-temporal, 1 KB contiguous per instruction, no
+// VGPR staging): the issue side runs one slot ahead of the compute side, across
+// segment boundaries, so a wave always has up to 32 KB of K/V in flight. Each
+// landed slot is read into registers (b128, rows XOR-swizzled) and refilled at
+// once. One wave per SIMD; the four waves of a workgroup share nothing.
 //
 // Softmax: with QK-norm the logits are bounded, |s| <= |q~| * sqrt(D) *
-// max|kw + w_offset|, so the fused path uses that bound as a fixed per-head
-// shift when it is <= 64 (log2 units); otherwise, and for the unfused operator,
-// a running max rescaled lazily (only when it grows by > 8).
+// max|kw + w_offset|, so when that bound is <= 64 (log2 units) the fused path
+// takes p = exp2(s) unshifted (p within 2^+-64, the merge's 1/l cancels the
+// common scale); otherwise, and for the unfused operator, a running max
+// rescaled lazily (only when it grows by > 8).
 #include "common.h"
 #include "kernels.h"
 
@@ -114,7 +119,8 @@ __device__ __forceinline__ void read_step(StepBuf& s, const uint16_t* lk, const 
 
 __device__ __forceinline__ void compute_step(StepBuf& s, int t, int hi, int n, int g,
                                              const uint4 (&qop)[8], const uint4 (&sel)[2],
-                                             f32x4 (&acc)[16], float& m_run, float& l_part) {
+                                             f32x4 (&acc)[16], float& m_run, float& l_part,
+                                             bool dyn) {
   if (t + DSTEP > hi && t + n >= hi) {
     // rows past the range may hold anything: p = 0 must meet finite v
 #pragma unroll
@@ -127,21 +133,25 @@ __device__ __forceinline__ void compute_step(StepBuf& s, int t, int hi, int n, i
 #pragma unroll
     for (int j = 0; j < 4; ++j) sc[j] = (t + 4 * g + j < hi) ? sc[j] : -INFINITY;
   }
-  // running max in log2 units, rescaled lazily: only when it grows by more
-  // than D_RESCALE_SLACK (never, when m_run starts at the QK-norm bound)
-  float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-  mx = wave_max_xor(mx, 16);
-  mx = wave_max_xor(mx, 32) * LOG2E;
-  const float m_new = fmaxf(m_run, mx);  // finite: token t is valid
-  const bool need = m_new > m_run + D_RESCALE_SLACK;
-  if (__ballot(need) != 0ull) {
-    const float m_use = need ? m_new : m_run;
-    const float alpha = (m_use == m_run) ? 1.0f : fast_exp2(m_run - m_use);
-    l_part *= alpha;
+  if (dyn) {
+    // running max in log2 units, rescaled lazily: only when it grows by more
+    // than D_RESCALE_SLACK (wave-uniform branch)
+    float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    mx = wave_max_xor(mx, 16);
+    mx = wave_max_xor(mx, 32) * LOG2E;
+    const float m_new = fmaxf(m_run, mx);  // finite: token t is valid
+    const bool need = m_new > m_run + D_RESCALE_SLACK;
+    if (__ballot(need) != 0ull) {
+      const float m_use = need ? m_new : m_run;
+      const float alpha = (m_use == m_run) ? 1.0f : fast_exp2(m_run - m_use);
+      l_part *= alpha;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] *= alpha;
-    m_run = m_use;
+      for (int i = 0; i < 16; ++i) acc[i] *= alpha;
+      m_run = m_use;
+    }
   }
+  // static mode: m_run = 0 and every |logit| <= 64 (log2 units), so p stays in
+  // [2^-64, 2^64] unshifted; the merge's 1/l cancels the common scale
   const float m_eff = m_run;
   float p[4];
 #pragma unroll
@@ -457,9 +467,14 @@ void decode_stream_kernel(DecodeArgs a) {
       qn2 += __shfl_xor(qn2, 32, 64);
     }
     float m_run = -INFINITY;
+    bool dyn = true;
     if (FUSED) {
+      // |logit| <= |q op| * |k~| (log2 units): within +-64 the shift is static
       const float bound = sqrtf(qn2) * 1.01f * kbound * LOG2E;
-      if (__ballot(n < G && !(bound <= D_STATIC_LIMIT)) == 0ull) m_run = bound;
+      if (__ballot(n < G && !(bound <= D_STATIC_LIMIT)) == 0ull) {
+        m_run = 0.f;
+        dyn = false;
+      }
     }
 
     // ---- stream tokens [lo, hm) of (b, hk)
@@ -472,7 +487,7 @@ void decode_stream_kernel(DecodeArgs a) {
       // that its loads overlap the K/V steps already in flight
       StepBuf sb;
       append_row(sb, a, cs.b, cs.hk, cs.hi - 1, n, g);
-      compute_step(sb, cs.hi - 1, cs.hi, n, g, qop, sel, acc, m_run, l_part);
+      compute_step(sb, cs.hi - 1, cs.hi, n, g, qop, sel, acc, m_run, l_part, dyn);
     }
     // one 16-token step from ring slot `slot` (inlined per slot: the two slots are
     // distinct LDS objects in the generated code)
@@ -485,7 +500,7 @@ void decode_stream_kernel(DecodeArgs a) {
       // the slot is free once its reads have returned; refill it
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       if (is.next(slot, a, gw1, last, lane, FUSED)) ++inflight;
-      compute_step(sb, ct, cs.hm, n, g, qop, sel, acc, m_run, l_part);
+      compute_step(sb, ct, cs.hm, n, g, qop, sel, acc, m_run, l_part, dyn);
       ct += DSTEP;
     };
     if (cslot == 1 && ct < cs.hm) {

@@ -68,11 +68,11 @@ struct CombineArgs {
 };
 
 struct PrefillArgs {
-  // q: normalised (QRAW = false) or the raw packed projection (QRAW = true)
+  // q: normalised (attention! operator) or the raw packed projection (fused path)
   const uint16_t* q;
   int64_t q_st, q_sh, q_sb;
-  const uint16_t* qw;
-  const uint16_t* kw;   // QRAW: bounds |k| for the static softmax max
+  const uint16_t* qw;   // fused path: q norm weight
+  const uint16_t* kw;   // fused path: bounds |k| for the static softmax shift
   const float* cos_tab;
   const float* sin_tab;
   float eps, w_offset;
@@ -81,7 +81,7 @@ struct PrefillArgs {
   int64_t kv_st, kv_sh, kv_sb;
   uint16_t* o;
   int64_t o_st, o_sh, o_sb;
-  const uint16_t* gate;   // GATE only
+  const uint16_t* gate;   // fused path: sigmoid gate logits
   int64_t g_st, g_sh, g_sb;
   const int32_t* k_lengths;  // nullable -> Lk
   const int32_t* q_lengths;  // nullable -> L
@@ -126,7 +126,7 @@ hipError_t launch_fill_normal(uint16_t* dst, int64_t n, uint64_t seed, float sca
                               hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, bool fused_q, hipStream_t st);
 hipError_t launch_combine(const CombineArgs& a, hipStream_t st);
-hipError_t launch_prefill(const PrefillArgs& a, bool qraw, bool gate, hipStream_t st);
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st);
 // fused gated prefill (q norm+RoPE prologue, sigmoid-gate epilogue), persistent
 // t0 / t1 (nullable): events stamped by the dispatch itself at the kernel's
 // start and end (hipExtLaunchKernelGGL), for timing without extra packets

@@ -1,7 +1,7 @@
 // prefill.hip — causal / non-causal GQA flash attention for prefill and chunked
-// prefill (the work of src/kernels/attention.jl:12-91, re-designed for CDNA4),
-// optionally fused with the q norm+RoPE prologue and the sigmoid-gate epilogue
-// of forward(::AttnLayer) (src/llm/qwen35.jl:292-318).
+// prefill: the attention! operator (src/kernels/attention.jl:12-129, re-designed
+// for CDNA4) on already-normalised q. The gated layer path with its fused
+// prologue and epilogue is prefill_fused.hip.
 //
 // Workgroup = 4 waves = 128 query rows of one (head, sequence); wave w owns 32
 // rows. Per 32-key tile, all on 32x32x16 bf16 MFMA with fp32 accumulate:
@@ -20,13 +20,11 @@
 // Rows are 512 B with the 16-byte chunks XOR-swizzled by row (swz_pf below) so that
 // both read patterns hit distinct banks.
 //
-// Softmax is exp2-based. With QK-norm the logits are bounded: |s| <= |q~| *
-// max|k~| and |k~| <= sqrt(D) * max|kw + w_offset| (RoPE preserves norms), so
-// the fused path uses that per-row bound as a fixed softmax shift (no running
-// max, no accumulator rescale) whenever it is <= 64 in log2 units, which keeps
-// every exp2 in [2^-128, ~1]. Rows with a larger bound, and the unfused
-// attention! operator, use the online running max (rescaled lazily, only when
-// it grows by > 8). Rows with no valid key produce 0 (attention.jl:86).
+// Softmax is exp2-based with an online running max, rescaled lazily (only when
+// it grows by > 8 in log2 units; the final 1/l cancels the common scale). No
+// weight bound is known to this operator, so there is no static shift. Rows
+// with no valid key (k_len = 0, or a causal row before the first key) produce
+// 0 (attention.jl:86).
 #include "common.h"
 #include "kernels.h"
 
@@ -36,7 +34,6 @@ constexpr int PF_BM = 128;                   // query rows per workgroup
 constexpr int PF_BN = 32;                    // keys per tile
 constexpr int TILE = PF_BN * HEAD_DIM;       // bf16 per K (or V) tile: 16 KB
 constexpr float RESCALE_SLACK = 8.0f;
-constexpr float STATIC_MAX_LIMIT = 64.0f;
 
 // Workgroup barrier without the release/acquire fences of __syncthreads(): those
 // would wait for every outstanding load (vmcnt(0)), including the tiles still in
@@ -136,7 +133,7 @@ __device__ __forceinline__ void mask_tile(const PrefillCtx& c, int jt, f32x16& s
 // One pipelined iteration on ring slot SLOT = jt % 4: wait for tile jt+1, issue
 // tile jt+3, then QK(jt+1) on the matrix cores while the VALU runs softmax(jt),
 // then PV(jt). `sc` holds S^T of tile jt on entry and of tile jt+1 on exit.
-template <bool STATIC, bool CAUSAL, int SLOT>
+template <bool CAUSAL, int SLOT>
 __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_tiles, int my_tiles,
                                           uint16_t* const (&K)[4], uint16_t* const (&V)[4],
                                           const uint4 (&qop)[16], f32x16 (&acc)[8], f32x16& sc,
@@ -159,26 +156,21 @@ __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_til
   // result is simply unused)
   const f32x16 sn = qk_tile(K[(SLOT + 1) & 3], qop, koff);
 
-  float m_eff;
-  if (STATIC) {
-    m_eff = m_run;
-  } else {
-    float mx = sc[0];
+  float mx = sc[0];
 #pragma unroll
-    for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sc[j]);
-    mx = wave_max_xor(mx, 32) * LOG2E;
-    const float m_new = fmaxf(m_run, mx);
-    const bool need = m_new > m_run + RESCALE_SLACK;
-    if (__ballot(need) != 0ull) {
-      const float m_use = need ? m_new : m_run;
-      const float alpha = (m_use == m_run) ? 1.0f : fast_exp2(m_run - m_use);
-      l_part *= alpha;
+  for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sc[j]);
+  mx = wave_max_xor(mx, 32) * LOG2E;
+  const float m_new = fmaxf(m_run, mx);
+  const bool need = m_new > m_run + RESCALE_SLACK;
+  if (__ballot(need) != 0ull) {
+    const float m_use = need ? m_new : m_run;
+    const float alpha = (m_use == m_run) ? 1.0f : fast_exp2(m_run - m_use);
+    l_part *= alpha;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-      m_run = m_use;
-    }
-    m_eff = m_run == -INFINITY ? 0.f : m_run;
+    for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+    m_run = m_use;
   }
+  const float m_eff = m_run == -INFINITY ? 0.f : m_run;
   float p[16], psum = 0.f;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
@@ -211,7 +203,7 @@ __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_til
 }
 
 // Ring of 4 tile slots; tiles 0..2 are issued by the caller.
-template <bool STATIC, bool CAUSAL>
+template <bool CAUSAL>
 __device__ __forceinline__ void tile_loop(const PrefillCtx& c, int n_tiles, int my_tiles,
                                           uint16_t* const (&K)[4], uint16_t* const (&V)[4],
                                           const uint4 (&qop)[16], f32x16 (&acc)[8],
@@ -228,21 +220,21 @@ __device__ __forceinline__ void tile_loop(const PrefillCtx& c, int n_tiles, int 
   f32x16 sc;
   if (my_tiles > 0) sc = qk_tile(K[0], qop, koff);
   for (int jt = 0; jt < n_tiles; jt += 4) {
-    tile_step<STATIC, CAUSAL, 0>(c, jt, n_tiles, my_tiles, K, V, qop, acc, sc, m_run, l_part,
+    tile_step<CAUSAL, 0>(c, jt, n_tiles, my_tiles, K, V, qop, acc, sc, m_run, l_part,
                                  koff, voff);
     if (jt + 1 < n_tiles)
-      tile_step<STATIC, CAUSAL, 1>(c, jt + 1, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
+      tile_step<CAUSAL, 1>(c, jt + 1, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
                                    l_part, koff, voff);
     if (jt + 2 < n_tiles)
-      tile_step<STATIC, CAUSAL, 2>(c, jt + 2, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
+      tile_step<CAUSAL, 2>(c, jt + 2, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
                                    l_part, koff, voff);
     if (jt + 3 < n_tiles)
-      tile_step<STATIC, CAUSAL, 3>(c, jt + 3, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
+      tile_step<CAUSAL, 3>(c, jt + 3, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
                                    l_part, koff, voff);
   }
 }
 
-template <bool QRAW, bool GATE, bool CAUSAL>
+template <bool CAUSAL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) uint16_t K0[TILE], K1[TILE], K2[TILE], K3[TILE];
@@ -265,8 +257,8 @@ void prefill_kernel(PrefillArgs a) {
   const int r0 = qt * PF_BM;
   const int row = r0 + 32 * wave + l32;  // query row in the chunk
 
-  // Raw q rows first: they depend on nothing the length lookups below return,
-  // so their HBM latency overlaps those lookups (rows past q_len are clamped
+  // q rows first: they depend on nothing the length lookups below return, so
+  // their HBM latency overlaps those lookups (rows past q_len are clamped
   // in-bounds and never used).
   const int qrow = min(row, a.L - 1);
   const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
@@ -275,12 +267,11 @@ void prefill_kernel(PrefillArgs a) {
 #pragma unroll
   for (int kk = 0; kk < 16; ++kk) qraw[kk] = load16(qp + 16 * kk);
 
-  // q_len > L is out of contract; clamp so rows past the tensor are never written
+  // q_len > L and k_len > Lk are out of contract; clamp so rows past the
+  // tensors are never read or written
   const int q_len = a.q_lengths ? min(a.q_lengths[b], a.L) : a.L;
   if (r0 >= q_len) return;
-  int k_len;
-  if (a.prior) k_len = a.prior[b] + q_len;
-  else k_len = a.k_lengths ? a.k_lengths[b] : a.Lk;
+  const int k_len = a.k_lengths ? max(0, min(a.k_lengths[b], a.Lk)) : a.Lk;
   const int off = k_len - q_len;  // queries are the suffix of keys
   const int kend = CAUSAL ? min(k_len, off + r0 + PF_BM) : k_len;
   const int n_tiles = kend > 0 ? (kend + PF_BN - 1) / PF_BN : 0;
@@ -292,92 +283,32 @@ void prefill_kernel(PrefillArgs a) {
   c.k_len = k_len; c.off = off; c.row = row; c.q_len = q_len;
   c.wrow0 = r0 + 32 * wave; c.wrow1 = c.wrow0 + 31;
   c.lane = lane; c.wave = wave;
-  c.krow_max = max(0, min(k_len, a.Lk) - 1);  // rows past k_len are masked; read finite data
+  c.krow_max = max(0, k_len - 1);  // rows past k_len are masked; read finite data
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 2 * (4 * wave + i) + (lane >> 5);
     c.dma_off[i] = r * (int)a.kv_st + (((lane & 31) ^ swz_pf(r)) * 8);
   }
 
-  // the first three tiles go out before the q prologue so their latency overlaps it
+  // the first three tiles go out before the q operand is formed so their
+  // latency overlaps it
   if (n_tiles > 0) issue_tile(c, 0, K0, V0);
   if (n_tiles > 1) issue_tile(c, 1, K1, V1);
   if (n_tiles > 2) issue_tile(c, 2, K2, V2);
   // tiles this wave computes (causal: keys <= off + its last row)
   int my_tiles = c.wrow0 < q_len ? n_tiles : 0;
-  if (CAUSAL && my_tiles > 0) my_tiles = min(n_tiles, (off + c.wrow1) / PF_BN + 1);
+  if (CAUSAL && my_tiles > 0) my_tiles = max(0, min(n_tiles, (off + c.wrow1) / PF_BN + 1));
 
-  // ---- Q operand: lane holds q[row][16kk + 8*h2 + j], pre-scaled by 1/16.
+  // ---- Q operand: lane holds q[row][16kk + 8*h2 + j], pre-scaled by 1/16
+  // (a power of two: exact in bf16).
   uint4 qop[16];
-  float qn2 = 0.f;  // |q operand|^2 (fp32, before rounding)
-  {
-    if (QRAW) {
-      float x[16][8];
 #pragma unroll
-      for (int kk = 0; kk < 16; ++kk) unpack8(qraw[kk], x[kk]);
-      float ss = 0.f;
+  for (int kk = 0; kk < 16; ++kk) {
+    float x[8];
+    unpack8(qraw[kk], x);
 #pragma unroll
-      for (int kk = 0; kk < 16; ++kk)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ss += x[kk][j] * x[kk][j];
-      ss += __shfl_xor(ss, 32, 64);
-      const float r = 1.0f / sqrtf(ss * (1.0f / HEAD_DIM) + a.eps);
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) {
-        float wf[8];
-        unpack8(load16(a.qw + 16 * kk + 8 * h2), wf);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[kk][j] = x[kk][j] * r * (wf[j] + a.w_offset);
-      }
-      const int64_t pos = min((int64_t)(a.prior ? a.prior[b] : 0) + qrow, (int64_t)a.Lk - 1);
-      const float* cs = a.cos_tab + pos * HALF_ROT + 8 * h2;
-      const float* sn = a.sin_tab + pos * HALF_ROT + 8 * h2;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float cc = cs[16 * kk + j], si = sn[16 * kk + j];
-          const float x1 = x[kk][j], x2 = x[kk + 2][j];
-          x[kk][j] = x1 * cc - x2 * si;
-          x[kk + 2][j] = x2 * cc + x1 * si;
-        }
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          x[kk][j] *= QK_SCALE;
-          qn2 += x[kk][j] * x[kk][j];
-        }
-        qop[kk] = pack8(x[kk]);
-      }
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) {
-        float x[8];
-        unpack8(qraw[kk], x);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] *= QK_SCALE;
-        qop[kk] = pack8(x);
-      }
-    }
-  }
-
-  // static softmax shift (fused path): bound on s * log2(e) for this row
-  bool use_static = false;
-  float m_run = -INFINITY;
-  if (QRAW) {
-    qn2 += __shfl_xor(qn2, 32, 64);
-    uint2 wv = *reinterpret_cast<const uint2*>(a.kw + 4 * lane);
-    float wmax = fmaxf(fmaxf(fabsf(__uint_as_float(wv.x << 16) + a.w_offset),
-                             fabsf(__uint_as_float(wv.x & 0xffff0000u) + a.w_offset)),
-                       fmaxf(fabsf(__uint_as_float(wv.y << 16) + a.w_offset),
-                             fabsf(__uint_as_float(wv.y & 0xffff0000u) + a.w_offset)));
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) wmax = fmaxf(wmax, __shfl_xor(wmax, m, 64));
-    const float kbound = 16.0f * wmax * 1.01f;                // sqrt(D) * max|kw+off|, + rounding
-    const float bound = sqrtf(qn2) * 1.01f * kbound * LOG2E;  // |q op| also rounded to bf16
-    use_static = __ballot(!(bound <= STATIC_MAX_LIMIT)) == 0ull;
-    if (use_static) m_run = bound;
+    for (int j = 0; j < 8; ++j) x[j] *= QK_SCALE;
+    qop[kk] = pack8(x);
   }
 
   // swizzled LDS read offsets (bytes). K: chunk c = 2kk + h2 of row l32 sits at
@@ -407,63 +338,36 @@ void prefill_kernel(PrefillArgs a) {
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[i][j] = 0.f;
-  float l_part = 0.f;
+  float l_part = 0.f, m_run = -INFINITY;
 
-  if (QRAW && use_static)
-    tile_loop<true, CAUSAL>(c, n_tiles, my_tiles, K, V, qop, acc, m_run, l_part, koff, voff);
-  else
-    tile_loop<false, CAUSAL>(c, n_tiles, my_tiles, K, V, qop, acc, m_run, l_part, koff, voff);
+  tile_loop<CAUSAL>(c, n_tiles, my_tiles, K, V, qop, acc, m_run, l_part, koff, voff);
 
-  // ---- epilogue: normalise, gate, store (row-major d within each row)
+  // ---- epilogue: normalise and store (row-major d within each row)
   if (row >= q_len) return;
   float l_tot = l_part + __shfl_xor(l_part, 32, 64);
-  const float inv = l_tot > 0.f ? fast_rcp(l_tot) : 0.f;  // fully-masked row -> 0
+  const float inv = l_tot > 0.f ? fast_rcp(l_tot) : 0.f;  // no valid key -> 0
   uint16_t* op = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)row * a.o_st;
-  // every gate load goes out before the first store (o and gate may alias as far
-  // as the compiler knows, so it would otherwise serialise load -> store pairs)
-  uint2 gv[8][4];
-  if (GATE) {
-    const uint16_t* gp = a.gate + (int64_t)b * a.g_sb + (int64_t)h * a.g_sh + (int64_t)row * a.g_st;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb)
-        gv[dt][jb] = *reinterpret_cast<const uint2*>(gp + 32 * dt + 8 * jb + 4 * h2);
-  }
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
       const int d0 = 32 * dt + 8 * jb + 4 * h2;
-      float o4[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) o4[q] = acc[dt][4 * jb + q] * inv;
-      if (GATE) {
-        const uint2 g2 = gv[dt][jb];
-        o4[0] *= sigmoidf(__uint_as_float(g2.x << 16));
-        o4[1] *= sigmoidf(__uint_as_float(g2.x & 0xffff0000u));
-        o4[2] *= sigmoidf(__uint_as_float(g2.y << 16));
-        o4[3] *= sigmoidf(__uint_as_float(g2.y & 0xffff0000u));
-      }
       uint2 ov;
-      ov.x = pack2(o4[0], o4[1]);
-      ov.y = pack2(o4[2], o4[3]);
+      ov.x = pack2(acc[dt][4 * jb + 0] * inv, acc[dt][4 * jb + 1] * inv);
+      ov.y = pack2(acc[dt][4 * jb + 2] * inv, acc[dt][4 * jb + 3] * inv);
       *reinterpret_cast<uint2*>(op + d0) = ov;
     }
   }
 }
 
-hipError_t launch_prefill(const PrefillArgs& a, bool qraw, bool gate, hipStream_t st) {
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st) {
   const int64_t nwg = (int64_t)a.n_qt * a.H * a.B;
   if (nwg == 0) return hipSuccess;
   dim3 grid((unsigned)nwg), block(256);
-  // the fused gated path is prefill_fused_kernel; this one serves the attention!
-  // operator (normalised q, no gate)
-  if (qraw || gate) return hipErrorInvalidValue;
   if (a.causal)
-    hipLaunchKernelGGL((prefill_kernel<false, false, true>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((prefill_kernel<true>), grid, block, 0, st, a);
   else
-    hipLaunchKernelGGL((prefill_kernel<false, false, false>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((prefill_kernel<false>), grid, block, 0, st, a);
   return hipGetLastError();
 }
 

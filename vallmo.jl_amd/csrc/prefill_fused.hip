@@ -276,8 +276,11 @@ __device__ __forceinline__ ItemGeo item_geo(const PrefillArgs& a, const FItem& i
   ig.r0 = it.qt * FM;
   ig.q_len = a.q_lengths ? min(a.q_lengths[it.b], a.L) : a.L;
   ig.prior = a.prior ? a.prior[it.b] : 0;
-  ig.k_len = ig.prior + ig.q_len;  // queries are the suffix of the attended keys
-  ig.off = ig.k_len - ig.q_len;
+  // queries are the suffix of the attended keys: row t sits at position prior + t.
+  // prior + q_len > Lk is out of contract (those keys were never appended): the
+  // keys past the cache are masked rather than read
+  ig.off = ig.prior;
+  ig.k_len = min(ig.prior + ig.q_len, a.Lk);
   ig.kend = causal ? min(ig.k_len, ig.off + ig.r0 + FM) : ig.k_len;
   return ig;
 }

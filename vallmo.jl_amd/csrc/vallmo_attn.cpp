@@ -443,7 +443,7 @@ int vm_attention_fwd(vm_bf16* o, int64_t o_st, int64_t o_sh, int64_t o_sb, const
   a.k_lengths = k_lengths; a.q_lengths = q_lengths; a.prior = nullptr;
   a.B = B; a.H = H; a.Hk = Hk; a.L = L; a.Lk = Lk; a.causal = causal ? 1 : 0;
   a.n_qt = (L + vm::PREFILL_ROWS_ABI - 1) / vm::PREFILL_ROWS_ABI;
-  return hip_status(timed(VM_K_PREFILL, S(st), [&] { return vm::launch_prefill(a, false, false, S(st)); }), "attention");
+  return hip_status(timed(VM_K_PREFILL, S(st), [&] { return vm::launch_prefill(a, S(st)); }), "attention");
 }
 
 // ---- a9 -------------------------------------------------------------------

@@ -23,7 +23,7 @@ from dataclasses import dataclass
 import torch
 
 from . import ops
-from ._lib import ArgumentError, call
+from ._lib import ArgumentError, BoundsError, DimensionMismatch, call
 from .sizes import sizes
 
 
@@ -144,17 +144,37 @@ def forward(l: AttnLayer, m: AttnModel, qkv, T: int, B: int, *, offset: int = 0,
     """
     cfg = m.cfg
     S = 2 * cfg.Hq + 2 * cfg.Hkv
+    ops._need(qkv, torch.bfloat16, "qkv")
     qkv4 = qkv.reshape(B, T, S, cfg.Dh)
     if qkv4.stride(3) != 1 or qkv4.stride(2) != cfg.Dh:
         raise ArgumentError("qkv must be packed along the slot axis")
     if prior is None:
         prior = torch.full((B,), int(offset), dtype=torch.int32, device="cuda")
-    d = sizes(K_cache=(l.K_cache, "Dh Ctx Hkv B"), prior=(prior, "B"),
-              q_lengths=(q_lengths, "B"))
+    d = sizes(K_cache=(l.K_cache, "Dh Ctx Hkv B"), V_cache=(l.V_cache, "Dh Ctx Hkv B"),
+              prior=(prior, "B"), q_lengths=(q_lengths, "B"), out=(out, f"{cfg.Hq * cfg.Dh} T B"))
     if d["B"] != B:
-        raise ArgumentError(f"cache batch {d['B']} != B = {B}")
+        raise DimensionMismatch(f"size(K_cache, 4) = {d['B']} does not match B = {B}")
+    if d["Dh"] != cfg.Dh or d["Hkv"] != cfg.Hkv:
+        raise DimensionMismatch(f"K_cache (Dh, Hkv) = ({d['Dh']}, {d['Hkv']}) does not match "
+                                f"the config ({cfg.Dh}, {cfg.Hkv})")
+    if out is not None and d["T"] != T:
+        raise DimensionMismatch(f"size(out, 2) = {d['T']} does not match T = {T}")
+    ops._need(l.K_cache, torch.bfloat16, "K_cache")
+    ops._need(l.V_cache, torch.bfloat16, "V_cache")
+    if l.K_cache.stride() != l.V_cache.stride():
+        raise ArgumentError("K_cache and V_cache must share strides")
+    ops._need(prior, torch.int32, "prior")
+    ops._need(q_lengths, torch.int32, "q_lengths")
+    # the reference's cache view K_cache[:, offset+1:offset+T, :, :] (qwen35.jl:306)
+    # throws a BoundsError past the capacity; a device-side prior is the caller's
+    # contract (prior[b] + q_lengths[b] <= Ctx), keys past the cache are masked
+    if int(offset) < 0 or int(offset) + T > d["Ctx"]:
+        raise BoundsError(f"attempt to access cache columns {int(offset) + 1}:{int(offset) + T} "
+                          f"of a cache with Ctx = {d['Ctx']}")
     if out is None:
         out = torch.empty((B, T, cfg.Hq * cfg.Dh), dtype=torch.bfloat16, device="cuda")
+    else:
+        ops._need(out, torch.bfloat16, "out")
     c = l.K_cache
     ws = m.prefill_workspace(B, d["Ctx"])
     call("vm_gated_attn_prefill", ops._p(out), out.stride(1), out.stride(0), ops._p(qkv4),
