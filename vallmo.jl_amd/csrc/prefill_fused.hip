@@ -315,25 +315,14 @@ struct QLoads {
   float4 cv[4], sv[4];
 };
 
-__device__ __forceinline__ void q_load_raw(const PrefillArgs& a, int b, int h, int row, int h2,
-                                           QLoads& ql) {
-  const int qrow = min(row, a.L - 1);
-  const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qrow * a.q_st + 8 * h2;
+// The q norm weight (the same for every row): lane reads w[16kk + 8h2 .. +7].
+// Issued from asm: a compiler-visible load here would be waited for with
+// vmcnt(0), i.e. behind the K tile loads issued after it.
+__device__ __forceinline__ void q_load_w(const PrefillArgs& a, int h2, u32x4 (&w)[16]) {
+  const uint16_t* p = a.qw + 8 * h2;
 #pragma unroll
-  for (int kk = 0; kk < 16; ++kk) ql.qraw[kk] = load16(qp + 16 * kk);
-}
-__device__ __forceinline__ void q_load_rest(const PrefillArgs& a, int row, int prior, int h2,
-                                            QLoads& ql) {
-#pragma unroll
-  for (int kk = 0; kk < 16; ++kk) ql.qwv[kk] = load16(a.qw + 16 * kk + 8 * h2);
-  const int64_t pos = min((int64_t)prior + min(row, a.L - 1), (int64_t)a.Lk - 1);
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      ql.cv[2 * kk + u] = *reinterpret_cast<const float4*>(a.cos_tab + pos * HALF_ROT + 8 * h2 + 16 * kk + 4 * u);
-      ql.sv[2 * kk + u] = *reinterpret_cast<const float4*>(a.sin_tab + pos * HALF_ROT + 8 * h2 + 16 * kk + 4 * u);
-    }
+  for (int kk = 0; kk < 16; ++kk)
+    asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(w[kk]) : "v"(p), "i"(32 * kk));
 }
 
 // q rows of one 32-row block: qnorm_rope (src/kernels/qknorm_rope_append.jl:25-57)
@@ -775,6 +764,75 @@ __device__ __forceinline__ void solo_prime(const SoloCtx& sc, const SoloLds& L) 
   for (int t = 0; t < 4; ++t) k_tile_load(sc.c, t, L.k + t * FT);
 }
 
+// The wave's 32 raw q rows and their RoPE table rows, staged in LDS by direct
+// global->LDS loads, each a coalesced 1-KB piece: q row r of the wave (16 KB per
+// wave, in the V objects, free until step -1) with its 16-byte chunk c at c ^
+// fswz(r), as the K tiles; cos and sin rows r (4 KB each per wave, in K object 2,
+// free until step -2) with chunk c at c ^ (r & 7). Read back in the Q^T operand
+// layout by q_read_lds, the banks of each b128 read are then distinct. 24 loads.
+__device__ __forceinline__ void q_stage(const PrefillArgs& a, const ItemGeo& ig, int wrow0, int wave,
+                                        int lane, const SoloLds& L) {
+  const int hl = lane >> 5, c = lane & 31;
+  const char* qb = reinterpret_cast<const char*>(a.q + (int64_t)ig.b * a.q_sb + (int64_t)ig.h * a.q_sh);
+  uint16_t* qd = L.v + wave * (32 * HEAD_DIM);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = 2 * i + hl;
+    const int64_t row = min(wrow0 + r, a.L - 1);
+    __builtin_amdgcn_global_load_lds((const void*)(qb + row * a.q_st * 2 + 16 * (c ^ fswz(r))),
+                                     (__attribute__((address_space(3))) void*)(qd + i * 512), 16, 0, 0);
+  }
+  float* td = reinterpret_cast<float*>(L.k + 2 * (2 * FT)) + wave * (2 * 32 * HALF_ROT);
+  const int pr = lane >> 3, ck = lane & 7;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * i + pr;
+    const int64_t pos = min((int64_t)ig.prior + min(wrow0 + r, a.L - 1), (int64_t)a.Lk - 1);
+    const int64_t off = pos * HALF_ROT + 4 * (ck ^ (r & 7));
+    __builtin_amdgcn_global_load_lds((const void*)(a.cos_tab + off),
+                                     (__attribute__((address_space(3))) void*)(td + i * 256), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(a.sin_tab + off),
+                                     (__attribute__((address_space(3))) void*)(td + 32 * HALF_ROT + i * 256),
+                                     16, 0, 0);
+  }
+}
+// lane (l32, h2): q[row l32][16kk + 8h2 .. +7] and the table floats 8h2 + 16kk + 4u.
+// The reads are issued from asm (a compiler-visible LDS read after the staging
+// loads would get a wait for every load in flight, the K tiles included) and
+// released by counted waits tied to their registers.
+__device__ __forceinline__ void q_read_lds(QLoads& ql, const SoloLds& L, int wave, int l32, int h2) {
+  const uint32_t qs = lds_addr(L.v + wave * (32 * HEAD_DIM) + l32 * HEAD_DIM);
+  const int sq = fswz(l32);
+  u32x4 q[16], t[8];
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) q[kk] = ds_b128<0>(qs + 16 * ((2 * kk + h2) ^ sq));
+  const uint32_t ts = lds_addr(reinterpret_cast<const float*>(L.k + 2 * (2 * FT)) +
+                               wave * (2 * 32 * HALF_ROT) + l32 * HALF_ROT);
+  const int st = l32 & 7;
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t ch = (uint32_t)(16 * ((2 * h2 + 4 * kk + u) ^ st));
+      t[2 * kk + u] = ds_b128<0>(ts + ch);
+      t[4 + 2 * kk + u] = ds_b128<4 * 32 * HALF_ROT>(ts + ch);
+    }
+  asm volatile("s_waitcnt lgkmcnt(8)"
+               : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(q[4]), "+v"(q[5]), "+v"(q[6]),
+                 "+v"(q[7]), "+v"(q[8]), "+v"(q[9]), "+v"(q[10]), "+v"(q[11]), "+v"(q[12]),
+                 "+v"(q[13]), "+v"(q[14]), "+v"(q[15]));
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]), "+v"(t[4]), "+v"(t[5]), "+v"(t[6]),
+                 "+v"(t[7]));
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) ql.qraw[kk] = __builtin_bit_cast(uint4, q[kk]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    ql.cv[i] = __builtin_bit_cast(float4, t[i]);
+    ql.sv[i] = __builtin_bit_cast(float4, t[4 + i]);
+  }
+}
+
 // One item. SHIFT = false: every logit is within +-64 (log2 units), so
 // P = exp2(S) needs no shift (the normalisation cancels any common scale);
 // SHIFT = true: an exact row-max pass first, P = exp2(S - row max).
@@ -800,11 +858,23 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
     for (int q = 0; q < 8; ++q) sc.kaddr[q] = lds_addr(L.k) + l32 * 512 + 16 * ((2 * q + h2) ^ sk);
   }
   sc.vaddr = lds_addr(L.v) + 16 * lane;
-  solo_prime(sc, L);  // K blocks 0, 1 land while q is loaded and rotated
+  // q and its table rows first (in-order completion: the q math waits for them
+  // only), then the norm weights, then K blocks 0 and 1, which land under the math
+  q_stage(a, ig, g.wrow0, wave, lane, L);
+  u32x4 qw[16];
+  q_load_w(a, h2, qw);
+  solo_prime(sc, L);
+  // the staging loads and the weights are in; the 16 K tile loads may not be
+  asm volatile("s_waitcnt vmcnt(16)"
+               : "+v"(qw[0]), "+v"(qw[1]), "+v"(qw[2]), "+v"(qw[3]), "+v"(qw[4]), "+v"(qw[5]),
+                 "+v"(qw[6]), "+v"(qw[7]), "+v"(qw[8]), "+v"(qw[9]), "+v"(qw[10]), "+v"(qw[11]),
+                 "+v"(qw[12]), "+v"(qw[13]), "+v"(qw[14]), "+v"(qw[15])
+               :
+               : "memory");
   QLoads ql;
-  q_load_raw(a, ig.b, ig.h, g.row, h2, ql);
-  q_load_rest(a, g.row, ig.prior, h2, ql);
-
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) ql.qwv[kk] = __builtin_bit_cast(uint4, qw[kk]);
+  q_read_lds(ql, L, wave, l32, h2);
   q_prologue(a, ql, st.qop);
   // rows past the chunk hold finite junk q; their outputs are never stored
 #pragma unroll
@@ -892,12 +962,17 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
       *reinterpret_cast<uint2*>(xr + el * XROW + 32 * db + 8 * jb + 4 * eh) = ov[db][jb];
   __builtin_amdgcn_s_waitcnt(0xc07f);
   asm volatile("" ::: "memory");
-  uint16_t* ob = a.o + (int64_t)ig.b * a.o_sb + (int64_t)ig.h * a.o_sh + 8 * el;
+  // every row chunk out of LDS first (one wait), then the stores along one pointer
+  u32x4 orow[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) orow[i] = *reinterpret_cast<const u32x4*>(xr + (2 * i + eh) * XROW + 8 * el);
+  uint16_t* op = a.o + (int64_t)ig.b * a.o_sb + (int64_t)ig.h * a.o_sh + 8 * el +
+                 (int64_t)(g.wrow0 + eh) * a.o_st;
+  const int64_t ostep = 2 * a.o_st;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int row = g.wrow0 + 2 * i + eh;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + (2 * i + eh) * XROW + 8 * el);
-    if (row < ig.q_len) *reinterpret_cast<u32x4*>(ob + (int64_t)row * a.o_st) = v;
+    if (g.wrow0 + 2 * i + eh < ig.q_len) *reinterpret_cast<u32x4*>(op) = orow[i];
+    op += ostep;
   }
 }
 
@@ -938,7 +1013,9 @@ void prefill_fused_kernel(PrefillArgs a) {
     solo_item<CAUSAL, false>(a, it, L);
   else
     solo_item<CAUSAL, true>(a, it, L);
-  fwait_vmcnt<0>();  // no LDS load may land after the workgroup is gone
+  // No global->LDS load is in flight here: the epilogue waited for all of them
+  // (vmcnt(0)) before its barrier, and an item that returns early issued none.
+  // Only the output stores may be outstanding, which need no wait.
 }
 
 hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st) {
