@@ -519,6 +519,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-config5", action="store_true", help="skip the config-5 prefill leg")
     ap.add_argument("--no-settle", action="store_true",
                     help="skip the clock-settle phase (counter-collection runs)")
     ap.add_argument("--no-decode", action="store_true")
@@ -554,7 +555,7 @@ def main():
             f"attn kernel {pf['attn_kernel_ms']:.3f} ms, "
             f"K/V append + V^T staging {pf['append_vt_kernel_ms']:.4f} ms")
     pf5 = None
-    if not args.no_prefill:
+    if not args.no_prefill and not args.no_config5:
         log("[bench] prefill config5 (ragged chunked, B=4)")
         pf5 = bench_prefill5(vm, torch, max(10, args.steps // 15), max(3, args.warmup // 30))
         log(f"[bench] prefill5: {pf5['ms_per_step']:.3f} ms/step, {pf5['tflops']:.1f} TFLOP/s, "
