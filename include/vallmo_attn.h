@@ -165,6 +165,27 @@ int vm_gated_attn_decode(vm_bf16* out, int64_t out_sb,
                          float eps, float w_offset, int n_splits,
                          void* scratch, size_t scratch_bytes, vm_stream stream);
 
+/* ---- a7 with no allocation of any kind. No counterpart in the reference: it
+ * is for callers that cannot allocate or hand over a workspace (code under
+ * graph capture that must not call hipMalloc, tight serving loops, harnesses
+ * that forbid allocation). Same step and arguments as vm_gated_attn_decode,
+ * but the workspace is a static array inside the library, one per GPU, of
+ * VM_DECODE_STATIC_SCRATCH_BYTES (16 MiB, held until the process ends). A step
+ * whose vm_decode_scratch_bytes(B, Hq, Hk, D, ctx, n_splits) exceeds it fails
+ * with VM_E_SCRATCH. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams or threads) race; calls ordered on one
+ * stream are safe. Nothing in the array has to start at zero.              */
+#define VM_DECODE_STATIC_SCRATCH_BYTES ((size_t)16 << 20)
+int vm_gated_attn_decode_noalloc(vm_bf16* out, int64_t out_sb,
+                                 const vm_bf16* qkv, int64_t qkv_sb,
+                                 vm_bf16* k_cache, vm_bf16* v_cache,
+                                 int64_t c_st, int64_t c_sh, int64_t c_sb, int64_t ctx,
+                                 const vm_bf16* qw, const vm_bf16* kw,
+                                 const float* cos_tab, const float* sin_tab,
+                                 int32_t* positions, int advance,
+                                 int B, int Hq, int Hk, int D, int half_rot,
+                                 float eps, float w_offset, int n_splits, vm_stream stream);
+
 /* ---- a12: advance! (src/llm/generate.jl:82-88): positions[b] += 1 ------ */
 int vm_advance_positions(int32_t* positions, int B, vm_stream stream);
 

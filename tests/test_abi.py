@@ -149,3 +149,19 @@ def test_sizes_contract_messages(vm):
     assert d == {"Dqk": 256, "Hq": 16, "B": 2}
     with pytest.raises(vm.DimensionMismatch):
         vm.sizes(R=(torch.empty(3, 4), "4 3"), S=(torch.empty(5), "4"))
+
+
+def test_noalloc_decode_rejects_steps_beyond_its_workspace(vm):
+    """vm_gated_attn_decode_noalloc serves steps whose workspace fits its static
+    16 MiB array and refuses larger ones with VM_E_SCRATCH, before any HIP call."""
+    lib = vm._lib.load()
+    B, Hq, Hk, ctx, n_splits = 1000, 16, 4, 4096, 8
+    need = lib.vm_decode_scratch_bytes(B, Hq, Hk, 256, ctx, n_splits)
+    assert need > (16 << 20)
+    rc = lib.vm_gated_attn_decode_noalloc(_p(FAKE), 256 * Hq, _p(FAKE), 256 * 40, _p(FAKE),
+                                          _p(FAKE), 256, 256 * ctx, 256 * ctx * Hk, ctx,
+                                          _p(FAKE), _p(FAKE), _p(FAKE), _p(FAKE), _p(FAKE), 0, B,
+                                          Hq, Hk, 256, 32, 1e-6, 1.0, n_splits, None)
+    assert rc == vm._lib.VM_E_SCRATCH
+    msg = lib.vm_last_error().decode()
+    assert "static workspace" in msg and str(need) in msg

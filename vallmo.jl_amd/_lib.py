@@ -88,6 +88,9 @@ _SIGS = {
     "vm_gated_attn_decode": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _p, _c_i64, _c_i64, _c_i64,
                                     _c_i64, _p, _p, _p, _p, _p, _c_i, _c_i, _c_i, _c_i, _c_i,
                                     _c_i, _c_f, _c_f, _c_i, _p, _c_sz, _p]),
+    "vm_gated_attn_decode_noalloc": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _p, _c_i64, _c_i64,
+                                            _c_i64, _c_i64, _p, _p, _p, _p, _p, _c_i, _c_i, _c_i,
+                                            _c_i, _c_i, _c_i, _c_f, _c_f, _c_i, _p]),
     "vm_advance_positions": (_c_i, [_p, _c_i, _p]),
     "vm_attention_fwd": (_c_i, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _c_i64, _c_i64, _p, _p,
                                 _c_i64, _c_i64, _c_i64, _p, _p, _c_i, _c_i, _c_i, _c_i, _c_i,

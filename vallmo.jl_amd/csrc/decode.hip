@@ -30,10 +30,39 @@
 // takes p = exp2(s) unshifted (p within 2^+-64, the merge's 1/l cancels the
 // common scale); otherwise, and for the unfused operator, a running max
 // rescaled lazily (only when it grows by > 8).
+#include <mutex>
+
 #include "common.h"
 #include "kernels.h"
 
 namespace vm {
+
+// Workspace of the no-allocation decode entry point (vm_gated_attn_decode_noalloc):
+// one copy per GPU, part of the code object, held until the process ends. Host
+// code never passes `scratch` itself to a kernel (in host code the name is a
+// stand-in, not a device address): decode_static_scratch() looks up this GPU's
+// address once and every launch takes that pointer.
+static __device__ __align__(256) unsigned char scratch[DECODE_STATIC_SCRATCH_BYTES];
+
+hipError_t decode_static_scratch(void** ptr) {
+  constexpr int MAX_DEV = 64;
+  static std::mutex mu;
+  static void* addr[MAX_DEV] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= MAX_DEV) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    // first call on this device, with it current: its own copy of the array
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    addr[dev] = p;
+  }
+  *ptr = addr[dev];
+  return hipSuccess;
+}
 
 constexpr int DSTEP = 16;                 // tokens per step
 constexpr float D_RESCALE_SLACK = 8.0f;

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/vallmo_attn.h"
+
 namespace vm {
 
 constexpr int HEAD_DIM_ABI = 256;     // compiled head_dim
@@ -133,6 +135,12 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st);
 hipError_t launch_prefill_fused(const PrefillArgs& a, hipStream_t st, hipEvent_t t0 = nullptr,
                                 hipEvent_t t1 = nullptr);
 hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st);
+
+// Static per-GPU workspace of the no-allocation decode entry point: the largest
+// decode scratch it serves (vm_decode_scratch_bytes), and its device address on
+// the current GPU (looked up once per GPU, then cached).
+constexpr size_t DECODE_STATIC_SCRATCH_BYTES = VM_DECODE_STATIC_SCRATCH_BYTES;
+hipError_t decode_static_scratch(void** ptr);
 
 // Decode stream partition shared by the scratch-size query and the launchers:
 // NW waves cover the token-heads sum_b len_b * Hk in equal contiguous chunks.

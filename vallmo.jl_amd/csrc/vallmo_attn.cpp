@@ -369,7 +369,7 @@ int vm_sigmoid_gate(vm_bf16* o, int64_t o_sh, int64_t o_sb, const vm_bf16* g, in
 }
 
 // ---- a7 -------------------------------------------------------------------
-int vm_gated_attn_decode(vm_bf16* out, int64_t out_sb, const vm_bf16* qkv, int64_t qkv_sb,
+static int gated_attn_decode(vm_bf16* out, int64_t out_sb, const vm_bf16* qkv, int64_t qkv_sb,
                          vm_bf16* kc, vm_bf16* vc, int64_t c_st, int64_t c_sh, int64_t c_sb,
                          int64_t ctx, const vm_bf16* qw, const vm_bf16* kw, const float* cs,
                          const float* sn, int32_t* positions, int advance, int B, int Hq, int Hk,
@@ -409,6 +409,42 @@ int vm_gated_attn_decode(vm_bf16* out, int64_t out_sb, const vm_bf16* qkv, int64
   c.gate = qkv + Dl; c.g_sh = 2 * Dl; c.g_sb = qkv_sb;
   c.advance = advance ? positions : nullptr;
   return hip_status(timed(VM_K_DECODE_COMBINE, S(st), [&] { return vm::launch_combine(c, S(st)); }), "gated_attn_decode combine");
+}
+
+int vm_gated_attn_decode(vm_bf16* out, int64_t out_sb, const vm_bf16* qkv, int64_t qkv_sb,
+                         vm_bf16* kc, vm_bf16* vc, int64_t c_st, int64_t c_sh, int64_t c_sb,
+                         int64_t ctx, const vm_bf16* qw, const vm_bf16* kw, const float* cs,
+                         const float* sn, int32_t* positions, int advance, int B, int Hq, int Hk,
+                         int D, int half_rot, float eps, float w_offset, int n_splits,
+                         void* scratch, size_t scratch_bytes, vm_stream st) {
+  return gated_attn_decode(out, out_sb, qkv, qkv_sb, kc, vc, c_st, c_sh,
+                           c_sb, ctx, qw, kw, cs, sn, positions, advance, B, Hq, Hk, D, half_rot,
+                           eps, w_offset, n_splits, scratch, scratch_bytes, st);
+}
+
+// The same step with its workspace in the library's static per-GPU array
+// (no allocation of any kind). Calls that overlap on one GPU share that array.
+int vm_gated_attn_decode_noalloc(vm_bf16* out, int64_t out_sb, const vm_bf16* qkv,
+                                 int64_t qkv_sb, vm_bf16* kc, vm_bf16* vc, int64_t c_st,
+                                 int64_t c_sh, int64_t c_sb, int64_t ctx, const vm_bf16* qw,
+                                 const vm_bf16* kw, const float* cs, const float* sn,
+                                 int32_t* positions, int advance, int B, int Hq, int Hk, int D,
+                                 int half_rot, float eps, float w_offset, int n_splits,
+                                 vm_stream st) {
+  REQUIRE(B >= 0 && Hq > 0 && Hk > 0 && Hq % Hk == 0 && ctx > 0 && n_splits >= 0, VM_E_ARG,
+          "gated_attn_decode_noalloc: B = %d, Hq = %d, Hk = %d, Ctx = %lld, n_splits = %d", B,
+          Hq, Hk, (long long)ctx, n_splits);
+  const size_t need = vm_decode_scratch_bytes(B > 0 ? B : 1, Hq, Hk, D, ctx, n_splits);
+  REQUIRE(need <= vm::DECODE_STATIC_SCRATCH_BYTES, VM_E_SCRATCH,
+          "gated_attn_decode_noalloc: this step needs %zu bytes of workspace, more than the "
+          "%zu-byte static workspace (use vm_gated_attn_decode with a caller buffer)",
+          need, (size_t)vm::DECODE_STATIC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  TRY(hip_status(vm::decode_static_scratch(&ws), "gated_attn_decode_noalloc workspace"));
+  return gated_attn_decode(out, out_sb, qkv, qkv_sb, kc, vc, c_st,
+                           c_sh, c_sb, ctx, qw, kw, cs, sn, positions, advance, B, Hq, Hk, D,
+                           half_rot, eps, w_offset, n_splits, ws, vm::DECODE_STATIC_SCRATCH_BYTES,
+                           st);
 }
 
 int vm_advance_positions(int32_t* positions, int B, vm_stream st) {
