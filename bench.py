@@ -120,7 +120,7 @@ def bench_prefill(vm, torch, steps, warmup, T=4096, seed=2, settle=True):
     prior = torch.zeros((B,), dtype=torch.int32, device="cuda")
 
     def step():
-        vm.forward(layer, m, qkv, T, B, prior=prior, out=out)
+        vm.gated_attn_prefill(layer, m, qkv, T, B, prior=prior, out=out)
 
     for _ in range(warmup):
         step()
@@ -185,7 +185,7 @@ def bench_prefill5(vm, torch, steps, warmup, seed=5):
     ql = torch.from_numpy(qlen).cuda()
 
     def step():   # appends the same chunk columns each time: same work per step
-        vm.forward(layer, m, qkv, T, B, prior=pr, q_lengths=ql, out=out)
+        vm.gated_attn_prefill(layer, m, qkv, T, B, prior=pr, q_lengths=ql, out=out)
 
     for _ in range(warmup):
         step()
@@ -235,11 +235,11 @@ def bench_decode1(vm, torch, steps, warmup, seed=1):
     gen.positions.fill_(L)
     O = torch.empty((B, HQ, D), dtype=torch.bfloat16, device="cuda")
     for _ in range(warmup):
-        vm.decode_(O, layer, m, gen, qkv)
+        vm.gated_attn_decode_(O, layer, m, gen, qkv)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        vm.decode_(O, layer, m, gen, qkv)   # same position each step: same bytes
+        vm.gated_attn_decode_(O, layer, m, gen, qkv)   # same position each step: same bytes
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     nbytes = decode_bytes([L])
@@ -275,20 +275,20 @@ def bench_decode3(vm, torch, steps, warmup, seed=3):
     O = torch.empty((B, HQ, D), dtype=torch.bfloat16, device="cuda")
     for _ in range(warmup):
         gen.positions.copy_(pos)
-        vm.decode_(O, layer, m, gen, qkv)
+        vm.gated_attn_decode_(O, layer, m, gen, qkv)
     torch.cuda.synchronize()
     gen.positions.copy_(pos)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        vm.decode_(O, layer, m, gen, qkv)   # same position each step: same bytes
+        vm.gated_attn_decode_(O, layer, m, gen, qkv)   # same position each step: same bytes
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     # untimed: both kernels on their own hipEvents
     lib = vm._lib
     lib.profile_enable(True)
     for _ in range(min(steps, 20)):
-        vm.decode_(O, layer, m, gen, qkv)
+        vm.gated_attn_decode_(O, layer, m, gen, qkv)
     torch.cuda.synchronize()
     n_s, ms_s = lib.profile_read(lib.VM_K_DECODE_SPLIT)
     n_c, ms_c = lib.profile_read(lib.VM_K_DECODE_COMBINE)
@@ -325,18 +325,18 @@ def bench_decode4(vm, torch, replays=256, seed=4):
     # eager warmup + split-kernel timing at the first position
     gen.positions.fill_(p0)
     for _ in range(3):
-        vm.decode_(O, layer, m, gen, qkv)
+        vm.gated_attn_decode_(O, layer, m, gen, qkv)
     torch.cuda.synchronize()
     lib = vm._lib
     lib.profile_enable(True)
     for _ in range(10):
-        vm.decode_(O, layer, m, gen, qkv)
+        vm.gated_attn_decode_(O, layer, m, gen, qkv)
     torch.cuda.synchronize()
     n_s, ms_s = lib.profile_read(lib.VM_K_DECODE_SPLIT)
     lib.profile_enable(False)
     gen.positions.fill_(p0)
     torch.cuda.synchronize()
-    sess = vm.CaptureSession().capture(lambda: vm.decode_(O, layer, m, gen, qkv, advance=True))
+    sess = vm.CaptureSession().capture(lambda: vm.gated_attn_decode_(O, layer, m, gen, qkv, advance=True))
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record()

@@ -250,6 +250,22 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb,
                           float eps, float w_offset, void* scratch, size_t scratch_bytes,
                           vm_stream stream);
 
+/* ---- f1: linear!((; y), x, W) (src/linear.jl:40-57): y = W^T x ------------
+ * The qkv projection in front of the block and the Wo projection after it
+ * (src/llm/qwen35.jl:194, :206, :296, :316-317). Column-major, as the
+ * reference: x :: (K, N) with column stride ldx >= K, W :: (K, M) (K-major,
+ * the checkpoint's orientation) with column stride ldw >= K, y :: (M, N) with
+ * column stride ldy >= M; all bf16, fp32 accumulation (linear.jl:29). A plan per
+ * problem (hipBLASLt) is built on the first call and cached (linear.jl:17-38);
+ * vm_linear_workspace_bytes builds it and returns the workspace it needs (at
+ * most 64 MiB), which the caller passes to vm_linear (the reference takes it
+ * from the ambient arena, linear.jl:62-66). Returns (size_t)-1 on failure.
+ * A problem with no algorithm is VM_E_UNSUPPORTED (no fallback path).        */
+size_t vm_linear_workspace_bytes(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy);
+int vm_linear(vm_bf16* y, int64_t ldy, const vm_bf16* x, int64_t ldx, const vm_bf16* w,
+              int64_t ldw, int M, int N, int K, void* workspace, size_t workspace_bytes,
+              vm_stream stream);
+
 /* ---- synthetic inputs for tests and benchmarks (not a reference op) ----
  * Fills n bf16 values with the seeded N(0,1) stream used by the CPU oracle
  * (SplitMix64 -> Box-Muller in f64 -> f32 -> bf16 RNE), element i of stream

@@ -58,6 +58,8 @@ def lib():
                                         _f32p, _f32p, i32, i32, i32, i32, i32, i32, f32, f32,
                                         _f32p, _f32p, _f32p, i32, i32]
         L.orc_gated_prefill.restype = None
+        L.orc_linear.argtypes = [_u16p, _u16p, _f32p, i32, i32, i32, i32]
+        L.orc_linear.restype = None
         L.orc_max_threads.restype = i32
         _LIB = L
     return _LIB
@@ -151,6 +153,56 @@ def gated_prefill(qkv, kc, vc, prior, q_len, qw, kw, cos_tab, sin_tab, *, Hq, Hk
                             _c(sin_tab, np.float32), B, T, Hq, Hk, D, cos_tab.shape[1], eps,
                             w_offset, out, kn, vn, int(row_step), int(nthreads))
     return out, kn, vn
+
+
+def linear(x, W, *, nthreads=0):
+    """y = W^T x in fp32 (src/linear.jl:40-57): x [..][K] bf16 bits (the reference's
+    (K, N)), W [M][K] bf16 bits (the reference's K-major (K, M)) -> y [..][M]."""
+    x = _c(x, np.uint16)
+    W = _c(W, np.uint16)
+    M, K = W.shape
+    lead = x.shape[:-1]
+    assert x.shape[-1] == K
+    N = int(np.prod(lead)) if lead else 1
+    y = np.empty(lead + (M,), np.float32)
+    lib().orc_linear(x.reshape(N, K), W, y.reshape(N, M), M, N, K, int(nthreads))
+    return y
+
+
+def decode_layer(xn, Wqkv, Wo, kc, vc, positions, qw, kw, cos_tab, sin_tab, *, Hq, Hk, eps,
+                 w_offset, nthreads=0):
+    """decode!(h, ::AttnLayer, m, gen, xn) (src/llm/qwen35.jl:187-208) for one step:
+    xn [B][Dm] bf16 bits -> h [B][Dm] fp32. The reference keeps qkv and the gated
+    attention output in bf16 buffers (qwen35.jl:193, :205); they are rounded to bf16
+    (RNE) here at those two points, everything else is fp32. Also returns the
+    appended (k_new, v_new) rows."""
+    B = xn.shape[0]
+    D = kc.shape[-1]
+    S = 2 * Hq + 2 * Hk
+    qkv = f32_to_bf16(linear(xn, Wqkv, nthreads=nthreads)).reshape(B, S, D)
+    o, kn, vn = gated_decode(qkv, kc, vc, positions, qw, kw, cos_tab, sin_tab, Hq=Hq, Hk=Hk,
+                             eps=eps, w_offset=w_offset, nthreads=nthreads)
+    h = linear(f32_to_bf16(o).reshape(B, Hq * D), Wo, nthreads=nthreads)
+    return h, kn, vn
+
+
+def prefill_layer(xn, Wqkv, Wo, kc, vc, prior, q_len, qw, kw, cos_tab, sin_tab, *, Hq, Hk, eps,
+                  w_offset, row_step=1, nthreads=0):
+    """forward(::AttnLayer, m, xn, T, B; offset) (src/llm/qwen35.jl:292-318), ragged:
+    xn [B][T][Dm] bf16 bits -> h [B][T][Dm] fp32 (rows not evaluated are NaN). qkv
+    and the gated attention output are rounded to bf16 as the reference stores
+    them (qwen35.jl:296, :312-315)."""
+    B, T = xn.shape[:2]
+    D = kc.shape[-1]
+    S = 2 * Hq + 2 * Hk
+    qkv = f32_to_bf16(linear(xn, Wqkv, nthreads=nthreads)).reshape(B, T, S, D)
+    o, kn, vn = gated_prefill(qkv, kc, vc, prior, q_len, qw, kw, cos_tab, sin_tab, Hq=Hq, Hk=Hk,
+                              eps=eps, w_offset=w_offset, row_step=row_step, nthreads=nthreads)
+    o = o.reshape(B, T, Hq * D)
+    rows = ~np.isnan(o[..., 0])
+    h = np.full((B, T, Wo.shape[0]), np.nan, np.float32)
+    h[rows] = linear(f32_to_bf16(o[rows]), Wo, nthreads=nthreads)
+    return h, kn, vn
 
 
 def threads_env() -> int:

@@ -22,6 +22,7 @@
  *   decode attention ........ src/kernels/attention_decode.jl:14-181 (unsplit here)
  *   sigmoid gate ............ src/kernels/kernels.jl:34, src/llm/qwen35.jl:205,315
  *   decode! / forward ....... src/llm/qwen35.jl:187-208, 292-318
+ *   linear! (y = W^T x) ..... src/linear.jl:40-57 (fp32 accumulation, linear.jl:29)
  */
 #include <math.h>
 #include <stdint.h>
@@ -364,6 +365,34 @@ void orc_gated_prefill(const uint16_t* qkv, const uint16_t* kc, const uint16_t* 
   free(vpf);
   free(qwf);
   free(kwf);
+}
+
+/* linear! (src/linear.jl:40-57): y = W^T x in fp32 from bf16 operands.
+ * Row-major views of the reference's column-major arrays: x [N][K] (x :: (K, N)),
+ * W [M][K] (W :: (K, M), K-major), y [N][M] (y :: (M, N)). */
+void orc_linear(const uint16_t* x, const uint16_t* w, float* y, int M, int N, int K,
+                int nthreads) {
+  set_threads(nthreads);
+  float* wf = (float*)malloc(sizeof(float) * (size_t)M * K);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < (int64_t)M * K; ++i) wf[i] = bf(w[i]);
+#pragma omp parallel
+  {
+    float* xr = (float*)malloc(sizeof(float) * (size_t)K);
+#pragma omp for schedule(static)
+    for (int n = 0; n < N; ++n) {
+      for (int k = 0; k < K; ++k) xr[k] = bf(x[(size_t)n * K + k]);
+      for (int m = 0; m < M; ++m) {
+        const float* wr = wf + (size_t)m * K;
+        float acc = 0.f;
+#pragma omp simd reduction(+ : acc)
+        for (int k = 0; k < K; ++k) acc += wr[k] * xr[k];
+        y[(size_t)n * M + m] = acc;
+      }
+    }
+    free(xr);
+  }
+  free(wf);
 }
 
 int orc_max_threads(void) {

@@ -41,7 +41,7 @@ def run_decode_vs_oracle(vm, orc, B, ctx, pos, Hq=HQ, Hk=HK, seed=0, n_splits=0,
     gen = vm.Generation(B)
     gen.positions.copy_(i32(pos))
     O = torch.empty((B, Hq, D), dtype=torch.bfloat16, device="cuda")
-    vm.decode_(O, layer, m, gen, to_dev(qkv))
+    vm.gated_attn_decode_(O, layer, m, gen, to_dev(qkv))
     torch.cuda.synchronize()
     c, s = orc.rope_tables(HALF, ctx, THETA)
     ref, kn, vn = orc.gated_decode(qkv, kc, vc, np.asarray(pos, np.int32), qw, kw, c, s, Hq=Hq,
@@ -174,7 +174,7 @@ def test_config3_batched_decode_full_size(vm, orc):
     gen = vm.Generation(B)
     gen.positions.copy_(i32(pos))
     O = torch.empty((B, HQ, D), dtype=torch.bfloat16, device="cuda")
-    vm.decode_(O, layer, m, gen, to_dev(qkv))
+    vm.gated_attn_decode_(O, layer, m, gen, to_dev(qkv))
     torch.cuda.synchronize()
     got = dev_f32(O)
     c, s = orc.rope_tables(HALF, ctx, THETA)
@@ -213,7 +213,7 @@ def test_config4_graph_replay_matches_eager(vm, orc):
     gen.positions.fill_(p0)
     eager = []
     for _ in range(n):
-        vm.decode_(O, layer, m, gen, qkv, advance=True)
+        vm.gated_attn_decode_(O, layer, m, gen, qkv, advance=True)
         eager.append(O.clone())
     torch.cuda.synchronize()
     assert gen.positions.item() == p0 + n
@@ -223,7 +223,7 @@ def test_config4_graph_replay_matches_eager(vm, orc):
     V.copy_(V0)
     gen.positions.fill_(p0)
     torch.cuda.synchronize()
-    sess = vm.CaptureSession().capture(lambda: vm.decode_(O, layer, m, gen, qkv, advance=True))
+    sess = vm.CaptureSession().capture(lambda: vm.gated_attn_decode_(O, layer, m, gen, qkv, advance=True))
     assert gen.positions.item() == p0          # capture records without executing
     replay = []
     for _ in range(n):

@@ -1,0 +1,149 @@
+"""The projections around the block and whole attention layers on the GPU vs the
+oracle: linear! (hipBLASLt, src/linear.jl:40-57) alone for the decode GEMV and
+prefill GEMM shapes, decode!(h, ::AttnLayer, m, gen, xn) (qwen35.jl:187-208) at
+BASELINE config 1 and forward(::AttnLayer, m, xn, T, B) (qwen35.jl:292-318) at
+config 2, hidden state to hidden state, and the whole decode layer step captured
+in a hipGraph and replayed with the position advancing (replays == eager)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import (D, EPS, HALF, HK, HQ, S, THETA, TOL_MAX, TOL_MEAN, banner, dev_f32,
+                      from_dev, i32, maxmean, to_dev)
+from oracle.rng import bf16_to_f32, normal_bf16
+
+pytestmark = pytest.mark.gpu
+
+DM = 2560  # hidden size of the layer (the Qwen3.5 small-model width)
+
+
+@pytest.mark.parametrize("M,N,K", [(S * D, 1, DM), (S * D, 32, DM), (DM, 4096, HQ * D),
+                                   (520, 300, 136)])
+def test_linear_operator(vm, orc, M, N, K):
+    """y = W^T x for the qkv GEMV (N = 1, 32), the Wo GEMM of a 4096-token
+    prefill and an odd shape; checked on every 8th column of y (N > 64)."""
+    banner(f"linear M={M} N={N} K={K}")
+    x = normal_bf16((N, K), 700 + N)
+    W = normal_bf16((M, K), 800 + M, scale=K ** -0.5)
+    y = vm.linear(to_dev(x), to_dev(W))["y"]
+    torch.cuda.synchronize()
+    rows = slice(None, None, 8) if N > 64 else slice(None)
+    ref = orc.linear(x[rows], W)
+    mx, mn = maxmean(dev_f32(y)[rows], ref)
+    print(f"linear {M}x{N}x{K}: max {mx:.3e} mean {mn:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN
+
+
+def _layer(vm, cfg, seed):
+    qw = normal_bf16((D,), seed + 1, scale=0.05)
+    kw = normal_bf16((D,), seed + 2, scale=0.05)
+    Wqkv = normal_bf16((S * D, DM), seed + 6, scale=DM ** -0.5)
+    Wo = normal_bf16((DM, HQ * D), seed + 7, scale=(HQ * D) ** -0.5)
+    return qw, kw, Wqkv, Wo
+
+
+def test_decode_layer_config1(vm, orc):
+    """BASELINE config 1 through the whole layer: xn -> qkv GEMV -> gated decode
+    -> Wo GEMV -> h, against the oracle; the appended cache row too."""
+    banner("decode layer config1 B=1 ctx=512 pos=512")
+    B, ctx, pos = 1, 512, 512
+    cfg = vm.AttnConfig(D=DM, Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx,
+                        B=B)
+    qw, kw, Wqkv, Wo = _layer(vm, cfg, 1000)
+    kc, vc = normal_bf16((B, HK, ctx, D), 1003), normal_bf16((B, HK, ctx, D), 1004)
+    xn = normal_bf16((B, DM), 1005)
+    m = vm.AttnModel(cfg)
+    layer = vm.AttnLayer(qw=to_dev(qw), kw=to_dev(kw), K_cache=to_dev(kc), V_cache=to_dev(vc),
+                         Wqkv=to_dev(Wqkv), Wo=to_dev(Wo))
+    gen = vm.Generation(B)
+    gen.positions.fill_(pos)
+    h = torch.empty((B, DM), dtype=torch.bfloat16, device="cuda")
+    vm.decode_(h, layer, m, gen, to_dev(xn))
+    torch.cuda.synchronize()
+    c, s = orc.rope_tables(HALF, ctx, THETA)
+    ref, kn, _ = orc.decode_layer(xn, Wqkv, Wo, kc, vc, np.array([pos], np.int32), qw, kw, c, s,
+                                  Hq=HQ, Hk=HK, eps=EPS, w_offset=1.0)
+    mx, mn = maxmean(dev_f32(h), ref)
+    kmx, _ = maxmean(bf16_to_f32(from_dev(layer.K_cache)[0, :, pos - 1]), kn[0])
+    print(f"decode layer: h max {mx:.3e} mean {mn:.3e} (|h| max {np.abs(ref).max():.3f}); "
+          f"K max {kmx:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN and kmx <= TOL_MAX
+
+
+def test_prefill_layer_config2(vm, orc):
+    """BASELINE config 2 through the whole layer: xn -> qkv GEMM -> gated prefill
+    -> Wo GEMM -> h, T = 4096; every 16th row against the oracle."""
+    banner("prefill layer config2 T=4096")
+    B, T = 1, 4096
+    cfg = vm.AttnConfig(D=DM, Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=T,
+                        B=B)
+    qw, kw, Wqkv, Wo = _layer(vm, cfg, 2000)
+    xn = normal_bf16((B, T, DM), 2005)
+    m = vm.AttnModel(cfg)
+    layer = vm.attn_layer(cfg, to_dev(qw), to_dev(kw), Wqkv=to_dev(Wqkv), Wo=to_dev(Wo))
+    h = vm.forward(layer, m, to_dev(xn), T, B)
+    torch.cuda.synchronize()
+    zero = np.zeros((B, HK, T, D), np.uint16)
+    c, s = orc.rope_tables(HALF, T, THETA)
+    ref, kn, _ = orc.prefill_layer(xn, Wqkv, Wo, zero, zero, np.zeros(B, np.int32),
+                                   np.full(B, T, np.int32), qw, kw, c, s, Hq=HQ, Hk=HK, eps=EPS,
+                                   w_offset=1.0, row_step=16)
+    got = dev_f32(h)
+    fin = ~np.isnan(ref)
+    mx, mn = maxmean(got[fin], ref[fin])
+    # the appended rows against the oracle's K norm + RoPE of the GPU's own qkv
+    # (the projection is deterministic: the same plan gives the same bits); the
+    # oracle's own bf16 qkv differs from it by summation-order roundings
+    qkv_gpu = from_dev(vm.linear(to_dev(xn).reshape(T, DM), to_dev(Wqkv))["y"])
+    _, kn, _ = orc.gated_prefill(qkv_gpu.reshape(B, T, S, D), zero, zero, np.zeros(B, np.int32),
+                                 np.full(B, T, np.int32), qw, kw, c, s, Hq=HQ, Hk=HK, eps=EPS,
+                                 w_offset=1.0, row_step=T)
+    kmx, kmn = maxmean(bf16_to_f32(from_dev(layer.K_cache)[0]).reshape(HK, T, D), kn[0])
+    print(f"prefill layer: h max {mx:.3e} mean {mn:.3e} (|h| max {np.nanmax(np.abs(ref)):.3f}); "
+          f"K max {kmx:.3e} mean {kmn:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN and kmx <= TOL_MAX and kmn <= TOL_MEAN
+
+
+def test_decode_layer_graph_replay(vm, orc):
+    """The whole layer step (qkv GEMV, gated attention, Wo GEMV, clock advance)
+    captured once in a hipGraph; 16 replays equal 16 eager steps bit for bit,
+    hidden states and cache rows (generate.jl:136-137, 185-191)."""
+    banner("decode layer graph replay B=4 ctx=2048")
+    B, ctx, n = 4, 2048, 16
+    p0 = np.array([1500, 7, 2000, 640], np.int32)
+    cfg = vm.AttnConfig(D=DM, Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx,
+                        B=B)
+    qw, kw, Wqkv, Wo = _layer(vm, cfg, 3000)
+    K0 = to_dev(normal_bf16((B, HK, ctx, D), 3003))
+    V0 = to_dev(normal_bf16((B, HK, ctx, D), 3004))
+    xn = to_dev(normal_bf16((B, DM), 3005))
+    m = vm.AttnModel(cfg)
+    layer = vm.AttnLayer(qw=to_dev(qw), kw=to_dev(kw), K_cache=K0.clone(), V_cache=V0.clone(),
+                         Wqkv=to_dev(Wqkv), Wo=to_dev(Wo))
+    h = torch.empty((B, DM), dtype=torch.bfloat16, device="cuda")
+    gen = vm.Generation(B)
+    gen.positions.copy_(i32(p0))
+    eager = []
+    for _ in range(n):
+        vm.decode_(h, layer, m, gen, xn, advance=True)
+        eager.append(h.clone())
+    torch.cuda.synchronize()
+    K_e, V_e = layer.K_cache.clone(), layer.V_cache.clone()
+    layer.K_cache.copy_(K0)
+    layer.V_cache.copy_(V0)
+    gen.positions.copy_(i32(p0))
+    torch.cuda.synchronize()
+    sess = vm.CaptureSession().capture(lambda: vm.decode_(h, layer, m, gen, xn, advance=True))
+    replay = []
+    for _ in range(n):
+        sess.launch()
+        replay.append(h.clone())
+    torch.cuda.synchronize()
+    sess.close()
+    assert np.array_equal(gen.positions.cpu().numpy(), p0 + n)
+    for a, b in zip(eager, replay):
+        assert torch.equal(a, b)
+    assert torch.equal(K_e, layer.K_cache) and torch.equal(V_e, layer.V_cache)
+    assert torch.isfinite(replay[-1].float()).all()

@@ -70,7 +70,7 @@ def _fused(vm, orc, B, T, ctx, prior, qlen, seed, row_step=1, fill_gpu=False):
     qkv = normal_bf16((B, T, S, D), seed + 5)
     m = vm.AttnModel(cfg)
     layer = vm.AttnLayer(qw=to_dev(qw), kw=to_dev(kw), K_cache=K, V_cache=V)
-    out = vm.forward(layer, m, to_dev(qkv), T, B, prior=i32(prior), q_lengths=i32(qlen))
+    out = vm.gated_attn_prefill(layer, m, to_dev(qkv), T, B, prior=i32(prior), q_lengths=i32(qlen))
     torch.cuda.synchronize()
     got = dev_f32(out).reshape(B, T, HQ, D)
     c, s = orc.rope_tables(HALF, ctx, THETA)
@@ -143,7 +143,7 @@ def test_fused_append_equals_standalone_append(vm):
     vc0 = to_dev(normal_bf16((B, HK, ctx, D), 74))
     qkv = to_dev(normal_bf16((B, T, S, D), 75))
     la = vm.AttnLayer(qw=qw, kw=kw, K_cache=kc0.clone(), V_cache=vc0.clone())
-    vm.forward(la, m, qkv, T, B, prior=i32(prior), q_lengths=i32(qlen))
+    vm.gated_attn_prefill(la, m, qkv, T, B, prior=i32(prior), q_lengths=i32(qlen))
     K, V = kc0.clone(), vc0.clone()
     pr, ql = i32(prior), i32(qlen)  # held: the C ABI takes bare device pointers
     call("vm_prefill_kv_append", ops._p(K), ops._p(V), K.stride(2), K.stride(1), K.stride(0), ctx,
@@ -165,13 +165,13 @@ def test_decode_equals_last_prefill_row(vm):
     qkv = to_dev(normal_bf16((B, T, S, D), 83))
     m = vm.AttnModel(cfg)
     la = vm.attn_layer(cfg, qw, kw)
-    full = vm.forward(la, m, qkv, T, B)
+    full = vm.gated_attn_prefill(la, m, qkv, T, B)
     lb = vm.attn_layer(cfg, qw, kw)
-    vm.forward(lb, m, qkv[:, :T - 1].contiguous(), T - 1, B)
+    vm.gated_attn_prefill(lb, m, qkv[:, :T - 1].contiguous(), T - 1, B)
     gen = vm.Generation(B)
     gen.positions.fill_(T)
     O = torch.empty((B, HQ, D), dtype=torch.bfloat16, device="cuda")
-    vm.decode_(O, lb, m, gen, qkv[:, T - 1].contiguous())
+    vm.gated_attn_decode_(O, lb, m, gen, qkv[:, T - 1].contiguous())
     torch.cuda.synchronize()
     a = full.reshape(B, T, HQ, D)[:, T - 1].float().cpu().numpy()
     b = O.float().cpu().numpy()
@@ -189,10 +189,10 @@ def test_chunked_equals_full_prefill(vm):
     qkv = to_dev(normal_bf16((B, T, S, D), 93))
     m = vm.AttnModel(cfg)
     la = vm.attn_layer(cfg, qw, kw)
-    full = vm.forward(la, m, qkv, T, B)
+    full = vm.gated_attn_prefill(la, m, qkv, T, B)
     lb = vm.attn_layer(cfg, qw, kw)
-    vm.forward(lb, m, qkv[:, :P].contiguous(), P, B)
-    part = vm.forward(lb, m, qkv[:, P:].contiguous(), T - P, B, offset=P)
+    vm.gated_attn_prefill(lb, m, qkv[:, :P].contiguous(), P, B)
+    part = vm.gated_attn_prefill(lb, m, qkv[:, P:].contiguous(), T - P, B, offset=P)
     torch.cuda.synchronize()
     mx, mn = maxmean(full[:, P:].float().cpu().numpy(), part.float().cpu().numpy())
     assert mx <= 1e-2 and mn <= 1e-3
@@ -249,7 +249,7 @@ def test_fused_prefill_online_max_path(vm, orc):
     qlen = np.array([384, 300], np.int32)
     m = vm.AttnModel(cfg)
     layer = vm.AttnLayer(qw=to_dev(qw), kw=to_dev(kw), K_cache=to_dev(kc), V_cache=to_dev(vc))
-    out = vm.forward(layer, m, to_dev(qkv), T, B, prior=i32(prior), q_lengths=i32(qlen))
+    out = vm.gated_attn_prefill(layer, m, to_dev(qkv), T, B, prior=i32(prior), q_lengths=i32(qlen))
     torch.cuda.synchronize()
     c, s = orc.rope_tables(HALF, ctx, THETA)
     ref, _, _ = orc.gated_prefill(qkv, kc, vc, prior, qlen, qw, kw, c, s, Hq=HQ, Hk=HK, eps=EPS,

@@ -287,3 +287,50 @@ def test_chunked_prefill_matches_full_prefill(orc):
     # the cached prefix went through one bf16 rounding of K
     assert np.max(np.abs(part[:, :T - P] - full[:, P:])) < 1e-2
     assert np.mean(np.abs(part[:, :T - P] - full[:, P:])) < 1e-3
+
+
+def test_linear_matches_torch_matmul(orc):
+    """orc.linear (y = W^T x, src/linear.jl:40-57) against torch.matmul in fp32 on
+    the CPU, for a GEMV (one column), a thin and a square problem; and two closed
+    forms: W = identity gives y = x, and scaling x by 2 scales y by 2 exactly."""
+    import torch
+    from oracle.rng import bf16_to_f32, f32_to_bf16, normal_bf16
+    for (N, K, M) in [(1, 256, 96), (7, 320, 130), (64, 128, 64)]:
+        x = normal_bf16((N, K), 500 + K)
+        W = normal_bf16((M, K), 600 + M, scale=K ** -0.5)
+        y = orc.linear(x, W)
+        ref = (torch.from_numpy(bf16_to_f32(x)) @ torch.from_numpy(bf16_to_f32(W)).T).numpy()
+        assert y.shape == (N, M)
+        assert np.max(np.abs(y - ref)) <= 1e-4 * max(1.0, np.max(np.abs(ref)))
+    x = normal_bf16((5, 64), 7)
+    eye = f32_to_bf16(np.eye(64, dtype=np.float32))
+    assert np.array_equal(orc.linear(x, eye), bf16_to_f32(x))
+    x2 = f32_to_bf16(2.0 * bf16_to_f32(x))
+    W = normal_bf16((33, 64), 8)
+    assert np.array_equal(orc.linear(x2, W), 2.0 * orc.linear(x, W))
+
+
+def test_decode_layer_is_the_composition(orc):
+    """orc.decode_layer = Wo-projection of the bf16-rounded gated decode of the
+    bf16-rounded qkv projection (qwen35.jl:193-206), recomposed here with torch
+    matmuls for the two projections."""
+    import torch
+    from conftest import D, EPS, HALF, HK, HQ, S, THETA
+    from oracle.rng import bf16_to_f32, f32_to_bf16, normal_bf16
+    B, ctx, Dm = 2, 64, 96
+    xn = normal_bf16((B, Dm), 11)
+    Wqkv = normal_bf16((S * D, Dm), 12, scale=Dm ** -0.5)
+    Wo = normal_bf16((Dm, HQ * D), 13, scale=(HQ * D) ** -0.5)
+    kc, vc = normal_bf16((B, HK, ctx, D), 14), normal_bf16((B, HK, ctx, D), 15)
+    qw, kw = normal_bf16((D,), 16, scale=0.05), normal_bf16((D,), 17, scale=0.05)
+    pos = np.array([64, 9], np.int32)
+    c, s = orc.rope_tables(HALF, ctx, THETA)
+    h, _, _ = orc.decode_layer(xn, Wqkv, Wo, kc, vc, pos, qw, kw, c, s, Hq=HQ, Hk=HK, eps=EPS,
+                               w_offset=1.0)
+    t = lambda a: torch.from_numpy(bf16_to_f32(a))
+    qkv = f32_to_bf16((t(xn) @ t(Wqkv).T).numpy()).reshape(B, S, D)
+    o, _, _ = orc.gated_decode(qkv, kc, vc, pos, qw, kw, c, s, Hq=HQ, Hk=HK, eps=EPS, w_offset=1.0)
+    ref = (t(f32_to_bf16(o).reshape(B, HQ * D)) @ t(Wo).T).numpy()
+    # torch sums in another order, so a few bf16 roundings of qkv / o flip by one ulp
+    assert np.max(np.abs(h - ref)) <= 2e-3 and np.mean(np.abs(h - ref)) <= 1e-4
+    assert np.max(np.abs(ref)) > 0.1

@@ -13,10 +13,10 @@ from ._lib import (ArgumentError, BoundsError, DimensionMismatch, HIPError,  # n
                    LIB_PATH, EXPORTED)
 from .sizes import sizes  # noqa: F401
 from .ops import (attention, attention_, decode_attention, decode_attention_,  # noqa: F401
-                  decode_scratch_bytes, fill_normal_, knorm_rope_append_, qnorm_rope_,
-                  rope_tables, sigmoid, sigmoid_gate_)
+                  decode_scratch_bytes, fill_normal_, knorm_rope_append_, linear, linear_,
+                  linear_workspace_bytes, qnorm_rope_, rope_tables, sigmoid, sigmoid_gate_)
 from .layer import (AttnConfig, AttnLayer, AttnModel, CaptureSession, Generation,  # noqa: F401
-                    attn_layer, decode_, forward)
+                    attn_layer, decode_, forward, gated_attn_decode_, gated_attn_prefill)
 from . import _lib  # noqa: F401
 
 __version__ = "0.1.0"

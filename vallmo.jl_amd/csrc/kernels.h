@@ -142,6 +142,16 @@ hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st);
 constexpr size_t DECODE_STATIC_SCRATCH_BYTES = VM_DECODE_STATIC_SCRATCH_BYTES;
 hipError_t decode_static_scratch(void** ptr);
 
+// Projections y = W^T x on hipBLASLt (linear.cpp): plan workspace size, and the
+// product on `st`. Return VM_OK, a VM_E_* code or a hipError_t, with the message
+// in err.
+constexpr size_t LINEAR_MAX_WORKSPACE_BYTES = (size_t)64 << 20;
+int linear_workspace(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, size_t* bytes,
+                     char* err, size_t errn);
+int linear_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w,
+               int64_t ldw, int M, int N, int K, void* workspace, size_t workspace_bytes,
+               hipStream_t st, char* err, size_t errn);
+
 // Decode stream partition shared by the scratch-size query and the launchers:
 // NW waves cover the token-heads sum_b len_b * Hk in equal contiguous chunks.
 constexpr int DECODE_MIN_CHUNK = 64;

@@ -1,0 +1,170 @@
+// linear.cpp — y = W^T x for the projections around the gated-attention block
+// (src/linear.jl:22-79): the qkv projection before it and Wo after it
+// (src/llm/qwen35.jl:194, :206, :296, :316-317). Host code only.
+//
+// Like the reference's cuBLASLt path, one plan per problem is built on first
+// use and cached for the process (linear.jl:17-38): hipBLASLt matmul
+// descriptor, matrix layouts and the heuristic's first algorithm, bf16 A/B/D
+// with fp32 compute and fp32 scaling (linear.jl:29). Column-major view, as in
+// the reference: x :: (K, N) with column stride ldx, W :: (K, M) (K-major) with
+// column stride ldw, y :: (M, N) with column stride ldy, so
+//     D (M x N) = op(A) B,  A = W (K x M, op = transpose), B = x (K x N).
+// The workspace comes from the caller (the reference takes it from the ambient
+// arena, linear.jl:62-66), so a warm call allocates nothing and can be
+// captured. There is no CPU or library fallback: a problem hipBLASLt has no
+// algorithm for is an error (VM_E_UNSUPPORTED).
+#include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <cstdio>
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "kernels.h"
+
+namespace vm {
+
+namespace {
+
+struct Plan {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  size_t workspace = 0;
+  bool ok = false;
+};
+
+using Key = std::tuple<int, int, int, int, int64_t, int64_t, int64_t>;  // dev, M, N, K, ldw, ldx, ldy
+
+std::mutex g_mu;
+std::map<int, hipblasLtHandle_t> g_handles;
+std::map<Key, Plan> g_plans;
+
+const char* status_name(hipblasStatus_t s) {
+  switch (s) {
+    case HIPBLAS_STATUS_SUCCESS: return "success";
+    case HIPBLAS_STATUS_NOT_INITIALIZED: return "not initialized";
+    case HIPBLAS_STATUS_ALLOC_FAILED: return "alloc failed";
+    case HIPBLAS_STATUS_INVALID_VALUE: return "invalid value";
+    case HIPBLAS_STATUS_ARCH_MISMATCH: return "arch mismatch";
+    case HIPBLAS_STATUS_EXECUTION_FAILED: return "execution failed";
+    case HIPBLAS_STATUS_NOT_SUPPORTED: return "not supported";
+    default: return "error";
+  }
+}
+
+// Builds (once) the plan of one problem on the current device. Returns 0, or a
+// VM_E_* / hipError_t code with `err` set.
+int get_plan(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, const Plan** out,
+             char* err, size_t errn) {
+  int dev = 0;
+  hipError_t he = hipGetDevice(&dev);
+  if (he != hipSuccess) {
+    snprintf(err, errn, "linear: hipGetDevice: %s", hipGetErrorString(he));
+    return (int)he;
+  }
+  std::lock_guard<std::mutex> lock(g_mu);
+  const Key key{dev, M, N, K, ldw, ldx, ldy};
+  auto it = g_plans.find(key);
+  if (it != g_plans.end()) {
+    if (!it->second.ok) {
+      snprintf(err, errn, "linear: hipBLASLt has no algorithm for M = %d, N = %d, K = %d", M, N, K);
+      return VM_E_UNSUPPORTED;
+    }
+    *out = &it->second;
+    return VM_OK;
+  }
+  hipblasLtHandle_t h;
+  auto hit = g_handles.find(dev);
+  if (hit == g_handles.end()) {
+    hipblasStatus_t s = hipblasLtCreate(&h);
+    if (s != HIPBLAS_STATUS_SUCCESS) {
+      snprintf(err, errn, "linear: hipblasLtCreate: %s", status_name(s));
+      return VM_E_UNSUPPORTED;
+    }
+    g_handles[dev] = h;
+  } else {
+    h = hit->second;
+  }
+  Plan p;
+  hipblasStatus_t s = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
+  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  if (s == HIPBLAS_STATUS_SUCCESS)
+    s = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta);
+  if (s == HIPBLAS_STATUS_SUCCESS)
+    s = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb);
+  if (s == HIPBLAS_STATUS_SUCCESS) s = hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, K, M, ldw);
+  if (s == HIPBLAS_STATUS_SUCCESS) s = hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, K, N, ldx);
+  if (s == HIPBLAS_STATUS_SUCCESS) s = hipblasLtMatrixLayoutCreate(&p.d, HIP_R_16BF, M, N, ldy);
+  hipblasLtMatmulPreference_t pref = nullptr;
+  if (s == HIPBLAS_STATUS_SUCCESS) s = hipblasLtMatmulPreferenceCreate(&pref);
+  const uint64_t cap = LINEAR_MAX_WORKSPACE_BYTES;
+  if (s == HIPBLAS_STATUS_SUCCESS)
+    s = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &cap,
+                                              sizeof cap);
+  // the heuristic's ranking, first candidate within the workspace cap (the cap
+  // preference alone does not bound what it returns)
+  constexpr int NREQ = 8;
+  hipblasLtMatmulHeuristicResult_t res[NREQ];
+  int n_res = 0;
+  if (s == HIPBLAS_STATUS_SUCCESS)
+    s = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.d, p.d, pref, NREQ, res, &n_res);
+  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  for (int i = 0; s == HIPBLAS_STATUS_SUCCESS && i < n_res; ++i) {
+    if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > cap) continue;
+    p.algo = res[i].algo;
+    p.workspace = res[i].workspaceSize;
+    p.ok = true;
+    break;
+  }
+  auto& slot = g_plans[key];  // remembered either way (linear.jl:20-21)
+  slot = p;
+  if (!slot.ok) {
+    snprintf(err, errn, "linear: hipBLASLt has no algorithm for M = %d, N = %d, K = %d (%s)", M,
+             N, K, status_name(s));
+    return VM_E_UNSUPPORTED;
+  }
+  *out = &slot;
+  return VM_OK;
+}
+
+}  // namespace
+
+int linear_workspace(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, size_t* bytes,
+                     char* err, size_t errn) {
+  const Plan* p = nullptr;
+  const int rc = get_plan(M, N, K, ldw, ldx, ldy, &p, err, errn);
+  if (rc == VM_OK) *bytes = p->workspace;
+  return rc;
+}
+
+int linear_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w,
+               int64_t ldw, int M, int N, int K, void* workspace, size_t workspace_bytes,
+               hipStream_t st, char* err, size_t errn) {
+  const Plan* p = nullptr;
+  int rc = get_plan(M, N, K, ldw, ldx, ldy, &p, err, errn);
+  if (rc != VM_OK) return rc;
+  if (p->workspace > 0 && (workspace == nullptr || workspace_bytes < p->workspace)) {
+    snprintf(err, errn, "linear: workspace of %zu bytes < %zu required (vm_linear_workspace_bytes)",
+             workspace_bytes, p->workspace);
+    return VM_E_SCRATCH;
+  }
+  hipblasLtHandle_t h;
+  {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lock(g_mu);
+    h = g_handles[dev];
+  }
+  const float alpha = 1.0f, beta = 0.0f;
+  const hipblasStatus_t s = hipblasLtMatmul(h, p->desc, &alpha, w, p->a, x, p->b, &beta, y, p->d, y,
+                                            p->d, &p->algo, workspace, p->workspace, st);
+  if (s != HIPBLAS_STATUS_SUCCESS) {
+    snprintf(err, errn, "linear: hipblasLtMatmul: %s", status_name(s));
+    return VM_E_UNSUPPORTED;
+  }
+  return VM_OK;
+}
+
+}  // namespace vm

@@ -615,6 +615,32 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm
                     "gated_attn_prefill");
 }
 
+// ---- f1: linear ------------------------------------------------------------
+static int linear_check(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy) {
+  REQUIRE(M > 0 && N > 0 && K > 0, VM_E_ARG, "linear: M = %d, N = %d, K = %d", M, N, K);
+  REQUIRE(ldw >= K && ldx >= K && ldy >= M, VM_E_DIM,
+          "linear: leading dimensions (W %lld, x %lld, y %lld) below (K, K, M) = (%d, %d, %d)",
+          (long long)ldw, (long long)ldx, (long long)ldy, K, K, M);
+  return VM_OK;
+}
+
+size_t vm_linear_workspace_bytes(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy) {
+  if (linear_check(M, N, K, ldw, ldx, ldy) != VM_OK) return (size_t)-1;
+  size_t n = 0;
+  if (vm::linear_workspace(M, N, K, ldw, ldx, ldy, &n, g_err, sizeof g_err) != VM_OK)
+    return (size_t)-1;
+  return n;
+}
+
+int vm_linear(vm_bf16* y, int64_t ldy, const vm_bf16* x, int64_t ldx, const vm_bf16* w,
+              int64_t ldw, int M, int N, int K, void* workspace, size_t workspace_bytes,
+              vm_stream st) {
+  TRY(linear_check(M, N, K, ldw, ldx, ldy));
+  REQUIRE(y && x && w, VM_E_ARG, "linear: NULL pointer argument");
+  return vm::linear_run(y, ldy, x, ldx, w, ldw, M, N, K, workspace, workspace_bytes, S(st), g_err,
+                        sizeof g_err);
+}
+
 // ---- synthetic inputs ------------------------------------------------------
 int vm_fill_normal_bf16(vm_bf16* dst, int64_t n, uint64_t seed, float scale, float shift,
                         vm_stream st) {

@@ -1,15 +1,20 @@
 """Attention-layer verbs and the decode clock — src/llm/qwen35.jl and generate.jl.
 
-The reference's ``decode!(h, l::AttnLayer, m, gen, xn)`` and
-``forward(l::AttnLayer, m, xn, T, B; offset)`` bracket the attention block
-between the qkv projection and the Wo projection (cuBLASLt GEMMs, outside this
-path). Here the verbs start from the packed projection ``qkv`` and end at the
-Wo input, which is exactly the part that runs on the gated-attention kernels:
+The reference's layer verbs run hidden state -> hidden state: the qkv
+projection, the gated attention block, the Wo projection (linear!, hipBLASLt
+here as cuBLASLt there):
 
-    decode_(O, l, m, gen, qkv)           qwen35.jl:195-205 (after the qkv GEMV,
-                                         before the Wo GEMV)
-    forward(l, m, qkv, T, B; offset)     qwen35.jl:293-317 (after the qkv GEMM,
-                                         returns the (Dh*Hq, T*B) Wo input)
+    decode_(h, l, m, gen, xn)            decode!(h, l::AttnLayer, m, gen, xn),
+                                         qwen35.jl:187-208
+    forward(l, m, xn, T, B; offset)      forward(l::AttnLayer, m, xn, T, B; offset),
+                                         qwen35.jl:292-318
+
+and their attention parts, from the packed projection ``qkv`` to the Wo input,
+are the fused gated-attention kernels:
+
+    gated_attn_decode_(O, l, m, gen, qkv)        qwen35.jl:195-205
+    gated_attn_prefill(l, m, qkv, T, B; offset)  qwen35.jl:293-317 (returns the
+                                                 (Dh*Hq, T*B) Wo input)
 
 Packed projection slots per token (qwen35.jl:189-192): [q1 g1 q2 g2 .. qHq gHq |
 k1..kHkv | v1..vHkv], each Dh wide. The KV cache layout (Dh, Ctx, Hkv, B) of
@@ -29,7 +34,9 @@ from .sizes import sizes
 
 @dataclass(frozen=True)
 class AttnConfig:
-    """The attention facts of a Qwen3.5 text config (qwen35.jl:82-96)."""
+    """The attention facts of a Qwen3.5 text config (qwen35.jl:82-96); D is the
+    hidden size (the projections' other side)."""
+    D: int = 2560
     Hq: int = 16
     Hkv: int = 4
     Dh: int = 256
@@ -42,25 +49,34 @@ class AttnConfig:
 
 @dataclass
 class AttnLayer:
-    """qwen35.jl:129-142: norm weights and the layer's own KV cache."""
+    """qwen35.jl:129-142: norm weights, the layer's own KV cache, and the two
+    projections (K-major, the checkpoint's orientation; None for callers of the
+    attention part only)."""
     qw: torch.Tensor            # (Dh,) bf16, applied as (w + 1)
     kw: torch.Tensor            # (Dh,) bf16
     K_cache: torch.Tensor       # (Dh, Ctx, Hkv, B) -> torch (B, Hkv, Ctx, Dh) bf16
     V_cache: torch.Tensor
+    Wqkv: torch.Tensor | None = None   # (D, Dh*(2Hq+2Hkv)) -> torch (Dh*(2Hq+2Hkv), D)
+    Wo: torch.Tensor | None = None     # (Dh*Hq, D) -> torch (D, Dh*Hq)
 
 
-def attn_layer(cfg: AttnConfig, qw: torch.Tensor, kw: torch.Tensor) -> AttnLayer:
+def attn_layer(cfg: AttnConfig, qw: torch.Tensor, kw: torch.Tensor, Wqkv=None,
+               Wo=None) -> AttnLayer:
     """Allocate a layer with zeroed caches (qwen35.jl:138-139)."""
     shape = (cfg.B, cfg.Hkv, cfg.Ctx, cfg.Dh)
     return AttnLayer(qw=qw, kw=kw,
                      K_cache=torch.zeros(shape, dtype=torch.bfloat16, device="cuda"),
-                     V_cache=torch.zeros(shape, dtype=torch.bfloat16, device="cuda"))
+                     V_cache=torch.zeros(shape, dtype=torch.bfloat16, device="cuda"),
+                     Wqkv=Wqkv, Wo=Wo)
 
 
 class AttnModel:
     """The model-level state the attention verbs read: cfg, RoPE tables and the
-    decode scratch space (the reference's Arena, qwen35.jl:110) sized once so a
-    captured step replays the same addresses."""
+    decode space (the reference's Arena, qwen35.jl:110), allocated once so a
+    captured step replays the same addresses: the split-KV scratch, the
+    projections' workspace, and the decode step's qkv and attention-output
+    buffers (the layer frame's temporaries, qwen35.jl:193)."""
+
 
     def __init__(self, cfg: AttnConfig, *, n_splits: int = 0):
         self.cfg = cfg
@@ -70,6 +86,25 @@ class AttnModel:
             cfg.B, cfg.Hq, cfg.Hkv, cfg.Dh, cfg.Ctx, self.n_splits))
         self.space = torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda")
         self.prefill_space = None
+        self.lin_space = None
+        self.qkv = None
+        self.attn_out = None
+
+    def linear_workspace(self, need: int = 0) -> torch.Tensor:
+        """The projections' workspace, grown to `need` bytes (eager calls size it;
+        a captured step then replays with the buffer its warm-up calls sized)."""
+        if self.lin_space is None or self.lin_space.numel() < need:
+            self.lin_space = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
+        return self.lin_space
+
+    def decode_buffers(self):
+        """(qkv (B, 2Hq+2Hkv, Dh), O (B, Hq, Dh)) bf16, allocated on first use."""
+        if self.qkv is None:
+            c = self.cfg
+            self.qkv = torch.empty((c.B, 2 * c.Hq + 2 * c.Hkv, c.Dh), dtype=torch.bfloat16,
+                                   device="cuda")
+            self.attn_out = torch.empty((c.B, c.Hq, c.Dh), dtype=torch.bfloat16, device="cuda")
+        return self.qkv, self.attn_out
 
     def prefill_workspace(self, B: int, ctx: int) -> torch.Tensor:
         """The prefill workspace (V staged transposed), grown on demand and kept,
@@ -103,7 +138,8 @@ def _qkv_views(qkv, cfg):
     return q, g, k, v
 
 
-def decode_(O, l: AttnLayer, m: AttnModel, gen: Generation, qkv, *, advance: bool = False):
+def gated_attn_decode_(O, l: AttnLayer, m: AttnModel, gen: Generation, qkv, *,
+                       advance: bool = False):
     """One decode step of the attention block (qwen35.jl:195-205), fused:
     qnorm_rope! + knorm_rope_append! + decode_attention + ``O .*= sigmoid.(q_gate)``.
 
@@ -129,8 +165,8 @@ def decode_(O, l: AttnLayer, m: AttnModel, gen: Generation, qkv, *, advance: boo
     return O
 
 
-def forward(l: AttnLayer, m: AttnModel, qkv, T: int, B: int, *, offset: int = 0,
-            prior=None, q_lengths=None, out=None):
+def gated_attn_prefill(l: AttnLayer, m: AttnModel, qkv, T: int, B: int, *, offset: int = 0,
+                       prior=None, q_lengths=None, out=None):
     """Prefill / chunked prefill of the attention block (qwen35.jl:293-317), fused:
     head_rmsnorm + apply_rope of q and k, the K/V cache write at columns
     offset+1..offset+T, causal attention over columns 1..offset+T, and the
@@ -183,6 +219,53 @@ def forward(l: AttnLayer, m: AttnModel, qkv, T: int, B: int, *, offset: int = 0,
          ops._p(m.rope["sin"]), ops._p(prior), ops._p(q_lengths), B, T, cfg.Hq, cfg.Hkv, cfg.Dh,
          cfg.rot_half, float(cfg.eps), 1.0, ops._p(ws), ws.numel(), ops._stream())
     return out
+
+
+def _need_proj(l: AttnLayer, cfg: AttnConfig):
+    S = 2 * cfg.Hq + 2 * cfg.Hkv
+    if l.Wqkv is None or l.Wo is None:
+        raise ArgumentError("this layer has no projections (Wqkv, Wo)")
+    sizes(Wqkv=(l.Wqkv, f"{cfg.D} {S * cfg.Dh}"), Wo=(l.Wo, f"{cfg.Hq * cfg.Dh} {cfg.D}"))
+
+
+def decode_(h, l: AttnLayer, m: AttnModel, gen: Generation, xn, *, advance: bool = False):
+    """decode!(h, l::AttnLayer, m, gen, xn) — qwen35.jl:187-208, hidden state to
+    hidden state for one token per sequence: qkv = linear(xn, Wqkv) (:194), the
+    fused gated attention (:195-205) into O, h = linear(O, Wo) (:206). xn, h ::
+    (D, B) (torch (B, D)). The temporaries are the model's decode buffers, so the
+    step allocates nothing once warm (capturable with ``advance``)."""
+    cfg = m.cfg
+    _need_proj(l, cfg)
+    d = sizes(xn=(xn, f"{cfg.D} B"), h=(h, f"{cfg.D} B"))
+    if d["B"] != cfg.B:
+        raise DimensionMismatch(f"size(xn, 2) = {d['B']} does not match B = {cfg.B}")
+    qkv, O = m.decode_buffers()
+    q2, O2 = qkv.view(cfg.B, -1), O.view(cfg.B, -1)
+    ws = m.linear_workspace(max(ops.linear_workspace_bytes(xn, l.Wqkv, q2),
+                                ops.linear_workspace_bytes(O2, l.Wo, h)))
+    ops.linear_({"y": q2}, xn, l.Wqkv, workspace=ws)
+    gated_attn_decode_(O, l, m, gen, qkv, advance=advance)
+    ops.linear_({"y": h}, O2, l.Wo, workspace=ws)
+    return h
+
+
+def forward(l: AttnLayer, m: AttnModel, xn, T: int, B: int, *, offset: int = 0, prior=None,
+            q_lengths=None):
+    """forward(l::AttnLayer, m, xn, T, B; offset) — qwen35.jl:292-318, hidden
+    state to hidden state for a prompt chunk: qkv = linear(xn, Wqkv) (:296), the
+    fused gated prefill (:297-315) into the Wo input, h = linear(·, Wo)
+    (:316-317). xn :: (D, T*B) (torch (B, T, D)); returns h, torch (B, T, D).
+    Eager: allocates its temporaries, as the reference's prefill does."""
+    cfg = m.cfg
+    _need_proj(l, cfg)
+    xn2 = xn.reshape(B * T, cfg.D)
+    qkv = ops.linear(xn2, l.Wqkv, workspace=m.linear_workspace(
+        ops.linear_workspace_bytes(xn2, l.Wqkv)))["y"]
+    o = gated_attn_prefill(l, m, qkv.view(B, T, 2 * cfg.Hq + 2 * cfg.Hkv, cfg.Dh), T, B,
+                           offset=offset, prior=prior, q_lengths=q_lengths)
+    o2 = o.reshape(B * T, cfg.Hq * cfg.Dh)
+    ws = m.linear_workspace(ops.linear_workspace_bytes(o2, l.Wo))
+    return ops.linear(o2, l.Wo, workspace=ws)["y"].view(B, T, cfg.D)
 
 
 class CaptureSession:

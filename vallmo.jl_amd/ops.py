@@ -23,7 +23,7 @@ from .sizes import sizes
 __all__ = [
     "rope_tables", "qnorm_rope_", "knorm_rope_append_", "attention_", "attention",
     "decode_attention_", "decode_attention", "decode_scratch_bytes", "sigmoid_gate_",
-    "sigmoid", "fill_normal_",
+    "sigmoid", "fill_normal_", "linear_", "linear", "linear_workspace_bytes",
 ]
 
 
@@ -205,6 +205,64 @@ def sigmoid_gate_(O, G):
     call("vm_sigmoid_gate", _p(O), O.stride(1), O.stride(0), _p(G), G.stride(1), G.stride(0),
          d["B"], d["H"], d["D"], _stream())
     return O
+
+
+def linear_workspace_bytes(x, W, y=None) -> int:
+    """Workspace the cached plan of this problem needs (builds the plan on first
+    use, linear.jl:22-38)."""
+    N, K = _rows(x), x.shape[-1]
+    M = W.shape[0]
+    ldy = M if y is None else y.stride(-2) if y.dim() > 1 else M
+    n = _lib.load().vm_linear_workspace_bytes(M, N, K, W.stride(0), _ld(x), ldy)
+    if n == ctypes.c_size_t(-1).value:
+        _lib.check(_lib.VM_E_UNSUPPORTED, "vm_linear_workspace_bytes")
+    return int(n)
+
+
+def _rows(t):
+    return 1 if t.dim() == 1 else int(t.numel() // t.shape[-1])
+
+
+def _ld(t):
+    """Column stride of the reference's column-major (K, N) view of a torch
+    (..., K) tensor whose leading dims collapse into N."""
+    if t.dim() == 1:
+        return t.shape[-1]
+    st = t.stride()
+    for d in range(t.dim() - 2, 0, -1):
+        if st[d - 1] != st[d] * t.shape[d]:
+            raise ArgumentError("leading dimensions must collapse into one column axis")
+    return st[-2]
+
+
+def linear_(outs, x, W, *, workspace=None):
+    """y .= W^T x — src/linear.jl:40-57 (hipBLASLt, fp32 accumulation).
+
+    x :: (K, N) (torch (..., K), leading dims collapse into N), W :: (K, M)
+    K-major (torch (M, K)), y :: (M, N) (torch (..., M)). ``workspace`` is a
+    uint8 GPU tensor of >= linear_workspace_bytes (the reference takes it from
+    the ambient arena, linear.jl:62-66); allocated here when None.
+    """
+    y = _out(outs, "y")
+    K, N, M = x.shape[-1], _rows(x), W.shape[0]
+    if W.dim() != 2 or W.shape[1] != K:
+        raise DimensionMismatch(f"size(W, 1) = {W.shape[-1]} does not match K = {K} (= size(x, 1))")
+    if y.shape[-1] != M or _rows(y) != N:
+        raise DimensionMismatch(f"y is ({y.shape[-1]}, {_rows(y)}), expected (M, N) = ({M}, {N})")
+    for t, n in ((x, "x"), (W, "W"), (y, "y")):
+        _need(t, torch.bfloat16, n)
+    need = linear_workspace_bytes(x, W, y)
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=x.device)
+    call("vm_linear", _p(y), _ld(y), _p(x), _ld(x), _p(W), W.stride(0), M, N, K,
+         _p(workspace), workspace.numel(), _stream())
+    return outs
+
+
+def linear(x, W, **kw) -> dict:
+    """Allocating linear (linear.jl:68-79): returns {"y": y}, torch (..., M)."""
+    y = torch.empty(tuple(x.shape[:-1]) + (W.shape[0],), dtype=x.dtype, device=x.device)
+    return linear_({"y": y}, x, W, **kw)
 
 
 def fill_normal_(X, seed: int, *, scale: float = 1.0, shift: float = 0.0):
