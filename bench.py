@@ -14,7 +14,9 @@ in a hipGraph and replayed 256 times with the position advancing on the device)
 in HBM GB/s of K/V actually attended (4096 B per token) + 32 KiB per sequence,
 and config 1 (B=1 at 512 tokens, launch-latency-bound) as time per step.
 Key "prefill_config5": BASELINE config 5 (B=4 ragged chunks after 8-32 K
-priors) in algorithmic TFLOP/s, step and attention kernel.
+priors) in algorithmic TFLOP/s, step and attention kernel. Key "layer": whole
+attention layers, hidden state to hidden state (the qkv and Wo projections on
+hipBLASLt around the block) at the config-2 prefill and config-3 decode shapes.
 
 ``roofline`` is for the dominant kernel (the prefill attention kernel): its
 launches, and only its, are bracketed by hipEvents on the launch stream inside
@@ -359,6 +361,102 @@ def bench_decode4(vm, torch, replays=256, seed=4):
     }
 
 
+DM = 2560   # hidden size of the layer benchmarks (the Qwen3.5 small-model width)
+
+
+def _event_ms(torch, fn, reps):
+    """Mean ms of fn() over reps launches on torch's current stream (events)."""
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def bench_layer(vm, torch, reps=20):
+    """Whole attention layers, hidden state to hidden state (qkv projection,
+    gated attention, Wo projection): the config-2 prefill layer (T = 4096) and the
+    config-3-shaped decode layer (B = 32), with the projections (hipBLASLt) timed
+    alone against their rooflines: GEMM FLOP / bf16 peak, GEMV weight bytes / HBM."""
+    res = {}
+    S_ = 2 * HQ + 2 * HK
+    # ---- prefill layer, config 2
+    T, B = 4096, 1
+    cfg = vm.AttnConfig(D=DM, Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=T, B=B)
+    qw = torch.empty(D, dtype=torch.bfloat16, device="cuda")
+    kw = torch.empty_like(qw)
+    vm.fill_normal_(qw, 2001, scale=0.05)
+    vm.fill_normal_(kw, 2002, scale=0.05)
+    Wqkv = torch.empty((S_ * D, DM), dtype=torch.bfloat16, device="cuda")
+    Wo = torch.empty((DM, HQ * D), dtype=torch.bfloat16, device="cuda")
+    vm.fill_normal_(Wqkv, 2006, scale=DM ** -0.5)
+    vm.fill_normal_(Wo, 2007, scale=(HQ * D) ** -0.5)
+    xn = torch.empty((B, T, DM), dtype=torch.bfloat16, device="cuda")
+    vm.fill_normal_(xn, 2005)
+    m = vm.AttnModel(cfg)
+    layer = vm.attn_layer(cfg, qw, kw, Wqkv=Wqkv, Wo=Wo)
+    fwd = lambda: vm.forward(layer, m, xn, T, B)
+    for _ in range(5):
+        fwd()
+    torch.cuda.synchronize()
+    t_layer = _event_ms(torch, fwd, reps)
+    x2 = xn.view(T, DM)
+    qkv = torch.empty((T, S_ * D), dtype=torch.bfloat16, device="cuda")
+    o = torch.empty((T, HQ * D), dtype=torch.bfloat16, device="cuda")
+    h = torch.empty((T, DM), dtype=torch.bfloat16, device="cuda")
+    ws = m.linear_workspace()
+    t_qkv = _event_ms(torch, lambda: vm.linear_({"y": qkv}, x2, Wqkv, workspace=ws), reps)
+    t_wo = _event_ms(torch, lambda: vm.linear_({"y": h}, o, Wo, workspace=ws), reps)
+    f_qkv, f_wo = 2.0 * T * DM * S_ * D, 2.0 * T * HQ * D * DM
+    f_attn = prefill_flops(T)
+    res["prefill_config2"] = {
+        "ms_per_layer": t_layer,
+        "tflops_layer": (f_qkv + f_wo + f_attn) / (t_layer * 1e-3) / 1e12,
+        "qkv_gemm_ms": t_qkv, "qkv_gemm_tflops": f_qkv / (t_qkv * 1e-3) / 1e12,
+        "qkv_gemm_frac_of_bf16_peak": f_qkv / (t_qkv * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+        "wo_gemm_ms": t_wo, "wo_gemm_tflops": f_wo / (t_wo * 1e-3) / 1e12,
+        "wo_gemm_frac_of_bf16_peak": f_wo / (t_wo * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+        "shape": f"hidden {DM}, T {T}: qkv {T}x{DM} -> {S_ * D}, Wo {T}x{HQ * D} -> {DM}",
+    }
+    del layer, m, qkv, o, h, xn, x2
+    # ---- decode layer, config-3 shape (B = 32, lengths ~U{1024..32768})
+    B, ctx = 32, 32768
+    lengths = np.random.default_rng(3).integers(1024, 32769, size=B).astype(np.int32)
+    cfg = vm.AttnConfig(D=DM, Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
+    m = vm.AttnModel(cfg)
+    layer = vm.attn_layer(cfg, qw, kw, Wqkv=Wqkv, Wo=Wo)
+    vm.fill_normal_(layer.K_cache, 303)
+    vm.fill_normal_(layer.V_cache, 304)
+    xd = torch.empty((B, DM), dtype=torch.bfloat16, device="cuda")
+    vm.fill_normal_(xd, 3005)
+    hd = torch.empty_like(xd)
+    gen = vm.Generation(B)
+    gen.positions.copy_(torch.from_numpy(lengths).cuda())
+    step = lambda: vm.decode_(hd, layer, m, gen, xd)
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    t_step = _event_ms(torch, step, reps)
+    qkv_d, O_d = m.decode_buffers()
+    ws = m.linear_workspace()
+    t_gv1 = _event_ms(torch, lambda: vm.linear_({"y": qkv_d.view(B, -1)}, xd, Wqkv, workspace=ws), reps)
+    t_gv2 = _event_ms(torch, lambda: vm.linear_({"y": hd}, O_d.view(B, -1), Wo, workspace=ws), reps)
+    b_qkv = 2.0 * (S_ * D * DM + B * DM + B * S_ * D)
+    b_wo = 2.0 * (DM * HQ * D + B * HQ * D + B * DM)
+    res["decode_config3"] = {
+        "ms_per_layer_step": t_step,
+        "kv_gbs_in_layer_step": decode_bytes(lengths) / (t_step * 1e-3) / 1e9,
+        "qkv_gemv_ms": t_gv1, "qkv_gemv_gbs": b_qkv / (t_gv1 * 1e-3) / 1e9,
+        "qkv_gemv_frac_of_hbm_peak": b_qkv / (t_gv1 * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        "wo_gemv_ms": t_gv2, "wo_gemv_gbs": b_wo / (t_gv2 * 1e-3) / 1e9,
+        "wo_gemv_frac_of_hbm_peak": b_wo / (t_gv2 * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        "shape": f"hidden {DM}, B {B}: qkv {B}x{DM} -> {S_ * D}, Wo {B}x{HQ * D} -> {DM}",
+    }
+    return res
+
+
 def cpu_info():
     """CPU model, sockets x physical cores per socket, and logical CPUs of this host."""
     import subprocess
@@ -502,6 +600,14 @@ def cpu_baseline(vm, torch):
                       "sample": f"the whole config5 problem ({fl / 1e12:.2f} TFLOP)"}
     del kc, vc
 
+    # ---- the Wo projection of the config-2 layer (fp32 GEMM, 4096 x 4096 -> 2560)
+    o = hb(_dev_normal(vm, torch, (4096, HQ * D), 2010))
+    Wo = hb(_dev_normal(vm, torch, (DM, HQ * D), 2007, (HQ * D) ** -0.5))
+    dt, n = _median_time(lambda: oracle.linear(o, Wo, nthreads=threads), 3, 3, 10.0)
+    fl = 2.0 * 4096 * HQ * D * DM
+    res["layer_wo_gemm"] = {"tflops": fl / dt / 1e12, "s_per_step": dt, "runs": n,
+                            "sample": f"the config-2 layer's Wo projection ({fl / 1e9:.1f} GFLOP)"}
+
     info = cpu_info()
     c2 = res["config2"]
     return {"value": c2["tflops"], "unit": "TFLOP/s", "cores": threads, "kind": "port",
@@ -520,6 +626,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-config5", action="store_true", help="skip the config-5 prefill leg")
+    ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer leg")
     ap.add_argument("--no-settle", action="store_true",
                     help="skip the clock-settle phase (counter-collection runs)")
     ap.add_argument("--no-decode", action="store_true")
@@ -576,6 +683,15 @@ def main():
         for d in (d3, d4, d1):
             d["frac_of_hbm_peak"] = d["gbs"] / PEAK_HBM_GBS
         decode = {"config3": d3, "config4": d4, "config1": d1, "peak_GBs": PEAK_HBM_GBS}
+    layer = None
+    if not args.no_layer:
+        log("[bench] layers (projections + attention), hidden 2560")
+        layer = bench_layer(vm, torch)
+        lp, ld = layer["prefill_config2"], layer["decode_config3"]
+        log(f"[bench] prefill layer: {lp['ms_per_layer']:.3f} ms, qkv GEMM {lp['qkv_gemm_tflops']:.0f} "
+            f"TFLOP/s, Wo GEMM {lp['wo_gemm_tflops']:.0f} TFLOP/s")
+        log(f"[bench] decode layer B=32: {ld['ms_per_layer_step']:.3f} ms, qkv GEMV "
+            f"{ld['qkv_gemv_gbs']:.0f} GB/s, Wo GEMV {ld['wo_gemv_gbs']:.0f} GB/s")
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle), configs 1-5")
@@ -614,6 +730,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill_config5": pf5,
         "decode": decode,
+        "layer": layer,
     }
     print(json.dumps(line), flush=True)
 

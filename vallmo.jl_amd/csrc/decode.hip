@@ -98,15 +98,6 @@ __device__ __forceinline__ int sload_len(const int32_t* lengths, int b) {
   return v;
 }
 
-__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(v, o, 64);
-    if (lane >= o) v += u;
-  }
-  return v;
-}
-
 struct StepBuf {
   uint4 k[8], v[8];
 };
@@ -223,8 +214,7 @@ __device__ __forceinline__ void append_row(StepBuf& s, const DecodeArgs& a, int 
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
   }
-  ss += __shfl_xor(ss, 16, 64);
-  ss += __shfl_xor(ss, 32, 64);
+  ss = col_sum4(ss);
   const float r = 1.0f / sqrtf(ss * (1.0f / HEAD_DIM) + a.eps);
   {
     // chunks 0 and 1 hold the rotate-half pairs (d, d + 32), d = 8g + j
@@ -284,8 +274,16 @@ __device__ __forceinline__ void seg_bounds(Seg& s, int pos, int gw1, const Decod
   s.hm = s.append ? s.hi - 1 : s.hi;
 }
 
+// lengths[b] for a wave-uniform b: from the register copy of the first 64
+// (lane b holds lengths[b]), else through a scalar load, which vmcnt does not
+// count, so reading it does not drain the K/V loads in flight
+__device__ __forceinline__ int seq_len_raw(const int32_t* lengths, int raw_l, int b) {
+  return b < 64 ? __builtin_amdgcn_readlane(raw_l, b) : sload_len(lengths, b);
+}
+
 // Move to the next non-empty segment of the chunk; false when the chunk ends.
-__device__ __forceinline__ bool seg_next(Seg& s, int gw1, const DecodeArgs& a, bool fused) {
+__device__ __forceinline__ bool seg_next(Seg& s, int gw1, const DecodeArgs& a, bool fused,
+                                         int raw_l) {
   const int pos = s.seg_b_start + s.hk * s.len + s.hi;
   if (pos >= gw1) return false;
   if (++s.hk == a.Hk) {
@@ -293,7 +291,7 @@ __device__ __forceinline__ bool seg_next(Seg& s, int gw1, const DecodeArgs& a, b
     s.seg_b_start += a.Hk * s.len;
     do {
       ++s.b;
-      s.raw = sload_len(a.lengths, s.b);
+      s.raw = seq_len_raw(a.lengths, raw_l, s.b);
       s.len = s.raw < 0 ? 0 : (s.raw > a.ctx ? (int)a.ctx : s.raw);
     } while (s.len == 0 && s.b + 1 < a.B);
   }
@@ -306,9 +304,9 @@ struct Issuer {
   Seg s;
   int t;
   __device__ __forceinline__ bool next(uint16_t* slot, const DecodeArgs& a, int gw1, int64_t last,
-                                       int lane, bool fused) {
+                                       int lane, bool fused, int raw_l) {
     while (t >= s.hm) {
-      if (!seg_next(s, gw1, a, fused)) return false;
+      if (!seg_next(s, gw1, a, fused, raw_l)) return false;
       t = s.lo;
     }
     const int64_t base = (int64_t)s.b * a.c_sb + (int64_t)s.hk * a.c_sh;
@@ -325,15 +323,33 @@ void decode_stream_kernel(DecodeArgs a) {
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int G = a.G, Hk = a.Hk;
-  // ---- stream partition: total work and this wave's chunk [gw0, gw1)
-  int W = 0;
-  for (int b0 = 0; b0 < a.B; b0 += 64) {
-    int v = (b0 + lane < a.B) ? clamp_len(a.lengths, b0 + lane, a.ctx) : 0;
+  // ---- first loads, independent of each other and all issued before any is
+  // used: lengths[lane] (the first 64 sequences, kept in a register for the
+  // partition, the segment search and the segment walk) and, fused, the norm
+  // weights (the same for every segment)
+  const int raw_l = lane < a.B ? a.lengths[lane] : 0;
+  uint2 kwv = make_uint2(0, 0);
+  uint4 qwv[8];
+  if (FUSED) {
+    kwv = *reinterpret_cast<const uint2*>(a.kw + 4 * lane);  // d = 4*lane .. +3
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    W += v;
+    for (int kk = 0; kk < 8; ++kk) qwv[kk] = load16(a.qw + 32 * kk + 8 * g);
   }
-  W = uniform(W * Hk);
+  const int len_l = raw_l < 0 ? 0 : (raw_l > a.ctx ? (int)a.ctx : raw_l);
+  // clamped lengths of sequences b0 + lane, b0 a multiple of 64
+  auto lens_at = [&](int b0) __attribute__((always_inline)) {
+    return b0 == 0 ? len_l : ((b0 + lane < a.B) ? clamp_len(a.lengths, b0 + lane, a.ctx) : 0);
+  };
+  // ---- stream partition: total work and this wave's chunk [gw0, gw1).
+  // incl_at(b0): inclusive prefix of len * Hk (token-heads) over sequences
+  // b0 .. b0 + lane, relative to b0
+  const int incl0 = wave_scan_add(len_l * Hk);
+  auto incl_at = [&](int b0) __attribute__((always_inline)) {
+    return b0 == 0 ? incl0 : wave_scan_add(lens_at(b0) * Hk);
+  };
+  int W = __builtin_amdgcn_readlane(incl0, 63);
+  for (int b0 = 64; b0 < a.B; b0 += 64) W += __builtin_amdgcn_readlane(incl_at(b0), 63);
+  W = uniform(W);
   const int chunk = stream_chunk(W, a.NW, a.min_chunk);
   if (w == 0) {
     // snapshot of the partition for the merge, which then never reads lengths
@@ -341,13 +357,13 @@ void decode_stream_kernel(DecodeArgs a) {
     // first token-head
     int pre = 0;
     for (int b0 = 0; b0 < a.B; b0 += 64) {
-      const int l = (b0 + lane < a.B) ? clamp_len(a.lengths, b0 + lane, a.ctx) : 0;
-      const int incl = wave_incl_scan(l * Hk, lane) + pre;
+      const int l = lens_at(b0);
+      const int incl = incl_at(b0) + pre;
       if (b0 + lane < a.B) {
         a.geom[1 + b0 + lane] = l;
         a.geom[1 + a.B + b0 + lane] = incl - l * Hk;
       }
-      pre = __shfl(incl, 63, 64);
+      pre = __builtin_amdgcn_readlane(incl, 63);
     }
     if (lane == 0) a.geom[0] = chunk;
   }
@@ -360,21 +376,21 @@ void decode_stream_kernel(DecodeArgs a) {
   {
     int pre = 0;
     for (int b0 = 0; b0 < a.B; b0 += 64) {
-      const int len = (b0 + lane < a.B) ? clamp_len(a.lengths, b0 + lane, a.ctx) : 0;
-      const int incl = wave_incl_scan(len * Hk, lane) + pre;
+      const int len = lens_at(b0);
+      const int incl = incl_at(b0) + pre;
       const uint64_t m = __ballot(b0 + lane < a.B && incl > gw0);
       if (m != 0ull) {
-        const int fl = __ffsll((unsigned long long)m) - 1;
+        const int fl = uniform(__ffsll((unsigned long long)m) - 1);
         b = b0 + fl;
-        seg_b_start = __shfl(incl - len * Hk, fl, 64);
+        seg_b_start = __builtin_amdgcn_readlane(incl - len * Hk, fl);
         break;
       }
-      pre = __shfl(incl, 63, 64);
+      pre = __builtin_amdgcn_readlane(incl, 63);
     }
   }
   b = uniform(b);
   seg_b_start = uniform(seg_b_start);
-  const int raw = a.lengths[b];
+  const int raw = seq_len_raw(a.lengths, raw_l, b);
   const int len = raw < 0 ? 0 : (raw > a.ctx ? (int)a.ctx : raw);
   const int hk = (gw0 - seg_b_start) / len;
 
@@ -394,14 +410,11 @@ void decode_stream_kernel(DecodeArgs a) {
   float kbound = 0.f;
   if (FUSED) {
     // |k~| <= sqrt(D) * max|kw + w_offset| (+ bf16 rounding of the cached rows)
-    const uint2 wv = *reinterpret_cast<const uint2*>(a.kw + 4 * lane);  // d = 4*lane .. +3
-    float wm = fmaxf(fmaxf(fabsf(__uint_as_float(wv.x << 16) + a.w_offset),
-                           fabsf(__uint_as_float(wv.x & 0xffff0000u) + a.w_offset)),
-                     fmaxf(fabsf(__uint_as_float(wv.y << 16) + a.w_offset),
-                           fabsf(__uint_as_float(wv.y & 0xffff0000u) + a.w_offset)));
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) wm = fmaxf(wm, __shfl_xor(wm, o, 64));
-    kbound = 16.0f * wm * 1.01f;
+    float wm = fmaxf(fmaxf(fabsf(__uint_as_float(kwv.x << 16) + a.w_offset),
+                           fabsf(__uint_as_float(kwv.x & 0xffff0000u) + a.w_offset)),
+                     fmaxf(fabsf(__uint_as_float(kwv.y << 16) + a.w_offset),
+                           fabsf(__uint_as_float(kwv.y & 0xffff0000u) + a.w_offset)));
+    kbound = 16.0f * wave_max_all(wm) * 1.01f;
   }
 
   // ---- one continuous 16-token step pipeline over the segments of the chunk:
@@ -435,13 +448,11 @@ void decode_stream_kernel(DecodeArgs a) {
           a.q + (int64_t)cs.b * a.q_sb + (int64_t)(cs.hk * G + nn) * a.q_sh + 8 * g;
       // every prologue load first; the first K/V steps go out right behind them
       // (loads return in order: the prologue math then runs under the K/V steps)
-      uint4 qraw[8], qwv[8];
+      uint4 qraw[8];
       float4 cv[2], sv[2];
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) qraw[kk] = load16(qp + 32 * kk);
       if (FUSED) {
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) qwv[kk] = load16(a.qw + 32 * kk + 8 * g);
         const int64_t p = cs.len - 1;  // fused decode: lengths are the positions
         const float4* cp = reinterpret_cast<const float4*>(a.cos_tab + p * HALF_ROT + 8 * g);
         const float4* sp = reinterpret_cast<const float4*>(a.sin_tab + p * HALF_ROT + 8 * g);
@@ -449,8 +460,8 @@ void decode_stream_kernel(DecodeArgs a) {
         sv[0] = sp[0]; sv[1] = sp[1];
       }
       if (!primed) {
-        if (is.next(r0, a, gw1, last, lane, FUSED)) ++inflight;
-        if (is.next(r1, a, gw1, last, lane, FUSED)) ++inflight;
+        if (is.next(r0, a, gw1, last, lane, FUSED, raw_l)) ++inflight;
+        if (is.next(r1, a, gw1, last, lane, FUSED, raw_l)) ++inflight;
         primed = true;
       }
       float x[8][8];
@@ -463,8 +474,7 @@ void decode_stream_kernel(DecodeArgs a) {
         for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
           for (int j = 0; j < 8; ++j) ss += x[kk][j] * x[kk][j];
-        ss += __shfl_xor(ss, 16, 64);
-        ss += __shfl_xor(ss, 32, 64);
+        ss = col_sum4(ss);
         const float r = 1.0f / sqrtf(ss * (1.0f / HEAD_DIM) + a.eps);
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
@@ -492,8 +502,7 @@ void decode_stream_kernel(DecodeArgs a) {
         qop[kk] = pack8(x[kk]);
         if (n >= G) qop[kk] = make_uint4(0, 0, 0, 0);
       }
-      qn2 += __shfl_xor(qn2, 16, 64);
-      qn2 += __shfl_xor(qn2, 32, 64);
+      qn2 = col_sum4(qn2);
     }
     float m_run = -INFINITY;
     bool dyn = true;
@@ -528,7 +537,7 @@ void decode_stream_kernel(DecodeArgs a) {
       --inflight;
       // the slot is free once its reads have returned; refill it
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      if (is.next(slot, a, gw1, last, lane, FUSED)) ++inflight;
+      if (is.next(slot, a, gw1, last, lane, FUSED, raw_l)) ++inflight;
       compute_step(sb, ct, cs.hm, n, g, qop, sel, acc, m_run, l_part, dyn);
       ct += DSTEP;
     };
@@ -545,8 +554,7 @@ void decode_stream_kernel(DecodeArgs a) {
     }
 
     // ---- partial for (w, segment): slot w + b*Hk + hk
-    float l_tot = l_part + __shfl_xor(l_part, 16, 64);
-    l_tot += __shfl_xor(l_tot, 32, 64);
+    const float l_tot = col_sum4(l_part);
     const int64_t slot = (int64_t)w + (int64_t)cs.b * Hk + cs.hk;
     if (n < G) {
       float* dst = a.part_o + (slot * G + n) * HEAD_DIM + 4 * g;
@@ -559,7 +567,7 @@ void decode_stream_kernel(DecodeArgs a) {
         a.part_ml[2 * (slot * G + n) + 1] = l_tot;
       }
     }
-    if (!seg_next(cs, gw1, a, FUSED)) break;
+    if (!seg_next(cs, gw1, a, FUSED, raw_l)) break;
     ct = cs.lo;
   }
   wait_vmcnt<0>();  // no LDS load may land after the wave is gone
