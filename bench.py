@@ -10,7 +10,8 @@ epilogue. ``value`` = algorithmic TFLOP/s =
 
 Also reported (same JSON line, key "decode"): BASELINE configs 3 (B=32 batched
 decode, lengths ~U{1024..32768}) and 4 (B=1 at 131072 tokens, one step captured
-in a hipGraph and replayed 256 times with the position advancing on the device)
+in a hipGraph and replayed 256 times on a dedicated stream with the position
+advancing on the device)
 in HBM GB/s of K/V actually attended (4096 B per token) + 32 KiB per sequence,
 and config 1 (B=1 at 512 tokens, launch-latency-bound) as time per step.
 Key "prefill_config5": BASELINE config 5 (B=4 ragged chunks after 8-32 K
@@ -41,6 +42,13 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
+
+# Graph replays (config 4) through the HIP runtime's plain dispatch path: on
+# this ROCm image its packet-capture path costs ~3 us more per replay of the
+# two-kernel decode step. Read when HIP initialises, so set before torch
+# touches the GPU; a value already in the environment wins. The setting used is
+# recorded next to the config-4 result.
+os.environ.setdefault("DEBUG_CLR_GRAPH_PACKET_CAPTURE", "0")
 
 HQ, HK, D, HALF, THETA, EPS = 16, 4, 256, 32, 1.0e7, 1.0e-6
 S = 2 * HQ + 2 * HK
@@ -339,12 +347,19 @@ def bench_decode4(vm, torch, replays=256, seed=4):
     gen.positions.fill_(p0)
     torch.cuda.synchronize()
     sess = vm.CaptureSession().capture(lambda: vm.gated_attn_decode_(O, layer, m, gen, qkv, advance=True))
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
-        sess.launch()
-    stop.record()
+    # replays on a stream of their own, as a serving loop runs them (the
+    # reference's generate loop replays on its task's stream): launches on the
+    # legacy default stream measure ~4 us more per replay (implicit
+    # synchronisation with the other streams)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(replays):
+            sess.launch()
+        stop.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop)
     assert gen.positions.item() == p0 + replays
@@ -353,6 +368,9 @@ def bench_decode4(vm, torch, replays=256, seed=4):
     nbytes = decode_bytes(lengths) / replays
     return {
         "config": "config4: long-context decode B=1, 131072..131327 tokens, 256 hipGraph replays",
+        "launch": "hipGraphLaunch on a dedicated non-default stream",
+        "runtime_env": {"DEBUG_CLR_GRAPH_PACKET_CAPTURE":
+                        os.environ.get("DEBUG_CLR_GRAPH_PACKET_CAPTURE", "(runtime default)")},
         "bytes_per_replay": nbytes,
         "ms_per_replay": ms / replays,
         "gbs": nbytes / (ms / replays * 1e-3) / 1e9,
