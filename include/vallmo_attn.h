@@ -58,7 +58,8 @@ enum {
   VM_K_DECODE_COMBINE = 2,/* LSE merge (+ gate)                              */
   VM_K_PREFILL = 3,       /* flash attention (prefill)                       */
   VM_K_ADVANCE = 4,       /* device clock                                    */
-  VM_K_COUNT = 5
+  VM_K_LM_HEAD = 5,       /* lm-head GEMV + argmax (split and combine)       */
+  VM_K_COUNT = 6
 };
 int vm_profile_enable(int on);
 int vm_profile_read(int kernel, int* count, double* total_ms);
@@ -265,6 +266,50 @@ size_t vm_linear_workspace_bytes(int M, int N, int K, int64_t ldw, int64_t ldx, 
 int vm_linear(vm_bf16* y, int64_t ldy, const vm_bf16* x, int64_t ldx, const vm_bf16* w,
               int64_t ldw, int M, int N, int K, void* workspace, size_t workspace_bytes,
               vm_stream stream);
+
+/* ---- f2: the rest of the decode step (src/llm/qwen35.jl:247-273) --------
+ * Matrices are column-major bf16 with an element column stride (a multiple of
+ * 8, pointers 16-byte aligned); M, I, D, K multiples of 8.
+ *
+ * rms_norm! (src/kernels/rms_norm.jl:38-50): Y[:, n] = X[:, n] * rstd_n *
+ * (w + offset), rstd_n = 1 / sqrt(sum(X[:, n]^2) / M + eps), fp32, one bf16
+ * rounding. M <= 16384 rows, N columns.                                      */
+int vm_rms_norm(vm_bf16* y, int64_t y_st, const vm_bf16* x, int64_t x_st, const vm_bf16* w,
+                int M, int N, float eps, float offset, vm_stream stream);
+/* fused_add_rms_norm! (src/kernels/residual_norm.jl:43-60): X' = bf16(X + dX)
+ * (xo may be x: the reference's in-place (; X' = x) use, qwen35.jl:265), Y =
+ * rms_norm of X' -- rstd from the fp32 sum, applied to the rounded X', as the
+ * reference's second pass reloads it.                                         */
+int vm_fused_add_rms_norm(vm_bf16* y, int64_t y_st, vm_bf16* xo, int64_t xo_st, const vm_bf16* x,
+                          int64_t x_st, const vm_bf16* dx, int64_t dx_st, const vm_bf16* w, int M,
+                          int N, float eps, float offset, vm_stream stream);
+/* The MLP's mid = silu(gate) .* up (src/llm/qwen35.jl:234-243): gate and up are
+ * rows 0..I-1 and I..2I-1 of each column of gu (the packed gate-up projection);
+ * mid (I, N). fp32, one rounding.                                            */
+int vm_silu_mul(vm_bf16* mid, int64_t mid_st, const vm_bf16* gu, int64_t gu_st, int I, int N,
+                vm_stream stream);
+/* x[:, b] = E[:, ids[b]] (src/llm/qwen35.jl:251), ids 1-based (an id outside
+ * 1..vocab reads the nearest valid column). E (D, vocab), column stride e_st. */
+int vm_embed(vm_bf16* x, int64_t x_st, const vm_bf16* e, int64_t e_st, const int32_t* ids, int D,
+             int B, int vocab, vm_stream stream);
+/* advance!(gen) (src/llm/generate.jl:82-88), the engine's clock on the device:
+ * tokens_out[step, b] = result[b] (column-major (max_new, B), column b at
+ * col_offsets[b]; nothing harvested when step is outside 1..max_new), then
+ * step += 1 and positions[b] += 1. One kernel: capturable.                   */
+int vm_generation_advance(int32_t* tokens_out, const int32_t* col_offsets, int32_t* step,
+                          int32_t* positions, const int32_t* result, int B, int max_new,
+                          vm_stream stream);
+
+/* ---- f3: lm_head_argmax! (src/kernels/lm_head_topk.jl:109-147) ----------
+ * Result[b] = argmax_v W[:, v] . X[:, b], 1-based, ties to the smallest v;
+ * bf16 products, fp32 sums; the logits are never written. X (K, B), W (K, N)
+ * K-major (the embedding's own orientation, so a tied head needs no copy).
+ * scratch: vm_lm_head_argmax_scratch_bytes(K, N, B) bytes of device memory
+ * (per-wave partials; the reference's LocalMax / LocalIdx), 16-byte aligned. */
+size_t vm_lm_head_argmax_scratch_bytes(int K, int N, int B);
+int vm_lm_head_argmax(int32_t* result, const vm_bf16* x, int64_t x_st, const vm_bf16* w,
+                      int64_t w_st, int K, int N, int B, void* scratch, size_t scratch_bytes,
+                      vm_stream stream);
 
 /* ---- synthetic inputs for tests and benchmarks (not a reference op) ----
  * Fills n bf16 values with the seeded N(0,1) stream used by the CPU oracle

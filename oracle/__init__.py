@@ -60,6 +60,13 @@ def lib():
         L.orc_gated_prefill.restype = None
         L.orc_linear.argtypes = [_u16p, _u16p, _f32p, i32, i32, i32, i32]
         L.orc_linear.restype = None
+        L.orc_rms_norm.argtypes = [_u16p, ctypes.c_void_p, _u16p, ctypes.c_void_p, _f32p, i32, i32,
+                                   f32, f32]
+        L.orc_rms_norm.restype = None
+        L.orc_silu_mul.argtypes = [_u16p, _f32p, i32, i32]
+        L.orc_silu_mul.restype = None
+        L.orc_lm_head_argmax.argtypes = [_u16p, _u16p, i32, i32, i32, _i32p, _f32p, i32]
+        L.orc_lm_head_argmax.restype = None
         L.orc_max_threads.restype = i32
         _LIB = L
     return _LIB
@@ -203,6 +210,75 @@ def prefill_layer(xn, Wqkv, Wo, kc, vc, prior, q_len, qw, kw, cos_tab, sin_tab, 
     h = np.full((B, T, Wo.shape[0]), np.nan, np.float32)
     h[rows] = linear(f32_to_bf16(o[rows]), Wo, nthreads=nthreads)
     return h, kn, vn
+
+
+def rms_norm(x, w, *, eps, offset, dx=None):
+    """rms_norm! (src/kernels/rms_norm.jl:3-31), or fused_add_rms_norm!
+    (src/kernels/residual_norm.jl:4-37) when dx is given: x, dx [N][M] bf16 bits
+    (the reference's (M, N) columns), w [M]. Returns y [N][M] fp32, and with dx
+    also x' = x + dx [N][M] fp32 (y is formed from bf16(x'), as the reference
+    reloads the stored x')."""
+    x = _c(x, np.uint16)
+    N, M = x.shape
+    y = np.empty((N, M), np.float32)
+    xo = np.empty((N, M), np.float32) if dx is not None else None
+    dxc = _c(dx, np.uint16) if dx is not None else None
+    lib().orc_rms_norm(x, dxc.ctypes.data if dxc is not None else None, _c(w, np.uint16),
+                       xo.ctypes.data if xo is not None else None, y, M, N, eps, offset)
+    return (y, xo) if dx is not None else y
+
+
+def silu_mul(gu):
+    """mid = silu(gate) .* up (src/llm/qwen35.jl:234-243): gu [N][2I] bf16 bits ->
+    mid [N][I] fp32."""
+    gu = _c(gu, np.uint16)
+    N, I2 = gu.shape
+    mid = np.empty((N, I2 // 2), np.float32)
+    lib().orc_silu_mul(gu, mid, I2 // 2, N)
+    return mid
+
+
+def lm_head_argmax(x, W, *, nthreads=0):
+    """lm_head_argmax! (src/kernels/lm_head_topk.jl:27-101): x [B][K], W [N][K] bf16
+    bits (the reference's (K, B) and K-major (K, N)). Returns (result [B] int32,
+    1-based, ties to the smallest index; gap [B]: best minus second-best logit)."""
+    x = _c(x, np.uint16)
+    W = _c(W, np.uint16)
+    B, K = x.shape
+    N = W.shape[0]
+    res = np.empty(B, np.int32)
+    gap = np.empty(B, np.float32)
+    lib().orc_lm_head_argmax(x, W, K, N, B, res, gap, nthreads or threads_env())
+    return res, gap
+
+
+def model_step(E, layers, norm_w, head, result, positions, cos_tab, sin_tab, *, Hq, Hk, eps,
+               nthreads=0):
+    """step!(m, gen) (src/llm/qwen35.jl:245-273) for a stack of attention layers,
+    greedy. The reference's step buffers are bf16 (the residual x, xn, h, the
+    MLP's gu and mid, qwen35.jl:235-250): every value is rounded to bf16 (RNE)
+    where the reference stores it, everything else is fp32.
+
+    E, head [vocab][Dm]; norm_w [Dm]; layers: dicts with norm1, norm2, Wqkv, Wo,
+    qw, kw, kc, vc (caches [B][Hk][ctx][D]), Wgu [2I][Dm], Wd [Dm][I] (bf16 bits);
+    result [B] 1-based tokens; positions [B]. Returns (next tokens [B] int32,
+    logit gaps [B], final xn [B][Dm] fp32 of the bf16 values)."""
+    r = np.clip(np.asarray(result, np.int64) - 1, 0, E.shape[0] - 1)
+    x = _c(E[r], np.uint16)
+    xn = f32_to_bf16(rms_norm(x, layers[0]["norm1"], eps=eps, offset=1.0))
+    for i, l in enumerate(layers):
+        h, _, _ = decode_layer(xn, l["Wqkv"], l["Wo"], l["kc"], l["vc"], positions, l["qw"],
+                               l["kw"], cos_tab, sin_tab, Hq=Hq, Hk=Hk, eps=eps, w_offset=1.0,
+                               nthreads=nthreads)
+        y, xo = rms_norm(x, l["norm2"], eps=eps, offset=1.0, dx=f32_to_bf16(h))
+        x, xn = f32_to_bf16(xo), f32_to_bf16(y)
+        gu = f32_to_bf16(linear(xn, l["Wgu"], nthreads=nthreads))
+        h = linear(f32_to_bf16(silu_mul(gu)), l["Wd"], nthreads=nthreads)
+        nw = norm_w if i == len(layers) - 1 else layers[i + 1]["norm1"]
+        y, xo = rms_norm(x, nw, eps=eps, offset=1.0, dx=f32_to_bf16(h))
+        x, xn = f32_to_bf16(xo), f32_to_bf16(y)
+    res, gap = lm_head_argmax(xn, head, nthreads=nthreads)
+    return res, gap, bf16_to_f32(xn)
 
 
 def threads_env() -> int:

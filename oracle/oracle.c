@@ -23,6 +23,11 @@
  *   sigmoid gate ............ src/kernels/kernels.jl:34, src/llm/qwen35.jl:205,315
  *   decode! / forward ....... src/llm/qwen35.jl:187-208, 292-318
  *   linear! (y = W^T x) ..... src/linear.jl:40-57 (fp32 accumulation, linear.jl:29)
+ *   rms_norm! ............... src/kernels/rms_norm.jl:3-31
+ *   fused_add_rms_norm! ..... src/kernels/residual_norm.jl:4-37 (the second pass
+ *                             reloads the stored bf16 x': rounded here too)
+ *   MLP silu(gate) .* up .... src/llm/qwen35.jl:234-243, src/kernels/kernels.jl:35
+ *   lm_head_argmax! ......... src/kernels/lm_head_topk.jl:27-101 (ties -> smallest)
  */
 #include <math.h>
 #include <stdint.h>
@@ -393,6 +398,85 @@ void orc_linear(const uint16_t* x, const uint16_t* w, float* y, int M, int N, in
     free(xr);
   }
   free(wf);
+}
+
+/* rms_norm! / fused_add_rms_norm! over N columns of M: x, dx [N][M] bf16 bits
+ * (dx NULL: plain norm), w [M]. xo [N][M] fp32 = x + dx (fused; NULL allowed),
+ * y [N][M] fp32 = x' * rstd * (w + off), rstd = 1/sqrt(sum x'^2 / M + eps) over
+ * the fp32 x'; fused, y uses bf16(x'), the value the reference stores and
+ * reloads (residual_norm.jl:26-36).                                          */
+void orc_rms_norm(const uint16_t* x, const uint16_t* dx, const uint16_t* w, float* xo, float* y,
+                  int M, int N, float eps, float off) {
+  for (int n = 0; n < N; ++n) {
+    const uint16_t* xr = x + (size_t)n * M;
+    float ss = 0.f;
+    for (int m = 0; m < M; ++m) {
+      float v = bf(xr[m]);
+      if (dx) v += bf(dx[(size_t)n * M + m]);
+      if (xo) xo[(size_t)n * M + m] = v;
+      ss += v * v;
+    }
+    const float rstd = 1.0f / sqrtf(ss / (float)M + eps);
+    for (int m = 0; m < M; ++m) {
+      float v = bf(xr[m]);
+      if (dx) v = bf(orc_f2bf(v + bf(dx[(size_t)n * M + m])));
+      y[(size_t)n * M + m] = v * rstd * (bf(w[m]) + off);
+    }
+  }
+}
+
+/* mid [N][I] = silu(gate) * up, gate / up = gu[n][0..I-1], gu[n][I..2I-1]. */
+void orc_silu_mul(const uint16_t* gu, float* mid, int I, int N) {
+  for (int n = 0; n < N; ++n)
+    for (int i = 0; i < I; ++i) {
+      const float g = bf(gu[(size_t)n * 2 * I + i]), u = bf(gu[(size_t)n * 2 * I + I + i]);
+      mid[(size_t)n * I + i] = g / (1.0f + expf(-g)) * u;
+    }
+}
+
+/* lm_head_argmax!: result[b] = 1 + argmax_v sum_k w[v][k] x[b][k] (fp32 sums in
+ * k order, ties to the smallest v); gap[b] = best - second best logit (the
+ * margin by which the choice is stable). x [B][K], w [N][K] bf16 bits.       */
+void orc_lm_head_argmax(const uint16_t* x, const uint16_t* w, int K, int N, int B,
+                        int32_t* result, float* gap, int nthreads) {
+  set_threads(nthreads);
+  for (int b = 0; b < B; ++b) {
+    float* xr = (float*)malloc(sizeof(float) * (size_t)K);
+    for (int k = 0; k < K; ++k) xr[k] = bf(x[(size_t)b * K + k]);
+    float best = -INFINITY, second = -INFINITY;
+    int besti = 0;
+#pragma omp parallel
+    {
+      float lb = -INFINITY, ls = -INFINITY;
+      int li = 0x7fffffff;
+#pragma omp for schedule(static)
+      for (int v = 0; v < N; ++v) {
+        const uint16_t* wr = w + (size_t)v * K;
+        float acc = 0.f;
+        for (int k = 0; k < K; ++k) acc += bf(wr[k]) * xr[k];
+        if (acc > lb || (acc == lb && v < li)) {
+          ls = lb;
+          lb = acc;
+          li = v;
+        } else if (acc > ls) {
+          ls = acc;
+        }
+      }
+#pragma omp critical
+      {
+        if (lb > best || (lb == best && li < besti)) {
+          second = fmaxf(second, fmaxf(best, ls));
+          best = lb;
+          besti = li;
+        } else {
+          second = fmaxf(second, lb);
+        }
+      }
+    }
+    result[b] = besti + 1;
+    gap[b] = best - second;
+    free(xr);
+  }
 }
 
 int orc_max_threads(void) {

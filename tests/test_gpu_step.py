@@ -1,0 +1,211 @@
+"""The rest of the decode step on the GPU vs the oracle: rms_norm! and
+fused_add_rms_norm! (src/kernels/rms_norm.jl, residual_norm.jl), the MLP's
+silu(gate) .* up (src/llm/qwen35.jl:234-243), the embedding gather (:251),
+advance! (src/llm/generate.jl:82-88), lm_head_argmax! (src/kernels/
+lm_head_topk.jl:109-147); then a whole step! of an attention-layer stack
+(qwen35.jl:245-273) against the oracle composition, and captured generation
+(generate.jl:147-196) against eager generation, token for token."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import (D, EPS, HALF, HK, HQ, S, THETA, TOL_MAX, TOL_MEAN, banner, dev_f32,
+                      from_dev, i32, maxmean, to_dev)
+from oracle.rng import bf16_to_f32, f32_to_bf16, normal_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("M,N", [(2560, 32), (16384, 3), (24, 5)])
+def test_rms_norm(vm, orc, M, N):
+    banner(f"rms_norm M={M} N={N}")
+    x = normal_bf16((N, M), 100 + M, scale=2.0)
+    w = normal_bf16((M,), 101, scale=0.05)
+    y = vm.rms_norm(to_dev(x), to_dev(w), eps=EPS, offset=1.0)["Y"]
+    mx, mn = maxmean(dev_f32(y), orc.rms_norm(x, w, eps=EPS, offset=1.0))
+    print(f"rms_norm {M}x{N}: max {mx:.3e} mean {mn:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN
+
+
+@pytest.mark.parametrize("inplace", [False, True])
+def test_fused_add_rms_norm(vm, orc, inplace):
+    """x' = x + dx stored (in place over x too, the decode step's use), y its norm."""
+    banner(f"fused_add_rms_norm inplace={inplace}")
+    M, N = 2560, 32
+    x = normal_bf16((N, M), 110)
+    dx = normal_bf16((N, M), 111, scale=0.5)
+    w = normal_bf16((M,), 112, scale=0.05)
+    X, dX = to_dev(x), to_dev(dx)
+    Y = torch.empty_like(X)
+    Xp = X if inplace else torch.empty_like(X)
+    vm.fused_add_rms_norm_({"Y": Y, "Xp": Xp}, X, dX, to_dev(w), eps=EPS, offset=1.0)
+    ry, rxo = orc.rms_norm(x, w, eps=EPS, offset=1.0, dx=dx)
+    mx, mn = maxmean(dev_f32(Y), ry)
+    # x' is one bf16 rounding of the exact fp32 sum
+    assert np.array_equal(from_dev(Xp), f32_to_bf16(rxo))
+    print(f"fused_add_rms_norm: y max {mx:.3e} mean {mn:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN
+
+
+def test_silu_mul(vm, orc):
+    banner("silu_mul I=9216 N=32")
+    I, N = 9216, 32
+    gu = normal_bf16((N, 2 * I), 120, scale=2.0)
+    mid = torch.empty((N, I), dtype=torch.bfloat16, device="cuda")
+    vm.silu_mul_(mid, to_dev(gu))
+    ref = orc.silu_mul(gu)
+    got = dev_f32(mid)
+    # values reach |g u| ~ 60 here: the bar is one bf16 ulp of the fp32 value
+    # (2^-7 relative), i.e. one rounding of an fp32 evaluation
+    err = np.abs(got.astype(np.float64) - ref) / (np.abs(ref) * 2.0 ** -7 + 1e-30)
+    print(f"silu_mul: max error {err.max():.3f} ulp (|mid| max {np.abs(ref).max():.1f})")
+    assert err.max() <= 1.0
+
+
+def test_embed_gather(vm):
+    """x[:, b] = E[:, ids[b]], 1-based, bit for bit; out-of-range ids clamp."""
+    banner("embed vocab=1000 D=2560 B=6")
+    E = normal_bf16((1000, 2560), 130)
+    ids = np.array([1, 1000, 17, 500, 0, 1005], np.int32)
+    x = torch.empty((6, 2560), dtype=torch.bfloat16, device="cuda")
+    vm.embed_(x, to_dev(E), i32(ids))
+    got = from_dev(x)
+    want = E[np.clip(ids - 1, 0, 999)]
+    assert np.array_equal(got, want)
+
+
+def test_generation_advance(vm):
+    """advance!: tokens_out[step, b] = result[b], step += 1, positions .+= 1; a
+    step past max_new harvests nothing."""
+    banner("generation advance B=3 max_new=2")
+    gen = vm.Generation(3, 2)
+    gen.positions.copy_(i32([5, 7, 9]))
+    gen.result.copy_(i32([11, 12, 13]))
+    gen.advance_()
+    gen.result.copy_(i32([21, 22, 23]))
+    gen.advance_()
+    gen.result.copy_(i32([31, 32, 33]))
+    gen.advance_()   # step 3 > max_new: no harvest
+    torch.cuda.synchronize()
+    assert gen.step.item() == 4
+    assert gen.positions.cpu().tolist() == [8, 10, 12]
+    assert gen.poll(1, 2).tolist() == [[11, 12, 13], [21, 22, 23]]
+
+
+@pytest.mark.parametrize("N,B", [(20011, 1), (20011, 5), (4099, 32), (4099, 37)])
+def test_lm_head_argmax(vm, orc, N, B):
+    """GEMV + argmax against the oracle wherever the oracle's top-2 margin is not
+    tiny (fp32 sums in another order); one column duplicated below the winner
+    checks the smallest-index tie rule; N not a multiple of the tile, B across
+    two batch tiles."""
+    banner(f"lm_head_argmax K=2560 N={N} B={B}")
+    K = 2560
+    x = normal_bf16((B, K), 140 + B)
+    W = normal_bf16((N, K), 141 + N, scale=0.05)
+    res, gap = orc.lm_head_argmax(x, W)
+    # a tie for sequence 0: its winner duplicated at a smaller index
+    dup = max(0, res[0] - 1 - 7)
+    W[dup] = W[res[0] - 1]
+    Wd, Xd = to_dev(W), to_dev(x)
+    got = vm.lm_head_argmax(Xd, Wd)["Result"].cpu().numpy()
+    # fp32 sums in another order differ by ~1e-4 at these logit sizes (|l| < 20)
+    ok = gap > 2e-3
+    ok[0] = True
+    want = res.copy()
+    want[0] = dup + 1
+    print(f"lm_head N={N} B={B}: margins min {gap.min():.3e}, compared {ok.sum()}/{B}")
+    assert ok.sum() >= (B + 1) // 2
+    assert np.array_equal(got[ok], want[ok]), (got, want, gap)
+
+
+def _tiny_cfg(vm, B=4, Ctx=64, tied=True):
+    a = vm.AttnConfig(D=512, Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=Ctx,
+                      B=B)
+    return vm.ModelConfig(attn=a, inter=1024, vocab=4099, n_layers=2, tied=tied)
+
+
+def _host_layers(m):
+    out = []
+    for l in m.layers:
+        out.append(dict(norm1=from_dev(l.norm1), norm2=from_dev(l.norm2), Wqkv=from_dev(l.Wqkv),
+                        Wo=from_dev(l.Wo), qw=from_dev(l.qw), kw=from_dev(l.kw),
+                        kc=from_dev(l.K_cache), vc=from_dev(l.V_cache), Wgu=from_dev(l.Wgu),
+                        Wd=from_dev(l.Wd)))
+    return out
+
+
+def test_decode_step_vs_oracle(vm, orc):
+    """One step! of a 2-layer stack (hidden 512, MLP 1024, vocab 4099, B = 4)
+    over random caches, against the oracle's composition with the reference's
+    bf16 buffers: the final normed hidden state within the bf16 bar, the greedy
+    tokens equal wherever the oracle's top-2 margin is not tiny."""
+    banner("decode step 2 layers B=4")
+    cfg = _tiny_cfg(vm, tied=False)  # an untied head: the tokens depend on every layer
+    m = vm.random_model(cfg, seed=3)
+    for i, l in enumerate(m.layers):
+        vm.fill_normal_(l.K_cache, 150 + i)
+        vm.fill_normal_(l.V_cache, 160 + i)
+    gen = vm.Generation(cfg.B, 4)
+    pos = np.array([5, 33, 64, 17], np.int32)
+    tok = np.array([1, 4099, 77, 2048], np.int32)
+    gen.positions.copy_(i32(pos))
+    gen.result.copy_(i32(tok))
+    layers = _host_layers(m)   # before the step appends its rows
+    vm.step_(m, gen)
+    torch.cuda.synchronize()
+    c, s = orc.rope_tables(HALF, cfg.attn.Ctx, THETA)
+    res, gap, xn = orc.model_step(from_dev(m.E), layers, from_dev(m.norm_w), from_dev(m.head), tok,
+                                  pos, c, s, Hq=HQ, Hk=HK, eps=EPS)
+    mx, mn = maxmean(dev_f32(m.xn), xn)
+    got = gen.result.cpu().numpy()
+    ok = gap > 0.05
+    rel = mn / np.abs(xn).mean()
+    print(f"step: xn max {mx:.3e} mean {mn:.3e} ({rel:.2%} of mean |xn|; |xn| max "
+          f"{np.abs(xn).max():.2f}); tokens {got.tolist()} oracle {res.tolist()} margins "
+          f"{np.round(gap, 3).tolist()}")
+    # a chain of bf16 buffers (x, xn, h, gu, mid, qkv, O per layer) each rounded in
+    # both evaluations, with sums in different orders: about half an ulp on average
+    assert mx <= 0.1 and rel <= 1e-2
+    assert ok.sum() >= cfg.B - 1 and np.array_equal(got[ok], res[ok])
+
+
+def test_identity_model_step(vm):
+    """Every projection zero, tied head: the next token is the input token."""
+    banner("identity model step")
+    cfg = _tiny_cfg(vm)
+    m = vm.random_model(cfg, seed=4)
+    for l in m.layers:
+        for t in (l.Wqkv, l.Wo, l.Wgu, l.Wd, l.norm1, l.norm2):
+            t.zero_()
+    m.norm_w.zero_()
+    gen = vm.Generation(cfg.B, 2)
+    gen.positions.copy_(i32([3, 4, 5, 6]))
+    tok = [1, 4099, 2, 3000]
+    gen.result.copy_(i32(tok))
+    vm.step_(m, gen)
+    assert gen.result.cpu().tolist() == tok
+
+
+def test_generate_captured_matches_eager(vm):
+    """generate_captured! == generate! token for token (generate.jl:132-196): prefill
+    of a 24-token prompt, then 12 tokens, 3 of them eager warm-up steps and the
+    rest hipGraph replays of (step!; advance!); the session's graph is reused by
+    a second captured run."""
+    banner("generate captured vs eager B=4 T=24 n=12")
+    cfg = _tiny_cfg(vm, tied=False)  # varied tokens (a tied head mostly repeats its input)
+    m = vm.random_model(cfg, seed=5)
+    ids = torch.as_tensor(np.random.default_rng(6).integers(1, cfg.vocab + 1, size=(cfg.B, 24)),
+                          dtype=torch.int32).cuda()
+    gen = vm.Generation(cfg.B, 16)
+    eager, t_e = vm.generate_(m, gen, ids, max_new_tokens=12, poll_every=5)
+    sess = vm.CaptureSession()
+    cap, t_c = vm.generate_captured_(m, gen, ids, max_new_tokens=12, warmup=3, session=sess)
+    cap2, _ = vm.generate_captured_(m, gen, ids, max_new_tokens=12, warmup=3, session=sess)
+    sess.close()
+    print(f"eager {eager.T.tolist()}\ncaptured {cap.T.tolist()}")
+    print(f"timing eager {t_e}, captured {t_c}")
+    assert eager.shape == (12, cfg.B)
+    assert np.array_equal(eager, cap) and np.array_equal(eager, cap2)
+    assert gen.positions.cpu().tolist() == [24 + 1 + 12] * cfg.B

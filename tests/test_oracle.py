@@ -334,3 +334,102 @@ def test_decode_layer_is_the_composition(orc):
     # torch sums in another order, so a few bf16 roundings of qkv / o flip by one ulp
     assert np.max(np.abs(h - ref)) <= 2e-3 and np.mean(np.abs(h - ref)) <= 1e-4
     assert np.max(np.abs(ref)) > 0.1
+
+
+# ---------------------------------------------------- the rest of the decode step
+def test_rms_norm_invariants(orc):
+    """rms_norm (rms_norm.jl:3-31): with w = 0 and offset 1 every output column
+    has unit RMS (a wrong divisor, a dropped square root or offset fails); a
+    power-of-two scale of x leaves y unchanged (eps negligible); the weight
+    multiplies by (w + offset); a 2-row known answer."""
+    x = normal_bf16((5, 2560), 11, scale=3.0)
+    zero = np.zeros(2560, np.uint16)
+    y = orc.rms_norm(x, zero, eps=1e-30, offset=1.0)
+    assert np.allclose(np.sqrt((y.astype(np.float64) ** 2).mean(axis=1)), 1.0, rtol=1e-5)
+    y2 = orc.rms_norm(f32_to_bf16(bf16_to_f32(x) * 4.0), zero, eps=1e-30, offset=1.0)
+    assert np.allclose(y, y2, rtol=1e-6, atol=1e-7)
+    w = normal_bf16((2560,), 12, scale=0.05)
+    yw = orc.rms_norm(x, w, eps=1e-30, offset=1.0)
+    assert np.allclose(yw, y * (bf16_to_f32(w) + 1.0), rtol=1e-6, atol=1e-7)
+    k = orc.rms_norm(f32_to_bf16(np.array([[3.0, 4.0]], np.float32)), np.zeros(2, np.uint16),
+                     eps=0.0, offset=2.0)
+    r = np.sqrt(12.5)
+    assert np.allclose(k, [[2 * 3 / r, 2 * 4 / r]], rtol=1e-6)
+
+
+def test_fused_add_rms_norm_is_the_norm_of_the_sum(orc):
+    """fused_add_rms_norm (residual_norm.jl:4-37): on integer-valued x, dx the sum
+    is exact in bf16, so x' == x + dx and y == rms_norm(x') bit for bit."""
+    rng = np.random.default_rng(13)
+    x = f32_to_bf16(rng.integers(-40, 40, size=(3, 1024)).astype(np.float32))
+    dx = f32_to_bf16(rng.integers(-40, 40, size=(3, 1024)).astype(np.float32))
+    w = normal_bf16((1024,), 14, scale=0.05)
+    y, xo = orc.rms_norm(x, w, eps=1e-6, offset=1.0, dx=dx)
+    s = bf16_to_f32(x) + bf16_to_f32(dx)
+    assert np.array_equal(xo, s)
+    assert np.array_equal(y, orc.rms_norm(f32_to_bf16(s), w, eps=1e-6, offset=1.0))
+
+
+def test_silu_mul_identities(orc):
+    """mid = silu(gate) * up (qwen35.jl:234-243, kernels.jl:35): silu(g) - silu(-g)
+    = g (a sign or sigmoid-argument slip fails), silu(0) = 0, silu(g) -> g for
+    large g, linear in up; gate is the first half of each column."""
+    g = normal_bf16((2, 512), 15, scale=3.0)
+    one = f32_to_bf16(np.ones((2, 512), np.float32))
+    pos = orc.silu_mul(np.concatenate([g, one], axis=1))
+    neg = orc.silu_mul(np.concatenate([f32_to_bf16(-bf16_to_f32(g)), one], axis=1))
+    assert np.allclose(pos - neg, bf16_to_f32(g), rtol=1e-5, atol=1e-6)
+    z = orc.silu_mul(np.concatenate([np.zeros((1, 8), np.uint16), one[:1, :8]], axis=1))
+    assert np.all(z == 0.0)
+    big = orc.silu_mul(np.concatenate([f32_to_bf16(np.full((1, 8), 40.0, np.float32)),
+                                       one[:1, :8]], axis=1))
+    assert np.allclose(big, 40.0, rtol=1e-6)
+    u = normal_bf16((2, 512), 16)
+    two_u = f32_to_bf16(2 * bf16_to_f32(u))
+    m1 = orc.silu_mul(np.concatenate([g, u], axis=1))
+    m2 = orc.silu_mul(np.concatenate([g, two_u], axis=1))
+    assert np.array_equal(m2, 2 * m1)
+
+
+def test_lm_head_argmax_known_answers(orc):
+    """lm_head_argmax (lm_head_topk.jl:27-101): 1-based; a planted column wins;
+    duplicated best columns resolve to the smallest index; agrees with a float64
+    numpy argmax wherever the margin is not tiny."""
+    K, N, B = 256, 3001, 6
+    x = normal_bf16((B, K), 17)
+    W = normal_bf16((N, K), 18, scale=0.1)
+    res, gap = orc.lm_head_argmax(x, W, nthreads=4)
+    logits = bf16_to_f32(W).astype(np.float64) @ bf16_to_f32(x).astype(np.float64).T
+    ref = logits.argmax(axis=0) + 1
+    ok = gap > 1e-3
+    assert ok.sum() >= B - 1 and np.array_equal(res[ok], ref[ok])
+    # plant: column 2000 (1-based 2001) is 10 x_0; its copy at column 77 (1-based 78)
+    W2 = W.copy()
+    W2[2000] = f32_to_bf16(10 * bf16_to_f32(x[0]))
+    res2, _ = orc.lm_head_argmax(x[:1], W2)
+    assert res2[0] == 2001
+    W2[77] = W2[2000]
+    res3, gap3 = orc.lm_head_argmax(x[:1], W2)
+    assert res3[0] == 78 and gap3[0] == 0.0
+
+
+def test_model_step_identity_model(orc):
+    """step! (qwen35.jl:245-273) with every projection zero and a tied head: the
+    mixer and the MLP add nothing, xn = rms_norm(E[token]) (norm weights 0, offset
+    1), and the greedy next token is the input token itself (|E_t|^2 ~ Dm dwarfs
+    E_v . E_t): pins the 1-based embedding gather, the norm chain and the head's
+    index convention together."""
+    Dm, I, V, B, ctx = 256, 64, 500, 3, 16
+    E = normal_bf16((V, Dm), 19)
+    z = lambda *s: np.zeros(s, np.uint16)  # noqa: E731
+    layer = dict(norm1=z(Dm), norm2=z(Dm), Wqkv=z(S * D, Dm), Wo=z(Dm, HQ * D), qw=z(D), kw=z(D),
+                 kc=normal_bf16((B, HK, ctx, D), 20), vc=normal_bf16((B, HK, ctx, D), 21),
+                 Wgu=z(2 * I, Dm), Wd=z(Dm, I))
+    c, s = orc.rope_tables(HALF, ctx, THETA)
+    tokens = np.array([1, 250, 500], np.int32)
+    res, gap, xn = orc.model_step(E, [layer, dict(layer)], z(Dm), E, tokens,
+                                  np.array([5, 9, 16], np.int32), c, s, Hq=HQ, Hk=HK, eps=EPS)
+    assert np.array_equal(res, tokens)
+    xe = bf16_to_f32(E[tokens - 1])
+    want = xe / np.sqrt((xe.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + EPS)
+    assert np.allclose(xn, want, rtol=1e-2, atol=1e-2)

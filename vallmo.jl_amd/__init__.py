@@ -13,10 +13,15 @@ from ._lib import (ArgumentError, BoundsError, DimensionMismatch, HIPError,  # n
                    LIB_PATH, EXPORTED)
 from .sizes import sizes  # noqa: F401
 from .ops import (attention, attention_, decode_attention, decode_attention_,  # noqa: F401
-                  decode_scratch_bytes, fill_normal_, knorm_rope_append_, linear, linear_,
-                  linear_workspace_bytes, qnorm_rope_, rope_tables, sigmoid, sigmoid_gate_)
+                  decode_scratch_bytes, embed_, fill_normal_, fused_add_rms_norm,
+                  fused_add_rms_norm_, knorm_rope_append_, linear, linear_,
+                  linear_workspace_bytes, lm_head_argmax, lm_head_argmax_,
+                  lm_head_argmax_scratch_bytes, qnorm_rope_, rms_norm, rms_norm_, rope_tables,
+                  sigmoid, sigmoid_gate_, silu_mul_)
 from .layer import (AttnConfig, AttnLayer, AttnModel, CaptureSession, Generation,  # noqa: F401
                     attn_layer, decode_, forward, gated_attn_decode_, gated_attn_prefill)
+from .model import (Model, ModelConfig, generate_, generate_captured_, mlp_,  # noqa: F401
+                    prefill_, random_model, step_)
 from . import _lib  # noqa: F401
 
 __version__ = "0.1.0"

@@ -18,7 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent / "csrc" / "libvallmo_attn.so"
 
 VM_E_ARG, VM_E_DIM, VM_E_UNSUPPORTED, VM_E_SCRATCH = -1, -2, -3, -4
 # kernel classes of vm_profile_read
-VM_K_ROWS, VM_K_DECODE_SPLIT, VM_K_DECODE_COMBINE, VM_K_PREFILL, VM_K_ADVANCE = range(5)
+VM_K_ROWS, VM_K_DECODE_SPLIT, VM_K_DECODE_COMBINE, VM_K_PREFILL, VM_K_ADVANCE, VM_K_LM_HEAD = range(6)
 
 
 class DimensionMismatch(ValueError):
@@ -107,6 +107,14 @@ _SIGS = {
                                      _c_i, _c_i, _c_i, _c_i, _c_f, _c_f, _p, _c_sz, _p]),
     "vm_linear_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i64, _c_i64, _c_i64]),
     "vm_linear": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i, _c_i, _c_i, _p, _c_sz, _p]),
+    "vm_rms_norm": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i, _c_i, _c_f, _c_f, _p]),
+    "vm_fused_add_rms_norm": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _p, _c_i64, _p, _c_i,
+                                     _c_i, _c_f, _c_f, _p]),
+    "vm_silu_mul": (_c_i, [_p, _c_i64, _p, _c_i64, _c_i, _c_i, _p]),
+    "vm_embed": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i, _c_i, _c_i, _p]),
+    "vm_generation_advance": (_c_i, [_p, _p, _p, _p, _p, _c_i, _c_i, _p]),
+    "vm_lm_head_argmax_scratch_bytes": (_c_sz, [_c_i, _c_i, _c_i]),
+    "vm_lm_head_argmax": (_c_i, [_p, _p, _c_i64, _p, _c_i64, _c_i, _c_i, _c_i, _p, _c_sz, _p]),
     "vm_fill_normal_bf16": (_c_i, [_p, _c_i64, _c_u64, _c_f, _c_f, _p]),
 }
 

@@ -152,6 +152,64 @@ int linear_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const u
                int64_t ldw, int M, int N, int K, void* workspace, size_t workspace_bytes,
                hipStream_t st, char* err, size_t errn);
 
+// ---- the rest of the decode step (step.hip) ----
+// RMSNorm of each column of x (M rows), optionally fused with the residual add:
+// dx != nullptr -> xo = bf16(x + dx) (xo may be x), y = norm of that.
+struct NormArgs {
+  uint16_t* y;
+  int64_t y_st;
+  uint16_t* xo;
+  int64_t xo_st;
+  const uint16_t* x;
+  int64_t x_st;
+  const uint16_t* dx;   // nullable
+  int64_t dx_st;
+  const uint16_t* w;
+  int M, N;             // M a multiple of 8, at most 16384
+  float offset, eps;
+};
+struct SiluMulArgs {
+  uint16_t* mid;        // (I, N), column stride mid_st
+  int64_t mid_st;
+  const uint16_t* gu;   // (2I, N): gate rows 0 .. I-1, up rows I .. 2I-1
+  int64_t gu_st;
+  int I, N;             // I a multiple of 8
+};
+struct EmbedArgs {
+  uint16_t* x;          // (D, B)
+  int64_t x_st;
+  const uint16_t* e;    // (D, vocab), column v at e + v * e_st
+  int64_t e_st;
+  const int32_t* ids;   // (B,) 1-based
+  int D, B, vocab;
+};
+struct AdvanceArgs {
+  int32_t* tokens_out;  // (max_new, B) column-major
+  const int32_t* col_offsets;
+  int32_t* step;        // (1,) 1-based row of tokens_out to write
+  int32_t* positions;   // (B,)
+  const int32_t* result;
+  int B, max_new;
+};
+struct LmHeadArgs {
+  const uint16_t* x;    // (K, B), column b at x + b * x_st
+  int64_t x_st;
+  const uint16_t* w;    // (K, N) K-major, column v at w + v * w_st
+  int64_t w_st;
+  int K, N, B;          // K a multiple of 8
+  int cols;             // vocab columns per wave (set by the launcher)
+  int NW;               // waves of the split pass (lm_head_waves())
+  float* pmax;          // partials [NW][B]
+  int32_t* pidx;
+  int32_t* result;      // (B,) 1-based
+};
+hipError_t launch_rms_norm(const NormArgs& a, hipStream_t st);
+hipError_t launch_silu_mul(const SiluMulArgs& a, hipStream_t st);
+hipError_t launch_embed(const EmbedArgs& a, hipStream_t st);
+hipError_t launch_gen_advance(const AdvanceArgs& a, hipStream_t st);
+int lm_head_waves();
+hipError_t launch_lm_head_argmax(LmHeadArgs a, hipStream_t st);
+
 // Decode stream partition shared by the scratch-size query and the launchers:
 // NW waves cover the token-heads sum_b len_b * Hk in equal contiguous chunks.
 constexpr int DECODE_MIN_CHUNK = 64;

@@ -615,6 +615,134 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm
                     "gated_attn_prefill");
 }
 
+// ---- f2: the rest of the decode step ----------------------------------------
+static int check_rows(int M, int N, int64_t st, const char* what, const char* name) {
+  REQUIRE(M > 0 && M % 8 == 0 && M <= 16384, VM_E_UNSUPPORTED,
+          "%s: M = %d (a multiple of 8, at most 16384)", what, M);
+  REQUIRE(N >= 0, VM_E_ARG, "%s: N = %d", what, N);
+  TRY(check_stride(st, name));
+  REQUIRE(N <= 1 || st >= M, VM_E_DIM, "%s: column stride %s = %lld < M = %d", what, name,
+          (long long)st, M);
+  return VM_OK;
+}
+
+int vm_rms_norm(vm_bf16* y, int64_t y_st, const vm_bf16* x, int64_t x_st, const vm_bf16* w, int M,
+                int N, float eps, float offset, vm_stream st) {
+  TRY(check_aligned(y, "Y"));
+  TRY(check_aligned(x, "X"));
+  TRY(check_aligned(w, "W"));
+  TRY(check_rows(M, N, y_st, "rms_norm", "y_st"));
+  TRY(check_rows(M, N, x_st, "rms_norm", "x_st"));
+  vm::NormArgs a{};
+  a.y = y; a.y_st = y_st; a.x = x; a.x_st = x_st; a.w = w;
+  a.M = M; a.N = N; a.offset = offset; a.eps = eps;
+  return hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_rms_norm(a, S(st)); }), "rms_norm");
+}
+
+int vm_fused_add_rms_norm(vm_bf16* y, int64_t y_st, vm_bf16* xo, int64_t xo_st, const vm_bf16* x,
+                          int64_t x_st, const vm_bf16* dx, int64_t dx_st, const vm_bf16* w, int M,
+                          int N, float eps, float offset, vm_stream st) {
+  TRY(check_aligned(y, "Y"));
+  TRY(check_aligned(xo, "X_out"));
+  TRY(check_aligned(x, "X"));
+  TRY(check_aligned(dx, "dX"));
+  TRY(check_aligned(w, "W"));
+  TRY(check_rows(M, N, y_st, "fused_add_rms_norm", "y_st"));
+  TRY(check_rows(M, N, xo_st, "fused_add_rms_norm", "xo_st"));
+  TRY(check_rows(M, N, x_st, "fused_add_rms_norm", "x_st"));
+  TRY(check_rows(M, N, dx_st, "fused_add_rms_norm", "dx_st"));
+  REQUIRE(xo != x || xo_st == x_st, VM_E_ARG,
+          "fused_add_rms_norm: X_out aliases X with a different column stride");
+  vm::NormArgs a{};
+  a.y = y; a.y_st = y_st; a.xo = xo; a.xo_st = xo_st; a.x = x; a.x_st = x_st;
+  a.dx = dx; a.dx_st = dx_st; a.w = w;
+  a.M = M; a.N = N; a.offset = offset; a.eps = eps;
+  return hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_rms_norm(a, S(st)); }),
+                    "fused_add_rms_norm");
+}
+
+int vm_silu_mul(vm_bf16* mid, int64_t mid_st, const vm_bf16* gu, int64_t gu_st, int I, int N,
+                vm_stream st) {
+  TRY(check_aligned(mid, "mid"));
+  TRY(check_aligned(gu, "gu"));
+  REQUIRE(I > 0 && I % 8 == 0, VM_E_UNSUPPORTED, "silu_mul: I = %d (a multiple of 8)", I);
+  REQUIRE(N >= 0, VM_E_ARG, "silu_mul: N = %d", N);
+  TRY(check_stride(mid_st, "mid_st"));
+  TRY(check_stride(gu_st, "gu_st"));
+  REQUIRE(N <= 1 || (mid_st >= I && gu_st >= 2 * (int64_t)I), VM_E_DIM,
+          "silu_mul: column strides (mid %lld, gu %lld) below (I, 2I) = (%d, %d)",
+          (long long)mid_st, (long long)gu_st, I, 2 * I);
+  vm::SiluMulArgs a{};
+  a.mid = mid; a.mid_st = mid_st; a.gu = gu; a.gu_st = gu_st; a.I = I; a.N = N;
+  return hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_silu_mul(a, S(st)); }), "silu_mul");
+}
+
+int vm_embed(vm_bf16* x, int64_t x_st, const vm_bf16* e, int64_t e_st, const int32_t* ids, int D,
+             int B, int vocab, vm_stream st) {
+  TRY(check_aligned(x, "x"));
+  TRY(check_aligned(e, "E"));
+  REQUIRE(ids || B == 0, VM_E_ARG, "embed: ids is NULL");
+  REQUIRE(D > 0 && D % 8 == 0, VM_E_UNSUPPORTED, "embed: D = %d (a multiple of 8)", D);
+  REQUIRE(B >= 0 && vocab > 0, VM_E_ARG, "embed: B = %d, vocab = %d", B, vocab);
+  TRY(check_stride(x_st, "x_st"));
+  TRY(check_stride(e_st, "e_st"));
+  REQUIRE((B <= 1 || x_st >= D) && (vocab <= 1 || e_st >= D), VM_E_DIM,
+          "embed: column strides (x %lld, E %lld) below D = %d", (long long)x_st, (long long)e_st, D);
+  vm::EmbedArgs a{};
+  a.x = x; a.x_st = x_st; a.e = e; a.e_st = e_st; a.ids = ids; a.D = D; a.B = B; a.vocab = vocab;
+  return hip_status(vm::launch_embed(a, S(st)), "embed");
+}
+
+int vm_generation_advance(int32_t* tokens_out, const int32_t* col_offsets, int32_t* step,
+                          int32_t* positions, const int32_t* result, int B, int max_new,
+                          vm_stream st) {
+  REQUIRE(step, VM_E_ARG, "generation_advance: step is NULL");
+  REQUIRE(B >= 0 && B <= 1 << 20, VM_E_ARG, "generation_advance: B = %d", B);
+  REQUIRE(B == 0 || (tokens_out && col_offsets && positions && result), VM_E_ARG,
+          "generation_advance: NULL pointer argument");
+  REQUIRE(max_new >= 0, VM_E_ARG, "generation_advance: max_new = %d", max_new);
+  vm::AdvanceArgs a{};
+  a.tokens_out = tokens_out; a.col_offsets = col_offsets; a.step = step; a.positions = positions;
+  a.result = result; a.B = B; a.max_new = max_new;
+  return hip_status(vm::launch_gen_advance(a, S(st)), "generation_advance");
+}
+
+// ---- f3: lm_head_argmax ------------------------------------------------------
+size_t vm_lm_head_argmax_scratch_bytes(int K, int N, int B) {
+  if (K <= 0 || N <= 0 || B < 0) return 0;
+  return (size_t)vm::lm_head_waves() * (size_t)B * (sizeof(float) + sizeof(int32_t));
+}
+
+int vm_lm_head_argmax(int32_t* result, const vm_bf16* x, int64_t x_st, const vm_bf16* w,
+                      int64_t w_st, int K, int N, int B, void* scratch, size_t scratch_bytes,
+                      vm_stream st) {
+  REQUIRE(result || B == 0, VM_E_ARG, "lm_head_argmax: Result is NULL");
+  TRY(check_aligned(x, "X"));
+  TRY(check_aligned(w, "W"));
+  REQUIRE(K > 0 && K % 8 == 0, VM_E_UNSUPPORTED, "lm_head_argmax: K = %d (a multiple of 8)", K);
+  REQUIRE(N > 0 && B >= 0, VM_E_ARG, "lm_head_argmax: N = %d, B = %d", N, B);
+  TRY(check_stride(x_st, "x_st"));
+  TRY(check_stride(w_st, "w_st"));
+  REQUIRE((B <= 1 || x_st >= K) && (N <= 1 || w_st >= K), VM_E_DIM,
+          "lm_head_argmax: column strides (X %lld, W %lld) below K = %d", (long long)x_st,
+          (long long)w_st, K);
+  if (B == 0) return VM_OK;
+  const size_t need = vm_lm_head_argmax_scratch_bytes(K, N, B);
+  REQUIRE(scratch != nullptr && scratch_bytes >= need, VM_E_SCRATCH,
+          "lm_head_argmax: scratch of %zu bytes < %zu required (vm_lm_head_argmax_scratch_bytes)",
+          scratch_bytes, need);
+  REQUIRE(((uintptr_t)scratch & 15) == 0, VM_E_ARG, "lm_head_argmax: scratch must be 16-byte aligned");
+  vm::LmHeadArgs a{};
+  a.x = x; a.x_st = x_st; a.w = w; a.w_st = w_st; a.K = K; a.N = N; a.B = B;
+  a.NW = vm::lm_head_waves();
+  a.pmax = reinterpret_cast<float*>(scratch);
+  a.pidx = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(scratch) +
+                                      (size_t)a.NW * B * sizeof(float));
+  a.result = result;
+  return hip_status(timed(VM_K_LM_HEAD, S(st), [&] { return vm::launch_lm_head_argmax(a, S(st)); }),
+                    "lm_head_argmax");
+}
+
 // ---- f1: linear ------------------------------------------------------------
 static int linear_check(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy) {
   REQUIRE(M > 0 && N > 0 && K > 0, VM_E_ARG, "linear: M = %d, N = %d, K = %d", M, N, K);

@@ -58,6 +58,12 @@ class AttnLayer:
     V_cache: torch.Tensor
     Wqkv: torch.Tensor | None = None   # (D, Dh*(2Hq+2Hkv)) -> torch (Dh*(2Hq+2Hkv), D)
     Wo: torch.Tensor | None = None     # (Dh*Hq, D) -> torch (D, Dh*Hq)
+    # the decoder-layer parts around the block (qwen35.jl:133-141): the two
+    # RMSNorm weights (applied as w + 1) and the MLP (mlp_parts, qwen35.jl:124-127)
+    norm1: torch.Tensor | None = None  # (D,)
+    norm2: torch.Tensor | None = None  # (D,)
+    Wgu: torch.Tensor | None = None    # (D, 2I) [gate | up] -> torch (2I, D)
+    Wd: torch.Tensor | None = None     # (I, D) -> torch (D, I)
 
 
 def attn_layer(cfg: AttnConfig, qw: torch.Tensor, kw: torch.Tensor, Wqkv=None,
@@ -116,17 +122,46 @@ class AttnModel:
 
 
 class Generation:
-    """The device clock (generate.jl:54-72): positions[b] is the 1-based column
-    of the current token = rope column = cache column = attended length."""
+    """The engine's device state (generate.jl:54-72). positions[b]: the 1-based
+    column of the current token = rope column = cache column = attended length
+    (the clock); step: the next 1-based row of tokens_out to write; result: the
+    last generated token per sequence (1-based); tokens_out: the harvested
+    tokens, (max_new, B) column-major (torch (B, max_new)); col_offsets[b] =
+    b * max_new. All on the device, so a captured step needs no host writes."""
 
-    def __init__(self, B: int):
-        self.positions = torch.zeros((B,), dtype=torch.int32, device="cuda")
+    def __init__(self, B: int, max_new: int = 1):
+        if B < 0 or max_new < 0:
+            raise ArgumentError(f"Generation(B = {B}, max_new = {max_new})")
+        dev = "cuda"
+        self.B, self.max_new = B, max_new
+        self.positions = torch.zeros((B,), dtype=torch.int32, device=dev)
+        self.step = torch.ones((1,), dtype=torch.int32, device=dev)
+        self.result = torch.ones((B,), dtype=torch.int32, device=dev)
+        self.tokens_out = torch.zeros((B, max_new), dtype=torch.int32, device=dev)
+        self.col_offsets = torch.arange(B, dtype=torch.int32, device=dev) * max_new
+
+    def reset_(self):
+        """reset!(gen) (generate.jl:74-78): step = 1, tokens_out = 0."""
+        self.step.fill_(1)
+        self.tokens_out.zero_()
+        return self
 
     def advance_(self):
-        """positions .+= 1 on the device (generate.jl:82-88)."""
-        call("vm_advance_positions", ops._p(self.positions), self.positions.numel(),
-             ops._stream())
+        """advance!(gen) (generate.jl:82-88), one kernel: tokens_out[step, :] =
+        result (when step <= max_new), step += 1, positions .+= 1."""
+        if self.max_new == 0:
+            call("vm_advance_positions", ops._p(self.positions), self.B, ops._stream())
+            self.step.add_(1)
+            return self
+        call("vm_generation_advance", ops._p(self.tokens_out), ops._p(self.col_offsets),
+             ops._p(self.step), ops._p(self.positions), ops._p(self.result), self.B,
+             self.max_new, ops._stream())
         return self
+
+    def poll(self, lo: int, hi: int):
+        """Rows lo..hi (1-based) of tokens_out on the host, (hi - lo + 1, B)
+        (generate.jl:92): one device-to-host copy."""
+        return self.tokens_out[:, lo - 1:hi].t().contiguous().cpu().numpy()
 
 
 def _qkv_views(qkv, cfg):
@@ -280,6 +315,7 @@ class CaptureSession:
     def __init__(self):
         self.exec = None
         self.stream = None
+        self.n_warm = 0     # eager warm-up steps spent (generate.jl:149-152)
 
     def capture(self, fn):
         if self.exec is not None:

@@ -1,0 +1,258 @@
+"""The decode engine around the gated-attention layers — src/llm/qwen35.jl:220-273
+(step!, the MLP), :389-419 (prefill!) and src/llm/generate.jl:54-196 (the clock,
+eager and captured generation).
+
+A model here is a stack of decoder layers whose mixer is the gated full-attention
+block (the reference's AttnLayer; its DeltaNet layers are not part of this
+path), each with its two RMSNorms and MLP, between an embedding table and an
+lm head (the embedding itself when tied). Greedy decoding only, as the
+reference's lm_head_argmax!.
+
+Every temporary of a decode step lives in buffers the model allocates once (the
+reference's Arena frames, qwen35.jl:1-6): the residual stream x, the normed xn,
+the mixer / MLP output h, the MLP's packed gate-up gu and mid, the lm-head
+partials, the projections' workspace. So ``step_`` allocates nothing once warm,
+every step uses the same addresses, and (step_; advance_) captures into a
+hipGraph that replays self-advancing: the decode loop is one graph launch per
+token and nothing else on the host.
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from . import ops
+from ._lib import ArgumentError, DimensionMismatch
+from .layer import (AttnConfig, AttnLayer, AttnModel, CaptureSession, Generation, attn_layer,
+                    decode_, forward)
+
+
+@dataclass(frozen=True)
+class ModelConfig:
+    """The text-config facts the step reads (qwen35.jl:82-96): the attention
+    block's (with D the hidden size and B, Ctx the decode batch and capacity),
+    the MLP's intermediate size, the vocabulary, the layer count."""
+    attn: AttnConfig = field(default_factory=AttnConfig)
+    inter: int = 9216
+    vocab: int = 151936
+    n_layers: int = 8
+    tied: bool = True           # tie_word_embeddings: the head IS the embedding
+
+    @property
+    def D(self) -> int:
+        return self.attn.D
+
+    @property
+    def B(self) -> int:
+        return self.attn.B
+
+
+class Model:
+    """Qwen35 (qwen35.jl:46-55) for a stack of attention layers: cfg, the
+    embedding E (D, vocab) (torch (vocab, D)), the head (E itself when tied), the
+    final norm weight, the layers, and the decode space."""
+
+    def __init__(self, cfg: ModelConfig, layers, E, head, norm_w):
+        if len(layers) == 0:
+            raise ArgumentError("a model needs at least one layer")
+        D, B, I = cfg.D, cfg.B, cfg.inter
+        if tuple(E.shape) != (cfg.vocab, D) or tuple(head.shape) != (cfg.vocab, D):
+            raise DimensionMismatch(f"E / head must be (D, vocab) = ({D}, {cfg.vocab})")
+        self.cfg, self.layers, self.E, self.head, self.norm_w = cfg, list(layers), E, head, norm_w
+        self.attn = AttnModel(cfg.attn)
+        bf = dict(dtype=torch.bfloat16, device="cuda")
+        # the step frame (qwen35.jl:248-250) and the layer frame's MLP temporaries
+        # (qwen35.jl:235-238), one set for the whole stack
+        self.x = torch.empty((B, D), **bf)
+        self.xn = torch.empty((B, D), **bf)
+        self.h = torch.empty((B, D), **bf)
+        self.gu = torch.empty((B, 2 * I), **bf)
+        self.mid = torch.empty((B, I), **bf)
+        self.lm_scratch = torch.empty(max(ops.lm_head_argmax_scratch_bytes(self.xn, head), 16),
+                                      dtype=torch.uint8, device="cuda")
+
+    def workspace(self) -> torch.Tensor:
+        """The projections' workspace, sized for every decode-step problem (grown
+        here, eagerly, so a captured step finds it already large enough)."""
+        l0 = self.layers[0]
+        need = max(ops.linear_workspace_bytes(self.xn, l0.Wgu, self.gu),
+                   ops.linear_workspace_bytes(self.mid, l0.Wd, self.h))
+        return self.attn.linear_workspace(need)
+
+
+def random_model(cfg: ModelConfig, *, seed: int = 0) -> Model:
+    """A model of `cfg` with seeded synthetic weights on the device (the fill
+    stream the CPU tests reproduce): projections N(0, 1/K), norm weights
+    N(0, 0.05) (applied as w + 1), embedding N(0, 1)."""
+    a, D, I = cfg.attn, cfg.D, cfg.inter
+    S = 2 * a.Hq + 2 * a.Hkv
+
+    def w(shape, s, scale):
+        t = torch.empty(shape, dtype=torch.bfloat16, device="cuda")
+        return ops.fill_normal_(t, s, scale=scale)
+
+    layers = []
+    for i in range(cfg.n_layers):
+        s0 = seed * 1000 + 16 * i
+        l = attn_layer(a, w((a.Dh,), s0 + 1, 0.05), w((a.Dh,), s0 + 2, 0.05),
+                       Wqkv=w((S * a.Dh, D), s0 + 3, D ** -0.5),
+                       Wo=w((D, a.Hq * a.Dh), s0 + 4, (a.Hq * a.Dh) ** -0.5))
+        l.norm1 = w((D,), s0 + 5, 0.05)
+        l.norm2 = w((D,), s0 + 6, 0.05)
+        l.Wgu = w((2 * I, D), s0 + 7, D ** -0.5)
+        l.Wd = w((D, I), s0 + 8, I ** -0.5)
+        layers.append(l)
+    E = w((cfg.vocab, D), seed * 1000 + 997, 1.0)
+    head = E if cfg.tied else w((cfg.vocab, D), seed * 1000 + 998, 1.0)
+    return Model(cfg, layers, E, head, w((D,), seed * 1000 + 999, 0.05))
+
+
+def _need_layer(l: AttnLayer):
+    for n in ("norm1", "norm2", "Wgu", "Wd", "Wqkv", "Wo"):
+        if getattr(l, n) is None:
+            raise ArgumentError(f"decoder layer has no {n}")
+
+
+def mlp_(h, l: AttnLayer, m: Model, xn):
+    """mlp!(h, mlp, cfg, xn) — qwen35.jl:234-243: gu = linear(xn, Wgu), mid =
+    silu(gate) .* up, h = linear(mid, Wd); temporaries in the model's space."""
+    ws = m.workspace()
+    ops.linear_({"y": m.gu}, xn, l.Wgu, workspace=ws)
+    ops.silu_mul_(m.mid, m.gu)
+    ops.linear_({"y": h}, m.mid, l.Wd, workspace=ws)
+    return h
+
+
+def step_(m: Model, gen: Generation):
+    """step!(m, gen) — qwen35.jl:245-273, one token per sequence, the capture
+    target: x = E[:, result]; xn = rms_norm(x, norm1 of layer 1); per layer the
+    mixer, the fused residual add + norm2, the MLP, the fused residual add + the
+    next layer's norm1 (the final norm after the last); result = argmax of the
+    head's logits. Reads gen.result and gen.positions only; writes gen.result.
+    Every norm is applied as (w + 1) (offset = 1)."""
+    cfg = m.cfg
+    if gen.B != cfg.B:
+        raise DimensionMismatch(f"Generation has B = {gen.B}, the model B = {cfg.B}")
+    eps = cfg.attn.eps
+    x, xn, h = m.x, m.xn, m.h
+    ops.embed_(x, m.E, gen.result)
+    ops.rms_norm_({"Y": xn}, x, m.layers[0].norm1, eps=eps, offset=1.0)
+    n = len(m.layers)
+    for i, l in enumerate(m.layers):
+        _need_layer(l)
+        decode_(h, l, m.attn, gen, xn)
+        ops.fused_add_rms_norm_({"Y": xn, "Xp": x}, x, h, l.norm2, eps=eps, offset=1.0)
+        mlp_(h, l, m, xn)
+        next_w = m.norm_w if i == n - 1 else m.layers[i + 1].norm1
+        ops.fused_add_rms_norm_({"Y": xn, "Xp": x}, x, h, next_w, eps=eps, offset=1.0)
+    ops.lm_head_argmax_({"Result": gen.result}, xn, m.head, scratch=m.lm_scratch)
+    return gen
+
+
+def prefill_(m: Model, gen: Generation, ids, *, offset: int = 0):
+    """prefill!(m, gen, ids; offset) — qwen35.jl:389-419, eager: ids (T, B)
+    (torch (B, T) int32, 1-based) continue a resident prefix of `offset` tokens;
+    fills every layer's cache columns offset+1 .. offset+T, puts the first
+    generated token in gen.result and, last, seeds the clock: positions =
+    offset + T + 1."""
+    cfg = m.cfg
+    if ids.dim() != 2 or ids.dtype != torch.int32:
+        raise ArgumentError("ids must be a (B, T) int32 tensor of 1-based token ids")
+    B, T = ids.shape
+    if B != cfg.B:
+        raise DimensionMismatch(f"size(ids, 2) = {B} does not match B = {cfg.B}")
+    if offset + T > cfg.attn.Ctx:
+        raise ArgumentError(f"prefill past Ctx: offset {offset} + {T} tokens > {cfg.attn.Ctx}")
+    eps = cfg.attn.eps
+    x = torch.empty((B, T, cfg.D), dtype=torch.bfloat16, device="cuda")
+    ops.embed_(x.view(B * T, cfg.D), m.E, ids.reshape(-1).contiguous())
+    xn = ops.rms_norm(x, m.layers[0].norm1, eps=eps, offset=1.0)["Y"]
+    n = len(m.layers)
+    for i, l in enumerate(m.layers):
+        _need_layer(l)
+        h = forward(l, m.attn, xn, T, B, offset=offset)
+        ops.fused_add_rms_norm_({"Y": xn, "Xp": x}, x, h, l.norm2, eps=eps, offset=1.0)
+        ws = m.attn.linear_workspace(ops.linear_workspace_bytes(xn, l.Wgu))
+        gu = ops.linear(xn, l.Wgu, workspace=ws)["y"]
+        mid = torch.empty((B, T, cfg.inter), dtype=torch.bfloat16, device="cuda")
+        ops.silu_mul_(mid, gu)
+        ws = m.attn.linear_workspace(ops.linear_workspace_bytes(mid, l.Wd))
+        h = ops.linear(mid, l.Wd, workspace=ws)["y"]
+        next_w = m.norm_w if i == n - 1 else m.layers[i + 1].norm1
+        ops.fused_add_rms_norm_({"Y": xn, "Xp": x}, x, h, next_w, eps=eps, offset=1.0)
+    ops.lm_head_argmax_({"Result": gen.result}, xn[:, T - 1, :], m.head, scratch=m.lm_scratch)
+    gen.positions.fill_(offset + T + 1)   # the final act: seed the clock
+    return gen
+
+
+def _run(m: Model, gen: Generation, ids, *, max_new_tokens: int, launch_step, eos, poll_every,
+         on_tokens, prefill_offset: int = 0):
+    """_run! (generate.jl:95-130): prefill, harvest its token as row 1, then
+    launch_step() per token with an amortised device->host poll every
+    `poll_every` tokens for streaming and EOS."""
+    if max_new_tokens < 1 or max_new_tokens > gen.max_new:
+        raise ArgumentError(f"max_new_tokens = {max_new_tokens} outside 1..{gen.max_new}")
+    gen.reset_()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ev[0].record()
+    prefill_(m, gen, ids, offset=prefill_offset)
+    gen.advance_()                       # harvest prefill's token as row 1
+    ev[1].record()
+    n, polled, stop = 1, 0, False
+    ev[2].record()
+    while n < max_new_tokens and not stop:
+        launch_step()
+        n += 1
+        if n - polled >= poll_every or n == max_new_tokens:
+            chunk = gen.poll(polled + 1, n)
+            if on_tokens is not None:
+                on_tokens(chunk)
+            if eos is not None:
+                stop = bool((chunk == int(eos)).any())
+            polled = n
+    ev[3].record()
+    torch.cuda.synchronize()
+    tokens = gen.poll(1, n)
+    prefill_s = ev[0].elapsed_time(ev[1]) * 1e-3
+    decode_s = ev[2].elapsed_time(ev[3]) * 1e-3
+    timing = dict(prefill_s=prefill_s, decode_s=decode_s, decode_tokens=n - 1,
+                  tok_s=(n - 1) / decode_s if n > 1 else 0.0,
+                  itl_ms=1e3 * decode_s / (n - 1) if n > 1 else 0.0)
+    return tokens, timing
+
+
+def generate_(m: Model, gen: Generation, ids, *, max_new_tokens: int, eos=None,
+              poll_every: int = 8, on_tokens=None, prefill_offset: int = 0):
+    """generate!(model, gen, ids; max_new_tokens, ...) (generate.jl:132-145):
+    eager, every step launched from the host; the baseline the captured run
+    must match token for token. Returns (tokens (n, B) numpy int32, timing)."""
+    return _run(m, gen, ids, max_new_tokens=max_new_tokens, eos=eos, poll_every=poll_every,
+                on_tokens=on_tokens, prefill_offset=prefill_offset,
+                launch_step=lambda: (step_(m, gen), gen.advance_()))
+
+
+def generate_captured_(m: Model, gen: Generation, ids, *, max_new_tokens: int, warmup: int = 3,
+                       session: CaptureSession | None = None, eos=None, poll_every: int = 8,
+                       on_tokens=None, prefill_offset: int = 0):
+    """generate_captured!(model, gen, ids; max_new_tokens, warmup, session, ...)
+    (generate.jl:147-196): `warmup` eager (step; advance) pairs, then one pair
+    captured into a hipGraph and replayed for the remaining tokens. Capture
+    records without executing, so warm-up's last state flows into the first
+    replay. A session passed across calls (same model and generation) keeps its
+    graph and warm-up count."""
+    s = session if session is not None else CaptureSession()
+
+    def launch_step():
+        if s.n_warm < warmup:
+            step_(m, gen)
+            gen.advance_()
+            s.n_warm += 1
+        else:
+            if s.exec is None:
+                s.capture(lambda: (step_(m, gen), gen.advance_()))
+            s.launch()
+
+    return _run(m, gen, ids, max_new_tokens=max_new_tokens, eos=eos, poll_every=poll_every,
+                on_tokens=on_tokens, prefill_offset=prefill_offset, launch_step=launch_step)

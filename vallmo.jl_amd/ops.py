@@ -24,6 +24,8 @@ __all__ = [
     "rope_tables", "qnorm_rope_", "knorm_rope_append_", "attention_", "attention",
     "decode_attention_", "decode_attention", "decode_scratch_bytes", "sigmoid_gate_",
     "sigmoid", "fill_normal_", "linear_", "linear", "linear_workspace_bytes",
+    "rms_norm_", "rms_norm", "fused_add_rms_norm_", "fused_add_rms_norm", "silu_mul_",
+    "embed_", "lm_head_argmax_", "lm_head_argmax", "lm_head_argmax_scratch_bytes",
 ]
 
 
@@ -263,6 +265,113 @@ def linear(x, W, **kw) -> dict:
     """Allocating linear (linear.jl:68-79): returns {"y": y}, torch (..., M)."""
     y = torch.empty(tuple(x.shape[:-1]) + (W.shape[0],), dtype=x.dtype, device=x.device)
     return linear_({"y": y}, x, W, **kw)
+
+
+def _cols(t, name, M=None):
+    """(M, N, column stride) of the reference's column-major (M, N) view of a
+    torch (..., M) bf16 tensor."""
+    _need(t, torch.bfloat16, name)
+    return t.shape[-1], _rows(t), _ld(t)
+
+
+def rms_norm_(outs, X, W, *, eps, offset=0.0):
+    """rms_norm!((; Y), X, W; eps, offset) — src/kernels/rms_norm.jl:33-50.
+    X, Y :: (M, N) (torch (..., M)), W :: (M,)."""
+    Y = _out(outs, "Y")
+    M, N, xs = _cols(X, "X")
+    My, Ny, ys = _cols(Y, "Y")
+    sizes(W=(W, f"{M}"))
+    if (My, Ny) != (M, N):
+        raise DimensionMismatch(f"Y is ({My}, {Ny}), X is ({M}, {N})")
+    _need(W, torch.bfloat16, "W")
+    call("vm_rms_norm", _p(Y), ys, _p(X), xs, _p(W), M, N, float(eps), float(offset), _stream())
+    return outs
+
+
+def rms_norm(X, W, **kw) -> dict:
+    """Allocating rms_norm (rms_norm.jl:52-57): {"Y": Y}."""
+    return rms_norm_({"Y": torch.empty_like(X)}, X, W, **kw)
+
+
+def fused_add_rms_norm_(outs, X, dX, W, *, eps, offset):
+    """fused_add_rms_norm!((; Y, X′), X, ΔX, W; eps, offset) —
+    src/kernels/residual_norm.jl:39-60: X′ = X + ΔX, Y = rms_norm(X′). X′ may be
+    X itself (the decode step's in-place residual, qwen35.jl:265). Keys "Y" and
+    "Xp" (X′)."""
+    Y, Xp = _out(outs, "Y"), _out(outs, "Xp")
+    M, N, xs = _cols(X, "X")
+    for t, n in ((dX, "dX"), (Y, "Y"), (Xp, "Xp")):
+        Mt, Nt, _ = _cols(t, n)
+        if (Mt, Nt) != (M, N):
+            raise DimensionMismatch(f"{n} is ({Mt}, {Nt}), X is ({M}, {N})")
+    sizes(W=(W, f"{M}"))
+    _need(W, torch.bfloat16, "W")
+    call("vm_fused_add_rms_norm", _p(Y), _ld(Y), _p(Xp), _ld(Xp), _p(X), xs, _p(dX), _ld(dX),
+         _p(W), M, N, float(eps), float(offset), _stream())
+    return outs
+
+
+def fused_add_rms_norm(X, dX, W, **kw) -> dict:
+    """Allocating fused_add_rms_norm (residual_norm.jl:62-65): {"Y": Y, "Xp": X′}."""
+    return fused_add_rms_norm_({"Y": torch.empty_like(X), "Xp": torch.empty_like(X)}, X, dX, W,
+                               **kw)
+
+
+def silu_mul_(mid, gu):
+    """mid .= silu.(gate) .* up, (gate; up) the two halves of each column of the
+    packed gate-up projection gu :: (2I, N) — the MLP of src/llm/qwen35.jl:234-243.
+    mid :: (I, N) (torch (..., I))."""
+    I2, N, gs = _cols(gu, "gu")
+    I, Nm, ms = _cols(mid, "mid")
+    if I2 != 2 * I or Nm != N:
+        raise DimensionMismatch(f"gu is ({I2}, {N}), mid is ({I}, {Nm}): expected (2I, N), (I, N)")
+    call("vm_silu_mul", _p(mid), ms, _p(gu), gs, I, N, _stream())
+    return mid
+
+
+def embed_(x, E, ids):
+    """x .= E[:, ids] — the decode step's embedding gather (src/llm/qwen35.jl:251).
+    E :: (D, vocab) (torch (vocab, D)), ids :: (B,) int32 1-based, x :: (D, B)."""
+    D, B, xs = _cols(x, "x")
+    De, vocab, es = _cols(E, "E")
+    if De != D:
+        raise DimensionMismatch(f"size(E, 1) = {De} does not match size(x, 1) = {D}")
+    sizes(ids=(ids, f"{B}"))
+    _need(ids, torch.int32, "ids")
+    call("vm_embed", _p(x), xs, _p(E), es, _p(ids), D, B, vocab, _stream())
+    return x
+
+
+def lm_head_argmax_scratch_bytes(X, W) -> int:
+    """Per-wave partials of lm_head_argmax! (the reference's LocalMax / LocalIdx,
+    lm_head_topk.jl:149-160)."""
+    return int(_lib.load().vm_lm_head_argmax_scratch_bytes(X.shape[-1], _rows(W), _rows(X)))
+
+
+def lm_head_argmax_(outs, X, W, *, scratch=None):
+    """lm_head_argmax!((; Result), X, W) — src/kernels/lm_head_topk.jl:109-147:
+    Result[b] = argmax(W^T X[:, b]), 1-based, ties to the smallest index, the
+    logits never written. X :: (K, B) (torch (B, K)), W :: (K, N) K-major (torch
+    (N, K): the embedding table itself for a tied head)."""
+    R = _out(outs, "Result")
+    K, B, xs = _cols(X, "X")
+    Kw, N, ws = _cols(W, "W")
+    if Kw != K:
+        raise DimensionMismatch(f"size(W, 1) = {Kw} does not match size(X, 1) = {K}")
+    sizes(Result=(R, f"{B}"))
+    _need(R, torch.int32, "Result")
+    need = lm_head_argmax_scratch_bytes(X, W)
+    if scratch is None:
+        scratch = torch.empty(max(need, 16), dtype=torch.uint8, device=X.device)
+    call("vm_lm_head_argmax", _p(R), _p(X), xs, _p(W), ws, K, N, B, _p(scratch), scratch.numel(),
+         _stream())
+    return outs
+
+
+def lm_head_argmax(X, W, **kw) -> dict:
+    """Allocating lm_head_argmax (lm_head_topk.jl:149-163): {"Result": (B,) int32}."""
+    R = torch.empty((_rows(X),), dtype=torch.int32, device=X.device)
+    return lm_head_argmax_({"Result": R}, X, W, **kw)
 
 
 def fill_normal_(X, seed: int, *, scale: float = 1.0, shift: float = 0.0):
