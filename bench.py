@@ -15,7 +15,9 @@ advancing on the device)
 in HBM GB/s of K/V actually attended (4096 B per token) + 32 KiB per sequence,
 and config 1 (B=1 at 512 tokens, launch-latency-bound) as time per step.
 Key "prefill_config5": BASELINE config 5 (B=4 ragged chunks after 8-32 K
-priors) in algorithmic TFLOP/s, step and attention kernel. Key "layer": whole
+priors) in algorithmic TFLOP/s, step and attention kernel. Key "decode_step": the
+whole captured decode step of an 8-layer attention stack with MLPs and the lm
+head (B = 32), and the lm-head GEMV + argmax alone. Key "layer": whole
 attention layers, hidden state to hidden state (the qkv and Wo projections on
 hipBLASLt around the block) at the config-2 prefill and config-3 decode shapes.
 
@@ -475,6 +477,86 @@ def bench_layer(vm, torch, reps=20):
     return res
 
 
+def bench_step(vm, torch, replays=60, seed=9):
+    """The whole decode step (§ row: step!, qwen35.jl:245-273) of a stack of 8
+    attention layers at hidden 2560 (MLP 9216, vocab 151936 as a stand-in),
+    B = 32 at ragged attended lengths ~U{1024..8128}: (step!; advance!) captured
+    once and replayed on a dedicated stream. HBM bytes per step: every weight
+    (projections, MLPs, norms, head) once, the attended K/V, the caches'
+    appended rows. Also the lm head alone (GEMV + argmax) at B = 1 and 32."""
+    B, Ctx, L = 32, 8192, 8
+    a = vm.AttnConfig(D=DM, Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=Ctx, B=B)
+    cfg = vm.ModelConfig(attn=a, inter=9216, vocab=151936, n_layers=L, tied=True)
+    m = vm.random_model(cfg, seed=seed)
+    for i, l in enumerate(m.layers):
+        vm.fill_normal_(l.K_cache, 9000 + i)
+        vm.fill_normal_(l.V_cache, 9100 + i)
+    rng = np.random.default_rng(seed)
+    pos0 = rng.integers(1024, Ctx - replays - 8, size=B).astype(np.int32)
+    gen = vm.Generation(B, replays + 16)
+    gen.positions.copy_(torch.as_tensor(pos0).cuda())
+    gen.result.copy_(torch.as_tensor(rng.integers(1, cfg.vocab + 1, size=B).astype(np.int32)).cuda())
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):   # warm-up: plans, workspace
+            vm.step_(m, gen)
+            gen.advance_()
+        sess = vm.CaptureSession().capture(lambda: (vm.step_(m, gen), gen.advance_()))
+        for _ in range(3):
+            sess.launch()
+        p_start = gen.positions.clone()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            sess.launch()
+        e1.record()
+    torch.cuda.synchronize()
+    sess.close()
+    ms = e0.elapsed_time(e1) / replays
+    p_start = p_start.cpu().numpy().astype(np.float64)
+    kv = float(np.sum(p_start + (replays - 1) / 2.0)) * HK * D * 2 * 2 * L  # attended K + V
+    w_layer = sum(t.numel() * 2 for t in (m.layers[0].Wqkv, m.layers[0].Wo, m.layers[0].Wgu,
+                                          m.layers[0].Wd))
+    w_bytes = float(L * w_layer + m.head.numel() * 2)
+    nbytes = w_bytes + kv
+    res = {
+        "config": f"{L} gated-attention layers + MLPs, hidden {DM}, MLP {cfg.inter}, vocab "
+                  f"{cfg.vocab} (tied head), B={B}, attended lengths U{{1024..8128}} (seed {seed}), "
+                  f"(step!; advance!) captured, {replays} replays on a dedicated stream",
+        "ms_per_step": ms,
+        "tokens_per_s": B / (ms * 1e-3),
+        "bytes_per_step": nbytes,
+        "weight_bytes": w_bytes,
+        "kv_bytes": kv,
+        "gbs": nbytes / (ms * 1e-3) / 1e9,
+        "frac_of_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+    }
+    # the lm head alone
+    lib = vm._lib
+    for b in (1, B):
+        x = m.xn[:b]
+        out = torch.empty((b,), dtype=torch.int32, device="cuda")
+        sc = torch.empty(max(vm.lm_head_argmax_scratch_bytes(x, m.head), 16), dtype=torch.uint8,
+                         device="cuda")
+        for _ in range(3):
+            vm.lm_head_argmax_({"Result": out}, x, m.head, scratch=sc)
+        lib.profile_select(lib.VM_K_LM_HEAD)
+        lib.profile_enable(True)
+        for _ in range(20):
+            vm.lm_head_argmax_({"Result": out}, x, m.head, scratch=sc)
+        torch.cuda.synchronize()
+        n, t = lib.profile_read(lib.VM_K_LM_HEAD)
+        lib.profile_enable(False)
+        lib.profile_select()
+        hb = m.head.numel() * 2.0
+        res[f"lm_head_B{b}"] = {"us": 1e3 * t / n, "gbs": hb / (t / n * 1e-3) / 1e9,
+                                "frac_of_hbm_peak": hb / (t / n * 1e-3) / 1e9 / PEAK_HBM_GBS}
+    del m
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_info():
     """CPU model, sockets x physical cores per socket, and logical CPUs of this host."""
     import subprocess
@@ -645,6 +727,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-config5", action="store_true", help="skip the config-5 prefill leg")
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer leg")
+    ap.add_argument("--no-step", action="store_true", help="skip the whole-decode-step leg")
     ap.add_argument("--no-settle", action="store_true",
                     help="skip the clock-settle phase (counter-collection runs)")
     ap.add_argument("--no-decode", action="store_true")
@@ -710,6 +793,13 @@ def main():
             f"TFLOP/s, Wo GEMM {lp['wo_gemm_tflops']:.0f} TFLOP/s")
         log(f"[bench] decode layer B=32: {ld['ms_per_layer_step']:.3f} ms, qkv GEMV "
             f"{ld['qkv_gemv_gbs']:.0f} GB/s, Wo GEMV {ld['wo_gemv_gbs']:.0f} GB/s")
+    step = None
+    if not args.no_step:
+        log("[bench] whole decode step, 8 attention layers + MLPs + lm head, B=32")
+        step = bench_step(vm, torch)
+        log(f"[bench] step: {step['ms_per_step']:.3f} ms/step, {step['tokens_per_s']:.0f} tok/s, "
+            f"{step['gbs']:.0f} GB/s; lm head alone B=1 {step['lm_head_B1']['gbs']:.0f} GB/s, "
+            f"B=32 {step['lm_head_B32']['gbs']:.0f} GB/s")
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle), configs 1-5")
@@ -749,6 +839,7 @@ def main():
         "prefill_config5": pf5,
         "decode": decode,
         "layer": layer,
+        "decode_step": step,
     }
     print(json.dumps(line), flush=True)
 

@@ -304,8 +304,9 @@ int vm_generation_advance(int32_t* tokens_out, const int32_t* col_offsets, int32
  * Result[b] = argmax_v W[:, v] . X[:, b], 1-based, ties to the smallest v;
  * bf16 products, fp32 sums; the logits are never written. X (K, B), W (K, N)
  * K-major (the embedding's own orientation, so a tied head needs no copy).
- * scratch: vm_lm_head_argmax_scratch_bytes(K, N, B) bytes of device memory
- * (per-wave partials; the reference's LocalMax / LocalIdx), 16-byte aligned. */
+ * K a multiple of 64. scratch: vm_lm_head_argmax_scratch_bytes(K, N, B) bytes
+ * of device memory (per-wave partials; the reference's LocalMax / LocalIdx),
+ * 16-byte aligned.                                                           */
 size_t vm_lm_head_argmax_scratch_bytes(int K, int N, int B);
 int vm_lm_head_argmax(int32_t* result, const vm_bf16* x, int64_t x_st, const vm_bf16* w,
                       int64_t w_st, int K, int N, int B, void* scratch, size_t scratch_bytes,

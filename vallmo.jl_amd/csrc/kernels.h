@@ -196,7 +196,7 @@ struct LmHeadArgs {
   int64_t x_st;
   const uint16_t* w;    // (K, N) K-major, column v at w + v * w_st
   int64_t w_st;
-  int K, N, B;          // K a multiple of 8
+  int K, N, B;          // K a multiple of 64
   int cols;             // vocab columns per wave (set by the launcher)
   int NW;               // waves of the split pass (lm_head_waves())
   float* pmax;          // partials [NW][B]

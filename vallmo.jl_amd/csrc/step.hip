@@ -165,47 +165,156 @@ hipError_t launch_gen_advance(const AdvanceArgs& a, hipStream_t st) {
 // ---- lm head: Result[b] = argmax_v W[:, v] . X[:, b] (1-based, ties to the
 // smallest v), without writing the logits.
 //
-// Wave w takes the vocab columns [w cols, (w + 1) cols) in passes of up to four
-// 32-column tiles and one 32-column batch tile (blockIdx.y). Per 16-deep k step
-// one 32x32x16 bf16 MFMA per tile: A = W^T (lane (j, h): column v0 + j, k + 8h
-// .. +7, one 16-byte load), B = X (lane (j, h): column b0 + j, the same k), so
+// Wave w takes the vocab columns [w cols, (w + 1) cols) in balanced passes of up
+// to four 32-column tiles, and one 32-column batch tile (blockIdx.y). The tiles
+// stream through the wave's own LDS in groups of 64 k, double buffered, by direct
+// global->LDS loads of 1 KB each (8 columns x 128 contiguous bytes), so every
+// weight byte is read once, in whole lines. Per 16-deep k step one 32x32x16
+// bf16 MFMA per tile: A = W^T (lane (j, h): column v0 + j, k + 8h .. +7, from
+// LDS), B = X (lane (j, h): column b0 + j, the same k, staged the same way), so
 // lane (j, h) ends with the logits of batch column b0 + j at vocab rows
-// 8 (r / 4) + 4 h + r % 4 of the tile. Each weight byte is read once. The next
-// four k steps' loads are in flight while the current ones multiply. The wave
-// keeps a running (max, smallest index) per batch column; LmCombine folds the
-// waves' partials.
+// 8 (r / 4) + 4 h + r % 4 of the tile. The wave keeps a running (max, smallest
+// index) per batch column; the combine kernel folds the waves' partials.
 namespace {
 
-constexpr int LM_KG = 4;  // k steps (of 16) per load group
-constexpr int LM_T = 4;   // vocab tiles per pass
-
-struct LmGroup {
-  uint4 w[LM_T][LM_KG];
-  uint4 x[LM_KG];
-};
-
-// the loads of k steps k0 .. k0 + 63; this lane's 8 values start at k + 8h
-// (already in wcol0 / xcol; K is a multiple of 8, so a slice is all in or out)
-__device__ __forceinline__ void lm_load(LmGroup& g, const LmHeadArgs& a, const uint16_t* wcol0,
-                                        const uint16_t* xcol, int h, int k0, int ntile,
-                                        const int (&vok)[LM_T]) {
-#pragma unroll
-  for (int s = 0; s < LM_KG; ++s) {
-    const int k = k0 + 16 * s;
-    const bool kin = k + 8 * h < a.K;
-    g.x[s] = kin ? load16(xcol + k) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int t = 0; t < LM_T; ++t) {
-      if (t < ntile)
-        g.w[t][s] = (kin && vok[t]) ? load16_nt(wcol0 + (int64_t)(32 * t) * a.w_st + k)
-                                    : make_uint4(0, 0, 0, 0);
-    }
-  }
-}
+constexpr int LM_TB = 2048;  // bf16 of one staged tile: 32 columns x 64 k (4 KB)
 
 // (v, i) beats (bv, bi): larger, or equal with the smaller index
 __device__ __forceinline__ bool lm_better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
+}
+
+// Direct global->LDS loads of k0 .. k0 + 63 of one 32-column tile of a K-major
+// matrix (column c at m + c * st), columns c0 .. c0 + 31 clamped to < n:
+// instruction i moves columns 8i .. 8i + 7, 128 contiguous bytes each (1 KB per
+// instruction, non-temporal); column c's 16-byte chunk q lands at position
+// q ^ (c & 7) of its 128-byte row (conflict-free operand reads).
+__device__ __forceinline__ void lm_dma_tile(uint16_t* dst, const uint16_t* m, int64_t st, int c0,
+                                            int n, int k0, int lane) {
+  const int cl = lane >> 3, p = lane & 7;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = 8 * i + cl;
+    const uint16_t* src = m + (int64_t)min(c0 + c, n - 1) * st + k0 + 8 * (p ^ (c & 7));
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dst + 512 * i),
+                                     16, 0, 2);
+  }
+}
+// a group: the T weight tiles at v0, then the batch tile at b0 (slot T)
+template <int T>
+__device__ __forceinline__ void lm_dma(uint16_t* buf, const LmHeadArgs& a, int v0, int b0, int k0,
+                                       int lane) {
+#pragma unroll
+  for (int t = 0; t < T; ++t) lm_dma_tile(buf + t * LM_TB, a.w, a.w_st, v0 + 32 * t, a.N, k0, lane);
+  lm_dma_tile(buf + T * LM_TB, a.x, a.x_st, b0, a.B, k0, lane);
+}
+
+// The products of one staged group: step s of tile t reads lane (j, h)'s A
+// operand, column j k 16s + 8h .. +7, from LDS. The reads are issued from asm
+// (a compiler-visible read would first drain every load in flight, the other
+// buffer's included) one step ahead, each released by a counted wait tied to
+// its registers.
+typedef unsigned int lm_u32x4 __attribute__((ext_vector_type(4)));  // asm register operand
+template <int T>
+__device__ __forceinline__ void lm_read(lm_u32x4 (&w)[T], const uint16_t* buf, int j, int h, int s) {
+  const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)buf;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const uint32_t addr = base + 2u * (uint32_t)(t * LM_TB + 64 * j + 8 * ((2 * s + h) ^ (j & 7)));
+    asm volatile("ds_read_b128 %0, %1" : "=v"(w[t]) : "v"(addr));
+  }
+}
+template <int N, int T>
+__device__ __forceinline__ void lm_take(lm_u32x4 (&w)[T]) {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+#pragma unroll
+  for (int t = 0; t < T; ++t) asm volatile("" : "+v"(w[t]));
+}
+template <int T>
+__device__ __forceinline__ void lm_mult(const uint16_t* buf, int j, int h, f32x16 (&acc)[T]) {
+  // slots 0 .. T-1: the weight tiles (A operands), slot T: the batch tile (B)
+  lm_u32x4 w0[T + 1], w1[T + 1];
+  lm_read<T + 1>(w0, buf, j, h, 0);
+  lm_read<T + 1>(w1, buf, j, h, 1);
+  lm_take<T + 1, T + 1>(w0);
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+    acc[t] = mfma32(__builtin_bit_cast(uint4, w0[t]), __builtin_bit_cast(uint4, w0[T]), acc[t]);
+  lm_read<T + 1>(w0, buf, j, h, 2);
+  lm_take<T + 1, T + 1>(w1);
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+    acc[t] = mfma32(__builtin_bit_cast(uint4, w1[t]), __builtin_bit_cast(uint4, w1[T]), acc[t]);
+  lm_read<T + 1>(w1, buf, j, h, 3);
+  lm_take<T + 1, T + 1>(w0);
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+    acc[t] = mfma32(__builtin_bit_cast(uint4, w0[t]), __builtin_bit_cast(uint4, w0[T]), acc[t]);
+  lm_take<0, T + 1>(w1);
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+    acc[t] = mfma32(__builtin_bit_cast(uint4, w1[t]), __builtin_bit_cast(uint4, w1[T]), acc[t]);
+}
+
+// one object per buffer: reads of one are seen not to alias the loads landing in
+// the other (no drain of every load in flight before each read)
+__shared__ __attribute__((aligned(16))) uint16_t lm_buf0[4][5 * LM_TB];
+__shared__ __attribute__((aligned(16))) uint16_t lm_buf1[4][5 * LM_TB];
+
+// One pass: T tiles (vocab columns v0 .. v0 + 32T - 1) over all of K (a multiple
+// of 64) in groups of 64, double buffered; then the running (max, index) of this
+// lane's batch column, in vocab order.
+template <int T>
+__device__ __forceinline__ void lm_pass(const LmHeadArgs& a, int v0, int vend, int bt0, int lane,
+                                        float& best, int& besti) {
+  const int j = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  uint16_t* b0 = lm_buf0[wv];
+  uint16_t* b1 = lm_buf1[wv];
+  f32x16 acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+  constexpr int PER = 4 * (T + 1);  // loads per group
+  const int G = a.K / 64;            // groups, >= 1
+  lm_dma<T>(b0, a, v0, bt0, 0, lane);
+  int g = 0;
+  // steady state, no branch in the body: groups g (in b0) and g + 1 (into b1),
+  // then g + 2 into b0 again
+  for (; g + 2 < G; g += 2) {
+    lm_dma<T>(b1, a, v0, bt0, 64 * (g + 1), lane);
+    wait_vmcnt<PER>();
+    lm_mult<T>(b0, j, h, acc);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // b0's reads are in: refill it
+    lm_dma<T>(b0, a, v0, bt0, 64 * (g + 2), lane);
+    wait_vmcnt<PER>();
+    lm_mult<T>(b1, j, h, acc);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+  if (g + 1 < G) {  // the last two groups
+    lm_dma<T>(b1, a, v0, bt0, 64 * (g + 1), lane);
+    wait_vmcnt<PER>();
+    lm_mult<T>(b0, j, h, acc);
+    wait_vmcnt<0>();
+    lm_mult<T>(b1, j, h, acc);
+  } else {          // the last group
+    wait_vmcnt<0>();
+    lm_mult<T>(b0, j, h, acc);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the next pass refills both
+  // lane (j, h): rows 8 (r / 4) + 4 h + r % 4 of each tile, increasing in r
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int v = v0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+      const float l = v < vend ? acc[t][r] : -INFINITY;
+      if (lm_better(l, v, best, besti)) {
+        best = l;
+        besti = v;
+      }
+    }
+  }
 }
 
 }  // namespace
@@ -219,52 +328,21 @@ void lm_head_split_kernel(LmHeadArgs a) {
   const int vbeg = w * a.cols, vend = min(vbeg + a.cols, a.N);
   float best = -INFINITY;
   int besti = 0x7fffffff;
-  const bool xok = b0 + j < a.B;  // padded batch lanes read column b0 (not stored)
-  const uint16_t* xcol = a.x + (int64_t)(xok ? b0 + j : b0) * a.x_st + 8 * h;
-  for (int v0 = vbeg; v0 < vend; v0 += 32 * LM_T) {
-    const int ntile = min(LM_T, (vend - v0 + 31) / 32);  // uniform
-    int vok[LM_T];
-#pragma unroll
-    for (int t = 0; t < LM_T; ++t) vok[t] = v0 + 32 * t + j < a.N;
-    // column v0 + 32 t + j of this lane, clamped into the table
-    const uint16_t* wcol0 = a.w + (int64_t)min(v0 + j, a.N - 1) * a.w_st + 8 * h;
-    f32x16 acc[LM_T];
-#pragma unroll
-    for (int t = 0; t < LM_T; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
-    // two register groups in turn: one multiplies while the other's loads land
-    constexpr int KS = 16 * LM_KG;
-    auto mult = [&](const LmGroup& g) __attribute__((always_inline)) {
-#pragma unroll
-      for (int s = 0; s < LM_KG; ++s)
-#pragma unroll
-        for (int t = 0; t < LM_T; ++t)
-          if (t < ntile) acc[t] = mfma32(g.w[t][s], g.x[s], acc[t]);
-    };
-    LmGroup g0, g1;
-    lm_load(g0, a, wcol0, xcol, h, 0, ntile, vok);
-    for (int k0 = 0; k0 < a.K; k0 += 2 * KS) {
-      if (k0 + KS < a.K) lm_load(g1, a, wcol0, xcol, h, k0 + KS, ntile, vok);
-      mult(g0);
-      if (k0 + 2 * KS < a.K) lm_load(g0, a, wcol0, xcol, h, k0 + 2 * KS, ntile, vok);
-      if (k0 + KS < a.K) mult(g1);
+  const bool xok = b0 + j < a.B;  // padded batch columns re-read the last one (not stored)
+  // the wave's tiles in balanced passes of at most four
+  const int ntiles = vend > vbeg ? (vend - vbeg + 31) / 32 : 0;
+  const int npass = (ntiles + 3) / 4;
+  int v0 = vbeg;
+  for (int p = 0; p < npass; ++p) {
+    const int rem = ntiles - (v0 - vbeg) / 32;
+    const int t_p = (rem + npass - p - 1) / (npass - p);
+    switch (t_p) {
+      case 4: lm_pass<4>(a, v0, vend, b0, lane, best, besti); break;
+      case 3: lm_pass<3>(a, v0, vend, b0, lane, best, besti); break;
+      case 2: lm_pass<2>(a, v0, vend, b0, lane, best, besti); break;
+      default: lm_pass<1>(a, v0, vend, b0, lane, best, besti); break;
     }
-    // the tiles' logits, in increasing vocab order within each lane half
-#pragma unroll
-    for (int t = 0; t < LM_T; ++t) {
-      if (t < ntile) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int v = v0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-          const float l = v < vend ? acc[t][r] : -INFINITY;
-          if (lm_better(l, v, best, besti)) {
-            best = l;
-            besti = v;
-          }
-        }
-      }
-    }
+    v0 += 32 * t_p;
   }
   // the two lane halves hold the same batch column: fold them
   const auto pv = __builtin_amdgcn_permlane32_swap(__float_as_uint(best), __float_as_uint(best), false, false);

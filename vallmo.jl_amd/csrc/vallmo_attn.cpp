@@ -719,7 +719,8 @@ int vm_lm_head_argmax(int32_t* result, const vm_bf16* x, int64_t x_st, const vm_
   REQUIRE(result || B == 0, VM_E_ARG, "lm_head_argmax: Result is NULL");
   TRY(check_aligned(x, "X"));
   TRY(check_aligned(w, "W"));
-  REQUIRE(K > 0 && K % 8 == 0, VM_E_UNSUPPORTED, "lm_head_argmax: K = %d (a multiple of 8)", K);
+  REQUIRE(K > 0 && K % 64 == 0, VM_E_UNSUPPORTED, "lm_head_argmax: K = %d (a multiple of 64)",
+          K);
   REQUIRE(N > 0 && B >= 0, VM_E_ARG, "lm_head_argmax: N = %d, B = %d", N, B);
   TRY(check_stride(x_st, "x_st"));
   TRY(check_stride(w_st, "w_st"));
