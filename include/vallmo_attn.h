@@ -256,7 +256,10 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb,
  * (src/llm/qwen35.jl:194, :206, :296, :316-317). Column-major, as the
  * reference: x :: (K, N) with column stride ldx >= K, W :: (K, M) (K-major,
  * the checkpoint's orientation) with column stride ldw >= K, y :: (M, N) with
- * column stride ldy >= M; all bf16, fp32 accumulation (linear.jl:29). A plan per
+ * column stride ldy >= M; all bf16, fp32 accumulation (linear.jl:29). Narrow
+ * problems (N <= 16, K % 64 == 0, M % 4 == 0, 16-byte aligned W and x columns)
+ * run on the library's split-K MFMA GEMV, whose K slices add in a fixed order
+ * (bitwise reproducible); the rest on hipBLASLt. A plan per
  * problem (hipBLASLt) is built on the first call and cached (linear.jl:17-38);
  * vm_linear_workspace_bytes builds it and returns the workspace it needs (at
  * most 64 MiB), which the caller passes to vm_linear (the reference takes it

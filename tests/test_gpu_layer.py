@@ -36,6 +36,67 @@ def test_linear_operator(vm, orc, M, N, K):
     assert mx <= TOL_MAX and mn <= TOL_MEAN
 
 
+NARROW = [(S * D, 1, DM), (S * D, 16, DM), (DM, 16, HQ * D), (DM, 1, HQ * D),
+          (2 * 9216, 16, DM), (DM, 16, 9216), (100, 7, 64), (4, 1, 64), (36, 16, 640),
+          (2 * 9216, 3, DM)]
+
+
+def _narrow_bar(x, W, ref):
+    """Per-element bar of a narrow product with fp32 accumulation: the bf16
+    rounding of the output (half an ulp, 2^-9 |y|, taken as one ulp) plus fp32
+    reassociation, bounded by 2^-20 sum_k |x_k w_k|."""
+    xa = np.abs(bf16_to_f32(x).astype(np.float64))
+    wa = np.abs(bf16_to_f32(W).astype(np.float64))
+    return 2.0 ** -8 * np.abs(ref) + 2.0 ** -20 * (xa.reshape(-1, xa.shape[-1]) @ wa.T).reshape(
+        ref.shape)
+
+
+@pytest.mark.parametrize("M,N,K", NARROW)
+def test_linear_narrow(vm, orc, M, N, K):
+    """The decode projections (N <= 16 columns) run on the library's split-K
+    MFMA kernel: every element within one bf16 ulp (plus fp32 reassociation)
+    of the fp32 oracle, the result bitwise the same on a second call (the
+    slices add in a fixed order), and strided x / y columns honoured."""
+    banner(f"linear narrow M={M} N={N} K={K}")
+    x = normal_bf16((N, K), 710 + N + K)
+    W = normal_bf16((M, K), 810 + M, scale=K ** -0.5)
+    xd, Wd = to_dev(x), to_dev(W)
+    print(f"workspace {vm.linear_workspace_bytes(xd, Wd)} B")
+    y1 = vm.linear(xd, Wd)["y"]
+    y2 = vm.linear(xd, Wd)["y"]
+    # x and y as columns of wider buffers (column strides K + 64, M + 8)
+    xw = torch.zeros((N, K + 64), dtype=torch.bfloat16, device="cuda")
+    xw[:, :K] = xd
+    yw = torch.full((N, M + 8), 7.0, dtype=torch.bfloat16, device="cuda")
+    vm.linear_({"y": yw[:, :M]}, xw[:, :K], Wd)
+    torch.cuda.synchronize()
+    ref = orc.linear(x, W).astype(np.float64)
+    bar = _narrow_bar(x, W, ref)
+    got = dev_f32(y1).astype(np.float64)
+    worst = float(np.max(np.abs(got - ref) / bar))
+    print(f"linear narrow {M}x{N}x{K}: worst |err|/bar {worst:.3f}")
+    assert worst <= 1.0
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    assert torch.equal(yw[:, :M].view(torch.int16), y1.view(torch.int16))
+    assert bool((yw[:, M:] == 7.0).all())
+
+
+def test_linear_narrow_misaligned_view(vm, orc):
+    """A view off the kernel's 16-byte alignment takes the GEMM library's
+    path for the same problem: same results to the parity bar."""
+    banner("linear narrow misaligned view")
+    M, N, K = 256, 4, 512
+    x = normal_bf16((N, K + 8), 733)
+    W = normal_bf16((M, K), 834, scale=K ** -0.5)
+    xd = to_dev(x)[:, 4:K + 4]  # 8-byte offset, column stride K + 8
+    y = vm.linear(xd, to_dev(W))["y"]
+    torch.cuda.synchronize()
+    ref = orc.linear(np.ascontiguousarray(x[:, 4:K + 4]), W).astype(np.float64)
+    mx, mn = maxmean(dev_f32(y), ref)
+    print(f"linear misaligned: max {mx:.3e} mean {mn:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN
+
+
 def _layer(vm, cfg, seed):
     qw = normal_bf16((D,), seed + 1, scale=0.05)
     kw = normal_bf16((D,), seed + 2, scale=0.05)

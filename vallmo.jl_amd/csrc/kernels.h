@@ -203,6 +203,25 @@ struct LmHeadArgs {
   int32_t* pidx;
   int32_t* result;      // (B,) 1-based
 };
+// y = W^T x for N <= 32 columns (the decode projections): W (K, M) K-major, x
+// (K, N), y (M, N), column strides w_st, x_st, y_st. K a multiple of 64, M of 4.
+struct GemvArgs {
+  const uint16_t* w;
+  int64_t w_st;
+  const uint16_t* x;
+  int64_t x_st;
+  uint16_t* y;
+  int64_t y_st;
+  int M, N, K;
+  int T, S2, gps, G;    // set by the launcher (gemv_plan)
+  float* part;          // S2 > 1: fp32 partials [S2][32][M] (gemv_workspace_bytes)
+};
+struct GemvPlan {
+  int T, S2, gps, ntg;
+};
+GemvPlan gemv_plan(int M, int K, int waves);
+size_t gemv_workspace_bytes(int M, int K);
+hipError_t launch_gemv(GemvArgs a, hipStream_t st);
 hipError_t launch_rms_norm(const NormArgs& a, hipStream_t st);
 hipError_t launch_silu_mul(const SiluMulArgs& a, hipStream_t st);
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t st);

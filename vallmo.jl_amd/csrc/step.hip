@@ -200,13 +200,23 @@ __device__ __forceinline__ void lm_dma_tile(uint16_t* dst, const uint16_t* m, in
                                      16, 0, 2);
   }
 }
+// A product's operands: W (K x M rows... K-major, column m at w + m * w_st, m <
+// nw) and X (K x B, column b at x + b * x_st, b < nx).
+struct MmSrc {
+  const uint16_t* w;
+  int64_t w_st;
+  int nw;
+  const uint16_t* x;
+  int64_t x_st;
+  int nx;
+};
 // a group: the T weight tiles at v0, then the batch tile at b0 (slot T)
 template <int T>
-__device__ __forceinline__ void lm_dma(uint16_t* buf, const LmHeadArgs& a, int v0, int b0, int k0,
+__device__ __forceinline__ void lm_dma(uint16_t* buf, const MmSrc& m, int v0, int b0, int k0,
                                        int lane) {
 #pragma unroll
-  for (int t = 0; t < T; ++t) lm_dma_tile(buf + t * LM_TB, a.w, a.w_st, v0 + 32 * t, a.N, k0, lane);
-  lm_dma_tile(buf + T * LM_TB, a.x, a.x_st, b0, a.B, k0, lane);
+  for (int t = 0; t < T; ++t) lm_dma_tile(buf + t * LM_TB, m.w, m.w_st, v0 + 32 * t, m.nw, k0, lane);
+  lm_dma_tile(buf + T * LM_TB, m.x, m.x_st, b0, m.nx, k0, lane);
 }
 
 // The products of one staged group: step s of tile t reads lane (j, h)'s A
@@ -261,38 +271,38 @@ __device__ __forceinline__ void lm_mult(const uint16_t* buf, int j, int h, f32x1
 __shared__ __attribute__((aligned(16))) uint16_t lm_buf0[4][5 * LM_TB];
 __shared__ __attribute__((aligned(16))) uint16_t lm_buf1[4][5 * LM_TB];
 
-// One pass: T tiles (vocab columns v0 .. v0 + 32T - 1) over all of K (a multiple
-// of 64) in groups of 64, double buffered; then the running (max, index) of this
-// lane's batch column, in vocab order.
+// acc[t] = W^T X over k = k0 .. k1 - 1 (multiples of 64) for the T 32-row tiles
+// at v0 and the 32-column batch tile at b0, in groups of 64 k, double buffered.
+// Lane (j, h) ends with batch column b0 + j at rows 8 (r / 4) + 4 h + r % 4 of
+// each tile.
 template <int T>
-__device__ __forceinline__ void lm_pass(const LmHeadArgs& a, int v0, int vend, int bt0, int lane,
-                                        float& best, int& besti) {
+__device__ __forceinline__ void mm_tiles(const MmSrc& m, int v0, int bt0, int k0, int k1, int lane,
+                                         f32x16 (&acc)[T]) {
   const int j = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
   uint16_t* b0 = lm_buf0[wv];
   uint16_t* b1 = lm_buf1[wv];
-  f32x16 acc[T];
 #pragma unroll
   for (int t = 0; t < T; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
   constexpr int PER = 4 * (T + 1);  // loads per group
-  const int G = a.K / 64;            // groups, >= 1
-  lm_dma<T>(b0, a, v0, bt0, 0, lane);
+  const int G = (k1 - k0) / 64;      // groups, >= 1
+  lm_dma<T>(b0, m, v0, bt0, k0, lane);
   int g = 0;
   // steady state, no branch in the body: groups g (in b0) and g + 1 (into b1),
   // then g + 2 into b0 again
   for (; g + 2 < G; g += 2) {
-    lm_dma<T>(b1, a, v0, bt0, 64 * (g + 1), lane);
+    lm_dma<T>(b1, m, v0, bt0, k0 + 64 * (g + 1), lane);
     wait_vmcnt<PER>();
     lm_mult<T>(b0, j, h, acc);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // b0's reads are in: refill it
-    lm_dma<T>(b0, a, v0, bt0, 64 * (g + 2), lane);
+    lm_dma<T>(b0, m, v0, bt0, k0 + 64 * (g + 2), lane);
     wait_vmcnt<PER>();
     lm_mult<T>(b1, j, h, acc);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
   if (g + 1 < G) {  // the last two groups
-    lm_dma<T>(b1, a, v0, bt0, 64 * (g + 1), lane);
+    lm_dma<T>(b1, m, v0, bt0, k0 + 64 * (g + 1), lane);
     wait_vmcnt<PER>();
     lm_mult<T>(b0, j, h, acc);
     wait_vmcnt<0>();
@@ -301,7 +311,18 @@ __device__ __forceinline__ void lm_pass(const LmHeadArgs& a, int v0, int vend, i
     wait_vmcnt<0>();
     lm_mult<T>(b0, j, h, acc);
   }
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the next pass refills both
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the next call refills both
+}
+
+// One lm-head pass: T tiles (vocab columns v0 .. v0 + 32T - 1) over all of K,
+// then the running (max, index) of this lane's batch column, in vocab order.
+template <int T>
+__device__ __forceinline__ void lm_pass(const LmHeadArgs& a, int v0, int vend, int bt0, int lane,
+                                        float& best, int& besti) {
+  const int h = lane >> 5;
+  const MmSrc m{a.w, a.w_st, a.N, a.x, a.x_st, a.B};
+  f32x16 acc[T];
+  mm_tiles<T>(m, v0, bt0, 0, a.K, lane, acc);
   // lane (j, h): rows 8 (r / 4) + 4 h + r % 4 of each tile, increasing in r
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -357,6 +378,147 @@ void lm_head_split_kernel(LmHeadArgs a) {
     a.pmax[(int64_t)w * a.B + b0 + j] = best;
     a.pidx[(int64_t)w * a.B + b0 + j] = besti;
   }
+}
+
+// ---- y = W^T x for a narrow x (N <= 32 columns; the library routes N <= 16
+// here): the decode step's projections (linear!, src/linear.jl:40-57, at N = B). HBM-bound like the lm
+// head and built the same way: one 32-column batch tile, 32-row weight tiles
+// staged through LDS by 1-KB direct loads, bf16 MFMAs, fp32 sums. Workgroup
+// (tile group tg, K slice s2) takes T tiles; its four waves split the slice's
+// 64-deep k groups in four contiguous runs and add their sums through LDS (the
+// staging buffers, free by then). With S2 > 1 slices the workgroups write fp32
+// partials, summed in slice order by gemv_reduce_kernel (deterministic).
+namespace {
+
+template <int T>
+__device__ __forceinline__ void gemv_wg(const GemvArgs& a, int tg, int s2, int lane) {
+  const int wv = threadIdx.x >> 6, j = lane & 31, h = lane >> 5;
+  const int v0 = 32 * T * tg;
+  // this workgroup's k groups, then this wave's run of them
+  const int gw0 = s2 * a.gps, gw1 = min(gw0 + a.gps, a.G);
+  const int per = (gw1 - gw0 + 3) / 4;
+  const int g0 = min(gw0 + wv * per, gw1), g1 = min(g0 + per, gw1);
+  const MmSrc m{a.w, a.w_st, a.M, a.x, a.x_st, a.N};
+  f32x16 acc[T];
+  if (g1 > g0) {
+    mm_tiles<T>(m, v0, 0, 64 * g0, 64 * g1, lane, acc);
+  } else {
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+  }
+  // the four waves' sums through LDS: wave w's tile t, register r, lane l at
+  // [w][t][r][l] (floats); then wave t adds tile t of all four
+  float* red = reinterpret_cast<float*>(lm_buf0[0]);
+  __syncthreads();  // every wave is done with the staging buffers
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[((wv * 4 + t) * 16 + r) * 64 + lane] = acc[t][r];
+  __syncthreads();
+  if (wv >= T || j >= a.N) return;
+  const int t = wv;
+  float o[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float v = red[((0 * 4 + t) * 16 + r) * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) v += red[((w * 4 + t) * 16 + r) * 64 + lane];
+    o[r] = v;
+  }
+  // lane (j, h): rows 8q + 4h .. +3 of the tile, q = 0..3, for batch column j
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int row = v0 + 32 * t + 8 * q + 4 * h;
+    if (row >= a.M) continue;
+    if (a.S2 == 1) {
+      const uint2 v = make_uint2(pack2(o[4 * q], o[4 * q + 1]), pack2(o[4 * q + 2], o[4 * q + 3]));
+      *reinterpret_cast<uint2*>(a.y + (int64_t)j * a.y_st + row) = v;
+    } else {
+      *reinterpret_cast<float4*>(a.part + ((int64_t)s2 * 32 + j) * a.M + row) =
+          make_float4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+    }
+  }
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemv_kernel(GemvArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int tg = blockIdx.x / a.S2, s2 = blockIdx.x % a.S2;
+  switch (a.T) {
+    case 4: gemv_wg<4>(a, tg, s2, lane); break;
+    case 2: gemv_wg<2>(a, tg, s2, lane); break;
+    default: gemv_wg<1>(a, tg, s2, lane); break;
+  }
+}
+
+// y[:, b] rows 4i .. 4i + 3 = the slices' partials added in slice order
+__global__ __launch_bounds__(256) void gemv_reduce_kernel(GemvArgs a) {
+  const int q4 = a.M / 4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)q4 * a.N) return;
+  const int b = (int)(idx / q4), row = 4 * (int)(idx % q4);
+  float4 s = *reinterpret_cast<const float4*>(a.part + (int64_t)b * a.M + row);
+  for (int k = 1; k < a.S2; ++k) {
+    const float4 v = *reinterpret_cast<const float4*>(a.part + ((int64_t)k * 32 + b) * a.M + row);
+    s.x += v.x;
+    s.y += v.y;
+    s.z += v.z;
+    s.w += v.w;
+  }
+  *reinterpret_cast<uint2*>(a.y + (int64_t)b * a.y_st + row) =
+      make_uint2(pack2(s.x, s.y), pack2(s.z, s.w));
+}
+
+// The split: T tiles per workgroup and S2 K slices, from a cost model of
+// one workgroup per CU (the staging buffers take the CU's LDS): the launch runs
+// in ceil(workgroups / CUs) rounds, a round lasts as long as its waves take to
+// stream their groups ((T + 1) tiles of 4 KB each, plus about two groups of
+// pipeline fill), and S2 > 1 adds the partials' write and read spread over all
+// waves. The smallest cost wins (ties: fewer slices, then wider tile groups).
+GemvPlan gemv_plan(int M, int K, int waves) {
+  const int tiles = (M + 31) / 32, G = K / 64;
+  const int cus = max(1, waves / 4);
+  GemvPlan best{1, 1, G, tiles};
+  double best_cost = 1e300;
+  for (int T : {4, 2, 1}) {
+    const int ntg = (tiles + T - 1) / T;
+    for (int S2 = 1; S2 <= G; ++S2) {
+      const int gps = (G + S2 - 1) / S2;
+      if ((G + gps - 1) / gps != S2) continue;  // every slice non-empty
+      const int rounds = (ntg * S2 + cus - 1) / cus;
+      const int per = (gps + 3) / 4;
+      double cost = (double)rounds * (per + 2) * (T + 1) * 4096.0;
+      if (S2 > 1) cost += 2.0 * S2 * 32.0 * M * 4.0 / (4.0 * cus);
+      if (cost < best_cost * (1 - 1e-9)) {
+        best_cost = cost;
+        best = GemvPlan{T, S2, gps, ntg};
+      }
+    }
+  }
+  return best;
+}
+
+size_t gemv_workspace_bytes(int M, int K) {
+  const GemvPlan p = gemv_plan(M, K, lm_head_waves());
+  return p.S2 > 1 ? (size_t)p.S2 * 32 * (size_t)M * sizeof(float) : 0;
+}
+
+hipError_t launch_gemv(GemvArgs a, hipStream_t st) {
+  const GemvPlan p = gemv_plan(a.M, a.K, lm_head_waves());
+  a.T = p.T;
+  a.S2 = p.S2;
+  a.gps = p.gps;
+  a.G = a.K / 64;
+  hipLaunchKernelGGL(gemv_kernel, dim3(p.ntg * p.S2), dim3(256), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.S2 == 1) return e;
+  const int64_t n = (int64_t)(a.M / 4) * a.N;
+  hipLaunchKernelGGL(gemv_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
+  return hipGetLastError();
 }
 
 // One workgroup per batch column: the best of the NW partials (ties to the
