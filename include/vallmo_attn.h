@@ -59,7 +59,9 @@ enum {
   VM_K_PREFILL = 3,       /* flash attention (prefill)                       */
   VM_K_ADVANCE = 4,       /* device clock                                    */
   VM_K_LM_HEAD = 5,       /* lm-head GEMV + argmax (split and combine)       */
-  VM_K_COUNT = 6
+  VM_K_DELTANET = 6,      /* delta-rule recurrence (decode step, sequence)   */
+  VM_K_CONV = 7,          /* causal conv1d (decode step, sequence)           */
+  VM_K_COUNT = 8
 };
 int vm_profile_enable(int on);
 int vm_profile_read(int kernel, int* count, double* total_ms);
@@ -314,6 +316,94 @@ size_t vm_lm_head_argmax_scratch_bytes(int K, int N, int B);
 int vm_lm_head_argmax(int32_t* result, const vm_bf16* x, int64_t x_st, const vm_bf16* w,
                       int64_t w_st, int K, int N, int B, void* scratch, size_t scratch_bytes,
                       vm_stream stream);
+
+/* ---- f4: the linear-attention layer parts (3 of every 4 Qwen3.5 layers,
+ * src/llm/gguf_llamacpp.jl:47) -------------------------------------------
+ * Column-major as the reference; element strides. All kernels run Dk = Dv =
+ * 128 (Qwen3.5, src/llm/qwen35.jl:19); other head sizes are VM_E_UNSUPPORTED.
+ * Hv % Hk != 0 is VM_E_DIM (deltanet_fused.jl:128-129). States may be updated
+ * in place (S_out == S, the reference's output_override at qwen35.jl:223,
+ * :229, :358) or written to a disjoint buffer; a partial overlap is VM_E_ARG. */
+
+/* causal_conv1d!((; Y, S'), X, S, Weight, Bias; sigma) — one decode step
+ * (src/kernels/causal_conv1d.jl:43-61, kernel :7-41): the ring S (D, K, B)
+ * (column stride s_cs, sequence stride s_sb) shifts one column left, X (D, B)
+ * enters as column K, Y (D, B) = sum_i S'[:, i] .* Weight[:, i] (+ Bias)
+ * (silu when act != 0, the call site's sigma = silu, qwen35.jl:222-223).
+ * Weight (D, K) column stride w_cs; Bias (D,) or NULL. bf16; D % 8 == 0,
+ * 16-byte aligned rows, 1 <= K <= 8. */
+int vm_causal_conv1d(vm_bf16* y, int64_t y_sb, const vm_bf16* x, int64_t x_sb,
+                     const vm_bf16* s_in, vm_bf16* s_out, int64_t s_cs, int64_t s_sb,
+                     const vm_bf16* w, int64_t w_cs, const vm_bf16* bias, int D, int K, int B,
+                     int act, vm_stream stream);
+
+/* causal_conv1d_sequence!((; Y), X, Weight, Bias; sigma, S') (causal_conv1d.jl:
+ * 130-149, kernel :73-128): X, Y (D, T, B) with token / sequence strides;
+ * Y[:, t] = sum_k Weight[:, k] X[:, t - K + k] with the left context zeros
+ * (s_in NULL) or the ring's columns 2..K (s_in: a prefix's ring, the suffix
+ * prefill of qwen35.jl:333-344, done here without the copy). s_out (NULL:
+ * none) receives the ring a decode step continues from: the last K inputs of
+ * the context-extended sequence, zeros where it is shorter. */
+int vm_causal_conv1d_sequence(vm_bf16* y, int64_t y_st, int64_t y_sb, const vm_bf16* x,
+                              int64_t x_st, int64_t x_sb, const vm_bf16* w, int64_t w_cs,
+                              const vm_bf16* bias, const vm_bf16* s_in, vm_bf16* s_out,
+                              int64_t s_cs, int64_t s_sb, int D, int K, int T, int B, int act,
+                              vm_stream stream);
+
+/* fused_deltanet_decode!((; O, S'), Q_raw, K_raw, V, Alpha, BetaRaw, Z, A_log,
+ * DtBias, NormWeight, S; eps) (src/kernels/deltanet_fused.jl:109-141, kernel
+ * :27-107): l2-normed q (also / sqrt(Dk)) and k of the shared qk head
+ * h_v / (Hv / Hk), decay = exp(-exp(A_log) softplus(Alpha + DtBias)), beta =
+ * sigmoid(BetaRaw), the delta-rule step on S (Dk, Dv, Hv, B) fp32, then
+ * O = o rstd NormWeight silu(Z). Q_raw, K_raw (Dk, Hk, B), V, Z, O (Dv, Hv, B),
+ * Alpha, BetaRaw (Hv, B): bf16, heads contiguous, per-sequence strides *_sb
+ * (Q_raw, K_raw 8-byte aligned); A_log, DtBias (Hv,) fp32; NormWeight (Dv,)
+ * bf16; S, S_out 16-byte aligned. */
+int vm_fused_deltanet_decode(vm_bf16* o, int64_t o_sb, const vm_bf16* q, int64_t q_sb,
+                             const vm_bf16* k, int64_t k_sb, const vm_bf16* v, int64_t v_sb,
+                             const vm_bf16* alpha, int64_t a_sb, const vm_bf16* beta_raw,
+                             int64_t b_sb, const vm_bf16* z, int64_t z_sb, const float* a_log,
+                             const float* dt_bias, const vm_bf16* norm_w, const float* s_in,
+                             float* s_out, int Dk, int Dv, int Hk, int Hv, int B, float eps,
+                             vm_stream stream);
+
+/* deltanet_recurrent_decode!((; O, S'), Q, K, V, Beta, Gate, S)
+ * (src/kernels/deltanet_recurrent.jl:72-95, kernel :15-70), fp32 throughout:
+ * Q, K (Dk, Hk, B), V, O (Dv, Hv, B), Beta, Gate (Hv, B) (decay = exp(Gate)),
+ * S (Dk, Dv, Hv, B); contiguous, 16-byte aligned. */
+int vm_deltanet_recurrent_decode(float* o, const float* q, const float* k, const float* v,
+                                 const float* beta, const float* gate, const float* s_in,
+                                 float* s_out, int Dk, int Dv, int Hk, int Hv, int B,
+                                 vm_stream stream);
+
+/* deltanet_sequence!((; O, S'), Q, K, V, Beta, Gate, S) (deltanet_recurrent.jl:
+ * 174-198, kernel :109-172): T steps in order, fp32. Q, K (Dk, T, Hk, B),
+ * V, O (Dv, T, Hv, B), Beta, Gate (Hv, T, B), S (Dk, Dv, Hv, B). T = 0 copies
+ * the state through. */
+int vm_deltanet_sequence(float* o, const float* q, const float* k, const float* v,
+                         const float* beta, const float* gate, const float* s_in, float* s_out,
+                         int Dk, int Dv, int T, int Hk, int Hv, int B, vm_stream stream);
+
+/* The prefill's inputs to deltanet_sequence! (forward(::DeltaNetLayer),
+ * src/llm/qwen35.jl:347-356): from the conv output cv (the q | k | v channels,
+ * n = 2 Hk Dk + Hv Dv rows per token, token stride cv_st, sequence stride
+ * cv_sb) and the alpha | beta projection ab (2 Hv rows, ab_st, ab_sb), bf16:
+ * qe, ke (Dk, T, Hk, B) = l2n(q) / sqrt(Dk), l2n(k); ve (Dv, T, Hv, B);
+ * beta = sigmoid(b), gate = -exp(A_log) softplus(a + DtBias) (Hv, T, B). fp32
+ * outputs, contiguous. */
+int vm_deltanet_prefill_prep(float* qe, float* ke, float* ve, float* beta, float* gate,
+                             const vm_bf16* cv, int64_t cv_st, int64_t cv_sb, const vm_bf16* ab,
+                             int64_t ab_st, int64_t ab_sb, const float* a_log,
+                             const float* dt_bias, int Dk, int Dv, int Hk, int Hv, int T, int B,
+                             vm_stream stream);
+
+/* The prefill's gated RMSNorm + z gate (qwen35.jl:360-364): o (Dv, T, Hv, B)
+ * fp32 and z (Dv, Hv) rows of each token (token stride z_st, sequence stride
+ * z_sb, bf16) -> y = o rstd NormWeight silu(z), bf16, (Dv, Hv) rows at y_st /
+ * y_sb: the out projection's input (Dv Hv, T B) (qwen35.jl:365). */
+int vm_gated_rms_norm(vm_bf16* y, int64_t y_st, int64_t y_sb, const float* o, const vm_bf16* z,
+                      int64_t z_st, int64_t z_sb, const vm_bf16* norm_w, int Dv, int Hv, int T,
+                      int B, float eps, vm_stream stream);
 
 /* ---- synthetic inputs for tests and benchmarks (not a reference op) ----
  * Fills n bf16 values with the seeded N(0,1) stream used by the CPU oracle

@@ -1,8 +1,10 @@
-"""CPU fp32 oracle for the gated full-attention path — TEST INFRASTRUCTURE.
+"""CPU fp32 oracle for the gated full-attention path and the linear-attention
+(DeltaNet + conv1d) layer parts — TEST INFRASTRUCTURE.
 
 Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
 may import this package, and only as the checker (never as the measured or
-shipped path). ``liboracle.so`` is built from ``oracle.c`` by ``oracle/Makefile``.
+shipped path). ``liboracle.so`` is built from ``oracle.c`` and ``deltanet.c`` by
+``oracle/Makefile``.
 
 Parity pinning (the reference ships no golden vectors or known-answer tests for
 this path; its tests cover checkpoint loaders only, test/runtests.jl:48-207):
@@ -68,6 +70,22 @@ def lib():
         L.orc_lm_head_argmax.argtypes = [_u16p, _u16p, i32, i32, i32, _i32p, _f32p, i32]
         L.orc_lm_head_argmax.restype = None
         L.orc_max_threads.restype = i32
+        vp = ctypes.c_void_p
+        L.orc_conv1d_update.argtypes = [_u16p, _u16p, _u16p, _u16p, vp, _f32p, i32, i32, i32, i32]
+        L.orc_conv1d_update.restype = None
+        L.orc_conv1d_sequence.argtypes = [_u16p, _u16p, vp, vp, vp, _f32p, i32, i32, i32, i32, i32]
+        L.orc_conv1d_sequence.restype = None
+        L.orc_deltanet_decode.argtypes = [_f32p] * 8 + [i32] * 5
+        L.orc_deltanet_decode.restype = None
+        L.orc_deltanet_sequence.argtypes = [_f32p] * 8 + [i32] * 6
+        L.orc_deltanet_sequence.restype = None
+        L.orc_fused_deltanet_decode.argtypes = [_u16p] * 6 + [_f32p, _f32p, _u16p, _f32p, _f32p,
+                                                              _f32p] + [i32] * 5 + [f32]
+        L.orc_fused_deltanet_decode.restype = None
+        L.orc_deltanet_prep.argtypes = [_u16p, _u16p, _f32p, _f32p] + [_f32p] * 5 + [i32] * 6
+        L.orc_deltanet_prep.restype = None
+        L.orc_gated_rms_norm.argtypes = [_f32p, _u16p, i64, _u16p, _f32p, i32, i32, i32, i32, f32]
+        L.orc_gated_rms_norm.restype = None
         _LIB = L
     return _LIB
 
@@ -279,6 +297,110 @@ def model_step(E, layers, norm_w, head, result, positions, cos_tab, sin_tab, *, 
         x, xn = f32_to_bf16(xo), f32_to_bf16(y)
     res, gap = lm_head_argmax(xn, head, nthreads=nthreads)
     return res, gap, bf16_to_f32(xn)
+
+
+# ---- linear-attention layer parts (oracle/deltanet.c) -----------------------
+
+def _vp(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def conv1d_update(x, s, w, bias=None, *, act=True):
+    """causal_conv1d! (src/kernels/causal_conv1d.jl:7-61), one step: x [B][D],
+    ring s [B][K][D], w [K][D], bias [D] or None (bf16 bits). Returns (y [B][D]
+    fp32, the shifted ring [B][K][D] bf16 bits)."""
+    x, s, w = _c(x, np.uint16), _c(s, np.uint16), _c(w, np.uint16)
+    bias = None if bias is None else _c(bias, np.uint16)
+    B, K, D = s.shape
+    y = np.empty((B, D), np.float32)
+    so = np.empty_like(s)
+    lib().orc_conv1d_update(x, s, so, w, _vp(bias), y, D, K, B, int(bool(act)))
+    return y, so
+
+
+def conv1d_sequence(x, w, bias=None, *, s_in=None, act=True):
+    """causal_conv1d_sequence! (causal_conv1d.jl:73-149): x [B][T][D] -> (y
+    [B][T][D] fp32, the seeded ring [B][K][D]); s_in (a prefix's ring) supplies
+    the left context of a suffix (qwen35.jl:333-344), zeros when None."""
+    x, w = _c(x, np.uint16), _c(w, np.uint16)
+    bias = None if bias is None else _c(bias, np.uint16)
+    s_in = None if s_in is None else _c(s_in, np.uint16)
+    B, T, D = x.shape
+    K = w.shape[0]
+    y = np.empty((B, T, D), np.float32)
+    so = np.empty((B, K, D), np.uint16)
+    lib().orc_conv1d_sequence(x, w, _vp(bias), _vp(s_in), _vp(so), y, D, K, T, B,
+                              int(bool(act)))
+    return y, so
+
+
+def deltanet_decode(q, k, v, beta, gate, s):
+    """deltanet_recurrent_decode! (src/kernels/deltanet_recurrent.jl:15-95), fp32:
+    q, k [B][Hk][Dk], v [B][Hv][Dv], beta, gate [B][Hv], s [B][Hv][Dv][Dk].
+    Returns (o [B][Hv][Dv], new state)."""
+    q, k, v, beta, gate, s = (_c(a, np.float32) for a in (q, k, v, beta, gate, s))
+    B, Hk, Dk = q.shape
+    Hv, Dv = v.shape[1], v.shape[2]
+    o = np.empty((B, Hv, Dv), np.float32)
+    so = np.empty_like(s)
+    lib().orc_deltanet_decode(q, k, v, beta, gate, s, so, o, Dk, Dv, Hk, Hv, B)
+    return o, so
+
+
+def deltanet_sequence(q, k, v, beta, gate, s):
+    """deltanet_sequence! (deltanet_recurrent.jl:109-198), fp32: q, k
+    [B][Hk][T][Dk], v [B][Hv][T][Dv], beta, gate [B][T][Hv], s [B][Hv][Dv][Dk].
+    Returns (o [B][Hv][T][Dv], final state)."""
+    q, k, v, beta, gate, s = (_c(a, np.float32) for a in (q, k, v, beta, gate, s))
+    B, Hk, T, Dk = q.shape
+    Hv, Dv = v.shape[1], v.shape[3]
+    o = np.empty((B, Hv, T, Dv), np.float32)
+    so = np.empty_like(s)
+    lib().orc_deltanet_sequence(q, k, v, beta, gate, s, so, o, Dk, Dv, T, Hk, Hv, B)
+    return o, so
+
+
+def fused_deltanet_decode(q, k, v, alpha, beta_raw, z, a_log, dt_bias, norm_w, s, *, eps):
+    """fused_deltanet_decode! (src/kernels/deltanet_fused.jl:27-141): q, k
+    [B][Hk][Dk], v, z [B][Hv][Dv], alpha, beta_raw [B][Hv], norm_w [Dv] bf16
+    bits; a_log, dt_bias [Hv], s [B][Hv][Dv][Dk] fp32. Returns (o [B][Hv][Dv]
+    fp32, new state)."""
+    q, k, v, alpha, beta_raw, z, norm_w = (_c(a, np.uint16)
+                                           for a in (q, k, v, alpha, beta_raw, z, norm_w))
+    a_log, dt_bias, s = (_c(a, np.float32) for a in (a_log, dt_bias, s))
+    B, Hk, Dk = q.shape
+    Hv, Dv = v.shape[1], v.shape[2]
+    o = np.empty((B, Hv, Dv), np.float32)
+    so = np.empty_like(s)
+    lib().orc_fused_deltanet_decode(q, k, v, alpha, beta_raw, z, a_log, dt_bias, norm_w, s, so,
+                                    o, Dk, Dv, Hk, Hv, B, float(eps))
+    return o, so
+
+
+def deltanet_prep(cv, ab, a_log, dt_bias, *, Dk, Dv, Hk, Hv):
+    """The prefill's inputs to deltanet_sequence! (src/llm/qwen35.jl:347-356):
+    cv [B][T][2 Hk Dk + Hv Dv], ab [B][T][2 Hv] bf16 bits. Returns dict q, k
+    [B][Hk][T][Dk], v [B][Hv][T][Dv], beta, gate [B][T][Hv] (fp32)."""
+    cv, ab = _c(cv, np.uint16), _c(ab, np.uint16)
+    a_log, dt_bias = _c(a_log, np.float32), _c(dt_bias, np.float32)
+    B, T, _ = cv.shape
+    out = dict(q=np.empty((B, Hk, T, Dk), np.float32), k=np.empty((B, Hk, T, Dk), np.float32),
+               v=np.empty((B, Hv, T, Dv), np.float32), beta=np.empty((B, T, Hv), np.float32),
+               gate=np.empty((B, T, Hv), np.float32))
+    lib().orc_deltanet_prep(cv, ab, a_log, dt_bias, out["q"], out["k"], out["v"], out["beta"],
+                            out["gate"], Dk, Dv, Hk, Hv, T, B)
+    return out
+
+
+def gated_rms_norm(o, z, norm_w, *, eps):
+    """The prefill epilogue (qwen35.jl:360-364): o [B][Hv][T][Dv] fp32, z
+    [B][T][Hv Dv] bf16 bits -> y [B][T][Hv][Dv] fp32 = o rstd norm_w silu(z)."""
+    o = _c(o, np.float32)
+    z, norm_w = _c(z, np.uint16), _c(norm_w, np.uint16)
+    B, Hv, T, Dv = o.shape
+    y = np.empty((B, T, Hv, Dv), np.float32)
+    lib().orc_gated_rms_norm(o, z, z.shape[-1], norm_w, y, Dv, Hv, T, B, float(eps))
+    return y
 
 
 def threads_env() -> int:

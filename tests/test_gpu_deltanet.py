@@ -1,0 +1,254 @@
+"""The linear-attention layer parts on the GPU vs the CPU oracle (oracle/deltanet.c):
+causal_conv1d! and causal_conv1d_sequence! (src/kernels/causal_conv1d.jl),
+fused_deltanet_decode! (deltanet_fused.jl), deltanet_recurrent_decode! and
+deltanet_sequence! (deltanet_recurrent.jl), and the prefill's prep and gated
+RMSNorm (src/llm/qwen35.jl:347-364), at the Qwen3.5 DeltaNet shape (Dk = Dv =
+128, Hk = 16, Hv = 32, conv kernel 4, 8192 conv channels) and at odd sizes.
+
+Bars: the conv ring (raw bf16 inputs) bit-exact; fp32 states and outputs
+within rtol 2e-5 of the oracle per step (5e-4 after 64 steps); bf16 outputs
+within one bf16 ulp of the fp32 oracle plus fp32 reassociation."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import banner, dev_f32, from_dev, to_dev
+from oracle.rng import bf16_to_f32, normal_bf16, normal_f32
+
+pytestmark = pytest.mark.gpu
+
+DK = DV = 128
+HK, HV, KC = 16, 32, 4
+NCH = 2 * HK * DK + HV * DV  # conv channels q | k | v
+EPS = 1e-6
+
+
+def f32dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+
+
+def bf16_bar(ref, extra=0.0):
+    """One bf16 ulp of the fp32 reference (2^-8 relative) plus an absolute floor."""
+    return 2.0 ** -8 * np.abs(ref) + 1e-6 + extra
+
+
+def assert_bf16_close(got, ref, what, extra=0.0):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    worst = float(np.max(np.abs(got - ref) / bf16_bar(ref, extra)))
+    print(f"{what}: worst |err| / bar = {worst:.3f}")
+    assert worst <= 1.0, what
+
+
+# ---------------------------------------------------------------- conv1d
+@pytest.mark.parametrize("B,bias,act", [(1, True, True), (3, False, True), (5, True, False)])
+def test_conv1d_update(vm, orc, B, bias, act):
+    """One decode step on the in-place ring; X a strided view (the q | k | v rows
+    of the projection, token stride NCH + HV * DV)."""
+    banner(f"conv1d update B={B} bias={bias} act={act}")
+    qz = normal_bf16((B, NCH + HV * DV), 900 + B)
+    ring = normal_bf16((B, KC, NCH), 901 + B)
+    w = normal_bf16((KC, NCH), 902, scale=0.5)
+    b = normal_bf16((NCH,), 903, scale=0.1) if bias else None
+    y_ref, ring_ref = orc.conv1d_update(qz[:, :NCH], ring, w, b, act=act)
+    X = to_dev(qz)[:, :NCH]
+    S = to_dev(ring)
+    out = vm.causal_conv1d(X, S, to_dev(w), None if b is None else to_dev(b),
+                           sigma="silu" if act else None, Sp=S)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_dev(S), ring_ref)
+    assert_bf16_close(dev_f32(out["Y"]), y_ref, "conv1d update")
+
+
+def test_conv1d_update_chain_equals_sequence(vm, orc):
+    """T decode steps from a zero ring == one sequence run (rows and ring)."""
+    banner("conv1d update chain == sequence")
+    B, T, D = 2, 9, 512
+    x = normal_bf16((B, T, D), 910)
+    w = normal_bf16((KC, D), 911, scale=0.5)
+    b = normal_bf16((D,), 912, scale=0.1)
+    X, W, Bi = to_dev(x), to_dev(w), to_dev(b)
+    seq = vm.causal_conv1d_sequence(X, W, Bi, sigma="silu",
+                                    Sp=torch.zeros((B, KC, D), dtype=torch.bfloat16,
+                                                   device="cuda"))
+    S = torch.zeros((B, KC, D), dtype=torch.bfloat16, device="cuda")
+    rows = []
+    for t in range(T):
+        rows.append(vm.causal_conv1d(X[:, t], S, W, Bi, sigma="silu", Sp=S)["Y"])
+    torch.cuda.synchronize()
+    y_ref, ring_ref = orc.conv1d_sequence(x, w, b, act=True)
+    assert_bf16_close(dev_f32(seq["Y"]), y_ref, "sequence")
+    assert_bf16_close(dev_f32(torch.stack(rows, 1)), y_ref, "update chain")
+    assert np.array_equal(from_dev(S), ring_ref)
+
+
+@pytest.mark.parametrize("B,T,prefix,bias", [(1, 37, False, True), (2, 16, False, False),
+                                             (2, 3, True, True), (3, 50, True, False),
+                                             (1, 1, True, True)])
+def test_conv1d_sequence(vm, orc, B, T, prefix, bias):
+    """The whole-sequence conv over a strided X, with the seeded ring; with a
+    prefix ring (the suffix prefill) read and overwritten in place."""
+    banner(f"conv1d sequence B={B} T={T} prefix={prefix} bias={bias}")
+    qz = normal_bf16((B, T, NCH + HV * DV), 920 + T)
+    x = np.ascontiguousarray(qz[..., :NCH])
+    w = normal_bf16((KC, NCH), 921, scale=0.5)
+    b = normal_bf16((NCH,), 922, scale=0.1) if bias else None
+    ring0 = normal_bf16((B, KC, NCH), 923) if prefix else None
+    y_ref, ring_ref = orc.conv1d_sequence(x, w, b, s_in=ring0, act=True)
+    X = to_dev(qz)[..., :NCH]
+    S = to_dev(ring0) if prefix else torch.empty((B, KC, NCH), dtype=torch.bfloat16,
+                                                  device="cuda")
+    out = vm.causal_conv1d_sequence(X, to_dev(w), None if b is None else to_dev(b),
+                                    sigma="silu", Sp=S, S=S if prefix else None)
+    torch.cuda.synchronize()
+    assert_bf16_close(dev_f32(out["Y"]), y_ref, "conv1d sequence")
+    assert np.array_equal(from_dev(S), ring_ref)
+
+
+# ---------------------------------------------------------------- delta rule
+def _fused_inputs(B, seed):
+    qz = normal_bf16((B, NCH + HV * DV), seed)  # conv output rows (q | k | v) + z
+    ab = normal_bf16((B, 2 * HV), seed + 1)
+    a_log = normal_f32(HV, seed + 2, scale=0.5)
+    dt_bias = normal_f32(HV, seed + 3, scale=0.5)
+    norm_w = normal_bf16((DV,), seed + 4, scale=0.2, shift=1.0)
+    s = normal_f32(B * HV * DV * DK, seed + 5, scale=0.05).reshape(B, HV, DV, DK)
+    return qz, ab, a_log, dt_bias, norm_w, s
+
+
+def _split(qz):
+    q = qz[..., :HK * DK]
+    k = qz[..., HK * DK:2 * HK * DK]
+    v = qz[..., 2 * HK * DK:NCH]
+    z = qz[..., NCH:]
+    return q, k, v, z
+
+
+@pytest.mark.parametrize("B,inplace", [(1, True), (4, False), (32, True), (33, True)])
+def test_fused_deltanet_decode(vm, orc, B, inplace):
+    """The layer's decode step: q, k, v, z, alpha, beta as strided views of the
+    projection outputs, the state updated in place or into a new buffer."""
+    banner(f"fused deltanet decode B={B} inplace={inplace}")
+    qz, ab, a_log, dt_bias, norm_w, s = _fused_inputs(B, 930 + B)
+    q, k, v, z = _split(qz)
+    o_ref, s_ref = orc.fused_deltanet_decode(
+        q.reshape(B, HK, DK), k.reshape(B, HK, DK), v.reshape(B, HV, DV), ab[:, :HV], ab[:, HV:],
+        z.reshape(B, HV, DV), a_log, dt_bias, norm_w, s, eps=EPS)
+    QZ, AB = to_dev(qz), to_dev(ab)
+    Qd, Kd, Vd, Zd = (t.unflatten(-1, (-1, DK)) for t in _split(QZ))
+    S = f32dev(s)
+    out = vm.fused_deltanet_decode(Qd, Kd, Vd, AB[:, :HV], AB[:, HV:], Zd, f32dev(a_log),
+                                   f32dev(dt_bias), to_dev(norm_w), S, eps=EPS,
+                                   Sp=S if inplace else None)
+    torch.cuda.synchronize()
+    s_got = (S if inplace else out["Sp"]).cpu().numpy()
+    np.testing.assert_allclose(s_got, s_ref, rtol=2e-5, atol=2e-6)
+    assert_bf16_close(dev_f32(out["O"]), o_ref, "fused decode O", extra=1e-5)
+
+
+def _prepped(B, T, seed):
+    cv = normal_bf16((B, T, NCH), seed)
+    ab = normal_bf16((B, T, 2 * HV), seed + 1)
+    a_log = normal_f32(HV, seed + 2, scale=0.5)
+    dt_bias = normal_f32(HV, seed + 3, scale=0.5)
+    return cv, ab, a_log, dt_bias
+
+
+@pytest.mark.parametrize("B,T", [(1, 64), (2, 17), (16, 4), (17, 3)])
+def test_deltanet_sequence(vm, orc, B, T):
+    """deltanet_sequence! on the prefill's prepped inputs: both launch shapes
+    (16 waves per head for B * Hv < 512, 4 above), in place."""
+    banner(f"deltanet sequence B={B} T={T}")
+    cv, ab, a_log, dt_bias = _prepped(B, T, 950 + B + T)
+    p = orc.deltanet_prep(cv, ab, a_log, dt_bias, Dk=DK, Dv=DV, Hk=HK, Hv=HV)
+    s = normal_f32(B * HV * DV * DK, 951, scale=0.05).reshape(B, HV, DV, DK)
+    o_ref, s_ref = orc.deltanet_sequence(p["q"], p["k"], p["v"], p["beta"], p["gate"], s)
+    S = f32dev(s)
+    out = vm.deltanet_sequence(f32dev(p["q"]), f32dev(p["k"]), f32dev(p["v"]), f32dev(p["beta"]),
+                               f32dev(p["gate"]), S, Sp=S)
+    torch.cuda.synchronize()
+    tol = 2e-5 if T <= 4 else 5e-4
+    np.testing.assert_allclose(S.cpu().numpy(), s_ref, rtol=tol, atol=tol * 0.1)
+    np.testing.assert_allclose(out["O"].cpu().numpy(), o_ref, rtol=tol, atol=tol * 0.1)
+
+
+def test_deltanet_recurrent_decode_chain(vm, orc):
+    """deltanet_recurrent_decode!: T single steps == the sequence run's rows."""
+    banner("deltanet recurrent decode chain")
+    B, T = 3, 5
+    cv, ab, a_log, dt_bias = _prepped(B, T, 960)
+    p = orc.deltanet_prep(cv, ab, a_log, dt_bias, Dk=DK, Dv=DV, Hk=HK, Hv=HV)
+    s = normal_f32(B * HV * DV * DK, 961, scale=0.05).reshape(B, HV, DV, DK)
+    o_ref, s_ref = orc.deltanet_sequence(p["q"], p["k"], p["v"], p["beta"], p["gate"], s)
+    S = f32dev(s)
+    for t in range(T):
+        o = vm.deltanet_recurrent_decode(
+            f32dev(p["q"][:, :, t]), f32dev(p["k"][:, :, t]), f32dev(p["v"][:, :, t]),
+            f32dev(p["beta"][:, t]), f32dev(p["gate"][:, t]), S, Sp=S)["O"]
+        np.testing.assert_allclose(o.cpu().numpy(), o_ref[:, :, t], rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(S.cpu().numpy(), s_ref, rtol=1e-4, atol=1e-5)
+
+
+def test_deltanet_sequence_zero_length_copies_state(vm):
+    banner("deltanet sequence T=0")
+    B = 2
+    s = normal_f32(B * HV * DV * DK, 970).reshape(B, HV, DV, DK)
+    e = torch.empty((B, HK, 0, DK), dtype=torch.float32, device="cuda")
+    ev = torch.empty((B, HV, 0, DV), dtype=torch.float32, device="cuda")
+    g = torch.empty((B, 0, HV), dtype=torch.float32, device="cuda")
+    out = vm.deltanet_sequence(e, e, ev, g, g, f32dev(s))
+    torch.cuda.synchronize()
+    assert np.array_equal(out["Sp"].cpu().numpy(), s)
+
+
+def test_prep_and_gated_norm(vm, orc):
+    """The prefill's prep from strided conv rows and its gated-norm epilogue
+    reading z from the projection."""
+    banner("deltanet prep + gated norm")
+    B, T = 2, 7
+    cv, ab, a_log, dt_bias = _prepped(B, T, 980)
+    p_ref = orc.deltanet_prep(cv, ab, a_log, dt_bias, Dk=DK, Dv=DV, Hk=HK, Hv=HV)
+    wide = np.zeros((B, T, NCH + 64), np.uint16)
+    wide[..., :NCH] = cv
+    CV = to_dev(wide)[..., :NCH]
+    outs = {"Q": torch.empty((B, HK, T, DK), dtype=torch.float32, device="cuda"),
+            "K": torch.empty((B, HK, T, DK), dtype=torch.float32, device="cuda"),
+            "V": torch.empty((B, HV, T, DV), dtype=torch.float32, device="cuda"),
+            "Beta": torch.empty((B, T, HV), dtype=torch.float32, device="cuda"),
+            "Gate": torch.empty((B, T, HV), dtype=torch.float32, device="cuda")}
+    vm.deltanet_prefill_prep_(outs, CV, to_dev(ab), f32dev(a_log), f32dev(dt_bias), Dk=DK,
+                              Dv=DV, Hk=HK, Hv=HV)
+    torch.cuda.synchronize()
+    for key, rk in (("Q", "q"), ("K", "k"), ("V", "v"), ("Beta", "beta"), ("Gate", "gate")):
+        np.testing.assert_allclose(outs[key].cpu().numpy(), p_ref[rk], rtol=2e-6, atol=1e-7,
+                                   err_msg=key)
+    o = normal_f32(B * HV * T * DV, 981).reshape(B, HV, T, DV)
+    qz = normal_bf16((B, T, NCH + HV * DV), 982)
+    norm_w = normal_bf16((DV,), 983, scale=0.2, shift=1.0)
+    y_ref = orc.gated_rms_norm(o, np.ascontiguousarray(qz[..., NCH:]), norm_w, eps=EPS)
+    Z = to_dev(qz)[..., NCH:].unflatten(-1, (HV, DV))
+    Y = torch.empty((B, T, HV, DV), dtype=torch.bfloat16, device="cuda")
+    vm.gated_rms_norm_(Y, f32dev(o), Z, to_dev(norm_w), eps=EPS)
+    torch.cuda.synchronize()
+    assert_bf16_close(dev_f32(Y), y_ref, "gated norm", extra=1e-6)
+
+
+def test_shape_errors(vm):
+    """The reference's DimensionMismatch on Hv % Hk, and head sizes the kernels
+    are not built for; checked before any launch."""
+    banner("deltanet shape errors")
+    B = 1
+    S = torch.zeros((B, 6, DV, DK), dtype=torch.float32, device="cuda")
+    q = torch.zeros((B, 4, DK), dtype=torch.float32, device="cuda")
+    v = torch.zeros((B, 6, DV), dtype=torch.float32, device="cuda")
+    g = torch.zeros((B, 6), dtype=torch.float32, device="cuda")
+    with pytest.raises(vm.DimensionMismatch):
+        vm.deltanet_recurrent_decode(q, q, v, g, g, S)
+    S64 = torch.zeros((B, 2, 64, 64), dtype=torch.float32, device="cuda")
+    q64 = torch.zeros((B, 1, 64), dtype=torch.float32, device="cuda")
+    v64 = torch.zeros((B, 2, 64), dtype=torch.float32, device="cuda")
+    g2 = torch.zeros((B, 2), dtype=torch.float32, device="cuda")
+    with pytest.raises(vm.UnsupportedShape):
+        vm.deltanet_recurrent_decode(q64, q64, v64, g2, g2, S64)

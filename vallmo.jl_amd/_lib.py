@@ -18,7 +18,8 @@ LIB_PATH = Path(__file__).resolve().parent / "csrc" / "libvallmo_attn.so"
 
 VM_E_ARG, VM_E_DIM, VM_E_UNSUPPORTED, VM_E_SCRATCH = -1, -2, -3, -4
 # kernel classes of vm_profile_read
-VM_K_ROWS, VM_K_DECODE_SPLIT, VM_K_DECODE_COMBINE, VM_K_PREFILL, VM_K_ADVANCE, VM_K_LM_HEAD = range(6)
+(VM_K_ROWS, VM_K_DECODE_SPLIT, VM_K_DECODE_COMBINE, VM_K_PREFILL, VM_K_ADVANCE, VM_K_LM_HEAD,
+ VM_K_DELTANET, VM_K_CONV) = range(8)
 
 
 class DimensionMismatch(ValueError):
@@ -115,6 +116,20 @@ _SIGS = {
     "vm_generation_advance": (_c_i, [_p, _p, _p, _p, _p, _c_i, _c_i, _p]),
     "vm_lm_head_argmax_scratch_bytes": (_c_sz, [_c_i, _c_i, _c_i]),
     "vm_lm_head_argmax": (_c_i, [_p, _p, _c_i64, _p, _c_i64, _c_i, _c_i, _c_i, _p, _c_sz, _p]),
+    "vm_causal_conv1d": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _p, _c_i64, _c_i64, _p, _c_i64, _p,
+                                _c_i, _c_i, _c_i, _c_i, _p]),
+    "vm_causal_conv1d_sequence": (_c_i, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _c_i64, _p,
+                                         _p, _p, _c_i64, _c_i64, _c_i, _c_i, _c_i, _c_i, _c_i,
+                                         _p]),
+    "vm_fused_deltanet_decode": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _p, _c_i64, _p,
+                                        _c_i64, _p, _c_i64, _p, _c_i64, _p, _p, _p, _p, _p, _c_i,
+                                        _c_i, _c_i, _c_i, _c_i, _c_f, _p]),
+    "vm_deltanet_recurrent_decode": (_c_i, [_p] * 8 + [_c_i] * 5 + [_p]),
+    "vm_deltanet_sequence": (_c_i, [_p] * 8 + [_c_i] * 6 + [_p]),
+    "vm_deltanet_prefill_prep": (_c_i, [_p] * 5 + [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _p]
+                                 + [_c_i] * 6 + [_p]),
+    "vm_gated_rms_norm": (_c_i, [_p, _c_i64, _c_i64, _p, _p, _c_i64, _c_i64, _p, _c_i, _c_i,
+                                 _c_i, _c_i, _c_f, _p]),
     "vm_fill_normal_bf16": (_c_i, [_p, _c_i64, _c_u64, _c_f, _c_f, _p]),
 }
 

@@ -1,0 +1,471 @@
+// deltanet.hip — the linear-attention layer parts of Qwen3.5 on gfx950: the
+// depthwise causal conv1d (one decode step with its ring state, and the whole
+// sequence) and the gated delta-rule recurrence (the fused decode step, the
+// plain step and the whole sequence), plus the prefill's prep (l2 norms, gates)
+// and its gated-RMSNorm epilogue.
+//
+// Reference: src/kernels/causal_conv1d.jl, src/kernels/deltanet_recurrent.jl,
+// src/kernels/deltanet_fused.jl and their call sites in src/llm/qwen35.jl
+// (decode!: :210-232, forward: :320-365).
+//
+// The recurrence: per (value head, sequence) a state S (Dk x Dv, fp32) with
+//   S = decay S;  delta = beta (v - S^T k);  S += k delta^T;  o = S^T q.
+// Every column of S evolves on its own given k, q, and its v entry, so the
+// kernels split the columns over waves with no cross-wave traffic: wave w
+// owns 2 NI columns; lane (j = lane % 32, h = lane / 32) holds rows 4j .. 4j+3
+// of columns 2 NI w + 2 i + h, i < NI (one 16-byte load per i: two adjacent
+// 512-byte columns per load instruction, 1 KB contiguous). The column sums
+// S^T k and S^T q are butterfly reduce-scatters over the 32 lanes of a half:
+// NI partial sums per lane become one full sum per lane group. The state is
+// read once and written once per step (the reference makes two passes).
+#include "common.h"
+#include "kernels.h"
+
+namespace vm {
+
+namespace {
+
+constexpr int DN_D = 128;  // Dk = Dv (Qwen3.5: deltanet.jl:12, qwen35.jl:19)
+
+__device__ __forceinline__ float accurate_silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float accurate_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// v[l ^ M] within each 32-lane half: DPP quad permutes for M = 1, 2, the
+// swizzle unit's bitmask mode (and 0x1f, xor M) for M = 4, 8, 16.
+template <int M>
+__device__ __forceinline__ float xor32(float v) {
+  const int x = __float_as_int(v);
+  if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+  if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(x, 0x1F | (M << 10)));
+}
+
+__device__ __forceinline__ float half_sum(float v) {
+  v += xor32<16>(v);
+  v += xor32<8>(v);
+  v += xor32<4>(v);
+  v += xor32<2>(v);
+  return v + xor32<1>(v);
+}
+
+// One scatter level over mask bit M: N values (index m + (N/2) * bit for the
+// kept half) -> N / 2, each summed with the partner lane's matching value.
+template <int M, int N>
+__device__ __forceinline__ void scatter_level(float (&p)[16], bool bit) {
+#pragma unroll
+  for (int m = 0; m < N / 2; ++m) {
+    const float keep = bit ? p[m + N / 2] : p[m];
+    const float send = bit ? p[m] : p[m + N / 2];
+    p[m] = keep + xor32<M>(send);
+  }
+}
+template <int M>
+__device__ __forceinline__ float sum_masks(float v) {  // plain sums over masks M, M/2, .., 1
+  if constexpr (M >= 1) return sum_masks<M / 2>(v + xor32<M>(v));
+  else return v;
+}
+template <int N, int M>
+__device__ __forceinline__ float rs_level(float (&p)[16], int j) {
+  if constexpr (N == 1) {
+    return sum_masks<M>(p[0]);
+  } else {
+    scatter_level<M, N>(p, (j & M) != 0);
+    return rs_level<N / 2, M / 2>(p, j);
+  }
+}
+// p[0 .. NI-1]: this lane's partial sums of its NI columns. Scatter levels on
+// masks 16, 8, .. (log2 NI of them) halve the values held, plain sums on the
+// rest of the mask bits finish: every lane then holds the sum over the 32 lanes
+// of its half for column index i = j >> (5 - log2 NI).
+template <int NI>
+__device__ __forceinline__ float reduce_scatter(float (&p)[16], int j) {
+  static_assert(NI == 16 || NI == 8 || NI == 4 || NI == 2, "NI");
+  return rs_level<NI, 16>(p, j);
+}
+
+// The sum of column index i sits in lanes (i << SH) .. of each half: lane
+// (j, h) fetches index i of its own half.
+template <int NI>
+__device__ __forceinline__ float column_value(float v, int i, int h) {
+  constexpr int SH = NI == 16 ? 1 : NI == 8 ? 2 : NI == 4 ? 3 : 4;
+  const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i << SH));
+  const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32 + (i << SH)));
+  return h ? hi : lo;
+}
+
+// One delta step of this lane's slice s[i][0..3] (rows 4j.., column index i):
+// returns o = S'^T q for column index j >> SH (the lane group's column).
+template <int NI>
+__device__ __forceinline__ float delta_step(float (&s)[16][4], const float (&kn)[4],
+                                            const float (&qn)[4], float v_col, float beta,
+                                            float decay, int j, int h) {
+  float p[16];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[i][e] *= decay;
+    p[i] = s[i][0] * kn[0] + s[i][1] * kn[1] + s[i][2] * kn[2] + s[i][3] * kn[3];
+  }
+  const float acc = reduce_scatter<NI>(p, j);
+  const float delta = beta * (v_col - acc);
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const float d = column_value<NI>(delta, i, h);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[i][e] += kn[e] * d;
+    p[i] = s[i][0] * qn[0] + s[i][1] * qn[1] + s[i][2] * qn[2] + s[i][3] * qn[3];
+  }
+  return reduce_scatter<NI>(p, j);
+}
+
+template <int NI>
+__device__ __forceinline__ void load_state(float (&s)[16][4], const float* base, int w, int lane) {
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const f32x4 t = __builtin_nontemporal_load(
+        reinterpret_cast<const f32x4*>(base + (int64_t)(2 * NI * w + 2 * i) * DN_D + 4 * lane));
+    s[i][0] = t[0];
+    s[i][1] = t[1];
+    s[i][2] = t[2];
+    s[i][3] = t[3];
+  }
+}
+template <int NI>
+__device__ __forceinline__ void store_state(const float (&s)[16][4], float* base, int w, int lane) {
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+    __builtin_nontemporal_store(f32x4{s[i][0], s[i][1], s[i][2], s[i][3]},
+                                reinterpret_cast<f32x4*>(base + (int64_t)(2 * NI * w + 2 * i) * DN_D + 4 * lane));
+}
+
+__device__ __forceinline__ void load4_bf16(const uint16_t* p, float (&x)[4]) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  x[0] = __uint_as_float(u.x << 16);
+  x[1] = __uint_as_float(u.x & 0xffff0000u);
+  x[2] = __uint_as_float(u.y << 16);
+  x[3] = __uint_as_float(u.y & 0xffff0000u);
+}
+
+}  // namespace
+
+// ---- fused_deltanet_decode! (deltanet_fused.jl:27-141): one block of four
+// waves per (value head, sequence), 32 columns per wave (NI = 16).
+__global__ __launch_bounds__(256) void deltanet_fused_decode_kernel(DeltaFusedArgs a) {
+  constexpr int NI = 16;
+  const int hv = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, j = lane & 31, h = lane >> 5;
+  const int hk = hv / (a.Hv / a.Hk);
+  const int64_t sb = ((int64_t)b * a.Hv + hv) * DN_D * DN_D;
+  float s[16][4];
+  load_state<NI>(s, a.s_in + sb, w, lane);
+  float q[4], k[4];
+  load4_bf16(a.q + b * a.q_sb + hk * DN_D + 4 * j, q);
+  load4_bf16(a.k + b * a.k_sb + hk * DN_D + 4 * j, k);
+  const int col = 2 * NI * w + 2 * (j >> 1) + h;  // this lane group's column
+  const float v_col = bf2f(a.v[b * a.v_sb + hv * DN_D + col]);
+  const float z_col = bf2f(a.z[b * a.z_sb + hv * DN_D + col]);
+  const float w_col = bf2f(a.norm_w[col]);
+  // per-value-head gates (deltanet_fused.jl:52-59)
+  const float spi = bf2f(a.alpha[b * a.a_sb + hv]) + a.dt_bias[hv];
+  const float sp = spi > 20.0f ? spi : logf(1.0f + expf(spi));
+  const float decay = expf(-expf(a.a_log[hv]) * sp);
+  const float beta = accurate_sigmoid(bf2f(a.beta[b * a.b_sb + hv]));
+  // l2 norms over the shared qk head (deltanet_fused.jl:61-71)
+  const float qss = half_sum(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
+  const float kss = half_sum(k[0] * k[0] + k[1] * k[1] + k[2] * k[2] + k[3] * k[3]);
+  const float qsc = 1.0f / sqrtf(qss + 1e-6f) / sqrtf((float)DN_D);
+  const float ksc = 1.0f / sqrtf(kss + 1e-6f);
+  float qn[4], kn[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    qn[e] = q[e] * qsc;
+    kn[e] = k[e] * ksc;
+  }
+  const float out = delta_step<NI>(s, kn, qn, v_col, beta, decay, j, h);
+  store_state<NI>(s, a.s_out + sb, w, lane);
+  // gated RMSNorm over the Dv columns (deltanet_fused.jl:98-105): lanes with j
+  // even hold each column once
+  __shared__ float red[4];
+  const float ss = half_sum((j & 1) ? 0.f : out * out);
+  const float wave_ss = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 0)) +
+                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 32));
+  if (lane == 0) red[w] = wave_ss;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  const float rstd = 1.0f / sqrtf(tot / (float)DN_D + a.eps);
+  if ((j & 1) == 0)
+    a.o[b * a.o_sb + hv * DN_D + col] = f2bf(out * rstd * w_col * accurate_silu(z_col));
+}
+
+// ---- deltanet_sequence! (deltanet_recurrent.jl:109-198) and, at T = 1,
+// deltanet_recurrent_decode! (:15-95): fp32 inputs already normed and gated.
+// Grid (columns / (2 NI * 4), Hv, B), four independent waves per block; the
+// state stays in registers across the T steps, the next step's inputs load
+// while the current one computes.
+template <int NI>
+__global__ __launch_bounds__(256) void deltanet_sequence_kernel(DeltaSeqArgs a) {
+  const int hv = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);  // wave index within the head
+  const int hk = hv / (a.Hv / a.Hk);
+  const int64_t sb = ((int64_t)b * a.Hv + hv) * DN_D * DN_D;
+  constexpr int SH = NI == 16 ? 1 : NI == 8 ? 2 : NI == 4 ? 3 : 4;
+  const int col = 2 * NI * w + 2 * (j >> SH) + h;
+  float s[16][4];
+  load_state<NI>(s, a.s_in + sb, w, lane);
+  const float* qp = a.q + ((int64_t)b * a.Hk + hk) * a.T * DN_D + 4 * j;
+  const float* kp = a.k + ((int64_t)b * a.Hk + hk) * a.T * DN_D + 4 * j;
+  const float* vp = a.v + ((int64_t)b * a.Hv + hv) * a.T * DN_D + col;
+  const float* bp = a.beta + (int64_t)b * a.T * a.Hv + hv;
+  const float* gp = a.gate + (int64_t)b * a.T * a.Hv + hv;
+  float* op = a.o + ((int64_t)b * a.Hv + hv) * a.T * DN_D + col;
+  float4 qv = *reinterpret_cast<const float4*>(qp);
+  float4 kv = *reinterpret_cast<const float4*>(kp);
+  float v_col = *vp, beta = *bp, gate = *gp;
+  for (int t = 0; t < a.T; ++t) {
+    const float qn[4] = {qv.x, qv.y, qv.z, qv.w};
+    const float kn[4] = {kv.x, kv.y, kv.z, kv.w};
+    const float vc = v_col, bt = beta, decay = expf(gate);
+    if (t + 1 < a.T) {  // the next step's inputs
+      const int64_t o4 = (int64_t)(t + 1) * DN_D;
+      qv = *reinterpret_cast<const float4*>(qp + o4);
+      kv = *reinterpret_cast<const float4*>(kp + o4);
+      v_col = vp[o4];
+      beta = bp[(int64_t)(t + 1) * a.Hv];
+      gate = gp[(int64_t)(t + 1) * a.Hv];
+    }
+    const float out = delta_step<NI>(s, kn, qn, vc, bt, decay, j, h);
+    if ((j & ((1 << SH) - 1)) == 0) op[(int64_t)t * DN_D] = out;
+  }
+  store_state<NI>(s, a.s_out + sb, w, lane);
+}
+
+// ---- the prefill's inputs to the recurrence (qwen35.jl:347-356): one wave per
+// (token, head): q / k heads l2-normed (q also by 1/sqrt(Dk)) from the conv
+// output, v heads widened to fp32, gates from the alpha | beta projection.
+__global__ __launch_bounds__(256) void deltanet_prep_kernel(DeltaPrepArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nh = 2 * a.Hk + a.Hv;  // q heads, k heads, v heads
+  const int64_t tok = wid / nh;    // b * T + t
+  if (tok >= (int64_t)a.B * a.T) return;
+  const int hh = (int)(wid % nh);
+  const int b = (int)(tok / a.T), t = (int)(tok % a.T);
+  const uint16_t* row = a.cv + (int64_t)b * a.cv_sb + (int64_t)t * a.cv_st + hh * DN_D;
+  const float x0 = bf2f(row[2 * lane]), x1 = bf2f(row[2 * lane + 1]);
+  if (hh < 2 * a.Hk) {
+    const int hk = hh % a.Hk;
+    float ss = x0 * x0 + x1 * x1;
+    ss += __shfl_xor(ss, 32);
+    ss = half_sum(ss);
+    const float den = sqrtf(ss + 1e-6f);
+    const bool isq = hh < a.Hk;
+    const float sc = isq ? 1.0f / sqrtf((float)DN_D) : 1.0f;
+    float* dst = (isq ? a.qe : a.ke) + (((int64_t)b * a.Hk + hk) * a.T + t) * DN_D;
+    *reinterpret_cast<float2*>(dst + 2 * lane) = make_float2(x0 / den * sc, x1 / den * sc);
+  } else {
+    const int hv = hh - 2 * a.Hk;
+    float* dst = a.ve + (((int64_t)b * a.Hv + hv) * a.T + t) * DN_D;
+    *reinterpret_cast<float2*>(dst + 2 * lane) = make_float2(x0, x1);
+    if (lane == 0) {
+      const uint16_t* ab = a.ab + (int64_t)b * a.ab_sb + (int64_t)t * a.ab_st;
+      const int64_t g = ((int64_t)b * a.T + t) * a.Hv + hv;
+      a.beta[g] = accurate_sigmoid(bf2f(ab[a.Hv + hv]));
+      a.gate[g] = -expf(a.a_log[hv]) * log1pf(expf(bf2f(ab[hv]) + a.dt_bias[hv]));
+    }
+  }
+}
+
+// ---- the prefill's epilogue (qwen35.jl:360-364): one wave per (head, token):
+// y = o rstd norm_w silu(z) in bf16, written in the out projection's input
+// layout (Dv, Hv, T, B).
+__global__ __launch_bounds__(256) void gated_rms_norm_kernel(GatedNormArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wid >= (int64_t)a.B * a.T * a.Hv) return;
+  const int hv = (int)(wid % a.Hv);
+  const int64_t tok = wid / a.Hv;
+  const int b = (int)(tok / a.T), t = (int)(tok % a.T);
+  const float2 o = *reinterpret_cast<const float2*>(
+      a.o + (((int64_t)b * a.Hv + hv) * a.T + t) * DN_D + 2 * lane);
+  float ss = o.x * o.x + o.y * o.y;
+  ss += __shfl_xor(ss, 32);
+  ss = half_sum(ss);
+  const float rstd = 1.0f / sqrtf(ss / (float)DN_D + a.eps);
+  const uint16_t* z = a.z + (int64_t)b * a.z_sb + (int64_t)t * a.z_st + hv * DN_D + 2 * lane;
+  const float w0 = bf2f(a.norm_w[2 * lane]), w1 = bf2f(a.norm_w[2 * lane + 1]);
+  const float y0 = o.x * rstd * w0 * accurate_silu(bf2f(z[0]));
+  const float y1 = o.y * rstd * w1 * accurate_silu(bf2f(z[1]));
+  *reinterpret_cast<uint32_t*>(a.y + (int64_t)b * a.y_sb + (int64_t)t * a.y_st + hv * DN_D +
+                               2 * lane) = pack2(y0, y1);
+}
+
+// ---- causal_conv1d! (causal_conv1d.jl:7-61): one thread per 8 channels of one
+// sequence. The ring's columns are all read before any is written, so the
+// shifted ring may overwrite the one read (in place, as the reference runs it).
+template <int K>
+__global__ __launch_bounds__(256) void conv1d_update_kernel(Conv1dArgs a) {
+  const int64_t c8 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (c8 * 8 >= a.D) return;
+  const int d = (int)c8 * 8;
+  uint4 raw[K];
+#pragma unroll
+  for (int i = 0; i < K - 1; ++i)
+    raw[i] = *reinterpret_cast<const uint4*>(a.s_in + b * a.s_sb + (int64_t)(i + 1) * a.s_cs + d);
+  raw[K - 1] = *reinterpret_cast<const uint4*>(a.x + b * a.x_sb + d);
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    float c[8], wf[8];
+    unpack8(raw[i], c);
+    unpack8(*reinterpret_cast<const uint4*>(a.w + (int64_t)i * a.w_cs + d), wf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += c[e] * wf[e];
+  }
+#pragma unroll
+  for (int i = 0; i < K; ++i)
+    *reinterpret_cast<uint4*>(a.s_out + b * a.s_sb + (int64_t)i * a.s_cs + d) = raw[i];
+  if (a.bias) {
+    float bf8[8];
+    unpack8(*reinterpret_cast<const uint4*>(a.bias + d), bf8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += bf8[e];
+  }
+  if (a.act) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = accurate_silu(acc[e]);
+  }
+  *reinterpret_cast<uint4*>(a.y + b * a.y_sb + d) = pack8(acc);
+}
+
+// ---- causal_conv1d_sequence! (causal_conv1d.jl:73-149): thread = 8 channels x
+// a run of CONV_TC tokens of one sequence, the window of the last K inputs in
+// registers. The left context of token 0 is the ring's columns 2..K (s_in:
+// the suffix prefill of qwen35.jl:333-344) or zeros. Only the threads of run 0
+// read s_in (CONV_TC >= K - 1), and they also write the seeded ring (the last
+// K inputs of the context-extended sequence) after reading, so s_out may alias
+// s_in.
+namespace {
+template <int K>
+__device__ __forceinline__ uint4 conv_ext(const Conv1dArgs& a, int b, int d, int t) {
+  // ext(t), t in [-(K-1), T): x[t] for t >= 0, else ring column K + t (0-based)
+  if (t >= 0) return *reinterpret_cast<const uint4*>(a.x + b * a.x_sb + (int64_t)t * a.x_st + d);
+  if (a.s_in)
+    return *reinterpret_cast<const uint4*>(a.s_in + b * a.s_sb + (int64_t)(K + t) * a.s_cs + d);
+  return make_uint4(0, 0, 0, 0);
+}
+}  // namespace
+
+template <int K>
+__global__ __launch_bounds__(256) void conv1d_sequence_kernel(Conv1dArgs a) {
+  static_assert(CONV_TC >= K - 1, "run 0 must cover the context reads");
+  const int64_t c8 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int run = blockIdx.y, b = blockIdx.z;
+  if (c8 * 8 >= a.D) return;
+  const int d = (int)c8 * 8;
+  const int t0 = run * CONV_TC;
+  const int t1 = min(t0 + CONV_TC, a.T);
+  float wf[K][8];
+#pragma unroll
+  for (int i = 0; i < K; ++i)
+    unpack8(*reinterpret_cast<const uint4*>(a.w + (int64_t)i * a.w_cs + d), wf[i]);
+  float bias8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (a.bias) unpack8(*reinterpret_cast<const uint4*>(a.bias + d), bias8);
+  float win[K][8];  // win[i] = ext(t - K + 1 + i) for the current t
+#pragma unroll
+  for (int i = 0; i < K - 1; ++i) unpack8(conv_ext<K>(a, b, d, t0 - K + 1 + i), win[i]);
+  for (int t = t0; t < t1; ++t) {
+    unpack8(conv_ext<K>(a, b, d, t), win[K - 1]);
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = 0.f;
+#pragma unroll
+      for (int i = 0; i < K; ++i) v += win[i][e] * wf[i][e];
+      v += bias8[e];
+      acc[e] = a.act ? accurate_silu(v) : v;
+    }
+    *reinterpret_cast<uint4*>(a.y + b * a.y_sb + (int64_t)t * a.y_st + d) = pack8(acc);
+#pragma unroll
+    for (int i = 0; i + 1 < K; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[i][e] = win[i + 1][e];
+  }
+  if (run == 0 && a.s_out) {
+    uint4 seed[K];  // column i = ext(T - K + i); every column read first (aliasing)
+#pragma unroll
+    for (int i = 0; i < K; ++i) seed[i] = conv_ext<K>(a, b, d, a.T - K + i);
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+      *reinterpret_cast<uint4*>(a.s_out + b * a.s_sb + (int64_t)i * a.s_cs + d) = seed[i];
+  }
+}
+
+// ---- launchers -----------------------------------------------------------
+hipError_t launch_deltanet_fused_decode(const DeltaFusedArgs& a, hipStream_t st) {
+  if (a.B == 0) return hipSuccess;
+  hipLaunchKernelGGL(deltanet_fused_decode_kernel, dim3(a.Hv, a.B), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_deltanet_sequence(const DeltaSeqArgs& a, hipStream_t st) {
+  if (a.B == 0 || a.T == 0) {
+    if (a.B > 0 && a.s_out != a.s_in)  // T = 0: the state passes through
+      return hipMemcpyAsync(a.s_out, a.s_in, (size_t)a.B * a.Hv * DN_D * DN_D * sizeof(float),
+                            hipMemcpyDeviceToDevice, st);
+    return hipSuccess;
+  }
+  // few blocks (small B * Hv): 16 waves per head (NI = 4), else 4 (NI = 16)
+  if ((int64_t)a.B * a.Hv >= 512) {
+    hipLaunchKernelGGL(deltanet_sequence_kernel<16>, dim3(1, a.Hv, a.B), dim3(256), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(deltanet_sequence_kernel<4>, dim3(4, a.Hv, a.B), dim3(256), 0, st, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_deltanet_prep(const DeltaPrepArgs& a, hipStream_t st) {
+  const int64_t waves = (int64_t)a.B * a.T * (2 * a.Hk + a.Hv);
+  if (waves == 0) return hipSuccess;
+  hipLaunchKernelGGL(deltanet_prep_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gated_rms_norm(const GatedNormArgs& a, hipStream_t st) {
+  const int64_t waves = (int64_t)a.B * a.T * a.Hv;
+  if (waves == 0) return hipSuccess;
+  hipLaunchKernelGGL(gated_rms_norm_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+#define VM_CONV_K_CASES(X) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
+
+hipError_t launch_conv1d_update(const Conv1dArgs& a, hipStream_t st) {
+  if (a.B == 0) return hipSuccess;
+  const dim3 grid((unsigned)((a.D / 8 + 255) / 256), a.B);
+  switch (a.K) {
+#define X(k) \
+  case k: hipLaunchKernelGGL(conv1d_update_kernel<k>, grid, dim3(256), 0, st, a); break;
+    VM_CONV_K_CASES(X)
+#undef X
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_conv1d_sequence(const Conv1dArgs& a, hipStream_t st) {
+  if (a.B == 0 || a.T == 0) return hipSuccess;
+  const int runs = (a.T + CONV_TC - 1) / CONV_TC;
+  const dim3 grid((unsigned)((a.D / 8 + 255) / 256), runs, a.B);
+  switch (a.K) {
+#define X(k) \
+  case k: hipLaunchKernelGGL(conv1d_sequence_kernel<k>, grid, dim3(256), 0, st, a); break;
+    VM_CONV_K_CASES(X)
+#undef X
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace vm

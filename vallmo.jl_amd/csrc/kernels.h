@@ -223,6 +223,81 @@ GemvPlan gemv_plan(int M, int K, int waves);
 size_t gemv_workspace_bytes(int M, int K);
 hipError_t launch_gemv(GemvArgs a, hipStream_t st);
 hipError_t launch_rms_norm(const NormArgs& a, hipStream_t st);
+
+// ---- linear-attention layer parts (deltanet.hip). Dk = Dv = 128; element
+// strides; state S (Dk, Dv, Hv, B) fp32 contiguous.
+// fused_deltanet_decode!: q, k (Dk, Hk, B), v, z (Dv, Hv, B), alpha, beta
+// (Hv, B) with per-sequence strides *_sb, heads contiguous; o (Dv, Hv, B) bf16.
+struct DeltaFusedArgs {
+  uint16_t* o;
+  int64_t o_sb;
+  const uint16_t *q, *k, *v, *z, *alpha, *beta;
+  int64_t q_sb, k_sb, v_sb, z_sb, a_sb, b_sb;
+  const float *a_log, *dt_bias;
+  const uint16_t* norm_w;
+  const float* s_in;
+  float* s_out;
+  int Hk, Hv, B;
+  float eps;
+};
+// deltanet_sequence! / deltanet_recurrent_decode! (T = 1): q, k (Dk, T, Hk, B),
+// v, o (Dv, T, Hv, B), beta, gate (Hv, T, B), all fp32 contiguous.
+struct DeltaSeqArgs {
+  float* o;
+  const float *q, *k, *v, *beta, *gate;
+  const float* s_in;
+  float* s_out;
+  int T, Hk, Hv, B;
+};
+// the prefill's prep: conv output cv (2 Hk Dk + Hv Dv channels, token stride
+// cv_st, sequence stride cv_sb), ab (alpha | beta, 2 Hv rows, ab_st, ab_sb) ->
+// qe, ke (Dk, T, Hk, B), ve (Dv, T, Hv, B), beta, gate (Hv, T, B) fp32.
+struct DeltaPrepArgs {
+  const uint16_t* cv;
+  int64_t cv_st, cv_sb;
+  const uint16_t* ab;
+  int64_t ab_st, ab_sb;
+  const float *a_log, *dt_bias;
+  float *qe, *ke, *ve, *beta, *gate;
+  int T, Hk, Hv, B;
+};
+// the prefill's gated RMSNorm: o (Dv, T, Hv, B) fp32, z (Dv, Hv) rows at token
+// stride z_st / sequence stride z_sb -> y (Dv, Hv) rows at y_st / y_sb, bf16.
+struct GatedNormArgs {
+  const float* o;
+  const uint16_t* z;
+  int64_t z_st, z_sb;
+  const uint16_t* norm_w;
+  uint16_t* y;
+  int64_t y_st, y_sb;
+  int T, Hv, B;
+  float eps;
+};
+// causal conv1d over D channels (D % 8 == 0, 16-byte aligned rows): x, y rows
+// at token stride *_st / sequence stride *_sb; ring (D, K, B) with column
+// stride s_cs and sequence stride s_sb; w (D, K) with column stride w_cs;
+// bias (D) or NULL; act: silu. Decode reads s_in and writes s_out (may alias);
+// the sequence form reads s_in (NULL: zero context) and seeds s_out (NULL: no).
+constexpr int CONV_TC = 16;  // tokens per thread in the sequence form
+struct Conv1dArgs {
+  uint16_t* y;
+  int64_t y_st, y_sb;
+  const uint16_t* x;
+  int64_t x_st, x_sb;
+  const uint16_t* s_in;
+  uint16_t* s_out;
+  int64_t s_cs, s_sb;
+  const uint16_t* w;
+  int64_t w_cs;
+  const uint16_t* bias;
+  int D, K, T, B, act;
+};
+hipError_t launch_deltanet_fused_decode(const DeltaFusedArgs& a, hipStream_t st);
+hipError_t launch_deltanet_sequence(const DeltaSeqArgs& a, hipStream_t st);
+hipError_t launch_deltanet_prep(const DeltaPrepArgs& a, hipStream_t st);
+hipError_t launch_gated_rms_norm(const GatedNormArgs& a, hipStream_t st);
+hipError_t launch_conv1d_update(const Conv1dArgs& a, hipStream_t st);
+hipError_t launch_conv1d_sequence(const Conv1dArgs& a, hipStream_t st);
 hipError_t launch_silu_mul(const SiluMulArgs& a, hipStream_t st);
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t st);
 hipError_t launch_gen_advance(const AdvanceArgs& a, hipStream_t st);

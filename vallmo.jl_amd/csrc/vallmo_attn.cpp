@@ -770,6 +770,214 @@ int vm_linear(vm_bf16* y, int64_t ldy, const vm_bf16* x, int64_t ldx, const vm_b
                         sizeof g_err);
 }
 
+// ---- f4: the linear-attention layer parts -----------------------------------
+namespace {
+int check_dn_heads(int Dk, int Dv, int Hk, int Hv, int B, const char* what) {
+  REQUIRE(Dk == 128 && Dv == 128, VM_E_UNSUPPORTED,
+          "%s: Dk = %d, Dv = %d; the kernels are built for Dk = Dv = 128", what, Dk, Dv);
+  REQUIRE(Hk > 0 && Hv > 0 && B >= 0, VM_E_ARG, "%s: Hk = %d, Hv = %d, B = %d", what, Hk, Hv, B);
+  REQUIRE(Hv % Hk == 0, VM_E_DIM, "value heads (%d) is not a multiple of key heads (%d)", Hv, Hk);
+  return VM_OK;
+}
+// the state out either is the state in (in place) or does not overlap it
+int check_alias(const void* in, const void* out, size_t bytes, const char* what) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(in), b = reinterpret_cast<uintptr_t>(out);
+  REQUIRE(a == b || a + bytes <= b || b + bytes <= a, VM_E_ARG,
+          "%s: state out partially overlaps state in (alias exactly or not at all)", what);
+  return VM_OK;
+}
+int check_align8(const void* p, int64_t stride, const char* name) {
+  REQUIRE(p != nullptr, VM_E_ARG, "%s is NULL", name);
+  REQUIRE((reinterpret_cast<uintptr_t>(p) & 7u) == 0 && stride >= 0 && stride % 4 == 0, VM_E_ARG,
+          "%s must be 8-byte aligned with a sequence stride that is a multiple of 4", name);
+  return VM_OK;
+}
+int check_conv(int D, int K, int B, int T, const char* what) {
+  REQUIRE(D > 0 && D % 8 == 0, VM_E_UNSUPPORTED, "%s: D = %d must be a positive multiple of 8",
+          what, D);
+  REQUIRE(K >= 1 && K <= 8, VM_E_UNSUPPORTED, "%s: kernel size K = %d outside 1..8", what, K);
+  REQUIRE(B >= 0 && T >= 0, VM_E_ARG, "%s: B = %d, T = %d", what, B, T);
+  return VM_OK;
+}
+}  // namespace
+
+int vm_causal_conv1d(vm_bf16* y, int64_t y_sb, const vm_bf16* x, int64_t x_sb,
+                     const vm_bf16* s_in, vm_bf16* s_out, int64_t s_cs, int64_t s_sb,
+                     const vm_bf16* w, int64_t w_cs, const vm_bf16* bias, int D, int K, int B,
+                     int act, vm_stream st) {
+  TRY(check_conv(D, K, B, 1, "causal_conv1d"));
+  if (B == 0) return VM_OK;
+  TRY(check_aligned(y, "Y"));
+  TRY(check_aligned(x, "X"));
+  TRY(check_aligned(s_in, "S"));
+  TRY(check_aligned(s_out, "S_out"));
+  TRY(check_aligned(w, "Weight"));
+  if (bias) TRY(check_aligned(bias, "Bias"));
+  for (int64_t v : {y_sb, x_sb, s_cs, s_sb, w_cs}) TRY(check_stride(v, "causal_conv1d"));
+  REQUIRE(s_cs >= D && w_cs >= D && (B <= 1 || (s_sb >= s_cs * K && y_sb >= D && x_sb >= D)),
+          VM_E_DIM, "causal_conv1d: strides below the extents (D = %d, K = %d)", D, K);
+  TRY(check_alias(s_in, s_out, (size_t)((B - 1) * s_sb + (K - 1) * s_cs + D) * 2, "causal_conv1d"));
+  vm::Conv1dArgs a{};
+  a.y = y; a.y_sb = y_sb; a.x = x; a.x_sb = x_sb; a.s_in = s_in; a.s_out = s_out;
+  a.s_cs = s_cs; a.s_sb = s_sb; a.w = w; a.w_cs = w_cs; a.bias = bias;
+  a.D = D; a.K = K; a.T = 1; a.B = B; a.act = act ? 1 : 0;
+  return hip_status(timed(VM_K_CONV, S(st), [&] { return vm::launch_conv1d_update(a, S(st)); }),
+                    "causal_conv1d");
+}
+
+int vm_causal_conv1d_sequence(vm_bf16* y, int64_t y_st, int64_t y_sb, const vm_bf16* x,
+                              int64_t x_st, int64_t x_sb, const vm_bf16* w, int64_t w_cs,
+                              const vm_bf16* bias, const vm_bf16* s_in, vm_bf16* s_out,
+                              int64_t s_cs, int64_t s_sb, int D, int K, int T, int B, int act,
+                              vm_stream st) {
+  TRY(check_conv(D, K, B, T, "causal_conv1d_sequence"));
+  if (B == 0 || T == 0) return VM_OK;
+  TRY(check_aligned(y, "Y"));
+  TRY(check_aligned(x, "X"));
+  TRY(check_aligned(w, "Weight"));
+  if (bias) TRY(check_aligned(bias, "Bias"));
+  if (s_in) TRY(check_aligned(s_in, "S"));
+  if (s_out) TRY(check_aligned(s_out, "S_out"));
+  for (int64_t v : {y_st, y_sb, x_st, x_sb, w_cs, s_cs, s_sb})
+    TRY(check_stride(v, "causal_conv1d_sequence"));
+  REQUIRE(w_cs >= D && (T <= 1 || (y_st >= D && x_st >= D)) &&
+              (B <= 1 || (y_sb >= y_st * T && x_sb >= x_st * T)),
+          VM_E_DIM, "causal_conv1d_sequence: strides below the extents (D = %d, T = %d)", D, T);
+  if (s_in || s_out)
+    REQUIRE(s_cs >= D && (B <= 1 || s_sb >= s_cs * K), VM_E_DIM,
+            "causal_conv1d_sequence: state strides below (D, K) = (%d, %d)", D, K);
+  if (s_in && s_out)
+    TRY(check_alias(s_in, s_out, (size_t)((B - 1) * s_sb + (K - 1) * s_cs + D) * 2,
+                    "causal_conv1d_sequence"));
+  vm::Conv1dArgs a{};
+  a.y = y; a.y_st = y_st; a.y_sb = y_sb; a.x = x; a.x_st = x_st; a.x_sb = x_sb;
+  a.s_in = s_in; a.s_out = s_out; a.s_cs = s_cs; a.s_sb = s_sb; a.w = w; a.w_cs = w_cs;
+  a.bias = bias; a.D = D; a.K = K; a.T = T; a.B = B; a.act = act ? 1 : 0;
+  return hip_status(timed(VM_K_CONV, S(st), [&] { return vm::launch_conv1d_sequence(a, S(st)); }),
+                    "causal_conv1d_sequence");
+}
+
+int vm_fused_deltanet_decode(vm_bf16* o, int64_t o_sb, const vm_bf16* q, int64_t q_sb,
+                             const vm_bf16* k, int64_t k_sb, const vm_bf16* v, int64_t v_sb,
+                             const vm_bf16* alpha, int64_t a_sb, const vm_bf16* beta_raw,
+                             int64_t b_sb, const vm_bf16* z, int64_t z_sb, const float* a_log,
+                             const float* dt_bias, const vm_bf16* norm_w, const float* s_in,
+                             float* s_out, int Dk, int Dv, int Hk, int Hv, int B, float eps,
+                             vm_stream st) {
+  TRY(check_dn_heads(Dk, Dv, Hk, Hv, B, "fused_deltanet_decode"));
+  if (B == 0) return VM_OK;
+  REQUIRE(o && v && z && alpha && beta_raw && a_log && dt_bias && norm_w, VM_E_ARG,
+          "fused_deltanet_decode: NULL pointer argument");
+  TRY(check_align8(q, q_sb, "Q_raw"));
+  TRY(check_align8(k, k_sb, "K_raw"));
+  TRY(check_aligned(s_in, "S"));
+  TRY(check_aligned(s_out, "S_out"));
+  REQUIRE(B <= 1 || (q_sb >= (int64_t)Hk * Dk && k_sb >= (int64_t)Hk * Dk &&
+                     v_sb >= (int64_t)Hv * Dv && z_sb >= (int64_t)Hv * Dv &&
+                     o_sb >= (int64_t)Hv * Dv && a_sb >= Hv && b_sb >= Hv),
+          VM_E_DIM, "fused_deltanet_decode: sequence strides below the head extents");
+  const size_t sbytes = (size_t)B * Hv * Dk * Dv * sizeof(float);
+  TRY(check_alias(s_in, s_out, sbytes, "fused_deltanet_decode"));
+  vm::DeltaFusedArgs a{};
+  a.o = o; a.o_sb = o_sb; a.q = q; a.q_sb = q_sb; a.k = k; a.k_sb = k_sb; a.v = v; a.v_sb = v_sb;
+  a.z = z; a.z_sb = z_sb; a.alpha = alpha; a.a_sb = a_sb; a.beta = beta_raw; a.b_sb = b_sb;
+  a.a_log = a_log; a.dt_bias = dt_bias; a.norm_w = norm_w; a.s_in = s_in; a.s_out = s_out;
+  a.Hk = Hk; a.Hv = Hv; a.B = B; a.eps = eps;
+  return hip_status(
+      timed(VM_K_DELTANET, S(st), [&] { return vm::launch_deltanet_fused_decode(a, S(st)); }),
+      "fused_deltanet_decode");
+}
+
+static int deltanet_seq(float* o, const float* q, const float* k, const float* v,
+                        const float* beta, const float* gate, const float* s_in, float* s_out,
+                        int Dk, int Dv, int T, int Hk, int Hv, int B, vm_stream st,
+                        const char* what) {
+  TRY(check_dn_heads(Dk, Dv, Hk, Hv, B, what));
+  REQUIRE(T >= 0, VM_E_ARG, "%s: T = %d", what, T);
+  if (B == 0) return VM_OK;
+  TRY(check_aligned(s_in, "S"));
+  TRY(check_aligned(s_out, "S_out"));
+  TRY(check_alias(s_in, s_out, (size_t)B * Hv * Dk * Dv * sizeof(float), what));
+  if (T > 0) {
+    TRY(check_aligned(o, "O"));
+    TRY(check_aligned(q, "Q"));
+    TRY(check_aligned(k, "K"));
+    TRY(check_aligned(v, "V"));
+    REQUIRE(beta && gate, VM_E_ARG, "%s: NULL Beta or Gate", what);
+  }
+  vm::DeltaSeqArgs a{};
+  a.o = o; a.q = q; a.k = k; a.v = v; a.beta = beta; a.gate = gate; a.s_in = s_in;
+  a.s_out = s_out; a.T = T; a.Hk = Hk; a.Hv = Hv; a.B = B;
+  return hip_status(
+      timed(VM_K_DELTANET, S(st), [&] { return vm::launch_deltanet_sequence(a, S(st)); }), what);
+}
+
+int vm_deltanet_recurrent_decode(float* o, const float* q, const float* k, const float* v,
+                                 const float* beta, const float* gate, const float* s_in,
+                                 float* s_out, int Dk, int Dv, int Hk, int Hv, int B,
+                                 vm_stream st) {
+  return deltanet_seq(o, q, k, v, beta, gate, s_in, s_out, Dk, Dv, 1, Hk, Hv, B, st,
+                      "deltanet_recurrent_decode");
+}
+
+int vm_deltanet_sequence(float* o, const float* q, const float* k, const float* v,
+                         const float* beta, const float* gate, const float* s_in, float* s_out,
+                         int Dk, int Dv, int T, int Hk, int Hv, int B, vm_stream st) {
+  return deltanet_seq(o, q, k, v, beta, gate, s_in, s_out, Dk, Dv, T, Hk, Hv, B, st,
+                      "deltanet_sequence");
+}
+
+int vm_deltanet_prefill_prep(float* qe, float* ke, float* ve, float* beta, float* gate,
+                             const vm_bf16* cv, int64_t cv_st, int64_t cv_sb, const vm_bf16* ab,
+                             int64_t ab_st, int64_t ab_sb, const float* a_log,
+                             const float* dt_bias, int Dk, int Dv, int Hk, int Hv, int T, int B,
+                             vm_stream st) {
+  TRY(check_dn_heads(Dk, Dv, Hk, Hv, B, "deltanet_prefill_prep"));
+  REQUIRE(T >= 0, VM_E_ARG, "deltanet_prefill_prep: T = %d", T);
+  if (B == 0 || T == 0) return VM_OK;
+  REQUIRE(qe && ke && ve && beta && gate && ab && a_log && dt_bias, VM_E_ARG,
+          "deltanet_prefill_prep: NULL pointer argument");
+  TRY(check_align8(cv, cv_st, "conv output"));
+  REQUIRE(cv_sb % 4 == 0, VM_E_ARG, "deltanet_prefill_prep: conv sequence stride %% 4 != 0");
+  for (const float* p : {qe, ke, ve})
+    REQUIRE((reinterpret_cast<uintptr_t>(p) & 7u) == 0, VM_E_ARG,
+            "deltanet_prefill_prep: fp32 outputs must be 8-byte aligned");
+  const int64_t n = 2LL * Hk * Dk + (int64_t)Hv * Dv;
+  REQUIRE((T <= 1 || (cv_st >= n && ab_st >= 2LL * Hv)) &&
+              (B <= 1 || (cv_sb >= cv_st * T && ab_sb >= ab_st * T)),
+          VM_E_DIM, "deltanet_prefill_prep: strides below the extents (n = %lld)", (long long)n);
+  vm::DeltaPrepArgs a{};
+  a.cv = cv; a.cv_st = cv_st; a.cv_sb = cv_sb; a.ab = ab; a.ab_st = ab_st; a.ab_sb = ab_sb;
+  a.a_log = a_log; a.dt_bias = dt_bias; a.qe = qe; a.ke = ke; a.ve = ve; a.beta = beta;
+  a.gate = gate; a.T = T; a.Hk = Hk; a.Hv = Hv; a.B = B;
+  return hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_deltanet_prep(a, S(st)); }),
+                    "deltanet_prefill_prep");
+}
+
+int vm_gated_rms_norm(vm_bf16* y, int64_t y_st, int64_t y_sb, const float* o, const vm_bf16* z,
+                      int64_t z_st, int64_t z_sb, const vm_bf16* norm_w, int Dv, int Hv, int T,
+                      int B, float eps, vm_stream st) {
+  REQUIRE(Dv == 128, VM_E_UNSUPPORTED, "gated_rms_norm: Dv = %d; built for 128", Dv);
+  REQUIRE(Hv > 0 && T >= 0 && B >= 0, VM_E_ARG, "gated_rms_norm: Hv = %d, T = %d, B = %d", Hv,
+          T, B);
+  if (B == 0 || T == 0) return VM_OK;
+  REQUIRE(o && norm_w && (reinterpret_cast<uintptr_t>(o) & 7u) == 0, VM_E_ARG,
+          "gated_rms_norm: O must be 8-byte aligned");
+  for (const void* p : {(const void*)y, (const void*)z})
+    REQUIRE(p && (reinterpret_cast<uintptr_t>(p) & 3u) == 0, VM_E_ARG,
+            "gated_rms_norm: Y and Z must be 4-byte aligned");
+  REQUIRE(y_st % 2 == 0 && y_sb % 2 == 0 && z_st % 2 == 0 && z_sb % 2 == 0, VM_E_ARG,
+          "gated_rms_norm: strides must be even");
+  REQUIRE((T <= 1 || (y_st >= (int64_t)Hv * Dv && z_st >= (int64_t)Hv * Dv)) &&
+              (B <= 1 || (y_sb >= y_st * T && z_sb >= z_st * T)),
+          VM_E_DIM, "gated_rms_norm: strides below the extents");
+  vm::GatedNormArgs a{};
+  a.o = o; a.z = z; a.z_st = z_st; a.z_sb = z_sb; a.norm_w = norm_w; a.y = y; a.y_st = y_st;
+  a.y_sb = y_sb; a.T = T; a.Hv = Hv; a.B = B; a.eps = eps;
+  return hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_gated_rms_norm(a, S(st)); }),
+                    "gated_rms_norm");
+}
+
 // ---- synthetic inputs ------------------------------------------------------
 int vm_fill_normal_bf16(vm_bf16* dst, int64_t n, uint64_t seed, float scale, float shift,
                         vm_stream st) {

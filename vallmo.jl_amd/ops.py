@@ -26,6 +26,10 @@ __all__ = [
     "sigmoid", "fill_normal_", "linear_", "linear", "linear_workspace_bytes",
     "rms_norm_", "rms_norm", "fused_add_rms_norm_", "fused_add_rms_norm", "silu_mul_",
     "embed_", "lm_head_argmax_", "lm_head_argmax", "lm_head_argmax_scratch_bytes",
+    "causal_conv1d_", "causal_conv1d", "causal_conv1d_sequence_", "causal_conv1d_sequence",
+    "fused_deltanet_decode_", "fused_deltanet_decode", "deltanet_recurrent_decode_",
+    "deltanet_recurrent_decode", "deltanet_sequence_", "deltanet_sequence",
+    "deltanet_prefill_prep_", "gated_rms_norm_",
 ]
 
 
@@ -372,6 +376,216 @@ def lm_head_argmax(X, W, **kw) -> dict:
     """Allocating lm_head_argmax (lm_head_topk.jl:149-163): {"Result": (B,) int32}."""
     R = torch.empty((_rows(X),), dtype=torch.int32, device=X.device)
     return lm_head_argmax_({"Result": R}, X, W, **kw)
+
+
+# ---- the linear-attention layer parts (src/kernels/causal_conv1d.jl,
+# deltanet_recurrent.jl, deltanet_fused.jl) -----------------------------------
+
+def _st(t, dim, canon):
+    """Stride of dim, or the canonical one when the extent is 1 (any stride is
+    valid there, torch may report an odd one)."""
+    return t.stride(dim) if t.shape[dim] > 1 else canon
+
+
+def _act(sigma):
+    if sigma is None:
+        return 0
+    if sigma == "silu" or getattr(sigma, "__name__", "") == "silu":
+        return 1
+    raise ArgumentError(f"σ = {sigma!r}: the kernels apply silu or nothing")
+
+
+def causal_conv1d_(outs, X, S, Weight, Bias=None, *, sigma=None):
+    """causal_conv1d!((; Y, S′), X, S, Weight, Bias; σ) — src/kernels/causal_conv1d.jl:43-61:
+    one decode step. X, Y :: (D, B) (torch (B, D), rows may be strided), the ring
+    S, S′ :: (D, K, B) (torch (B, K, D)), Weight :: (D, K) (torch (K, D)), Bias ::
+    (D,) or None; σ None or "silu". S′ may be S itself (in place, qwen35.jl:223)."""
+    Y, Sp = _out(outs, "Y"), _out(outs, "Sp")
+    dims = sizes(Y=(Y, "D B"), X=(X, "D B"), S=(S, "D K B"), Sp=(Sp, "D K B"),
+                 Weight=(Weight, "D K"), Bias=(Bias, "D"))
+    D, K, B = dims["D"], dims["K"], dims["B"]
+    for t, n in ((Y, "Y"), (X, "X"), (S, "S"), (Sp, "S′"), (Weight, "Weight"), (Bias, "Bias")):
+        _need(t, torch.bfloat16, n)
+    if S.stride() != Sp.stride():
+        raise ArgumentError("S and S′ must share strides")
+    call("vm_causal_conv1d", _p(Y), _st(Y, 0, D), _p(X), _st(X, 0, D), _p(S), _p(Sp),
+         _st(S, 1, D), _st(S, 0, K * D), _p(Weight), _st(Weight, 0, D), _p(Bias), D, K, B,
+         _act(sigma), _stream())
+    return outs
+
+
+def causal_conv1d(X, S, Weight, Bias=None, *, sigma=None, Sp=None) -> dict:
+    """Allocating causal_conv1d (causal_conv1d.jl:63-66): {"Y", "Sp"}; pass Sp=S for
+    the in-place ring (the reference's output_override, qwen35.jl:222-223)."""
+    Y = torch.empty((X.shape[0], X.shape[-1]), dtype=X.dtype, device=X.device)
+    return causal_conv1d_({"Y": Y, "Sp": torch.empty_like(S) if Sp is None else Sp}, X, S,
+                          Weight, Bias, sigma=sigma)
+
+
+def causal_conv1d_sequence_(outs, X, Weight, Bias=None, *, sigma=None, Sp=None, S=None):
+    """causal_conv1d_sequence!((; Y), X, Weight, Bias; σ, S′) — causal_conv1d.jl:130-149.
+    X, Y :: (D, T, B) (torch (B, T, D), token rows may be strided); Sp :: (D, K, B)
+    receives the ring a decode step continues from. S (not in the reference's
+    signature): a prefix's ring whose columns 2..K are the left context, the
+    suffix prefill of qwen35.jl:333-344 without its copy; None = zeros."""
+    Y = _out(outs, "Y")
+    dims = sizes(Y=(Y, "D T B"), X=(X, "D T B"), Weight=(Weight, "D K"), Bias=(Bias, "D"),
+                 Sp=(Sp, "D K B"), S=(S, "D K B"))
+    D, T, B, K = dims["D"], dims["T"], dims["B"], dims["K"]
+    for t, n in ((Y, "Y"), (X, "X"), (Weight, "Weight"), (Bias, "Bias"), (Sp, "S′"), (S, "S")):
+        _need(t, torch.bfloat16, n)
+    ring = Sp if Sp is not None else S
+    if Sp is not None and S is not None and S.stride() != Sp.stride():
+        raise ArgumentError("S and S′ must share strides")
+    s_cs = _st(ring, 1, D) if ring is not None else D
+    s_sb = _st(ring, 0, K * D) if ring is not None else K * D
+    call("vm_causal_conv1d_sequence", _p(Y), _st(Y, 1, D), _st(Y, 0, T * D), _p(X),
+         _st(X, 1, D), _st(X, 0, T * D), _p(Weight), _st(Weight, 0, D), _p(Bias), _p(S), _p(Sp),
+         s_cs, s_sb, D, K, T, B, _act(sigma), _stream())
+    return outs
+
+
+def causal_conv1d_sequence(X, Weight, Bias=None, **kw) -> dict:
+    """Allocating causal_conv1d_sequence (causal_conv1d.jl:151-154): {"Y"}."""
+    Y = torch.empty(X.shape, dtype=X.dtype, device=X.device)
+    return causal_conv1d_sequence_({"Y": Y}, X, Weight, Bias, **kw)
+
+
+def fused_deltanet_decode_(outs, Q_raw, K_raw, V, Alpha, BetaRaw, Z, A_log, DtBias, NormWeight,
+                           S, *, eps=1e-6):
+    """fused_deltanet_decode!((; O, S′), Q_raw, K_raw, V, Alpha, BetaRaw, Z, A_log,
+    DtBias, NormWeight, S; eps) — src/kernels/deltanet_fused.jl:109-141. Q_raw,
+    K_raw :: (Dk, Hk, B), V, Z, O :: (Dv, Hv, B), Alpha, BetaRaw :: (Hv, B) bf16
+    (torch reversed; the per-sequence dim may be strided, e.g. views of the
+    projection); A_log, DtBias :: (Hv,) fp32; NormWeight :: (Dv,) bf16; S, S′ ::
+    (Dk, Dv, Hv, B) fp32 contiguous (S′ may be S)."""
+    O, Sp = _out(outs, "O"), _out(outs, "Sp")
+    dims = sizes(O=(O, "Dv Hv B"), Q_raw=(Q_raw, "Dk Hk B"), K_raw=(K_raw, "Dk Hk B"),
+                 V=(V, "Dv Hv B"), Alpha=(Alpha, "Hv B"), BetaRaw=(BetaRaw, "Hv B"),
+                 Z=(Z, "Dv Hv B"), A_log=(A_log, "Hv"), DtBias=(DtBias, "Hv"),
+                 NormWeight=(NormWeight, "Dv"), S=(S, "Dk Dv Hv B"), Sp=(Sp, "Dk Dv Hv B"))
+    Dk, Dv, Hk, Hv, B = (dims[n] for n in ("Dk", "Dv", "Hk", "Hv", "B"))
+    if Hv % Hk:
+        raise DimensionMismatch(f"Value heads ({Hv}) is not a multiple of qk heads ({Hk})")
+    for t, n in ((O, "O"), (Q_raw, "Q_raw"), (K_raw, "K_raw"), (V, "V"), (Alpha, "Alpha"),
+                 (BetaRaw, "BetaRaw"), (Z, "Z"), (NormWeight, "NormWeight")):
+        _need(t, torch.bfloat16, n)
+        if t.dim() == 3 and t.stride(1) != t.shape[2]:
+            raise ArgumentError(f"{n}: heads must be contiguous")
+    for t, n in ((A_log, "A_log"), (DtBias, "DtBias"), (S, "S"), (Sp, "S′")):
+        _need(t, torch.float32, n)
+    _need_contig(S, "S")
+    _need_contig(Sp, "S′")
+    call("vm_fused_deltanet_decode", _p(O), _st(O, 0, Hv * Dv), _p(Q_raw), _st(Q_raw, 0, Hk * Dk),
+         _p(K_raw), _st(K_raw, 0, Hk * Dk), _p(V), _st(V, 0, Hv * Dv), _p(Alpha),
+         _st(Alpha, 0, Hv), _p(BetaRaw), _st(BetaRaw, 0, Hv), _p(Z), _st(Z, 0, Hv * Dv),
+         _p(A_log), _p(DtBias), _p(NormWeight), _p(S), _p(Sp), Dk, Dv, Hk, Hv, B, float(eps),
+         _stream())
+    return outs
+
+
+def fused_deltanet_decode(Q_raw, K_raw, V, Alpha, BetaRaw, Z, A_log, DtBias, NormWeight, S, *,
+                          eps=1e-6, Sp=None) -> dict:
+    """Allocating fused_deltanet_decode (deltanet_fused.jl:143-147): {"O", "Sp"}; pass
+    Sp=S for the in-place state (qwen35.jl:227-229)."""
+    O = torch.empty(V.shape, dtype=V.dtype, device=V.device)
+    return fused_deltanet_decode_({"O": O, "Sp": torch.empty_like(S) if Sp is None else Sp},
+                                  Q_raw, K_raw, V, Alpha, BetaRaw, Z, A_log, DtBias, NormWeight,
+                                  S, eps=eps)
+
+
+def _deltanet_fp32(name, outs, Q, K, V, Beta, Gate, S, spec_qk, spec_v, spec_g):
+    O, Sp = _out(outs, "O"), _out(outs, "Sp")
+    dims = sizes(O=(O, spec_v), Q=(Q, spec_qk), K=(K, spec_qk), V=(V, spec_v),
+                 Beta=(Beta, spec_g), Gate=(Gate, spec_g), S=(S, "Dk Dv Hv B"),
+                 Sp=(Sp, "Dk Dv Hv B"))
+    Hk, Hv = dims["Hk"], dims["Hv"]
+    if Hv % Hk:
+        raise DimensionMismatch(f"value heads ({Hv}) is not a multiple of key heads ({Hk})")
+    for t, n in ((O, "O"), (Q, "Q"), (K, "K"), (V, "V"), (Beta, "Beta"), (Gate, "Gate"),
+                 (S, "S"), (Sp, "S′")):
+        _need(t, torch.float32, n)
+        _need_contig(t, n)
+    return O, Sp, dims
+
+
+def deltanet_recurrent_decode_(outs, Q, K, V, Beta, Gate, S):
+    """deltanet_recurrent_decode!((; O, S′), Q, K, V, Beta, Gate, S) —
+    src/kernels/deltanet_recurrent.jl:72-95, fp32: Q, K :: (Dk, Hk, B), V, O ::
+    (Dv, Hv, B), Beta, Gate :: (Hv, B) (decay = exp(Gate)), S, S′ :: (Dk, Dv, Hv, B)."""
+    O, Sp, d = _deltanet_fp32("deltanet_recurrent_decode", outs, Q, K, V, Beta, Gate, S,
+                              "Dk Hk B", "Dv Hv B", "Hv B")
+    call("vm_deltanet_recurrent_decode", _p(O), _p(Q), _p(K), _p(V), _p(Beta), _p(Gate), _p(S),
+         _p(Sp), d["Dk"], d["Dv"], d["Hk"], d["Hv"], d["B"], _stream())
+    return outs
+
+
+def deltanet_recurrent_decode(Q, K, V, Beta, Gate, S, *, Sp=None) -> dict:
+    """Allocating deltanet_recurrent_decode (deltanet_recurrent.jl:97-100)."""
+    O = torch.empty(V.shape, dtype=torch.float32, device=V.device)
+    return deltanet_recurrent_decode_({"O": O, "Sp": torch.empty_like(S) if Sp is None else Sp},
+                                      Q, K, V, Beta, Gate, S)
+
+
+def deltanet_sequence_(outs, Q, K, V, Beta, Gate, S):
+    """deltanet_sequence!((; O, S′), Q, K, V, Beta, Gate, S) — deltanet_recurrent.jl:
+    174-198, fp32: Q, K :: (Dk, T, Hk, B), V, O :: (Dv, T, Hv, B), Beta, Gate ::
+    (Hv, T, B), S, S′ :: (Dk, Dv, Hv, B) (S′ may be S, qwen35.jl:358)."""
+    O, Sp, d = _deltanet_fp32("deltanet_sequence", outs, Q, K, V, Beta, Gate, S,
+                              "Dk T Hk B", "Dv T Hv B", "Hv T B")
+    call("vm_deltanet_sequence", _p(O), _p(Q), _p(K), _p(V), _p(Beta), _p(Gate), _p(S), _p(Sp),
+         d["Dk"], d["Dv"], d["T"], d["Hk"], d["Hv"], d["B"], _stream())
+    return outs
+
+
+def deltanet_sequence(Q, K, V, Beta, Gate, S, *, Sp=None) -> dict:
+    """Allocating deltanet_sequence (deltanet_recurrent.jl:200-203)."""
+    O = torch.empty(V.shape, dtype=torch.float32, device=V.device)
+    return deltanet_sequence_({"O": O, "Sp": torch.empty_like(S) if Sp is None else Sp}, Q, K, V,
+                              Beta, Gate, S)
+
+
+def deltanet_prefill_prep_(outs, CV, AB, A_log, DtBias, *, Dk, Dv, Hk, Hv):
+    """The prefill's inputs to deltanet_sequence! (src/llm/qwen35.jl:347-356): CV ::
+    (2 Hk Dk + Hv Dv, T, B) conv output, AB :: (2 Hv, T, B) (alpha | beta), bf16
+    (torch (B, T, n), token rows may be strided) -> outs "Q", "K" (Dk, T, Hk, B),
+    "V" (Dv, T, Hv, B), "Beta", "Gate" (Hv, T, B), fp32 contiguous."""
+    n = 2 * Hk * Dk + Hv * Dv
+    dims = sizes(CV=(CV, f"{n} T B"), AB=(AB, f"{2 * Hv} T B"), A_log=(A_log, f"{Hv}"),
+                 DtBias=(DtBias, f"{Hv}"), Q=(outs["Q"], f"{Dk} T {Hk} B"),
+                 K=(outs["K"], f"{Dk} T {Hk} B"), V=(outs["V"], f"{Dv} T {Hv} B"),
+                 Beta=(outs["Beta"], f"{Hv} T B"), Gate=(outs["Gate"], f"{Hv} T B"))
+    T, B = dims["T"], dims["B"]
+    _need(CV, torch.bfloat16, "CV")
+    _need(AB, torch.bfloat16, "AB")
+    for n_ in ("Q", "K", "V", "Beta", "Gate"):
+        _need(outs[n_], torch.float32, n_)
+        _need_contig(outs[n_], n_)
+    call("vm_deltanet_prefill_prep", _p(outs["Q"]), _p(outs["K"]), _p(outs["V"]),
+         _p(outs["Beta"]), _p(outs["Gate"]), _p(CV), _st(CV, 1, n), _st(CV, 0, T * n), _p(AB),
+         _st(AB, 1, 2 * Hv), _st(AB, 0, T * 2 * Hv), _p(A_log), _p(DtBias), Dk, Dv, Hk, Hv, T, B,
+         _stream())
+    return outs
+
+
+def gated_rms_norm_(Y, O, Z, NormWeight, *, eps):
+    """The prefill's gated RMSNorm + z gate (src/llm/qwen35.jl:360-364): O ::
+    (Dv, T, Hv, B) fp32, Z :: (Dv, Hv, T, B) bf16 (torch (B, T, Hv, Dv), token and
+    sequence dims may be strided) -> Y :: (Dv, Hv, T, B) bf16 = O rstd NormWeight
+    silu(Z), the out projection's input."""
+    dims = sizes(O=(O, "Dv T Hv B"), Z=(Z, "Dv Hv T B"), Y=(Y, "Dv Hv T B"),
+                 NormWeight=(NormWeight, "Dv"))
+    Dv, Hv, T, B = (dims[n] for n in ("Dv", "Hv", "T", "B"))
+    _need(O, torch.float32, "O")
+    _need_contig(O, "O")
+    for t, n in ((Z, "Z"), (Y, "Y"), (NormWeight, "NormWeight")):
+        _need(t, torch.bfloat16, n)
+        if t.dim() == 4 and t.stride(2) != Dv:
+            raise ArgumentError(f"{n}: heads must be contiguous")
+    call("vm_gated_rms_norm", _p(Y), _st(Y, 1, Hv * Dv), _st(Y, 0, T * Hv * Dv), _p(O), _p(Z),
+         _st(Z, 1, Hv * Dv), _st(Z, 0, T * Hv * Dv), _p(NormWeight), Dv, Hv, T, B, float(eps),
+         _stream())
+    return Y
 
 
 def fill_normal_(X, seed: int, *, scale: float = 1.0, shift: float = 0.0):
