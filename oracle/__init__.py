@@ -270,12 +270,35 @@ def lm_head_argmax(x, W, *, nthreads=0):
     return res, gap
 
 
+def deltanet_decode_layer(xn, l, *, Dk, Dv, Hk, Hv, eps, nthreads=0):
+    """decode!(h, l::DeltaNetLayer, m, gen, xn) (src/llm/qwen35.jl:210-232) for
+    one step: xn [B][Dm] bf16 bits -> (h [B][Dm] fp32, new ring, new state).
+    The reference's bf16 buffers (qz, ab, the conv output, O) are rounded to
+    bf16 (RNE) at those points. l: dict with Wqz, Wab, Wout, conv_w, conv_b (or
+    None), ring [B][K][n], A_log, dt_bias, gnorm_w, S [B][Hv][Dv][Dk]."""
+    B = xn.shape[0]
+    n = 2 * Hk * Dk + Hv * Dv
+    qz = f32_to_bf16(linear(xn, l["Wqz"], nthreads=nthreads))
+    ab = f32_to_bf16(linear(xn, l["Wab"], nthreads=nthreads))
+    y, ring = conv1d_update(qz[:, :n], l["ring"], l["conv_w"], l.get("conv_b"), act=True)
+    y = f32_to_bf16(y)
+    hk = Hk * Dk
+    o, S = fused_deltanet_decode(
+        y[:, :hk].reshape(B, Hk, Dk), y[:, hk:2 * hk].reshape(B, Hk, Dk),
+        y[:, 2 * hk:].reshape(B, Hv, Dv), ab[:, :Hv], ab[:, Hv:], qz[:, n:].reshape(B, Hv, Dv),
+        l["A_log"], l["dt_bias"], l["gnorm_w"], l["S"], eps=eps)
+    h = linear(f32_to_bf16(o).reshape(B, Hv * Dv), l["Wout"], nthreads=nthreads)
+    return h, ring, S
+
+
 def model_step(E, layers, norm_w, head, result, positions, cos_tab, sin_tab, *, Hq, Hk, eps,
-               nthreads=0):
-    """step!(m, gen) (src/llm/qwen35.jl:245-273) for a stack of attention layers,
-    greedy. The reference's step buffers are bf16 (the residual x, xn, h, the
-    MLP's gu and mid, qwen35.jl:235-250): every value is rounded to bf16 (RNE)
-    where the reference stores it, everything else is fp32.
+               nthreads=0, linear_cfg=None):
+    """step!(m, gen) (src/llm/qwen35.jl:245-273) for a stack of attention and
+    DeltaNet layers (dicts with kind "linear_attention", see deltanet_decode_layer;
+    linear_cfg = dict(Dk, Dv, Hk, Hv)), greedy. The reference's step buffers are
+    bf16 (the residual x, xn, h, the MLP's gu and mid, qwen35.jl:235-250): every
+    value is rounded to bf16 (RNE) where the reference stores it, everything
+    else is fp32.
 
     E, head [vocab][Dm]; norm_w [Dm]; layers: dicts with norm1, norm2, Wqkv, Wo,
     qw, kw, kc, vc (caches [B][Hk][ctx][D]), Wgu [2I][Dm], Wd [Dm][I] (bf16 bits);
@@ -285,9 +308,12 @@ def model_step(E, layers, norm_w, head, result, positions, cos_tab, sin_tab, *, 
     x = _c(E[r], np.uint16)
     xn = f32_to_bf16(rms_norm(x, layers[0]["norm1"], eps=eps, offset=1.0))
     for i, l in enumerate(layers):
-        h, _, _ = decode_layer(xn, l["Wqkv"], l["Wo"], l["kc"], l["vc"], positions, l["qw"],
-                               l["kw"], cos_tab, sin_tab, Hq=Hq, Hk=Hk, eps=eps, w_offset=1.0,
-                               nthreads=nthreads)
+        if l.get("kind") == "linear_attention":
+            h, _, _ = deltanet_decode_layer(xn, l, eps=eps, nthreads=nthreads, **linear_cfg)
+        else:
+            h, _, _ = decode_layer(xn, l["Wqkv"], l["Wo"], l["kc"], l["vc"], positions, l["qw"],
+                                   l["kw"], cos_tab, sin_tab, Hq=Hq, Hk=Hk, eps=eps, w_offset=1.0,
+                                   nthreads=nthreads)
         y, xo = rms_norm(x, l["norm2"], eps=eps, offset=1.0, dx=f32_to_bf16(h))
         x, xn = f32_to_bf16(xo), f32_to_bf16(y)
         gu = f32_to_bf16(linear(xn, l["Wgu"], nthreads=nthreads))

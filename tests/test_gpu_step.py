@@ -209,3 +209,153 @@ def test_generate_captured_matches_eager(vm):
     assert eager.shape == (12, cfg.B)
     assert np.array_equal(eager, cap) and np.array_equal(eager, cap2)
     assert gen.positions.cpu().tolist() == [24 + 1 + 12] * cfg.B
+
+
+# ---------------------------------------------------------------- mixed stacks
+def _mixed_cfg(vm, B=3, Ctx=64, tied=False, n_layers=4):
+    """Qwen3.5's layer pattern (every 4th layer full attention) at a small width:
+    hidden 512, DeltaNet Dk = Dv = 128 with Hk = 2, Hv = 4 (1024 conv channels)."""
+    a = vm.AttnConfig(D=512, Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=Ctx,
+                      B=B)
+    return vm.ModelConfig(attn=a, inter=1024, vocab=4099, n_layers=n_layers, tied=tied,
+                          linear=vm.DeltaNetConfig(Dk=128, Dv=128, Hk=2, Hv=4, convK=4),
+                          interval=4)
+
+
+def _host_mixed_layers(vm, m):
+    out = []
+    for l in m.layers:
+        common = dict(norm1=from_dev(l.norm1), norm2=from_dev(l.norm2), Wgu=from_dev(l.Wgu),
+                      Wd=from_dev(l.Wd))
+        if isinstance(l, vm.DeltaNetLayer):
+            common.update(kind="linear_attention", Wqz=from_dev(l.Wqz), Wab=from_dev(l.Wab),
+                          Wout=from_dev(l.Wout), conv_w=from_dev(l.conv_w), conv_b=None,
+                          ring=from_dev(l.conv_state), A_log=l.A_log.cpu().numpy(),
+                          dt_bias=l.dt_bias.cpu().numpy(), gnorm_w=from_dev(l.gnorm_w),
+                          S=l.S.cpu().numpy())
+        else:
+            common.update(Wqkv=from_dev(l.Wqkv), Wo=from_dev(l.Wo), qw=from_dev(l.qw),
+                          kw=from_dev(l.kw), kc=from_dev(l.K_cache), vc=from_dev(l.V_cache))
+        out.append(common)
+    return out
+
+
+def test_decode_step_mixed_vs_oracle(vm, orc):
+    """One step! of 3 DeltaNet layers + 1 attention layer (B = 3) from random
+    states, rings and caches, against the oracle's composition: the final normed
+    hidden state within the bf16 bar, the greedy tokens where margins allow, and
+    each DeltaNet state and ring as the oracle leaves them."""
+    banner("decode step mixed 3 DeltaNet + 1 attention B=3")
+    cfg = _mixed_cfg(vm)
+    m = vm.random_model(cfg, seed=7)
+    assert cfg.layer_types == ("linear_attention",) * 3 + ("full_attention",)
+    for i, l in enumerate(m.layers):
+        if isinstance(l, vm.DeltaNetLayer):
+            l.S.copy_(torch.randn(l.S.shape, generator=torch.Generator().manual_seed(i)) * 0.05)
+            vm.fill_normal_(l.conv_state, 170 + i)
+        else:
+            vm.fill_normal_(l.K_cache, 150 + i)
+            vm.fill_normal_(l.V_cache, 160 + i)
+    gen = vm.Generation(cfg.B, 4)
+    pos = np.array([5, 33, 64], np.int32)
+    tok = np.array([1, 4099, 77], np.int32)
+    gen.positions.copy_(i32(pos))
+    gen.result.copy_(i32(tok))
+    layers = _host_mixed_layers(vm, m)
+    vm.step_(m, gen)
+    torch.cuda.synchronize()
+    c, s = orc.rope_tables(HALF, cfg.attn.Ctx, THETA)
+    lc = cfg.linear
+    res, gap, xn = orc.model_step(from_dev(m.E), layers, from_dev(m.norm_w), from_dev(m.head), tok,
+                                  pos, c, s, Hq=HQ, Hk=HK, eps=EPS,
+                                  linear_cfg=dict(Dk=lc.Dk, Dv=lc.Dv, Hk=lc.Hk, Hv=lc.Hv))
+    mx, mn = maxmean(dev_f32(m.xn), xn)
+    got = gen.result.cpu().numpy()
+    ok = gap > 0.05
+    rel = mn / np.abs(xn).mean()
+    print(f"mixed step: xn max {mx:.3e} mean {mn:.3e} ({rel:.2%}); tokens {got.tolist()} "
+          f"oracle {res.tolist()} margins {np.round(gap, 3).tolist()}")
+    assert mx <= 0.1 and rel <= 1e-2
+    assert ok.sum() >= cfg.B - 1 and np.array_equal(got[ok], res[ok])
+    # the first DeltaNet layer's state and ring after the step, from the same xn
+    l0, h0 = m.layers[0], layers[0]
+    xn0 = orc.f32_to_bf16(orc.rms_norm(from_dev(m.E)[tok - 1], h0["norm1"], eps=EPS, offset=1.0))
+    _, ring1, S1 = orc.deltanet_decode_layer(xn0, h0, eps=EPS, Dk=lc.Dk, Dv=lc.Dv, Hk=lc.Hk,
+                                             Hv=lc.Hv)
+    ring_got = from_dev(l0.conv_state)
+    assert np.array_equal(ring_got[:, :-1], h0["ring"][:, 1:])   # shifted exactly
+    new_col, want = bf16_to_f32(ring_got[:, -1]), bf16_to_f32(ring1[:, -1])
+    assert np.all(np.abs(new_col - want) <= 2.0 ** -7 * np.abs(want) + 1e-6)  # the projection
+    np.testing.assert_allclose(l0.S.cpu().numpy(), S1, rtol=1e-3, atol=1e-4)
+
+
+def test_generate_captured_matches_eager_mixed(vm):
+    """generate_captured! == generate! token for token on the mixed stack, the
+    recurrent state reset before each run (reset!, qwen35.jl:175-185); without
+    the reset the second run continues the first's state and differs."""
+    banner("generate captured vs eager, mixed stack B=3")
+    cfg = _mixed_cfg(vm)
+    m = vm.random_model(cfg, seed=8)
+    ids = torch.as_tensor(np.random.default_rng(9).integers(1, cfg.vocab + 1, size=(cfg.B, 20)),
+                          dtype=torch.int32).cuda()
+    gen = vm.Generation(cfg.B, 16)
+    m.reset_()
+    eager, _ = vm.generate_(m, gen, ids, max_new_tokens=10, poll_every=4)
+    m.reset_()
+    sess = vm.CaptureSession()
+    cap, _ = vm.generate_captured_(m, gen, ids, max_new_tokens=10, warmup=3, session=sess)
+    carried, _ = vm.generate_captured_(m, gen, ids, max_new_tokens=10, warmup=3, session=sess)
+    sess.close()
+    print(f"eager {eager.T.tolist()}\ncaptured {cap.T.tolist()}\ncarried {carried.T.tolist()}")
+    assert np.array_equal(eager, cap)
+    assert not np.array_equal(eager, carried)
+
+
+def test_prefix_prefill_with_restore_matches_full(vm):
+    """prefill!(prefix); snapshot; ...; restore!; prefill!(suffix; offset) leaves
+    the DeltaNet states, rings and next tokens of one whole prefill (the
+    reference's prefix caching, qwen35.jl:397-427 and the suffix conv path,
+    :333-344)."""
+    banner("prefix prefill + restore vs full prefill, mixed stack B=3")
+    cfg = _mixed_cfg(vm)
+    m = vm.random_model(cfg, seed=10)
+    ids = torch.as_tensor(np.random.default_rng(11).integers(1, cfg.vocab + 1, size=(cfg.B, 21)),
+                          dtype=torch.int32).cuda()
+    gen = vm.Generation(cfg.B, 2)
+    m.reset_()
+    vm.prefill_(m, gen, ids)
+    full = [(l.S.clone(), l.conv_state.clone()) for l in m.dn_layers]
+    res_full = gen.result.clone()
+    m.reset_()
+    vm.prefill_(m, gen, ids[:, :13].contiguous())
+    snap = m.snapshot()
+    m.reset_()                      # state lost (another request ran) ...
+    m.restore_(snap)                # ... and restored from the snapshot
+    vm.prefill_(m, gen, ids[:, 13:].contiguous(), offset=13)
+    torch.cuda.synchronize()
+    for (S_f, r_f), l in zip(full, m.dn_layers):
+        scale = float(S_f.abs().max())
+        np.testing.assert_allclose(l.S.cpu().numpy(), S_f.cpu().numpy(), rtol=0.05,
+                                   atol=0.02 * scale)
+        diff = (dev_f32(l.conv_state) - dev_f32(r_f))
+        assert np.abs(diff).max() <= 0.05 * np.abs(dev_f32(r_f)).max()
+    print(f"tokens full {res_full.tolist()} split {gen.result.tolist()}")
+    assert gen.positions.cpu().tolist() == [22] * cfg.B
+
+
+def test_identity_mixed_model_step(vm):
+    """Every projection zero on the mixed stack: the next token is the input."""
+    banner("identity mixed model step")
+    cfg = _mixed_cfg(vm, tied=True)
+    m = vm.random_model(cfg, seed=12)
+    for l in m.layers:
+        ts = (l.Wqz, l.Wab, l.Wout) if isinstance(l, vm.DeltaNetLayer) else (l.Wqkv, l.Wo)
+        for t in ts + (l.Wgu, l.Wd, l.norm1, l.norm2):
+            t.zero_()
+    m.norm_w.zero_()
+    gen = vm.Generation(cfg.B, 2)
+    gen.positions.copy_(i32([3, 4, 5]))
+    tok = [1, 4099, 2]
+    gen.result.copy_(i32(tok))
+    vm.step_(m, gen)
+    assert gen.result.cpu().tolist() == tok

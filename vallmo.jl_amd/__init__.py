@@ -25,6 +25,8 @@ from .layer import (AttnConfig, AttnLayer, AttnModel, CaptureSession, Generation
                     attn_layer, decode_, forward, gated_attn_decode_, gated_attn_prefill)
 from .model import (Model, ModelConfig, generate_, generate_captured_, mlp_,  # noqa: F401
                     prefill_, random_model, step_)
+from .deltanet_layer import (DeltaNetConfig, DeltaNetLayer, DeltaNetSpace,  # noqa: F401
+                             deltanet_layer)
 from . import _lib  # noqa: F401
 
 __version__ = "0.1.0"

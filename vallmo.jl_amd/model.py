@@ -1,20 +1,25 @@
-"""The decode engine around the gated-attention layers — src/llm/qwen35.jl:220-273
-(step!, the MLP), :389-419 (prefill!) and src/llm/generate.jl:54-196 (the clock,
-eager and captured generation).
+"""The decode engine around the decoder layers — src/llm/qwen35.jl:168-185
+(reset!), :220-273 (step!, the MLP), :369-395 (prefill!), :397-427 (snapshot /
+restore!) and src/llm/generate.jl:54-196 (the clock, eager and captured
+generation).
 
-A model here is a stack of decoder layers whose mixer is the gated full-attention
-block (the reference's AttnLayer; its DeltaNet layers are not part of this
-path), each with its two RMSNorms and MLP, between an embedding table and an
-lm head (the embedding itself when tied). Greedy decoding only, as the
-reference's lm_head_argmax!.
+A model here is a stack of decoder layers whose mixer is either the gated
+full-attention block (AttnLayer) or the Gated DeltaNet linear-attention block
+(DeltaNetLayer), in the checkpoint's layer_types order (Qwen3.5: every
+full_attention_interval-th layer is full attention, gguf_llamacpp.jl:47), each
+with its two RMSNorms and MLP, between an embedding table and an lm head (the
+embedding itself when tied). Greedy decoding only, as the reference's
+lm_head_argmax!.
 
 Every temporary of a decode step lives in buffers the model allocates once (the
 reference's Arena frames, qwen35.jl:1-6): the residual stream x, the normed xn,
-the mixer / MLP output h, the MLP's packed gate-up gu and mid, the lm-head
-partials, the projections' workspace. So ``step_`` allocates nothing once warm,
-every step uses the same addresses, and (step_; advance_) captures into a
-hipGraph that replays self-advancing: the decode loop is one graph launch per
-token and nothing else on the host.
+the mixer / MLP output h, the MLP's packed gate-up gu and mid, the DeltaNet
+layers' projections, conv output and gated output, the lm-head partials, the
+projections' workspace. So ``step_`` allocates nothing once warm, every step
+uses the same addresses, and (step_; advance_) captures into a hipGraph that
+replays self-advancing: the decode loop is one graph launch per token and
+nothing else on the host. The DeltaNet state and conv ring advance in place and
+carry across generations until ``reset_`` (qwen35.jl:168-185).
 """
 from __future__ import annotations
 
@@ -23,8 +28,10 @@ from dataclasses import dataclass, field
 
 import torch
 
+from . import deltanet_layer as dn
 from . import ops
 from ._lib import ArgumentError, DimensionMismatch
+from .deltanet_layer import DeltaNetConfig, DeltaNetLayer, DeltaNetSpace
 from .layer import (AttnConfig, AttnLayer, AttnModel, CaptureSession, Generation, attn_layer,
                     decode_, forward)
 
@@ -33,12 +40,17 @@ from .layer import (AttnConfig, AttnLayer, AttnModel, CaptureSession, Generation
 class ModelConfig:
     """The text-config facts the step reads (qwen35.jl:82-96): the attention
     block's (with D the hidden size and B, Ctx the decode batch and capacity),
-    the MLP's intermediate size, the vocabulary, the layer count."""
+    the linear-attention block's, the MLP's intermediate size, the vocabulary,
+    the layer count and pattern: with ``interval`` k > 0, layer i (1-based) is
+    full attention when i % k == 0 and DeltaNet otherwise (Qwen3.5: k = 4,
+    gguf_llamacpp.jl:47-49); k = 0 makes every layer full attention."""
     attn: AttnConfig = field(default_factory=AttnConfig)
     inter: int = 9216
     vocab: int = 151936
     n_layers: int = 8
     tied: bool = True           # tie_word_embeddings: the head IS the embedding
+    linear: DeltaNetConfig = field(default_factory=DeltaNetConfig)
+    interval: int = 0           # full_attention_interval (0: all full attention)
 
     @property
     def D(self) -> int:
@@ -48,11 +60,17 @@ class ModelConfig:
     def B(self) -> int:
         return self.attn.B
 
+    @property
+    def layer_types(self) -> tuple:
+        k = self.interval
+        return tuple("full_attention" if k == 0 or i % k == 0 else "linear_attention"
+                     for i in range(1, self.n_layers + 1))
+
 
 class Model:
-    """Qwen35 (qwen35.jl:46-55) for a stack of attention layers: cfg, the
-    embedding E (D, vocab) (torch (vocab, D)), the head (E itself when tied), the
-    final norm weight, the layers, and the decode space."""
+    """Qwen35 (qwen35.jl:46-55): cfg, the embedding E (D, vocab) (torch (vocab,
+    D)), the head (E itself when tied), the final norm weight, the layers
+    (AttnLayer / DeltaNetLayer), and the decode space."""
 
     def __init__(self, cfg: ModelConfig, layers, E, head, norm_w):
         if len(layers) == 0:
@@ -72,33 +90,90 @@ class Model:
         self.mid = torch.empty((B, I), **bf)
         self.lm_scratch = torch.empty(max(ops.lm_head_argmax_scratch_bytes(self.xn, head), 16),
                                       dtype=torch.uint8, device="cuda")
+        self.dn_layers = [l for l in self.layers if isinstance(l, DeltaNetLayer)]
+        self.dn = DeltaNetSpace(cfg.linear, B) if self.dn_layers else None
+        for l in self.dn_layers:
+            dn.check_layer(l, cfg.linear, D, B)
+        self._ws_need = None
 
     def workspace(self) -> torch.Tensor:
         """The projections' workspace, sized for every decode-step problem (grown
         here, eagerly, so a captured step finds it already large enough)."""
-        l0 = self.layers[0]
-        need = max(ops.linear_workspace_bytes(self.xn, l0.Wgu, self.gu),
-                   ops.linear_workspace_bytes(self.mid, l0.Wd, self.h))
-        return self.attn.linear_workspace(need)
+        if self._ws_need is None:
+            l0 = self.layers[0]
+            need = max(ops.linear_workspace_bytes(self.xn, l0.Wgu, self.gu),
+                       ops.linear_workspace_bytes(self.mid, l0.Wd, self.h))
+            if self.dn_layers:
+                l, c = self.dn_layers[0], self.cfg.linear
+                need = max(need, ops.linear_workspace_bytes(self.xn, l.Wqz, self.dn.qz),
+                           ops.linear_workspace_bytes(self.xn, l.Wab, self.dn.ab),
+                           ops.linear_workspace_bytes(self.dn.O.view(self.cfg.B, -1), l.Wout,
+                                                      self.h))
+            self._ws_need = need
+        return self.attn.linear_workspace(self._ws_need)
+
+    def reset_(self):
+        """reset!(m) — qwen35.jl:167-185: zero every DeltaNet state and conv ring
+        (they carry across generations; the K/V caches need no reset)."""
+        for l in self.dn_layers:
+            l.reset_()
+        return self
+
+    def snapshot(self) -> list:
+        """snapshot(m) — qwen35.jl:399-414: copies of each DeltaNet layer's
+        (S, conv ring), None for attention layers."""
+        return [(l.S.clone(), l.conv_state.clone()) if isinstance(l, DeltaNetLayer) else None
+                for l in self.layers]
+
+    def snapshot_(self, snap: list) -> list:
+        """snapshot!(snap, m) — qwen35.jl:415-420: refresh a snapshot in place."""
+        for s_, l in zip(snap, self.layers):
+            if s_ is not None:
+                s_[0].copy_(l.S)
+                s_[1].copy_(l.conv_state)
+        return snap
+
+    def restore_(self, snap: list):
+        """restore!(m, snap) — qwen35.jl:422-427: put a snapshot's states back
+        (before a suffix prefill with offset)."""
+        for s_, l in zip(snap, self.layers):
+            if s_ is not None:
+                l.S.copy_(s_[0])
+                l.conv_state.copy_(s_[1])
+        return self
 
 
 def random_model(cfg: ModelConfig, *, seed: int = 0) -> Model:
     """A model of `cfg` with seeded synthetic weights on the device (the fill
-    stream the CPU tests reproduce): projections N(0, 1/K), norm weights
-    N(0, 0.05) (applied as w + 1), embedding N(0, 1)."""
-    a, D, I = cfg.attn, cfg.D, cfg.inter
+    stream the CPU tests reproduce), layers in cfg.layer_types order:
+    projections N(0, 1/K), RMSNorm weights N(0, 0.05) (applied as w + 1),
+    embedding N(0, 1); DeltaNet layers: conv weight N(0, 1/K_conv), no conv bias
+    (Qwen3.5's conv1d has none), A_log N(0.5, 0.5), dt_bias N(0, 0.5), gated-norm
+    weight N(1, 0.05), zero state and ring."""
+    a, D, I, c = cfg.attn, cfg.D, cfg.inter, cfg.linear
     S = 2 * a.Hq + 2 * a.Hkv
 
-    def w(shape, s, scale):
+    def w(shape, s, scale, shift=0.0):
         t = torch.empty(shape, dtype=torch.bfloat16, device="cuda")
-        return ops.fill_normal_(t, s, scale=scale)
+        return ops.fill_normal_(t, s, scale=scale, shift=shift)
 
     layers = []
-    for i in range(cfg.n_layers):
+    for i, kind in enumerate(cfg.layer_types):
         s0 = seed * 1000 + 16 * i
-        l = attn_layer(a, w((a.Dh,), s0 + 1, 0.05), w((a.Dh,), s0 + 2, 0.05),
-                       Wqkv=w((S * a.Dh, D), s0 + 3, D ** -0.5),
-                       Wo=w((D, a.Hq * a.Dh), s0 + 4, (a.Hq * a.Dh) ** -0.5))
+        if kind == "full_attention":
+            l = attn_layer(a, w((a.Dh,), s0 + 1, 0.05), w((a.Dh,), s0 + 2, 0.05),
+                           Wqkv=w((S * a.Dh, D), s0 + 3, D ** -0.5),
+                           Wo=w((D, a.Hq * a.Dh), s0 + 4, (a.Hq * a.Dh) ** -0.5))
+        else:
+            HvDv = c.Hv * c.Dv
+            l = dn.deltanet_layer(
+                c, cfg.B, Wqz=w((c.n + HvDv, D), s0 + 9, D ** -0.5),
+                Wab=w((2 * c.Hv, D), s0 + 10, D ** -0.5),
+                Wout=w((D, HvDv), s0 + 11, HvDv ** -0.5),
+                conv_w=w((c.convK, c.n), s0 + 12, c.convK ** -0.5),
+                A_log=w((c.Hv,), s0 + 13, 0.5, 0.5).float(),
+                dt_bias=w((c.Hv,), s0 + 14, 0.5).float(),
+                gnorm_w=w((c.Dv,), s0 + 15, 0.05, 1.0))
         l.norm1 = w((D,), s0 + 5, 0.05)
         l.norm2 = w((D,), s0 + 6, 0.05)
         l.Wgu = w((2 * I, D), s0 + 7, D ** -0.5)
@@ -109,13 +184,23 @@ def random_model(cfg: ModelConfig, *, seed: int = 0) -> Model:
     return Model(cfg, layers, E, head, w((D,), seed * 1000 + 999, 0.05))
 
 
-def _need_layer(l: AttnLayer):
+def _need_layer(l):
+    if isinstance(l, DeltaNetLayer):
+        dn.need(l)
+        return
     for n in ("norm1", "norm2", "Wgu", "Wd", "Wqkv", "Wo"):
         if getattr(l, n) is None:
             raise ArgumentError(f"decoder layer has no {n}")
 
 
-def mlp_(h, l: AttnLayer, m: Model, xn):
+def _mixer_decode(h, l, m: "Model", gen: Generation, xn):
+    if isinstance(l, DeltaNetLayer):
+        dn.decode_(h, l, m.cfg.linear, m.dn, xn, eps=m.cfg.attn.eps, workspace=m.workspace())
+    else:
+        decode_(h, l, m.attn, gen, xn)
+
+
+def mlp_(h, l, m: Model, xn):
     """mlp!(h, mlp, cfg, xn) — qwen35.jl:234-243: gu = linear(xn, Wgu), mid =
     silu(gate) .* up, h = linear(mid, Wd); temporaries in the model's space."""
     ws = m.workspace()
@@ -142,7 +227,7 @@ def step_(m: Model, gen: Generation):
     n = len(m.layers)
     for i, l in enumerate(m.layers):
         _need_layer(l)
-        decode_(h, l, m.attn, gen, xn)
+        _mixer_decode(h, l, m, gen, xn)
         ops.fused_add_rms_norm_({"Y": xn, "Xp": x}, x, h, l.norm2, eps=eps, offset=1.0)
         mlp_(h, l, m, xn)
         next_w = m.norm_w if i == n - 1 else m.layers[i + 1].norm1
@@ -152,7 +237,7 @@ def step_(m: Model, gen: Generation):
 
 
 def prefill_(m: Model, gen: Generation, ids, *, offset: int = 0):
-    """prefill!(m, gen, ids; offset) — qwen35.jl:389-419, eager: ids (T, B)
+    """prefill!(m, gen, ids; offset) — qwen35.jl:369-395, eager: ids (T, B)
     (torch (B, T) int32, 1-based) continue a resident prefix of `offset` tokens;
     fills every layer's cache columns offset+1 .. offset+T, puts the first
     generated token in gen.result and, last, seeds the clock: positions =
@@ -170,9 +255,13 @@ def prefill_(m: Model, gen: Generation, ids, *, offset: int = 0):
     ops.embed_(x.view(B * T, cfg.D), m.E, ids.reshape(-1).contiguous())
     xn = ops.rms_norm(x, m.layers[0].norm1, eps=eps, offset=1.0)["Y"]
     n = len(m.layers)
+    ws_for = lambda x_, W_: m.attn.linear_workspace(ops.linear_workspace_bytes(x_, W_))
     for i, l in enumerate(m.layers):
         _need_layer(l)
-        h = forward(l, m.attn, xn, T, B, offset=offset)
+        if isinstance(l, DeltaNetLayer):
+            h = dn.forward(l, cfg.linear, xn, T, B, eps=eps, offset=offset, workspace_for=ws_for)
+        else:
+            h = forward(l, m.attn, xn, T, B, offset=offset)
         ops.fused_add_rms_norm_({"Y": xn, "Xp": x}, x, h, l.norm2, eps=eps, offset=1.0)
         ws = m.attn.linear_workspace(ops.linear_workspace_bytes(xn, l.Wgu))
         gu = ops.linear(xn, l.Wgu, workspace=ws)["y"]
