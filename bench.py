@@ -16,8 +16,10 @@ in HBM GB/s of K/V actually attended (4096 B per token) + 32 KiB per sequence,
 and config 1 (B=1 at 512 tokens, launch-latency-bound) as time per step.
 Key "prefill_config5": BASELINE config 5 (B=4 ragged chunks after 8-32 K
 priors) in algorithmic TFLOP/s, step and attention kernel. Key "decode_step": the
-whole captured decode step of an 8-layer attention stack with MLPs and the lm
-head (B = 32), and the lm-head GEMV + argmax alone. Key "layer": whole
+whole captured decode step of a Qwen3.5-4B-shaped model (24 Gated DeltaNet + 8
+gated-attention layers, MLPs, lm head; B = 32), and the lm-head GEMV + argmax
+alone. Key "deltanet": the DeltaNet layer kernels alone (fused decode step and
+conv step against the HBM roofline, the prefill recurrence in tokens/s). Key "layer": whole
 attention layers, hidden state to hidden state (the qkv and Wo projections on
 hipBLASLt around the block) at the config-2 prefill and config-3 decode shapes.
 
@@ -395,6 +397,33 @@ def _event_ms(torch, fn, reps):
     return a.elapsed_time(b) / reps
 
 
+def _graph_ms(torch, fn, n=20, reps=5):
+    """Median ms of one fn() call: n calls captured in a graph on a side stream,
+    replayed reps times (kernel time without the host's per-call dispatch)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=side):
+            for _ in range(n):
+                fn()
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ts = []
+    for _ in range(reps):
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b) / n)
+    del g
+    return float(np.median(ts))
+
+
 def bench_layer(vm, torch, reps=20):
     """Whole attention layers, hidden state to hidden state (qkv projection,
     gated attention, Wo projection): the config-2 prefill layer (T = 4096) and the
@@ -461,8 +490,10 @@ def bench_layer(vm, torch, reps=20):
     t_step = _event_ms(torch, step, reps)
     qkv_d, O_d = m.decode_buffers()
     ws = m.linear_workspace()
-    t_gv1 = _event_ms(torch, lambda: vm.linear_({"y": qkv_d.view(B, -1)}, xd, Wqkv, workspace=ws), reps)
-    t_gv2 = _event_ms(torch, lambda: vm.linear_({"y": hd}, O_d.view(B, -1), Wo, workspace=ws), reps)
+    # the GEMVs alone, timed from graph replays (a host loop of these ~10 us
+    # launches measures Python's dispatch, not the kernels)
+    t_gv1 = _graph_ms(torch, lambda: vm.linear_({"y": qkv_d.view(B, -1)}, xd, Wqkv, workspace=ws))
+    t_gv2 = _graph_ms(torch, lambda: vm.linear_({"y": hd}, O_d.view(B, -1), Wo, workspace=ws))
     b_qkv = 2.0 * (S_ * D * DM + B * DM + B * S_ * D)
     b_wo = 2.0 * (DM * HQ * D + B * HQ * D + B * DM)
     res["decode_config3"] = {
@@ -477,18 +508,22 @@ def bench_layer(vm, torch, reps=20):
     return res
 
 
-def bench_step(vm, torch, replays=60, seed=9):
-    """The whole decode step (§ row: step!, qwen35.jl:245-273) of a stack of 8
-    attention layers at hidden 2560 (MLP 9216, vocab 151936 as a stand-in),
-    B = 32 at ragged attended lengths ~U{1024..8128}: (step!; advance!) captured
-    once and replayed on a dedicated stream. HBM bytes per step: every weight
-    (projections, MLPs, norms, head) once, the attended K/V, the caches'
-    appended rows. Also the lm head alone (GEMV + argmax) at B = 1 and 32."""
-    B, Ctx, L = 32, 8192, 8
+def bench_step(vm, torch, replays=40, seed=9):
+    """The whole decode step (step!, qwen35.jl:245-273) of a Qwen3.5-4B-shaped
+    model: 32 layers in its pattern (every 4th gated full attention, the rest
+    Gated DeltaNet: Dk = Dv = 128, 16 qk / 32 value heads, conv 4), hidden 2560,
+    MLP 9216, vocab 151936 (tied head), random weights; B = 32 with the attention
+    layers at ragged attended lengths ~U{1024..8128}: (step!; advance!) captured
+    once and replayed on a dedicated stream. HBM bytes per step: every weight once
+    (projections, MLPs, conv, head), the attended K/V, the DeltaNet states read
+    and written (fp32) and their conv rings. Also the lm head alone (GEMV +
+    argmax) at B = 1 and 32."""
+    B, Ctx, L = 32, 8192, 32
     a = vm.AttnConfig(D=DM, Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=Ctx, B=B)
-    cfg = vm.ModelConfig(attn=a, inter=9216, vocab=151936, n_layers=L, tied=True)
+    cfg = vm.ModelConfig(attn=a, inter=9216, vocab=151936, n_layers=L, tied=True, interval=4)
     m = vm.random_model(cfg, seed=seed)
-    for i, l in enumerate(m.layers):
+    attn = [l for l in m.layers if not isinstance(l, vm.DeltaNetLayer)]
+    for i, l in enumerate(attn):
         vm.fill_normal_(l.K_cache, 9000 + i)
         vm.fill_normal_(l.V_cache, 9100 + i)
     rng = np.random.default_rng(seed)
@@ -515,20 +550,27 @@ def bench_step(vm, torch, replays=60, seed=9):
     sess.close()
     ms = e0.elapsed_time(e1) / replays
     p_start = p_start.cpu().numpy().astype(np.float64)
-    kv = float(np.sum(p_start + (replays - 1) / 2.0)) * HK * D * 2 * 2 * L  # attended K + V
-    w_layer = sum(t.numel() * 2 for t in (m.layers[0].Wqkv, m.layers[0].Wo, m.layers[0].Wgu,
-                                          m.layers[0].Wd))
-    w_bytes = float(L * w_layer + m.head.numel() * 2)
-    nbytes = w_bytes + kv
+    La = len(attn)
+    kv = float(np.sum(p_start + (replays - 1) / 2.0)) * HK * D * 2 * 2 * La  # attended K + V
+    w_bytes = float(m.head.numel() * 2)
+    for l in m.layers:
+        ts = ((l.Wqz, l.Wab, l.Wout, l.conv_w) if isinstance(l, vm.DeltaNetLayer)
+              else (l.Wqkv, l.Wo))
+        w_bytes += sum(t.numel() * 2 for t in ts + (l.Wgu, l.Wd))
+    dn_state = float(sum(2 * l.S.numel() * 4 + 2 * l.conv_state.numel() * 2
+                         for l in m.dn_layers))
+    nbytes = w_bytes + kv + dn_state
     res = {
-        "config": f"{L} gated-attention layers + MLPs, hidden {DM}, MLP {cfg.inter}, vocab "
-                  f"{cfg.vocab} (tied head), B={B}, attended lengths U{{1024..8128}} (seed {seed}), "
-                  f"(step!; advance!) captured, {replays} replays on a dedicated stream",
+        "config": f"Qwen3.5-4B shape: {L} layers ({L - La} Gated DeltaNet + {La} gated attention, "
+                  f"full_attention_interval 4), hidden {DM}, MLP {cfg.inter}, vocab {cfg.vocab} "
+                  f"(tied head), random weights, B={B}, attended lengths U{{1024..8128}} (seed "
+                  f"{seed}), (step!; advance!) captured, {replays} replays on a dedicated stream",
         "ms_per_step": ms,
         "tokens_per_s": B / (ms * 1e-3),
         "bytes_per_step": nbytes,
         "weight_bytes": w_bytes,
         "kv_bytes": kv,
+        "deltanet_state_bytes": dn_state,
         "gbs": nbytes / (ms * 1e-3) / 1e9,
         "frac_of_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
     }
@@ -554,6 +596,97 @@ def bench_step(vm, torch, replays=60, seed=9):
                                 "frac_of_hbm_peak": hb / (t / n * 1e-3) / 1e9 / PEAK_HBM_GBS}
     del m
     torch.cuda.empty_cache()
+    return res
+
+
+def _profiled_us(vm, torch, kernel, fn, n=20):
+    """Mean us per launch of one kernel class (events around its launches)."""
+    lib = vm._lib
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    lib.profile_select(kernel)
+    lib.profile_enable(True)
+    for _ in range(n):
+        fn()
+    torch.cuda.synchronize()
+    cnt, t = lib.profile_read(kernel)
+    lib.profile_enable(False)
+    lib.profile_select()
+    return 1e3 * t / cnt
+
+
+def bench_deltanet(vm, torch, seed=11):
+    """The Gated DeltaNet layer kernels alone at the Qwen3.5-4B shape (Dk = Dv =
+    128, Hk = 16, Hv = 32, 8192 conv channels, conv 4), against the HBM roofline:
+    the fused decode step (its bytes: the fp32 state read and written, q / k / v /
+    z / gates read, O written) at B = 1 and 32; the decode conv step at B = 32
+    (ring read and written, input, weight, output); the prefill's recurrence
+    (deltanet_sequence!) over T = 4096 at B = 1 (latency-bound: reported as
+    tokens/s), with its prep, conv and gated-norm kernels."""
+    Dk = Dv = 128
+    Hk, Hv, K = 16, 32, 4
+    n = 2 * Hk * Dk + Hv * Dv
+    res = {}
+    f32 = dict(dtype=torch.float32, device="cuda")
+    for B in (1, 32):
+        qz = _dev_normal(vm, torch, (B, n + Hv * Dv), seed + B)
+        ab = _dev_normal(vm, torch, (B, 2 * Hv), seed + 100 + B)
+        S = torch.randn((B, Hv, Dv, Dk), **f32) * 0.05
+        a_log = torch.randn((Hv,), **f32) * 0.5
+        dt = torch.randn((Hv,), **f32) * 0.5
+        gw = _dev_normal(vm, torch, (Dv,), seed + 7)
+        O = torch.empty((B, Hv, Dv), dtype=torch.bfloat16, device="cuda")
+        hk = Hk * Dk
+        q = qz[:, :hk].unflatten(-1, (Hk, Dk))
+        k = qz[:, hk:2 * hk].unflatten(-1, (Hk, Dk))
+        v = qz[:, 2 * hk:n].unflatten(-1, (Hv, Dv))
+        z = qz[:, n:].unflatten(-1, (Hv, Dv))
+        fn = lambda: vm.fused_deltanet_decode_({"O": O, "Sp": S}, q, k, v, ab[:, :Hv],
+                                               ab[:, Hv:], z, a_log, dt, gw, S, eps=EPS)
+        us = _profiled_us(vm, torch, vm._lib.VM_K_DELTANET, fn)
+        nbytes = B * Hv * (2.0 * Dk * Dv * 4 + 3 * Dv * 2 + 4) + B * 2 * hk * 2
+        res[f"fused_decode_B{B}"] = {"us": us, "bytes": nbytes,
+                                     "gbs": nbytes / (us * 1e-6) / 1e9,
+                                     "frac_of_hbm_peak": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS}
+    B = 32
+    x = _dev_normal(vm, torch, (B, n), seed + 200)
+    ring = _dev_normal(vm, torch, (B, K, n), seed + 201)
+    w = _dev_normal(vm, torch, (K, n), seed + 202, scale=0.5)
+    y = torch.empty((B, n), dtype=torch.bfloat16, device="cuda")
+    us = _profiled_us(vm, torch, vm._lib.VM_K_CONV,
+                      lambda: vm.causal_conv1d_({"Y": y, "Sp": ring}, x, ring, w, None,
+                                                sigma="silu"))
+    nbytes = 2.0 * (B * n * (1 + (K - 1) + K + 1) + K * n)
+    res["conv_decode_B32"] = {"us": us, "bytes": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9,
+                              "frac_of_hbm_peak": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS}
+    # prefill pieces, B = 1, T = 4096
+    B, T = 1, 4096
+    X = _dev_normal(vm, torch, (B, T, n), seed + 300)
+    Y = torch.empty_like(X)
+    Sp = torch.zeros((B, K, n), dtype=torch.bfloat16, device="cuda")
+    us_conv = _profiled_us(vm, torch, vm._lib.VM_K_CONV,
+                           lambda: vm.causal_conv1d_sequence_({"Y": Y}, X, w, None, sigma="silu",
+                                                              Sp=Sp), n=5)
+    ab = _dev_normal(vm, torch, (B, T, 2 * Hv), seed + 301)
+    p = {"Q": torch.empty((B, Hk, T, Dk), **f32), "K": torch.empty((B, Hk, T, Dk), **f32),
+         "V": torch.empty((B, Hv, T, Dv), **f32), "Beta": torch.empty((B, T, Hv), **f32),
+         "Gate": torch.empty((B, T, Hv), **f32)}
+    a_log = torch.randn((Hv,), **f32) * 0.5
+    dt = torch.randn((Hv,), **f32) * 0.5
+    vm.deltanet_prefill_prep_(p, Y, ab, a_log, dt, Dk=Dk, Dv=Dv, Hk=Hk, Hv=Hv)
+    S = torch.zeros((B, Hv, Dv, Dk), **f32)
+    o = torch.empty((B, Hv, T, Dv), **f32)
+    us_seq = _profiled_us(vm, torch, vm._lib.VM_K_DELTANET,
+                          lambda: vm.deltanet_sequence_({"O": o, "Sp": S}, p["Q"], p["K"], p["V"],
+                                                        p["Beta"], p["Gate"], S), n=3)
+    res["prefill_B1_T4096"] = {
+        "conv_sequence_us": us_conv,
+        "conv_sequence_gbs": 2.0 * (2 * T * n + K * n) / (us_conv * 1e-6) / 1e9,
+        "sequence_ms": us_seq * 1e-3,
+        "sequence_tokens_per_s": T / (us_seq * 1e-6),
+        "sequence_us_per_token": us_seq / T,
+    }
     return res
 
 
@@ -728,6 +861,7 @@ def main():
     ap.add_argument("--no-config5", action="store_true", help="skip the config-5 prefill leg")
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer leg")
     ap.add_argument("--no-step", action="store_true", help="skip the whole-decode-step leg")
+    ap.add_argument("--no-deltanet", action="store_true", help="skip the DeltaNet kernel leg")
     ap.add_argument("--no-settle", action="store_true",
                     help="skip the clock-settle phase (counter-collection runs)")
     ap.add_argument("--no-decode", action="store_true")
@@ -793,9 +927,19 @@ def main():
             f"TFLOP/s, Wo GEMM {lp['wo_gemm_tflops']:.0f} TFLOP/s")
         log(f"[bench] decode layer B=32: {ld['ms_per_layer_step']:.3f} ms, qkv GEMV "
             f"{ld['qkv_gemv_gbs']:.0f} GB/s, Wo GEMV {ld['wo_gemv_gbs']:.0f} GB/s")
+    dnet = None
+    if not args.no_deltanet:
+        log("[bench] Gated DeltaNet kernels (Qwen3.5-4B shape)")
+        dnet = bench_deltanet(vm, torch)
+        f1, f32_, cv = dnet["fused_decode_B1"], dnet["fused_decode_B32"], dnet["conv_decode_B32"]
+        pp = dnet["prefill_B1_T4096"]
+        log(f"[bench] deltanet: fused decode B=1 {f1['us']:.1f} us, B=32 {f32_['us']:.1f} us = "
+            f"{f32_['gbs']:.0f} GB/s; conv decode B=32 {cv['us']:.1f} us = {cv['gbs']:.0f} GB/s; "
+            f"prefill T=4096: conv {pp['conv_sequence_us']:.1f} us, recurrence "
+            f"{pp['sequence_ms']:.2f} ms ({pp['sequence_us_per_token']:.2f} us/token)")
     step = None
     if not args.no_step:
-        log("[bench] whole decode step, 8 attention layers + MLPs + lm head, B=32")
+        log("[bench] whole decode step, Qwen3.5-4B shape (24 DeltaNet + 8 attention), B=32")
         step = bench_step(vm, torch)
         log(f"[bench] step: {step['ms_per_step']:.3f} ms/step, {step['tokens_per_s']:.0f} tok/s, "
             f"{step['gbs']:.0f} GB/s; lm head alone B=1 {step['lm_head_B1']['gbs']:.0f} GB/s, "
@@ -809,7 +953,8 @@ def main():
             log(f"[bench] cpu {k}: {fig} ({v['sample']}, {v['runs']} runs)")
 
     if pf is None:
-        print(json.dumps({"decode": decode, "cpu_baseline": cpu}), flush=True)
+        print(json.dumps({"decode": decode, "layer": layer, "decode_step": step, "deltanet": dnet,
+                          "cpu_baseline": cpu}), flush=True)
         return
     achieved = pf["flops"] / (pf["attn_kernel_ms"] * 1e-3) / 1e12
     line = {
@@ -840,6 +985,7 @@ def main():
         "decode": decode,
         "layer": layer,
         "decode_step": step,
+        "deltanet": dnet,
     }
     print(json.dumps(line), flush=True)
 
