@@ -554,7 +554,7 @@ def bench_step(vm, torch, replays=40, seed=9):
     kv = float(np.sum(p_start + (replays - 1) / 2.0)) * HK * D * 2 * 2 * La  # attended K + V
     w_bytes = float(m.head.numel() * 2)
     for l in m.layers:
-        ts = ((l.Wqz, l.Wab, l.Wout, l.conv_w) if isinstance(l, vm.DeltaNetLayer)
+        ts = ((l.W_in, l.Wout, l.conv_w) if isinstance(l, vm.DeltaNetLayer)
               else (l.Wqkv, l.Wo))
         w_bytes += sum(t.numel() * 2 for t in ts + (l.Wgu, l.Wd))
     dn_state = float(sum(2 * l.S.numel() * 4 + 2 * l.conv_state.numel() * 2

@@ -259,7 +259,8 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb,
  * reference: x :: (K, N) with column stride ldx >= K, W :: (K, M) (K-major,
  * the checkpoint's orientation) with column stride ldw >= K, y :: (M, N) with
  * column stride ldy >= M; all bf16, fp32 accumulation (linear.jl:29). Narrow
- * problems (N <= 16, K % 64 == 0, M % 4 == 0, 16-byte aligned W and x columns)
+ * problems (N <= 16, or N <= 32 with M <= 4096; K % 64 == 0, M % 4 == 0,
+ * 16-byte aligned W and x columns)
  * run on the library's split-K MFMA GEMV, whose K slices add in a fixed order
  * (bitwise reproducible); the rest on hipBLASLt. A plan per
  * problem (hipBLASLt) is built on the first call and cached (linear.jl:17-38);

@@ -38,7 +38,7 @@ def test_linear_operator(vm, orc, M, N, K):
 
 NARROW = [(S * D, 1, DM), (S * D, 16, DM), (DM, 16, HQ * D), (DM, 1, HQ * D),
           (2 * 9216, 16, DM), (DM, 16, 9216), (100, 7, 64), (4, 1, 64), (36, 16, 640),
-          (2 * 9216, 3, DM)]
+          (2 * 9216, 3, DM), (DM, 32, HQ * D), (DM, 32, 9216), (4096, 25, 1024)]
 
 
 def _narrow_bar(x, W, ref):
@@ -53,7 +53,7 @@ def _narrow_bar(x, W, ref):
 
 @pytest.mark.parametrize("M,N,K", NARROW)
 def test_linear_narrow(vm, orc, M, N, K):
-    """The decode projections (N <= 16 columns) run on the library's split-K
+    """The decode projections (N <= 16, or N <= 32 with M <= 4096) run on the library's split-K
     MFMA kernel: every element within one bf16 ulp (plus fp32 reassociation)
     of the fp32 oracle, the result bitwise the same on a second call (the
     slices add in a fixed order), and strided x / y columns honoured."""

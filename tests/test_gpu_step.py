@@ -349,7 +349,7 @@ def test_identity_mixed_model_step(vm):
     cfg = _mixed_cfg(vm, tied=True)
     m = vm.random_model(cfg, seed=12)
     for l in m.layers:
-        ts = (l.Wqz, l.Wab, l.Wout) if isinstance(l, vm.DeltaNetLayer) else (l.Wqkv, l.Wo)
+        ts = (l.W_in, l.Wout) if isinstance(l, vm.DeltaNetLayer) else (l.Wqkv, l.Wo)
         for t in ts + (l.Wgu, l.Wd, l.norm1, l.norm2):
             t.zero_()
     m.norm_w.zero_()

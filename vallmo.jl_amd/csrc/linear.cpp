@@ -131,16 +131,18 @@ int get_plan(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, const P
   return VM_OK;
 }
 
-// Narrow problems (N <= 16 columns: the decode step's projections at small
-// batch) run on the library's own split-K MFMA kernel (launch_gemv). Measured
-// under graph replay on MI355X it streams the MLP's 18432 x 2560 gate-up
-// weight in half the time of the GEMM library's pick (21 vs 41 us at N = 1..16)
-// and matches it within ~8% on the other decode shapes; from N = 32 the
-// library's kernels are faster (12.1 vs 15.3 us for 10240 x 2560). Its loads
-// need 16-byte aligned columns of W and x and 8-byte aligned columns of y.
-constexpr int GEMV_MAX_N = 16;
+// Narrow problems run on the library's own split-K MFMA kernel (launch_gemv):
+// every N <= 16, and N <= 32 when M <= 4096 (the short, deep out projections
+// and the MLP's down projection). Measured under graph replay on MI355X with
+// the weights cold (rotating copies larger than the 256 MB last-level cache),
+// against the GEMM library's pick: N = 1..16 faster on every decode shape
+// (18432 x 2560 gate-up: 25 vs 56 us), at N = 32 faster for 2560 x 4096 (11.1
+// vs 12.4 us) and 2560 x 9216 (15.6 vs 20.5 us) and 3-6% slower for the
+// wide 10-18K-row projections, which stay on the library. Its loads need
+// 16-byte aligned columns of W and x and 8-byte aligned columns of y.
 bool gemv_shape(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy) {
-  return N <= GEMV_MAX_N && K % 64 == 0 && M % 4 == 0 && ldw % 8 == 0 && ldx % 8 == 0 && ldy % 4 == 0;
+  const bool narrow = N <= 16 || (N <= 32 && M <= 4096);
+  return narrow && K % 64 == 0 && M % 4 == 0 && ldw % 8 == 0 && ldx % 8 == 0 && ldy % 4 == 0;
 }
 bool gemv_aligned(const void* y, const void* x, const void* w) {
   return ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0) && ((uintptr_t)y % 8 == 0);

@@ -380,8 +380,7 @@ void lm_head_split_kernel(LmHeadArgs a) {
   }
 }
 
-// ---- y = W^T x for a narrow x (N <= 32 columns; the library routes N <= 16
-// here): the decode step's projections (linear!, src/linear.jl:40-57, at N = B). HBM-bound like the lm
+// ---- y = W^T x for a narrow x (N <= 32 columns; linear.cpp picks which): the decode step's projections (linear!, src/linear.jl:40-57, at N = B). HBM-bound like the lm
 // head and built the same way: one 32-column batch tile, 32-row weight tiles
 // staged through LDS by 1-KB direct loads, bf16 MFMAs, fp32 sums. Workgroup
 // (tile group tg, K slice s2) takes T tiles; its four waves split the slice's

@@ -49,9 +49,16 @@ class DeltaNetLayer:
     conv weight (D, K) (torch (K, n)), bias or None, the ring (n, K, B) (torch
     (B, K, n)) bf16, A_log and dt_bias (Hv,) fp32, the gated-norm weight (Dv,),
     the state S (Dk, Dv, Hv, B) fp32 (torch (B, Hv, Dv, Dk)), and the decoder
-    parts around the mixer (the two RMSNorms and the MLP)."""
-    Wqz: torch.Tensor           # (D, n + Dv Hv) -> torch (n + Dv Hv, D)
-    Wab: torch.Tensor           # (D, 2 Hv) -> torch (2 Hv, D)
+    parts around the mixer (the two RMSNorms and the MLP).
+
+    The reference runs [qkv | z] and [a | b] as two GEMVs because 12352 rows do
+    not divide by Dk for its tiles (qwen35.jl:152-154); the narrow GEMV here
+    needs only M % 4 == 0, so the layer stores them as one (n + Dv Hv + 2 Hv)-row
+    projection W_in and keeps Wqz and Wab as its row blocks: one launch per
+    token instead of two (the 64-row one alone cost a whole launch)."""
+    W_in: torch.Tensor          # (D, n + Dv Hv + 2 Hv): [Wqz | Wab] in one projection
+    Wqz: torch.Tensor           # (D, n + Dv Hv) -> torch (n + Dv Hv, D), a view of W_in
+    Wab: torch.Tensor           # (D, 2 Hv) -> torch (2 Hv, D), a view of W_in
     Wout: torch.Tensor          # (Dv Hv, D) -> torch (D, Dv Hv)
     conv_w: torch.Tensor        # (n, K) -> torch (K, n)
     conv_b: torch.Tensor | None
@@ -76,8 +83,13 @@ def deltanet_layer(c: DeltaNetConfig, B: int, *, Wqz, Wab, Wout, conv_w, A_log, 
                    conv_b=None) -> DeltaNetLayer:
     """Allocate a layer with zeroed state (qwen35.jl:159-162)."""
     dev = Wqz.device
+    if Wqz.shape[-1] != Wab.shape[-1]:
+        raise DimensionMismatch(f"Wqz and Wab have different input widths "
+                                f"({Wqz.shape[-1]}, {Wab.shape[-1]})")
+    W_in = torch.cat([Wqz, Wab], 0)
+    m = Wqz.shape[0]
     return DeltaNetLayer(
-        Wqz=Wqz, Wab=Wab, Wout=Wout, conv_w=conv_w, conv_b=conv_b,
+        W_in=W_in, Wqz=W_in[:m], Wab=W_in[m:], Wout=Wout, conv_w=conv_w, conv_b=conv_b,
         conv_state=torch.zeros((B, c.convK, c.n), dtype=torch.bfloat16, device=dev),
         A_log=A_log, dt_bias=dt_bias, gnorm_w=gnorm_w,
         S=torch.zeros((B, c.Hv, c.Dv, c.Dk), dtype=torch.float32, device=dev))
@@ -89,15 +101,17 @@ class DeltaNetSpace:
 
     def __init__(self, c: DeltaNetConfig, B: int, device="cuda"):
         bf = dict(dtype=torch.bfloat16, device=device)
-        self.qz = torch.empty((B, c.n + c.Dv * c.Hv), **bf)
-        self.ab = torch.empty((B, 2 * c.Hv), **bf)
+        m = c.n + c.Dv * c.Hv
+        self.qzab = torch.empty((B, m + 2 * c.Hv), **bf)   # W_in's output
+        self.qz, self.ab = self.qzab[:, :m], self.qzab[:, m:]
         self.conv = torch.empty((B, c.n), **bf)
         self.O = torch.empty((B, c.Hv, c.Dv), **bf)
 
 
 def check_layer(l: DeltaNetLayer, c: DeltaNetConfig, D: int, B: int):
     n, HvDv = c.n, c.Hv * c.Dv
-    sizes(Wqz=(l.Wqz, f"{D} {n + HvDv}"), Wab=(l.Wab, f"{D} {2 * c.Hv}"),
+    sizes(W_in=(l.W_in, f"{D} {n + HvDv + 2 * c.Hv}"), Wqz=(l.Wqz, f"{D} {n + HvDv}"),
+          Wab=(l.Wab, f"{D} {2 * c.Hv}"),
           Wout=(l.Wout, f"{HvDv} {D}"), conv_w=(l.conv_w, f"{n} {c.convK}"),
           conv_state=(l.conv_state, f"{n} {c.convK} {B}"), A_log=(l.A_log, f"{c.Hv}"),
           dt_bias=(l.dt_bias, f"{c.Hv}"), gnorm_w=(l.gnorm_w, f"{c.Dv}"),
@@ -126,8 +140,7 @@ def decode_(h, l: DeltaNetLayer, c: DeltaNetConfig, space: DeltaNetSpace, xn, *,
     B = xn.shape[0]
     if space.qz.shape[0] != B:
         raise DimensionMismatch(f"size(xn, 2) = {B} does not match the decode space's B")
-    ops.linear_({"y": space.qz}, xn, l.Wqz, workspace=workspace)
-    ops.linear_({"y": space.ab}, xn, l.Wab, workspace=workspace)
+    ops.linear_({"y": space.qzab}, xn, l.W_in, workspace=workspace)  # [qz | ab], :212-213
     conv_in, z = _views(space.qz, c)
     ops.causal_conv1d_({"Y": space.conv, "Sp": l.conv_state}, conv_in, l.conv_state, l.conv_w,
                        l.conv_b, sigma="silu")
@@ -150,8 +163,9 @@ def forward(l: DeltaNetLayer, c: DeltaNetConfig, xn, T: int, B: int, *, eps: flo
     ``workspace_for(x, W)`` returns a projection workspace for that problem."""
     D = xn.shape[-1]
     xn2 = xn.reshape(B * T, D)
-    qz = ops.linear(xn2, l.Wqz, workspace=workspace_for(xn2, l.Wqz))["y"].view(B, T, -1)
-    ab = ops.linear(xn2, l.Wab, workspace=workspace_for(xn2, l.Wab))["y"].view(B, T, -1)
+    m = c.n + c.Dv * c.Hv
+    qzab = ops.linear(xn2, l.W_in, workspace=workspace_for(xn2, l.W_in))["y"].view(B, T, -1)
+    qz, ab = qzab[..., :m], qzab[..., m:]                               # :322-323
     X, z = _views(qz, c)
     conv = torch.empty((B, T, c.n), dtype=torch.bfloat16, device=xn.device)
     ops.causal_conv1d_sequence_({"Y": conv}, X, l.conv_w, l.conv_b, sigma="silu",

@@ -105,8 +105,7 @@ class Model:
                        ops.linear_workspace_bytes(self.mid, l0.Wd, self.h))
             if self.dn_layers:
                 l, c = self.dn_layers[0], self.cfg.linear
-                need = max(need, ops.linear_workspace_bytes(self.xn, l.Wqz, self.dn.qz),
-                           ops.linear_workspace_bytes(self.xn, l.Wab, self.dn.ab),
+                need = max(need, ops.linear_workspace_bytes(self.xn, l.W_in, self.dn.qzab),
                            ops.linear_workspace_bytes(self.dn.O.view(self.cfg.B, -1), l.Wout,
                                                       self.h))
             self._ws_need = need
