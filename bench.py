@@ -424,6 +424,17 @@ def _graph_ms(torch, fn, n=20, reps=5):
     return float(np.median(ts))
 
 
+def _cold_gemv_ms(vm, torch, W, x, y, ws, total_bytes=1.2e9):
+    """ms per y = W^T x with W streamed from HBM: the graph rotates over copies
+    of W (total > the last-level cache), one call per copy."""
+    nc = max(2, int(total_bytes // (W.numel() * 2)) + 1)
+    Ws = [W.clone() for _ in range(nc)]
+    calls = [(lambda Wc=Wc: vm.linear_({"y": y}, x, Wc, workspace=ws)) for Wc in Ws]
+    t = _graph_ms(torch, lambda: [f() for f in calls], n=1) / nc
+    del Ws
+    return t
+
+
 def bench_layer(vm, torch, reps=20):
     """Whole attention layers, hidden state to hidden state (qkv projection,
     gated attention, Wo projection): the config-2 prefill layer (T = 4096) and the
@@ -491,9 +502,11 @@ def bench_layer(vm, torch, reps=20):
     qkv_d, O_d = m.decode_buffers()
     ws = m.linear_workspace()
     # the GEMVs alone, timed from graph replays (a host loop of these ~10 us
-    # launches measures Python's dispatch, not the kernels)
-    t_gv1 = _graph_ms(torch, lambda: vm.linear_({"y": qkv_d.view(B, -1)}, xd, Wqkv, workspace=ws))
-    t_gv2 = _graph_ms(torch, lambda: vm.linear_({"y": hd}, O_d.view(B, -1), Wo, workspace=ws))
+    # launches measures Python's dispatch, not the kernels) that rotate over
+    # copies of the weight totalling > 1 GB, so each call streams it from HBM as
+    # in a decode step (one copy re-read would sit in the 256 MB last-level cache)
+    t_gv1 = _cold_gemv_ms(vm, torch, Wqkv, xd, qkv_d.view(B, -1), ws)
+    t_gv2 = _cold_gemv_ms(vm, torch, Wo, O_d.view(B, -1), hd, ws)
     b_qkv = 2.0 * (S_ * D * DM + B * DM + B * S_ * D)
     b_wo = 2.0 * (DM * HQ * D + B * HQ * D + B * DM)
     res["decode_config3"] = {
@@ -841,6 +854,41 @@ def cpu_baseline(vm, torch):
     res["layer_wo_gemm"] = {"tflops": fl / dt / 1e12, "s_per_step": dt, "runs": n,
                             "sample": f"the config-2 layer's Wo projection ({fl / 1e9:.1f} GFLOP)"}
 
+    # ---- the DeltaNet kernels (Qwen3.5-4B shape): the fused decode step at B = 32
+    # (the oracle is one thread per call: cores 1 for this entry) and the prefill
+    # recurrence over a 512-token sample at B = 1 (OpenMP over the 32 value heads)
+    Dk = Dv = 128
+    Hk, Hv, B = 16, 32, 32
+    rng = np.random.default_rng(21)
+    qz = hb(_dev_normal(vm, torch, (B, 2 * Hk * Dk + 2 * Hv * Dv), 2101))
+    ab = hb(_dev_normal(vm, torch, (B, 2 * Hv), 2102))
+    n = 2 * Hk * Dk + Hv * Dv
+    S0 = (rng.standard_normal((B, Hv, Dv, Dk)) * 0.05).astype(np.float32)
+    a_log = rng.standard_normal(Hv).astype(np.float32) * 0.5
+    dtb = rng.standard_normal(Hv).astype(np.float32) * 0.5
+    gw = hb(_dev_normal(vm, torch, (Dv,), 2103))
+    hk = Hk * Dk
+    args = (qz[:, :hk].reshape(B, Hk, Dk), qz[:, hk:2 * hk].reshape(B, Hk, Dk),
+            qz[:, 2 * hk:n].reshape(B, Hv, Dv), ab[:, :Hv], ab[:, Hv:],
+            qz[:, n:].reshape(B, Hv, Dv), a_log, dtb, gw, S0)
+    dt, nr = _median_time(lambda: oracle.fused_deltanet_decode(*args, eps=EPS), 3, 7, 5.0)
+    nb = B * Hv * (2.0 * Dk * Dv * 4 + 3 * Dv * 2 + 4) + B * 2 * hk * 2
+    res["deltanet_decode_B32"] = {"gbs": nb / dt / 1e9, "us_per_step": 1e6 * dt, "runs": nr,
+                                  "cores": 1,
+                                  "sample": "one fused DeltaNet decode step, B=32, Hv=32, "
+                                            "Dk=Dv=128 (single-threaded oracle)"}
+    T = 512
+    cv = hb(_dev_normal(vm, torch, (1, T, n), 2104))
+    abT = hb(_dev_normal(vm, torch, (1, T, 2 * Hv), 2105))
+    p = oracle.deltanet_prep(cv, abT, a_log, dtb, Dk=Dk, Dv=Dv, Hk=Hk, Hv=Hv)
+    Sz = np.zeros((1, Hv, Dv, Dk), np.float32)
+    dt, nr = _median_time(lambda: oracle.deltanet_sequence(p["q"], p["k"], p["v"], p["beta"],
+                                                           p["gate"], Sz), 1, 3, 10.0)
+    res["deltanet_sequence_B1"] = {"tokens_per_s": T / dt, "us_per_token": 1e6 * dt / T,
+                                   "runs": nr,
+                                   "sample": f"the prefill recurrence over {T} tokens, B=1 "
+                                             f"({threads} OpenMP threads over value heads)"}
+
     info = cpu_info()
     c2 = res["config2"]
     return {"value": c2["tflops"], "unit": "TFLOP/s", "cores": threads, "kind": "port",
@@ -949,7 +997,8 @@ def main():
         log("[bench] cpu baseline (oracle), configs 1-5")
         cpu = cpu_baseline(vm, torch)
         for k, v in sorted(cpu["configs"].items()):
-            fig = f"{v['tflops']:.4f} TFLOP/s" if "tflops" in v else f"{v['gbs']:.1f} GB/s"
+            fig = (f"{v['tflops']:.4f} TFLOP/s" if "tflops" in v else
+                   f"{v['gbs']:.1f} GB/s" if "gbs" in v else f"{v['tokens_per_s']:.0f} tokens/s")
             log(f"[bench] cpu {k}: {fig} ({v['sample']}, {v['runs']} runs)")
 
     if pf is None:
