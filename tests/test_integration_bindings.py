@@ -142,7 +142,12 @@ def test_every_binding_matches_the_header():
         seen.add(name)
     for must in ("vm_gated_attn_decode", "vm_gated_attn_prefill", "vm_attention_fwd",
                  "vm_decode_attention", "vm_qnorm_rope", "vm_knorm_rope_append",
-                 "vm_decode_scratch_bytes", "vm_prefill_scratch_bytes"):
+                 "vm_decode_scratch_bytes", "vm_prefill_scratch_bytes", "vm_linear",
+                 "vm_rms_norm", "vm_fused_add_rms_norm", "vm_silu_mul", "vm_embed",
+                 "vm_generation_advance", "vm_lm_head_argmax", "vm_causal_conv1d",
+                 "vm_causal_conv1d_sequence", "vm_fused_deltanet_decode",
+                 "vm_deltanet_recurrent_decode", "vm_deltanet_sequence",
+                 "vm_deltanet_prefill_prep", "vm_gated_rms_norm"):
         assert must in seen, f"INTEGRATION.md has no binding for {must}"
 
 
