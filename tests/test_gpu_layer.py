@@ -81,6 +81,50 @@ def test_linear_narrow(vm, orc, M, N, K):
     assert bool((yw[:, M:] == 7.0).all())
 
 
+def test_linear_narrow_split_workspace(vm):
+    """A split GEMV keeps its K slices' fp32 partials in the workspace: a
+    workspace full of garbage, one shared by problems in turn, and a captured
+    graph replayed with other problems run eagerly between the replays all give
+    the fresh-workspace results, bit for bit."""
+    banner("linear narrow split workspace")
+    probs = [(DM, 32, 9216), (DM, 16, HQ * D), (DM, 3, HQ * D), (4096, 25, 1024)]
+    xs, Ws, refs = [], [], []
+    for i, (M, N, K) in enumerate(probs):
+        x = to_dev(normal_bf16((N, K), 740 + i))
+        W = to_dev(normal_bf16((M, K), 840 + i, scale=K ** -0.5))
+        need = vm.linear_workspace_bytes(x, W)
+        print(f"M={M} N={N} K={K}: workspace {need} B")
+        assert need > 0, "expected a split problem"
+        y = vm.linear(x, W, workspace=torch.zeros(need, dtype=torch.uint8, device="cuda"))["y"]
+        xs.append(x)
+        Ws.append(W)
+        refs.append(y)
+    nmax = max(vm.linear_workspace_bytes(x, W) for x, W in zip(xs, Ws))
+    ws = torch.randint(0, 256, (nmax,), dtype=torch.uint8, device="cuda")  # garbage
+    ys = [torch.empty_like(r) for r in refs]
+    for _ in range(2):
+        for x, W, y, r in zip(xs, Ws, ys, refs):
+            vm.linear_({"y": y}, x, W, workspace=ws)
+            torch.cuda.synchronize()
+            assert torch.equal(y.view(torch.int16), r.view(torch.int16))
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            vm.linear_({"y": ys[0]}, xs[0], Ws[0], workspace=ws)
+    torch.cuda.synchronize()
+    for k in range(4):
+        ys[0].zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ys[0].view(torch.int16), refs[0].view(torch.int16)), f"replay {k}"
+        vm.linear_({"y": ys[1 + k % 3]}, xs[1 + k % 3], Ws[1 + k % 3], workspace=ws)  # between
+        torch.cuda.synchronize()
+        assert torch.equal(ys[1 + k % 3].view(torch.int16), refs[1 + k % 3].view(torch.int16))
+    del g
+
+
 def test_linear_narrow_misaligned_view(vm, orc):
     """A view off the kernel's 16-byte alignment takes the GEMM library's
     path for the same problem: same results to the parity bar."""
