@@ -273,6 +273,25 @@ int vm_linear(vm_bf16* y, int64_t ldy, const vm_bf16* x, int64_t ldx, const vm_b
               int64_t ldw, int M, int N, int K, void* workspace, size_t workspace_bytes,
               vm_stream stream);
 
+/* ---- linear! + fused_add_rms_norm! in one call ---------------------------
+ * No counterpart in the reference: its decode step runs linear! into a bf16 h
+ * and then fused_add_rms_norm! on it, after every out projection and MLP
+ * (src/llm/qwen35.jl:206 + :265, :241 + :268). This does exactly that in one
+ * call, for callers that want the launches saved:
+ *   h = bf16(W^T a)          (linear!, a :: (K, N), W :: (K, M) K-major)
+ *   x = bf16(x + h)          in place (X' = X, residual_norm.jl:39-60)
+ *   y = x rstd (w + offset)  rstd over the fp32 x + h, y from the stored x
+ * bit-identical to the two calls. A narrow problem whose GEMV splits K hands
+ * its fp32 slices straight to the norm, which adds them in slice order (no
+ * reduce launch, no h in HBM). M a multiple of 8, at most 16384; workspace
+ * (256-byte aligned) of vm_linear_add_rms_norm_workspace_bytes bytes
+ * ((size_t)-1 on a bad shape).                                              */
+size_t vm_linear_add_rms_norm_workspace_bytes(int M, int N, int K, int64_t ldw, int64_t lda);
+int vm_linear_add_rms_norm(vm_bf16* y, int64_t y_st, vm_bf16* x, int64_t x_st, const vm_bf16* a,
+                           int64_t lda, const vm_bf16* w, int64_t ldw, const vm_bf16* norm_w,
+                           int M, int N, int K, float eps, float offset, void* workspace,
+                           size_t workspace_bytes, vm_stream stream);
+
 /* ---- f2: the rest of the decode step (src/llm/qwen35.jl:247-273) --------
  * Matrices are column-major bf16 with an element column stride (a multiple of
  * 8, pointers 16-byte aligned); M, I, D, K multiples of 8.

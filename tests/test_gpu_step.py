@@ -359,3 +359,46 @@ def test_identity_mixed_model_step(vm):
     gen.result.copy_(i32(tok))
     vm.step_(m, gen)
     assert gen.result.cpu().tolist() == tok
+
+
+@pytest.mark.parametrize("D_,N,K", [(2560, 32, 4096), (2560, 3, 9216), (2560, 16, 64),
+                                   (2560, 64, 4096), (1024, 25, 1024)])
+def test_linear_add_rms_norm_is_the_two_calls(vm, D_, N, K):
+    """linear! + fused_add_rms_norm! in one call (the split GEMV's slices summed
+    by the norm; one slice; the GEMM library's path at N = 64) is bit-identical
+    to the two calls, residual updated in place."""
+    banner(f"linear_add_rms_norm D={D_} N={N} K={K}")
+    a = to_dev(normal_bf16((N, K), 990 + K))
+    W = to_dev(normal_bf16((D_, K), 991 + D_, scale=K ** -0.5))
+    x0 = to_dev(normal_bf16((N, D_), 992))
+    nw = to_dev(normal_bf16((D_,), 993, scale=0.05))
+    h = vm.linear(a, W)["y"]
+    x_ref = x0.clone()
+    y_ref = torch.empty_like(x0)
+    vm.fused_add_rms_norm_({"Y": y_ref, "Xp": x_ref}, x_ref, h, nw, eps=EPS, offset=1.0)
+    x = x0.clone()
+    y = torch.empty_like(x0)
+    print(f"workspace {vm.linear_add_rms_norm_workspace_bytes(a, W)} B")
+    vm.linear_add_rms_norm_({"Y": y, "X": x}, a, W, nw, eps=EPS, offset=1.0)
+    torch.cuda.synchronize()
+    assert torch.equal(x.view(torch.int16), x_ref.view(torch.int16))
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+
+
+def test_linear_add_rms_norm_misaligned_input(vm):
+    """An input view off the GEMV's alignment takes the GEMM library's path."""
+    banner("linear_add_rms_norm misaligned input")
+    D_, N, K = 2560, 4, 512
+    a_full = to_dev(normal_bf16((N, K + 8), 994))
+    a = a_full[:, 4:K + 4]
+    W = to_dev(normal_bf16((D_, K), 995, scale=K ** -0.5))
+    x0 = to_dev(normal_bf16((N, D_), 996))
+    nw = to_dev(normal_bf16((D_,), 997, scale=0.05))
+    h = vm.linear(a, W)["y"]
+    x_ref, y_ref = x0.clone(), torch.empty_like(x0)
+    vm.fused_add_rms_norm_({"Y": y_ref, "Xp": x_ref}, x_ref, h, nw, eps=EPS, offset=1.0)
+    x, y = x0.clone(), torch.empty_like(x0)
+    vm.linear_add_rms_norm_({"Y": y, "X": x}, a, W, nw, eps=EPS, offset=1.0)
+    torch.cuda.synchronize()
+    assert torch.equal(x.view(torch.int16), x_ref.view(torch.int16))
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))

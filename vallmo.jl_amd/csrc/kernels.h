@@ -148,6 +148,15 @@ hipError_t decode_static_scratch(void** ptr);
 constexpr size_t LINEAR_MAX_WORKSPACE_BYTES = (size_t)64 << 20;
 int linear_workspace(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, size_t* bytes,
                      char* err, size_t errn);
+// y = W^T a, then x = bf16(x + bf16(y)) in place and yn = rms_norm(x): linear!
+// and fused_add_rms_norm! back to back; a split narrow GEMV hands its fp32
+// slices straight to the norm (no reduce launch, no bf16 y in HBM)
+int linear_add_norm_workspace(int M, int N, int K, int64_t ldw, int64_t lda, size_t* bytes,
+                              char* err, size_t errn);
+int linear_add_norm_run(uint16_t* yn, int64_t yn_st, uint16_t* x, int64_t x_st, const uint16_t* a,
+                        int64_t lda, const uint16_t* w, int64_t ldw, const uint16_t* nw, int M,
+                        int N, int K, float eps, float offset, void* workspace,
+                        size_t workspace_bytes, hipStream_t st, char* err, size_t errn);
 int linear_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w,
                int64_t ldw, int M, int N, int K, void* workspace, size_t workspace_bytes,
                hipStream_t st, char* err, size_t errn);
@@ -167,6 +176,11 @@ struct NormArgs {
   const uint16_t* w;
   int M, N;             // M a multiple of 8, at most 16384
   float offset, eps;
+  // instead of dx: dx = bf16(sum of S2 fp32 slices in slice order), slice k of
+  // column n at dpart + k * dpart_ss + n * dpart_cs (a split GEMV's partials)
+  const float* dpart;
+  int64_t dpart_ss, dpart_cs;
+  int S2;
 };
 struct SiluMulArgs {
   uint16_t* mid;        // (I, N), column stride mid_st
@@ -222,6 +236,9 @@ struct GemvPlan {
 GemvPlan gemv_plan(int M, int K, int waves);
 size_t gemv_workspace_bytes(int M, int K);
 hipError_t launch_gemv(GemvArgs a, hipStream_t st);
+// the split GEMV without its reduce: leaves the slices' fp32 partials in
+// a.part (layout [S2][32][M]); returns the plan through *plan
+hipError_t launch_gemv_partials(GemvArgs a, GemvPlan* plan, hipStream_t st);
 hipError_t launch_rms_norm(const NormArgs& a, hipStream_t st);
 
 // ---- linear-attention layer parts (deltanet.hip). Dk = Dv = 128; element

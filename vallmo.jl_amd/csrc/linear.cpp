@@ -218,4 +218,100 @@ int linear_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const u
   return VM_OK;
 }
 
+namespace {
+size_t round256(size_t n) { return (n + 255) / 256 * 256; }
+}  // namespace
+
+int linear_add_norm_workspace(int M, int N, int K, int64_t ldw, int64_t lda, size_t* bytes,
+                              char* err, size_t errn) {
+  const size_t hbytes = round256((size_t)M * N * sizeof(uint16_t));  // a bf16 y, ld M
+  if (gemv_shape(M, N, K, ldw, lda, M)) {
+    const size_t part = gemv_workspace_bytes(M, K);
+    // a split plan needs its partials; a single-slice one a bf16 y (and the
+    // GEMM library's path for a misaligned view of the same shape: below)
+    size_t lin = 0;
+    const int rc = linear_workspace(M, N, K, ldw, lda, M, &lin, err, errn);
+    *bytes = std::max(std::max(part, hbytes), (rc == VM_OK ? round256(lin) + hbytes : 0));
+    return VM_OK;
+  }
+  size_t lin = 0;
+  const int rc = linear_workspace(M, N, K, ldw, lda, M, &lin, err, errn);
+  if (rc != VM_OK) return rc;
+  *bytes = round256(lin) + hbytes;
+  return VM_OK;
+}
+
+int linear_add_norm_run(uint16_t* yn, int64_t yn_st, uint16_t* x, int64_t x_st, const uint16_t* a,
+                        int64_t lda, const uint16_t* w, int64_t ldw, const uint16_t* nw, int M,
+                        int N, int K, float eps, float offset, void* workspace,
+                        size_t workspace_bytes, hipStream_t st, char* err, size_t errn) {
+  size_t need = 0;
+  int rc = linear_add_norm_workspace(M, N, K, ldw, lda, &need, err, errn);
+  if (rc != VM_OK) return rc;
+  if (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 256 != 0) {
+    snprintf(err, errn,
+             "linear_add_rms_norm: workspace of %zu bytes (256-byte aligned) < %zu required "
+             "(vm_linear_add_rms_norm_workspace_bytes)", workspace_bytes, need);
+    return VM_E_SCRATCH;
+  }
+  NormArgs na{};
+  na.y = yn;
+  na.y_st = yn_st;
+  na.xo = x;
+  na.xo_st = x_st;
+  na.x = x;
+  na.x_st = x_st;
+  na.w = nw;
+  na.M = M;
+  na.N = N;
+  na.offset = offset;
+  na.eps = eps;
+  uint16_t* h = static_cast<uint16_t*>(workspace);  // the bf16 y when one is formed
+  if (gemv_shape(M, N, K, ldw, lda, M) && gemv_aligned(h, a, w)) {
+    GemvArgs g{};
+    g.w = w;
+    g.w_st = ldw;
+    g.x = a;
+    g.x_st = lda;
+    g.y = h;
+    g.y_st = M;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.part = static_cast<float*>(workspace);
+    GemvPlan p{};
+    hipError_t e = launch_gemv_partials(g, &p, st);
+    if (e == hipSuccess && p.S2 > 1) {
+      na.dpart = g.part;
+      na.dpart_ss = (int64_t)32 * M;
+      na.dpart_cs = M;
+      na.S2 = p.S2;
+    } else {
+      na.dx = h;
+      na.dx_st = M;
+    }
+    if (e == hipSuccess) e = launch_rms_norm(na, st);
+    if (e != hipSuccess) {
+      snprintf(err, errn, "linear_add_rms_norm: %s", hipGetErrorString(e));
+      return (int)e;
+    }
+    return VM_OK;
+  }
+  // the GEMM library's path: y into the workspace after the plan's own space
+  size_t lin = 0;
+  rc = linear_workspace(M, N, K, ldw, lda, M, &lin, err, errn);
+  if (rc != VM_OK) return rc;
+  h = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + round256(lin));
+  rc = linear_run(h, M, a, lda, w, ldw, M, N, K, workspace, lin, st, err, errn);
+  if (rc != VM_OK) return rc;
+  na.dx = h;
+  na.dx_st = M;
+  const hipError_t e = launch_rms_norm(na, st);
+  if (e != hipSuccess) {
+    snprintf(err, errn, "linear_add_rms_norm: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  return VM_OK;
+}
+
 }  // namespace vm

@@ -63,7 +63,20 @@ __global__ __launch_bounds__(RT) void rms_norm_kernel(NormArgs a) {
       load8f(x + 8 * c, v[i]);
       if (FUSED) {
         float d[8];
-        load8f(a.dx + (int64_t)n * a.dx_st + 8 * c, d);
+        if (a.dpart) {  // a split GEMV's slices, summed in slice order, rounded
+          const float* p = a.dpart + (int64_t)n * a.dpart_cs + 8 * c;
+          float4 lo = *reinterpret_cast<const float4*>(p), hi = *reinterpret_cast<const float4*>(p + 4);
+          for (int k = 1; k < a.S2; ++k) {
+            const float4 l2 = *reinterpret_cast<const float4*>(p + k * a.dpart_ss);
+            const float4 h2 = *reinterpret_cast<const float4*>(p + k * a.dpart_ss + 4);
+            lo.x += l2.x; lo.y += l2.y; lo.z += l2.z; lo.w += l2.w;
+            hi.x += h2.x; hi.y += h2.y; hi.z += h2.z; hi.w += h2.w;
+          }
+          const float s8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+          unpack8(pack8(s8), d);  // the bf16 h the reference stores
+        } else {
+          load8f(a.dx + (int64_t)n * a.dx_st + 8 * c, d);
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float s = v[i][j] + d[j];
@@ -96,7 +109,7 @@ __global__ __launch_bounds__(RT) void rms_norm_kernel(NormArgs a) {
 
 hipError_t launch_rms_norm(const NormArgs& a, hipStream_t st) {
   if (a.N == 0) return hipSuccess;
-  if (a.dx)
+  if (a.dx || a.dpart)
     hipLaunchKernelGGL(rms_norm_kernel<true>, dim3(a.N), dim3(RT), 0, st, a);
   else
     hipLaunchKernelGGL(rms_norm_kernel<false>, dim3(a.N), dim3(RT), 0, st, a);
@@ -504,6 +517,17 @@ GemvPlan gemv_plan(int M, int K, int waves) {
 size_t gemv_workspace_bytes(int M, int K) {
   const GemvPlan p = gemv_plan(M, K, lm_head_waves());
   return p.S2 > 1 ? (size_t)p.S2 * 32 * (size_t)M * sizeof(float) : 0;
+}
+
+hipError_t launch_gemv_partials(GemvArgs a, GemvPlan* plan, hipStream_t st) {
+  const GemvPlan p = gemv_plan(a.M, a.K, lm_head_waves());
+  *plan = p;
+  a.T = p.T;
+  a.S2 = p.S2;
+  a.gps = p.gps;
+  a.G = a.K / 64;
+  hipLaunchKernelGGL(gemv_kernel, dim3(p.ntg * p.S2), dim3(256), 0, st, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemv(GemvArgs a, hipStream_t st) {

@@ -978,6 +978,30 @@ int vm_gated_rms_norm(vm_bf16* y, int64_t y_st, int64_t y_sb, const float* o, co
                     "gated_rms_norm");
 }
 
+// ---- linear! + fused_add_rms_norm! in one call -------------------------------
+size_t vm_linear_add_rms_norm_workspace_bytes(int M, int N, int K, int64_t ldw, int64_t lda) {
+  if (linear_check(M, N, K, ldw, lda, M) != VM_OK) return (size_t)-1;
+  size_t n = 0;
+  if (vm::linear_add_norm_workspace(M, N, K, ldw, lda, &n, g_err, sizeof g_err) != VM_OK)
+    return (size_t)-1;
+  return n;
+}
+
+int vm_linear_add_rms_norm(vm_bf16* y, int64_t y_st, vm_bf16* x, int64_t x_st, const vm_bf16* a,
+                           int64_t lda, const vm_bf16* w, int64_t ldw, const vm_bf16* norm_w,
+                           int M, int N, int K, float eps, float offset, void* workspace,
+                           size_t workspace_bytes, vm_stream st) {
+  TRY(linear_check(M, N, K, ldw, lda, M));
+  TRY(check_rows(M, N, y_st, "linear_add_rms_norm", "y_st"));
+  TRY(check_rows(M, N, x_st, "linear_add_rms_norm", "x_st"));
+  TRY(check_aligned(y, "Y"));
+  TRY(check_aligned(x, "X"));
+  TRY(check_aligned(norm_w, "W_norm"));
+  REQUIRE(a && w, VM_E_ARG, "linear_add_rms_norm: NULL pointer argument");
+  return vm::linear_add_norm_run(y, y_st, x, x_st, a, lda, w, ldw, norm_w, M, N, K, eps, offset,
+                                 workspace, workspace_bytes, S(st), g_err, sizeof g_err);
+}
+
 // ---- synthetic inputs ------------------------------------------------------
 int vm_fill_normal_bf16(vm_bf16* dst, int64_t n, uint64_t seed, float scale, float shift,
                         vm_stream st) {

@@ -133,10 +133,12 @@ def _qkv(conv, c: DeltaNetConfig):
 
 
 def decode_(h, l: DeltaNetLayer, c: DeltaNetConfig, space: DeltaNetSpace, xn, *, eps: float,
-            workspace):
+            workspace, project: bool = True):
     """decode!(h, l::DeltaNetLayer, m, gen, xn) — qwen35.jl:210-232: one token per
     sequence, hidden state to hidden state; the ring and S advance in place. xn,
-    h :: (D, B) (torch (B, D)). Reads no clock: the recurrence carries position."""
+    h :: (D, B) (torch (B, D)). Reads no clock: the recurrence carries position.
+    With ``project=False`` the out projection is left to the caller and its
+    input (Dv·Hv, B) is returned."""
     B = xn.shape[0]
     if space.qz.shape[0] != B:
         raise DimensionMismatch(f"size(xn, 2) = {B} does not match the decode space's B")
@@ -148,6 +150,8 @@ def decode_(h, l: DeltaNetLayer, c: DeltaNetConfig, space: DeltaNetSpace, xn, *,
     ops.fused_deltanet_decode_({"O": space.O, "Sp": l.S}, q, k, v, space.ab[:, :c.Hv],
                                space.ab[:, c.Hv:], z.unflatten(-1, (c.Hv, c.Dv)), l.A_log,
                                l.dt_bias, l.gnorm_w, l.S, eps=eps)
+    if not project:
+        return space.O.view(B, c.Hv * c.Dv)
     ops.linear_({"y": h}, space.O.view(B, c.Hv * c.Dv), l.Wout, workspace=workspace)
     return h
 

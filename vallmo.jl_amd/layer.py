@@ -263,12 +263,15 @@ def _need_proj(l: AttnLayer, cfg: AttnConfig):
     sizes(Wqkv=(l.Wqkv, f"{cfg.D} {S * cfg.Dh}"), Wo=(l.Wo, f"{cfg.Hq * cfg.Dh} {cfg.D}"))
 
 
-def decode_(h, l: AttnLayer, m: AttnModel, gen: Generation, xn, *, advance: bool = False):
+def decode_(h, l: AttnLayer, m: AttnModel, gen: Generation, xn, *, advance: bool = False,
+            project: bool = True):
     """decode!(h, l::AttnLayer, m, gen, xn) — qwen35.jl:187-208, hidden state to
     hidden state for one token per sequence: qkv = linear(xn, Wqkv) (:194), the
     fused gated attention (:195-205) into O, h = linear(O, Wo) (:206). xn, h ::
     (D, B) (torch (B, D)). The temporaries are the model's decode buffers, so the
-    step allocates nothing once warm (capturable with ``advance``)."""
+    step allocates nothing once warm (capturable with ``advance``). With
+    ``project=False`` the Wo projection is left to the caller (the step fuses it
+    with the residual norm) and the Wo input (Hq·Dh, B) is returned."""
     cfg = m.cfg
     _need_proj(l, cfg)
     d = sizes(xn=(xn, f"{cfg.D} B"), h=(h, f"{cfg.D} B"))
@@ -280,6 +283,8 @@ def decode_(h, l: AttnLayer, m: AttnModel, gen: Generation, xn, *, advance: bool
                                 ops.linear_workspace_bytes(O2, l.Wo, h)))
     ops.linear_({"y": q2}, xn, l.Wqkv, workspace=ws)
     gated_attn_decode_(O, l, m, gen, qkv, advance=advance)
+    if not project:
+        return O2
     ops.linear_({"y": h}, O2, l.Wo, workspace=ws)
     return h
 

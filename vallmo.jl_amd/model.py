@@ -102,12 +102,19 @@ class Model:
         if self._ws_need is None:
             l0 = self.layers[0]
             need = max(ops.linear_workspace_bytes(self.xn, l0.Wgu, self.gu),
-                       ops.linear_workspace_bytes(self.mid, l0.Wd, self.h))
+                       ops.linear_workspace_bytes(self.mid, l0.Wd, self.h),
+                       ops.linear_add_rms_norm_workspace_bytes(self.mid, l0.Wd))
             if self.dn_layers:
                 l, c = self.dn_layers[0], self.cfg.linear
+                O2 = self.dn.O.view(self.cfg.B, -1)
                 need = max(need, ops.linear_workspace_bytes(self.xn, l.W_in, self.dn.qzab),
-                           ops.linear_workspace_bytes(self.dn.O.view(self.cfg.B, -1), l.Wout,
-                                                      self.h))
+                           ops.linear_workspace_bytes(O2, l.Wout, self.h),
+                           ops.linear_add_rms_norm_workspace_bytes(O2, l.Wout))
+            attn = [l for l in self.layers if not isinstance(l, DeltaNetLayer)]
+            if attn:
+                _, O = self.attn.decode_buffers()
+                need = max(need, ops.linear_add_rms_norm_workspace_bytes(
+                    O.view(self.cfg.B, -1), attn[0].Wo))
             self._ws_need = need
         return self.attn.linear_workspace(self._ws_need)
 
@@ -192,11 +199,13 @@ def _need_layer(l):
             raise ArgumentError(f"decoder layer has no {n}")
 
 
-def _mixer_decode(h, l, m: "Model", gen: Generation, xn):
+def _mixer_decode(l, m: "Model", gen: Generation, xn):
+    """The mixer up to its out projection: (its input, its weight)."""
     if isinstance(l, DeltaNetLayer):
-        dn.decode_(h, l, m.cfg.linear, m.dn, xn, eps=m.cfg.attn.eps, workspace=m.workspace())
-    else:
-        decode_(h, l, m.attn, gen, xn)
+        o = dn.decode_(None, l, m.cfg.linear, m.dn, xn, eps=m.cfg.attn.eps,
+                       workspace=m.workspace(), project=False)
+        return o, l.Wout
+    return decode_(None, l, m.attn, gen, xn, project=False), l.Wo
 
 
 def mlp_(h, l, m: Model, xn):
@@ -224,13 +233,20 @@ def step_(m: Model, gen: Generation):
     ops.embed_(x, m.E, gen.result)
     ops.rms_norm_({"Y": xn}, x, m.layers[0].norm1, eps=eps, offset=1.0)
     n = len(m.layers)
+    ws = m.workspace()
     for i, l in enumerate(m.layers):
         _need_layer(l)
-        _mixer_decode(h, l, m, gen, xn)
-        ops.fused_add_rms_norm_({"Y": xn, "Xp": x}, x, h, l.norm2, eps=eps, offset=1.0)
-        mlp_(h, l, m, xn)
+        # the mixer, then its out projection fused with the residual add + norm2
+        # (linear! + fused_add_rms_norm!, :206 + :265, bit-identical)
+        o, W_out = _mixer_decode(l, m, gen, xn)
+        ops.linear_add_rms_norm_({"Y": xn, "X": x}, o, W_out, l.norm2, eps=eps, offset=1.0,
+                                 workspace=ws)
+        # the MLP (mlp!, :234-243), its down projection fused with the next norm
+        ops.linear_({"y": m.gu}, xn, l.Wgu, workspace=ws)
+        ops.silu_mul_(m.mid, m.gu)
         next_w = m.norm_w if i == n - 1 else m.layers[i + 1].norm1
-        ops.fused_add_rms_norm_({"Y": xn, "Xp": x}, x, h, next_w, eps=eps, offset=1.0)
+        ops.linear_add_rms_norm_({"Y": xn, "X": x}, m.mid, l.Wd, next_w, eps=eps, offset=1.0,
+                                 workspace=ws)
     ops.lm_head_argmax_({"Result": gen.result}, xn, m.head, scratch=m.lm_scratch)
     return gen
 

@@ -29,7 +29,8 @@ __all__ = [
     "causal_conv1d_", "causal_conv1d", "causal_conv1d_sequence_", "causal_conv1d_sequence",
     "fused_deltanet_decode_", "fused_deltanet_decode", "deltanet_recurrent_decode_",
     "deltanet_recurrent_decode", "deltanet_sequence_", "deltanet_sequence",
-    "deltanet_prefill_prep_", "gated_rms_norm_",
+    "deltanet_prefill_prep_", "gated_rms_norm_", "linear_add_rms_norm_",
+    "linear_add_rms_norm_workspace_bytes",
 ]
 
 
@@ -269,6 +270,41 @@ def linear(x, W, **kw) -> dict:
     """Allocating linear (linear.jl:68-79): returns {"y": y}, torch (..., M)."""
     y = torch.empty(tuple(x.shape[:-1]) + (W.shape[0],), dtype=x.dtype, device=x.device)
     return linear_({"y": y}, x, W, **kw)
+
+
+def linear_add_rms_norm_workspace_bytes(a, W) -> int:
+    """Workspace of linear_add_rms_norm_ for this problem."""
+    M, K, N = W.shape[0], a.shape[-1], _rows(a)
+    n = _lib.load().vm_linear_add_rms_norm_workspace_bytes(M, N, K, W.stride(0), _ld(a))
+    if n == ctypes.c_size_t(-1).value:
+        _lib.check(_lib.VM_E_UNSUPPORTED, "vm_linear_add_rms_norm_workspace_bytes")
+    return int(n)
+
+
+def linear_add_rms_norm_(outs, a, W, norm_w, *, eps, offset, workspace=None):
+    """linear! then fused_add_rms_norm! in one call, bit-identical to the two
+    (the decode step's pairs at src/llm/qwen35.jl:206 + :265, :241 + :268):
+    h = bf16(W^T a); X = bf16(X + h) in place; Y = rms_norm(X) (w + offset).
+    outs: "Y" (D, N) and "X" (D, N), the residual stream updated in place;
+    a :: (K, N), W :: (K, D) K-major (torch (D, K)). No reference counterpart
+    as one op; saves the reduce launch of a split GEMV and the bf16 h."""
+    Y, X = _out(outs, "Y"), _out(outs, "X")
+    D, N, ys = _cols(Y, "Y")
+    Dx, Nx, xs = _cols(X, "X")
+    K, Na, as_ = _cols(a, "a")
+    if W.dim() != 2 or tuple(W.shape) != (D, K) or (Dx, Nx) != (D, N) or Na != N:
+        raise DimensionMismatch(f"linear_add_rms_norm: a ({K}, {Na}), W {tuple(W.shape)}, "
+                                f"X ({Dx}, {Nx}), Y ({D}, {N})")
+    _need(W, torch.bfloat16, "W")
+    _need(norm_w, torch.bfloat16, "norm_w")
+    sizes(norm_w=(norm_w, f"{D}"))
+    need = linear_add_rms_norm_workspace_bytes(a, W)
+    if workspace is None:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=a.device)
+    call("vm_linear_add_rms_norm", _p(Y), ys, _p(X), xs, _p(a), as_, _p(W), W.stride(0),
+         _p(norm_w), D, N, K, float(eps), float(offset), _p(workspace), workspace.numel(),
+         _stream())
+    return outs
 
 
 def _cols(t, name, M=None):
