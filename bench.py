@@ -693,12 +693,22 @@ def bench_deltanet(vm, torch, seed=11):
     us_seq = _profiled_us(vm, torch, vm._lib.VM_K_DELTANET,
                           lambda: vm.deltanet_sequence_({"O": o, "Sp": S}, p["Q"], p["K"], p["V"],
                                                         p["Beta"], p["Gate"], S), n=3)
+    ws = torch.empty(vm.deltanet_sequence_workspace_bytes(T, Hv, B), dtype=torch.uint8,
+                     device="cuda")
+    us_chk = _profiled_us(vm, torch, vm._lib.VM_K_DELTANET,
+                          lambda: vm.deltanet_sequence_chunked_({"O": o, "Sp": S}, p["Q"], p["K"],
+                                                                p["V"], p["Beta"], p["Gate"], S,
+                                                                workspace=ws), n=5)
+    # chunked form's work: per 64-token chunk and value head, phase 1's two Grams,
+    # triangular solve and operand writes, phase 2's 4 x 112 MFMAs per column block
     res["prefill_B1_T4096"] = {
         "conv_sequence_us": us_conv,
         "conv_sequence_gbs": 2.0 * (2 * T * n + K * n) / (us_conv * 1e-6) / 1e9,
         "sequence_ms": us_seq * 1e-3,
         "sequence_tokens_per_s": T / (us_seq * 1e-6),
         "sequence_us_per_token": us_seq / T,
+        "chunked_ms": us_chk * 1e-3,
+        "chunked_tokens_per_s": T / (us_chk * 1e-6),
     }
     return res
 
@@ -984,7 +994,8 @@ def main():
         log(f"[bench] deltanet: fused decode B=1 {f1['us']:.1f} us, B=32 {f32_['us']:.1f} us = "
             f"{f32_['gbs']:.0f} GB/s; conv decode B=32 {cv['us']:.1f} us = {cv['gbs']:.0f} GB/s; "
             f"prefill T=4096: conv {pp['conv_sequence_us']:.1f} us, recurrence "
-            f"{pp['sequence_ms']:.2f} ms ({pp['sequence_us_per_token']:.2f} us/token)")
+            f"{pp['sequence_ms']:.2f} ms sequential ({pp['sequence_us_per_token']:.2f} us/token), "
+            f"{pp['chunked_ms']:.3f} ms chunked")
     step = None
     if not args.no_step:
         log("[bench] whole decode step, Qwen3.5-4B shape (24 DeltaNet + 8 attention), B=32")

@@ -404,6 +404,21 @@ int vm_deltanet_sequence(float* o, const float* q, const float* k, const float* 
                          const float* beta, const float* gate, const float* s_in, float* s_out,
                          int Dk, int Dv, int T, int Hk, int Hv, int B, vm_stream stream);
 
+/* deltanet_sequence! in its chunked form: the same arguments and results (to
+ * fp32 rounding), computed per 64-token chunk as a lower-triangular solve and
+ * fp32 MFMA products (delta = U - W S_0, O = gamma Q S_0 + M delta, S_C =
+ * gamma_C S_0 + K~^T delta: the sequential recurrence's exact algebra), the
+ * chunks' state carried by one sequential scan. No separate reference
+ * function: the reference runs the sequential loop (deltanet_recurrent.jl:
+ * 109-172); this is the same operator, parallel over each chunk. workspace:
+ * vm_deltanet_sequence_workspace_bytes(T, Hv, B) bytes, 256-byte aligned
+ * (147 712 B per 64-token chunk per value head and sequence). */
+size_t vm_deltanet_sequence_workspace_bytes(int T, int Hv, int B);
+int vm_deltanet_sequence_chunked(float* o, const float* q, const float* k, const float* v,
+                                 const float* beta, const float* gate, const float* s_in,
+                                 float* s_out, int Dk, int Dv, int T, int Hk, int Hv, int B,
+                                 void* workspace, size_t workspace_bytes, vm_stream stream);
+
 /* The prefill's inputs to deltanet_sequence! (forward(::DeltaNetLayer),
  * src/llm/qwen35.jl:347-356): from the conv output cv (the q | k | v channels,
  * n = 2 Hk Dk + Hv Dv rows per token, token stride cv_st, sequence stride

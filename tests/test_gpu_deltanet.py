@@ -252,3 +252,56 @@ def test_shape_errors(vm):
     g2 = torch.zeros((B, 2), dtype=torch.float32, device="cuda")
     with pytest.raises(vm.UnsupportedShape):
         vm.deltanet_recurrent_decode(q64, q64, v64, g2, g2, S64)
+
+
+@pytest.mark.parametrize("B,T", [(1, 1), (1, 63), (1, 64), (2, 65), (1, 200), (17, 70),
+                                 (1, 1000)])
+def test_deltanet_sequence_chunked(vm, orc, B, T):
+    """deltanet_sequence! in its chunked form (triangular solve + fp32 MFMA per
+    64-token chunk, one scan over chunks) against the sequential oracle: every
+    output and the final state within rtol 5e-4 (chunk edges, partial last
+    chunks, B > 1, the state updated in place)."""
+    banner(f"deltanet sequence chunked B={B} T={T}")
+    cv, ab, a_log, dt_bias = _prepped(B, T, 1950 + B + T)
+    p = orc.deltanet_prep(cv, ab, a_log, dt_bias, Dk=DK, Dv=DV, Hk=HK, Hv=HV)
+    s = normal_f32(B * HV * DV * DK, 1951, scale=0.05).reshape(B, HV, DV, DK)
+    o_ref, s_ref = orc.deltanet_sequence(p["q"], p["k"], p["v"], p["beta"], p["gate"], s)
+    S = f32dev(s)
+    o = torch.empty((B, HV, T, DV), dtype=torch.float32, device="cuda")
+    ws = torch.full((vm.deltanet_sequence_workspace_bytes(T, HV, B),), 255, dtype=torch.uint8,
+                    device="cuda")   # garbage: every byte read is written first
+    vm.deltanet_sequence_chunked_({"O": o, "Sp": S}, f32dev(p["q"]), f32dev(p["k"]),
+                                  f32dev(p["v"]), f32dev(p["beta"]), f32dev(p["gate"]), S,
+                                  workspace=ws)
+    torch.cuda.synchronize()
+    for got, ref, name in ((o.cpu().numpy(), o_ref, "O"), (S.cpu().numpy(), s_ref, "S")):
+        err = np.abs(got - ref).max() / np.abs(ref).max()
+        print(f"chunked {name}: max err / max |ref| = {err:.2e}")
+        assert err <= 5e-4, name
+
+
+def test_deltanet_sequence_chunked_equals_sequential_at_4096(vm):
+    """At the prefill size (T = 4096, B = 1) the chunked and the sequential
+    kernels agree: outputs and final state within 1e-3 of their maxima."""
+    banner("deltanet sequence chunked vs sequential T=4096")
+    B, T = 1, 4096
+    f32 = dict(dtype=torch.float32, device="cuda")
+    cv = torch.empty((B, T, NCH), dtype=torch.bfloat16, device="cuda")
+    vm.fill_normal_(cv, 1960)
+    ab = torch.empty((B, T, 2 * HV), dtype=torch.bfloat16, device="cuda")
+    vm.fill_normal_(ab, 1961)
+    p = {"Q": torch.empty((B, HK, T, DK), **f32), "K": torch.empty((B, HK, T, DK), **f32),
+         "V": torch.empty((B, HV, T, DV), **f32), "Beta": torch.empty((B, T, HV), **f32),
+         "Gate": torch.empty((B, T, HV), **f32)}
+    vm.deltanet_prefill_prep_(p, cv, ab, f32dev(normal_f32(HV, 1962, scale=0.5)),
+                              f32dev(normal_f32(HV, 1963, scale=0.5)), Dk=DK, Dv=DV, Hk=HK, Hv=HV)
+    S0 = torch.randn((B, HV, DV, DK), **f32) * 0.05
+    seq = vm.deltanet_sequence(p["Q"], p["K"], p["V"], p["Beta"], p["Gate"], S0)
+    chk = {"O": torch.empty_like(seq["O"]), "Sp": torch.empty_like(S0)}
+    vm.deltanet_sequence_chunked_(chk, p["Q"], p["K"], p["V"], p["Beta"], p["Gate"], S0)
+    torch.cuda.synchronize()
+    for name in ("O", "Sp"):
+        a, b_ = chk[name], seq[name]
+        err = float((a - b_).abs().max() / b_.abs().max())
+        print(f"{name}: max err / max = {err:.2e}")
+        assert err <= 1e-3, name

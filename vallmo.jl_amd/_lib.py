@@ -129,6 +129,8 @@ _SIGS = {
                                         _c_i, _c_i, _c_i, _c_i, _c_f, _p]),
     "vm_deltanet_recurrent_decode": (_c_i, [_p] * 8 + [_c_i] * 5 + [_p]),
     "vm_deltanet_sequence": (_c_i, [_p] * 8 + [_c_i] * 6 + [_p]),
+    "vm_deltanet_sequence_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i]),
+    "vm_deltanet_sequence_chunked": (_c_i, [_p] * 8 + [_c_i] * 6 + [_p, _c_sz, _p]),
     "vm_deltanet_prefill_prep": (_c_i, [_p] * 5 + [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _p]
                                  + [_c_i] * 6 + [_p]),
     "vm_gated_rms_norm": (_c_i, [_p, _c_i64, _c_i64, _p, _p, _c_i64, _c_i64, _p, _c_i, _c_i,

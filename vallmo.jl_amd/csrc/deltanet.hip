@@ -240,6 +240,247 @@ __global__ __launch_bounds__(256) void deltanet_sequence_kernel(DeltaSeqArgs a) 
   store_state<NI>(s, a.s_out + sb, w, lane);
 }
 
+// ---- the chunked form of deltanet_sequence! ---------------------------------
+// Over a chunk of C tokens (G the in-chunk cumulative log decay, gamma = exp G,
+// D_ij = gamma_i / gamma_j) the recurrence's per-token corrections delta_i =
+// beta_i (v_i - alpha_i S_{i-1}^T k_i) satisfy the lower-triangular system
+//     (I + L) delta = beta V - (beta gamma K) S_0,   L_ij = beta_i D_ij k_i.k_j (i > j)
+// so delta = U - W S_0 with U = (I + L)^-1 beta V, W = (I + L)^-1 beta gamma K;
+// then O = gamma Q S_0 + M delta with M_ij = D_ij q_i.k_j (j <= i), and
+// S_C = gamma_C S_0 + K~^T delta with K~_j = (gamma_C / gamma_j) k_j (exact
+// algebra of the sequential update; fp32 throughout).
+// Phase 1 (deltanet_chunk_kernel, chunk-parallel): the Grams, the triangular
+// solve, and every operand of phase 2 written in the fp32 MFMA operand order
+// of v_mfma_f32_16x16x4f32 (A lane l = A[l % 16][l / 16], B lane l =
+// B[l / 16][l % 16], D lane l reg r = D[4 (l / 16) + r][l % 16]), 16 bytes per
+// lane per four k-steps, so phase 2 reads 1 KB contiguous per wave load.
+// Phase 2 (deltanet_scan_kernel, sequential over chunks): one workgroup per 16
+// state columns of a value head; per chunk 112 MFMAs per wave, the next
+// chunk's operands loading into a second register set meanwhile.
+namespace {
+constexpr int DC = 64;   // chunk length
+constexpr int CBW = 16;  // state columns per scan workgroup
+// per (chunk, value head, sequence) unit, floats
+constexpr int UO_W = 0;      // -W:       [w 4][s4 8][lane][4], A[i = r][k = dk]
+constexpr int UO_Q = 8192;   // gamma Q:  same order
+constexpr int UO_M = 16384;  // M:        [w 4][s4 4][lane][4], A[i = r][k = j]
+constexpr int UO_K = 20480;  // K~^T:     [d 8][s4 4][lane][4], A[i = dk][k = r]
+constexpr int UO_U = 28672;  // U:        [cb 8][w 4][lane][4], D[r][dv] tiles
+constexpr int UO_G = 36864;  // gamma_C
+constexpr int UNIT = 36928;  // floats per unit (147 712 B, a multiple of 256)
+
+__device__ __forceinline__ int pos_rowk(int r, int k, int nsteps4) {  // A[i = r][k], 16-row tiles
+  return (((r >> 4) * nsteps4 + (k >> 4)) * 64 + (r & 15) + 16 * (k & 3)) * 4 + ((k >> 2) & 3);
+}
+__device__ __forceinline__ int pos_acc(int r, int dv) {  // D[r][dv], 16 x 16 tiles
+  return ((((dv >> 4) * 4 + (r >> 4)) * 64) + 16 * ((r & 15) >> 2) + (dv & 15)) * 4 + (r & 3);
+}
+}  // namespace
+
+__global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
+  const DeltaSeqArgs& q = a.s;
+  const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
+  const int hk = hv / (q.Hv / q.Hk);
+  const int t0 = c * DC, n = min(DC, q.T - t0);
+  const int NC = (q.T + DC - 1) / DC;
+  float* u = a.ws + ((int64_t)(b * q.Hv + hv) * NC + c) * UNIT;
+  __shared__ __attribute__((aligned(16))) float Ks[DC][132];
+  __shared__ __attribute__((aligned(16))) float Qs[DC][132];
+  __shared__ __attribute__((aligned(16))) float Ls[DC][DC];
+  __shared__ float Gs[DC], Bs[DC], Es[DC];
+  const float* kp = q.k + (((int64_t)b * q.Hk + hk) * q.T + t0) * DN_D;
+  const float* qp = q.q + (((int64_t)b * q.Hk + hk) * q.T + t0) * DN_D;
+  for (int i = t; i < DC * 32; i += 256) {  // float4 (row i / 32, column group i % 32)
+    const int r = i >> 5, c4 = i & 31, rr = min(r, n - 1);  // rows past the end read as 0
+    float4 kv = *reinterpret_cast<const float4*>(kp + rr * DN_D + 4 * c4);
+    float4 qv = *reinterpret_cast<const float4*>(qp + rr * DN_D + 4 * c4);
+    if (r >= n) kv = qv = make_float4(0.f, 0.f, 0.f, 0.f);
+    *reinterpret_cast<float4*>(&Ks[r][4 * c4]) = kv;
+    *reinterpret_cast<float4*>(&Qs[r][4 * c4]) = qv;
+  }
+  if (t < 64) {  // wave 0: gates, inclusive cumulative sum of the log decay
+    const int64_t g = ((int64_t)b * q.T + t0 + min(t, n - 1)) * q.Hv + hv;  // in bounds
+    const float gt = t < n ? q.gate[g] : 0.f;
+    float G = gt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float o = __shfl_up(G, off);
+      if (t >= off) G += o;
+    }
+    Gs[t] = G;
+    Bs[t] = t < n ? q.beta[g] : 0.f;
+    Es[t] = expf(G);
+  }
+  __syncthreads();
+  // Grams: thread (bi, bj) takes rows bi + 16x, columns bj + 16y, x, y < 4
+  const int bi = t >> 4, bj = t & 15;
+  float A[4][4], P[4][4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 4; ++y) A[x][y] = P[x][y] = 0.f;
+  for (int kk = 0; kk < DN_D; kk += 4) {
+    float4 ki[4], qi[4], kj[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      ki[x] = *reinterpret_cast<const float4*>(&Ks[bi + 16 * x][kk]);
+      qi[x] = *reinterpret_cast<const float4*>(&Qs[bi + 16 * x][kk]);
+      kj[x] = *reinterpret_cast<const float4*>(&Ks[bj + 16 * x][kk]);
+    }
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        A[x][y] += ki[x].x * kj[y].x + ki[x].y * kj[y].y + ki[x].z * kj[y].z + ki[x].w * kj[y].w;
+        P[x][y] += qi[x].x * kj[y].x + qi[x].y * kj[y].y + qi[x].z * kj[y].z + qi[x].w * kj[y].w;
+      }
+  }
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 4; ++y) {
+      const int i = bi + 16 * x, j = bj + 16 * y;
+      const float d = j <= i ? expf(Gs[i] - Gs[j]) : 0.f;  // gamma_i / gamma_j
+      Ls[i][j] = i > j ? Bs[i] * d * A[x][y] : 0.f;
+      u[UO_M + pos_rowk(i, j, 4)] = d * P[x][y];
+    }
+  __syncthreads();
+  // (I + L) X = R, R = [beta V | beta gamma K]: thread t owns column t
+  float X[DC];
+  if (t < DN_D) {
+    const float* vp = q.v + (((int64_t)b * q.Hv + hv) * q.T + t0) * DN_D + t;
+#pragma unroll
+    for (int r = 0; r < DC; ++r) X[r] = Bs[r] * vp[(int64_t)min(r, n - 1) * DN_D];  // Bs = 0 past n
+  } else {
+#pragma unroll
+    for (int r = 0; r < DC; ++r) X[r] = Bs[r] * Es[r] * Ks[r][t - DN_D];
+  }
+#pragma unroll
+  for (int i = 1; i < DC; ++i) {
+    float acc[4] = {X[i], 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < i; ++j) acc[j & 3] -= Ls[i][j] * X[j];
+    X[i] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  }
+  if (t < DN_D) {
+#pragma unroll
+    for (int r = 0; r < DC; ++r) u[UO_U + pos_acc(r, t)] = X[r];
+  } else {
+#pragma unroll
+    for (int r = 0; r < DC; ++r) u[UO_W + pos_rowk(r, t - DN_D, 8)] = -X[r];
+  }
+  // gamma Q (A[i = r][k = dk]) and K~^T (A[i = dk][k = r]), gamma_C
+  const float Gl = Gs[DC - 1];
+  for (int i = t; i < DC * DN_D; i += 256) {
+    const int r = i >> 7, dk = i & (DN_D - 1);
+    u[UO_Q + pos_rowk(r, dk, 8)] = Es[r] * Qs[r][dk];
+    u[UO_K + pos_rowk(dk, r, 4)] = expf(Gl - Gs[r]) * Ks[r][dk];
+  }
+  if (t == 0) u[UO_G] = expf(Gl);
+}
+
+namespace {
+struct ScanOps {
+  f32x4 w[8], q[8], m[4], k[8], u;
+  float gl;
+};
+__device__ __forceinline__ void scan_load(ScanOps& o, const float* unit, int w, int cb, int lane) {
+#pragma unroll
+  for (int s4 = 0; s4 < 8; ++s4) {
+    o.w[s4] = *reinterpret_cast<const f32x4*>(unit + UO_W + ((w * 8 + s4) * 64 + lane) * 4);
+    o.q[s4] = *reinterpret_cast<const f32x4*>(unit + UO_Q + ((w * 8 + s4) * 64 + lane) * 4);
+  }
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) {
+    o.m[s4] = *reinterpret_cast<const f32x4*>(unit + UO_M + ((w * 4 + s4) * 64 + lane) * 4);
+    o.k[s4] = *reinterpret_cast<const f32x4*>(unit + UO_K + (((2 * w) * 4 + s4) * 64 + lane) * 4);
+    o.k[4 + s4] =
+        *reinterpret_cast<const f32x4*>(unit + UO_K + (((2 * w + 1) * 4 + s4) * 64 + lane) * 4);
+  }
+  o.u = *reinterpret_cast<const f32x4*>(unit + UO_U + ((cb * 4 + w) * 64 + lane) * 4);
+  o.gl = unit[UO_G];
+}
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+// one chunk: delta = U - W S, O = gamma Q S + M delta, S = gamma_C S + K~^T delta
+__device__ __forceinline__ void scan_chunk(const ScanOps& o, f32x4 (&St)[2], float* Sl, float* Dl,
+                                           const DeltaSeqArgs& q, int b, int hv, int c, int dv0,
+                                           int w, int lane) {
+  const int row4 = lane >> 4, col = lane & 15;
+  f32x4 dacc = o.u, oacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 32; ++s) {
+    const float sv = Sl[(4 * s + row4) * CBW + col];
+    dacc = mfma4(o.w[s >> 2][s & 3], sv, dacc);
+    oacc = mfma4(o.q[s >> 2][s & 3], sv, oacc);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) Dl[(16 * w + 4 * row4 + e) * CBW + col] = dacc[e];
+  __syncthreads();
+  f32x4 s0 = St[0] * o.gl, s1 = St[1] * o.gl;
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const float dv = Dl[(4 * s + row4) * CBW + col];
+    oacc = mfma4(o.m[s >> 2][s & 3], dv, oacc);
+    s0 = mfma4(o.k[s >> 2][s & 3], dv, s0);
+    s1 = mfma4(o.k[4 + (s >> 2)][s & 3], dv, s1);
+  }
+  St[0] = s0;
+  St[1] = s1;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int t = c * DC + 16 * w + 4 * row4 + e;
+    if (t < q.T) q.o[(((int64_t)b * q.Hv + hv) * q.T + t) * DN_D + dv0 + col] = oacc[e];
+  }
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Sl[(16 * (2 * w + x) + 4 * row4 + e) * CBW + col] = St[x][e];
+  __syncthreads();
+}
+}  // namespace
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void deltanet_scan_kernel(DeltaChunkArgs a) {
+  const DeltaSeqArgs& q = a.s;
+  const int HB = q.Hv * q.B;
+  // the 8 column blocks of a head share an XCD (workgroup id mod 8) when HB % 8 == 0
+  const int head = blockIdx.x % HB, cb = blockIdx.x / HB;
+  const int hv = head % q.Hv, b = head / q.Hv;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row4 = lane >> 4, col = lane & 15;
+  __shared__ __attribute__((aligned(16))) float Sl[DN_D * CBW];  // S[dk][c]
+  __shared__ __attribute__((aligned(16))) float Dl[DC * CBW];    // delta[r][c]
+  const int dv0 = cb * CBW;
+  const int64_t sb = ((int64_t)b * q.Hv + hv) * DN_D * DN_D;
+  f32x4 St[2];  // state tiles d = 2w, 2w + 1: lane l reg e = S[16 d + 4 (l / 16) + e][l % 16]
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int d = 2 * w + x;
+    St[x] = *reinterpret_cast<const f32x4*>(q.s_in + sb + (int64_t)(dv0 + col) * DN_D + 16 * d +
+                                            4 * row4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Sl[(16 * d + 4 * row4 + e) * CBW + col] = St[x][e];
+  }
+  __syncthreads();
+  const int NC = (q.T + DC - 1) / DC;
+  const float* units = a.ws + (int64_t)(b * q.Hv + hv) * NC * UNIT;
+  ScanOps o0, o1;
+  scan_load(o0, units, w, cb, lane);
+  for (int c = 0; c < NC; c += 2) {
+    if (c + 1 < NC) scan_load(o1, units + (int64_t)(c + 1) * UNIT, w, cb, lane);
+    scan_chunk(o0, St, Sl, Dl, q, b, hv, c, dv0, w, lane);
+    if (c + 1 >= NC) break;
+    if (c + 2 < NC) scan_load(o0, units + (int64_t)(c + 2) * UNIT, w, cb, lane);
+    scan_chunk(o1, St, Sl, Dl, q, b, hv, c + 1, dv0, w, lane);
+  }
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+    *reinterpret_cast<f32x4*>(q.s_out + sb + (int64_t)(dv0 + col) * DN_D + 16 * (2 * w + x) +
+                              4 * row4) = St[x];
+}
+
 // ---- the prefill's inputs to the recurrence (qwen35.jl:347-356): one wave per
 // (token, head): q / k heads l2-normed (q also by 1/sqrt(Dk)) from the conv
 // output, v heads widened to fp32, gates from the alpha | beta projection.
@@ -422,6 +663,22 @@ hipError_t launch_deltanet_sequence(const DeltaSeqArgs& a, hipStream_t st) {
   } else {
     hipLaunchKernelGGL(deltanet_sequence_kernel<4>, dim3(4, a.Hv, a.B), dim3(256), 0, st, a);
   }
+  return hipGetLastError();
+}
+
+size_t deltanet_chunk_workspace_bytes(int T, int Hv, int B) {
+  const int64_t NC = (T + DC - 1) / DC;
+  return (size_t)NC * Hv * B * UNIT * sizeof(float);
+}
+
+hipError_t launch_deltanet_sequence_chunked(const DeltaChunkArgs& a, hipStream_t st) {
+  const DeltaSeqArgs& q = a.s;
+  if (q.B == 0 || q.T == 0) return launch_deltanet_sequence(q, st);  // state copy / no-op
+  const int NC = (q.T + DC - 1) / DC;
+  hipLaunchKernelGGL(deltanet_chunk_kernel, dim3(NC, q.Hv, q.B), dim3(256), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(deltanet_scan_kernel, dim3(q.Hv * q.B * (DN_D / CBW)), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

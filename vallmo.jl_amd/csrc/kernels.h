@@ -309,6 +309,14 @@ struct Conv1dArgs {
   const uint16_t* bias;
   int D, K, T, B, act;
 };
+// the chunked form of deltanet_sequence!: same arguments, plus a workspace of
+// deltanet_chunk_workspace_bytes(T, Hv, B) bytes (256-byte aligned)
+struct DeltaChunkArgs {
+  DeltaSeqArgs s;
+  float* ws;
+};
+size_t deltanet_chunk_workspace_bytes(int T, int Hv, int B);
+hipError_t launch_deltanet_sequence_chunked(const DeltaChunkArgs& a, hipStream_t st);
 hipError_t launch_deltanet_fused_decode(const DeltaFusedArgs& a, hipStream_t st);
 hipError_t launch_deltanet_sequence(const DeltaSeqArgs& a, hipStream_t st);
 hipError_t launch_deltanet_prep(const DeltaPrepArgs& a, hipStream_t st);

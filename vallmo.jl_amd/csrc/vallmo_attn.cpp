@@ -927,6 +927,42 @@ int vm_deltanet_sequence(float* o, const float* q, const float* k, const float* 
                       "deltanet_sequence");
 }
 
+size_t vm_deltanet_sequence_workspace_bytes(int T, int Hv, int B) {
+  if (T < 0 || Hv <= 0 || B < 0) return (size_t)-1;
+  return vm::deltanet_chunk_workspace_bytes(T, Hv, B);
+}
+
+int vm_deltanet_sequence_chunked(float* o, const float* q, const float* k, const float* v,
+                                 const float* beta, const float* gate, const float* s_in,
+                                 float* s_out, int Dk, int Dv, int T, int Hk, int Hv, int B,
+                                 void* workspace, size_t workspace_bytes, vm_stream st) {
+  const char* what = "deltanet_sequence_chunked";
+  TRY(check_dn_heads(Dk, Dv, Hk, Hv, B, what));
+  REQUIRE(T >= 0, VM_E_ARG, "%s: T = %d", what, T);
+  if (B == 0) return VM_OK;
+  TRY(check_aligned(s_in, "S"));
+  TRY(check_aligned(s_out, "S_out"));
+  TRY(check_alias(s_in, s_out, (size_t)B * Hv * Dk * Dv * sizeof(float), what));
+  if (T > 0) {
+    TRY(check_aligned(o, "O"));
+    TRY(check_aligned(q, "Q"));
+    TRY(check_aligned(k, "K"));
+    TRY(check_aligned(v, "V"));
+    REQUIRE(beta && gate, VM_E_ARG, "%s: NULL Beta or Gate", what);
+    const size_t need = vm::deltanet_chunk_workspace_bytes(T, Hv, B);
+    REQUIRE(workspace && workspace_bytes >= need && (reinterpret_cast<uintptr_t>(workspace) & 255) == 0,
+            VM_E_SCRATCH, "%s: workspace of %zu bytes (256-byte aligned) < %zu required "
+            "(vm_deltanet_sequence_workspace_bytes)", what, workspace_bytes, need);
+  }
+  vm::DeltaChunkArgs a{};
+  a.s.o = o; a.s.q = q; a.s.k = k; a.s.v = v; a.s.beta = beta; a.s.gate = gate; a.s.s_in = s_in;
+  a.s.s_out = s_out; a.s.T = T; a.s.Hk = Hk; a.s.Hv = Hv; a.s.B = B;
+  a.ws = static_cast<float*>(workspace);
+  return hip_status(
+      timed(VM_K_DELTANET, S(st), [&] { return vm::launch_deltanet_sequence_chunked(a, S(st)); }),
+      what);
+}
+
 int vm_deltanet_prefill_prep(float* qe, float* ke, float* ve, float* beta, float* gate,
                              const vm_bf16* cv, int64_t cv_st, int64_t cv_sb, const vm_bf16* ab,
                              int64_t ab_st, int64_t ab_sb, const float* a_log,

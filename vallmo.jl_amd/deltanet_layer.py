@@ -162,7 +162,8 @@ def forward(l: DeltaNetLayer, c: DeltaNetConfig, xn, T: int, B: int, *, eps: flo
     chunk of T tokens per sequence: projections, the sequence conv (zero left
     context at offset 0, else the ring's last K-1 prefix inputs, read in place
     rather than copied, :333-344), the prep (l2 norms, gates), the recurrence in
-    place on S, the gated norm with z, Wout. xn :: (D, T*B) (torch (B, T, D));
+    place on S (deltanet_sequence! in its chunked, MFMA form), the gated norm
+    with z, Wout. xn :: (D, T*B) (torch (B, T, D));
     returns h, torch (B, T, D). Eager: allocates its temporaries.
     ``workspace_for(x, W)`` returns a projection workspace for that problem."""
     D = xn.shape[-1]
@@ -181,7 +182,8 @@ def forward(l: DeltaNetLayer, c: DeltaNetConfig, xn, T: int, B: int, *, eps: flo
     ops.deltanet_prefill_prep_(p, conv, ab, l.A_log, l.dt_bias, Dk=c.Dk, Dv=c.Dv, Hk=c.Hk,
                                Hv=c.Hv)
     o = torch.empty((B, c.Hv, T, c.Dv), **f32)
-    ops.deltanet_sequence_({"O": o, "Sp": l.S}, p["Q"], p["K"], p["V"], p["Beta"], p["Gate"], l.S)
+    ops.deltanet_sequence_chunked_({"O": o, "Sp": l.S}, p["Q"], p["K"], p["V"], p["Beta"],
+                                   p["Gate"], l.S)
     y = torch.empty((B, T, c.Hv, c.Dv), dtype=torch.bfloat16, device=xn.device)
     ops.gated_rms_norm_(y, o, z.unflatten(-1, (c.Hv, c.Dv)), l.gnorm_w, eps=eps)
     y2 = y.view(B * T, c.Hv * c.Dv)

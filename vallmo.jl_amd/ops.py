@@ -30,6 +30,7 @@ __all__ = [
     "fused_deltanet_decode_", "fused_deltanet_decode", "deltanet_recurrent_decode_",
     "deltanet_recurrent_decode", "deltanet_sequence_", "deltanet_sequence",
     "deltanet_prefill_prep_", "gated_rms_norm_", "linear_add_rms_norm_",
+    "deltanet_sequence_chunked_", "deltanet_sequence_workspace_bytes",
     "linear_add_rms_norm_workspace_bytes",
 ]
 
@@ -571,6 +572,30 @@ def deltanet_sequence_(outs, Q, K, V, Beta, Gate, S):
                               "Dk T Hk B", "Dv T Hv B", "Hv T B")
     call("vm_deltanet_sequence", _p(O), _p(Q), _p(K), _p(V), _p(Beta), _p(Gate), _p(S), _p(Sp),
          d["Dk"], d["Dv"], d["T"], d["Hk"], d["Hv"], d["B"], _stream())
+    return outs
+
+
+def deltanet_sequence_workspace_bytes(T: int, Hv: int, B: int) -> int:
+    """Workspace of deltanet_sequence_chunked_ (147 712 B per 64-token chunk per
+    value head and sequence)."""
+    return int(_lib.load().vm_deltanet_sequence_workspace_bytes(T, Hv, B))
+
+
+def deltanet_sequence_chunked_(outs, Q, K, V, Beta, Gate, S, *, workspace=None):
+    """deltanet_sequence! computed per 64-token chunk (a triangular solve and fp32
+    MFMA products, the chunks' state carried by one scan): the same operator and
+    arguments as deltanet_sequence_ (deltanet_recurrent.jl:174-198), results
+    equal to fp32 rounding. workspace: a uint8 GPU tensor of at least
+    deltanet_sequence_workspace_bytes(T, Hv, B), 256-byte aligned (allocated
+    here when None)."""
+    O, Sp, d = _deltanet_fp32("deltanet_sequence", outs, Q, K, V, Beta, Gate, S,
+                              "Dk T Hk B", "Dv T Hv B", "Hv T B")
+    need = deltanet_sequence_workspace_bytes(d["T"], d["Hv"], d["B"])
+    if workspace is None:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=Q.device)
+    call("vm_deltanet_sequence_chunked", _p(O), _p(Q), _p(K), _p(V), _p(Beta), _p(Gate), _p(S),
+         _p(Sp), d["Dk"], d["Dv"], d["T"], d["Hk"], d["Hv"], d["B"], _p(workspace),
+         workspace.numel(), _stream())
     return outs
 
 
