@@ -412,7 +412,7 @@ int vm_deltanet_sequence(float* o, const float* q, const float* k, const float* 
  * function: the reference runs the sequential loop (deltanet_recurrent.jl:
  * 109-172); this is the same operator, parallel over each chunk. workspace:
  * vm_deltanet_sequence_workspace_bytes(T, Hv, B) bytes, 256-byte aligned
- * (147 712 B per 64-token chunk per value head and sequence). */
+ * (147 968 B per 64-token chunk per value head and sequence). */
 size_t vm_deltanet_sequence_workspace_bytes(int T, int Hv, int B);
 int vm_deltanet_sequence_chunked(float* o, const float* q, const float* k, const float* v,
                                  const float* beta, const float* gate, const float* s_in,

@@ -267,7 +267,7 @@ constexpr int UO_M = 16384;  // M:        [w 4][s4 4][lane][4], A[i = r][k = j]
 constexpr int UO_K = 20480;  // K~^T:     [d 8][s4 4][lane][4], A[i = dk][k = r]
 constexpr int UO_U = 28672;  // U:        [cb 8][w 4][lane][4], D[r][dv] tiles
 constexpr int UO_G = 36864;  // gamma_C
-constexpr int UNIT = 36928;  // floats per unit (147 712 B, a multiple of 256)
+constexpr int UNIT = 36992;  // floats per unit (147 968 B, a multiple of 256)
 
 __device__ __forceinline__ int pos_rowk(int r, int k, int nsteps4) {  // A[i = r][k], 16-row tiles
   return (((r >> 4) * nsteps4 + (k >> 4)) * 64 + (r & 15) + 16 * (k & 3)) * 4 + ((k >> 2) & 3);
@@ -283,20 +283,26 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
   const int hk = hv / (q.Hv / q.Hk);
   const int t0 = c * DC, n = min(DC, q.T - t0);
   const int NC = (q.T + DC - 1) / DC;
-  float* u = a.ws + ((int64_t)(b * q.Hv + hv) * NC + c) * UNIT;
+  float* u = a.ws + ((int64_t)(b * q.Hv + hv) * (NC + 1) + c) * UNIT;
+  if (c == 0) {  // unit NC: the identity chunk (all zero, gamma_C = 1), the scan's pad
+    float* id = u + (int64_t)NC * UNIT;
+    for (int i = t; i < UNIT / 4; i += 256)
+      reinterpret_cast<float4*>(id)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    __syncthreads();
+    if (t == 0) id[UO_G] = 1.f;
+  }
+  // K (later the -W rows) and L (later M) in LDS, ~51 KB: three workgroups per
+  // CU; Q is read from global memory (L2) where it is used
   __shared__ __attribute__((aligned(16))) float Ks[DC][132];
-  __shared__ __attribute__((aligned(16))) float Qs[DC][132];
-  __shared__ __attribute__((aligned(16))) float Ls[DC][DC];
+  __shared__ float Ls[DC][DC + 1];
   __shared__ float Gs[DC], Bs[DC], Es[DC];
   const float* kp = q.k + (((int64_t)b * q.Hk + hk) * q.T + t0) * DN_D;
   const float* qp = q.q + (((int64_t)b * q.Hk + hk) * q.T + t0) * DN_D;
   for (int i = t; i < DC * 32; i += 256) {  // float4 (row i / 32, column group i % 32)
     const int r = i >> 5, c4 = i & 31, rr = min(r, n - 1);  // rows past the end read as 0
     float4 kv = *reinterpret_cast<const float4*>(kp + rr * DN_D + 4 * c4);
-    float4 qv = *reinterpret_cast<const float4*>(qp + rr * DN_D + 4 * c4);
-    if (r >= n) kv = qv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r >= n) kv = make_float4(0.f, 0.f, 0.f, 0.f);
     *reinterpret_cast<float4*>(&Ks[r][4 * c4]) = kv;
-    *reinterpret_cast<float4*>(&Qs[r][4 * c4]) = qv;
   }
   if (t < 64) {  // wave 0: gates, inclusive cumulative sum of the log decay
     const int64_t g = ((int64_t)b * q.T + t0 + min(t, n - 1)) * q.Hv + hv;  // in bounds
@@ -314,6 +320,13 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
   __syncthreads();
   // Grams: thread (bi, bj) takes rows bi + 16x, columns bj + 16y, x, y < 4
   const int bi = t >> 4, bj = t & 15;
+  const float* qrow[4];  // this thread's Q rows (a row past the end reads as row n-1, masked)
+  float qmask[4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    qrow[x] = qp + (int64_t)min(bi + 16 * x, n - 1) * DN_D;
+    qmask[x] = bi + 16 * x < n ? 1.f : 0.f;
+  }
   float A[4][4], P[4][4];
 #pragma unroll
   for (int x = 0; x < 4; ++x)
@@ -324,7 +337,7 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
       ki[x] = *reinterpret_cast<const float4*>(&Ks[bi + 16 * x][kk]);
-      qi[x] = *reinterpret_cast<const float4*>(&Qs[bi + 16 * x][kk]);
+      qi[x] = *reinterpret_cast<const float4*>(qrow[x] + kk);
       kj[x] = *reinterpret_cast<const float4*>(&Ks[bj + 16 * x][kk]);
     }
 #pragma unroll
@@ -342,8 +355,28 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
       const int i = bi + 16 * x, j = bj + 16 * y;
       const float d = j <= i ? expf(Gs[i] - Gs[j]) : 0.f;  // gamma_i / gamma_j
       Ls[i][j] = i > j ? Bs[i] * d * A[x][y] : 0.f;
-      u[UO_M + pos_rowk(i, j, 4)] = d * P[x][y];
+      P[x][y] *= d * qmask[x];                             // M, kept for later
     }
+  // gamma Q and K~^T in operand order, one coalesced float4 per lane and slot
+  const float Gl = Gs[DC - 1];
+  for (int f = t; f < 2048; f += 256) {
+    const int l = f & 63;
+    {  // gamma Q: tile f / 512, s4 (f / 64) % 8: row 16 w + l % 16, k = 16 s4 + l / 16 + 4 e
+      const int r = 16 * (f >> 9) + (l & 15), kb = 16 * ((f >> 6) & 7) + (l >> 4);
+      const float e = r < n ? Es[r] : 0.f;
+      const float* qr = qp + (int64_t)min(r, n - 1) * DN_D + kb;
+      *reinterpret_cast<float4*>(u + UO_Q + 4 * f) =
+          make_float4(e * qr[0], e * qr[4], e * qr[8], e * qr[12]);
+    }
+    {  // K~^T: tile f / 256, s4 (f / 64) % 4: dk 16 d + l % 16, r = 16 s4 + l / 16 + 4 e
+      const int dk = 16 * (f >> 8) + (l & 15), rb = 16 * ((f >> 6) & 3) + (l >> 4);
+      float v4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v4[e] = expf(Gl - Gs[rb + 4 * e]) * Ks[rb + 4 * e][dk];
+      *reinterpret_cast<float4*>(u + UO_K + 4 * f) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+    }
+  }
+  if (t == 0) u[UO_G] = expf(Gl);
   __syncthreads();
   // (I + L) X = R, R = [beta V | beta gamma K]: thread t owns column t
   float X[DC];
@@ -362,34 +395,55 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
     for (int j = 0; j < i; ++j) acc[j & 3] -= Ls[i][j] * X[j];
     X[i] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   }
-  if (t < DN_D) {
+  __syncthreads();  // L and K are free: M and -W staged there
+  if (t < DN_D) {   // U: rows 4qq .. 4qq + 3 of column t are one accumulator float4
 #pragma unroll
-    for (int r = 0; r < DC; ++r) u[UO_U + pos_acc(r, t)] = X[r];
+    for (int qq = 0; qq < DC / 4; ++qq)
+      *reinterpret_cast<float4*>(u + UO_U + pos_acc(4 * qq, t)) =
+          make_float4(X[4 * qq], X[4 * qq + 1], X[4 * qq + 2], X[4 * qq + 3]);
   } else {
 #pragma unroll
-    for (int r = 0; r < DC; ++r) u[UO_W + pos_rowk(r, t - DN_D, 8)] = -X[r];
+    for (int r = 0; r < DC; ++r) Ks[r][t - DN_D] = -X[r];
   }
-  // gamma Q (A[i = r][k = dk]) and K~^T (A[i = dk][k = r]), gamma_C
-  const float Gl = Gs[DC - 1];
-  for (int i = t; i < DC * DN_D; i += 256) {
-    const int r = i >> 7, dk = i & (DN_D - 1);
-    u[UO_Q + pos_rowk(r, dk, 8)] = Es[r] * Qs[r][dk];
-    u[UO_K + pos_rowk(dk, r, 4)] = expf(Gl - Gs[r]) * Ks[r][dk];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 4; ++y) Ls[bi + 16 * x][bj + 16 * y] = P[x][y];
+  __syncthreads();
+  for (int f = t; f < 2048; f += 256) {  // -W: the gamma Q order
+    const int l = f & 63;
+    const int r = 16 * (f >> 9) + (l & 15), kb = 16 * ((f >> 6) & 7) + (l >> 4);
+    *reinterpret_cast<float4*>(u + UO_W + 4 * f) =
+        make_float4(Ks[r][kb], Ks[r][kb + 4], Ks[r][kb + 8], Ks[r][kb + 12]);
   }
-  if (t == 0) u[UO_G] = expf(Gl);
+  for (int f = t; f < 1024; f += 256) {  // M: tile f / 256, s4 (f / 64) % 4
+    const int l = f & 63;
+    const int r = 16 * (f >> 8) + (l & 15), jb = 16 * ((f >> 6) & 3) + (l >> 4);
+    *reinterpret_cast<float4*>(u + UO_M + 4 * f) =
+        make_float4(Ls[r][jb], Ls[r][jb + 4], Ls[r][jb + 8], Ls[r][jb + 12]);
+  }
 }
 
 namespace {
-struct ScanOps {
-  f32x4 w[8], q[8], m[4], k[8], u;
+// a chunk's operands, split by the step that consumes them: step A (the S
+// products) and step B (the delta products)
+struct ScanOpsA {
+  f32x4 w[8], q[8], u;
+};
+struct ScanOpsB {
+  f32x4 m[4], k[8];
   float gl;
 };
-__device__ __forceinline__ void scan_load(ScanOps& o, const float* unit, int w, int cb, int lane) {
+__device__ __forceinline__ void scan_load_a(ScanOpsA& o, const float* unit, int w, int cb,
+                                            int lane) {
 #pragma unroll
   for (int s4 = 0; s4 < 8; ++s4) {
     o.w[s4] = *reinterpret_cast<const f32x4*>(unit + UO_W + ((w * 8 + s4) * 64 + lane) * 4);
     o.q[s4] = *reinterpret_cast<const f32x4*>(unit + UO_Q + ((w * 8 + s4) * 64 + lane) * 4);
   }
+  o.u = *reinterpret_cast<const f32x4*>(unit + UO_U + ((cb * 4 + w) * 64 + lane) * 4);
+}
+__device__ __forceinline__ void scan_load_b(ScanOpsB& o, const float* unit, int w, int lane) {
 #pragma unroll
   for (int s4 = 0; s4 < 4; ++s4) {
     o.m[s4] = *reinterpret_cast<const f32x4*>(unit + UO_M + ((w * 4 + s4) * 64 + lane) * 4);
@@ -397,41 +451,43 @@ __device__ __forceinline__ void scan_load(ScanOps& o, const float* unit, int w, 
     o.k[4 + s4] =
         *reinterpret_cast<const f32x4*>(unit + UO_K + (((2 * w + 1) * 4 + s4) * 64 + lane) * 4);
   }
-  o.u = *reinterpret_cast<const f32x4*>(unit + UO_U + ((cb * 4 + w) * 64 + lane) * 4);
   o.gl = unit[UO_G];
 }
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
-// one chunk: delta = U - W S, O = gamma Q S + M delta, S = gamma_C S + K~^T delta
-__device__ __forceinline__ void scan_chunk(const ScanOps& o, f32x4 (&St)[2], float* Sl, float* Dl,
-                                           const DeltaSeqArgs& q, int b, int hv, int c, int dv0,
-                                           int w, int lane) {
+// one chunk: delta = U - W S, Og = gamma Q S (step A), then O = Og + M delta,
+// S = gamma_C S + K~^T delta (step B). Rows past T are stored to `spare`.
+__device__ __forceinline__ void scan_chunk(const ScanOpsA& oa, const ScanOpsB& ob, f32x4 (&St)[2],
+                                           float* Sl, float* Dl, const DeltaSeqArgs& q, int b,
+                                           int hv, int c, int dv0, int w, int lane, float* spare) {
   const int row4 = lane >> 4, col = lane & 15;
-  f32x4 dacc = o.u, oacc = {0.f, 0.f, 0.f, 0.f};
+  f32x4 dacc = oa.u, oacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < 32; ++s) {
     const float sv = Sl[(4 * s + row4) * CBW + col];
-    dacc = mfma4(o.w[s >> 2][s & 3], sv, dacc);
-    oacc = mfma4(o.q[s >> 2][s & 3], sv, oacc);
+    dacc = mfma4(oa.w[s >> 2][s & 3], sv, dacc);
+    oacc = mfma4(oa.q[s >> 2][s & 3], sv, oacc);
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) Dl[(16 * w + 4 * row4 + e) * CBW + col] = dacc[e];
   __syncthreads();
-  f32x4 s0 = St[0] * o.gl, s1 = St[1] * o.gl;
+  f32x4 s0 = St[0] * ob.gl, s1 = St[1] * ob.gl;
 #pragma unroll
   for (int s = 0; s < 16; ++s) {
     const float dv = Dl[(4 * s + row4) * CBW + col];
-    oacc = mfma4(o.m[s >> 2][s & 3], dv, oacc);
-    s0 = mfma4(o.k[s >> 2][s & 3], dv, s0);
-    s1 = mfma4(o.k[4 + (s >> 2)][s & 3], dv, s1);
+    oacc = mfma4(ob.m[s >> 2][s & 3], dv, oacc);
+    s0 = mfma4(ob.k[s >> 2][s & 3], dv, s0);
+    s1 = mfma4(ob.k[4 + (s >> 2)][s & 3], dv, s1);
   }
   St[0] = s0;
   St[1] = s1;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int t = c * DC + 16 * w + 4 * row4 + e;
-    if (t < q.T) q.o[(((int64_t)b * q.Hv + hv) * q.T + t) * DN_D + dv0 + col] = oacc[e];
+    float* dst =
+        t < q.T ? q.o + (((int64_t)b * q.Hv + hv) * q.T + t) * DN_D + dv0 + col : spare + lane;
+    *dst = oacc[e];
   }
 #pragma unroll
   for (int x = 0; x < 2; ++x)
@@ -463,17 +519,31 @@ void deltanet_scan_kernel(DeltaChunkArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) Sl[(16 * d + 4 * row4 + e) * CBW + col] = St[x][e];
   }
-  __syncthreads();
   const int NC = (q.T + DC - 1) / DC;
-  const float* units = a.ws + (int64_t)(b * q.Hv + hv) * NC * UNIT;
-  ScanOps o0, o1;
-  scan_load(o0, units, w, cb, lane);
+  const float* units = a.ws + (int64_t)(b * q.Hv + hv) * (NC + 1) * UNIT;
+  // the identity unit's spare tail (UNIT - UO_G - 1 >= 64 floats): a sink for the
+  // padded rows of the last chunks, never read
+  float* spare = a.ws + ((int64_t)(b * q.Hv + hv) * (NC + 1) + NC) * UNIT + UO_G + 1;
+  static_assert(UNIT - UO_G - 1 >= 64, "spare tail");
+  // Two register sets, chunks in pairs, each set reloaded two chunks ahead right
+  // after its chunk; chunk indices past the end read the identity unit (an odd
+  // count pads with it). Branch-free, so the compiler's waits count exactly.
+  ScanOpsA ax, ay;
+  ScanOpsB bx, by;
+  scan_load_a(ax, units, w, cb, lane);
+  scan_load_b(bx, units, w, lane);
+  scan_load_a(ay, units + (int64_t)min(1, NC) * UNIT, w, cb, lane);
+  scan_load_b(by, units + (int64_t)min(1, NC) * UNIT, w, lane);
+  __syncthreads();
   for (int c = 0; c < NC; c += 2) {
-    if (c + 1 < NC) scan_load(o1, units + (int64_t)(c + 1) * UNIT, w, cb, lane);
-    scan_chunk(o0, St, Sl, Dl, q, b, hv, c, dv0, w, lane);
-    if (c + 1 >= NC) break;
-    if (c + 2 < NC) scan_load(o0, units + (int64_t)(c + 2) * UNIT, w, cb, lane);
-    scan_chunk(o1, St, Sl, Dl, q, b, hv, c + 1, dv0, w, lane);
+    scan_chunk(ax, bx, St, Sl, Dl, q, b, hv, c, dv0, w, lane, spare);
+    const float* u2 = units + (int64_t)min(c + 2, NC) * UNIT;
+    scan_load_a(ax, u2, w, cb, lane);
+    scan_load_b(bx, u2, w, lane);
+    scan_chunk(ay, by, St, Sl, Dl, q, b, hv, c + 1, dv0, w, lane, spare);
+    const float* u3 = units + (int64_t)min(c + 3, NC) * UNIT;
+    scan_load_a(ay, u3, w, cb, lane);
+    scan_load_b(by, u3, w, lane);
   }
 #pragma unroll
   for (int x = 0; x < 2; ++x)
@@ -668,7 +738,7 @@ hipError_t launch_deltanet_sequence(const DeltaSeqArgs& a, hipStream_t st) {
 
 size_t deltanet_chunk_workspace_bytes(int T, int Hv, int B) {
   const int64_t NC = (T + DC - 1) / DC;
-  return (size_t)NC * Hv * B * UNIT * sizeof(float);
+  return (size_t)(NC + 1) * Hv * B * UNIT * sizeof(float);  // + the identity unit per head
 }
 
 hipError_t launch_deltanet_sequence_chunked(const DeltaChunkArgs& a, hipStream_t st) {

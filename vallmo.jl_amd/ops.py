@@ -576,7 +576,7 @@ def deltanet_sequence_(outs, Q, K, V, Beta, Gate, S):
 
 
 def deltanet_sequence_workspace_bytes(T: int, Hv: int, B: int) -> int:
-    """Workspace of deltanet_sequence_chunked_ (147 712 B per 64-token chunk per
+    """Workspace of deltanet_sequence_chunked_ (147 968 B per 64-token chunk per
     value head and sequence)."""
     return int(_lib.load().vm_deltanet_sequence_workspace_bytes(T, Hv, B))
 
