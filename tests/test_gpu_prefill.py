@@ -322,3 +322,71 @@ def test_prefill_q_norm_rope_operator(vm, orc):
     print(f"prefill q norm+rope: max {mx:.3e} mean {mn:.3e}")
     assert mx <= TOL_MAX and mn <= TOL_MEAN
     assert np.all(got[~fin] == 7.0)
+
+
+# ---- paired items: one sequence, causal, >= 2 items per CU (H n_qt >= 2 x 256) --
+# Each workgroup of the fused kernel then runs a heavy and a light q-block of
+# one head; B > 1 keeps one item per workgroup. Per item the arithmetic is the
+# same either way.
+
+def test_paired_prefill_equals_one_item_per_workgroup(vm):
+    """B = 1, T = 4096 (paired workgroups) against the same sequence twice at
+    B = 2 (one item per workgroup): outputs and appended cache rows bit-equal."""
+    banner("paired prefill == unpaired (B=1 vs B=2 copies, T=4096)")
+    T, ctx = 4096, 4096
+    qw, kw = to_dev(normal_bf16((D,), 301, scale=0.05)), to_dev(normal_bf16((D,), 302, scale=0.05))
+    qkv1 = torch.empty((1, T, S, D), dtype=torch.bfloat16, device="cuda")
+    vm.fill_normal_(qkv1, 303)
+    outs, caches = [], []
+    for B in (1, 2):
+        cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
+        m = vm.AttnModel(cfg)
+        layer = vm.attn_layer(cfg, qw, kw)
+        qkv = qkv1.expand(B, -1, -1, -1).contiguous()
+        outs.append(vm.gated_attn_prefill(layer, m, qkv, T, B))
+        caches.append((layer.K_cache, layer.V_cache))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][0], outs[1][1])
+    assert torch.equal(caches[0][0][0], caches[1][0][0]) and torch.equal(caches[0][1][0], caches[1][1][0])
+
+
+def test_paired_prefill_prior_and_short_chunk(vm, orc):
+    """Paired workgroups after 300 cached tokens with q_lengths = 2999 of T = 4096:
+    the heavy q-blocks past the chunk return at once and their light partners
+    still run; every 16th row against the oracle, every appended row checked."""
+    banner("paired prefill prior=300 q_len=2999 T=4096")
+    (mx, mn), (kmx, kmn), ok, _ = _fused(vm, orc, 1, 4096, 4396, np.array([300], np.int32),
+                                         np.array([2999], np.int32), 310, row_step=16,
+                                         fill_gpu=True)
+    print(f"paired prior: out max {mx:.3e} mean {mn:.3e}; K max {kmx:.3e} mean {kmn:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN and kmx <= TOL_MAX and kmn <= TOL_MEAN and ok
+
+
+def test_paired_prefill_online_max_path(vm, orc):
+    """The online running-max path (kw[0] = 4 lifts the logit bound past 64) on
+    paired workgroups (B = 1, T = 4096); every 16th row against the oracle."""
+    banner("paired prefill online-max path T=4096")
+    B, T, ctx = 1, 4096, 4096
+    cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
+    qw = normal_bf16((D,), 321, scale=0.05)
+    kw = normal_bf16((D,), 322, scale=0.05)
+    kw[0] = 0x4080  # bf16 4.0
+    K = torch.empty((B, HK, ctx, D), dtype=torch.bfloat16, device="cuda")
+    V = torch.empty_like(K)
+    vm.fill_normal_(K, 323)
+    vm.fill_normal_(V, 324)
+    kc, vc = from_dev(K), from_dev(V)
+    qkv = normal_bf16((B, T, S, D), 325)
+    m = vm.AttnModel(cfg)
+    layer = vm.AttnLayer(qw=to_dev(qw), kw=to_dev(kw), K_cache=K, V_cache=V)
+    prior, qlen = np.zeros(1, np.int32), np.full(1, T, np.int32)
+    out = vm.gated_attn_prefill(layer, m, to_dev(qkv), T, B, prior=i32(prior), q_lengths=i32(qlen))
+    torch.cuda.synchronize()
+    c, s = orc.rope_tables(HALF, ctx, THETA)
+    ref, _, _ = orc.gated_prefill(qkv, kc, vc, prior, qlen, qw, kw, c, s, Hq=HQ, Hk=HK, eps=EPS,
+                                  w_offset=1.0, row_step=16)
+    got = dev_f32(out).reshape(B, T, HQ, D)
+    fin = ~np.isnan(ref)
+    mx, mn = maxmean(got[fin], ref[fin])
+    print(f"paired online-max: out max {mx:.3e} mean {mn:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN

@@ -91,6 +91,7 @@ struct PrefillArgs {
   int B, H, Hk, L, Lk, n_qt, causal;
   const uint16_t* vt;        // fused path: V^T tiles of the attended keys (workspace)
   int vt_tiles;              // tiles per (b, hk) in the workspace: ceil(Lk / 32)
+  int pairs;                 // fused path, set by the launcher: one heavy + one light item per workgroup
 };
 
 // V cache -> V^T tiles for the fused prefill (one 16-KB tile per 32 keys)

@@ -270,12 +270,14 @@ struct ItemGeo {
   int b, h, hk, r0, q_len, prior, k_len, off, kend;
 };
 
-__device__ __forceinline__ ItemGeo item_geo(const PrefillArgs& a, const FItem& it, bool causal) {
+// q_len_raw, prior: q_lengths[b] (or L) and prior[b] (or 0), loaded by the caller
+__device__ __forceinline__ ItemGeo item_geo(const PrefillArgs& a, const FItem& it, bool causal,
+                                            int q_len_raw, int prior) {
   ItemGeo ig;
   ig.b = it.b; ig.h = it.h; ig.hk = it.hk;
   ig.r0 = it.qt * FM;
-  ig.q_len = a.q_lengths ? min(a.q_lengths[it.b], a.L) : a.L;
-  ig.prior = a.prior ? a.prior[it.b] : 0;
+  ig.q_len = min(q_len_raw, a.L);
+  ig.prior = prior;
   // queries are the suffix of the attended keys: row t sits at position prior + t.
   // prior + q_len > Lk is out of contract (those keys were never appended): the
   // keys past the cache are masked rather than read
@@ -326,8 +328,9 @@ __device__ __forceinline__ void q_load_w(const PrefillArgs& a, int h2, u32x4 (&w
 }
 
 // q rows of one 32-row block: qnorm_rope (src/kernels/qknorm_rope_append.jl:25-57)
-// and the 1/16 scale, with the per-row 1/rms folded into that final scale (RoPE
-// is linear); lane holds q[row][16kk + 8h2 + j]
+// and the 1/16 scale. RoPE is linear, so the per-row 1/rms and the scale fold
+// into the weight factor: x (w + offset) scale = x fma(w, scale, offset scale).
+// Lane holds q[row][16kk + 8h2 + j]
 __device__ __forceinline__ void q_prologue(const PrefillArgs& a, const QLoads& ql, uint4 (&qop)[16]) {
   // sum of squares straight from the packed pairs (bf16 products are exact in f32)
   float ss = 0.f;
@@ -341,6 +344,7 @@ __device__ __forceinline__ void q_prologue(const PrefillArgs& a, const QLoads& q
   }
   ss += __shfl_xor(ss, 32, 64);
   const float scale = QK_SCALE * LOG2E / sqrtf(ss * (1.0f / HEAD_DIM) + a.eps);
+  const float wscale = a.w_offset * scale;  // x (w + offset) scale = x fma(w, scale, offset scale)
   const float* cs = reinterpret_cast<const float*>(ql.cv);
   const float* sn = reinterpret_cast<const float*>(ql.sv);
 #pragma unroll
@@ -350,7 +354,7 @@ __device__ __forceinline__ void q_prologue(const PrefillArgs& a, const QLoads& q
     unpack8(ql.qraw[kk], x1);
     unpack8(ql.qwv[kk], wf);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x1[j] *= wf[j] + a.w_offset;
+    for (int j = 0; j < 8; ++j) x1[j] *= fmaf(wf[j], scale, wscale);
     if (kk < 2) {
       // d-steps 0..3 carry the rotary dims: pairs (d, d + 32) = d-steps (kk, kk + 2)
       float x2[8];
@@ -358,19 +362,15 @@ __device__ __forceinline__ void q_prologue(const PrefillArgs& a, const QLoads& q
       unpack8(ql.qwv[kk + 2], wf);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        x2[j] *= wf[j] + a.w_offset;
+        x2[j] *= fmaf(wf[j], scale, wscale);
         const float cc = cs[8 * kk + j], si = sn[8 * kk + j];
         const float r1 = x1[j] * cc - x2[j] * si;
         const float r2 = x2[j] * cc + x1[j] * si;
         x1[j] = r1;
         x2[j] = r2;
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) x2[j] *= scale;
       qop[kk + 2] = pack8(x2);
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x1[j] *= scale;
     qop[kk] = pack8(x1);
   }
 }
@@ -557,10 +557,11 @@ __device__ __forceinline__ void pv_w(f32x16& o, const u32x4& v, const u32x4& p) 
 
 // Slot m of step i: QK d-step m of both tiles of block i + 2, PV d-blocks
 // 2(m & 3), 2(m & 3) + 1 of key step m >> 2 of block i, softmax word m of block
-// i + 1, one LDS read of slot m + 2 after each product, and one of this wave's 16
-// tile loads of the step: V^T of block i + 1 (m < 8, needed next step), K of
-// block i + 4 (needed two steps on; kd: its object; ks, vs: the tiles' sources).
-// The VALU work sits between the products (fences keep it there).
+// i + 1, one LDS read of slot m + 2 after each product, and this wave's tile
+// loads of the step: two pieces of V^T block i + 1 in each of slots 0-3 (needed
+// next step, so issued first), one piece of K block i + 4 in each of slots 4-11
+// (needed two steps on; kd: its object; ks, vs: the tiles' sources). The VALU
+// work sits between the products (fences keep it there).
 template <bool SHIFT, bool QK, bool SM, bool PV, bool DV, bool FIRST, int J, int M>
 __device__ __forceinline__ void solo_slot(SoloState& st, const SoloCtx& sc, const SoloLds& L,
                                           const uint32_t (&kb)[8], uint16_t* kd, const TileSrc (&ks)[2],
@@ -623,10 +624,13 @@ __device__ __forceinline__ void solo_slot(SoloState& st, const SoloCtx& sc, cons
     }
   }
 #undef SLOT_READ
-  if constexpr (M < 8) {
-    if constexpr (DV) v_piece<M & 3>(sc, vs[M >> 2].p, L.v + (1 - J) * (2 * FT) + (M >> 2) * FT);
-  } else {
-    k_piece<M & 3>(sc.c, ks[(M - 8) >> 2], kd + ((M - 8) >> 2) * FT);
+  if constexpr (M < 4) {
+    if constexpr (DV) {
+      v_piece<(2 * M) & 3>(sc, vs[M >> 1].p, L.v + (1 - J) * (2 * FT) + (M >> 1) * FT);
+      v_piece<(2 * M + 1) & 3>(sc, vs[M >> 1].p, L.v + (1 - J) * (2 * FT) + (M >> 1) * FT);
+    }
+  } else if constexpr (M < 12) {
+    k_piece<(M - 4) & 3>(sc.c, ks[(M - 4) >> 2], kd + ((M - 4) >> 2) * FT);
   }
   sfence();
 }
@@ -837,10 +841,11 @@ __device__ __forceinline__ void q_read_lds(QLoads& ql, const SoloLds& L, int wav
 // P = exp2(S) needs no shift (the normalisation cancels any common scale);
 // SHIFT = true: an exact row-max pass first, P = exp2(S - row max).
 template <bool CAUSAL, bool SHIFT>
-__device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it, const SoloLds& L) {
+__device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it, const SoloLds& L,
+                                          int q_len_raw, int prior) {
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int l32 = lane & 31, h2 = lane >> 5;
-  const ItemGeo ig = item_geo(a, it, CAUSAL);
+  const ItemGeo ig = item_geo(a, it, CAUSAL, q_len_raw, prior);
   SoloGeo g;
   g.wrow0 = ig.r0 + 32 * wave;
   g.row = g.wrow0 + l32;
@@ -936,7 +941,9 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's own writes are in
   asm volatile("" ::: "memory");
   const float l_tot = st.lsum + __shfl_xor(st.lsum, 32, 64);
-  const float inv = l_tot > 0.f ? fast_rcp(l_tot) : 0.f;  // fully-masked row -> 0
+  // o sigma(g) / l = o / (l + l 2^(-g log2 e)); a fully-masked row (l = 0, o = 0)
+  // takes a finite stand-in for l, so its output stays 0 for every gate
+  const float lt = l_tot > 0.f ? l_tot : 3.0e38f;
   uint2 ov[8][4];
 #pragma unroll
   for (int db = 0; db < 8; ++db) {
@@ -945,10 +952,10 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
     for (int jb = 0; jb < 4; ++jb) {
       const int d0 = 32 * db + 8 * jb + 4 * eh;
       const uint2 g2 = *reinterpret_cast<const uint2*>(xr + el * XROW + d0);
-      const float o0 = acc[4 * jb + 0] * inv * sigmoidf(__uint_as_float(g2.x << 16));
-      const float o1 = acc[4 * jb + 1] * inv * sigmoidf(__uint_as_float(g2.x & 0xffff0000u));
-      const float o2 = acc[4 * jb + 2] * inv * sigmoidf(__uint_as_float(g2.y << 16));
-      const float o3 = acc[4 * jb + 3] * inv * sigmoidf(__uint_as_float(g2.y & 0xffff0000u));
+      const float o0 = acc[4 * jb + 0] * fast_rcp(fmaf(lt, fast_exp2(__uint_as_float(g2.x << 16) * -LOG2E), lt));
+      const float o1 = acc[4 * jb + 1] * fast_rcp(fmaf(lt, fast_exp2(__uint_as_float(g2.x & 0xffff0000u) * -LOG2E), lt));
+      const float o2 = acc[4 * jb + 2] * fast_rcp(fmaf(lt, fast_exp2(__uint_as_float(g2.y << 16) * -LOG2E), lt));
+      const float o3 = acc[4 * jb + 3] * fast_rcp(fmaf(lt, fast_exp2(__uint_as_float(g2.y & 0xffff0000u) * -LOG2E), lt));
       ov[db][jb].x = pack2(o0, o1);
       ov[db][jb].y = pack2(o2, o3);
     }
@@ -983,6 +990,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_fused_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) uint16_t KO[3 * 2 * FT], VO[2 * 2 * FT];
   const int lane = threadIdx.x & 63;
+  // the items first, so that their sequence's lengths load beside the norm weights.
+  // Pairs (causal, B = 1): workgroup g runs the q-blocks of rank r and n_qt - 1 - r
+  // of one head, n_qt + 1 blocks of keys in all for every workgroup
+  FItem it0, it1;
+  int n_it = 1;
+  if (CAUSAL && a.pairs) {
+    const int HB = a.H * a.B, r = blockIdx.x / HB, rem = blockIdx.x % HB;
+    it0 = item_at(a, r * HB + rem);
+    it1 = item_at(a, (a.n_qt - 1 - r) * HB + rem);
+    n_it = 2;
+  } else {
+    it0 = item_ranked(a, blockIdx.x, CAUSAL, reinterpret_cast<int*>(KO));
+    it1 = it0;
+  }
+  const int q_len_raw = a.q_lengths ? a.q_lengths[it0.b] : a.L;
+  const int prior = a.prior ? a.prior[it0.b] : 0;
   // static bounds from the norm weights: |k~| <= sqrt(D) * max|kw + w_offset| for
   // every cached row, |q op| <= max|qw + w_offset| for every scaled query row
   // (RMS-normalised rows have norm <= sqrt(D)); 1% covers the bf16 roundings
@@ -1008,11 +1031,19 @@ void prefill_fused_kernel(PrefillArgs a) {
   SoloLds L;
   L.k = KO;
   L.v = VO;
-  const FItem it = item_ranked(a, blockIdx.x, CAUSAL, reinterpret_cast<int*>(KO));
-  if (bound <= FSTATIC_LIMIT)
-    solo_item<CAUSAL, false>(a, it, L);
-  else
-    solo_item<CAUSAL, true>(a, it, L);
+  if (bound <= FSTATIC_LIMIT) {
+    solo_item<CAUSAL, false>(a, it0, L, q_len_raw, prior);
+    if (CAUSAL && n_it == 2) {
+      fbarrier();  // every wave is done with the first item's LDS
+      solo_item<CAUSAL, false>(a, it1, L, q_len_raw, prior);
+    }
+  } else {
+    solo_item<CAUSAL, true>(a, it0, L, q_len_raw, prior);
+    if (CAUSAL && n_it == 2) {
+      fbarrier();
+      solo_item<CAUSAL, true>(a, it1, L, q_len_raw, prior);
+    }
+  }
   // No global->LDS load is in flight here: the epilogue waited for all of them
   // (vmcnt(0)) before its barrier, and an item that returns early issued none.
   // Only the output stores may be outstanding, which need no wait.
@@ -1024,12 +1055,21 @@ hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_prefill_fused(const PrefillArgs& a, hipStream_t st, hipEvent_t t0, hipEvent_t t1) {
-  const int64_t n_items = (int64_t)a.n_qt * a.H * a.B;
+hipError_t launch_prefill_fused(const PrefillArgs& a0, hipStream_t st, hipEvent_t t0, hipEvent_t t1) {
+  const int64_t n_items = (int64_t)a0.n_qt * a0.H * a0.B;
   if (n_items == 0) return hipSuccess;
-  // one item per workgroup, heaviest first (the hardware hands the next item to
-  // the first CU that frees up)
-  const dim3 grid((unsigned)n_items), block(256);
+  PrefillArgs a = a0;
+  // causal, one sequence, an even number of q-blocks and at least two items per
+  // CU: each workgroup runs a heavy and a light q-block of one head (all
+  // workgroups equal work, one launch and length fetch per pair); otherwise one
+  // item per workgroup, heaviest first (the hardware hands the next item to the
+  // first CU that frees up)
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  a.pairs = a.causal && a.B == 1 && (a.n_qt & 1) == 0 && n_items >= 2 * (int64_t)cus;
+  const dim3 grid((unsigned)(a.pairs ? n_items / 2 : n_items)), block(256);
   if (t0 && t1) {
     if (a.causal)
       hipExtLaunchKernelGGL((prefill_fused_kernel<true>), grid, block, 0, st, t0, t1, 0, a);
