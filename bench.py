@@ -18,7 +18,8 @@ Key "prefill_config5": BASELINE config 5 (B=4 ragged chunks after 8-32 K
 priors) in algorithmic TFLOP/s, step and attention kernel. Key "decode_step": the
 whole captured decode step of a Qwen3.5-4B-shaped model (24 Gated DeltaNet + 8
 gated-attention layers, MLPs, lm head; B = 32), and the lm-head GEMV + argmax
-alone. Key "deltanet": the DeltaNet layer kernels alone (fused decode step and
+alone. Key "prefill_model": prefill! of that model at B = 1 over 4096 prompt
+tokens, eager (tokens/s, TFLOP/s of its projections and attention). Key "deltanet": the DeltaNet layer kernels alone (fused decode step and
 conv step against the HBM roofline, the prefill recurrence in tokens/s). Key "layer": whole
 attention layers, hidden state to hidden state (the qkv and Wo projections on
 hipBLASLt around the block) at the config-2 prefill and config-3 decode shapes.
@@ -612,6 +613,55 @@ def bench_step(vm, torch, replays=40, seed=9):
     return res
 
 
+def bench_prefill_model(vm, torch, T=4096, runs=5, seed=13):
+    """prefill!(m, gen, ids) (qwen35.jl:369-395) of the same Qwen3.5-4B-shaped
+    model as bench_step at B = 1 over T = 4096 prompt tokens, eager, from a reset
+    state: embedding, 24 Gated DeltaNet layers (projection, sequence conv, prep,
+    chunked recurrence, gated norm, out projection), 8 gated-attention layers
+    (projection, K/V append + fused attention, Wo), the MLPs and norms, and the
+    lm head for the last token. Events bracket each whole prefill. FLOP: every
+    projection weight twice per token, plus the causal attention's 4 D Hq sum i
+    per attention layer (the DeltaNet recurrence and the norms not counted)."""
+    B, L = 1, 32
+    a = vm.AttnConfig(D=DM, Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=T, B=B)
+    cfg = vm.ModelConfig(attn=a, inter=9216, vocab=151936, n_layers=L, tied=True, interval=4)
+    m = vm.random_model(cfg, seed=seed)
+    gen = vm.Generation(B, 16)
+    rng = np.random.default_rng(seed)
+    ids = torch.as_tensor(rng.integers(1, cfg.vocab + 1, size=(B, T)).astype(np.int32)).cuda()
+    for _ in range(2):
+        m.reset_()
+        vm.prefill_(m, gen, ids)
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(runs):
+        m.reset_()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        vm.prefill_(m, gen, ids)
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    w = 0
+    for l in m.layers:
+        ts = ((l.W_in, l.Wout) if isinstance(l, vm.DeltaNetLayer) else (l.Wqkv, l.Wo))
+        w += sum(t.numel() for t in ts + (l.Wgu, l.Wd))
+    n_attn = sum(1 for l in m.layers if not isinstance(l, vm.DeltaNetLayer))
+    flops = 2.0 * w * T * B + n_attn * prefill_flops(T)
+    t = float(np.median(ms))
+    del m
+    torch.cuda.empty_cache()
+    return {
+        "config": f"Qwen3.5-4B shape: {L} layers ({L - n_attn} Gated DeltaNet + {n_attn} gated "
+                  f"attention), hidden {DM}, MLP {cfg.inter}, vocab {cfg.vocab} (tied head), random "
+                  f"weights, B={B}, T={T} prompt tokens from a reset state, eager, median of {runs}",
+        "ms": t,
+        "tokens_per_s": B * T / (t * 1e-3),
+        "flops": flops,
+        "tflops": flops / (t * 1e-3) / 1e12,
+    }
+
+
 def _profiled_us(vm, torch, kernel, fn, n=20):
     """Mean us per launch of one kernel class (events around its launches)."""
     lib = vm._lib
@@ -920,6 +970,8 @@ def main():
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer leg")
     ap.add_argument("--no-step", action="store_true", help="skip the whole-decode-step leg")
     ap.add_argument("--no-deltanet", action="store_true", help="skip the DeltaNet kernel leg")
+    ap.add_argument("--no-model-prefill", action="store_true",
+                    help="skip the whole-model prefill leg")
     ap.add_argument("--no-settle", action="store_true",
                     help="skip the clock-settle phase (counter-collection runs)")
     ap.add_argument("--no-decode", action="store_true")
@@ -1003,6 +1055,12 @@ def main():
         log(f"[bench] step: {step['ms_per_step']:.3f} ms/step, {step['tokens_per_s']:.0f} tok/s, "
             f"{step['gbs']:.0f} GB/s; lm head alone B=1 {step['lm_head_B1']['gbs']:.0f} GB/s, "
             f"B=32 {step['lm_head_B32']['gbs']:.0f} GB/s")
+    pmodel = None
+    if not args.no_model_prefill:
+        log("[bench] whole-model prefill, Qwen3.5-4B shape, B=1 T=4096")
+        pmodel = bench_prefill_model(vm, torch)
+        log(f"[bench] model prefill: {pmodel['ms']:.2f} ms = {pmodel['tokens_per_s']:.0f} tokens/s, "
+            f"{pmodel['tflops']:.0f} TFLOP/s (projections + attention)")
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle), configs 1-5")
@@ -1014,7 +1072,7 @@ def main():
 
     if pf is None:
         print(json.dumps({"decode": decode, "layer": layer, "decode_step": step, "deltanet": dnet,
-                          "cpu_baseline": cpu}), flush=True)
+                          "prefill_model": pmodel, "cpu_baseline": cpu}), flush=True)
         return
     achieved = pf["flops"] / (pf["attn_kernel_ms"] * 1e-3) / 1e12
     line = {
@@ -1045,6 +1103,7 @@ def main():
         "decode": decode,
         "layer": layer,
         "decode_step": step,
+        "prefill_model": pmodel,
         "deltanet": dnet,
     }
     print(json.dumps(line), flush=True)

@@ -4,8 +4,10 @@
 //
 // Like the reference's cuBLASLt path, one plan per problem is built on first
 // use and cached for the process (linear.jl:17-38): hipBLASLt matmul
-// descriptor, matrix layouts and the heuristic's first algorithm, bf16 A/B/D
-// with fp32 compute and fp32 scaling (linear.jl:29). Column-major view, as in
+// descriptor, matrix layouts and an algorithm, bf16 A/B/D with fp32 compute and
+// fp32 scaling (linear.jl:29). The reference takes the heuristic's first
+// algorithm; here a new plan times the heuristic's top candidates once and
+// keeps the fastest (tune_algo below). Column-major view, as in
 // the reference: x :: (K, N) with column stride ldx, W :: (K, M) (K-major) with
 // column stride ldw, y :: (M, N) with column stride ldy, so
 //     D (M x N) = op(A) B,  A = W (K x M, op = transpose), B = x (K x N).
@@ -19,6 +21,8 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -56,10 +60,83 @@ const char* status_name(hipblasStatus_t s) {
   }
 }
 
+// The heuristic ranks candidates by a model, and on MI355X its first pick can
+// be a third slower than the best of its own top candidates (M x N x K =
+// 18432 x 4096 x 2560: 381 against 286 us). So a new plan times up to NTUNE
+// candidates on scratch buffers of the problem's shape (N(0,1) bf16 data, one
+// warm-up and three timed runs each, on a private stream) and keeps the
+// fastest. The heuristic's first is kept unless another beats it by 3% or
+// more, so close calls do not flip from process to process.
+// VM_LINEAR_TUNE=0 keeps the first always. If any step fails (for example an
+// allocation while a stream of the device is being captured), the plan keeps
+// the first and the error is cleared. Returns the chosen index into `cand`.
+constexpr int NTUNE = 16;
+int tune_algo(hipblasLtHandle_t h, const Plan& p, const hipblasLtMatmulHeuristicResult_t* res,
+              const int* cand, int nc, int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy) {
+  const char* env = getenv("VM_LINEAR_TUNE");
+  if (nc < 2 || (env && strcmp(env, "0") == 0)) return 0;
+  size_t wsmax = 0;
+  for (int i = 0; i < nc; ++i) wsmax = std::max(wsmax, (size_t)res[cand[i]].workspaceSize);
+  void *A = nullptr, *B = nullptr, *D = nullptr, *W = nullptr;
+  hipStream_t st = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int best = 0;
+  bool ok = hipStreamCreateWithFlags(&st, hipStreamNonBlocking) == hipSuccess &&
+            hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess &&
+            hipMalloc(&A, (size_t)ldw * M * 2) == hipSuccess &&
+            hipMalloc(&B, (size_t)ldx * N * 2) == hipSuccess &&
+            hipMalloc(&D, (size_t)ldy * N * 2) == hipSuccess &&
+            (wsmax == 0 || hipMalloc(&W, wsmax) == hipSuccess) &&
+            launch_fill_normal(static_cast<uint16_t*>(A), (int64_t)ldw * M, 0x51u, 1.0f, 0.0f, st) ==
+                hipSuccess &&
+            launch_fill_normal(static_cast<uint16_t*>(B), (int64_t)ldx * N, 0x52u, 1.0f, 0.0f, st) ==
+                hipSuccess;
+  if (ok) {
+    const float alpha = 1.0f, beta = 0.0f;
+    float t_first = -1.f, t_best = -1.f;
+    for (int i = 0; i < nc && ok; ++i) {
+      const hipblasLtMatmulHeuristicResult_t& r = res[cand[i]];
+      bool run_ok = true;
+      for (int rep = 0; rep < 4 && run_ok; ++rep) {
+        if (rep == 1) run_ok = hipEventRecord(e0, st) == hipSuccess;
+        run_ok = run_ok && hipblasLtMatmul(h, p.desc, &alpha, A, p.a, B, p.b, &beta, D, p.d, D, p.d,
+                                           &r.algo, W, r.workspaceSize, st) == HIPBLAS_STATUS_SUCCESS;
+      }
+      float ms = 0.f;
+      run_ok = run_ok && hipEventRecord(e1, st) == hipSuccess &&
+               hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+      if (!run_ok) {
+        if (i == 0) ok = false;  // the first must run: it is the fallback
+        continue;
+      }
+      if (i == 0) t_first = ms;
+      if (t_best < 0.f || ms < t_best) {
+        t_best = ms;
+        best = i;
+      }
+    }
+    if (!ok || t_first <= 1.03f * t_best) best = 0;
+  }
+  if (A) (void)hipFree(A);
+  if (B) (void)hipFree(B);
+  if (D) (void)hipFree(D);
+  if (W) (void)hipFree(W);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (st) (void)hipStreamDestroy(st);
+  if (!ok) {
+    (void)hipGetLastError();
+    best = 0;
+  }
+  return best;
+}
+
 // Builds (once) the plan of one problem on the current device. Returns 0, or a
 // VM_E_* / hipError_t code with `err` set.
+// tune: time the candidates (tune_algo) when the plan is new; false keeps the
+// heuristic's first (a plan first needed inside a stream capture).
 int get_plan(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, const Plan** out,
-             char* err, size_t errn) {
+             char* err, size_t errn, bool tune = true) {
   int dev = 0;
   hipError_t he = hipGetDevice(&dev);
   if (he != hipSuccess) {
@@ -105,20 +182,31 @@ int get_plan(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, const P
   if (s == HIPBLAS_STATUS_SUCCESS)
     s = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &cap,
                                               sizeof cap);
-  // the heuristic's ranking, first candidate within the workspace cap (the cap
-  // preference alone does not bound what it returns)
-  constexpr int NREQ = 8;
+  // the heuristic's ranking, candidates within the workspace cap (the cap
+  // preference alone does not bound what it returns), then the timed choice
+  constexpr int NREQ = 32;
   hipblasLtMatmulHeuristicResult_t res[NREQ];
   int n_res = 0;
   if (s == HIPBLAS_STATUS_SUCCESS)
     s = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.d, p.d, pref, NREQ, res, &n_res);
   if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-  for (int i = 0; s == HIPBLAS_STATUS_SUCCESS && i < n_res; ++i) {
-    if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > cap) continue;
-    p.algo = res[i].algo;
-    p.workspace = res[i].workspaceSize;
+  int cand[NTUNE];
+  int nc = 0;
+  for (int i = 0; s == HIPBLAS_STATUS_SUCCESS && i < n_res && nc < NTUNE; ++i)
+    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= cap) cand[nc++] = i;
+  if (nc > 0) {
+    int pick = cand[0];
+    if (tune) {
+      // relaxed capture mode for this thread meanwhile, so that the scratch
+      // allocations cannot invalidate another stream's capture
+      hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+      const bool swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
+      pick = cand[tune_algo(h, p, res, cand, nc, M, N, K, ldw, ldx, ldy)];
+      if (swapped) (void)hipThreadExchangeStreamCaptureMode(&mode);
+    }
+    p.algo = res[pick].algo;
+    p.workspace = res[pick].workspaceSize;
     p.ok = true;
-    break;
   }
   auto& slot = g_plans[key];  // remembered either way (linear.jl:20-21)
   slot = p;
@@ -194,7 +282,9 @@ int linear_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const u
     return VM_OK;
   }
   const Plan* p = nullptr;
-  int rc = get_plan(M, N, K, ldw, ldx, ldy, &p, err, errn);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) cs = hipStreamCaptureStatusActive;
+  int rc = get_plan(M, N, K, ldw, ldx, ldy, &p, err, errn, cs == hipStreamCaptureStatusNone);
   if (rc != VM_OK) return rc;
   if (p->workspace > 0 && (workspace == nullptr || workspace_bytes < p->workspace)) {
     snprintf(err, errn, "linear: workspace of %zu bytes < %zu required (vm_linear_workspace_bytes)",
