@@ -737,7 +737,9 @@ def bench_deltanet(vm, torch, seed=11):
          "Gate": torch.empty((B, T, Hv), **f32)}
     a_log = torch.randn((Hv,), **f32) * 0.5
     dt = torch.randn((Hv,), **f32) * 0.5
-    vm.deltanet_prefill_prep_(p, Y, ab, a_log, dt, Dk=Dk, Dv=Dv, Hk=Hk, Hv=Hv)
+    us_prep = _profiled_us(vm, torch, vm._lib.VM_K_ROWS,
+                           lambda: vm.deltanet_prefill_prep_(p, Y, ab, a_log, dt, Dk=Dk, Dv=Dv,
+                                                             Hk=Hk, Hv=Hv), n=5)
     S = torch.zeros((B, Hv, Dv, Dk), **f32)
     o = torch.empty((B, Hv, T, Dv), **f32)
     us_seq = _profiled_us(vm, torch, vm._lib.VM_K_DELTANET,
@@ -749,6 +751,15 @@ def bench_deltanet(vm, torch, seed=11):
                           lambda: vm.deltanet_sequence_chunked_({"O": o, "Sp": S}, p["Q"], p["K"],
                                                                 p["V"], p["Beta"], p["Gate"], S,
                                                                 workspace=ws), n=5)
+    z = _dev_normal(vm, torch, (B, T, Hv, Dv), seed + 302)
+    gw = _dev_normal(vm, torch, (Dv,), seed + 303, 0.2)
+    yb = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device="cuda")
+    us_gn = _profiled_us(vm, torch, vm._lib.VM_K_ROWS,
+                         lambda: vm.gated_rms_norm_(yb, o, z, gw, eps=EPS), n=5)
+    # prep: conv rows read (bf16), fp32 q, k, v written, ab read, gates written;
+    # gated norm: fp32 o and bf16 z read, bf16 y written
+    prep_bytes = 2.0 * T * n + 4.0 * T * n + 2.0 * T * 2 * Hv + 8.0 * T * Hv
+    gn_bytes = (4.0 + 2.0 + 2.0) * T * Hv * Dv
     # chunked form's work: per 64-token chunk and value head, phase 1's two Grams,
     # triangular solve and operand writes, phase 2's 4 x 112 MFMAs per column block
     res["prefill_B1_T4096"] = {
@@ -759,6 +770,10 @@ def bench_deltanet(vm, torch, seed=11):
         "sequence_us_per_token": us_seq / T,
         "chunked_ms": us_chk * 1e-3,
         "chunked_tokens_per_s": T / (us_chk * 1e-6),
+        "prep_us": us_prep,
+        "prep_gbs": prep_bytes / (us_prep * 1e-6) / 1e9,
+        "gated_norm_us": us_gn,
+        "gated_norm_gbs": gn_bytes / (us_gn * 1e-6) / 1e9,
     }
     return res
 
@@ -1047,7 +1062,8 @@ def main():
             f"{f32_['gbs']:.0f} GB/s; conv decode B=32 {cv['us']:.1f} us = {cv['gbs']:.0f} GB/s; "
             f"prefill T=4096: conv {pp['conv_sequence_us']:.1f} us, recurrence "
             f"{pp['sequence_ms']:.2f} ms sequential ({pp['sequence_us_per_token']:.2f} us/token), "
-            f"{pp['chunked_ms']:.3f} ms chunked")
+            f"{pp['chunked_ms']:.3f} ms chunked; prep {pp['prep_us']:.1f} us = {pp['prep_gbs']:.0f} "
+            f"GB/s, gated norm {pp['gated_norm_us']:.1f} us = {pp['gated_norm_gbs']:.0f} GB/s")
     step = None
     if not args.no_step:
         log("[bench] whole decode step, Qwen3.5-4B shape (24 DeltaNet + 8 attention), B=32")

@@ -203,16 +203,18 @@ def test_deltanet_sequence_zero_length_copies_state(vm):
     assert np.array_equal(out["Sp"].cpu().numpy(), s)
 
 
-def test_prep_and_gated_norm(vm, orc):
+@pytest.mark.parametrize("off", [0, 4])
+def test_prep_and_gated_norm(vm, orc, off):
     """The prefill's prep from strided conv rows and its gated-norm epilogue
-    reading z from the projection."""
-    banner("deltanet prep + gated norm")
+    reading z from the projection. off = 0: 16-byte aligned rows (the vectorised
+    kernels); off = 4: rows 8-byte aligned only (the one-wave-per-head kernels)."""
+    banner(f"deltanet prep + gated norm, rows at element offset {off}")
     B, T = 2, 7
     cv, ab, a_log, dt_bias = _prepped(B, T, 980)
     p_ref = orc.deltanet_prep(cv, ab, a_log, dt_bias, Dk=DK, Dv=DV, Hk=HK, Hv=HV)
     wide = np.zeros((B, T, NCH + 64), np.uint16)
-    wide[..., :NCH] = cv
-    CV = to_dev(wide)[..., :NCH]
+    wide[..., off:off + NCH] = cv
+    CV = to_dev(wide)[..., off:off + NCH]
     outs = {"Q": torch.empty((B, HK, T, DK), dtype=torch.float32, device="cuda"),
             "K": torch.empty((B, HK, T, DK), dtype=torch.float32, device="cuda"),
             "V": torch.empty((B, HV, T, DV), dtype=torch.float32, device="cuda"),
@@ -225,11 +227,12 @@ def test_prep_and_gated_norm(vm, orc):
         np.testing.assert_allclose(outs[key].cpu().numpy(), p_ref[rk], rtol=2e-6, atol=1e-7,
                                    err_msg=key)
     o = normal_f32(B * HV * T * DV, 981).reshape(B, HV, T, DV)
-    qz = normal_bf16((B, T, NCH + HV * DV), 982)
+    qz = normal_bf16((B, T, NCH + off + HV * DV), 982)
     norm_w = normal_bf16((DV,), 983, scale=0.2, shift=1.0)
-    y_ref = orc.gated_rms_norm(o, np.ascontiguousarray(qz[..., NCH:]), norm_w, eps=EPS)
-    Z = to_dev(qz)[..., NCH:].unflatten(-1, (HV, DV))
-    Y = torch.empty((B, T, HV, DV), dtype=torch.bfloat16, device="cuda")
+    y_ref = orc.gated_rms_norm(o, np.ascontiguousarray(qz[..., NCH + off:]), norm_w, eps=EPS)
+    Z = to_dev(qz)[..., NCH + off:].unflatten(-1, (HV, DV))
+    Yw = torch.empty((B, T, HV * DV + off), dtype=torch.bfloat16, device="cuda")
+    Y = Yw[..., off:].unflatten(-1, (HV, DV))
     vm.gated_rms_norm_(Y, f32dev(o), Z, to_dev(norm_w), eps=EPS)
     torch.cuda.synchronize()
     assert_bf16_close(dev_f32(Y), y_ref, "gated norm", extra=1e-6)
