@@ -56,6 +56,12 @@ __global__ __launch_bounds__(RT) void rms_norm_kernel(NormArgs a) {
   const uint16_t* x = a.x + (int64_t)n * a.x_st;
   float v[RCHUNK][8];
   float ss = 0.f;
+  // the norm weight first: its loads are in flight with the row's (a load after
+  // the block reduction would add a memory latency to this latency-bound kernel)
+  float w[RCHUNK][8];
+#pragma unroll
+  for (int i = 0; i < RCHUNK; ++i)
+    if (t + RT * i < nc) load8f(a.w + 8 * (t + RT * i), w[i]);
 #pragma unroll
   for (int i = 0; i < RCHUNK; ++i) {
     const int c = t + RT * i;
@@ -64,13 +70,23 @@ __global__ __launch_bounds__(RT) void rms_norm_kernel(NormArgs a) {
       if (FUSED) {
         float d[8];
         if (a.dpart) {  // a split GEMV's slices, summed in slice order, rounded
+          // up to 8 slices' loads issued together, then added in slice order
           const float* p = a.dpart + (int64_t)n * a.dpart_cs + 8 * c;
           float4 lo = *reinterpret_cast<const float4*>(p), hi = *reinterpret_cast<const float4*>(p + 4);
-          for (int k = 1; k < a.S2; ++k) {
-            const float4 l2 = *reinterpret_cast<const float4*>(p + k * a.dpart_ss);
-            const float4 h2 = *reinterpret_cast<const float4*>(p + k * a.dpart_ss + 4);
-            lo.x += l2.x; lo.y += l2.y; lo.z += l2.z; lo.w += l2.w;
-            hi.x += h2.x; hi.y += h2.y; hi.z += h2.z; hi.w += h2.w;
+          for (int k0 = 1; k0 < a.S2; k0 += 8) {
+            float4 l2[8], h2[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+              if (k0 + k < a.S2) {
+                l2[k] = *reinterpret_cast<const float4*>(p + (k0 + k) * a.dpart_ss);
+                h2[k] = *reinterpret_cast<const float4*>(p + (k0 + k) * a.dpart_ss + 4);
+              }
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+              if (k0 + k < a.S2) {
+                lo.x += l2[k].x; lo.y += l2[k].y; lo.z += l2[k].z; lo.w += l2[k].w;
+                hi.x += h2[k].x; hi.y += h2[k].y; hi.z += h2[k].z; hi.w += h2[k].w;
+              }
           }
           const float s8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
           unpack8(pack8(s8), d);  // the bf16 h the reference stores
@@ -98,10 +114,9 @@ __global__ __launch_bounds__(RT) void rms_norm_kernel(NormArgs a) {
   for (int i = 0; i < RCHUNK; ++i) {
     const int c = t + RT * i;
     if (c < nc) {
-      float w[8], y[8];
-      load8f(a.w + 8 * c, w);
+      float y[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) y[j] = v[i][j] * rstd * (w[j] + a.offset);
+      for (int j = 0; j < 8; ++j) y[j] = v[i][j] * rstd * (w[i][j] + a.offset);
       *reinterpret_cast<uint4*>(a.y + (int64_t)n * a.y_st + 8 * c) = pack8(y);
     }
   }
