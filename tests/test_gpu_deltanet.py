@@ -238,6 +238,30 @@ def test_prep_and_gated_norm(vm, orc, off):
     assert_bf16_close(dev_f32(Y), y_ref, "gated norm", extra=1e-6)
 
 
+def test_prep_many_value_heads(vm, orc):
+    """The prep with more value heads than a wave has lanes (Hk = 2, Hv = 72): the
+    gates of heads 64 .. 71 too."""
+    banner("deltanet prep, Hv = 72")
+    B, T, hk, hv = 1, 3, 2, 72
+    n = 2 * hk * DK + hv * DV
+    cv = normal_bf16((B, T, n), 990)
+    ab = normal_bf16((B, T, 2 * hv), 991)
+    a_log = normal_f32(hv, 992, scale=0.5)
+    dt_bias = normal_f32(hv, 993, scale=0.5)
+    ref = orc.deltanet_prep(cv, ab, a_log, dt_bias, Dk=DK, Dv=DV, Hk=hk, Hv=hv)
+    outs = {"Q": torch.empty((B, hk, T, DK), dtype=torch.float32, device="cuda"),
+            "K": torch.empty((B, hk, T, DK), dtype=torch.float32, device="cuda"),
+            "V": torch.empty((B, hv, T, DV), dtype=torch.float32, device="cuda"),
+            "Beta": torch.empty((B, T, hv), dtype=torch.float32, device="cuda"),
+            "Gate": torch.empty((B, T, hv), dtype=torch.float32, device="cuda")}
+    vm.deltanet_prefill_prep_(outs, to_dev(cv), to_dev(ab), f32dev(a_log), f32dev(dt_bias), Dk=DK,
+                              Dv=DV, Hk=hk, Hv=hv)
+    torch.cuda.synchronize()
+    for key, rk in (("Q", "q"), ("K", "k"), ("V", "v"), ("Beta", "beta"), ("Gate", "gate")):
+        np.testing.assert_allclose(outs[key].cpu().numpy(), ref[rk], rtol=2e-6, atol=1e-7,
+                                   err_msg=key)
+
+
 def test_shape_errors(vm):
     """The reference's DimensionMismatch on Hv % Hk, and head sizes the kernels
     are not built for; checked before any launch."""

@@ -591,8 +591,8 @@ __global__ __launch_bounds__(256) void deltanet_prep_kernel(DeltaPrepArgs a) {
 // with strides of whole 8-element chunks, fp32 outputs 16-byte aligned; the
 // launcher checks): one wave per token, four heads per pass (16 lanes of 8
 // channels per head: 16-byte reads, 32-byte writes), the q / k sums of squares
-// reduced over each 16-lane group, then lanes 0 .. Hv-1 take one head's gates
-// each. The one-wave-per-(token, head) kernel above issued 64 times the waves
+// reduced over each 16-lane group, then lane l takes the gates of heads l, l + 64,
+// ... The one-wave-per-(token, head) kernel above issued 64 times the waves
 // for 4-byte reads, and ran at 2 TB/s.
 __global__ __launch_bounds__(256) void deltanet_prep_vec_kernel(DeltaPrepArgs a) {
   const int lane = threadIdx.x & 63;
@@ -631,11 +631,11 @@ __global__ __launch_bounds__(256) void deltanet_prep_vec_kernel(DeltaPrepArgs a)
       d4[1] = make_float4(x[4], x[5], x[6], x[7]);
     }
   }
-  if (lane < a.Hv) {
-    const uint16_t* ab = a.ab + (int64_t)b * a.ab_sb + (int64_t)t * a.ab_st;
-    const int64_t gi = ((int64_t)b * a.T + t) * a.Hv + lane;
-    a.beta[gi] = accurate_sigmoid(bf2f(ab[a.Hv + lane]));
-    a.gate[gi] = -expf(a.a_log[lane]) * log1pf(expf(bf2f(ab[lane]) + a.dt_bias[lane]));
+  const uint16_t* ab = a.ab + (int64_t)b * a.ab_sb + (int64_t)t * a.ab_st;
+  for (int hv = lane; hv < a.Hv; hv += 64) {
+    const int64_t gi = ((int64_t)b * a.T + t) * a.Hv + hv;
+    a.beta[gi] = accurate_sigmoid(bf2f(ab[a.Hv + hv]));
+    a.gate[gi] = -expf(a.a_log[hv]) * log1pf(expf(bf2f(ab[hv]) + a.dt_bias[hv]));
   }
 }
 
