@@ -44,14 +44,13 @@ __device__ __forceinline__ void load8f(const uint16_t* p, float* f) { unpack8(lo
 }  // namespace
 
 // ---- RMSNorm, optionally fused with the residual add before it. One workgroup
-// per column n: x' = x + dx in fp32 (FUSED; stored rounded to bf16 into xo, which
+// (or, for many columns, one wave) per column n: x' = x + dx in fp32 (FUSED; stored rounded to bf16 into xo, which
 // may be x itself), rstd = 1 / sqrt(sum(x'^2) / M + eps) over the fp32 x', then
 // y = x' * rstd * (w + offset) -- on the stored, rounded x' when fused, as the
 // reference reloads it (residual_norm.jl:36-41).
-template <bool FUSED>
-__global__ __launch_bounds__(RT) void rms_norm_kernel(NormArgs a) {
-  __shared__ float red[4];
-  const int n = blockIdx.x, t = threadIdx.x;
+// DPART (FUSED only): dx from a split GEMV's fp32 slices (a.dpart), else a.dx
+template <bool FUSED, bool DPART, int NT, int RCHUNK, typename Reduce>
+__device__ __forceinline__ void rms_norm_row(const NormArgs& a, int n, int t, Reduce reduce) {
   const int nc = a.M / 8;
   const uint16_t* x = a.x + (int64_t)n * a.x_st;
   float v[RCHUNK][8];
@@ -61,15 +60,15 @@ __global__ __launch_bounds__(RT) void rms_norm_kernel(NormArgs a) {
   float w[RCHUNK][8];
 #pragma unroll
   for (int i = 0; i < RCHUNK; ++i)
-    if (t + RT * i < nc) load8f(a.w + 8 * (t + RT * i), w[i]);
+    if (t + NT * i < nc) load8f(a.w + 8 * (t + NT * i), w[i]);
 #pragma unroll
   for (int i = 0; i < RCHUNK; ++i) {
-    const int c = t + RT * i;
+    const int c = t + NT * i;
     if (c < nc) {
       load8f(x + 8 * c, v[i]);
       if (FUSED) {
         float d[8];
-        if (a.dpart) {  // a split GEMV's slices, summed in slice order, rounded
+        if constexpr (DPART) {  // a split GEMV's slices, summed in slice order, rounded
           // up to 8 slices' loads issued together, then added in slice order
           const float* p = a.dpart + (int64_t)n * a.dpart_cs + 8 * c;
           float4 lo = *reinterpret_cast<const float4*>(p), hi = *reinterpret_cast<const float4*>(p + 4);
@@ -108,11 +107,11 @@ __global__ __launch_bounds__(RT) void rms_norm_kernel(NormArgs a) {
       }
     }
   }
-  ss = block_sum(ss, red);
+  ss = reduce(ss);
   const float rstd = 1.0f / sqrtf(ss / (float)a.M + a.eps);
 #pragma unroll
   for (int i = 0; i < RCHUNK; ++i) {
-    const int c = t + RT * i;
+    const int c = t + NT * i;
     if (c < nc) {
       float y[8];
 #pragma unroll
@@ -122,12 +121,48 @@ __global__ __launch_bounds__(RT) void rms_norm_kernel(NormArgs a) {
   }
 }
 
+template <bool FUSED, bool DPART>
+__global__ __launch_bounds__(RT) void rms_norm_kernel(NormArgs a) {
+  __shared__ float red[4];
+  rms_norm_row<FUSED, DPART, RT, vm::RCHUNK>(a, blockIdx.x, threadIdx.x,
+                                             [&](float v) { return block_sum(v, red); });
+}
+// the same with one wave per column, four columns per workgroup, for many
+// columns (a prefill's T x B tokens) of at most 64 x 8 x 8 = 4096: no workgroup
+// barrier, and RC (= M / 512 rounded up) chunks per lane, so the registers and
+// the waves a SIMD holds follow M
+template <bool FUSED, bool DPART, int RC>
+__global__ __launch_bounds__(RT) void rms_norm_wave_kernel(NormArgs a) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= a.N) return;
+  rms_norm_row<FUSED, DPART, 64, RC>(a, n, threadIdx.x & 63,
+                                     [](float v) { return wave_sum_dpp(v); });
+}
+
 hipError_t launch_rms_norm(const NormArgs& a, hipStream_t st) {
   if (a.N == 0) return hipSuccess;
-  if (a.dx || a.dpart)
-    hipLaunchKernelGGL(rms_norm_kernel<true>, dim3(a.N), dim3(RT), 0, st, a);
-  else
-    hipLaunchKernelGGL(rms_norm_kernel<false>, dim3(a.N), dim3(RT), 0, st, a);
+  const int mode = a.dpart ? 2 : (a.dx ? 1 : 0);  // dx: none, a bf16 row, fp32 slices
+  if (a.N >= 256 && a.M <= 64 * 8 * 8 && mode != 2) {
+    const dim3 grid((unsigned)((a.N + 3) / 4));
+    switch ((a.M / 8 + 63) / 64) {
+#define X(rc)                                                                         \
+  case rc:                                                                            \
+    if (mode == 1)                                                                    \
+      hipLaunchKernelGGL((rms_norm_wave_kernel<true, false, rc>), grid, dim3(RT), 0, st, a); \
+    else                                                                              \
+      hipLaunchKernelGGL((rms_norm_wave_kernel<false, false, rc>), grid, dim3(RT), 0, st, a); \
+    break;
+      X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
+#undef X
+      default: return hipErrorInvalidValue;
+    }
+  } else if (mode == 2) {
+    hipLaunchKernelGGL((rms_norm_kernel<true, true>), dim3(a.N), dim3(RT), 0, st, a);
+  } else if (mode == 1) {
+    hipLaunchKernelGGL((rms_norm_kernel<true, false>), dim3(a.N), dim3(RT), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((rms_norm_kernel<false, false>), dim3(a.N), dim3(RT), 0, st, a);
+  }
   return hipGetLastError();
 }
 
