@@ -67,14 +67,20 @@ const char* status_name(hipblasStatus_t s) {
 // warm-up and three timed runs each, on a private stream) and keeps the
 // fastest. The heuristic's first is kept unless another beats it by 3% or
 // more, so close calls do not flip from process to process.
+// Problems with fewer than TUNE_MIN_N columns (decode batches) are not timed:
+// their kernels are memory-bound and run about as long as the host takes to
+// submit one, so back-to-back runs measure the host, and their weights sit in
+// the last-level cache between runs, which a model's step never sees (a pick
+// made that way ran 30 us in a decode step where the first runs 23.5 us).
 // VM_LINEAR_TUNE=0 keeps the first always. If any step fails (for example an
 // allocation while a stream of the device is being captured), the plan keeps
 // the first and the error is cleared. Returns the chosen index into `cand`.
 constexpr int NTUNE = 16;
+constexpr int TUNE_MIN_N = 256;
 int tune_algo(hipblasLtHandle_t h, const Plan& p, const hipblasLtMatmulHeuristicResult_t* res,
               const int* cand, int nc, int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy) {
   const char* env = getenv("VM_LINEAR_TUNE");
-  if (nc < 2 || (env && strcmp(env, "0") == 0)) return 0;
+  if (nc < 2 || N < TUNE_MIN_N || (env && strcmp(env, "0") == 0)) return 0;
   size_t wsmax = 0;
   for (int i = 0; i < nc; ++i) wsmax = std::max(wsmax, (size_t)res[cand[i]].workspaceSize);
   void *A = nullptr, *B = nullptr, *D = nullptr, *W = nullptr;
