@@ -15,7 +15,8 @@ advancing on the device)
 in HBM GB/s of K/V actually attended (4096 B per token) + 32 KiB per sequence,
 and config 1 (B=1 at 512 tokens, launch-latency-bound) as time per step.
 Key "prefill_config5": BASELINE config 5 (B=4 ragged chunks after 8-32 K
-priors) in algorithmic TFLOP/s, step and attention kernel. Key "decode_step": the
+priors) in algorithmic TFLOP/s, step and attention kernel, and the step with the
+layer's V^T workspace kept between chunks (staging the chunk only). Key "decode_step": the
 whole captured decode step of a Qwen3.5-4B-shaped model (24 Gated DeltaNet + 8
 gated-attention layers, MLPs, lm head; B = 32), and the lm-head GEMV + argmax
 alone. Key "prefill_model": prefill! of that model at B = 1 over 4096 prompt
@@ -235,6 +236,19 @@ def bench_prefill5(vm, torch, steps, warmup, seed=5):
     lib.profile_enable(False)
     lib.profile_select()
     assert n_attn == steps
+    # the same chunk with the layer's V^T workspace kept (StagedV, as a chunk-by-
+    # chunk prefill runs): after the first call, a call stages the chunk's rows only
+    staged = vm.StagedV(cfg, B)
+    vm.gated_attn_prefill(layer, m, qkv, T, B, prior=pr, q_lengths=ql, out=out, staged=staged)
+    for _ in range(warmup):
+        vm.gated_attn_prefill(layer, m, qkv, T, B, prior=pr, q_lengths=ql, out=out, staged=staged)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        vm.gated_attn_prefill(layer, m, qkv, T, B, prior=pr, q_lengths=ql, out=out, staged=staged)
+    torch.cuda.synchronize()
+    wall_staged = time.perf_counter() - t0
+    del staged
     c, p = qlen.astype(np.float64), prior.astype(np.float64)
     flops = float(4 * D * HQ * np.sum(c * p + c * (c + 1) / 2))
     kms = ms_attn / n_attn
@@ -244,6 +258,8 @@ def bench_prefill5(vm, torch, steps, warmup, seed=5):
         "flop_per_step": flops,
         "ms_per_step": 1e3 * wall / steps,
         "tflops": flops / (wall / steps) / 1e12,
+        "ms_per_step_staged": 1e3 * wall_staged / steps,
+        "tflops_staged": flops / (wall_staged / steps) / 1e12,
         "attn_kernel_ms": kms,
         "attn_kernel_tflops": flops / (kms * 1e-3) / 1e12,
         "frac_of_bf16_peak": flops / (kms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
@@ -1045,7 +1061,8 @@ def main():
         log("[bench] prefill config5 (ragged chunked, B=4)")
         pf5 = bench_prefill5(vm, torch, max(10, args.steps // 15), max(3, args.warmup // 30))
         log(f"[bench] prefill5: {pf5['ms_per_step']:.3f} ms/step, {pf5['tflops']:.1f} TFLOP/s, "
-            f"attn kernel {pf5['attn_kernel_ms']:.3f} ms = {pf5['attn_kernel_tflops']:.1f} TFLOP/s")
+            f"attn kernel {pf5['attn_kernel_ms']:.3f} ms = {pf5['attn_kernel_tflops']:.1f} TFLOP/s; "
+            f"V^T kept between chunks: {pf5['ms_per_step_staged']:.3f} ms/step")
     decode = None
     if not args.no_decode:
         log("[bench] decode config3 B=32")

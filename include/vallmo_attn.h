@@ -258,6 +258,32 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb,
                           int B, int T, int Hq, int Hk, int D, int half_rot,
                           float eps, float w_offset, void* scratch, size_t scratch_bytes,
                           vm_stream stream);
+/* vm_gated_attn_prefill for a prefill run as successive chunks (the same
+ * forward(::AttnLayer, …; offset) of src/llm/qwen35.jl:292-318, called chunk
+ * after chunk): `vt` (device, 256-byte aligned, at least
+ * vm_prefill_scratch_bytes(B, Hk, D, ctx) bytes) persists between the calls of
+ * one layer and holds the V^T tiles of the rows staged so far; vt_rows (device
+ * int32[2B], zeroed before the first call) holds in [b] how many leading cache
+ * rows of sequence b those are, and in [B + b] a counter the library uses
+ * during a call and leaves zero. A call
+ * stages only rows min(vt_rows[b], prior[b]) .. prior[b]+q_len[b]-1 (the chunk,
+ * and any rows written since, such as decode steps' appends), so its cost
+ * scales with the chunk, not with the prior; it then sets vt_rows[b] =
+ * min(prior[b] + q_len[b], ctx). The caller zeroes vt_rows[b] (or lowers it
+ * to the rows it knows unchanged) for a new sequence in slot b and
+ * whenever it writes V cache rows below vt_rows[b] by other means (a copied
+ * prefix, for example). Outputs equal vm_gated_attn_prefill's bit for bit.
+ * No counterpart in the reference, which keeps no transposed V.              */
+int vm_gated_attn_prefill_staged(vm_bf16* out, int64_t out_st, int64_t out_sb,
+                                 const vm_bf16* qkv, int64_t qkv_st, int64_t qkv_sb,
+                                 vm_bf16* k_cache, vm_bf16* v_cache,
+                                 int64_t c_st, int64_t c_sh, int64_t c_sb, int64_t ctx,
+                                 const vm_bf16* qw, const vm_bf16* kw,
+                                 const float* cos_tab, const float* sin_tab,
+                                 const int32_t* prior, const int32_t* q_lengths,
+                                 int B, int T, int Hq, int Hk, int D, int half_rot,
+                                 float eps, float w_offset, int32_t* vt_rows,
+                                 void* vt, size_t vt_bytes, vm_stream stream);
 
 /* ---- f1: linear!((; y), x, W) (src/linear.jl:40-57): y = W^T x ------------
  * The qkv projection in front of the block and the Wo projection after it

@@ -414,3 +414,49 @@ def test_profile_skip_staging_reuses_staged_rows(vm):
     torch.cuda.synchronize()
     assert torch.equal(out1, out2)
     assert torch.equal(k1, layer.K_cache) and torch.equal(v1, layer.V_cache)
+
+
+def test_staged_prefill_chunks_equal_full_staging(vm):
+    """vm_gated_attn_prefill_staged over a chunk-by-chunk, ragged prefill (B = 2):
+    each chunk stages only its own rows into the kept V^T workspace, and rows
+    written at a sequence's end between chunks (as decode steps append them) are
+    staged by the next chunk. Every output and both caches equal those of the
+    per-call full staging, bit for bit, and rows[b] = prior[b] + q_len[b] after
+    each call. After reset_(b), a rewritten prefix of sequence b is staged
+    again."""
+    banner("staged V^T prefill: chunks == full staging")
+    B, T, ctx = 2, 384, 2048
+    cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
+    qw, kw = to_dev(normal_bf16((D,), 351, scale=0.05)), to_dev(normal_bf16((D,), 352, scale=0.05))
+    m = vm.AttnModel(cfg)
+    la = vm.attn_layer(cfg, qw, kw)  # full staging on every call
+    lb = vm.attn_layer(cfg, qw, kw)  # kept V^T workspace
+    st = vm.StagedV(cfg, B)
+
+    def chunk(prior, qlen, seed):
+        qkv = to_dev(normal_bf16((B, T, S, D), seed))
+        p, q = i32(np.array(prior, np.int32)), i32(np.array(qlen, np.int32))
+        oa = vm.gated_attn_prefill(la, m, qkv, T, B, prior=p, q_lengths=q)
+        ob = vm.gated_attn_prefill(lb, m, qkv, T, B, prior=p, q_lengths=q, staged=st)
+        torch.cuda.synchronize()
+        print(f"chunk prior={prior} q_len={qlen}: rows held {st.rows.tolist()}", flush=True)
+        for bb in range(B):  # rows past q_len[b] are not written
+            assert torch.equal(oa[bb, :qlen[bb]].view(torch.int16), ob[bb, :qlen[bb]].view(torch.int16))
+        assert torch.equal(la.K_cache, lb.K_cache) and torch.equal(la.V_cache, lb.V_cache)
+        assert st.rows.tolist() == [a + b for a, b in zip(prior, qlen)]
+        assert st.state[B:].tolist() == [0] * B  # arrival counters left zero
+
+    def write_rows(b, r0, r1, seed):
+        for c, s in ((la.K_cache, seed), (la.V_cache, seed + 1)):
+            c[b, :, r0:r1, :] = to_dev(normal_bf16((HK, r1 - r0, D), s))
+        lb.K_cache.copy_(la.K_cache)
+        lb.V_cache.copy_(la.V_cache)
+
+    chunk([0, 0], [384, 200], 353)
+    chunk([384, 200], [100, 384], 354)
+    write_rows(0, 484, 491, 355)  # 7 rows past each sequence's end, not staged yet
+    write_rows(1, 584, 591, 357)
+    chunk([491, 591], [250, 31], 359)
+    write_rows(0, 0, 64, 360)  # a rewritten prefix: sequence 0 must be staged again
+    st.reset_(0)
+    chunk([741, 622], [64, 64], 362)

@@ -24,7 +24,7 @@ from .ops import (attention, attention_, decode_attention, decode_attention_,  #
                   linear_add_rms_norm_, linear_add_rms_norm_workspace_bytes,
                   deltanet_sequence_chunked_, deltanet_sequence_workspace_bytes)
 from .layer import (AttnConfig, AttnLayer, AttnModel, CaptureSession, Generation,  # noqa: F401
-                    attn_layer, decode_, forward, gated_attn_decode_, gated_attn_prefill)
+                    StagedV, attn_layer, decode_, forward, gated_attn_decode_, gated_attn_prefill)
 from .model import (Model, ModelConfig, generate_, generate_captured_, mlp_,  # noqa: F401
                     prefill_, random_model, step_)
 from .deltanet_layer import (DeltaNetConfig, DeltaNetLayer, DeltaNetSpace,  # noqa: F401

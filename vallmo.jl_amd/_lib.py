@@ -107,6 +107,10 @@ _SIGS = {
     "vm_gated_attn_prefill": (_c_i, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _p, _c_i64,
                                      _c_i64, _c_i64, _c_i64, _p, _p, _p, _p, _p, _p, _c_i, _c_i,
                                      _c_i, _c_i, _c_i, _c_i, _c_f, _c_f, _p, _c_sz, _p]),
+    "vm_gated_attn_prefill_staged": (_c_i, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _p,
+                                            _c_i64, _c_i64, _c_i64, _c_i64, _p, _p, _p, _p, _p,
+                                            _p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_f,
+                                            _p, _p, _c_sz, _p]),
     "vm_linear_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i64, _c_i64, _c_i64]),
     "vm_linear": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i, _c_i, _c_i, _p, _c_sz, _p]),
     "vm_rms_norm": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i, _c_i, _c_f, _c_f, _p]),

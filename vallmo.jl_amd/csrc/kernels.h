@@ -102,6 +102,11 @@ struct VtArgs {
   int vt_tiles;
   const int32_t* prior;      // nullable -> 0
   const int32_t* q_lengths;  // nullable -> L
+  // nullable, int32[2B]: [b] = leading V rows of sequence b that vt already
+  // holds from earlier calls (rows below min(vt_rows[b], prior[b]) are not
+  // staged again; set to k_len at the end), [B + b] = an arrival counter that
+  // is zero between calls
+  int32_t* vt_rows;
   int B, Hk, L;
   int64_t ctx;
   // fused cache append (k_raw != nullptr): the chunk's K rows are normed,

@@ -119,9 +119,14 @@ __device__ __forceinline__ FItem item_ranked(const PrefillArgs& a, int i, bool c
 // the key order of the P^T operand that lane half h holds for key half ks (the
 // S^T accumulator layout).
 //
-// One workgroup per (32-key tile, kv head, sequence): the tile's 32 V rows into
-// LDS (one 512-byte row per wave load), out as one V^T tile (coalesced). Keys
-// past the attended length repeat the last one (they are masked; V stays finite).
+// Workgroup x of (kv head, sequence) stages tiles t0 + x, t0 + x + gridDim.x, ...
+// below the attended length: the tile's 32 V rows into LDS (one 512-byte row per
+// wave load), out as one V^T tile (coalesced). t0 = 0, or with vt_rows the tile
+// holding row min(vt_rows[b], prior[b]): the rows below it are already in the
+// workspace from earlier calls, so a chunk-by-chunk prefill stages each row once
+// (plus the one partial tile at each chunk's start); the last workgroup of the
+// sequence to finish sets vt_rows[b] = k_len, counting arrivals in vt_rows[B + b]. Keys past the attended
+// length repeat the last one (they are masked; V stays finite).
 // With the fused append (k_raw set), the chunk's keys prior .. k_len-1 come from
 // the packed projection instead of the cache: their K rows are normed and
 // rotated into the K cache and their V rows copied into the V cache, as
@@ -129,67 +134,84 @@ __device__ __forceinline__ FItem item_ranked(const PrefillArgs& a, int i, bool c
 // src/llm/qwen35.jl:306-307), and the V^T tile is built from the same rows.
 constexpr int VT_WAVES = 16;  // waves per V^T staging workgroup
 __global__ __launch_bounds__(64 * VT_WAVES) void vt_transpose_kernel(VtArgs a) {
-  const int t = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int hk = blockIdx.y, b = blockIdx.z;
   const int q_len = a.q_lengths ? min(a.q_lengths[b], a.L) : a.L;
   const int64_t prior = a.prior ? a.prior[b] : 0;
   const int64_t k_len = min(prior + q_len, a.ctx);
-  if ((int64_t)t * FN >= k_len) return;
+  const int64_t held = a.vt_rows ? min((int64_t)max(a.vt_rows[b], 0), prior) : 0;
+  const int t_end = (int)((k_len + FN - 1) / FN);
   __shared__ __attribute__((aligned(16))) uint16_t tile[FN][HEAD_DIM + 8];  // 16-B row pad
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t cache_off = (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
   const bool fused = a.k_raw != nullptr;
   constexpr int RW = FN / VT_WAVES;  // rows per wave: r = wave + VT_WAVES j
-  // every load of the wave's rows first (one memory latency, not RW of them)
-  uint2 vv[RW], kv[RW];
-  float4 cv[RW], sv[RW];
-  bool app[RW];
-  int64_t key_of[RW];
+  for (int t = (int)(held / FN) + blockIdx.x; t < t_end; t += gridDim.x) {
+    // every load of the wave's rows first (one memory latency, not RW of them)
+    uint2 vv[RW], kv[RW];
+    float4 cv[RW], sv[RW];
+    bool app[RW];
+    int64_t key_of[RW];
 #pragma unroll
-  for (int j = 0; j < RW; ++j) {
-    const int64_t key = (int64_t)t * FN + wave + VT_WAVES * j;
-    const int64_t src = min(key, k_len - 1);
-    const bool chunk = fused && src >= prior;  // a key of this chunk: not in the cache yet
-    const int64_t raw_off = (int64_t)b * a.raw_sb + (int64_t)hk * a.raw_sh + (src - prior) * a.raw_st;
-    const uint16_t* vp = chunk ? a.v_raw + raw_off : a.v + cache_off + src * a.v_st;
-    vv[j] = *reinterpret_cast<const uint2*>(vp + 4 * lane);
-    app[j] = chunk && key == src;  // append column `key` (position key, 0-based)
-    key_of[j] = key;
-    if (app[j]) {
-      kv[j] = *reinterpret_cast<const uint2*>(a.k_raw + raw_off + 4 * lane);
-      const int i0 = 4 * (lane & 7);
-      cv[j] = *reinterpret_cast<const float4*>(a.cos_tab + key * HALF_ROT + i0);
-      sv[j] = *reinterpret_cast<const float4*>(a.sin_tab + key * HALF_ROT + i0);
+    for (int j = 0; j < RW; ++j) {
+      const int64_t key = (int64_t)t * FN + wave + VT_WAVES * j;
+      const int64_t src = min(key, k_len - 1);
+      const bool chunk = fused && src >= prior;  // a key of this chunk: not in the cache yet
+      const int64_t raw_off = (int64_t)b * a.raw_sb + (int64_t)hk * a.raw_sh + (src - prior) * a.raw_st;
+      const uint16_t* vp = chunk ? a.v_raw + raw_off : a.v + cache_off + src * a.v_st;
+      vv[j] = *reinterpret_cast<const uint2*>(vp + 4 * lane);
+      app[j] = chunk && key == src;  // append column `key` (position key, 0-based)
+      key_of[j] = key;
+      if (app[j]) {
+        kv[j] = *reinterpret_cast<const uint2*>(a.k_raw + raw_off + 4 * lane);
+        const int i0 = 4 * (lane & 7);
+        cv[j] = *reinterpret_cast<const float4*>(a.cos_tab + key * HALF_ROT + i0);
+        sv[j] = *reinterpret_cast<const float4*>(a.sin_tab + key * HALF_ROT + i0);
+      }
     }
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+      const int r = wave + VT_WAVES * j;
+      *reinterpret_cast<uint2*>(&tile[r][4 * lane]) = vv[j];
+      if (app[j]) {
+        const int64_t key = key_of[j];
+        *reinterpret_cast<uint2*>(a.v + cache_off + key * a.v_st + 4 * lane) = vv[j];
+        float x[4] = {__uint_as_float(kv[j].x << 16), __uint_as_float(kv[j].x & 0xffff0000u),
+                      __uint_as_float(kv[j].y << 16), __uint_as_float(kv[j].y & 0xffff0000u)};
+        norm_rope_row_cs(x, a.kw, cv[j], sv[j], a.eps, a.w_offset, lane);
+        store_row4(a.kc + cache_off + key * a.v_st, lane, x);
+      }
+    }
+    __syncthreads();
+    uint16_t* dst = a.vt + ((int64_t)b * a.Hk + hk) * a.vt_tiles * FT + (int64_t)t * FT;
+#pragma unroll
+    for (int o = tid; o < HEAD_DIM * 4; o += 64 * VT_WAVES) {
+      const int f = o >> 6, l = o & 63;
+      const int d = 32 * (f >> 1) + (l & 31);
+      const int k0 = 16 * (f & 1) + 4 * (l >> 5);
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int u0 = 2 * e, u1 = 2 * e + 1;  // element u: key k0 + (u & 3) + 8 (u >> 2)
+        const uint32_t lo = tile[k0 + (u0 & 3) + 8 * (u0 >> 2)][d];
+        const uint32_t hi = tile[k0 + (u1 & 3) + 8 * (u1 >> 2)][d];
+        w[e] = lo | (hi << 16);
+      }
+      *reinterpret_cast<uint4*>(dst + o * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    __syncthreads();  // the tile is read out before the next one is written
   }
-#pragma unroll
-  for (int j = 0; j < RW; ++j) {
-    const int r = wave + VT_WAVES * j;
-    *reinterpret_cast<uint2*>(&tile[r][4 * lane]) = vv[j];
-    if (app[j]) {
-      const int64_t key = key_of[j];
-      *reinterpret_cast<uint2*>(a.v + cache_off + key * a.v_st + 4 * lane) = vv[j];
-      float x[4] = {__uint_as_float(kv[j].x << 16), __uint_as_float(kv[j].x & 0xffff0000u),
-                    __uint_as_float(kv[j].y << 16), __uint_as_float(kv[j].y & 0xffff0000u)};
-      norm_rope_row_cs(x, a.kw, cv[j], sv[j], a.eps, a.w_offset, lane);
-      store_row4(a.kc + cache_off + key * a.v_st, lane, x);
+  if (a.vt_rows) {
+    // the last of the sequence's workgroups to finish records the rows the tiles
+    // now hold: every workgroup has read vt_rows[b] by then (its loop bounds)
+    __syncthreads();
+    if (tid == 0) {
+      int32_t* arrived = a.vt_rows + a.B + b;
+      const int n = (int)(gridDim.x * gridDim.y);
+      if (atomicAdd(arrived, 1) == n - 1) {
+        a.vt_rows[b] = (int32_t)k_len;
+        *arrived = 0;  // zero again for the next call
+      }
     }
-  }
-  __syncthreads();
-  uint16_t* dst = a.vt + ((int64_t)b * a.Hk + hk) * a.vt_tiles * FT + (int64_t)t * FT;
-#pragma unroll
-  for (int o = tid; o < HEAD_DIM * 4; o += 64 * VT_WAVES) {
-    const int f = o >> 6, l = o & 63;
-    const int d = 32 * (f >> 1) + (l & 31);
-    const int k0 = 16 * (f & 1) + 4 * (l >> 5);
-    uint32_t w[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int u0 = 2 * e, u1 = 2 * e + 1;  // element u: key k0 + (u & 3) + 8 (u >> 2)
-      const uint32_t lo = tile[k0 + (u0 & 3) + 8 * (u0 >> 2)][d];
-      const uint32_t hi = tile[k0 + (u1 & 3) + 8 * (u1 >> 2)][d];
-      w[e] = lo | (hi << 16);
-    }
-    *reinterpret_cast<uint4*>(dst + o * 8) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 
@@ -1051,7 +1073,12 @@ void prefill_fused_kernel(PrefillArgs a) {
 
 hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st) {
   if (a.B == 0 || a.Hk == 0 || a.vt_tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL(vt_transpose_kernel, dim3(a.vt_tiles, a.Hk, a.B), dim3(64 * VT_WAVES), 0, st, a);
+  // with vt_rows, a chunk of at most L rows spans at most L / 32 + 1 new tiles;
+  // rows between vt_rows and the prior (written since, e.g. by decode steps)
+  // are staged by the same workgroups' later iterations
+  const int chunk_tiles = (a.L + FN - 1) / FN + 1;
+  const int gx = a.vt_rows && chunk_tiles < a.vt_tiles ? chunk_tiles : a.vt_tiles;
+  hipLaunchKernelGGL(vt_transpose_kernel, dim3(gx, a.Hk, a.B), dim3(64 * VT_WAVES), 0, st, a);
   return hipGetLastError();
 }
 

@@ -563,13 +563,15 @@ size_t vm_prefill_scratch_bytes(int B, int Hk, int D, int64_t ctx) {
   return (size_t)B * Hk * prefill_vt_tiles(ctx) * vm::PREFILL_VT_TILE_BYTES;
 }
 
-int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm_bf16* qkv,
-                          int64_t qkv_st, int64_t qkv_sb, vm_bf16* kc, vm_bf16* vc, int64_t c_st,
-                          int64_t c_sh, int64_t c_sb, int64_t ctx, const vm_bf16* qw,
-                          const vm_bf16* kw, const float* cs, const float* sn,
-                          const int32_t* prior, const int32_t* q_lengths, int B, int T, int Hq,
-                          int Hk, int D, int half_rot, float eps, float w_offset, void* scratch,
-                          size_t scratch_bytes, vm_stream st) {
+// vm_gated_attn_prefill and vm_gated_attn_prefill_staged (vt_rows set)
+static int gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm_bf16* qkv,
+                              int64_t qkv_st, int64_t qkv_sb, vm_bf16* kc, vm_bf16* vc,
+                              int64_t c_st, int64_t c_sh, int64_t c_sb, int64_t ctx,
+                              const vm_bf16* qw, const vm_bf16* kw, const float* cs,
+                              const float* sn, const int32_t* prior, const int32_t* q_lengths,
+                              int B, int T, int Hq, int Hk, int D, int half_rot, float eps,
+                              float w_offset, int32_t* vt_rows, void* scratch,
+                              size_t scratch_bytes, vm_stream st) {
   // every argument is checked before anything is launched
   REQUIRE(out && qw, VM_E_ARG, "gated_attn_prefill: NULL pointer argument");
   TRY(check_aligned(out, "out"));
@@ -609,7 +611,8 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm
   vm::VtArgs t{};
   t.v = vc; t.v_st = c_st; t.v_sh = c_sh; t.v_sb = c_sb;
   t.vt = reinterpret_cast<uint16_t*>(scratch); t.vt_tiles = (int)prefill_vt_tiles(ctx);
-  t.prior = prior; t.q_lengths = q_lengths; t.B = B; t.Hk = Hk; t.L = T; t.ctx = ctx;
+  t.prior = prior; t.q_lengths = q_lengths; t.vt_rows = vt_rows;
+  t.B = B; t.Hk = Hk; t.L = T; t.ctx = ctx;
   t.kc = kc; t.k_raw = qkv + 2 * Hq * Dl; t.v_raw = qkv + (2 * Hq + Hk) * Dl;
   t.raw_st = qkv_st; t.raw_sh = Dl; t.raw_sb = qkv_sb;
   t.kw = kw; t.cos_tab = cs; t.sin_tab = sn; t.eps = eps; t.w_offset = w_offset;
@@ -620,6 +623,34 @@ int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm
   return hip_status(timed_ext(VM_K_PREFILL, S(st),
                               [&](hipEvent_t t0, hipEvent_t t1) { return vm::launch_prefill_fused(a, S(st), t0, t1); }),
                     "gated_attn_prefill");
+}
+
+int vm_gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm_bf16* qkv,
+                          int64_t qkv_st, int64_t qkv_sb, vm_bf16* kc, vm_bf16* vc, int64_t c_st,
+                          int64_t c_sh, int64_t c_sb, int64_t ctx, const vm_bf16* qw,
+                          const vm_bf16* kw, const float* cs, const float* sn,
+                          const int32_t* prior, const int32_t* q_lengths, int B, int T, int Hq,
+                          int Hk, int D, int half_rot, float eps, float w_offset, void* scratch,
+                          size_t scratch_bytes, vm_stream st) {
+  return gated_attn_prefill(out, out_st, out_sb, qkv, qkv_st, qkv_sb, kc, vc, c_st, c_sh, c_sb, ctx,
+                            qw, kw, cs, sn, prior, q_lengths, B, T, Hq, Hk, D, half_rot, eps,
+                            w_offset, nullptr, scratch, scratch_bytes, st);
+}
+
+int vm_gated_attn_prefill_staged(vm_bf16* out, int64_t out_st, int64_t out_sb, const vm_bf16* qkv,
+                                 int64_t qkv_st, int64_t qkv_sb, vm_bf16* kc, vm_bf16* vc,
+                                 int64_t c_st, int64_t c_sh, int64_t c_sb, int64_t ctx,
+                                 const vm_bf16* qw, const vm_bf16* kw, const float* cs,
+                                 const float* sn, const int32_t* prior, const int32_t* q_lengths,
+                                 int B, int T, int Hq, int Hk, int D, int half_rot, float eps,
+                                 float w_offset, int32_t* vt_rows, void* vt, size_t vt_bytes,
+                                 vm_stream st) {
+  REQUIRE(vt_rows != nullptr, VM_E_ARG, "gated_attn_prefill_staged: NULL vt_rows");
+  REQUIRE(((uintptr_t)vt_rows & 3) == 0, VM_E_ARG,
+          "gated_attn_prefill_staged: vt_rows must be 4-byte aligned");
+  return gated_attn_prefill(out, out_st, out_sb, qkv, qkv_st, qkv_sb, kc, vc, c_st, c_sh, c_sb, ctx,
+                            qw, kw, cs, sn, prior, q_lengths, B, T, Hq, Hk, D, half_rot, eps,
+                            w_offset, vt_rows, vt, vt_bytes, st);
 }
 
 // ---- f2: the rest of the decode step ----------------------------------------

@@ -121,6 +121,32 @@ class AttnModel:
         return self.prefill_space
 
 
+class StagedV:
+    """One attention layer's V^T workspace kept between the chunks of a chunk-by-
+    chunk prefill (vm_gated_attn_prefill_staged): ``vt`` holds the V^T tiles of
+    the first ``rows[b]`` cache rows of each sequence, so a chunk stages only its
+    own rows (and rows appended since, e.g. by decode steps) instead of the
+    whole prior. ``reset_(b)`` (all sequences when b is None) forgets what is
+    held: call it for a new sequence in slot b and after writing V cache rows
+    below ``rows[b]`` by any other means."""
+
+    def __init__(self, cfg: AttnConfig, B: int, ctx: int | None = None):
+        ctx = cfg.Ctx if ctx is None else int(ctx)
+        need = int(ops._lib.load().vm_prefill_scratch_bytes(B, cfg.Hkv, cfg.Dh, ctx))
+        self.B, self.ctx = B, ctx
+        self.vt = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
+        # [0, B): rows held per sequence; [B, 2B): the library's arrival counters
+        self.state = torch.zeros(2 * B, dtype=torch.int32, device="cuda")
+        self.rows = self.state[:B]
+
+    def reset_(self, b: int | None = None):
+        if b is None:
+            self.rows.zero_()
+        else:
+            self.rows[b] = 0
+        return self
+
+
 class Generation:
     """The engine's device state (generate.jl:54-72). positions[b]: the 1-based
     column of the current token = rope column = cache column = attended length
@@ -201,7 +227,7 @@ def gated_attn_decode_(O, l: AttnLayer, m: AttnModel, gen: Generation, qkv, *,
 
 
 def gated_attn_prefill(l: AttnLayer, m: AttnModel, qkv, T: int, B: int, *, offset: int = 0,
-                       prior=None, q_lengths=None, out=None):
+                       prior=None, q_lengths=None, out=None, staged: StagedV | None = None):
     """Prefill / chunked prefill of the attention block (qwen35.jl:293-317), fused:
     head_rmsnorm + apply_rope of q and k, the K/V cache write at columns
     offset+1..offset+T, causal attention over columns 1..offset+T, and the
@@ -211,6 +237,8 @@ def gated_attn_prefill(l: AttnLayer, m: AttnModel, qkv, T: int, B: int, *, offse
     ``offset`` is the uniform prior cache length (the reference's keyword);
     ``prior``/``q_lengths`` (B,) int32 device tensors make the batch ragged
     (each sequence b appends q_lengths[b] <= T tokens after prior[b]).
+    ``staged`` (this layer's StagedV) keeps the V^T workspace between chunks, so
+    the call stages only the chunk (vm_gated_attn_prefill_staged; same outputs).
     Returns out :: torch (B, T, Hq*Dh).
     """
     cfg = m.cfg
@@ -247,12 +275,20 @@ def gated_attn_prefill(l: AttnLayer, m: AttnModel, qkv, T: int, B: int, *, offse
     else:
         ops._need(out, torch.bfloat16, "out")
     c = l.K_cache
-    ws = m.prefill_workspace(B, d["Ctx"])
-    call("vm_gated_attn_prefill", ops._p(out), out.stride(1), out.stride(0), ops._p(qkv4),
-         qkv4.stride(1), qkv4.stride(0), ops._p(l.K_cache), ops._p(l.V_cache), c.stride(2),
-         c.stride(1), c.stride(0), d["Ctx"], ops._p(l.qw), ops._p(l.kw), ops._p(m.rope["cos"]),
-         ops._p(m.rope["sin"]), ops._p(prior), ops._p(q_lengths), B, T, cfg.Hq, cfg.Hkv, cfg.Dh,
-         cfg.rot_half, float(cfg.eps), 1.0, ops._p(ws), ws.numel(), ops._stream())
+    args = (ops._p(out), out.stride(1), out.stride(0), ops._p(qkv4), qkv4.stride(1),
+            qkv4.stride(0), ops._p(l.K_cache), ops._p(l.V_cache), c.stride(2), c.stride(1),
+            c.stride(0), d["Ctx"], ops._p(l.qw), ops._p(l.kw), ops._p(m.rope["cos"]),
+            ops._p(m.rope["sin"]), ops._p(prior), ops._p(q_lengths), B, T, cfg.Hq, cfg.Hkv,
+            cfg.Dh, cfg.rot_half, float(cfg.eps), 1.0)
+    if staged is None:
+        ws = m.prefill_workspace(B, d["Ctx"])
+        call("vm_gated_attn_prefill", *args, ops._p(ws), ws.numel(), ops._stream())
+        return out
+    if staged.B != B or staged.ctx != d["Ctx"]:
+        raise DimensionMismatch(f"StagedV for (B, Ctx) = ({staged.B}, {staged.ctx}) used with "
+                                f"({B}, {d['Ctx']})")
+    call("vm_gated_attn_prefill_staged", *args, ops._p(staged.state), ops._p(staged.vt),
+         staged.vt.numel(), ops._stream())
     return out
 
 
@@ -290,19 +326,20 @@ def decode_(h, l: AttnLayer, m: AttnModel, gen: Generation, xn, *, advance: bool
 
 
 def forward(l: AttnLayer, m: AttnModel, xn, T: int, B: int, *, offset: int = 0, prior=None,
-            q_lengths=None):
+            q_lengths=None, staged: StagedV | None = None):
     """forward(l::AttnLayer, m, xn, T, B; offset) — qwen35.jl:292-318, hidden
     state to hidden state for a prompt chunk: qkv = linear(xn, Wqkv) (:296), the
     fused gated prefill (:297-315) into the Wo input, h = linear(·, Wo)
     (:316-317). xn :: (D, T*B) (torch (B, T, D)); returns h, torch (B, T, D).
-    Eager: allocates its temporaries, as the reference's prefill does."""
+    Eager: allocates its temporaries, as the reference's prefill does. ``staged``:
+    as for gated_attn_prefill."""
     cfg = m.cfg
     _need_proj(l, cfg)
     xn2 = xn.reshape(B * T, cfg.D)
     qkv = ops.linear(xn2, l.Wqkv, workspace=m.linear_workspace(
         ops.linear_workspace_bytes(xn2, l.Wqkv)))["y"]
     o = gated_attn_prefill(l, m, qkv.view(B, T, 2 * cfg.Hq + 2 * cfg.Hkv, cfg.Dh), T, B,
-                           offset=offset, prior=prior, q_lengths=q_lengths)
+                           offset=offset, prior=prior, q_lengths=q_lengths, staged=staged)
     o2 = o.reshape(B * T, cfg.Hq * cfg.Dh)
     ws = m.linear_workspace(ops.linear_workspace_bytes(o2, l.Wo))
     return ops.linear(o2, l.Wo, workspace=ws)["y"].view(B, T, cfg.D)
