@@ -63,38 +63,46 @@ const char* status_name(hipblasStatus_t s) {
 // The heuristic ranks candidates by a model, and on MI355X its first pick can
 // be a third slower than the best of its own top candidates (M x N x K =
 // 18432 x 4096 x 2560: 381 against 286 us). So a new plan times up to NTUNE
-// candidates on scratch buffers of the problem's shape (N(0,1) bf16 data, one
-// warm-up and three timed runs each, on a private stream) and keeps the
-// fastest. The heuristic's first is kept unless another beats it by 3% or
-// more, so close calls do not flip from process to process.
-// Problems with fewer than TUNE_MIN_N columns (decode batches) are not timed:
-// their kernels are memory-bound and run about as long as the host takes to
-// submit one, so back-to-back runs measure the host, and their weights sit in
-// the last-level cache between runs, which a model's step never sees (a pick
-// made that way ran 30 us in a decode step where the first runs 23.5 us).
+// candidates on scratch buffers of the problem's shape (N(0,1) bf16 data, on
+// a private stream) and keeps the fastest. The heuristic's first is kept
+// unless another beats it by 3% or more, so close calls do not flip from
+// process to process.
+// Problems of fewer than COLD_N columns (decode batches) are memory-bound and
+// a model's step streams their weights from HBM: timed on one weight buffer,
+// the buffer stays in the 256 MB last-level cache and the ranking is wrong (a
+// pick made that way ran 30.1 us in a decode step, the heuristic's first 25.5,
+// another candidate 23.5). They are timed on rotating copies of the weights
+// that together exceed that cache, 2 x copies launches per candidate after a
+// warm-up pass, queued back to back so that the GPU, not the host, sets the
+// time. Larger problems: one warm-up and three timed runs on one buffer.
 // VM_LINEAR_TUNE=0 keeps the first always. If any step fails (for example an
 // allocation while a stream of the device is being captured), the plan keeps
 // the first and the error is cleared. Returns the chosen index into `cand`.
 constexpr int NTUNE = 16;
-constexpr int TUNE_MIN_N = 256;
+constexpr int COLD_N = 256;
+constexpr size_t COLD_BYTES = (size_t)768 << 20;  // rotated weights: 3x the last-level cache
 int tune_algo(hipblasLtHandle_t h, const Plan& p, const hipblasLtMatmulHeuristicResult_t* res,
               const int* cand, int nc, int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy) {
   const char* env = getenv("VM_LINEAR_TUNE");
-  if (nc < 2 || N < TUNE_MIN_N || (env && strcmp(env, "0") == 0)) return 0;
+  if (nc < 2 || (env && strcmp(env, "0") == 0)) return 0;
   size_t wsmax = 0;
   for (int i = 0; i < nc; ++i) wsmax = std::max(wsmax, (size_t)res[cand[i]].workspaceSize);
+  const size_t abytes = ((size_t)ldw * M * 2 + 255) & ~(size_t)255;  // one copy, 256-B aligned
+  const int copies =
+      N < COLD_N ? (int)std::min<size_t>(64, std::max<size_t>(2, COLD_BYTES / abytes + 1)) : 1;
+  const int warm = copies > 1 ? copies : 1, timed = copies > 1 ? 2 * copies : 3;
   void *A = nullptr, *B = nullptr, *D = nullptr, *W = nullptr;
   hipStream_t st = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   int best = 0;
   bool ok = hipStreamCreateWithFlags(&st, hipStreamNonBlocking) == hipSuccess &&
             hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess &&
-            hipMalloc(&A, (size_t)ldw * M * 2) == hipSuccess &&
+            hipMalloc(&A, abytes * copies) == hipSuccess &&
             hipMalloc(&B, (size_t)ldx * N * 2) == hipSuccess &&
             hipMalloc(&D, (size_t)ldy * N * 2) == hipSuccess &&
             (wsmax == 0 || hipMalloc(&W, wsmax) == hipSuccess) &&
-            launch_fill_normal(static_cast<uint16_t*>(A), (int64_t)ldw * M, 0x51u, 1.0f, 0.0f, st) ==
-                hipSuccess &&
+            launch_fill_normal(static_cast<uint16_t*>(A), (int64_t)(abytes / 2) * copies, 0x51u, 1.0f,
+                               0.0f, st) == hipSuccess &&
             launch_fill_normal(static_cast<uint16_t*>(B), (int64_t)ldx * N, 0x52u, 1.0f, 0.0f, st) ==
                 hipSuccess;
   if (ok) {
@@ -103,9 +111,10 @@ int tune_algo(hipblasLtHandle_t h, const Plan& p, const hipblasLtMatmulHeuristic
     for (int i = 0; i < nc && ok; ++i) {
       const hipblasLtMatmulHeuristicResult_t& r = res[cand[i]];
       bool run_ok = true;
-      for (int rep = 0; rep < 4 && run_ok; ++rep) {
-        if (rep == 1) run_ok = hipEventRecord(e0, st) == hipSuccess;
-        run_ok = run_ok && hipblasLtMatmul(h, p.desc, &alpha, A, p.a, B, p.b, &beta, D, p.d, D, p.d,
+      for (int rep = 0; rep < warm + timed && run_ok; ++rep) {
+        if (rep == warm) run_ok = hipEventRecord(e0, st) == hipSuccess;
+        const void* a = static_cast<const char*>(A) + abytes * (size_t)(rep % copies);
+        run_ok = run_ok && hipblasLtMatmul(h, p.desc, &alpha, a, p.a, B, p.b, &beta, D, p.d, D, p.d,
                                            &r.algo, W, r.workspaceSize, st) == HIPBLAS_STATUS_SUCCESS;
       }
       float ms = 0.f;
