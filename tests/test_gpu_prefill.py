@@ -460,3 +460,18 @@ def test_staged_prefill_chunks_equal_full_staging(vm):
     write_rows(0, 0, 64, 360)  # a rewritten prefix: sequence 0 must be staged again
     st.reset_(0)
     chunk([741, 622], [64, 64], 362)
+    # the same StagedV used with another layer's cache (same prefix length, other
+    # rows) forgets what it held: that cache's prefix is staged
+    lc, ld = vm.attn_layer(cfg, qw, kw), vm.attn_layer(cfg, qw, kw)
+    for c, sd in ((lc.K_cache, 364), (lc.V_cache, 365)):
+        c[:, :, :64, :] = to_dev(normal_bf16((B, HK, 64, D), sd))
+    ld.K_cache.copy_(lc.K_cache)
+    ld.V_cache.copy_(lc.V_cache)
+    qkv = to_dev(normal_bf16((B, T, S, D), 363))
+    p, q = i32(np.array([64, 64], np.int32)), i32(np.array([100, 50], np.int32))
+    oc = vm.gated_attn_prefill(lc, m, qkv, T, B, prior=p, q_lengths=q)
+    od = vm.gated_attn_prefill(ld, m, qkv, T, B, prior=p, q_lengths=q, staged=st)
+    torch.cuda.synchronize()
+    assert st.rows.tolist() == [164, 114]
+    for bb, n in enumerate([100, 50]):
+        assert torch.equal(oc[bb, :n].view(torch.int16), od[bb, :n].view(torch.int16))

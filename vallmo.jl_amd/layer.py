@@ -128,7 +128,8 @@ class StagedV:
     own rows (and rows appended since, e.g. by decode steps) instead of the
     whole prior. ``reset_(b)`` (all sequences when b is None) forgets what is
     held: call it for a new sequence in slot b and after writing V cache rows
-    below ``rows[b]`` by any other means."""
+    below ``rows[b]`` by any other means. It belongs to one layer: used with
+    another layer's cache, it forgets everything first."""
 
     def __init__(self, cfg: AttnConfig, B: int, ctx: int | None = None):
         ctx = cfg.Ctx if ctx is None else int(ctx)
@@ -138,6 +139,7 @@ class StagedV:
         # [0, B): rows held per sequence; [B, 2B): the library's arrival counters
         self.state = torch.zeros(2 * B, dtype=torch.int32, device="cuda")
         self.rows = self.state[:B]
+        self.cache = None  # data_ptr of the V cache whose rows vt holds
 
     def reset_(self, b: int | None = None):
         if b is None:
@@ -287,6 +289,9 @@ def gated_attn_prefill(l: AttnLayer, m: AttnModel, qkv, T: int, B: int, *, offse
     if staged.B != B or staged.ctx != d["Ctx"]:
         raise DimensionMismatch(f"StagedV for (B, Ctx) = ({staged.B}, {staged.ctx}) used with "
                                 f"({B}, {d['Ctx']})")
+    if staged.cache != l.V_cache.data_ptr():  # another layer's tiles: stage everything
+        staged.reset_()
+        staged.cache = l.V_cache.data_ptr()
     call("vm_gated_attn_prefill_staged", *args, ops._p(staged.state), ops._p(staged.vt),
          staged.vt.numel(), ops._stream())
     return out
