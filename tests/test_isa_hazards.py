@@ -13,8 +13,8 @@ kernel by a data-flow pass over its basic blocks:
      every vector-memory / LDS operation in issue order;
   2. no instruction other than a dependent MFMA touches an MFMA's destination
      within 11 wait states of its issue (8-pass XDL write -> VALU read);
-  3. the fused prefill's epilogue drains its tile loads before the barrier after
-     which it reuses their LDS.
+  3. the fused prefill drains its tile loads before each barrier after which it
+     writes the LDS afresh (a pair's second item, the row-max re-prime).
 The checks were validated against deliberately weakened builds (a vmcnt raised
 by 8, a spill of a pending AGPR load) that they flag.
 """
@@ -181,20 +181,32 @@ def test_fused_prefill_no_async_or_mfma_hazard(fused_asm, causal):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-def test_fused_prefill_epilogue_waits_for_tile_loads_before_its_barrier(fused_asm, causal):
-    """The epilogue reuses K-object LDS for the gate/output regrouping, and the last
-    steps' tile loads (global_load_lds) write those objects. Each wave must drain
-    its own loads (vmcnt(0)) before the barrier that opens the epilogue, so no
-    wave's late tile load lands after another wave has started writing there."""
+def test_fused_prefill_lds_reuse_waits_for_tile_loads_before_its_barrier(fused_asm, causal):
+    """Where a workgroup starts writing LDS objects afresh -- a pair's second item
+    staging its q rows and first K tiles, the row-max pass re-priming its K
+    objects -- each wave must drain its own tile loads (vmcnt(0)) before the
+    barrier that releases the LDS, so no wave's late tile load lands after another
+    wave has started writing there. Such a restart is a global->LDS load after a
+    barrier with no product between them (the steps put products first)."""
     ks = kernels(fused_asm)
     body = ks[next(k for k in ks if "prefill_fused_kernel" in k and ("ILb1" in k) == causal)]
-    writes = [i for i, l in enumerate(body) if re.match(r"ds_write_b128 v\d+, a\[", l)]
-    assert writes, "epilogue gate writes (ds_write_b128 from AGPRs) not found"
-    first = writes[0]
-    bar = max(i for i in range(first) if body[i].startswith("s_barrier"))
-    last_dma = max((i for i in range(bar) if body[i].startswith("global_load_lds")), default=-1)
-    drains = [i for i in range(last_dma + 1, bar) if re.match(r"s_waitcnt vmcnt\(0\)", body[i])]
-    assert drains, "no vmcnt(0) between the last tile load and the epilogue's barrier"
+    restarts = 0
+    for i, line in enumerate(body):
+        if not line.startswith("global_load_lds"):
+            continue
+        bars = [j for j in range(i) if body[j].startswith("s_barrier")]
+        if not bars:
+            continue  # the workgroup's first loads
+        bar = bars[-1]
+        if any(body[j].startswith("v_mfma") for j in range(bar, i)):
+            continue  # a pipelined step: its loads target objects no wave still reads
+        if any(body[j].startswith("global_load_lds") for j in range(bar, i)):
+            continue  # checked at the first load after this barrier
+        restarts += 1
+        last_dma = max((j for j in range(bar) if body[j].startswith("global_load_lds")), default=-1)
+        drains = [j for j in range(last_dma + 1, bar) if re.match(r"s_waitcnt vmcnt\(0\)", body[j])]
+        assert drains, f"no vmcnt(0) between the last tile load (line {last_dma}) and the barrier at {bar}"
+    assert restarts >= 1, "no LDS restart found (the pair's second item or the row-max re-prime)"
 
 
 def test_checker_flags_a_read_before_its_wait():

@@ -150,9 +150,11 @@ __device__ __forceinline__ float sigmoidf(float x) { return fast_rcp(1.0f + __ex
 // 8-byte load). The rotate-half partner of d < 32 is d + 32, i.e. lane l ^ 8.
 // Norm + RoPE of one row held as 4 floats per lane (d = 4*lane + c):
 // qknorm_rope_append.jl:41-54 / :80-92.
-__device__ __forceinline__ void norm_rope_row_cs(float x[4], const uint16_t* __restrict__ w,
-                                                 float4 cv, float4 sv, float eps, float w_offset,
-                                                 int lane) {
+// wv: this lane's 4 norm weights (w + 4 lane, loaded by the caller: a kernel
+// that stages several rows loads them once, ahead of its stores, so no row's
+// weight load waits behind an earlier row's stores)
+__device__ __forceinline__ void norm_rope_row_wv(float x[4], uint2 wv, float4 cv, float4 sv, float eps,
+                                                 float w_offset, int lane) {
   // Every rounding step is spelled out (fmaf / __fmul_rn / __fadd_rn): left to
   // contraction, the compiler would fuse differently in each kernel that
   // inlines this, and the cache rows that decode and prefill append must be
@@ -163,7 +165,6 @@ __device__ __forceinline__ void norm_rope_row_cs(float x[4], const uint16_t* __r
   ss = fmaf(x[3], x[3], ss);
   ss = wave_sum_all(ss);
   const float r = 1.0f / sqrtf(fmaf(ss, 1.0f / HEAD_DIM, eps));
-  uint2 wv = *reinterpret_cast<const uint2*>(w + 4 * lane);
   float wf[4] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xffff0000u),
                  __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xffff0000u)};
 #pragma unroll
@@ -182,6 +183,11 @@ __device__ __forceinline__ void norm_rope_row_cs(float x[4], const uint16_t* __r
       for (int c = 0; c < 4; ++c) x[c] = fmaf(x[c], cc[c], __fmul_rn(other[c], ssn[c]));
     }
   }
+}
+__device__ __forceinline__ void norm_rope_row_cs(float x[4], const uint16_t* __restrict__ w,
+                                                 float4 cv, float4 sv, float eps, float w_offset,
+                                                 int lane) {
+  norm_rope_row_wv(x, *reinterpret_cast<const uint2*>(w + 4 * lane), cv, sv, eps, w_offset, lane);
 }
 // cs, sn: the position's cos / sin table rows (lanes 0..15 read 4 each)
 __device__ __forceinline__ void norm_rope_row(float x[4], const uint16_t* __restrict__ w,

@@ -133,6 +133,7 @@ __device__ __forceinline__ FItem item_ranked(const PrefillArgs& a, int i, bool c
 // knorm_rope_append does (src/kernels/qknorm_rope_append.jl:59-98; prefill
 // src/llm/qwen35.jl:306-307), and the V^T tile is built from the same rows.
 constexpr int VT_WAVES = 16;  // waves per V^T staging workgroup
+constexpr int VT_TP = 1;      // tiles per pass: their loads are issued together
 __global__ __launch_bounds__(64 * VT_WAVES) void vt_transpose_kernel(VtArgs a) {
   const int hk = blockIdx.y, b = blockIdx.z;
   const int q_len = a.q_lengths ? min(a.q_lengths[b], a.L) : a.L;
@@ -140,12 +141,15 @@ __global__ __launch_bounds__(64 * VT_WAVES) void vt_transpose_kernel(VtArgs a) {
   const int64_t k_len = min(prior + q_len, a.ctx);
   const int64_t held = a.vt_rows ? min((int64_t)max(a.vt_rows[b], 0), prior) : 0;
   const int t_end = (int)((k_len + FN - 1) / FN);
-  __shared__ __attribute__((aligned(16))) uint16_t tile[FN][HEAD_DIM + 8];  // 16-B row pad
+  __shared__ __attribute__((aligned(16))) uint16_t tile[VT_TP * FN][HEAD_DIM + 8];  // 16-B row pad
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t cache_off = (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
   const bool fused = a.k_raw != nullptr;
-  constexpr int RW = FN / VT_WAVES;  // rows per wave: r = wave + VT_WAVES j
-  for (int t = (int)(held / FN) + blockIdx.x; t < t_end; t += gridDim.x) {
+  // the K norm weights once, before any store (a load issued after this
+  // workgroup's stores would wait for them: memory counts retire in order)
+  const uint2 kwv = fused ? *reinterpret_cast<const uint2*>(a.kw + 4 * lane) : make_uint2(0u, 0u);
+  constexpr int RW = VT_TP * FN / VT_WAVES;  // rows per wave: r = wave + VT_WAVES j
+  for (int t = (int)(held / FN) + VT_TP * blockIdx.x; t < t_end; t += VT_TP * gridDim.x) {
     // every load of the wave's rows first (one memory latency, not RW of them)
     uint2 vv[RW], kv[RW];
     float4 cv[RW], sv[RW];
@@ -177,23 +181,25 @@ __global__ __launch_bounds__(64 * VT_WAVES) void vt_transpose_kernel(VtArgs a) {
         *reinterpret_cast<uint2*>(a.v + cache_off + key * a.v_st + 4 * lane) = vv[j];
         float x[4] = {__uint_as_float(kv[j].x << 16), __uint_as_float(kv[j].x & 0xffff0000u),
                       __uint_as_float(kv[j].y << 16), __uint_as_float(kv[j].y & 0xffff0000u)};
-        norm_rope_row_cs(x, a.kw, cv[j], sv[j], a.eps, a.w_offset, lane);
+        norm_rope_row_wv(x, kwv, cv[j], sv[j], a.eps, a.w_offset, lane);
         store_row4(a.kc + cache_off + key * a.v_st, lane, x);
       }
     }
     __syncthreads();
     uint16_t* dst = a.vt + ((int64_t)b * a.Hk + hk) * a.vt_tiles * FT + (int64_t)t * FT;
 #pragma unroll
-    for (int o = tid; o < HEAD_DIM * 4; o += 64 * VT_WAVES) {
-      const int f = o >> 6, l = o & 63;
+    for (int o = tid; o < VT_TP * HEAD_DIM * 4; o += 64 * VT_WAVES) {
+      if (t + (o >> 10) >= t_end) break;  // a pass's tiles past the attended ones
+      const int f = (o >> 6) & 15, l = o & 63;
+      const int tb = FN * (o >> 10);  // the pass tile's first row
       const int d = 32 * (f >> 1) + (l & 31);
       const int k0 = 16 * (f & 1) + 4 * (l >> 5);
       uint32_t w[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int u0 = 2 * e, u1 = 2 * e + 1;  // element u: key k0 + (u & 3) + 8 (u >> 2)
-        const uint32_t lo = tile[k0 + (u0 & 3) + 8 * (u0 >> 2)][d];
-        const uint32_t hi = tile[k0 + (u1 & 3) + 8 * (u1 >> 2)][d];
+        const uint32_t lo = tile[tb + k0 + (u0 & 3) + 8 * (u0 >> 2)][d];
+        const uint32_t hi = tile[tb + k0 + (u1 & 3) + 8 * (u1 >> 2)][d];
         w[e] = lo | (hi << 16);
       }
       *reinterpret_cast<uint4*>(dst + o * 8) = make_uint4(w[0], w[1], w[2], w[3]);
@@ -338,16 +344,6 @@ struct QLoads {
   uint4 qraw[16], qwv[16];
   float4 cv[4], sv[4];
 };
-
-// The q norm weight (the same for every row): lane reads w[16kk + 8h2 .. +7].
-// Issued from asm: a compiler-visible load here would be waited for with
-// vmcnt(0), i.e. behind the K tile loads issued after it.
-__device__ __forceinline__ void q_load_w(const PrefillArgs& a, int h2, u32x4 (&w)[16]) {
-  const uint16_t* p = a.qw + 8 * h2;
-#pragma unroll
-  for (int kk = 0; kk < 16; ++kk)
-    asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(w[kk]) : "v"(p), "i"(32 * kk));
-}
 
 // q rows of one 32-row block: qnorm_rope (src/kernels/qknorm_rope_append.jl:25-57)
 // and the 1/16 scale. RoPE is linear, so the per-row 1/rms and the scale fold
@@ -759,29 +755,36 @@ __device__ __forceinline__ float solo_max(const SoloState& st, const SoloCtx& sc
   return xor32_max(m);
 }
 
-// Gate logits of the wave's 32 rows, loaded once into AGPRs after the prologue
-// and held to the epilogue: load i holds row 2i + h of the wave (h = lane / 32),
-// bf16 8 (lane % 32) .. +7 -- one 1-KB coalesced access per load. The epilogue
-// regroups them (and the output) through LDS.
-__device__ __forceinline__ void gate_loads(const uint16_t* base, int64_t row_st, int row0, int last_row,
+// Gate logits of this lane's row, loaded once into AGPRs after the prologue and
+// held to the epilogue: load i holds bf16 16 i + 8 h .. +7 of the row (h = lane /
+// 32; 32 contiguous bytes per row and load). Rows past the last valid one read
+// that row (the epilogue stores no row past it). swap_halves() turns a pair of
+// these chunks into the O^T accumulator's layout, and an output pair back.
+__device__ __forceinline__ void gate_loads(const uint16_t* base, int64_t row_st, int row, int last_row, int h,
                                            u32x4 (&g)[16]) {
-  // one pointer steps through the rows; it stops at the last valid row (the
-  // epilogue stores no row past it, so any in-bounds gate serves there)
-  const uint16_t* p = base + (int64_t)min(row0, last_row) * row_st;
-  const int64_t step = 2 * row_st;
+  const uint16_t* p = base + (int64_t)min(row, last_row) * row_st + 8 * h;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    asm volatile("global_load_dwordx4 %0, %1, off" : "=a"(g[i]) : "v"(p));
-    if (i < 15) {
-      p += row0 + 2 * i + 2 <= last_row ? step : 0;
-      asm volatile("" : "+v"(p));
-    }
-  }
+  for (int i = 0; i < 16; ++i)
+    asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=a"(g[i]) : "v"(p), "i"(32 * i));
 }
 __device__ __forceinline__ void gate_take(u32x4 (&g)[16]) {
 #pragma unroll
   for (int i = 0; i < 16; i += 4)
     asm volatile("s_waitcnt vmcnt(0)" : "+a"(g[i]), "+a"(g[i + 1]), "+a"(g[i + 2]), "+a"(g[i + 3]));
+}
+// Lane half h holds 8 bf16 of its row at 16 i + 8 h (words x..w). The O^T
+// accumulator gives the lane 4 columns at 16 i + 4 h (j' = 2 (i & 1)) and 4 at
+// 16 i + 8 + 4 h: words z, w of the low half trade places with words x, y of the
+// high half. After it the lane's x, y are its first 4 columns and z, w its second
+// 4 -- and the same swap applied to an output packed that way gives each lane 8
+// contiguous columns at 16 i + 8 h again.
+__device__ __forceinline__ void swap_halves(u32x4& v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+  v.x = a[0];
+  v.z = a[1];
+  v.y = b[0];
+  v.w = b[1];
 }
 
 // K blocks 0 and 1 (tiles 0 .. 3) into K objects 0 and 1
@@ -790,38 +793,6 @@ __device__ __forceinline__ void solo_prime(const SoloCtx& sc, const SoloLds& L) 
   for (int t = 0; t < 4; ++t) k_tile_load(sc.c, t, L.k + t * FT);
 }
 
-// The wave's 32 raw q rows and their RoPE table rows, staged in LDS by direct
-// global->LDS loads, each a coalesced 1-KB piece: q row r of the wave (16 KB per
-// wave, in the V objects, free until step -1) with its 16-byte chunk c at c ^
-// fswz(r), as the K tiles; cos and sin rows r (4 KB each per wave, in K object 2,
-// free until step -2) with chunk c at c ^ (r & 7). Read back in the Q^T operand
-// layout by q_read_lds, the banks of each b128 read are then distinct. 24 loads.
-__device__ __forceinline__ void q_stage(const PrefillArgs& a, const ItemGeo& ig, int wrow0, int wave,
-                                        int lane, const SoloLds& L) {
-  const int hl = lane >> 5, c = lane & 31;
-  const char* qb = reinterpret_cast<const char*>(a.q + (int64_t)ig.b * a.q_sb + (int64_t)ig.h * a.q_sh);
-  uint16_t* qd = L.v + wave * (32 * HEAD_DIM);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int r = 2 * i + hl;
-    const int64_t row = min(wrow0 + r, a.L - 1);
-    __builtin_amdgcn_global_load_lds((const void*)(qb + row * a.q_st * 2 + 16 * (c ^ fswz(r))),
-                                     (__attribute__((address_space(3))) void*)(qd + i * 512), 16, 0, 0);
-  }
-  float* td = reinterpret_cast<float*>(L.k + 2 * (2 * FT)) + wave * (2 * 32 * HALF_ROT);
-  const int pr = lane >> 3, ck = lane & 7;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 8 * i + pr;
-    const int64_t pos = min((int64_t)ig.prior + min(wrow0 + r, a.L - 1), (int64_t)a.Lk - 1);
-    const int64_t off = pos * HALF_ROT + 4 * (ck ^ (r & 7));
-    __builtin_amdgcn_global_load_lds((const void*)(a.cos_tab + off),
-                                     (__attribute__((address_space(3))) void*)(td + i * 256), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const void*)(a.sin_tab + off),
-                                     (__attribute__((address_space(3))) void*)(td + 32 * HALF_ROT + i * 256),
-                                     16, 0, 0);
-  }
-}
 // lane (l32, h2): q[row l32][16kk + 8h2 .. +7] and the table floats 8h2 + 16kk + 4u.
 // The reads are issued from asm (a compiler-visible LDS read after the staging
 // loads would get a wait for every load in flight, the K tiles included) and
@@ -859,45 +830,96 @@ __device__ __forceinline__ void q_read_lds(QLoads& ql, const SoloLds& L, int wav
   }
 }
 
-// One item. SHIFT = false: every logit is within +-64 (log2 units), so
-// P = exp2(S) needs no shift (the normalisation cancels any common scale);
-// SHIFT = true: an exact row-max pass first, P = exp2(S - row max).
-template <bool CAUSAL, bool SHIFT>
-__device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it, const SoloLds& L,
-                                          int q_len_raw, int prior) {
-  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int l32 = lane & 31, h2 = lane >> 5;
-  const ItemGeo ig = item_geo(a, it, CAUSAL, q_len_raw, prior);
+// The lane id recomputed from the hardware: values derived from it after a long
+// loop are formed there rather than held in registers across the loop
+__device__ __forceinline__ int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+// One item's fixed context: geometry, tile sources and LDS read addresses.
+struct SoloItem {
+  ItemGeo ig;
   SoloGeo g;
-  g.wrow0 = ig.r0 + 32 * wave;
-  g.row = g.wrow0 + l32;
-  g.off = ig.off;
-  g.k_len = ig.k_len;
-  if (ig.r0 >= ig.q_len) return;  // uniform over the workgroup
-  SoloState st;
   SoloCtx sc;
-  init_fctx(sc.c, a, ig, wave, lane);
-  sc.vt = reinterpret_cast<const char*>(sc.c.vtbase);
-  sc.vsrc = (uint32_t)(wave * 4096 + 16 * lane);
-  {
-    const int sk = fswz(l32);
+  bool live;  // the item has rows (uniform over the workgroup)
+};
+
+template <bool CAUSAL>
+__device__ __forceinline__ void item_setup(SoloItem& I, const PrefillArgs& a, const FItem& it, const SoloLds& L,
+                                           int q_len_raw, int prior, int wave, int lane) {
+  const int l32 = lane & 31, h2 = lane >> 5;
+  I.ig = item_geo(a, it, CAUSAL, q_len_raw, prior);
+  I.g.wrow0 = I.ig.r0 + 32 * wave;
+  I.g.row = I.g.wrow0 + l32;
+  I.g.off = I.ig.off;
+  I.g.k_len = I.ig.k_len;
+  I.live = I.ig.r0 < I.ig.q_len;
+  init_fctx(I.sc.c, a, I.ig, wave, lane);
+  I.sc.vt = reinterpret_cast<const char*>(I.sc.c.vtbase);
+  I.sc.vsrc = (uint32_t)(wave * 4096 + 16 * lane);
+  const int sk = fswz(l32);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) sc.kaddr[q] = lds_addr(L.k) + l32 * 512 + 16 * ((2 * q + h2) ^ sk);
+  for (int q = 0; q < 8; ++q) I.sc.kaddr[q] = lds_addr(L.k) + l32 * 512 + 16 * ((2 * q + h2) ^ sk);
+  I.sc.vaddr = lds_addr(L.v) + 16 * lane;
+}
+
+// The item's 56 prologue loads, in issue order: 0..15 its q rows into LDS (the V
+// objects; piece i = rows 2 i, 2 i + 1 of the wave, as q_stage), 16..23 their
+// RoPE table rows (K object 2; cos, sin of rows 8 i .. 8 i + 7 in turn), 24..39
+// the q norm weights into `qw` (as q_load_w), 40..55 K tiles 0..3 into K objects
+// 0 and 1 (as solo_prime). Every LDS object must be free: no earlier load of the
+// workgroup still writing LDS, every wave done reading it.
+template <int N>
+__device__ __forceinline__ void pro_load(const SoloItem& I, const PrefillArgs& a, const SoloLds& L, int wave,
+                                         int lane, u32x4 (&qw)[16]) {
+  if constexpr (N < 16) {
+    const int hl = lane >> 5, c = lane & 31, r = 2 * N + hl;
+    const char* qb = reinterpret_cast<const char*>(a.q + (int64_t)I.ig.b * a.q_sb + (int64_t)I.ig.h * a.q_sh);
+    const int64_t row = min(I.g.wrow0 + r, a.L - 1);
+    __builtin_amdgcn_global_load_lds((const void*)(qb + row * a.q_st * 2 + 16 * (c ^ fswz(r))),
+                                     (__attribute__((address_space(3))) void*)(L.v + wave * (32 * HEAD_DIM) + N * 512),
+                                     16, 0, 0);
+  } else if constexpr (N < 24) {
+    constexpr int i = (N - 16) >> 1;
+    constexpr bool SN = ((N - 16) & 1) != 0;
+    const int pr = lane >> 3, ck = lane & 7, r = 8 * i + pr;
+    const int64_t pos = min((int64_t)I.ig.prior + min(I.g.wrow0 + r, a.L - 1), (int64_t)a.Lk - 1);
+    const int64_t off = pos * HALF_ROT + 4 * (ck ^ (r & 7));
+    float* td = reinterpret_cast<float*>(L.k + 2 * (2 * FT)) + wave * (2 * 32 * HALF_ROT) + (SN ? 32 * HALF_ROT : 0);
+    __builtin_amdgcn_global_load_lds((const void*)((SN ? a.sin_tab : a.cos_tab) + off),
+                                     (__attribute__((address_space(3))) void*)(td + i * 256), 16, 0, 0);
+  } else if constexpr (N < 40) {
+    constexpr int kk = N - 24;
+    const uint16_t* p = a.qw + 8 * (lane >> 5);
+    asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(qw[kk]) : "v"(p), "i"(32 * kk));
+  } else {
+    constexpr int t = (N - 40) >> 2, P = (N - 40) & 3;
+    k_piece<P>(I.sc.c, k_tile(I.sc.c, t), L.k + t * FT);
   }
-  sc.vaddr = lds_addr(L.v) + 16 * lane;
-  // q and its table rows first (in-order completion: the q math waits for them
-  // only), then the norm weights, then K blocks 0 and 1, which land under the math
-  q_stage(a, ig, g.wrow0, wave, lane, L);
-  u32x4 qw[16];
-  q_load_w(a, h2, qw);
-  solo_prime(sc, L);
-  // the staging loads and the weights are in; the 16 K tile loads may not be
-  asm volatile("s_waitcnt vmcnt(16)"
-               : "+v"(qw[0]), "+v"(qw[1]), "+v"(qw[2]), "+v"(qw[3]), "+v"(qw[4]), "+v"(qw[5]),
-                 "+v"(qw[6]), "+v"(qw[7]), "+v"(qw[8]), "+v"(qw[9]), "+v"(qw[10]), "+v"(qw[11]),
-                 "+v"(qw[12]), "+v"(qw[13]), "+v"(qw[14]), "+v"(qw[15])
-               :
-               : "memory");
+}
+template <int N0, int N1>
+__device__ __forceinline__ void pro_loads(const SoloItem& I, const PrefillArgs& a, const SoloLds& L, int wave,
+                                          int lane, u32x4 (&qw)[16]) {
+  if constexpr (N0 < N1) {
+    pro_load<N0>(I, a, L, wave, lane, qw);
+    sfence();  // each load's address is formed next to it (few live registers)
+    pro_loads<N0 + 1, N1>(I, a, L, wave, lane, qw);
+  }
+}
+
+// The rest of the item once q, its table rows and `qw` have landed (the caller's
+// wait is tied to `qw`): q norm + RoPE into st.qop, the gate loads, the row-max
+// pass (SHIFT), the pipelined steps. Ends with every load of the workgroup landed
+// (vmcnt(0), gates included) and a barrier after which no wave reads the tile
+// objects: all of the LDS is free, and st.o, st.gv, st.lsum hold the result.
+template <bool CAUSAL, bool SHIFT>
+__device__ __forceinline__ void item_run(SoloItem& I, SoloState& st, const PrefillArgs& a, const SoloLds& L,
+                                         u32x4 (&qw)[16], int wave, int lane) {
+  const int l32 = lane & 31, h2 = lane >> 5;
+  SoloCtx& sc = I.sc;
+  const SoloGeo& g = I.g;
   QLoads ql;
 #pragma unroll
   for (int kk = 0; kk < 16; ++kk) ql.qwv[kk] = __builtin_bit_cast(uint4, qw[kk]);
@@ -908,8 +930,7 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
   for (int kk = 0; kk < 16; ++kk) pin_acc(st.qop[kk]);
   // gate logits now (after q is in: the compiler's waits for q know nothing of
   // these); the two pipeline-filling steps leave them in flight
-  gate_loads(a.gate + (int64_t)ig.b * a.g_sb + (int64_t)ig.h * a.g_sh + 8 * l32, a.g_st, g.wrow0 + h2,
-             a.L - 1, st.gv);
+  gate_loads(a.gate + (int64_t)I.ig.b * a.g_sb + (int64_t)I.ig.h * a.g_sh, a.g_st, g.row, a.L - 1, h2, st.gv);
   st.lsum = 0.f;
 
   const int nb = (sc.c.n_tiles + 1) >> 1;  // step blocks of two tiles
@@ -940,68 +961,128 @@ __device__ __forceinline__ void solo_item(const PrefillArgs& a, const FItem& it,
   }
   if (i < nb) solo_step<CAUSAL, SHIFT, 1, true, true, true, true>(st, sc, L, g, i, lane, kst, vst);
 
-  // ---- epilogue: normalise, gate (sigmoid, src/kernels/kernels.jl:34), store in
-  // the Wo input layout. The gates (coalesced) and the result (this lane's row)
-  // change layout through a padded 32-row region of LDS per wave.
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
                : "+a"(st.o[0]), "+a"(st.o[1]), "+a"(st.o[2]), "+a"(st.o[3]),
                  "+a"(st.o[4]), "+a"(st.o[5]), "+a"(st.o[6]), "+a"(st.o[7]));
   // vmcnt(0) before the barrier: this wave's gate loads and its last tile loads
-  // (which target the K objects the region below reuses) have landed, so after
-  // the barrier no tile load of any wave is still writing LDS
+  // have landed, so after the barrier no tile load of any wave is still writing
+  // LDS and no wave reads a tile object again
   gate_take(st.gv);
-  fbarrier();  // every wave is done with the tile objects
-  // lane index recomputed here so no prologue value has to live this long
-  int elane;
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(elane));
-  const int el = elane & 31, eh = elane >> 5;
-  constexpr int XROW = HEAD_DIM + 8;  // elements per row of the region (16-B pad)
-  uint16_t* xr = L.k + wave * (32 * XROW);
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    *reinterpret_cast<u32x4*>(xr + (2 * i + eh) * XROW + 8 * el) = st.gv[i];
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's own writes are in
-  asm volatile("" ::: "memory");
+  fbarrier();
+}
+
+// Epilogue (no LDS): o sigma(g) / l for this lane's row (sigmoid:
+// src/kernels/kernels.jl:34; the gate: src/llm/qwen35.jl:315), in 16 chunks:
+// chunk i forms and stores the 8 contiguous bf16 at columns 16 i + 8 h .. +7.
+// O^T d-block db = i / 2 holds the row at columns 32 db + 8 j' + 4 h + (0..3),
+// j' = 0..3. With NEXT, chunks 0..7 first issue 7 each of the next item's 56
+// prologue loads, so their address work overlaps this arithmetic.
+struct EpiCtx {
+  float lt;      // the row's l (or a finite stand-in for an empty row)
+  uint16_t* op;  // this lane's first output column
+  bool store;    // the row is inside the chunk
+};
+__device__ __forceinline__ EpiCtx epi_ctx(const SoloItem& I, const SoloState& st, const PrefillArgs& a, int lane) {
+  const int l32 = lane & 31, h2 = lane >> 5;
+  EpiCtx e;
   const float l_tot = st.lsum + __shfl_xor(st.lsum, 32, 64);
   // o sigma(g) / l = o / (l + l 2^(-g log2 e)); a fully-masked row (l = 0, o = 0)
   // takes a finite stand-in for l, so its output stays 0 for every gate
-  const float lt = l_tot > 0.f ? l_tot : 3.0e38f;
-  uint2 ov[8][4];
+  e.lt = l_tot > 0.f ? l_tot : 3.0e38f;
+  e.store = I.g.row < I.ig.q_len;
+  e.op = a.o + (int64_t)I.ig.b * a.o_sb + (int64_t)I.ig.h * a.o_sh + (int64_t)(I.g.wrow0 + l32) * a.o_st + 8 * h2;
+  return e;
+}
+template <int C>
+__device__ __forceinline__ void epi_chunk(const SoloState& st, const EpiCtx& e) {
+  u32x4 gq = st.gv[C];
+  swap_halves(gq);  // x, y: columns of j' = 2 (C & 1); z, w: j' = 2 (C & 1) + 1
+  const f32x16& acc = st.o[C >> 1];
+  const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w};
+  uint32_t ow[4];
 #pragma unroll
-  for (int db = 0; db < 8; ++db) {
-    const f32x16& acc = st.o[db];
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
-      const int d0 = 32 * db + 8 * jb + 4 * eh;
-      const uint2 g2 = *reinterpret_cast<const uint2*>(xr + el * XROW + d0);
-      const float o0 = acc[4 * jb + 0] * fast_rcp(fmaf(lt, fast_exp2(__uint_as_float(g2.x << 16) * -LOG2E), lt));
-      const float o1 = acc[4 * jb + 1] * fast_rcp(fmaf(lt, fast_exp2(__uint_as_float(g2.x & 0xffff0000u) * -LOG2E), lt));
-      const float o2 = acc[4 * jb + 2] * fast_rcp(fmaf(lt, fast_exp2(__uint_as_float(g2.y << 16) * -LOG2E), lt));
-      const float o3 = acc[4 * jb + 3] * fast_rcp(fmaf(lt, fast_exp2(__uint_as_float(g2.y & 0xffff0000u) * -LOG2E), lt));
-      ov[db][jb].x = pack2(o0, o1);
-      ov[db][jb].y = pack2(o2, o3);
-    }
+  for (int u = 0; u < 4; ++u) {
+    const int j = 4 * (2 * (C & 1) + (u >> 1)) + 2 * (u & 1);  // acc index of the word's first column
+    const float o0 = acc[j] * fast_rcp(fmaf(e.lt, fast_exp2(__uint_as_float(gw[u] << 16) * -LOG2E), e.lt));
+    const float o1 = acc[j + 1] * fast_rcp(fmaf(e.lt, fast_exp2(__uint_as_float(gw[u] & 0xffff0000u) * -LOG2E), e.lt));
+    ow[u] = pack2(o0, o1);
   }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // every gate read is done before the region is rewritten
-  asm volatile("" ::: "memory");
-#pragma unroll
-  for (int db = 0; db < 8; ++db)
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
-      *reinterpret_cast<uint2*>(xr + el * XROW + 32 * db + 8 * jb + 4 * eh) = ov[db][jb];
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  asm volatile("" ::: "memory");
-  // every row chunk out of LDS first (one wait), then the stores along one pointer
-  u32x4 orow[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) orow[i] = *reinterpret_cast<const u32x4*>(xr + (2 * i + eh) * XROW + 8 * el);
-  uint16_t* op = a.o + (int64_t)ig.b * a.o_sb + (int64_t)ig.h * a.o_sh + 8 * el +
-                 (int64_t)(g.wrow0 + eh) * a.o_st;
-  const int64_t ostep = 2 * a.o_st;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if (g.wrow0 + 2 * i + eh < ig.q_len) *reinterpret_cast<u32x4*>(op) = orow[i];
-    op += ostep;
+  u32x4 out = u32x4{ow[0], ow[1], ow[2], ow[3]};
+  swap_halves(out);  // 8 contiguous columns at 16 C + 8 h
+  if (e.store) *reinterpret_cast<u32x4*>(e.op + 16 * C) = out;
+}
+template <int C, bool NEXT>
+__device__ __forceinline__ void epi_chunks(const SoloState& st, const EpiCtx& e, const SoloItem& Bn,
+                                           const PrefillArgs& a, const SoloLds& L, int wave, int lane,
+                                           u32x4 (&qw)[16]) {
+  if constexpr (C < 16) {
+    if constexpr (NEXT && C < 8) pro_loads<7 * C, 7 * C + 7>(Bn, a, L, wave, lane, qw);
+    sfence();
+    epi_chunk<C>(st, e);
+    sfence();
+    epi_chunks<C + 1, NEXT>(st, e, Bn, a, L, wave, lane, qw);
+  }
+}
+
+// q, its table rows and the weights (prologue loads 0..39) have landed: at most
+// the 16 K tile loads, or younger operations, are in flight (vector-memory
+// counts retire in issue order; more younger operations only make it stricter)
+__device__ __forceinline__ void wait_q(u32x4 (&qw)[16]) {
+  asm volatile("s_waitcnt vmcnt(16)"
+               : "+v"(qw[0]), "+v"(qw[1]), "+v"(qw[2]), "+v"(qw[3]), "+v"(qw[4]), "+v"(qw[5]),
+                 "+v"(qw[6]), "+v"(qw[7]), "+v"(qw[8]), "+v"(qw[9]), "+v"(qw[10]), "+v"(qw[11]),
+                 "+v"(qw[12]), "+v"(qw[13]), "+v"(qw[14]), "+v"(qw[15])
+               :
+               : "memory");
+}
+
+// The workgroup's items (one, or a causal pair). SHIFT = false: every logit is
+// within +-64 (log2 units), so P = exp2(S) needs no shift (the normalisation
+// cancels any common scale); SHIFT = true: an exact row-max pass first per item,
+// P = exp2(S - row max). A pair's second item issues its prologue loads as soon
+// as the first item's loop has released the LDS, before the first item's
+// epilogue, which then runs while they are in flight.
+template <bool CAUSAL, bool SHIFT>
+__device__ __forceinline__ void solo_items(const PrefillArgs& a, const FItem& it0, const FItem& it1, int n_it,
+                                           const SoloLds& L, int q_len_raw, int prior) {
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  SoloState st;
+  u32x4 qw[16];
+  SoloItem A, B;
+  item_setup<CAUSAL>(A, a, it0, L, q_len_raw, prior, wave, lane);
+  if (A.live) {
+    pro_loads<0, 56>(A, a, L, wave, lane, qw);
+    wait_q(qw);
+    item_run<CAUSAL, SHIFT>(A, st, a, L, qw, wave, lane);
+  }
+  B.live = false;
+  // after A's loop every lane-derived value is formed afresh, not held across it
+  const int lane2 = fresh_lane();
+  if (n_it == 2) {
+    // B's geometry is formed here, not hoisted above A's loop (its registers
+    // would be held across the loop): its inputs become opaque at this point
+    FItem ib = it1;
+    asm volatile("" : "+s"(ib.b), "+s"(ib.h), "+s"(ib.hk), "+s"(ib.qt));
+    item_setup<CAUSAL>(B, a, ib, L, q_len_raw, prior, wave, lane2);
+  }
+  // every path waits for B's q before the paths join: a register whose load is
+  // still in flight must not reach a join (the allocator may copy it there)
+  if (A.live) {
+    const EpiCtx e = epi_ctx(A, st, a, lane2);
+    if (B.live) {
+      epi_chunks<0, true>(st, e, B, a, L, wave, lane2, qw);
+      wait_q(qw);
+    } else {
+      epi_chunks<0, false>(st, e, B, a, L, wave, lane2, qw);
+    }
+  } else if (B.live) {
+    pro_loads<0, 56>(B, a, L, wave, lane2, qw);
+    wait_q(qw);
+  }
+  if (B.live) {
+    item_run<CAUSAL, SHIFT>(B, st, a, L, qw, wave, lane2);
+    const EpiCtx e = epi_ctx(B, st, a, lane2);
+    epi_chunks<0, false>(st, e, B, a, L, wave, lane2, qw);
   }
 }
 
@@ -1053,22 +1134,13 @@ void prefill_fused_kernel(PrefillArgs a) {
   SoloLds L;
   L.k = KO;
   L.v = VO;
-  if (bound <= FSTATIC_LIMIT) {
-    solo_item<CAUSAL, false>(a, it0, L, q_len_raw, prior);
-    if (CAUSAL && n_it == 2) {
-      fbarrier();  // every wave is done with the first item's LDS
-      solo_item<CAUSAL, false>(a, it1, L, q_len_raw, prior);
-    }
-  } else {
-    solo_item<CAUSAL, true>(a, it0, L, q_len_raw, prior);
-    if (CAUSAL && n_it == 2) {
-      fbarrier();
-      solo_item<CAUSAL, true>(a, it1, L, q_len_raw, prior);
-    }
-  }
-  // No global->LDS load is in flight here: the epilogue waited for all of them
-  // (vmcnt(0)) before its barrier, and an item that returns early issued none.
-  // Only the output stores may be outstanding, which need no wait.
+  if (bound <= FSTATIC_LIMIT)
+    solo_items<CAUSAL, false>(a, it0, it1, n_it, L, q_len_raw, prior);
+  else
+    solo_items<CAUSAL, true>(a, it0, it1, n_it, L, q_len_raw, prior);
+  // No global->LDS load is in flight here: each item ends with vmcnt(0) before
+  // its last barrier, and an item with no rows issued none. Only the output
+  // stores may be outstanding, which need no wait.
 }
 
 hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st) {
@@ -1079,7 +1151,9 @@ hipError_t launch_vt_transpose(const VtArgs& a, hipStream_t st) {
   // workgroup: at config 2 (512 tiles over 256 CUs) 14.4 against 15.7 us for
   // one tile per workgroup, 18.6 us for four
   const int chunk_tiles = (a.L + FN - 1) / FN + 1;
-  const int gx = a.vt_rows && chunk_tiles < a.vt_tiles ? chunk_tiles : (a.vt_tiles + 1) / 2;
+  constexpr int PASSES = 2;  // passes per workgroup without vt_rows
+  const int gx = a.vt_rows && chunk_tiles < a.vt_tiles ? (chunk_tiles + VT_TP - 1) / VT_TP
+                                                         : (a.vt_tiles + PASSES * VT_TP - 1) / (PASSES * VT_TP);
   hipLaunchKernelGGL(vt_transpose_kernel, dim3(gx, a.Hk, a.B), dim3(64 * VT_WAVES), 0, st, a);
   return hipGetLastError();
 }
