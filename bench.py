@@ -585,7 +585,7 @@ def bench_step(vm, torch, replays=40, seed=9):
         for _ in range(3):   # warm-up: plans, workspace
             vm.step_(m, gen)
             gen.advance_()
-        sess = vm.CaptureSession().capture(lambda: (vm.step_(m, gen), gen.advance_()))
+        sess = vm.CaptureSession().capture(lambda: (vm.step_(m, gen), gen.advance_()), models=(m.attn,))
         for _ in range(3):
             sess.launch()
         p_start = gen.positions.clone()

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from conftest import banner, dev_f32, from_dev, to_dev
-from oracle.rng import bf16_to_f32, normal_bf16, normal_f32
+from oracle.rng import bf16_to_f32, f32_to_bf16, normal_bf16, normal_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -304,6 +304,37 @@ def test_deltanet_sequence_chunked(vm, orc, B, T):
     for got, ref, name in ((o.cpu().numpy(), o_ref, "O"), (S.cpu().numpy(), s_ref, "S")):
         err = np.abs(got - ref).max() / np.abs(ref).max()
         print(f"chunked {name}: max err / max |ref| = {err:.2e}")
+        assert err <= 5e-4, name
+
+
+def test_deltanet_sequence_chunked_overflowing_softplus(vm, orc):
+    """A gate input past softplus' fp32 overflow (alpha + dt_bias > 88.7: the
+    prep's log1p(exp(x)) is +inf, the log decay -inf, the decay exactly 0, as in
+    the reference's prefill, qwen35.jl:30, :354) in the middle of a chunk: the
+    chunked form still matches the sequential oracle, with no NaN in O or the
+    carried state (tokens before it stop contributing; those after it do)."""
+    banner("deltanet chunked with an overflowing softplus")
+    B, T = 1, 100
+    cv, ab, a_log, dt_bias = _prepped(B, T, 1970)
+    # alpha of value head 3 at token 37 (chunk 0) and of head 9 at token 70 (chunk 1)
+    big = f32_to_bf16(np.array([200.0], np.float32))[0]
+    ab = ab.copy()
+    ab[0, 37, 3] = big
+    ab[0, 70, 9] = big
+    p = orc.deltanet_prep(cv, ab, a_log, dt_bias, Dk=DK, Dv=DV, Hk=HK, Hv=HV)
+    assert np.isneginf(p["gate"][0, 37, 3]) and np.isneginf(p["gate"][0, 70, 9])
+    s = normal_f32(B * HV * DV * DK, 1971, scale=0.05).reshape(B, HV, DV, DK)
+    o_ref, s_ref = orc.deltanet_sequence(p["q"], p["k"], p["v"], p["beta"], p["gate"], s)
+    assert np.isfinite(o_ref).all() and np.isfinite(s_ref).all()
+    S = f32dev(s)
+    o = torch.empty((B, HV, T, DV), dtype=torch.float32, device="cuda")
+    vm.deltanet_sequence_chunked_({"O": o, "Sp": S}, f32dev(p["q"]), f32dev(p["k"]),
+                                  f32dev(p["v"]), f32dev(p["beta"]), f32dev(p["gate"]), S)
+    torch.cuda.synchronize()
+    for got, ref, name in ((o.cpu().numpy(), o_ref, "O"), (S.cpu().numpy(), s_ref, "S")):
+        assert np.isfinite(got).all(), name
+        err = np.abs(got - ref).max() / np.abs(ref).max()
+        print(f"chunked {name} with -inf log decays: max err / max |ref| = {err:.2e}")
         assert err <= 5e-4, name
 
 

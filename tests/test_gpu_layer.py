@@ -240,7 +240,7 @@ def test_decode_layer_graph_replay(vm, orc):
     layer.V_cache.copy_(V0)
     gen.positions.copy_(i32(p0))
     torch.cuda.synchronize()
-    sess = vm.CaptureSession().capture(lambda: vm.decode_(h, layer, m, gen, xn, advance=True))
+    sess = vm.CaptureSession().capture(lambda: vm.decode_(h, layer, m, gen, xn, advance=True), models=(m,))
     replay = []
     for _ in range(n):
         sess.launch()

@@ -306,7 +306,11 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
   }
   if (t < 64) {  // wave 0: gates, inclusive cumulative sum of the log decay
     const int64_t g = ((int64_t)b * q.T + t0 + min(t, n - 1)) * q.Hv + hv;  // in bounds
-    const float gt = t < n ? q.gate[g] : 0.f;
+    // log decays below -110 are taken as -110: expf underflows to exactly 0 below
+    // about -104, so every decay the recurrence applies is unchanged, while the
+    // cumulative sums stay finite (a -inf log decay, e.g. from softplus
+    // overflowing in log1p(exp(x)) at x > 88.7, would make their differences NaN)
+    const float gt = t < n ? fmaxf(q.gate[g], -110.0f) : 0.f;
     float G = gt;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {

@@ -79,9 +79,10 @@ def attn_layer(cfg: AttnConfig, qw: torch.Tensor, kw: torch.Tensor, Wqkv=None,
 class AttnModel:
     """The model-level state the attention verbs read: cfg, RoPE tables and the
     decode space (the reference's Arena, qwen35.jl:110), allocated once so a
-    captured step replays the same addresses: the split-KV scratch, the
+    captured step replays the same addresses: the split-KV scratch, the decode
     projections' workspace, and the decode step's qkv and attention-output
-    buffers (the layer frame's temporaries, qwen35.jl:193)."""
+    buffers (the layer frame's temporaries, qwen35.jl:193). Prefill and forward
+    use a workspace of their own that grows freely: a graph never records it."""
 
 
     def __init__(self, cfg: AttnConfig, *, n_splits: int = 0):
@@ -93,15 +94,31 @@ class AttnModel:
         self.space = torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda")
         self.prefill_space = None
         self.lin_space = None
+        self.dec_space = None
+        self.dec_frozen = False   # set once a graph may have recorded dec_space
         self.qkv = None
         self.attn_out = None
 
     def linear_workspace(self, need: int = 0) -> torch.Tensor:
-        """The projections' workspace, grown to `need` bytes (eager calls size it;
-        a captured step then replays with the buffer its warm-up calls sized)."""
+        """The eager (prefill, forward) projections' workspace, grown to `need`
+        bytes. Never passed to a captured step: growing it replaces the tensor."""
         if self.lin_space is None or self.lin_space.numel() < need:
             self.lin_space = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
         return self.lin_space
+
+    def decode_workspace(self, need: int = 0) -> torch.Tensor:
+        """The decode step's projections' workspace: sized by the first (eager)
+        calls, then fixed, because a captured step replays its address. Once
+        ``dec_frozen`` is set (a graph may hold the buffer) a larger need raises
+        instead of replacing it; so does one inside a stream capture."""
+        if self.dec_space is None or self.dec_space.numel() < need:
+            if self.dec_frozen or torch.cuda.is_current_stream_capturing():
+                have = 0 if self.dec_space is None else self.dec_space.numel()
+                raise ArgumentError(
+                    f"the decode workspace holds {have} bytes and a captured step may use it; "
+                    f"this call needs {need}: size it eagerly before capturing")
+            self.dec_space = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
+        return self.dec_space
 
     def decode_buffers(self):
         """(qkv (B, 2Hq+2Hkv, Dh), O (B, Hq, Dh)) bf16, allocated on first use."""
@@ -320,7 +337,7 @@ def decode_(h, l: AttnLayer, m: AttnModel, gen: Generation, xn, *, advance: bool
         raise DimensionMismatch(f"size(xn, 2) = {d['B']} does not match B = {cfg.B}")
     qkv, O = m.decode_buffers()
     q2, O2 = qkv.view(cfg.B, -1), O.view(cfg.B, -1)
-    ws = m.linear_workspace(max(ops.linear_workspace_bytes(xn, l.Wqkv, q2),
+    ws = m.decode_workspace(max(ops.linear_workspace_bytes(xn, l.Wqkv, q2),
                                 ops.linear_workspace_bytes(O2, l.Wo, h)))
     ops.linear_({"y": q2}, xn, l.Wqkv, workspace=ws)
     gated_attn_decode_(O, l, m, gen, qkv, advance=advance)
@@ -364,7 +381,12 @@ class CaptureSession:
         self.stream = None
         self.n_warm = 0     # eager warm-up steps spent (generate.jl:149-152)
 
-    def capture(self, fn):
+    def capture(self, fn, models=()):
+        """``models``: the AttnModels whose decode workspace ``fn`` uses; they
+        are frozen (a later larger need raises instead of freeing the buffer
+        the graph holds)."""
+        for am in models:
+            am.dec_frozen = True
         if self.exec is not None:
             raise ArgumentError("session already holds a graph")
         self.stream = torch.cuda.Stream()

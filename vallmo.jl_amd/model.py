@@ -112,11 +112,15 @@ class Model:
                            ops.linear_add_rms_norm_workspace_bytes(O2, l.Wout))
             attn = [l for l in self.layers if not isinstance(l, DeltaNetLayer)]
             if attn:
-                _, O = self.attn.decode_buffers()
-                need = max(need, ops.linear_add_rms_norm_workspace_bytes(
-                    O.view(self.cfg.B, -1), attn[0].Wo))
+                qkv, O = self.attn.decode_buffers()
+                O2 = O.view(self.cfg.B, -1)
+                need = max(need, ops.linear_add_rms_norm_workspace_bytes(O2, attn[0].Wo),
+                           ops.linear_workspace_bytes(self.xn, attn[0].Wqkv, qkv.view(self.cfg.B, -1)),
+                           ops.linear_workspace_bytes(O2, attn[0].Wo, self.h))
             self._ws_need = need
-        return self.attn.linear_workspace(self._ws_need)
+        # the decode workspace (never the eager prefill one): a captured step
+        # replays this address, and it is sized here for every step problem
+        return self.attn.decode_workspace(self._ws_need)
 
     def reset_(self):
         """reset!(m) — qwen35.jl:167-185: zero every DeltaNet state and conv ring
@@ -255,8 +259,8 @@ def prefill_(m: Model, gen: Generation, ids, *, offset: int = 0):
     """prefill!(m, gen, ids; offset) — qwen35.jl:369-395, eager: ids (T, B)
     (torch (B, T) int32, 1-based) continue a resident prefix of `offset` tokens;
     fills every layer's cache columns offset+1 .. offset+T, puts the first
-    generated token in gen.result and, last, seeds the clock: positions =
-    offset + T + 1."""
+    generated token in gen.result (the last token's final-normed hidden row
+    is left in m.xn) and, last, seeds the clock: positions = offset + T + 1."""
     cfg = m.cfg
     if ids.dim() != 2 or ids.dtype != torch.int32:
         raise ArgumentError("ids must be a (B, T) int32 tensor of 1-based token ids")
@@ -286,7 +290,10 @@ def prefill_(m: Model, gen: Generation, ids, *, offset: int = 0):
         h = ops.linear(mid, l.Wd, workspace=ws)["y"]
         next_w = m.norm_w if i == n - 1 else m.layers[i + 1].norm1
         ops.fused_add_rms_norm_({"Y": xn, "Xp": x}, x, h, next_w, eps=eps, offset=1.0)
-    ops.lm_head_argmax_({"Result": gen.result}, xn[:, T - 1, :], m.head, scratch=m.lm_scratch)
+    # the last token's final-normed row goes to the step's xn buffer (the head's
+    # input, qwen35.jl:392), where callers can read it
+    m.xn.copy_(xn[:, T - 1, :])
+    ops.lm_head_argmax_({"Result": gen.result}, m.xn, m.head, scratch=m.lm_scratch)
     gen.positions.fill_(offset + T + 1)   # the final act: seed the clock
     return gen
 
@@ -355,7 +362,8 @@ def generate_captured_(m: Model, gen: Generation, ids, *, max_new_tokens: int, w
             s.n_warm += 1
         else:
             if s.exec is None:
-                s.capture(lambda: (step_(m, gen), gen.advance_()))
+                m.workspace()  # sized before capture, then fixed
+                s.capture(lambda: (step_(m, gen), gen.advance_()), models=(m.attn,))
             s.launch()
 
     return _run(m, gen, ids, max_new_tokens=max_new_tokens, eos=eos, poll_every=poll_every,
