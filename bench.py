@@ -535,7 +535,7 @@ def bench_layer(vm, torch, reps=20):
     torch.cuda.synchronize()
     t_step = _event_ms(torch, step, reps)
     qkv_d, O_d = m.decode_buffers()
-    ws = m.linear_workspace()
+    ws = m.decode_workspace()
     # the GEMVs alone, timed from graph replays (a host loop of these ~10 us
     # launches measures Python's dispatch, not the kernels) that rotate over
     # copies of the weight totalling > 1 GB, so each call streams it from HBM as

@@ -13,9 +13,10 @@
  *   - Tensor layouts are named in the reference's column-major order, e.g.
  *     K_cache (D, Ctx, Hk, B), which is row-major [B][Hk][Ctx][D] here.
  *   - Compute entry points are asynchronous on `stream` (NULL = default
- *     stream), allocate nothing, never synchronise, and are legal under
- *     hipStreamBeginCapture (hipGraph replay), as the reference requires of
- *     its decode step (src/llm/generate.jl:17-27).
+ *     stream), allocate no device memory, never synchronise, and are legal
+ *     under hipStreamBeginCapture (hipGraph replay), as the reference requires
+ *     of its decode step (src/llm/generate.jl:17-27). The one exception is
+ *     vm_linear_tune, a load-time call, marked where it is declared.
  *   - Compiled for head_dim D = 256 and HALF_ROT = 32 (rotary dim 64), the
  *     Qwen3.5 attention facts (src/llm/qwen35.jl:15-23). Other D/HALF_ROT are
  *     rejected with VM_E_UNSUPPORTED. GQA group H/Hk <= 8 for decode.
@@ -295,12 +296,29 @@ int vm_gated_attn_prefill_staged(vm_bf16* out, int64_t out_st, int64_t out_sb,
  * 16-byte aligned W and x columns)
  * run on the library's split-K MFMA GEMV, whose K slices add in a fixed order
  * (bitwise reproducible); the rest on hipBLASLt. A plan per
- * problem (hipBLASLt) is built on the first call and cached (linear.jl:17-38);
+ * problem (hipBLASLt) is built on the first call and cached (linear.jl:17-38)
+ * with the heuristic's first algorithm, as the reference takes it: building it
+ * is host work only, so the first call of a shape may run inside a capture;
  * vm_linear_workspace_bytes builds it and returns the workspace it needs (at
  * most 64 MiB), which the caller passes to vm_linear (the reference takes it
  * from the ambient arena, linear.jl:62-66). Returns (size_t)-1 on failure.
  * A problem with no algorithm is VM_E_UNSUPPORTED (no fallback path).        */
 size_t vm_linear_workspace_bytes(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy);
+/* vm_linear_tune: no counterpart in the reference (its plan keeps the
+ * heuristic's first). For callers that load a model and then run it: times up
+ * to 48 of the heuristic's candidates for the problem's plan and keeps the
+ * fastest (on MI355X the first can be a third slower). The exception to the
+ * conventions above: it allocates scratch buffers (up to ~800 MB for the
+ * timing of a narrow problem's weights), runs the timing on a private stream
+ * and waits for it, so it must not be called while the device is captured.
+ * Call it at load, before vm_linear_workspace_bytes (a tuned plan may need a
+ * larger workspace); once per problem (later calls return at once).
+ * VM_LINEAR_TUNE=0 in the environment keeps the first. Narrow problems that
+ * run the GEMV have nothing to tune.
+ * vm_linear_plan_state: -2 no plan, -1 the heuristic's first, k >= 0 tuned
+ * (candidate k kept, 0 = the heuristic's first).                              */
+int vm_linear_tune(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy);
+int vm_linear_plan_state(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy);
 int vm_linear(vm_bf16* y, int64_t ldy, const vm_bf16* x, int64_t ldx, const vm_bf16* w,
               int64_t ldw, int M, int N, int K, void* workspace, size_t workspace_bytes,
               vm_stream stream);

@@ -141,6 +141,62 @@ def test_linear_narrow_misaligned_view(vm, orc):
     assert mx <= TOL_MAX and mn <= TOL_MEAN
 
 
+def test_linear_first_call_captured_then_tuned(vm, orc):
+    """vm_linear keeps the header's contract on the first call of a new problem:
+    it builds the plan with the heuristic's first algorithm (host work only), so
+    that call can sit inside a capture (which any device allocation on the
+    capturing thread would fail). vm_linear_tune is the separate load-time call
+    that times the candidates; once tuned, the pick stays the same for later
+    calls, eager or captured. Problems of this test's shapes occur nowhere else,
+    so their plans are new here."""
+    banner("linear: first call under capture, then tuned")
+    lib = vm._lib
+    for M, N, K in ((1000, 48, 768), (1016, 40, 832)):
+        x = normal_bf16((N, K), 740 + N, scale=1.0)
+        W = normal_bf16((M, K), 741 + N, scale=K ** -0.5)
+        xd, Wd = to_dev(x), to_dev(W)
+        y = torch.empty((N, M), dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")  # the plan's cap
+        prob = (M, N, K, K, K, M)
+        ref = orc.linear(x, W).astype(np.float64)
+
+        def run():
+            lib.call("vm_linear", vm.ops._p(y), M, vm.ops._p(xd), K, vm.ops._p(Wd), K, M, N, K,
+                     vm.ops._p(ws), ws.numel(), vm.ops._stream())
+
+        def check(what):
+            torch.cuda.synchronize()
+            mx, mn = maxmean(dev_f32(y), ref)
+            print(f"linear {M}x{N}x{K} {what}: max {mx:.3e} mean {mn:.3e}, plan state "
+                  f"{lib.load().vm_linear_plan_state(*prob)}")
+            assert mx <= TOL_MAX and mn <= TOL_MEAN
+
+        assert lib.load().vm_linear_plan_state(*prob) == -2  # no plan yet
+        if M == 1000:
+            # the very first call is captured: the plan is built untuned
+            sess = vm.CaptureSession().capture(run)
+            assert lib.load().vm_linear_plan_state(*prob) == -1
+            y.zero_()
+            sess.launch()
+            check("first call captured, replayed")
+            sess.close()
+            lib.call("vm_linear_tune", *prob)
+        else:
+            lib.call("vm_linear_tune", *prob)  # tuned before any call
+        pick = lib.load().vm_linear_plan_state(*prob)
+        assert pick >= 0
+        y.zero_()
+        run()
+        check("eager after tuning")
+        sess = vm.CaptureSession().capture(run)
+        y.zero_()
+        sess.launch()
+        check("captured after tuning")
+        sess.close()
+        lib.call("vm_linear_tune", *prob)  # a second tune keeps the plan
+        assert lib.load().vm_linear_plan_state(*prob) == pick
+
+
 def _layer(vm, cfg, seed):
     qw = normal_bf16((D,), seed + 1, scale=0.05)
     kw = normal_bf16((D,), seed + 2, scale=0.05)

@@ -15,7 +15,7 @@ from .sizes import sizes  # noqa: F401
 from .ops import (attention, attention_, decode_attention, decode_attention_,  # noqa: F401
                   decode_scratch_bytes, embed_, fill_normal_, fused_add_rms_norm,
                   fused_add_rms_norm_, knorm_rope_append_, linear, linear_,
-                  linear_workspace_bytes, lm_head_argmax, lm_head_argmax_,
+                  linear_tune, linear_workspace_bytes, lm_head_argmax, lm_head_argmax_,
                   lm_head_argmax_scratch_bytes, qnorm_rope_, rms_norm, rms_norm_, rope_tables,
                   sigmoid, sigmoid_gate_, silu_mul_, causal_conv1d, causal_conv1d_,
                   causal_conv1d_sequence, causal_conv1d_sequence_, fused_deltanet_decode,

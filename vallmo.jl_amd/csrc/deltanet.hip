@@ -269,9 +269,6 @@ constexpr int UO_U = 28672;  // U:        [cb 8][w 4][lane][4], D[r][dv] tiles
 constexpr int UO_G = 36864;  // gamma_C
 constexpr int UNIT = 36992;  // floats per unit (147 968 B, a multiple of 256)
 
-__device__ __forceinline__ int pos_rowk(int r, int k, int nsteps4) {  // A[i = r][k], 16-row tiles
-  return (((r >> 4) * nsteps4 + (k >> 4)) * 64 + (r & 15) + 16 * (k & 3)) * 4 + ((k >> 2) & 3);
-}
 __device__ __forceinline__ int pos_acc(int r, int dv) {  // D[r][dv], 16 x 16 tiles
   return ((((dv >> 4) * 4 + (r >> 4)) * 64) + 16 * ((r & 15) >> 2) + (dv & 15)) * 4 + (r & 3);
 }

@@ -152,6 +152,11 @@ hipError_t decode_static_scratch(void** ptr);
 // product on `st`. Return VM_OK, a VM_E_* code or a hipError_t, with the message
 // in err.
 constexpr size_t LINEAR_MAX_WORKSPACE_BYTES = (size_t)64 << 20;
+// the one linear call that allocates (scratch) and synchronises: times the
+// heuristic's candidates for a problem's plan and keeps the fastest
+int linear_tune(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, char* err, size_t errn);
+// -2: no plan; -1: the heuristic's first, untuned; k >= 0: tuned, candidate k kept
+int linear_plan_state(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy);
 int linear_workspace(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, size_t* bytes,
                      char* err, size_t errn);
 // y = W^T a, then x = bf16(x + bf16(y)) in place and yn = rms_norm(x): linear!

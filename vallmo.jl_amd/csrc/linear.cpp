@@ -5,9 +5,12 @@
 // Like the reference's cuBLASLt path, one plan per problem is built on first
 // use and cached for the process (linear.jl:17-38): hipBLASLt matmul
 // descriptor, matrix layouts and an algorithm, bf16 A/B/D with fp32 compute and
-// fp32 scaling (linear.jl:29). The reference takes the heuristic's first
-// algorithm; here a new plan times the heuristic's top candidates once and
-// keeps the fastest (tune_algo below). Column-major view, as in
+// fp32 scaling (linear.jl:29). A plan built on first use takes the heuristic's
+// first algorithm, as the reference does, and costs no device allocation and no
+// synchronisation, so the first call of a shape may be captured. linear_tune
+// (vm_linear_tune) is the one call that times the heuristic's top candidates
+// and keeps the fastest (tune_algo below): it allocates scratch buffers and
+// waits for the timing runs, and belongs at model load. Column-major view, as in
 // the reference: x :: (K, N) with column stride ldx, W :: (K, M) (K-major) with
 // column stride ldw, y :: (M, N) with column stride ldy, so
 //     D (M x N) = op(A) B,  A = W (K x M, op = transpose), B = x (K x N).
@@ -39,6 +42,7 @@ struct Plan {
   hipblasLtMatmulAlgo_t algo{};
   size_t workspace = 0;
   bool ok = false;
+  int pick = -1;  // the heuristic candidate kept once tuned (0 = its first); -1: not tuned
 };
 
 using Key = std::tuple<int, int, int, int, int64_t, int64_t, int64_t>;  // dev, M, N, K, ldw, ldx, ldy
@@ -62,7 +66,7 @@ const char* status_name(hipblasStatus_t s) {
 
 // The heuristic ranks candidates by a model, and on MI355X its first pick can
 // be a third slower than the best of its own top candidates (M x N x K =
-// 18432 x 4096 x 2560: 381 against 286 us). So a new plan times up to NTUNE
+// 18432 x 4096 x 2560: 381 against 286 us). So linear_tune times up to NTUNE
 // candidates on scratch buffers of the problem's shape (N(0,1) bf16 data, on
 // a private stream) and keeps the fastest. The heuristic's first is kept
 // unless another beats it by 3% or more, so close calls do not flip from
@@ -146,29 +150,36 @@ int tune_algo(hipblasLtHandle_t h, const Plan& p, const hipblasLtMatmulHeuristic
   return best;
 }
 
-// Builds (once) the plan of one problem on the current device. Returns 0, or a
-// VM_E_* / hipError_t code with `err` set.
-// tune: time the candidates (tune_algo) when the plan is new; false keeps the
-// heuristic's first (a plan first needed inside a stream capture).
-int get_plan(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, const Plan** out,
-             char* err, size_t errn, bool tune = true) {
-  int dev = 0;
-  hipError_t he = hipGetDevice(&dev);
-  if (he != hipSuccess) {
-    snprintf(err, errn, "linear: hipGetDevice: %s", hipGetErrorString(he));
-    return (int)he;
-  }
-  std::lock_guard<std::mutex> lock(g_mu);
+// The heuristic's candidates for a plan's problem, within the workspace cap
+// (the cap preference alone does not bound what it returns): up to NTUNE, in
+// its ranking, as indices into res. Returns their count (0 on failure).
+constexpr int NREQ = 64;
+int candidates(hipblasLtHandle_t h, const Plan& p, hipblasLtMatmulHeuristicResult_t (&res)[NREQ],
+               int (&cand)[NTUNE], hipblasStatus_t* status) {
+  hipblasLtMatmulPreference_t pref = nullptr;
+  hipblasStatus_t s = hipblasLtMatmulPreferenceCreate(&pref);
+  const uint64_t cap = LINEAR_MAX_WORKSPACE_BYTES;
+  if (s == HIPBLAS_STATUS_SUCCESS)
+    s = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &cap,
+                                              sizeof cap);
+  int n_res = 0;
+  if (s == HIPBLAS_STATUS_SUCCESS)
+    s = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.d, p.d, pref, NREQ, res, &n_res);
+  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  int nc = 0;
+  for (int i = 0; s == HIPBLAS_STATUS_SUCCESS && i < n_res && nc < NTUNE; ++i)
+    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= cap) cand[nc++] = i;
+  *status = s;
+  return nc;
+}
+
+// Finds, or builds with the heuristic's first algorithm, the plan of one
+// problem on the current device (host work only: descriptors and the heuristic
+// query; no device allocation, no synchronisation). Returns 0, or a VM_E_* /
+// hipError_t code with `err` set. g_mu must be held.
+int find_plan(int dev, int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, Plan** out,
+              hipblasLtHandle_t* handle, char* err, size_t errn) {
   const Key key{dev, M, N, K, ldw, ldx, ldy};
-  auto it = g_plans.find(key);
-  if (it != g_plans.end()) {
-    if (!it->second.ok) {
-      snprintf(err, errn, "linear: hipBLASLt has no algorithm for M = %d, N = %d, K = %d", M, N, K);
-      return VM_E_UNSUPPORTED;
-    }
-    *out = &it->second;
-    return VM_OK;
-  }
   hipblasLtHandle_t h;
   auto hit = g_handles.find(dev);
   if (hit == g_handles.end()) {
@@ -181,6 +192,16 @@ int get_plan(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, const P
   } else {
     h = hit->second;
   }
+  *handle = h;
+  auto it = g_plans.find(key);
+  if (it != g_plans.end()) {
+    if (!it->second.ok) {
+      snprintf(err, errn, "linear: hipBLASLt has no algorithm for M = %d, N = %d, K = %d", M, N, K);
+      return VM_E_UNSUPPORTED;
+    }
+    *out = &it->second;
+    return VM_OK;
+  }
   Plan p;
   hipblasStatus_t s = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
   const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
@@ -191,36 +212,12 @@ int get_plan(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, const P
   if (s == HIPBLAS_STATUS_SUCCESS) s = hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, K, M, ldw);
   if (s == HIPBLAS_STATUS_SUCCESS) s = hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, K, N, ldx);
   if (s == HIPBLAS_STATUS_SUCCESS) s = hipblasLtMatrixLayoutCreate(&p.d, HIP_R_16BF, M, N, ldy);
-  hipblasLtMatmulPreference_t pref = nullptr;
-  if (s == HIPBLAS_STATUS_SUCCESS) s = hipblasLtMatmulPreferenceCreate(&pref);
-  const uint64_t cap = LINEAR_MAX_WORKSPACE_BYTES;
-  if (s == HIPBLAS_STATUS_SUCCESS)
-    s = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &cap,
-                                              sizeof cap);
-  // the heuristic's ranking, candidates within the workspace cap (the cap
-  // preference alone does not bound what it returns), then the timed choice
-  constexpr int NREQ = 64;
   hipblasLtMatmulHeuristicResult_t res[NREQ];
-  int n_res = 0;
-  if (s == HIPBLAS_STATUS_SUCCESS)
-    s = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.d, p.d, pref, NREQ, res, &n_res);
-  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
   int cand[NTUNE];
-  int nc = 0;
-  for (int i = 0; s == HIPBLAS_STATUS_SUCCESS && i < n_res && nc < NTUNE; ++i)
-    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= cap) cand[nc++] = i;
+  const int nc = s == HIPBLAS_STATUS_SUCCESS ? candidates(h, p, res, cand, &s) : 0;
   if (nc > 0) {
-    int pick = cand[0];
-    if (tune) {
-      // relaxed capture mode for this thread meanwhile, so that the scratch
-      // allocations cannot invalidate another stream's capture
-      hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
-      const bool swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
-      pick = cand[tune_algo(h, p, res, cand, nc, M, N, K, ldw, ldx, ldy)];
-      if (swapped) (void)hipThreadExchangeStreamCaptureMode(&mode);
-    }
-    p.algo = res[pick].algo;
-    p.workspace = res[pick].workspaceSize;
+    p.algo = res[cand[0]].algo;
+    p.workspace = res[cand[0]].workspaceSize;
     p.ok = true;
   }
   auto& slot = g_plans[key];  // remembered either way (linear.jl:20-21)
@@ -232,6 +229,22 @@ int get_plan(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, const P
   }
   *out = &slot;
   return VM_OK;
+}
+
+int get_plan(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, const Plan** out,
+             char* err, size_t errn) {
+  int dev = 0;
+  hipError_t he = hipGetDevice(&dev);
+  if (he != hipSuccess) {
+    snprintf(err, errn, "linear: hipGetDevice: %s", hipGetErrorString(he));
+    return (int)he;
+  }
+  std::lock_guard<std::mutex> lock(g_mu);
+  Plan* p = nullptr;
+  hipblasLtHandle_t h;
+  const int rc = find_plan(dev, M, N, K, ldw, ldx, ldy, &p, &h, err, errn);
+  if (rc == VM_OK) *out = p;
+  return rc;
 }
 
 // Narrow problems run on the library's own split-K MFMA kernel (launch_gemv):
@@ -252,6 +265,54 @@ bool gemv_aligned(const void* y, const void* x, const void* w) {
 }
 
 }  // namespace
+
+int linear_tune(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, char* err, size_t errn) {
+  if (gemv_shape(M, N, K, ldw, ldx, ldy)) {
+    // aligned views run the GEMV, which has nothing to tune; the plan stays
+    // the heuristic's first (it only serves misaligned views)
+    const Plan* p = nullptr;
+    const int rc = get_plan(M, N, K, ldw, ldx, ldy, &p, err, errn);
+    return rc == VM_E_UNSUPPORTED ? VM_OK : rc;
+  }
+  int dev = 0;
+  hipError_t he = hipGetDevice(&dev);
+  if (he != hipSuccess) {
+    snprintf(err, errn, "linear: hipGetDevice: %s", hipGetErrorString(he));
+    return (int)he;
+  }
+  std::lock_guard<std::mutex> lock(g_mu);
+  Plan* p = nullptr;
+  hipblasLtHandle_t h;
+  int rc = find_plan(dev, M, N, K, ldw, ldx, ldy, &p, &h, err, errn);
+  if (rc != VM_OK || p->pick >= 0) return rc;
+  hipblasLtMatmulHeuristicResult_t res[NREQ];
+  int cand[NTUNE];
+  hipblasStatus_t s;
+  const int nc = candidates(h, *p, res, cand, &s);
+  if (nc == 0) {
+    p->pick = 0;  // keeps what it has
+    return VM_OK;
+  }
+  // relaxed capture mode for this thread meanwhile, so that the scratch
+  // allocations cannot invalidate a capture running on another stream
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  const bool swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
+  const int k = tune_algo(h, *p, res, cand, nc, M, N, K, ldw, ldx, ldy);
+  if (swapped) (void)hipThreadExchangeStreamCaptureMode(&mode);
+  p->algo = res[cand[k]].algo;
+  p->workspace = res[cand[k]].workspaceSize;
+  p->pick = k;
+  return VM_OK;
+}
+
+int linear_plan_state(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -2;
+  std::lock_guard<std::mutex> lock(g_mu);
+  auto it = g_plans.find(Key{dev, M, N, K, ldw, ldx, ldy});
+  if (it == g_plans.end() || !it->second.ok) return -2;
+  return it->second.pick;
+}
 
 int linear_workspace(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, size_t* bytes,
                      char* err, size_t errn) {
@@ -297,9 +358,7 @@ int linear_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const u
     return VM_OK;
   }
   const Plan* p = nullptr;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess) cs = hipStreamCaptureStatusActive;
-  int rc = get_plan(M, N, K, ldw, ldx, ldy, &p, err, errn, cs == hipStreamCaptureStatusNone);
+  int rc = get_plan(M, N, K, ldw, ldx, ldy, &p, err, errn);
   if (rc != VM_OK) return rc;
   if (p->workspace > 0 && (workspace == nullptr || workspace_bytes < p->workspace)) {
     snprintf(err, errn, "linear: workspace of %zu bytes < %zu required (vm_linear_workspace_bytes)",

@@ -799,6 +799,15 @@ size_t vm_linear_workspace_bytes(int M, int N, int K, int64_t ldw, int64_t ldx, 
   return n;
 }
 
+int vm_linear_tune(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy) {
+  TRY(linear_check(M, N, K, ldw, ldx, ldy));
+  return vm::linear_tune(M, N, K, ldw, ldx, ldy, g_err, sizeof g_err);
+}
+
+int vm_linear_plan_state(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy) {
+  return vm::linear_plan_state(M, N, K, ldw, ldx, ldy);
+}
+
 int vm_linear(vm_bf16* y, int64_t ldy, const vm_bf16* x, int64_t ldx, const vm_bf16* w,
               int64_t ldw, int M, int N, int K, void* workspace, size_t workspace_bytes,
               vm_stream st) {

@@ -23,7 +23,7 @@ from .sizes import sizes
 __all__ = [
     "rope_tables", "qnorm_rope_", "knorm_rope_append_", "attention_", "attention",
     "decode_attention_", "decode_attention", "decode_scratch_bytes", "sigmoid_gate_",
-    "sigmoid", "fill_normal_", "linear_", "linear", "linear_workspace_bytes",
+    "sigmoid", "fill_normal_", "linear_", "linear", "linear_workspace_bytes", "linear_tune",
     "rms_norm_", "rms_norm", "fused_add_rms_norm_", "fused_add_rms_norm", "silu_mul_",
     "embed_", "lm_head_argmax_", "lm_head_argmax", "lm_head_argmax_scratch_bytes",
     "causal_conv1d_", "causal_conv1d", "causal_conv1d_sequence_", "causal_conv1d_sequence",
@@ -215,12 +215,37 @@ def sigmoid_gate_(O, G):
     return O
 
 
+_TUNED = set()
+
+
+def _tune(M, N, K, ldw, ldx, ldy):
+    """vm_linear_tune once per problem and device, outside any stream capture
+    (the timing allocates and waits); under capture the plan keeps the
+    heuristic's first, as the reference's does."""
+    key = (torch.cuda.current_device(), M, N, K, ldw, ldx, ldy)
+    if key in _TUNED or torch.cuda.is_current_stream_capturing():
+        return
+    call("vm_linear_tune", M, N, K, ldw, ldx, ldy)
+    _TUNED.add(key)
+
+
+def linear_tune(x, W, y=None):
+    """Time the candidate algorithms of this problem's plan and keep the fastest
+    (vm_linear_tune: a load-time call that allocates scratch and synchronises;
+    no counterpart in the reference, whose plan keeps the heuristic's first).
+    linear_workspace_bytes calls it for a new problem when no capture runs."""
+    N, K, M = _rows(x), x.shape[-1], W.shape[0]
+    ldy = M if y is None else y.stride(-2) if y.dim() > 1 else M
+    _tune(M, N, K, W.stride(0), _ld(x), ldy)
+
+
 def linear_workspace_bytes(x, W, y=None) -> int:
     """Workspace the cached plan of this problem needs (builds the plan on first
-    use, linear.jl:22-38)."""
+    use, linear.jl:22-38; tuned first when no capture runs, see linear_tune)."""
     N, K = _rows(x), x.shape[-1]
     M = W.shape[0]
     ldy = M if y is None else y.stride(-2) if y.dim() > 1 else M
+    _tune(M, N, K, W.stride(0), _ld(x), ldy)
     n = _lib.load().vm_linear_workspace_bytes(M, N, K, W.stride(0), _ld(x), ldy)
     if n == ctypes.c_size_t(-1).value:
         _lib.check(_lib.VM_E_UNSUPPORTED, "vm_linear_workspace_bytes")
@@ -276,6 +301,7 @@ def linear(x, W, **kw) -> dict:
 def linear_add_rms_norm_workspace_bytes(a, W) -> int:
     """Workspace of linear_add_rms_norm_ for this problem."""
     M, K, N = W.shape[0], a.shape[-1], _rows(a)
+    _tune(M, N, K, W.stride(0), _ld(a), M)
     n = _lib.load().vm_linear_add_rms_norm_workspace_bytes(M, N, K, W.stride(0), _ld(a))
     if n == ctypes.c_size_t(-1).value:
         _lib.check(_lib.VM_E_UNSUPPORTED, "vm_linear_add_rms_norm_workspace_bytes")
