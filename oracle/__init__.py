@@ -325,6 +325,69 @@ def model_step(E, layers, norm_w, head, result, positions, cos_tab, sin_tab, *, 
     return res, gap, bf16_to_f32(xn)
 
 
+def deltanet_prefill_layer(xn, l, *, Dk, Dv, Hk, Hv, eps, offset, nthreads=0):
+    """forward(l::DeltaNetLayer, m, xn, T, B; offset) (src/llm/qwen35.jl:320-365):
+    xn [B][T][Dm] bf16 bits -> (h [B][T][Dm] fp32, new ring, new state). qz, ab
+    and the conv output are bf16 buffers in the reference (:322-323, :328), as
+    is the gated norm's output fed to Wout (:363-364): rounded there. A suffix
+    (offset > 0) takes its conv's left context from the ring (:333-344). l: as
+    deltanet_decode_layer."""
+    B, T, Dm = xn.shape
+    n = 2 * Hk * Dk + Hv * Dv
+    x2 = _c(xn, np.uint16).reshape(B * T, Dm)
+    qz = f32_to_bf16(linear(x2, l["Wqz"], nthreads=nthreads)).reshape(B, T, -1)
+    ab = f32_to_bf16(linear(x2, l["Wab"], nthreads=nthreads)).reshape(B, T, 2 * Hv)
+    conv, ring = conv1d_sequence(np.ascontiguousarray(qz[..., :n]), l["conv_w"], l.get("conv_b"),
+                                 s_in=l["ring"] if offset > 0 else None, act=True)
+    p = deltanet_prep(f32_to_bf16(conv), ab, l["A_log"], l["dt_bias"], Dk=Dk, Dv=Dv, Hk=Hk, Hv=Hv)
+    o, S = deltanet_sequence(p["q"], p["k"], p["v"], p["beta"], p["gate"], l["S"])
+    y = gated_rms_norm(o, np.ascontiguousarray(qz[..., n:]), l["gnorm_w"], eps=eps)
+    h = linear(f32_to_bf16(y).reshape(B * T, Hv * Dv), l["Wout"], nthreads=nthreads)
+    return h.reshape(B, T, Dm), ring, S
+
+
+def prefill_model(E, layers, norm_w, head, ids, offset, cos_tab, sin_tab, *, Hq, Hk, eps,
+                  nthreads=0, linear_cfg=None):
+    """prefill!(m, gen, ids; offset) (src/llm/qwen35.jl:369-395), greedy: ids [B][T]
+    1-based tokens continuing `offset` resident ones. Layers as model_step: the
+    attention layers' caches hold `offset` prior rows, the DeltaNet layers' ring
+    and state carry the prefix. The residual x, xn, h, gu and mid are bf16 in
+    the reference (:375-388): rounded there. Returns (next tokens [B], logit gaps
+    [B], the last token's final xn [B][Dm] fp32, new states: per layer (K cache,
+    V cache) or (ring, S))."""
+    ids = np.asarray(ids, np.int64)
+    B, T = ids.shape
+    Dm = E.shape[1]
+    x = _c(E[np.clip(ids - 1, 0, E.shape[0] - 1)], np.uint16).reshape(B * T, Dm)
+    xn = f32_to_bf16(rms_norm(x, layers[0]["norm1"], eps=eps, offset=1.0))
+    states = []
+    for i, l in enumerate(layers):
+        if l.get("kind") == "linear_attention":
+            h, ring, S = deltanet_prefill_layer(xn.reshape(B, T, Dm), l, eps=eps, offset=offset,
+                                                nthreads=nthreads, **linear_cfg)
+            states.append((ring, S))
+        else:
+            prior = np.full(B, offset, np.int32)
+            h, kn, vn = prefill_layer(xn.reshape(B, T, Dm), l["Wqkv"], l["Wo"], l["kc"], l["vc"],
+                                      prior, np.full(B, T, np.int32), l["qw"], l["kw"], cos_tab,
+                                      sin_tab, Hq=Hq, Hk=Hk, eps=eps, w_offset=1.0,
+                                      nthreads=nthreads)
+            kc, vc = _c(l["kc"], np.uint16).copy(), _c(l["vc"], np.uint16).copy()
+            kc[:, :, offset:offset + T] = f32_to_bf16(kn)
+            vc[:, :, offset:offset + T] = f32_to_bf16(vn)
+            states.append((kc, vc))
+        y, xo = rms_norm(x, l["norm2"], eps=eps, offset=1.0, dx=f32_to_bf16(h.reshape(B * T, Dm)))
+        x, xn = f32_to_bf16(xo), f32_to_bf16(y)
+        gu = f32_to_bf16(linear(xn, l["Wgu"], nthreads=nthreads))
+        h = linear(f32_to_bf16(silu_mul(gu)), l["Wd"], nthreads=nthreads)
+        nw = norm_w if i == len(layers) - 1 else layers[i + 1]["norm1"]
+        y, xo = rms_norm(x, nw, eps=eps, offset=1.0, dx=f32_to_bf16(h))
+        x, xn = f32_to_bf16(xo), f32_to_bf16(y)
+    last = np.ascontiguousarray(xn.reshape(B, T, Dm)[:, T - 1])
+    res, gap = lm_head_argmax(last, head, nthreads=nthreads)
+    return res, gap, bf16_to_f32(last), states
+
+
 # ---- linear-attention layer parts (oracle/deltanet.c) -----------------------
 
 def _vp(a):

@@ -159,7 +159,8 @@ def test_decode_attention_operator(vm, orc):
 
 def test_config3_batched_decode_full_size(vm, orc):
     """BASELINE config 3 at full size: B=32, capacity 32768, attended lengths
-    ~U{1024..32768} (seeded); 6 sequences re-evaluated by the oracle."""
+    ~U{1024..32768} (seeded); every sequence re-evaluated by the oracle (its
+    caches copied to the host one sequence at a time), with its appended row."""
     banner("config3 decode B=32 ctx=32768")
     B, ctx = 32, 32768
     rng = np.random.default_rng(3)
@@ -177,19 +178,23 @@ def test_config3_batched_decode_full_size(vm, orc):
     vm.gated_attn_decode_(O, layer, m, gen, to_dev(qkv))
     torch.cuda.synchronize()
     got = dev_f32(O)
-    c, s = orc.rope_tables(HALF, ctx, THETA)
-    sample = [0, 1, 7, 15, 22, 31]
-    kc = from_dev(K[sample])
-    vc = from_dev(V[sample])
-    ref, kn, _ = orc.gated_decode(qkv[sample], kc, vc, pos[sample], qw, kw, c, s, Hq=HQ, Hk=HK,
-                                  eps=EPS, w_offset=1.0)
-    mx, mn = maxmean(got[sample], ref)
-    print(f"config3 sample: out max {mx:.3e} mean {mn:.3e}")
-    assert mx <= TOL_MAX and mn <= TOL_MEAN
-    kg = np.stack([bf16_to_f32(kc[i][:, pos[b] - 1]) for i, b in enumerate(sample)])
-    kmx, kmn = maxmean(kg, kn)
-    assert kmx <= TOL_MAX and kmn <= TOL_MEAN
     assert np.all(np.isfinite(got))
+    c, s = orc.rope_tables(HALF, ctx, THETA)
+    errs, kerrs = [], []
+    for b in range(B):
+        # the step appended row pos[b] - 1: the oracle re-does the append from the
+        # raw projection, so the prior rows it reads are the cache as written
+        kc, vc = from_dev(K[b:b + 1]), from_dev(V[b:b + 1])
+        ref, kn, _ = orc.gated_decode(qkv[b:b + 1], kc, vc, pos[b:b + 1], qw, kw, c, s, Hq=HQ, Hk=HK,
+                                      eps=EPS, w_offset=1.0)
+        errs.append(np.abs(got[b:b + 1].astype(np.float64) - ref))
+        kerrs.append(np.abs(bf16_to_f32(kc[0][:, pos[b] - 1]).astype(np.float64) - kn[0]))
+    e, ke = np.concatenate([x.ravel() for x in errs]), np.concatenate([x.ravel() for x in kerrs])
+    worst = int(np.argmax([x.max() for x in errs]))
+    print(f"config3, all {B} sequences: out max {e.max():.3e} (sequence {worst}, length "
+          f"{pos[worst]}) mean {e.mean():.3e}; K max {ke.max():.3e} mean {ke.mean():.3e}")
+    assert e.max() <= TOL_MAX and e.mean() <= TOL_MEAN
+    assert ke.max() <= TOL_MAX and ke.mean() <= TOL_MEAN
 
 
 def test_config4_graph_replay_matches_eager(vm, orc):

@@ -394,6 +394,153 @@ def test_prefix_prefill_with_restore_matches_full(vm):
     assert gen.positions.cpu().tolist() == [22] * cfg.B
 
 
+def _lin_cfg(cfg):
+    lc = cfg.linear
+    return dict(Dk=lc.Dk, Dv=lc.Dv, Hk=lc.Hk, Hv=lc.Hv)
+
+
+def _check_prefill(vm, m, gen, res, gap, xn, states, what):
+    """GPU prefill_ results against orc.prefill_model's: the last token's final
+    xn, the tokens where the oracle's margin allows, each DeltaNet state and
+    ring, each attention layer's cache rows."""
+    mx, mn = maxmean(dev_f32(m.xn), xn)
+    rel = mn / np.abs(xn).mean()
+    got = gen.result.cpu().numpy()
+    ok = gap > 0.05
+    print(f"{what}: xn max {mx:.3e} mean {mn:.3e} ({rel:.2%}); tokens {got.tolist()} oracle "
+          f"{res.tolist()} margins {np.round(gap, 3).tolist()}")
+    assert mx <= 0.1 and rel <= 1e-2
+    assert ok.sum() >= len(got) - 1 and np.array_equal(got[ok], res[ok])
+    for i, (l, st) in enumerate(zip(m.layers, states)):
+        if isinstance(l, vm.DeltaNetLayer):
+            ring_o, S_o = st
+            s_err = float(np.abs(l.S.cpu().numpy() - S_o).max() / np.abs(S_o).max())
+            r_err = float(np.abs(dev_f32(l.conv_state) - bf16_to_f32(ring_o)).max() /
+                          np.abs(bf16_to_f32(ring_o)).max())
+            print(f"  layer {i} DeltaNet: S max err / max {s_err:.2e}, ring {r_err:.2e}")
+            assert s_err <= 1e-2 and r_err <= 1e-2
+        else:
+            kc_o, vc_o = st
+            k_err = float(np.abs(dev_f32(l.K_cache) - bf16_to_f32(kc_o)).max())
+            v_err = float(np.abs(dev_f32(l.V_cache) - bf16_to_f32(vc_o)).max())
+            print(f"  layer {i} attention: cache max err K {k_err:.2e} V {v_err:.2e}")
+            assert k_err <= 5e-2 and v_err <= 5e-2
+
+
+def test_prefill_mixed_vs_oracle(vm, orc):
+    """prefill! (qwen35.jl:369-395) of the mixed stack (3 DeltaNet + 1 attention,
+    B = 3) from a reset state over 21 tokens, against orc.prefill_model; then a
+    13-token prefix and an 8-token suffix (offset 13, the suffix conv's left
+    context from the ring) against the oracle run the same way."""
+    banner("prefill mixed 3 DeltaNet + 1 attention B=3 T=21, and 13 + 8")
+    cfg = _mixed_cfg(vm)
+    m = vm.random_model(cfg, seed=21)
+    ids = np.random.default_rng(22).integers(1, cfg.vocab + 1, size=(cfg.B, 21)).astype(np.int32)
+    c, s = orc.rope_tables(HALF, cfg.attn.Ctx, THETA)
+    kw = dict(Hq=HQ, Hk=HK, eps=EPS, linear_cfg=_lin_cfg(cfg))
+    E, nw, head = from_dev(m.E), from_dev(m.norm_w), from_dev(m.head)
+    gen = vm.Generation(cfg.B, 2)
+    m.reset_()
+    for l in m.layers:
+        if not isinstance(l, vm.DeltaNetLayer):
+            l.K_cache.zero_()
+            l.V_cache.zero_()
+    layers0 = _host_mixed_layers(vm, m)     # reset DeltaNet states, zero caches
+    vm.prefill_(m, gen, torch.from_numpy(ids).cuda())
+    torch.cuda.synchronize()
+    res, gap, xn, states = orc.prefill_model(E, layers0, nw, head, ids, 0, c, s, **kw)
+    _check_prefill(vm, m, gen, res, gap, xn, states, "prefill T=21")
+    # prefix + suffix, on both sides
+    m.reset_()
+    vm.prefill_(m, gen, torch.from_numpy(ids[:, :13]).cuda())
+    vm.prefill_(m, gen, torch.from_numpy(ids[:, 13:]).cuda(), offset=13)
+    torch.cuda.synchronize()
+    _, _, _, st13 = orc.prefill_model(E, layers0, nw, head, ids[:, :13], 0, c, s, **kw)
+    cont = [dict(l) for l in layers0]
+    for l, st in zip(cont, st13):
+        if l.get("kind") == "linear_attention":
+            l["ring"], l["S"] = st
+        else:
+            l["kc"], l["vc"] = st
+    res2, gap2, xn2, states2 = orc.prefill_model(E, cont, nw, head, ids[:, 13:], 13, c, s, **kw)
+    _check_prefill(vm, m, gen, res2, gap2, xn2, states2, "prefill 13 + 8")
+    assert gen.positions.cpu().tolist() == [22] * cfg.B
+
+
+def test_decode_step_qwen35_4b_shape_vs_oracle(vm, orc):
+    """One step! of the Qwen3.5-4B-shaped model the bench reports (32 layers,
+    24 Gated DeltaNet + 8 gated attention, hidden 2560, MLP 9216, vocab 151936,
+    tied head, random weights; B = 32 at ragged positions, random DeltaNet states
+    and rings), against orc.model_step on four of the sequences: the tokens where
+    the margin allows, and the final normed hidden state within twice the
+    distance one extra bf16 rounding of the input moves the oracle's own."""
+    banner("decode step Qwen3.5-4B shape B=32, 4 sequences vs oracle")
+    B, Ctx = 32, 2048
+    a = vm.AttnConfig(D=2560, Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=Ctx,
+                      B=B)
+    cfg = vm.ModelConfig(attn=a, inter=9216, vocab=151936, n_layers=32, tied=True, interval=4)
+    m = vm.random_model(cfg, seed=23)
+    g = torch.Generator(device="cuda").manual_seed(24)
+    for i, l in enumerate(m.layers):
+        if isinstance(l, vm.DeltaNetLayer):
+            l.S.copy_(torch.randn(l.S.shape, generator=g, device="cuda") * 0.05)
+            vm.fill_normal_(l.conv_state, 240 + i)
+        else:
+            vm.fill_normal_(l.K_cache, 250 + i)
+            vm.fill_normal_(l.V_cache, 260 + i)
+    rng = np.random.default_rng(25)
+    pos = rng.integers(256, Ctx + 1, size=B).astype(np.int32)
+    tok = rng.integers(1, cfg.vocab + 1, size=B).astype(np.int32)
+    sample = np.array([0, 9, 20, 31])
+    pos[sample[0]] = Ctx
+    gen = vm.Generation(B, 2)
+    gen.positions.copy_(i32(pos))
+    gen.result.copy_(i32(tok))
+    # the sampled sequences' states before the step, and the weights
+    layers = []
+    for l in m.layers:
+        d = dict(norm1=from_dev(l.norm1), norm2=from_dev(l.norm2), Wgu=from_dev(l.Wgu),
+                 Wd=from_dev(l.Wd))
+        if isinstance(l, vm.DeltaNetLayer):
+            d.update(kind="linear_attention", Wqz=from_dev(l.Wqz), Wab=from_dev(l.Wab),
+                     Wout=from_dev(l.Wout), conv_w=from_dev(l.conv_w), conv_b=None,
+                     ring=from_dev(l.conv_state[sample]), A_log=l.A_log.cpu().numpy(),
+                     dt_bias=l.dt_bias.cpu().numpy(), gnorm_w=from_dev(l.gnorm_w),
+                     S=l.S[sample].cpu().numpy())
+        else:
+            d.update(Wqkv=from_dev(l.Wqkv), Wo=from_dev(l.Wo), qw=from_dev(l.qw), kw=from_dev(l.kw),
+                     kc=from_dev(l.K_cache[sample]), vc=from_dev(l.V_cache[sample]))
+        layers.append(d)
+    vm.step_(m, gen)
+    torch.cuda.synchronize()
+    c, s = orc.rope_tables(HALF, Ctx, THETA)
+    res, gap, xn = orc.model_step(from_dev(m.E), layers, from_dev(m.norm_w), from_dev(m.head),
+                                  tok[sample], pos[sample], c, s, Hq=HQ, Hk=HK, eps=EPS,
+                                  linear_cfg=_lin_cfg(cfg))
+    mx, mn = maxmean(dev_f32(m.xn)[sample], xn)
+    got = gen.result.cpu().numpy()[sample]
+    ok = gap > 0.05
+    # the model's own sensitivity: the oracle again with every input embedding
+    # element moved by one bf16 ulp (a random sign), i.e. one different rounding
+    # of the step's first buffer
+    E = from_dev(m.E)
+    rows = tok[sample] - 1
+    flip = np.random.default_rng(26).choice(np.array([-1, 1], np.int32), size=(len(sample), E.shape[1]))
+    Ep = E.copy()
+    Ep[rows] = (E[rows].astype(np.int32) + flip).astype(np.uint16)
+    _, _, xn_p = orc.model_step(Ep, layers, from_dev(m.norm_w), from_dev(m.head), tok[sample],
+                                pos[sample], c, s, Hq=HQ, Hk=HK, eps=EPS, linear_cfg=_lin_cfg(cfg))
+    pmx, pmn = maxmean(xn_p, xn)
+    print(f"4B-shape step, sequences {sample.tolist()}: xn vs oracle max {mx:.3e} mean {mn:.3e} "
+          f"({mn / np.abs(xn).mean():.2%}); oracle vs its 1-ulp-input twin max {pmx:.3e} mean "
+          f"{pmn:.3e}; tokens {got.tolist()} oracle {res.tolist()} margins {np.round(gap, 3).tolist()}")
+    # a 32-layer random-weight stack amplifies a one-ulp change of its input to a
+    # few % of |xn|: the GPU step may differ from the oracle by no more than twice
+    # what that single extra rounding does (measured: 0.8x mean, 1.1x max)
+    assert mn <= 2.0 * pmn and mx <= 2.0 * pmx
+    assert ok.sum() >= len(sample) - 1 and np.array_equal(got[ok], res[ok])
+
+
 def test_identity_mixed_model_step(vm):
     """Every projection zero on the mixed stack: the next token is the input."""
     banner("identity mixed model step")
