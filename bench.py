@@ -14,6 +14,9 @@ in a hipGraph and replayed 256 times on a dedicated stream with the position
 advancing on the device)
 in HBM GB/s of K/V actually attended (4096 B per token) + 32 KiB per sequence,
 and config 1 (B=1 at 512 tokens, launch-latency-bound) as time per step.
+Key "prefill_config2_online_max": the config-2 prefill with one K-norm weight
+of 4 (kw[0] = 4), whose logit bound passes the static shift's 64 so the kernel
+takes its online-max softmax; "decode.config3_running_max" likewise for config 3.
 Key "prefill_config5": BASELINE config 5 (B=4 ragged chunks after 8-32 K
 priors) in algorithmic TFLOP/s, step and attention kernel, and the step with the
 layer's V^T workspace kept between chunks (staging the chunk only). Key "decode_step": the
@@ -121,13 +124,23 @@ def settle_clocks(vm, torch, step, block=20, tol=0.01, min_s=0.25, max_s=5.0):
             if len(means) > 6 else [round(1e3 * m, 2) for m in means]}
 
 
-def bench_prefill(vm, torch, steps, warmup, T=4096, seed=2, settle=True):
+def _big_kw0(kw, kw0):
+    """kw[0] = kw0 (bf16): with (w + 1) weights, max|kw + 1| = kw0 + 1 lifts the
+    static logit bound past 64 (log2 units), so the kernels take their exact
+    online-max softmax (prefill and decode alike: a running row max, rescaled
+    lazily)."""
+    if kw0 is not None:
+        kw[0] = float(kw0)
+
+
+def bench_prefill(vm, torch, steps, warmup, T=4096, seed=2, settle=True, kw0=None):
     B, ctx = 1, T
     cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
     qw = torch.empty(D, dtype=torch.bfloat16, device="cuda")
     kw = torch.empty_like(qw)
     vm.fill_normal_(qw, seed * 100 + 1, scale=0.05)
     vm.fill_normal_(kw, seed * 100 + 2, scale=0.05)
+    _big_kw0(kw, kw0)
     qkv = torch.empty((B, T, S, D), dtype=torch.bfloat16, device="cuda")
     vm.fill_normal_(qkv, seed * 100 + 3)
     m = vm.AttnModel(cfg)
@@ -304,7 +317,7 @@ def decode_bytes(lengths):
     return float(np.sum(np.asarray(lengths, np.float64)) * 4096.0 + 32768.0 * len(lengths))
 
 
-def bench_decode3(vm, torch, steps, warmup, seed=3):
+def bench_decode3(vm, torch, steps, warmup, seed=3, kw0=None):
     B, ctx = 32, 32768
     rng = np.random.default_rng(seed)
     lengths = rng.integers(1024, 32769, size=B).astype(np.int32)
@@ -313,6 +326,7 @@ def bench_decode3(vm, torch, steps, warmup, seed=3):
     kw = torch.empty_like(qw)
     vm.fill_normal_(qw, 301, scale=0.05)
     vm.fill_normal_(kw, 302, scale=0.05)
+    _big_kw0(kw, kw0)
     layer = vm.attn_layer(cfg, qw, kw)
     vm.fill_normal_(layer.K_cache, 303)
     vm.fill_normal_(layer.V_cache, 304)
@@ -1056,6 +1070,23 @@ def main():
             f"attn kernel {pf['attn_kernel_ms'] * 1e3:.1f} us back to back "
             f"({pf['attn_kernel_ms_events'] * 1e3:.1f} us on per-dispatch events), "
             f"K/V append + V^T staging {pf['append_vt_kernel_ms']:.4f} ms")
+    pf_shift = None
+    if not args.no_prefill:
+        # the exact-softmax path the kernel takes when the norm weights allow
+        # logits past the static bound: one K-norm weight of 4 (kw[0] = 4)
+        log("[bench] prefill config2 with kw[0] = 4 (online-max softmax)")
+        r = bench_prefill(vm, torch, max(20, args.steps // 5), 5, settle=False, kw0=4.0)
+        pf_shift = {"kw0": 4.0, "softmax": "online row max, moved lazily (by > 8 in log2 units), "
+                                           "O and l rescaled when it moves",
+                    "ms_per_step": r["ms_per_step"], "tflops": r["tflops"],
+                    "attn_kernel_ms": r["attn_kernel_ms"],
+                    "attn_kernel_tflops": r["flops"] / (r["attn_kernel_ms"] * 1e-3) / 1e12,
+                    "attn_kernel_frac_of_bf16_peak":
+                        r["flops"] / (r["attn_kernel_ms"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                    "vs_static_kernel": r["attn_kernel_ms"] / pf["attn_kernel_ms"] if pf else None}
+        log(f"[bench] prefill kw[0]=4: attn kernel {r['attn_kernel_ms'] * 1e3:.1f} us = "
+            f"{pf_shift['attn_kernel_tflops']:.0f} TFLOP/s ({pf_shift['vs_static_kernel']:.2f}x the "
+            f"static path)")
     pf5 = None
     if not args.no_prefill and not args.no_config5:
         log("[bench] prefill config5 (ragged chunked, B=4)")
@@ -1069,6 +1100,11 @@ def main():
         d3 = bench_decode3(vm, torch, max(10, args.steps // 2), 3)
         log(f"[bench] decode3: {d3['ms_per_step']:.3f} ms/step {d3['gbs']:.0f} GB/s "
             f"(split kernel {d3['split_kernel_gbs']:.0f} GB/s)")
+        log("[bench] decode config3 with kw[0] = 4 (running-max softmax)")
+        d3s = bench_decode3(vm, torch, max(10, args.steps // 2), 3, kw0=4.0)
+        d3s["kw0"] = 4.0
+        d3s["softmax"] = "running max, rescaled lazily (only when it grows by > 8 in log2 units)"
+        log(f"[bench] decode3 kw[0]=4: {d3s['ms_per_step']:.3f} ms/step {d3s['gbs']:.0f} GB/s")
         log("[bench] decode config4 B=1 131072, 256 graph replays")
         d4 = bench_decode4(vm, torch)
         log(f"[bench] decode4: {d4['ms_per_replay'] * 1e3:.1f} us/replay {d4['gbs']:.0f} GB/s "
@@ -1076,9 +1112,10 @@ def main():
         log("[bench] decode config1 B=1 at 512")
         d1 = bench_decode1(vm, torch, max(20, args.steps // 3), 10)
         log(f"[bench] decode1: {d1['us_per_step']:.1f} us/step")
-        for d in (d3, d4, d1):
+        for d in (d3, d3s, d4, d1):
             d["frac_of_hbm_peak"] = d["gbs"] / PEAK_HBM_GBS
-        decode = {"config3": d3, "config4": d4, "config1": d1, "peak_GBs": PEAK_HBM_GBS}
+        decode = {"config3": d3, "config3_running_max": d3s, "config4": d4, "config1": d1,
+                  "peak_GBs": PEAK_HBM_GBS}
     layer = None
     if not args.no_layer:
         log("[bench] layers (projections + attention), hidden 2560")
@@ -1155,6 +1192,7 @@ def main():
                                "per-dispatch events of the timed steps",
                      "flop_per_launch": pf["flops"]},
         "cpu_baseline": cpu,
+        "prefill_config2_online_max": pf_shift,
         "prefill_config5": pf5,
         "decode": decode,
         "layer": layer,

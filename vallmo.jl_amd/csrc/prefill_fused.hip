@@ -28,8 +28,9 @@
 // Softmax: the QK-norm weights bound every logit (|q op| <= max|qw + w_offset|,
 // |k~| <= 16 max|kw + w_offset|). When the bound is at most 64 in log2 units,
 // P = exp2(S) needs no shift (P stays within 2^+-64 and the final 1/l cancels any
-// common scale). Otherwise an exact row max is taken first by a QK-only pass over
-// the same tiles and P = exp2(S - max).
+// common scale). Otherwise an online row max, moved lazily (only when it grows
+// by more than 8 in log2 units), shifts P = exp2(S - max); O and l are rescaled
+// when it moves.
 #include <hip/hip_ext.h>
 
 #include "common.h"
@@ -271,22 +272,6 @@ __device__ __forceinline__ u32x4 ds_b128(uint32_t addr) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
   return r;
 }
-template <int N>
-__device__ __forceinline__ void lgkm_take(u32x4& x, u32x4& y) {
-  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N));
-}
-// S^T[key][row] (+)= K fragment . Q^T (S in VGPRs, Q in AGPRs); the builtin would
-// accumulate in AGPRs. A dependent product always has another MFMA between it and
-// its producer (the two row blocks alternate), which needs no wait states.
-__device__ __forceinline__ void mfma_qk0(f32x16& s, const u32x4& k, const uint4& q) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0"
-               : "=&v"(s) : "v"(k), "a"(__builtin_bit_cast(u32x4, q)));
-}
-__device__ __forceinline__ void mfma_qk(f32x16& s, const u32x4& k, const uint4& q) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
-               : "+v"(s) : "v"(k), "a"(__builtin_bit_cast(u32x4, q)));
-}
-
 // 11+ wait states before a VALU reads what an 8-pass MFMA wrote (threaded
 // through the results so no reader moves above the padding)
 __device__ __forceinline__ void mfma_drain(f32x16& s0, f32x16& s1) {
@@ -406,6 +391,7 @@ struct SoloState {
   f32x16 s[2][2];    // S^T in log2 units, by step parity and tile
   u32x4 p[2][4];     // packed P^T, by step parity and key step
   float negm;        // minus this lane's row shift (log2 units)
+  float mrun;        // SHIFT: the running row max the shift follows (-inf before any key)
   uint32_t kb[8];    // LDS address of K fragment q (q + 8 at +256) in this step's K object
   u32x4 gv[16];      // gate logits of this wave's rows, coalesced (see gate_loads; AGPRs)
   float lsum;        // row sum of this lane's packed P^T
@@ -507,13 +493,6 @@ __device__ __forceinline__ void v_piece(const SoloCtx& sc, const char* src, uint
   __builtin_amdgcn_global_load_lds((const void*)(src + sc.vsrc),
                                    (__attribute__((address_space(3))) void*)(dst + 4 * sc.c.wave * 512),
                                    16, 1024 * P, 0);
-}
-__device__ __forceinline__ void k_tile_load(const FCtx& c, int t, uint16_t* dst) {
-  const TileSrc src = k_tile(c, t);
-  k_piece<0>(c, src, dst);
-  k_piece<1>(c, src, dst);
-  k_piece<2>(c, src, dst);
-  k_piece<3>(c, src, dst);
 }
 
 __device__ __forceinline__ TileStream v_stream(const SoloCtx& sc, int t0) {
@@ -653,6 +632,34 @@ __device__ __forceinline__ void solo_slot(SoloState& st, const SoloCtx& sc, cons
   sfence();
 }
 
+// SHIFT: the online row max, updated at the start of each softmax stage from the
+// block's (masked) logits in s[1 - J], lazily: the shift moves only when a row's
+// max grows by more than 8 (log2 units; P then stays below 2^8). The row sum is
+// rescaled at once; the returned factor (1 for rows whose shift stays) is owed by
+// O, whose products of this step still use the old shift (the caller applies it
+// after them). A row with no valid key yet keeps shift 0 (its P are 0).
+template <int J>
+__device__ __forceinline__ float online_max(SoloState& st) {
+  float mb = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mb = fmaxf(mb, st.s[1 - J][t][j]);
+  mb = xor32_max(mb);
+  const float m_new = fmaxf(st.mrun, mb);
+  const bool need = m_new > st.mrun + 8.0f;  // false while both are -inf
+  float resc = 1.0f;
+  if (__ballot(need) != 0ull) {
+    if (need) {
+      resc = st.mrun == -INFINITY ? 1.0f : fast_exp2(st.mrun - m_new);
+      st.lsum *= resc;
+      st.mrun = m_new;
+      st.negm = -m_new;
+    }
+  }
+  return resc;
+}
+
 // Step i (parity J = i & 1): QK of block i + 2 (K object (i + 2) % 3) into s[J],
 // the softmax of block i + 1 from s[1 - J] into p[1 - J], PV of block i from p[J]
 // (V object J); this wave's loads of V^T block i + 1 (V object 1 - J) and then K
@@ -696,63 +703,33 @@ __device__ __forceinline__ void solo_step(SoloState& st, const SoloCtx& sc, cons
   if constexpr (SM) {
     if (solo_needs_mask<CAUSAL>(g, i + 1)) solo_mask<CAUSAL>(g, i + 1, lane, st.s[1 - J]);
   }
+  float resc = 1.0f;  // SHIFT: O's rescale, owed after this step's products
+  if constexpr (SHIFT && SM) resc = online_max<J>(st);
   sfence();
 #define SS(m) solo_slot<SHIFT, QK, SM, PV, DV, FIRST, J, m>(st, sc, L, kb, kd, ks, vs, ops)
   SS(0); SS(1); SS(2); SS(3); SS(4); SS(5); SS(6); SS(7);
   SS(8); SS(9); SS(10); SS(11); SS(12); SS(13); SS(14); SS(15);
 #undef SS
   if constexpr (QK) mfma_drain(st.s[J][0], st.s[J][1]);
+  if constexpr (SHIFT && SM && PV) {
+    if (__ballot(resc != 1.0f) != 0ull) {
+      // O now holds blocks <= i at the old shift: move it to the new one before
+      // the next step adds block i + 1 (rare: the max grows by > 8 a few times)
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
+                   : "+a"(st.o[0]), "+a"(st.o[1]), "+a"(st.o[2]), "+a"(st.o[3]),
+                     "+a"(st.o[4]), "+a"(st.o[5]), "+a"(st.o[6]), "+a"(st.o[7]));
+#pragma unroll
+      for (int db = 0; db < 8; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) st.o[db][e] *= resc;
+    }
+  }
   {
     // next step's K object: (i + 3) % 3
     const int dk = (i + 2) % 3 == 2 ? -65536 : 32768;
 #pragma unroll
     for (int q = 0; q < 8; ++q) st.kb[q] += dk;
   }
-}
-
-// Exact row max of the shifted-free S over the item's keys (QK only, K object
-// b & 1 for block b; block 0 primed by the caller). Returns the row max (log2
-// units) of this lane's row.
-template <bool CAUSAL>
-__device__ __forceinline__ float solo_max(const SoloState& st, const SoloCtx& sc, const SoloLds& L,
-                                       const SoloGeo& g, int nb, int lane) {
-  float m = -INFINITY;
-  for (int b = 0; b < nb; ++b) {
-    fwait_vmcnt<0>();
-    fbarrier();
-    uint16_t* nxt = L.k + ((b + 1) & 1) * (2 * FT);
-    k_tile_load(sc.c, 2 * (b + 1), nxt);
-    k_tile_load(sc.c, 2 * (b + 1) + 1, nxt + FT);
-    const uint32_t ob = (b & 1) * 32768;
-    f32x16 s[2];
-    u32x4 kf[3][2];
-    kf[0][0] = ds_b128<0>(sc.kaddr[0] + ob);
-    kf[0][1] = ds_b128<16384>(sc.kaddr[0] + ob);
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      if (kk < 15) {
-        kf[(kk + 1) % 3][0] = ds_b128<0>(sc.kaddr[(kk + 1) & 7] + ob + 256 * ((kk + 1) >> 3));
-        kf[(kk + 1) % 3][1] = ds_b128<16384>(sc.kaddr[(kk + 1) & 7] + ob + 256 * ((kk + 1) >> 3));
-        lgkm_take<2>(kf[kk % 3][0], kf[kk % 3][1]);
-      } else {
-        lgkm_take<0>(kf[kk % 3][0], kf[kk % 3][1]);
-      }
-      if (kk == 0) {
-        mfma_qk0(s[0], kf[0][0], st.qop[0]);
-        mfma_qk0(s[1], kf[0][1], st.qop[0]);
-      } else {
-        mfma_qk(s[0], kf[kk % 3][0], st.qop[kk]);
-        mfma_qk(s[1], kf[kk % 3][1], st.qop[kk]);
-      }
-    }
-    mfma_drain(s[0], s[1]);
-    if (solo_needs_mask<CAUSAL>(g, b)) solo_mask<CAUSAL>(g, b, lane, s);
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) m = fmaxf(m, s[t][j]);
-  }
-  return xor32_max(m);
 }
 
 // Gate logits of this lane's row, loaded once into AGPRs after the prologue and
@@ -785,12 +762,6 @@ __device__ __forceinline__ void swap_halves(u32x4& v) {
   v.z = a[1];
   v.y = b[0];
   v.w = b[1];
-}
-
-// K blocks 0 and 1 (tiles 0 .. 3) into K objects 0 and 1
-__device__ __forceinline__ void solo_prime(const SoloCtx& sc, const SoloLds& L) {
-#pragma unroll
-  for (int t = 0; t < 4; ++t) k_tile_load(sc.c, t, L.k + t * FT);
 }
 
 // lane (l32, h2): q[row l32][16kk + 8h2 .. +7] and the table floats 8h2 + 16kk + 4u.
@@ -910,8 +881,8 @@ __device__ __forceinline__ void pro_loads(const SoloItem& I, const PrefillArgs& 
 }
 
 // The rest of the item once q, its table rows and `qw` have landed (the caller's
-// wait is tied to `qw`): q norm + RoPE into st.qop, the gate loads, the row-max
-// pass (SHIFT), the pipelined steps. Ends with every load of the workgroup landed
+// wait is tied to `qw`): q norm + RoPE into st.qop, the gate loads, the pipelined
+// steps. Ends with every load of the workgroup landed
 // (vmcnt(0), gates included) and a barrier after which no wave reads the tile
 // objects: all of the LDS is free, and st.o, st.gv, st.lsum hold the result.
 template <bool CAUSAL, bool SHIFT>
@@ -934,22 +905,14 @@ __device__ __forceinline__ void item_run(SoloItem& I, SoloState& st, const Prefi
   st.lsum = 0.f;
 
   const int nb = (sc.c.n_tiles + 1) >> 1;  // step blocks of two tiles
-  float negm = 0.f;
-  if constexpr (SHIFT) {
-    const float mr = solo_max<CAUSAL>(st, sc, L, g, nb, lane);
-    negm = mr == -INFINITY ? 0.f : -mr;  // fully-masked row: P = 0
-    fwait_vmcnt<0>();
-    fbarrier();  // every wave is done with the K objects
-    solo_prime(sc, L);
-  }
-  st.negm = negm;
+  st.negm = 0.f;  // SHIFT: moved by online_max from the first block on
+  st.mrun = -INFINITY;
 
   TileStream kst = k_stream(sc.c, 4), vst = v_stream(sc, 0);
 #pragma unroll
   for (int q = 0; q < 8; ++q) st.kb[q] = sc.kaddr[q];  // step -2 reads K object 0
-  // younger than K block 0 (-2) / 1 (-1): 8 tile loads, and the 16 gate loads
-  // unless the row-max pass has already waited for them
-  constexpr int WG = SHIFT ? 8 : 24;
+  // younger than K block 0 (-2) / 1 (-1): 8 tile loads and the 16 gate loads
+  constexpr int WG = 24;
   solo_step<CAUSAL, SHIFT, 0, true, false, false, false, false, WG>(st, sc, L, g, -2, lane, kst, vst);
   solo_step<CAUSAL, SHIFT, 1, true, true, false, true, false, WG>(st, sc, L, g, -1, lane, kst, vst);
   // step 0 starts O (its first products take a zero accumulator)
@@ -1038,8 +1001,8 @@ __device__ __forceinline__ void wait_q(u32x4 (&qw)[16]) {
 
 // The workgroup's items (one, or a causal pair). SHIFT = false: every logit is
 // within +-64 (log2 units), so P = exp2(S) needs no shift (the normalisation
-// cancels any common scale); SHIFT = true: an exact row-max pass first per item,
-// P = exp2(S - row max). A pair's second item issues its prologue loads as soon
+// cancels any common scale); SHIFT = true: P = exp2(S - m) with m an online row
+// max (online_max). A pair's second item issues its prologue loads as soon
 // as the first item's loop has released the LDS, before the first item's
 // epilogue, which then runs while they are in flight.
 template <bool CAUSAL, bool SHIFT>
