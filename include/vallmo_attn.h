@@ -342,6 +342,26 @@ int vm_linear_add_rms_norm(vm_bf16* y, int64_t y_st, vm_bf16* x, int64_t x_st, c
                            int M, int N, int K, float eps, float offset, void* workspace,
                            size_t workspace_bytes, vm_stream stream);
 
+/* ---- linear! + silu .* mul in one call --------------------------------
+ * No counterpart in the reference as one op: its MLP runs linear! into the
+ * packed bf16 gate-up projection gu and then silu .* mul on it
+ * (src/llm/qwen35.jl:234-243, :249-250 in step!). This does both:
+ *   gu  = W^T x               (W :: (K, 2I) K-major, gate rows 0 .. I-1, up
+ *                              rows I .. 2I-1; x :: (K, N)), rounded to bf16
+ *   mid = silu(gate) .* up    fp32 from the bf16 gate and up, one rounding
+ * for callers that want the bf16 gu never written. At N <= 32 (a decode
+ * batch; K a multiple of 64, aligned columns) the projection runs a stream-K
+ * GEMV whose fp32 partials the silu kernel adds in a fixed order (bitwise
+ * repeatable; the same rounding points as the two calls, the sums in another
+ * order). Otherwise it is linear! + silu .* mul. I a multiple of 8; mid a
+ * 16-byte aligned (I, N) with an element column stride (a multiple of 8);
+ * workspace (256-byte aligned) of vm_linear_silu_mul_workspace_bytes bytes
+ * ((size_t)-1 on a bad shape).                                              */
+size_t vm_linear_silu_mul_workspace_bytes(int I, int N, int K, int64_t ldw, int64_t ldx);
+int vm_linear_silu_mul(vm_bf16* mid, int64_t mid_st, const vm_bf16* x, int64_t ldx,
+                       const vm_bf16* w, int64_t ldw, int I, int N, int K, void* workspace,
+                       size_t workspace_bytes, vm_stream stream);
+
 /* ---- f2: the rest of the decode step (src/llm/qwen35.jl:247-273) --------
  * Matrices are column-major bf16 with an element column stride (a multiple of
  * 8, pointers 16-byte aligned); M, I, D, K multiples of 8.

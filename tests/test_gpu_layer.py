@@ -12,7 +12,7 @@ import torch
 
 from conftest import (D, EPS, HALF, HK, HQ, S, THETA, TOL_MAX, TOL_MEAN, banner, dev_f32,
                       from_dev, i32, maxmean, to_dev)
-from oracle.rng import bf16_to_f32, normal_bf16
+from oracle.rng import bf16_to_f32, f32_to_bf16, normal_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -139,6 +139,81 @@ def test_linear_narrow_misaligned_view(vm, orc):
     mx, mn = maxmean(dev_f32(y), ref)
     print(f"linear misaligned: max {mx:.3e} mean {mn:.3e}")
     assert mx <= TOL_MAX and mn <= TOL_MEAN
+
+
+def _silu_mul_bar(orc, x, W, I):
+    """The oracle's mid (orc.linear's fp32 gate-up rounded to bf16, as the
+    reference stores gu, then orc.silu_mul, rounded) and a per-element bar:
+    mid's own bf16 rounding (2^-7 |mid|, one ulp taken generously) plus what
+    one ulp and the fp32 reassociation of gate and up (2^-7 |g| + 2^-20
+    sum_k |x_k w_k|) move it by through d mid / d g = u silu'(g) and
+    d mid / d u = silu(g)."""
+    gu = f32_to_bf16(orc.linear(x, W))
+    ref = bf16_to_f32(f32_to_bf16(orc.silu_mul(gu))).astype(np.float64)
+    g = bf16_to_f32(gu[:, :I]).astype(np.float64)
+    u = bf16_to_f32(gu[:, I:]).astype(np.float64)
+    sg = 1.0 / (1.0 + np.exp(-g))
+    silu = g * sg
+    xa = np.abs(bf16_to_f32(x).astype(np.float64))
+    wa = np.abs(bf16_to_f32(W).astype(np.float64))
+    ra = xa @ wa.T
+    dg = 2.0 ** -7 * np.abs(g) + 2.0 ** -20 * ra[:, :I]
+    du = 2.0 ** -7 * np.abs(u) + 2.0 ** -20 * ra[:, I:]
+    dsilu = sg * (1.0 + g * (1.0 - sg))
+    bar = 2.0 ** -7 * np.abs(ref) + np.abs(u * dsilu) * dg + np.abs(silu) * du + 1e-30
+    return ref, bar
+
+
+@pytest.mark.parametrize("I,N,K", [(9216, 32, 2560), (9216, 1, 2560), (1000, 20, 640),
+                                   (1024, 7, 512), (512, 40, 256)])
+def test_linear_silu_mul(vm, orc, I, N, K):
+    """linear! + silu .* mul in one call (the MLP's first half, qwen35.jl:234-243):
+    at N <= 32 the stream-K GEMV's fp32 partials summed by the silu kernel (I =
+    9216: the decode step's shape; 1000: row groups past the end of W), at N =
+    40 linear! + silu .* mul. Every element within the bar of the propagated
+    bf16 roundings of gate and up; a second call bitwise equal; a strided mid
+    honoured."""
+    banner(f"linear_silu_mul I={I} N={N} K={K}")
+    x = normal_bf16((N, K), 900 + N + K)
+    W = normal_bf16((2 * I, K), 910 + I, scale=K ** -0.5)
+    xd, Wd = to_dev(x), to_dev(W)
+    ws = torch.empty(vm.linear_silu_mul_workspace_bytes(xd, Wd), dtype=torch.uint8, device="cuda")
+    m1 = torch.empty((N, I), dtype=torch.bfloat16, device="cuda")
+    m2 = torch.empty_like(m1)
+    vm.linear_silu_mul_(m1, xd, Wd, workspace=ws)
+    vm.linear_silu_mul_(m2, xd, Wd, workspace=ws)
+    mw = torch.full((N, I + 16), 3.0, dtype=torch.bfloat16, device="cuda")
+    vm.linear_silu_mul_(mw[:, :I], xd, Wd, workspace=ws)
+    torch.cuda.synchronize()
+    ref, bar = _silu_mul_bar(orc, x, W, I)
+    got = dev_f32(m1).astype(np.float64)
+    worst = float(np.max(np.abs(got - ref) / bar))
+    print(f"linear_silu_mul {I}x{N}x{K}: worst |err|/bar {worst:.3f}, "
+          f"mean |err| {np.abs(got - ref).mean():.2e} (|mid| mean {np.abs(ref).mean():.2e})")
+    assert worst <= 1.0
+    assert torch.equal(m1.view(torch.int16), m2.view(torch.int16))
+    assert torch.equal(mw[:, :I].view(torch.int16), m1.view(torch.int16))
+    assert bool((mw[:, I:] == 3.0).all())
+
+
+def test_linear_silu_mul_misaligned_input(vm, orc):
+    """x one element off 16-byte alignment: the call takes linear! + silu .* mul
+    (within the same bar)."""
+    banner("linear_silu_mul misaligned x")
+    I, N, K = 1024, 8, 512
+    x = normal_bf16((N, K), 930)
+    W = normal_bf16((2 * I, K), 931, scale=K ** -0.5)
+    xb = torch.zeros((N * (K + 8) + 1,), dtype=torch.bfloat16, device="cuda")
+    xv = xb[1:1 + N * (K + 8)].view(N, K + 8)[:, :K]
+    xv.copy_(to_dev(x))
+    Wd = to_dev(W)
+    mid = torch.empty((N, I), dtype=torch.bfloat16, device="cuda")
+    vm.linear_silu_mul_(mid, xv, Wd)
+    torch.cuda.synchronize()
+    ref, bar = _silu_mul_bar(orc, x, W, I)
+    worst = float(np.max(np.abs(dev_f32(mid).astype(np.float64) - ref) / bar))
+    print(f"misaligned: worst |err|/bar {worst:.3f}")
+    assert worst <= 1.0
 
 
 def test_linear_first_call_captured_then_tuned(vm, orc):

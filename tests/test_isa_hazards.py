@@ -1,6 +1,7 @@
 """Hazards the compiler cannot see, checked on the compiled gfx950 ISA (CPU only).
 
-The fused prefill kernel issues its LDS reads and its MFMAs from inline asm:
+The fused prefill kernel issues its LDS reads and its MFMAs from inline asm (the
+lm head and the GEMVs of step.hip their LDS reads):
   * an asm output is taken to be ready at the asm statement, so the compiler may
     copy, spill or overwrite a load's destination before the data has landed;
   * the compiler inserts no wait states after an asm MFMA, so a VALU read of its
@@ -207,6 +208,23 @@ def test_fused_prefill_lds_reuse_waits_for_tile_loads_before_its_barrier(fused_a
         drains = [j for j in range(last_dma + 1, bar) if re.match(r"s_waitcnt vmcnt\(0\)", body[j])]
         assert drains, f"no vmcnt(0) between the last tile load (line {last_dma}) and the barrier at {bar}"
     assert restarts >= 1, "no LDS restart found (the pair's second item or the row-max re-prime)"
+
+
+@pytest.fixture(scope="module")
+def step_asm():
+    return build_asm("step.hip")
+
+
+def test_step_kernels_no_async_or_mfma_hazard(step_asm):
+    """The lm head, the split-K GEMV and the stream-K GEMV issue their LDS
+    operand reads from asm too: the same check over every kernel of step.hip."""
+    ks = kernels(step_asm)
+    for want in ("lm_head_split_kernel", "gemv_kernel", "gemv_sk_kernel", "silu_mul_sk_kernel"):
+        assert any(want in k for k in ks), want
+    for name, body in ks.items():
+        bad = check(body)
+        assert not bad, name + ":\n" + "\n".join(
+            f"{kind}: '{line}' touches {what}" for kind, line, what in bad[:20])
 
 
 def test_checker_flags_a_read_before_its_wait():

@@ -116,6 +116,9 @@ _SIGS = {
     "vm_linear_plan_state": (_c_i, [_c_i, _c_i, _c_i, _c_i64, _c_i64, _c_i64]),
     "vm_linear": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i, _c_i, _c_i, _p, _c_sz, _p]),
     "vm_rms_norm": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i, _c_i, _c_f, _c_f, _p]),
+    "vm_linear_silu_mul_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i64, _c_i64]),
+    "vm_linear_silu_mul": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i, _c_i, _c_i, _p, _c_sz,
+                                  _p]),
     "vm_linear_add_rms_norm_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i64, _c_i64]),
     "vm_linear_add_rms_norm": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _p, _c_i64, _p, _c_i,
                                       _c_i, _c_i, _c_f, _c_f, _p, _c_sz, _p]),

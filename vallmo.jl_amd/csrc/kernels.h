@@ -246,6 +246,47 @@ struct GemvPlan {
 };
 GemvPlan gemv_plan(int M, int K, int waves);
 size_t gemv_workspace_bytes(int M, int K);
+
+// Stream-K GEMV for wide weights at N <= 32 (step.hip): y = W^T x as fp32
+// partials, one 16 KB slot per (workgroup, 128-row group) it touches; the
+// consumer adds a row's slots in workgroup order (gemv_sk_sum4).
+struct GemvSkPlan {
+  int G;      // 64-k groups of K
+  int RG;     // 128-row groups of M
+  int U;      // units = RG * G
+  int chunk;  // units per workgroup
+  int nwg;    // workgroups
+};
+struct GemvSkArgs {
+  const uint16_t* w;    // (K, M) K-major: row m of W^T at w + m * w_st
+  int64_t w_st;
+  const uint16_t* x;    // (K, N): column n at x + n * x_st
+  int64_t x_st;
+  float* part;          // slots [nwg + RG - 1][4 tiles][32 columns][32 rows]
+  int M, N, K;
+  GemvSkPlan p;
+};
+GemvSkPlan gemv_sk_plan(int M, int K);
+size_t gemv_sk_workspace_bytes(int M, int K);
+hipError_t launch_gemv_sk(const GemvSkArgs& a, hipStream_t st);
+// mid = silu(bf16(g)) .* bf16(u) from the stream-K partials of the packed
+// gate-up projection (gate rows 0 .. I-1, up rows I .. 2I-1)
+struct SiluMulSkArgs {
+  uint16_t* mid;
+  int64_t mid_st;
+  const float* part;
+  int I, N;
+  GemvSkPlan p;
+};
+hipError_t launch_silu_mul_sk(const SiluMulSkArgs& a, hipStream_t st);
+// linear! + silu .* mul (linear.cpp): mid (I, N) from x (K, N) and the packed
+// gate-up W (K, 2I); the stream-K GEMV + silu_mul_sk_kernel at N <= 32, else
+// linear! into a bf16 gu in the workspace and silu_mul_kernel
+int linear_silu_mul_workspace(int I, int N, int K, int64_t ldw, int64_t ldx, size_t* bytes,
+                              char* err, size_t errn);
+int linear_silu_mul_run(uint16_t* mid, int64_t mid_st, const uint16_t* x, int64_t ldx,
+                        const uint16_t* w, int64_t ldw, int I, int N, int K, void* workspace,
+                        size_t workspace_bytes, hipStream_t st, char* err, size_t errn);
 hipError_t launch_gemv(GemvArgs a, hipStream_t st);
 // the split GEMV without its reduce: leaves the slices' fp32 partials in
 // a.part (layout [S2][32][M]); returns the plan through *plan

@@ -478,4 +478,92 @@ int linear_add_norm_run(uint16_t* yn, int64_t yn_st, uint16_t* x, int64_t x_st, 
   return VM_OK;
 }
 
+// ---- linear! + silu .* mul (the MLP's gate-up half, qwen35.jl:234-243) -------
+namespace {
+// the stream-K path: a decode batch, whole 64-k groups, aligned columns
+bool sk_shape(int M, int N, int K, int64_t ldw, int64_t ldx) {
+  return N >= 1 && N <= 32 && K > 0 && K % 64 == 0 && M % 8 == 0 && ldw % 8 == 0 && ldx % 8 == 0;
+}
+}  // namespace
+
+int linear_silu_mul_workspace(int I, int N, int K, int64_t ldw, int64_t ldx, size_t* bytes,
+                              char* err, size_t errn) {
+  const int M = 2 * I;
+  if (sk_shape(M, N, K, ldw, ldx)) {
+    // the stream-K partials; a misaligned view takes the two-call path below
+    // in the same workspace
+    size_t lin = 0;
+    const int rc = linear_workspace(M, N, K, ldw, ldx, M, &lin, err, errn);
+    const size_t two = rc == VM_OK ? round256(lin) + round256((size_t)M * N * sizeof(uint16_t)) : 0;
+    *bytes = std::max(round256(gemv_sk_workspace_bytes(M, K)), two);
+    return VM_OK;
+  }
+  size_t lin = 0;
+  const int rc = linear_workspace(M, N, K, ldw, ldx, M, &lin, err, errn);
+  if (rc != VM_OK) return rc;
+  *bytes = round256(lin) + round256((size_t)M * N * sizeof(uint16_t));
+  return VM_OK;
+}
+
+int linear_silu_mul_run(uint16_t* mid, int64_t mid_st, const uint16_t* x, int64_t ldx,
+                        const uint16_t* w, int64_t ldw, int I, int N, int K, void* workspace,
+                        size_t workspace_bytes, hipStream_t st, char* err, size_t errn) {
+  const int M = 2 * I;
+  size_t need = 0;
+  int rc = linear_silu_mul_workspace(I, N, K, ldw, ldx, &need, err, errn);
+  if (rc != VM_OK) return rc;
+  if (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 256 != 0) {
+    snprintf(err, errn,
+             "linear_silu_mul: workspace of %zu bytes (256-byte aligned) < %zu required "
+             "(vm_linear_silu_mul_workspace_bytes)", workspace_bytes, need);
+    return VM_E_SCRATCH;
+  }
+  if (sk_shape(M, N, K, ldw, ldx) && (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0) {
+    GemvSkArgs g{};
+    g.w = w;
+    g.w_st = ldw;
+    g.x = x;
+    g.x_st = ldx;
+    g.part = static_cast<float*>(workspace);
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.p = gemv_sk_plan(M, K);
+    SiluMulSkArgs a{};
+    a.mid = mid;
+    a.mid_st = mid_st;
+    a.part = g.part;
+    a.I = I;
+    a.N = N;
+    a.p = g.p;
+    hipError_t e = launch_gemv_sk(g, st);
+    if (e == hipSuccess) e = launch_silu_mul_sk(a, st);
+    if (e != hipSuccess) {
+      snprintf(err, errn, "linear_silu_mul: %s", hipGetErrorString(e));
+      return (int)e;
+    }
+    return VM_OK;
+  }
+  // linear! into a bf16 gu after the plan's own space, then silu .* mul
+  size_t lin = 0;
+  rc = linear_workspace(M, N, K, ldw, ldx, M, &lin, err, errn);
+  if (rc != VM_OK) return rc;
+  uint16_t* gu = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + round256(lin));
+  rc = linear_run(gu, M, x, ldx, w, ldw, M, N, K, workspace, lin, st, err, errn);
+  if (rc != VM_OK) return rc;
+  SiluMulArgs a{};
+  a.mid = mid;
+  a.mid_st = mid_st;
+  a.gu = gu;
+  a.gu_st = M;
+  a.I = I;
+  a.N = N;
+  const hipError_t e = launch_silu_mul(a, st);
+  if (e != hipSuccess) {
+    snprintf(err, errn, "linear_silu_mul: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  return VM_OK;
+}
+
 }  // namespace vm

@@ -594,6 +594,172 @@ hipError_t launch_gemv(GemvArgs a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// ---- y = W^T x for the wide decode projections (N <= 32 batch columns, M of
+// thousands of rows), stream-K over the weight: the unit of work is one 64-k
+// group of one 128-row group of W (16 KB), numbered row-group-major. Workgroup
+// b takes units [b chunk, (b + 1) chunk); its wave v computes the 32-row tile
+// 4 rg + v of each unit, so the four waves share the unit's batch tile (32
+// columns x 64 k, 4 KB), each DMAing a quarter of it into the workgroup's slot.
+// The batch tile then costs a quarter of the weight bytes in L2 traffic (the
+// narrow kernel above loads one per one or two weight tiles, which is what
+// keeps it from the streaming rate at these sizes). Tiles stream through LDS
+// by 1-KB direct loads, one barrier per unit; a unit's slot is refilled after
+// the next barrier, once every wave has read it. A workgroup writes one fp32
+// partial per row group it touches into slot (b + rg); the consumer adds a
+// row's slots in workgroup order, so results are bitwise repeatable.
+constexpr int SK_NB = 4;   // ring slots per wave (three units in flight)
+constexpr int SK_TE = 2048;  // bf16 of one staged 32 x 64 tile (4 KB)
+
+namespace {
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemv_sk_kernel(GemvSkArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t wring[4][SK_NB][SK_TE];
+  __shared__ __attribute__((aligned(16))) uint16_t xring[SK_NB][SK_TE];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int G = a.p.G;
+  const int u0 = blockIdx.x * a.p.chunk;
+  if (u0 >= a.p.U) return;  // the whole workgroup
+  const int u1 = min(u0 + a.p.chunk, a.p.U);
+  const int n = u1 - u0;
+  // unit u into ring slot s: this wave's weight tile (4 loads) and rows
+  // 8 wv .. 8 wv + 7 of the batch tile (1 load; the batch stays in L2, so the
+  // default cache policy)
+  auto issue = [&](int u, int s) __attribute__((always_inline)) {
+    const int rg = u / G, g = u - rg * G;
+    lm_dma_tile(wring[wv][s], a.w, a.w_st, 32 * (4 * rg + wv), a.M, 64 * g, lane);
+    const int c = 8 * wv + (lane >> 3), p = lane & 7;
+    const uint16_t* src = a.x + (int64_t)min(c, a.N - 1) * a.x_st + 64 * g + 8 * (p ^ (c & 7));
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(&xring[s][512 * wv]),
+                                     16, 0, 0);
+  };
+  int issued = 0;
+  for (; issued < SK_NB - 1 && issued < n; ++issued) issue(u0 + issued, issued);
+  f32x16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  int rcur = u0 / G;
+  // this wave's partial of row group rg: lane (j, h) holds batch column j at
+  // rows 8 q + 4 h .. +3 of the tile (the 32x32x16 MFMA's D layout)
+  auto flush = [&](int rg) __attribute__((always_inline)) {
+    float* dst = a.part + (((int64_t)(blockIdx.x + rg) * 4 + wv) * 32 + j) * 32 + 4 * h;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<float4*>(dst + 8 * q) =
+          make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+  };
+  for (int i = 0; i < n; ++i) {
+    // this wave's loads of unit i are in (loads retire in order; the partial
+    // stores issued later only make the count conservative), then every
+    // wave's: the barrier also tells that unit i - 1's slot is read
+    if (issued - i - 1 >= SK_NB - 2) wait_vmcnt<5 * (SK_NB - 2)>(); else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    if (issued < n) {
+      issue(u0 + issued, issued % SK_NB);
+      ++issued;
+    }
+    const int s = i % SK_NB;
+    const int rg = (u0 + i) / G;
+    if (rg != rcur) {
+      flush(rcur);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+      rcur = rg;
+    }
+    // operands from asm reads (a compiler-visible read would first drain every
+    // load in flight), released by one counted wait tied to their registers
+    lm_u32x4 wa[4], xb[4];
+    const uint32_t wbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)wring[wv][s];
+    const uint32_t xbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)xring[s];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const uint32_t off = 2u * (uint32_t)(64 * j + 8 * ((2 * st + h) ^ (j & 7)));
+      asm volatile("ds_read_b128 %0, %1" : "=v"(wa[st]) : "v"(wbase + off));
+      asm volatile("ds_read_b128 %0, %1" : "=v"(xb[st]) : "v"(xbase + off));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int st = 0; st < 4; ++st) asm volatile("" : "+v"(wa[st]), "+v"(xb[st]));
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+      acc = mfma32(__builtin_bit_cast(uint4, wa[st]), __builtin_bit_cast(uint4, xb[st]), acc);
+  }
+  flush(rcur);
+}
+
+// rows m .. m + 3 (m % 4 == 0, m < M) of batch column n: the partials of row
+// group m / 128, added in workgroup order
+__device__ __forceinline__ float4 gemv_sk_sum4(const float* part, const GemvSkPlan& p, int m,
+                                               int n) {
+  const int rg = m >> 7, v = (m >> 5) & 3, r = m & 31;
+  const int wf = (rg * p.G) / p.chunk, wl = ((rg + 1) * p.G - 1) / p.chunk;
+  const float* src = part + ((int64_t)(wf + rg) * 4 + v) * 1024 + n * 32 + r;
+  float4 s = *reinterpret_cast<const float4*>(src);
+#pragma unroll 4
+  for (int w = wf + 1; w <= wl; ++w) {
+    src += 4096;  // the next workgroup's slot of the same row group
+    const float4 t = *reinterpret_cast<const float4*>(src);
+    s.x += t.x;
+    s.y += t.y;
+    s.z += t.z;
+    s.w += t.w;
+  }
+  return s;
+}
+
+// ---- mid = silu(gate) .* up (qwen35.jl:237-239) from the gate-up projection's
+// stream-K partials: gate and up rounded to bf16 first, as the reference stores
+// them in gu, then one fp32 evaluation and one rounding, as silu_mul_kernel.
+__global__ __launch_bounds__(RT) void silu_mul_sk_kernel(SiluMulSkArgs a) {
+  const int nc = a.I / 8;
+  const int64_t idx = (int64_t)blockIdx.x * RT + threadIdx.x;
+  if (idx >= (int64_t)nc * a.N) return;
+  const int n = (int)(idx / nc), i = 8 * (int)(idx % nc);
+  const float4 g0 = gemv_sk_sum4(a.part, a.p, i, n), g1 = gemv_sk_sum4(a.part, a.p, i + 4, n);
+  const float4 u0 = gemv_sk_sum4(a.part, a.p, a.I + i, n);
+  const float4 u1 = gemv_sk_sum4(a.part, a.p, a.I + i + 4, n);
+  const float g8[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+  const float u8[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+  float gf[8], uf[8], m[8];
+  unpack8(pack8(g8), gf);
+  unpack8(pack8(u8), uf);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) m[k] = gf[k] / (1.0f + __expf(-gf[k])) * uf[k];
+  *reinterpret_cast<uint4*>(a.mid + (int64_t)n * a.mid_st + i) = pack8(m);
+}
+
+}  // namespace
+
+GemvSkPlan gemv_sk_plan(int M, int K) {
+  GemvSkPlan p;
+  p.G = K / 64;
+  p.RG = (M + 127) / 128;
+  p.U = p.RG * p.G;
+  const int wgs = max(1, lm_head_waves() / 4);  // one workgroup per CU
+  p.chunk = max(1, (p.U + wgs - 1) / wgs);
+  p.nwg = p.U > 0 ? (p.U + p.chunk - 1) / p.chunk : 0;
+  return p;
+}
+
+size_t gemv_sk_workspace_bytes(int M, int K) {
+  const GemvSkPlan p = gemv_sk_plan(M, K);
+  return p.U > 0 ? (size_t)(p.nwg + p.RG - 1) * 4 * 1024 * sizeof(float) : 0;
+}
+
+hipError_t launch_gemv_sk(const GemvSkArgs& a, hipStream_t st) {
+  if (a.p.U == 0 || a.N == 0) return hipSuccess;
+  hipLaunchKernelGGL(gemv_sk_kernel, dim3(a.p.nwg), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_sk(const SiluMulSkArgs& a, hipStream_t st) {
+  const int64_t n = (int64_t)(a.I / 8) * a.N;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(silu_mul_sk_kernel, dim3((unsigned)((n + RT - 1) / RT)), dim3(RT), 0, st, a);
+  return hipGetLastError();
+}
+
 // One workgroup per batch column: the best of the NW partials (ties to the
 // smallest index), stored 1-based.
 __global__ __launch_bounds__(256) void lm_head_combine_kernel(LmHeadArgs a) {

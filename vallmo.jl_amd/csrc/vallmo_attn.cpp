@@ -1085,6 +1085,30 @@ int vm_linear_add_rms_norm(vm_bf16* y, int64_t y_st, vm_bf16* x, int64_t x_st, c
                                  workspace, workspace_bytes, S(st), g_err, sizeof g_err);
 }
 
+// ---- linear! + the MLP's silu .* mul in one call -----------------------------
+size_t vm_linear_silu_mul_workspace_bytes(int I, int N, int K, int64_t ldw, int64_t ldx) {
+  if (I <= 0 || I % 8 != 0 || linear_check(2 * I, N, K, ldw, ldx, 2 * (int64_t)I) != VM_OK)
+    return (size_t)-1;
+  size_t n = 0;
+  if (vm::linear_silu_mul_workspace(I, N, K, ldw, ldx, &n, g_err, sizeof g_err) != VM_OK)
+    return (size_t)-1;
+  return n;
+}
+
+int vm_linear_silu_mul(vm_bf16* mid, int64_t mid_st, const vm_bf16* x, int64_t ldx,
+                       const vm_bf16* w, int64_t ldw, int I, int N, int K, void* workspace,
+                       size_t workspace_bytes, vm_stream st) {
+  REQUIRE(I > 0 && I % 8 == 0, VM_E_UNSUPPORTED, "linear_silu_mul: I = %d (a multiple of 8)", I);
+  TRY(linear_check(2 * I, N, K, ldw, ldx, 2 * (int64_t)I));
+  TRY(check_aligned(mid, "mid"));
+  TRY(check_stride(mid_st, "mid_st"));
+  REQUIRE(N <= 1 || mid_st >= I, VM_E_DIM, "linear_silu_mul: mid column stride %lld below I = %d",
+          (long long)mid_st, I);
+  REQUIRE(x && w, VM_E_ARG, "linear_silu_mul: NULL pointer argument");
+  return vm::linear_silu_mul_run(mid, mid_st, x, ldx, w, ldw, I, N, K, workspace, workspace_bytes,
+                                 S(st), g_err, sizeof g_err);
+}
+
 // ---- synthetic inputs ------------------------------------------------------
 int vm_fill_normal_bf16(vm_bf16* dst, int64_t n, uint64_t seed, float scale, float shift,
                         vm_stream st) {

@@ -102,6 +102,7 @@ class Model:
         if self._ws_need is None:
             l0 = self.layers[0]
             need = max(ops.linear_workspace_bytes(self.xn, l0.Wgu, self.gu),
+                       ops.linear_silu_mul_workspace_bytes(self.xn, l0.Wgu),
                        ops.linear_workspace_bytes(self.mid, l0.Wd, self.h),
                        ops.linear_add_rms_norm_workspace_bytes(self.mid, l0.Wd))
             if self.dn_layers:
@@ -245,9 +246,9 @@ def step_(m: Model, gen: Generation):
         o, W_out = _mixer_decode(l, m, gen, xn)
         ops.linear_add_rms_norm_({"Y": xn, "X": x}, o, W_out, l.norm2, eps=eps, offset=1.0,
                                  workspace=ws)
-        # the MLP (mlp!, :234-243), its down projection fused with the next norm
-        ops.linear_({"y": m.gu}, xn, l.Wgu, workspace=ws)
-        ops.silu_mul_(m.mid, m.gu)
+        # the MLP (mlp!, :234-243): the gate-up projection and silu .* mul in one
+        # call (gu never written), the down projection fused with the next norm
+        ops.linear_silu_mul_(m.mid, xn, l.Wgu, workspace=ws)
         next_w = m.norm_w if i == n - 1 else m.layers[i + 1].norm1
         ops.linear_add_rms_norm_({"Y": xn, "X": x}, m.mid, l.Wd, next_w, eps=eps, offset=1.0,
                                  workspace=ws)

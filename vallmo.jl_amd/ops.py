@@ -334,6 +334,37 @@ def linear_add_rms_norm_(outs, a, W, norm_w, *, eps, offset, workspace=None):
     return outs
 
 
+def linear_silu_mul_workspace_bytes(x, W) -> int:
+    """Workspace of linear_silu_mul_ for this problem."""
+    M, K, N = W.shape[0], x.shape[-1], _rows(x)
+    _tune(M, N, K, W.stride(0), _ld(x), M)  # the two-call path's plan (N > 32)
+    n = _lib.load().vm_linear_silu_mul_workspace_bytes(M // 2, N, K, W.stride(0), _ld(x))
+    if n == ctypes.c_size_t(-1).value:
+        _lib.check(_lib.VM_E_UNSUPPORTED, "vm_linear_silu_mul_workspace_bytes")
+    return int(n)
+
+
+def linear_silu_mul_(mid, x, W, *, workspace=None):
+    """linear! then silu .* mul in one call (the MLP's first half,
+    src/llm/qwen35.jl:234-243): gu = bf16(W^T x), mid = bf16(silu(gate) .* up).
+    x :: (K, N), W :: (K, 2I) K-major (torch (2I, K)), gate rows first; mid ::
+    (I, N) (torch (..., I)). No reference counterpart as one op: at N <= 32 the
+    projection's fp32 partials go straight to the silu kernel, gu is never
+    written."""
+    I, N, ms = _cols(mid, "mid")
+    K, Nx, xs = _cols(x, "x")
+    if W.dim() != 2 or tuple(W.shape) != (2 * I, K) or Nx != N:
+        raise DimensionMismatch(f"linear_silu_mul: x ({K}, {Nx}), W {tuple(W.shape)}, "
+                                f"mid ({I}, {N}): expected W (2I, K) = ({2 * I}, {K})")
+    _need(W, torch.bfloat16, "W")
+    need = linear_silu_mul_workspace_bytes(x, W)
+    if workspace is None:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+    call("vm_linear_silu_mul", _p(mid), ms, _p(x), xs, _p(W), W.stride(0), I, N, K,
+         _p(workspace), workspace.numel(), _stream())
+    return mid
+
+
 def _cols(t, name, M=None):
     """(M, N, column stride) of the reference's column-major (M, N) view of a
     torch (..., M) bf16 tensor."""
