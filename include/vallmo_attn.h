@@ -362,6 +362,32 @@ int vm_linear_silu_mul(vm_bf16* mid, int64_t mid_st, const vm_bf16* x, int64_t l
                        const vm_bf16* w, int64_t ldw, int I, int N, int K, void* workspace,
                        size_t workspace_bytes, vm_stream stream);
 
+/* ---- linear! + causal_conv1d! in one call -------------------------------
+ * No counterpart in the reference as one op: the DeltaNet layer's decode step
+ * runs linear! into its packed projection [q k v | z | alpha beta] and then
+ * causal_conv1d! on the first D channels (src/llm/qwen35.jl:212-223). This does
+ * both:
+ *   y = bf16(W^T x)   W :: (K, M) K-major, x :: (K, N), y :: (M, N) (every
+ *                     channel written, as linear! leaves it)
+ *   causal_conv1d!((; Y, S'), y[1:D, :], S, Weight, Bias; sigma) as
+ *                     vm_causal_conv1d (yc = Y, s_in/s_out = S/S', the ring
+ *                     strides, conv_w = Weight, conv_b = Bias or NULL, Kc its
+ *                     kernel size, act = 1 for silu)
+ * At N <= 32 (a decode batch; K a multiple of 64, aligned columns) the
+ * projection runs a stream-K GEMV whose fp32 partials the conv kernel adds in a
+ * fixed order (bitwise repeatable; the same rounding points as the two calls,
+ * the sums in another order); otherwise it is linear! + causal_conv1d!. M and
+ * D multiples of 8, D <= M; workspace (256-byte aligned) of
+ * vm_linear_causal_conv1d_workspace_bytes bytes ((size_t)-1 on a bad shape). */
+size_t vm_linear_causal_conv1d_workspace_bytes(int M, int N, int K, int64_t ldw, int64_t ldx,
+                                               int64_t ldy);
+int vm_linear_causal_conv1d(vm_bf16* y, int64_t ldy, const vm_bf16* x, int64_t ldx,
+                            const vm_bf16* w, int64_t ldw, int M, int N, int K, vm_bf16* yc,
+                            int64_t yc_sb, const vm_bf16* s_in, vm_bf16* s_out, int64_t s_cs,
+                            int64_t s_sb, const vm_bf16* conv_w, int64_t conv_w_cs,
+                            const vm_bf16* conv_b, int D, int Kc, int act, void* workspace,
+                            size_t workspace_bytes, vm_stream stream);
+
 /* ---- f2: the rest of the decode step (src/llm/qwen35.jl:247-273) --------
  * Matrices are column-major bf16 with an element column stride (a multiple of
  * 8, pointers 16-byte aligned); M, I, D, K multiples of 8.

@@ -62,6 +62,53 @@ def test_conv1d_update(vm, orc, B, bias, act):
     assert_bf16_close(dev_f32(out["Y"]), y_ref, "conv1d update")
 
 
+def _narrow_bar(x, W, ref):
+    """One bf16 ulp (2^-8 |y|) plus fp32 reassociation (2^-20 sum_k |x_k w_k|)."""
+    xa = np.abs(bf16_to_f32(x).astype(np.float64))
+    wa = np.abs(bf16_to_f32(W).astype(np.float64))
+    return 2.0 ** -8 * np.abs(ref) + 2.0 ** -20 * (xa @ wa.T) + 1e-30
+
+
+@pytest.mark.parametrize("B,Kdim,bias", [(32, 2560, False), (1, 2560, True), (5, 640, True),
+                                         (40, 256, False)])
+def test_linear_causal_conv1d(vm, orc, B, Kdim, bias):
+    """linear! + causal_conv1d! in one call (the DeltaNet layer's decode step,
+    qwen35.jl:212-223) at the Qwen3.5 shape: W_in 12352 x K, the conv on the first
+    8192 channels, the ring in place. The projection within one bf16 ulp plus
+    fp32 reassociation of the oracle's; the conv output and ring equal to the
+    oracle's conv step on that bf16 projection (bit-exact ring); a second call
+    from the same ring bitwise equal. B = 40 is linear! + causal_conv1d!."""
+    banner(f"linear_causal_conv1d B={B} K={Kdim} bias={bias}")
+    M = NCH + HV * DV + 2 * HV
+    x = normal_bf16((B, Kdim), 940 + B)
+    W = normal_bf16((M, Kdim), 941, scale=Kdim ** -0.5)
+    ring = normal_bf16((B, KC, NCH), 942 + B)
+    w = normal_bf16((KC, NCH), 943, scale=0.5)
+    b = normal_bf16((NCH,), 944, scale=0.1) if bias else None
+    xd, Wd, wd = to_dev(x), to_dev(W), to_dev(w)
+    bd = None if b is None else to_dev(b)
+    outs = []
+    for _ in range(2):
+        S = to_dev(ring)
+        y = torch.empty((B, M), dtype=torch.bfloat16, device="cuda")
+        Y = torch.empty((B, NCH), dtype=torch.bfloat16, device="cuda")
+        vm.linear_causal_conv1d_({"y": y, "Y": Y, "Sp": S}, xd, Wd, S, wd, bd, sigma="silu")
+        outs.append((y, Y, S))
+    torch.cuda.synchronize()
+    y, Y, S = outs[0]
+    ref = orc.linear(x, W).astype(np.float64)
+    got = dev_f32(y).astype(np.float64)
+    worst = float(np.max(np.abs(got - ref) / _narrow_bar(x, W, ref)))
+    print(f"projection: worst |err| / bar = {worst:.3f}")
+    assert worst <= 1.0
+    yb = from_dev(y)
+    y_ref, ring_ref = orc.conv1d_update(yb[:, :NCH], ring, w, b, act=True)
+    assert np.array_equal(from_dev(S), ring_ref)
+    assert_bf16_close(dev_f32(Y), y_ref, "conv of the projection")
+    for t0, t1 in zip(outs[0], outs[1]):
+        assert torch.equal(t0.view(torch.int16), t1.view(torch.int16))
+
+
 def test_conv1d_update_chain_equals_sequence(vm, orc):
     """T decode steps from a zero ring == one sequence run (rows and ring)."""
     banner("conv1d update chain == sequence")

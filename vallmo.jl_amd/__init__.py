@@ -23,6 +23,7 @@ from .ops import (attention, attention_, decode_attention, decode_attention_,  #
                   deltanet_sequence, deltanet_sequence_, deltanet_prefill_prep_, gated_rms_norm_,
                   linear_add_rms_norm_, linear_add_rms_norm_workspace_bytes,
                   linear_silu_mul_, linear_silu_mul_workspace_bytes,
+                  linear_causal_conv1d_, linear_causal_conv1d_workspace_bytes,
                   deltanet_sequence_chunked_, deltanet_sequence_workspace_bytes)
 from .layer import (AttnConfig, AttnLayer, AttnModel, CaptureSession, Generation,  # noqa: F401
                     StagedV, attn_layer, decode_, forward, gated_attn_decode_, gated_attn_prefill)

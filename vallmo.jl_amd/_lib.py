@@ -116,6 +116,10 @@ _SIGS = {
     "vm_linear_plan_state": (_c_i, [_c_i, _c_i, _c_i, _c_i64, _c_i64, _c_i64]),
     "vm_linear": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i, _c_i, _c_i, _p, _c_sz, _p]),
     "vm_rms_norm": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i, _c_i, _c_f, _c_f, _p]),
+    "vm_linear_causal_conv1d_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i64, _c_i64, _c_i64]),
+    "vm_linear_causal_conv1d": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i, _c_i, _c_i, _p,
+                                       _c_i64, _p, _p, _c_i64, _c_i64, _p, _c_i64, _p, _c_i,
+                                       _c_i, _c_i, _p, _c_sz, _p]),
     "vm_linear_silu_mul_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i64, _c_i64]),
     "vm_linear_silu_mul": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i, _c_i, _c_i, _p, _c_sz,
                                   _p]),

@@ -213,4 +213,26 @@ __device__ __forceinline__ void store_row4(uint16_t* p, int lane, const float x[
   *reinterpret_cast<uint2*>(p + 4 * lane) = v;
 }
 
+// Rows m .. m + 3 (m % 4 == 0) of batch column n of a stream-K GEMV's result
+// (step.hip, gemv_sk_kernel; G 64-k groups, chunk units per workgroup): the
+// partials of row group m / 128, one 16 KB slot per workgroup that touched it
+// ([4 tiles][32 columns][32 rows] fp32, slot = workgroup + row group), added
+// in workgroup order.
+__device__ __forceinline__ float4 gemv_sk_sum4(const float* part, int G, int chunk, int m, int n) {
+  const int rg = m >> 7, v = (m >> 5) & 3, r = m & 31;
+  const int wf = (rg * G) / chunk, wl = ((rg + 1) * G - 1) / chunk;
+  const float* src = part + ((int64_t)(wf + rg) * 4 + v) * 1024 + n * 32 + r;
+  float4 s = *reinterpret_cast<const float4*>(src);
+#pragma unroll 4
+  for (int w = wf + 1; w <= wl; ++w) {
+    src += 4096;  // the next workgroup's slot of the same row group
+    const float4 t = *reinterpret_cast<const float4*>(src);
+    s.x += t.x;
+    s.y += t.y;
+    s.z += t.z;
+    s.w += t.w;
+  }
+  return s;
+}
+
 }  // namespace vm

@@ -740,6 +740,55 @@ __global__ __launch_bounds__(256) void conv1d_update_kernel(Conv1dArgs a) {
   *reinterpret_cast<uint4*>(a.y + b * a.y_sb + d) = pack8(acc);
 }
 
+// ---- linear! + causal_conv1d! (the decode step's in-projection and conv,
+// qwen35.jl:212-223) from the projection's stream-K partials (gemv_sk_kernel,
+// step.hip): thread = 8 channels of one sequence. Each thread adds its rows'
+// partials in workgroup order, stores them rounded to bf16 as the projection's
+// output (every channel: the conv's input, z, alpha, beta), and for the first
+// D channels runs the conv step of conv1d_update_kernel on that bf16 input.
+template <int K>
+__global__ __launch_bounds__(256) void conv1d_update_sk_kernel(Conv1dSkArgs a) {
+  const Conv1dArgs& c = a.c;
+  const int64_t c8 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (c8 * 8 >= a.M) return;
+  const int d = (int)c8 * 8;
+  const float4 lo = gemv_sk_sum4(a.part, a.G, a.chunk, d, b);
+  const float4 hi = gemv_sk_sum4(a.part, a.G, a.chunk, d + 4, b);
+  const float s8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  const uint4 xr = pack8(s8);
+  *reinterpret_cast<uint4*>(a.yp + b * a.yp_sb + d) = xr;
+  if (d >= c.D) return;
+  uint4 raw[K];
+#pragma unroll
+  for (int i = 0; i < K - 1; ++i)
+    raw[i] = *reinterpret_cast<const uint4*>(c.s_in + b * c.s_sb + (int64_t)(i + 1) * c.s_cs + d);
+  raw[K - 1] = xr;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    float v[8], wf[8];
+    unpack8(raw[i], v);
+    unpack8(*reinterpret_cast<const uint4*>(c.w + (int64_t)i * c.w_cs + d), wf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += v[e] * wf[e];
+  }
+#pragma unroll
+  for (int i = 0; i < K; ++i)
+    *reinterpret_cast<uint4*>(c.s_out + b * c.s_sb + (int64_t)i * c.s_cs + d) = raw[i];
+  if (c.bias) {
+    float bf8[8];
+    unpack8(*reinterpret_cast<const uint4*>(c.bias + d), bf8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += bf8[e];
+  }
+  if (c.act) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = accurate_silu(acc[e]);
+  }
+  *reinterpret_cast<uint4*>(c.y + b * c.y_sb + d) = pack8(acc);
+}
+
 // ---- causal_conv1d_sequence! (causal_conv1d.jl:73-149): thread = 8 channels x
 // a run of CONV_TC tokens of one sequence, the window of the last K inputs in
 // registers. The left context of token 0 is the ring's columns 2..K (s_in:
@@ -879,6 +928,19 @@ hipError_t launch_conv1d_update(const Conv1dArgs& a, hipStream_t st) {
   switch (a.K) {
 #define X(k) \
   case k: hipLaunchKernelGGL(conv1d_update_kernel<k>, grid, dim3(256), 0, st, a); break;
+    VM_CONV_K_CASES(X)
+#undef X
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_conv1d_update_sk(const Conv1dSkArgs& a, hipStream_t st) {
+  if (a.c.B == 0 || a.M == 0) return hipSuccess;
+  const dim3 grid((unsigned)((a.M / 8 + 255) / 256), a.c.B);
+  switch (a.c.K) {
+#define X(k) \
+  case k: hipLaunchKernelGGL(conv1d_update_sk_kernel<k>, grid, dim3(256), 0, st, a); break;
     VM_CONV_K_CASES(X)
 #undef X
     default: return hipErrorInvalidValue;

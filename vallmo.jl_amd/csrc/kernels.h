@@ -361,6 +361,25 @@ struct Conv1dArgs {
   const uint16_t* bias;
   int D, K, T, B, act;
 };
+// causal_conv1d! on the first D channels of a projection given as stream-K
+// partials (gemv_sk_kernel): the projection's M channels are written rounded to
+// bf16 at yp (column stride yp_sb), c.x is unused
+struct Conv1dSkArgs {
+  Conv1dArgs c;
+  uint16_t* yp;
+  int64_t yp_sb;
+  const float* part;
+  int G, chunk, M;
+};
+hipError_t launch_conv1d_update_sk(const Conv1dSkArgs& a, hipStream_t st);
+// linear! + causal_conv1d! (linear.cpp): y (M, N) = W^T x, then the conv step
+// on y's first conv.D channels; the stream-K GEMV + conv1d_update_sk_kernel at
+// N <= 32, else linear! + conv1d_update_kernel
+int linear_conv_workspace(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy,
+                          size_t* bytes, char* err, size_t errn);
+int linear_conv_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                    int64_t ldw, int M, int N, int K, Conv1dArgs conv, void* workspace,
+                    size_t workspace_bytes, hipStream_t st, char* err, size_t errn);
 // the chunked form of deltanet_sequence!: same arguments, plus a workspace of
 // deltanet_chunk_workspace_bytes(T, Hv, B) bytes (256-byte aligned)
 struct DeltaChunkArgs {

@@ -566,4 +566,73 @@ int linear_silu_mul_run(uint16_t* mid, int64_t mid_st, const uint16_t* x, int64_
   return VM_OK;
 }
 
+// ---- linear! + causal_conv1d! (the DeltaNet layer's decode step, qwen35.jl:212-223)
+int linear_conv_workspace(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy,
+                          size_t* bytes, char* err, size_t errn) {
+  size_t lin = 0;
+  const int rc = linear_workspace(M, N, K, ldw, ldx, ldy, &lin, err, errn);
+  if (sk_shape(M, N, K, ldw, ldx)) {
+    // a misaligned view takes linear! + the conv in the same workspace
+    *bytes = std::max(round256(gemv_sk_workspace_bytes(M, K)), rc == VM_OK ? lin : (size_t)0);
+    return VM_OK;
+  }
+  if (rc != VM_OK) return rc;
+  *bytes = lin;
+  return VM_OK;
+}
+
+int linear_conv_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                    int64_t ldw, int M, int N, int K, Conv1dArgs conv, void* workspace,
+                    size_t workspace_bytes, hipStream_t st, char* err, size_t errn) {
+  size_t need = 0;
+  int rc = linear_conv_workspace(M, N, K, ldw, ldx, ldy, &need, err, errn);
+  if (rc != VM_OK) return rc;
+  if (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 256 != 0) {
+    snprintf(err, errn,
+             "linear_causal_conv1d: workspace of %zu bytes (256-byte aligned) < %zu required "
+             "(vm_linear_causal_conv1d_workspace_bytes)", workspace_bytes, need);
+    return VM_E_SCRATCH;
+  }
+  hipError_t e = hipSuccess;
+  if (sk_shape(M, N, K, ldw, ldx) && ldy % 8 == 0 && (uintptr_t)x % 16 == 0 &&
+      (uintptr_t)w % 16 == 0 && (uintptr_t)y % 16 == 0) {
+    // the stream-K GEMV; the conv kernel adds each channel's partials, stores
+    // the bf16 projection and convolves its first D channels
+    GemvSkArgs g{};
+    g.w = w;
+    g.w_st = ldw;
+    g.x = x;
+    g.x_st = ldx;
+    g.part = static_cast<float*>(workspace);
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.p = gemv_sk_plan(M, K);
+    Conv1dSkArgs a{};
+    a.c = conv;
+    a.yp = y;
+    a.yp_sb = ldy;
+    a.part = g.part;
+    a.G = g.p.G;
+    a.chunk = g.p.chunk;
+    a.M = M;
+    e = launch_gemv_sk(g, st);
+    if (e == hipSuccess) e = launch_conv1d_update_sk(a, st);
+  } else {
+    size_t lin = 0;
+    rc = linear_workspace(M, N, K, ldw, ldx, ldy, &lin, err, errn);
+    if (rc != VM_OK) return rc;
+    rc = linear_run(y, ldy, x, ldx, w, ldw, M, N, K, workspace, lin, st, err, errn);
+    if (rc != VM_OK) return rc;
+    conv.x = y;
+    conv.x_sb = ldy;
+    e = launch_conv1d_update(conv, st);
+  }
+  if (e != hipSuccess) {
+    snprintf(err, errn, "linear_causal_conv1d: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  return VM_OK;
+}
+
 }  // namespace vm

@@ -606,7 +606,8 @@ hipError_t launch_gemv(GemvArgs a, hipStream_t st) {
 // by 1-KB direct loads, one barrier per unit; a unit's slot is refilled after
 // the next barrier, once every wave has read it. A workgroup writes one fp32
 // partial per row group it touches into slot (b + rg); the consumer adds a
-// row's slots in workgroup order, so results are bitwise repeatable.
+// row's slots in workgroup order (gemv_sk_sum4, common.h), so results are
+// bitwise repeatable.
 constexpr int SK_NB = 4;   // ring slots per wave (three units in flight)
 constexpr int SK_TE = 2048;  // bf16 of one staged 32 x 64 tile (4 KB)
 
@@ -688,26 +689,6 @@ void gemv_sk_kernel(GemvSkArgs a) {
   flush(rcur);
 }
 
-// rows m .. m + 3 (m % 4 == 0, m < M) of batch column n: the partials of row
-// group m / 128, added in workgroup order
-__device__ __forceinline__ float4 gemv_sk_sum4(const float* part, const GemvSkPlan& p, int m,
-                                               int n) {
-  const int rg = m >> 7, v = (m >> 5) & 3, r = m & 31;
-  const int wf = (rg * p.G) / p.chunk, wl = ((rg + 1) * p.G - 1) / p.chunk;
-  const float* src = part + ((int64_t)(wf + rg) * 4 + v) * 1024 + n * 32 + r;
-  float4 s = *reinterpret_cast<const float4*>(src);
-#pragma unroll 4
-  for (int w = wf + 1; w <= wl; ++w) {
-    src += 4096;  // the next workgroup's slot of the same row group
-    const float4 t = *reinterpret_cast<const float4*>(src);
-    s.x += t.x;
-    s.y += t.y;
-    s.z += t.z;
-    s.w += t.w;
-  }
-  return s;
-}
-
 // ---- mid = silu(gate) .* up (qwen35.jl:237-239) from the gate-up projection's
 // stream-K partials: gate and up rounded to bf16 first, as the reference stores
 // them in gu, then one fp32 evaluation and one rounding, as silu_mul_kernel.
@@ -716,9 +697,10 @@ __global__ __launch_bounds__(RT) void silu_mul_sk_kernel(SiluMulSkArgs a) {
   const int64_t idx = (int64_t)blockIdx.x * RT + threadIdx.x;
   if (idx >= (int64_t)nc * a.N) return;
   const int n = (int)(idx / nc), i = 8 * (int)(idx % nc);
-  const float4 g0 = gemv_sk_sum4(a.part, a.p, i, n), g1 = gemv_sk_sum4(a.part, a.p, i + 4, n);
-  const float4 u0 = gemv_sk_sum4(a.part, a.p, a.I + i, n);
-  const float4 u1 = gemv_sk_sum4(a.part, a.p, a.I + i + 4, n);
+  const int G = a.p.G, ch = a.p.chunk;
+  const float4 g0 = gemv_sk_sum4(a.part, G, ch, i, n), g1 = gemv_sk_sum4(a.part, G, ch, i + 4, n);
+  const float4 u0 = gemv_sk_sum4(a.part, G, ch, a.I + i, n);
+  const float4 u1 = gemv_sk_sum4(a.part, G, ch, a.I + i + 4, n);
   const float g8[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
   const float u8[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
   float gf[8], uf[8], m[8];

@@ -1109,6 +1109,47 @@ int vm_linear_silu_mul(vm_bf16* mid, int64_t mid_st, const vm_bf16* x, int64_t l
                                  S(st), g_err, sizeof g_err);
 }
 
+// ---- linear! + causal_conv1d! in one call -------------------------------------
+size_t vm_linear_causal_conv1d_workspace_bytes(int M, int N, int K, int64_t ldw, int64_t ldx,
+                                               int64_t ldy) {
+  if (linear_check(M, N, K, ldw, ldx, ldy) != VM_OK) return (size_t)-1;
+  size_t n = 0;
+  if (vm::linear_conv_workspace(M, N, K, ldw, ldx, ldy, &n, g_err, sizeof g_err) != VM_OK)
+    return (size_t)-1;
+  return n;
+}
+
+int vm_linear_causal_conv1d(vm_bf16* y, int64_t ldy, const vm_bf16* x, int64_t ldx,
+                            const vm_bf16* w, int64_t ldw, int M, int N, int K, vm_bf16* yc,
+                            int64_t yc_sb, const vm_bf16* s_in, vm_bf16* s_out, int64_t s_cs,
+                            int64_t s_sb, const vm_bf16* conv_w, int64_t conv_w_cs,
+                            const vm_bf16* conv_b, int D, int Kc, int act, void* workspace,
+                            size_t workspace_bytes, vm_stream st) {
+  TRY(linear_check(M, N, K, ldw, ldx, ldy));
+  TRY(check_conv(D, Kc, N, 1, "linear_causal_conv1d"));
+  REQUIRE(M % 8 == 0 && D <= M, VM_E_DIM,
+          "linear_causal_conv1d: the conv's D = %d channels must lie within the projection's M = %d "
+          "(a multiple of 8)", D, M);
+  REQUIRE(x && w, VM_E_ARG, "linear_causal_conv1d: NULL pointer argument");
+  TRY(check_aligned(y, "y"));
+  TRY(check_aligned(yc, "Y"));
+  TRY(check_aligned(s_in, "S"));
+  TRY(check_aligned(s_out, "S_out"));
+  TRY(check_aligned(conv_w, "Weight"));
+  if (conv_b) TRY(check_aligned(conv_b, "Bias"));
+  for (int64_t v : {ldy, yc_sb, s_cs, s_sb, conv_w_cs}) TRY(check_stride(v, "linear_causal_conv1d"));
+  REQUIRE(s_cs >= D && conv_w_cs >= D && (N <= 1 || (s_sb >= s_cs * Kc && yc_sb >= D)), VM_E_DIM,
+          "linear_causal_conv1d: strides below the extents (D = %d, K = %d)", D, Kc);
+  TRY(check_alias(s_in, s_out, (size_t)((N - 1) * s_sb + (Kc - 1) * s_cs + D) * 2,
+                  "linear_causal_conv1d"));
+  vm::Conv1dArgs c{};
+  c.y = yc; c.y_sb = yc_sb; c.s_in = s_in; c.s_out = s_out; c.s_cs = s_cs; c.s_sb = s_sb;
+  c.w = conv_w; c.w_cs = conv_w_cs; c.bias = conv_b; c.D = D; c.K = Kc; c.T = 1; c.B = N;
+  c.act = act ? 1 : 0;
+  return vm::linear_conv_run(y, ldy, x, ldx, w, ldw, M, N, K, c, workspace, workspace_bytes,
+                             S(st), g_err, sizeof g_err);
+}
+
 // ---- synthetic inputs ------------------------------------------------------
 int vm_fill_normal_bf16(vm_bf16* dst, int64_t n, uint64_t seed, float scale, float shift,
                         vm_stream st) {

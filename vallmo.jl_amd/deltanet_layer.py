@@ -142,10 +142,13 @@ def decode_(h, l: DeltaNetLayer, c: DeltaNetConfig, space: DeltaNetSpace, xn, *,
     B = xn.shape[0]
     if space.qz.shape[0] != B:
         raise DimensionMismatch(f"size(xn, 2) = {B} does not match the decode space's B")
-    ops.linear_({"y": space.qzab}, xn, l.W_in, workspace=workspace)  # [qz | ab], :212-213
-    conv_in, z = _views(space.qz, c)
-    ops.causal_conv1d_({"Y": space.conv, "Sp": l.conv_state}, conv_in, l.conv_state, l.conv_w,
-                       l.conv_b, sigma="silu")
+    # the projection [qz | ab] (:212-213) and the conv of its first n channels
+    # (:222-223) in one call: at B <= 32 the projection's partials go straight
+    # to the conv kernel
+    ops.linear_causal_conv1d_({"y": space.qzab, "Y": space.conv, "Sp": l.conv_state}, xn,
+                              l.W_in, l.conv_state, l.conv_w, l.conv_b, sigma="silu",
+                              workspace=workspace)
+    _, z = _views(space.qz, c)
     q, k, v = _qkv(space.conv, c)
     ops.fused_deltanet_decode_({"O": space.O, "Sp": l.S}, q, k, v, space.ab[:, :c.Hv],
                                space.ab[:, c.Hv:], z.unflatten(-1, (c.Hv, c.Dv)), l.A_log,

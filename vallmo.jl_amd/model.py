@@ -109,6 +109,7 @@ class Model:
                 l, c = self.dn_layers[0], self.cfg.linear
                 O2 = self.dn.O.view(self.cfg.B, -1)
                 need = max(need, ops.linear_workspace_bytes(self.xn, l.W_in, self.dn.qzab),
+                           ops.linear_causal_conv1d_workspace_bytes(self.xn, l.W_in, self.dn.qzab),
                            ops.linear_workspace_bytes(O2, l.Wout, self.h),
                            ops.linear_add_rms_norm_workspace_bytes(O2, l.Wout))
             attn = [l for l in self.layers if not isinstance(l, DeltaNetLayer)]

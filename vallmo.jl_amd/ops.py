@@ -508,6 +508,49 @@ def causal_conv1d_(outs, X, S, Weight, Bias=None, *, sigma=None):
     return outs
 
 
+def linear_causal_conv1d_workspace_bytes(x, W, y) -> int:
+    """Workspace of linear_causal_conv1d_ for this problem."""
+    M, K, N = W.shape[0], x.shape[-1], _rows(x)
+    _tune(M, N, K, W.stride(0), _ld(x), _ld(y))  # the two-call path's plan (N > 32)
+    n = _lib.load().vm_linear_causal_conv1d_workspace_bytes(M, N, K, W.stride(0), _ld(x), _ld(y))
+    if n == ctypes.c_size_t(-1).value:
+        _lib.check(_lib.VM_E_UNSUPPORTED, "vm_linear_causal_conv1d_workspace_bytes")
+    return int(n)
+
+
+def linear_causal_conv1d_(outs, x, W, S, Weight, Bias=None, *, sigma=None, workspace=None):
+    """linear! then causal_conv1d! on the projection's first D channels in one
+    call (the DeltaNet layer's decode step, src/llm/qwen35.jl:212-223):
+    y = bf16(W^T x) (every channel written), then causal_conv1d!((; Y, S′),
+    y[1:D, :], S, Weight, Bias; σ). outs: "y" (M, N) (torch (N, M)), "Y" (D, N),
+    "Sp" (D, K, N), which may be S itself. x :: (K, N), W :: (K, M) K-major (torch
+    (M, K)). No reference counterpart as one op: at N <= 32 the projection's fp32
+    partials go straight to the conv kernel."""
+    y, Y, Sp = _out(outs, "y"), _out(outs, "Y"), _out(outs, "Sp")
+    M, N, ldy = _cols(y, "y")
+    K, Nx, ldx = _cols(x, "x")
+    if W.dim() != 2 or tuple(W.shape) != (M, K) or Nx != N:
+        raise DimensionMismatch(f"linear_causal_conv1d: x ({K}, {Nx}), W {tuple(W.shape)}, "
+                                f"y ({M}, {N})")
+    dims = sizes(Y=(Y, "D B"), S=(S, "D Kc B"), Sp=(Sp, "D Kc B"), Weight=(Weight, "D Kc"),
+                 Bias=(Bias, "D"))
+    D, Kc = dims["D"], dims["Kc"]
+    if dims["B"] != N:
+        raise DimensionMismatch(f"linear_causal_conv1d: the conv has B = {dims['B']}, x has N = {N}")
+    for t, n in ((W, "W"), (Y, "Y"), (S, "S"), (Sp, "S′"), (Weight, "Weight"), (Bias, "Bias")):
+        _need(t, torch.bfloat16, n)
+    if S.stride() != Sp.stride():
+        raise ArgumentError("S and S′ must share strides")
+    need = linear_causal_conv1d_workspace_bytes(x, W, y)
+    if workspace is None:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+    call("vm_linear_causal_conv1d", _p(y), ldy, _p(x), ldx, _p(W), W.stride(0), M, N, K,
+         _p(Y), _st(Y, 0, D), _p(S), _p(Sp), _st(S, 1, D), _st(S, 0, Kc * D), _p(Weight),
+         _st(Weight, 0, D), _p(Bias), D, Kc, _act(sigma), _p(workspace), workspace.numel(),
+         _stream())
+    return outs
+
+
 def causal_conv1d(X, S, Weight, Bias=None, *, sigma=None, Sp=None) -> dict:
     """Allocating causal_conv1d (causal_conv1d.jl:63-66): {"Y", "Sp"}; pass Sp=S for
     the in-place ring (the reference's output_override, qwen35.jl:222-223)."""
