@@ -302,7 +302,11 @@ int vm_gated_attn_prefill_staged(vm_bf16* out, int64_t out_st, int64_t out_sb,
  * vm_linear_workspace_bytes builds it and returns the workspace it needs (at
  * most 64 MiB), which the caller passes to vm_linear (the reference takes it
  * from the ambient arena, linear.jl:62-66). Returns (size_t)-1 on failure.
- * A problem with no algorithm is VM_E_UNSUPPORTED (no fallback path).        */
+ * The role of the reference's mul! fallback (linear.jl:59-61, :67) is the
+ * library's general bf16 MFMA GEMM (any shape, 2-byte alignment, no
+ * workspace): it takes a problem hipBLASLt has no algorithm for, views whose
+ * column strides are not multiples of 8 (outside the GEMV's reach) or whose
+ * pointers are not 16-byte aligned, and calls hipBLASLt refuses.          */
 size_t vm_linear_workspace_bytes(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy);
 /* vm_linear_tune: no counterpart in the reference (its plan keeps the
  * heuristic's first). For callers that load a model and then run it: times up

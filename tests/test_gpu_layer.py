@@ -51,6 +51,59 @@ def _narrow_bar(x, W, ref):
         ref.shape)
 
 
+def _offset_view(t, off, ld):
+    """t (rows, cols) copied into a buffer as rows of `ld` elements starting `off`
+    elements in: a view with column stride ld and a data pointer off * 2 bytes
+    past an aligned one."""
+    rows, cols = t.shape
+    buf = torch.full((off + rows * ld,), 3.0, dtype=torch.bfloat16, device="cuda")
+    v = buf[off:].view(rows, ld)[:, :cols]
+    v.copy_(t)
+    return v, buf
+
+
+# (M, N, K, x offset / stride, W offset / stride, y offset / stride)
+GENERAL = [(37, 5, 29, (0, 31), (0, 29), (0, 37)),         # odd strides everywhere
+           (520, 300, 136, (0, 136), (1, 136), (0, 520)),  # W 2 bytes off alignment
+           (197, 70, 1000, (1, 1000), (0, 1000), (3, 197)),
+           (10, 3, 1, (0, 1), (0, 1), (0, 10)),             # K = 1
+           (2560, 257, 2048, (0, 2048), (0, 2048), (1, 2560)),
+           (64, 64, 64, (0, 72), (0, 65), (0, 64))]
+
+
+@pytest.mark.parametrize("M,N,K,xs,ws,ys", GENERAL)
+def test_linear_general_kernel(vm, orc, M, N, K, xs, ws, ys):
+    """Views the GEMM library is not given (column strides that are not
+    multiples of 8, data pointers off 16-byte alignment) run on the library's
+    general bf16 MFMA kernel, the role of the reference's mul! fallback
+    (linear.jl:59-61, :67): every element within one bf16 ulp (plus fp32
+    reassociation) of the fp32 oracle, elements outside the view untouched,
+    and no workspace needed."""
+    banner(f"linear general M={M} N={N} K={K} x{xs} W{ws} y{ys}")
+    x = normal_bf16((N, K), 730 + N + K)
+    W = normal_bf16((M, K), 830 + M, scale=K ** -0.5)
+    xv, _ = _offset_view(to_dev(x), *xs)
+    Wv, _ = _offset_view(to_dev(W), *ws)
+    yv, flat = _offset_view(torch.full((N, M), 3.0, dtype=torch.bfloat16, device="cuda"), *ys)
+    if ys[1] % 8 or xs[1] % 8 or ws[1] % 8:
+        assert vm.linear_workspace_bytes(xv, Wv, yv) == 0
+    vm.linear_({"y": yv}, xv, Wv, workspace=torch.empty(16, dtype=torch.uint8, device="cuda"))
+    torch.cuda.synchronize()
+    rows = slice(None, None, 8) if N > 64 else slice(None)
+    ref = orc.linear(x[rows], W).astype(np.float64)
+    bar = _narrow_bar(x[rows], W, ref)
+    got = dev_f32(yv)[rows].astype(np.float64)
+    worst = float(np.max(np.abs(got - ref) / bar))
+    print(f"linear general {M}x{N}x{K}: worst |err|/bar {worst:.3f}")
+    assert worst <= 1.0
+    # the padding around the view keeps its fill (3.0), and so do the elements before it
+    off, ld = ys
+    pad = flat[off:off + N * ld].view(N, ld)[:, M:]
+    assert bool((pad == 3.0).all())
+    if off:
+        assert bool((flat[:off] == 3.0).all())
+
+
 @pytest.mark.parametrize("M,N,K", NARROW)
 def test_linear_narrow(vm, orc, M, N, K):
     """The decode projections (N <= 16, or N <= 32 with M <= 4096) run on the library's split-K

@@ -288,6 +288,18 @@ int linear_silu_mul_run(uint16_t* mid, int64_t mid_st, const uint16_t* x, int64_
                         const uint16_t* w, int64_t ldw, int I, int N, int K, void* workspace,
                         size_t workspace_bytes, hipStream_t st, char* err, size_t errn);
 hipError_t launch_gemv(GemvArgs a, hipStream_t st);
+
+// y = W^T x for a problem the GEMM library has no algorithm for (gemm.hip):
+// column-major x (K, N) / W (K, M) / y (M, N) with column strides, any shape,
+// any stride, 2-byte alignment; no workspace
+struct GemmAnyArgs {
+  const uint16_t* w;
+  const uint16_t* x;
+  uint16_t* y;
+  int64_t ldw, ldx, ldy;
+  int64_t M, N, K;
+};
+hipError_t launch_gemm_any(const GemmAnyArgs& a, hipStream_t st);
 // the split GEMV without its reduce: leaves the slices' fp32 partials in
 // a.part (layout [S2][32][M]); returns the plan through *plan
 hipError_t launch_gemv_partials(GemvArgs a, GemvPlan* plan, hipStream_t st);

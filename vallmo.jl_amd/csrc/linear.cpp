@@ -16,8 +16,13 @@
 //     D (M x N) = op(A) B,  A = W (K x M, op = transpose), B = x (K x N).
 // The workspace comes from the caller (the reference takes it from the ambient
 // arena, linear.jl:62-66), so a warm call allocates nothing and can be
-// captured. There is no CPU or library fallback: a problem hipBLASLt has no
-// algorithm for is an error (VM_E_UNSUPPORTED).
+// captured. A problem hipBLASLt has no algorithm for (remembered as such, as
+// the reference remembers `nothing`), a view whose column strides are not
+// multiples of 8 elements or whose pointers are not 16-byte aligned, and a
+// call the library refuses run on the library's own general GEMM kernel
+// (gemm.hip): the role of the reference's mul! fallback for problems without
+// an Lt algorithm and for anything not a plain CuMatrix (linear.jl:59-61,
+// :67). It needs no workspace.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -264,9 +269,40 @@ bool gemv_aligned(const void* y, const void* x, const void* w) {
   return ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0) && ((uintptr_t)y % 8 == 0);
 }
 
+// views the GEMM library is not asked to take (see the file comment)
+bool general_strides(int64_t ldw, int64_t ldx, int64_t ldy) {
+  return (ldw % 8) != 0 || (ldx % 8) != 0 || (ldy % 8) != 0;
+}
+bool general_view(const void* y, const void* x, const void* w, int64_t ldw, int64_t ldx,
+                  int64_t ldy) {
+  return general_strides(ldw, ldx, ldy) || ((uintptr_t)x % 16) != 0 || ((uintptr_t)w % 16) != 0 ||
+         ((uintptr_t)y % 16) != 0;
+}
+
+int run_gemm_any(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                 int64_t ldw, int M, int N, int K, hipStream_t st, char* err, size_t errn) {
+  GemmAnyArgs a{};
+  a.w = w;
+  a.x = x;
+  a.y = y;
+  a.ldw = ldw;
+  a.ldx = ldx;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  const hipError_t e = launch_gemm_any(a, st);
+  if (e != hipSuccess) {
+    snprintf(err, errn, "linear (general kernel): %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  return VM_OK;
+}
+
 }  // namespace
 
 int linear_tune(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, char* err, size_t errn) {
+  if (general_strides(ldw, ldx, ldy)) return VM_OK;  // the general kernel: nothing to tune
   if (gemv_shape(M, N, K, ldw, ldx, ldy)) {
     // aligned views run the GEMV, which has nothing to tune; the plan stays
     // the heuristic's first (it only serves misaligned views)
@@ -284,6 +320,7 @@ int linear_tune(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, char
   Plan* p = nullptr;
   hipblasLtHandle_t h;
   int rc = find_plan(dev, M, N, K, ldw, ldx, ldy, &p, &h, err, errn);
+  if (rc == VM_E_UNSUPPORTED) return VM_OK;  // the general kernel: nothing to tune
   if (rc != VM_OK || p->pick >= 0) return rc;
   hipblasLtMatmulHeuristicResult_t res[NREQ];
   int cand[NTUNE];
@@ -316,6 +353,12 @@ int linear_plan_state(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy
 
 int linear_workspace(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy, size_t* bytes,
                      char* err, size_t errn) {
+  if (general_strides(ldw, ldx, ldy)) {
+    // the GEMV (which takes y columns in steps of 4) or the general kernel,
+    // which needs no workspace
+    *bytes = gemv_shape(M, N, K, ldw, ldx, ldy) ? gemv_workspace_bytes(M, K) : 0;
+    return VM_OK;
+  }
   const Plan* p = nullptr;
   const int rc = get_plan(M, N, K, ldw, ldx, ldy, &p, err, errn);
   if (gemv_shape(M, N, K, ldw, ldx, ldy)) {
@@ -324,6 +367,10 @@ int linear_workspace(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t ldy,
     return VM_OK;
   }
   if (rc == VM_OK) *bytes = p->workspace;
+  if (rc == VM_E_UNSUPPORTED) {  // the general kernel needs no workspace
+    *bytes = 0;
+    return VM_OK;
+  }
   return rc;
 }
 
@@ -357,8 +404,11 @@ int linear_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const u
     }
     return VM_OK;
   }
+  if (general_view(y, x, w, ldw, ldx, ldy))
+    return run_gemm_any(y, ldy, x, ldx, w, ldw, M, N, K, st, err, errn);
   const Plan* p = nullptr;
   int rc = get_plan(M, N, K, ldw, ldx, ldy, &p, err, errn);
+  if (rc == VM_E_UNSUPPORTED) return run_gemm_any(y, ldy, x, ldx, w, ldw, M, N, K, st, err, errn);
   if (rc != VM_OK) return rc;
   if (p->workspace > 0 && (workspace == nullptr || workspace_bytes < p->workspace)) {
     snprintf(err, errn, "linear: workspace of %zu bytes < %zu required (vm_linear_workspace_bytes)",
@@ -376,8 +426,9 @@ int linear_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const u
   const hipblasStatus_t s = hipblasLtMatmul(h, p->desc, &alpha, w, p->a, x, p->b, &beta, y, p->d, y,
                                             p->d, &p->algo, workspace, p->workspace, st);
   if (s != HIPBLAS_STATUS_SUCCESS) {
-    snprintf(err, errn, "linear: hipblasLtMatmul: %s", status_name(s));
-    return VM_E_UNSUPPORTED;
+    // the plan's algorithm refused these operands (e.g. a misaligned view):
+    // the general kernel, as the reference's mul! (linear.jl:60)
+    return run_gemm_any(y, ldy, x, ldx, w, ldw, M, N, K, st, err, errn);
   }
   return VM_OK;
 }
