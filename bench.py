@@ -806,12 +806,15 @@ def bench_deltanet(vm, torch, seed=11):
     yb = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device="cuda")
     us_gn = _profiled_us(vm, torch, vm._lib.VM_K_ROWS,
                          lambda: vm.gated_rms_norm_(yb, o, z, gw, eps=EPS), n=5)
+    # the layer's form: the chunked recurrence with the gated norm in its output kernel
+    us_chk_gn = _profiled_us(vm, torch, vm._lib.VM_K_DELTANET,
+                             lambda: vm.deltanet_sequence_chunked_gated_norm_(
+                                 {"Y": yb, "Sp": S}, z, gw, p["Q"], p["K"], p["V"], p["Beta"],
+                                 p["Gate"], S, eps=EPS, workspace=ws), n=5)
     # prep: conv rows read (bf16), fp32 q, k, v written, ab read, gates written;
     # gated norm: fp32 o and bf16 z read, bf16 y written
     prep_bytes = 2.0 * T * n + 4.0 * T * n + 2.0 * T * 2 * Hv + 8.0 * T * Hv
     gn_bytes = (4.0 + 2.0 + 2.0) * T * Hv * Dv
-    # chunked form's work: per 64-token chunk and value head, phase 1's two Grams,
-    # triangular solve and operand writes, phase 2's 4 x 112 MFMAs per column block
     res["prefill_B1_T4096"] = {
         "conv_sequence_us": us_conv,
         "conv_sequence_gbs": 2.0 * (2 * T * n + K * n) / (us_conv * 1e-6) / 1e9,
@@ -820,6 +823,7 @@ def bench_deltanet(vm, torch, seed=11):
         "sequence_us_per_token": us_seq / T,
         "chunked_ms": us_chk * 1e-3,
         "chunked_tokens_per_s": T / (us_chk * 1e-6),
+        "chunked_gated_norm_ms": us_chk_gn * 1e-3,
         "prep_us": us_prep,
         "prep_gbs": prep_bytes / (us_prep * 1e-6) / 1e9,
         "gated_norm_us": us_gn,
@@ -1176,7 +1180,8 @@ def main():
             f"{f32_['gbs']:.0f} GB/s; conv decode B=32 {cv['us']:.1f} us = {cv['gbs']:.0f} GB/s; "
             f"prefill T=4096: conv {pp['conv_sequence_us']:.1f} us, recurrence "
             f"{pp['sequence_ms']:.2f} ms sequential ({pp['sequence_us_per_token']:.2f} us/token), "
-            f"{pp['chunked_ms']:.3f} ms chunked; prep {pp['prep_us']:.1f} us = {pp['prep_gbs']:.0f} "
+            f"{pp['chunked_ms']:.3f} ms chunked ({pp['chunked_gated_norm_ms']:.3f} ms with the gated "
+            f"norm fused, the layer's form); prep {pp['prep_us']:.1f} us = {pp['prep_gbs']:.0f} "
             f"GB/s, gated norm {pp['gated_norm_us']:.1f} us = {pp['gated_norm_gbs']:.0f} GB/s")
     step = None
     if not args.no_step:

@@ -510,14 +510,32 @@ int vm_deltanet_sequence(float* o, const float* q, const float* k, const float* 
  * gamma_C S_0 + K~^T delta: the sequential recurrence's exact algebra), the
  * chunks' state carried by one sequential scan. No separate reference
  * function: the reference runs the sequential loop (deltanet_recurrent.jl:
- * 109-172); this is the same operator, parallel over each chunk. workspace:
- * vm_deltanet_sequence_workspace_bytes(T, Hv, B) bytes, 256-byte aligned
- * (147 968 B per 64-token chunk per value head and sequence). */
+ * 109-172); this is the same operator, parallel over each chunk: a chunk
+ * kernel, one sequential scan over the chunks' states, and a chunk-parallel
+ * output kernel. workspace: vm_deltanet_sequence_workspace_bytes(T, Hv, B)
+ * bytes, 256-byte aligned (about 197 KB per 64-token chunk per value head
+ * and sequence). */
 size_t vm_deltanet_sequence_workspace_bytes(int T, int Hv, int B);
 int vm_deltanet_sequence_chunked(float* o, const float* q, const float* k, const float* v,
                                  const float* beta, const float* gate, const float* s_in,
                                  float* s_out, int Dk, int Dv, int T, int Hk, int Hv, int B,
                                  void* workspace, size_t workspace_bytes, vm_stream stream);
+
+/* forward(::DeltaNetLayer)'s recurrence and gated norm in one call
+ * (src/llm/qwen35.jl:357-364: deltanet_sequence! into O, then y = O rstd
+ * NormWeight silu(z), the out projection's input): the chunked recurrence of
+ * vm_deltanet_sequence_chunked with the norm applied in its output kernel,
+ * so O never reaches memory. y, z :: (Dv, Hv, T, B) bf16 rows at token
+ * stride *_st and sequence stride *_sb (heads contiguous), as
+ * vm_gated_rms_norm; the state and workspace as vm_deltanet_sequence_chunked. */
+int vm_deltanet_sequence_chunked_gated_norm(vm_bf16* y, int64_t y_st, int64_t y_sb,
+                                            const vm_bf16* z, int64_t z_st, int64_t z_sb,
+                                            const vm_bf16* norm_w, float eps, const float* q,
+                                            const float* k, const float* v, const float* beta,
+                                            const float* gate, const float* s_in, float* s_out,
+                                            int Dk, int Dv, int T, int Hk, int Hv, int B,
+                                            void* workspace, size_t workspace_bytes,
+                                            vm_stream stream);
 
 /* The prefill's inputs to deltanet_sequence! (forward(::DeltaNetLayer),
  * src/llm/qwen35.jl:347-356): from the conv output cv (the q | k | v channels,

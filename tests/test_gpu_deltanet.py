@@ -354,6 +354,47 @@ def test_deltanet_sequence_chunked(vm, orc, B, T):
         assert err <= 5e-4, name
 
 
+@pytest.mark.parametrize("B,T,off", [(1, 100, 0), (2, 65, 8), (1, 1, 0), (3, 129, 0)])
+def test_deltanet_sequence_chunked_gated_norm(vm, orc, B, T, off):
+    """forward(::DeltaNetLayer)'s recurrence and gated norm as one call
+    (qwen35.jl:357-364): y = O rstd NormWeight silu(z) formed where each chunk's
+    O is. The output kernel forms O the same way with or without the norm, so y
+    is checked against the oracle's gated norm of the unfused call's O (itself
+    checked against the sequential oracle), to one bf16 ulp; z is read from the
+    projection's rows, y written as a strided view, the state updated in place
+    and equal to the unfused call's bit for bit."""
+    banner(f"deltanet chunked + gated norm B={B} T={T} off={off}")
+    cv, ab, a_log, dt_bias = _prepped(B, T, 2950 + B + T)
+    p = orc.deltanet_prep(cv, ab, a_log, dt_bias, Dk=DK, Dv=DV, Hk=HK, Hv=HV)
+    s = normal_f32(B * HV * DV * DK, 2951, scale=0.05).reshape(B, HV, DV, DK)
+    o_ref, s_ref = orc.deltanet_sequence(p["q"], p["k"], p["v"], p["beta"], p["gate"], s)
+    args = [f32dev(p[n]) for n in ("q", "k", "v", "beta", "gate")]
+    S1 = f32dev(s)
+    o = torch.empty((B, HV, T, DV), dtype=torch.float32, device="cuda")
+    vm.deltanet_sequence_chunked_({"O": o, "Sp": S1}, *args, S1)
+    qz = normal_bf16((B, T, NCH + HV * DV), 2952)
+    norm_w = normal_bf16((DV,), 2953, scale=0.2, shift=1.0)
+    Z = to_dev(qz)[..., NCH:].unflatten(-1, (HV, DV))
+    Yw = torch.full((B, T, HV * DV + off), 5.0, dtype=torch.bfloat16, device="cuda")
+    Y = Yw[..., off:].unflatten(-1, (HV, DV))
+    S2 = f32dev(s)
+    vm.deltanet_sequence_chunked_gated_norm_({"Y": Y, "Sp": S2}, Z, to_dev(norm_w), *args, S2,
+                                             eps=EPS)
+    torch.cuda.synchronize()
+    og = o.cpu().numpy()
+    err = np.abs(og - o_ref).max() / np.abs(o_ref).max()
+    print(f"unfused O: max err / max |ref| = {err:.2e}")
+    assert err <= 5e-4
+    y_ref = orc.gated_rms_norm(og, np.ascontiguousarray(qz[..., NCH:]), norm_w, eps=EPS)
+    assert_bf16_close(dev_f32(Y), y_ref, "gated y", extra=1e-6)
+    if off:
+        assert bool((Yw[..., :off] == 5.0).all())
+    assert torch.equal(S1, S2)
+    err = np.abs(S2.cpu().numpy() - s_ref).max() / np.abs(s_ref).max()
+    print(f"chunked + norm S: max err / max |ref| = {err:.2e}")
+    assert err <= 5e-4
+
+
 def test_deltanet_sequence_chunked_overflowing_softplus(vm, orc):
     """A gate input past softplus' fp32 overflow (alpha + dt_bias > 88.7: the
     prep's log1p(exp(x)) is +inf, the log decay -inf, the decay exactly 0, as in

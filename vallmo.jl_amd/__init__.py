@@ -24,7 +24,8 @@ from .ops import (attention, attention_, decode_attention, decode_attention_,  #
                   linear_add_rms_norm_, linear_add_rms_norm_workspace_bytes,
                   linear_silu_mul_, linear_silu_mul_workspace_bytes,
                   linear_causal_conv1d_, linear_causal_conv1d_workspace_bytes,
-                  deltanet_sequence_chunked_, deltanet_sequence_workspace_bytes)
+                  deltanet_sequence_chunked_, deltanet_sequence_workspace_bytes,
+                  deltanet_sequence_chunked_gated_norm_)
 from .layer import (AttnConfig, AttnLayer, AttnModel, CaptureSession, Generation,  # noqa: F401
                     StagedV, attn_layer, decode_, forward, gated_attn_decode_, gated_attn_prefill)
 from .model import (Model, ModelConfig, generate_, generate_captured_, mlp_,  # noqa: F401

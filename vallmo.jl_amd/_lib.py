@@ -145,6 +145,9 @@ _SIGS = {
     "vm_deltanet_sequence": (_c_i, [_p] * 8 + [_c_i] * 6 + [_p]),
     "vm_deltanet_sequence_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i]),
     "vm_deltanet_sequence_chunked": (_c_i, [_p] * 8 + [_c_i] * 6 + [_p, _c_sz, _p]),
+    "vm_deltanet_sequence_chunked_gated_norm": (_c_i, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p,
+                                                        _c_f] + [_p] * 7 + [_c_i] * 6
+                                                + [_p, _c_sz, _p]),
     "vm_deltanet_prefill_prep": (_c_i, [_p] * 5 + [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _p]
                                  + [_c_i] * 6 + [_p]),
     "vm_gated_rms_norm": (_c_i, [_p, _c_i64, _c_i64, _p, _p, _c_i64, _c_i64, _p, _c_i, _c_i,

@@ -248,31 +248,77 @@ __global__ __launch_bounds__(256) void deltanet_sequence_kernel(DeltaSeqArgs a) 
 // so delta = U - W S_0 with U = (I + L)^-1 beta V, W = (I + L)^-1 beta gamma K;
 // then O = gamma Q S_0 + M delta with M_ij = D_ij q_i.k_j (j <= i), and
 // S_C = gamma_C S_0 + K~^T delta with K~_j = (gamma_C / gamma_j) k_j (exact
-// algebra of the sequential update; fp32 throughout).
-// Phase 1 (deltanet_chunk_kernel, chunk-parallel): the Grams, the triangular
-// solve, and every operand of phase 2 written in the fp32 MFMA operand order
-// of v_mfma_f32_16x16x4f32 (A lane l = A[l % 16][l / 16], B lane l =
-// B[l / 16][l % 16], D lane l reg r = D[4 (l / 16) + r][l % 16]), 16 bytes per
-// lane per four k-steps, so phase 2 reads 1 KB contiguous per wave load.
+// algebra of the sequential update; fp32 throughout). Three launches:
+// Phase 1 (deltanet_chunk_kernel, chunk-parallel): the Gram K K^T, the
+// triangular solve, and the operands of the state chain (-W, K~^T, U,
+// gamma_C) written in the fp32 MFMA operand order of v_mfma_f32_16x16x4f32
+// (A lane l = A[l % 16][l / 16], B lane l = B[l / 16][l % 16], D lane l reg r
+// = D[4 (l / 16) + r][l % 16]), 16 bytes per lane per four k-steps, so phase 2
+// reads 1 KB contiguous per wave load.
 // Phase 2 (deltanet_scan_kernel, sequential over chunks): one workgroup per 16
-// state columns of a value head; per chunk 112 MFMAs per wave, the next
-// chunk's operands loading into a second register set meanwhile.
+// state columns of a value head; per chunk 64 MFMAs per wave (delta, then the
+// state), writing each chunk's start state S_0 and its delta for phase 3, the
+// next chunk's operands loading into a second register set meanwhile.
+// Phase 3 (deltanet_out_kernel, chunk-parallel): Q K^T, M and O = gamma Q S_0 +
+// M delta on the same MFMA, then either O (fp32, the operator's output) or,
+// fused, the layer's gated RMSNorm with z (qwen35.jl:360-364) in bf16. The
+// products take their k index as 16 s4 + 4 (l / 16) + e for lane l, register e
+// of the f32x4 of group s4 (any order of the k sum is the same product), so
+// every operand is one 16-byte load of 4 contiguous floats: q and k rows,
+// and S_0 and delta exactly as the scan holds them in its accumulators.
 namespace {
 constexpr int DC = 64;   // chunk length
 constexpr int CBW = 16;  // state columns per scan workgroup
-// per (chunk, value head, sequence) unit, floats
+// per (chunk, value head, sequence) unit of the scan's operands, floats
 constexpr int UO_W = 0;      // -W:       [w 4][s4 8][lane][4], A[i = r][k = dk]
-constexpr int UO_Q = 8192;   // gamma Q:  same order
-constexpr int UO_M = 16384;  // M:        [w 4][s4 4][lane][4], A[i = r][k = j]
-constexpr int UO_K = 20480;  // K~^T:     [d 8][s4 4][lane][4], A[i = dk][k = r]
-constexpr int UO_U = 28672;  // U:        [cb 8][w 4][lane][4], D[r][dv] tiles
-constexpr int UO_G = 36864;  // gamma_C
-constexpr int UNIT = 36992;  // floats per unit (147 968 B, a multiple of 256)
+constexpr int UO_K = 8192;   // K~^T:     [d 8][s4 4][lane][4], A[i = dk][k = r]
+constexpr int UO_U = 16384;  // U:        [cb 8][w 4][lane][4], D[r][dv] tiles
+constexpr int UO_G = 24576;  // gamma_C
+constexpr int UNIT = 24640;  // floats per unit (98 560 B, a multiple of 256)
+// per (chunk, value head, sequence), written by the scan for phase 3, floats:
+// S_0 [cb 8][d 8][lane][4] (lane l reg e = S_0[16 d + 4 (l / 16) + e][16 cb + l % 16])
+// and delta [cb 8][w 4][lane][4] (lane l reg e = delta[16 w + 4 (l / 16) + e][16 cb + l % 16])
+constexpr int S0_UNIT = DN_D * DN_D;
+constexpr int DL_UNIT = DC * DN_D;
 
 __device__ __forceinline__ int pos_acc(int r, int dv) {  // D[r][dv], 16 x 16 tiles
   return ((((dv >> 4) * 4 + (r >> 4)) * 64) + 16 * ((r & 15) >> 2) + (dv & 15)) * 4 + (r & 3);
 }
+
+// the chunk's inclusive cumulative log decay (wave 0, one token per lane; log
+// decays below -110 are taken as -110: expf underflows to exactly 0 below
+// about -104, so every decay the recurrence applies is unchanged, while the
+// cumulative sums stay finite; a -inf log decay, e.g. from softplus
+// overflowing in log1p(exp(x)) at x > 88.7, would make their differences NaN)
+__device__ __forceinline__ float chunk_cumsum(const DeltaSeqArgs& q, int b, int hv, int t0, int n,
+                                              int t) {
+  const int64_t g = ((int64_t)b * q.T + t0 + min(t, n - 1)) * q.Hv + hv;  // in bounds
+  const float gt = t < n ? fmaxf(q.gate[g], -110.0f) : 0.f;
+  float G = gt;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float o = __shfl_up(G, off);
+    if (t >= off) G += o;
+  }
+  return G;
+}
 }  // namespace
+
+// the (chunk, value head, sequence) workspaces of the three phases
+__host__ __device__ __forceinline__ int64_t dn_units_floats(int NC) { return (int64_t)(NC + 1) * UNIT; }
+__host__ __device__ __forceinline__ int64_t dn_s0_floats(int NC) { return (int64_t)(NC + 1) * S0_UNIT; }
+__host__ __device__ __forceinline__ int64_t dn_dl_floats(int NC) { return (int64_t)(NC + 1) * DL_UNIT; }
+__device__ __forceinline__ float* dn_units(const DeltaChunkArgs& a, int b, int hv, int NC) {
+  return a.ws + ((int64_t)b * a.s.Hv + hv) * dn_units_floats(NC);
+}
+__device__ __forceinline__ float* dn_s0(const DeltaChunkArgs& a, int b, int hv, int NC) {
+  return a.ws + (int64_t)a.s.B * a.s.Hv * dn_units_floats(NC) +
+         ((int64_t)b * a.s.Hv + hv) * dn_s0_floats(NC);
+}
+__device__ __forceinline__ float* dn_dl(const DeltaChunkArgs& a, int b, int hv, int NC) {
+  return a.ws + (int64_t)a.s.B * a.s.Hv * (dn_units_floats(NC) + dn_s0_floats(NC)) +
+         ((int64_t)b * a.s.Hv + hv) * dn_dl_floats(NC);
+}
 
 __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
   const DeltaSeqArgs& q = a.s;
@@ -280,7 +326,7 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
   const int hk = hv / (q.Hv / q.Hk);
   const int t0 = c * DC, n = min(DC, q.T - t0);
   const int NC = (q.T + DC - 1) / DC;
-  float* u = a.ws + ((int64_t)(b * q.Hv + hv) * (NC + 1) + c) * UNIT;
+  float* u = dn_units(a, b, hv, NC) + (int64_t)c * UNIT;
   if (c == 0) {  // unit NC: the identity chunk (all zero, gamma_C = 1), the scan's pad
     float* id = u + (int64_t)NC * UNIT;
     for (int i = t; i < UNIT / 4; i += 256)
@@ -288,13 +334,11 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
     __syncthreads();
     if (t == 0) id[UO_G] = 1.f;
   }
-  // K (later the -W rows) and L (later M) in LDS, ~51 KB: three workgroups per
-  // CU; Q is read from global memory (L2) where it is used
+  // K (later the -W rows) and L in LDS, ~51 KB: three workgroups per CU
   __shared__ __attribute__((aligned(16))) float Ks[DC][132];
   __shared__ float Ls[DC][DC + 1];
   __shared__ float Gs[DC], Bs[DC], Es[DC];
   const float* kp = q.k + (((int64_t)b * q.Hk + hk) * q.T + t0) * DN_D;
-  const float* qp = q.q + (((int64_t)b * q.Hk + hk) * q.T + t0) * DN_D;
   for (int i = t; i < DC * 32; i += 256) {  // float4 (row i / 32, column group i % 32)
     const int r = i >> 5, c4 = i & 31, rr = min(r, n - 1);  // rows past the end read as 0
     float4 kv = *reinterpret_cast<const float4*>(kp + rr * DN_D + 4 * c4);
@@ -302,52 +346,32 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
     *reinterpret_cast<float4*>(&Ks[r][4 * c4]) = kv;
   }
   if (t < 64) {  // wave 0: gates, inclusive cumulative sum of the log decay
-    const int64_t g = ((int64_t)b * q.T + t0 + min(t, n - 1)) * q.Hv + hv;  // in bounds
-    // log decays below -110 are taken as -110: expf underflows to exactly 0 below
-    // about -104, so every decay the recurrence applies is unchanged, while the
-    // cumulative sums stay finite (a -inf log decay, e.g. from softplus
-    // overflowing in log1p(exp(x)) at x > 88.7, would make their differences NaN)
-    const float gt = t < n ? fmaxf(q.gate[g], -110.0f) : 0.f;
-    float G = gt;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float o = __shfl_up(G, off);
-      if (t >= off) G += o;
-    }
+    const float G = chunk_cumsum(q, b, hv, t0, n, t);
+    const int64_t g = ((int64_t)b * q.T + t0 + min(t, n - 1)) * q.Hv + hv;
     Gs[t] = G;
     Bs[t] = t < n ? q.beta[g] : 0.f;
     Es[t] = expf(G);
   }
   __syncthreads();
-  // Grams: thread (bi, bj) takes rows bi + 16x, columns bj + 16y, x, y < 4
+  // Gram K K^T: thread (bi, bj) takes rows bi + 16x, columns bj + 16y, x, y < 4
   const int bi = t >> 4, bj = t & 15;
-  const float* qrow[4];  // this thread's Q rows (a row past the end reads as row n-1, masked)
-  float qmask[4];
-#pragma unroll
-  for (int x = 0; x < 4; ++x) {
-    qrow[x] = qp + (int64_t)min(bi + 16 * x, n - 1) * DN_D;
-    qmask[x] = bi + 16 * x < n ? 1.f : 0.f;
-  }
-  float A[4][4], P[4][4];
+  float A[4][4];
 #pragma unroll
   for (int x = 0; x < 4; ++x)
 #pragma unroll
-    for (int y = 0; y < 4; ++y) A[x][y] = P[x][y] = 0.f;
+    for (int y = 0; y < 4; ++y) A[x][y] = 0.f;
   for (int kk = 0; kk < DN_D; kk += 4) {
-    float4 ki[4], qi[4], kj[4];
+    float4 ki[4], kj[4];
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
       ki[x] = *reinterpret_cast<const float4*>(&Ks[bi + 16 * x][kk]);
-      qi[x] = *reinterpret_cast<const float4*>(qrow[x] + kk);
       kj[x] = *reinterpret_cast<const float4*>(&Ks[bj + 16 * x][kk]);
     }
 #pragma unroll
     for (int x = 0; x < 4; ++x)
 #pragma unroll
-      for (int y = 0; y < 4; ++y) {
+      for (int y = 0; y < 4; ++y)
         A[x][y] += ki[x].x * kj[y].x + ki[x].y * kj[y].y + ki[x].z * kj[y].z + ki[x].w * kj[y].w;
-        P[x][y] += qi[x].x * kj[y].x + qi[x].y * kj[y].y + qi[x].z * kj[y].z + qi[x].w * kj[y].w;
-      }
   }
 #pragma unroll
   for (int x = 0; x < 4; ++x)
@@ -356,26 +380,17 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
       const int i = bi + 16 * x, j = bj + 16 * y;
       const float d = j <= i ? expf(Gs[i] - Gs[j]) : 0.f;  // gamma_i / gamma_j
       Ls[i][j] = i > j ? Bs[i] * d * A[x][y] : 0.f;
-      P[x][y] *= d * qmask[x];                             // M, kept for later
     }
-  // gamma Q and K~^T in operand order, one coalesced float4 per lane and slot
+  // K~^T in operand order, one coalesced float4 per lane and slot
   const float Gl = Gs[DC - 1];
   for (int f = t; f < 2048; f += 256) {
     const int l = f & 63;
-    {  // gamma Q: tile f / 512, s4 (f / 64) % 8: row 16 w + l % 16, k = 16 s4 + l / 16 + 4 e
-      const int r = 16 * (f >> 9) + (l & 15), kb = 16 * ((f >> 6) & 7) + (l >> 4);
-      const float e = r < n ? Es[r] : 0.f;
-      const float* qr = qp + (int64_t)min(r, n - 1) * DN_D + kb;
-      *reinterpret_cast<float4*>(u + UO_Q + 4 * f) =
-          make_float4(e * qr[0], e * qr[4], e * qr[8], e * qr[12]);
-    }
-    {  // K~^T: tile f / 256, s4 (f / 64) % 4: dk 16 d + l % 16, r = 16 s4 + l / 16 + 4 e
-      const int dk = 16 * (f >> 8) + (l & 15), rb = 16 * ((f >> 6) & 3) + (l >> 4);
-      float v4[4];
+    // tile f / 256, s4 (f / 64) % 4: dk 16 d + l % 16, r = 16 s4 + l / 16 + 4 e
+    const int dk = 16 * (f >> 8) + (l & 15), rb = 16 * ((f >> 6) & 3) + (l >> 4);
+    float v4[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v4[e] = expf(Gl - Gs[rb + 4 * e]) * Ks[rb + 4 * e][dk];
-      *reinterpret_cast<float4*>(u + UO_K + 4 * f) = make_float4(v4[0], v4[1], v4[2], v4[3]);
-    }
+    for (int e = 0; e < 4; ++e) v4[e] = expf(Gl - Gs[rb + 4 * e]) * Ks[rb + 4 * e][dk];
+    *reinterpret_cast<float4*>(u + UO_K + 4 * f) = make_float4(v4[0], v4[1], v4[2], v4[3]);
   }
   if (t == 0) u[UO_G] = expf(Gl);
   __syncthreads();
@@ -396,7 +411,7 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
     for (int j = 0; j < i; ++j) acc[j & 3] -= Ls[i][j] * X[j];
     X[i] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   }
-  __syncthreads();  // L and K are free: M and -W staged there
+  __syncthreads();  // K is free: -W staged there
   if (t < DN_D) {   // U: rows 4qq .. 4qq + 3 of column t are one accumulator float4
 #pragma unroll
     for (int qq = 0; qq < DC / 4; ++qq)
@@ -406,48 +421,35 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
 #pragma unroll
     for (int r = 0; r < DC; ++r) Ks[r][t - DN_D] = -X[r];
   }
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 4; ++y) Ls[bi + 16 * x][bj + 16 * y] = P[x][y];
   __syncthreads();
-  for (int f = t; f < 2048; f += 256) {  // -W: the gamma Q order
+  for (int f = t; f < 2048; f += 256) {  // -W: tile f / 512, s4 (f / 64) % 8
     const int l = f & 63;
     const int r = 16 * (f >> 9) + (l & 15), kb = 16 * ((f >> 6) & 7) + (l >> 4);
     *reinterpret_cast<float4*>(u + UO_W + 4 * f) =
         make_float4(Ks[r][kb], Ks[r][kb + 4], Ks[r][kb + 8], Ks[r][kb + 12]);
   }
-  for (int f = t; f < 1024; f += 256) {  // M: tile f / 256, s4 (f / 64) % 4
-    const int l = f & 63;
-    const int r = 16 * (f >> 8) + (l & 15), jb = 16 * ((f >> 6) & 3) + (l >> 4);
-    *reinterpret_cast<float4*>(u + UO_M + 4 * f) =
-        make_float4(Ls[r][jb], Ls[r][jb + 4], Ls[r][jb + 8], Ls[r][jb + 12]);
-  }
 }
 
 namespace {
-// a chunk's operands, split by the step that consumes them: step A (the S
-// products) and step B (the delta products)
+// a chunk's operands, split by the step that consumes them: step A (the delta
+// products) and step B (the state products)
 struct ScanOpsA {
-  f32x4 w[8], q[8], u;
+  f32x4 w[8], u;
 };
 struct ScanOpsB {
-  f32x4 m[4], k[8];
+  f32x4 k[8];
   float gl;
 };
 __device__ __forceinline__ void scan_load_a(ScanOpsA& o, const float* unit, int w, int cb,
                                             int lane) {
 #pragma unroll
-  for (int s4 = 0; s4 < 8; ++s4) {
+  for (int s4 = 0; s4 < 8; ++s4)
     o.w[s4] = *reinterpret_cast<const f32x4*>(unit + UO_W + ((w * 8 + s4) * 64 + lane) * 4);
-    o.q[s4] = *reinterpret_cast<const f32x4*>(unit + UO_Q + ((w * 8 + s4) * 64 + lane) * 4);
-  }
   o.u = *reinterpret_cast<const f32x4*>(unit + UO_U + ((cb * 4 + w) * 64 + lane) * 4);
 }
 __device__ __forceinline__ void scan_load_b(ScanOpsB& o, const float* unit, int w, int lane) {
 #pragma unroll
   for (int s4 = 0; s4 < 4; ++s4) {
-    o.m[s4] = *reinterpret_cast<const f32x4*>(unit + UO_M + ((w * 4 + s4) * 64 + lane) * 4);
     o.k[s4] = *reinterpret_cast<const f32x4*>(unit + UO_K + (((2 * w) * 4 + s4) * 64 + lane) * 4);
     o.k[4 + s4] =
         *reinterpret_cast<const f32x4*>(unit + UO_K + (((2 * w + 1) * 4 + s4) * 64 + lane) * 4);
@@ -457,39 +459,35 @@ __device__ __forceinline__ void scan_load_b(ScanOpsB& o, const float* unit, int 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
-// one chunk: delta = U - W S, Og = gamma Q S (step A), then O = Og + M delta,
-// S = gamma_C S + K~^T delta (step B). Rows past T are stored to `spare`.
+// one chunk: S_0 out for phase 3, delta = U - W S_0 (step A), delta out, then
+// S = gamma_C S_0 + K~^T delta (step B). s0 / dl: this chunk's S_0 and delta
+// slots of this workgroup's column block.
 __device__ __forceinline__ void scan_chunk(const ScanOpsA& oa, const ScanOpsB& ob, f32x4 (&St)[2],
-                                           float* Sl, float* Dl, const DeltaSeqArgs& q, int b,
-                                           int hv, int c, int dv0, int w, int lane, float* spare) {
+                                           float* Sl, float* Dl, float* s0, float* dl, int w,
+                                           int lane) {
   const int row4 = lane >> 4, col = lane & 15;
-  f32x4 dacc = oa.u, oacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+    *reinterpret_cast<f32x4*>(s0 + ((2 * w + x) * 64 + lane) * 4) = St[x];
+  f32x4 dacc = oa.u;
 #pragma unroll
   for (int s = 0; s < 32; ++s) {
     const float sv = Sl[(4 * s + row4) * CBW + col];
     dacc = mfma4(oa.w[s >> 2][s & 3], sv, dacc);
-    oacc = mfma4(oa.q[s >> 2][s & 3], sv, oacc);
   }
+  *reinterpret_cast<f32x4*>(dl + (w * 64 + lane) * 4) = dacc;
 #pragma unroll
   for (int e = 0; e < 4; ++e) Dl[(16 * w + 4 * row4 + e) * CBW + col] = dacc[e];
   __syncthreads();
-  f32x4 s0 = St[0] * ob.gl, s1 = St[1] * ob.gl;
+  f32x4 s0v = St[0] * ob.gl, s1v = St[1] * ob.gl;
 #pragma unroll
   for (int s = 0; s < 16; ++s) {
     const float dv = Dl[(4 * s + row4) * CBW + col];
-    oacc = mfma4(ob.m[s >> 2][s & 3], dv, oacc);
-    s0 = mfma4(ob.k[s >> 2][s & 3], dv, s0);
-    s1 = mfma4(ob.k[4 + (s >> 2)][s & 3], dv, s1);
+    s0v = mfma4(ob.k[s >> 2][s & 3], dv, s0v);
+    s1v = mfma4(ob.k[4 + (s >> 2)][s & 3], dv, s1v);
   }
-  St[0] = s0;
-  St[1] = s1;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int t = c * DC + 16 * w + 4 * row4 + e;
-    float* dst =
-        t < q.T ? q.o + (((int64_t)b * q.Hv + hv) * q.T + t) * DN_D + dv0 + col : spare + lane;
-    *dst = oacc[e];
-  }
+  St[0] = s0v;
+  St[1] = s1v;
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -521,14 +519,14 @@ void deltanet_scan_kernel(DeltaChunkArgs a) {
     for (int e = 0; e < 4; ++e) Sl[(16 * d + 4 * row4 + e) * CBW + col] = St[x][e];
   }
   const int NC = (q.T + DC - 1) / DC;
-  const float* units = a.ws + (int64_t)(b * q.Hv + hv) * (NC + 1) * UNIT;
-  // the identity unit's spare tail (UNIT - UO_G - 1 >= 64 floats): a sink for the
-  // padded rows of the last chunks, never read
-  float* spare = a.ws + ((int64_t)(b * q.Hv + hv) * (NC + 1) + NC) * UNIT + UO_G + 1;
-  static_assert(UNIT - UO_G - 1 >= 64, "spare tail");
+  const float* units = dn_units(a, b, hv, NC);
+  // phase 3's inputs of this column block: chunk c at + c * unit + cb * block
+  float* s0b = dn_s0(a, b, hv, NC) + cb * (S0_UNIT / 8);
+  float* dlb = dn_dl(a, b, hv, NC) + cb * (DL_UNIT / 8);
   // Two register sets, chunks in pairs, each set reloaded two chunks ahead right
   // after its chunk; chunk indices past the end read the identity unit (an odd
-  // count pads with it). Branch-free, so the compiler's waits count exactly.
+  // count pads with it; its S_0 and delta go to the spare slot NC). Branch-free,
+  // so the compiler's waits count exactly.
   ScanOpsA ax, ay;
   ScanOpsB bx, by;
   scan_load_a(ax, units, w, cb, lane);
@@ -537,11 +535,12 @@ void deltanet_scan_kernel(DeltaChunkArgs a) {
   scan_load_b(by, units + (int64_t)min(1, NC) * UNIT, w, lane);
   __syncthreads();
   for (int c = 0; c < NC; c += 2) {
-    scan_chunk(ax, bx, St, Sl, Dl, q, b, hv, c, dv0, w, lane, spare);
+    scan_chunk(ax, bx, St, Sl, Dl, s0b + (int64_t)c * S0_UNIT, dlb + (int64_t)c * DL_UNIT, w, lane);
     const float* u2 = units + (int64_t)min(c + 2, NC) * UNIT;
     scan_load_a(ax, u2, w, cb, lane);
     scan_load_b(bx, u2, w, lane);
-    scan_chunk(ay, by, St, Sl, Dl, q, b, hv, c + 1, dv0, w, lane, spare);
+    const int c1 = min(c + 1, NC);
+    scan_chunk(ay, by, St, Sl, Dl, s0b + (int64_t)c1 * S0_UNIT, dlb + (int64_t)c1 * DL_UNIT, w, lane);
     const float* u3 = units + (int64_t)min(c + 3, NC) * UNIT;
     scan_load_a(ay, u3, w, cb, lane);
     scan_load_b(by, u3, w, lane);
@@ -550,6 +549,183 @@ void deltanet_scan_kernel(DeltaChunkArgs a) {
   for (int x = 0; x < 2; ++x)
     *reinterpret_cast<f32x4*>(q.s_out + sb + (int64_t)(dv0 + col) * DN_D + 16 * (2 * w + x) +
                               4 * row4) = St[x];
+}
+
+// Phase 3: one workgroup per (chunk, value head, sequence). First each wave w
+// forms rows 16 w .. 16 w + 15 of M and of gamma Q into LDS: lane l holds q row
+// i = 16 w + l % 16 at columns 16 s4 + 4 (l / 16) .. +3 (s4 < 8), the B operand
+// of P^T = K Q^T, whose result tiles (tile jt: lane l reg r = P[i][16 jt + 4
+// (l / 16) + r]) are masked and decayed into M. Then wave w forms output
+// columns 32 w .. 32 w + 31 (the scan's column blocks 2 w, 2 w + 1) of all 64
+// rows: its S_0 and delta operands (24 x 16 bytes per lane, loaded once the
+// first phase is done: fewer live registers, three workgroups per CU), and
+// gamma Q and M from LDS. With NORM the row's RMS
+// over Dv is taken from the tile staged in LDS, and y = o rstd norm_w silu(z)
+// (the layer's gated norm, as gated_rms_norm_kernel) is stored in bf16
+// instead of o.
+constexpr int OQW = DN_D + 4;  // LDS row of gamma Q (floats; 16-byte aligned, banks skewed)
+constexpr int OMW = DC + 4;    // LDS row of M
+template <bool NORM>
+__global__ __launch_bounds__(256) void deltanet_out_kernel(DeltaChunkArgs a) {
+  const DeltaSeqArgs& q = a.s;
+  const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
+  const int lane = t & 63, w = t >> 6, l16 = lane & 15, r4 = lane >> 4;
+  const int hk = hv / (q.Hv / q.Hk);
+  const int t0 = c * DC, n = min(DC, q.T - t0);
+  const int NC = (q.T + DC - 1) / DC;
+  __shared__ float Gs[DC];
+  __shared__ __attribute__((aligned(16))) float Qs[DC * OQW];  // gamma Q [i][dk]
+  __shared__ __attribute__((aligned(16))) float Ms[DC * OMW];  // M [i][j]
+  // this wave's B operands, column blocks 2 w and 2 w + 1: S_0 (d < 8) and delta (jt < 4)
+  const float* s0 = dn_s0(a, b, hv, NC) + (int64_t)c * S0_UNIT + (2 * w) * (S0_UNIT / 8);
+  const float* dl = dn_dl(a, b, hv, NC) + (int64_t)c * DL_UNIT + (2 * w) * (DL_UNIT / 8);
+  if (t < 64) Gs[t] = chunk_cumsum(q, b, hv, t0, n, t);
+  const float* qp = q.q + (((int64_t)b * q.Hk + hk) * q.T + t0) * DN_D;
+  const float* kp = q.k + (((int64_t)b * q.Hk + hk) * q.T + t0) * DN_D;
+  {
+    const int i = 16 * w + l16;  // this lane's q row
+    f32x4 qv[8];
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4)
+      qv[s4] = *reinterpret_cast<const f32x4*>(qp + (int64_t)min(i, n - 1) * DN_D + 16 * s4 + 4 * r4);
+    // P^T tiles: D[j][i] = sum_dk K[j][dk] Q[i][dk], A lane l = K[16 jt + l % 16][dk];
+    // the four tiles' chains interleaved
+    f32x4 P[4];
+    const float* kr[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      P[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      kr[jt] = kp + (int64_t)min(16 * jt + l16, n - 1) * DN_D + 4 * r4;
+    }
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {
+      f32x4 kv[4];
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) kv[jt] = *reinterpret_cast<const f32x4*>(kr[jt] + 16 * s4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) P[jt] = mfma4(kv[jt][e], qv[s4][e], P[jt]);
+    }
+    __syncthreads();  // Gs
+    // M = P D on j <= i < n, j < n (rows or keys past the chunk: 0); lane l reg r
+    // of tile jt is (i, j = 16 jt + 4 (l / 16) + r)
+    const float Gi = Gs[i];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      f32x4 m;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * jt + 4 * r4 + r;
+        m[r] = (j <= i && i < n) ? P[jt][r] * expf(Gi - Gs[j]) : 0.f;
+      }
+      *reinterpret_cast<f32x4*>(&Ms[i * OMW + 16 * jt + 4 * r4]) = m;
+    }
+    const float gi = i < n ? expf(Gi) : 0.f;  // gamma_i (rows past the chunk: 0)
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4)
+      *reinterpret_cast<f32x4*>(&Qs[i * OQW + 16 * s4 + 4 * r4]) = qv[s4] * gi;
+  }
+  f32x4 sb[2][8], db[2][4];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+      sb[x][d] = *reinterpret_cast<const f32x4*>(s0 + x * (S0_UNIT / 8) + (d * 64 + lane) * 4);
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+      db[x][jt] = *reinterpret_cast<const f32x4*>(dl + x * (DL_UNIT / 8) + (jt * 64 + lane) * 4);
+  }
+  __syncthreads();
+  // O = gamma Q S_0 + M delta: row tile rt, column block 2 w + x; eight
+  // independent accumulators between dependent products
+  f32x4 O[4][2];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int x = 0; x < 2; ++x) O[rt][x] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    f32x4 av[4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+      av[rt] = *reinterpret_cast<const f32x4*>(&Qs[(16 * rt + l16) * OQW + 16 * d + 4 * r4]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int x = 0; x < 2; ++x) O[rt][x] = mfma4(av[rt][e], sb[x][d][e], O[rt][x]);
+  }
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) {
+    f32x4 av[4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+      av[rt] = *reinterpret_cast<const f32x4*>(&Ms[(16 * rt + l16) * OMW + 16 * jt + 4 * r4]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int x = 0; x < 2; ++x) O[rt][x] = mfma4(av[rt][e], db[x][jt][e], O[rt][x]);
+  }
+  // lane l reg r of O[rt][x] = O[16 rt + 4 (l / 16) + r][32 w + 16 x + l % 16]: the
+  // tile goes through LDS (the gamma Q rows, free once every wave is past its
+  // products) so that a thread then holds 32 contiguous columns of one row
+  __syncthreads();
+  float* Os = Qs;
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int x = 0; x < 2; ++x) Os[(16 * rt + 4 * r4 + r) * OQW + 32 * w + 16 * x + l16] = O[rt][x][r];
+  __syncthreads();
+  const int row = t >> 2, c0 = 32 * (t & 3);  // thread t: row t / 4, columns c0 .. c0 + 31
+  float o[32];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(&Os[row * OQW + c0 + 4 * j]);
+    o[4 * j] = v[0]; o[4 * j + 1] = v[1]; o[4 * j + 2] = v[2]; o[4 * j + 3] = v[3];
+  }
+  const int64_t tok = t0 + row;
+  if constexpr (!NORM) {
+    if (row < n) {
+      float* op = q.o + (((int64_t)b * q.Hv + hv) * q.T + tok) * DN_D + c0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        *reinterpret_cast<float4*>(op + 4 * j) = make_float4(o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]);
+    }
+  } else {
+    const GatedNormArgs& g = a.g;
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) ss += o[j] * o[j];
+    ss += __shfl_xor(ss, 1);  // the row's four threads
+    ss += __shfl_xor(ss, 2);
+    const float rstd = 1.0f / sqrtf(ss / (float)DN_D + g.eps);
+    if (row < n) {
+      const uint16_t* z = g.z + (int64_t)b * g.z_sb + tok * g.z_st + hv * DN_D + c0;
+      uint16_t* y = g.y + (int64_t)b * g.y_sb + tok * g.y_st + hv * DN_D + c0;
+      if (((reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(y) |
+            reinterpret_cast<uintptr_t>(g.norm_w)) & 15u) == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float zf[8], wf[8], yv[8];
+          unpack8(*reinterpret_cast<const uint4*>(z + 8 * j), zf);
+          unpack8(*reinterpret_cast<const uint4*>(g.norm_w + c0 + 8 * j), wf);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) yv[e] = o[8 * j + e] * rstd * wf[e] * accurate_silu(zf[e]);
+          *reinterpret_cast<uint4*>(y + 8 * j) = pack8(yv);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+          y[j] = f2bf(o[j] * rstd * bf2f(g.norm_w[c0 + j]) * accurate_silu(bf2f(z[j])));
+      }
+    }
+  }
 }
 
 // ---- the prefill's inputs to the recurrence (qwen35.jl:347-356): one wave per
@@ -876,8 +1052,9 @@ hipError_t launch_deltanet_sequence(const DeltaSeqArgs& a, hipStream_t st) {
 }
 
 size_t deltanet_chunk_workspace_bytes(int T, int Hv, int B) {
-  const int64_t NC = (T + DC - 1) / DC;
-  return (size_t)(NC + 1) * Hv * B * UNIT * sizeof(float);  // + the identity unit per head
+  const int NC = (T + DC - 1) / DC;  // each per (b, hv): the units (+ the identity), S_0, delta
+  return (size_t)((dn_units_floats(NC) + dn_s0_floats(NC) + dn_dl_floats(NC)) * Hv * B) *
+         sizeof(float);
 }
 
 hipError_t launch_deltanet_sequence_chunked(const DeltaChunkArgs& a, hipStream_t st) {
@@ -888,6 +1065,12 @@ hipError_t launch_deltanet_sequence_chunked(const DeltaChunkArgs& a, hipStream_t
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(deltanet_scan_kernel, dim3(q.Hv * q.B * (DN_D / CBW)), dim3(256), 0, st, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (a.g.y)
+    hipLaunchKernelGGL(deltanet_out_kernel<true>, dim3(NC, q.Hv, q.B), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(deltanet_out_kernel<false>, dim3(NC, q.Hv, q.B), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -397,6 +397,9 @@ int linear_conv_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, co
 struct DeltaChunkArgs {
   DeltaSeqArgs s;
   float* ws;
+  // g.y set: the gated RMSNorm with z (qwen35.jl:360-364) is fused into the
+  // output phase, which writes y (bf16) instead of s.o; g.o is unused
+  GatedNormArgs g;
 };
 size_t deltanet_chunk_workspace_bytes(int T, int Hv, int B);
 hipError_t launch_deltanet_sequence_chunked(const DeltaChunkArgs& a, hipStream_t st);

@@ -979,11 +979,13 @@ size_t vm_deltanet_sequence_workspace_bytes(int T, int Hv, int B) {
   return vm::deltanet_chunk_workspace_bytes(T, Hv, B);
 }
 
-int vm_deltanet_sequence_chunked(float* o, const float* q, const float* k, const float* v,
-                                 const float* beta, const float* gate, const float* s_in,
-                                 float* s_out, int Dk, int Dv, int T, int Hk, int Hv, int B,
-                                 void* workspace, size_t workspace_bytes, vm_stream st) {
-  const char* what = "deltanet_sequence_chunked";
+namespace {
+// the chunked recurrence; with g.y set, the gated RMSNorm fused into its output
+// phase (o unused)
+int deltanet_chunked(const char* what, float* o, const float* q, const float* k, const float* v,
+                     const float* beta, const float* gate, const float* s_in, float* s_out, int Dk,
+                     int Dv, int T, int Hk, int Hv, int B, void* workspace, size_t workspace_bytes,
+                     const vm::GatedNormArgs& g, vm_stream st) {
   TRY(check_dn_heads(Dk, Dv, Hk, Hv, B, what));
   REQUIRE(T >= 0, VM_E_ARG, "%s: T = %d", what, T);
   if (B == 0) return VM_OK;
@@ -991,7 +993,7 @@ int vm_deltanet_sequence_chunked(float* o, const float* q, const float* k, const
   TRY(check_aligned(s_out, "S_out"));
   TRY(check_alias(s_in, s_out, (size_t)B * Hv * Dk * Dv * sizeof(float), what));
   if (T > 0) {
-    TRY(check_aligned(o, "O"));
+    if (!g.y) TRY(check_aligned(o, "O"));
     TRY(check_aligned(q, "Q"));
     TRY(check_aligned(k, "K"));
     TRY(check_aligned(v, "V"));
@@ -1005,9 +1007,48 @@ int vm_deltanet_sequence_chunked(float* o, const float* q, const float* k, const
   a.s.o = o; a.s.q = q; a.s.k = k; a.s.v = v; a.s.beta = beta; a.s.gate = gate; a.s.s_in = s_in;
   a.s.s_out = s_out; a.s.T = T; a.s.Hk = Hk; a.s.Hv = Hv; a.s.B = B;
   a.ws = static_cast<float*>(workspace);
+  a.g = g;
   return hip_status(
       timed(VM_K_DELTANET, S(st), [&] { return vm::launch_deltanet_sequence_chunked(a, S(st)); }),
       what);
+}
+}  // namespace
+
+int vm_deltanet_sequence_chunked(float* o, const float* q, const float* k, const float* v,
+                                 const float* beta, const float* gate, const float* s_in,
+                                 float* s_out, int Dk, int Dv, int T, int Hk, int Hv, int B,
+                                 void* workspace, size_t workspace_bytes, vm_stream st) {
+  const vm::GatedNormArgs none{};
+  return deltanet_chunked("deltanet_sequence_chunked", o, q, k, v, beta, gate, s_in, s_out, Dk, Dv,
+                          T, Hk, Hv, B, workspace, workspace_bytes, none, st);
+}
+
+int vm_deltanet_sequence_chunked_gated_norm(vm_bf16* y, int64_t y_st, int64_t y_sb,
+                                            const vm_bf16* z, int64_t z_st, int64_t z_sb,
+                                            const vm_bf16* norm_w, float eps, const float* q,
+                                            const float* k, const float* v, const float* beta,
+                                            const float* gate, const float* s_in, float* s_out,
+                                            int Dk, int Dv, int T, int Hk, int Hv, int B,
+                                            void* workspace, size_t workspace_bytes, vm_stream st) {
+  const char* what = "deltanet_sequence_chunked_gated_norm";
+  TRY(check_dn_heads(Dk, Dv, Hk, Hv, B, what));
+  REQUIRE(T >= 0, VM_E_ARG, "%s: T = %d", what, T);
+  if (B > 0 && T > 0) {
+    REQUIRE(y && z && norm_w, VM_E_ARG, "%s: NULL Y, Z or NormWeight", what);
+    for (const void* p : {(const void*)y, (const void*)z, (const void*)norm_w})
+      REQUIRE((reinterpret_cast<uintptr_t>(p) & 1u) == 0, VM_E_ARG, "%s: Y, Z and NormWeight must "
+              "be 2-byte aligned", what);
+    REQUIRE(y_st >= 0 && y_sb >= 0 && z_st >= 0 && z_sb >= 0, VM_E_ARG, "%s: negative stride",
+            what);
+    REQUIRE((T <= 1 || (y_st >= (int64_t)Hv * Dv && z_st >= (int64_t)Hv * Dv)) &&
+                (B <= 1 || (y_sb >= y_st * T && z_sb >= z_st * T)),
+            VM_E_DIM, "%s: strides below the extents", what);
+  }
+  vm::GatedNormArgs g{};
+  g.z = z; g.z_st = z_st; g.z_sb = z_sb; g.norm_w = norm_w; g.y = y; g.y_st = y_st; g.y_sb = y_sb;
+  g.T = T; g.Hv = Hv; g.B = B; g.eps = eps;
+  return deltanet_chunked(what, nullptr, q, k, v, beta, gate, s_in, s_out, Dk, Dv, T, Hk, Hv, B,
+                          workspace, workspace_bytes, g, st);
 }
 
 int vm_deltanet_prefill_prep(float* qe, float* ke, float* ve, float* beta, float* gate,

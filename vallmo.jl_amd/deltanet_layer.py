@@ -184,11 +184,12 @@ def forward(l: DeltaNetLayer, c: DeltaNetConfig, xn, T: int, B: int, *, eps: flo
          "Gate": torch.empty((B, T, c.Hv), **f32)}
     ops.deltanet_prefill_prep_(p, conv, ab, l.A_log, l.dt_bias, Dk=c.Dk, Dv=c.Dv, Hk=c.Hk,
                                Hv=c.Hv)
-    o = torch.empty((B, c.Hv, T, c.Dv), **f32)
-    ops.deltanet_sequence_chunked_({"O": o, "Sp": l.S}, p["Q"], p["K"], p["V"], p["Beta"],
-                                   p["Gate"], l.S)
     y = torch.empty((B, T, c.Hv, c.Dv), dtype=torch.bfloat16, device=xn.device)
-    ops.gated_rms_norm_(y, o, z.unflatten(-1, (c.Hv, c.Dv)), l.gnorm_w, eps=eps)
+    # the recurrence in place on S with the gated norm fused into its output
+    # kernel (:357-364: O never reaches memory)
+    ops.deltanet_sequence_chunked_gated_norm_({"Y": y, "Sp": l.S}, z.unflatten(-1, (c.Hv, c.Dv)),
+                                              l.gnorm_w, p["Q"], p["K"], p["V"], p["Beta"],
+                                              p["Gate"], l.S, eps=eps)
     y2 = y.view(B * T, c.Hv * c.Dv)
     return ops.linear(y2, l.Wout, workspace=workspace_for(y2, l.Wout))["y"].view(B, T, D)
 

@@ -31,6 +31,7 @@ __all__ = [
     "deltanet_recurrent_decode", "deltanet_sequence_", "deltanet_sequence",
     "deltanet_prefill_prep_", "gated_rms_norm_", "linear_add_rms_norm_",
     "deltanet_sequence_chunked_", "deltanet_sequence_workspace_bytes",
+    "deltanet_sequence_chunked_gated_norm_",
     "linear_add_rms_norm_workspace_bytes",
 ]
 
@@ -676,8 +677,9 @@ def deltanet_sequence_(outs, Q, K, V, Beta, Gate, S):
 
 
 def deltanet_sequence_workspace_bytes(T: int, Hv: int, B: int) -> int:
-    """Workspace of deltanet_sequence_chunked_ (147 968 B per 64-token chunk per
-    value head and sequence)."""
+    """Workspace of deltanet_sequence_chunked_ (about 197 KB per 64-token chunk per
+    value head and sequence: the scan's operands, each chunk's start state and
+    its delta)."""
     return int(_lib.load().vm_deltanet_sequence_workspace_bytes(T, Hv, B))
 
 
@@ -704,6 +706,40 @@ def deltanet_sequence(Q, K, V, Beta, Gate, S, *, Sp=None) -> dict:
     O = torch.empty(V.shape, dtype=torch.float32, device=V.device)
     return deltanet_sequence_({"O": O, "Sp": torch.empty_like(S) if Sp is None else Sp}, Q, K, V,
                               Beta, Gate, S)
+
+
+def deltanet_sequence_chunked_gated_norm_(outs, Z, NormWeight, Q, K, V, Beta, Gate, S, *, eps,
+                                          workspace=None):
+    """forward(::DeltaNetLayer)'s recurrence and gated norm in one call
+    (src/llm/qwen35.jl:357-364): deltanet_sequence! in its chunked form with
+    y = O rstd NormWeight silu(Z) applied in the output kernel, so O never
+    reaches memory. outs "Y" :: (Dv, Hv, T, B) bf16 (torch (B, T, Hv, Dv), token
+    and sequence dims may be strided, heads contiguous), "Sp" the state out
+    (may be S); Z like Y; Q, K, V, Beta, Gate, S as deltanet_sequence_chunked_."""
+    Y, Sp = _out(outs, "Y"), _out(outs, "Sp")
+    dims = sizes(Y=(Y, "Dv Hv T B"), Z=(Z, "Dv Hv T B"), NormWeight=(NormWeight, "Dv"),
+                 Q=(Q, "Dk T Hk B"), K=(K, "Dk T Hk B"), V=(V, "Dv T Hv B"),
+                 Beta=(Beta, "Hv T B"), Gate=(Gate, "Hv T B"), S=(S, "Dk Dv Hv B"),
+                 Sp=(Sp, "Dk Dv Hv B"))
+    Dk, Dv, Hk, Hv, T, B = (dims[n] for n in ("Dk", "Dv", "Hk", "Hv", "T", "B"))
+    if Hv % Hk:
+        raise DimensionMismatch(f"value heads ({Hv}) is not a multiple of key heads ({Hk})")
+    for t, n in ((Q, "Q"), (K, "K"), (V, "V"), (Beta, "Beta"), (Gate, "Gate"), (S, "S"),
+                 (Sp, "S′")):
+        _need(t, torch.float32, n)
+        _need_contig(t, n)
+    for t, n in ((Z, "Z"), (Y, "Y"), (NormWeight, "NormWeight")):
+        _need(t, torch.bfloat16, n)
+        if t.dim() == 4 and t.stride(2) != Dv:
+            raise ArgumentError(f"{n}: heads must be contiguous")
+    need = deltanet_sequence_workspace_bytes(T, Hv, B)
+    if workspace is None:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=Q.device)
+    call("vm_deltanet_sequence_chunked_gated_norm", _p(Y), _st(Y, 1, Hv * Dv),
+         _st(Y, 0, T * Hv * Dv), _p(Z), _st(Z, 1, Hv * Dv), _st(Z, 0, T * Hv * Dv),
+         _p(NormWeight), float(eps), _p(Q), _p(K), _p(V), _p(Beta), _p(Gate), _p(S), _p(Sp), Dk,
+         Dv, T, Hk, Hv, B, _p(workspace), workspace.numel(), _stream())
+    return outs
 
 
 def deltanet_prefill_prep_(outs, CV, AB, A_log, DtBias, *, Dk, Dv, Hk, Hv):
