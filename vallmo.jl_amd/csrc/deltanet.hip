@@ -249,23 +249,25 @@ __global__ __launch_bounds__(256) void deltanet_sequence_kernel(DeltaSeqArgs a) 
 // then O = gamma Q S_0 + M delta with M_ij = D_ij q_i.k_j (j <= i), and
 // S_C = gamma_C S_0 + K~^T delta with K~_j = (gamma_C / gamma_j) k_j (exact
 // algebra of the sequential update; fp32 throughout). Three launches:
-// Phase 1 (deltanet_chunk_kernel, chunk-parallel): the Gram K K^T, the
-// triangular solve, and the operands of the state chain (-W, K~^T, U,
-// gamma_C) written in the fp32 MFMA operand order of v_mfma_f32_16x16x4f32
-// (A lane l = A[l % 16][l / 16], B lane l = B[l / 16][l % 16], D lane l reg r
-// = D[4 (l / 16) + r][l % 16]), 16 bytes per lane per four k-steps, so phase 2
-// reads 1 KB contiguous per wave load.
+// Phase 1 (deltanet_chunk_kernel, chunk-parallel): the Gram K K^T and the
+// products [U | W] = T [beta V | beta gamma K] with T = (I + L)^-1 on the bf16
+// MFMA in split precision (see phase 3), T itself by fp32 forward
+// substitution, and the operands of the state chain (-W, K~^T, U, gamma_C)
+// written in the fp32 MFMA operand order of v_mfma_f32_16x16x4f32 (A lane l =
+// A[l % 16][l / 16], B lane l = B[l / 16][l % 16], D lane l reg r = D[4 (l /
+// 16) + r][l % 16]), 16 bytes per lane per four k-steps, so phase 2 reads 1 KB
+// contiguous per wave load.
 // Phase 2 (deltanet_scan_kernel, sequential over chunks): one workgroup per 16
 // state columns of a value head; per chunk 64 MFMAs per wave (delta, then the
 // state), writing each chunk's start state S_0 and its delta for phase 3, the
 // next chunk's operands loading into a second register set meanwhile.
 // Phase 3 (deltanet_out_kernel, chunk-parallel): Q K^T, M and O = gamma Q S_0 +
-// M delta on the same MFMA, then either O (fp32, the operator's output) or,
-// fused, the layer's gated RMSNorm with z (qwen35.jl:360-364) in bf16. The
-// products take their k index as 16 s4 + 4 (l / 16) + e for lane l, register e
-// of the f32x4 of group s4 (any order of the k sum is the same product), so
-// every operand is one 16-byte load of 4 contiguous floats: q and k rows,
-// and S_0 and delta exactly as the scan holds them in its accumulators.
+// M delta on the bf16 MFMA (v_mfma_f32_16x16x32_bf16) in split precision:
+// each fp32 operand x is hi = bf16(x) and lo = bf16(x - hi), and a product is
+// hi hi + hi lo + lo hi with fp32 accumulation (about 2^-16 relative per
+// product), then either O (fp32, the operator's output) or, fused, the layer's
+// gated RMSNorm with z (qwen35.jl:360-364) in bf16. The scan writes S_0 and
+// delta already split, in that MFMA's B operand order.
 namespace {
 constexpr int DC = 64;   // chunk length
 constexpr int CBW = 16;  // state columns per scan workgroup
@@ -275,15 +277,14 @@ constexpr int UO_K = 8192;   // K~^T:     [d 8][s4 4][lane][4], A[i = dk][k = r]
 constexpr int UO_U = 16384;  // U:        [cb 8][w 4][lane][4], D[r][dv] tiles
 constexpr int UO_G = 24576;  // gamma_C
 constexpr int UNIT = 24640;  // floats per unit (98 560 B, a multiple of 256)
-// per (chunk, value head, sequence), written by the scan for phase 3, floats:
-// S_0 [cb 8][d 8][lane][4] (lane l reg e = S_0[16 d + 4 (l / 16) + e][16 cb + l % 16])
-// and delta [cb 8][w 4][lane][4] (lane l reg e = delta[16 w + 4 (l / 16) + e][16 cb + l % 16])
+// per (chunk, value head, sequence), written by the scan for phase 3, in
+// float-sized units: S_0 and delta split into bf16 hi and lo parts, in the B
+// operand order of v_mfma_f32_16x16x32_bf16 for column block cb and 32-deep k
+// step ks: [cb 8][ks][hl 2][lane 64][8] bf16 with lane l element j =
+// X[32 ks + 8 (l / 16) + j][16 cb + l % 16] (hl 0: hi, 1: lo); ks < 4 for S_0
+// (k = dk), ks < 2 for delta (k = the chunk's token)
 constexpr int S0_UNIT = DN_D * DN_D;
 constexpr int DL_UNIT = DC * DN_D;
-
-__device__ __forceinline__ int pos_acc(int r, int dv) {  // D[r][dv], 16 x 16 tiles
-  return ((((dv >> 4) * 4 + (r >> 4)) * 64) + 16 * ((r & 15) >> 2) + (dv & 15)) * 4 + (r & 3);
-}
 
 // the chunk's inclusive cumulative log decay (wave 0, one token per lane; log
 // decays below -110 are taken as -110: expf underflows to exactly 0 below
@@ -320,9 +321,54 @@ __device__ __forceinline__ float* dn_dl(const DeltaChunkArgs& a, int b, int hv, 
          ((int64_t)b * a.s.Hv + hv) * dn_dl_floats(NC);
 }
 
-__global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
+namespace {
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+// 4 fp32 values as bf16 hi and lo parts (x = hi + lo to about 2^-16), 4 each
+__device__ __forceinline__ void split4(const f32x4& x, uint2& hi, uint2& lo) {
+  hi = make_uint2(pack2(x[0], x[1]), pack2(x[2], x[3]));
+  lo = make_uint2(pack2(x[0] - __uint_as_float(hi.x << 16), x[1] - __uint_as_float(hi.x & 0xffff0000u)),
+                  pack2(x[2] - __uint_as_float(hi.y << 16), x[3] - __uint_as_float(hi.y & 0xffff0000u)));
+}
+__device__ __forceinline__ void split8(const f32x4& a, const f32x4& b, uint4& hi, uint4& lo) {
+  uint2 h0, l0, h1, l1;
+  split4(a, h0, l0);
+  split4(b, h1, l1);
+  hi = make_uint4(h0.x, h0.y, h1.x, h1.y);
+  lo = make_uint4(l0.x, l0.y, l1.x, l1.y);
+}
+// acc += A B in split precision (hi hi + hi lo + lo hi) on v_mfma_f32_16x16x32_bf16
+// (A lane l = A[l % 16][8 (l / 16) + j], B lane l = B[8 (l / 16) + j][l % 16], D
+// lane l reg r = D[4 (l / 16) + r][l % 16])
+__device__ __forceinline__ f32x4 mfma_x3(const uint4& ah, const uint4& al, const uint4& bh,
+                                         const uint4& bl, f32x4 acc) {
+  acc = mfma16(al, bh, acc);
+  acc = mfma16(ah, bl, acc);
+  return mfma16(ah, bh, acc);
+}
+constexpr int KSW = DN_D + 4;  // LDS row of K (floats; 16-byte aligned, banks skewed)
+constexpr int LSW = DC + 4;    // LDS row of L (floats)
+constexpr int TW = DC + 8;     // LDS row of T hi / lo (bf16)
+}  // namespace
+
+// One workgroup per (chunk, value head, sequence). Wave w forms Gram row block
+// w into L (L[i][j] = beta_i gamma_i / gamma_j k_i . k_j below the diagonal),
+// then wave 3 solves (I + L) T = I, lane c for column c, in fp32 (row i + 1 of
+// L read from LDS while row i is reduced), and stores T split into bf16 hi /
+// lo over L, while waves 0-2 write K~^T and gather their operands of the
+// products below. Then waves 0, 1 form U = T (beta V) (value columns 64 w ..)
+// in the scan's accumulator order, and waves 2, 3 form W^T = (beta gamma K)^T
+// T^T (key columns 64 (w - 2) ..): their A operand lane l gathers key column
+// 16 ct + (l % 16) / 4 + 4 (l % 4), so that result lane l reg r is W[i][16 ct +
+// l / 16 + 4 r], the -W operand order of the scan.
+// (three waves per SIMD: the phases are latency-bound, and three workgroups fit a CU's LDS)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+void deltanet_chunk_kernel(DeltaChunkArgs a) {
   const DeltaSeqArgs& q = a.s;
   const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
+  const int lane = t & 63, l16 = lane & 15, r4 = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: scalar branches
   const int hk = hv / (q.Hv / q.Hk);
   const int t0 = c * DC, n = min(DC, q.T - t0);
   const int NC = (q.T + DC - 1) / DC;
@@ -334,99 +380,201 @@ __global__ __launch_bounds__(256) void deltanet_chunk_kernel(DeltaChunkArgs a) {
     __syncthreads();
     if (t == 0) id[UO_G] = 1.f;
   }
-  // K (later the -W rows) and L in LDS, ~51 KB: three workgroups per CU
-  __shared__ __attribute__((aligned(16))) float Ks[DC][132];
-  __shared__ float Ls[DC][DC + 1];
-  __shared__ float Gs[DC], Bs[DC], Es[DC];
+  // K rows, and L, later T (hi, lo) in its place: ~52 KB, three workgroups per CU
+  __shared__ __attribute__((aligned(16))) float Ks[DC * KSW];
+  __shared__ __attribute__((aligned(16))) float LT[DC * TW];
+  static_assert(sizeof(LT) >= DC * LSW * sizeof(float), "L");
+  __shared__ __attribute__((aligned(16))) float Gs[DC], Bs[DC], Es[DC];
+  uint16_t* const Th = reinterpret_cast<uint16_t*>(LT);
+  uint16_t* const Tl = Th + DC * TW;
   const float* kp = q.k + (((int64_t)b * q.Hk + hk) * q.T + t0) * DN_D;
-  for (int i = t; i < DC * 32; i += 256) {  // float4 (row i / 32, column group i % 32)
-    const int r = i >> 5, c4 = i & 31, rr = min(r, n - 1);  // rows past the end read as 0
-    float4 kv = *reinterpret_cast<const float4*>(kp + rr * DN_D + 4 * c4);
-    if (r >= n) kv = make_float4(0.f, 0.f, 0.f, 0.f);
-    *reinterpret_cast<float4*>(&Ks[r][4 * c4]) = kv;
-  }
-  if (t < 64) {  // wave 0: gates, inclusive cumulative sum of the log decay
-    const float G = chunk_cumsum(q, b, hv, t0, n, t);
-    const int64_t g = ((int64_t)b * q.T + t0 + min(t, n - 1)) * q.Hv + hv;
-    Gs[t] = G;
-    Bs[t] = t < n ? q.beta[g] : 0.f;
-    Es[t] = expf(G);
+  {  // K: float4 t + 256 m = (row, column group) ((t + 256 m) / 32, t % 32), all loads in flight at once
+    float4 kv[DC / 8];
+#pragma unroll
+    for (int m = 0; m < DC / 8; ++m)
+      kv[m] = *reinterpret_cast<const float4*>(kp + min((t >> 5) + 8 * m, n - 1) * DN_D + 4 * (t & 31));
+    float bt = 0.f;
+    if (t < 64) {  // wave 0: beta, gates, inclusive cumulative sum of the log decay
+      bt = q.beta[((int64_t)b * q.T + t0 + min(t, n - 1)) * q.Hv + hv];
+      const float G = chunk_cumsum(q, b, hv, t0, n, t);
+      Gs[t] = G;
+      Bs[t] = t < n ? bt : 0.f;
+      Es[t] = expf(G);
+    }
+#pragma unroll
+    for (int m = 0; m < DC / 8; ++m) {  // rows past the end read as 0
+      const int r = (t >> 5) + 8 * m;
+      *reinterpret_cast<float4*>(&Ks[r * KSW + 4 * (t & 31)]) = r < n ? kv[m] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
   }
   __syncthreads();
-  // Gram K K^T: thread (bi, bj) takes rows bi + 16x, columns bj + 16y, x, y < 4
-  const int bi = t >> 4, bj = t & 15;
-  float A[4][4];
+  {  // Gram tiles (w, jt), jt <= w: lane l reg r = k_i . k_j, i = 16 w + 4 (l / 16) + r, j = 16 jt + l % 16
+    uint4 ah[4], al[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const float* kr = &Ks[(16 * w + l16) * KSW + 32 * ks + 8 * r4];
+      split8(*reinterpret_cast<const f32x4*>(kr), *reinterpret_cast<const f32x4*>(kr + 4), ah[ks], al[ks]);
+    }
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      if (jt > w) break;
+      f32x4 G = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const float* kr = &Ks[(16 * jt + l16) * KSW + 32 * ks + 8 * r4];
+        uint4 bh, bl;
+        split8(*reinterpret_cast<const f32x4*>(kr), *reinterpret_cast<const f32x4*>(kr + 4), bh, bl);
+        G = mfma_x3(ah[ks], al[ks], bh, bl, G);
+      }
+      const int j = 16 * jt + l16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * w + 4 * r4 + r;
+        LT[i * LSW + j] = i > j ? Bs[i] * expf(Gs[i] - Gs[j]) * G[r] : 0.f;
+      }
+    }
+  }
+  __syncthreads();
+  // the products' operands from V or K (rows j = 32 ks + 8 (l / 16) + e of R),
+  // scaled and split: waves 0, 1 B = beta_j V[j][64 w + 16 ct + l % 16] (rows past
+  // the end: beta = 0), waves 2, 3 A = beta_j gamma_j K[j][key column]
+  const bool uw = w < 2;
+  uint4 rh[2][4], rl[2][4];  // [ks][ct]
+  auto gather = [&]() __attribute__((always_inline)) {
+    const float* vp = q.v + (((int64_t)b * q.Hv + hv) * q.T + t0) * DN_D + 64 * (w & 1) + l16;
+    const int pc = 64 * (w & 1) + (l16 >> 2) + 4 * (l16 & 3);  // gathered key column, + 16 ct
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int j0 = 32 * ks + 8 * r4;
+      f32x4 s0 = *reinterpret_cast<const f32x4*>(&Bs[j0]), s1 = *reinterpret_cast<const f32x4*>(&Bs[j0 + 4]);
+      if (!uw) {
+        s0 = s0 * *reinterpret_cast<const f32x4*>(&Es[j0]);
+        s1 = s1 * *reinterpret_cast<const f32x4*>(&Es[j0 + 4]);
+      }
+      f32x4 r0[4], r1[4];
+      if (uw) {
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            r0[ct][e] = vp[(int64_t)min(j0 + e, n - 1) * DN_D + 16 * ct];
+            r1[ct][e] = vp[(int64_t)min(j0 + 4 + e, n - 1) * DN_D + 16 * ct];
+          }
+      } else {
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            r0[ct][e] = Ks[(j0 + e) * KSW + pc + 16 * ct];
+            r1[ct][e] = Ks[(j0 + 4 + e) * KSW + pc + 16 * ct];
+          }
+      }
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) split8(r0[ct] * s0, r1[ct] * s1, rh[ks][ct], rl[ks][ct]);
+    }
+  };
+  if (w == 3) {
+    // (I + L) T = I: lane c holds column c (rows above c stay 0, T[c][c] = 1).
+    // The float4s of L's rows 1 .. 63 (j < i) are read in order through a ring
+    // of SD registers, SD ahead of their use (the cursor (pi, pj) is a
+    // constant once the loops are unrolled). All four lanes of a float4 enter
+    // the sums: the ones at j >= i hold L's zeros above the diagonal (the Gram
+    // tiles on it are written whole) times x[j] = 0, and a load whose every
+    // register is used keeps the allocator from reloading into one in flight.
+    constexpr int SD = 12;
+    float x[DC];
+#pragma unroll
+    for (int i = 0; i < DC; ++i) x[i] = 0.f;
+    f32x4 ring[SD];
+    int pi = 1, pj = 0;  // next float4 to read: row pi, columns 4 pj ..
+#pragma unroll
+    for (int d = 0; d < SD; ++d) {
+      ring[d] = *reinterpret_cast<const f32x4*>(&LT[pi * LSW + 4 * pj]);
+      if (4 * (pj + 1) < pi) ++pj; else { ++pi; pj = 0; }
+    }
+    x[0] = lane == 0 ? 1.f : 0.f;
+    int idx = 0;
+#pragma unroll
+    for (int i = 1; i < DC; ++i) {
+      float acc[4] = {i == lane ? 1.f : 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j4 = 0; 4 * j4 < i; ++j4) {
+        const f32x4 l4 = ring[idx % SD];
+        if (pi < DC) {
+          ring[idx % SD] = *reinterpret_cast<const f32x4*>(&LT[pi * LSW + 4 * pj]);
+          if (4 * (pj + 1) < pi) ++pj; else { ++pi; pj = 0; }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] -= l4[e] * x[4 * j4 + e];
+        ++idx;
+      }
+      x[i] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    }
+    // T rows, split: columns (c & ~1, c | 1) as one pair, lane c even stores the
+    // hi pair, odd the lo pair (L is dead: every read of it is above)
+#pragma unroll
+    for (int i = 0; i < DC; ++i) {
+      const float xo = __shfl_xor(x[i], 1);
+      const float x0 = (lane & 1) ? xo : x[i], x1 = (lane & 1) ? x[i] : xo;
+      const uint32_t hi = pack2(x0, x1);
+      const uint32_t lo = pack2(x0 - __uint_as_float(hi << 16), x1 - __uint_as_float(hi & 0xffff0000u));
+      *reinterpret_cast<uint32_t*>(((lane & 1) ? Tl : Th) + i * TW + (lane & ~1)) = (lane & 1) ? lo : hi;
+    }
+  } else {
+    // K~^T in operand order, one coalesced float4 per lane and slot
+    const float Gl = Gs[DC - 1];
+    for (int f = t; f < 2048; f += 192) {
+      const int l = f & 63;
+      // tile f / 256, s4 (f / 64) % 4: dk 16 d + l % 16, r = 16 s4 + l / 16 + 4 e
+      const int dk = 16 * (f >> 8) + (l & 15), rb = 16 * ((f >> 6) & 3) + (l >> 4);
+      float v4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v4[e] = expf(Gl - Gs[rb + 4 * e]) * Ks[(rb + 4 * e) * KSW + dk];
+      *reinterpret_cast<float4*>(u + UO_K + 4 * f) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+    }
+    if (t == 0) u[UO_G] = expf(Gl);
+    gather();
+  }
+  __syncthreads();
+  if (w == 3) gather();
+  f32x4 acc[4][4];  // [row tile][column tile] (U) or [column tile][row tile] (W^T)
 #pragma unroll
   for (int x = 0; x < 4; ++x)
 #pragma unroll
-    for (int y = 0; y < 4; ++y) A[x][y] = 0.f;
-  for (int kk = 0; kk < DN_D; kk += 4) {
-    float4 ki[4], kj[4];
+    for (int y = 0; y < 4; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      ki[x] = *reinterpret_cast<const float4*>(&Ks[bi + 16 * x][kk]);
-      kj[x] = *reinterpret_cast<const float4*>(&Ks[bj + 16 * x][kk]);
+  for (int ks = 0; ks < 2; ++ks) {
+    const int j0 = 32 * ks + 8 * r4;
+    uint4 th[4], tl[4];  // T[16 rt + l % 16][j0 ..]
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      th[rt] = *reinterpret_cast<const uint4*>(&Th[(16 * rt + l16) * TW + j0]);
+      tl[rt] = *reinterpret_cast<const uint4*>(&Tl[(16 * rt + l16) * TW + j0]);
     }
 #pragma unroll
-    for (int x = 0; x < 4; ++x)
+    for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-      for (int y = 0; y < 4; ++y)
-        A[x][y] += ki[x].x * kj[y].x + ki[x].y * kj[y].y + ki[x].z * kj[y].z + ki[x].w * kj[y].w;
+      for (int rt = 0; rt < 4; ++rt) {
+        if (uw)
+          acc[rt][ct] = mfma_x3(th[rt], tl[rt], rh[ks][ct], rl[ks][ct], acc[rt][ct]);
+        else
+          acc[ct][rt] = mfma_x3(rh[ks][ct], rl[ks][ct], th[rt], tl[rt], acc[ct][rt]);
+      }
   }
+  if (uw) {  // U tile (rt, column block 4 w + ct): lane l reg r = U[16 rt + 4 (l / 16) + r][..]
 #pragma unroll
-  for (int x = 0; x < 4; ++x)
+    for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (int y = 0; y < 4; ++y) {
-      const int i = bi + 16 * x, j = bj + 16 * y;
-      const float d = j <= i ? expf(Gs[i] - Gs[j]) : 0.f;  // gamma_i / gamma_j
-      Ls[i][j] = i > j ? Bs[i] * d * A[x][y] : 0.f;
-    }
-  // K~^T in operand order, one coalesced float4 per lane and slot
-  const float Gl = Gs[DC - 1];
-  for (int f = t; f < 2048; f += 256) {
-    const int l = f & 63;
-    // tile f / 256, s4 (f / 64) % 4: dk 16 d + l % 16, r = 16 s4 + l / 16 + 4 e
-    const int dk = 16 * (f >> 8) + (l & 15), rb = 16 * ((f >> 6) & 3) + (l >> 4);
-    float v4[4];
+      for (int ct = 0; ct < 4; ++ct)
+        *reinterpret_cast<f32x4*>(u + UO_U + (((4 * w + ct) * 4 + rt) * 64 + lane) * 4) = acc[rt][ct];
+  } else {  // -W tile (row tile rt, key block 4 (w - 2) + ct)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v4[e] = expf(Gl - Gs[rb + 4 * e]) * Ks[rb + 4 * e][dk];
-    *reinterpret_cast<float4*>(u + UO_K + 4 * f) = make_float4(v4[0], v4[1], v4[2], v4[3]);
-  }
-  if (t == 0) u[UO_G] = expf(Gl);
-  __syncthreads();
-  // (I + L) X = R, R = [beta V | beta gamma K]: thread t owns column t
-  float X[DC];
-  if (t < DN_D) {
-    const float* vp = q.v + (((int64_t)b * q.Hv + hv) * q.T + t0) * DN_D + t;
+    for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-    for (int r = 0; r < DC; ++r) X[r] = Bs[r] * vp[(int64_t)min(r, n - 1) * DN_D];  // Bs = 0 past n
-  } else {
-#pragma unroll
-    for (int r = 0; r < DC; ++r) X[r] = Bs[r] * Es[r] * Ks[r][t - DN_D];
-  }
-#pragma unroll
-  for (int i = 1; i < DC; ++i) {
-    float acc[4] = {X[i], 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < i; ++j) acc[j & 3] -= Ls[i][j] * X[j];
-    X[i] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-  }
-  __syncthreads();  // K is free: -W staged there
-  if (t < DN_D) {   // U: rows 4qq .. 4qq + 3 of column t are one accumulator float4
-#pragma unroll
-    for (int qq = 0; qq < DC / 4; ++qq)
-      *reinterpret_cast<float4*>(u + UO_U + pos_acc(4 * qq, t)) =
-          make_float4(X[4 * qq], X[4 * qq + 1], X[4 * qq + 2], X[4 * qq + 3]);
-  } else {
-#pragma unroll
-    for (int r = 0; r < DC; ++r) Ks[r][t - DN_D] = -X[r];
-  }
-  __syncthreads();
-  for (int f = t; f < 2048; f += 256) {  // -W: tile f / 512, s4 (f / 64) % 8
-    const int l = f & 63;
-    const int r = 16 * (f >> 9) + (l & 15), kb = 16 * ((f >> 6) & 7) + (l >> 4);
-    *reinterpret_cast<float4*>(u + UO_W + 4 * f) =
-        make_float4(Ks[r][kb], Ks[r][kb + 4], Ks[r][kb + 8], Ks[r][kb + 12]);
+      for (int rt = 0; rt < 4; ++rt)
+        *reinterpret_cast<f32x4*>(u + UO_W + ((rt * 8 + 4 * (w - 2) + ct) * 64 + lane) * 4) =
+            -acc[ct][rt];
   }
 }
 
@@ -456,26 +604,33 @@ __device__ __forceinline__ void scan_load_b(ScanOpsB& o, const float* unit, int 
   }
   o.gl = unit[UO_G];
 }
-__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+// an accumulator tile (lane (r4, n) rows 16 d + 4 r4 + e, column n) split into
+// the phase-3 B operand order: k step d / 2, lane 16 (2 (d % 2) + r4 / 2) + n,
+// elements 4 (r4 % 2) .. +3 (ks: this tile's k step; blk: the block's base)
+__device__ __forceinline__ void store_split(uint16_t* blk, int ks, int half, const f32x4& x, int lane) {
+  const int r4 = lane >> 4, n = lane & 15;
+  const int l2 = 16 * (2 * half + (r4 >> 1)) + n;
+  uint2 hi, lo;
+  split4(x, hi, lo);
+  *reinterpret_cast<uint2*>(blk + ((ks * 2 + 0) * 64 + l2) * 8 + 4 * (r4 & 1)) = hi;
+  *reinterpret_cast<uint2*>(blk + ((ks * 2 + 1) * 64 + l2) * 8 + 4 * (r4 & 1)) = lo;
 }
 // one chunk: S_0 out for phase 3, delta = U - W S_0 (step A), delta out, then
 // S = gamma_C S_0 + K~^T delta (step B). s0 / dl: this chunk's S_0 and delta
-// slots of this workgroup's column block.
+// blocks of this workgroup's column block (bf16 hi / lo, see S0_UNIT).
 __device__ __forceinline__ void scan_chunk(const ScanOpsA& oa, const ScanOpsB& ob, f32x4 (&St)[2],
-                                           float* Sl, float* Dl, float* s0, float* dl, int w,
+                                           float* Sl, float* Dl, uint16_t* s0, uint16_t* dl, int w,
                                            int lane) {
   const int row4 = lane >> 4, col = lane & 15;
 #pragma unroll
-  for (int x = 0; x < 2; ++x)
-    *reinterpret_cast<f32x4*>(s0 + ((2 * w + x) * 64 + lane) * 4) = St[x];
+  for (int x = 0; x < 2; ++x) store_split(s0, w, x, St[x], lane);  // rows 16 (2 w + x) ..
   f32x4 dacc = oa.u;
 #pragma unroll
   for (int s = 0; s < 32; ++s) {
     const float sv = Sl[(4 * s + row4) * CBW + col];
     dacc = mfma4(oa.w[s >> 2][s & 3], sv, dacc);
   }
-  *reinterpret_cast<f32x4*>(dl + (w * 64 + lane) * 4) = dacc;
+  store_split(dl, w >> 1, w & 1, dacc, lane);  // rows 16 w ..
 #pragma unroll
   for (int e = 0; e < 4; ++e) Dl[(16 * w + 4 * row4 + e) * CBW + col] = dacc[e];
   __syncthreads();
@@ -521,8 +676,8 @@ void deltanet_scan_kernel(DeltaChunkArgs a) {
   const int NC = (q.T + DC - 1) / DC;
   const float* units = dn_units(a, b, hv, NC);
   // phase 3's inputs of this column block: chunk c at + c * unit + cb * block
-  float* s0b = dn_s0(a, b, hv, NC) + cb * (S0_UNIT / 8);
-  float* dlb = dn_dl(a, b, hv, NC) + cb * (DL_UNIT / 8);
+  uint16_t* s0b = reinterpret_cast<uint16_t*>(dn_s0(a, b, hv, NC) + cb * (S0_UNIT / 8));
+  uint16_t* dlb = reinterpret_cast<uint16_t*>(dn_dl(a, b, hv, NC) + cb * (DL_UNIT / 8));
   // Two register sets, chunks in pairs, each set reloaded two chunks ahead right
   // after its chunk; chunk indices past the end read the identity unit (an odd
   // count pads with it; its S_0 and delta go to the spare slot NC). Branch-free,
@@ -535,12 +690,14 @@ void deltanet_scan_kernel(DeltaChunkArgs a) {
   scan_load_b(by, units + (int64_t)min(1, NC) * UNIT, w, lane);
   __syncthreads();
   for (int c = 0; c < NC; c += 2) {
-    scan_chunk(ax, bx, St, Sl, Dl, s0b + (int64_t)c * S0_UNIT, dlb + (int64_t)c * DL_UNIT, w, lane);
+    scan_chunk(ax, bx, St, Sl, Dl, s0b + 2 * (int64_t)c * S0_UNIT, dlb + 2 * (int64_t)c * DL_UNIT, w,
+               lane);
     const float* u2 = units + (int64_t)min(c + 2, NC) * UNIT;
     scan_load_a(ax, u2, w, cb, lane);
     scan_load_b(bx, u2, w, lane);
     const int c1 = min(c + 1, NC);
-    scan_chunk(ay, by, St, Sl, Dl, s0b + (int64_t)c1 * S0_UNIT, dlb + (int64_t)c1 * DL_UNIT, w, lane);
+    scan_chunk(ay, by, St, Sl, Dl, s0b + 2 * (int64_t)c1 * S0_UNIT, dlb + 2 * (int64_t)c1 * DL_UNIT, w,
+               lane);
     const float* u3 = units + (int64_t)min(c + 3, NC) * UNIT;
     scan_load_a(ay, u3, w, cb, lane);
     scan_load_b(by, u3, w, lane);
@@ -552,19 +709,22 @@ void deltanet_scan_kernel(DeltaChunkArgs a) {
 }
 
 // Phase 3: one workgroup per (chunk, value head, sequence). First each wave w
-// forms rows 16 w .. 16 w + 15 of M and of gamma Q into LDS: lane l holds q row
-// i = 16 w + l % 16 at columns 16 s4 + 4 (l / 16) .. +3 (s4 < 8), the B operand
-// of P^T = K Q^T, whose result tiles (tile jt: lane l reg r = P[i][16 jt + 4
-// (l / 16) + r]) are masked and decayed into M. Then wave w forms output
-// columns 32 w .. 32 w + 31 (the scan's column blocks 2 w, 2 w + 1) of all 64
-// rows: its S_0 and delta operands (24 x 16 bytes per lane, loaded once the
-// first phase is done: fewer live registers, three workgroups per CU), and
-// gamma Q and M from LDS. With NORM the row's RMS
-// over Dv is taken from the tile staged in LDS, and y = o rstd norm_w silu(z)
-// (the layer's gated norm, as gated_rms_norm_kernel) is stored in bf16
-// instead of o.
-constexpr int OQW = DN_D + 4;  // LDS row of gamma Q (floats; 16-byte aligned, banks skewed)
-constexpr int OMW = DC + 4;    // LDS row of M
+// forms rows 16 w .. 16 w + 15 of M and of gamma Q into LDS, split into bf16
+// hi and lo parts: lane l holds q row i = 16 w + l % 16 at columns 32 ks + 8
+// (l / 16) .. +7 (ks < 4), the B operand of P^T = K Q^T, whose result tiles
+// (tile jt: lane l reg r = P[i][16 jt + 4 (l / 16) + r]) are masked and
+// decayed into M. Then wave w forms output columns 32 w .. 32 w + 31 (the
+// scan's column blocks 2 w, 2 w + 1) of all 64 rows: its S_0 and delta
+// operands (the scan's split blocks) are loaded once the first phase is done,
+// and gamma Q and M come from LDS. Each product is hi hi + hi lo + lo hi on
+// v_mfma_f32_16x16x32_bf16 (A lane l = A[l % 16][8 (l / 16) + j], B lane l =
+// B[8 (l / 16) + j][l % 16], D lane l reg r = D[4 (l / 16) + r][l % 16]). The
+// output tile is staged through LDS, so that a thread then holds 32
+// contiguous columns of one row: O, or with NORM y = o rstd norm_w silu(z)
+// (the layer's gated norm, as gated_rms_norm_kernel) in bf16.
+constexpr int OQW = DN_D + 8;  // LDS row of gamma Q hi / lo (bf16; 16-byte aligned, banks skewed)
+constexpr int OMW = DC + 8;    // LDS row of M hi / lo (bf16)
+constexpr int OOW = DN_D + 4;  // LDS row of the output tile (floats)
 template <bool NORM>
 __global__ __launch_bounds__(256) void deltanet_out_kernel(DeltaChunkArgs a) {
   const DeltaSeqArgs& q = a.s;
@@ -574,38 +734,40 @@ __global__ __launch_bounds__(256) void deltanet_out_kernel(DeltaChunkArgs a) {
   const int t0 = c * DC, n = min(DC, q.T - t0);
   const int NC = (q.T + DC - 1) / DC;
   __shared__ float Gs[DC];
-  __shared__ __attribute__((aligned(16))) float Qs[DC * OQW];  // gamma Q [i][dk]
-  __shared__ __attribute__((aligned(16))) float Ms[DC * OMW];  // M [i][j]
-  // this wave's B operands, column blocks 2 w and 2 w + 1: S_0 (d < 8) and delta (jt < 4)
-  const float* s0 = dn_s0(a, b, hv, NC) + (int64_t)c * S0_UNIT + (2 * w) * (S0_UNIT / 8);
-  const float* dl = dn_dl(a, b, hv, NC) + (int64_t)c * DL_UNIT + (2 * w) * (DL_UNIT / 8);
+  __shared__ __attribute__((aligned(16))) uint16_t Qhl[2][DC * OQW];  // gamma Q [i][dk] hi, lo
+  uint16_t* const Qh = Qhl[0];
+  uint16_t* const Ql = Qhl[1];
+  __shared__ __attribute__((aligned(16))) uint16_t Mh[DC * OMW], Ml[DC * OMW];  // M [i][j]
   if (t < 64) Gs[t] = chunk_cumsum(q, b, hv, t0, n, t);
   const float* qp = q.q + (((int64_t)b * q.Hk + hk) * q.T + t0) * DN_D;
   const float* kp = q.k + (((int64_t)b * q.Hk + hk) * q.T + t0) * DN_D;
   {
     const int i = 16 * w + l16;  // this lane's q row
-    f32x4 qv[8];
+    f32x4 qv[8];                 // q[i][32 ks + 8 (l / 16) + 4 u .. +3] at qv[2 ks + u]
 #pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4)
-      qv[s4] = *reinterpret_cast<const f32x4*>(qp + (int64_t)min(i, n - 1) * DN_D + 16 * s4 + 4 * r4);
-    // P^T tiles: D[j][i] = sum_dk K[j][dk] Q[i][dk], A lane l = K[16 jt + l % 16][dk];
-    // the four tiles' chains interleaved
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        qv[2 * ks + u] = *reinterpret_cast<const f32x4*>(qp + (int64_t)min(i, n - 1) * DN_D + 32 * ks +
+                                                         8 * r4 + 4 * u);
+    uint4 qh[4], ql[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) split8(qv[2 * ks], qv[2 * ks + 1], qh[ks], ql[ks]);
+    // P^T tiles: D[j][i] = sum_dk K[j][dk] Q[i][dk], A lane l = K[16 jt + l % 16][dk]
     f32x4 P[4];
-    const float* kr[4];
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      P[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      kr[jt] = kp + (int64_t)min(16 * jt + l16, n - 1) * DN_D + 4 * r4;
-    }
+    for (int jt = 0; jt < 4; ++jt) P[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4) {
-      f32x4 kv[4];
+    for (int ks = 0; ks < 4; ++ks) {
+      uint4 kh[4], kl[4];
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) kv[jt] = *reinterpret_cast<const f32x4*>(kr[jt] + 16 * s4);
+      for (int jt = 0; jt < 4; ++jt) {
+        const float* kr = kp + (int64_t)min(16 * jt + l16, n - 1) * DN_D + 32 * ks + 8 * r4;
+        split8(*reinterpret_cast<const f32x4*>(kr), *reinterpret_cast<const f32x4*>(kr + 4), kh[jt],
+               kl[jt]);
+      }
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) P[jt] = mfma4(kv[jt][e], qv[s4][e], P[jt]);
+      for (int jt = 0; jt < 4; ++jt) P[jt] = mfma_x3(kh[jt], kl[jt], qh[ks], ql[ks], P[jt]);
     }
     __syncthreads();  // Gs
     // M = P D on j <= i < n, j < n (rows or keys past the chunk: 0); lane l reg r
@@ -619,74 +781,92 @@ __global__ __launch_bounds__(256) void deltanet_out_kernel(DeltaChunkArgs a) {
         const int j = 16 * jt + 4 * r4 + r;
         m[r] = (j <= i && i < n) ? P[jt][r] * expf(Gi - Gs[j]) : 0.f;
       }
-      *reinterpret_cast<f32x4*>(&Ms[i * OMW + 16 * jt + 4 * r4]) = m;
+      uint2 mh, ml;
+      split4(m, mh, ml);
+      *reinterpret_cast<uint2*>(&Mh[i * OMW + 16 * jt + 4 * r4]) = mh;
+      *reinterpret_cast<uint2*>(&Ml[i * OMW + 16 * jt + 4 * r4]) = ml;
     }
     const float gi = i < n ? expf(Gi) : 0.f;  // gamma_i (rows past the chunk: 0)
 #pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4)
-      *reinterpret_cast<f32x4*>(&Qs[i * OQW + 16 * s4 + 4 * r4]) = qv[s4] * gi;
+    for (int ks = 0; ks < 4; ++ks) {
+      uint4 gh, gl;
+      split8(qv[2 * ks] * gi, qv[2 * ks + 1] * gi, gh, gl);
+      *reinterpret_cast<uint4*>(&Qh[i * OQW + 32 * ks + 8 * r4]) = gh;
+      *reinterpret_cast<uint4*>(&Ql[i * OQW + 32 * ks + 8 * r4]) = gl;
+    }
   }
-  f32x4 sb[2][8], db[2][4];
+  // this wave's B operands, column blocks 2 w + x: S_0 (ks < 4) and delta (ks < 2)
+  const uint16_t* s0 = reinterpret_cast<const uint16_t*>(dn_s0(a, b, hv, NC) + (int64_t)c * S0_UNIT) +
+                       2 * (2 * w) * (S0_UNIT / 8);
+  const uint16_t* dl = reinterpret_cast<const uint16_t*>(dn_dl(a, b, hv, NC) + (int64_t)c * DL_UNIT) +
+                       2 * (2 * w) * (DL_UNIT / 8);
+  uint4 sb[2][4][2], db[2][2][2];
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
 #pragma unroll
-    for (int d = 0; d < 8; ++d)
-      sb[x][d] = *reinterpret_cast<const f32x4*>(s0 + x * (S0_UNIT / 8) + (d * 64 + lane) * 4);
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-      db[x][jt] = *reinterpret_cast<const f32x4*>(dl + x * (DL_UNIT / 8) + (jt * 64 + lane) * 4);
+      for (int hl = 0; hl < 2; ++hl)
+        sb[x][ks][hl] = *reinterpret_cast<const uint4*>(s0 + 2 * x * (S0_UNIT / 8) + ((ks * 2 + hl) * 64 + lane) * 8);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl)
+        db[x][ks][hl] = *reinterpret_cast<const uint4*>(dl + 2 * x * (DL_UNIT / 8) + ((ks * 2 + hl) * 64 + lane) * 8);
   }
   __syncthreads();
-  // O = gamma Q S_0 + M delta: row tile rt, column block 2 w + x; eight
-  // independent accumulators between dependent products
+  // O = gamma Q S_0 + M delta: row tile rt, column block 2 w + x
   f32x4 O[4][2];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
     for (int x = 0; x < 2; ++x) O[rt][x] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int d = 0; d < 8; ++d) {
-    f32x4 av[4];
+  for (int ks = 0; ks < 4; ++ks) {
+    uint4 ah[4], al[4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      ah[rt] = *reinterpret_cast<const uint4*>(&Qh[(16 * rt + l16) * OQW + 32 * ks + 8 * r4]);
+      al[rt] = *reinterpret_cast<const uint4*>(&Ql[(16 * rt + l16) * OQW + 32 * ks + 8 * r4]);
+    }
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
-      av[rt] = *reinterpret_cast<const f32x4*>(&Qs[(16 * rt + l16) * OQW + 16 * d + 4 * r4]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-        for (int x = 0; x < 2; ++x) O[rt][x] = mfma4(av[rt][e], sb[x][d][e], O[rt][x]);
+      for (int x = 0; x < 2; ++x)
+        O[rt][x] = mfma_x3(ah[rt], al[rt], sb[x][ks][0], sb[x][ks][1], O[rt][x]);
   }
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt) {
-    f32x4 av[4];
+  for (int ks = 0; ks < 2; ++ks) {
+    uint4 ah[4], al[4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      ah[rt] = *reinterpret_cast<const uint4*>(&Mh[(16 * rt + l16) * OMW + 32 * ks + 8 * r4]);
+      al[rt] = *reinterpret_cast<const uint4*>(&Ml[(16 * rt + l16) * OMW + 32 * ks + 8 * r4]);
+    }
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
-      av[rt] = *reinterpret_cast<const f32x4*>(&Ms[(16 * rt + l16) * OMW + 16 * jt + 4 * r4]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-        for (int x = 0; x < 2; ++x) O[rt][x] = mfma4(av[rt][e], db[x][jt][e], O[rt][x]);
+      for (int x = 0; x < 2; ++x)
+        O[rt][x] = mfma_x3(ah[rt], al[rt], db[x][ks][0], db[x][ks][1], O[rt][x]);
   }
   // lane l reg r of O[rt][x] = O[16 rt + 4 (l / 16) + r][32 w + 16 x + l % 16]: the
-  // tile goes through LDS (the gamma Q rows, free once every wave is past its
-  // products) so that a thread then holds 32 contiguous columns of one row
+  // tile goes through LDS (the gamma Q and M rows, free once every wave is past
+  // its products) so that a thread then holds 32 contiguous columns of one row
   __syncthreads();
-  float* Os = Qs;
+  float* Os = reinterpret_cast<float*>(&Qhl[0][0]);  // 2 x 17 KB >= 64 rows of OOW floats
+  static_assert(sizeof(Qhl) >= DC * OOW * sizeof(float), "output tile");
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
-      for (int x = 0; x < 2; ++x) Os[(16 * rt + 4 * r4 + r) * OQW + 32 * w + 16 * x + l16] = O[rt][x][r];
+      for (int x = 0; x < 2; ++x) Os[(16 * rt + 4 * r4 + r) * OOW + 32 * w + 16 * x + l16] = O[rt][x][r];
   __syncthreads();
   const int row = t >> 2, c0 = 32 * (t & 3);  // thread t: row t / 4, columns c0 .. c0 + 31
   float o[32];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(&Os[row * OQW + c0 + 4 * j]);
+    const f32x4 v = *reinterpret_cast<const f32x4*>(&Os[row * OOW + c0 + 4 * j]);
     o[4 * j] = v[0]; o[4 * j + 1] = v[1]; o[4 * j + 2] = v[2]; o[4 * j + 3] = v[3];
   }
   const int64_t tok = t0 + row;
