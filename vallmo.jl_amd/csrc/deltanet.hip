@@ -252,15 +252,16 @@ __global__ __launch_bounds__(256) void deltanet_sequence_kernel(DeltaSeqArgs a) 
 // Phase 1 (deltanet_chunk_kernel, chunk-parallel): the Gram K K^T and the
 // products [U | W] = T [beta V | beta gamma K] with T = (I + L)^-1 on the bf16
 // MFMA in split precision (see phase 3), T itself by fp32 forward
-// substitution, and the operands of the state chain (-W, K~^T, U, gamma_C)
-// written in the fp32 MFMA operand order of v_mfma_f32_16x16x4f32 (A lane l =
-// A[l % 16][l / 16], B lane l = B[l / 16][l % 16], D lane l reg r = D[4 (l /
-// 16) + r][l % 16]), 16 bytes per lane per four k-steps, so phase 2 reads 1 KB
-// contiguous per wave load.
+// substitution, and the operands of the state chain (-W, K~^T split, U,
+// gamma_C) written in the operand orders phase 2 loads them in, 16 bytes per
+// lane, so phase 2 reads 1 KB contiguous per wave load.
 // Phase 2 (deltanet_scan_kernel, sequential over chunks): one workgroup per 16
-// state columns of a value head; per chunk 64 MFMAs per wave (delta, then the
-// state), writing each chunk's start state S_0 and its delta for phase 3, the
-// next chunk's operands loading into a second register set meanwhile.
+// state columns of a value head; per chunk 24 split-precision MFMAs per wave
+// (delta, then the state, fp32 accumulators), writing each chunk's start state
+// S_0 and its delta for phase 3, the next chunk's operands loading into a
+// second register set meanwhile. The state and delta pass between the waves
+// through LDS split and transposed ([column][k]), so that a B operand is one
+// 16-byte read.
 // Phase 3 (deltanet_out_kernel, chunk-parallel): Q K^T, M and O = gamma Q S_0 +
 // M delta on the bf16 MFMA (v_mfma_f32_16x16x32_bf16) in split precision:
 // each fp32 operand x is hi = bf16(x) and lo = bf16(x - hi), and a product is
@@ -272,9 +273,12 @@ namespace {
 constexpr int DC = 64;   // chunk length
 constexpr int CBW = 16;  // state columns per scan workgroup
 // per (chunk, value head, sequence) unit of the scan's operands, floats
-constexpr int UO_W = 0;      // -W:       [w 4][s4 8][lane][4], A[i = r][k = dk]
-constexpr int UO_K = 8192;   // K~^T:     [d 8][s4 4][lane][4], A[i = dk][k = r]
-constexpr int UO_U = 16384;  // U:        [cb 8][w 4][lane][4], D[r][dv] tiles
+// (-W and K~^T split into bf16 hi / lo in the A operand order of
+// v_mfma_f32_16x16x32_bf16, 8 bf16 per lane: lane l element j = A[16 tile + l %
+// 16][32 ks + 8 (l / 16) + j]; U fp32 in accumulator order)
+constexpr int UO_W = 0;      // -W:   [w 4][ks 4][hl 2][lane][8] bf16, A[i = r][k = dk]
+constexpr int UO_K = 8192;   // K~^T: [d 8][ks 2][hl 2][lane][8] bf16, A[i = dk][k = r]
+constexpr int UO_U = 16384;  // U:    [cb 8][w 4][lane][4] floats, D[r][dv] tiles
 constexpr int UO_G = 24576;  // gamma_C
 constexpr int UNIT = 24640;  // floats per unit (98 560 B, a multiple of 256)
 // per (chunk, value head, sequence), written by the scan for phase 3, in
@@ -322,9 +326,6 @@ __device__ __forceinline__ float* dn_dl(const DeltaChunkArgs& a, int b, int hv, 
 }
 
 namespace {
-__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 // 4 fp32 values as bf16 hi and lo parts (x = hi + lo to about 2^-16), 4 each
 __device__ __forceinline__ void split4(const f32x4& x, uint2& hi, uint2& lo) {
   hi = make_uint2(pack2(x[0], x[1]), pack2(x[2], x[3]));
@@ -359,9 +360,10 @@ constexpr int TW = DC + 8;     // LDS row of T hi / lo (bf16)
 // lo over L, while waves 0-2 write K~^T and gather their operands of the
 // products below. Then waves 0, 1 form U = T (beta V) (value columns 64 w ..)
 // in the scan's accumulator order, and waves 2, 3 form W^T = (beta gamma K)^T
-// T^T (key columns 64 (w - 2) ..): their A operand lane l gathers key column
-// 16 ct + (l % 16) / 4 + 4 (l % 4), so that result lane l reg r is W[i][16 ct +
-// l / 16 + 4 r], the -W operand order of the scan.
+// T^T (key columns 64 (w - 2) ..): their A operand lane l of tile ct gathers
+// key column 32 (ct / 2) + 4 (ct % 2) + 8 ((l % 16) / 4) + l % 4, so that
+// result tiles 2 h, 2 h + 1, lane l reg r hold W[i][32 h + 8 (l / 16) + 4 (tile
+// % 2) + r]: 8 consecutive keys per lane, the -W operand order of the scan.
 // (three waves per SIMD: the phases are latency-bound, and three workgroups fit a CU's LDS)
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 void deltanet_chunk_kernel(DeltaChunkArgs a) {
@@ -384,7 +386,7 @@ void deltanet_chunk_kernel(DeltaChunkArgs a) {
   __shared__ __attribute__((aligned(16))) float Ks[DC * KSW];
   __shared__ __attribute__((aligned(16))) float LT[DC * TW];
   static_assert(sizeof(LT) >= DC * LSW * sizeof(float), "L");
-  __shared__ __attribute__((aligned(16))) float Gs[DC], Bs[DC], Es[DC];
+  __shared__ __attribute__((aligned(16))) float Gs[DC], Bs[DC], Es[DC], Ek[DC];
   uint16_t* const Th = reinterpret_cast<uint16_t*>(LT);
   uint16_t* const Tl = Th + DC * TW;
   const float* kp = q.k + (((int64_t)b * q.Hk + hk) * q.T + t0) * DN_D;
@@ -400,6 +402,7 @@ void deltanet_chunk_kernel(DeltaChunkArgs a) {
       Gs[t] = G;
       Bs[t] = t < n ? bt : 0.f;
       Es[t] = expf(G);
+      Ek[t] = expf(__shfl(G, DC - 1) - G);  // gamma_C / gamma_t
     }
 #pragma unroll
     for (int m = 0; m < DC / 8; ++m) {  // rows past the end read as 0
@@ -442,7 +445,8 @@ void deltanet_chunk_kernel(DeltaChunkArgs a) {
   uint4 rh[2][4], rl[2][4];  // [ks][ct]
   auto gather = [&]() __attribute__((always_inline)) {
     const float* vp = q.v + (((int64_t)b * q.Hv + hv) * q.T + t0) * DN_D + 64 * (w & 1) + l16;
-    const int pc = 64 * (w & 1) + (l16 >> 2) + 4 * (l16 & 3);  // gathered key column, + 16 ct
+    // gathered key column of tile ct: 64 (w % 2) + 32 (ct / 2) + 4 (ct % 2) + pc
+    const int pc = 64 * (w & 1) + 8 * (l16 >> 2) + (l16 & 3);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int j0 = 32 * ks + 8 * r4;
@@ -465,8 +469,8 @@ void deltanet_chunk_kernel(DeltaChunkArgs a) {
         for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            r0[ct][e] = Ks[(j0 + e) * KSW + pc + 16 * ct];
-            r1[ct][e] = Ks[(j0 + 4 + e) * KSW + pc + 16 * ct];
+            r0[ct][e] = Ks[(j0 + e) * KSW + pc + 32 * (ct >> 1) + 4 * (ct & 1)];
+            r1[ct][e] = Ks[(j0 + 4 + e) * KSW + pc + 32 * (ct >> 1) + 4 * (ct & 1)];
           }
       }
 #pragma unroll
@@ -522,18 +526,23 @@ void deltanet_chunk_kernel(DeltaChunkArgs a) {
       *reinterpret_cast<uint32_t*>(((lane & 1) ? Tl : Th) + i * TW + (lane & ~1)) = (lane & 1) ? lo : hi;
     }
   } else {
-    // K~^T in operand order, one coalesced float4 per lane and slot
-    const float Gl = Gs[DC - 1];
-    for (int f = t; f < 2048; f += 192) {
-      const int l = f & 63;
-      // tile f / 256, s4 (f / 64) % 4: dk 16 d + l % 16, r = 16 s4 + l / 16 + 4 e
-      const int dk = 16 * (f >> 8) + (l & 15), rb = 16 * ((f >> 6) & 3) + (l >> 4);
-      float v4[4];
+    // K~^T split, in operand order: slot f = (tile d, ks) = (f / 128, (f / 64) % 2),
+    // lane f % 64: dk 16 d + l % 16, r = 32 ks + 8 (l / 16) + j
+    uint16_t* const kt = reinterpret_cast<uint16_t*>(u + UO_K);
+    for (int f = t; f < 1024; f += 192) {
+      const int l = f & 63, dk = 16 * (f >> 7) + (l & 15), r0 = 32 * ((f >> 6) & 1) + 8 * (l >> 4);
+      f32x4 v0, v1;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v4[e] = expf(Gl - Gs[rb + 4 * e]) * Ks[(rb + 4 * e) * KSW + dk];
-      *reinterpret_cast<float4*>(u + UO_K + 4 * f) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+      for (int e = 0; e < 4; ++e) {
+        v0[e] = Ek[r0 + e] * Ks[(r0 + e) * KSW + dk];
+        v1[e] = Ek[r0 + 4 + e] * Ks[(r0 + 4 + e) * KSW + dk];
+      }
+      uint4 hi, lo;
+      split8(v0, v1, hi, lo);
+      *reinterpret_cast<uint4*>(kt + ((2 * (f >> 6) + 0) * 64 + l) * 8) = hi;
+      *reinterpret_cast<uint4*>(kt + ((2 * (f >> 6) + 1) * 64 + l) * 8) = lo;
     }
-    if (t == 0) u[UO_G] = expf(Gl);
+    if (t == 0) u[UO_G] = expf(Gs[DC - 1]);
     gather();
   }
   __syncthreads();
@@ -568,85 +577,124 @@ void deltanet_chunk_kernel(DeltaChunkArgs a) {
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct)
         *reinterpret_cast<f32x4*>(u + UO_U + (((4 * w + ct) * 4 + rt) * 64 + lane) * 4) = acc[rt][ct];
-  } else {  // -W tile (row tile rt, key block 4 (w - 2) + ct)
+  } else {  // -W, row tile rt, k step ks = 2 (w - 2) + h: tiles 2 h, 2 h + 1 hold
+            // lane l's dk 32 ks + 8 (l / 16) + j, j < 4 and j >= 4
+    uint16_t* const wm = reinterpret_cast<uint16_t*>(u + UO_W);
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
-        *reinterpret_cast<f32x4*>(u + UO_W + ((rt * 8 + 4 * (w - 2) + ct) * 64 + lane) * 4) =
-            -acc[ct][rt];
+      for (int rt = 0; rt < 4; ++rt) {
+        const int ks = 2 * (w - 2) + h;
+        uint4 hi, lo;
+        split8(-acc[2 * h][rt], -acc[2 * h + 1][rt], hi, lo);
+        *reinterpret_cast<uint4*>(wm + (((rt * 4 + ks) * 2 + 0) * 64 + lane) * 8) = hi;
+        *reinterpret_cast<uint4*>(wm + (((rt * 4 + ks) * 2 + 1) * 64 + lane) * 8) = lo;
+      }
   }
 }
 
 namespace {
 // a chunk's operands, split by the step that consumes them: step A (the delta
-// products) and step B (the state products)
+// products) and step B (the state products); bf16 hi / lo pairs [.][hl]
 struct ScanOpsA {
-  f32x4 w[8], u;
+  uint4 w[4][2];  // -W rows 16 w .., k step ks
+  f32x4 u;
 };
 struct ScanOpsB {
-  f32x4 k[8];
+  uint4 k[2][2][2];  // K~^T tiles 2 w + x, k step ks
   float gl;
 };
 __device__ __forceinline__ void scan_load_a(ScanOpsA& o, const float* unit, int w, int cb,
                                             int lane) {
+  const uint16_t* wm = reinterpret_cast<const uint16_t*>(unit + UO_W);
 #pragma unroll
-  for (int s4 = 0; s4 < 8; ++s4)
-    o.w[s4] = *reinterpret_cast<const f32x4*>(unit + UO_W + ((w * 8 + s4) * 64 + lane) * 4);
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int hl = 0; hl < 2; ++hl)
+      o.w[ks][hl] = *reinterpret_cast<const uint4*>(wm + (((w * 4 + ks) * 2 + hl) * 64 + lane) * 8);
   o.u = *reinterpret_cast<const f32x4*>(unit + UO_U + ((cb * 4 + w) * 64 + lane) * 4);
 }
 __device__ __forceinline__ void scan_load_b(ScanOpsB& o, const float* unit, int w, int lane) {
+  const uint16_t* kt = reinterpret_cast<const uint16_t*>(unit + UO_K);
 #pragma unroll
-  for (int s4 = 0; s4 < 4; ++s4) {
-    o.k[s4] = *reinterpret_cast<const f32x4*>(unit + UO_K + (((2 * w) * 4 + s4) * 64 + lane) * 4);
-    o.k[4 + s4] =
-        *reinterpret_cast<const f32x4*>(unit + UO_K + (((2 * w + 1) * 4 + s4) * 64 + lane) * 4);
-  }
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl)
+        o.k[x][ks][hl] =
+            *reinterpret_cast<const uint4*>(kt + ((((2 * w + x) * 2 + ks) * 2 + hl) * 64 + lane) * 8);
   o.gl = unit[UO_G];
 }
 // an accumulator tile (lane (r4, n) rows 16 d + 4 r4 + e, column n) split into
 // the phase-3 B operand order: k step d / 2, lane 16 (2 (d % 2) + r4 / 2) + n,
 // elements 4 (r4 % 2) .. +3 (ks: this tile's k step; blk: the block's base)
-__device__ __forceinline__ void store_split(uint16_t* blk, int ks, int half, const f32x4& x, int lane) {
+__device__ __forceinline__ void store_split(uint16_t* blk, int ks, int half, const uint2& hi,
+                                            const uint2& lo, int lane) {
   const int r4 = lane >> 4, n = lane & 15;
   const int l2 = 16 * (2 * half + (r4 >> 1)) + n;
-  uint2 hi, lo;
-  split4(x, hi, lo);
   *reinterpret_cast<uint2*>(blk + ((ks * 2 + 0) * 64 + l2) * 8 + 4 * (r4 & 1)) = hi;
   *reinterpret_cast<uint2*>(blk + ((ks * 2 + 1) * 64 + l2) * 8 + 4 * (r4 & 1)) = lo;
 }
+constexpr int SSW = DN_D + 8;  // LDS row (one state column) of S hi / lo, bf16
+constexpr int DSW = DC + 8;    // LDS row (one state column) of delta hi / lo, bf16
+// the scan's LDS: S and delta split, transposed: X[k][column c] at [c][k]
+struct ScanLds {
+  uint16_t sh[CBW * SSW], sl[CBW * SSW], dh[CBW * DSW], dl[CBW * DSW];
+};
+// accumulator tile rows k0 + 4 (l / 16) .. +3 of column l % 16, split, into LDS
+__device__ __forceinline__ void lds_put(uint16_t* h, uint16_t* l, int ld, int k0, const uint2& hi,
+                                        const uint2& lo, int lane) {
+  const int o = (lane & 15) * ld + k0 + 4 * (lane >> 4);
+  *reinterpret_cast<uint2*>(h + o) = hi;
+  *reinterpret_cast<uint2*>(l + o) = lo;
+}
 // one chunk: S_0 out for phase 3, delta = U - W S_0 (step A), delta out, then
 // S = gamma_C S_0 + K~^T delta (step B). s0 / dl: this chunk's S_0 and delta
-// blocks of this workgroup's column block (bf16 hi / lo, see S0_UNIT).
+// blocks of this workgroup's column block (bf16 hi / lo, see S0_UNIT). B
+// operand of k step ks, lane l: X[32 ks + 8 (l / 16) + j][l % 16], one LDS read
+// each of hi and lo.
 __device__ __forceinline__ void scan_chunk(const ScanOpsA& oa, const ScanOpsB& ob, f32x4 (&St)[2],
-                                           float* Sl, float* Dl, uint16_t* s0, uint16_t* dl, int w,
+                                           ScanLds& sm, uint16_t* s0, uint16_t* dl, int w,
                                            int lane) {
   const int row4 = lane >> 4, col = lane & 15;
 #pragma unroll
-  for (int x = 0; x < 2; ++x) store_split(s0, w, x, St[x], lane);  // rows 16 (2 w + x) ..
+  for (int x = 0; x < 2; ++x) {  // rows 16 (2 w + x) ..
+    uint2 hi, lo;
+    split4(St[x], hi, lo);
+    store_split(s0, w, x, hi, lo, lane);
+  }
   f32x4 dacc = oa.u;
 #pragma unroll
-  for (int s = 0; s < 32; ++s) {
-    const float sv = Sl[(4 * s + row4) * CBW + col];
-    dacc = mfma4(oa.w[s >> 2][s & 3], sv, dacc);
+  for (int ks = 0; ks < 4; ++ks) {
+    const int o = col * SSW + 32 * ks + 8 * row4;
+    dacc = mfma_x3(oa.w[ks][0], oa.w[ks][1], *reinterpret_cast<const uint4*>(&sm.sh[o]),
+                   *reinterpret_cast<const uint4*>(&sm.sl[o]), dacc);
   }
-  store_split(dl, w >> 1, w & 1, dacc, lane);  // rows 16 w ..
-#pragma unroll
-  for (int e = 0; e < 4; ++e) Dl[(16 * w + 4 * row4 + e) * CBW + col] = dacc[e];
+  {  // delta rows 16 w ..
+    uint2 hi, lo;
+    split4(dacc, hi, lo);
+    store_split(dl, w >> 1, w & 1, hi, lo, lane);
+    lds_put(sm.dh, sm.dl, DSW, 16 * w, hi, lo, lane);
+  }
   __syncthreads();
   f32x4 s0v = St[0] * ob.gl, s1v = St[1] * ob.gl;
 #pragma unroll
-  for (int s = 0; s < 16; ++s) {
-    const float dv = Dl[(4 * s + row4) * CBW + col];
-    s0v = mfma4(ob.k[s >> 2][s & 3], dv, s0v);
-    s1v = mfma4(ob.k[4 + (s >> 2)][s & 3], dv, s1v);
+  for (int ks = 0; ks < 2; ++ks) {
+    const int o = col * DSW + 32 * ks + 8 * row4;
+    const uint4 bh = *reinterpret_cast<const uint4*>(&sm.dh[o]);
+    const uint4 bl = *reinterpret_cast<const uint4*>(&sm.dl[o]);
+    s0v = mfma_x3(ob.k[0][ks][0], ob.k[0][ks][1], bh, bl, s0v);
+    s1v = mfma_x3(ob.k[1][ks][0], ob.k[1][ks][1], bh, bl, s1v);
   }
   St[0] = s0v;
   St[1] = s1v;
 #pragma unroll
-  for (int x = 0; x < 2; ++x)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) Sl[(16 * (2 * w + x) + 4 * row4 + e) * CBW + col] = St[x][e];
+  for (int x = 0; x < 2; ++x) {
+    uint2 hi, lo;
+    split4(St[x], hi, lo);
+    lds_put(sm.sh, sm.sl, SSW, 16 * (2 * w + x), hi, lo, lane);
+  }
   __syncthreads();
 }
 }  // namespace
@@ -660,8 +708,7 @@ void deltanet_scan_kernel(DeltaChunkArgs a) {
   const int hv = head % q.Hv, b = head / q.Hv;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int row4 = lane >> 4, col = lane & 15;
-  __shared__ __attribute__((aligned(16))) float Sl[DN_D * CBW];  // S[dk][c]
-  __shared__ __attribute__((aligned(16))) float Dl[DC * CBW];    // delta[r][c]
+  __shared__ __attribute__((aligned(16))) ScanLds sm;
   const int dv0 = cb * CBW;
   const int64_t sb = ((int64_t)b * q.Hv + hv) * DN_D * DN_D;
   f32x4 St[2];  // state tiles d = 2w, 2w + 1: lane l reg e = S[16 d + 4 (l / 16) + e][l % 16]
@@ -670,8 +717,9 @@ void deltanet_scan_kernel(DeltaChunkArgs a) {
     const int d = 2 * w + x;
     St[x] = *reinterpret_cast<const f32x4*>(q.s_in + sb + (int64_t)(dv0 + col) * DN_D + 16 * d +
                                             4 * row4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) Sl[(16 * d + 4 * row4 + e) * CBW + col] = St[x][e];
+    uint2 hi, lo;
+    split4(St[x], hi, lo);
+    lds_put(sm.sh, sm.sl, SSW, 16 * d, hi, lo, lane);
   }
   const int NC = (q.T + DC - 1) / DC;
   const float* units = dn_units(a, b, hv, NC);
@@ -688,20 +736,35 @@ void deltanet_scan_kernel(DeltaChunkArgs a) {
   scan_load_b(bx, units, w, lane);
   scan_load_a(ay, units + (int64_t)min(1, NC) * UNIT, w, cb, lane);
   scan_load_b(by, units + (int64_t)min(1, NC) * UNIT, w, lane);
+  // every prologue load complete (s_waitcnt vmcnt(0)): the loop is then entered
+  // with no load in flight, and the compiler's count of the loads each wait in
+  // the loop must see is the one its own body implies (else it takes the
+  // prologue's order, where a register the loop reloads early was loaded last).
+  // NC >= 1 (the launch returns before T = 0): a do-while has no guard branch
+  // that the prologue's loads could be sunk past.
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+  __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
-  for (int c = 0; c < NC; c += 2) {
-    scan_chunk(ax, bx, St, Sl, Dl, s0b + 2 * (int64_t)c * S0_UNIT, dlb + 2 * (int64_t)c * DL_UNIT, w,
+  int c = 0;
+  do {
+    scan_chunk(ax, bx, St, sm, s0b + 2 * (int64_t)c * S0_UNIT, dlb + 2 * (int64_t)c * DL_UNIT, w,
                lane);
     const float* u2 = units + (int64_t)min(c + 2, NC) * UNIT;
+    __builtin_amdgcn_sched_barrier(0);  // the reloads issue here, between the chunks
     scan_load_a(ax, u2, w, cb, lane);
     scan_load_b(bx, u2, w, lane);
+    __builtin_amdgcn_sched_barrier(0);
     const int c1 = min(c + 1, NC);
-    scan_chunk(ay, by, St, Sl, Dl, s0b + 2 * (int64_t)c1 * S0_UNIT, dlb + 2 * (int64_t)c1 * DL_UNIT, w,
+    scan_chunk(ay, by, St, sm, s0b + 2 * (int64_t)c1 * S0_UNIT, dlb + 2 * (int64_t)c1 * DL_UNIT, w,
                lane);
     const float* u3 = units + (int64_t)min(c + 3, NC) * UNIT;
+    __builtin_amdgcn_sched_barrier(0);
     scan_load_a(ay, u3, w, cb, lane);
     scan_load_b(by, u3, w, lane);
-  }
+    __builtin_amdgcn_sched_barrier(0);
+    c += 2;
+  } while (c < NC);
 #pragma unroll
   for (int x = 0; x < 2; ++x)
     *reinterpret_cast<f32x4*>(q.s_out + sb + (int64_t)(dv0 + col) * DN_D + 16 * (2 * w + x) +
