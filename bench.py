@@ -790,6 +790,10 @@ def bench_deltanet(vm, torch, seed=11):
     us_prep = _profiled_us(vm, torch, vm._lib.VM_K_ROWS,
                            lambda: vm.deltanet_prefill_prep_(p, Y, ab, a_log, dt, Dk=Dk, Dv=Dv,
                                                              Hk=Hk, Hv=Hv), n=5)
+    # the layer's form: the conv and the prep in one pass (the conv output not written)
+    us_cp = _profiled_us(vm, torch, vm._lib.VM_K_CONV,
+                         lambda: vm.deltanet_conv_prep_(p, X, w, ab, a_log, dt, Dk=Dk, Dv=Dv,
+                                                        Hk=Hk, Hv=Hv, Sp=Sp), n=5)
     S = torch.zeros((B, Hv, Dv, Dk), **f32)
     o = torch.empty((B, Hv, T, Dv), **f32)
     us_seq = _profiled_us(vm, torch, vm._lib.VM_K_DELTANET,
@@ -814,6 +818,8 @@ def bench_deltanet(vm, torch, seed=11):
     # prep: conv rows read (bf16), fp32 q, k, v written, ab read, gates written;
     # gated norm: fp32 o and bf16 z read, bf16 y written
     prep_bytes = 2.0 * T * n + 4.0 * T * n + 2.0 * T * 2 * Hv + 8.0 * T * Hv
+    # conv + prep: projection rows read (bf16), fp32 q, k, v written, ab, gates, ring
+    cp_bytes = 2.0 * T * n + 4.0 * T * n + 2.0 * T * 2 * Hv + 8.0 * T * Hv + 2.0 * 2 * K * n
     gn_bytes = (4.0 + 2.0 + 2.0) * T * Hv * Dv
     res["prefill_B1_T4096"] = {
         "conv_sequence_us": us_conv,
@@ -826,6 +832,8 @@ def bench_deltanet(vm, torch, seed=11):
         "chunked_gated_norm_ms": us_chk_gn * 1e-3,
         "prep_us": us_prep,
         "prep_gbs": prep_bytes / (us_prep * 1e-6) / 1e9,
+        "conv_prep_us": us_cp,
+        "conv_prep_gbs": cp_bytes / (us_cp * 1e-6) / 1e9,
         "gated_norm_us": us_gn,
         "gated_norm_gbs": gn_bytes / (us_gn * 1e-6) / 1e9,
     }
@@ -1182,7 +1190,9 @@ def main():
             f"{pp['sequence_ms']:.2f} ms sequential ({pp['sequence_us_per_token']:.2f} us/token), "
             f"{pp['chunked_ms']:.3f} ms chunked ({pp['chunked_gated_norm_ms']:.3f} ms with the gated "
             f"norm fused, the layer's form); prep {pp['prep_us']:.1f} us = {pp['prep_gbs']:.0f} "
-            f"GB/s, gated norm {pp['gated_norm_us']:.1f} us = {pp['gated_norm_gbs']:.0f} GB/s")
+            f"GB/s, conv + prep in one pass {pp['conv_prep_us']:.1f} us = "
+            f"{pp['conv_prep_gbs']:.0f} GB/s (the layer's form), gated norm "
+            f"{pp['gated_norm_us']:.1f} us = {pp['gated_norm_gbs']:.0f} GB/s")
     step = None
     if not args.no_step:
         log("[bench] whole decode step, Qwen3.5-4B shape (24 DeltaNet + 8 attention), B=32")

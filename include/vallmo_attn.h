@@ -550,6 +550,23 @@ int vm_deltanet_prefill_prep(float* qe, float* ke, float* ve, float* beta, float
                              const float* dt_bias, int Dk, int Dv, int Hk, int Hv, int T, int B,
                              vm_stream stream);
 
+/* forward(::DeltaNetLayer)'s sequence conv and prep in one pass
+ * (src/llm/qwen35.jl:333-356: causal_conv1d_sequence! with sigma = silu, then
+ * the l2 norms and gates): x the projection's q | k | v channels (n = 2 Hk Dk
+ * + Hv Dv rows per token, x_st, x_sb), the conv weight, bias and ring as
+ * vm_causal_conv1d_sequence (s_in NULL: zero left context; s_out NULL: no
+ * ring written), ab and the outputs as vm_deltanet_prefill_prep. The results
+ * are bit for bit those of vm_causal_conv1d_sequence (act = 1) followed by
+ * vm_deltanet_prefill_prep: the conv output is rounded to bf16 in registers
+ * and never written. 16-byte aligned rows (x, weight, bias, ring, the fp32
+ * outputs) with strides of whole 8-element chunks. */
+int vm_deltanet_conv_prep(float* qe, float* ke, float* ve, float* beta, float* gate,
+                          const vm_bf16* x, int64_t x_st, int64_t x_sb, const vm_bf16* w,
+                          int64_t w_cs, const vm_bf16* bias, const vm_bf16* s_in, vm_bf16* s_out,
+                          int64_t s_cs, int64_t s_sb, int K, const vm_bf16* ab, int64_t ab_st,
+                          int64_t ab_sb, const float* a_log, const float* dt_bias, int Dk, int Dv,
+                          int Hk, int Hv, int T, int B, vm_stream stream);
+
 /* The prefill's gated RMSNorm + z gate (qwen35.jl:360-364): o (Dv, T, Hv, B)
  * fp32 and z (Dv, Hv) rows of each token (token stride z_st, sequence stride
  * z_sb, bf16) -> y = o rstd NormWeight silu(z), bf16, (Dv, Hv) rows at y_st /

@@ -285,6 +285,60 @@ def test_prep_and_gated_norm(vm, orc, off):
     assert_bf16_close(dev_f32(Y), y_ref, "gated norm", extra=1e-6)
 
 
+@pytest.mark.parametrize("B,T,prefix,bias,hk,hv", [(1, 37, False, True, HK, HV),
+                                                   (2, 16, True, False, HK, HV),
+                                                   (3, 5, True, True, HK, HV),
+                                                   (1, 100, False, False, HK, HV),
+                                                   (2, 33, True, True, 2, 6)])
+def test_deltanet_conv_prep(vm, orc, B, T, prefix, bias, hk, hv):
+    """The prefill's conv and prep in one pass equal, bit for bit, the conv
+    (silu) followed by the prep on the GPU, from strided projection rows, with
+    and without a prefix ring; the prep of the conv's output also against the
+    oracle's, and the ring against the oracle's."""
+    banner(f"deltanet conv + prep B={B} T={T} prefix={prefix} bias={bias} Hk={hk} Hv={hv}")
+    nch = 2 * hk * DK + hv * DV
+    qz = normal_bf16((B, T, nch + hv * DV), 1990 + T)  # q | k | v | z projection rows
+    abw = normal_bf16((B, T, 2 * hv + 8), 1991)
+    w = normal_bf16((KC, nch), 1992, scale=0.5)
+    b = normal_bf16((nch,), 1993, scale=0.1) if bias else None
+    ring0 = normal_bf16((B, KC, nch), 1994) if prefix else None
+    a_log = normal_f32(hv, 1995, scale=0.5)
+    dt_bias = normal_f32(hv, 1996, scale=0.5)
+    X = to_dev(qz)[..., :nch]
+    AB = to_dev(abw)[..., 4:4 + 2 * hv]
+    W, Bb = to_dev(w), (None if b is None else to_dev(b))
+    A, Dt = f32dev(a_log), f32dev(dt_bias)
+
+    def outs():
+        f = dict(dtype=torch.float32, device="cuda")
+        return {"Q": torch.empty((B, hk, T, DK), **f), "K": torch.empty((B, hk, T, DK), **f),
+                "V": torch.empty((B, hv, T, DV), **f), "Beta": torch.empty((B, T, hv), **f),
+                "Gate": torch.empty((B, T, hv), **f)}
+
+    def ring():
+        return to_dev(ring0) if prefix else torch.zeros((B, KC, nch), dtype=torch.bfloat16,
+                                                         device="cuda")
+    S1, S2 = ring(), ring()
+    conv = vm.causal_conv1d_sequence(X, W, Bb, sigma="silu", Sp=S1, S=S1 if prefix else None)["Y"]
+    two = outs()
+    vm.deltanet_prefill_prep_(two, conv, AB, A, Dt, Dk=DK, Dv=DV, Hk=hk, Hv=hv)
+    one = outs()
+    vm.deltanet_conv_prep_(one, X, W, AB, A, Dt, Bb, Dk=DK, Dv=DV, Hk=hk, Hv=hv, Sp=S2,
+                           S=S2 if prefix else None)
+    torch.cuda.synchronize()
+    for key in ("Q", "K", "V", "Beta", "Gate"):
+        assert torch.equal(one[key], two[key]), key
+    assert torch.equal(S1, S2)
+    _, ring_ref = orc.conv1d_sequence(np.ascontiguousarray(qz[..., :nch]), w, b, s_in=ring0,
+                                      act=True)
+    assert np.array_equal(from_dev(S2), ring_ref)
+    p_ref = orc.deltanet_prep(from_dev(conv), np.ascontiguousarray(abw[..., 4:4 + 2 * hv]),
+                              a_log, dt_bias, Dk=DK, Dv=DV, Hk=hk, Hv=hv)
+    for key, rk in (("Q", "q"), ("K", "k"), ("V", "v"), ("Beta", "beta"), ("Gate", "gate")):
+        np.testing.assert_allclose(one[key].cpu().numpy(), p_ref[rk], rtol=2e-6, atol=1e-7,
+                                   err_msg=key)
+
+
 def test_prep_many_value_heads(vm, orc):
     """The prep with more value heads than a wave has lanes (Hk = 2, Hv = 72): the
     gates of heads 64 .. 71 too."""

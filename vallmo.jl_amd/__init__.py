@@ -20,7 +20,8 @@ from .ops import (attention, attention_, decode_attention, decode_attention_,  #
                   sigmoid, sigmoid_gate_, silu_mul_, causal_conv1d, causal_conv1d_,
                   causal_conv1d_sequence, causal_conv1d_sequence_, fused_deltanet_decode,
                   fused_deltanet_decode_, deltanet_recurrent_decode, deltanet_recurrent_decode_,
-                  deltanet_sequence, deltanet_sequence_, deltanet_prefill_prep_, gated_rms_norm_,
+                  deltanet_sequence, deltanet_sequence_, deltanet_prefill_prep_,
+                  deltanet_conv_prep_, gated_rms_norm_,
                   linear_add_rms_norm_, linear_add_rms_norm_workspace_bytes,
                   linear_silu_mul_, linear_silu_mul_workspace_bytes,
                   linear_causal_conv1d_, linear_causal_conv1d_workspace_bytes,

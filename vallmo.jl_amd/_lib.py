@@ -150,6 +150,9 @@ _SIGS = {
                                                 + [_p, _c_sz, _p]),
     "vm_deltanet_prefill_prep": (_c_i, [_p] * 5 + [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _p]
                                  + [_c_i] * 6 + [_p]),
+    "vm_deltanet_conv_prep": (_c_i, [_p] * 5 + [_p, _c_i64, _c_i64, _p, _c_i64, _p, _p, _p, _c_i64,
+                                      _c_i64, _c_i, _p, _c_i64, _c_i64, _p, _p]
+                              + [_c_i] * 6 + [_p]),
     "vm_gated_rms_norm": (_c_i, [_p, _c_i64, _c_i64, _p, _p, _c_i64, _c_i64, _p, _c_i, _c_i,
                                  _c_i, _c_i, _c_f, _p]),
     "vm_fill_normal_bf16": (_c_i, [_p, _c_i64, _c_u64, _c_f, _c_f, _p]),

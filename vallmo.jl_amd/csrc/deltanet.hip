@@ -1271,6 +1271,98 @@ __global__ __launch_bounds__(256) void conv1d_sequence_kernel(Conv1dArgs a) {
   }
 }
 
+// ---- the prefill's conv and prep in one pass (qwen35.jl:333-356): thread = 8
+// channels x a run of CONV_TC tokens as in conv1d_sequence_kernel, the 16
+// lanes of a head's 128 channels in one 16-lane group. Per token the conv
+// output is rounded to bf16 (the value the two-kernel form stores between the
+// kernels), then each q / k head row is scaled by its inverse L2 norm (q also
+// by Dk^-1/2) over the group, and the row is written fp32 to Q / K / V, head
+// major, as deltanet_prep_vec_kernel writes it: bit for bit the two-kernel
+// result, without the conv output's round trip through memory. Workgroup
+// column 0 also writes beta and the gate of its run's tokens.
+template <int K>
+__global__ __launch_bounds__(256) void deltanet_conv_prep_kernel(ConvPrepArgs a) {
+  static_assert(CONV_TC >= K - 1, "run 0 must cover the context reads");
+  const Conv1dArgs& c = a.c;
+  const DeltaPrepArgs& p = a.p;
+  const int run = blockIdx.y, b = blockIdx.z;
+  const int t0 = run * CONV_TC;
+  const int t1 = min(t0 + CONV_TC, c.T);
+  if (blockIdx.x == 0) {
+    const uint16_t* ab = p.ab + (int64_t)b * p.ab_sb;
+    for (int i = threadIdx.x; i < (t1 - t0) * p.Hv; i += 256) {
+      const int t = t0 + i / p.Hv, hv = i % p.Hv;
+      const int64_t gi = ((int64_t)b * p.T + t) * p.Hv + hv;
+      p.beta[gi] = accurate_sigmoid(bf2f(ab[(int64_t)t * p.ab_st + p.Hv + hv]));
+      p.gate[gi] = -expf(p.a_log[hv]) * log1pf(expf(bf2f(ab[(int64_t)t * p.ab_st + hv]) + p.dt_bias[hv]));
+    }
+  }
+  const int64_t c8 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c8 * 8 >= c.D) return;  // whole heads: a 16-lane group is all in or all out
+  const int d = (int)c8 * 8;
+  const int hh = d / DN_D, dc = d % DN_D;
+  float* dst;  // this lane's 8 columns of head hh, token 0
+  if (hh < p.Hk)
+    dst = p.qe + ((int64_t)b * p.Hk + hh) * p.T * DN_D + dc;
+  else if (hh < 2 * p.Hk)
+    dst = p.ke + ((int64_t)b * p.Hk + hh - p.Hk) * p.T * DN_D + dc;
+  else
+    dst = p.ve + ((int64_t)b * p.Hv + hh - 2 * p.Hk) * p.T * DN_D + dc;
+  const bool qk = hh < 2 * p.Hk;
+  const float sc = hh < p.Hk ? 1.0f / sqrtf((float)DN_D) : 1.0f;
+  float wf[K][8];
+#pragma unroll
+  for (int i = 0; i < K; ++i)
+    unpack8(*reinterpret_cast<const uint4*>(c.w + (int64_t)i * c.w_cs + d), wf[i]);
+  float bias8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (c.bias) unpack8(*reinterpret_cast<const uint4*>(c.bias + d), bias8);
+  float win[K][8];  // win[i] = ext(t - K + 1 + i) for the current t
+#pragma unroll
+  for (int i = 0; i < K - 1; ++i) unpack8(conv_ext<K>(c, b, d, t0 - K + 1 + i), win[i]);
+  for (int t = t0; t < t1; ++t) {
+    unpack8(conv_ext<K>(c, b, d, t), win[K - 1]);
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = 0.f;
+#pragma unroll
+      for (int i = 0; i < K; ++i) v += win[i][e] * wf[i][e];
+      v += bias8[e];
+      acc[e] = c.act ? accurate_silu(v) : v;
+    }
+    float x[8];
+    unpack8(pack8(acc), x);  // the conv output, bf16
+    float den = 1.0f;
+    if (qk) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+      ss += xor32<8>(ss);
+      ss += xor32<4>(ss);
+      ss += xor32<2>(ss);
+      ss += xor32<1>(ss);
+      den = sqrtf(ss + 1e-6f);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = x[j] / den * sc;
+    float4* d4 = reinterpret_cast<float4*>(dst + (int64_t)t * DN_D);
+    d4[0] = make_float4(x[0], x[1], x[2], x[3]);
+    d4[1] = make_float4(x[4], x[5], x[6], x[7]);
+#pragma unroll
+    for (int i = 0; i + 1 < K; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[i][e] = win[i + 1][e];
+  }
+  if (run == 0 && c.s_out) {
+    uint4 seed[K];  // column i = ext(T - K + i); every column read first (aliasing)
+#pragma unroll
+    for (int i = 0; i < K; ++i) seed[i] = conv_ext<K>(c, b, d, c.T - K + i);
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+      *reinterpret_cast<uint4*>(c.s_out + b * c.s_sb + (int64_t)i * c.s_cs + d) = seed[i];
+  }
+}
+
 // ---- launchers -----------------------------------------------------------
 hipError_t launch_deltanet_fused_decode(const DeltaFusedArgs& a, hipStream_t st) {
   if (a.B == 0) return hipSuccess;
@@ -1367,6 +1459,20 @@ hipError_t launch_conv1d_update_sk(const Conv1dSkArgs& a, hipStream_t st) {
   switch (a.c.K) {
 #define X(k) \
   case k: hipLaunchKernelGGL(conv1d_update_sk_kernel<k>, grid, dim3(256), 0, st, a); break;
+    VM_CONV_K_CASES(X)
+#undef X
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_deltanet_conv_prep(const ConvPrepArgs& a, hipStream_t st) {
+  if (a.c.B == 0 || a.c.T == 0) return hipSuccess;
+  const int runs = (a.c.T + CONV_TC - 1) / CONV_TC;
+  const dim3 grid((unsigned)((a.c.D / 8 + 255) / 256), runs, a.c.B);
+  switch (a.c.K) {
+#define X(k) \
+  case k: hipLaunchKernelGGL(deltanet_conv_prep_kernel<k>, grid, dim3(256), 0, st, a); break;
     VM_CONV_K_CASES(X)
 #undef X
     default: return hipErrorInvalidValue;

@@ -373,6 +373,13 @@ struct Conv1dArgs {
   const uint16_t* bias;
   int D, K, T, B, act;
 };
+// the prefill's conv (c: x the projection's q | k | v channels, D = (2 Hk + Hv)
+// Dk, c.y unused) and prep (p: p.cv unused; outputs and gates as DeltaPrepArgs)
+// in one pass; the launcher's caller checks 16-byte alignment of every row
+struct ConvPrepArgs {
+  Conv1dArgs c;
+  DeltaPrepArgs p;
+};
 // causal_conv1d! on the first D channels of a projection given as stream-K
 // partials (gemv_sk_kernel): the projection's M channels are written rounded to
 // bf16 at yp (column stride yp_sb), c.x is unused
@@ -409,6 +416,7 @@ hipError_t launch_deltanet_prep(const DeltaPrepArgs& a, hipStream_t st);
 hipError_t launch_gated_rms_norm(const GatedNormArgs& a, hipStream_t st);
 hipError_t launch_conv1d_update(const Conv1dArgs& a, hipStream_t st);
 hipError_t launch_conv1d_sequence(const Conv1dArgs& a, hipStream_t st);
+hipError_t launch_deltanet_conv_prep(const ConvPrepArgs& a, hipStream_t st);
 hipError_t launch_silu_mul(const SiluMulArgs& a, hipStream_t st);
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t st);
 hipError_t launch_gen_advance(const AdvanceArgs& a, hipStream_t st);

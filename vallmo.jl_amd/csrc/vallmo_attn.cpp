@@ -1078,6 +1078,48 @@ int vm_deltanet_prefill_prep(float* qe, float* ke, float* ve, float* beta, float
                     "deltanet_prefill_prep");
 }
 
+int vm_deltanet_conv_prep(float* qe, float* ke, float* ve, float* beta, float* gate,
+                          const vm_bf16* x, int64_t x_st, int64_t x_sb, const vm_bf16* w,
+                          int64_t w_cs, const vm_bf16* bias, const vm_bf16* s_in, vm_bf16* s_out,
+                          int64_t s_cs, int64_t s_sb, int K, const vm_bf16* ab, int64_t ab_st,
+                          int64_t ab_sb, const float* a_log, const float* dt_bias, int Dk, int Dv,
+                          int Hk, int Hv, int T, int B, vm_stream st) {
+  TRY(check_dn_heads(Dk, Dv, Hk, Hv, B, "deltanet_conv_prep"));
+  const int D = 2 * Hk * Dk + Hv * Dv;
+  TRY(check_conv(D, K, B, T, "deltanet_conv_prep"));
+  if (B == 0 || T == 0) return VM_OK;
+  REQUIRE(qe && ke && ve && beta && gate && ab && a_log && dt_bias, VM_E_ARG,
+          "deltanet_conv_prep: NULL pointer argument");
+  TRY(check_aligned(x, "X"));
+  TRY(check_aligned(w, "Weight"));
+  if (bias) TRY(check_aligned(bias, "Bias"));
+  if (s_in) TRY(check_aligned(s_in, "S"));
+  if (s_out) TRY(check_aligned(s_out, "S_out"));
+  for (const float* p : {qe, ke, ve})
+    REQUIRE((reinterpret_cast<uintptr_t>(p) & 15u) == 0, VM_E_ARG,
+            "deltanet_conv_prep: fp32 outputs must be 16-byte aligned");
+  for (int64_t v : {x_st, x_sb, w_cs, s_cs, s_sb}) TRY(check_stride(v, "deltanet_conv_prep"));
+  REQUIRE(ab_st >= 0 && ab_sb >= 0, VM_E_ARG, "deltanet_conv_prep: negative ab stride");
+  REQUIRE(w_cs >= D && (T <= 1 || (x_st >= D && ab_st >= 2LL * Hv)) &&
+              (B <= 1 || (x_sb >= x_st * T && ab_sb >= ab_st * T)),
+          VM_E_DIM, "deltanet_conv_prep: strides below the extents (n = %d, T = %d)", D, T);
+  if (s_in || s_out)
+    REQUIRE(s_cs >= D && (B <= 1 || s_sb >= s_cs * K), VM_E_DIM,
+            "deltanet_conv_prep: state strides below (n, K) = (%d, %d)", D, K);
+  if (s_in && s_out)
+    TRY(check_alias(s_in, s_out, (size_t)((B - 1) * s_sb + (K - 1) * s_cs + D) * 2,
+                    "deltanet_conv_prep"));
+  vm::ConvPrepArgs a{};
+  a.c.x = x; a.c.x_st = x_st; a.c.x_sb = x_sb; a.c.s_in = s_in; a.c.s_out = s_out;
+  a.c.s_cs = s_cs; a.c.s_sb = s_sb; a.c.w = w; a.c.w_cs = w_cs; a.c.bias = bias;
+  a.c.D = D; a.c.K = K; a.c.T = T; a.c.B = B; a.c.act = 1;
+  a.p.ab = ab; a.p.ab_st = ab_st; a.p.ab_sb = ab_sb; a.p.a_log = a_log; a.p.dt_bias = dt_bias;
+  a.p.qe = qe; a.p.ke = ke; a.p.ve = ve; a.p.beta = beta; a.p.gate = gate;
+  a.p.T = T; a.p.Hk = Hk; a.p.Hv = Hv; a.p.B = B;
+  return hip_status(timed(VM_K_CONV, S(st), [&] { return vm::launch_deltanet_conv_prep(a, S(st)); }),
+                    "deltanet_conv_prep");
+}
+
 int vm_gated_rms_norm(vm_bf16* y, int64_t y_st, int64_t y_sb, const float* o, const vm_bf16* z,
                       int64_t z_st, int64_t z_sb, const vm_bf16* norm_w, int Dv, int Hv, int T,
                       int B, float eps, vm_stream st) {

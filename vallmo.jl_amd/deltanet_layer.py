@@ -175,15 +175,15 @@ def forward(l: DeltaNetLayer, c: DeltaNetConfig, xn, T: int, B: int, *, eps: flo
     qzab = ops.linear(xn2, l.W_in, workspace=workspace_for(xn2, l.W_in))["y"].view(B, T, -1)
     qz, ab = qzab[..., :m], qzab[..., m:]                               # :322-323
     X, z = _views(qz, c)
-    conv = torch.empty((B, T, c.n), dtype=torch.bfloat16, device=xn.device)
-    ops.causal_conv1d_sequence_({"Y": conv}, X, l.conv_w, l.conv_b, sigma="silu",
-                                Sp=l.conv_state, S=l.conv_state if offset > 0 else None)
     f32 = dict(dtype=torch.float32, device=xn.device)
     p = {"Q": torch.empty((B, c.Hk, T, c.Dk), **f32), "K": torch.empty((B, c.Hk, T, c.Dk), **f32),
          "V": torch.empty((B, c.Hv, T, c.Dv), **f32), "Beta": torch.empty((B, T, c.Hv), **f32),
          "Gate": torch.empty((B, T, c.Hv), **f32)}
-    ops.deltanet_prefill_prep_(p, conv, ab, l.A_log, l.dt_bias, Dk=c.Dk, Dv=c.Dv, Hk=c.Hk,
-                               Hv=c.Hv)
+    # the sequence conv (silu) and the prep in one pass: the conv output stays in
+    # registers (causal_conv1d_sequence! then :347-356, bit for bit)
+    ops.deltanet_conv_prep_(p, X, l.conv_w, ab, l.A_log, l.dt_bias, l.conv_b, Dk=c.Dk, Dv=c.Dv,
+                            Hk=c.Hk, Hv=c.Hv, Sp=l.conv_state,
+                            S=l.conv_state if offset > 0 else None)
     y = torch.empty((B, T, c.Hv, c.Dv), dtype=torch.bfloat16, device=xn.device)
     # the recurrence in place on S with the gated norm fused into its output
     # kernel (:357-364: O never reaches memory)

@@ -29,7 +29,7 @@ __all__ = [
     "causal_conv1d_", "causal_conv1d", "causal_conv1d_sequence_", "causal_conv1d_sequence",
     "fused_deltanet_decode_", "fused_deltanet_decode", "deltanet_recurrent_decode_",
     "deltanet_recurrent_decode", "deltanet_sequence_", "deltanet_sequence",
-    "deltanet_prefill_prep_", "gated_rms_norm_", "linear_add_rms_norm_",
+    "deltanet_prefill_prep_", "deltanet_conv_prep_", "gated_rms_norm_", "linear_add_rms_norm_",
     "deltanet_sequence_chunked_", "deltanet_sequence_workspace_bytes",
     "deltanet_sequence_chunked_gated_norm_",
     "linear_add_rms_norm_workspace_bytes",
@@ -762,6 +762,39 @@ def deltanet_prefill_prep_(outs, CV, AB, A_log, DtBias, *, Dk, Dv, Hk, Hv):
          _p(outs["Beta"]), _p(outs["Gate"]), _p(CV), _st(CV, 1, n), _st(CV, 0, T * n), _p(AB),
          _st(AB, 1, 2 * Hv), _st(AB, 0, T * 2 * Hv), _p(A_log), _p(DtBias), Dk, Dv, Hk, Hv, T, B,
          _stream())
+    return outs
+
+
+def deltanet_conv_prep_(outs, X, Weight, AB, A_log, DtBias, Bias=None, *, Dk, Dv, Hk, Hv, Sp=None,
+                        S=None):
+    """The prefill's sequence conv and prep in one pass (src/llm/qwen35.jl:333-356):
+    causal_conv1d_sequence_ of X (the q | k | v rows of the projection, (n, T, B),
+    torch (B, T, n), token rows may be strided) with σ = silu, Weight (n, K), Bias,
+    the ring S / S′ (Sp) as there, then deltanet_prefill_prep_ of its output and AB
+    into outs "Q", "K", "V", "Beta", "Gate" — the same values bit for bit, the conv
+    output never written."""
+    n = 2 * Hk * Dk + Hv * Dv
+    dims = sizes(X=(X, f"{n} T B"), Weight=(Weight, f"{n} K"), Bias=(Bias, f"{n}"),
+                 Sp=(Sp, f"{n} K B"), S=(S, f"{n} K B"), AB=(AB, f"{2 * Hv} T B"),
+                 A_log=(A_log, f"{Hv}"), DtBias=(DtBias, f"{Hv}"),
+                 Q=(outs["Q"], f"{Dk} T {Hk} B"), K=(outs["K"], f"{Dk} T {Hk} B"),
+                 V=(outs["V"], f"{Dv} T {Hv} B"), Beta=(outs["Beta"], f"{Hv} T B"),
+                 Gate=(outs["Gate"], f"{Hv} T B"))
+    T, B, K = dims["T"], dims["B"], dims["K"]
+    for t, nm in ((X, "X"), (Weight, "Weight"), (Bias, "Bias"), (Sp, "S′"), (S, "S"), (AB, "AB")):
+        _need(t, torch.bfloat16, nm)
+    for n_ in ("Q", "K", "V", "Beta", "Gate"):
+        _need(outs[n_], torch.float32, n_)
+        _need_contig(outs[n_], n_)
+    ring = Sp if Sp is not None else S
+    if Sp is not None and S is not None and S.stride() != Sp.stride():
+        raise ArgumentError("S and S′ must share strides")
+    s_cs = _st(ring, 1, n) if ring is not None else n
+    s_sb = _st(ring, 0, K * n) if ring is not None else K * n
+    call("vm_deltanet_conv_prep", _p(outs["Q"]), _p(outs["K"]), _p(outs["V"]), _p(outs["Beta"]),
+         _p(outs["Gate"]), _p(X), _st(X, 1, n), _st(X, 0, T * n), _p(Weight), _st(Weight, 0, n),
+         _p(Bias), _p(S), _p(Sp), s_cs, s_sb, K, _p(AB), _st(AB, 1, 2 * Hv),
+         _st(AB, 0, T * 2 * Hv), _p(A_log), _p(DtBias), Dk, Dv, Hk, Hv, T, B, _stream())
     return outs
 
 
