@@ -504,11 +504,13 @@ int vm_deltanet_sequence(float* o, const float* q, const float* k, const float* 
                          const float* beta, const float* gate, const float* s_in, float* s_out,
                          int Dk, int Dv, int T, int Hk, int Hv, int B, vm_stream stream);
 
-/* deltanet_sequence! in its chunked form: the same arguments and results (to
- * fp32 rounding), computed per 64-token chunk as a lower-triangular solve and
- * fp32 MFMA products (delta = U - W S_0, O = gamma Q S_0 + M delta, S_C =
- * gamma_C S_0 + K~^T delta: the sequential recurrence's exact algebra), the
- * chunks' state carried by one sequential scan. No separate reference
+/* deltanet_sequence! in its chunked form: the same arguments and results
+ * (within 5e-4 of the sequential fp32 result, the tests' bar), computed per
+ * 64-token chunk as a lower-triangular solve and matrix products (delta = U -
+ * W S_0, O = gamma Q S_0 + M delta, S_C = gamma_C S_0 + K~^T delta: the
+ * sequential recurrence's exact algebra) on the bf16 MFMA in split precision
+ * (each fp32 operand as bf16 hi + lo, products hi hi + hi lo + lo hi, fp32
+ * accumulation and state), the chunks' state carried by one sequential scan. No separate reference
  * function: the reference runs the sequential loop (deltanet_recurrent.jl:
  * 109-172); this is the same operator, parallel over each chunk: a chunk
  * kernel, one sequential scan over the chunks' states, and a chunk-parallel
