@@ -392,6 +392,27 @@ int vm_linear_causal_conv1d(vm_bf16* y, int64_t ldy, const vm_bf16* x, int64_t l
                             const vm_bf16* conv_b, int D, int Kc, int act, void* workspace,
                             size_t workspace_bytes, vm_stream stream);
 
+/* decode!(h, ::DeltaNetLayer, ...) through its recurrence in one call
+ * (src/llm/qwen35.jl:212-232 without the out projection): linear! of the
+ * projection W (K, M) K-major over x (K, B) into [q | k | v | z | alpha |
+ * beta] (M = 2 Hk Dk + 2 Hv Dv + 2 Hv rows), causal_conv1d! of its q | k | v
+ * channels on the ring (sigma = silu) and fused_deltanet_decode! into O
+ * (Dv, Hv, B) (sequence stride o_sb) and the state: the results of
+ * vm_linear_causal_conv1d (act = 1) followed by vm_fused_deltanet_decode on
+ * its outputs, bit for bit. At B <= 32 with 16-byte aligned x and W and Hv /
+ * Hk in {1, 2, 4} the projection's stream-K partials go straight to one
+ * kernel per (qk head, sequence) and y (ldy) and yc (the conv output,
+ * yc_sb) are not written; otherwise the two calls run, through y and yc.
+ * workspace: vm_linear_causal_conv1d_workspace_bytes(M, B, K, ldw, ldx, ldy). */
+int vm_linear_deltanet_decode(vm_bf16* o, int64_t o_sb, vm_bf16* y, int64_t ldy, vm_bf16* yc,
+                              int64_t yc_sb, const vm_bf16* x, int64_t ldx, const vm_bf16* w,
+                              int64_t ldw, int M, int K, const vm_bf16* ring_in, vm_bf16* ring_out,
+                              int64_t s_cs, int64_t s_sb, const vm_bf16* conv_w,
+                              int64_t conv_w_cs, const vm_bf16* conv_b, int Kc, const float* a_log,
+                              const float* dt_bias, const vm_bf16* norm_w, const float* s_in,
+                              float* s_out, int Dk, int Dv, int Hk, int Hv, int B, float eps,
+                              void* workspace, size_t workspace_bytes, vm_stream stream);
+
 /* ---- f2: the rest of the decode step (src/llm/qwen35.jl:247-273) --------
  * Matrices are column-major bf16 with an element column stride (a multiple of
  * 8, pointers 16-byte aligned); M, I, D, K multiples of 8.

@@ -195,6 +195,92 @@ def test_fused_deltanet_decode(vm, orc, B, inplace):
     assert_bf16_close(dev_f32(out["O"]), o_ref, "fused decode O", extra=1e-5)
 
 
+@pytest.mark.parametrize("B,hk,hv,bias", [(32, HK, HV, False), (1, HK, HV, True),
+                                           (5, 16, 16, True), (3, 8, 32, False),
+                                           (40, HK, HV, True)])
+def test_linear_deltanet_decode(vm, orc, B, hk, hv, bias):
+    """The DeltaNet layer's decode step up to its out projection in one call
+    (qwen35.jl:212-232): O, the state and the ring bit for bit equal to
+    linear_causal_conv1d_ followed by fused_deltanet_decode_ on the same inputs,
+    for Hv / Hk = 2, 1, 4 (one kernel per (qk head, sequence) at B <= 32; B = 40
+    runs the two calls); O and the state also within the bars of the oracle's
+    conv step and fused decode on the two-call path's bf16 projection. Two steps
+    in a row from the in-place ring and state."""
+    banner(f"linear_deltanet_decode B={B} Hk={hk} Hv={hv} bias={bias}")
+    Kdim = 640
+    nch = 2 * hk * DK + hv * DV
+    M = nch + hv * DV + 2 * hv
+    x = normal_bf16((2, B, Kdim), 960 + B)
+    W = normal_bf16((M, Kdim), 961, scale=Kdim ** -0.5)
+    ring = normal_bf16((B, KC, nch), 962 + B)
+    w = normal_bf16((KC, nch), 963, scale=0.5)
+    b = normal_bf16((nch,), 964, scale=0.1) if bias else None
+    a_log = normal_f32(hv, 965, scale=0.5)
+    dt_bias = normal_f32(hv, 966, scale=0.5)
+    norm_w = normal_bf16((DV,), 967, scale=0.2, shift=1.0)
+    s = normal_f32(B * hv * DV * DK, 968, scale=0.05).reshape(B, hv, DV, DK)
+    Wd, wd, nd = to_dev(W), to_dev(w), to_dev(norm_w)
+    bd = None if b is None else to_dev(b)
+    al, dt = f32dev(a_log), f32dev(dt_bias)
+    m = nch + hv * DV
+
+    def two_calls():
+        S_ring, S = to_dev(ring), f32dev(s)
+        y = torch.empty((B, M), dtype=torch.bfloat16, device="cuda")
+        Y = torch.empty((B, nch), dtype=torch.bfloat16, device="cuda")
+        O = torch.empty((B, hv, DV), dtype=torch.bfloat16, device="cuda")
+        ys, Os = [], []
+        for t in range(2):
+            vm.linear_causal_conv1d_({"y": y, "Y": Y, "Sp": S_ring}, to_dev(x[t]), Wd, S_ring,
+                                     wd, bd, sigma="silu")
+            q = Y[:, :hk * DK].unflatten(-1, (hk, DK))
+            k = Y[:, hk * DK:2 * hk * DK].unflatten(-1, (hk, DK))
+            v = Y[:, 2 * hk * DK:].unflatten(-1, (hv, DV))
+            z = y[:, nch:m].unflatten(-1, (hv, DV))
+            vm.fused_deltanet_decode_({"O": O, "Sp": S}, q, k, v, y[:, m:m + hv],
+                                      y[:, m + hv:], z, al, dt, nd, S, eps=EPS)
+            ys.append((y.clone(), Y.clone()))
+            Os.append(O.clone())
+        return Os, S, S_ring, ys
+
+    def one_call():
+        S_ring, S = to_dev(ring), f32dev(s)
+        y = torch.empty((B, M), dtype=torch.bfloat16, device="cuda")
+        Y = torch.empty((B, nch), dtype=torch.bfloat16, device="cuda")
+        O = torch.empty((B, hv, DV), dtype=torch.bfloat16, device="cuda")
+        Os = []
+        for t in range(2):
+            vm.linear_deltanet_decode_({"O": O, "y": y, "Y": Y, "Sp_ring": S_ring, "Sp": S},
+                                       to_dev(x[t]), Wd, S_ring, wd, bd, al, dt, nd, S, Dk=DK,
+                                       Dv=DV, Hk=hk, Hv=hv, eps=EPS)
+            Os.append(O.clone())
+        return Os, S, S_ring
+
+    O2, S2, R2, ys = two_calls()
+    O1, S1, R1 = one_call()
+    torch.cuda.synchronize()
+    for t in range(2):
+        assert torch.equal(O1[t].view(torch.int16), O2[t].view(torch.int16)), f"O step {t}"
+    assert torch.equal(S1, S2)
+    assert torch.equal(R1.view(torch.int16), R2.view(torch.int16))
+    # the first step against the oracle's fused decode on the two-call path's
+    # bf16 projection and conv output (those two are pinned by
+    # test_linear_causal_conv1d)
+    yb, cv = from_dev(ys[0][0]), from_dev(ys[0][1])
+    o_ref, s_ref = orc.fused_deltanet_decode(
+        cv[:, :hk * DK].reshape(B, hk, DK), cv[:, hk * DK:2 * hk * DK].reshape(B, hk, DK),
+        cv[:, 2 * hk * DK:].reshape(B, hv, DV), yb[:, m:m + hv], yb[:, m + hv:],
+        yb[:, nch:m].reshape(B, hv, DV), a_log, dt_bias, norm_w, s, eps=EPS)
+    assert_bf16_close(dev_f32(O1[0]), o_ref, "one-call decode O", extra=1e-5)
+    if B == 1:
+        s1 = f32dev(s)
+        vm.linear_deltanet_decode_({"O": O1[0], "y": ys[0][0], "Y": ys[0][1], "Sp_ring": R1,
+                                    "Sp": s1}, to_dev(x[0]), Wd, to_dev(ring), wd, bd, al, dt, nd,
+                                   f32dev(s), Dk=DK, Dv=DV, Hk=hk, Hv=hv, eps=EPS)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(s1.cpu().numpy(), s_ref, rtol=2e-5, atol=2e-6)
+
+
 def _prepped(B, T, seed):
     cv = normal_bf16((B, T, NCH), seed)
     ab = normal_bf16((B, T, 2 * HV), seed + 1)

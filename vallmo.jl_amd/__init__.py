@@ -25,6 +25,7 @@ from .ops import (attention, attention_, decode_attention, decode_attention_,  #
                   linear_add_rms_norm_, linear_add_rms_norm_workspace_bytes,
                   linear_silu_mul_, linear_silu_mul_workspace_bytes,
                   linear_causal_conv1d_, linear_causal_conv1d_workspace_bytes,
+                  linear_deltanet_decode_,
                   deltanet_sequence_chunked_, deltanet_sequence_workspace_bytes,
                   deltanet_sequence_chunked_gated_norm_)
 from .layer import (AttnConfig, AttnLayer, AttnModel, CaptureSession, Generation,  # noqa: F401

@@ -120,6 +120,10 @@ _SIGS = {
     "vm_linear_causal_conv1d": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i, _c_i, _c_i, _p,
                                        _c_i64, _p, _p, _c_i64, _c_i64, _p, _c_i64, _p, _c_i,
                                        _c_i, _c_i, _p, _c_sz, _p]),
+    "vm_linear_deltanet_decode": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _p, _c_i64, _p,
+                                         _c_i64, _c_i, _c_i, _p, _p, _c_i64, _c_i64, _p, _c_i64,
+                                         _p, _c_i, _p, _p, _p, _p, _p, _c_i, _c_i, _c_i, _c_i,
+                                         _c_i, _c_f, _p, _c_sz, _p]),
     "vm_linear_silu_mul_workspace_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i64, _c_i64]),
     "vm_linear_silu_mul": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i, _c_i, _c_i, _p, _c_sz,
                                   _p]),

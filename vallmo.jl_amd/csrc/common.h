@@ -218,6 +218,18 @@ __device__ __forceinline__ void store_row4(uint16_t* p, int lane, const float x[
 // partials of row group m / 128, one 16 KB slot per workgroup that touched it
 // ([4 tiles][32 columns][32 rows] fp32, slot = workgroup + row group), added
 // in workgroup order.
+// one row's sum (the same additions as gemv_sk_sum4's lane for it)
+__device__ __forceinline__ float gemv_sk_sum1(const float* part, int G, int chunk, int m, int n) {
+  const int rg = m >> 7, v = (m >> 5) & 3, r = m & 31;
+  const int wf = (rg * G) / chunk, wl = ((rg + 1) * G - 1) / chunk;
+  const float* src = part + ((int64_t)(wf + rg) * 4 + v) * 1024 + n * 32 + r;
+  float s = *src;
+  for (int w = wf + 1; w <= wl; ++w) {
+    src += 4096;
+    s += *src;
+  }
+  return s;
+}
 __device__ __forceinline__ float4 gemv_sk_sum4(const float* part, int G, int chunk, int m, int n) {
   const int rg = m >> 7, v = (m >> 5) & 3, r = m & 31;
   const int wf = (rg * G) / chunk, wl = ((rg + 1) * G - 1) / chunk;

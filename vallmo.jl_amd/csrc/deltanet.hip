@@ -197,6 +197,138 @@ __global__ __launch_bounds__(256) void deltanet_fused_decode_kernel(DeltaFusedAr
     a.o[b * a.o_sb + hv * DN_D + col] = f2bf(out * rstd * w_col * accurate_silu(z_col));
 }
 
+// ---- the DeltaNet layer's decode step after its projection in one kernel
+// (qwen35.jl:212-232): one workgroup of 4 R waves per (qk head hk, sequence),
+// R = Hv / Hk value heads. First every thread takes 4-channel groups of the
+// projection [q | k | v | z | alpha | beta] of this head: the stream-K
+// partials summed in workgroup order and rounded to bf16 (the value linear!
+// stores), then for q, k and v the conv step as conv1d_update_sk_kernel
+// (ring shift, silu, bf16), into LDS, the channels' ring columns written
+// (each channel has one owner: the qk head's q and k, its R heads' v). The
+// state loads are issued first and land meanwhile. Then wave group j runs
+// fused_deltanet_decode! for value head hk R + j as deltanet_fused_decode_kernel,
+// its inputs from LDS: bit for bit the results of linear_causal_conv1d
+// followed by fused_deltanet_decode, one launch and the bf16 projection and
+// conv output round trips fewer.
+namespace {
+__device__ __forceinline__ void unpack4(const uint2& u, float (&x)[4]) {
+  x[0] = __uint_as_float(u.x << 16);
+  x[1] = __uint_as_float(u.x & 0xffff0000u);
+  x[2] = __uint_as_float(u.y << 16);
+  x[3] = __uint_as_float(u.y & 0xffff0000u);
+}
+}  // namespace
+
+template <int KC, int R>
+__global__ __launch_bounds__(256 * R) void deltanet_decode_sk_kernel(DeltaDecodeSkArgs a) {
+  constexpr int NI = 16;
+  const DeltaFusedArgs& f = a.f;
+  const Conv1dArgs& c = a.c;
+  const int hk = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int j = tid >> 8, t = tid & 255;  // value head hk R + j; thread t of its group
+  const int lane = t & 63, w = t >> 6, jl = lane & 31, h = lane >> 5;
+  const int hv = hk * R + j;
+  const int64_t sb = ((int64_t)b * f.Hv + hv) * DN_D * DN_D;
+  float s[16][4];
+  load_state<NI>(s, f.s_in + sb, w, lane);
+  // LDS: q, k, v[R], z[R] (DN_D each), alpha[R], beta[R]
+  __shared__ float xs[(2 + 2 * R) * DN_D + 2 * R];
+  __shared__ float red[R][4];
+  constexpr int XA = (2 + 2 * R) * DN_D;
+  for (int g = tid; g < 64 + 64 * R; g += 256 * R) {
+    int ch, xo;  // projection channel and LDS slot of the group's first element
+    if (g < 64) {  // q (g < 32) or k of head hk
+      ch = (g < 32 ? 0 : f.Hk * DN_D) + hk * DN_D + 4 * (g & 31);
+      xo = (g >> 5) * DN_D + 4 * (g & 31);
+    } else if (g < 64 + 32 * R) {  // v of head hk R + jj
+      const int jj = (g - 64) >> 5;
+      ch = 2 * f.Hk * DN_D + (hk * R + jj) * DN_D + 4 * (g & 31);
+      xo = (2 + jj) * DN_D + 4 * (g & 31);
+    } else {  // z of head hk R + jj
+      const int jj = (g - 64 - 32 * R) >> 5;
+      ch = c.D + (hk * R + jj) * DN_D + 4 * (g & 31);
+      xo = (2 + R + jj) * DN_D + 4 * (g & 31);
+    }
+    const float4 sum = gemv_sk_sum4(a.part, a.G, a.chunk, ch, b);
+    const uint2 xr = make_uint2(pack2(sum.x, sum.y), pack2(sum.z, sum.w));  // bf16 projection
+    float x4[4];
+    if (g < 64 + 32 * R) {
+      uint2 raw[KC];
+#pragma unroll
+      for (int i = 0; i < KC - 1; ++i)
+        raw[i] = *reinterpret_cast<const uint2*>(c.s_in + b * c.s_sb + (int64_t)(i + 1) * c.s_cs + ch);
+      raw[KC - 1] = xr;
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < KC; ++i) {
+        float v[4], wf[4];
+        unpack4(raw[i], v);
+        unpack4(*reinterpret_cast<const uint2*>(c.w + (int64_t)i * c.w_cs + ch), wf);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += v[e] * wf[e];
+      }
+#pragma unroll
+      for (int i = 0; i < KC; ++i)
+        *reinterpret_cast<uint2*>(c.s_out + b * c.s_sb + (int64_t)i * c.s_cs + ch) = raw[i];
+      if (c.bias) {
+        float bf4[4];
+        unpack4(*reinterpret_cast<const uint2*>(c.bias + ch), bf4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += bf4[e];
+      }
+      if (c.act) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = accurate_silu(acc[e]);
+      }
+      unpack4(make_uint2(pack2(acc[0], acc[1]), pack2(acc[2], acc[3])), x4);  // bf16 conv output
+    } else {
+      unpack4(xr, x4);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xs[xo + e] = x4[e];
+  }
+  if (tid < 2 * R) {  // alpha (tid < R) and beta of head hk R + tid % R
+    const int ch = c.D + f.Hv * DN_D + (tid < R ? 0 : f.Hv) + hk * R + tid % R;
+    xs[XA + tid] = __uint_as_float(pack2(gemv_sk_sum1(a.part, a.G, a.chunk, ch, b), 0.f) << 16);
+  }
+  __syncthreads();
+  float q[4], k[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    q[e] = xs[4 * jl + e];
+    k[e] = xs[DN_D + 4 * jl + e];
+  }
+  const int col = 2 * NI * w + 2 * (jl >> 1) + h;  // this lane group's column
+  const float v_col = xs[(2 + j) * DN_D + col];
+  const float z_col = xs[(2 + R + j) * DN_D + col];
+  const float w_col = bf2f(f.norm_w[col]);
+  const float spi = xs[XA + j] + f.dt_bias[hv];
+  const float sp = spi > 20.0f ? spi : logf(1.0f + expf(spi));
+  const float decay = expf(-expf(f.a_log[hv]) * sp);
+  const float beta = accurate_sigmoid(xs[XA + R + j]);
+  const float qss = half_sum(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
+  const float kss = half_sum(k[0] * k[0] + k[1] * k[1] + k[2] * k[2] + k[3] * k[3]);
+  const float qsc = 1.0f / sqrtf(qss + 1e-6f) / sqrtf((float)DN_D);
+  const float ksc = 1.0f / sqrtf(kss + 1e-6f);
+  float qn[4], kn[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    qn[e] = q[e] * qsc;
+    kn[e] = k[e] * ksc;
+  }
+  const float out = delta_step<NI>(s, kn, qn, v_col, beta, decay, jl, h);
+  store_state<NI>(s, f.s_out + sb, w, lane);
+  const float ss = half_sum((jl & 1) ? 0.f : out * out);
+  const float wave_ss = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 0)) +
+                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 32));
+  if (lane == 0) red[j][w] = wave_ss;
+  __syncthreads();
+  const float tot = red[j][0] + red[j][1] + red[j][2] + red[j][3];
+  const float rstd = 1.0f / sqrtf(tot / (float)DN_D + f.eps);
+  if ((jl & 1) == 0)
+    f.o[b * f.o_sb + hv * DN_D + col] = f2bf(out * rstd * w_col * accurate_silu(z_col));
+}
+
 // ---- deltanet_sequence! (deltanet_recurrent.jl:109-198) and, at T = 1,
 // deltanet_recurrent_decode! (:15-95): fp32 inputs already normed and gated.
 // Grid (columns / (2 NI * 4), Hv, B), four independent waves per block; the
@@ -1370,6 +1502,29 @@ hipError_t launch_deltanet_fused_decode(const DeltaFusedArgs& a, hipStream_t st)
   return hipGetLastError();
 }
 
+#define VM_CONV_K_CASES(X) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
+
+hipError_t launch_deltanet_decode_sk(const DeltaDecodeSkArgs& a, hipStream_t st) {
+  if (a.f.B == 0) return hipSuccess;
+  const int R = a.f.Hv / a.f.Hk;
+  const dim3 grid(a.f.Hk, a.f.B);
+#define DN_SK(kc, r) hipLaunchKernelGGL((deltanet_decode_sk_kernel<kc, r>), grid, dim3(256 * r), 0, st, a)
+#define X(kc)                              \
+  case kc:                                 \
+    if (R == 1) DN_SK(kc, 1);              \
+    else if (R == 2) DN_SK(kc, 2);         \
+    else if (R == 4) DN_SK(kc, 4);         \
+    else return hipErrorInvalidValue;      \
+    break;
+  switch (a.c.K) {
+    VM_CONV_K_CASES(X)
+    default: return hipErrorInvalidValue;
+  }
+#undef X
+#undef DN_SK
+  return hipGetLastError();
+}
+
 hipError_t launch_deltanet_sequence(const DeltaSeqArgs& a, hipStream_t st) {
   if (a.B == 0 || a.T == 0) {
     if (a.B > 0 && a.s_out != a.s_in)  // T = 0: the state passes through
@@ -1438,7 +1593,6 @@ hipError_t launch_gated_rms_norm(const GatedNormArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-#define VM_CONV_K_CASES(X) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
 
 hipError_t launch_conv1d_update(const Conv1dArgs& a, hipStream_t st) {
   if (a.B == 0) return hipSuccess;

@@ -399,6 +399,15 @@ int linear_conv_workspace(int M, int N, int K, int64_t ldw, int64_t ldx, int64_t
 int linear_conv_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w,
                     int64_t ldw, int M, int N, int K, Conv1dArgs conv, void* workspace,
                     size_t workspace_bytes, hipStream_t st, char* err, size_t errn);
+// the DeltaNet layer's decode step through its recurrence: linear! of the
+// projection, causal_conv1d! of its first conv.D channels and
+// fused_deltanet_decode! (f: q .. beta point into y and conv.y, used by the
+// two-call form only); at N <= 32 with aligned views the projection's
+// stream-K partials go straight to deltanet_decode_sk_kernel
+int linear_dn_decode_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx,
+                         const uint16_t* w, int64_t ldw, int M, int N, int K, Conv1dArgs conv,
+                         const DeltaFusedArgs& f, void* workspace, size_t workspace_bytes,
+                         hipStream_t st, char* err, size_t errn);
 // the chunked form of deltanet_sequence!: same arguments, plus a workspace of
 // deltanet_chunk_workspace_bytes(T, Hv, B) bytes (256-byte aligned)
 struct DeltaChunkArgs {
@@ -411,6 +420,18 @@ struct DeltaChunkArgs {
 size_t deltanet_chunk_workspace_bytes(int T, int Hv, int B);
 hipError_t launch_deltanet_sequence_chunked(const DeltaChunkArgs& a, hipStream_t st);
 hipError_t launch_deltanet_fused_decode(const DeltaFusedArgs& a, hipStream_t st);
+// The DeltaNet layer's decode step after its stream-K projection: f's state,
+// gates, norm and output (f.q .. f.beta unused: they come from the partials),
+// c's ring, weight and bias (c.x, c.y unused; c.D = 2 Hk Dk + Hv Dv conv
+// channels, c.B = f.B), the projection's partials (GemvSkArgs::part, its G
+// and chunk); Hv / Hk in {1, 2, 4}
+struct DeltaDecodeSkArgs {
+  DeltaFusedArgs f;
+  Conv1dArgs c;
+  const float* part;
+  int G, chunk;
+};
+hipError_t launch_deltanet_decode_sk(const DeltaDecodeSkArgs& a, hipStream_t st);
 hipError_t launch_deltanet_sequence(const DeltaSeqArgs& a, hipStream_t st);
 hipError_t launch_deltanet_prep(const DeltaPrepArgs& a, hipStream_t st);
 hipError_t launch_gated_rms_norm(const GatedNormArgs& a, hipStream_t st);

@@ -686,4 +686,52 @@ int linear_conv_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, co
   return VM_OK;
 }
 
+int linear_dn_decode_run(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx,
+                         const uint16_t* w, int64_t ldw, int M, int N, int K, Conv1dArgs conv,
+                         const DeltaFusedArgs& f, void* workspace, size_t workspace_bytes,
+                         hipStream_t st, char* err, size_t errn) {
+  size_t need = 0;
+  int rc = linear_conv_workspace(M, N, K, ldw, ldx, ldy, &need, err, errn);
+  if (rc != VM_OK) return rc;
+  if (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 256 != 0) {
+    snprintf(err, errn,
+             "linear_deltanet_decode: workspace of %zu bytes (256-byte aligned) < %zu required "
+             "(vm_linear_causal_conv1d_workspace_bytes)", workspace_bytes, need);
+    return VM_E_SCRATCH;
+  }
+  const int R = f.Hv / f.Hk;
+  hipError_t e = hipSuccess;
+  if (sk_shape(M, N, K, ldw, ldx) && (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 &&
+      (R == 1 || R == 2 || R == 4) && M == conv.D + f.Hv * 128 + 2 * f.Hv) {  // Dv = 128
+    GemvSkArgs g{};
+    g.w = w;
+    g.w_st = ldw;
+    g.x = x;
+    g.x_st = ldx;
+    g.part = static_cast<float*>(workspace);
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.p = gemv_sk_plan(M, K);
+    DeltaDecodeSkArgs a{};
+    a.f = f;
+    a.c = conv;
+    a.part = g.part;
+    a.G = g.p.G;
+    a.chunk = g.p.chunk;
+    e = launch_gemv_sk(g, st);
+    if (e == hipSuccess) e = launch_deltanet_decode_sk(a, st);
+  } else {
+    rc = linear_conv_run(y, ldy, x, ldx, w, ldw, M, N, K, conv, workspace, workspace_bytes, st, err,
+                         errn);
+    if (rc != VM_OK) return rc;
+    e = launch_deltanet_fused_decode(f, st);
+  }
+  if (e != hipSuccess) {
+    snprintf(err, errn, "linear_deltanet_decode: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  return VM_OK;
+}
+
 }  // namespace vm

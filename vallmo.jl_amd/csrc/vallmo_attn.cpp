@@ -1233,6 +1233,54 @@ int vm_linear_causal_conv1d(vm_bf16* y, int64_t ldy, const vm_bf16* x, int64_t l
                              S(st), g_err, sizeof g_err);
 }
 
+int vm_linear_deltanet_decode(vm_bf16* o, int64_t o_sb, vm_bf16* y, int64_t ldy, vm_bf16* yc,
+                              int64_t yc_sb, const vm_bf16* x, int64_t ldx, const vm_bf16* w,
+                              int64_t ldw, int M, int K, const vm_bf16* ring_in, vm_bf16* ring_out,
+                              int64_t s_cs, int64_t s_sb, const vm_bf16* conv_w,
+                              int64_t conv_w_cs, const vm_bf16* conv_b, int Kc, const float* a_log,
+                              const float* dt_bias, const vm_bf16* norm_w, const float* s_in,
+                              float* s_out, int Dk, int Dv, int Hk, int Hv, int B, float eps,
+                              void* workspace, size_t workspace_bytes, vm_stream st) {
+  const char* what = "linear_deltanet_decode";
+  TRY(check_dn_heads(Dk, Dv, Hk, Hv, B, what));
+  if (B == 0) return VM_OK;
+  TRY(linear_check(M, B, K, ldw, ldx, ldy));
+  const int D = 2 * Hk * Dk + Hv * Dv;
+  TRY(check_conv(D, Kc, B, 1, what));
+  REQUIRE(M == D + Hv * Dv + 2 * Hv, VM_E_DIM,
+          "%s: the projection has M = %d rows, not [q | k | v | z | alpha | beta] = %d", what, M,
+          D + Hv * Dv + 2 * Hv);
+  REQUIRE(o && x && w && a_log && dt_bias && norm_w, VM_E_ARG, "%s: NULL pointer argument", what);
+  TRY(check_aligned(y, "y"));
+  TRY(check_aligned(yc, "Y"));
+  TRY(check_aligned(ring_in, "S_ring"));
+  TRY(check_aligned(ring_out, "S_ring_out"));
+  TRY(check_aligned(conv_w, "Weight"));
+  if (conv_b) TRY(check_aligned(conv_b, "Bias"));
+  TRY(check_aligned(s_in, "S"));
+  TRY(check_aligned(s_out, "S_out"));
+  for (int64_t v : {ldy, yc_sb, s_cs, s_sb, conv_w_cs}) TRY(check_stride(v, what));
+  REQUIRE(s_cs >= D && conv_w_cs >= D && (B <= 1 || (s_sb >= s_cs * Kc && yc_sb >= D)), VM_E_DIM,
+          "%s: strides below the extents (D = %d, K = %d)", what, D, Kc);
+  REQUIRE(B <= 1 || o_sb >= (int64_t)Hv * Dv, VM_E_DIM, "%s: O's sequence stride < Hv Dv", what);
+  TRY(check_alias(ring_in, ring_out, (size_t)((B - 1) * s_sb + (Kc - 1) * s_cs + D) * 2, what));
+  TRY(check_alias(s_in, s_out, (size_t)B * Hv * Dk * Dv * sizeof(float), what));
+  vm::Conv1dArgs c{};
+  c.y = yc; c.y_sb = yc_sb; c.s_in = ring_in; c.s_out = ring_out; c.s_cs = s_cs; c.s_sb = s_sb;
+  c.w = conv_w; c.w_cs = conv_w_cs; c.bias = conv_b; c.D = D; c.K = Kc; c.T = 1; c.B = B;
+  c.act = 1;
+  vm::DeltaFusedArgs f{};
+  f.o = o; f.o_sb = o_sb;
+  f.q = yc; f.k = yc + (int64_t)Hk * Dk; f.v = yc + 2LL * Hk * Dk;
+  f.q_sb = f.k_sb = f.v_sb = yc_sb;
+  f.z = y + D; f.alpha = y + D + (int64_t)Hv * Dv; f.beta = f.alpha + Hv;
+  f.z_sb = f.a_sb = f.b_sb = ldy;
+  f.a_log = a_log; f.dt_bias = dt_bias; f.norm_w = norm_w; f.s_in = s_in; f.s_out = s_out;
+  f.Hk = Hk; f.Hv = Hv; f.B = B; f.eps = eps;
+  return vm::linear_dn_decode_run(y, ldy, x, ldx, w, ldw, M, B, K, c, f, workspace,
+                                  workspace_bytes, S(st), g_err, sizeof g_err);
+}
+
 // ---- synthetic inputs ------------------------------------------------------
 int vm_fill_normal_bf16(vm_bf16* dst, int64_t n, uint64_t seed, float scale, float shift,
                         vm_stream st) {

@@ -123,15 +123,6 @@ def _views(qz, c: DeltaNetConfig):
     return qz[..., :c.n], qz[..., c.n:]
 
 
-def _qkv(conv, c: DeltaNetConfig):
-    """q, k (Dk, Hk, ·), v (Dv, Hv, ·) views of the conv output (qwen35.jl:224-225)."""
-    hk = c.Hk * c.Dk
-    q = conv[..., :hk].unflatten(-1, (c.Hk, c.Dk))
-    k = conv[..., hk:2 * hk].unflatten(-1, (c.Hk, c.Dk))
-    v = conv[..., 2 * hk:].unflatten(-1, (c.Hv, c.Dv))
-    return q, k, v
-
-
 def decode_(h, l: DeltaNetLayer, c: DeltaNetConfig, space: DeltaNetSpace, xn, *, eps: float,
             workspace, project: bool = True):
     """decode!(h, l::DeltaNetLayer, m, gen, xn) — qwen35.jl:210-232: one token per
@@ -142,17 +133,13 @@ def decode_(h, l: DeltaNetLayer, c: DeltaNetConfig, space: DeltaNetSpace, xn, *,
     B = xn.shape[0]
     if space.qz.shape[0] != B:
         raise DimensionMismatch(f"size(xn, 2) = {B} does not match the decode space's B")
-    # the projection [qz | ab] (:212-213) and the conv of its first n channels
-    # (:222-223) in one call: at B <= 32 the projection's partials go straight
-    # to the conv kernel
-    ops.linear_causal_conv1d_({"y": space.qzab, "Y": space.conv, "Sp": l.conv_state}, xn,
-                              l.W_in, l.conv_state, l.conv_w, l.conv_b, sigma="silu",
-                              workspace=workspace)
-    _, z = _views(space.qz, c)
-    q, k, v = _qkv(space.conv, c)
-    ops.fused_deltanet_decode_({"O": space.O, "Sp": l.S}, q, k, v, space.ab[:, :c.Hv],
-                               space.ab[:, c.Hv:], z.unflatten(-1, (c.Hv, c.Dv)), l.A_log,
-                               l.dt_bias, l.gnorm_w, l.S, eps=eps)
+    # the projection [qz | ab] (:212-213), the conv of its first n channels
+    # (:222-223) and the fused recurrence (:224-229) in one call: at B <= 32 the
+    # projection's partials go straight to one kernel per (qk head, sequence)
+    ops.linear_deltanet_decode_({"O": space.O, "y": space.qzab, "Y": space.conv,
+                                 "Sp_ring": l.conv_state, "Sp": l.S}, xn, l.W_in, l.conv_state,
+                                l.conv_w, l.conv_b, l.A_log, l.dt_bias, l.gnorm_w, l.S, Dk=c.Dk,
+                                Dv=c.Dv, Hk=c.Hk, Hv=c.Hv, eps=eps, workspace=workspace)
     if not project:
         return space.O.view(B, c.Hv * c.Dv)
     ops.linear_({"y": h}, space.O.view(B, c.Hv * c.Dv), l.Wout, workspace=workspace)

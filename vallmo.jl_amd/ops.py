@@ -31,7 +31,7 @@ __all__ = [
     "deltanet_recurrent_decode", "deltanet_sequence_", "deltanet_sequence",
     "deltanet_prefill_prep_", "deltanet_conv_prep_", "gated_rms_norm_", "linear_add_rms_norm_",
     "deltanet_sequence_chunked_", "deltanet_sequence_workspace_bytes",
-    "deltanet_sequence_chunked_gated_norm_",
+    "deltanet_sequence_chunked_gated_norm_", "linear_deltanet_decode_",
     "linear_add_rms_norm_workspace_bytes",
 ]
 
@@ -549,6 +549,55 @@ def linear_causal_conv1d_(outs, x, W, S, Weight, Bias=None, *, sigma=None, works
          _p(Y), _st(Y, 0, D), _p(S), _p(Sp), _st(S, 1, D), _st(S, 0, Kc * D), _p(Weight),
          _st(Weight, 0, D), _p(Bias), D, Kc, _act(sigma), _p(workspace), workspace.numel(),
          _stream())
+    return outs
+
+
+def linear_deltanet_decode_(outs, x, W, S_ring, Weight, Bias, A_log, DtBias, NormWeight, S, *,
+                            Dk, Dv, Hk, Hv, eps=1e-6, workspace=None):
+    """The DeltaNet layer's decode step up to its out projection in one call
+    (src/llm/qwen35.jl:212-232): linear! of W (the in projection [q | k | v | z |
+    alpha | beta], torch (M, K)) over x (K, B) (torch (B, K)) into outs["y"] (M, B),
+    causal_conv1d! (silu) of its q | k | v channels on the ring S_ring into
+    outs["Y"] (D, B) and outs["Sp_ring"], then fused_deltanet_decode! into
+    outs["O"] (Dv, Hv, B) and outs["Sp"] (S′; either ring or state may be in
+    place). Results equal linear_causal_conv1d_ then fused_deltanet_decode_ bit
+    for bit. At B <= 32 on aligned views y and Y are not written (the projection's
+    partials feed one kernel per (qk head, sequence)). No reference counterpart
+    as one op."""
+    O, y, Y = _out(outs, "O"), _out(outs, "y"), _out(outs, "Y")
+    Sp_ring, Sp = _out(outs, "Sp_ring"), _out(outs, "Sp")
+    M, N, ldy = _cols(y, "y")
+    K, Nx, ldx = _cols(x, "x")
+    if W.dim() != 2 or tuple(W.shape) != (M, K) or Nx != N:
+        raise DimensionMismatch(f"linear_deltanet_decode: x ({K}, {Nx}), W {tuple(W.shape)}, "
+                                f"y ({M}, {N})")
+    dims = sizes(Y=(Y, "D B"), S_ring=(S_ring, "D Kc B"), Sp_ring=(Sp_ring, "D Kc B"),
+                 Weight=(Weight, "D Kc"), Bias=(Bias, "D"), S=(S, "Dk Dv Hv B"),
+                 Sp=(Sp, "Dk Dv Hv B"), O=(O, "Dv Hv B"), A_log=(A_log, "Hv"),
+                 DtBias=(DtBias, "Hv"), NormWeight=(NormWeight, "Dv"))
+    D, Kc = dims["D"], dims["Kc"]
+    if dims["B"] != N or (dims["Dk"], dims["Dv"], dims["Hv"]) != (Dk, Dv, Hv):
+        raise DimensionMismatch(f"linear_deltanet_decode: B {dims['B']} vs N {N}, state "
+                                f"({dims['Dk']}, {dims['Dv']}, {dims['Hv']}) vs ({Dk}, {Dv}, {Hv})")
+    for t, n in ((W, "W"), (y, "y"), (Y, "Y"), (S_ring, "S_ring"), (Sp_ring, "S_ring′"),
+                 (Weight, "Weight"), (Bias, "Bias"), (O, "O"), (NormWeight, "NormWeight")):
+        _need(t, torch.bfloat16, n)
+    for t, n in ((A_log, "A_log"), (DtBias, "DtBias"), (S, "S"), (Sp, "S′")):
+        _need(t, torch.float32, n)
+    _need_contig(S, "S")
+    _need_contig(Sp, "S′")
+    if S_ring.stride() != Sp_ring.stride():
+        raise ArgumentError("S_ring and S_ring′ must share strides")
+    if O.dim() == 3 and O.stride(1) != O.shape[2]:
+        raise ArgumentError("O: heads must be contiguous")
+    need = linear_causal_conv1d_workspace_bytes(x, W, y)
+    if workspace is None:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+    call("vm_linear_deltanet_decode", _p(O), _st(O, 0, Hv * Dv), _p(y), ldy, _p(Y),
+         _st(Y, 0, D), _p(x), ldx, _p(W), W.stride(0), M, K, _p(S_ring), _p(Sp_ring),
+         _st(S_ring, 1, D), _st(S_ring, 0, Kc * D), _p(Weight), _st(Weight, 0, D), _p(Bias), Kc,
+         _p(A_log), _p(DtBias), _p(NormWeight), _p(S), _p(Sp), Dk, Dv, Hk, Hv, N, float(eps),
+         _p(workspace), workspace.numel(), _stream())
     return outs
 
 
