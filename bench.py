@@ -181,30 +181,12 @@ def bench_prefill(vm, torch, steps, warmup, T=4096, seed=2, settle=True, kw0=Non
     lib.profile_enable(False)
     lib.profile_select()
     assert n_rows == n_side
-    # the attention kernel back to back: the staging skipped (its rows and tiles
-    # from the steps above serve: same inputs, same workspace), one event pair
-    # around `steps` launches on the launch stream, so no per-launch event
-    # overhead (the per-dispatch events above read ~3% above a profiler trace)
-    lib.profile_skip_staging(True)
-    try:
-        for _ in range(5):
-            step()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(steps):
-            step()
-        e1.record()
-        torch.cuda.synchronize()
-    finally:
-        lib.profile_skip_staging(False)
-    ms_b2b = e0.elapsed_time(e1) / steps
     flops = prefill_flops(T)
     return {
         "settle": settle,
         "ms_per_step": 1e3 * wall / steps,
         "tflops": flops / (wall / steps) / 1e12,
-        "attn_kernel_ms": ms_b2b,
-        "attn_kernel_ms_events": ms_attn / n_attn,
+        "attn_kernel_ms": ms_attn / n_attn,
         "append_vt_kernel_ms": ms_rows / n_rows,
         "flops": flops,
     }
@@ -1115,8 +1097,7 @@ def main():
         pf = bench_prefill(vm, torch, args.steps, args.warmup, settle=not args.no_settle)
         log(f"[bench] settle: {pf['settle']}")
         log(f"[bench] prefill: {pf['ms_per_step']:.3f} ms/step, {pf['tflops']:.1f} TFLOP/s, "
-            f"attn kernel {pf['attn_kernel_ms'] * 1e3:.1f} us back to back "
-            f"({pf['attn_kernel_ms_events'] * 1e3:.1f} us on per-dispatch events), "
+            f"attn kernel {pf['attn_kernel_ms'] * 1e3:.1f} us (per-dispatch events), "
             f"K/V append + V^T staging {pf['append_vt_kernel_ms']:.4f} ms")
     pf_shift = None
     if not args.no_prefill:
@@ -1242,10 +1223,9 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": profiled_traffic(), "kernel": "prefill_fused_kernel<CAUSAL>",
                      "kernel_ms": round(pf["attn_kernel_ms"], 5),
-                     "kernel_ms_events": round(pf["attn_kernel_ms_events"], 5),
-                     "timing": "kernel_ms: `steps` back-to-back launches of the attention kernel "
-                               "alone between two events on its stream; kernel_ms_events: the "
-                               "per-dispatch events of the timed steps",
+                     "timing": "kernel_ms: mean of the HIP events recorded around each "
+                               "dispatch of the attention kernel in the timed steps, on its "
+                               "launch stream",
                      "flop_per_launch": pf["flops"]},
         "cpu_baseline": cpu,
         "prefill_config2_online_max": pf_shift,

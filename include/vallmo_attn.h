@@ -70,12 +70,6 @@ int vm_profile_read(int kernel, int* count, double* total_ms);
  * set in kernel_mask (default: all), so a benchmark can time one kernel
  * without events around the others.                                          */
 int vm_profile_select(unsigned kernel_mask);
-/* Benchmark hook: while on (calling thread), vm_gated_attn_prefill launches
- * its attention kernel only, reading the cache rows and V^T tiles that an
- * earlier call with the same inputs and workspace staged (those rows are not
- * rewritten). Lets a benchmark time that kernel back to back between two
- * events, without per-launch event overhead.                                 */
-int vm_profile_skip_staging(int on);
 
 /* ---- runtime (thin HIP wrappers so FFI hosts need no HIP headers) ------ */
 int vm_malloc(void** ptr, size_t bytes);

@@ -392,30 +392,6 @@ def test_paired_prefill_online_max_path(vm, orc):
     assert mx <= TOL_MAX and mn <= TOL_MEAN
 
 
-def test_profile_skip_staging_reuses_staged_rows(vm):
-    """vm_profile_skip_staging (a benchmark hook): with it on, the gated prefill
-    launches only its attention kernel over what the previous call staged, so
-    the same inputs give the same output, bit for bit, and the cache is left as
-    that call wrote it."""
-    banner("vm_profile_skip_staging")
-    T, ctx, B = 512, 512, 1
-    cfg = vm.AttnConfig(Hq=HQ, Hkv=HK, Dh=D, rot_half=HALF, theta=THETA, eps=EPS, Ctx=ctx, B=B)
-    qw, kw = to_dev(normal_bf16((D,), 341, scale=0.05)), to_dev(normal_bf16((D,), 342, scale=0.05))
-    qkv = to_dev(normal_bf16((B, T, S, D), 343))
-    m = vm.AttnModel(cfg)
-    layer = vm.attn_layer(cfg, qw, kw)
-    out1 = vm.gated_attn_prefill(layer, m, qkv, T, B).clone()
-    k1, v1 = layer.K_cache.clone(), layer.V_cache.clone()
-    vm._lib.profile_skip_staging(True)
-    try:
-        out2 = vm.gated_attn_prefill(layer, m, qkv, T, B)
-    finally:
-        vm._lib.profile_skip_staging(False)
-    torch.cuda.synchronize()
-    assert torch.equal(out1, out2)
-    assert torch.equal(k1, layer.K_cache) and torch.equal(v1, layer.V_cache)
-
-
 def test_staged_prefill_chunks_equal_full_staging(vm):
     """vm_gated_attn_prefill_staged over a chunk-by-chunk, ragged prefill (B = 2):
     each chunk stages only its own rows into the kept V^T workspace, and rows

@@ -57,7 +57,6 @@ _SIGS = {
     "vm_profile_enable": (_c_i, [_c_i]),
     "vm_profile_read": (_c_i, [_c_i, ctypes.POINTER(_c_i), ctypes.POINTER(_c_d)]),
     "vm_profile_select": (_c_i, [ctypes.c_uint]),
-    "vm_profile_skip_staging": (_c_i, [ctypes.c_int]),
     "vm_malloc": (_c_i, [ctypes.POINTER(_p), _c_sz]),
     "vm_free": (_c_i, [_p]),
     "vm_memcpy_h2d": (_c_i, [_p, _p, _c_sz, _p]),
@@ -215,12 +214,6 @@ def profile_select(*kernels: int) -> None:
     """Bracket only these kernel classes while profiling (none given: all)."""
     mask = 0xFFFFFFFF if not kernels else sum(1 << int(k) for k in set(kernels))
     call("vm_profile_select", mask)
-
-
-def profile_skip_staging(on: bool = True) -> None:
-    """While on, the gated prefill launches its attention kernel only (reusing
-    what an earlier call on the same inputs staged): for back-to-back timing."""
-    call("vm_profile_skip_staging", int(bool(on)))
 
 
 def profile_read(kernel: int) -> tuple[int, float]:

@@ -23,7 +23,6 @@ struct ProfRec {
 struct Prof {
   bool on = false;
   unsigned mask = ~0u;  // kernel classes bracketed while on
-  bool skip_staging = false;  // vm_profile_skip_staging
   std::vector<ProfRec> recs;
   std::vector<hipEvent_t> pool;
 };
@@ -152,10 +151,6 @@ int vm_profile_enable(int on) {
 }
 int vm_profile_select(unsigned kernel_mask) {
   g_prof.mask = kernel_mask;
-  return VM_OK;
-}
-int vm_profile_skip_staging(int on) {
-  g_prof.skip_staging = on != 0;
   return VM_OK;
 }
 int vm_profile_read(int kernel, int* count, double* total_ms) {
@@ -616,9 +611,8 @@ static int gated_attn_prefill(vm_bf16* out, int64_t out_st, int64_t out_sb, cons
   t.kc = kc; t.k_raw = qkv + 2 * Hq * Dl; t.v_raw = qkv + (2 * Hq + Hk) * Dl;
   t.raw_st = qkv_st; t.raw_sh = Dl; t.raw_sb = qkv_sb;
   t.kw = kw; t.cos_tab = cs; t.sin_tab = sn; t.eps = eps; t.w_offset = w_offset;
-  if (!g_prof.skip_staging)
-    TRY(hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_vt_transpose(t, S(st)); }),
-                   "gated_attn_prefill append"));
+  TRY(hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_vt_transpose(t, S(st)); }),
+                 "gated_attn_prefill append"));
   a.vt = t.vt; a.vt_tiles = t.vt_tiles;
   return hip_status(timed_ext(VM_K_PREFILL, S(st),
                               [&](hipEvent_t t0, hipEvent_t t1) { return vm::launch_prefill_fused(a, S(st), t0, t1); }),
