@@ -446,11 +446,70 @@ void lm_head_split_kernel(LmHeadArgs a) {
 // ---- y = W^T x for a narrow x (N <= 32 columns; linear.cpp picks which): the decode step's projections (linear!, src/linear.jl:40-57, at N = B). HBM-bound like the lm
 // head and built the same way: one 32-column batch tile, 32-row weight tiles
 // staged through LDS by 1-KB direct loads, bf16 MFMAs, fp32 sums. Workgroup
-// (tile group tg, K slice s2) takes T tiles; its four waves split the slice's
-// 64-deep k groups in four contiguous runs and add their sums through LDS (the
-// staging buffers, free by then). With S2 > 1 slices the workgroups write fp32
-// partials, summed in slice order by gemv_reduce_kernel (deterministic).
+// (tile group tg, K slice s2) takes T <= 2 tiles; its four waves split the
+// slice's 64-deep k groups in four contiguous runs and add their sums through
+// LDS (the staging buffers, free by then). With S2 > 1 slices the workgroups
+// write fp32 partials, summed in slice order by gemv_reduce_kernel
+// (deterministic).
+//
+// A wave's run is short (a few groups: the whole launch streams ~100 KB per
+// CU), so the groups stream through a ring of three slots (12 KB each, 144 KB
+// per workgroup): the first three are issued at once and each slot is refilled
+// as soon as its products have read it, two groups in flight behind the one
+// being multiplied. A run of up to three groups then costs one memory latency.
 namespace {
+
+// one object per slot (the reads of one are seen not to alias the loads
+// landing in the others)
+__shared__ __attribute__((aligned(16))) uint16_t gv_buf0[4][3 * LM_TB];
+__shared__ __attribute__((aligned(16))) uint16_t gv_buf1[4][3 * LM_TB];
+__shared__ __attribute__((aligned(16))) uint16_t gv_buf2[4][3 * LM_TB];
+
+// wait until at most `left` groups (of PER loads each) issued after the one
+// about to be multiplied are still in flight
+template <int PER>
+__device__ __forceinline__ void gv_wait(int left) {
+  if (left >= 2) wait_vmcnt<2 * PER>();
+  else if (left == 1) wait_vmcnt<PER>();
+  else wait_vmcnt<0>();
+}
+
+// group g of the run (in slot S): wait for it, multiply, refill the slot with
+// group g + 3
+template <int T, int S>
+__device__ __forceinline__ void gv_group(uint16_t* buf, const MmSrc& m, int v0, int k0, int g,
+                                         int G, int j, int h, int lane, f32x16 (&acc)[T]) {
+  constexpr int PER = 4 * (T + 1);
+  gv_wait<PER>(min(G - 1 - g, 2));
+  lm_mult<T>(buf, j, h, acc);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot's reads are in: refill it
+  if (g + 3 < G) lm_dma<T>(buf, m, v0, 0, k0 + 64 * (g + 3), lane);
+}
+
+// acc[t] = W^T X over k = k0 .. k1 - 1 (multiples of 64, k1 > k0) for the T
+// 32-row tiles at v0 and the batch tile, through the three-slot ring (lane
+// layout of mm_tiles)
+template <int T>
+__device__ __forceinline__ void gv_tiles(const MmSrc& m, int v0, int k0, int k1, int lane,
+                                         f32x16 (&acc)[T]) {
+  const int j = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  uint16_t* b0 = gv_buf0[wv];
+  uint16_t* b1 = gv_buf1[wv];
+  uint16_t* b2 = gv_buf2[wv];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+  const int G = (k1 - k0) / 64;
+  lm_dma<T>(b0, m, v0, 0, k0, lane);
+  if (G > 1) lm_dma<T>(b1, m, v0, 0, k0 + 64, lane);
+  if (G > 2) lm_dma<T>(b2, m, v0, 0, k0 + 128, lane);
+  for (int g = 0; g < G; g += 3) {
+    gv_group<T, 0>(b0, m, v0, k0, g, G, j, h, lane, acc);
+    if (g + 1 < G) gv_group<T, 1>(b1, m, v0, k0, g + 1, G, j, h, lane, acc);
+    if (g + 2 < G) gv_group<T, 2>(b2, m, v0, k0, g + 2, G, j, h, lane, acc);
+  }
+}
 
 template <int T>
 __device__ __forceinline__ void gemv_wg(const GemvArgs& a, int tg, int s2, int lane) {
@@ -463,7 +522,7 @@ __device__ __forceinline__ void gemv_wg(const GemvArgs& a, int tg, int s2, int l
   const MmSrc m{a.w, a.w_st, a.M, a.x, a.x_st, a.N};
   f32x16 acc[T];
   if (g1 > g0) {
-    mm_tiles<T>(m, v0, 0, 64 * g0, 64 * g1, lane, acc);
+    gv_tiles<T>(m, v0, 64 * g0, 64 * g1, lane, acc);
   } else {
 #pragma unroll
     for (int t = 0; t < T; ++t)
@@ -471,22 +530,24 @@ __device__ __forceinline__ void gemv_wg(const GemvArgs& a, int tg, int s2, int l
       for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
   }
   // the four waves' sums through LDS: wave w's tile t, register r, lane l at
-  // [w][t][r][l] (floats); then wave t adds tile t of all four
-  float* red = reinterpret_cast<float*>(lm_buf0[0]);
+  // [w][t][r][l] (floats, 32 KB at T = 2, in the first two slots); then wave t
+  // adds tile t of all four
+  static_assert(4 * 2 * 16 * 64 * sizeof(float) <= 2 * sizeof(gv_buf0), "reduction space");
+  float* red = reinterpret_cast<float*>(gv_buf0[0]);
   __syncthreads();  // every wave is done with the staging buffers
 #pragma unroll
   for (int t = 0; t < T; ++t)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[((wv * 4 + t) * 16 + r) * 64 + lane] = acc[t][r];
+    for (int r = 0; r < 16; ++r) red[((wv * T + t) * 16 + r) * 64 + lane] = acc[t][r];
   __syncthreads();
   if (wv >= T || j >= a.N) return;
   const int t = wv;
   float o[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    float v = red[((0 * 4 + t) * 16 + r) * 64 + lane];
+    float v = red[((0 * T + t) * 16 + r) * 64 + lane];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) v += red[((w * 4 + t) * 16 + r) * 64 + lane];
+    for (int w = 1; w < 4; ++w) v += red[((w * T + t) * 16 + r) * 64 + lane];
     o[r] = v;
   }
   // lane (j, h): rows 8q + 4h .. +3 of the tile, q = 0..3, for batch column j
@@ -510,11 +571,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemv_kernel(GemvArgs a) {
   const int lane = threadIdx.x & 63;
   const int tg = blockIdx.x / a.S2, s2 = blockIdx.x % a.S2;
-  switch (a.T) {
-    case 4: gemv_wg<4>(a, tg, s2, lane); break;
-    case 2: gemv_wg<2>(a, tg, s2, lane); break;
-    default: gemv_wg<1>(a, tg, s2, lane); break;
-  }
+  if (a.T == 2) gemv_wg<2>(a, tg, s2, lane);
+  else gemv_wg<1>(a, tg, s2, lane);
 }
 
 // y[:, b] rows 4i .. 4i + 3 = the slices' partials added in slice order
@@ -546,7 +604,7 @@ GemvPlan gemv_plan(int M, int K, int waves) {
   const int cus = max(1, waves / 4);
   GemvPlan best{1, 1, G, tiles};
   double best_cost = 1e300;
-  for (int T : {4, 2, 1}) {
+  for (int T : {2, 1}) {
     const int ntg = (tiles + T - 1) / T;
     for (int S2 = 1; S2 <= G; ++S2) {
       const int gps = (G + S2 - 1) / S2;
