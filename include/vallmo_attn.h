@@ -103,7 +103,9 @@ int vm_rope_tables(float* cos_tab, float* sin_tab, int half_rot, int64_t ctx,
 /* ---- a3: qnorm_rope! (src/kernels/qknorm_rope_append.jl:100-117) -------
  * In place on Q :: (D, Hq, B) bf16 with head stride q_sh, batch stride q_sb.
  * q = q / sqrt(mean(q^2) + eps) * (qw + w_offset), then rotate-half RoPE on
- * dims [0, 2*half_rot) at 0-based position positions[b]-1.                  */
+ * dims [0, 2*half_rot) at 0-based position positions[b]-1. D is a power of
+ * two from 16 to 512 (qknorm_rope_append.jl:108), 1 <= half_rot <= D/2; D =
+ * 256 with half_rot = 32 runs the tuned row kernel, other shapes a generic one. */
 int vm_qnorm_rope(vm_bf16* q, int64_t q_sh, int64_t q_sb,
                   const vm_bf16* qw, const float* cos_tab, const float* sin_tab,
                   int64_t ctx, const int32_t* positions,
@@ -111,22 +113,31 @@ int vm_qnorm_rope(vm_bf16* q, int64_t q_sh, int64_t q_sb,
                   vm_stream stream);
 
 /* ---- a4: knorm_rope_append! (src/kernels/qknorm_rope_append.jl:119-141)
- * K_cache/V_cache :: (D, Ctx, Hk, B) with strides (c_st, c_sh, c_sb);
- * K_raw/V_raw :: (D, Hk, B) with strides (r_sh, r_sb) (one set for both).
- * Writes norm+RoPE(k) and v into cache column positions[b] (1-based).      */
-int vm_knorm_rope_append(vm_bf16* k_cache, vm_bf16* v_cache,
-                         int64_t c_st, int64_t c_sh, int64_t c_sb, int64_t ctx,
-                         const vm_bf16* k_raw, const vm_bf16* v_raw,
-                         int64_t r_sh, int64_t r_sb,
+ * K_cache :: (Dk, Ctx, Hk, B) strides (kc_st, kc_sh, kc_sb), V_cache :: (Dv,
+ * Ctx, Hk, B) strides (vc_st, vc_sh, vc_sb); K_raw :: (Dk, Hk, B) strides
+ * (kr_sh, kr_sb), V_raw :: (Dv, Hk, B) strides (vr_sh, vr_sb). Writes
+ * norm+RoPE(k) and v into cache column positions[b] (1-based). Dk, Dv powers
+ * of two from 16 to 512 (:132), 1 <= half_rot <= Dk/2; Dk = Dv = 256, half_rot
+ * = 32 with K and V sharing strides runs the tuned kernel.                   */
+int vm_knorm_rope_append(vm_bf16* k_cache, int64_t kc_st, int64_t kc_sh, int64_t kc_sb,
+                         vm_bf16* v_cache, int64_t vc_st, int64_t vc_sh, int64_t vc_sb,
+                         int64_t ctx,
+                         const vm_bf16* k_raw, int64_t kr_sh, int64_t kr_sb,
+                         const vm_bf16* v_raw, int64_t vr_sh, int64_t vr_sb,
                          const vm_bf16* kw, const float* cos_tab, const float* sin_tab,
                          const int32_t* positions,
-                         int B, int Hk, int D, int half_rot, float eps, float w_offset,
+                         int B, int Hk, int Dk, int Dv, int half_rot, float eps, float w_offset,
                          vm_stream stream);
 
 /* ---- a5: decode_attention! (src/kernels/attention_decode.jl:134-200) ----
- * Split-KV flash-decoding: Q :: (D, H, B) (normalised + rotated), caches as
- * above, lengths[b] = attended keys (cache columns 1..len). O :: (D, H, B).
- * Work is split as a stream over all token-heads sum_b lengths[b] * Hk: NW
+ * Split-KV flash-decoding: Q :: (Dk, H, B) (normalised + rotated), K cache ::
+ * (Dk, Ctx, Hk, B) strides (k_st, k_sh, k_sb), V cache :: (Dv, Ctx, Hk, B)
+ * strides (v_st, v_sh, v_sb), lengths[b] = attended keys (cache columns
+ * 1..len). O :: (Dv, H, B). Dk, Dv powers of two from 16 to 512, any H / Hk.
+ *
+ * Dk = Dv = 256, H / Hk <= 8, K and V sharing strides and B*Ctx*Hk < 2^31
+ * run the tuned stream kernel. Its work is split as a stream over all
+ * token-heads sum_b lengths[b] * Hk: NW
  * waves each take one contiguous equal chunk (>= 64 keys, a multiple of 16),
  * so every CU streams the same bytes whatever the length mix. n_splits > 0
  * gives NW = n_splits * B * Hk (the reference's n_splits per (b, hk) on
@@ -134,16 +145,22 @@ int vm_knorm_rope_append(vm_bf16* k_cache, vm_bf16* v_cache,
  * does not depend on NW beyond fp32 rounding of the merge.
  * scratch holds one fp32 partial (G*D values + G (max, sum) pairs) per wave
  * and per (b, hk) segment, then a snapshot of the partition (1 + 2B int32
- * in whole 256-byte blocks) that the merge reads instead of lengths; size it with
- * vm_decode_scratch_bytes using the same (B, H, Hk, D, ctx, n_splits).
- * H / Hk <= 8.                                                              */
+ * in whole 256-byte blocks) that the merge reads instead of lengths.
+ *
+ * Other shapes run a generic kernel with the reference's split: n_splits
+ * tile-aligned key ranges per (b, hk) (n_splits = 0: about two workgroups
+ * per CU, at least 256 keys each), partials (Dv values, max, sum) per split,
+ * sequence and head, merged in split order.
+ *
+ * Size scratch with vm_decode_scratch_bytes(B, H, Hk, Dv, ctx, n_splits)
+ * (D = Dv; 0 for an invalid shape).                                         */
 size_t vm_decode_scratch_bytes(int B, int H, int Hk, int D, int64_t ctx, int n_splits);
 int vm_decode_attention(vm_bf16* o, int64_t o_sh, int64_t o_sb,
                         const vm_bf16* q, int64_t q_sh, int64_t q_sb,
-                        const vm_bf16* k_cache, const vm_bf16* v_cache,
-                        int64_t c_st, int64_t c_sh, int64_t c_sb, int64_t ctx,
-                        const int32_t* lengths, int B, int H, int Hk, int D,
-                        int n_splits, void* scratch, size_t scratch_bytes,
+                        const vm_bf16* k_cache, int64_t k_st, int64_t k_sh, int64_t k_sb,
+                        const vm_bf16* v_cache, int64_t v_st, int64_t v_sh, int64_t v_sb,
+                        int64_t ctx, const int32_t* lengths, int B, int H, int Hk, int Dk,
+                        int Dv, int n_splits, void* scratch, size_t scratch_bytes,
                         vm_stream stream);
 
 /* ---- a6: decode gate O .*= sigmoid.(q_gate) (src/llm/qwen35.jl:205) ---- */
@@ -194,17 +211,20 @@ int vm_gated_attn_decode_noalloc(vm_bf16* out, int64_t out_sb,
 int vm_advance_positions(int32_t* positions, int B, vm_stream stream);
 
 /* ---- a8: attention! (src/kernels/attention.jl:93-129) ------------------
- * Flash attention. Q :: (D, L, H, B) strides (q_st, q_sh, q_sb); K, V ::
- * (D, Lk, Hk, B) strides (kv_st, kv_sh, kv_sb) (typically a cache prefix);
- * O :: (D, L, H, B). k_lengths/q_lengths (device, nullable) give ragged
- * lengths; queries are the suffix of keys, causal offset = k_len - q_len.
- * Rows t >= q_len[b] are not written.                                      */
+ * Flash attention. Q :: (Dk, L, H, B) strides (q_st, q_sh, q_sb); K :: (Dk,
+ * Lk, Hk, B) strides (k_st, k_sh, k_sb), V :: (Dv, Lk, Hk, B) strides (v_st,
+ * v_sh, v_sb) (typically cache prefixes); O :: (Dv, L, H, B); scores scaled
+ * by 1/sqrt(Dk). k_lengths/q_lengths (device, nullable) give ragged lengths;
+ * queries are the suffix of keys, causal offset = k_len - q_len. Rows t >=
+ * q_len[b] are not written. Dk, Dv powers of two from 16 to 512; Dk = Dv = 256
+ * with K and V sharing strides runs the tuned MFMA kernel, other shapes a
+ * generic one.                                                              */
 int vm_attention_fwd(vm_bf16* o, int64_t o_st, int64_t o_sh, int64_t o_sb,
                      const vm_bf16* q, int64_t q_st, int64_t q_sh, int64_t q_sb,
-                     const vm_bf16* k, const vm_bf16* v,
-                     int64_t kv_st, int64_t kv_sh, int64_t kv_sb,
+                     const vm_bf16* k, int64_t k_st, int64_t k_sh, int64_t k_sb,
+                     const vm_bf16* v, int64_t v_st, int64_t v_sh, int64_t v_sb,
                      const int32_t* k_lengths, const int32_t* q_lengths,
-                     int B, int H, int Hk, int D, int L, int Lk, int causal,
+                     int B, int H, int Hk, int Dk, int Dv, int L, int Lk, int causal,
                      vm_stream stream);
 
 /* ---- a9: prefill prologue (src/llm/qwen35.jl:293-307) ------------------

@@ -51,7 +51,7 @@ def lib():
         L.orc_head_norm_rope.argtypes = [_f32p, _f32p, f32, f32, _f32p, _f32p, i64, i32, i32, _f32p]
         L.orc_head_norm_rope.restype = None
         L.orc_attention.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_void_p, ctypes.c_void_p,
-                                    i32, i32, i32, i32, i32, i32, i32, i32, i32]
+                                    i32, i32, i32, i32, i32, i32, i32, i32, i32, i32]
         L.orc_attention.restype = None
         L.orc_gated_decode.argtypes = [_u16p, _u16p, _u16p, i64, _i32p, _u16p, _u16p, _f32p, _f32p,
                                        i32, i32, i32, i32, i32, f32, f32, _f32p, _f32p, _f32p, i32]
@@ -117,22 +117,24 @@ def head_norm_rope(x, w, eps, w_offset, cos_tab, sin_tab, pos):
 
 
 def attention(q, k, v, *, causal, k_lengths=None, q_lengths=None, row_step=1, nthreads=0):
-    """o = softmax(q k^T / sqrt(D)) v per (b, h); q [B][H][L][D], k/v [B][Hk][Lk][D] fp32.
+    """o = softmax(q k^T / sqrt(Dk)) v per (b, h); q [B][H][L][Dk], k [B][Hk][Lk][Dk],
+    v [B][Hk][Lk][Dv] fp32 -> o [B][H][L][Dv].
 
     src/kernels/attention.jl:12-91: GQA head h uses kv head h // (H/Hk); causal
     offset k_len - q_len; o = 0 for rows with no key. Rows t >= q_len (and rows
     skipped by row_step) are returned as NaN.
     """
     q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
-    B, H, L, D = q.shape
-    Hk, Lk = k.shape[1], k.shape[2]
-    o = np.full_like(q, np.nan)
+    B, H, L, Dk = q.shape
+    Hk, Lk, Dv = k.shape[1], k.shape[2], v.shape[3]
+    o = np.full((B, H, L, Dv), np.nan, np.float32)
     kl = _c(k_lengths, np.int32) if k_lengths is not None else None
     ql = _c(q_lengths, np.int32) if q_lengths is not None else None
     lib().orc_attention(q, k, v, o,
                         kl.ctypes.data if kl is not None else None,
                         ql.ctypes.data if ql is not None else None,
-                        B, H, Hk, L, Lk, D, int(bool(causal)), int(row_step), int(nthreads))
+                        B, H, Hk, L, Lk, Dk, Dv, int(bool(causal)), int(row_step),
+                        int(nthreads))
     return o
 
 

@@ -86,10 +86,11 @@ void orc_head_norm_rope(const float* x, const float* w, float eps, float w_off,
 static inline float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 /* One query row against keys [0, nk): o = softmax(scale * q.k) v, o = 0 if nk == 0
- * (attention.jl:86). k_rows/v_rows are arrays of row pointers (so the oracle can
- * mix cache rows and freshly computed rows without copying). */
+ * (attention.jl:86). q, k rows of Dk, v, o rows of Dv. k_rows/v_rows are arrays
+ * of row pointers (so the oracle can mix cache rows and freshly computed rows
+ * without copying). */
 static void attend_row(const float* q, const float* const* k_rows, const float* const* v_rows,
-                       int64_t nk, int D, float scale, float* s_buf, float* o) {
+                       int64_t nk, int Dk, int D, float scale, float* s_buf, float* o) {
   for (int d = 0; d < D; ++d) o[d] = 0.f;
   if (nk <= 0) return;
   float m = -INFINITY;
@@ -97,7 +98,7 @@ static void attend_row(const float* q, const float* const* k_rows, const float* 
     const float* k = k_rows[u];
     float acc = 0.f;
 #pragma omp simd reduction(+ : acc)
-    for (int d = 0; d < D; ++d) acc += q[d] * k[d];
+    for (int d = 0; d < Dk; ++d) acc += q[d] * k[d];
     s_buf[u] = acc * scale;
     if (s_buf[u] > m) m = s_buf[u];
   }
@@ -121,17 +122,18 @@ static void set_threads(int nthreads) {
 #endif
 }
 
-/* attention! core (attention.jl:12-91): q [B][H][L][D], k/v [B][Hk][Lk][D] (fp32),
- * o [B][H][L][D]. k_len = k_lengths ? k_lengths[b] : Lk, q_len likewise; the
+/* attention! core (attention.jl:12-91): q [B][H][L][Dk], k [B][Hk][Lk][Dk], v
+ * [B][Hk][Lk][Dv] (fp32), o [B][H][L][Dv], scale 1/sqrt(Dk) (attention.jl:114).
+ * k_len = k_lengths ? k_lengths[b] : Lk, q_len likewise; the
  * causal offset is k_len - q_len (queries are the suffix of keys). Rows
  * t >= q_len are left untouched. row_step > 1 evaluates every row_step-th row
  * only (the others are left untouched) to bound the cost of large checks. */
 void orc_attention(const float* q, const float* k, const float* v, float* o,
                    const int32_t* k_lengths, const int32_t* q_lengths, int B, int H, int Hk,
-                   int L, int Lk, int D, int causal, int row_step, int nthreads) {
+                   int L, int Lk, int Dk, int Dv, int causal, int row_step, int nthreads) {
   set_threads(nthreads);
   const int G = H / Hk;
-  const float scale = 1.0f / sqrtf((float)D);
+  const float scale = 1.0f / sqrtf((float)Dk);
   if (row_step < 1) row_step = 1;
 #pragma omp parallel
   {
@@ -150,14 +152,14 @@ void orc_attention(const float* q, const float* k, const float* v, float* o,
           int64_t nk = causal ? (int64_t)t + off + 1 : k_len;
           if (nk > k_len) nk = k_len;
           if (nk < 0) nk = 0;
-          const float* kb = k + ((size_t)b * Hk + hk) * (size_t)Lk * D;
-          const float* vb = v + ((size_t)b * Hk + hk) * (size_t)Lk * D;
+          const float* kb = k + ((size_t)b * Hk + hk) * (size_t)Lk * Dk;
+          const float* vb = v + ((size_t)b * Hk + hk) * (size_t)Lk * Dv;
           for (int64_t u = 0; u < nk; ++u) {
-            kr[u] = kb + u * D;
-            vr[u] = vb + u * D;
+            kr[u] = kb + u * Dk;
+            vr[u] = vb + u * Dv;
           }
-          attend_row(q + (((size_t)b * H + h) * L + t) * D, kr, vr, nk, D, scale, s_buf,
-                     o + (((size_t)b * H + h) * L + t) * D);
+          attend_row(q + (((size_t)b * H + h) * L + t) * Dk, kr, vr, nk, Dk, Dv, scale, s_buf,
+                     o + (((size_t)b * H + h) * L + t) * Dv);
         }
     free(s_buf);
     free(kr);
@@ -358,7 +360,7 @@ void orc_gated_prefill(const uint16_t* qkv, const uint16_t* kc, const uint16_t* 
             kp[P + u] = kout + (((size_t)b * Hk + hk) * T + u) * D;
             vp[P + u] = vout + (((size_t)b * Hk + hk) * T + u) * D;
           }
-          attend_row(qn, kp, vp, nk, D, scale, s_buf, o);
+          attend_row(qn, kp, vp, nk, D, D, scale, s_buf, o);
           float* orow = out + (((size_t)b * T + t) * Hq + h) * D;
           for (int d = 0; d < D; ++d) orow[d] = o[d] * sigmoid_f(bf(gr[d]));
         }

@@ -55,8 +55,8 @@ def _p(x):
 def test_attention_rejects_gqa_mismatch(vm):
     lib = vm._lib.load()
     rc = lib.vm_attention_fwd(_p(FAKE), 256, 256 * 8, 256 * 8 * 16, _p(FAKE), 256, 256 * 8,
-                              256 * 8 * 16, _p(FAKE), _p(FAKE), 256, 256 * 8, 256 * 8 * 3, None,
-                              None, 1, 16, 3, 256, 8, 8, 1, None)
+                              256 * 8 * 16, _p(FAKE), 256, 256 * 8, 256 * 8 * 3, _p(FAKE), 256,
+                              256 * 8, 256 * 8 * 3, None, None, 1, 16, 3, 256, 256, 8, 8, 1, None)
     assert rc == vm._lib.VM_E_DIM
     assert lib.vm_last_error().decode() == \
         "Attention heads (16) is not a multiple of key-value heads (3)"
@@ -65,25 +65,38 @@ def test_attention_rejects_gqa_mismatch(vm):
 
 
 def test_unsupported_head_dim(vm):
+    """Head dims are powers of two from 16 to 512 (qknorm_rope_append.jl:108);
+    the operators reject others before any launch."""
     lib = vm._lib.load()
-    rc = lib.vm_attention_fwd(_p(FAKE), 128, 128, 128, _p(FAKE), 128, 128, 128, _p(FAKE),
-                              _p(FAKE), 128, 128, 128, None, None, 1, 16, 4, 128, 8, 8, 1, None)
+    rc = lib.vm_attention_fwd(_p(FAKE), 96, 96, 96, _p(FAKE), 96, 96, 96, _p(FAKE), 96, 96, 96,
+                              _p(FAKE), 96, 96, 96, None, None, 1, 16, 4, 96, 96, 8, 8, 1, None)
     assert rc == vm._lib.VM_E_UNSUPPORTED
-    assert "D = 128" in lib.vm_last_error().decode()
+    assert "Dk = 96" in lib.vm_last_error().decode()
+    rc = lib.vm_attention_fwd(_p(FAKE), 1024, 1024, 1024, _p(FAKE), 128, 128, 128, _p(FAKE), 128,
+                              128, 128, _p(FAKE), 1024, 1024, 1024, None, None, 1, 16, 4, 128,
+                              1024, 8, 8, 1, None)
+    assert rc == vm._lib.VM_E_UNSUPPORTED
+    assert "Dv = 1024" in lib.vm_last_error().decode()
+    rc = lib.vm_qnorm_rope(_p(FAKE), 128, 128 * 16, _p(FAKE), _p(FAKE), _p(FAKE), 512, _p(FAKE), 1,
+                           16, 128, 65, 1e-6, 1.0, None)
+    assert rc == vm._lib.VM_E_ARG  # the rotary part 2 * 65 exceeds D = 128
+    assert "HALF_ROT = 65" in lib.vm_last_error().decode()
 
 
 def test_misaligned_pointer_rejected(vm):
     lib = vm._lib.load()
-    rc = lib.vm_attention_fwd(_p(FAKE + 2), 256, 256, 256, _p(FAKE), 256, 256, 256, _p(FAKE),
-                              _p(FAKE), 256, 256, 256, None, None, 1, 16, 4, 256, 8, 8, 1, None)
+    rc = lib.vm_attention_fwd(_p(FAKE + 2), 256, 256, 256, _p(FAKE), 256, 256, 256, _p(FAKE), 256,
+                              256, 256, _p(FAKE), 256, 256, 256, None, None, 1, 16, 4, 256, 256, 8,
+                              8, 1, None)
     assert rc == vm._lib.VM_E_ARG
     assert "aligned" in lib.vm_last_error().decode()
 
 
 def test_bad_stride_rejected(vm):
     lib = vm._lib.load()
-    rc = lib.vm_attention_fwd(_p(FAKE), 256, 256, 256, _p(FAKE), 250, 256, 256, _p(FAKE),
-                              _p(FAKE), 256, 256, 256, None, None, 1, 16, 4, 256, 8, 8, 1, None)
+    rc = lib.vm_attention_fwd(_p(FAKE), 256, 256, 256, _p(FAKE), 250, 256, 256, _p(FAKE), 256,
+                              256, 256, _p(FAKE), 256, 256, 256, None, None, 1, 16, 4, 256, 256, 8,
+                              8, 1, None)
     assert rc == vm._lib.VM_E_ARG
 
 
@@ -97,18 +110,35 @@ def test_decode_scratch_size_and_shortfall(vm):
     body = slots * 4 * (256 + 2) * 4
     assert n == -(-body // 256) * 256 + -(-(1 + 2 * 32) * 4 // 256) * 256
     assert lib.vm_decode_scratch_bytes(1, 16, 3, 256, 512, 0) == 0  # invalid GQA -> 0
-    rc = lib.vm_decode_attention(_p(FAKE), 256, 4096, _p(FAKE), 256, 4096, _p(FAKE), _p(FAKE),
-                                 256, 256 * 512, 256 * 512 * 4, 512, _p(FAKE), 1, 16, 4, 256, 0,
-                                 _p(FAKE), 64, None)
+    rc = lib.vm_decode_attention(_p(FAKE), 256, 4096, _p(FAKE), 256, 4096, _p(FAKE), 256,
+                                 256 * 512, 256 * 512 * 4, _p(FAKE), 256, 256 * 512,
+                                 256 * 512 * 4, 512, _p(FAKE), 1, 16, 4, 256, 256, 0, _p(FAKE), 64,
+                                 None)
     assert rc == vm._lib.VM_E_SCRATCH
     assert "scratch" in lib.vm_last_error().decode()
 
 
-def test_decode_rejects_large_group(vm):
+def test_generic_decode_scratch(vm):
+    """Shapes outside the tuned decode (here Dv = 128, a group of 16) size one
+    (Dv + 2)-float partial row per split, sequence and head: n_splits per (b,
+    kv head) as given, or about two workgroups per CU for 0 (at least 256 keys
+    per split); a short scratch is refused before any launch."""
     lib = vm._lib.load()
-    rc = lib.vm_decode_attention(_p(FAKE), 256, 4096, _p(FAKE), 256, 4096, _p(FAKE), _p(FAKE),
-                                 256, 256 * 512, 256 * 512, 512, _p(FAKE), 1, 16, 1, 256, 0,
-                                 _p(FAKE), 1 << 30, None)
+    assert lib.vm_decode_scratch_bytes(2, 16, 1, 128, 4096, 8) == -(-8 * 2 * 16 * 130 * 4 // 256) * 256
+    # n_splits = 0: 512 / (B Hk) = 256 workgroups' worth, capped at ctx / 256 = 16 splits
+    assert lib.vm_decode_scratch_bytes(2, 16, 1, 128, 4096, 0) == -(-16 * 2 * 16 * 130 * 4 // 256) * 256
+    assert lib.vm_decode_scratch_bytes(1, 16, 4, 96, 512, 0) == 0  # not a power of two
+    rc = lib.vm_decode_attention(_p(FAKE), 128, 2048, _p(FAKE), 128, 2048, _p(FAKE), 128,
+                                 128 * 512, 128 * 512, _p(FAKE), 128, 128 * 512, 128 * 512, 512,
+                                 _p(FAKE), 1, 16, 1, 128, 128, 0, _p(FAKE), 64, None)
+    assert rc == vm._lib.VM_E_SCRATCH
+
+
+def test_decode_rejects_unsupported_head_dim(vm):
+    lib = vm._lib.load()
+    rc = lib.vm_decode_attention(_p(FAKE), 1024, 4096, _p(FAKE), 1024, 4096, _p(FAKE), 1024,
+                                 1024 * 512, 1024 * 512, _p(FAKE), 1024, 1024 * 512, 1024 * 512,
+                                 512, _p(FAKE), 1, 16, 1, 1024, 1024, 0, _p(FAKE), 1 << 30, None)
     assert rc == vm._lib.VM_E_UNSUPPORTED
 
 

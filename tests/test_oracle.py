@@ -77,19 +77,19 @@ def test_rope_tables_closed_forms(orc):
 
 
 # ---------------------------------------------------------------- norm + rope
-def _torch_norm_rope(x, w, pos, ctx=2048):
+def _torch_norm_rope(x, w, pos, ctx=2048, half=HALF):
     """Independent restatement: torch rms_norm with weight (w + 1), then the first
-    64 dims rotated as 32 complex numbers (x_i + i x_{i+32}) * exp(i angle_i)."""
+    2 half dims rotated as half complex numbers (x_i + i x_{i+half}) * exp(i angle_i)."""
     xt = torch.from_numpy(np.asarray(x, np.float32))
     wt = torch.from_numpy(np.asarray(w, np.float32)) + 1.0
     y = F.rms_norm(xt, (xt.shape[-1],), weight=wt, eps=EPS)
-    inv = torch.tensor([THETA ** (-i / HALF) for i in range(HALF)], dtype=torch.float64).float()
+    inv = torch.tensor([THETA ** (-i / half) for i in range(half)], dtype=torch.float64).float()
     ang = (inv * torch.tensor(float(pos), dtype=torch.float32)).double()
-    z = torch.complex(y[..., :HALF].double(), y[..., HALF:2 * HALF].double())
+    z = torch.complex(y[..., :half].double(), y[..., half:2 * half].double())
     z = z * torch.polar(torch.ones_like(ang), ang)
     out = y.clone().double()
-    out[..., :HALF] = z.real
-    out[..., HALF:2 * HALF] = z.imag
+    out[..., :half] = z.real
+    out[..., half:2 * half] = z.imag
     return out.numpy()
 
 
@@ -102,6 +102,18 @@ def test_head_norm_rope_vs_torch(orc, pos):
     ref = _torch_norm_rope(x, w, pos)
     assert np.max(np.abs(y - ref)) < 2e-5
     assert np.array_equal(y[2 * HALF:] != 0, ref[2 * HALF:] != 0)
+
+
+@pytest.mark.parametrize("Dh,half", [(16, 8), (64, 8), (128, 64), (512, 32), (128, 1)])
+def test_head_norm_rope_head_dims_vs_torch(orc, Dh, half):
+    """Other head dims and rotary widths (qknorm_rope_append.jl:100-141 take any
+    power-of-two D and any HALF_ROT up to D/2)."""
+    c, s = orc.rope_tables(half, 4096, THETA)
+    x = bf16_to_f32(normal_bf16((Dh,), 300 + Dh))
+    w = bf16_to_f32(normal_bf16((Dh,), 301, scale=0.05))
+    y = orc.head_norm_rope(x, w, EPS, 1.0, c, s, 777)
+    ref = _torch_norm_rope(x, w, 777, half=half)
+    assert np.max(np.abs(y - ref)) < 2e-5
 
 
 def test_head_norm_invariants(orc):
@@ -136,7 +148,7 @@ def _torch_attention(q, k, v, causal, k_lengths=None, q_lengths=None):
     """SDPA per sequence with KV heads repeated and a suffix-aligned causal mask."""
     B, H, L, _ = q.shape
     Hk, Lk = k.shape[1], k.shape[2]
-    out = np.full(q.shape, np.nan, np.float32)
+    out = np.full((B, H, L, v.shape[3]), np.nan, np.float32)
     for b in range(B):
         kl = int(k_lengths[b]) if k_lengths is not None else Lk
         ql = int(q_lengths[b]) if q_lengths is not None else L
@@ -176,6 +188,22 @@ def test_attention_ragged_vs_sdpa(orc):
     ref = _torch_attention(q, k, v, True, kl, ql)
     finite = ~np.isnan(ref)
     assert np.array_equal(finite, ~np.isnan(o))       # rows past q_len untouched
+    assert np.max(np.abs(o[finite] - ref[finite])) < 2e-6
+
+
+@pytest.mark.parametrize("Dk,Dv,causal", [(64, 128, True), (128, 32, False), (16, 512, True)])
+def test_attention_head_dims_vs_sdpa(orc, Dk, Dv, causal):
+    """Dk != Dv and head dims other than 256 (attention.jl:93-101 takes any):
+    scores scaled by 1/sqrt(Dk), outputs Dv wide; ragged lengths, GQA 4:1."""
+    B, H, Hk, L, Lk = 2, 8, 2, 11, 37
+    q, k, v = _rand((B, H, L, Dk), 7), _rand((B, Hk, Lk, Dk), 8), _rand((B, Hk, Lk, Dv), 9)
+    kl = np.array([37, 20], np.int32)
+    ql = np.array([11, 6], np.int32)
+    o = orc.attention(q, k, v, causal=causal, k_lengths=kl, q_lengths=ql)
+    ref = _torch_attention(q, k, v, causal, kl, ql)
+    assert o.shape == (B, H, L, Dv)
+    finite = ~np.isnan(ref)
+    assert np.array_equal(finite, ~np.isnan(o))
     assert np.max(np.abs(o[finite] - ref[finite])) < 2e-6
 
 

@@ -78,13 +78,13 @@ _SIGS = {
     "vm_rope_tables": (_c_i, [_p, _p, _c_i, _c_i64, _c_d, _p]),
     "vm_qnorm_rope": (_c_i, [_p, _c_i64, _c_i64, _p, _p, _p, _c_i64, _p,
                              _c_i, _c_i, _c_i, _c_i, _c_f, _c_f, _p]),
-    "vm_knorm_rope_append": (_c_i, [_p, _p, _c_i64, _c_i64, _c_i64, _c_i64, _p, _p, _c_i64,
-                                    _c_i64, _p, _p, _p, _p, _c_i, _c_i, _c_i, _c_i, _c_f, _c_f,
-                                    _p]),
+    "vm_knorm_rope_append": (_c_i, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _c_i64, _c_i64,
+                                    _c_i64, _p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _p, _p,
+                                    _p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_f, _p]),
     "vm_decode_scratch_bytes": (_c_sz, [_c_i, _c_i, _c_i, _c_i, _c_i64, _c_i]),
-    "vm_decode_attention": (_c_i, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _p, _c_i64,
-                                   _c_i64, _c_i64, _c_i64, _p, _c_i, _c_i, _c_i, _c_i, _c_i, _p,
-                                   _c_sz, _p]),
+    "vm_decode_attention": (_c_i, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _c_i64, _c_i64,
+                                   _c_i64, _p, _c_i64, _c_i64, _c_i64, _c_i64, _p, _c_i, _c_i,
+                                   _c_i, _c_i, _c_i, _c_i, _p, _c_sz, _p]),
     "vm_sigmoid_gate": (_c_i, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _c_i, _c_i, _c_i, _p]),
     "vm_gated_attn_decode": (_c_i, [_p, _c_i64, _p, _c_i64, _p, _p, _c_i64, _c_i64, _c_i64,
                                     _c_i64, _p, _p, _p, _p, _p, _c_i, _c_i, _c_i, _c_i, _c_i,
@@ -93,9 +93,9 @@ _SIGS = {
                                             _c_i64, _c_i64, _p, _p, _p, _p, _p, _c_i, _c_i, _c_i,
                                             _c_i, _c_i, _c_i, _c_f, _c_f, _c_i, _p]),
     "vm_advance_positions": (_c_i, [_p, _c_i, _p]),
-    "vm_attention_fwd": (_c_i, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _c_i64, _c_i64, _p, _p,
-                                _c_i64, _c_i64, _c_i64, _p, _p, _c_i, _c_i, _c_i, _c_i, _c_i,
-                                _c_i, _c_i, _p]),
+    "vm_attention_fwd": (_c_i, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _c_i64, _c_i64, _p,
+                                _c_i64, _c_i64, _c_i64, _p, _c_i64, _c_i64, _c_i64, _p, _p, _c_i,
+                                _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _p]),
     "vm_prefill_kv_append": (_c_i, [_p, _p, _c_i64, _c_i64, _c_i64, _c_i64, _p, _c_i64, _c_i64,
                                     _p, _p, _p, _p, _p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i,
                                     _c_f, _c_f, _p]),

@@ -1,0 +1,303 @@
+// generic.hip — the attention operators at head shapes outside the tuned
+// kernels: qnorm_rope! and knorm_rope_append! (src/kernels/qknorm_rope_append.jl:
+// 100-141), attention! (src/kernels/attention.jl:93-129) and decode_attention!
+// (src/kernels/attention_decode.jl:134-200) for any power-of-two head dims from
+// 16 to 512, Dk != Dv, any rotary half-width and any GQA group. The tuned
+// kernels (rows.hip, prefill.hip, decode.hip) are built for Qwen3.5's head
+// shape (D = 256, a 64-dim rotary part, groups up to 8); these take every other
+// shape the reference's operators take. fp32 arithmetic on bf16 operands staged
+// in LDS, one workgroup per 16 query rows: correct at any shape, not tuned.
+#include <algorithm>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace vm {
+
+namespace {
+
+__device__ __forceinline__ float bfv(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+constexpr int AQ = 16;  // query rows per workgroup: 16 threads per row
+constexpr int AK = 32;  // keys per staged tile
+
+}  // namespace
+
+// ---- rows: one wave per (head, sequence) row; lane l holds d = l + 64 e. The
+// rotate-half partner of d < 2 half is read raw and normed by the same lane, so
+// every load of the row comes before its first store (Q is updated in place).
+template <int E>
+__global__ __launch_bounds__(256) void norm_rope_any_kernel(RowAnyArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (int64_t)a.B * a.H) return;
+  const int h = (int)(row % a.H), b = (int)(row / a.H);
+  const int64_t pos = (int64_t)a.positions[b] - 1;
+  if (pos < 0 || pos >= a.ctx) return;  // out-of-contract position: write nothing
+  const uint16_t* src = a.in + b * a.in_sb + h * a.in_sh;
+  uint16_t* dst = a.out + b * a.out_sb + h * a.out_sh + (a.out_at_pos ? pos * a.out_st : 0);
+  const int D = a.D, half = a.half;
+  float x[E], xp[E];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int d = lane + 64 * e;
+    x[e] = 0.f;
+    xp[e] = 0.f;
+    if (d < D) {
+      x[e] = bfv(src[d]);
+      if (d < 2 * half) xp[e] = bfv(src[d < half ? d + half : d - half]);
+    }
+    ss = fmaf(x[e], x[e], ss);
+  }
+  ss = wave_sum_all(ss);
+  const float r = 1.0f / sqrtf(ss / (float)D + a.eps);
+  const float* cs = a.cos_tab + pos * half;
+  const float* sn = a.sin_tab + pos * half;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int d = lane + 64 * e;
+    if (d >= D) continue;
+    float y = x[e] * r * (bfv(a.w[d]) + a.w_offset);
+    if (d < 2 * half) {
+      const bool first = d < half;
+      const int i = first ? d : d - half;
+      const float yp = xp[e] * r * (bfv(a.w[first ? d + half : d - half]) + a.w_offset);
+      y = first ? y * cs[i] - yp * sn[i] : y * cs[i] + yp * sn[i];
+    }
+    dst[d] = f2bf(y);
+  }
+  if (a.in2) {  // V rides along: copied into the same cache column
+    const uint16_t* s2 = a.in2 + b * a.in2_sb + h * a.in2_sh;
+    uint16_t* d2 = a.out2 + b * a.out2_sb + h * a.out2_sh + pos * a.out2_st;
+    for (int d = lane; d < a.D2; d += 64) d2[d] = s2[d];
+  }
+}
+
+// ---- attention over staged tiles. Workgroup (row block, (b, kv head), split):
+// rows rho = g L + t enumerate the group's G query heads x L queries, so the
+// heads of a kv group share every staged K/V tile. Thread (r, c) = (tid / 16,
+// tid % 16) scores keys c and c + 16 of each tile for row r, and owns the
+// output columns c + 16 i of that row. Online softmax per row (max and sum over
+// the row's 16 threads, one 16-lane group of a wave). With part set (decode
+// splits) it writes the unnormalised row, its max and its sum instead.
+template <int DVT>
+__global__ __launch_bounds__(256) void attn_any_kernel(AttnAnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int Dk = a.Dk, Dv = a.Dv;
+  const int qs_st = Dk + 4;  // floats per staged Q row (rows on distinct banks)
+  const int ks_st = Dk + 8;  // bf16 per staged K row (the 16 keys a row group reads: distinct banks)
+  const int vs_st = Dv + 8;
+  float* qs = reinterpret_cast<float*>(smem);
+  uint16_t* ks = reinterpret_cast<uint16_t*>(qs + AQ * qs_st);
+  uint16_t* vs = ks + AK * ks_st;
+  float* ps = reinterpret_cast<float*>(vs + AK * vs_st);  // [AQ][AK + 1]
+  const int G = a.H / a.Hk;
+  const int hk = blockIdx.y % a.Hk, b = blockIdx.y / a.Hk, z = blockIdx.z;
+  const int rows = G * a.L, rho0 = blockIdx.x * AQ;
+  const int tid = threadIdx.x, r = tid >> 4, c = tid & 15;
+  const int k_len = min(a.k_lengths ? a.k_lengths[b] : a.Lk, a.Lk);
+  const int q_len = min(a.q_lengths ? a.q_lengths[b] : a.L, a.L);
+  const int off = k_len - q_len;  // queries are the suffix of the keys
+  const int rho = rho0 + r;
+  const int g = rho / a.L, t = rho % a.L;
+  const bool active = rho < rows && t < q_len;
+  const int h = hk * G + g;
+  // the block's key range: this split's keys, up to its last row's causal limit
+  int tmax = -1;
+  for (int i = 0; i < AQ; ++i) {
+    const int rr = rho0 + i;
+    if (rr < rows && rr % a.L < q_len) tmax = max(tmax, rr % a.L);
+  }
+  if (tmax < 0 && a.part == nullptr) return;  // no row of this block is written
+  const int kb0 = (int)min((int64_t)z * a.split_keys, (int64_t)k_len);
+  int kb1 = (int)min((int64_t)kb0 + a.split_keys, (int64_t)k_len);
+  if (a.causal) kb1 = min(kb1, max(kb0, off + tmax + 1));
+  const int lim = a.causal ? min(kb1 - 1, t + off) : kb1 - 1;  // this row's last key
+  // Q rows of the block, fp32
+  for (int i = tid; i < AQ * Dk; i += 256) {
+    const int rr = i / Dk, d = i % Dk, q_rho = rho0 + rr;
+    float v = 0.f;
+    if (q_rho < rows) {
+      const int qg = q_rho / a.L, qt = q_rho % a.L;
+      v = bfv(a.q[b * a.q_sb + (int64_t)(hk * G + qg) * a.q_sh + (int64_t)qt * a.q_st + d]);
+    }
+    qs[rr * qs_st + d] = v;
+  }
+  float m = -INFINITY, l = 0.f, acc[DVT];
+#pragma unroll
+  for (int i = 0; i < DVT; ++i) acc[i] = 0.f;
+  const uint16_t* kbase = a.k + b * a.k_sb + (int64_t)hk * a.k_sh;
+  const uint16_t* vbase = a.v + b * a.v_sb + (int64_t)hk * a.v_sh;
+  for (int j0 = kb0; j0 < kb1; j0 += AK) {
+    __syncthreads();  // the previous tile's reads are done (and Q is staged)
+    const int kc8 = Dk / 8, vc8 = Dv / 8;
+    for (int i = tid; i < AK * kc8; i += 256) {
+      const int key = i / kc8, ch = i % kc8, j = j0 + key;
+      uint4 u = make_uint4(0u, 0u, 0u, 0u);
+      if (j < kb1) u = *reinterpret_cast<const uint4*>(kbase + (int64_t)j * a.k_st + 8 * ch);
+      *reinterpret_cast<uint4*>(ks + key * ks_st + 8 * ch) = u;
+    }
+    for (int i = tid; i < AK * vc8; i += 256) {
+      const int key = i / vc8, ch = i % vc8, j = j0 + key;
+      uint4 u = make_uint4(0u, 0u, 0u, 0u);
+      if (j < kb1) u = *reinterpret_cast<const uint4*>(vbase + (int64_t)j * a.v_st + 8 * ch);
+      *reinterpret_cast<uint4*>(vs + key * vs_st + 8 * ch) = u;
+    }
+    __syncthreads();
+    float s0 = 0.f, s1 = 0.f;
+    const float* qr = qs + r * qs_st;
+    const uint32_t* k0 = reinterpret_cast<const uint32_t*>(ks + c * ks_st);
+    const uint32_t* k1 = reinterpret_cast<const uint32_t*>(ks + (c + 16) * ks_st);
+    for (int d2 = 0; d2 < Dk / 2; ++d2) {
+      const float qa = qr[2 * d2], qb = qr[2 * d2 + 1];
+      const uint32_t u0 = k0[d2], u1 = k1[d2];
+      s0 = fmaf(qa, bf_lo(u0), s0);
+      s0 = fmaf(qb, bf_hi(u0), s0);
+      s1 = fmaf(qa, bf_lo(u1), s1);
+      s1 = fmaf(qb, bf_hi(u1), s1);
+    }
+    s0 = active && j0 + c <= lim ? s0 * a.scale : -INFINITY;
+    s1 = active && j0 + c + 16 <= lim ? s1 * a.scale : -INFINITY;
+    float bm = fmaxf(s0, s1);
+#pragma unroll
+    for (int x = 8; x >= 1; x >>= 1) bm = fmaxf(bm, __shfl_xor(bm, x, 64));
+    const float mn = fmaxf(m, bm);
+    float corr = 1.f, p0 = 0.f, p1 = 0.f;
+    if (mn != -INFINITY) {
+      corr = expf(m - mn);  // 0 while m is still -inf
+      p0 = expf(s0 - mn);
+      p1 = expf(s1 - mn);
+    }
+    float ls = p0 + p1;
+#pragma unroll
+    for (int x = 8; x >= 1; x >>= 1) ls += __shfl_xor(ls, x, 64);
+    l = l * corr + ls;
+    m = mn;
+    ps[r * (AK + 1) + c] = p0;
+    ps[r * (AK + 1) + c + 16] = p1;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < DVT; ++i) acc[i] *= corr;
+    for (int kk = 0; kk < AK; ++kk) {
+      const float p = ps[r * (AK + 1) + kk];
+      const uint16_t* vr = vs + kk * vs_st + c;
+#pragma unroll
+      for (int i = 0; i < DVT; ++i) acc[i] = fmaf(p, bfv(vr[16 * i]), acc[i]);
+    }
+  }
+  if (!active) return;
+  if (a.part == nullptr) {
+    const float inv = l > 0.f ? 1.0f / l : 0.f;  // no key: o = 0 (attention.jl:86)
+    uint16_t* orow = a.o + b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)t * a.o_st;
+#pragma unroll
+    for (int i = 0; i < DVT; ++i) orow[c + 16 * i] = f2bf(acc[i] * inv);
+  } else {
+    float* pr = a.part + (((int64_t)z * a.B + b) * a.H + h) * (Dv + 2);
+#pragma unroll
+    for (int i = 0; i < DVT; ++i) pr[c + 16 * i] = acc[i];
+    if (c == 0) {
+      pr[Dv] = m;
+      pr[Dv + 1] = l;
+    }
+  }
+}
+
+// The decode splits merged per (b, head), in split order
+// (attention_decode.jl:85-132): o = sum_z e^(m_z - m) acc_z / sum_z e^(m_z - m) l_z.
+__global__ __launch_bounds__(256) void attn_any_combine_kernel(AttnAnyArgs a) {
+  const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
+  const int Dv = a.Dv;
+  const int64_t zst = (int64_t)a.B * a.H * (Dv + 2);
+  const float* p0 = a.part + ((int64_t)b * a.H + h) * (Dv + 2);
+  float mx = -INFINITY;
+  for (int z = 0; z < a.n_split; ++z) mx = fmaxf(mx, p0[z * zst + Dv]);
+  float sum = 0.f;
+  if (mx != -INFINITY)
+    for (int z = 0; z < a.n_split; ++z) {
+      const float mz = p0[z * zst + Dv];
+      if (mz != -INFINITY) sum += p0[z * zst + Dv + 1] * expf(mz - mx);
+    }
+  const float inv = sum > 0.f ? 1.0f / sum : 0.f;
+  uint16_t* orow = a.o + b * a.o_sb + (int64_t)h * a.o_sh;
+  for (int d = threadIdx.x; d < Dv; d += 256) {
+    float o = 0.f;
+    if (mx != -INFINITY)
+      for (int z = 0; z < a.n_split; ++z) {
+        const float mz = p0[z * zst + Dv];
+        if (mz != -INFINITY) o += p0[z * zst + d] * expf(mz - mx);
+      }
+    orow[d] = f2bf(o * inv);
+  }
+}
+
+// ---- launchers ---------------------------------------------------------------
+hipError_t launch_norm_rope_any(const RowAnyArgs& a, hipStream_t st) {
+  const int64_t rows = (int64_t)a.B * a.H;
+  if (rows == 0) return hipSuccess;
+  const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  switch (a.D <= 64 ? 1 : a.D / 64) {
+    case 1: hipLaunchKernelGGL(norm_rope_any_kernel<1>, grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL(norm_rope_any_kernel<2>, grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL(norm_rope_any_kernel<4>, grid, block, 0, st, a); break;
+    case 8: hipLaunchKernelGGL(norm_rope_any_kernel<8>, grid, block, 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+size_t attn_any_lds_bytes(int Dk, int Dv) {
+  return (size_t)AQ * (Dk + 4) * 4 + (size_t)AK * (Dk + 8) * 2 + (size_t)AK * (Dv + 8) * 2 +
+         (size_t)AQ * (AK + 1) * 4;
+}
+
+int attn_any_splits(int B, int H, int Hk, int64_t ctx, int n_splits) {
+  if (n_splits > 0) return n_splits;  // the reference's fixed split count
+  const int G = H / Hk;
+  const int64_t blocks = (int64_t)B * Hk * ((G + AQ - 1) / AQ);
+  int64_t s = (512 + blocks - 1) / blocks;  // about two workgroups per CU
+  s = std::min<int64_t>(s, (ctx + 255) / 256);  // at least 256 keys per split
+  return (int)std::max<int64_t>(1, s);
+}
+
+int attn_any_split_keys(int64_t ctx, int n_split) {
+  // tile-aligned split boundaries (attention_decode.jl:159)
+  const int64_t per = (ctx + n_split - 1) / n_split;
+  return (int)std::max<int64_t>(AK, (per + AK - 1) / AK * AK);
+}
+
+template <int DVT>
+static hipError_t launch_attn_any_t(const AttnAnyArgs& a, dim3 grid, size_t lds, hipStream_t st) {
+  if (lds > 65536) {  // lift the dynamic-LDS cap of the current device for this kernel
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_any_kernel<DVT>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(attn_any_kernel<DVT>, grid, dim3(256), lds, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_any(const AttnAnyArgs& a, hipStream_t st) {
+  if (a.B == 0 || a.L == 0) return hipSuccess;
+  const int G = a.H / a.Hk;
+  const dim3 grid((unsigned)((G * a.L + AQ - 1) / AQ), (unsigned)(a.Hk * a.B),
+                  (unsigned)(a.part ? a.n_split : 1));
+  const size_t lds = attn_any_lds_bytes(a.Dk, a.Dv);
+  hipError_t e;
+  switch (a.Dv / 16) {
+    case 1: e = launch_attn_any_t<1>(a, grid, lds, st); break;
+    case 2: e = launch_attn_any_t<2>(a, grid, lds, st); break;
+    case 4: e = launch_attn_any_t<4>(a, grid, lds, st); break;
+    case 8: e = launch_attn_any_t<8>(a, grid, lds, st); break;
+    case 16: e = launch_attn_any_t<16>(a, grid, lds, st); break;
+    case 32: e = launch_attn_any_t<32>(a, grid, lds, st); break;
+    default: return hipErrorInvalidValue;
+  }
+  if (e != hipSuccess || a.part == nullptr) return e;
+  hipLaunchKernelGGL(attn_any_combine_kernel, dim3((unsigned)(a.B * a.H)), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace vm

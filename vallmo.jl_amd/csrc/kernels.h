@@ -31,6 +31,47 @@ struct RowArgs {
   float eps, w_offset;
 };
 
+// ---- generic.hip: the operators at head shapes outside the tuned kernels
+// (power-of-two head dims 16..512, Dk != Dv, any rotary half-width, any group)
+struct RowAnyArgs {
+  const uint16_t* in;  // rows normed + rotated (Q in place, or raw K)
+  int64_t in_sh, in_sb;
+  uint16_t* out;
+  int64_t out_st, out_sh, out_sb;  // out_st: the cache's token stride (append)
+  const uint16_t* in2;             // optional V rows, copied (D2 wide)
+  int64_t in2_sh, in2_sb;
+  uint16_t* out2;
+  int64_t out2_st, out2_sh, out2_sb;
+  const uint16_t* w;  // norm weight (D,), applied as (w + w_offset)
+  const float* cos_tab;
+  const float* sin_tab;
+  int64_t ctx;
+  const int32_t* positions;  // 1-based column per sequence
+  int B, H, D, D2, half;
+  int out_at_pos;  // 1: the output row is the cache column positions[b] - 1
+  float eps, w_offset;
+};
+hipError_t launch_norm_rope_any(const RowAnyArgs& a, hipStream_t st);
+struct AttnAnyArgs {
+  const uint16_t* q;
+  int64_t q_st, q_sh, q_sb;
+  const uint16_t* k;
+  int64_t k_st, k_sh, k_sb;
+  const uint16_t* v;
+  int64_t v_st, v_sh, v_sb;
+  uint16_t* o;
+  int64_t o_st, o_sh, o_sb;
+  const int32_t* k_lengths;  // nullable
+  const int32_t* q_lengths;  // nullable
+  float* part;  // decode: n_split x B x H partial rows of Dv + 2 floats, merged; NULL: O direct
+  int B, H, Hk, Dk, Dv, L, Lk, causal, n_split, split_keys;
+  float scale;
+};
+size_t attn_any_lds_bytes(int Dk, int Dv);
+int attn_any_splits(int B, int H, int Hk, int64_t ctx, int n_splits);
+int attn_any_split_keys(int64_t ctx, int n_split);
+hipError_t launch_attn_any(const AttnAnyArgs& a, hipStream_t st);
+
 struct DecodeArgs {
   const uint16_t* q;    // raw q (fused) or normalised q
   int64_t q_sh, q_sb;

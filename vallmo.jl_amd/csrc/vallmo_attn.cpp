@@ -6,6 +6,8 @@
 // > 0 = hipError_t passed through. Shape errors mirror @sizes
 // (src/sizes.jl:3-22) and the H % Hk check (src/kernels/attention.jl:110-111).
 #include <hip/hip_runtime.h>
+#include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -97,6 +99,17 @@ int check_head(int D, int half_rot) {
           "head_dim D = %d is not supported (this build is compiled for D = 256)", D);
   REQUIRE(half_rot == vm::HALF_ROT_ABI, VM_E_UNSUPPORTED,
           "HALF_ROT = %d is not supported (this build is compiled for HALF_ROT = 32)", half_rot);
+  return VM_OK;
+}
+// the generic operators' head shapes: power-of-two dims 16..512
+int check_head_any(int D, const char* what, const char* name) {
+  REQUIRE(D >= 16 && D <= 512 && (D & (D - 1)) == 0, VM_E_UNSUPPORTED,
+          "%s: %s = %d (head dims are powers of two from 16 to 512)", what, name, D);
+  return VM_OK;
+}
+int check_rot(int D, int half_rot, const char* what) {
+  REQUIRE(half_rot >= 1 && 2 * half_rot <= D, VM_E_ARG,
+          "%s: HALF_ROT = %d (the rotary part 2 HALF_ROT must fit in D = %d)", what, half_rot, D);
   return VM_OK;
 }
 int check_gqa(int H, int Hk) {
@@ -253,12 +266,22 @@ int vm_rope_tables(float* c, float* s, int half_rot, int64_t ctx, double theta, 
 int vm_qnorm_rope(vm_bf16* q, int64_t q_sh, int64_t q_sb, const vm_bf16* qw, const float* cs,
                   const float* sn, int64_t ctx, const int32_t* positions, int B, int Hq, int D,
                   int half_rot, float eps, float w_offset, vm_stream st) {
-  TRY(check_head(D, half_rot));
+  TRY(check_head_any(D, "qnorm_rope", "D"));
+  TRY(check_rot(D, half_rot, "qnorm_rope"));
   REQUIRE(B >= 0 && Hq > 0 && ctx > 0, VM_E_ARG, "qnorm_rope: B = %d, Hq = %d, Ctx = %lld", B, Hq,
           (long long)ctx);
   REQUIRE(q && qw && cs && sn && positions, VM_E_ARG, "qnorm_rope: NULL pointer argument");
   TRY(check_stride(q_sh, "q_sh"));
   TRY(check_stride(q_sb, "q_sb"));
+  if (D != vm::HEAD_DIM_ABI || half_rot != vm::HALF_ROT_ABI) {  // the generic row kernel
+    vm::RowAnyArgs g{};
+    g.in = q; g.in_sh = q_sh; g.in_sb = q_sb;
+    g.out = q; g.out_sh = q_sh; g.out_sb = q_sb;
+    g.w = qw; g.cos_tab = cs; g.sin_tab = sn; g.ctx = ctx; g.positions = positions;
+    g.B = B; g.H = Hq; g.D = D; g.half = half_rot; g.eps = eps; g.w_offset = w_offset;
+    return hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_norm_rope_any(g, S(st)); }),
+                      "qnorm_rope");
+  }
   vm::RowArgs a{};
   a.in = q; a.out = q; a.in_sh = a.out_sh = q_sh; a.in_sb = a.out_sb = q_sb;
   a.w = qw; a.cos_tab = cs; a.sin_tab = sn; a.ctx = ctx; a.positions = positions;
@@ -267,36 +290,67 @@ int vm_qnorm_rope(vm_bf16* q, int64_t q_sh, int64_t q_sb, const vm_bf16* qw, con
 }
 
 // ---- a4 -------------------------------------------------------------------
-int vm_knorm_rope_append(vm_bf16* kc, vm_bf16* vc, int64_t c_st, int64_t c_sh, int64_t c_sb,
-                         int64_t ctx, const vm_bf16* k_raw, const vm_bf16* v_raw, int64_t r_sh,
-                         int64_t r_sb, const vm_bf16* kw, const float* cs, const float* sn,
-                         const int32_t* positions, int B, int Hk, int D, int half_rot, float eps,
-                         float w_offset, vm_stream st) {
-  TRY(check_head(D, half_rot));
+int vm_knorm_rope_append(vm_bf16* kc, int64_t kc_st, int64_t kc_sh, int64_t kc_sb, vm_bf16* vc,
+                         int64_t vc_st, int64_t vc_sh, int64_t vc_sb, int64_t ctx,
+                         const vm_bf16* k_raw, int64_t kr_sh, int64_t kr_sb, const vm_bf16* v_raw,
+                         int64_t vr_sh, int64_t vr_sb, const vm_bf16* kw, const float* cs,
+                         const float* sn, const int32_t* positions, int B, int Hk, int Dk, int Dv,
+                         int half_rot, float eps, float w_offset, vm_stream st) {
+  TRY(check_head_any(Dk, "knorm_rope_append", "Dk"));
+  TRY(check_head_any(Dv, "knorm_rope_append", "Dv"));
+  TRY(check_rot(Dk, half_rot, "knorm_rope_append"));
   REQUIRE(B >= 0 && Hk > 0 && ctx > 0, VM_E_ARG, "knorm_rope_append: B = %d, Hk = %d, Ctx = %lld",
           B, Hk, (long long)ctx);
   REQUIRE(kc && vc && k_raw && v_raw && kw && cs && sn && positions, VM_E_ARG,
           "knorm_rope_append: NULL pointer argument");
-  TRY(check_stride(c_st, "c_st"));
-  TRY(check_stride(c_sh, "c_sh"));
-  TRY(check_stride(c_sb, "c_sb"));
-  TRY(check_stride(r_sh, "r_sh"));
-  TRY(check_stride(r_sb, "r_sb"));
+  for (int64_t v : {kc_st, kc_sh, kc_sb, vc_st, vc_sh, vc_sb, kr_sh, kr_sb, vr_sh, vr_sb})
+    TRY(check_stride(v, "knorm_rope_append"));
+  const bool tuned = Dk == vm::HEAD_DIM_ABI && Dv == Dk && half_rot == vm::HALF_ROT_ABI &&
+                     kc_st == vc_st && kc_sh == vc_sh && kc_sb == vc_sb && kr_sh == vr_sh &&
+                     kr_sb == vr_sb;
+  if (!tuned) {  // the generic row kernel: K normed and rotated, V copied
+    vm::RowAnyArgs g{};
+    g.in = k_raw; g.in_sh = kr_sh; g.in_sb = kr_sb;
+    g.out = kc; g.out_st = kc_st; g.out_sh = kc_sh; g.out_sb = kc_sb;
+    g.in2 = v_raw; g.in2_sh = vr_sh; g.in2_sb = vr_sb;
+    g.out2 = vc; g.out2_st = vc_st; g.out2_sh = vc_sh; g.out2_sb = vc_sb;
+    g.w = kw; g.cos_tab = cs; g.sin_tab = sn; g.ctx = ctx; g.positions = positions;
+    g.B = B; g.H = Hk; g.D = Dk; g.D2 = Dv; g.half = half_rot; g.out_at_pos = 1;
+    g.eps = eps; g.w_offset = w_offset;
+    return hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_norm_rope_any(g, S(st)); }),
+                      "knorm_rope_append");
+  }
   vm::RowArgs a{};
-  a.in = k_raw; a.in2 = v_raw; a.in_sh = r_sh; a.in_sb = r_sb;
-  a.out = kc; a.out2 = vc; a.out_st = c_st; a.out_sh = c_sh; a.out_sb = c_sb;
+  a.in = k_raw; a.in2 = v_raw; a.in_sh = kr_sh; a.in_sb = kr_sb;
+  a.out = kc; a.out2 = vc; a.out_st = kc_st; a.out_sh = kc_sh; a.out_sb = kc_sb;
   a.w = kw; a.cos_tab = cs; a.sin_tab = sn; a.ctx = ctx; a.positions = positions;
   a.B = B; a.H = Hk; a.T = 1; a.out_at_pos = 1; a.eps = eps; a.w_offset = w_offset;
   return hip_status(timed(VM_K_ROWS, S(st), [&] { return vm::launch_norm_rope_rows(a, S(st)); }), "knorm_rope_append");
 }
 
 // ---- a5 -------------------------------------------------------------------
-size_t vm_decode_scratch_bytes(int B, int H, int Hk, int D, int64_t ctx, int n_splits) {
-  if (B <= 0 || H <= 0 || Hk <= 0 || H % Hk || D != vm::HEAD_DIM_ABI || ctx <= 0) return 0;
+// the tuned split-KV decode's workspace (D = 256, groups up to 8)
+static size_t tuned_decode_scratch_bytes(int B, int H, int Hk, int64_t ctx, int n_splits) {
+  if (B <= 0 || H <= 0 || Hk <= 0 || H % Hk || ctx <= 0 || n_splits < 0) return 0;
   const int NW = vm::decode_stream_waves(B, Hk, n_splits);
   const int G = H / Hk;
   const size_t pm_end = decode_part_o_bytes(B, Hk, NW, G) + decode_part_ml_bytes(B, Hk, NW, G);
   return (pm_end + 255) / 256 * 256 + decode_geom_bytes(B);
+}
+// the generic decode's workspace: one (Dv + 2)-float partial row per split,
+// sequence and head (the reference's O_partial, M_partial, L_partial)
+static size_t generic_decode_scratch_bytes(int B, int H, int Hk, int Dv, int64_t ctx,
+                                           int n_splits) {
+  const int ns = vm::attn_any_splits(B, H, Hk, ctx, n_splits);
+  return ((size_t)ns * B * H * (Dv + 2) * sizeof(float) + 255) / 256 * 256;
+}
+
+size_t vm_decode_scratch_bytes(int B, int H, int Hk, int D, int64_t ctx, int n_splits) {
+  if (B <= 0 || H <= 0 || Hk <= 0 || H % Hk || ctx <= 0 || n_splits < 0) return 0;
+  if (D < 16 || D > 512 || (D & (D - 1))) return 0;
+  const size_t generic = generic_decode_scratch_bytes(B, H, Hk, D, ctx, n_splits);
+  if (D != vm::HEAD_DIM_ABI || H / Hk > 8) return generic;
+  return std::max(generic, tuned_decode_scratch_bytes(B, H, Hk, ctx, n_splits));
 }
 
 static int decode_common(vm::DecodeArgs& a, vm::CombineArgs& c, void* scratch, size_t scratch_bytes,
@@ -329,18 +383,53 @@ static int decode_common(vm::DecodeArgs& a, vm::CombineArgs& c, void* scratch, s
 }
 
 int vm_decode_attention(vm_bf16* o, int64_t o_sh, int64_t o_sb, const vm_bf16* q, int64_t q_sh,
-                        int64_t q_sb, const vm_bf16* kc, const vm_bf16* vc, int64_t c_st,
-                        int64_t c_sh, int64_t c_sb, int64_t ctx, const int32_t* lengths, int B,
-                        int H, int Hk, int D, int n_splits, void* scratch, size_t scratch_bytes,
+                        int64_t q_sb, const vm_bf16* kc, int64_t k_st, int64_t k_sh, int64_t k_sb,
+                        const vm_bf16* vc, int64_t v_st, int64_t v_sh, int64_t v_sb,
+                        int64_t ctx, const int32_t* lengths, int B, int H, int Hk, int Dk,
+                        int Dv, int n_splits, void* scratch, size_t scratch_bytes,
                         vm_stream st) {
-  REQUIRE(D == vm::HEAD_DIM_ABI, VM_E_UNSUPPORTED,
-          "head_dim D = %d is not supported (this build is compiled for D = 256)", D);
+  TRY(check_head_any(Dk, "decode_attention", "Dk"));
+  TRY(check_head_any(Dv, "decode_attention", "Dv"));
   REQUIRE(B >= 0, VM_E_ARG, "decode_attention: B = %d", B);
   REQUIRE(o && lengths, VM_E_ARG, "decode_attention: NULL pointer argument");
+  TRY(check_aligned(o, "O"));
   TRY(check_aligned(q, "Q"));
   TRY(check_aligned(kc, "K"));
   TRY(check_aligned(vc, "V"));
-  for (int64_t s : {o_sh, o_sb, q_sh, q_sb, c_st, c_sh, c_sb}) TRY(check_stride(s, "decode"));
+  for (int64_t s : {o_sh, o_sb, q_sh, q_sb, k_st, k_sh, k_sb, v_st, v_sh, v_sb})
+    TRY(check_stride(s, "decode"));
+  TRY(check_gqa(H, Hk));
+  REQUIRE(n_splits >= 0, VM_E_ARG, "decode: n_splits = %d", n_splits);
+  REQUIRE(ctx > 0, VM_E_ARG, "decode: Ctx = %lld", (long long)ctx);
+  const bool tuned = Dk == vm::HEAD_DIM_ABI && Dv == Dk && H / Hk <= 8 && k_st == v_st &&
+                     k_sh == v_sh && k_sb == v_sb &&
+                     (int64_t)B * ctx * Hk < ((int64_t)1 << 31);
+  if (!tuned) {  // the generic split-KV kernel and its merge
+    REQUIRE((int64_t)B * Hk <= 65535 && n_splits <= 65535, VM_E_UNSUPPORTED,
+            "decode: B*Hk = %lld, n_splits = %d (at most 65535 each)", (long long)B * Hk,
+            n_splits);
+    const size_t need = generic_decode_scratch_bytes(B, H, Hk, Dv, ctx, n_splits);
+    REQUIRE(scratch != nullptr && scratch_bytes >= need, VM_E_SCRATCH,
+            "decode: scratch of %zu bytes < %zu required (vm_decode_scratch_bytes)",
+            scratch_bytes, need);
+    TRY(check_aligned(scratch, "scratch"));
+    if (B == 0) return VM_OK;
+    vm::AttnAnyArgs g{};
+    g.q = q; g.q_st = 0; g.q_sh = q_sh; g.q_sb = q_sb;
+    g.k = kc; g.k_st = k_st; g.k_sh = k_sh; g.k_sb = k_sb;
+    g.v = vc; g.v_st = v_st; g.v_sh = v_sh; g.v_sb = v_sb;
+    g.o = o; g.o_st = 0; g.o_sh = o_sh; g.o_sb = o_sb;
+    g.k_lengths = lengths; g.q_lengths = nullptr;
+    g.part = static_cast<float*>(scratch);
+    g.B = B; g.H = H; g.Hk = Hk; g.Dk = Dk; g.Dv = Dv; g.L = 1;
+    g.Lk = (int)std::min<int64_t>(ctx, INT32_MAX); g.causal = 0;
+    g.n_split = vm::attn_any_splits(B, H, Hk, ctx, n_splits);
+    g.split_keys = vm::attn_any_split_keys(ctx, g.n_split);
+    g.scale = 1.0f / sqrtf((float)Dk);
+    return hip_status(timed(VM_K_DECODE_SPLIT, S(st), [&] { return vm::launch_attn_any(g, S(st)); }),
+                      "decode_attention");
+  }
+  const int64_t c_st = k_st, c_sh = k_sh, c_sb = k_sb;
   vm::DecodeArgs a{};
   vm::CombineArgs c{};
   TRY(decode_common(a, c, scratch, scratch_bytes, B, H, Hk, ctx, n_splits));
@@ -434,7 +523,8 @@ int vm_gated_attn_decode_noalloc(vm_bf16* out, int64_t out_sb, const vm_bf16* qk
   REQUIRE(B >= 0 && Hq > 0 && Hk > 0 && Hq % Hk == 0 && ctx > 0 && n_splits >= 0, VM_E_ARG,
           "gated_attn_decode_noalloc: B = %d, Hq = %d, Hk = %d, Ctx = %lld, n_splits = %d", B,
           Hq, Hk, (long long)ctx, n_splits);
-  const size_t need = vm_decode_scratch_bytes(B > 0 ? B : 1, Hq, Hk, D, ctx, n_splits);
+  TRY(check_head(D, half_rot));
+  const size_t need = tuned_decode_scratch_bytes(B > 0 ? B : 1, Hq, Hk, ctx, n_splits);
   REQUIRE(need <= vm::DECODE_STATIC_SCRATCH_BYTES, VM_E_SCRATCH,
           "gated_attn_decode_noalloc: this step needs %zu bytes of workspace, more than the "
           "%zu-byte static workspace (use vm_gated_attn_decode with a caller buffer)",
@@ -455,23 +545,40 @@ int vm_advance_positions(int32_t* positions, int B, vm_stream st) {
 
 // ---- a8 -------------------------------------------------------------------
 int vm_attention_fwd(vm_bf16* o, int64_t o_st, int64_t o_sh, int64_t o_sb, const vm_bf16* q,
-                     int64_t q_st, int64_t q_sh, int64_t q_sb, const vm_bf16* k, const vm_bf16* v,
-                     int64_t kv_st, int64_t kv_sh, int64_t kv_sb, const int32_t* k_lengths,
-                     const int32_t* q_lengths, int B, int H, int Hk, int D, int L, int Lk,
-                     int causal, vm_stream st) {
-  REQUIRE(D == vm::HEAD_DIM_ABI, VM_E_UNSUPPORTED,
-          "head_dim D = %d is not supported (this build is compiled for D = 256)", D);
+                     int64_t q_st, int64_t q_sh, int64_t q_sb, const vm_bf16* k, int64_t k_st,
+                     int64_t k_sh, int64_t k_sb, const vm_bf16* v, int64_t v_st, int64_t v_sh,
+                     int64_t v_sb, const int32_t* k_lengths, const int32_t* q_lengths, int B,
+                     int H, int Hk, int Dk, int Dv, int L, int Lk, int causal, vm_stream st) {
+  TRY(check_head_any(Dk, "attention", "Dk"));
+  TRY(check_head_any(Dv, "attention", "Dv"));
   TRY(check_gqa(H, Hk));
   REQUIRE(B >= 0 && L >= 0 && Lk >= 0, VM_E_ARG, "attention: B = %d, L = %d, Lk = %d", B, L, Lk);
   TRY(check_aligned(o, "O"));
   TRY(check_aligned(q, "Q"));
   TRY(check_aligned(k, "K"));
   TRY(check_aligned(v, "V"));
-  for (int64_t s : {o_st, o_sh, o_sb, q_st, q_sh, q_sb, kv_st, kv_sh, kv_sb})
+  for (int64_t s : {o_st, o_sh, o_sb, q_st, q_sh, q_sb, k_st, k_sh, k_sb, v_st, v_sh, v_sb})
     TRY(check_stride(s, "attention"));
   if (B == 0 || L == 0) return VM_OK;
   REQUIRE(Lk > 0, VM_E_ARG, "attention: k_len must be >= 1 (Lk = 0)");
-  REQUIRE(kv_st < ((int64_t)1 << 25), VM_E_ARG, "attention: K/V token stride too large");
+  const bool tuned = Dk == vm::HEAD_DIM_ABI && Dv == Dk && k_st == v_st && k_sh == v_sh &&
+                     k_sb == v_sb && k_st < ((int64_t)1 << 25);
+  if (!tuned) {  // the generic kernel
+    REQUIRE((int64_t)B * Hk <= 65535, VM_E_UNSUPPORTED, "attention: B*Hk = %lld > 65535",
+            (long long)B * Hk);
+    vm::AttnAnyArgs g{};
+    g.q = q; g.q_st = q_st; g.q_sh = q_sh; g.q_sb = q_sb;
+    g.k = k; g.k_st = k_st; g.k_sh = k_sh; g.k_sb = k_sb;
+    g.v = v; g.v_st = v_st; g.v_sh = v_sh; g.v_sb = v_sb;
+    g.o = o; g.o_st = o_st; g.o_sh = o_sh; g.o_sb = o_sb;
+    g.k_lengths = k_lengths; g.q_lengths = q_lengths; g.part = nullptr;
+    g.B = B; g.H = H; g.Hk = Hk; g.Dk = Dk; g.Dv = Dv; g.L = L; g.Lk = Lk;
+    g.causal = causal ? 1 : 0; g.n_split = 1; g.split_keys = Lk;
+    g.scale = 1.0f / sqrtf((float)Dk);
+    return hip_status(timed(VM_K_PREFILL, S(st), [&] { return vm::launch_attn_any(g, S(st)); }),
+                      "attention");
+  }
+  const int64_t kv_st = k_st, kv_sh = k_sh, kv_sb = k_sb;
   vm::PrefillArgs a{};
   a.q = q; a.q_st = q_st; a.q_sh = q_sh; a.q_sb = q_sb;
   a.k = k; a.v = v; a.kv_st = kv_st; a.kv_sh = kv_sh; a.kv_sb = kv_sb;

@@ -84,7 +84,8 @@ def qnorm_rope_(Q, QW, Cos, Sin, *, positions, eps, offset):
 
     src/kernels/qknorm_rope_append.jl:100-117. Q :: (D, Hq, B) (may be a strided
     view of the packed projection), QW :: (D,), Cos/Sin :: (HALF_ROT, Ctx),
-    positions :: (B,) int32, 1-based column = rope column.
+    positions :: (B,) int32, 1-based column = rope column. D: a power of two
+    from 16 to 512.
     """
     d = sizes(Q=(Q, "D Hq B"), QW=(QW, "D"), Cos=(Cos, "HALF_ROT Ctx"),
               Sin=(Sin, "HALF_ROT Ctx"), positions=(positions, "B"))
@@ -103,8 +104,10 @@ def qnorm_rope_(Q, QW, Cos, Sin, *, positions, eps, offset):
 def knorm_rope_append_(K_cache, V_cache, K_raw, V_raw, KW, Cos, Sin, *, positions, eps, offset):
     """K norm + RoPE written into K_cache at column positions[b]; V copied alongside.
 
-    src/kernels/qknorm_rope_append.jl:119-141. K_cache/V_cache :: (D, Ctx, Hk, B),
-    K_raw/V_raw :: (D, Hk, B) (views of the packed projection), KW :: (D,).
+    src/kernels/qknorm_rope_append.jl:119-141. K_cache :: (Dk, Ctx, Hk, B),
+    V_cache :: (Dv, Ctx, Hk, B), K_raw :: (Dk, Hk, B), V_raw :: (Dv, Hk, B)
+    (views of the packed projection), KW :: (Dk,). Dk, Dv: powers of two from
+    16 to 512.
     """
     d = sizes(K_cache=(K_cache, "Dk Ctx Hk B"), V_cache=(V_cache, "Dv Ctx Hk B"),
               K_raw=(K_raw, "Dk Hk B"), V_raw=(V_raw, "Dv Hk B"), KW=(KW, "Dk"),
@@ -114,14 +117,11 @@ def knorm_rope_append_(K_cache, V_cache, K_raw, V_raw, KW, Cos, Sin, *, position
         _need(t, torch.bfloat16, n)
     _need(positions, torch.int32, "positions")
     _need_contig(Cos, "Cos"); _need_contig(Sin, "Sin")
-    if K_cache.stride() != V_cache.stride() or K_raw.stride() != V_raw.stride():
-        raise ArgumentError("K and V operands must share strides")
-    if d["Dk"] != d["Dv"]:
-        raise ArgumentError("Dk != Dv is not supported")
-    call("vm_knorm_rope_append", _p(K_cache), _p(V_cache), K_cache.stride(2), K_cache.stride(1),
-         K_cache.stride(0), d["Ctx"], _p(K_raw), _p(V_raw), K_raw.stride(1), K_raw.stride(0),
-         _p(KW), _p(Cos), _p(Sin), _p(positions), d["B"], d["Hk"], d["Dk"], d["HALF_ROT"],
-         float(eps), float(offset), _stream())
+    call("vm_knorm_rope_append", _p(K_cache), K_cache.stride(2), K_cache.stride(1),
+         K_cache.stride(0), _p(V_cache), V_cache.stride(2), V_cache.stride(1), V_cache.stride(0),
+         d["Ctx"], _p(K_raw), K_raw.stride(1), K_raw.stride(0), _p(V_raw), V_raw.stride(1),
+         V_raw.stride(0), _p(KW), _p(Cos), _p(Sin), _p(positions), d["B"], d["Hk"], d["Dk"],
+         d["Dv"], d["HALF_ROT"], float(eps), float(offset), _stream())
 
 
 def _out(outs, key="O"):
@@ -145,12 +145,10 @@ def attention_(outs, Q, K, V, *, causal=False, k_lengths=None, q_lengths=None):
     for t, n in ((Q, "Q"), (K, "K"), (V, "V"), (O, "O")):
         _need(t, torch.bfloat16, n)
     _need(k_lengths, torch.int32, "k_lengths"); _need(q_lengths, torch.int32, "q_lengths")
-    if K.stride() != V.stride():
-        raise ArgumentError("K and V must share strides")
     call("vm_attention_fwd", _p(O), O.stride(2), O.stride(1), O.stride(0), _p(Q), Q.stride(2),
-         Q.stride(1), Q.stride(0), _p(K), _p(V), K.stride(2), K.stride(1), K.stride(0),
-         _p(k_lengths), _p(q_lengths), d["B"], d["H"], d["Hk"], d["Dk"], d["L"], d["Lk"],
-         int(bool(causal)), _stream())
+         Q.stride(1), Q.stride(0), _p(K), K.stride(2), K.stride(1), K.stride(0), _p(V),
+         V.stride(2), V.stride(1), V.stride(0), _p(k_lengths), _p(q_lengths), d["B"], d["H"],
+         d["Hk"], d["Dk"], d["Dv"], d["L"], d["Lk"], int(bool(causal)), _stream())
     return outs
 
 
@@ -161,11 +159,13 @@ def attention(Q, K, V, **kw) -> dict:
     return attention_({"O": O}, Q, K, V, **kw)
 
 
-def decode_scratch_bytes(Q, K, *, n_splits=0) -> int:
-    """Scratch the split-KV decode needs (Pol.scratch, attention_decode.jl:186-197)."""
-    B, H, D = Q.shape
+def decode_scratch_bytes(Q, K, V=None, *, n_splits=0) -> int:
+    """Scratch the split-KV decode needs (Pol.scratch, attention_decode.jl:186-197);
+    V (default: K) gives Dv."""
+    B, H, _ = Q.shape
     Hk, L = K.shape[1], K.shape[2]
-    return int(_lib.load().vm_decode_scratch_bytes(B, H, Hk, D, L, int(n_splits)))
+    Dv = (K if V is None else V).shape[3]
+    return int(_lib.load().vm_decode_scratch_bytes(B, H, Hk, Dv, L, int(n_splits)))
 
 
 def decode_attention_(outs, Q, K, V, *, lengths, n_splits=0, scratch=None):
@@ -187,14 +187,13 @@ def decode_attention_(outs, Q, K, V, *, lengths, n_splits=0, scratch=None):
     for t, n in ((Q, "Q"), (K, "K"), (V, "V"), (O, "O")):
         _need(t, torch.bfloat16, n)
     _need(lengths, torch.int32, "lengths")
-    if K.stride() != V.stride():
-        raise ArgumentError("K and V must share strides")
-    need = decode_scratch_bytes(Q, K, n_splits=n_splits)
+    need = decode_scratch_bytes(Q, K, V, n_splits=n_splits)
     if scratch is None:
         scratch = torch.empty(max(need, 16), dtype=torch.uint8, device=Q.device)
     call("vm_decode_attention", _p(O), O.stride(1), O.stride(0), _p(Q), Q.stride(1), Q.stride(0),
-         _p(K), _p(V), K.stride(2), K.stride(1), K.stride(0), d["L"], _p(lengths), d["Batch"],
-         d["H"], d["Hk"], d["Dk"], int(n_splits), _p(scratch), scratch.numel(), _stream())
+         _p(K), K.stride(2), K.stride(1), K.stride(0), _p(V), V.stride(2), V.stride(1),
+         V.stride(0), d["L"], _p(lengths), d["Batch"], d["H"], d["Hk"], d["Dk"], d["Dv"],
+         int(n_splits), _p(scratch), scratch.numel(), _stream())
     return outs
 
 
