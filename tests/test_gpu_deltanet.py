@@ -450,8 +450,9 @@ def test_prep_many_value_heads(vm, orc):
 
 
 def test_shape_errors(vm):
-    """The reference's DimensionMismatch on Hv % Hk, and head sizes the kernels
-    are not built for; checked before any launch."""
+    """The reference's DimensionMismatch on Hv % Hk, and head sizes no kernel
+    takes (Dk a multiple of 16 up to 256, deltanet_recurrent.jl:86 tiles by 16);
+    checked before any launch."""
     banner("deltanet shape errors")
     B = 1
     S = torch.zeros((B, 6, DV, DK), dtype=torch.float32, device="cuda")
@@ -460,12 +461,13 @@ def test_shape_errors(vm):
     g = torch.zeros((B, 6), dtype=torch.float32, device="cuda")
     with pytest.raises(vm.DimensionMismatch):
         vm.deltanet_recurrent_decode(q, q, v, g, g, S)
-    S64 = torch.zeros((B, 2, 64, 64), dtype=torch.float32, device="cuda")
-    q64 = torch.zeros((B, 1, 64), dtype=torch.float32, device="cuda")
-    v64 = torch.zeros((B, 2, 64), dtype=torch.float32, device="cuda")
     g2 = torch.zeros((B, 2), dtype=torch.float32, device="cuda")
-    with pytest.raises(vm.UnsupportedShape):
-        vm.deltanet_recurrent_decode(q64, q64, v64, g2, g2, S64)
+    for dk in (24, 320):
+        Sx = torch.zeros((B, 2, 64, dk), dtype=torch.float32, device="cuda")
+        qx = torch.zeros((B, 1, dk), dtype=torch.float32, device="cuda")
+        vx = torch.zeros((B, 2, 64), dtype=torch.float32, device="cuda")
+        with pytest.raises(vm.UnsupportedShape):
+            vm.deltanet_recurrent_decode(qx, qx, vx, g2, g2, Sx)
 
 
 @pytest.mark.parametrize("B,T", [(1, 1), (1, 63), (1, 64), (2, 65), (1, 200), (17, 70),

@@ -3,8 +3,11 @@ vs the CPU oracle: qnorm_rope! and knorm_rope_append!
 (src/kernels/qknorm_rope_append.jl:100-141) at power-of-two head dims 16..512
 and other rotary widths, attention! (src/kernels/attention.jl:93-129) and
 decode_attention! (src/kernels/attention_decode.jl:134-200) at Dk != Dv, other
-head dims and GQA groups above 8. The oracle is pinned at these shapes by
-tests/test_oracle.py (torch rms_norm + complex rotation, SDPA).
+head dims and GQA groups above 8; fused_deltanet_decode!, deltanet_sequence! and
+deltanet_recurrent_decode! (deltanet_fused.jl, deltanet_recurrent.jl) at Dk, Dv
+other than 128. The oracle is pinned at these shapes by tests/test_oracle.py
+(torch rms_norm + complex rotation, SDPA) and tests/test_oracle_deltanet.py
+(the float64 product form at Dk, Dv = 16, 24, 32, 8, 12).
 
 Bar: the north-star parity bar on bf16 outputs (max-abs 2e-2, mean-abs 2e-3);
 cache columns and rows that must not be written are compared bit for bit."""
@@ -158,3 +161,71 @@ def test_decode_splits_agree(vm):
     for o in outs[1:]:
         mx, _ = maxmean(o, outs[0])
         assert mx <= 4e-3
+
+
+# ---------------------------------------------------------------- DeltaNet
+def _f32dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+
+
+@pytest.mark.parametrize("Dk,Dv,Hk,Hv,inplace", [(64, 64, 4, 8, True), (256, 128, 2, 4, False),
+                                                 (128, 256, 2, 2, True), (16, 48, 1, 3, True),
+                                                 (192, 64, 1, 2, False)])
+def test_fused_deltanet_decode_head_dims(vm, orc, Dk, Dv, Hk, Hv, inplace):
+    """fused_deltanet_decode! at head dims other than Dk = Dv = 128
+    (deltanet_fused.jl:109-141 tiles any Dk by 16): the generic kernel against
+    the oracle, state in place or into a new buffer."""
+    from oracle.rng import normal_f32
+    banner(f"fused_deltanet_decode Dk={Dk} Dv={Dv} Hk={Hk} Hv={Hv} inplace={inplace}")
+    B = 3
+    q, k = normal_bf16((B, Hk, Dk), 450), normal_bf16((B, Hk, Dk), 451)
+    v, z = normal_bf16((B, Hv, Dv), 452), normal_bf16((B, Hv, Dv), 453)
+    ab = normal_bf16((B, 2 * Hv), 454)
+    a_log, dt_bias = normal_f32(Hv, 455, scale=0.5), normal_f32(Hv, 456, scale=0.5)
+    norm_w = normal_bf16((Dv,), 457, scale=0.2, shift=1.0)
+    s = normal_f32(B * Hv * Dv * Dk, 458, scale=0.05).reshape(B, Hv, Dv, Dk)
+    o_ref, s_ref = orc.fused_deltanet_decode(q, k, v, ab[:, :Hv], ab[:, Hv:], z, a_log, dt_bias,
+                                             norm_w, s, eps=EPS)
+    AB = to_dev(ab)
+    S = _f32dev(s)
+    out = vm.fused_deltanet_decode(to_dev(q), to_dev(k), to_dev(v), AB[:, :Hv], AB[:, Hv:],
+                                   to_dev(z), _f32dev(a_log), _f32dev(dt_bias), to_dev(norm_w), S,
+                                   eps=EPS, Sp=S if inplace else None)
+    torch.cuda.synchronize()
+    s_got = (S if inplace else out["Sp"]).cpu().numpy()
+    np.testing.assert_allclose(s_got, s_ref, rtol=2e-5, atol=2e-6)
+    got = dev_f32(out["O"])
+    bar = 2.0 ** -8 * np.abs(o_ref) + 1e-5
+    assert np.max(np.abs(got - o_ref) / bar) <= 1.0
+
+
+@pytest.mark.parametrize("Dk,Dv,Hk,Hv,B,T", [(64, 32, 2, 4, 2, 20), (192, 128, 1, 2, 1, 9),
+                                             (32, 256, 2, 2, 3, 5)])
+def test_deltanet_sequence_head_dims(vm, orc, Dk, Dv, Hk, Hv, B, T):
+    """deltanet_sequence! at other head dims (the generic kernel, state in
+    registers across the T steps), in place; T single steps of
+    deltanet_recurrent_decode! give the same rows."""
+    from oracle.rng import normal_f32
+    banner(f"deltanet_sequence Dk={Dk} Dv={Dv} Hk={Hk} Hv={Hv} B={B} T={T}")
+    cv = normal_bf16((B, T, 2 * Hk * Dk + Hv * Dv), 460)
+    ab = normal_bf16((B, T, 2 * Hv), 461)
+    a_log, dt_bias = normal_f32(Hv, 462, scale=0.5), normal_f32(Hv, 463, scale=0.5)
+    p = orc.deltanet_prep(cv, ab, a_log, dt_bias, Dk=Dk, Dv=Dv, Hk=Hk, Hv=Hv)
+    s = normal_f32(B * Hv * Dv * Dk, 464, scale=0.05).reshape(B, Hv, Dv, Dk)
+    o_ref, s_ref = orc.deltanet_sequence(p["q"], p["k"], p["v"], p["beta"], p["gate"], s)
+    S = _f32dev(s)
+    qd, kd, vd = _f32dev(p["q"]), _f32dev(p["k"]), _f32dev(p["v"])
+    bd, gd = _f32dev(p["beta"]), _f32dev(p["gate"])
+    out = vm.deltanet_sequence(qd, kd, vd, bd, gd, S, Sp=S)
+    S2 = _f32dev(s)
+    rows = []
+    for t in range(T):
+        r = vm.deltanet_recurrent_decode(qd[:, :, t].contiguous(), kd[:, :, t].contiguous(),
+                                         vd[:, :, t].contiguous(), bd[:, t].contiguous(),
+                                         gd[:, t].contiguous(), S2, Sp=S2)
+        rows.append(r["O"])
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(S.cpu().numpy(), s_ref, rtol=5e-4, atol=5e-5)
+    np.testing.assert_allclose(out["O"].cpu().numpy(), o_ref, rtol=5e-4, atol=5e-5)
+    assert torch.equal(S2, S)
+    assert torch.equal(torch.stack(rows, 2), out["O"])

@@ -96,6 +96,10 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// silu and sigmoid with the full-precision exp (the DeltaNet gates and norms)
+__device__ __forceinline__ float accurate_silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float accurate_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
 __device__ __forceinline__ float wave_max_xor(float v, int mask) {
   return fmaxf(v, __shfl_xor(v, mask, 64));
 }

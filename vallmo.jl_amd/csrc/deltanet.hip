@@ -27,9 +27,6 @@ namespace {
 
 constexpr int DN_D = 128;  // Dk = Dv (Qwen3.5: deltanet.jl:12, qwen35.jl:19)
 
-__device__ __forceinline__ float accurate_silu(float x) { return x / (1.0f + expf(-x)); }
-__device__ __forceinline__ float accurate_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
-
 // v[l ^ M] within each 32-lane half: DPP quad permutes for M = 1, 2, the
 // swizzle unit's bitmask mode (and 0x1f, xor M) for M = 4, 8, 16.
 template <int M>

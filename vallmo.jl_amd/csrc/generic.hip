@@ -7,6 +7,8 @@
 // shape (D = 256, a 64-dim rotary part, groups up to 8); these take every other
 // shape the reference's operators take. fp32 arithmetic on bf16 operands staged
 // in LDS, one workgroup per 16 query rows: correct at any shape, not tuned.
+// Likewise the DeltaNet operators (fused decode, recurrent decode, sequence)
+// for Dk, Dv multiples of 16 up to 256 beside the tuned Dk = Dv = 128 kernels.
 #include <algorithm>
 
 #include "common.h"
@@ -233,6 +235,163 @@ __global__ __launch_bounds__(256) void attn_any_combine_kernel(AttnAnyArgs a) {
   }
 }
 
+// ---- the DeltaNet operators at head dims outside the tuned kernels (Dk, Dv
+// multiples of 16 up to 256; src/kernels/deltanet_fused.jl:109-141,
+// deltanet_recurrent.jl:72-198 tile any Dk by 16). One workgroup of 16 waves
+// per (value head, sequence): wave w owns value columns j0 .. j0 + nc - 1 (j0 =
+// w nc, nc = Dv / 16) and keeps their state in registers, lane l rows l + 64 e.
+// Per column: S *= decay, delta = beta (v - S^T k), S += k delta^T, o = S^T q
+// (the reference's two passes in one: every state element is read and written
+// once per step).
+namespace {
+
+constexpr int DN_NC = 16;  // columns per wave at Dv = 256
+
+template <int KE>
+__device__ __forceinline__ void dn_any_load(float (&s)[DN_NC][KE], const float* base, int Dk,
+                                            int j0, int nc, int lane) {
+#pragma unroll
+  for (int c = 0; c < DN_NC; ++c) {
+#pragma unroll
+    for (int e = 0; e < KE; ++e) {
+      const int i = lane + 64 * e;
+      s[c][e] = c < nc && i < Dk ? base[(int64_t)(j0 + c) * Dk + i] : 0.f;
+    }
+  }
+}
+template <int KE>
+__device__ __forceinline__ void dn_any_store(const float (&s)[DN_NC][KE], float* base, int Dk,
+                                             int j0, int nc, int lane) {
+#pragma unroll
+  for (int c = 0; c < DN_NC; ++c) {
+#pragma unroll
+    for (int e = 0; e < KE; ++e) {
+      const int i = lane + 64 * e;
+      if (c < nc && i < Dk) base[(int64_t)(j0 + c) * Dk + i] = s[c][e];
+    }
+  }
+}
+// one delta step on the wave's columns; vv: lane c holds v of column j0 + c;
+// o[c] (every lane) the column's output
+template <int KE>
+__device__ __forceinline__ void dn_any_step(float (&s)[DN_NC][KE], const float (&k)[KE],
+                                            const float (&q)[KE], float vv, float decay,
+                                            float beta, int nc, float (&o)[DN_NC]) {
+#pragma unroll
+  for (int c = 0; c < DN_NC; ++c) {
+    if (c >= nc) continue;  // wave-uniform
+    float ks = 0.f;
+#pragma unroll
+    for (int e = 0; e < KE; ++e) {
+      s[c][e] *= decay;
+      ks = fmaf(s[c][e], k[e], ks);
+    }
+    ks = wave_sum_all(ks);
+    const float delta = beta * (__shfl(vv, c, 64) - ks);
+    float os = 0.f;
+#pragma unroll
+    for (int e = 0; e < KE; ++e) {
+      s[c][e] = fmaf(k[e], delta, s[c][e]);
+      os = fmaf(s[c][e], q[e], os);
+    }
+    o[c] = wave_sum_all(os);
+  }
+}
+// lane c's copy of o[c] (registers are not indexable by lane)
+__device__ __forceinline__ float dn_pick(const float (&o)[DN_NC], int lane) {
+  float r = 0.f;
+#pragma unroll
+  for (int c = 0; c < DN_NC; ++c) r = lane == c ? o[c] : r;
+  return r;
+}
+
+}  // namespace
+
+// deltanet_sequence! and, at T = 1, deltanet_recurrent_decode!: fp32 inputs
+// already normed and gated (decay = exp(gate)), the state carried in registers
+template <int KE>
+__global__ __launch_bounds__(1024) void deltanet_any_seq_kernel(DeltaSeqArgs a, int Dk, int Dv) {
+  const int hv = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nc = Dv / 16, j0 = w * nc;
+  const int hk = hv / (a.Hv / a.Hk);
+  const int64_t sb = ((int64_t)b * a.Hv + hv) * Dv * Dk;
+  float s[DN_NC][KE], o[DN_NC];
+  dn_any_load<KE>(s, a.s_in + sb, Dk, j0, nc, lane);
+  for (int t = 0; t < a.T; ++t) {
+    const int64_t qk = (((int64_t)b * a.Hk + hk) * a.T + t) * Dk;
+    const int64_t vo = (((int64_t)b * a.Hv + hv) * a.T + t) * Dv;
+    const int64_t g = ((int64_t)b * a.T + t) * a.Hv + hv;
+    float q[KE], k[KE];
+#pragma unroll
+    for (int e = 0; e < KE; ++e) {
+      const int i = lane + 64 * e;
+      q[e] = i < Dk ? a.q[qk + i] : 0.f;
+      k[e] = i < Dk ? a.k[qk + i] : 0.f;
+    }
+    const float vv = lane < nc ? a.v[vo + j0 + lane] : 0.f;
+    dn_any_step<KE>(s, k, q, vv, expf(a.gate[g]), a.beta[g], nc, o);
+    if (lane < nc) a.o[vo + j0 + lane] = dn_pick(o, lane);
+  }
+  dn_any_store<KE>(s, a.s_out + sb, Dk, j0, nc, lane);
+}
+
+// fused_deltanet_decode!: raw bf16 q, k (l2-normed here, q also by 1/sqrt(Dk)),
+// the gates from alpha and beta_raw, then the gated RMSNorm with silu(z)
+// (deltanet_fused.jl:27-105)
+template <int KE>
+__global__ __launch_bounds__(1024) void deltanet_any_fused_kernel(DeltaFusedArgs a, int Dk, int Dv) {
+  const int hv = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nc = Dv / 16, j0 = w * nc;
+  const int hk = hv / (a.Hv / a.Hk);
+  const int64_t sb = ((int64_t)b * a.Hv + hv) * Dv * Dk;
+  float s[DN_NC][KE], o[DN_NC];
+  dn_any_load<KE>(s, a.s_in + sb, Dk, j0, nc, lane);
+  float q[KE], k[KE], qss = 0.f, kss = 0.f;
+#pragma unroll
+  for (int e = 0; e < KE; ++e) {
+    const int i = lane + 64 * e;
+    q[e] = i < Dk ? bfv(a.q[b * a.q_sb + (int64_t)hk * Dk + i]) : 0.f;
+    k[e] = i < Dk ? bfv(a.k[b * a.k_sb + (int64_t)hk * Dk + i]) : 0.f;
+    qss = fmaf(q[e], q[e], qss);
+    kss = fmaf(k[e], k[e], kss);
+  }
+  qss = wave_sum_all(qss);
+  kss = wave_sum_all(kss);
+  const float qsc = 1.0f / sqrtf(qss + 1e-6f) / sqrtf((float)Dk);
+  const float ksc = 1.0f / sqrtf(kss + 1e-6f);
+#pragma unroll
+  for (int e = 0; e < KE; ++e) {
+    q[e] *= qsc;
+    k[e] *= ksc;
+  }
+  const float spi = bfv(a.alpha[b * a.a_sb + hv]) + a.dt_bias[hv];
+  const float sp = spi > 20.0f ? spi : logf(1.0f + expf(spi));
+  const float decay = expf(-expf(a.a_log[hv]) * sp);
+  const float beta = accurate_sigmoid(bfv(a.beta[b * a.b_sb + hv]));
+  const float vv = lane < nc ? bfv(a.v[b * a.v_sb + (int64_t)hv * Dv + j0 + lane]) : 0.f;
+  dn_any_step<KE>(s, k, q, vv, decay, beta, nc, o);
+  dn_any_store<KE>(s, a.s_out + sb, Dk, j0, nc, lane);
+  // gated RMSNorm over the Dv columns
+  __shared__ float red[16];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < DN_NC; ++c)
+    if (c < nc) ss = fmaf(o[c], o[c], ss);
+  if (lane == 0) red[w] = ss;
+  __syncthreads();
+  float tot = 0.f;
+  for (int i = 0; i < 16; ++i) tot += red[i];
+  const float rstd = 1.0f / sqrtf(tot / (float)Dv + a.eps);
+  if (lane < nc) {
+    const int j = j0 + lane;
+    const float z = bfv(a.z[b * a.z_sb + (int64_t)hv * Dv + j]);
+    a.o[b * a.o_sb + (int64_t)hv * Dv + j] =
+        f2bf(dn_pick(o, lane) * rstd * bfv(a.norm_w[j]) * accurate_silu(z));
+  }
+}
+
 // ---- launchers ---------------------------------------------------------------
 hipError_t launch_norm_rope_any(const RowAnyArgs& a, hipStream_t st) {
   const int64_t rows = (int64_t)a.B * a.H;
@@ -297,6 +456,25 @@ hipError_t launch_attn_any(const AttnAnyArgs& a, hipStream_t st) {
   }
   if (e != hipSuccess || a.part == nullptr) return e;
   hipLaunchKernelGGL(attn_any_combine_kernel, dim3((unsigned)(a.B * a.H)), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_deltanet_any(const DeltaSeqArgs* seq, const DeltaFusedArgs* fused, int Dk,
+                               int Dv, hipStream_t st) {
+  const int B = seq ? seq->B : fused->B, Hv = seq ? seq->Hv : fused->Hv;
+  if (B == 0) return hipSuccess;
+  const dim3 grid((unsigned)Hv, (unsigned)B), block(1024);
+#define DN_ANY(ke)                                                                         \
+  if (seq) hipLaunchKernelGGL(deltanet_any_seq_kernel<ke>, grid, block, 0, st, *seq, Dk, Dv); \
+  else hipLaunchKernelGGL(deltanet_any_fused_kernel<ke>, grid, block, 0, st, *fused, Dk, Dv);
+  switch ((Dk + 63) / 64) {
+    case 1: DN_ANY(1); break;
+    case 2: DN_ANY(2); break;
+    case 3: DN_ANY(3); break;
+    case 4: DN_ANY(4); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef DN_ANY
   return hipGetLastError();
 }
 

@@ -371,6 +371,10 @@ struct DeltaSeqArgs {
   float* s_out;
   int T, Hk, Hv, B;
 };
+// the generic forms (generic.hip): Dk, Dv multiples of 16 up to 256; one of
+// seq (deltanet_sequence! / recurrent decode) or fused (fused_deltanet_decode!)
+hipError_t launch_deltanet_any(const DeltaSeqArgs* seq, const DeltaFusedArgs* fused, int Dk,
+                               int Dv, hipStream_t st);
 // the prefill's prep: conv output cv (2 Hk Dk + Hv Dv channels, token stride
 // cv_st, sequence stride cv_sb), ab (alpha | beta, 2 Hv rows, ab_st, ab_sb) ->
 // qe, ke (Dk, T, Hk, B), ve (Dv, T, Hv, B), beta, gate (Hv, T, B) fp32.

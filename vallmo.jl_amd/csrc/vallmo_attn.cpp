@@ -927,6 +927,16 @@ int check_dn_heads(int Dk, int Dv, int Hk, int Hv, int B, const char* what) {
   REQUIRE(Hv % Hk == 0, VM_E_DIM, "value heads (%d) is not a multiple of key heads (%d)", Hv, Hk);
   return VM_OK;
 }
+// the operators' generic forms: Dk, Dv multiples of 16 up to 256
+int check_dn_heads_any(int Dk, int Dv, int Hk, int Hv, int B, const char* what) {
+  REQUIRE(Dk >= 16 && Dk <= 256 && Dk % 16 == 0 && Dv >= 16 && Dv <= 256 && Dv % 16 == 0,
+          VM_E_UNSUPPORTED, "%s: Dk = %d, Dv = %d (multiples of 16 up to 256)", what, Dk, Dv);
+  REQUIRE(Hk > 0 && Hv > 0 && B >= 0, VM_E_ARG, "%s: Hk = %d, Hv = %d, B = %d", what, Hk, Hv, B);
+  REQUIRE(Hv % Hk == 0, VM_E_DIM, "value heads (%d) is not a multiple of key heads (%d)", Hv, Hk);
+  REQUIRE((int64_t)B <= 65535, VM_E_UNSUPPORTED, "%s: B = %d > 65535", what, B);
+  return VM_OK;
+}
+bool dn_tuned(int Dk, int Dv) { return Dk == 128 && Dv == 128; }
 // the state out either is the state in (in place) or does not overlap it
 int check_alias(const void* in, const void* out, size_t bytes, const char* what) {
   const uintptr_t a = reinterpret_cast<uintptr_t>(in), b = reinterpret_cast<uintptr_t>(out);
@@ -1012,7 +1022,7 @@ int vm_fused_deltanet_decode(vm_bf16* o, int64_t o_sb, const vm_bf16* q, int64_t
                              const float* dt_bias, const vm_bf16* norm_w, const float* s_in,
                              float* s_out, int Dk, int Dv, int Hk, int Hv, int B, float eps,
                              vm_stream st) {
-  TRY(check_dn_heads(Dk, Dv, Hk, Hv, B, "fused_deltanet_decode"));
+  TRY(check_dn_heads_any(Dk, Dv, Hk, Hv, B, "fused_deltanet_decode"));
   if (B == 0) return VM_OK;
   REQUIRE(o && v && z && alpha && beta_raw && a_log && dt_bias && norm_w, VM_E_ARG,
           "fused_deltanet_decode: NULL pointer argument");
@@ -1031,6 +1041,10 @@ int vm_fused_deltanet_decode(vm_bf16* o, int64_t o_sb, const vm_bf16* q, int64_t
   a.z = z; a.z_sb = z_sb; a.alpha = alpha; a.a_sb = a_sb; a.beta = beta_raw; a.b_sb = b_sb;
   a.a_log = a_log; a.dt_bias = dt_bias; a.norm_w = norm_w; a.s_in = s_in; a.s_out = s_out;
   a.Hk = Hk; a.Hv = Hv; a.B = B; a.eps = eps;
+  if (!dn_tuned(Dk, Dv))
+    return hip_status(timed(VM_K_DELTANET, S(st),
+                            [&] { return vm::launch_deltanet_any(nullptr, &a, Dk, Dv, S(st)); }),
+                      "fused_deltanet_decode");
   return hip_status(
       timed(VM_K_DELTANET, S(st), [&] { return vm::launch_deltanet_fused_decode(a, S(st)); }),
       "fused_deltanet_decode");
@@ -1040,7 +1054,7 @@ static int deltanet_seq(float* o, const float* q, const float* k, const float* v
                         const float* beta, const float* gate, const float* s_in, float* s_out,
                         int Dk, int Dv, int T, int Hk, int Hv, int B, vm_stream st,
                         const char* what) {
-  TRY(check_dn_heads(Dk, Dv, Hk, Hv, B, what));
+  TRY(check_dn_heads_any(Dk, Dv, Hk, Hv, B, what));
   REQUIRE(T >= 0, VM_E_ARG, "%s: T = %d", what, T);
   if (B == 0) return VM_OK;
   TRY(check_aligned(s_in, "S"));
@@ -1056,6 +1070,10 @@ static int deltanet_seq(float* o, const float* q, const float* k, const float* v
   vm::DeltaSeqArgs a{};
   a.o = o; a.q = q; a.k = k; a.v = v; a.beta = beta; a.gate = gate; a.s_in = s_in;
   a.s_out = s_out; a.T = T; a.Hk = Hk; a.Hv = Hv; a.B = B;
+  if (!dn_tuned(Dk, Dv))
+    return hip_status(timed(VM_K_DELTANET, S(st),
+                            [&] { return vm::launch_deltanet_any(&a, nullptr, Dk, Dv, S(st)); }),
+                      what);
   return hip_status(
       timed(VM_K_DELTANET, S(st), [&] { return vm::launch_deltanet_sequence(a, S(st)); }), what);
 }
