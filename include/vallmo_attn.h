@@ -148,8 +148,8 @@ int vm_knorm_rope_append(vm_bf16* k_cache, int64_t kc_st, int64_t kc_sh, int64_t
  * in whole 256-byte blocks) that the merge reads instead of lengths.
  *
  * Other shapes run a generic kernel with the reference's split: n_splits
- * tile-aligned key ranges per (b, hk) (n_splits = 0: about two workgroups
- * per CU, at least 256 keys each), partials (Dv values, max, sum) per split,
+ * tile-aligned key ranges per (b, hk) (n_splits = 0: about four workgroups
+ * per CU, at least 128 keys each), partials (Dv values, max, sum) per split,
  * sequence and head, merged in split order.
  *
  * Size scratch with vm_decode_scratch_bytes(B, H, Hk, Dv, ctx, n_splits)

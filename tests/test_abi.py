@@ -121,12 +121,12 @@ def test_decode_scratch_size_and_shortfall(vm):
 def test_generic_decode_scratch(vm):
     """Shapes outside the tuned decode (here Dv = 128, a group of 16) size one
     (Dv + 2)-float partial row per split, sequence and head: n_splits per (b,
-    kv head) as given, or about two workgroups per CU for 0 (at least 256 keys
+    kv head) as given, or about four workgroups per CU for 0 (at least 128 keys
     per split); a short scratch is refused before any launch."""
     lib = vm._lib.load()
     assert lib.vm_decode_scratch_bytes(2, 16, 1, 128, 4096, 8) == -(-8 * 2 * 16 * 130 * 4 // 256) * 256
-    # n_splits = 0: 512 / (B Hk) = 256 workgroups' worth, capped at ctx / 256 = 16 splits
-    assert lib.vm_decode_scratch_bytes(2, 16, 1, 128, 4096, 0) == -(-16 * 2 * 16 * 130 * 4 // 256) * 256
+    # n_splits = 0: 1024 / (B Hk) = 512 splits' worth, capped at ctx / 128 = 32 splits
+    assert lib.vm_decode_scratch_bytes(2, 16, 1, 128, 4096, 0) == -(-32 * 2 * 16 * 130 * 4 // 256) * 256
     assert lib.vm_decode_scratch_bytes(1, 16, 4, 96, 512, 0) == 0  # not a power of two
     rc = lib.vm_decode_attention(_p(FAKE), 128, 2048, _p(FAKE), 128, 2048, _p(FAKE), 128,
                                  128 * 512, 128 * 512, _p(FAKE), 128, 128 * 512, 128 * 512, 512,

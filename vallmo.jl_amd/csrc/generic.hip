@@ -416,8 +416,8 @@ int attn_any_splits(int B, int H, int Hk, int64_t ctx, int n_splits) {
   if (n_splits > 0) return n_splits;  // the reference's fixed split count
   const int G = H / Hk;
   const int64_t blocks = (int64_t)B * Hk * ((G + AQ - 1) / AQ);
-  int64_t s = (512 + blocks - 1) / blocks;  // about two workgroups per CU
-  s = std::min<int64_t>(s, (ctx + 255) / 256);  // at least 256 keys per split
+  int64_t s = (1024 + blocks - 1) / blocks;  // about four workgroups per CU
+  s = std::min<int64_t>(s, (ctx + 127) / 128);  // at least 128 keys per split
   return (int)std::max<int64_t>(1, s);
 }
 
