@@ -6,7 +6,7 @@
 // kernels (rows.hip, prefill.hip, decode.hip) are built for Qwen3.5's head
 // shape (D = 256, a 64-dim rotary part, groups up to 8); these take every other
 // shape the reference's operators take. fp32 arithmetic on bf16 operands staged
-// in LDS, one workgroup per 16 query rows: correct at any shape, not tuned.
+// in LDS, one workgroup per 4 or 16 query rows: correct at any shape, not tuned.
 // Likewise the DeltaNet operators (fused decode, recurrent decode, sequence)
 // for Dk, Dv multiples of 16 up to 256 beside the tuned Dk = Dv = 128 kernels.
 #include <algorithm>
@@ -22,7 +22,6 @@ __device__ __forceinline__ float bfv(uint16_t u) { return __uint_as_float((uint3
 __device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 
-constexpr int AQ = 16;  // query rows per workgroup: 16 threads per row
 constexpr int AK = 32;  // keys per staged tile
 
 }  // namespace
@@ -80,26 +79,33 @@ __global__ __launch_bounds__(256) void norm_rope_any_kernel(RowAnyArgs a) {
 
 // ---- attention over staged tiles. Workgroup (row block, (b, kv head), split):
 // rows rho = g L + t enumerate the group's G query heads x L queries, so the
-// heads of a kv group share every staged K/V tile. Thread (r, c) = (tid / 16,
-// tid % 16) scores keys c and c + 16 of each tile for row r, and owns the
-// output columns c + 16 i of that row. Online softmax per row (max and sum over
-// the row's 16 threads, one 16-lane group of a wave). With part set (decode
-// splits) it writes the unnormalised row, its max and its sum instead.
-template <int DVT>
+// heads of a kv group share every staged K/V tile. A block holds RPB rows of
+// TPR = 256 / RPB threads: RPB = 16 (16 threads per row, each scoring keys c
+// and c + 16 of a 32-key tile over all of Dk) or, where a kv group has at most
+// 4 rows (decode), RPB = 4 (64 threads per row, one wave: key c % 32 over half
+// of Dk, the halves added across the wave). Each thread owns the output
+// columns c + TPR i of its row. Online softmax per row over the row's threads.
+// With part set (decode splits) it writes the unnormalised row, its max and
+// its sum instead.
+template <int RPB, int DVT>
 __global__ __launch_bounds__(256) void attn_any_kernel(AttnAnyArgs a) {
+  constexpr int TPR = 256 / RPB;                 // threads per row
+  constexpr int KPT = TPR >= AK ? 1 : AK / TPR;  // keys scored per thread
+  constexpr int DP = TPR >= AK ? TPR / AK : 1;   // parts of Dk per key
+  constexpr int RX = (TPR < AK ? TPR : AK) / 2;  // first xor of the row reductions
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int Dk = a.Dk, Dv = a.Dv;
   const int qs_st = Dk + 4;  // floats per staged Q row (rows on distinct banks)
-  const int ks_st = Dk + 8;  // bf16 per staged K row (the 16 keys a row group reads: distinct banks)
+  const int ks_st = Dk + 8;  // bf16 per staged K row (the keys a row group reads: distinct banks)
   const int vs_st = Dv + 8;
   float* qs = reinterpret_cast<float*>(smem);
-  uint16_t* ks = reinterpret_cast<uint16_t*>(qs + AQ * qs_st);
+  uint16_t* ks = reinterpret_cast<uint16_t*>(qs + RPB * qs_st);
   uint16_t* vs = ks + AK * ks_st;
-  float* ps = reinterpret_cast<float*>(vs + AK * vs_st);  // [AQ][AK + 1]
+  float* ps = reinterpret_cast<float*>(vs + AK * vs_st);  // [RPB][AK + 1]
   const int G = a.H / a.Hk;
   const int hk = blockIdx.y % a.Hk, b = blockIdx.y / a.Hk, z = blockIdx.z;
-  const int rows = G * a.L, rho0 = blockIdx.x * AQ;
-  const int tid = threadIdx.x, r = tid >> 4, c = tid & 15;
+  const int rows = G * a.L, rho0 = blockIdx.x * RPB;
+  const int tid = threadIdx.x, r = tid / TPR, c = tid % TPR;
   const int k_len = min(a.k_lengths ? a.k_lengths[b] : a.Lk, a.Lk);
   const int q_len = min(a.q_lengths ? a.q_lengths[b] : a.L, a.L);
   const int off = k_len - q_len;  // queries are the suffix of the keys
@@ -109,7 +115,7 @@ __global__ __launch_bounds__(256) void attn_any_kernel(AttnAnyArgs a) {
   const int h = hk * G + g;
   // the block's key range: this split's keys, up to its last row's causal limit
   int tmax = -1;
-  for (int i = 0; i < AQ; ++i) {
+  for (int i = 0; i < RPB; ++i) {
     const int rr = rho0 + i;
     if (rr < rows && rr % a.L < q_len) tmax = max(tmax, rr % a.L);
   }
@@ -119,7 +125,7 @@ __global__ __launch_bounds__(256) void attn_any_kernel(AttnAnyArgs a) {
   if (a.causal) kb1 = min(kb1, max(kb0, off + tmax + 1));
   const int lim = a.causal ? min(kb1 - 1, t + off) : kb1 - 1;  // this row's last key
   // Q rows of the block, fp32
-  for (int i = tid; i < AQ * Dk; i += 256) {
+  for (int i = tid; i < RPB * Dk; i += 256) {
     const int rr = i / Dk, d = i % Dk, q_rho = rho0 + rr;
     float v = 0.f;
     if (q_rho < rows) {
@@ -133,6 +139,11 @@ __global__ __launch_bounds__(256) void attn_any_kernel(AttnAnyArgs a) {
   for (int i = 0; i < DVT; ++i) acc[i] = 0.f;
   const uint16_t* kbase = a.k + b * a.k_sb + (int64_t)hk * a.k_sh;
   const uint16_t* vbase = a.v + b * a.v_sb + (int64_t)hk * a.v_sh;
+  const int key0 = c % AK, dpart = c / AK;    // DP > 1: this thread's key and Dk part
+  // the thread's output columns c + TPR i: Dv is TPR * DVT, or (DVT = 1) less
+  // than TPR, where threads c >= Dv own none (they read column 0, store nothing)
+  const bool col_ok = c < Dv;
+  const int dlen = Dk / DP, dbeg = DP > 1 ? dpart * dlen : 0;
   for (int j0 = kb0; j0 < kb1; j0 += AK) {
     __syncthreads();  // the previous tile's reads are done (and Q is staged)
     const int kc8 = Dk / 8, vc8 = Dv / 8;
@@ -149,57 +160,78 @@ __global__ __launch_bounds__(256) void attn_any_kernel(AttnAnyArgs a) {
       *reinterpret_cast<uint4*>(vs + key * vs_st + 8 * ch) = u;
     }
     __syncthreads();
-    float s0 = 0.f, s1 = 0.f;
-    const float* qr = qs + r * qs_st;
-    const uint32_t* k0 = reinterpret_cast<const uint32_t*>(ks + c * ks_st);
-    const uint32_t* k1 = reinterpret_cast<const uint32_t*>(ks + (c + 16) * ks_st);
-    for (int d2 = 0; d2 < Dk / 2; ++d2) {
-      const float qa = qr[2 * d2], qb = qr[2 * d2 + 1];
-      const uint32_t u0 = k0[d2], u1 = k1[d2];
-      s0 = fmaf(qa, bf_lo(u0), s0);
-      s0 = fmaf(qb, bf_hi(u0), s0);
-      s1 = fmaf(qa, bf_lo(u1), s1);
-      s1 = fmaf(qb, bf_hi(u1), s1);
-    }
-    s0 = active && j0 + c <= lim ? s0 * a.scale : -INFINITY;
-    s1 = active && j0 + c + 16 <= lim ? s1 * a.scale : -INFINITY;
-    float bm = fmaxf(s0, s1);
+    // scores: keys key0 + TPR x (x < KPT) over dims dbeg .. dbeg + dlen - 1
+    float sc[KPT];
+    const uint32_t* kp[KPT];
+    const float* qr = qs + r * qs_st + dbeg;
 #pragma unroll
-    for (int x = 8; x >= 1; x >>= 1) bm = fmaxf(bm, __shfl_xor(bm, x, 64));
+    for (int x = 0; x < KPT; ++x) {
+      sc[x] = 0.f;
+      kp[x] = reinterpret_cast<const uint32_t*>(ks + (DP > 1 ? key0 : c + TPR * x) * ks_st + dbeg);
+    }
+    for (int d2 = 0; d2 < dlen / 2; ++d2) {
+      const float qa = qr[2 * d2], qb = qr[2 * d2 + 1];  // one q read for the thread's keys
+#pragma unroll
+      for (int x = 0; x < KPT; ++x) {
+        const uint32_t u = kp[x][d2];
+        sc[x] = fmaf(qa, bf_lo(u), sc[x]);
+        sc[x] = fmaf(qb, bf_hi(u), sc[x]);
+      }
+    }
+    if (DP > 1) {
+#pragma unroll
+      for (int x = 0; x < KPT; ++x) sc[x] += __shfl_xor(sc[x], AK, 64);  // the other half of Dk
+    }
+    float bm = -INFINITY;
+#pragma unroll
+    for (int x = 0; x < KPT; ++x) {
+      const int key = DP > 1 ? key0 : c + TPR * x;
+      sc[x] = active && j0 + key <= lim ? sc[x] * a.scale : -INFINITY;
+      bm = fmaxf(bm, sc[x]);
+    }
+#pragma unroll
+    for (int x = RX; x >= 1; x >>= 1) bm = fmaxf(bm, __shfl_xor(bm, x, 64));
     const float mn = fmaxf(m, bm);
-    float corr = 1.f, p0 = 0.f, p1 = 0.f;
-    if (mn != -INFINITY) {
-      corr = expf(m - mn);  // 0 while m is still -inf
-      p0 = expf(s0 - mn);
-      p1 = expf(s1 - mn);
-    }
-    float ls = p0 + p1;
+    float corr = 1.f, ls = 0.f;
 #pragma unroll
-    for (int x = 8; x >= 1; x >>= 1) ls += __shfl_xor(ls, x, 64);
+    for (int x = 0; x < KPT; ++x) {
+      const float p = mn != -INFINITY ? expf(sc[x] - mn) : 0.f;
+      ls += p;
+      sc[x] = p;
+    }
+    if (mn != -INFINITY) corr = expf(m - mn);  // 0 while m is still -inf
+#pragma unroll
+    for (int x = RX; x >= 1; x >>= 1) ls += __shfl_xor(ls, x, 64);
     l = l * corr + ls;
     m = mn;
-    ps[r * (AK + 1) + c] = p0;
-    ps[r * (AK + 1) + c + 16] = p1;
+    if (DP == 1 || dpart == 0) {
+#pragma unroll
+      for (int x = 0; x < KPT; ++x) ps[r * (AK + 1) + (DP > 1 ? key0 : c + TPR * x)] = sc[x];
+    }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < DVT; ++i) acc[i] *= corr;
     for (int kk = 0; kk < AK; ++kk) {
       const float p = ps[r * (AK + 1) + kk];
-      const uint16_t* vr = vs + kk * vs_st + c;
+      const uint16_t* vr = vs + kk * vs_st + (col_ok ? c : 0);
 #pragma unroll
-      for (int i = 0; i < DVT; ++i) acc[i] = fmaf(p, bfv(vr[16 * i]), acc[i]);
+      for (int i = 0; i < DVT; ++i) acc[i] = fmaf(p, bfv(vr[TPR * i]), acc[i]);
     }
   }
   if (!active) return;
   if (a.part == nullptr) {
     const float inv = l > 0.f ? 1.0f / l : 0.f;  // no key: o = 0 (attention.jl:86)
     uint16_t* orow = a.o + b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)t * a.o_st;
+    if (col_ok) {
 #pragma unroll
-    for (int i = 0; i < DVT; ++i) orow[c + 16 * i] = f2bf(acc[i] * inv);
+      for (int i = 0; i < DVT; ++i) orow[c + TPR * i] = f2bf(acc[i] * inv);
+    }
   } else {
     float* pr = a.part + (((int64_t)z * a.B + b) * a.H + h) * (Dv + 2);
+    if (col_ok) {
 #pragma unroll
-    for (int i = 0; i < DVT; ++i) pr[c + 16 * i] = acc[i];
+      for (int i = 0; i < DVT; ++i) pr[c + TPR * i] = acc[i];
+    }
     if (c == 0) {
       pr[Dv] = m;
       pr[Dv + 1] = l;
@@ -407,15 +439,19 @@ hipError_t launch_norm_rope_any(const RowAnyArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-size_t attn_any_lds_bytes(int Dk, int Dv) {
-  return (size_t)AQ * (Dk + 4) * 4 + (size_t)AK * (Dk + 8) * 2 + (size_t)AK * (Dv + 8) * 2 +
-         (size_t)AQ * (AK + 1) * 4;
+// rows per block: 4 where a kv group has at most 4 rows (decode at G <= 4), else 16
+static int attn_any_rpb(const AttnAnyArgs& a) { return (a.H / a.Hk) * a.L <= 4 ? 4 : 16; }
+
+static size_t attn_any_lds(int rpb, int Dk, int Dv) {
+  return (size_t)rpb * (Dk + 4) * 4 + (size_t)AK * (Dk + 8) * 2 + (size_t)AK * (Dv + 8) * 2 +
+         (size_t)rpb * (AK + 1) * 4;
 }
 
 int attn_any_splits(int B, int H, int Hk, int64_t ctx, int n_splits) {
   if (n_splits > 0) return n_splits;  // the reference's fixed split count
   const int G = H / Hk;
-  const int64_t blocks = (int64_t)B * Hk * ((G + AQ - 1) / AQ);
+  const int rpb = G <= 4 ? 4 : 16;  // rows per workgroup at L = 1 (attn_any_rpb)
+  const int64_t blocks = (int64_t)B * Hk * ((G + rpb - 1) / rpb);
   int64_t s = (1024 + blocks - 1) / blocks;  // about four workgroups per CU
   s = std::min<int64_t>(s, (ctx + 127) / 128);  // at least 128 keys per split
   return (int)std::max<int64_t>(1, s);
@@ -427,32 +463,43 @@ int attn_any_split_keys(int64_t ctx, int n_split) {
   return (int)std::max<int64_t>(AK, (per + AK - 1) / AK * AK);
 }
 
-template <int DVT>
+template <int RPB, int DVT>
 static hipError_t launch_attn_any_t(const AttnAnyArgs& a, dim3 grid, size_t lds, hipStream_t st) {
   if (lds > 65536) {  // lift the dynamic-LDS cap of the current device for this kernel
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_any_kernel<DVT>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&attn_any_kernel<RPB, DVT>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(attn_any_kernel<DVT>, grid, dim3(256), lds, st, a);
+  hipLaunchKernelGGL((attn_any_kernel<RPB, DVT>), grid, dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
 hipError_t launch_attn_any(const AttnAnyArgs& a, hipStream_t st) {
   if (a.B == 0 || a.L == 0) return hipSuccess;
-  const int G = a.H / a.Hk;
-  const dim3 grid((unsigned)((G * a.L + AQ - 1) / AQ), (unsigned)(a.Hk * a.B),
+  const int G = a.H / a.Hk, rpb = attn_any_rpb(a);
+  const dim3 grid((unsigned)((G * a.L + rpb - 1) / rpb), (unsigned)(a.Hk * a.B),
                   (unsigned)(a.part ? a.n_split : 1));
-  const size_t lds = attn_any_lds_bytes(a.Dk, a.Dv);
+  const size_t lds = attn_any_lds(rpb, a.Dk, a.Dv);
   hipError_t e;
-  switch (a.Dv / 16) {
-    case 1: e = launch_attn_any_t<1>(a, grid, lds, st); break;
-    case 2: e = launch_attn_any_t<2>(a, grid, lds, st); break;
-    case 4: e = launch_attn_any_t<4>(a, grid, lds, st); break;
-    case 8: e = launch_attn_any_t<8>(a, grid, lds, st); break;
-    case 16: e = launch_attn_any_t<16>(a, grid, lds, st); break;
-    case 32: e = launch_attn_any_t<32>(a, grid, lds, st); break;
-    default: return hipErrorInvalidValue;
+  if (rpb == 16) {
+    switch (a.Dv / 16) {  // DVT = Dv / 16 columns per thread
+      case 1: e = launch_attn_any_t<16, 1>(a, grid, lds, st); break;
+      case 2: e = launch_attn_any_t<16, 2>(a, grid, lds, st); break;
+      case 4: e = launch_attn_any_t<16, 4>(a, grid, lds, st); break;
+      case 8: e = launch_attn_any_t<16, 8>(a, grid, lds, st); break;
+      case 16: e = launch_attn_any_t<16, 16>(a, grid, lds, st); break;
+      case 32: e = launch_attn_any_t<16, 32>(a, grid, lds, st); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (a.Dv <= 64 ? 1 : a.Dv / 64) {  // DVT = ceil(Dv / 64) columns per thread
+      case 1: e = launch_attn_any_t<4, 1>(a, grid, lds, st); break;
+      case 2: e = launch_attn_any_t<4, 2>(a, grid, lds, st); break;
+      case 4: e = launch_attn_any_t<4, 4>(a, grid, lds, st); break;
+      case 8: e = launch_attn_any_t<4, 8>(a, grid, lds, st); break;
+      default: return hipErrorInvalidValue;
+    }
   }
   if (e != hipSuccess || a.part == nullptr) return e;
   hipLaunchKernelGGL(attn_any_combine_kernel, dim3((unsigned)(a.B * a.H)), dim3(256), 0, st, a);

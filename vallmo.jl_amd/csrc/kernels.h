@@ -67,7 +67,6 @@ struct AttnAnyArgs {
   int B, H, Hk, Dk, Dv, L, Lk, causal, n_split, split_keys;
   float scale;
 };
-size_t attn_any_lds_bytes(int Dk, int Dv);
 int attn_any_splits(int B, int H, int Hk, int64_t ctx, int n_splits);
 int attn_any_split_keys(int64_t ctx, int n_split);
 hipError_t launch_attn_any(const AttnAnyArgs& a, hipStream_t st);
