@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void norm_rope_any_kernel(RowAnyArgs a) {
 // columns c + TPR i of its row. Online softmax per row over the row's threads.
 // With part set (decode splits) it writes the unnormalised row, its max and
 // its sum instead.
-template <int RPB, int DVT>
+template <int RPB, int DVT, bool PREF>
 __global__ __launch_bounds__(256) void attn_any_kernel(AttnAnyArgs a) {
   constexpr int TPR = 256 / RPB;                 // threads per row
   constexpr int KPT = TPR >= AK ? 1 : AK / TPR;  // keys scored per thread
@@ -144,20 +144,55 @@ __global__ __launch_bounds__(256) void attn_any_kernel(AttnAnyArgs a) {
   // than TPR, where threads c >= Dv own none (they read column 0, store nothing)
   const bool col_ok = c < Dv;
   const int dlen = Dk / DP, dbeg = DP > 1 ? dpart * dlen : 0;
+  // PREF (decode, bound by its loads): the tiles go through registers, one tile
+  // ahead: thread tid holds 16-byte chunks tid + 256 n of the tile's K (then V)
+  // rows, n < Dk / 64 (Dv / 64). Otherwise each tile is loaded after the
+  // barrier (fewer registers, more workgroups per CU for the products).
+  const int kc8 = Dk / 8, vc8 = Dv / 8;
+  constexpr int NPF = PREF ? 8 : 1;
+  uint4 kr[NPF], vr8[NPF];
+  auto fetch = [&](int j0) {
+#pragma unroll
+    for (int n = 0; n < NPF; ++n) {
+      const int i = tid + 256 * n;
+      kr[n] = make_uint4(0u, 0u, 0u, 0u);
+      vr8[n] = make_uint4(0u, 0u, 0u, 0u);
+      if (i < AK * kc8) {
+        const int j = j0 + i / kc8;
+        if (j < kb1) kr[n] = *reinterpret_cast<const uint4*>(kbase + (int64_t)j * a.k_st + 8 * (i % kc8));
+      }
+      if (i < AK * vc8) {
+        const int j = j0 + i / vc8;
+        if (j < kb1) vr8[n] = *reinterpret_cast<const uint4*>(vbase + (int64_t)j * a.v_st + 8 * (i % vc8));
+      }
+    }
+  };
+  if constexpr (PREF) {
+    if (kb0 < kb1) fetch(kb0);
+  }
   for (int j0 = kb0; j0 < kb1; j0 += AK) {
     __syncthreads();  // the previous tile's reads are done (and Q is staged)
-    const int kc8 = Dk / 8, vc8 = Dv / 8;
-    for (int i = tid; i < AK * kc8; i += 256) {
-      const int key = i / kc8, ch = i % kc8, j = j0 + key;
-      uint4 u = make_uint4(0u, 0u, 0u, 0u);
-      if (j < kb1) u = *reinterpret_cast<const uint4*>(kbase + (int64_t)j * a.k_st + 8 * ch);
-      *reinterpret_cast<uint4*>(ks + key * ks_st + 8 * ch) = u;
-    }
-    for (int i = tid; i < AK * vc8; i += 256) {
-      const int key = i / vc8, ch = i % vc8, j = j0 + key;
-      uint4 u = make_uint4(0u, 0u, 0u, 0u);
-      if (j < kb1) u = *reinterpret_cast<const uint4*>(vbase + (int64_t)j * a.v_st + 8 * ch);
-      *reinterpret_cast<uint4*>(vs + key * vs_st + 8 * ch) = u;
+    if constexpr (PREF) {
+#pragma unroll
+      for (int n = 0; n < NPF; ++n) {
+        const int i = tid + 256 * n;
+        if (i < AK * kc8) *reinterpret_cast<uint4*>(ks + (i / kc8) * ks_st + 8 * (i % kc8)) = kr[n];
+        if (i < AK * vc8) *reinterpret_cast<uint4*>(vs + (i / vc8) * vs_st + 8 * (i % vc8)) = vr8[n];
+      }
+      if (j0 + AK < kb1) fetch(j0 + AK);  // in flight during this tile's products
+    } else {
+      for (int i = tid; i < AK * kc8; i += 256) {
+        const int key = i / kc8, ch = i % kc8, j = j0 + key;
+        uint4 u = make_uint4(0u, 0u, 0u, 0u);
+        if (j < kb1) u = *reinterpret_cast<const uint4*>(kbase + (int64_t)j * a.k_st + 8 * ch);
+        *reinterpret_cast<uint4*>(ks + key * ks_st + 8 * ch) = u;
+      }
+      for (int i = tid; i < AK * vc8; i += 256) {
+        const int key = i / vc8, ch = i % vc8, j = j0 + key;
+        uint4 u = make_uint4(0u, 0u, 0u, 0u);
+        if (j < kb1) u = *reinterpret_cast<const uint4*>(vbase + (int64_t)j * a.v_st + 8 * ch);
+        *reinterpret_cast<uint4*>(vs + key * vs_st + 8 * ch) = u;
+      }
     }
     __syncthreads();
     // scores: keys key0 + TPR x (x < KPT) over dims dbeg .. dbeg + dlen - 1
@@ -463,16 +498,22 @@ int attn_any_split_keys(int64_t ctx, int n_split) {
   return (int)std::max<int64_t>(AK, (per + AK - 1) / AK * AK);
 }
 
-template <int RPB, int DVT>
-static hipError_t launch_attn_any_t(const AttnAnyArgs& a, dim3 grid, size_t lds, hipStream_t st) {
+template <int RPB, int DVT, bool PREF>
+static hipError_t launch_attn_any_p(const AttnAnyArgs& a, dim3 grid, size_t lds, hipStream_t st) {
   if (lds > 65536) {  // lift the dynamic-LDS cap of the current device for this kernel
     const hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&attn_any_kernel<RPB, DVT>),
+        reinterpret_cast<const void*>(&attn_any_kernel<RPB, DVT, PREF>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((attn_any_kernel<RPB, DVT>), grid, dim3(256), lds, st, a);
+  hipLaunchKernelGGL((attn_any_kernel<RPB, DVT, PREF>), grid, dim3(256), lds, st, a);
   return hipGetLastError();
+}
+// decode (split partials, one query per row) prefetches its tiles
+template <int RPB, int DVT>
+static hipError_t launch_attn_any_t(const AttnAnyArgs& a, dim3 grid, size_t lds, hipStream_t st) {
+  return a.part ? launch_attn_any_p<RPB, DVT, true>(a, grid, lds, st)
+                : launch_attn_any_p<RPB, DVT, false>(a, grid, lds, st);
 }
 
 hipError_t launch_attn_any(const AttnAnyArgs& a, hipStream_t st) {
