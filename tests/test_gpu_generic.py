@@ -88,12 +88,14 @@ def test_knorm_rope_append_head_dims(vm, orc, Dk, Dv, half):
 
 
 @pytest.mark.parametrize("Dk,Dv,H,Hk,causal", [(64, 64, 8, 2, True), (128, 128, 8, 2, False),
+                                               (128, 128, 16, 4, True), (128, 128, 4, 4, True),
                                                (64, 128, 8, 2, True), (128, 32, 4, 4, True),
                                                (512, 512, 4, 1, True), (16, 16, 16, 1, False),
                                                (256, 128, 32, 2, True)])
 def test_attention_head_dims(vm, orc, Dk, Dv, H, Hk, causal):
     """attention! on cache-prefix views (Lk of a longer cache), ragged k/q
-    lengths, queries the suffix of the keys; rows past q_len untouched."""
+    lengths, queries the suffix of the keys; rows past q_len untouched. D = 128
+    runs the MFMA kernel's 128-wide form, the other shapes the generic one."""
     banner(f"attention_ Dk={Dk} Dv={Dv} H={H} Hk={Hk} causal={causal}")
     B, L, Lk, ctx = 2, 37, 100, 128
     q_bits = normal_bf16((B, H, L, Dk), 420)
@@ -115,6 +117,31 @@ def test_attention_head_dims(vm, orc, Dk, Dv, H, Hk, causal):
     print(f"max {mx:.3e} mean {mn:.3e}")
     assert mx <= TOL_MAX and mn <= TOL_MEAN
     assert np.array_equal(from_dev(O)[~fin.any(axis=-1)], o_bits[~fin.any(axis=-1)])
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_d128_long(vm, orc, causal):
+    """The MFMA kernel at D = 128 over many tiles and query blocks (B = 2, 300
+    queries against 1000 keys, ragged), every row checked."""
+    banner(f"attention_ D=128 long causal={causal}")
+    B, H, Hk, L, Lk, Dh = 2, 8, 2, 300, 1000, 128
+    q_bits = normal_bf16((B, H, L, Dh), 425)
+    k_bits = normal_bf16((B, Hk, Lk, Dh), 426)
+    v_bits = normal_bf16((B, Hk, Lk, Dh), 427)
+    kl = np.array([1000, 517], np.int32)
+    ql = np.array([300, 129], np.int32)
+    O = torch.zeros((B, H, L, Dh), dtype=torch.bfloat16, device="cuda")
+    vm.attention_({"O": O}, to_dev(q_bits), to_dev(k_bits), to_dev(v_bits), causal=causal,
+                  k_lengths=i32(kl), q_lengths=i32(ql))
+    torch.cuda.synchronize()
+    ref = orc.attention(bf16_to_f32(q_bits), bf16_to_f32(k_bits), bf16_to_f32(v_bits),
+                        causal=causal, k_lengths=kl, q_lengths=ql)
+    got = dev_f32(O)
+    fin = ~np.isnan(ref)
+    mx, mn = maxmean(got[fin], ref[fin])
+    print(f"max {mx:.3e} mean {mn:.3e}")
+    assert mx <= TOL_MAX and mn <= TOL_MEAN
+    assert not got[~fin].any()
 
 
 @pytest.mark.parametrize("Dk,Dv,H,Hk,n_splits", [(128, 128, 16, 1, 0), (64, 256, 8, 2, 8),

@@ -32,8 +32,25 @@ namespace vm {
 
 constexpr int PF_BM = 128;                   // query rows per workgroup
 constexpr int PF_BN = 32;                    // keys per tile
-constexpr int TILE = PF_BN * HEAD_DIM;       // bf16 per K (or V) tile: 16 KB
 constexpr float RESCALE_SLACK = 8.0f;
+
+// Head dims D = 256 (Qwen3.5) and 128. A tile is 32 rows of 2D bytes, loaded
+// as 1-KB slots (D / 16 of them, D / 64 per wave), each slot 512 / D rows of
+// D / 8 lanes. The swizzle below keeps 16-chunk blocks, so it serves both row
+// widths (16 or 32 chunks of 16 bytes). Q is pre-scaled by 1/16 at D = 256
+// (exact in bf16); at D = 128 the 1/sqrt(128) goes into the exp2 factor.
+template <int D> struct PfShape {
+  static constexpr int TILE = PF_BN * D;           // bf16 per K (or V) tile
+  static constexpr int RB = 2 * D;                 // bytes per row
+  static constexpr int SPW = D / 64;               // 1-KB slots per wave and tile (K or V)
+  static constexpr int RPS = 512 / D;              // rows per slot
+  static constexpr int LPR = D / 8;                // lanes per row in a slot
+  static constexpr int LOADS = 2 * SPW;            // vmem instructions per wave per tile
+  static constexpr int KK = D / 16;                // 16-deep k-steps of QK
+  static constexpr int DT = D / 32;                // 32-wide d-blocks of O
+  static constexpr float QPRE = D == 256 ? QK_SCALE : 1.0f;
+  static constexpr float SL = D == 256 ? LOG2E : LOG2E * 0.08838834764831845f;  // 1/sqrt(128)
+};
 
 // Workgroup barrier without the release/acquire fences of __syncthreads(): those
 // would wait for every outstanding load (vmcnt(0)), including the tiles still in
@@ -58,22 +75,22 @@ struct PrefillCtx {
   int64_t kv_st;
   int k_len, off, row, wrow0, wrow1, q_len, lane, wave;
   int krow_max;            // last row that may be read (finite data)
-  int dma_off[4];          // per-lane element offsets of this wave's 4 DMA slots
+  int dma_off[4];          // per-lane element offsets of this wave's DMA slots
 };
 
-// Issue this wave's share (4 K + 4 V instructions of 1 KB) of tile `jt`: the
-// 16-KB tile is 16 one-KB slots of two 512-byte rows each, 4 slots per wave.
-constexpr int LOADS_PER_TILE = 8;  // vmem instructions per wave per tile
+// Issue this wave's share (SPW K + SPW V instructions of 1 KB) of tile `jt`.
+template <int D>
 __device__ __forceinline__ void issue_tile(const PrefillCtx& c, int jt, uint16_t* kd,
                                            uint16_t* vd) {
+  using Sh = PfShape<D>;
   const int row0 = jt * PF_BN;
   if (row0 + PF_BN - 1 <= c.krow_max) {
     // whole tile in range: uniform tile base + precomputed per-lane offsets
     const uint16_t* kt = c.kbase + (int64_t)row0 * c.kv_st;
     const uint16_t* vt = c.vbase + (int64_t)row0 * c.kv_st;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int g = 4 * c.wave + i;  // 1-KB slot of the tile: rows 2g, 2g+1
+    for (int i = 0; i < Sh::SPW; ++i) {
+      const int g = Sh::SPW * c.wave + i;  // 1-KB slot of the tile: rows RPS g ..
       __builtin_amdgcn_global_load_lds((const void*)(kt + c.dma_off[i]),
                                        (__attribute__((address_space(3))) void*)(kd + g * 512),
                                        16, 0, 0);
@@ -85,10 +102,10 @@ __device__ __forceinline__ void issue_tile(const PrefillCtx& c, int jt, uint16_t
     // last tile: rows past the last readable row re-read it (their keys are masked)
     const int l = c.lane;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int g = 4 * c.wave + i;
-      const int r = 2 * g + (l >> 5);
-      const int chunk = (l & 31) ^ swz_pf(r);
+    for (int i = 0; i < Sh::SPW; ++i) {
+      const int g = Sh::SPW * c.wave + i;
+      const int r = Sh::RPS * g + l / Sh::LPR;
+      const int chunk = (l % Sh::LPR) ^ swz_pf(r);
       const int64_t key = min(row0 + r, c.krow_max);
       const int64_t go = key * c.kv_st + chunk * 8;
       __builtin_amdgcn_global_load_lds((const void*)(c.kbase + go),
@@ -103,18 +120,20 @@ __device__ __forceinline__ void issue_tile(const PrefillCtx& c, int jt, uint16_t
 
 // S^T = K Q^T for one tile: chunk 2kk+h2 of row l%32 sits at
 // ((2kk+h2) ^ swz_pf) -> koff[kk&7] + 256*(kk>>3) bytes.
+template <int D>
 __device__ __forceinline__ f32x16 qk_tile(const uint16_t* kb, const uint4 (&qop)[16],
                                           const int (&koff)[8]) {
+  constexpr int KK = PfShape<D>::KK;
   const char* kl = reinterpret_cast<const char*>(kb);
-  uint4 kf[16];
+  uint4 kf[KK];
 #pragma unroll
-  for (int kk = 0; kk < 16; ++kk)
+  for (int kk = 0; kk < KK; ++kk)
     kf[kk] = *reinterpret_cast<const uint4*>(kl + koff[kk & 7] + 256 * (kk >> 3));
   f32x16 s;
 #pragma unroll
   for (int j = 0; j < 16; ++j) s[j] = 0.f;
 #pragma unroll
-  for (int kk = 0; kk < 16; ++kk) s = mfma32(kf[kk], qop[kk], s);
+  for (int kk = 0; kk < KK; ++kk) s = mfma32(kf[kk], qop[kk], s);
   return s;
 }
 
@@ -133,19 +152,20 @@ __device__ __forceinline__ void mask_tile(const PrefillCtx& c, int jt, f32x16& s
 // One pipelined iteration on ring slot SLOT = jt % 4: wait for tile jt+1, issue
 // tile jt+3, then QK(jt+1) on the matrix cores while the VALU runs softmax(jt),
 // then PV(jt). `sc` holds S^T of tile jt on entry and of tile jt+1 on exit.
-template <bool CAUSAL, int SLOT>
+template <bool CAUSAL, int SLOT, int D>
 __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_tiles, int my_tiles,
                                           uint16_t* const (&K)[4], uint16_t* const (&V)[4],
                                           const uint4 (&qop)[16], f32x16 (&acc)[8], f32x16& sc,
                                           float& m_run, float& l_part, const int (&koff)[8],
                                           const int (&voff)[4][2]) {
+  using Sh = PfShape<D>;
   // tiles jt+1 and jt+2 may be in flight; tile jt+1 must be resident for all waves
   if (jt + 2 < n_tiles)
-    wait_vmcnt<LOADS_PER_TILE>();
+    wait_vmcnt<Sh::LOADS>();
   else
     wait_vmcnt<0>();
   lds_barrier();
-  if (jt + 3 < n_tiles) issue_tile(c, jt + 3, K[(SLOT + 3) & 3], V[(SLOT + 3) & 3]);
+  if (jt + 3 < n_tiles) issue_tile<D>(c, jt + 3, K[(SLOT + 3) & 3], V[(SLOT + 3) & 3]);
   if (jt >= my_tiles) return;
 
   const bool need_mask = (jt * PF_BN + PF_BN > c.k_len) ||
@@ -154,12 +174,12 @@ __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_til
 
   // S^T of the next tile (its slot is resident; past this wave's last tile the
   // result is simply unused)
-  const f32x16 sn = qk_tile(K[(SLOT + 1) & 3], qop, koff);
+  const f32x16 sn = qk_tile<D>(K[(SLOT + 1) & 3], qop, koff);
 
   float mx = sc[0];
 #pragma unroll
   for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sc[j]);
-  mx = wave_max_xor(mx, 32) * LOG2E;
+  mx = wave_max_xor(mx, 32) * Sh::SL;
   const float m_new = fmaxf(m_run, mx);
   const bool need = m_new > m_run + RESCALE_SLACK;
   if (__ballot(need) != 0ull) {
@@ -167,14 +187,14 @@ __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_til
     const float alpha = (m_use == m_run) ? 1.0f : fast_exp2(m_run - m_use);
     l_part *= alpha;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+    for (int i = 0; i < Sh::DT; ++i) acc[i] *= alpha;
     m_run = m_use;
   }
   const float m_eff = m_run == -INFINITY ? 0.f : m_run;
   float p[16], psum = 0.f;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    p[j] = fast_exp2(__builtin_fmaf(sc[j], LOG2E, -m_eff));
+    p[j] = fast_exp2(__builtin_fmaf(sc[j], Sh::SL, -m_eff));
     psum += p[j];
   }
   l_part += psum;
@@ -187,13 +207,13 @@ __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_til
     pop[ks].w = pack2(p[8 * ks + 6], p[8 * ks + 7]);
   }
   // O^T += V^T P^T; d-block dt, key half ks, row half hi at
-  // voff[dt&3][hi] + 256*(dt>>2) + 8192*ks bytes
+  // voff[dt&3][hi] + 256*(dt>>2) + 16 RB ks bytes
   const char* vl = reinterpret_cast<const char*>(V[SLOT]);
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
+  for (int dt = 0; dt < Sh::DT; ++dt) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const char* p0 = vl + 256 * (dt >> 2) + 8192 * ks;
+      const char* p0 = vl + 256 * (dt >> 2) + 16 * Sh::RB * ks;
       const uint2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(p0 + voff[dt & 3][0]));
       const uint2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(p0 + voff[dt & 3][1]));
       acc[dt] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), pop[ks], acc[dt]);
@@ -203,7 +223,7 @@ __device__ __forceinline__ void tile_step(const PrefillCtx& c, int jt, int n_til
 }
 
 // Ring of 4 tile slots; tiles 0..2 are issued by the caller.
-template <bool CAUSAL>
+template <bool CAUSAL, int D>
 __device__ __forceinline__ void tile_loop(const PrefillCtx& c, int n_tiles, int my_tiles,
                                           uint16_t* const (&K)[4], uint16_t* const (&V)[4],
                                           const uint4 (&qop)[16], f32x16 (&acc)[8],
@@ -211,32 +231,34 @@ __device__ __forceinline__ void tile_loop(const PrefillCtx& c, int n_tiles, int 
                                           const int (&voff)[4][2]) {
   // tile 0 resident (tiles 1 and 2 may still be in flight), then S^T of tile 0
   if (n_tiles > 2)
-    wait_vmcnt<2 * LOADS_PER_TILE>();
+    wait_vmcnt<2 * PfShape<D>::LOADS>();
   else if (n_tiles > 1)
-    wait_vmcnt<LOADS_PER_TILE>();
+    wait_vmcnt<PfShape<D>::LOADS>();
   else
     wait_vmcnt<0>();
   lds_barrier();
   f32x16 sc;
-  if (my_tiles > 0) sc = qk_tile(K[0], qop, koff);
+  if (my_tiles > 0) sc = qk_tile<D>(K[0], qop, koff);
   for (int jt = 0; jt < n_tiles; jt += 4) {
-    tile_step<CAUSAL, 0>(c, jt, n_tiles, my_tiles, K, V, qop, acc, sc, m_run, l_part,
+    tile_step<CAUSAL, 0, D>(c, jt, n_tiles, my_tiles, K, V, qop, acc, sc, m_run, l_part,
                                  koff, voff);
     if (jt + 1 < n_tiles)
-      tile_step<CAUSAL, 1>(c, jt + 1, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
+      tile_step<CAUSAL, 1, D>(c, jt + 1, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
                                    l_part, koff, voff);
     if (jt + 2 < n_tiles)
-      tile_step<CAUSAL, 2>(c, jt + 2, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
+      tile_step<CAUSAL, 2, D>(c, jt + 2, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
                                    l_part, koff, voff);
     if (jt + 3 < n_tiles)
-      tile_step<CAUSAL, 3>(c, jt + 3, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
+      tile_step<CAUSAL, 3, D>(c, jt + 3, n_tiles, my_tiles, K, V, qop, acc, sc, m_run,
                                    l_part, koff, voff);
   }
 }
 
-template <bool CAUSAL>
+template <bool CAUSAL, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_kernel(PrefillArgs a) {
+  using Sh = PfShape<D>;
+  constexpr int TILE = Sh::TILE;
   __shared__ __attribute__((aligned(1024))) uint16_t K0[TILE], K1[TILE], K2[TILE], K3[TILE];
   __shared__ __attribute__((aligned(1024))) uint16_t V0[TILE], V1[TILE], V2[TILE], V3[TILE];
   uint16_t* const K[4] = {K0, K1, K2, K3};
@@ -265,7 +287,7 @@ void prefill_kernel(PrefillArgs a) {
                        (int64_t)qrow * a.q_st + 8 * h2;
   uint4 qraw[16];
 #pragma unroll
-  for (int kk = 0; kk < 16; ++kk) qraw[kk] = load16(qp + 16 * kk);
+  for (int kk = 0; kk < Sh::KK; ++kk) qraw[kk] = load16(qp + 16 * kk);
 
   // q_len > L and k_len > Lk are out of contract; clamp so rows past the
   // tensors are never read or written
@@ -285,29 +307,29 @@ void prefill_kernel(PrefillArgs a) {
   c.lane = lane; c.wave = wave;
   c.krow_max = max(0, k_len - 1);  // rows past k_len are masked; read finite data
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 2 * (4 * wave + i) + (lane >> 5);
-    c.dma_off[i] = r * (int)a.kv_st + (((lane & 31) ^ swz_pf(r)) * 8);
+  for (int i = 0; i < Sh::SPW; ++i) {
+    const int r = Sh::RPS * (Sh::SPW * wave + i) + lane / Sh::LPR;
+    c.dma_off[i] = r * (int)a.kv_st + (((lane % Sh::LPR) ^ swz_pf(r)) * 8);
   }
 
   // the first three tiles go out before the q operand is formed so their
   // latency overlaps it
-  if (n_tiles > 0) issue_tile(c, 0, K0, V0);
-  if (n_tiles > 1) issue_tile(c, 1, K1, V1);
-  if (n_tiles > 2) issue_tile(c, 2, K2, V2);
+  if (n_tiles > 0) issue_tile<D>(c, 0, K0, V0);
+  if (n_tiles > 1) issue_tile<D>(c, 1, K1, V1);
+  if (n_tiles > 2) issue_tile<D>(c, 2, K2, V2);
   // tiles this wave computes (causal: keys <= off + its last row)
   int my_tiles = c.wrow0 < q_len ? n_tiles : 0;
   if (CAUSAL && my_tiles > 0) my_tiles = max(0, min(n_tiles, (off + c.wrow1) / PF_BN + 1));
 
-  // ---- Q operand: lane holds q[row][16kk + 8*h2 + j], pre-scaled by 1/16
-  // (a power of two: exact in bf16).
+  // ---- Q operand: lane holds q[row][16kk + 8*h2 + j], pre-scaled by 1/16 at
+  // D = 256 (a power of two: exact in bf16)
   uint4 qop[16];
 #pragma unroll
-  for (int kk = 0; kk < 16; ++kk) {
+  for (int kk = 0; kk < Sh::KK; ++kk) {
     float x[8];
     unpack8(qraw[kk], x);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] *= QK_SCALE;
+    for (int j = 0; j < 8; ++j) x[j] *= Sh::QPRE;
     qop[kk] = pack8(x);
   }
 
@@ -321,7 +343,7 @@ void prefill_kernel(PrefillArgs a) {
   {
     const int sk = swz_pf(l32);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) koff[q] = l32 * 512 + 16 * ((2 * q + h2) ^ sk);
+    for (int q = 0; q < 8; ++q) koff[q] = l32 * Sh::RB + 16 * ((2 * q + h2) ^ sk);
     const int m = lane >> 4, i = lane & 15;
     const int u = 2 * (m & 1) + ((i & 3) >> 1);
 #pragma unroll
@@ -329,18 +351,18 @@ void prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int hi = 0; hi < 2; ++hi) {
         const int rr = 8 * hi + 4 * (m >> 1) + (i >> 2);
-        voff[d3][hi] = rr * 512 + 16 * ((4 * d3 + u) ^ swz_pf(rr)) + 8 * (i & 1);
+        voff[d3][hi] = rr * Sh::RB + 16 * ((4 * d3 + u) ^ swz_pf(rr)) + 8 * (i & 1);
       }
   }
 
   f32x16 acc[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < Sh::DT; ++i)
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[i][j] = 0.f;
   float l_part = 0.f, m_run = -INFINITY;
 
-  tile_loop<CAUSAL>(c, n_tiles, my_tiles, K, V, qop, acc, m_run, l_part, koff, voff);
+  tile_loop<CAUSAL, D>(c, n_tiles, my_tiles, K, V, qop, acc, m_run, l_part, koff, voff);
 
   // ---- epilogue: normalise and store (row-major d within each row)
   if (row >= q_len) return;
@@ -348,7 +370,7 @@ void prefill_kernel(PrefillArgs a) {
   const float inv = l_tot > 0.f ? fast_rcp(l_tot) : 0.f;  // no valid key -> 0
   uint16_t* op = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)row * a.o_st;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
+  for (int dt = 0; dt < Sh::DT; ++dt) {
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
       const int d0 = 32 * dt + 8 * jb + 4 * h2;
@@ -364,10 +386,16 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st) {
   const int64_t nwg = (int64_t)a.n_qt * a.H * a.B;
   if (nwg == 0) return hipSuccess;
   dim3 grid((unsigned)nwg), block(256);
-  if (a.causal)
-    hipLaunchKernelGGL((prefill_kernel<true>), grid, block, 0, st, a);
-  else
-    hipLaunchKernelGGL((prefill_kernel<false>), grid, block, 0, st, a);
+  if (a.D == 128) {
+    if (a.causal)
+      hipLaunchKernelGGL((prefill_kernel<true, 128>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((prefill_kernel<false, 128>), grid, block, 0, st, a);
+  } else if (a.causal) {
+    hipLaunchKernelGGL((prefill_kernel<true, 256>), grid, block, 0, st, a);
+  } else {
+    hipLaunchKernelGGL((prefill_kernel<false, 256>), grid, block, 0, st, a);
+  }
   return hipGetLastError();
 }
 

@@ -561,8 +561,9 @@ int vm_attention_fwd(vm_bf16* o, int64_t o_st, int64_t o_sh, int64_t o_sb, const
     TRY(check_stride(s, "attention"));
   if (B == 0 || L == 0) return VM_OK;
   REQUIRE(Lk > 0, VM_E_ARG, "attention: k_len must be >= 1 (Lk = 0)");
-  const bool tuned = Dk == vm::HEAD_DIM_ABI && Dv == Dk && k_st == v_st && k_sh == v_sh &&
-                     k_sb == v_sb && k_st < ((int64_t)1 << 25);
+  // the MFMA kernel takes D = 256 (Qwen3.5) and 128
+  const bool tuned = (Dk == vm::HEAD_DIM_ABI || Dk == 128) && Dv == Dk && k_st == v_st &&
+                     k_sh == v_sh && k_sb == v_sb && k_st < ((int64_t)1 << 25);
   if (!tuned) {  // the generic kernel
     REQUIRE((int64_t)B * Hk <= 65535, VM_E_UNSUPPORTED, "attention: B*Hk = %lld > 65535",
             (long long)B * Hk);
@@ -584,7 +585,7 @@ int vm_attention_fwd(vm_bf16* o, int64_t o_st, int64_t o_sh, int64_t o_sb, const
   a.k = k; a.v = v; a.kv_st = kv_st; a.kv_sh = kv_sh; a.kv_sb = kv_sb;
   a.o = o; a.o_st = o_st; a.o_sh = o_sh; a.o_sb = o_sb;
   a.k_lengths = k_lengths; a.q_lengths = q_lengths; a.prior = nullptr;
-  a.B = B; a.H = H; a.Hk = Hk; a.L = L; a.Lk = Lk; a.causal = causal ? 1 : 0;
+  a.B = B; a.H = H; a.Hk = Hk; a.L = L; a.Lk = Lk; a.causal = causal ? 1 : 0; a.D = Dk;
   a.n_qt = (L + vm::PREFILL_ROWS_ABI - 1) / vm::PREFILL_ROWS_ABI;
   return hip_status(timed(VM_K_PREFILL, S(st), [&] { return vm::launch_prefill(a, S(st)); }), "attention");
 }
