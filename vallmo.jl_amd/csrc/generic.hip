@@ -314,11 +314,11 @@ namespace {
 
 constexpr int DN_NC = 16;  // columns per wave at Dv = 256
 
-template <int KE>
+template <int KE, int NC>
 __device__ __forceinline__ void dn_any_load(float (&s)[DN_NC][KE], const float* base, int Dk,
                                             int j0, int nc, int lane) {
 #pragma unroll
-  for (int c = 0; c < DN_NC; ++c) {
+  for (int c = 0; c < NC; ++c) {
 #pragma unroll
     for (int e = 0; e < KE; ++e) {
       const int i = lane + 64 * e;
@@ -326,11 +326,11 @@ __device__ __forceinline__ void dn_any_load(float (&s)[DN_NC][KE], const float* 
     }
   }
 }
-template <int KE>
+template <int KE, int NC>
 __device__ __forceinline__ void dn_any_store(const float (&s)[DN_NC][KE], float* base, int Dk,
                                              int j0, int nc, int lane) {
 #pragma unroll
-  for (int c = 0; c < DN_NC; ++c) {
+  for (int c = 0; c < NC; ++c) {
 #pragma unroll
     for (int e = 0; e < KE; ++e) {
       const int i = lane + 64 * e;
@@ -338,37 +338,50 @@ __device__ __forceinline__ void dn_any_store(const float (&s)[DN_NC][KE], float*
     }
   }
 }
-// one delta step on the wave's columns; vv: lane c holds v of column j0 + c;
-// o[c] (every lane) the column's output
-template <int KE>
+// one delta step on the wave's NC columns (NC a power of two >= the wave's
+// columns; the extra ones hold zeros and are never stored), in phases so that
+// the columns' independent cross-lane sums overlap; vv: lane c holds v of
+// column j0 + c; o[c] (every lane) the column's output
+template <int KE, int NC>
 __device__ __forceinline__ void dn_any_step(float (&s)[DN_NC][KE], const float (&k)[KE],
                                             const float (&q)[KE], float vv, float decay,
-                                            float beta, int nc, float (&o)[DN_NC]) {
+                                            float beta, float (&o)[DN_NC]) {
+  float ks[NC];
 #pragma unroll
-  for (int c = 0; c < DN_NC; ++c) {
-    if (c >= nc) continue;  // wave-uniform
-    float ks = 0.f;
+  for (int c = 0; c < NC; ++c) {
+    ks[c] = 0.f;
 #pragma unroll
     for (int e = 0; e < KE; ++e) {
       s[c][e] *= decay;
-      ks = fmaf(s[c][e], k[e], ks);
+      ks[c] = fmaf(s[c][e], k[e], ks[c]);
     }
-    ks = wave_sum_all(ks);
-    const float delta = beta * (__shfl(vv, c, 64) - ks);
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) ks[c] += __shfl_xor(ks[c], m, 64);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const float delta = beta * (__shfl(vv, c, 64) - ks[c]);
     float os = 0.f;
 #pragma unroll
     for (int e = 0; e < KE; ++e) {
       s[c][e] = fmaf(k[e], delta, s[c][e]);
       os = fmaf(s[c][e], q[e], os);
     }
-    o[c] = wave_sum_all(os);
+    o[c] = os;
   }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) o[c] += __shfl_xor(o[c], m, 64);
 }
 // lane c's copy of o[c] (registers are not indexable by lane)
+template <int NC>
 __device__ __forceinline__ float dn_pick(const float (&o)[DN_NC], int lane) {
   float r = 0.f;
 #pragma unroll
-  for (int c = 0; c < DN_NC; ++c) r = lane == c ? o[c] : r;
+  for (int c = 0; c < NC; ++c) r = lane == c ? o[c] : r;
   return r;
 }
 
@@ -376,15 +389,15 @@ __device__ __forceinline__ float dn_pick(const float (&o)[DN_NC], int lane) {
 
 // deltanet_sequence! and, at T = 1, deltanet_recurrent_decode!: fp32 inputs
 // already normed and gated (decay = exp(gate)), the state carried in registers
-template <int KE>
+template <int KE, int NC>
 __global__ __launch_bounds__(1024) void deltanet_any_seq_kernel(DeltaSeqArgs a, int Dk, int Dv) {
   const int hv = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int nc = Dv / 16, j0 = w * nc;
   const int hk = hv / (a.Hv / a.Hk);
   const int64_t sb = ((int64_t)b * a.Hv + hv) * Dv * Dk;
-  float s[DN_NC][KE], o[DN_NC];
-  dn_any_load<KE>(s, a.s_in + sb, Dk, j0, nc, lane);
+  float s[DN_NC][KE], o[DN_NC] = {};
+  dn_any_load<KE, NC>(s, a.s_in + sb, Dk, j0, nc, lane);
   for (int t = 0; t < a.T; ++t) {
     const int64_t qk = (((int64_t)b * a.Hk + hk) * a.T + t) * Dk;
     const int64_t vo = (((int64_t)b * a.Hv + hv) * a.T + t) * Dv;
@@ -397,24 +410,24 @@ __global__ __launch_bounds__(1024) void deltanet_any_seq_kernel(DeltaSeqArgs a, 
       k[e] = i < Dk ? a.k[qk + i] : 0.f;
     }
     const float vv = lane < nc ? a.v[vo + j0 + lane] : 0.f;
-    dn_any_step<KE>(s, k, q, vv, expf(a.gate[g]), a.beta[g], nc, o);
-    if (lane < nc) a.o[vo + j0 + lane] = dn_pick(o, lane);
+    dn_any_step<KE, NC>(s, k, q, vv, expf(a.gate[g]), a.beta[g], o);
+    if (lane < nc) a.o[vo + j0 + lane] = dn_pick<NC>(o, lane);
   }
-  dn_any_store<KE>(s, a.s_out + sb, Dk, j0, nc, lane);
+  dn_any_store<KE, NC>(s, a.s_out + sb, Dk, j0, nc, lane);
 }
 
 // fused_deltanet_decode!: raw bf16 q, k (l2-normed here, q also by 1/sqrt(Dk)),
 // the gates from alpha and beta_raw, then the gated RMSNorm with silu(z)
 // (deltanet_fused.jl:27-105)
-template <int KE>
+template <int KE, int NC>
 __global__ __launch_bounds__(1024) void deltanet_any_fused_kernel(DeltaFusedArgs a, int Dk, int Dv) {
   const int hv = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int nc = Dv / 16, j0 = w * nc;
   const int hk = hv / (a.Hv / a.Hk);
   const int64_t sb = ((int64_t)b * a.Hv + hv) * Dv * Dk;
-  float s[DN_NC][KE], o[DN_NC];
-  dn_any_load<KE>(s, a.s_in + sb, Dk, j0, nc, lane);
+  float s[DN_NC][KE], o[DN_NC] = {};
+  dn_any_load<KE, NC>(s, a.s_in + sb, Dk, j0, nc, lane);
   float q[KE], k[KE], qss = 0.f, kss = 0.f;
 #pragma unroll
   for (int e = 0; e < KE; ++e) {
@@ -438,14 +451,13 @@ __global__ __launch_bounds__(1024) void deltanet_any_fused_kernel(DeltaFusedArgs
   const float decay = expf(-expf(a.a_log[hv]) * sp);
   const float beta = accurate_sigmoid(bfv(a.beta[b * a.b_sb + hv]));
   const float vv = lane < nc ? bfv(a.v[b * a.v_sb + (int64_t)hv * Dv + j0 + lane]) : 0.f;
-  dn_any_step<KE>(s, k, q, vv, decay, beta, nc, o);
-  dn_any_store<KE>(s, a.s_out + sb, Dk, j0, nc, lane);
+  dn_any_step<KE, NC>(s, k, q, vv, decay, beta, o);
+  dn_any_store<KE, NC>(s, a.s_out + sb, Dk, j0, nc, lane);
   // gated RMSNorm over the Dv columns
   __shared__ float red[16];
   float ss = 0.f;
 #pragma unroll
-  for (int c = 0; c < DN_NC; ++c)
-    if (c < nc) ss = fmaf(o[c], o[c], ss);
+  for (int c = 0; c < NC; ++c) ss = fmaf(o[c], o[c], ss);  // columns past nc hold 0
   if (lane == 0) red[w] = ss;
   __syncthreads();
   float tot = 0.f;
@@ -455,7 +467,7 @@ __global__ __launch_bounds__(1024) void deltanet_any_fused_kernel(DeltaFusedArgs
     const int j = j0 + lane;
     const float z = bfv(a.z[b * a.z_sb + (int64_t)hv * Dv + j]);
     a.o[b * a.o_sb + (int64_t)hv * Dv + j] =
-        f2bf(dn_pick(o, lane) * rstd * bfv(a.norm_w[j]) * accurate_silu(z));
+        f2bf(dn_pick<NC>(o, lane) * rstd * bfv(a.norm_w[j]) * accurate_silu(z));
   }
 }
 
@@ -552,16 +564,30 @@ hipError_t launch_deltanet_any(const DeltaSeqArgs* seq, const DeltaFusedArgs* fu
   const int B = seq ? seq->B : fused->B, Hv = seq ? seq->Hv : fused->Hv;
   if (B == 0) return hipSuccess;
   const dim3 grid((unsigned)Hv, (unsigned)B), block(1024);
-#define DN_ANY(ke)                                                                         \
-  if (seq) hipLaunchKernelGGL(deltanet_any_seq_kernel<ke>, grid, block, 0, st, *seq, Dk, Dv); \
-  else hipLaunchKernelGGL(deltanet_any_fused_kernel<ke>, grid, block, 0, st, *fused, Dk, Dv);
+  int ncp = 1;  // the wave's columns, rounded up to a power of two
+  while (ncp < Dv / 16) ncp *= 2;
+#define DN_ANY(ke, nc)                                                                       \
+  if (seq)                                                                                   \
+    hipLaunchKernelGGL((deltanet_any_seq_kernel<ke, nc>), grid, block, 0, st, *seq, Dk, Dv); \
+  else                                                                                       \
+    hipLaunchKernelGGL((deltanet_any_fused_kernel<ke, nc>), grid, block, 0, st, *fused, Dk, Dv);
+#define DN_NCS(ke)                              \
+  switch (ncp) {                                \
+    case 1: DN_ANY(ke, 1); break;               \
+    case 2: DN_ANY(ke, 2); break;               \
+    case 4: DN_ANY(ke, 4); break;               \
+    case 8: DN_ANY(ke, 8); break;               \
+    case 16: DN_ANY(ke, 16); break;             \
+    default: return hipErrorInvalidValue;       \
+  }
   switch ((Dk + 63) / 64) {
-    case 1: DN_ANY(1); break;
-    case 2: DN_ANY(2); break;
-    case 3: DN_ANY(3); break;
-    case 4: DN_ANY(4); break;
+    case 1: DN_NCS(1); break;
+    case 2: DN_NCS(2); break;
+    case 3: DN_NCS(3); break;
+    case 4: DN_NCS(4); break;
     default: return hipErrorInvalidValue;
   }
+#undef DN_NCS
 #undef DN_ANY
   return hipGetLastError();
 }
