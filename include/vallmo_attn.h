@@ -216,9 +216,9 @@ int vm_advance_positions(int32_t* positions, int B, vm_stream stream);
  * v_sh, v_sb) (typically cache prefixes); O :: (Dv, L, H, B); scores scaled
  * by 1/sqrt(Dk). k_lengths/q_lengths (device, nullable) give ragged lengths;
  * queries are the suffix of keys, causal offset = k_len - q_len. Rows t >=
- * q_len[b] are not written. Dk, Dv powers of two from 16 to 512; Dk = Dv = 256
- * or 128 with K and V sharing strides runs the tuned MFMA kernel, other shapes
- * a generic one.                                                            */
+ * q_len[b] are not written. Dk, Dv powers of two from 16 to 512; Dk = Dv = 256,
+ * 128 or 64 with K and V sharing strides runs the tuned MFMA kernel, other
+ * shapes a generic one.                                                     */
 int vm_attention_fwd(vm_bf16* o, int64_t o_st, int64_t o_sh, int64_t o_sb,
                      const vm_bf16* q, int64_t q_st, int64_t q_sh, int64_t q_sb,
                      const vm_bf16* k, int64_t k_st, int64_t k_sh, int64_t k_sb,

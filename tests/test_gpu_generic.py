@@ -94,8 +94,8 @@ def test_knorm_rope_append_head_dims(vm, orc, Dk, Dv, half):
                                                (256, 128, 32, 2, True)])
 def test_attention_head_dims(vm, orc, Dk, Dv, H, Hk, causal):
     """attention! on cache-prefix views (Lk of a longer cache), ragged k/q
-    lengths, queries the suffix of the keys; rows past q_len untouched. D = 128
-    runs the MFMA kernel's 128-wide form, the other shapes the generic one."""
+    lengths, queries the suffix of the keys; rows past q_len untouched. Dk = Dv
+    = 128 or 64 runs the MFMA kernel, the other shapes the generic one."""
     banner(f"attention_ Dk={Dk} Dv={Dv} H={H} Hk={Hk} causal={causal}")
     B, L, Lk, ctx = 2, 37, 100, 128
     q_bits = normal_bf16((B, H, L, Dk), 420)
@@ -119,12 +119,12 @@ def test_attention_head_dims(vm, orc, Dk, Dv, H, Hk, causal):
     assert np.array_equal(from_dev(O)[~fin.any(axis=-1)], o_bits[~fin.any(axis=-1)])
 
 
-@pytest.mark.parametrize("causal", [True, False])
-def test_attention_d128_long(vm, orc, causal):
-    """The MFMA kernel at D = 128 over many tiles and query blocks (B = 2, 300
-    queries against 1000 keys, ragged), every row checked."""
-    banner(f"attention_ D=128 long causal={causal}")
-    B, H, Hk, L, Lk, Dh = 2, 8, 2, 300, 1000, 128
+@pytest.mark.parametrize("Dh,causal", [(128, True), (128, False), (64, True), (64, False)])
+def test_attention_mfma_head_dims_long(vm, orc, Dh, causal):
+    """The MFMA kernel at D = 128 and 64 over many tiles and query blocks (B =
+    2, 300 queries against 1000 keys, ragged), every row checked."""
+    banner(f"attention_ D={Dh} long causal={causal}")
+    B, H, Hk, L, Lk = 2, 8, 2, 300, 1000
     q_bits = normal_bf16((B, H, L, Dh), 425)
     k_bits = normal_bf16((B, Hk, Lk, Dh), 426)
     v_bits = normal_bf16((B, Hk, Lk, Dh), 427)

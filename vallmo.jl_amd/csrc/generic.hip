@@ -5,7 +5,7 @@
 // 16 to 512, Dk != Dv, any rotary half-width and any GQA group. The tuned
 // kernels (rows.hip, prefill.hip, decode.hip) are built for Qwen3.5's head
 // shape (D = 256, a 64-dim rotary part, groups up to 8; prefill.hip also
-// D = 128); these take every other shape the reference's operators take. fp32 arithmetic on bf16 operands staged
+// D = 128 and 64); these take every other shape the reference's operators take. fp32 arithmetic on bf16 operands staged
 // in LDS, one workgroup per 4 or 16 query rows: correct at any shape, not tuned.
 // Likewise the DeltaNet operators (fused decode, recurrent decode, sequence)
 // for Dk, Dv multiples of 16 up to 256 beside the tuned Dk = Dv = 128 kernels.

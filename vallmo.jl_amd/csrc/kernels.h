@@ -129,7 +129,7 @@ struct PrefillArgs {
   const int32_t* q_lengths;  // nullable -> L
   const int32_t* prior;      // fused path: k_len = prior + q_len (nullable -> 0)
   int B, H, Hk, L, Lk, n_qt, causal;
-  int D;                     // attention! operator: head dim 128 or 256 (0: 256)
+  int D;                     // attention! operator: head dim 64, 128 or 256 (0: 256)
   const uint16_t* vt;        // fused path: V^T tiles of the attended keys (workspace)
   int vt_tiles;              // tiles per (b, hk) in the workspace: ceil(Lk / 32)
   int pairs;                 // fused path, set by the launcher: one heavy + one light item per workgroup

@@ -34,11 +34,12 @@ constexpr int PF_BM = 128;                   // query rows per workgroup
 constexpr int PF_BN = 32;                    // keys per tile
 constexpr float RESCALE_SLACK = 8.0f;
 
-// Head dims D = 256 (Qwen3.5) and 128. A tile is 32 rows of 2D bytes, loaded
-// as 1-KB slots (D / 16 of them, D / 64 per wave), each slot 512 / D rows of
-// D / 8 lanes. The swizzle below keeps 16-chunk blocks, so it serves both row
-// widths (16 or 32 chunks of 16 bytes). Q is pre-scaled by 1/16 at D = 256
-// (exact in bf16); at D = 128 the 1/sqrt(128) goes into the exp2 factor.
+// Head dims D = 256 (Qwen3.5), 128 and 64. A tile is 32 rows of 2D bytes,
+// loaded as 1-KB slots (D / 16 of them, D / 64 per wave), each slot 512 / D
+// rows of D / 8 lanes. The swizzle below keeps 16-chunk blocks (masked to the
+// row's 8 chunks at D = 64), so it serves every row width. Q is pre-scaled by
+// 1/sqrt(D) where that is a power of two (1/16, 1/8: exact in bf16); at D = 128
+// the 1/sqrt(128) goes into the exp2 factor.
 template <int D> struct PfShape {
   static constexpr int TILE = PF_BN * D;           // bf16 per K (or V) tile
   static constexpr int RB = 2 * D;                 // bytes per row
@@ -48,8 +49,9 @@ template <int D> struct PfShape {
   static constexpr int LOADS = 2 * SPW;            // vmem instructions per wave per tile
   static constexpr int KK = D / 16;                // 16-deep k-steps of QK
   static constexpr int DT = D / 32;                // 32-wide d-blocks of O
-  static constexpr float QPRE = D == 256 ? QK_SCALE : 1.0f;
-  static constexpr float SL = D == 256 ? LOG2E : LOG2E * 0.08838834764831845f;  // 1/sqrt(128)
+  static constexpr int CM = D / 8 < 16 ? D / 8 - 1 : 15;  // swizzle mask (chunks per row)
+  static constexpr float QPRE = D == 256 ? QK_SCALE : D == 64 ? 0.125f : 1.0f;
+  static constexpr float SL = D == 128 ? LOG2E * 0.08838834764831845f : LOG2E;  // 1/sqrt(128)
 };
 
 // Workgroup barrier without the release/acquire fences of __syncthreads(): those
@@ -105,7 +107,7 @@ __device__ __forceinline__ void issue_tile(const PrefillCtx& c, int jt, uint16_t
     for (int i = 0; i < Sh::SPW; ++i) {
       const int g = Sh::SPW * c.wave + i;
       const int r = Sh::RPS * g + l / Sh::LPR;
-      const int chunk = (l % Sh::LPR) ^ swz_pf(r);
+      const int chunk = (l % Sh::LPR) ^ (swz_pf(r) & Sh::CM);
       const int64_t key = min(row0 + r, c.krow_max);
       const int64_t go = key * c.kv_st + chunk * 8;
       __builtin_amdgcn_global_load_lds((const void*)(c.kbase + go),
@@ -309,7 +311,7 @@ void prefill_kernel(PrefillArgs a) {
 #pragma unroll
   for (int i = 0; i < Sh::SPW; ++i) {
     const int r = Sh::RPS * (Sh::SPW * wave + i) + lane / Sh::LPR;
-    c.dma_off[i] = r * (int)a.kv_st + (((lane % Sh::LPR) ^ swz_pf(r)) * 8);
+    c.dma_off[i] = r * (int)a.kv_st + (((lane % Sh::LPR) ^ (swz_pf(r) & Sh::CM)) * 8);
   }
 
   // the first three tiles go out before the q operand is formed so their
@@ -341,7 +343,7 @@ void prefill_kernel(PrefillArgs a) {
   // 4((dt&3) ^ (i>>2)) + 16(dt>>2) + (u ^ (2hi + (m>>1))).
   int koff[8], voff[4][2];
   {
-    const int sk = swz_pf(l32);
+    const int sk = swz_pf(l32) & Sh::CM;
 #pragma unroll
     for (int q = 0; q < 8; ++q) koff[q] = l32 * Sh::RB + 16 * ((2 * q + h2) ^ sk);
     const int m = lane >> 4, i = lane & 15;
@@ -351,7 +353,7 @@ void prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int hi = 0; hi < 2; ++hi) {
         const int rr = 8 * hi + 4 * (m >> 1) + (i >> 2);
-        voff[d3][hi] = rr * Sh::RB + 16 * ((4 * d3 + u) ^ swz_pf(rr)) + 8 * (i & 1);
+        voff[d3][hi] = rr * Sh::RB + 16 * ((4 * d3 + u) ^ (swz_pf(rr) & Sh::CM)) + 8 * (i & 1);
       }
   }
 
@@ -391,6 +393,11 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st) {
       hipLaunchKernelGGL((prefill_kernel<true, 128>), grid, block, 0, st, a);
     else
       hipLaunchKernelGGL((prefill_kernel<false, 128>), grid, block, 0, st, a);
+  } else if (a.D == 64) {
+    if (a.causal)
+      hipLaunchKernelGGL((prefill_kernel<true, 64>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((prefill_kernel<false, 64>), grid, block, 0, st, a);
   } else if (a.causal) {
     hipLaunchKernelGGL((prefill_kernel<true, 256>), grid, block, 0, st, a);
   } else {

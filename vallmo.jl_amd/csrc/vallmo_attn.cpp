@@ -561,8 +561,8 @@ int vm_attention_fwd(vm_bf16* o, int64_t o_st, int64_t o_sh, int64_t o_sb, const
     TRY(check_stride(s, "attention"));
   if (B == 0 || L == 0) return VM_OK;
   REQUIRE(Lk > 0, VM_E_ARG, "attention: k_len must be >= 1 (Lk = 0)");
-  // the MFMA kernel takes D = 256 (Qwen3.5) and 128
-  const bool tuned = (Dk == vm::HEAD_DIM_ABI || Dk == 128) && Dv == Dk && k_st == v_st &&
+  // the MFMA kernel takes D = 256 (Qwen3.5), 128 and 64
+  const bool tuned = (Dk == vm::HEAD_DIM_ABI || Dk == 128 || Dk == 64) && Dv == Dk && k_st == v_st &&
                      k_sh == v_sh && k_sb == v_sb && k_st < ((int64_t)1 << 25);
   if (!tuned) {  // the generic kernel
     REQUIRE((int64_t)B * Hk <= 65535, VM_E_UNSUPPORTED, "attention: B*Hk = %lld > 65535",
