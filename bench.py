@@ -1046,6 +1046,66 @@ def config4_packet_capture_off():
     return json.loads(lines[-1])["config4"]
 
 
+def bench_operators(vm, torch, reps=20, seed=15):
+    """The operators at head shapes other than Qwen3.5's: attention! on the MFMA
+    kernel at D = 128 and 64 and on the generic kernel at Dk != Dv, and the
+    generic decode_attention! and fused_deltanet_decode! (seeded N(0,1)
+    inputs, one event pair around `reps` launches each)."""
+    import numpy as np
+    g = torch.Generator(device="cuda").manual_seed(seed)
+
+    def rnd(*shape):
+        return torch.randn(*shape, device="cuda", generator=g).to(torch.bfloat16)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    res = {}
+    B, H, Hk, L = 1, 16, 4, 4096
+    for Dk, Dv, path in ((128, 128, "mfma"), (64, 64, "mfma"), (128, 64, "generic")):
+        Q, K, V = rnd(B, H, L, Dk), rnd(B, Hk, L, Dk), rnd(B, Hk, L, Dv)
+        O = torch.empty(B, H, L, Dv, dtype=torch.bfloat16, device="cuda")
+        ms = timed(lambda: vm.attention_({"O": O}, Q, K, V, causal=True))
+        fl = 2 * (Dk + Dv) * H * L * (L + 1) / 2
+        res[f"attention_causal_T4096_Dk{Dk}_Dv{Dv}"] = {
+            "kernel": path, "us": 1e3 * ms, "tflops": fl / (ms * 1e-3) / 1e12,
+            "frac_of_bf16_peak": fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+    rng = np.random.default_rng(seed)
+    B, H, Hk, D, ctx = 32, 16, 4, 128, 32768
+    lens = torch.from_numpy(rng.integers(1024, ctx + 1, B).astype(np.int32)).cuda()
+    Q, K, V = rnd(B, H, D), rnd(B, Hk, ctx, D), rnd(B, Hk, ctx, D)
+    O = torch.empty(B, H, D, dtype=torch.bfloat16, device="cuda")
+    sc = torch.empty(vm.decode_scratch_bytes(Q, K, V), dtype=torch.uint8, device="cuda")
+    ms = timed(lambda: vm.decode_attention_({"O": O}, Q, K, V, lengths=lens, scratch=sc))
+    nb = int(lens.sum()) * Hk * D * 2 * 2
+    res["decode_attention_B32_D128"] = {"kernel": "generic", "us": 1e3 * ms,
+                                        "gbs": nb / (ms * 1e-3) / 1e9,
+                                        "frac_of_hbm_peak": nb / (ms * 1e-3) / 1e9 / 8000.0}
+    del K, V
+    B, Hk, Hv, Dd = 32, 16, 32, 64
+    q, k, v, z = rnd(B, Hk, Dd), rnd(B, Hk, Dd), rnd(B, Hv, Dd), rnd(B, Hv, Dd)
+    ab = rnd(B, 2 * Hv)
+    zero = torch.zeros(Hv, device="cuda")
+    S = torch.randn(B, Hv, Dd, Dd, device="cuda", generator=g) * 0.05
+    nw = rnd(Dd)
+    ms = timed(lambda: vm.fused_deltanet_decode(q, k, v, ab[:, :Hv], ab[:, Hv:], z, zero, zero,
+                                                nw, S, Sp=S))
+    nb = B * Hv * Dd * Dd * 4 * 2
+    res["fused_deltanet_decode_B32_D64"] = {"kernel": "generic", "us": 1e3 * ms,
+                                            "gbs": nb / (ms * 1e-3) / 1e9,
+                                            "frac_of_hbm_peak": nb / (ms * 1e-3) / 1e9 / 8000.0}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1058,6 +1118,8 @@ def main():
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer leg")
     ap.add_argument("--no-step", action="store_true", help="skip the whole-decode-step leg")
     ap.add_argument("--no-deltanet", action="store_true", help="skip the DeltaNet kernel leg")
+    ap.add_argument("--no-operators", action="store_true",
+                    help="skip the leg of the operators at other head shapes")
     ap.add_argument("--no-model-prefill", action="store_true",
                     help="skip the whole-model prefill leg")
     ap.add_argument("--no-settle", action="store_true",
@@ -1168,6 +1230,13 @@ def main():
             f"TFLOP/s, Wo GEMM {lp['wo_gemm_tflops']:.0f} TFLOP/s")
         log(f"[bench] decode layer B=32: {ld['ms_per_layer_step']:.3f} ms, qkv GEMV "
             f"{ld['qkv_gemv_gbs']:.0f} GB/s, Wo GEMV {ld['wo_gemv_gbs']:.0f} GB/s")
+    ops_other = None
+    if not args.no_operators:
+        log("[bench] operators at other head shapes (D = 128 / 64, Dk != Dv)")
+        ops_other = bench_operators(vm, torch)
+        for k, v in ops_other.items():
+            fig = f"{v['tflops']:.1f} TFLOP/s" if "tflops" in v else f"{v['gbs']:.0f} GB/s"
+            log(f"[bench] {k} ({v['kernel']}): {v['us']:.1f} us = {fig}")
     dnet = None
     if not args.no_deltanet:
         log("[bench] Gated DeltaNet kernels (Qwen3.5-4B shape)")
@@ -1207,6 +1276,7 @@ def main():
 
     if pf is None:
         print(json.dumps({"decode": decode, "layer": layer, "decode_step": step, "deltanet": dnet,
+                          "operators_other_shapes": ops_other,
                           "prefill_model": pmodel, "cpu_baseline": cpu}), flush=True)
         return
     achieved = pf["flops"] / (pf["attn_kernel_ms"] * 1e-3) / 1e12
@@ -1244,6 +1314,7 @@ def main():
         "decode_step": step,
         "prefill_model": pmodel,
         "deltanet": dnet,
+        "operators_other_shapes": ops_other,
     }
     print(json.dumps(line), flush=True)
 
